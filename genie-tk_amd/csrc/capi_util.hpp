@@ -1,0 +1,39 @@
+// Host-side helpers shared by the extern "C" entry points: error reporting,
+// launch checks and argument validation.  Every entry point returns 0 on
+// success or a GTK_E* code; the message is available from gtk_last_error().
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <string>
+
+#include "../../include/genie_tk.h"
+
+namespace gtk {
+
+void set_error(const char* fmt, ...);
+
+#define GTK_REQUIRE(cond, code, ...)        \
+  do {                                      \
+    if (!(cond)) {                          \
+      ::gtk::set_error(__VA_ARGS__);        \
+      return (code);                        \
+    }                                       \
+  } while (0)
+
+#define GTK_HIP_CHECK(expr)                                                         \
+  do {                                                                              \
+    hipError_t _e = (expr);                                                         \
+    if (_e != hipSuccess) {                                                         \
+      ::gtk::set_error("HIP error %s at %s:%d: %s", hipGetErrorName(_e), __FILE__, \
+                       __LINE__, hipGetErrorString(_e));                            \
+      return GTK_EHIP;                                                              \
+    }                                                                               \
+  } while (0)
+
+// Check the launch that was just enqueued.
+#define GTK_LAUNCH_CHECK() GTK_HIP_CHECK(hipGetLastError())
+
+inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+}  // namespace gtk

@@ -1,0 +1,208 @@
+// Shared device-side building blocks for the gfx950 (CDNA4) pair-stack kernels.
+//
+// Conventions used by every kernel in this library
+// -------------------------------------------------
+// * A "row tile" is 32 pair rows handled by one wavefront (64 lanes).  Lane l
+//   owns pair row (l & 31) and one half of that row's channels:
+//   half = l >> 5 owns channels [half*C/2, half*C/2 + C/2).
+// * Matrix-core work uses v_mfma_f32_32x32x16_bf16 (bf16 inputs) or
+//   v_mfma_f32_32x32x2_f32 (fp32 inputs), always with fp32 accumulation.
+//   Both instructions take, per lane, operand values for ONE row (A) or ONE
+//   column (B) indexed by (l & 31), and a k-group selected by (l >> 5).
+//   Because A and B use the same lane->k assignment, any bijection between
+//   "k-slot" and real contraction index is valid as long as both operands use
+//   it.  We use: chunk ks, lane half h, element e  <->  k = h*K/2 + ks*8 + e,
+//   so every lane reads 8 *consecutive* channels (16 B of bf16) per chunk.
+// * Accumulator layout of a 32x32 MFMA tile (16 fp32 per lane):
+//   acc[4*g + r]  <->  row 8*g + 4*(l>>5) + r,  column (l & 31).
+// * bf16 is stored as the compiler's native __bf16; fp32 -> bf16 conversion
+//   is round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gtk {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---------------------------------------------------------------------------
+// 8-element fragments: the per-lane operand of one 16-wide k chunk.
+// ---------------------------------------------------------------------------
+template <typename T> struct Frag;
+
+template <> struct Frag<bf16> {
+  bf16x8 v;
+  __device__ __forceinline__ void load(const bf16* p) { v = *reinterpret_cast<const bf16x8*>(p); }
+  __device__ __forceinline__ void zero() {
+    for (int e = 0; e < 8; ++e) v[e] = (bf16)0.0f;
+  }
+  __device__ __forceinline__ void set(const float* f) {
+    for (int e = 0; e < 8; ++e) v[e] = (bf16)f[e];
+  }
+  __device__ __forceinline__ float get(int e) const { return (float)v[e]; }
+};
+
+template <> struct Frag<float> {
+  f32x4 lo, hi;
+  __device__ __forceinline__ void load(const float* p) {
+    lo = *reinterpret_cast<const f32x4*>(p);
+    hi = *reinterpret_cast<const f32x4*>(p + 4);
+  }
+  __device__ __forceinline__ void zero() {
+    lo = f32x4{0.f, 0.f, 0.f, 0.f};
+    hi = lo;
+  }
+  __device__ __forceinline__ void set(const float* f) {
+    for (int e = 0; e < 4; ++e) { lo[e] = f[e]; hi[e] = f[e + 4]; }
+  }
+  __device__ __forceinline__ float get(int e) const { return e < 4 ? lo[e] : hi[e - 4]; }
+};
+
+// acc += A(32x16 chunk) * B(16x32 chunk)
+__device__ __forceinline__ void mma(f32x16& acc, const Frag<bf16>& a, const Frag<bf16>& b) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.v, b.v, acc, 0, 0, 0);
+}
+__device__ __forceinline__ void mma(f32x16& acc, const Frag<float>& a, const Frag<float>& b) {
+  for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.lo[e], b.lo[e], acc, 0, 0, 0);
+  for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.hi[e], b.hi[e], acc, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+  for (int e = 0; e < 16; ++e) z[e] = 0.f;
+  return z;
+}
+
+// ---------------------------------------------------------------------------
+// Scalar conversions and small vector stores.
+// ---------------------------------------------------------------------------
+template <typename T> __device__ __forceinline__ T cvt(float f);
+template <> __device__ __forceinline__ float cvt<float>(float f) { return f; }
+template <> __device__ __forceinline__ bf16 cvt<bf16>(float f) { return (bf16)f; }
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(bf16 x) { return (float)x; }
+
+// Store 4 consecutive values.
+__device__ __forceinline__ void store4(bf16* p, float a, float b, float c, float d) {
+  bf16x4 v;
+  v[0] = (bf16)a; v[1] = (bf16)b; v[2] = (bf16)c; v[3] = (bf16)d;
+  *reinterpret_cast<bf16x4*>(p) = v;
+}
+__device__ __forceinline__ void store4(float* p, float a, float b, float c, float d) {
+  *reinterpret_cast<f32x4*>(p) = f32x4{a, b, c, d};
+}
+// Load 4 consecutive values as fp32.
+__device__ __forceinline__ f32x4 load4f(const bf16* p) {
+  bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+  return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
+}
+__device__ __forceinline__ f32x4 load4f(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+// Value held by lane (l ^ 32).
+__device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); }
+
+// ---------------------------------------------------------------------------
+// Row-tile LayerNorm in fragment layout.
+//
+// Lane l holds pair row (l & 31), channels half*C/2 + [0, C/2) as C/16
+// fragments of 8.  The row statistics combine the lane's own half with lane
+// (l ^ 32)'s half.  Two-pass (mean, then centred sum of squares), biased
+// variance, eps inside the square root: y = (x - mu) / sqrt(var + eps) * w + b.
+// ---------------------------------------------------------------------------
+template <int C> struct RowHalf {
+  static constexpr int NCH = C / 16;  // fragments per lane
+  float v[C / 2];
+};
+
+template <typename TIn, int C>
+__device__ __forceinline__ void load_row_half(RowHalf<C>& r, const TIn* row_base, bool valid) {
+  const int half = (threadIdx.x & 63) >> 5;
+  const TIn* p = row_base + half * (C / 2);
+  if (valid) {
+#pragma unroll
+    for (int ch = 0; ch < C / 16; ++ch) {
+      Frag<TIn> f;
+      f.load(p + ch * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) r.v[ch * 8 + e] = f.get(e);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < C / 2; ++i) r.v[i] = 0.f;
+  }
+}
+
+// Returns (mean, rstd) of the full row of C channels.
+template <int C>
+__device__ __forceinline__ f32x2 row_stats(const RowHalf<C>& r, float eps) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < C / 2; ++i) s += r.v[i];
+  s += xor32(s);
+  const float mean = s * (1.0f / C);
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < C / 2; ++i) {
+    const float d = r.v[i] - mean;
+    q += d * d;
+  }
+  q += xor32(q);
+  const float var = q * (1.0f / C);
+  return f32x2{mean, 1.0f / sqrtf(var + eps)};
+}
+
+// Normalise + affine, then pack into MFMA fragments of type T.
+template <typename T, int C>
+__device__ __forceinline__ void ln_to_frags(Frag<T>* frags, const RowHalf<C>& r, f32x2 st,
+                                            const float* __restrict__ w, const float* __restrict__ b) {
+  const int half = (threadIdx.x & 63) >> 5;
+#pragma unroll
+  for (int ch = 0; ch < C / 16; ++ch) {
+    float f[8];
+    const int c0 = half * (C / 2) + ch * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = (r.v[ch * 8 + e] - st[0]) * st[1] * w[c0 + e] + b[c0 + e];
+    frags[ch].set(f);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Packed weight fragments.
+//
+// A Linear weight W[out][in] (nn.Linear layout) is packed for K = in so that
+// fragment (tile nt, chunk ks) is 64 lanes x 8 contiguous elements:
+//   packed[((nt*KCH + ks)*64 + l)*8 + e] = W[nt*32 + (l&31)][(l>>5)*K/2 + ks*8 + e]
+// (zero for out >= OUT).  One wave reads a fragment as 1 KiB (bf16) contiguous.
+// ---------------------------------------------------------------------------
+template <typename T>
+__device__ __forceinline__ void load_wfrag(Frag<T>& f, const T* __restrict__ packed, int nt, int ks, int kch) {
+  const int l = threadIdx.x & 63;
+  f.load(packed + ((size_t)(nt * kch + ks) * 64 + l) * 8);
+}
+
+// acc(32 pairs x 32 outputs of tile nt) = rows . W_nt^T over K = C.
+// SWAP=false: acc rows = pairs, cols = outputs.  SWAP=true: rows = outputs, cols = pairs.
+template <typename T, int C, bool SWAP>
+__device__ __forceinline__ f32x16 row_gemm_tile(const Frag<T>* xf, const T* __restrict__ packed, int nt) {
+  f32x16 acc = zero16();
+#pragma unroll
+  for (int ks = 0; ks < C / 16; ++ks) {
+    Frag<T> w;
+    load_wfrag<T>(w, packed, nt, ks, C / 16);
+    if (SWAP) mma(acc, w, xf[ks]);
+    else mma(acc, xf[ks], w);
+  }
+  return acc;
+}
+
+}  // namespace gtk

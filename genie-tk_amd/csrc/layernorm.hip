@@ -1,0 +1,235 @@
+// LayerNorm and LayerNorm+Linear for gfx950.
+//
+// gtk_layernorm: one pass over HBM.  A row of D channels is spread over D/8
+// lanes (8 contiguous channels = 16 B of bf16 per lane), so one wave covers
+// 64*8/D rows per step with fully coalesced 16 B loads and stores; U steps
+// are issued before any arithmetic so each wave keeps U loads in flight.
+// Statistics use an xor-butterfly inside the row's lane group.
+//
+// gtk_fused_layernorm_linear: the row is normalised in MFMA fragment layout
+// (see common.hpp) and multiplied with the packed weight on the matrix cores.
+#include "capi_util.hpp"
+#include "common.hpp"
+#include "pack.hpp"
+
+namespace gtk {
+
+template <typename T, int D, int U>
+__global__ __launch_bounds__(256) void ln_rows_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                      const float* __restrict__ gamma,
+                                                      const float* __restrict__ beta, int64_t rows,
+                                                      float eps) {
+  constexpr int LPR = D / 8;     // lanes per row
+  constexpr int RPW = 64 / LPR;  // rows per wave per step
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int sub = lane / LPR;
+  const int c0 = (lane % LPR) * 8;
+  float g[8], bt[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    g[e] = gamma[c0 + e];
+    bt[e] = beta[c0 + e];
+  }
+  const int64_t row0 = ((int64_t)blockIdx.x * 4 + wave) * (RPW * U) + sub;
+  float v[U][8];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t r = row0 + (int64_t)u * RPW;
+    if (r < rows) {
+      Frag<T> f;
+      f.load(x + r * D + c0);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[u][e] = f.get(e);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[u][e] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += v[u][e];
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    const float mean = s * (1.0f / D);
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float d = v[u][e] - mean;
+      q += d * d;
+    }
+#pragma unroll
+    for (int off = LPR / 2; off > 0; off >>= 1) q += __shfl_xor(q, off, 64);
+    const float rstd = 1.0f / sqrtf(q * (1.0f / D) + eps);
+    const int64_t r = row0 + (int64_t)u * RPW;
+    if (r < rows) {
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (v[u][e] - mean) * rstd * g[e] + bt[e];
+      Frag<T> f;
+      f.set(o);
+      if constexpr (sizeof(T) == 2) {
+        *reinterpret_cast<bf16x8*>(y + r * D + c0) = f.v;
+      } else {
+        *reinterpret_cast<f32x4*>(y + r * D + c0) = f.lo;
+        *reinterpret_cast<f32x4*>(y + r * D + c0 + 4) = f.hi;
+      }
+    }
+  }
+}
+
+// Any D: one wave per row, three sweeps (sum, centred squares, write).
+template <typename T>
+__global__ __launch_bounds__(256) void ln_rows_generic_kernel(const T* __restrict__ x,
+                                                              T* __restrict__ y,
+                                                              const float* __restrict__ gamma,
+                                                              const float* __restrict__ beta,
+                                                              int64_t rows, int D, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;
+  const T* xr = x + r * D;
+  float s = 0.f;
+  for (int c = lane; c < D; c += 64) s += to_f32(xr[c]);
+  for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+  const float mean = s / (float)D;
+  float q = 0.f;
+  for (int c = lane; c < D; c += 64) {
+    const float d = to_f32(xr[c]) - mean;
+    q += d * d;
+  }
+  for (int off = 32; off > 0; off >>= 1) q += __shfl_xor(q, off, 64);
+  const float rstd = 1.0f / sqrtf(q / (float)D + eps);
+  for (int c = lane; c < D; c += 64)
+    y[r * D + c] = cvt<T>((to_f32(xr[c]) - mean) * rstd * gamma[c] + beta[c]);
+}
+
+template <typename T>
+static int launch_ln(const T* x, T* y, const float* g, const float* b, int64_t rows, int64_t d,
+                     float eps, hipStream_t st) {
+  constexpr int U = 4;
+  auto grid_for = [&](int D) {
+    const int64_t rows_per_block = 4 * (64 / (D / 8)) * U;
+    return (unsigned)((rows + rows_per_block - 1) / rows_per_block);
+  };
+  switch (d) {
+    case 64: ln_rows_kernel<T, 64, U><<<grid_for(64), 256, 0, st>>>(x, y, g, b, rows, eps); break;
+    case 128: ln_rows_kernel<T, 128, U><<<grid_for(128), 256, 0, st>>>(x, y, g, b, rows, eps); break;
+    case 256: ln_rows_kernel<T, 256, U><<<grid_for(256), 256, 0, st>>>(x, y, g, b, rows, eps); break;
+    case 512: ln_rows_kernel<T, 512, U><<<grid_for(512), 256, 0, st>>>(x, y, g, b, rows, eps); break;
+    default:
+      ln_rows_generic_kernel<T><<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(x, y, g, b, rows,
+                                                                            (int)d, eps);
+  }
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+// ---------------------------------------------------------------------------
+// LayerNorm + Linear: y = LN(x) @ W + bias, W packed (see pack.hpp).
+// One wave = 32 rows; lane (l&31) owns a row, (l>>5) a channel half.
+// ---------------------------------------------------------------------------
+template <typename T, int DIN>
+__global__ __launch_bounds__(256) void ln_linear_kernel(const T* __restrict__ x, T* __restrict__ y,
+                                                        const float* __restrict__ gamma,
+                                                        const float* __restrict__ beta,
+                                                        const T* __restrict__ wp,
+                                                        const float* __restrict__ bias,
+                                                        int64_t rows, int d_out, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int half = lane >> 5;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t row = tile * 32 + (lane & 31);
+  if (tile * 32 >= rows) return;  // whole wave idle (uniform)
+  const bool valid = row < rows;
+  RowHalf<DIN> rh;
+  load_row_half<T, DIN>(rh, x + (valid ? row : 0) * DIN, valid);
+  const f32x2 st = row_stats<DIN>(rh, eps);
+  Frag<T> xf[DIN / 16];
+  ln_to_frags<T, DIN>(xf, rh, st, gamma, beta);
+  const int ntiles = (d_out + 31) / 32;
+  for (int nt = 0; nt < ntiles; ++nt) {
+    const f32x16 acc = row_gemm_tile<T, DIN, true>(xf, wp, nt);
+    if (!valid) continue;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int o0 = nt * 32 + 8 * g + 4 * half;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int o = o0 + r;
+        if (o < d_out) y[row * d_out + o] = cvt<T>(acc[4 * g + r] + (bias ? bias[o] : 0.f));
+      }
+    }
+  }
+}
+
+}  // namespace gtk
+
+using namespace gtk;
+
+extern "C" int gtk_layernorm(const void* x, void* y, const float* gamma, const float* beta,
+                             int64_t rows, int64_t d, float eps, int dtype, void* stream) {
+  GTK_REQUIRE(rows >= 0 && d >= 1, GTK_EINVAL, "gtk_layernorm: bad shape rows=%lld d=%lld",
+              (long long)rows, (long long)d);
+  GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL, "gtk_layernorm: bad dtype %d",
+              dtype);
+  if (rows == 0) return GTK_OK;
+  GTK_REQUIRE(x && y && gamma && beta, GTK_EINVAL, "gtk_layernorm: null pointer");
+  GTK_REQUIRE(rows <= (int64_t)1 << 40, GTK_EINVAL, "gtk_layernorm: too many rows");
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == GTK_F32) return launch_ln<float>((const float*)x, (float*)y, gamma, beta, rows, d, eps, st);
+  return launch_ln<bf16>((const bf16*)x, (bf16*)y, gamma, beta, rows, d, eps, st);
+}
+
+extern "C" size_t gtk_fused_layernorm_linear_workspace_size(int64_t d_in, int64_t d_out, int dtype) {
+  if (d_in < 16 || d_out < 1) return 0;
+  return (size_t)packed_elems(d_out, d_in) * dtype_size(dtype);
+}
+
+extern "C" int gtk_fused_layernorm_linear(const void* x, void* y, const float* gamma,
+                                          const float* beta, const void* weight, int weight_dtype,
+                                          const float* bias, int64_t rows, int64_t d_in,
+                                          int64_t d_out, float eps, int dtype, void* workspace,
+                                          size_t workspace_bytes, void* stream) {
+  GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL,
+              "gtk_fused_layernorm_linear: bad dtype %d", dtype);
+  GTK_REQUIRE(weight_dtype == GTK_F32 || weight_dtype == GTK_BF16, GTK_EINVAL,
+              "gtk_fused_layernorm_linear: bad weight dtype %d", weight_dtype);
+  GTK_REQUIRE(d_in == 64 || d_in == 128 || d_in == 256, GTK_EUNSUPPORTED,
+              "gtk_fused_layernorm_linear: d_in=%lld not in {64,128,256}", (long long)d_in);
+  GTK_REQUIRE(d_out >= 1 && d_out <= (1 << 16) && rows >= 0, GTK_EINVAL,
+              "gtk_fused_layernorm_linear: bad shape");
+  if (rows == 0) return GTK_OK;
+  GTK_REQUIRE(x && y && gamma && beta && weight && workspace, GTK_EINVAL,
+              "gtk_fused_layernorm_linear: null pointer");
+  const size_t need = gtk_fused_layernorm_linear_workspace_size(d_in, d_out, dtype);
+  GTK_REQUIRE(workspace_bytes >= need, GTK_EWORKSPACE,
+              "gtk_fused_layernorm_linear: workspace %zu < %zu bytes", workspace_bytes, need);
+  hipStream_t st = (hipStream_t)stream;
+  const unsigned grid = (unsigned)(((rows + 31) / 32 + 3) / 4);
+  // weight is [d_in][d_out]: logical W[out][in] has s_out = 1, s_in = d_out.
+  int rc;
+  if (dtype == GTK_F32) {
+    float* wp = (float*)workspace;
+    if ((rc = launch_pack<float>(wp, weight, weight_dtype, (int)d_out, (int)d_in, 1, d_out, 1.f, st)))
+      return rc;
+    switch (d_in) {
+      case 64: ln_linear_kernel<float, 64><<<grid, 256, 0, st>>>((const float*)x, (float*)y, gamma, beta, wp, bias, rows, (int)d_out, eps); break;
+      case 128: ln_linear_kernel<float, 128><<<grid, 256, 0, st>>>((const float*)x, (float*)y, gamma, beta, wp, bias, rows, (int)d_out, eps); break;
+      default: ln_linear_kernel<float, 256><<<grid, 256, 0, st>>>((const float*)x, (float*)y, gamma, beta, wp, bias, rows, (int)d_out, eps); break;
+    }
+  } else {
+    bf16* wp = (bf16*)workspace;
+    if ((rc = launch_pack<bf16>(wp, weight, weight_dtype, (int)d_out, (int)d_in, 1, d_out, 1.f, st)))
+      return rc;
+    switch (d_in) {
+      case 64: ln_linear_kernel<bf16, 64><<<grid, 256, 0, st>>>((const bf16*)x, (bf16*)y, gamma, beta, wp, bias, rows, (int)d_out, eps); break;
+      case 128: ln_linear_kernel<bf16, 128><<<grid, 256, 0, st>>>((const bf16*)x, (bf16*)y, gamma, beta, wp, bias, rows, (int)d_out, eps); break;
+      default: ln_linear_kernel<bf16, 256><<<grid, 256, 0, st>>>((const bf16*)x, (bf16*)y, gamma, beta, wp, bias, rows, (int)d_out, eps); break;
+    }
+  }
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}

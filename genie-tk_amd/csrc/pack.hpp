@@ -1,0 +1,104 @@
+// Weight packing into MFMA fragment order, and small vector conversions.
+//
+// A weight matrix W (logical [out][in], arbitrary strides) is packed for
+// contraction over K = in:
+//   dst[((nt*KCH + ks)*64 + l)*8 + e] = scale * W[nt*32 + (l&31)][(l>>5)*K/2 + ks*8 + e]
+// with KCH = K/16 chunks and zero rows for out >= OUT.  This is the order the
+// device helpers in common.hpp (load_wfrag / row_gemm_tile) read.
+#pragma once
+#include "capi_util.hpp"
+#include "common.hpp"
+
+namespace gtk {
+
+inline int64_t packed_elems(int64_t out_dim, int64_t k_dim) {
+  return ((out_dim + 31) / 32) * (k_dim / 16) * 512;
+}
+
+template <typename Tout, typename Tin>
+__global__ void pack_weight_kernel(Tout* __restrict__ dst, const Tin* __restrict__ src, int out_dim,
+                                   int k_dim, int64_t s_out, int64_t s_in, float scale,
+                                   int64_t total) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int kch = k_dim / 16;
+  const int e = idx & 7;
+  const int l = (idx >> 3) & 63;
+  const int64_t rest = idx >> 9;
+  const int ks = (int)(rest % kch);
+  const int nt = (int)(rest / kch);
+  const int o = nt * 32 + (l & 31);
+  const int k = (l >> 5) * (k_dim / 2) + ks * 8 + e;
+  float v = 0.f;
+  if (o < out_dim) v = scale * to_f32(src[o * s_out + k * s_in]);
+  dst[idx] = cvt<Tout>(v);
+}
+
+template <typename Tin>
+__global__ void to_f32_kernel(float* __restrict__ dst, const Tin* __restrict__ src, int n,
+                              float scale, float fill) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  dst[i] = src ? scale * to_f32(src[i]) : fill;
+}
+
+// Pack W (element type `wdtype`) into dst (element type Tout).
+template <typename Tout>
+inline int launch_pack(Tout* dst, const void* src, int wdtype, int out_dim, int k_dim,
+                       int64_t s_out, int64_t s_in, float scale, hipStream_t st) {
+  const int64_t total = packed_elems(out_dim, k_dim);
+  const int blocks = (int)((total + 255) / 256);
+  if (wdtype == GTK_F32)
+    pack_weight_kernel<Tout, float><<<blocks, 256, 0, st>>>(dst, (const float*)src, out_dim, k_dim,
+                                                            s_out, s_in, scale, total);
+  else
+    pack_weight_kernel<Tout, bf16><<<blocks, 256, 0, st>>>(dst, (const bf16*)src, out_dim, k_dim,
+                                                           s_out, s_in, scale, total);
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+// Convert a parameter vector to fp32 (src == nullptr -> filled with `fill`).
+inline int launch_to_f32(float* dst, const void* src, int dtype, int n, float scale, float fill,
+                         hipStream_t st) {
+  const int blocks = (n + 255) / 256;
+  if (dtype == GTK_F32)
+    to_f32_kernel<float><<<blocks, 256, 0, st>>>(dst, (const float*)src, n, scale, fill);
+  else
+    to_f32_kernel<bf16><<<blocks, 256, 0, st>>>(dst, (const bf16*)src, n, scale, fill);
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+// Zero a device buffer with a kernel (not hipMemsetAsync, so that callers
+// may capture the enqueue into a HIP graph).
+static __global__ void zero_fill_kernel(f32x4* __restrict__ p, int64_t n16) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n16) p[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+inline int launch_zero(void* p, size_t bytes, hipStream_t st) {
+  const int64_t n16 = (int64_t)(bytes / 16);
+  if (n16 == 0) return GTK_OK;
+  zero_fill_kernel<<<(unsigned)((n16 + 255) / 256), 256, 0, st>>>((f32x4*)p, n16);
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+// Bump allocator over a caller-provided buffer (256-byte aligned slices).
+struct Carve {
+  char* base;
+  size_t cap;
+  size_t off = 0;
+  Carve(void* b, size_t c) : base((char*)b), cap(c) {}
+  template <typename T> T* take(int64_t n) {
+    off = (off + 255) & ~size_t(255);
+    T* p = (T*)(base ? base + off : nullptr);
+    off += sizeof(T) * (size_t)n;
+    return p;
+  }
+  bool fits() const { return off <= cap; }
+};
+
+inline size_t dtype_size(int dtype) { return dtype == GTK_F32 ? 4 : 2; }
+
+}  // namespace gtk

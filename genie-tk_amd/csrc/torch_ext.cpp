@@ -1,0 +1,289 @@
+// genie_tk._C — thin PyTorch binding over the C ABI in include/genie_tk.h.
+//
+// Mirrors the operator surface of the reference extension
+// (kernels/bindings.cpp:69-101: triangle_mul_outgoing/incoming,
+// triangle_attention_starting/ending, layernorm, fused_layernorm_linear) and
+// adds the fused module entry points used by the modules' _forward_cuda.
+// Tensors are checked, made contiguous, and every launch goes to the caller's
+// current HIP stream; scratch comes from torch's caching allocator.
+#include <c10/hip/HIPStream.h>
+#include <torch/extension.h>
+
+#include <vector>
+
+#include "../../include/genie_tk.h"
+
+namespace {
+
+int gtk_dtype_of(const at::Tensor& t, const char* what) {
+  if (t.scalar_type() == at::kFloat) return GTK_F32;
+  if (t.scalar_type() == at::kBFloat16) return GTK_BF16;
+  TORCH_CHECK(false, "genie_tk._C: ", what, " must be float32 or bfloat16, got ", t.scalar_type());
+  return -1;
+}
+
+void check_rc(int rc) { TORCH_CHECK(rc == GTK_OK, "genie_tk._C: ", gtk_last_error()); }
+
+void* cur_stream(const at::Tensor& t) {
+  return (void*)c10::hip::getCurrentHIPStream(t.device().index()).stream();
+}
+
+void check_gpu(const at::Tensor& t, const char* what) {
+  TORCH_CHECK(t.is_cuda(), what, " must be CUDA tensor");
+}
+
+at::Tensor f32c(const at::Tensor& t) { return t.to(at::kFloat).contiguous(); }
+
+at::Tensor workspace(const at::Tensor& like, size_t bytes) {
+  return at::empty({(int64_t)std::max<size_t>(bytes, 1)}, like.options().dtype(at::kByte));
+}
+
+// ---------------------------------------------------------------------------
+// Reference operator surface
+// ---------------------------------------------------------------------------
+at::Tensor layernorm(const at::Tensor& x, const at::Tensor& gamma, const at::Tensor& beta,
+                     double eps) {
+  check_gpu(x, "x");
+  check_gpu(gamma, "gamma");
+  check_gpu(beta, "beta");
+  const at::DeviceGuard guard(x.device());
+  TORCH_CHECK(x.dim() >= 1, "x must have at least one dimension");
+  auto xc = x.contiguous();
+  const int64_t d = xc.size(-1);
+  const int64_t rows = d ? xc.numel() / d : 0;
+  auto g = f32c(gamma), b = f32c(beta);
+  TORCH_CHECK(g.numel() == d && b.numel() == d, "gamma/beta must have ", d, " elements");
+  auto y = at::empty_like(xc);
+  check_rc(gtk_layernorm(xc.data_ptr(), y.data_ptr(), g.data_ptr<float>(), b.data_ptr<float>(),
+                         rows, d, (float)eps, gtk_dtype_of(xc, "x"), cur_stream(xc)));
+  return y;
+}
+
+at::Tensor fused_layernorm_linear(const at::Tensor& x, const at::Tensor& gamma,
+                                  const at::Tensor& beta, const at::Tensor& weight,
+                                  const c10::optional<at::Tensor>& bias, double eps) {
+  check_gpu(x, "x");
+  check_gpu(weight, "weight");
+  const at::DeviceGuard guard(x.device());
+  auto xc = x.contiguous();
+  const int64_t d_in = xc.size(-1);
+  TORCH_CHECK(weight.dim() == 2 && weight.size(0) == d_in, "weight must be [D_IN, D_OUT]");
+  const int64_t d_out = weight.size(1);
+  const int64_t rows = d_in ? xc.numel() / d_in : 0;
+  auto g = f32c(gamma), b = f32c(beta);
+  TORCH_CHECK(g.numel() == d_in && b.numel() == d_in, "gamma/beta must have ", d_in, " elements");
+  auto w = weight.contiguous();
+  at::Tensor bb;
+  if (bias.has_value()) {
+    bb = f32c(*bias);
+    TORCH_CHECK(bb.numel() == d_out, "bias must have ", d_out, " elements");
+  }
+  auto sizes = xc.sizes().vec();
+  sizes.back() = d_out;
+  auto y = at::empty(sizes, xc.options());
+  const int dt = gtk_dtype_of(xc, "x");
+  auto ws = workspace(xc, gtk_fused_layernorm_linear_workspace_size(d_in, d_out, dt));
+  check_rc(gtk_fused_layernorm_linear(xc.data_ptr(), y.data_ptr(), g.data_ptr<float>(),
+                                      b.data_ptr<float>(), w.data_ptr(), gtk_dtype_of(w, "weight"),
+                                      bias.has_value() ? bb.data_ptr<float>() : nullptr, rows, d_in,
+                                      d_out, (float)eps, dt, ws.data_ptr(), ws.numel(),
+                                      cur_stream(xc)));
+  return y;
+}
+
+at::Tensor triangle_mul_raw(const at::Tensor& a, const at::Tensor& b, const at::Tensor& mask,
+                            bool outgoing) {
+  check_gpu(a, "a");
+  check_gpu(b, "b");
+  const at::DeviceGuard guard(a.device());
+  TORCH_CHECK(a.dim() == 4 && a.sizes() == b.sizes() && a.size(1) == a.size(2),
+              "a and b must both be [B, N, N, C]");
+  TORCH_CHECK(a.scalar_type() == b.scalar_type(), "a and b must have the same dtype");
+  TORCH_CHECK(mask.numel() == a.size(0) * a.size(1) * a.size(2), "mask must be [B, N, N]");
+  auto ac = a.contiguous(), bc = b.contiguous();
+  const int64_t B = ac.size(0), N = ac.size(1), C = ac.size(3);
+  const int dt = gtk_dtype_of(ac, "a");
+  auto x = at::empty_like(ac);
+  auto ws = workspace(ac, gtk_triangle_mul_workspace_size(B, N, C, dt));
+  auto fn = outgoing ? gtk_triangle_mul_outgoing : gtk_triangle_mul_incoming;
+  check_rc(fn(ac.data_ptr(), bc.data_ptr(), nullptr, x.data_ptr(), B, N, C, dt, ws.data_ptr(),
+              ws.numel(), cur_stream(ac)));
+  return x;
+}
+
+at::Tensor triangle_mul_outgoing(const at::Tensor& a, const at::Tensor& b, const at::Tensor& mask) {
+  return triangle_mul_raw(a, b, mask, true);
+}
+at::Tensor triangle_mul_incoming(const at::Tensor& a, const at::Tensor& b, const at::Tensor& mask) {
+  return triangle_mul_raw(a, b, mask, false);
+}
+
+at::Tensor triangle_attention_raw(const at::Tensor& q, const at::Tensor& k, const at::Tensor& v,
+                                  const at::Tensor& bias, const at::Tensor& mask, double scale,
+                                  bool starting) {
+  check_gpu(q, "q");
+  const at::DeviceGuard guard(q.device());
+  TORCH_CHECK(q.dim() == 5 && q.sizes() == k.sizes() && q.sizes() == v.sizes() &&
+                  q.size(2) == q.size(3),
+              "q, k, v must be [B, H, N, N, D]");
+  TORCH_CHECK(q.scalar_type() == k.scalar_type() && q.scalar_type() == v.scalar_type(),
+              "q, k, v must have the same dtype");
+  const int64_t B = q.size(0), H = q.size(1), N = q.size(2), D = q.size(4);
+  TORCH_CHECK(bias.numel() == B * H * N * N, "bias must be [B, H, N, N]");
+  TORCH_CHECK(mask.numel() == B * N * N, "mask must be [B, N, N]");
+  auto qc = q.contiguous(), kc = k.contiguous(), vc = v.contiguous();
+  auto bc = f32c(bias), mc = f32c(mask);
+  const int dt = gtk_dtype_of(qc, "q");
+  auto out = at::empty({B, N, N, H * D}, qc.options());
+  auto ws = workspace(qc, gtk_triangle_attention_workspace_size(B, H, N, D, dt));
+  auto fn = starting ? gtk_triangle_attention_starting : gtk_triangle_attention_ending;
+  check_rc(fn(qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), bc.data_ptr<float>(),
+              mc.data_ptr<float>(), (float)scale, out.data_ptr(), B, H, N, D, dt, ws.data_ptr(),
+              ws.numel(), cur_stream(qc)));
+  return out;
+}
+
+at::Tensor triangle_attention_starting(const at::Tensor& q, const at::Tensor& k,
+                                       const at::Tensor& v, const at::Tensor& bias,
+                                       const at::Tensor& mask, double scale) {
+  return triangle_attention_raw(q, k, v, bias, mask, scale, true);
+}
+at::Tensor triangle_attention_ending(const at::Tensor& q, const at::Tensor& k,
+                                     const at::Tensor& v, const at::Tensor& bias,
+                                     const at::Tensor& mask, double scale) {
+  return triangle_attention_raw(q, k, v, bias, mask, scale, false);
+}
+
+// ---------------------------------------------------------------------------
+// Fused module forwards
+// ---------------------------------------------------------------------------
+int common_param_dtype(std::vector<at::Tensor>& ps) {
+  bool all_bf16 = true;
+  for (auto& p : ps)
+    if (p.defined() && p.scalar_type() != at::kBFloat16) all_bf16 = false;
+  for (auto& p : ps)
+    if (p.defined()) p = (all_bf16 ? p : p.to(at::kFloat)).contiguous();
+  return all_bf16 ? GTK_BF16 : GTK_F32;
+}
+
+const void* ptr_or_null(const at::Tensor& t) { return t.defined() ? t.data_ptr() : nullptr; }
+
+// params: ln_in_w, ln_in_b, a_p_w, a_p_b, a_g_w, a_g_b, b_p_w, b_p_b, b_g_w, b_g_b,
+//         g_w, g_b, ln_out_w, ln_out_b, z_w, z_b
+at::Tensor tri_mul_pack(std::vector<at::Tensor> ps, int64_t c_z, int64_t c, bool fp32) {
+  TORCH_CHECK(ps.size() == 16, "tri_mul_pack expects 16 parameter tensors");
+  check_gpu(ps[2], "weights");
+  const at::DeviceGuard guard(ps[2].device());
+  gtk_tri_mul_weights w;
+  w.dtype = common_param_dtype(ps);
+  const void** slots[16] = {&w.ln_in_w, &w.ln_in_b, &w.a_p_w, &w.a_p_b, &w.a_g_w, &w.a_g_b,
+                            &w.b_p_w,   &w.b_p_b,   &w.b_g_w, &w.b_g_b, &w.g_w,   &w.g_b,
+                            &w.ln_out_w, &w.ln_out_b, &w.z_w, &w.z_b};
+  for (int i = 0; i < 16; ++i) *slots[i] = ptr_or_null(ps[i]);
+  const int dt = fp32 ? GTK_F32 : GTK_BF16;
+  const size_t bytes = gtk_tri_mul_packed_size(c_z, c, dt);
+  TORCH_CHECK(bytes > 0, "genie_tk._C: tri_mul shape c_z=", c_z, " c=", c, " unsupported");
+  auto packed = workspace(ps[2], bytes);
+  check_rc(gtk_tri_mul_pack(&w, c_z, c, dt, packed.data_ptr(), packed.numel(), cur_stream(ps[2])));
+  return packed;
+}
+
+at::Tensor tri_mul_forward(const at::Tensor& z, const c10::optional<at::Tensor>& mask,
+                           const at::Tensor& packed, int64_t c_z, int64_t c, bool outgoing,
+                           bool residual, double eps_in, double eps_out) {
+  check_gpu(z, "z");
+  const at::DeviceGuard guard(z.device());
+  TORCH_CHECK(z.dim() == 4 && z.size(1) == z.size(2) && z.size(3) == c_z, "z must be [B, N, N, c_z]");
+  auto zc = z.contiguous();
+  const int64_t B = zc.size(0), N = zc.size(1);
+  at::Tensor mc;
+  if (mask.has_value()) {
+    TORCH_CHECK(mask->numel() == B * N * N, "mask must be [B, N, N]");
+    mc = f32c(*mask);
+  }
+  const int dt = gtk_dtype_of(zc, "z");
+  auto out = at::empty_like(zc);
+  auto ws = workspace(zc, gtk_tri_mul_workspace_size(B, N, c_z, c, dt));
+  check_rc(gtk_tri_mul_forward(zc.data_ptr(), mask.has_value() ? mc.data_ptr<float>() : nullptr,
+                               out.data_ptr(), packed.data_ptr(), B, N, c_z, c, outgoing ? 1 : 0,
+                               residual ? 1 : 0, (float)eps_in, (float)eps_out, dt, ws.data_ptr(),
+                               ws.numel(), cur_stream(zc)));
+  return out;
+}
+
+// params: ln_w, ln_b, tri_w, q_w, k_w, v_w, g_w, g_b, o_w, o_b
+at::Tensor tri_attn_pack(std::vector<at::Tensor> ps, int64_t c_in, int64_t c_h, int64_t H,
+                         bool fp32) {
+  TORCH_CHECK(ps.size() == 10, "tri_attn_pack expects 10 parameter tensors");
+  check_gpu(ps[3], "weights");
+  const at::DeviceGuard guard(ps[3].device());
+  gtk_tri_attn_weights w;
+  w.dtype = common_param_dtype(ps);
+  const void** slots[10] = {&w.ln_w, &w.ln_b, &w.tri_w, &w.q_w, &w.k_w,
+                            &w.v_w,  &w.g_w,  &w.g_b,   &w.o_w, &w.o_b};
+  for (int i = 0; i < 10; ++i) *slots[i] = ptr_or_null(ps[i]);
+  const int dt = fp32 ? GTK_F32 : GTK_BF16;
+  const size_t bytes = gtk_tri_attn_packed_size(c_in, c_h, H, dt);
+  TORCH_CHECK(bytes > 0, "genie_tk._C: tri_attn shape c_in=", c_in, " c_h=", c_h, " H=", H,
+              " unsupported");
+  auto packed = workspace(ps[3], bytes);
+  check_rc(gtk_tri_attn_pack(&w, c_in, c_h, H, dt, packed.data_ptr(), packed.numel(),
+                             cur_stream(ps[3])));
+  return packed;
+}
+
+at::Tensor tri_attn_forward(const at::Tensor& x, const c10::optional<at::Tensor>& mask,
+                            const at::Tensor& packed, int64_t c_in, int64_t c_h, int64_t H,
+                            bool starting, bool residual, double eps) {
+  check_gpu(x, "x");
+  const at::DeviceGuard guard(x.device());
+  TORCH_CHECK(x.dim() == 4 && x.size(1) == x.size(2) && x.size(3) == c_in, "x must be [B, N, N, c_in]");
+  auto xc = x.contiguous();
+  const int64_t B = xc.size(0), N = xc.size(1);
+  at::Tensor mc;
+  if (mask.has_value()) {
+    TORCH_CHECK(mask->numel() == B * N * N, "mask must be [B, N, N]");
+    mc = f32c(*mask);
+  }
+  const int dt = gtk_dtype_of(xc, "x");
+  auto out = at::empty_like(xc);
+  auto ws = workspace(xc, gtk_tri_attn_workspace_size(B, N, c_in, c_h, H, dt));
+  check_rc(gtk_tri_attn_forward(xc.data_ptr(), mask.has_value() ? mc.data_ptr<float>() : nullptr,
+                                out.data_ptr(), packed.data_ptr(), B, N, c_in, c_h, H,
+                                starting ? 1 : 0, residual ? 1 : 0, (float)eps, dt, ws.data_ptr(),
+                                ws.numel(), cur_stream(xc)));
+  return out;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_C, m) {
+  m.doc() = "genie_tk._C: gfx950 HIP kernels for the pair-representation hot path";
+  m.def("triangle_mul_outgoing", &triangle_mul_outgoing, "Triangle contraction, outgoing edges",
+        py::arg("a"), py::arg("b"), py::arg("mask"));
+  m.def("triangle_mul_incoming", &triangle_mul_incoming, "Triangle contraction, incoming edges",
+        py::arg("a"), py::arg("b"), py::arg("mask"));
+  m.def("triangle_attention_starting", &triangle_attention_starting,
+        "Triangle attention core, starting node", py::arg("q"), py::arg("k"), py::arg("v"),
+        py::arg("bias"), py::arg("mask"), py::arg("scale"));
+  m.def("triangle_attention_ending", &triangle_attention_ending,
+        "Triangle attention core, ending node", py::arg("q"), py::arg("k"), py::arg("v"),
+        py::arg("bias"), py::arg("mask"), py::arg("scale"));
+  m.def("layernorm", &layernorm, "LayerNorm forward", py::arg("x"), py::arg("gamma"),
+        py::arg("beta"), py::arg("eps") = 1e-5);
+  m.def("fused_layernorm_linear", &fused_layernorm_linear, "LayerNorm + Linear forward",
+        py::arg("x"), py::arg("gamma"), py::arg("beta"), py::arg("weight"),
+        py::arg("bias") = py::none(), py::arg("eps") = 1e-5);
+  m.def("tri_mul_pack", &tri_mul_pack, "Pack TriangleMultiplicativeUpdate parameters",
+        py::arg("params"), py::arg("c_z"), py::arg("c"), py::arg("fp32"));
+  m.def("tri_mul_forward", &tri_mul_forward, "Fused TriangleMultiplicativeUpdate forward",
+        py::arg("z"), py::arg("mask"), py::arg("packed"), py::arg("c_z"), py::arg("c"),
+        py::arg("outgoing"), py::arg("residual") = false, py::arg("eps_in") = 1e-5,
+        py::arg("eps_out") = 1e-5);
+  m.def("tri_attn_pack", &tri_attn_pack, "Pack TriangleAttention parameters", py::arg("params"),
+        py::arg("c_in"), py::arg("c_h"), py::arg("no_heads"), py::arg("fp32"));
+  m.def("tri_attn_forward", &tri_attn_forward, "Fused TriangleAttention forward", py::arg("x"),
+        py::arg("mask"), py::arg("packed"), py::arg("c_in"), py::arg("c_h"), py::arg("no_heads"),
+        py::arg("starting"), py::arg("residual") = false, py::arg("eps") = 1e-5);
+  m.def("version", []() { return gtk_version(); });
+}

@@ -1,0 +1,587 @@
+// Triangle attention (starting / ending node) for gfx950.
+//
+// Both nodes run in "destination" coordinates: row r is the axis whose
+// entries are independent attention problems, positions j inside a row are
+// queries and keys.  Starting node: (r, j) = pair (i, j).  Ending node:
+// (r, j) = pair (j, i) of the input, i.e. the transposed problem
+// (ending(x, m) = starting(x^T, m^T)^T).
+//
+//  1. prologue: per pair, LN -> q (pre-scaled by log2(e)/sqrt(d)), k, v,
+//     gate sigmoid(. + b_g) and the triangle bias (scaled by log2(e)), all on
+//     the matrix cores.  Workspace layouts (Np = N rounded up to 64):
+//        q, k  [B][Np r][H][Np j][32]     v^T [B][Np r][H][32][Np j]
+//        gate  [B][Np r][Np j][c_h]       bias [B][H][Np q][Np k] (fp32)
+//  2. flash core: one wave = one head x 32 queries of one row; keys in tiles
+//     of 32.  S^T = K Q^T is accumulated on top of the bias tile, so lane l
+//     owns one query and 16 of its keys; the row max needs one lane^32
+//     exchange.  Online softmax in fp32 with exp2, P cast to bf16 and
+//     O^T += V^T P^T on the matrix cores.
+//  3. fused epilogue (module forward): o * gate for all heads staged in LDS,
+//     then the output projection W_o on the matrix cores, + b_o, optional
+//     residual, stored back at the source pair.
+//
+// Masking: key k of row r is excluded when mask == 0.  A row without any
+// valid key attends uniformly over all N keys: that is what the reference's
+// additive -1e9 bias produces in fp32 (every logit rounds to -1e9).
+#include "capi_util.hpp"
+#include "common.hpp"
+#include "pack.hpp"
+
+namespace gtk {
+
+constexpr int HD = 32;  // head dimension handled by the kernels
+
+template <typename T> struct TriAttnPacked {
+  T *w_q, *w_k, *w_v, *w_g, *w_b, *w_o;
+  float *ln_w, *ln_b, *b_g, *b_o;
+};
+
+template <typename T>
+static TriAttnPacked<T> carve_triattn(Carve& cv, int cin, int ch, int H) {
+  TriAttnPacked<T> p;
+  p.w_q = cv.take<T>(packed_elems(ch, cin));
+  p.w_k = cv.take<T>(packed_elems(ch, cin));
+  p.w_v = cv.take<T>(packed_elems(ch, cin));
+  p.w_g = cv.take<T>(packed_elems(ch, cin));
+  p.w_b = cv.take<T>(packed_elems(H, cin));
+  p.w_o = cv.take<T>(packed_elems(cin, ch));
+  p.ln_w = cv.take<float>(cin);
+  p.ln_b = cv.take<float>(cin);
+  p.b_g = cv.take<float>(ch);
+  p.b_o = cv.take<float>(cin);
+  return p;
+}
+
+template <typename T> struct AttnWs {
+  T *q, *k, *vt, *gate;
+  float* bias;
+};
+
+template <typename T>
+static AttnWs<T> carve_attn_ws(Carve& cv, int64_t B, int64_t Np, int H, int ch) {
+  AttnWs<T> w;
+  const int64_t qkv = B * Np * H * Np * HD;
+  w.q = cv.take<T>(qkv);
+  w.k = cv.take<T>(qkv);
+  w.vt = cv.take<T>(qkv);
+  w.gate = cv.take<T>(ch > 0 ? B * Np * Np * ch : 0);
+  w.bias = cv.take<float>(B * H * Np * Np);
+  return w;
+}
+
+// ---------------------------------------------------------------------------
+// 1. Prologue (fused module path)
+// ---------------------------------------------------------------------------
+template <typename T, int CIN, int H>
+__global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restrict__ x,
+                                                               TriAttnPacked<T> w, AttnWs<T> ws,
+                                                               int B, int N, int Np, int starting,
+                                                               float eps) {
+  constexpr int CH = H * HD;
+  const int lane = threadIdx.x & 63;
+  const int half = lane >> 5;
+  const int t32 = lane & 31;
+  const int vtiles = Np / 32;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile >= (int64_t)B * Np * vtiles) return;
+  const int vt = (int)(tile % vtiles);
+  const int r = (int)((tile / vtiles) % Np);  // destination row
+  const int b = (int)(tile / ((int64_t)vtiles * Np));
+  const int j = vt * 32 + t32;                // destination position
+  const bool valid = r < N && j < N;
+  const int p = starting ? r : j, q = starting ? j : r;  // source pair
+  const int64_t pair = ((int64_t)b * N + (valid ? p : 0)) * N + (valid ? q : 0);
+
+  RowHalf<CIN> rh;
+  load_row_half<T, CIN>(rh, x + pair * CIN, valid);
+  const f32x2 st = row_stats<CIN>(rh, eps);
+  Frag<T> xf[CIN / 16];
+  ln_to_frags<T, CIN>(xf, rh, st, w.ln_w, w.ln_b);
+  const float keep = valid ? 1.f : 0.f;
+
+  const int64_t rowbase = ((int64_t)b * Np + r);  // (b, r)
+#pragma unroll 1
+  for (int h = 0; h < H; ++h) {
+    // q, k: [b][r][h][j][d], lane holds d = 8g + 4*half + rr -> 4 consecutive d
+    const f32x16 aq = row_gemm_tile<T, CIN, true>(xf, w.w_q, h);
+    const f32x16 ak = row_gemm_tile<T, CIN, true>(xf, w.w_k, h);
+    const f32x16 av = row_gemm_tile<T, CIN, true>(xf, w.w_v, h);
+    T* qd = ws.q + ((rowbase * H + h) * Np + j) * HD;
+    T* kd = ws.k + ((rowbase * H + h) * Np + j) * HD;
+    T* vd = ws.vt + (rowbase * H + h) * HD * (int64_t)Np + j;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 8 * g + 4 * half;
+      store4(qd + d0, aq[4 * g] * keep, aq[4 * g + 1] * keep, aq[4 * g + 2] * keep, aq[4 * g + 3] * keep);
+      store4(kd + d0, ak[4 * g] * keep, ak[4 * g + 1] * keep, ak[4 * g + 2] * keep, ak[4 * g + 3] * keep);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) vd[(int64_t)(d0 + rr) * Np] = cvt<T>(av[4 * g + rr] * keep);
+    }
+  }
+  // gate: [b][r][j][CH]
+  T* gd = ws.gate + (rowbase * Np + j) * CH;
+#pragma unroll 1
+  for (int nt = 0; nt < CH / 32; ++nt) {
+    const f32x16 ag = row_gemm_tile<T, CIN, true>(xf, w.w_g, nt);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int c0 = nt * 32 + 8 * g + 4 * half;
+      store4(gd + c0, sigmoidf_(ag[4 * g] + w.b_g[c0]), sigmoidf_(ag[4 * g + 1] + w.b_g[c0 + 1]),
+             sigmoidf_(ag[4 * g + 2] + w.b_g[c0 + 2]), sigmoidf_(ag[4 * g + 3] + w.b_g[c0 + 3]));
+    }
+  }
+  // triangle bias: [b][h][r][j] (rows h >= H of the packed tile are zero)
+  {
+    const f32x16 ab = row_gemm_tile<T, CIN, true>(xf, w.w_b, 0);
+    if (half == 0) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+        if (rr < H) ws.bias[(((int64_t)b * H + rr) * Np + r) * Np + j] = ab[rr] * keep;
+    }
+    if (H > 4) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int h = 8 * g + 4 * half + rr;
+          if (h >= 4 && h < H) ws.bias[(((int64_t)b * H + h) * Np + r) * Np + j] = ab[4 * g + rr] * keep;
+        }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. Flash core: returns the normalised O^T tile of one (row, head, 32 queries)
+//    lane l: query q0 + (l&31), o[4g + rr] <-> d = 8g + 4*(l>>5) + rr
+// ---------------------------------------------------------------------------
+struct MaskView {
+  const float* m;  // nullptr: all valid
+  int64_t row_stride, key_stride;
+};
+
+template <typename T>
+__device__ __forceinline__ f32x16 flash_row_head(const T* __restrict__ qh, const T* __restrict__ kh,
+                                                 const T* __restrict__ vth,
+                                                 const float* __restrict__ biash, MaskView mv,
+                                                 int q0, int N, int Np) {
+  const int lane = threadIdx.x & 63;
+  const int half = lane >> 5;
+  const int t32 = lane & 31;
+
+  // Does this row have any valid key?
+  bool row_valid = true;
+  if (mv.m) {
+    bool any = false;
+    for (int k0 = 0; k0 < N; k0 += 64) {
+      const int k = k0 + lane;
+      const bool ok = k < N && mv.m[k * mv.key_stride] != 0.f;
+      any = any || (__ballot(ok) != 0ull);
+    }
+    row_valid = any;
+  }
+
+  Frag<T> qf[2];
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    if (row_valid) qf[m].load(qh + (int64_t)(q0 + t32) * HD + m * 16 + half * 8);
+    else qf[m].zero();
+  }
+  const float* brow = biash + (int64_t)(q0 + t32) * Np;
+
+  f32x16 o = zero16();
+  float m_run = -INFINITY, l_run = 0.f;
+  const int ktiles = (N + 31) / 32;
+  for (int kt = 0; kt < ktiles; ++kt) {
+    const int k0 = kt * 32;
+    f32x16 s;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      f32x4 bv = row_valid ? load4f(brow + k0 + 8 * g + 4 * half) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) s[4 * g + rr] = bv[rr];
+    }
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      Frag<T> kf;
+      kf.load(kh + (int64_t)(k0 + t32) * HD + m * 16 + half * 8);
+      mma(s, kf, qf[m]);
+    }
+    // exclusion: padded keys always, masked keys when the row has a valid key
+    const bool tail = k0 + 32 > N;
+    if (tail || (mv.m && row_valid)) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int k = k0 + 8 * g + 4 * half + rr;
+          bool ex = k >= N;
+          if (!ex && mv.m && row_valid) ex = mv.m[k * mv.key_stride] == 0.f;
+          if (ex) s[4 * g + rr] = -INFINITY;
+        }
+    }
+    float mt = s[0];
+#pragma unroll
+    for (int e = 1; e < 16; ++e) mt = fmaxf(mt, s[e]);
+    mt = fmaxf(mt, xor32(mt));
+    const float m_new = fmaxf(m_run, mt);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = exp2f(m_run - m_use);
+    float ls = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      s[e] = exp2f(s[e] - m_use);
+      ls += s[e];
+    }
+    l_run = l_run * alpha + ls;
+    m_run = m_new;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[e] *= alpha;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      Frag<T> pf, vf;
+      float pv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pv[e] = s[8 * c + e];
+      pf.set(pv);
+      // V^T fragment: row d = t32; slots e<4 -> key 16c+4h+e, e>=4 -> key 16c+8+4h+(e-4)
+      const T* vr = vth + (int64_t)t32 * Np + k0 + 16 * c + 4 * half;
+      float vv[8];
+      const f32x4 v0 = load4f(vr);
+      const f32x4 v1 = load4f(vr + 8);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) { vv[e] = v0[e]; vv[4 + e] = v1[e]; }
+      vf.set(vv);
+      mma(o, vf, pf);
+    }
+  }
+  const float l_tot = l_run + xor32(l_run);
+  const float inv = 1.0f / l_tot;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) o[e] *= inv;
+  return o;
+}
+
+// ---------------------------------------------------------------------------
+// 3a. Fused module kernel: all H heads of 32 queries of one row per block.
+// ---------------------------------------------------------------------------
+template <typename T, int CIN, int H>
+__global__ __launch_bounds__(64 * H) void triattn_fused_kernel(const T* __restrict__ x,
+                                                               const float* __restrict__ mask,
+                                                               T* __restrict__ out,
+                                                               TriAttnPacked<T> w, AttnWs<T> ws,
+                                                               int B, int N, int Np, int starting,
+                                                               int residual) {
+  constexpr int CH = H * HD;
+  constexpr int OPITCH = CH + 8;
+  __shared__ __attribute__((aligned(16))) T os[32 * OPITCH];
+  const int lane = threadIdx.x & 63;
+  const int h = threadIdx.x >> 6;
+  const int half = lane >> 5;
+  const int t32 = lane & 31;
+  const int qtiles = (N + 31) / 32;
+  const int qt = blockIdx.x % qtiles;
+  const int r = (blockIdx.x / qtiles) % N;
+  const int b = blockIdx.x / (qtiles * N);
+  const int q0 = qt * 32;
+
+  const int64_t rowbase = (int64_t)b * Np + r;
+  MaskView mv;
+  if (mask) {
+    // starting: key k of row r is pair (r, k); ending: pair (k, r)
+    mv.m = mask + (int64_t)b * N * N + (starting ? (int64_t)r * N : r);
+    mv.row_stride = 0;
+    mv.key_stride = starting ? 1 : N;
+  } else {
+    mv.m = nullptr;
+    mv.row_stride = mv.key_stride = 0;
+  }
+  const f32x16 o = flash_row_head<T>(ws.q + (rowbase * H + h) * Np * HD,
+                                     ws.k + (rowbase * H + h) * Np * HD,
+                                     ws.vt + (rowbase * H + h) * HD * (int64_t)Np,
+                                     ws.bias + ((int64_t)b * H + h) * Np * Np, mv, q0, N, Np);
+  // gate and stage o*g in LDS as [query][CH]
+  {
+    const T* gr = ws.gate + (rowbase * Np + q0 + t32) * CH + h * HD;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 8 * g + 4 * half;
+      const f32x4 gv = load4f(gr + d0);
+      store4(os + t32 * OPITCH + h * HD + d0, o[4 * g] * gv[0], o[4 * g + 1] * gv[1],
+             o[4 * g + 2] * gv[2], o[4 * g + 3] * gv[3]);
+    }
+  }
+  __syncthreads();
+  Frag<T> of[CH / 16];
+#pragma unroll
+  for (int ks = 0; ks < CH / 16; ++ks) of[ks].load(os + t32 * OPITCH + half * (CH / 2) + ks * 8);
+  const int q = q0 + t32;
+  const bool qvalid = q < N;
+  const int p0 = starting ? r : q, p1 = starting ? q : r;
+  const int64_t pair = ((int64_t)b * N + (qvalid ? p0 : 0)) * N + (qvalid ? p1 : 0);
+  for (int nt = h; nt < CIN / 32; nt += H) {
+    const f32x16 acc = row_gemm_tile<T, CH, true>(of, w.w_o, nt);
+    if (qvalid) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c0 = nt * 32 + 8 * g + 4 * half;
+        float v[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) v[rr] = acc[4 * g + rr] + w.b_o[c0 + rr];
+        if (residual) {
+          const f32x4 xr = load4f(x + pair * CIN + c0);
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) v[rr] += xr[rr];
+        }
+        store4(out + pair * CIN + c0, v[0], v[1], v[2], v[3]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 3b. Raw attention op: relayout of q/k/v/bias, then flash per (row, head).
+// ---------------------------------------------------------------------------
+// src: [B][H][N][N][D]; element (b, h, a1, a2, d).  Destination row/position:
+// starting (r, j) = (a1, a2); ending (r, j) = (a2, a1).
+template <typename T>
+__global__ void relayout_qkv_kernel(const T* __restrict__ src, T* __restrict__ dst, int B, int H,
+                                    int N, int Np, int starting, int transpose_v, float scale) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)B * H * N * N * HD;
+  if (idx >= total) return;
+  const int d = (int)(idx % HD);
+  int64_t t = idx / HD;
+  const int a2 = (int)(t % N); t /= N;
+  const int a1 = (int)(t % N); t /= N;
+  const int h = (int)(t % H);
+  const int b = (int)(t / H);
+  const int r = starting ? a1 : a2, j = starting ? a2 : a1;
+  const int64_t base = ((int64_t)b * Np + r) * H + h;
+  const float v = to_f32(src[idx]) * scale;
+  if (transpose_v) dst[(base * HD + d) * Np + j] = cvt<T>(v);
+  else dst[(base * Np + j) * HD + d] = cvt<T>(v);
+}
+
+__global__ void relayout_bias_kernel(const float* __restrict__ src, float* __restrict__ dst,
+                                     int B, int H, int N, int Np) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)B * H * N * N;
+  if (idx >= total) return;
+  const int k = (int)(idx % N);
+  const int64_t t = idx / N;
+  const int q = (int)(t % N);
+  const int64_t bh = t / N;
+  dst[(bh * Np + q) * Np + k] = src[idx] * kLog2e;
+}
+
+template <typename T>
+__global__ __launch_bounds__(64) void triattn_raw_kernel(const float* __restrict__ mask,
+                                                         T* __restrict__ out, AttnWs<T> ws, int B,
+                                                         int H, int N, int Np, int starting) {
+  const int lane = threadIdx.x & 63;
+  const int half = lane >> 5;
+  const int t32 = lane & 31;
+  const int qtiles = (N + 31) / 32;
+  int64_t t = blockIdx.x;
+  const int qt = (int)(t % qtiles); t /= qtiles;
+  const int h = (int)(t % H); t /= H;
+  const int r = (int)(t % N);
+  const int b = (int)(t / N);
+  const int q0 = qt * 32;
+  const int64_t rowbase = (int64_t)b * Np + r;
+  MaskView mv;
+  mv.m = mask + (int64_t)b * N * N + (starting ? (int64_t)r * N : r);
+  mv.row_stride = 0;
+  mv.key_stride = starting ? 1 : N;
+  const f32x16 o = flash_row_head<T>(ws.q + (rowbase * H + h) * Np * HD,
+                                     ws.k + (rowbase * H + h) * Np * HD,
+                                     ws.vt + (rowbase * H + h) * HD * (int64_t)Np,
+                                     ws.bias + ((int64_t)b * H + h) * Np * Np, mv, q0, N, Np);
+  const int q = q0 + t32;
+  if (q >= N) return;
+  const int p0 = starting ? r : q, p1 = starting ? q : r;
+  T* dst = out + (((int64_t)b * N + p0) * N + p1) * (int64_t)(H * HD) + h * HD;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int d0 = 8 * g + 4 * half;
+    store4(dst + d0, o[4 * g], o[4 * g + 1], o[4 * g + 2], o[4 * g + 3]);
+  }
+}
+
+template <typename T>
+static int raw_attention(const void* q, const void* k, const void* v, const float* bias,
+                         const float* mask, float scale, void* out, int64_t B, int64_t H,
+                         int64_t N, void* ws, int starting, hipStream_t st) {
+  const int Np = (int)round_up(N, 64);
+  Carve cv(ws, SIZE_MAX);
+  AttnWs<T> w = carve_attn_ws<T>(cv, B, Np, (int)H, 0);
+  // zero the padded workspace so padded keys/queries read finite values
+  int rc = launch_zero(w.q, (size_t)((char*)(w.bias + B * H * (int64_t)Np * Np) - (char*)w.q), st);
+  if (rc) return rc;
+  const int64_t total = B * H * N * N * HD;
+  const unsigned g1 = (unsigned)((total + 255) / 256);
+  relayout_qkv_kernel<T><<<g1, 256, 0, st>>>((const T*)q, w.q, (int)B, (int)H, (int)N, Np, starting, 0, scale * kLog2e);
+  GTK_LAUNCH_CHECK();
+  relayout_qkv_kernel<T><<<g1, 256, 0, st>>>((const T*)k, w.k, (int)B, (int)H, (int)N, Np, starting, 0, 1.f);
+  GTK_LAUNCH_CHECK();
+  relayout_qkv_kernel<T><<<g1, 256, 0, st>>>((const T*)v, w.vt, (int)B, (int)H, (int)N, Np, starting, 1, 1.f);
+  GTK_LAUNCH_CHECK();
+  const int64_t tb = B * H * N * N;
+  relayout_bias_kernel<<<(unsigned)((tb + 255) / 256), 256, 0, st>>>(bias, w.bias, (int)B, (int)H, (int)N, Np);
+  GTK_LAUNCH_CHECK();
+  const int64_t blocks = B * N * H * ((N + 31) / 32);
+  GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "attention grid too large");
+  triattn_raw_kernel<T><<<(unsigned)blocks, 64, 0, st>>>(mask, (T*)out, w, (int)B, (int)H, (int)N, Np, starting);
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+static int raw_attn_entry(const void* q, const void* k, const void* v, const float* bias,
+                          const float* mask, float scale, void* out, int64_t B, int64_t H,
+                          int64_t N, int64_t D, int dtype, void* ws, size_t ws_bytes,
+                          void* stream, int starting) {
+  const char* name = starting ? "gtk_triangle_attention_starting" : "gtk_triangle_attention_ending";
+  GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL, "%s: bad dtype %d", name, dtype);
+  GTK_REQUIRE(D == HD, GTK_EUNSUPPORTED, "%s: head dim %lld unsupported (32)", name, (long long)D);
+  GTK_REQUIRE(B >= 0 && H >= 1 && N >= 0 && N <= 8192, GTK_EINVAL, "%s: bad shape", name);
+  if (B == 0 || N == 0) return GTK_OK;
+  GTK_REQUIRE(q && k && v && bias && mask && out && ws, GTK_EINVAL, "%s: null pointer", name);
+  const size_t need = gtk_triangle_attention_workspace_size(B, H, N, D, dtype);
+  GTK_REQUIRE(ws_bytes >= need, GTK_EWORKSPACE, "%s: workspace %zu < %zu bytes", name, ws_bytes, need);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == GTK_F32) return raw_attention<float>(q, k, v, bias, mask, scale, out, B, H, N, ws, starting, st);
+  return raw_attention<bf16>(q, k, v, bias, mask, scale, out, B, H, N, ws, starting, st);
+}
+
+// ---------------------------------------------------------------------------
+// Fused module forward
+// ---------------------------------------------------------------------------
+template <typename T>
+static int pack_triattn(const gtk_tri_attn_weights* w, int cin, int ch, int H, void* packed,
+                        hipStream_t st) {
+  Carve cv(packed, SIZE_MAX);
+  TriAttnPacked<T> p = carve_triattn<T>(cv, cin, ch, H);
+  const int wd = w->dtype;
+  const float qscale = kLog2e / sqrtf((float)(ch / H));
+  int rc;
+  if ((rc = launch_pack<T>(p.w_q, w->q_w, wd, ch, cin, cin, 1, qscale, st))) return rc;
+  if ((rc = launch_pack<T>(p.w_k, w->k_w, wd, ch, cin, cin, 1, 1.f, st))) return rc;
+  if ((rc = launch_pack<T>(p.w_v, w->v_w, wd, ch, cin, cin, 1, 1.f, st))) return rc;
+  if ((rc = launch_pack<T>(p.w_g, w->g_w, wd, ch, cin, cin, 1, 1.f, st))) return rc;
+  if ((rc = launch_pack<T>(p.w_b, w->tri_w, wd, H, cin, cin, 1, kLog2e, st))) return rc;
+  if ((rc = launch_pack<T>(p.w_o, w->o_w, wd, cin, ch, ch, 1, 1.f, st))) return rc;
+  if ((rc = launch_to_f32(p.ln_w, w->ln_w, wd, cin, 1.f, 1.f, st))) return rc;
+  if ((rc = launch_to_f32(p.ln_b, w->ln_b, wd, cin, 1.f, 0.f, st))) return rc;
+  if ((rc = launch_to_f32(p.b_g, w->g_b, wd, ch, 1.f, 0.f, st))) return rc;
+  if ((rc = launch_to_f32(p.b_o, w->o_b, wd, cin, 1.f, 0.f, st))) return rc;
+  return GTK_OK;
+}
+
+template <typename T, int CIN, int H>
+static int fwd_triattn(const void* x, const float* mask, void* out, const void* packed, int64_t B,
+                       int64_t N, int starting, int residual, float eps, void* ws, hipStream_t st) {
+  constexpr int CH = H * HD;
+  Carve pc((void*)packed, SIZE_MAX);
+  TriAttnPacked<T> w = carve_triattn<T>(pc, CIN, CH, H);
+  const int Np = (int)round_up(N, 64);
+  Carve cv(ws, SIZE_MAX);
+  AttnWs<T> a = carve_attn_ws<T>(cv, B, Np, H, CH);
+  const int64_t ptiles = B * (int64_t)Np * (Np / 32);
+  triattn_prologue_kernel<T, CIN, H><<<(unsigned)((ptiles + 3) / 4), 256, 0, st>>>(
+      (const T*)x, w, a, (int)B, (int)N, Np, starting, eps);
+  GTK_LAUNCH_CHECK();
+  const int64_t blocks = B * N * ((N + 31) / 32);
+  GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "attention grid too large");
+  triattn_fused_kernel<T, CIN, H><<<(unsigned)blocks, 64 * H, 0, st>>>(
+      (const T*)x, mask, (T*)out, w, a, (int)B, (int)N, Np, starting, residual);
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+static bool triattn_shape_ok(int64_t cin, int64_t ch, int64_t H) {
+  return cin == 128 && H == 4 && ch == H * HD;
+}
+
+}  // namespace gtk
+
+using namespace gtk;
+
+extern "C" size_t gtk_triangle_attention_workspace_size(int64_t B, int64_t H, int64_t N, int64_t D,
+                                                        int dtype) {
+  if (B < 0 || H < 1 || N < 0 || D != HD) return 0;
+  Carve cv(nullptr, SIZE_MAX);
+  if (dtype == GTK_F32) carve_attn_ws<float>(cv, B, round_up(N, 64), (int)H, 0);
+  else carve_attn_ws<bf16>(cv, B, round_up(N, 64), (int)H, 0);
+  return cv.off;
+}
+
+extern "C" int gtk_triangle_attention_starting(const void* q, const void* k, const void* v,
+                                               const float* bias, const float* mask, float scale,
+                                               void* out, int64_t B, int64_t H, int64_t N,
+                                               int64_t D, int dtype, void* ws, size_t ws_bytes,
+                                               void* stream) {
+  return raw_attn_entry(q, k, v, bias, mask, scale, out, B, H, N, D, dtype, ws, ws_bytes, stream, 1);
+}
+
+extern "C" int gtk_triangle_attention_ending(const void* q, const void* k, const void* v,
+                                             const float* bias, const float* mask, float scale,
+                                             void* out, int64_t B, int64_t H, int64_t N, int64_t D,
+                                             int dtype, void* ws, size_t ws_bytes, void* stream) {
+  return raw_attn_entry(q, k, v, bias, mask, scale, out, B, H, N, D, dtype, ws, ws_bytes, stream, 0);
+}
+
+extern "C" size_t gtk_tri_attn_packed_size(int64_t c_in, int64_t c_h, int64_t H, int dtype) {
+  if (!triattn_shape_ok(c_in, c_h, H)) return 0;
+  Carve cv(nullptr, SIZE_MAX);
+  if (dtype == GTK_F32) carve_triattn<float>(cv, (int)c_in, (int)c_h, (int)H);
+  else carve_triattn<bf16>(cv, (int)c_in, (int)c_h, (int)H);
+  return cv.off;
+}
+
+extern "C" int gtk_tri_attn_pack(const gtk_tri_attn_weights* w, int64_t c_in, int64_t c_h,
+                                 int64_t H, int dtype, void* packed, size_t packed_bytes,
+                                 void* stream) {
+  GTK_REQUIRE(w && packed, GTK_EINVAL, "gtk_tri_attn_pack: null pointer");
+  GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL, "gtk_tri_attn_pack: bad dtype %d", dtype);
+  GTK_REQUIRE(w->dtype == GTK_F32 || w->dtype == GTK_BF16, GTK_EINVAL,
+              "gtk_tri_attn_pack: bad weight dtype %d", w->dtype);
+  GTK_REQUIRE(triattn_shape_ok(c_in, c_h, H), GTK_EUNSUPPORTED,
+              "gtk_tri_attn_pack: c_in=%lld c_h=%lld H=%lld unsupported (c_in=128, H=4, d=32)",
+              (long long)c_in, (long long)c_h, (long long)H);
+  GTK_REQUIRE(w->q_w && w->k_w && w->v_w && w->g_w && w->o_w && w->tri_w, GTK_EINVAL,
+              "gtk_tri_attn_pack: null weight");
+  const size_t need = gtk_tri_attn_packed_size(c_in, c_h, H, dtype);
+  GTK_REQUIRE(packed_bytes >= need, GTK_EWORKSPACE, "gtk_tri_attn_pack: buffer %zu < %zu bytes",
+              packed_bytes, need);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == GTK_F32) return pack_triattn<float>(w, (int)c_in, (int)c_h, (int)H, packed, st);
+  return pack_triattn<bf16>(w, (int)c_in, (int)c_h, (int)H, packed, st);
+}
+
+extern "C" size_t gtk_tri_attn_workspace_size(int64_t B, int64_t N, int64_t c_in, int64_t c_h,
+                                              int64_t H, int dtype) {
+  if (!triattn_shape_ok(c_in, c_h, H) || B < 0 || N < 0) return 0;
+  Carve cv(nullptr, SIZE_MAX);
+  if (dtype == GTK_F32) carve_attn_ws<float>(cv, B, round_up(N, 64), (int)H, (int)c_h);
+  else carve_attn_ws<bf16>(cv, B, round_up(N, 64), (int)H, (int)c_h);
+  return cv.off;
+}
+
+extern "C" int gtk_tri_attn_forward(const void* x, const float* mask, void* out, const void* packed,
+                                    int64_t B, int64_t N, int64_t c_in, int64_t c_h, int64_t H,
+                                    int starting, int residual, float eps, int dtype, void* ws,
+                                    size_t ws_bytes, void* stream) {
+  GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL, "gtk_tri_attn_forward: bad dtype %d", dtype);
+  GTK_REQUIRE(triattn_shape_ok(c_in, c_h, H), GTK_EUNSUPPORTED,
+              "gtk_tri_attn_forward: c_in=%lld c_h=%lld H=%lld unsupported (c_in=128, H=4, d=32)",
+              (long long)c_in, (long long)c_h, (long long)H);
+  GTK_REQUIRE(B >= 0 && N >= 0 && N <= 8192, GTK_EINVAL, "gtk_tri_attn_forward: bad shape");
+  if (B == 0 || N == 0) return GTK_OK;
+  GTK_REQUIRE(x && out && packed && ws, GTK_EINVAL, "gtk_tri_attn_forward: null pointer");
+  const size_t need = gtk_tri_attn_workspace_size(B, N, c_in, c_h, H, dtype);
+  GTK_REQUIRE(ws_bytes >= need, GTK_EWORKSPACE, "gtk_tri_attn_forward: workspace %zu < %zu bytes",
+              ws_bytes, need);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == GTK_F32) return fwd_triattn<float, 128, 4>(x, mask, out, packed, B, N, starting, residual, eps, ws, st);
+  return fwd_triattn<bf16, 128, 4>(x, mask, out, packed, B, N, starting, residual, eps, ws, st);
+}

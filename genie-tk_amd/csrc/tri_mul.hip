@@ -1,0 +1,579 @@
+// Triangle multiplicative update (outgoing / incoming) for gfx950.
+//
+// Three kernels, all reading/writing HBM in the layouts below:
+//
+//  1. prologue   z[B][N][N][c_z]  ->  A, Bm planes [B][c][Np][Np]
+//       LN_in in fragment layout, the four c_z->c projections on the matrix
+//       cores, sigmoid gates and the pair mask fused; results written
+//       channel-major so that the contraction reads both operands with k
+//       contiguous.  Outgoing stores pair (p,q) at plane[c][p][q], incoming at
+//       plane[c][q][p]; after that both directions are the same GEMM.
+//  2. contract   X[b][c] = A[b][c] . Bm[b][c]^T     (B*c GEMMs of Np x Np x Np)
+//       128x128 (or 64x64) tiles, 4 waves, k staged through LDS in 128-byte
+//       rows with double buffering, fp32 accumulation.
+//  3. epilogue   X planes + z  ->  out[B][N][N][c_z]
+//       X tile transposed through LDS into fragment layout, LN_out and W_z on
+//       the matrix cores, gate sigmoid(LN_in(z) W_g^T + b_g) recomputed from z
+//       (cheaper than storing it), optional residual add.
+//
+// Np = N rounded up to 64; the prologue writes zeros for padded pairs so the
+// contraction needs no bounds checks.
+#include "capi_util.hpp"
+#include "common.hpp"
+#include "pack.hpp"
+
+namespace gtk {
+
+// Packed parameters of one TriangleMultiplicativeUpdate, carved in this order.
+template <typename T> struct TriMulPacked {
+  T *w_ap, *w_ag, *w_bp, *w_bg, *w_g, *w_z;
+  float *ln_in_w, *ln_in_b, *b_ap, *b_ag, *b_bp, *b_bg, *b_g, *ln_out_w, *ln_out_b, *b_z;
+};
+
+template <typename T>
+static TriMulPacked<T> carve_trimul(Carve& cv, int cz, int c) {
+  TriMulPacked<T> p;
+  p.w_ap = cv.take<T>(packed_elems(c, cz));
+  p.w_ag = cv.take<T>(packed_elems(c, cz));
+  p.w_bp = cv.take<T>(packed_elems(c, cz));
+  p.w_bg = cv.take<T>(packed_elems(c, cz));
+  p.w_g = cv.take<T>(packed_elems(cz, cz));
+  p.w_z = cv.take<T>(packed_elems(cz, c));
+  p.ln_in_w = cv.take<float>(cz);
+  p.ln_in_b = cv.take<float>(cz);
+  p.b_ap = cv.take<float>(c);
+  p.b_ag = cv.take<float>(c);
+  p.b_bp = cv.take<float>(c);
+  p.b_bg = cv.take<float>(c);
+  p.b_g = cv.take<float>(cz);
+  p.ln_out_w = cv.take<float>(c);
+  p.ln_out_b = cv.take<float>(c);
+  p.b_z = cv.take<float>(cz);
+  return p;
+}
+
+// XCD-aware block order: hardware deals consecutive block ids to the 8 XCDs
+// round-robin; remap so that each XCD receives a contiguous range of logical
+// blocks (tiles of the same channel share that XCD's L2).
+__device__ __forceinline__ int64_t xcd_remap(int64_t lin, int64_t total) {
+  if (total % 8 != 0) return lin;
+  const int64_t per = total / 8;
+  return (lin % 8) * per + lin / 8;
+}
+
+// ---------------------------------------------------------------------------
+// 1. Prologue
+// ---------------------------------------------------------------------------
+template <typename T, int CZ, int CH>
+__global__ __launch_bounds__(256) void trimul_prologue_kernel(
+    const T* __restrict__ z, const float* __restrict__ mask, T* __restrict__ pa,
+    T* __restrict__ pb, TriMulPacked<T> w, int B, int N, int Np, int outgoing, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int half = lane >> 5;
+  const int t32 = lane & 31;
+  const int vtiles = Np / 32;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile >= (int64_t)B * Np * vtiles) return;
+  const int vt = (int)(tile % vtiles);
+  const int f = (int)((tile / vtiles) % Np);
+  const int b = (int)(tile / ((int64_t)vtiles * Np));
+  const int v = vt * 32 + t32;
+  const int p = outgoing ? f : v;
+  const int q = outgoing ? v : f;
+  const bool valid = (p < N) && (q < N);
+  const int64_t pair = ((int64_t)b * N + (valid ? p : 0)) * N + (valid ? q : 0);
+
+  RowHalf<CZ> rh;
+  load_row_half<T, CZ>(rh, z + pair * CZ, valid);
+  const f32x2 st = row_stats<CZ>(rh, eps);
+  Frag<T> xf[CZ / 16];
+  ln_to_frags<T, CZ>(xf, rh, st, w.ln_in_w, w.ln_in_b);
+  const float m = valid ? (mask ? mask[pair] : 1.0f) : 0.0f;
+
+  const int64_t plane = (int64_t)Np * Np;
+  const int64_t off_fv = (int64_t)f * Np + v;
+#pragma unroll 1
+  for (int side = 0; side < 2; ++side) {
+    const T* wp = side ? w.w_bp : w.w_ap;
+    const T* wg = side ? w.w_bg : w.w_ag;
+    const float* bp = side ? w.b_bp : w.b_ap;
+    const float* bg = side ? w.b_bg : w.b_ag;
+    T* dst = (side ? pb : pa) + (int64_t)b * CH * plane + off_fv;
+#pragma unroll 1
+    for (int nt = 0; nt < CH / 32; ++nt) {
+      const f32x16 ap = row_gemm_tile<T, CZ, true>(xf, wp, nt);
+      const f32x16 ag = row_gemm_tile<T, CZ, true>(xf, wg, nt);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int c = nt * 32 + 8 * g + 4 * half + r;
+          const float val = (ap[4 * g + r] + bp[c]) * sigmoidf_(ag[4 * g + r] + bg[c]) * m;
+          dst[(int64_t)c * plane] = cvt<T>(val);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2. Per-channel contraction  X = A . Bm^T   (A, Bm, X: [Np][Np] planes)
+// ---------------------------------------------------------------------------
+template <typename T, int TILE>
+__global__ __launch_bounds__(256) void trimul_contract_kernel(const T* __restrict__ pa,
+                                                              const T* __restrict__ pb,
+                                                              T* __restrict__ px, int Np,
+                                                              int64_t nplanes) {
+  constexpr int BK = 128 / sizeof(T);            // k elements per stage (128-byte rows)
+  constexpr int PITCH = 144;                     // LDS row pitch in bytes (16 B pad)
+  constexpr int WT = TILE / 2;                   // per-wave tile (2x2 waves)
+  constexpr int MB = WT / 32;                    // 32x32 MFMA blocks per wave side
+  constexpr int CHUNKS = TILE * 8;               // 16-byte chunks per operand per stage
+  constexpr int CPT = CHUNKS / 256;              // chunks per thread per operand
+  constexpr int EPC = 16 / sizeof(T);            // elements per 16-byte chunk
+  __shared__ __attribute__((aligned(16))) char smem[2][2][TILE * PITCH];
+
+  const int tiles_1d = Np / TILE;
+  const int64_t total = (int64_t)tiles_1d * tiles_1d * nplanes;
+  const int64_t lin = xcd_remap((int64_t)blockIdx.x, total);
+  const int64_t pl = lin / ((int64_t)tiles_1d * tiles_1d);
+  const int trem = (int)(lin % ((int64_t)tiles_1d * tiles_1d));
+  const int i0 = (trem / tiles_1d) * TILE;
+  const int j0 = (trem % tiles_1d) * TILE;
+  const int64_t plane = (int64_t)Np * Np;
+  const T* A = pa + pl * plane;
+  const T* Bm = pb + pl * plane;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wi = (wave >> 1) * WT;  // wave row offset (i)
+  const int wj = (wave & 1) * WT;   // wave col offset (j)
+
+  f32x16 acc[MB][MB];
+#pragma unroll
+  for (int x = 0; x < MB; ++x)
+#pragma unroll
+    for (int y = 0; y < MB; ++y) acc[x][y] = zero16();
+
+  f32x4 ra[CPT], rb[CPT];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+      const int id = tid + 256 * u;
+      const int row = id >> 3, cc = id & 7;
+      ra[u] = *reinterpret_cast<const f32x4*>(A + (int64_t)(i0 + row) * Np + k0 + cc * EPC);
+      rb[u] = *reinterpret_cast<const f32x4*>(Bm + (int64_t)(j0 + row) * Np + k0 + cc * EPC);
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+      const int id = tid + 256 * u;
+      const int row = id >> 3, cc = id & 7;
+      *reinterpret_cast<f32x4*>(&smem[buf][0][row * PITCH + cc * 16]) = ra[u];
+      *reinterpret_cast<f32x4*>(&smem[buf][1][row * PITCH + cc * 16]) = rb[u];
+    }
+  };
+
+  const int KT = Np / BK;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  const int half = lane >> 5;
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < KT) gload((kt + 1) * BK);
+#pragma unroll
+    for (int kc = 0; kc < BK / 16; ++kc) {
+      Frag<T> fa[MB], fb[MB];
+#pragma unroll
+      for (int x = 0; x < MB; ++x) {
+        const int ra_row = wi + x * 32 + (lane & 31);
+        const int rb_row = wj + x * 32 + (lane & 31);
+        const int koff = (kc * 16 + half * 8) * (int)sizeof(T);
+        fa[x].load(reinterpret_cast<const T*>(&smem[cur][0][ra_row * PITCH + koff]));
+        fb[x].load(reinterpret_cast<const T*>(&smem[cur][1][rb_row * PITCH + koff]));
+      }
+#pragma unroll
+      for (int x = 0; x < MB; ++x)
+#pragma unroll
+        for (int y = 0; y < MB; ++y) mma(acc[x][y], fb[y], fa[x]);  // rows j, cols i
+    }
+    if (kt + 1 < KT) sstore(cur ^ 1);
+    __syncthreads();
+  }
+
+  // acc[x][y]: lane holds X[i = wi + 32x + (l&31)][j = wj + 32y + 8g + 4h + r]
+  T* X = px + pl * plane;
+#pragma unroll
+  for (int x = 0; x < MB; ++x) {
+    const int i = i0 + wi + x * 32 + (lane & 31);
+#pragma unroll
+    for (int y = 0; y < MB; ++y) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int j = j0 + wj + y * 32 + 8 * g + 4 * half;
+        store4(X + (int64_t)i * Np + j, acc[x][y][4 * g + 0], acc[x][y][4 * g + 1],
+               acc[x][y][4 * g + 2], acc[x][y][4 * g + 3]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 3. Epilogue
+// ---------------------------------------------------------------------------
+template <typename T, int CZ, int CH>
+__global__ __launch_bounds__(256) void trimul_epilogue_kernel(
+    const T* __restrict__ z, const T* __restrict__ px, T* __restrict__ out, TriMulPacked<T> w,
+    int B, int N, int Np, int residual, float eps_in, float eps_out) {
+  constexpr int XPITCH = CH + 8;  // LDS row pitch (elements) of the transposed x tile
+  __shared__ __attribute__((aligned(16))) T xs[4][32 * XPITCH];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int half = lane >> 5;
+  const int t32 = lane & 31;
+  const int jtiles = (N + 31) / 32;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave;
+  if (tile >= (int64_t)B * N * jtiles) return;
+  const int jt = (int)(tile % jtiles);
+  const int i = (int)((tile / jtiles) % N);
+  const int b = (int)(tile / ((int64_t)jtiles * N));
+  const int j = jt * 32 + t32;
+  const bool valid = j < N;
+  const int64_t pair = ((int64_t)b * N + i) * N + (valid ? j : 0);
+
+  // Gate from z.
+  f32x16 gate[CZ / 32];
+  {
+    RowHalf<CZ> rh;
+    load_row_half<T, CZ>(rh, z + pair * CZ, valid);
+    const f32x2 st = row_stats<CZ>(rh, eps_in);
+    Frag<T> xf[CZ / 16];
+    ln_to_frags<T, CZ>(xf, rh, st, w.ln_in_w, w.ln_in_b);
+#pragma unroll
+    for (int nt = 0; nt < CZ / 32; ++nt) {
+      gate[nt] = row_gemm_tile<T, CZ, true>(xf, w.w_g, nt);
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int c = nt * 32 + 8 * g + 4 * half + r;
+          gate[nt][4 * g + r] = sigmoidf_(gate[nt][4 * g + r] + w.b_g[c]);
+        }
+    }
+  }
+
+  // Transpose the x tile X[b][c][i][jt*32 .. +32] through LDS into [j][c].
+  {
+    constexpr int EPC = 16 / sizeof(T);   // elements per 16-byte chunk
+    constexpr int CPR = 32 / EPC;         // chunks per c-row of 32 elements
+    constexpr int TOTAL = CH * CPR;
+    const int64_t plane = (int64_t)Np * Np;
+    const T* xb = px + (int64_t)b * CH * plane + (int64_t)i * Np + jt * 32;
+    T* s = xs[wave];
+#pragma unroll 4
+    for (int id = lane; id < TOTAL; id += 64) {
+      const int c = id / CPR, part = id % CPR;
+      const f32x4 raw = *reinterpret_cast<const f32x4*>(xb + (int64_t)c * plane + part * EPC);
+      const T* e = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+      for (int k = 0; k < EPC; ++k) s[(part * EPC + k) * XPITCH + c] = e[k];
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+
+  RowHalf<CH> xh;
+  {
+    const T* s = xs[wave] + t32 * XPITCH + half * (CH / 2);
+#pragma unroll
+    for (int ch = 0; ch < CH / 16; ++ch) {
+      Frag<T> f;
+      f.load(s + ch * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xh.v[ch * 8 + e] = f.get(e);
+    }
+  }
+  const f32x2 st = row_stats<CH>(xh, eps_out);
+  Frag<T> yf[CH / 16];
+  ln_to_frags<T, CH>(yf, xh, st, w.ln_out_w, w.ln_out_b);
+
+#pragma unroll
+  for (int nt = 0; nt < CZ / 32; ++nt) {
+    const f32x16 acc = row_gemm_tile<T, CH, true>(yf, w.w_z, nt);
+    if (valid) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c0 = nt * 32 + 8 * g + 4 * half;
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = (acc[4 * g + r] + w.b_z[c0 + r]) * gate[nt][4 * g + r];
+        if (residual) {
+          const f32x4 zr = load4f(z + pair * CZ + c0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[r] += zr[r];
+        }
+        store4(out + pair * CZ + c0, o[0], o[1], o[2], o[3]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Layout conversion for the raw contraction op:
+//   pairs [B][N][N][C]  <->  planes [B][C][Np][Np]
+// ---------------------------------------------------------------------------
+template <typename T>
+__global__ __launch_bounds__(256) void pairs_to_planes_kernel(const T* __restrict__ src,
+                                                              T* __restrict__ dst, int B, int N,
+                                                              int Np, int C, int outgoing) {
+  const int lane = threadIdx.x & 63;
+  const int half = lane >> 5;
+  const int vtiles = Np / 32;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile >= (int64_t)B * Np * vtiles) return;
+  const int vt = (int)(tile % vtiles);
+  const int f = (int)((tile / vtiles) % Np);
+  const int b = (int)(tile / ((int64_t)vtiles * Np));
+  const int v = vt * 32 + (lane & 31);
+  const int p = outgoing ? f : v, q = outgoing ? v : f;
+  const bool valid = p < N && q < N;
+  const T* s = src + (((int64_t)b * N + (valid ? p : 0)) * N + (valid ? q : 0)) * C;
+  const int64_t plane = (int64_t)Np * Np;
+  T* d = dst + (int64_t)b * C * plane + (int64_t)f * Np + v;
+  for (int c = half * (C / 2); c < (half + 1) * (C / 2); c += 8) {
+    Frag<T> fr;
+    if (valid) fr.load(s + c);
+    else fr.zero();
+#pragma unroll
+    for (int e = 0; e < 8; ++e) d[(int64_t)(c + e) * plane] = cvt<T>(fr.get(e));
+  }
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void planes_to_pairs_kernel(const T* __restrict__ src,
+                                                              T* __restrict__ dst, int B, int N,
+                                                              int Np, int C) {
+  const int lane = threadIdx.x & 63;
+  const int half = lane >> 5;
+  const int jtiles = (N + 31) / 32;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile >= (int64_t)B * N * jtiles) return;
+  const int jt = (int)(tile % jtiles);
+  const int i = (int)((tile / jtiles) % N);
+  const int b = (int)(tile / ((int64_t)jtiles * N));
+  const int j = jt * 32 + (lane & 31);
+  if (j >= N) return;
+  const int64_t plane = (int64_t)Np * Np;
+  const T* s = src + (int64_t)b * C * plane + (int64_t)i * Np + j;
+  T* d = dst + (((int64_t)b * N + i) * N + j) * C;
+  for (int c = half * (C / 2); c < (half + 1) * (C / 2); c += 8) {
+    float f8[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f8[e] = to_f32(s[(int64_t)(c + e) * plane]);
+    Frag<T> fr;
+    fr.set(f8);
+    if constexpr (sizeof(T) == 2) {
+      *reinterpret_cast<bf16x8*>(d + c) = fr.v;
+    } else {
+      *reinterpret_cast<f32x4*>(d + c) = fr.lo;
+      *reinterpret_cast<f32x4*>(d + c + 4) = fr.hi;
+    }
+  }
+}
+
+template <typename T>
+static int launch_contract(const T* pa, const T* pb, T* px, int Np, int64_t nplanes,
+                           hipStream_t st) {
+  if (Np % 128 == 0) {
+    const int64_t blocks = (int64_t)(Np / 128) * (Np / 128) * nplanes;
+    GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "contraction grid too large");
+    trimul_contract_kernel<T, 128><<<(unsigned)blocks, 256, 0, st>>>(pa, pb, px, Np, nplanes);
+  } else {
+    const int64_t blocks = (int64_t)(Np / 64) * (Np / 64) * nplanes;
+    GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "contraction grid too large");
+    trimul_contract_kernel<T, 64><<<(unsigned)blocks, 256, 0, st>>>(pa, pb, px, Np, nplanes);
+  }
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+static size_t plane_bytes(int64_t B, int64_t N, int64_t C, int dtype) {
+  const int64_t Np = round_up(N, 64);
+  return (size_t)(B * C * Np * Np) * dtype_size(dtype);
+}
+
+template <typename T>
+static int raw_contract(const void* a, const void* b, void* x, int64_t B, int64_t N, int64_t C,
+                        int outgoing, void* ws, hipStream_t st) {
+  const int Np = (int)round_up(N, 64);
+  Carve cv(ws, SIZE_MAX);
+  T* pa = cv.take<T>(B * C * (int64_t)Np * Np);
+  T* pb = cv.take<T>(B * C * (int64_t)Np * Np);
+  T* px = cv.take<T>(B * C * (int64_t)Np * Np);
+  const int64_t ptiles = B * (int64_t)Np * (Np / 32);
+  const unsigned pgrid = (unsigned)((ptiles + 3) / 4);
+  pairs_to_planes_kernel<T><<<pgrid, 256, 0, st>>>((const T*)a, pa, (int)B, (int)N, Np, (int)C, outgoing);
+  GTK_LAUNCH_CHECK();
+  pairs_to_planes_kernel<T><<<pgrid, 256, 0, st>>>((const T*)b, pb, (int)B, (int)N, Np, (int)C, outgoing);
+  GTK_LAUNCH_CHECK();
+  int rc = launch_contract<T>(pa, pb, px, Np, B * C, st);
+  if (rc) return rc;
+  const int64_t otiles = B * N * ((N + 31) / 32);
+  planes_to_pairs_kernel<T><<<(unsigned)((otiles + 3) / 4), 256, 0, st>>>(px, (T*)x, (int)B, (int)N, Np, (int)C);
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+static int raw_trimul(const void* a, const void* b, const float* mask, void* x, int64_t B,
+                      int64_t N, int64_t C, int dtype, void* ws, size_t ws_bytes, void* stream,
+                      int outgoing) {
+  (void)mask;
+  const char* name = outgoing ? "gtk_triangle_mul_outgoing" : "gtk_triangle_mul_incoming";
+  GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL, "%s: bad dtype %d", name, dtype);
+  GTK_REQUIRE(B >= 0 && N >= 0 && C >= 1, GTK_EINVAL, "%s: bad shape", name);
+  GTK_REQUIRE(C % 16 == 0, GTK_EUNSUPPORTED, "%s: C=%lld must be a multiple of 16", name, (long long)C);
+  GTK_REQUIRE(N <= 16384, GTK_EUNSUPPORTED, "%s: N=%lld too large", name, (long long)N);
+  if (B == 0 || N == 0) return GTK_OK;
+  GTK_REQUIRE(a && b && x && ws, GTK_EINVAL, "%s: null pointer", name);
+  const size_t need = gtk_triangle_mul_workspace_size(B, N, C, dtype);
+  GTK_REQUIRE(ws_bytes >= need, GTK_EWORKSPACE, "%s: workspace %zu < %zu bytes", name, ws_bytes, need);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == GTK_F32) return raw_contract<float>(a, b, x, B, N, C, outgoing, ws, st);
+  return raw_contract<bf16>(a, b, x, B, N, C, outgoing, ws, st);
+}
+
+// ---------------------------------------------------------------------------
+// Fused forward
+// ---------------------------------------------------------------------------
+template <typename T>
+static int pack_trimul(const gtk_tri_mul_weights* w, int cz, int c, void* packed, hipStream_t st) {
+  Carve cv(packed, SIZE_MAX);
+  TriMulPacked<T> p = carve_trimul<T>(cv, cz, c);
+  const int wd = w->dtype;
+  int rc = 0;
+  // nn.Linear weight [out][in]: s_out = in, s_in = 1.
+  if ((rc = launch_pack<T>(p.w_ap, w->a_p_w, wd, c, cz, cz, 1, 1.f, st))) return rc;
+  if ((rc = launch_pack<T>(p.w_ag, w->a_g_w, wd, c, cz, cz, 1, 1.f, st))) return rc;
+  if ((rc = launch_pack<T>(p.w_bp, w->b_p_w, wd, c, cz, cz, 1, 1.f, st))) return rc;
+  if ((rc = launch_pack<T>(p.w_bg, w->b_g_w, wd, c, cz, cz, 1, 1.f, st))) return rc;
+  if ((rc = launch_pack<T>(p.w_g, w->g_w, wd, cz, cz, cz, 1, 1.f, st))) return rc;
+  if ((rc = launch_pack<T>(p.w_z, w->z_w, wd, cz, c, c, 1, 1.f, st))) return rc;
+  if ((rc = launch_to_f32(p.ln_in_w, w->ln_in_w, wd, cz, 1.f, 1.f, st))) return rc;
+  if ((rc = launch_to_f32(p.ln_in_b, w->ln_in_b, wd, cz, 1.f, 0.f, st))) return rc;
+  if ((rc = launch_to_f32(p.b_ap, w->a_p_b, wd, c, 1.f, 0.f, st))) return rc;
+  if ((rc = launch_to_f32(p.b_ag, w->a_g_b, wd, c, 1.f, 0.f, st))) return rc;
+  if ((rc = launch_to_f32(p.b_bp, w->b_p_b, wd, c, 1.f, 0.f, st))) return rc;
+  if ((rc = launch_to_f32(p.b_bg, w->b_g_b, wd, c, 1.f, 0.f, st))) return rc;
+  if ((rc = launch_to_f32(p.b_g, w->g_b, wd, cz, 1.f, 0.f, st))) return rc;
+  if ((rc = launch_to_f32(p.ln_out_w, w->ln_out_w, wd, c, 1.f, 1.f, st))) return rc;
+  if ((rc = launch_to_f32(p.ln_out_b, w->ln_out_b, wd, c, 1.f, 0.f, st))) return rc;
+  if ((rc = launch_to_f32(p.b_z, w->z_b, wd, cz, 1.f, 0.f, st))) return rc;
+  return GTK_OK;
+}
+
+template <typename T, int CZ, int CH>
+static int fwd_trimul(const void* z, const float* mask, void* out, const void* packed, int64_t B,
+                      int64_t N, int outgoing, int residual, float eps_in, float eps_out, void* ws,
+                      hipStream_t st) {
+  Carve pc((void*)packed, SIZE_MAX);
+  TriMulPacked<T> w = carve_trimul<T>(pc, CZ, CH);
+  const int Np = (int)round_up(N, 64);
+  Carve cv(ws, SIZE_MAX);
+  T* pa = cv.take<T>(B * CH * (int64_t)Np * Np);
+  T* pb = cv.take<T>(B * CH * (int64_t)Np * Np);
+  T* px = cv.take<T>(B * CH * (int64_t)Np * Np);
+  const int64_t ptiles = B * (int64_t)Np * (Np / 32);
+  trimul_prologue_kernel<T, CZ, CH><<<(unsigned)((ptiles + 3) / 4), 256, 0, st>>>(
+      (const T*)z, mask, pa, pb, w, (int)B, (int)N, Np, outgoing, eps_in);
+  GTK_LAUNCH_CHECK();
+  int rc = launch_contract<T>(pa, pb, px, Np, B * CH, st);
+  if (rc) return rc;
+  const int64_t etiles = B * N * ((N + 31) / 32);
+  trimul_epilogue_kernel<T, CZ, CH><<<(unsigned)((etiles + 3) / 4), 256, 0, st>>>(
+      (const T*)z, px, (T*)out, w, (int)B, (int)N, Np, residual, eps_in, eps_out);
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+}  // namespace gtk
+
+using namespace gtk;
+
+extern "C" size_t gtk_triangle_mul_workspace_size(int64_t B, int64_t N, int64_t C, int dtype) {
+  if (B < 0 || N < 0 || C < 0) return 0;
+  return 3 * (plane_bytes(B, N, C, dtype) + 256);
+}
+
+extern "C" int gtk_triangle_mul_outgoing(const void* a, const void* b, const float* mask, void* x,
+                                         int64_t B, int64_t N, int64_t C, int dtype, void* ws,
+                                         size_t ws_bytes, void* stream) {
+  return raw_trimul(a, b, mask, x, B, N, C, dtype, ws, ws_bytes, stream, 1);
+}
+
+extern "C" int gtk_triangle_mul_incoming(const void* a, const void* b, const float* mask, void* x,
+                                         int64_t B, int64_t N, int64_t C, int dtype, void* ws,
+                                         size_t ws_bytes, void* stream) {
+  return raw_trimul(a, b, mask, x, B, N, C, dtype, ws, ws_bytes, stream, 0);
+}
+
+static bool trimul_shape_ok(int64_t cz, int64_t c) { return cz == 128 && (c == 64 || c == 128); }
+
+extern "C" size_t gtk_tri_mul_packed_size(int64_t c_z, int64_t c, int dtype) {
+  if (!trimul_shape_ok(c_z, c)) return 0;
+  Carve cv(nullptr, SIZE_MAX);
+  if (dtype == GTK_F32) carve_trimul<float>(cv, (int)c_z, (int)c);
+  else carve_trimul<bf16>(cv, (int)c_z, (int)c);
+  return cv.off;
+}
+
+extern "C" int gtk_tri_mul_pack(const gtk_tri_mul_weights* w, int64_t c_z, int64_t c, int dtype,
+                                void* packed, size_t packed_bytes, void* stream) {
+  GTK_REQUIRE(w && packed, GTK_EINVAL, "gtk_tri_mul_pack: null pointer");
+  GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL, "gtk_tri_mul_pack: bad dtype %d", dtype);
+  GTK_REQUIRE(w->dtype == GTK_F32 || w->dtype == GTK_BF16, GTK_EINVAL,
+              "gtk_tri_mul_pack: bad weight dtype %d", w->dtype);
+  GTK_REQUIRE(trimul_shape_ok(c_z, c), GTK_EUNSUPPORTED,
+              "gtk_tri_mul_pack: c_z=%lld c=%lld unsupported (c_z == 128, c in {64,128})",
+              (long long)c_z, (long long)c);
+  GTK_REQUIRE(w->a_p_w && w->a_g_w && w->b_p_w && w->b_g_w && w->g_w && w->z_w, GTK_EINVAL,
+              "gtk_tri_mul_pack: null weight");
+  const size_t need = gtk_tri_mul_packed_size(c_z, c, dtype);
+  GTK_REQUIRE(packed_bytes >= need, GTK_EWORKSPACE, "gtk_tri_mul_pack: buffer %zu < %zu bytes",
+              packed_bytes, need);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == GTK_F32) return pack_trimul<float>(w, (int)c_z, (int)c, packed, st);
+  return pack_trimul<bf16>(w, (int)c_z, (int)c, packed, st);
+}
+
+extern "C" size_t gtk_tri_mul_workspace_size(int64_t B, int64_t N, int64_t c_z, int64_t c, int dtype) {
+  (void)c_z;
+  if (B < 0 || N < 0 || c < 0) return 0;
+  return 3 * (plane_bytes(B, N, c, dtype) + 256);
+}
+
+extern "C" int gtk_tri_mul_forward(const void* z, const float* mask, void* out, const void* packed,
+                                   int64_t B, int64_t N, int64_t c_z, int64_t c, int outgoing,
+                                   int residual, float eps_in, float eps_out, int dtype, void* ws,
+                                   size_t ws_bytes, void* stream) {
+  GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL, "gtk_tri_mul_forward: bad dtype %d", dtype);
+  GTK_REQUIRE(trimul_shape_ok(c_z, c), GTK_EUNSUPPORTED,
+              "gtk_tri_mul_forward: c_z=%lld c=%lld unsupported (c_z == 128, c in {64,128})",
+              (long long)c_z, (long long)c);
+  GTK_REQUIRE(B >= 0 && N >= 0 && N <= 16384, GTK_EINVAL, "gtk_tri_mul_forward: bad shape B=%lld N=%lld",
+              (long long)B, (long long)N);
+  if (B == 0 || N == 0) return GTK_OK;
+  GTK_REQUIRE(z && out && packed && ws, GTK_EINVAL, "gtk_tri_mul_forward: null pointer");
+  const size_t need = gtk_tri_mul_workspace_size(B, N, c_z, c, dtype);
+  GTK_REQUIRE(ws_bytes >= need, GTK_EWORKSPACE, "gtk_tri_mul_forward: workspace %zu < %zu bytes",
+              ws_bytes, need);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == GTK_F32) {
+    if (c == 128) return fwd_trimul<float, 128, 128>(z, mask, out, packed, B, N, outgoing, residual, eps_in, eps_out, ws, st);
+    return fwd_trimul<float, 128, 64>(z, mask, out, packed, B, N, outgoing, residual, eps_in, eps_out, ws, st);
+  }
+  if (c == 128) return fwd_trimul<bf16, 128, 128>(z, mask, out, packed, B, N, outgoing, residual, eps_in, eps_out, ws, st);
+  return fwd_trimul<bf16, 128, 64>(z, mask, out, packed, B, N, outgoing, residual, eps_in, eps_out, ws, st);
+}

@@ -1,0 +1,63 @@
+"""Shared plumbing of the modules' kernel path: capability checks, the packed
+weight cache and the autograd rule.
+
+The HIP kernels are forward-only.  A call that must produce gradients
+(autograd enabled and the input or a parameter requires grad) runs the
+module's PyTorch path, which is autograd-capable; every other call on a GPU
+tensor with ``use_fused_kernel=True`` runs the HIP kernels.
+"""
+from __future__ import annotations
+
+import warnings
+from typing import Callable, List, Optional, Tuple
+
+import torch
+from torch import Tensor, nn
+
+SUPPORTED_DTYPES = (torch.float32, torch.bfloat16)
+
+_warned: set = set()
+
+
+def needs_autograd(x: Tensor, module: nn.Module) -> bool:
+    if not torch.is_grad_enabled():
+        return False
+    return x.requires_grad or any(p.requires_grad for p in module.parameters())
+
+
+def warn_once(key: str, msg: str) -> None:
+    if key not in _warned:
+        _warned.add(key)
+        warnings.warn(msg, stacklevel=3)
+
+
+class PackedWeights:
+    """Device copy of a module's parameters in the kernels' fragment order.
+
+    Rebuilt when any parameter is replaced, modified in place (tensor version
+    counter), moved, or when the compute precision changes.
+    """
+
+    def __init__(self) -> None:
+        self._key: Optional[Tuple] = None
+        self._packed: Optional[Tensor] = None
+
+    def get(self, params: List[Optional[Tensor]], fp32: bool,
+            pack: Callable[[List[Optional[Tensor]], bool], Tensor]) -> Tensor:
+        key = (fp32,) + tuple(
+            (None if p is None else (p.data_ptr(), p._version, p.dtype, p.device)) for p in params)
+        if key != self._key or self._packed is None:
+            with torch.no_grad():
+                self._packed = pack([None if p is None else p.detach() for p in params], fp32)
+            self._key = key
+        return self._packed
+
+
+def flatten_batch(x: Tensor, mask: Optional[Tensor]) -> Tuple[Tensor, Optional[Tensor], Tuple]:
+    """[*, N, N, C] -> [B, N, N, C] (and the mask likewise); returns the leading shape."""
+    lead = tuple(x.shape[:-3])
+    n, c = x.shape[-2], x.shape[-1]
+    xb = x.reshape(-1, n, n, c)
+    mb = None if mask is None else mask.expand(*lead, n, n).reshape(-1, n, n)
+    return xb, mb, lead
+

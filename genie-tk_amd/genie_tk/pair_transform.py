@@ -1,0 +1,127 @@
+"""Pair transform stack: the caller of the triangle operators.
+
+API of ``src/genie_tk/pair_transform.py`` in the reference (DropoutRowwise
+:26-42, DropoutColumnwise :45-61, PairTransition :64-84, PairTransformLayer
+:87-195, PairTransformNet :198-258).  Update order per layer (:180-193):
+tri-mul out, tri-mul in, tri-attn start, tri-attn end (each added to p with
+row/column-shared dropout), pair transition, then p * mask.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch.nn as nn
+from torch import Tensor
+
+from genie_tk.primitives import Linear
+from genie_tk.triangle_attention import TriangleAttentionEndingNode, TriangleAttentionStartingNode
+from genie_tk.triangle_mul import TriangleMultiplicationIncoming, TriangleMultiplicationOutgoing
+
+
+class _SharedDropout(nn.Module):
+    """Dropout whose mask is shared along one spatial axis of [*, L, L, C]."""
+
+    def __init__(self, p: float, shared_dim: int):
+        super().__init__()
+        self.p = p
+        self.dropout = nn.Dropout(p)
+        self._shared_dim = shared_dim
+
+    def forward(self, x: Tensor) -> Tensor:
+        if not self.training or self.p == 0:
+            return x
+        shape = list(x.shape)
+        shape[self._shared_dim] = 1
+        return x * self.dropout(x.new_ones(shape))
+
+
+class DropoutRowwise(_SharedDropout):
+    """Same dropout mask for every row (broadcast over dim -3)."""
+
+    def __init__(self, p: float):
+        super().__init__(p, -3)
+
+
+class DropoutColumnwise(_SharedDropout):
+    """Same dropout mask for every column (broadcast over dim -2)."""
+
+    def __init__(self, p: float):
+        super().__init__(p, -2)
+
+
+class PairTransition(nn.Module):
+    """LN -> Linear(c_p, n*c_p) -> ReLU -> Linear(n*c_p, c_p) (final init)."""
+
+    def __init__(self, c_p: int, n: int = 4):
+        super().__init__()
+        self.c_p = c_p
+        self.n = n
+        self.layer_norm = nn.LayerNorm(c_p)
+        self.linear_1 = Linear(c_p, c_p * n)
+        self.relu = nn.ReLU()
+        self.linear_2 = Linear(c_p * n, c_p, init="final")
+
+    def forward(self, p: Tensor, mask: Optional[Tensor] = None) -> Tensor:
+        return self.linear_2(self.relu(self.linear_1(self.layer_norm(p))))
+
+
+class PairTransformLayer(nn.Module):
+    """One pair-stack block; forward((p, p_mask)) -> (p, p_mask)."""
+
+    def __init__(self, c_p: int, include_mul_update: bool = True, include_tri_att: bool = True,
+                 c_hidden_mul: int = 128, c_hidden_tri_att: int = 32, n_head_tri: int = 4,
+                 tri_dropout: float = 0.25, pair_transition_n: int = 4,
+                 use_fused_kernel: bool = True):
+        super().__init__()
+        self.include_mul_update = include_mul_update
+        self.include_tri_att = include_tri_att
+        if include_mul_update:
+            self.tri_mul_out = TriangleMultiplicationOutgoing(
+                c_z=c_p, c_hidden=c_hidden_mul, use_fused_kernel=use_fused_kernel)
+            self.tri_mul_in = TriangleMultiplicationIncoming(
+                c_z=c_p, c_hidden=c_hidden_mul, use_fused_kernel=use_fused_kernel)
+        if include_tri_att:
+            self.tri_att_start = TriangleAttentionStartingNode(
+                c_in=c_p, c_hidden=c_hidden_tri_att, no_heads=n_head_tri,
+                use_fused_kernel=use_fused_kernel)
+            self.tri_att_end = TriangleAttentionEndingNode(
+                c_in=c_p, c_hidden=c_hidden_tri_att, no_heads=n_head_tri,
+                use_fused_kernel=use_fused_kernel)
+        self.pair_transition = PairTransition(c_p, pair_transition_n)
+        self.dropout_row = DropoutRowwise(tri_dropout)
+        self.dropout_col = DropoutColumnwise(tri_dropout)
+
+    def forward(self, inputs: Tuple[Tensor, Tensor]) -> Tuple[Tensor, Tensor]:
+        p, p_mask = inputs
+        if self.include_mul_update:
+            p = p + self.dropout_row(self.tri_mul_out(p, p_mask))
+            p = p + self.dropout_row(self.tri_mul_in(p, p_mask))
+        if self.include_tri_att:
+            p = p + self.dropout_row(self.tri_att_start(p, p_mask))
+            p = p + self.dropout_col(self.tri_att_end(p, p_mask))
+        p = p + self.pair_transition(p, p_mask)
+        p = p * p_mask.unsqueeze(-1)
+        return p, p_mask
+
+
+class PairTransformNet(nn.Module):
+    """``n_layers`` PairTransformLayers applied in sequence."""
+
+    def __init__(self, c_p: int, n_layers: int, include_mul_update: bool = True,
+                 include_tri_att: bool = True, c_hidden_mul: int = 128,
+                 c_hidden_tri_att: int = 32, n_head_tri: int = 4, tri_dropout: float = 0.25,
+                 pair_transition_n: int = 4, use_fused_kernel: bool = True):
+        super().__init__()
+        self.layers = nn.ModuleList([
+            PairTransformLayer(c_p=c_p, include_mul_update=include_mul_update,
+                               include_tri_att=include_tri_att, c_hidden_mul=c_hidden_mul,
+                               c_hidden_tri_att=c_hidden_tri_att, n_head_tri=n_head_tri,
+                               tri_dropout=tri_dropout, pair_transition_n=pair_transition_n,
+                               use_fused_kernel=use_fused_kernel)
+            for _ in range(n_layers)
+        ])
+
+    def forward(self, p: Tensor, p_mask: Tensor) -> Tensor:
+        for layer in self.layers:
+            p, p_mask = layer((p, p_mask))
+        return p

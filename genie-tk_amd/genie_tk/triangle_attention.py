@@ -1,0 +1,125 @@
+"""Triangle attention (AlphaFold2 Algorithms 13 and 14).
+
+Drop-in for ``src/genie_tk/triangle_attention.py`` of the reference: same
+classes, constructor arguments, parameter names and ``forward(x, mask=None)``
+returning the update (no residual).
+
+Kernel path (``use_fused_kernel=True``, GPU tensor, no autograd needed):
+``genie_tk._C.tri_attn_forward`` — a gfx950 prologue (LN, q/k/v/gate and
+triangle-bias projections on the matrix cores) and a flash-style kernel
+(online softmax, bias streamed from HBM, gate and output projection fused).
+PyTorch path: ``_forward_pytorch``, the reference fallback semantics
+(triangle_attention.py:100-143).
+
+Mask semantics of the kernel path: keys with mask == 0 get zero weight; a row
+without any valid key attends uniformly over all keys, which is what the
+PyTorch path produces with the default ``inf=1e9`` (every logit rounds to
+-1e9 in fp32 while |logit| < 32).
+"""
+from __future__ import annotations
+
+from functools import partialmethod
+from typing import Optional
+
+import torch
+import torch.nn as nn
+from torch import Tensor
+
+from genie_tk import _dispatch, _ext
+from genie_tk.primitives import Attention, Linear
+from genie_tk.utils import has_cuda_kernels, permute_final_dims
+
+_CUDA_AVAILABLE = has_cuda_kernels()
+
+
+class TriangleAttention(nn.Module):
+    """Row-wise (starting) or column-wise (ending) gated attention with a
+    triangle bias tri[h, q, k] = linear(LN(x))[q, k, h] shared by every row."""
+
+    def __init__(self, c_in: int, c_hidden: int, no_heads: int, starting: bool = True,
+                 inf: float = 1e9, use_fused_kernel: bool = True):
+        super().__init__()
+        self.c_in = c_in
+        self.c_hidden = c_hidden
+        self.no_heads = no_heads
+        self.starting = starting
+        self.inf = inf
+        self._fused_requested = use_fused_kernel
+        self.use_fused_kernel = use_fused_kernel and _CUDA_AVAILABLE
+        self.layer_norm = nn.LayerNorm(c_in)
+        self.linear = Linear(c_in, no_heads, bias=False, init="normal")
+        self.mha = Attention(c_q=c_in, c_k=c_in, c_v=c_in, c_hidden=c_hidden, no_heads=no_heads)
+        self._packed = _dispatch.PackedWeights()
+
+    # -- reference fallback -------------------------------------------------
+    def _compute_triangle_bias(self, x: Tensor) -> Tensor:
+        """[*, I, J, C] normalised input -> [*, H, I, J]."""
+        return permute_final_dims(self.linear(x), 2, 0, 1)
+
+    def _forward_pytorch(self, x: Tensor, mask: Optional[Tensor] = None) -> Tensor:
+        if mask is None:
+            mask = x.new_ones(x.shape[:-1])
+        if not self.starting:
+            x = x.transpose(-2, -3)
+            mask = mask.transpose(-1, -2)
+        x = self.layer_norm(x)
+        # [*, I, 1, 1, J]: added to the scores of every head and query of row I
+        mask_bias = (self.inf * (mask - 1))[..., :, None, None, :]
+        # [*, 1, H, Q, K]: the same triangle bias for every row
+        tri = self._compute_triangle_bias(x).unsqueeze(-4)
+        x = self.mha(q_x=x, k_x=x, v_x=x, biases=[mask_bias, tri])
+        if not self.starting:
+            x = x.transpose(-2, -3)
+        return x
+
+    # -- HIP kernel path ----------------------------------------------------
+    def _kernel_supported(self, x: Tensor) -> bool:
+        return (x.dim() >= 3 and x.shape[-2] == x.shape[-3] and x.shape[-1] == self.c_in
+                and self.c_in == 128 and self.no_heads == 4 and self.c_hidden == 128
+                and self.mha.gating and x.dtype in _dispatch.SUPPORTED_DTYPES
+                and self.layer_norm.elementwise_affine)
+
+    def _pack(self, params, fp32: bool) -> Tensor:
+        return _ext.require().tri_attn_pack(params, self.c_in, self.c_hidden, self.no_heads, fp32)
+
+    def _packed_params(self, fp32: bool) -> Tensor:
+        m = self.mha
+        ps = [self.layer_norm.weight, self.layer_norm.bias, self.linear.weight,
+              m.linear_q.weight, m.linear_k.weight, m.linear_v.weight,
+              m.linear_g.weight, m.linear_g.bias, m.linear_o.weight, m.linear_o.bias]
+        return self._packed.get(ps, fp32, self._pack)
+
+    def _forward_cuda(self, x: Tensor, mask: Optional[Tensor] = None,
+                      residual: bool = False) -> Tensor:
+        """HIP path; returns the update (plus x when ``residual``)."""
+        C = _ext.require()
+        xb, mb, lead = _dispatch.flatten_batch(x, mask)
+        packed = self._packed_params(x.dtype == torch.float32)
+        out = C.tri_attn_forward(xb, mb, packed, self.c_in, self.c_hidden, self.no_heads,
+                                 self.starting, residual, self.layer_norm.eps)
+        return out.reshape(*lead, *out.shape[1:])
+
+    def forward(self, x: Tensor, mask: Optional[Tensor] = None) -> Tensor:
+        """x: [*, N, N, c_in], mask: [*, N, N] -> update [*, N, N, c_in]."""
+        if x.is_cuda and self._fused_requested:
+            if not _CUDA_AVAILABLE:
+                _ext.require()
+            if self.use_fused_kernel and self._kernel_supported(x):
+                if not _dispatch.needs_autograd(x, self):
+                    return self._forward_cuda(x, mask)
+                _dispatch.warn_once("tri_attn_grad", "genie_tk: gradients requested; "
+                                    "TriangleAttention runs its PyTorch path "
+                                    "(the HIP kernels are forward-only)")
+        return self._forward_pytorch(x, mask)
+
+
+class TriangleAttentionStartingNode(TriangleAttention):
+    """Algorithm 13: attention along j within each row i."""
+
+    __init__ = partialmethod(TriangleAttention.__init__, starting=True)
+
+
+class TriangleAttentionEndingNode(TriangleAttention):
+    """Algorithm 14: attention along i within each column j."""
+
+    __init__ = partialmethod(TriangleAttention.__init__, starting=False)

@@ -1,0 +1,133 @@
+"""Triangle multiplicative update (AlphaFold2 Algorithms 11 and 12).
+
+Drop-in for ``src/genie_tk/triangle_mul.py`` of the reference: same classes,
+constructor arguments, parameter names (state_dict keys) and ``forward(z,
+mask=None)`` returning the update (no residual).
+
+Kernel path (``use_fused_kernel=True``, GPU tensor, no autograd needed):
+``genie_tk._C.tri_mul_forward``, three gfx950 kernels (prologue
+LN + gated projections + mask, matrix-core contraction per channel, epilogue
+LN + output projection + gate).  PyTorch path: ``_forward_pytorch``, the
+reference fallback semantics (triangle_mul.py:103-132).
+"""
+from __future__ import annotations
+
+from functools import partialmethod
+from typing import Optional
+
+import torch
+import torch.nn as nn
+from torch import Tensor
+
+from genie_tk import _dispatch, _ext
+from genie_tk.primitives import Linear
+from genie_tk.utils import has_cuda_kernels, permute_final_dims
+
+_CUDA_AVAILABLE = has_cuda_kernels()
+
+
+class TriangleMultiplicativeUpdate(nn.Module):
+    """Triangle multiplicative update over a pair representation ``z [*, N, N, c_z]``.
+
+    outgoing: x[i,j,c] = sum_k a[i,k,c] b[j,k,c];  incoming: x[i,j,c] = sum_k a[k,i,c] b[k,j,c]
+    with a, b the sigmoid-gated, masked projections of LN_in(z); the result is
+    LN_out(x) -> linear_z, gated by sigmoid(linear_g(LN_in(z))).
+    """
+
+    def __init__(self, c_z: int, c_hidden: int, _outgoing: bool = True,
+                 use_fused_kernel: bool = True):
+        super().__init__()
+        self.c_z = c_z
+        self.c_hidden = c_hidden
+        self._outgoing = _outgoing
+        self._fused_requested = use_fused_kernel
+        self.use_fused_kernel = use_fused_kernel and _CUDA_AVAILABLE
+
+        self.linear_a_p = Linear(c_z, c_hidden)
+        self.linear_a_g = Linear(c_z, c_hidden, init="gating")
+        self.linear_b_p = Linear(c_z, c_hidden)
+        self.linear_b_g = Linear(c_z, c_hidden, init="gating")
+        self.linear_g = Linear(c_z, c_z, init="gating")
+        self.linear_z = Linear(c_hidden, c_z, init="final")
+        self.layer_norm_in = nn.LayerNorm(c_z)
+        self.layer_norm_out = nn.LayerNorm(c_hidden)
+        self.sigmoid = nn.Sigmoid()
+        self._packed = _dispatch.PackedWeights()
+
+    # -- reference fallback -------------------------------------------------
+    def _outgoing_matmul(self, a: Tensor, b: Tensor) -> Tensor:
+        """x[*, i, j, c] = sum_k a[*, i, k, c] b[*, j, k, c] as a batched [c] matmul."""
+        x = torch.matmul(permute_final_dims(a, 2, 0, 1), permute_final_dims(b, 2, 1, 0))
+        return permute_final_dims(x, 1, 2, 0)
+
+    def _incoming_matmul(self, a: Tensor, b: Tensor) -> Tensor:
+        """x[*, i, j, c] = sum_k a[*, k, i, c] b[*, k, j, c] as a batched [c] matmul."""
+        x = torch.matmul(permute_final_dims(a, 2, 1, 0), permute_final_dims(b, 2, 0, 1))
+        return permute_final_dims(x, 1, 2, 0)
+
+    def _forward_pytorch(self, z: Tensor, mask: Optional[Tensor] = None) -> Tensor:
+        if mask is None:
+            mask = z.new_ones(z.shape[:-1])
+        m = mask.unsqueeze(-1)
+        zn = self.layer_norm_in(z)
+        a = self.linear_a_p(zn) * self.sigmoid(self.linear_a_g(zn)) * m
+        b = self.linear_b_p(zn) * self.sigmoid(self.linear_b_g(zn)) * m
+        x = self._outgoing_matmul(a, b) if self._outgoing else self._incoming_matmul(a, b)
+        x = self.linear_z(self.layer_norm_out(x))
+        return x * self.sigmoid(self.linear_g(zn))
+
+    # -- HIP kernel path ----------------------------------------------------
+    def _kernel_supported(self, z: Tensor) -> bool:
+        return (z.dim() >= 3 and z.shape[-2] == z.shape[-3] and z.shape[-1] == self.c_z
+                and self.c_z == 128 and self.c_hidden in (64, 128)
+                and z.dtype in _dispatch.SUPPORTED_DTYPES
+                and self.layer_norm_in.elementwise_affine and self.layer_norm_out.elementwise_affine)
+
+    def _pack(self, params, fp32: bool) -> Tensor:
+        return _ext.require().tri_mul_pack(params, self.c_z, self.c_hidden, fp32)
+
+    def _packed_params(self, fp32: bool) -> Tensor:
+        ps = [self.layer_norm_in.weight, self.layer_norm_in.bias,
+              self.linear_a_p.weight, self.linear_a_p.bias,
+              self.linear_a_g.weight, self.linear_a_g.bias,
+              self.linear_b_p.weight, self.linear_b_p.bias,
+              self.linear_b_g.weight, self.linear_b_g.bias,
+              self.linear_g.weight, self.linear_g.bias,
+              self.layer_norm_out.weight, self.layer_norm_out.bias,
+              self.linear_z.weight, self.linear_z.bias]
+        return self._packed.get(ps, fp32, self._pack)
+
+    def _forward_cuda(self, z: Tensor, mask: Optional[Tensor] = None,
+                      residual: bool = False) -> Tensor:
+        """HIP path; returns the update (plus z when ``residual``)."""
+        C = _ext.require()
+        zb, mb, lead = _dispatch.flatten_batch(z, mask)
+        packed = self._packed_params(z.dtype == torch.float32)
+        out = C.tri_mul_forward(zb, mb, packed, self.c_z, self.c_hidden, self._outgoing,
+                                residual, self.layer_norm_in.eps, self.layer_norm_out.eps)
+        return out.reshape(*lead, *out.shape[1:])
+
+    def forward(self, z: Tensor, mask: Optional[Tensor] = None) -> Tensor:
+        """z: [*, N, N, c_z], mask: [*, N, N] -> update [*, N, N, c_z]."""
+        if z.is_cuda and self._fused_requested:
+            if not _CUDA_AVAILABLE:
+                _ext.require()
+            if self.use_fused_kernel and self._kernel_supported(z):
+                if not _dispatch.needs_autograd(z, self):
+                    return self._forward_cuda(z, mask)
+                _dispatch.warn_once("tri_mul_grad", "genie_tk: gradients requested; "
+                                    "TriangleMultiplicativeUpdate runs its PyTorch path "
+                                    "(the HIP kernels are forward-only)")
+        return self._forward_pytorch(z, mask)
+
+
+class TriangleMultiplicationOutgoing(TriangleMultiplicativeUpdate):
+    """Algorithm 11: x[i,j] = sum_k a[i,k] * b[j,k]."""
+
+    __init__ = partialmethod(TriangleMultiplicativeUpdate.__init__, _outgoing=True)
+
+
+class TriangleMultiplicationIncoming(TriangleMultiplicativeUpdate):
+    """Algorithm 12: x[i,j] = sum_k a[k,i] * b[k,j]."""
+
+    __init__ = partialmethod(TriangleMultiplicativeUpdate.__init__, _outgoing=False)

@@ -1,0 +1,186 @@
+/*
+ * genie_tk.h — C ABI of the MI355X (gfx950) pair-stack kernels.
+ *
+ * Every function takes device pointers, plain sizes and a HIP stream passed
+ * as `void*` (a hipStream_t; NULL means the legacy default stream).  No
+ * function allocates device memory: scratch space is passed in by the caller
+ * as (workspace, workspace_bytes), sized with the matching *_workspace_size()
+ * query.  Every function enqueues work on `stream` and returns without
+ * synchronising.  Return value: GTK_OK (0) or a GTK_E* code; the message of
+ * the last failure on the calling thread is returned by gtk_last_error().
+ *
+ * Element types: GTK_F32 (float) and GTK_BF16 (bfloat16, round-to-nearest-even
+ * on every conversion).  bf16 inputs are contracted on the bf16 matrix cores
+ * with fp32 accumulation; fp32 inputs use the fp32 matrix cores.
+ *
+ * Layouts (row-major, innermost last):
+ *   pair tensor z / x        [B][N][N][C]
+ *   pair mask                [B][N][N]   float, 1 = valid, 0 = masked
+ *   nn.Linear weight         [out][in]
+ *
+ * The reference interface each entry point replaces is cited as
+ * path:line in the upstream Genie-TK repository.
+ */
+#ifndef GENIE_TK_H_
+#define GENIE_TK_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum gtk_dtype { GTK_F32 = 0, GTK_BF16 = 1 };
+
+enum gtk_status {
+  GTK_OK = 0,
+  GTK_EINVAL = 1,       /* bad pointer, size or dtype */
+  GTK_EUNSUPPORTED = 2, /* a shape the kernels are not built for */
+  GTK_EWORKSPACE = 3,   /* workspace / packed buffer too small */
+  GTK_EHIP = 4          /* a HIP runtime call or launch failed */
+};
+
+/* Message of the last error on this thread ("" if none). */
+const char* gtk_last_error(void);
+/* Library version: major*10000 + minor*100 + patch. */
+int gtk_version(void);
+
+/* ------------------------------------------------------------------------
+ * LayerNorm over the last dimension.
+ * Replaces _C.layernorm(x, gamma, beta, eps)
+ *   kernels/bindings.cpp:93-95 -> kernels/fused_layernorm/layernorm.cu:17-44.
+ * y = (x - mean) / sqrt(var_biased + eps) * gamma + beta, per row of d.
+ * x, y: [rows][d] of `dtype`; gamma, beta: [d] float.  y may not alias x.
+ * ------------------------------------------------------------------------ */
+int gtk_layernorm(const void* x, void* y, const float* gamma, const float* beta, int64_t rows,
+                  int64_t d, float eps, int dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * LayerNorm followed by a linear map.
+ * Replaces _C.fused_layernorm_linear(x, gamma, beta, weight, bias, eps)
+ *   kernels/bindings.cpp:97-100 -> kernels/fused_layernorm/layernorm.cu:46-79.
+ * y[r][o] = sum_k LN(x)[r][k] * weight[k][o] + bias[o]
+ * weight: [d_in][d_out] (in x out, as the reference) of `weight_dtype`;
+ * bias: [d_out] float or NULL.  d_in in {64, 128, 256}; any d_out >= 1.
+ * ------------------------------------------------------------------------ */
+size_t gtk_fused_layernorm_linear_workspace_size(int64_t d_in, int64_t d_out, int dtype);
+int gtk_fused_layernorm_linear(const void* x, void* y, const float* gamma, const float* beta,
+                               const void* weight, int weight_dtype, const float* bias,
+                               int64_t rows, int64_t d_in, int64_t d_out, float eps, int dtype,
+                               void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Triangle contraction on already gated and masked projections.
+ * Replaces _C.triangle_mul_outgoing / _C.triangle_mul_incoming(a, b, mask)
+ *   kernels/bindings.cpp:73-79 (declared at :16-26); caller
+ *   src/genie_tk/triangle_mul.py:151-159.
+ * outgoing: x[b][i][j][c] = sum_k a[b][i][k][c] * b[b][j][k][c]
+ * incoming: x[b][i][j][c] = sum_k a[b][k][i][c] * b[b][k][j][c]
+ * a, b, x: [B][N][N][C] of `dtype`.  `mask` ([B][N][N] float) is accepted for
+ * signature compatibility and not read: a and b arrive masked.
+ * C % 8 == 0.
+ * ------------------------------------------------------------------------ */
+size_t gtk_triangle_mul_workspace_size(int64_t B, int64_t N, int64_t C, int dtype);
+int gtk_triangle_mul_outgoing(const void* a, const void* b, const float* mask, void* x, int64_t B,
+                              int64_t N, int64_t C, int dtype, void* workspace,
+                              size_t workspace_bytes, void* stream);
+int gtk_triangle_mul_incoming(const void* a, const void* b, const float* mask, void* x, int64_t B,
+                              int64_t N, int64_t C, int dtype, void* workspace,
+                              size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Triangle attention core on projected q, k, v.
+ * Replaces _C.triangle_attention_starting / _ending(q, k, v, bias, mask, scale)
+ *   kernels/bindings.cpp:82-90 (declared at :29-47).
+ * q, k, v: [B][H][N][N][D] of `dtype`; bias: [B][H][N][N] float; mask:
+ * [B][N][N] float; out: [B][N][N][H*D] of `dtype`.
+ * starting (attention along the second spatial axis, rows i independent):
+ *   out[b][i][q][h*D+d] = sum_k softmax_k(scale*<q[b,h,i,q], k[b,h,i,k]>
+ *                              + mask_bias[b,i,k] + bias[b,h,q,k]) * v[b,h,i,k,d]
+ * ending (attention along the first spatial axis, columns j independent):
+ *   out[b][q][j][h*D+d] = sum_k softmax_k(scale*<q[b,h,q,j], k[b,h,k,j]>
+ *                              + mask_bias[b,k,j] + bias[b,h,q,k]) * v[b,h,k,j,d]
+ * mask_bias is -inf for mask == 0 keys; a row with no valid key attends
+ * uniformly over all N keys (the limit of the reference's -1e9 additive
+ * bias).  D == 32.
+ * ------------------------------------------------------------------------ */
+size_t gtk_triangle_attention_workspace_size(int64_t B, int64_t H, int64_t N, int64_t D, int dtype);
+int gtk_triangle_attention_starting(const void* q, const void* k, const void* v, const float* bias,
+                                    const float* mask, float scale, void* out, int64_t B,
+                                    int64_t H, int64_t N, int64_t D, int dtype, void* workspace,
+                                    size_t workspace_bytes, void* stream);
+int gtk_triangle_attention_ending(const void* q, const void* k, const void* v, const float* bias,
+                                  const float* mask, float scale, void* out, int64_t B, int64_t H,
+                                  int64_t N, int64_t D, int dtype, void* workspace,
+                                  size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused TriangleMultiplicativeUpdate forward (outgoing / incoming).
+ * Replaces TriangleMultiplicativeUpdate._forward_cuda
+ *   src/genie_tk/triangle_mul.py:134-169 (semantics of _forward_pytorch :103-132):
+ *   zn  = LN_in(z)
+ *   a   = (zn W_ap^T + b_ap) * sigmoid(zn W_ag^T + b_ag) * mask
+ *   b   = (zn W_bp^T + b_bp) * sigmoid(zn W_bg^T + b_bg) * mask
+ *   x   = outgoing ? einsum(bikc,bjkc->bijc) : einsum(bkic,bkjc->bijc)
+ *   out = (LN_out(x) W_z^T + b_z) * sigmoid(zn W_g^T + b_g)   [+ z if residual]
+ * Weights are first packed once with gtk_tri_mul_pack (the packed buffer
+ * stays valid until the parameters change).  c_z == 128, c in {64, 128}.
+ * ------------------------------------------------------------------------ */
+typedef struct gtk_tri_mul_weights {
+  int dtype;                     /* element type of every pointer below */
+  const void *ln_in_w, *ln_in_b; /* [c_z]            layer_norm_in   */
+  const void *a_p_w, *a_p_b;     /* [c][c_z], [c]    linear_a_p      */
+  const void *a_g_w, *a_g_b;     /* [c][c_z], [c]    linear_a_g      */
+  const void *b_p_w, *b_p_b;     /* [c][c_z], [c]    linear_b_p      */
+  const void *b_g_w, *b_g_b;     /* [c][c_z], [c]    linear_b_g      */
+  const void *g_w, *g_b;         /* [c_z][c_z],[c_z] linear_g        */
+  const void *ln_out_w, *ln_out_b; /* [c]            layer_norm_out  */
+  const void *z_w, *z_b;         /* [c_z][c], [c_z]  linear_z        */
+} gtk_tri_mul_weights;
+
+size_t gtk_tri_mul_packed_size(int64_t c_z, int64_t c, int dtype);
+int gtk_tri_mul_pack(const gtk_tri_mul_weights* w, int64_t c_z, int64_t c, int dtype, void* packed,
+                     size_t packed_bytes, void* stream);
+size_t gtk_tri_mul_workspace_size(int64_t B, int64_t N, int64_t c_z, int64_t c, int dtype);
+/* mask may be NULL (all ones).  out may not alias z. */
+int gtk_tri_mul_forward(const void* z, const float* mask, void* out, const void* packed, int64_t B,
+                        int64_t N, int64_t c_z, int64_t c, int outgoing, int residual,
+                        float eps_in, float eps_out, int dtype, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Fused TriangleAttention forward (starting / ending node).
+ * Replaces TriangleAttention._forward_cuda src/genie_tk/triangle_attention.py:145-179
+ * (semantics of _forward_pytorch :100-143 and Attention.forward
+ * src/genie_tk/primitives.py:114-178); ending(x, m) = starting(x^T, m^T)^T.
+ *   xn   = LN(x);  tri[h,q,k] = xn[q,k] . W_tri[h]
+ *   o    = softmax(q k^T / sqrt(d) + mask_bias + tri) v        per row, head
+ *   out  = (o * sigmoid(xn W_g^T + b_g)) W_o^T + b_o    [+ x if residual]
+ * Mask semantics as gtk_triangle_attention_starting.
+ * c_in == 128, H*d == c_h, d == 32, H <= 8.
+ * ------------------------------------------------------------------------ */
+typedef struct gtk_tri_attn_weights {
+  int dtype;                 /* element type of every pointer below */
+  const void *ln_w, *ln_b;   /* [c_in]                layer_norm        */
+  const void* tri_w;         /* [H][c_in]             linear (no bias)  */
+  const void *q_w, *k_w, *v_w; /* [c_h][c_in]         mha.linear_q/k/v  */
+  const void *g_w, *g_b;     /* [c_h][c_in], [c_h]    mha.linear_g      */
+  const void *o_w, *o_b;     /* [c_in][c_h], [c_in]   mha.linear_o      */
+} gtk_tri_attn_weights;
+
+size_t gtk_tri_attn_packed_size(int64_t c_in, int64_t c_h, int64_t H, int dtype);
+int gtk_tri_attn_pack(const gtk_tri_attn_weights* w, int64_t c_in, int64_t c_h, int64_t H,
+                      int dtype, void* packed, size_t packed_bytes, void* stream);
+size_t gtk_tri_attn_workspace_size(int64_t B, int64_t N, int64_t c_in, int64_t c_h, int64_t H,
+                                   int dtype);
+/* mask may be NULL (all ones).  out may not alias x. */
+int gtk_tri_attn_forward(const void* x, const float* mask, void* out, const void* packed,
+                         int64_t B, int64_t N, int64_t c_in, int64_t c_h, int64_t H, int starting,
+                         int residual, float eps, int dtype, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GENIE_TK_H_ */

@@ -1,0 +1,135 @@
+"""Scalar-loop restatement of the pair hot path for tiny inputs (float64).
+
+Written index-by-index from the equations (AlphaFold2 Algorithms 11-14 as
+used by src/genie_tk/triangle_mul.py:103-132 and
+src/genie_tk/triangle_attention.py:100-143 / primitives.py:114-178) without
+matmuls, transposes or broadcasting, so that it shares no code path with
+pair_ops.  Sizes: N <= 12, channels <= 32.
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict, List, Optional
+
+import numpy as np
+
+
+def _ln(v: List[float], w, b, eps: float) -> List[float]:
+    n = len(v)
+    mu = sum(v) / n
+    var = sum((t - mu) ** 2 for t in v) / n
+    r = 1.0 / math.sqrt(var + eps)
+    return [(v[c] - mu) * r * float(w[c]) + float(b[c]) for c in range(n)]
+
+
+def _lin(v: List[float], W, b=None) -> List[float]:
+    out = []
+    for o in range(W.shape[0]):
+        s = 0.0 if b is None else float(b[o])
+        for c in range(W.shape[1]):
+            s += float(W[o, c]) * v[c]
+        out.append(s)
+    return out
+
+
+def _sig(t: float) -> float:
+    return 1.0 / (1.0 + math.exp(-t))
+
+
+def tri_mul(z: np.ndarray, mask: Optional[np.ndarray], P: Dict[str, np.ndarray],
+            outgoing: bool, eps: float = 1e-5) -> np.ndarray:
+    B, N, _, cz = z.shape
+    c = P["linear_a_p.weight"].shape[0]
+    out = np.zeros((B, N, N, cz))
+    for bb in range(B):
+        zn = [[_ln([float(t) for t in z[bb, i, j]], P["layer_norm_in.weight"],
+                   P["layer_norm_in.bias"], eps) for j in range(N)] for i in range(N)]
+        a = [[None] * N for _ in range(N)]
+        bv = [[None] * N for _ in range(N)]
+        for i in range(N):
+            for j in range(N):
+                mij = 1.0 if mask is None else float(mask[bb, i, j])
+                ap = _lin(zn[i][j], P["linear_a_p.weight"], P["linear_a_p.bias"])
+                ag = _lin(zn[i][j], P["linear_a_g.weight"], P["linear_a_g.bias"])
+                bp = _lin(zn[i][j], P["linear_b_p.weight"], P["linear_b_p.bias"])
+                bg = _lin(zn[i][j], P["linear_b_g.weight"], P["linear_b_g.bias"])
+                a[i][j] = [ap[t] * _sig(ag[t]) * mij for t in range(c)]
+                bv[i][j] = [bp[t] * _sig(bg[t]) * mij for t in range(c)]
+        for i in range(N):
+            for j in range(N):
+                x = []
+                for ch in range(c):
+                    s = 0.0
+                    for k in range(N):
+                        if outgoing:
+                            s += a[i][k][ch] * bv[j][k][ch]
+                        else:
+                            s += a[k][i][ch] * bv[k][j][ch]
+                    x.append(s)
+                y = _lin(_ln(x, P["layer_norm_out.weight"], P["layer_norm_out.bias"], eps),
+                         P["linear_z.weight"], P["linear_z.bias"])
+                g = _lin(zn[i][j], P["linear_g.weight"], P["linear_g.bias"])
+                for o in range(cz):
+                    out[bb, i, j, o] = y[o] * _sig(g[o])
+    return out
+
+
+def tri_attn(x: np.ndarray, mask: Optional[np.ndarray], P: Dict[str, np.ndarray],
+             starting: bool, no_heads: int, inf: float = 1e9, eps: float = 1e-5) -> np.ndarray:
+    """Attention over positions of each row; ending node indexes columns directly.
+
+    A masked key's score is exactly -inf_value (the fp32 absorption of the
+    reference's additive -1e9 term, valid for |logit| < 32), so a row whose
+    keys are all masked gets uniform weights.
+    """
+    B, N, _, cin = x.shape
+    ch = P["mha.linear_q.weight"].shape[0]
+    d = ch // no_heads
+    scale = 1.0 / math.sqrt(d)
+    out = np.zeros((B, N, N, cin))
+
+    def at(bb, r, j):  # pair of row r, position j in the input's coordinates
+        return (bb, r, j) if starting else (bb, j, r)
+
+    for bb in range(B):
+        xn = {}
+        for r in range(N):
+            for j in range(N):
+                xn[(r, j)] = _ln([float(t) for t in x[at(bb, r, j)]], P["layer_norm.weight"],
+                                 P["layer_norm.bias"], eps)
+        tri = {(q, k): _lin(xn[(q, k)], P["linear.weight"]) for q in range(N) for k in range(N)}
+        for r in range(N):
+            valid = [1.0 if mask is None else float(mask[at(bb, r, k)]) for k in range(N)]
+            qv = [_lin(xn[(r, j)], P["mha.linear_q.weight"]) for j in range(N)]
+            kv = [_lin(xn[(r, j)], P["mha.linear_k.weight"]) for j in range(N)]
+            vv = [_lin(xn[(r, j)], P["mha.linear_v.weight"]) for j in range(N)]
+            for q in range(N):
+                o = [0.0] * ch
+                for h in range(no_heads):
+                    logits = []
+                    for k in range(N):
+                        s = sum(qv[q][h * d + t] * kv[k][h * d + t] for t in range(d)) * scale
+                        s += tri[(q, k)][h]
+                        if valid[k] == 0.0:
+                            s = -inf
+                        logits.append(s)
+                    mx = max(logits)
+                    w = [math.exp(t - mx) for t in logits]
+                    tot = sum(w)
+                    for t in range(d):
+                        o[h * d + t] = sum(w[k] * vv[k][h * d + t] for k in range(N)) / tot
+                g = _lin(xn[(r, q)], P["mha.linear_g.weight"], P["mha.linear_g.bias"])
+                o = [o[t] * _sig(g[t]) for t in range(ch)]
+                y = _lin(o, P["mha.linear_o.weight"], P["mha.linear_o.bias"])
+                for c in range(cin):
+                    out[at(bb, r, q) + (c,)] = y[c]
+    return out
+
+
+def layer_norm(x: np.ndarray, w, b, eps: float = 1e-5) -> np.ndarray:
+    out = np.zeros(x.shape)
+    flat = x.reshape(-1, x.shape[-1])
+    of = out.reshape(-1, x.shape[-1])
+    for r in range(flat.shape[0]):
+        of[r] = _ln([float(t) for t in flat[r]], w, b, eps)
+    return out

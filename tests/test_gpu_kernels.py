@@ -1,0 +1,193 @@
+"""GPU parity of every HIP entry point against the CPU oracle (small shapes,
+ragged N, masks, both precisions).  Calls go through genie_tk._C, which calls
+the C ABI of libgenie_tk_hip.so."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import pair_ops
+from tests import helpers as H
+from tests.gpu_common import check_bf16, check_fp32, ext, log, to_np, trimul_module, triattn_module
+
+pytestmark = pytest.mark.gpu
+DT = {"fp32": torch.float32, "bf16": torch.bfloat16}
+
+
+def _dev(a, dtype):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda", dtype)
+
+
+# ---------------------------------------------------------------- LayerNorm
+@pytest.mark.parametrize("dname", ["fp32", "bf16"])
+@pytest.mark.parametrize("D", [64, 128, 256, 512, 100])
+def test_layernorm(dname, D):
+    log(f"layernorm {dname} D={D}")
+    rng = np.random.default_rng(D)
+    x = (rng.standard_normal((3, 337, D)) * 2 + 0.5).astype(np.float32)
+    w = (1 + 0.2 * rng.standard_normal(D)).astype(np.float32)
+    b = (0.2 * rng.standard_normal(D)).astype(np.float32)
+    if dname == "bf16":
+        x = H.bf16_round(x)
+    y = ext().layernorm(_dev(x, DT[dname]), _dev(w, torch.float32), _dev(b, torch.float32), 1e-5)
+    torch.cuda.synchronize()
+    assert y.dtype == DT[dname] and y.shape == (3, 337, D)
+    ref = pair_ops.layer_norm(x.astype(np.float64), w, b, 1e-5)
+    if dname == "fp32":
+        check_fp32(to_np(y), ref, "layernorm", atol=2e-5)
+    else:
+        check_bf16(to_np(y), ref, "layernorm")
+
+
+@pytest.mark.parametrize("dname", ["fp32", "bf16"])
+@pytest.mark.parametrize("d_in,d_out", [(128, 96), (64, 7), (256, 128)])
+def test_fused_layernorm_linear(dname, d_in, d_out):
+    log(f"fused_layernorm_linear {dname} {d_in}->{d_out}")
+    rng = np.random.default_rng(d_in + d_out)
+    x = rng.standard_normal((2, 45, d_in)).astype(np.float32)
+    w = (1 + 0.2 * rng.standard_normal(d_in)).astype(np.float32)
+    b = (0.2 * rng.standard_normal(d_in)).astype(np.float32)
+    W = (rng.standard_normal((d_in, d_out)) / np.sqrt(d_in)).astype(np.float32)
+    bias = rng.standard_normal(d_out).astype(np.float32)
+    if dname == "bf16":
+        x, W = H.bf16_round(x), H.bf16_round(W)
+    y = ext().fused_layernorm_linear(_dev(x, DT[dname]), _dev(w, torch.float32), _dev(b, torch.float32),
+                                     _dev(W, DT[dname]), _dev(bias, torch.float32), 1e-5)
+    y0 = ext().fused_layernorm_linear(_dev(x, DT[dname]), _dev(w, torch.float32), _dev(b, torch.float32),
+                                      _dev(W, DT[dname]), None, 1e-5)
+    torch.cuda.synchronize()
+    assert y.shape == (2, 45, d_out)
+    ln = pair_ops.layer_norm(x.astype(np.float64), w, b, 1e-5)
+    if dname == "bf16":
+        ln = H.bf16_round(ln.astype(np.float32)).astype(np.float64)
+    ref = ln @ W + bias
+    chk = check_fp32 if dname == "fp32" else check_bf16
+    chk(to_np(y), ref, "fused_layernorm_linear")
+    chk(to_np(y0), ref - bias, "fused_layernorm_linear (no bias)")
+
+
+# ------------------------------------------------------- raw contraction
+@pytest.mark.parametrize("dname", ["fp32", "bf16"])
+@pytest.mark.parametrize("outgoing", [True, False])
+@pytest.mark.parametrize("N,C", [(64, 32), (48, 16), (130, 32), (256, 64)])
+def test_raw_triangle_mul(dname, outgoing, N, C):
+    log(f"triangle_mul raw {dname} out={outgoing} N={N} C={C}")
+    rng = np.random.default_rng(N * 7 + C)
+    a = rng.standard_normal((2, N, N, C)).astype(np.float32)
+    b = rng.standard_normal((2, N, N, C)).astype(np.float32)
+    if dname == "bf16":
+        a, b = H.bf16_round(a), H.bf16_round(b)
+    mask = torch.ones(2, N, N, device="cuda")
+    fn = ext().triangle_mul_outgoing if outgoing else ext().triangle_mul_incoming
+    x = fn(_dev(a, DT[dname]), _dev(b, DT[dname]), mask)
+    torch.cuda.synchronize()
+    ref = pair_ops.contract(a.astype(np.float64), b.astype(np.float64), outgoing)
+    got = to_np(x)
+    if dname == "fp32":
+        check_fp32(got, ref, "contraction", atol=1e-4 * np.sqrt(N))
+    else:
+        # bf16 output of sums of N products: tolerance relative to the sum's scale
+        scale = np.sqrt(N)
+        check_bf16(got / scale, ref / scale, "contraction")
+
+
+# --------------------------------------------------------- raw attention
+@pytest.mark.parametrize("dname", ["fp32", "bf16"])
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("N", [40, 64])
+def test_raw_triangle_attention(dname, starting, N):
+    log(f"triangle_attention raw {dname} start={starting} N={N}")
+    rng = np.random.default_rng(N + starting)
+    B, Hh, D = 1, 4, 32
+    q, k, v = (rng.standard_normal((B, Hh, N, N, D)).astype(np.float32) for _ in range(3))
+    bias = rng.standard_normal((B, Hh, N, N)).astype(np.float32)
+    m = (rng.random((B, N, N)) > 0.25).astype(np.float32)
+    if starting:
+        m[0, 3, :] = 0  # a row with no valid key
+    else:
+        m[0, :, 3] = 0
+    if dname == "bf16":
+        q, k, v = H.bf16_round(q), H.bf16_round(k), H.bf16_round(v)
+    scale = 1 / np.sqrt(D)
+    fn = ext().triangle_attention_starting if starting else ext().triangle_attention_ending
+    o = fn(_dev(q, DT[dname]), _dev(k, DT[dname]), _dev(v, DT[dname]), _dev(bias, torch.float32),
+           _dev(m, torch.float32), scale)
+    torch.cuda.synchronize()
+    assert o.shape == (B, N, N, Hh * D)
+    ref = pair_ops.attention_core(q, k, v, bias, m, scale, starting, dtype=np.float64)
+    (check_fp32 if dname == "fp32" else check_bf16)(to_np(o), ref, "attention core")
+
+
+# --------------------------------------------------------- fused modules
+@pytest.mark.parametrize("dname", ["fp32", "bf16"])
+@pytest.mark.parametrize("outgoing", [True, False])
+@pytest.mark.parametrize("N,c", [(64, 128), (37, 128), (100, 64)])
+def test_tri_mul_module(dname, outgoing, N, c):
+    log(f"tri_mul module {dname} out={outgoing} N={N} c={c}")
+    P = H.draw_params(H.tri_mul_shapes(128, c), seed=N + c, ln_random=True, bias_random=True)
+    z = H.pair_input(2, N, 128, seed=N)
+    m = H.tail_mask(2, N, [N, N - 9])
+    if dname == "bf16":
+        P, z = H.bf16_params(P), H.bf16_round(z)
+    mod = trimul_module(P, outgoing, DT[dname])
+    with torch.no_grad():
+        y = mod._forward_cuda(_dev(z, DT[dname]), _dev(m, DT[dname]))
+        y_res = mod._forward_cuda(_dev(z, DT[dname]), _dev(m, DT[dname]), residual=True)
+        y_nomask = mod(_dev(z, DT[dname]))
+    torch.cuda.synchronize()
+    ref = pair_ops.tri_mul(z, m, P, outgoing, dtype=np.float64)
+    ref_nm = pair_ops.tri_mul(z, None, P, outgoing, dtype=np.float64)
+    if dname == "fp32":
+        check_fp32(to_np(y), ref, "tri_mul")
+        check_fp32(to_np(y_res), ref + z, "tri_mul residual")
+        check_fp32(to_np(y_nomask), ref_nm, "tri_mul mask=None")
+    else:
+        check_bf16(to_np(y), ref, "tri_mul")
+        check_bf16(to_np(y_res), ref + z, "tri_mul residual")
+        check_bf16(to_np(y_nomask), ref_nm, "tri_mul mask=None")
+
+
+@pytest.mark.parametrize("dname", ["fp32", "bf16"])
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("N", [64, 45])
+def test_tri_attn_module(dname, starting, N):
+    log(f"tri_attn module {dname} start={starting} N={N}")
+    P = H.draw_params(H.tri_attn_shapes(128, 128, 4), seed=N + 1, ln_random=True, bias_random=True)
+    x = H.pair_input(2, N, 128, seed=N + 2)
+    m = H.tail_mask(2, N, [N, N - 7])
+    if dname == "bf16":
+        P, x = H.bf16_params(P), H.bf16_round(x)
+    mod = triattn_module(P, starting, 4, DT[dname])
+    with torch.no_grad():
+        y = mod._forward_cuda(_dev(x, DT[dname]), _dev(m, DT[dname]))
+        y_nomask = mod(_dev(x, DT[dname]))
+    torch.cuda.synchronize()
+    ref = pair_ops.tri_attn(x, m, P, starting, 4, dtype=np.float64)
+    ref_nm = pair_ops.tri_attn(x, None, P, starting, 4, dtype=np.float64)
+    chk = check_fp32 if dname == "fp32" else check_bf16
+    chk(to_np(y), ref, "tri_attn")
+    chk(to_np(y_nomask), ref_nm, "tri_attn mask=None")
+
+
+def test_forward_dispatches_to_hip(monkeypatch):
+    """With use_fused_kernel=True, forward() on a GPU tensor under no_grad runs the
+    HIP path (the PyTorch path is made to raise)."""
+    P = H.draw_params(H.tri_mul_shapes(128, 128), seed=1)
+    mod = trimul_module(P, True, torch.bfloat16)
+    monkeypatch.setattr(mod, "_forward_pytorch", lambda *a, **k: (_ for _ in ()).throw(AssertionError("fallback")))
+    z = torch.randn(1, 32, 32, 128, device="cuda", dtype=torch.bfloat16)
+    with torch.no_grad():
+        y = mod(z, torch.ones(1, 32, 32, device="cuda"))
+    assert y.shape == z.shape and torch.isfinite(y).all()
+
+
+def test_deterministic_and_leading_dims():
+    P = H.draw_params(H.tri_attn_shapes(128, 128, 4), seed=3)
+    mod = triattn_module(P, True, 4, torch.bfloat16)
+    x = torch.randn(2, 3, 40, 40, 128, device="cuda", dtype=torch.bfloat16)
+    with torch.no_grad():
+        y1 = mod(x)
+        y2 = mod(x)
+        y3 = mod(x[1, 2])  # no batch dimension
+    assert torch.equal(y1, y2)
+    assert y1.shape == x.shape
+    assert torch.equal(y3, y1[1, 2])

@@ -1,0 +1,217 @@
+"""Pins of the CPU oracle (oracle/pair_ops.py) — CPU only.
+
+Each check is chosen so that a plausible restatement mistake (a transposed
+operand, a wrong index, a dropped bias term, the mask applied in the wrong
+place) fails at least one of them:
+  * float64 agreement with the scalar loops in oracle/brute.py;
+  * agreement with library routines (torch layer_norm, einsum, SDPA);
+  * identities (incoming vs transposed outgoing, ending vs transposed starting);
+  * closed forms (zero output under default init, constant gate, padded
+    tri-mul rows, uniform attention on fully masked rows);
+  * planted mistakes in a copy of the oracle are detected.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import brute, pair_ops
+from tests import helpers as H
+
+F64 = np.float64
+
+
+def _tm_params(cz=16, c=8, seed=0, **kw):
+    kw.setdefault("ln_random", True)
+    kw.setdefault("bias_random", True)
+    return H.draw_params(H.tri_mul_shapes(cz, c), seed, **kw)
+
+
+def _ta_params(cin=16, ch=8, nh=2, seed=0, **kw):
+    kw.setdefault("ln_random", True)
+    kw.setdefault("bias_random", True)
+    return H.draw_params(H.tri_attn_shapes(cin, ch, nh), seed, **kw)
+
+
+def _partial_mask(B, N, seed=3):
+    rng = np.random.default_rng(seed)
+    m = (rng.random((B, N, N)) > 0.3).astype(np.float32)
+    return m
+
+
+# ---------------------------------------------------------------- LayerNorm
+def test_layer_norm_matches_torch_and_loops():
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((5, 7, 24)) * 3 + 1.5
+    w = rng.standard_normal(24)
+    b = rng.standard_normal(24)
+    ref = F.layer_norm(torch.from_numpy(x), (24,), torch.from_numpy(w), torch.from_numpy(b), 1e-5)
+    got = pair_ops.layer_norm(x, w, b, 1e-5)
+    np.testing.assert_allclose(got, ref.numpy(), rtol=0, atol=1e-12)
+    np.testing.assert_allclose(brute.layer_norm(x, w, b, 1e-5), got, rtol=0, atol=1e-12)
+
+
+# -------------------------------------------------------------- contraction
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_contract_matches_einsum(outgoing):
+    rng = np.random.default_rng(1)
+    a = rng.standard_normal((2, 9, 9, 5))
+    b = rng.standard_normal((2, 9, 9, 5))
+    eq = "bikc,bjkc->bijc" if outgoing else "bkic,bkjc->bijc"
+    ref = torch.einsum(eq, torch.from_numpy(a), torch.from_numpy(b)).numpy()
+    np.testing.assert_allclose(pair_ops.contract(a, b, outgoing), ref, atol=1e-12)
+    rows = [0, 4, 8]
+    np.testing.assert_allclose(pair_ops.contract(a, b, outgoing, rows), ref[:, rows], atol=1e-12)
+
+
+# ------------------------------------------------------------------ tri-mul
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_tri_mul_matches_loops(outgoing):
+    P = _tm_params()
+    z = H.pair_input(2, 6, 16, seed=4).astype(F64)
+    m = _partial_mask(2, 6)
+    ref = brute.tri_mul(z, m, P, outgoing)
+    got = pair_ops.tri_mul(z, m, P, outgoing, dtype=F64)
+    np.testing.assert_allclose(got, ref, rtol=0, atol=1e-11)
+    rows = [1, 5]
+    got_r = pair_ops.tri_mul(z, m, P, outgoing, dtype=F64, rows=rows)
+    np.testing.assert_allclose(got_r, ref[:, rows], rtol=0, atol=1e-11)
+
+
+def test_tri_mul_incoming_is_transposed_outgoing():
+    P = _tm_params(seed=5)
+    swapped = dict(P)
+    for part in ("weight", "bias"):
+        swapped[f"linear_a_p.{part}"], swapped[f"linear_b_p.{part}"] = P[f"linear_b_p.{part}"], P[f"linear_a_p.{part}"]
+        swapped[f"linear_a_g.{part}"], swapped[f"linear_b_g.{part}"] = P[f"linear_b_g.{part}"], P[f"linear_a_g.{part}"]
+    z = H.pair_input(1, 10, 16, seed=6).astype(F64)
+    m = _partial_mask(1, 10, seed=7)
+    inc = pair_ops.tri_mul(z, m, P, False, dtype=F64)
+    out_t = pair_ops.tri_mul(z.swapaxes(1, 2), m.swapaxes(1, 2), swapped, True, dtype=F64)
+    np.testing.assert_allclose(inc, out_t.swapaxes(1, 2), atol=1e-11)
+
+
+def test_tri_mul_closed_forms():
+    cz, c = 16, 8
+    z = H.pair_input(1, 8, cz, seed=8).astype(F64)
+    # default init of the reference: linear_z is zero ("final") -> exactly zero output
+    P = _tm_params(cz, c, seed=9)
+    P["linear_z.weight"][:] = 0
+    P["linear_z.bias"][:] = 0
+    assert np.all(pair_ops.tri_mul(z, None, P, True, dtype=F64) == 0)
+    # gating init (W_g = 0, b_g = 1) and constant output bias -> t * sigmoid(1)
+    P = _tm_params(cz, c, seed=10)
+    P["linear_z.weight"][:] = 0
+    P["linear_z.bias"][:] = np.linspace(-1, 1, cz)
+    P["linear_g.weight"][:] = 0
+    P["linear_g.bias"][:] = 1
+    got = pair_ops.tri_mul(z, None, P, False, dtype=F64)
+    np.testing.assert_allclose(got, np.broadcast_to(P["linear_z.bias"] * 0.7310585786300049, got.shape),
+                               atol=1e-12)
+    # padded rows (mask 0 for i >= L): x = 0 -> LN_out(0) = beta_out
+    P = _tm_params(cz, c, seed=11)
+    L = 5
+    m = H.tail_mask(1, 8, [L])
+    got = pair_ops.tri_mul(z, m, P, True, dtype=F64)
+    zn = pair_ops.layer_norm(z, P["layer_norm_in.weight"].astype(F64), P["layer_norm_in.bias"].astype(F64))
+    gate = pair_ops.sigmoid(zn @ P["linear_g.weight"].T.astype(F64) + P["linear_g.bias"])
+    const = P["linear_z.weight"].astype(F64) @ P["layer_norm_out.bias"] + P["linear_z.bias"]
+    np.testing.assert_allclose(got[0, L:], (const * gate)[0, L:], atol=1e-10)
+
+
+# ----------------------------------------------------------------- tri-attn
+@pytest.mark.parametrize("starting", [True, False])
+def test_tri_attn_matches_loops(starting):
+    P = _ta_params()
+    x = H.pair_input(2, 6, 16, seed=12).astype(F64)
+    m = _partial_mask(2, 6, seed=13)
+    m[0, 2, :] = 0  # a row (starting) / column (ending) with every key masked
+    m[1, :, 3] = 0
+    ref = brute.tri_attn(x, m, P, starting, 2)
+    got = pair_ops.tri_attn(x, m, P, starting, 2, dtype=F64)
+    np.testing.assert_allclose(got, ref, rtol=0, atol=1e-11)
+    rows = [0, 2, 5]
+    got_r = pair_ops.tri_attn(x, m, P, starting, 2, dtype=F64, rows=rows)
+    sel = ref[:, rows] if starting else ref[:, :, rows]
+    np.testing.assert_allclose(got_r, sel, rtol=0, atol=1e-11)
+
+
+def test_tri_attn_ending_is_transposed_starting():
+    P = _ta_params(seed=14)
+    x = H.pair_input(1, 9, 16, seed=15).astype(F64)
+    m = _partial_mask(1, 9, seed=16)
+    end = pair_ops.tri_attn(x, m, P, False, 2, dtype=F64)
+    start_t = pair_ops.tri_attn(x.swapaxes(1, 2), m.swapaxes(1, 2), P, True, 2, dtype=F64)
+    np.testing.assert_allclose(end, start_t.swapaxes(1, 2), atol=1e-12)
+
+
+def test_tri_attn_fully_masked_row_is_uniform():
+    P = _ta_params(seed=17)
+    N, cin, ch, nh = 7, 16, 8, 2
+    x = H.pair_input(1, N, cin, seed=18).astype(F64)
+    m = np.ones((1, N, N), np.float32)
+    m[0, 4, :] = 0
+    for dt in (F64, np.float32):
+        got = pair_ops.tri_attn(x, m, P, True, nh, dtype=dt)
+        xn = pair_ops.layer_norm(x[0, 4], P["layer_norm.weight"].astype(F64), P["layer_norm.bias"].astype(F64))
+        v = xn @ P["mha.linear_v.weight"].T.astype(F64)
+        o = np.broadcast_to(v.mean(axis=0), (N, ch))
+        o = o * pair_ops.sigmoid(xn @ P["mha.linear_g.weight"].T.astype(F64) + P["mha.linear_g.bias"])
+        want = o @ P["mha.linear_o.weight"].T.astype(F64) + P["mha.linear_o.bias"]
+        np.testing.assert_allclose(got[0, 4], want, atol=1e-5 if dt == np.float32 else 1e-12)
+
+
+@pytest.mark.parametrize("starting", [True, False])
+def test_attention_core_matches_sdpa(starting):
+    rng = np.random.default_rng(19)
+    B, Hh, N, D = 1, 3, 8, 4
+    q, k, v = (rng.standard_normal((B, Hh, N, N, D)) for _ in range(3))
+    bias = rng.standard_normal((B, Hh, N, N))
+    m = _partial_mask(B, N, seed=20)
+    m[:, :, 0] = 1  # every row keeps a valid key
+    m[:, 0, :] = 1
+    scale = 0.37
+    got = pair_ops.attention_core(q, k, v, bias, m, scale, starting, dtype=F64)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a))  # noqa: E731
+    qq, kk, vv, mm = (q, k, v, m) if starting else (q.swapaxes(2, 3), k.swapaxes(2, 3), v.swapaxes(2, 3), m.swapaxes(1, 2))
+    # rows -> batch: [B, H, R, N, D] -> [B, R, H, N, D]
+    qq, kk, vv = (t(a).transpose(1, 2) for a in (qq, kk, vv))
+    addm = t(1e9 * (mm - 1))[:, :, None, None, :] + t(bias)[:, None]
+    o = F.scaled_dot_product_attention(qq, kk, vv, attn_mask=addm, scale=scale)  # [B, R, H, N, D]
+    want = o.transpose(2, 3).reshape(B, N, N, Hh * D).numpy()
+    if not starting:
+        want = want.swapaxes(1, 2)
+    np.testing.assert_allclose(got, want, atol=1e-10)
+
+
+# ------------------------------------------------------- planted mistakes
+def test_planted_mistakes_are_detected(monkeypatch):
+    """A transposed contraction operand, a dropped mask bias and a gate taken from
+    the raw input each break one of the pins above."""
+    P = _tm_params()
+    z = H.pair_input(1, 5, 16, seed=21).astype(F64)
+    m = _partial_mask(1, 5, seed=22)
+    ref = brute.tri_mul(z, m, P, True)
+
+    orig_contract = pair_ops.contract
+    monkeypatch.setattr(pair_ops, "contract", lambda a, b, o, rows=None: orig_contract(b, a, o, rows))
+    assert np.abs(pair_ops.tri_mul(z, m, P, True, dtype=F64) - ref).max() > 1e-3
+    monkeypatch.undo()
+
+    orig_ln = pair_ops.layer_norm
+    calls = {"n": 0}
+
+    def ln_skip_first(x, w, b, eps=1e-5):  # LN_in dropped: gate and projections see raw z
+        calls["n"] += 1
+        return x if calls["n"] == 1 else orig_ln(x, w, b, eps)
+
+    monkeypatch.setattr(pair_ops, "layer_norm", ln_skip_first)
+    assert np.abs(pair_ops.tri_mul(z, m, P, True, dtype=F64) - ref).max() > 1e-3
+    monkeypatch.undo()
+
+    PA = _ta_params()
+    x = H.pair_input(1, 5, 16, seed=23).astype(F64)
+    ma = _partial_mask(1, 5, seed=24)
+    ref_a = brute.tri_attn(x, ma, PA, True, 2)
+    monkeypatch.setattr(pair_ops, "_masked_scores", lambda qk, km, tri, inf, dt: qk + tri)
+    assert np.abs(pair_ops.tri_attn(x, ma, PA, True, 2, dtype=F64) - ref_a).max() > 1e-3
