@@ -1,0 +1,308 @@
+#!/usr/bin/env python
+"""Benchmark of the pair-representation hot path on one MI355X.
+
+Workload (one "step"): B=1, N=512, c_z=128, bf16, synthetic seeded inputs
+(z ~ N(0,1), mask all ones) and random weights (W ~ N(0, 1/fan_in), tri-mul
+gate biases 1.0, other biases 0; tri-attn H=4, d=32, c_h=128):
+    triangle multiplication outgoing + incoming, triangle attention starting
+    + ending node, and LayerNorm over the pair tensor,
+each through the genie_tk modules' HIP kernel path (forward).
+
+Prints one JSON line.  value = algorithmic TFLOP/s of the step (dense
+2*M*N*K of every projection and contraction; LayerNorm and softmax count 0),
+with per-operator ms / TFLOP/s / fraction of the 2516.6 TFLOP/s bf16 MFMA
+peak, LayerNorm GB/s against 8 TB/s HBM, the roofline of the dominant kernel
+(per-kernel durations from HIP events recorded on the launch stream) and the
+CPU baseline (the numpy oracle on the host cores, bounded sample).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "genie-tk_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_BF16_FLOPS = 2516.6e12
+PEAK_HBM_BYTES = 8.0e12
+METRIC = "fwd ms + % bf16 MFMA peak, tri-mul & tri-attn at N=512 c_z=128; LN GB/s"
+C_Z, C_HID, HEADS, HEAD_DIM = 128, 128, 4, 32
+
+
+def trimul_flops(N: int, B: int = 1) -> dict:
+    return {
+        "trimul_prologue": 2.0 * B * N * N * C_Z * 4 * C_HID,
+        "trimul_contract": 2.0 * B * N ** 3 * C_HID,
+        "trimul_epilogue": 2.0 * B * N * N * (C_Z * C_Z + C_HID * C_Z),
+    }
+
+
+def triattn_flops(N: int, B: int = 1) -> dict:
+    ch = HEADS * HEAD_DIM
+    return {
+        "triattn_prologue": 2.0 * B * N * N * C_Z * (4 * ch + HEADS),
+        "triattn_flash": 4.0 * B * HEADS * HEAD_DIM * N ** 3 + 2.0 * B * N * N * ch * C_Z,
+    }
+
+
+def ln_bytes(N: int, B: int = 1, elem: int = 2) -> float:
+    return 2.0 * B * N * N * C_Z * elem
+
+
+def build_modules(torch, N: int, dev: str):
+    import numpy as np
+
+    from genie_tk import (TriangleAttentionEndingNode, TriangleAttentionStartingNode,
+                          TriangleMultiplicationIncoming, TriangleMultiplicationOutgoing)
+
+    def init_(mod, seed, gate_names=()):
+        g = torch.Generator().manual_seed(seed)
+        sd = {}
+        for name, p in sorted(mod.state_dict().items()):
+            if name.endswith("weight") and p.dim() == 2:
+                v = torch.randn(p.shape, generator=g) / np.sqrt(p.shape[1])
+            elif "layer_norm" in name:
+                v = torch.ones(p.shape) if name.endswith("weight") else torch.zeros(p.shape)
+            else:
+                v = torch.full(p.shape, 1.0) if name.rsplit(".", 1)[0] in gate_names else torch.zeros(p.shape)
+            sd[name] = v
+        mod.load_state_dict(sd)
+        return mod.to(dev, torch.bfloat16).eval()
+
+    gates = ("linear_a_g", "linear_b_g", "linear_g")
+    mods = {
+        "tri_mul_out": init_(TriangleMultiplicationOutgoing(C_Z, C_HID), 1, gates),
+        "tri_mul_in": init_(TriangleMultiplicationIncoming(C_Z, C_HID), 2, gates),
+        "tri_att_start": init_(TriangleAttentionStartingNode(C_Z, HEADS * HEAD_DIM, HEADS), 3),
+        "tri_att_end": init_(TriangleAttentionEndingNode(C_Z, HEADS * HEAD_DIM, HEADS), 4),
+    }
+    for m in mods.values():
+        assert m.use_fused_kernel, "HIP kernel path not enabled"
+    return mods
+
+
+def event_time_ms(torch, fn, reps: int, warm: int = 2, flush=None) -> list:
+    """Per-repetition durations from events on the current stream."""
+    for _ in range(warm):
+        fn()
+    out = []
+    for _ in range(reps):
+        if flush is not None:
+            flush()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        fn()
+        b.record()
+        b.synchronize()
+        out.append(a.elapsed_time(b))
+    return out
+
+
+def cpu_baseline(N: int, seed: int = 0) -> dict:
+    """The numpy oracle (fp32) on the host, bounded sample of the same step."""
+    import numpy as np
+
+    from oracle import pair_ops
+    from tests import helpers as H
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+    except Exception:  # pragma: no cover
+        threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
+    z = H.pair_input(1, N, C_Z, seed)
+    m = np.ones((1, N, N), np.float32)
+    Pm = H.draw_params(H.tri_mul_shapes(C_Z, C_HID), 1, gate_bias=1.0, gate_keys=H.TRI_MUL_GATES)
+    Pa = H.draw_params(H.tri_attn_shapes(C_Z, HEADS * HEAD_DIM, HEADS), 3)
+    t0 = time.perf_counter()
+    pair_ops.tri_mul(z, m, Pm, True, dtype=np.float32)
+    t_mul = time.perf_counter() - t0
+    rows = list(range(0, N, 16))  # every 16th attention row: rows are independent problems
+    t0 = time.perf_counter()
+    pair_ops.tri_attn(z, m, Pa, True, HEADS, dtype=np.float32, rows=rows)
+    t_att = (time.perf_counter() - t0) * N / len(rows)
+    t0 = time.perf_counter()
+    pair_ops.layer_norm(z, np.ones(C_Z, np.float32), np.zeros(C_Z, np.float32))
+    t_ln = time.perf_counter() - t0
+    step_s = 2 * t_mul + 2 * t_att + t_ln
+    flops = 2 * sum(trimul_flops(N).values()) + 2 * sum(triattn_flops(N).values())
+    return {
+        "value": round(flops / step_s / 1e12, 4),
+        "unit": "TFLOP/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": (f"numpy fp32 oracle of the same step at N={N}: tri-mul outgoing full "
+                   f"({t_mul:.2f} s, counted for outgoing and incoming), tri-attn starting on "
+                   f"{len(rows)} of {N} rows ({t_att * len(rows) / N:.2f} s, scaled x{N // len(rows)}, "
+                   f"counted for starting and ending), LayerNorm full ({t_ln:.2f} s); "
+                   f"step {step_s:.1f} s"),
+        "ms_per_step": round(step_s * 1e3, 1),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--n", type=int, default=512, help="pair length N")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the path has no multi-GPU implementation)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from genie_tk import _ext
+
+    C = _ext.require()
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    N = args.n
+    torch.manual_seed(0)
+    z = torch.randn(1, N, N, C_Z, device=dev).to(torch.bfloat16)
+    mask = torch.ones(1, N, N, device=dev)
+    ln_w = torch.ones(C_Z, device=dev)
+    ln_b = torch.zeros(C_Z, device=dev)
+    mods = build_modules(torch, N, dev)
+
+    ops = {
+        "tri_mul_out": lambda: mods["tri_mul_out"](z, mask),
+        "tri_mul_in": lambda: mods["tri_mul_in"](z, mask),
+        "tri_att_start": lambda: mods["tri_att_start"](z, mask),
+        "tri_att_end": lambda: mods["tri_att_end"](z, mask),
+        "layernorm": lambda: C.layernorm(z, ln_w, ln_b, 1e-5),
+    }
+
+    def step():
+        for f in ops.values():
+            f()
+
+    with torch.no_grad():
+        print(f"[bench] N={N} warmup {args.warmup}", file=sys.stderr, flush=True)
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            step()
+        torch.cuda.synchronize()
+        step_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+        print(f"[bench] timed {args.steps} steps: {step_ms:.3f} ms/step", file=sys.stderr, flush=True)
+
+        # per-operator event timing
+        reps = max(5, args.steps)
+        op_ms = {k: statistics.median(event_time_ms(torch, f, reps)) for k, f in ops.items()}
+
+        # per-kernel durations from events around each launch
+        C.timing_enable(True)
+        for _ in range(args.steps):
+            step()
+        rep = C.timing_report()
+        C.timing_enable(False)
+
+        # LayerNorm bandwidth with the 256 MiB MALL flushed before every launch
+        flush_buf = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        ln_ms_cold = statistics.median(event_time_ms(torch, ops["layernorm"], reps,
+                                                     flush=lambda: flush_buf.zero_()))
+        del flush_buf
+        z2 = torch.randn(1, 2 * N, 2 * N, C_Z, device=dev).to(torch.bfloat16)
+        ln2_ms = statistics.median(event_time_ms(torch, lambda: C.layernorm(z2, ln_w, ln_b, 1e-5), reps))
+        del z2
+    torch.cuda.synchronize()
+
+    fm, fa = trimul_flops(N), triattn_flops(N)
+    op_flops = {"tri_mul_out": sum(fm.values()), "tri_mul_in": sum(fm.values()),
+                "tri_att_start": sum(fa.values()), "tri_att_end": sum(fa.values())}
+    per_op = {}
+    for k, fl in op_flops.items():
+        tf = fl / (op_ms[k] * 1e-3) / 1e12
+        per_op[k] = {"ms": round(op_ms[k], 4), "gflop": round(fl / 1e9, 2),
+                     "tflops": round(tf, 2), "frac_bf16_peak": round(tf * 1e12 / PEAK_BF16_FLOPS, 4)}
+    lnb = ln_bytes(N)
+    per_op["layernorm"] = {
+        "ms": round(op_ms["layernorm"], 4), "mb": round(lnb / 1e6, 1),
+        "gbps_warm": round(lnb / (op_ms["layernorm"] * 1e-3) / 1e9, 1),
+        "ms_cold": round(ln_ms_cold, 4),
+        "gbps_cold": round(lnb / (ln_ms_cold * 1e-3) / 1e9, 1),
+        "frac_hbm_cold": round(lnb / (ln_ms_cold * 1e-3) / PEAK_HBM_BYTES, 4),
+        "note": "cold = 1 GiB write before each launch evicts the 256 MiB MALL",
+    }
+    ln2b = ln_bytes(2 * N)
+    per_op[f"layernorm_n{2 * N}"] = {
+        "ms": round(ln2_ms, 4), "mb": round(ln2b / 1e6, 1),
+        "gbps": round(ln2b / (ln2_ms * 1e-3) / 1e9, 1),
+        "frac_hbm": round(ln2b / (ln2_ms * 1e-3) / PEAK_HBM_BYTES, 4),
+    }
+
+    work = dict(fm)
+    work.update(fa)
+    kernels = {}
+    for name, (cnt, total, mn, mx) in rep.items():
+        avg = total / cnt
+        entry = {"launches": cnt, "avg_ms": round(avg, 4), "total_ms": round(total, 3)}
+        if name in work:
+            a = work[name] / (avg * 1e-3)
+            entry.update({"bound": "mfma", "achieved_tflops": round(a / 1e12, 2),
+                          "frac": round(a / PEAK_BF16_FLOPS, 4)})
+        elif name == "layernorm":
+            a = lnb / (avg * 1e-3)
+            entry.update({"bound": "hbm", "achieved_gbps": round(a / 1e9, 1),
+                          "frac": round(a / PEAK_HBM_BYTES, 4)})
+        kernels[name] = entry
+    dom = max((k for k in kernels if k in work), key=lambda k: kernels[k]["total_ms"])
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tfile):
+        with open(tfile) as fh:
+            traffic = json.load(fh).get(f"{dom}@N={N}")
+    dom_avg_s = kernels[dom]["avg_ms"] * 1e-3
+    roofline = {"kernel": dom, "bound": "mfma",
+                "achieved": round(work[dom] / dom_avg_s / 1e12, 2),
+                "peak": PEAK_BF16_FLOPS / 1e12, "unit": "TFLOP/s",
+                "frac": round(work[dom] / dom_avg_s / PEAK_BF16_FLOPS, 4),
+                "traffic": traffic,
+                "algorithmic_gflop_per_launch": round(work[dom] / 1e9, 3)}
+
+    step_flops = sum(op_flops.values())
+    cpu = None
+    if not args.no_cpu:
+        print("[bench] CPU baseline (numpy oracle)", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(N)
+    out = {
+        "metric": METRIC,
+        "value": round(step_flops / (step_ms * 1e-3) / 1e12, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(step_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded z ~ N(0,1), mask ones, random weights)",
+        "config": {"workload": "pair-stack forward step: tri-mul out+in, tri-attn start+end, LayerNorm",
+                   "B": 1, "N": N, "c_z": C_Z, "c_hidden_mul": C_HID, "heads": HEADS,
+                   "head_dim": HEAD_DIM, "parallelism": "single GPU"},
+        "ops": per_op,
+        "kernels": kernels,
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -36,4 +36,20 @@ void set_error(const char* fmt, ...);
 
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
+// Per-kernel timing (gtk_timing_enable / gtk_timing_report): when enabled, a
+// StageTimer records one HIP event before and one after the launch it
+// scopes, on the launch stream.  Disabled, it costs one relaxed load.
+class StageTimer {
+ public:
+  StageTimer(const char* name, hipStream_t st);
+  ~StageTimer();
+  StageTimer(const StageTimer&) = delete;
+  StageTimer& operator=(const StageTimer&) = delete;
+
+ private:
+  const char* name_;
+  hipStream_t st_;
+  hipEvent_t begin_ = nullptr;
+};
+
 }  // namespace gtk

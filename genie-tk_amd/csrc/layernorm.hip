@@ -110,6 +110,7 @@ template <typename T>
 static int launch_ln(const T* x, T* y, const float* g, const float* b, int64_t rows, int64_t d,
                      float eps, hipStream_t st) {
   constexpr int U = 4;
+  StageTimer timer("layernorm", st);
   auto grid_for = [&](int D) {
     const int64_t rows_per_block = 4 * (64 / (D / 8)) * U;
     return (unsigned)((rows + rows_per_block - 1) / rows_per_block);

@@ -255,6 +255,23 @@ at::Tensor tri_attn_forward(const at::Tensor& x, const c10::optional<at::Tensor>
   return out;
 }
 
+py::dict timing_report() {
+  std::vector<char> buf(1 << 16);
+  check_rc(gtk_timing_report(buf.data(), buf.size()));
+  py::dict out;
+  const char* p = buf.data();
+  while (*p) {
+    char name[128];
+    int n = 0, used = 0;
+    double total = 0, mn = 0, mx = 0;
+    if (sscanf(p, "%127s %d %lf %lf %lf%n", name, &n, &total, &mn, &mx, &used) != 5) break;
+    out[py::str(name)] = py::make_tuple(n, total, mn, mx);
+    p += used;
+    while (*p == '\n') ++p;
+  }
+  return out;
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_C, m) {
@@ -286,4 +303,8 @@ PYBIND11_MODULE(_C, m) {
         py::arg("mask"), py::arg("packed"), py::arg("c_in"), py::arg("c_h"), py::arg("no_heads"),
         py::arg("starting"), py::arg("residual") = false, py::arg("eps") = 1e-5);
   m.def("version", []() { return gtk_version(); });
+  m.def("timing_enable", [](bool on) { check_rc(gtk_timing_enable(on ? 1 : 0)); },
+        "Record HIP events around every kernel launch (per-kernel timing)", py::arg("on"));
+  m.def("timing_report", &timing_report,
+        "Wait for recorded kernels; {name: (count, total_ms, min_ms, max_ms)}; clears records");
 }

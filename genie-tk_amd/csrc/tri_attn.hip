@@ -431,7 +431,10 @@ static int raw_attention(const void* q, const void* k, const void* v, const floa
   GTK_LAUNCH_CHECK();
   const int64_t blocks = B * N * H * ((N + 31) / 32);
   GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "attention grid too large");
-  triattn_raw_kernel<T><<<(unsigned)blocks, 64, 0, st>>>(mask, (T*)out, w, (int)B, (int)H, (int)N, Np, starting);
+  {
+    StageTimer timer("triattn_raw", st);
+    triattn_raw_kernel<T><<<(unsigned)blocks, 64, 0, st>>>(mask, (T*)out, w, (int)B, (int)H, (int)N, Np, starting);
+  }
   GTK_LAUNCH_CHECK();
   return GTK_OK;
 }
@@ -487,13 +490,19 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
   Carve cv(ws, SIZE_MAX);
   AttnWs<T> a = carve_attn_ws<T>(cv, B, Np, H, CH);
   const int64_t ptiles = B * (int64_t)Np * (Np / 32);
-  triattn_prologue_kernel<T, CIN, H><<<(unsigned)((ptiles + 3) / 4), 256, 0, st>>>(
-      (const T*)x, w, a, (int)B, (int)N, Np, starting, eps);
+  {
+    StageTimer timer("triattn_prologue", st);
+    triattn_prologue_kernel<T, CIN, H><<<(unsigned)((ptiles + 3) / 4), 256, 0, st>>>(
+        (const T*)x, w, a, (int)B, (int)N, Np, starting, eps);
+  }
   GTK_LAUNCH_CHECK();
   const int64_t blocks = B * N * ((N + 31) / 32);
   GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "attention grid too large");
-  triattn_fused_kernel<T, CIN, H><<<(unsigned)blocks, 64 * H, 0, st>>>(
-      (const T*)x, mask, (T*)out, w, a, (int)B, (int)N, Np, starting, residual);
+  {
+    StageTimer timer("triattn_flash", st);
+    triattn_fused_kernel<T, CIN, H><<<(unsigned)blocks, 64 * H, 0, st>>>(
+        (const T*)x, mask, (T*)out, w, a, (int)B, (int)N, Np, starting, residual);
+  }
   GTK_LAUNCH_CHECK();
   return GTK_OK;
 }

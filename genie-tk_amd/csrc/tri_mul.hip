@@ -390,10 +390,12 @@ static int launch_contract(const T* pa, const T* pb, T* px, int Np, int64_t npla
   if (Np % 128 == 0) {
     const int64_t blocks = (int64_t)(Np / 128) * (Np / 128) * nplanes;
     GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "contraction grid too large");
+    StageTimer timer("trimul_contract", st);
     trimul_contract_kernel<T, 128><<<(unsigned)blocks, 256, 0, st>>>(pa, pb, px, Np, nplanes);
   } else {
     const int64_t blocks = (int64_t)(Np / 64) * (Np / 64) * nplanes;
     GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "contraction grid too large");
+    StageTimer timer("trimul_contract", st);
     trimul_contract_kernel<T, 64><<<(unsigned)blocks, 256, 0, st>>>(pa, pb, px, Np, nplanes);
   }
   GTK_LAUNCH_CHECK();
@@ -486,14 +488,20 @@ static int fwd_trimul(const void* z, const float* mask, void* out, const void* p
   T* pb = cv.take<T>(B * CH * (int64_t)Np * Np);
   T* px = cv.take<T>(B * CH * (int64_t)Np * Np);
   const int64_t ptiles = B * (int64_t)Np * (Np / 32);
-  trimul_prologue_kernel<T, CZ, CH><<<(unsigned)((ptiles + 3) / 4), 256, 0, st>>>(
-      (const T*)z, mask, pa, pb, w, (int)B, (int)N, Np, outgoing, eps_in);
+  {
+    StageTimer timer("trimul_prologue", st);
+    trimul_prologue_kernel<T, CZ, CH><<<(unsigned)((ptiles + 3) / 4), 256, 0, st>>>(
+        (const T*)z, mask, pa, pb, w, (int)B, (int)N, Np, outgoing, eps_in);
+  }
   GTK_LAUNCH_CHECK();
   int rc = launch_contract<T>(pa, pb, px, Np, B * CH, st);
   if (rc) return rc;
   const int64_t etiles = B * N * ((N + 31) / 32);
-  trimul_epilogue_kernel<T, CZ, CH><<<(unsigned)((etiles + 3) / 4), 256, 0, st>>>(
-      (const T*)z, px, (T*)out, w, (int)B, (int)N, Np, residual, eps_in, eps_out);
+  {
+    StageTimer timer("trimul_epilogue", st);
+    trimul_epilogue_kernel<T, CZ, CH><<<(unsigned)((etiles + 3) / 4), 256, 0, st>>>(
+        (const T*)z, px, (T*)out, w, (int)B, (int)N, Np, residual, eps_in, eps_out);
+  }
   GTK_LAUNCH_CHECK();
   return GTK_OK;
 }

@@ -180,6 +180,16 @@ int gtk_tri_attn_forward(const void* x, const float* mask, void* out, const void
                          int residual, float eps, int dtype, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Per-kernel timing (instrumentation; no counterpart in the reference).
+ * gtk_timing_enable(1) makes every subsequent launch record a HIP event
+ * before and after each kernel on its stream; gtk_timing_report() waits for
+ * them and writes one line per kernel name, "name count total_ms min_ms
+ * max_ms\n", then clears the records.  gtk_timing_enable(0) stops recording.
+ * ------------------------------------------------------------------------ */
+int gtk_timing_enable(int on);
+int gtk_timing_report(char* buf, size_t buf_bytes);
+
 #ifdef __cplusplus
 }
 #endif

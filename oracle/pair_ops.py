@@ -53,8 +53,11 @@ def contract(a: np.ndarray, b: np.ndarray, outgoing: bool,
         b = b.swapaxes(1, 2)
     if rows is not None:
         a = a[:, list(rows)]
-    # per channel: X_c = A_c B_c^T with A_c[i, k] = a[i, k, c]
-    x = np.matmul(a.transpose(0, 3, 1, 2), b.transpose(0, 3, 2, 1))  # [B, C, I, J]
+    # per channel: X_c = A_c B_c^T with A_c[i, k] = a[i, k, c]; contiguous
+    # operands keep np.matmul on its BLAS path
+    ac = np.ascontiguousarray(a.transpose(0, 3, 1, 2))
+    bc = np.ascontiguousarray(b.transpose(0, 3, 1, 2))
+    x = np.matmul(ac, bc.swapaxes(-1, -2))  # [B, C, I, J]
     return x.transpose(0, 2, 3, 1)
 
 
