@@ -49,10 +49,15 @@ def _run(cmd: list[str]) -> None:
         print(out)
 
 
+# Per-source extra flags.  tri_attn.hip: the softmax never sees NaN, and
+# without NaN semantics chains of fmaxf fuse into v_max3_f32.
+EXTRA_FLAGS = {"tri_attn.hip": ["-fno-honor-nans"]}
+
+
 def _compile_hip(src: str) -> Path:
     obj = BUILD / (Path(src).stem + ".o")
     lang = ["-x", "hip"] if src.endswith(".cpp") else []
-    _run([HIPCC, *HIP_FLAGS, *lang, "-c", str(CSRC / src), "-o", str(obj)])
+    _run([HIPCC, *HIP_FLAGS, *EXTRA_FLAGS.get(src, []), *lang, "-c", str(CSRC / src), "-o", str(obj)])
     return obj
 
 

@@ -8,9 +8,10 @@
 //
 //  1. prologue: per pair, LN -> q (pre-scaled by log2(e)/sqrt(d)), k, v,
 //     gate sigmoid(. + b_g) and the triangle bias (scaled by log2(e)), all on
-//     the matrix cores.  Workspace layouts (Np = N rounded up to 64):
+//     the matrix cores.  Workspace layouts (Np = N rounded up to 128):
 //        q, k  [B][Np r][H][Np j][32]     v^T [B][Np r][H][32][Np j]
-//        gate  [B][Np r][Np j][c_h]       bias [B][H][Np q][Np k] (fp32)
+//        gate  [B][Np r][Np j][c_h]       bias [B][H][Np q][Np k]
+//     (all in the compute type: bf16 for bf16 inputs, fp32 for fp32)
 //  2. flash core: one wave = one head x 32 queries of one row; keys in tiles
 //     of 32.  S^T = K Q^T is accumulated on top of the bias tile, so lane l
 //     owns one query and 16 of its keys; the row max needs one lane^32
@@ -53,9 +54,11 @@ static TriAttnPacked<T> carve_triattn(Carve& cv, int cin, int ch, int H) {
 }
 
 template <typename T> struct AttnWs {
-  T *q, *k, *vt, *gate;
-  float* bias;
+  T *q, *k, *vt, *gate, *bias;
 };
+
+// Rows and positions are padded to a multiple of the flash kernel's query block.
+inline int64_t attn_pad(int64_t N) { return round_up(N, 128); }
 
 template <typename T>
 static AttnWs<T> carve_attn_ws(Carve& cv, int64_t B, int64_t Np, int H, int ch) {
@@ -65,7 +68,7 @@ static AttnWs<T> carve_attn_ws(Carve& cv, int64_t B, int64_t Np, int H, int ch) 
   w.k = cv.take<T>(qkv);
   w.vt = cv.take<T>(qkv);
   w.gate = cv.take<T>(ch > 0 ? B * Np * Np * ch : 0);
-  w.bias = cv.take<float>(B * H * Np * Np);
+  w.bias = cv.take<T>(B * H * Np * Np);
   return w;
 }
 
@@ -136,7 +139,7 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
     if (half == 0) {
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr)
-        if (rr < H) ws.bias[(((int64_t)b * H + rr) * Np + r) * Np + j] = ab[rr] * keep;
+        if (rr < H) ws.bias[(((int64_t)b * H + rr) * Np + r) * Np + j] = cvt<T>(ab[rr] * keep);
     }
     if (H > 4) {
 #pragma unroll
@@ -144,7 +147,7 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int h = 8 * g + 4 * half + rr;
-          if (h >= 4 && h < H) ws.bias[(((int64_t)b * H + h) * Np + r) * Np + j] = ab[4 * g + rr] * keep;
+          if (h >= 4 && h < H) ws.bias[(((int64_t)b * H + h) * Np + r) * Np + j] = cvt<T>(ab[4 * g + rr] * keep);
         }
     }
   }
@@ -162,7 +165,7 @@ struct MaskView {
 template <typename T>
 __device__ __forceinline__ f32x16 flash_row_head(const T* __restrict__ qh, const T* __restrict__ kh,
                                                  const T* __restrict__ vth,
-                                                 const float* __restrict__ biash, MaskView mv,
+                                                 const T* __restrict__ biash, MaskView mv,
                                                  int q0, int N, int Np) {
   const int lane = threadIdx.x & 63;
   const int half = lane >> 5;
@@ -186,7 +189,7 @@ __device__ __forceinline__ f32x16 flash_row_head(const T* __restrict__ qh, const
     if (row_valid) qf[m].load(qh + (int64_t)(q0 + t32) * HD + m * 16 + half * 8);
     else qf[m].zero();
   }
-  const float* brow = biash + (int64_t)(q0 + t32) * Np;
+  const T* brow = biash + (int64_t)(q0 + t32) * Np;
 
   f32x16 o = zero16();
   float m_run = -INFINITY, l_run = 0.f;
@@ -339,6 +342,235 @@ __global__ __launch_bounds__(64 * H) void triattn_fused_kernel(const T* __restri
 }
 
 // ---------------------------------------------------------------------------
+// 3c. bf16 module kernel: 1024 threads = H heads x 4 query tiles of 32, for a
+//     block of 128 queries of one row.  Key blocks of 64 keys (K rows and V^T
+//     columns of every head) are staged through double-buffered LDS and
+//     shared by the 4 waves of each head.  The triangle bias enters on the
+//     matrix cores: S^T += I . Bias^T with a constant identity fragment, so
+//     the bias tile needs no VALU work and is read as 16-byte bf16 fragments.
+//     Online softmax with lazy rescaling: the running reference max only
+//     moves when a tile exceeds it by more than 8 (log2 units), so O and l
+//     are rescaled rarely; exponentials stay <= 2^8 and the result is exact
+//     after the final division by l.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float lane_pair_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float lane_pair_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <int CIN, int H>
+__global__ __launch_bounds__(1024) void triattn_flash_kernel(
+    const bf16* __restrict__ x, const float* __restrict__ mask, bf16* __restrict__ out,
+    TriAttnPacked<bf16> w, AttnWs<bf16> ws, int N, int Np, int starting, int residual) {
+  constexpr int CH = H * HD;
+  constexpr int QB = 128;                  // queries per block
+  constexpr int QT = QB / 32;              // query tiles (waves) per head
+  constexpr int KB = 64;                   // keys per staged block
+  constexpr int KP = HD + 8;               // K row pitch in LDS (80 B)
+  constexpr int VP = KB + 8;               // V^T row pitch in LDS (144 B)
+  constexpr int OP = CH + 8;               // gated-o row pitch in LDS
+  constexpr float kRescale = 8.0f;         // lazy-rescale threshold (log2 units)
+  static_assert(H * QT * 64 == 1024, "block is 16 waves");
+  static_assert(QB * OP <= 2 * H * KB * KP, "o staging must fit in the K buffers");
+  __shared__ __attribute__((aligned(16))) bf16 kbuf[2][H][KB][KP];
+  __shared__ __attribute__((aligned(16))) bf16 vbuf[2][H][HD][VP];
+  __shared__ __attribute__((aligned(16))) float kbias[2][KB];
+  __shared__ int kflag[2];
+  __shared__ int row_any;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int half = lane >> 5;
+  const int t32 = lane & 31;
+  const int h = wave / QT;
+  const int qt = wave % QT;
+  const int qblocks = (N + QB - 1) / QB;
+  const int qb = blockIdx.x % qblocks;
+  const int r = (blockIdx.x / qblocks) % N;
+  const int b = blockIdx.x / (qblocks * N);
+  const int q0 = qb * QB + qt * 32;
+  const int64_t rowbase = (int64_t)b * Np + r;
+
+  // mask of this row: key k is pair (r, k) (starting) or (k, r) (ending)
+  const float* mrow = mask ? mask + (int64_t)b * N * N + (starting ? (int64_t)r * N : r) : nullptr;
+  const int64_t mks = starting ? 1 : N;
+  if (tid == 0) row_any = mrow ? 0 : 1;
+  __syncthreads();
+  if (mrow) {
+    bool any = false;
+    for (int k = tid; k < N; k += 1024) any = any || (mrow[k * mks] != 0.f);
+    if (__ballot(any) != 0ull && lane == 0) row_any = 1;
+  }
+  __syncthreads();
+  const bool row_valid = row_any != 0;
+  const bool use_kbias = (mrow != nullptr) || (N % KB != 0);
+
+  // query fragments (zero for a row without valid keys: uniform attention)
+  Frag<bf16> qf[2];
+  const bf16* qrow = ws.q + ((rowbase * H + h) * Np + q0 + t32) * HD;
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    if (row_valid) qf[m].load(qrow + m * 16 + half * 8);
+    else qf[m].zero();
+  }
+  // identity fragments: row key (t32), slot half*8+e of chunk cb <-> key cb*16+half*8+e
+  Frag<bf16> idf[2];
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) idf[cb].v[e] = (bf16)((t32 == cb * 16 + half * 8 + e) ? 1.0f : 0.0f);
+  const bf16* brow = ws.bias + ((int64_t)(b * H + h) * Np + q0 + t32) * Np;
+
+  // staging: thread tid moves one 16-byte chunk of K and one of V^T per block
+  const int sh = tid >> 8, srem = tid & 255;
+  const int k_key = srem >> 2, k_part = srem & 3;
+  const int v_d = srem >> 3, v_part = srem & 7;
+  const bf16* ksrc = ws.k + ((rowbase * H + sh) * Np + k_key) * HD + k_part * 8;
+  const bf16* vsrc = ws.vt + ((rowbase * H + sh) * HD + v_d) * (int64_t)Np + v_part * 8;
+  bf16x8 kreg, vreg;
+  auto gload = [&](int k0) {
+    kreg = *reinterpret_cast<const bf16x8*>(ksrc + (int64_t)k0 * HD);
+    vreg = *reinterpret_cast<const bf16x8*>(vsrc + k0);
+  };
+  auto sstore = [&](int s, int k0) {
+    *reinterpret_cast<bf16x8*>(&kbuf[s][sh][k_key][k_part * 8]) = kreg;
+    *reinterpret_cast<bf16x8*>(&vbuf[s][sh][v_d][v_part * 8]) = vreg;
+    if (use_kbias && tid < KB) {
+      const int k = k0 + tid;
+      bool ex = k >= N;
+      if (!ex && row_valid && mrow) ex = mrow[k * mks] == 0.f;
+      kbias[s][tid] = ex ? -INFINITY : 0.f;
+      const unsigned long long anyex = __ballot(ex);
+      if (tid == 0) kflag[s] = anyex != 0ull;
+    }
+  };
+
+  f32x16 o = zero16();
+  float m_ref = -INFINITY, l_run = 0.f;
+  const int nkb = (N + KB - 1) / KB;
+  gload(0);
+  sstore(0, 0);
+  __syncthreads();
+  for (int kb = 0; kb < nkb; ++kb) {
+    const int cur = kb & 1;
+    const int k0 = kb * KB;
+    if (kb + 1 < nkb) gload(k0 + KB);
+    Frag<bf16> bfr[2][2];
+    if (row_valid) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) bfr[kt][cb].load(brow + k0 + kt * 32 + cb * 16 + half * 8);
+    }
+    const bool masked_blk = use_kbias && kflag[cur];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      f32x16 s = zero16();
+      if (row_valid) {
+        mma(s, idf[0], bfr[kt][0]);
+        mma(s, idf[1], bfr[kt][1]);
+#pragma unroll
+        for (int m = 0; m < 2; ++m) {
+          Frag<bf16> kf;
+          kf.load(&kbuf[cur][h][kt * 32 + t32][m * 16 + half * 8]);
+          mma(s, kf, qf[m]);
+        }
+      }
+      if (masked_blk) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 kb4 = *reinterpret_cast<const f32x4*>(&kbias[cur][kt * 32 + 8 * g + 4 * half]);
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) s[4 * g + rr] += kb4[rr];
+        }
+      }
+      float mt = fmaxf(fmaxf(s[0], s[1]), s[2]);
+#pragma unroll
+      for (int e = 3; e < 15; e += 2) mt = fmaxf(fmaxf(mt, s[e]), s[e + 1]);
+      mt = fmaxf(mt, s[15]);
+      mt = lane_pair_max(mt);
+      if (__ballot(mt > m_ref + kRescale) != 0ull) {
+        const float m_new = fmaxf(m_ref, mt);
+        const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[e] *= alpha;
+        m_ref = m_new;
+      }
+      const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
+      float ls = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        s[e] = __builtin_amdgcn_exp2f(s[e] - m_use);
+        ls += s[e];
+      }
+      l_run += ls;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        Frag<bf16> pf, vf;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pf.v[e] = (bf16)s[8 * c + e];
+        const bf16* vr = &vbuf[cur][h][t32][kt * 32 + 16 * c + 4 * half];
+        const bf16x4 v0 = *reinterpret_cast<const bf16x4*>(vr);
+        const bf16x4 v1 = *reinterpret_cast<const bf16x4*>(vr + 8);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) { vf.v[e] = v0[e]; vf.v[4 + e] = v1[e]; }
+        mma(o, vf, pf);
+      }
+    }
+    if (kb + 1 < nkb) sstore(cur ^ 1, k0 + KB);
+    __syncthreads();
+  }
+  const float inv = 1.0f / lane_pair_sum(l_run);
+
+  // o * gate for all heads, staged as [query][CH] over the K buffers
+  bf16* os = &kbuf[0][0][0][0];
+  {
+    const bf16* gr = ws.gate + (rowbase * Np + q0 + t32) * CH + h * HD;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 8 * g + 4 * half;
+      const f32x4 gv = load4f(gr + d0);
+      store4(os + (qt * 32 + t32) * OP + h * HD + d0, o[4 * g] * inv * gv[0],
+             o[4 * g + 1] * inv * gv[1], o[4 * g + 2] * inv * gv[2], o[4 * g + 3] * inv * gv[3]);
+    }
+  }
+  __syncthreads();
+  // output projection: wave -> (query tile, output tile)
+  constexpr int NT = CIN / 32;
+  for (int t = wave; t < QT * NT; t += H * QT) {
+    const int oq = t / NT, nt = t % NT;
+    Frag<bf16> of[CH / 16];
+#pragma unroll
+    for (int ks = 0; ks < CH / 16; ++ks) of[ks].load(os + (oq * 32 + t32) * OP + half * (CH / 2) + ks * 8);
+    const f32x16 acc = row_gemm_tile<bf16, CH, true>(of, w.w_o, nt);
+    const int q = qb * QB + oq * 32 + t32;
+    if (q < N) {
+      const int p0 = starting ? r : q, p1 = starting ? q : r;
+      const int64_t pair = ((int64_t)b * N + p0) * N + p1;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c0 = nt * 32 + 8 * g + 4 * half;
+        float v[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) v[rr] = acc[4 * g + rr] + w.b_o[c0 + rr];
+        if (residual) {
+          const f32x4 xr = load4f(x + pair * CIN + c0);
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) v[rr] += xr[rr];
+        }
+        store4(out + pair * CIN + c0, v[0], v[1], v[2], v[3]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // 3b. Raw attention op: relayout of q/k/v/bias, then flash per (row, head).
 // ---------------------------------------------------------------------------
 // src: [B][H][N][N][D]; element (b, h, a1, a2, d).  Destination row/position:
@@ -362,7 +594,8 @@ __global__ void relayout_qkv_kernel(const T* __restrict__ src, T* __restrict__ d
   else dst[(base * Np + j) * HD + d] = cvt<T>(v);
 }
 
-__global__ void relayout_bias_kernel(const float* __restrict__ src, float* __restrict__ dst,
+template <typename T>
+__global__ void relayout_bias_kernel(const float* __restrict__ src, T* __restrict__ dst,
                                      int B, int H, int N, int Np) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = (int64_t)B * H * N * N;
@@ -371,7 +604,7 @@ __global__ void relayout_bias_kernel(const float* __restrict__ src, float* __res
   const int64_t t = idx / N;
   const int q = (int)(t % N);
   const int64_t bh = t / N;
-  dst[(bh * Np + q) * Np + k] = src[idx] * kLog2e;
+  dst[(bh * Np + q) * Np + k] = cvt<T>(src[idx] * kLog2e);
 }
 
 template <typename T>
@@ -412,7 +645,7 @@ template <typename T>
 static int raw_attention(const void* q, const void* k, const void* v, const float* bias,
                          const float* mask, float scale, void* out, int64_t B, int64_t H,
                          int64_t N, void* ws, int starting, hipStream_t st) {
-  const int Np = (int)round_up(N, 64);
+  const int Np = (int)attn_pad(N);
   Carve cv(ws, SIZE_MAX);
   AttnWs<T> w = carve_attn_ws<T>(cv, B, Np, (int)H, 0);
   // zero the padded workspace so padded keys/queries read finite values
@@ -427,7 +660,7 @@ static int raw_attention(const void* q, const void* k, const void* v, const floa
   relayout_qkv_kernel<T><<<g1, 256, 0, st>>>((const T*)v, w.vt, (int)B, (int)H, (int)N, Np, starting, 1, 1.f);
   GTK_LAUNCH_CHECK();
   const int64_t tb = B * H * N * N;
-  relayout_bias_kernel<<<(unsigned)((tb + 255) / 256), 256, 0, st>>>(bias, w.bias, (int)B, (int)H, (int)N, Np);
+  relayout_bias_kernel<T><<<(unsigned)((tb + 255) / 256), 256, 0, st>>>(bias, w.bias, (int)B, (int)H, (int)N, Np);
   GTK_LAUNCH_CHECK();
   const int64_t blocks = B * N * H * ((N + 31) / 32);
   GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "attention grid too large");
@@ -486,7 +719,7 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
   constexpr int CH = H * HD;
   Carve pc((void*)packed, SIZE_MAX);
   TriAttnPacked<T> w = carve_triattn<T>(pc, CIN, CH, H);
-  const int Np = (int)round_up(N, 64);
+  const int Np = (int)attn_pad(N);
   Carve cv(ws, SIZE_MAX);
   AttnWs<T> a = carve_attn_ws<T>(cv, B, Np, H, CH);
   const int64_t ptiles = B * (int64_t)Np * (Np / 32);
@@ -498,7 +731,12 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
   GTK_LAUNCH_CHECK();
   const int64_t blocks = B * N * ((N + 31) / 32);
   GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "attention grid too large");
-  {
+  if constexpr (sizeof(T) == 2) {
+    const int64_t fblocks = B * N * ((N + 127) / 128);
+    StageTimer timer("triattn_flash", st);
+    triattn_flash_kernel<CIN, H><<<(unsigned)fblocks, 1024, 0, st>>>(
+        (const bf16*)x, mask, (bf16*)out, w, a, (int)N, Np, starting, residual);
+  } else {
     StageTimer timer("triattn_flash", st);
     triattn_fused_kernel<T, CIN, H><<<(unsigned)blocks, 64 * H, 0, st>>>(
         (const T*)x, mask, (T*)out, w, a, (int)B, (int)N, Np, starting, residual);
@@ -519,8 +757,8 @@ extern "C" size_t gtk_triangle_attention_workspace_size(int64_t B, int64_t H, in
                                                         int dtype) {
   if (B < 0 || H < 1 || N < 0 || D != HD) return 0;
   Carve cv(nullptr, SIZE_MAX);
-  if (dtype == GTK_F32) carve_attn_ws<float>(cv, B, round_up(N, 64), (int)H, 0);
-  else carve_attn_ws<bf16>(cv, B, round_up(N, 64), (int)H, 0);
+  if (dtype == GTK_F32) carve_attn_ws<float>(cv, B, attn_pad(N), (int)H, 0);
+  else carve_attn_ws<bf16>(cv, B, attn_pad(N), (int)H, 0);
   return cv.off;
 }
 
@@ -571,8 +809,8 @@ extern "C" size_t gtk_tri_attn_workspace_size(int64_t B, int64_t N, int64_t c_in
                                               int64_t H, int dtype) {
   if (!triattn_shape_ok(c_in, c_h, H) || B < 0 || N < 0) return 0;
   Carve cv(nullptr, SIZE_MAX);
-  if (dtype == GTK_F32) carve_attn_ws<float>(cv, B, round_up(N, 64), (int)H, (int)c_h);
-  else carve_attn_ws<bf16>(cv, B, round_up(N, 64), (int)H, (int)c_h);
+  if (dtype == GTK_F32) carve_attn_ws<float>(cv, B, attn_pad(N), (int)H, (int)c_h);
+  else carve_attn_ws<bf16>(cv, B, attn_pad(N), (int)H, (int)c_h);
   return cv.off;
 }
 
