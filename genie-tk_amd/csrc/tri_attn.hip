@@ -60,6 +60,14 @@ template <typename T> struct AttnWs {
 // Rows and positions are padded to a multiple of the flash kernel's query block.
 inline int64_t attn_pad(int64_t N) { return round_up(N, 128); }
 
+// Position of key j inside a V^T row: within each group of 16 keys, keys
+// 4..7 and 8..11 trade places, so that the 8 keys one lane feeds to the PV
+// product (16c + 4h + {0..3} and 16c + 8 + 4h + {0..3}, h = lane half) are
+// 8 consecutive elements at 16c + 8h.
+__host__ __device__ __forceinline__ int vt_pos(int j) {
+  return (j & ~15) | (j & 3) | ((j & 4) << 1) | ((j & 8) >> 1);
+}
+
 template <typename T>
 static AttnWs<T> carve_attn_ws(Carve& cv, int64_t B, int64_t Np, int H, int ch) {
   AttnWs<T> w;
@@ -111,7 +119,7 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
     const f32x16 av = row_gemm_tile<T, CIN, true>(xf, w.w_v, h);
     T* qd = ws.q + ((rowbase * H + h) * Np + j) * HD;
     T* kd = ws.k + ((rowbase * H + h) * Np + j) * HD;
-    T* vd = ws.vt + (rowbase * H + h) * HD * (int64_t)Np + j;
+    T* vd = ws.vt + (rowbase * H + h) * HD * (int64_t)Np + vt_pos(j);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int d0 = 8 * g + 4 * half;
@@ -246,14 +254,9 @@ __device__ __forceinline__ f32x16 flash_row_head(const T* __restrict__ qh, const
 #pragma unroll
       for (int e = 0; e < 8; ++e) pv[e] = s[8 * c + e];
       pf.set(pv);
-      // V^T fragment: row d = t32; slots e<4 -> key 16c+4h+e, e>=4 -> key 16c+8+4h+(e-4)
-      const T* vr = vth + (int64_t)t32 * Np + k0 + 16 * c + 4 * half;
-      float vv[8];
-      const f32x4 v0 = load4f(vr);
-      const f32x4 v1 = load4f(vr + 8);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) { vv[e] = v0[e]; vv[4 + e] = v1[e]; }
-      vf.set(vv);
+      // V^T fragment: row d = t32; slots e<4 -> key 16c+4h+e, e>=4 -> key
+      // 16c+8+4h+(e-4): 8 consecutive elements at 16c+8h (see vt_pos)
+      vf.load(vth + (int64_t)t32 * Np + k0 + 16 * c + 8 * half);
       mma(o, vf, pf);
     }
   }
@@ -343,15 +346,19 @@ __global__ __launch_bounds__(64 * H) void triattn_fused_kernel(const T* __restri
 
 // ---------------------------------------------------------------------------
 // 3c. bf16 module kernel: 1024 threads = H heads x 4 query tiles of 32, for a
-//     block of 128 queries of one row.  Key blocks of 64 keys (K rows and V^T
-//     columns of every head) are staged through double-buffered LDS and
-//     shared by the 4 waves of each head.  The triangle bias enters on the
-//     matrix cores: S^T += I . Bias^T with a constant identity fragment, so
-//     the bias tile needs no VALU work and is read as 16-byte bf16 fragments.
-//     Online softmax with lazy rescaling: the running reference max only
-//     moves when a tile exceeds it by more than 8 (log2 units), so O and l
-//     are rescaled rarely; exponentials stay <= 2^8 and the result is exact
-//     after the final division by l.
+//     block of 128 queries of one row.
+//   * Key blocks of 64 keys (K rows and V^T columns of all heads, 32 KiB)
+//     stream into a 3-stage LDS ring with direct global->LDS loads
+//     (global_load_lds_dwordx4), issued two blocks ahead: no staging VGPRs,
+//     one barrier per block.  Tiles are XOR-swizzled in 16-byte chunks so the
+//     fragment reads are bank-conflict free.
+//   * The triangle bias enters on the matrix cores: S^T += I . Bias^T with a
+//     constant identity fragment, so the bias tile needs no VALU work; its
+//     16-byte bf16 fragments for the next block are fetched as soon as the
+//     current ones have been consumed.
+//   * Online softmax with lazy rescaling: the reference max only moves when a
+//     tile exceeds it by more than 8 (log2 units); exponentials stay <= 2^8
+//     and the result is exact after the final division by l.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ float lane_pair_max(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -362,6 +369,20 @@ __device__ __forceinline__ float lane_pair_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+// Hardware deals consecutive block ids to the 8 XCDs round-robin; remap so
+// each XCD receives a contiguous range of logical blocks.
+__device__ __forceinline__ int64_t xcd_remap(int64_t lin, int64_t total) {
+  if (total % 8 != 0) return lin;
+  return (lin % 8) * (total / 8) + lin / 8;
+}
+
+// 16 bytes per lane from global memory into LDS at (wave-uniform base) + lane*16.
+__device__ __forceinline__ void g2lds16(const void* gptr, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(gptr, (lds_void_ptr)lds_wave_base, 16, 0, 0);
+}
+
 template <int CIN, int H>
 __global__ __launch_bounds__(1024) void triattn_flash_kernel(
     const bf16* __restrict__ x, const float* __restrict__ mask, bf16* __restrict__ out,
@@ -369,17 +390,17 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
   constexpr int CH = H * HD;
   constexpr int QB = 128;                  // queries per block
   constexpr int QT = QB / 32;              // query tiles (waves) per head
-  constexpr int KB = 64;                   // keys per staged block
-  constexpr int KP = HD + 8;               // K row pitch in LDS (80 B)
-  constexpr int VP = KB + 8;               // V^T row pitch in LDS (144 B)
-  constexpr int OP = CH + 8;               // gated-o row pitch in LDS
+  constexpr int KB = 64;                   // keys per stage
+  constexpr int NS = 3;                    // LDS ring stages
+  constexpr int OP = CH + 8;               // gated-o row pitch in LDS (elements)
+  constexpr int HEAD_BYTES = KB * HD * 2;  // K (or V^T) bytes of one head per stage: 4 KiB
+  constexpr int STAGE_BYTES = 2 * H * HEAD_BYTES;
   constexpr float kRescale = 8.0f;         // lazy-rescale threshold (log2 units)
-  static_assert(H * QT * 64 == 1024, "block is 16 waves");
-  static_assert(QB * OP <= 2 * H * KB * KP, "o staging must fit in the K buffers");
-  __shared__ __attribute__((aligned(16))) bf16 kbuf[2][H][KB][KP];
-  __shared__ __attribute__((aligned(16))) bf16 vbuf[2][H][HD][VP];
-  __shared__ __attribute__((aligned(16))) float kbias[2][KB];
-  __shared__ int kflag[2];
+  static_assert(H == 4 && H * QT * 64 == 1024, "block is 16 waves");
+  static_assert(QB * OP * 2 <= NS * STAGE_BYTES, "o staging must fit in the ring");
+  __shared__ __attribute__((aligned(1024))) char ring[NS][STAGE_BYTES];
+  __shared__ __attribute__((aligned(16))) float kbias[NS][KB];
+  __shared__ int kflag[NS];
   __shared__ int row_any;
 
   const int tid = threadIdx.x;
@@ -390,9 +411,11 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
   const int h = wave / QT;
   const int qt = wave % QT;
   const int qblocks = (N + QB - 1) / QB;
-  const int qb = blockIdx.x % qblocks;
-  const int r = (blockIdx.x / qblocks) % N;
-  const int b = blockIdx.x / (qblocks * N);
+  // XCD-aware order: the query blocks of one row run back to back on one XCD
+  const int64_t lin = xcd_remap(blockIdx.x, gridDim.x);
+  const int qb = (int)(lin % qblocks);
+  const int r = (int)((lin / qblocks) % N);
+  const int b = (int)(lin / ((int64_t)qblocks * N));
   const int q0 = qb * QB + qt * 32;
   const int64_t rowbase = (int64_t)b * Np + r;
 
@@ -410,6 +433,47 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
   const bool row_valid = row_any != 0;
   const bool use_kbias = (mrow != nullptr) || (N % KB != 0);
 
+  // Async stage load.  A stage is 32 regions of 1 KiB (64 lanes x 16 B);
+  // wave w moves regions 2w and 2w+1.  Regions 0..15: K, head reg/4, chunks
+  // P = (reg%4)*64 + lane of that head's [64 keys][32 d] tile; regions
+  // 16..31: V^T, head (reg-16)/4, chunks of its [32 d][64 keys] tile.
+  // Physical chunk P of a K tile holds row P/4, logical chunk
+  // (P%4) ^ ((row>>1)&3); of a V^T tile row d = P/8, logical chunk (P%8) ^ (d&7).
+  const bf16* kbase = ws.k + (rowbase * H) * (int64_t)Np * HD;
+  const bf16* vbase = ws.vt + (rowbase * H) * (int64_t)HD * Np;
+  const bool k_region = wave < 8;          // waves 0..7 move K, 8..15 move V^T
+  const int rg_head = (wave & 7) >> 1;
+  const int rg_sub0 = (wave & 1) * 2;
+  auto issue_stage = [&](int stage, int k0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int sub = rg_sub0 + i;
+      const int P = sub * 64 + lane;
+      const void* g;
+      char* dst;
+      if (k_region) {
+        const int row = P >> 2;
+        const int c = (P & 3) ^ ((row >> 1) & 3);
+        g = kbase + ((int64_t)rg_head * Np + k0 + row) * HD + c * 8;
+        dst = ring[stage] + rg_head * HEAD_BYTES + sub * 1024;
+      } else {
+        const int d = P >> 3;
+        const int c = (P & 7) ^ (d & 7);
+        g = vbase + ((int64_t)rg_head * HD + d) * Np + k0 + c * 8;
+        dst = ring[stage] + (H + rg_head) * HEAD_BYTES + sub * 1024;
+      }
+      g2lds16(g, dst);
+    }
+    if (use_kbias && wave == 0) {
+      const int k = k0 + lane;
+      bool ex = k >= N;
+      if (!ex && row_valid && mrow) ex = mrow[k * mks] == 0.f;
+      kbias[stage][lane] = ex ? -INFINITY : 0.f;
+      const unsigned long long anyex = __ballot(ex);
+      if (lane == 0) kflag[stage] = anyex != 0ull;
+    }
+  };
+
   // query fragments (zero for a row without valid keys: uniform attention)
   Frag<bf16> qf[2];
   const bf16* qrow = ws.q + ((rowbase * H + h) * Np + q0 + t32) * HD;
@@ -424,112 +488,106 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
   for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
     for (int e = 0; e < 8; ++e) idf[cb].v[e] = (bf16)((t32 == cb * 16 + half * 8 + e) ? 1.0f : 0.0f);
-  const bf16* brow = ws.bias + ((int64_t)(b * H + h) * Np + q0 + t32) * Np;
-
-  // staging: thread tid moves one 16-byte chunk of K and one of V^T per block
-  const int sh = tid >> 8, srem = tid & 255;
-  const int k_key = srem >> 2, k_part = srem & 3;
-  const int v_d = srem >> 3, v_part = srem & 7;
-  const bf16* ksrc = ws.k + ((rowbase * H + sh) * Np + k_key) * HD + k_part * 8;
-  const bf16* vsrc = ws.vt + ((rowbase * H + sh) * HD + v_d) * (int64_t)Np + v_part * 8;
-  bf16x8 kreg, vreg;
-  auto gload = [&](int k0) {
-    kreg = *reinterpret_cast<const bf16x8*>(ksrc + (int64_t)k0 * HD);
-    vreg = *reinterpret_cast<const bf16x8*>(vsrc + k0);
+  const bf16* brow = ws.bias + ((int64_t)(b * H + h) * Np + q0 + t32) * Np + half * 8;
+  Frag<bf16> bfr[2];  // bias fragments of the next S tile to issue
+  auto load_bias = [&](int t) {
+    if (row_valid) {
+      bfr[0].load(brow + t * 32);
+      bfr[1].load(brow + t * 32 + 16);
+    }
   };
-  auto sstore = [&](int s, int k0) {
-    *reinterpret_cast<bf16x8*>(&kbuf[s][sh][k_key][k_part * 8]) = kreg;
-    *reinterpret_cast<bf16x8*>(&vbuf[s][sh][v_d][v_part * 8]) = vreg;
-    if (use_kbias && tid < KB) {
-      const int k = k0 + tid;
-      bool ex = k >= N;
-      if (!ex && row_valid && mrow) ex = mrow[k * mks] == 0.f;
-      kbias[s][tid] = ex ? -INFINITY : 0.f;
-      const unsigned long long anyex = __ballot(ex);
-      if (tid == 0) kflag[s] = anyex != 0ull;
+  // S^T of 32-key tile t: I.Bias^T + K Q^T (zero for a row without valid keys)
+  auto s_tile = [&](int t, f32x16& s) {
+    s = zero16();
+    if (row_valid) {
+      mma(s, idf[0], bfr[0]);
+      mma(s, idf[1], bfr[1]);
+      const char* kt_base = ring[(t >> 1) % NS] + h * HEAD_BYTES;
+      const int row = (t & 1) * 32 + t32;
+#pragma unroll
+      for (int m = 0; m < 2; ++m) {
+        Frag<bf16> kf;
+        const int c = (m * 2 + half) ^ ((row >> 1) & 3);
+        kf.load(reinterpret_cast<const bf16*>(kt_base + row * 64 + c * 16));
+        mma(s, kf, qf[m]);
+      }
     }
   };
 
+  const int nkb = (N + KB - 1) / KB;
+  const int ntiles = 2 * nkb;
+  issue_stage(0, 0);
+  load_bias(0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (nkb > 1) issue_stage(1, KB);
+  f32x16 s_cur, s_next;
+  s_tile(0, s_cur);
+  if (ntiles > 1) load_bias(1);
+
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t ones2 = {(bf16)1.0f, (bf16)1.0f};
   f32x16 o = zero16();
   float m_ref = -INFINITY, l_run = 0.f;
-  const int nkb = (N + KB - 1) / KB;
-  gload(0);
-  sstore(0, 0);
-  __syncthreads();
-  for (int kb = 0; kb < nkb; ++kb) {
-    const int cur = kb & 1;
-    const int k0 = kb * KB;
-    if (kb + 1 < nkb) gload(k0 + KB);
-    Frag<bf16> bfr[2][2];
-    if (row_valid) {
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) bfr[kt][cb].load(brow + k0 + kt * 32 + cb * 16 + half * 8);
+  for (int t = 0; t < ntiles; ++t) {
+    // issue the next tile's S on the matrix cores before this tile's softmax
+    if (t + 1 < ntiles) {
+      if (((t + 1) & 1) == 0) {           // tile t+1 opens key block kb
+        const int kb = (t + 1) >> 1;
+        __builtin_amdgcn_s_waitcnt(0);    // stage kb and pending bias loads landed
+        __syncthreads();                  // ... for every wave; block kb-2 fully consumed
+        if (kb + 1 < nkb) issue_stage((kb + 1) % NS, (kb + 1) * KB);
+      }
+      s_tile(t + 1, s_next);
+      if (t + 2 < ntiles) load_bias(t + 2);
     }
-    const bool masked_blk = use_kbias && kflag[cur];
+    const int cur = (t >> 1) % NS;
+    if (use_kbias && kflag[cur]) {
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      f32x16 s = zero16();
-      if (row_valid) {
-        mma(s, idf[0], bfr[kt][0]);
-        mma(s, idf[1], bfr[kt][1]);
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 kb4 = *reinterpret_cast<const f32x4*>(&kbias[cur][(t & 1) * 32 + 8 * g + 4 * half]);
 #pragma unroll
-        for (int m = 0; m < 2; ++m) {
-          Frag<bf16> kf;
-          kf.load(&kbuf[cur][h][kt * 32 + t32][m * 16 + half * 8]);
-          mma(s, kf, qf[m]);
-        }
-      }
-      if (masked_blk) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 kb4 = *reinterpret_cast<const f32x4*>(&kbias[cur][kt * 32 + 8 * g + 4 * half]);
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) s[4 * g + rr] += kb4[rr];
-        }
-      }
-      float mt = fmaxf(fmaxf(s[0], s[1]), s[2]);
-#pragma unroll
-      for (int e = 3; e < 15; e += 2) mt = fmaxf(fmaxf(mt, s[e]), s[e + 1]);
-      mt = fmaxf(mt, s[15]);
-      mt = lane_pair_max(mt);
-      if (__ballot(mt > m_ref + kRescale) != 0ull) {
-        const float m_new = fmaxf(m_ref, mt);
-        const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
-        l_run *= alpha;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) o[e] *= alpha;
-        m_ref = m_new;
-      }
-      const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
-      float ls = 0.f;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        s[e] = __builtin_amdgcn_exp2f(s[e] - m_use);
-        ls += s[e];
-      }
-      l_run += ls;
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        Frag<bf16> pf, vf;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pf.v[e] = (bf16)s[8 * c + e];
-        const bf16* vr = &vbuf[cur][h][t32][kt * 32 + 16 * c + 4 * half];
-        const bf16x4 v0 = *reinterpret_cast<const bf16x4*>(vr);
-        const bf16x4 v1 = *reinterpret_cast<const bf16x4*>(vr + 8);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) { vf.v[e] = v0[e]; vf.v[4 + e] = v1[e]; }
-        mma(o, vf, pf);
+        for (int rr = 0; rr < 4; ++rr) s_cur[4 * g + rr] += kb4[rr];
       }
     }
-    if (kb + 1 < nkb) sstore(cur ^ 1, k0 + KB);
-    __syncthreads();
+    float mt = fmaxf(fmaxf(s_cur[0], s_cur[1]), s_cur[2]);
+#pragma unroll
+    for (int e = 3; e < 15; e += 2) mt = fmaxf(fmaxf(mt, s_cur[e]), s_cur[e + 1]);
+    mt = fmaxf(mt, s_cur[15]);
+    mt = lane_pair_max(mt);
+    if (__ballot(mt > m_ref + kRescale) != 0ull) {
+      const float m_new = fmaxf(m_ref, mt);
+      const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[e] *= alpha;
+      m_ref = m_new;
+    }
+    const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
+    const char* vt_base = ring[cur] + (H + h) * HEAD_BYTES;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      Frag<bf16> pf, vf;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pf.v[e] = (bf16)__builtin_amdgcn_exp2f(s_cur[8 * c + e] - m_use);
+      // row sum over the bf16 probabilities that enter P V
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const bf16x2_t pp = {pf.v[e], pf.v[e + 1]};
+        l_run = __builtin_amdgcn_fdot2_f32_bf16(pp, ones2, l_run, false);
+      }
+      // V^T row d = t32, keys (t&1)*32 + 16c + 8*half .. +8
+      const int lc = ((t & 1) * 4 + 2 * c + half) ^ (t32 & 7);
+      vf.load(reinterpret_cast<const bf16*>(vt_base + t32 * 128 + lc * 16));
+      mma(o, vf, pf);
+    }
+    s_cur = s_next;
   }
   const float inv = 1.0f / lane_pair_sum(l_run);
 
-  // o * gate for all heads, staged as [query][CH] over the K buffers
-  bf16* os = &kbuf[0][0][0][0];
+  // o * gate for all heads, staged as [query][CH] over the ring
+  __syncthreads();
+  bf16* os = reinterpret_cast<bf16*>(&ring[0][0]);
   {
     const bf16* gr = ws.gate + (rowbase * Np + q0 + t32) * CH + h * HD;
 #pragma unroll
@@ -543,8 +601,8 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
   __syncthreads();
   // output projection: wave -> (query tile, output tile)
   constexpr int NT = CIN / 32;
-  for (int t = wave; t < QT * NT; t += H * QT) {
-    const int oq = t / NT, nt = t % NT;
+  for (int tt = wave; tt < QT * NT; tt += H * QT) {
+    const int oq = tt / NT, nt = tt % NT;
     Frag<bf16> of[CH / 16];
 #pragma unroll
     for (int ks = 0; ks < CH / 16; ++ks) of[ks].load(os + (oq * 32 + t32) * OP + half * (CH / 2) + ks * 8);
@@ -590,7 +648,7 @@ __global__ void relayout_qkv_kernel(const T* __restrict__ src, T* __restrict__ d
   const int r = starting ? a1 : a2, j = starting ? a2 : a1;
   const int64_t base = ((int64_t)b * Np + r) * H + h;
   const float v = to_f32(src[idx]) * scale;
-  if (transpose_v) dst[(base * HD + d) * Np + j] = cvt<T>(v);
+  if (transpose_v) dst[(base * HD + d) * Np + vt_pos(j)] = cvt<T>(v);
   else dst[(base * Np + j) * HD + d] = cvt<T>(v);
 }
 
