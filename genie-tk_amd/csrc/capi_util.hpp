@@ -36,6 +36,10 @@ void set_error(const char* fmt, ...);
 
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
+// Compute units of the current device (cached per device; persistent kernels
+// launch one block per CU).
+int device_cus();
+
 // Per-kernel timing (gtk_timing_enable / gtk_timing_report): when enabled, a
 // StageTimer records one HIP event before and one after the launch it
 // scopes, on the launch stream.  Disabled, it costs one relaxed load.

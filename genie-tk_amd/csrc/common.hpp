@@ -117,7 +117,10 @@ __device__ __forceinline__ float xor32(float v) { return __shfl_xor(v, 32, 64); 
 // Lane l holds pair row (l & 31), channels half*C/2 + [0, C/2) as C/16
 // fragments of 8.  The row statistics combine the lane's own half with lane
 // (l ^ 32)'s half.  Two-pass (mean, then centred sum of squares), biased
-// variance, eps inside the square root: y = (x - mu) / sqrt(var + eps) * w + b.
+// variance, eps inside the square root: x_hat = (x - mu) / sqrt(var + eps).
+// The LayerNorm weight w and bias b never reach the kernels: a LayerNorm
+// followed by a linear map W, c is computed as (W diag(w)) x_hat + (W b + c),
+// with both terms prepared when the weights are packed.
 // ---------------------------------------------------------------------------
 template <int C> struct RowHalf {
   static constexpr int NCH = C / 16;  // fragments per lane
@@ -161,18 +164,56 @@ __device__ __forceinline__ f32x2 row_stats(const RowHalf<C>& r, float eps) {
   return f32x2{mean, 1.0f / sqrtf(var + eps)};
 }
 
-// Normalise + affine, then pack into MFMA fragments of type T.
+// Normalise (no affine: the LayerNorm weight and bias are folded into the
+// packed weights of the linear map that follows), then pack into fragments.
 template <typename T, int C>
-__device__ __forceinline__ void ln_to_frags(Frag<T>* frags, const RowHalf<C>& r, f32x2 st,
-                                            const float* __restrict__ w, const float* __restrict__ b) {
-  const int half = (threadIdx.x & 63) >> 5;
+__device__ __forceinline__ void ln_to_frags(Frag<T>* frags, const RowHalf<C>& r, f32x2 st) {
 #pragma unroll
   for (int ch = 0; ch < C / 16; ++ch) {
     float f[8];
-    const int c0 = half * (C / 2) + ch * 8;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = (r.v[ch * 8 + e] - st[0]) * st[1] * w[c0 + e] + b[c0 + e];
+    for (int e = 0; e < 8; ++e) f[e] = (r.v[ch * 8 + e] - st[0]) * st[1];
     frags[ch].set(f);
+  }
+}
+
+// Row-tile LayerNorm (normalise only) straight from bf16 storage into bf16
+// fragments: the raw
+// half row stays packed (C/4 VGPRs) and is widened on the fly, so the peak
+// register footprint is two sets of packed fragments.
+template <int C>
+__device__ __forceinline__ void ln_row_bf16(Frag<bf16>* xf, const bf16* row_base, bool valid,
+                                            float eps) {
+  const int half = (threadIdx.x & 63) >> 5;
+  Frag<bf16> raw[C / 16];
+#pragma unroll
+  for (int ch = 0; ch < C / 16; ++ch) {
+    if (valid) raw[ch].load(row_base + half * (C / 2) + ch * 8);
+    else raw[ch].zero();
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int ch = 0; ch < C / 16; ++ch)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s += raw[ch].get(e);
+  s += xor32(s);
+  const float mean = s * (1.0f / C);
+  float q = 0.f;
+#pragma unroll
+  for (int ch = 0; ch < C / 16; ++ch)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float d = raw[ch].get(e) - mean;
+      q += d * d;
+    }
+  q += xor32(q);
+  const float rstd = 1.0f / sqrtf(q * (1.0f / C) + eps);
+#pragma unroll
+  for (int ch = 0; ch < C / 16; ++ch) {
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = (raw[ch].get(e) - mean) * rstd;
+    xf[ch].set(f);
   }
 }
 
@@ -188,6 +229,44 @@ template <typename T>
 __device__ __forceinline__ void load_wfrag(Frag<T>& f, const T* __restrict__ packed, int nt, int ks, int kch) {
   const int l = threadIdx.x & 63;
   f.load(packed + ((size_t)(nt * kch + ks) * 64 + l) * 8);
+}
+
+// Same fragment from a packed weight copy resident in LDS (64 lanes read
+// 1 KiB contiguous: bank-conflict free).
+__device__ __forceinline__ void load_wfrag_lds(Frag<bf16>& f, const bf16* packed_lds, int nt, int ks,
+                                               int kch) {
+  const int l = threadIdx.x & 63;
+  f.load(packed_lds + ((nt * kch + ks) * 64 + l) * 8);
+}
+
+typedef __attribute__((address_space(3))) void* lds_void_ptr;
+
+// 16 bytes per lane from global memory straight into LDS at
+// (wave-uniform base) + lane * 16 (global_load_lds_dwordx4, no VGPR staging).
+__device__ __forceinline__ void g2lds16(const void* gptr, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(gptr, (lds_void_ptr)lds_wave_base, 16, 0, 0);
+}
+
+// Asynchronously copy `bytes` (a multiple of 1 KiB) from global memory into
+// LDS with the whole block: every load is issued before any is waited for.
+// The caller waits (s_waitcnt vmcnt(0)) and synchronises the block.
+__device__ __forceinline__ void copy_to_lds_async(void* dst, const void* __restrict__ src, int bytes) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+  for (int blk = wave; blk * 1024 < bytes; blk += nwaves)
+    g2lds16((const char*)src + blk * 1024 + lane * 16, (char*)dst + blk * 1024);
+}
+
+// acc = A . B with a zero accumulator input (inline constant, no register init).
+__device__ __forceinline__ f32x16 mma0(const Frag<bf16>& a, const Frag<bf16>& b) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.v, b.v, zero16(), 0, 0, 0);
+}
+
+// sigmoid(x) for u = -x * log2(e) (gate projections are packed pre-scaled):
+// 1 / (1 + 2^u) with the hardware reciprocal.
+__device__ __forceinline__ float gate_from_u(float u) {
+  return __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(u));
 }
 
 // acc(32 pairs x 32 outputs of tile nt) = rows . W_nt^T over K = C.

@@ -129,13 +129,13 @@ static int launch_ln(const T* x, T* y, const float* g, const float* b, int64_t r
 }
 
 // ---------------------------------------------------------------------------
-// LayerNorm + Linear: y = LN(x) @ W + bias, W packed (see pack.hpp).
-// One wave = 32 rows; lane (l&31) owns a row, (l>>5) a channel half.
+// LayerNorm + Linear: y = LN(x) @ W + bias with the LayerNorm affine folded
+// in: y = x_hat @ (diag(gamma) W) + (beta @ W + bias), both prepared in the
+// workspace (see pack.hpp).  One wave = 32 rows; lane (l&31) owns a row,
+// (l>>5) a channel half.
 // ---------------------------------------------------------------------------
 template <typename T, int DIN>
 __global__ __launch_bounds__(256) void ln_linear_kernel(const T* __restrict__ x, T* __restrict__ y,
-                                                        const float* __restrict__ gamma,
-                                                        const float* __restrict__ beta,
                                                         const T* __restrict__ wp,
                                                         const float* __restrict__ bias,
                                                         int64_t rows, int d_out, float eps) {
@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256) void ln_linear_kernel(const T* __restrict__ x,
   load_row_half<T, DIN>(rh, x + (valid ? row : 0) * DIN, valid);
   const f32x2 st = row_stats<DIN>(rh, eps);
   Frag<T> xf[DIN / 16];
-  ln_to_frags<T, DIN>(xf, rh, st, gamma, beta);
+  ln_to_frags<T, DIN>(xf, rh, st);
   const int ntiles = (d_out + 31) / 32;
   for (int nt = 0; nt < ntiles; ++nt) {
     const f32x16 acc = row_gemm_tile<T, DIN, true>(xf, wp, nt);
@@ -160,7 +160,7 @@ __global__ __launch_bounds__(256) void ln_linear_kernel(const T* __restrict__ x,
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int o = o0 + r;
-        if (o < d_out) y[row * d_out + o] = cvt<T>(acc[4 * g + r] + (bias ? bias[o] : 0.f));
+        if (o < d_out) y[row * d_out + o] = cvt<T>(acc[4 * g + r] + bias[o]);
       }
     }
   }
@@ -184,9 +184,24 @@ extern "C" int gtk_layernorm(const void* x, void* y, const float* gamma, const f
   return launch_ln<bf16>((const bf16*)x, (bf16*)y, gamma, beta, rows, d, eps, st);
 }
 
+// Workspace: packed diag(gamma) W, then the folded bias (fp32, d_out).
+template <typename T>
+static void carve_ln_linear(Carve& cv, int64_t d_in, int64_t d_out, T** wp, float** bias) {
+  *wp = cv.take<T>(packed_elems(d_out, d_in));
+  *bias = cv.take<float>(d_out);
+}
+
 extern "C" size_t gtk_fused_layernorm_linear_workspace_size(int64_t d_in, int64_t d_out, int dtype) {
   if (d_in < 16 || d_out < 1) return 0;
-  return (size_t)packed_elems(d_out, d_in) * dtype_size(dtype);
+  Carve cv(nullptr, SIZE_MAX);
+  if (dtype == GTK_F32) {
+    float* w; float* b;
+    carve_ln_linear<float>(cv, d_in, d_out, &w, &b);
+  } else {
+    bf16* w; float* b;
+    carve_ln_linear<bf16>(cv, d_in, d_out, &w, &b);
+  }
+  return cv.off;
 }
 
 extern "C" int gtk_fused_layernorm_linear(const void* x, void* y, const float* gamma,
@@ -211,24 +226,35 @@ extern "C" int gtk_fused_layernorm_linear(const void* x, void* y, const float* g
   hipStream_t st = (hipStream_t)stream;
   const unsigned grid = (unsigned)(((rows + 31) / 32 + 3) / 4);
   // weight is [d_in][d_out]: logical W[out][in] has s_out = 1, s_in = d_out.
+  // The caller's bias has fp32 type; the folded bias starts from it.
   int rc;
+  Carve cv(workspace, workspace_bytes);
+  float* fb;
   if (dtype == GTK_F32) {
-    float* wp = (float*)workspace;
-    if ((rc = launch_pack<float>(wp, weight, weight_dtype, (int)d_out, (int)d_in, 1, d_out, 1.f, st)))
+    float* wp;
+    carve_ln_linear<float>(cv, d_in, d_out, &wp, &fb);
+    if ((rc = launch_pack<float>(wp, weight, weight_dtype, (int)d_out, (int)d_in, 1, d_out, 1.f, st, gamma)))
       return rc;
+    if ((rc = launch_fold_bias(fb, weight, nullptr, weight_dtype, beta, (int)d_out, (int)d_in, 1, d_out, 1.f, st)))
+      return rc;
+    if (bias && (rc = launch_add_f32(fb, bias, (int)d_out, st))) return rc;
     switch (d_in) {
-      case 64: ln_linear_kernel<float, 64><<<grid, 256, 0, st>>>((const float*)x, (float*)y, gamma, beta, wp, bias, rows, (int)d_out, eps); break;
-      case 128: ln_linear_kernel<float, 128><<<grid, 256, 0, st>>>((const float*)x, (float*)y, gamma, beta, wp, bias, rows, (int)d_out, eps); break;
-      default: ln_linear_kernel<float, 256><<<grid, 256, 0, st>>>((const float*)x, (float*)y, gamma, beta, wp, bias, rows, (int)d_out, eps); break;
+      case 64: ln_linear_kernel<float, 64><<<grid, 256, 0, st>>>((const float*)x, (float*)y, wp, fb, rows, (int)d_out, eps); break;
+      case 128: ln_linear_kernel<float, 128><<<grid, 256, 0, st>>>((const float*)x, (float*)y, wp, fb, rows, (int)d_out, eps); break;
+      default: ln_linear_kernel<float, 256><<<grid, 256, 0, st>>>((const float*)x, (float*)y, wp, fb, rows, (int)d_out, eps); break;
     }
   } else {
-    bf16* wp = (bf16*)workspace;
-    if ((rc = launch_pack<bf16>(wp, weight, weight_dtype, (int)d_out, (int)d_in, 1, d_out, 1.f, st)))
+    bf16* wp;
+    carve_ln_linear<bf16>(cv, d_in, d_out, &wp, &fb);
+    if ((rc = launch_pack<bf16>(wp, weight, weight_dtype, (int)d_out, (int)d_in, 1, d_out, 1.f, st, gamma)))
       return rc;
+    if ((rc = launch_fold_bias(fb, weight, nullptr, weight_dtype, beta, (int)d_out, (int)d_in, 1, d_out, 1.f, st)))
+      return rc;
+    if (bias && (rc = launch_add_f32(fb, bias, (int)d_out, st))) return rc;
     switch (d_in) {
-      case 64: ln_linear_kernel<bf16, 64><<<grid, 256, 0, st>>>((const bf16*)x, (bf16*)y, gamma, beta, wp, bias, rows, (int)d_out, eps); break;
-      case 128: ln_linear_kernel<bf16, 128><<<grid, 256, 0, st>>>((const bf16*)x, (bf16*)y, gamma, beta, wp, bias, rows, (int)d_out, eps); break;
-      default: ln_linear_kernel<bf16, 256><<<grid, 256, 0, st>>>((const bf16*)x, (bf16*)y, gamma, beta, wp, bias, rows, (int)d_out, eps); break;
+      case 64: ln_linear_kernel<bf16, 64><<<grid, 256, 0, st>>>((const bf16*)x, (bf16*)y, wp, fb, rows, (int)d_out, eps); break;
+      case 128: ln_linear_kernel<bf16, 128><<<grid, 256, 0, st>>>((const bf16*)x, (bf16*)y, wp, fb, rows, (int)d_out, eps); break;
+      default: ln_linear_kernel<bf16, 256><<<grid, 256, 0, st>>>((const bf16*)x, (bf16*)y, wp, fb, rows, (int)d_out, eps); break;
     }
   }
   GTK_LAUNCH_CHECK();

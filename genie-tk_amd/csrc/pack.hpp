@@ -15,10 +15,12 @@ inline int64_t packed_elems(int64_t out_dim, int64_t k_dim) {
   return ((out_dim + 31) / 32) * (k_dim / 16) * 512;
 }
 
+// `gamma` (optional, fp32 [k_dim]) scales input column k: packing W diag(gamma)
+// folds a preceding LayerNorm's elementwise weight into the linear map.
 template <typename Tout, typename Tin>
 __global__ void pack_weight_kernel(Tout* __restrict__ dst, const Tin* __restrict__ src, int out_dim,
                                    int k_dim, int64_t s_out, int64_t s_in, float scale,
-                                   int64_t total) {
+                                   const float* __restrict__ gamma, int64_t total) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= total) return;
   const int kch = k_dim / 16;
@@ -30,8 +32,24 @@ __global__ void pack_weight_kernel(Tout* __restrict__ dst, const Tin* __restrict
   const int o = nt * 32 + (l & 31);
   const int k = (l >> 5) * (k_dim / 2) + ks * 8 + e;
   float v = 0.f;
-  if (o < out_dim) v = scale * to_f32(src[o * s_out + k * s_in]);
+  if (o < out_dim) v = scale * to_f32(src[o * s_out + k * s_in]) * (gamma ? gamma[k] : 1.f);
   dst[idx] = cvt<Tout>(v);
+}
+
+// dst[o] = scale * (bias[o] + sum_k W[o][k] * beta[k]): the bias of a linear
+// map applied after a LayerNorm whose elementwise bias beta is folded in.
+template <typename Tin>
+__global__ void fold_bias_kernel(float* __restrict__ dst, const Tin* __restrict__ w,
+                                 const void* __restrict__ bias, int bias_bf16,
+                                 const float* __restrict__ beta, int out_dim, int k_dim,
+                                 int64_t s_out, int64_t s_in, float scale) {
+  const int o = blockIdx.x * blockDim.x + threadIdx.x;
+  if (o >= out_dim) return;
+  float acc = 0.f;
+  if (bias) acc = bias_bf16 ? (float)((const bf16*)bias)[o] : ((const float*)bias)[o];
+  if (beta)
+    for (int k = 0; k < k_dim; ++k) acc += to_f32(w[o * s_out + k * s_in]) * beta[k];
+  dst[o] = scale * acc;
 }
 
 template <typename Tin>
@@ -45,15 +63,32 @@ __global__ void to_f32_kernel(float* __restrict__ dst, const Tin* __restrict__ s
 // Pack W (element type `wdtype`) into dst (element type Tout).
 template <typename Tout>
 inline int launch_pack(Tout* dst, const void* src, int wdtype, int out_dim, int k_dim,
-                       int64_t s_out, int64_t s_in, float scale, hipStream_t st) {
+                       int64_t s_out, int64_t s_in, float scale, hipStream_t st,
+                       const float* gamma = nullptr) {
   const int64_t total = packed_elems(out_dim, k_dim);
   const int blocks = (int)((total + 255) / 256);
   if (wdtype == GTK_F32)
     pack_weight_kernel<Tout, float><<<blocks, 256, 0, st>>>(dst, (const float*)src, out_dim, k_dim,
-                                                            s_out, s_in, scale, total);
+                                                            s_out, s_in, scale, gamma, total);
   else
     pack_weight_kernel<Tout, bf16><<<blocks, 256, 0, st>>>(dst, (const bf16*)src, out_dim, k_dim,
-                                                           s_out, s_in, scale, total);
+                                                           s_out, s_in, scale, gamma, total);
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+// Bias of a linear map with a LayerNorm beta folded in (see fold_bias_kernel);
+// `bias` has the weights' element type, or is null.
+inline int launch_fold_bias(float* dst, const void* w, const void* bias, int wdtype,
+                            const float* beta, int out_dim, int k_dim, int64_t s_out, int64_t s_in,
+                            float scale, hipStream_t st) {
+  const int blocks = (out_dim + 63) / 64;
+  if (wdtype == GTK_F32)
+    fold_bias_kernel<float><<<blocks, 64, 0, st>>>(dst, (const float*)w, bias, 0, beta, out_dim,
+                                                    k_dim, s_out, s_in, scale);
+  else
+    fold_bias_kernel<bf16><<<blocks, 64, 0, st>>>(dst, (const bf16*)w, bias, 1, beta, out_dim,
+                                                   k_dim, s_out, s_in, scale);
   GTK_LAUNCH_CHECK();
   return GTK_OK;
 }
@@ -66,6 +101,16 @@ inline int launch_to_f32(float* dst, const void* src, int dtype, int n, float sc
     to_f32_kernel<float><<<blocks, 256, 0, st>>>(dst, (const float*)src, n, scale, fill);
   else
     to_f32_kernel<bf16><<<blocks, 256, 0, st>>>(dst, (const bf16*)src, n, scale, fill);
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+static __global__ void add_f32_kernel(float* __restrict__ dst, const float* __restrict__ src, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] += src[i];
+}
+inline int launch_add_f32(float* dst, const float* src, int n, hipStream_t st) {
+  add_f32_kernel<<<(n + 255) / 256, 256, 0, st>>>(dst, src, n);
   GTK_LAUNCH_CHECK();
   return GTK_OK;
 }

@@ -32,9 +32,15 @@ namespace gtk {
 
 constexpr int HD = 32;  // head dimension handled by the kernels
 
+// Packed parameters of one TriangleAttention.  The LayerNorm weight is folded
+// into w_q/w_k/w_v/w_g/w_b and its bias into b_q/b_k/b_v/b_g/b_b (b = W beta
+// + c); w_q and b_q also carry log2(e)/sqrt(d), w_b and b_b carry log2(e), so
+// that the softmax runs on exp2; w_g and b_g carry -log2(e) (gate = 1 /
+// (1 + 2^u)).  ln_* are fp32 copies used while packing.
 template <typename T> struct TriAttnPacked {
   T *w_q, *w_k, *w_v, *w_g, *w_b, *w_o;
-  float *ln_w, *ln_b, *b_g, *b_o;
+  float *b_q, *b_k, *b_v, *b_g, *b_b, *b_o;
+  float *ln_w, *ln_b;
 };
 
 template <typename T>
@@ -46,10 +52,14 @@ static TriAttnPacked<T> carve_triattn(Carve& cv, int cin, int ch, int H) {
   p.w_g = cv.take<T>(packed_elems(ch, cin));
   p.w_b = cv.take<T>(packed_elems(H, cin));
   p.w_o = cv.take<T>(packed_elems(cin, ch));
+  p.b_q = cv.take<float>(ch);
+  p.b_k = cv.take<float>(ch);
+  p.b_v = cv.take<float>(ch);
+  p.b_g = cv.take<float>(ch);
+  p.b_b = cv.take<float>(32);
+  p.b_o = cv.take<float>(cin);
   p.ln_w = cv.take<float>(cin);
   p.ln_b = cv.take<float>(cin);
-  p.b_g = cv.take<float>(ch);
-  p.b_o = cv.take<float>(cin);
   return p;
 }
 
@@ -107,7 +117,7 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
   load_row_half<T, CIN>(rh, x + pair * CIN, valid);
   const f32x2 st = row_stats<CIN>(rh, eps);
   Frag<T> xf[CIN / 16];
-  ln_to_frags<T, CIN>(xf, rh, st, w.ln_w, w.ln_b);
+  ln_to_frags<T, CIN>(xf, rh, st);
   const float keep = valid ? 1.f : 0.f;
 
   const int64_t rowbase = ((int64_t)b * Np + r);  // (b, r)
@@ -123,10 +133,15 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int d0 = 8 * g + 4 * half;
-      store4(qd + d0, aq[4 * g] * keep, aq[4 * g + 1] * keep, aq[4 * g + 2] * keep, aq[4 * g + 3] * keep);
-      store4(kd + d0, ak[4 * g] * keep, ak[4 * g + 1] * keep, ak[4 * g + 2] * keep, ak[4 * g + 3] * keep);
+      const float* bq = w.b_q + h * HD + d0;
+      const float* bk = w.b_k + h * HD + d0;
+      const float* bv = w.b_v + h * HD + d0;
+      store4(qd + d0, (aq[4 * g] + bq[0]) * keep, (aq[4 * g + 1] + bq[1]) * keep,
+             (aq[4 * g + 2] + bq[2]) * keep, (aq[4 * g + 3] + bq[3]) * keep);
+      store4(kd + d0, (ak[4 * g] + bk[0]) * keep, (ak[4 * g + 1] + bk[1]) * keep,
+             (ak[4 * g + 2] + bk[2]) * keep, (ak[4 * g + 3] + bk[3]) * keep);
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) vd[(int64_t)(d0 + rr) * Np] = cvt<T>(av[4 * g + rr] * keep);
+      for (int rr = 0; rr < 4; ++rr) vd[(int64_t)(d0 + rr) * Np] = cvt<T>((av[4 * g + rr] + bv[rr]) * keep);
     }
   }
   // gate: [b][r][j][CH]
@@ -137,8 +152,8 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int c0 = nt * 32 + 8 * g + 4 * half;
-      store4(gd + c0, sigmoidf_(ag[4 * g] + w.b_g[c0]), sigmoidf_(ag[4 * g + 1] + w.b_g[c0 + 1]),
-             sigmoidf_(ag[4 * g + 2] + w.b_g[c0 + 2]), sigmoidf_(ag[4 * g + 3] + w.b_g[c0 + 3]));
+      store4(gd + c0, gate_from_u(ag[4 * g] + w.b_g[c0]), gate_from_u(ag[4 * g + 1] + w.b_g[c0 + 1]),
+             gate_from_u(ag[4 * g + 2] + w.b_g[c0 + 2]), gate_from_u(ag[4 * g + 3] + w.b_g[c0 + 3]));
     }
   }
   // triangle bias: [b][h][r][j] (rows h >= H of the packed tile are zero)
@@ -147,7 +162,7 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
     if (half == 0) {
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr)
-        if (rr < H) ws.bias[(((int64_t)b * H + rr) * Np + r) * Np + j] = cvt<T>(ab[rr] * keep);
+        if (rr < H) ws.bias[(((int64_t)b * H + rr) * Np + r) * Np + j] = cvt<T>((ab[rr] + w.b_b[rr]) * keep);
     }
     if (H > 4) {
 #pragma unroll
@@ -155,7 +170,7 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int h = 8 * g + 4 * half + rr;
-          if (h >= 4 && h < H) ws.bias[(((int64_t)b * H + h) * Np + r) * Np + j] = cvt<T>(ab[4 * g + rr] * keep);
+          if (h >= 4 && h < H) ws.bias[(((int64_t)b * H + h) * Np + r) * Np + j] = cvt<T>((ab[4 * g + rr] + w.b_b[h]) * keep);
         }
     }
   }
@@ -369,8 +384,6 @@ __device__ __forceinline__ float lane_pair_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-typedef __attribute__((address_space(3))) void* lds_void_ptr;
-
 // Hardware deals consecutive block ids to the 8 XCDs round-robin; remap so
 // each XCD receives a contiguous range of logical blocks.
 __device__ __forceinline__ int64_t xcd_remap(int64_t lin, int64_t total) {
@@ -378,10 +391,6 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t lin, int64_t total) {
   return (lin % 8) * (total / 8) + lin / 8;
 }
 
-// 16 bytes per lane from global memory into LDS at (wave-uniform base) + lane*16.
-__device__ __forceinline__ void g2lds16(const void* gptr, void* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(gptr, (lds_void_ptr)lds_wave_base, 16, 0, 0);
-}
 
 template <int CIN, int H>
 __global__ __launch_bounds__(1024) void triattn_flash_kernel(
@@ -758,15 +767,22 @@ static int pack_triattn(const gtk_tri_attn_weights* w, int cin, int ch, int H, v
   const int wd = w->dtype;
   const float qscale = kLog2e / sqrtf((float)(ch / H));
   int rc;
-  if ((rc = launch_pack<T>(p.w_q, w->q_w, wd, ch, cin, cin, 1, qscale, st))) return rc;
-  if ((rc = launch_pack<T>(p.w_k, w->k_w, wd, ch, cin, cin, 1, 1.f, st))) return rc;
-  if ((rc = launch_pack<T>(p.w_v, w->v_w, wd, ch, cin, cin, 1, 1.f, st))) return rc;
-  if ((rc = launch_pack<T>(p.w_g, w->g_w, wd, ch, cin, cin, 1, 1.f, st))) return rc;
-  if ((rc = launch_pack<T>(p.w_b, w->tri_w, wd, H, cin, cin, 1, kLog2e, st))) return rc;
-  if ((rc = launch_pack<T>(p.w_o, w->o_w, wd, cin, ch, ch, 1, 1.f, st))) return rc;
   if ((rc = launch_to_f32(p.ln_w, w->ln_w, wd, cin, 1.f, 1.f, st))) return rc;
   if ((rc = launch_to_f32(p.ln_b, w->ln_b, wd, cin, 1.f, 0.f, st))) return rc;
-  if ((rc = launch_to_f32(p.b_g, w->g_b, wd, ch, 1.f, 0.f, st))) return rc;
+  // nn.Linear weight [out][in]: s_out = in, s_in = 1.  Linears after the LayerNorm.
+  struct Lin { T* dst; float* bdst; const void* wsrc; const void* bsrc; int out; float scale; };
+  const Lin lins[5] = {{p.w_q, p.b_q, w->q_w, nullptr, ch, qscale},
+                       {p.w_k, p.b_k, w->k_w, nullptr, ch, 1.f},
+                       {p.w_v, p.b_v, w->v_w, nullptr, ch, 1.f},
+                       {p.w_g, p.b_g, w->g_w, w->g_b, ch, -kLog2e},
+                       {p.w_b, p.b_b, w->tri_w, nullptr, H, kLog2e}};
+  for (const Lin& l : lins) {
+    if ((rc = launch_pack<T>(l.dst, l.wsrc, wd, l.out, cin, cin, 1, l.scale, st, p.ln_w))) return rc;
+    if ((rc = launch_fold_bias(l.bdst, l.wsrc, l.bsrc, wd, p.ln_b, l.out, cin, cin, 1, l.scale, st)))
+      return rc;
+  }
+  // output projection acts on the gated attention output (no LayerNorm)
+  if ((rc = launch_pack<T>(p.w_o, w->o_w, wd, cin, ch, ch, 1, 1.f, st))) return rc;
   if ((rc = launch_to_f32(p.b_o, w->o_b, wd, cin, 1.f, 0.f, st))) return rc;
   return GTK_OK;
 }

@@ -18,6 +18,8 @@
 //
 // Np = N rounded up to 64; the prologue writes zeros for padded pairs so the
 // contraction needs no bounds checks.
+#include <algorithm>
+
 #include "capi_util.hpp"
 #include "common.hpp"
 #include "pack.hpp"
@@ -25,9 +27,13 @@
 namespace gtk {
 
 // Packed parameters of one TriangleMultiplicativeUpdate, carved in this order.
+// The weights carry the LayerNorm weights folded in (w_ap..w_g: layer_norm_in,
+// w_z: layer_norm_out) and the biases the LayerNorm biases (b = W beta + c).
+// ln_* keep fp32 copies of the LayerNorm parameters, used only while packing.
 template <typename T> struct TriMulPacked {
   T *w_ap, *w_ag, *w_bp, *w_bg, *w_g, *w_z;
-  float *ln_in_w, *ln_in_b, *b_ap, *b_ag, *b_bp, *b_bg, *b_g, *ln_out_w, *ln_out_b, *b_z;
+  float *b_ap, *b_ag, *b_bp, *b_bg, *b_g, *b_z;
+  float *ln_in_w, *ln_in_b, *ln_out_w, *ln_out_b;
 };
 
 template <typename T>
@@ -39,16 +45,16 @@ static TriMulPacked<T> carve_trimul(Carve& cv, int cz, int c) {
   p.w_bg = cv.take<T>(packed_elems(c, cz));
   p.w_g = cv.take<T>(packed_elems(cz, cz));
   p.w_z = cv.take<T>(packed_elems(cz, c));
-  p.ln_in_w = cv.take<float>(cz);
-  p.ln_in_b = cv.take<float>(cz);
   p.b_ap = cv.take<float>(c);
   p.b_ag = cv.take<float>(c);
   p.b_bp = cv.take<float>(c);
   p.b_bg = cv.take<float>(c);
   p.b_g = cv.take<float>(cz);
+  p.b_z = cv.take<float>(cz);
+  p.ln_in_w = cv.take<float>(cz);
+  p.ln_in_b = cv.take<float>(cz);
   p.ln_out_w = cv.take<float>(c);
   p.ln_out_b = cv.take<float>(c);
-  p.b_z = cv.take<float>(cz);
   return p;
 }
 
@@ -87,7 +93,7 @@ __global__ __launch_bounds__(256) void trimul_prologue_kernel(
   load_row_half<T, CZ>(rh, z + pair * CZ, valid);
   const f32x2 st = row_stats<CZ>(rh, eps);
   Frag<T> xf[CZ / 16];
-  ln_to_frags<T, CZ>(xf, rh, st, w.ln_in_w, w.ln_in_b);
+  ln_to_frags<T, CZ>(xf, rh, st);
   const float m = valid ? (mask ? mask[pair] : 1.0f) : 0.0f;
 
   const int64_t plane = (int64_t)Np * Np;
@@ -108,8 +114,85 @@ __global__ __launch_bounds__(256) void trimul_prologue_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int c = nt * 32 + 8 * g + 4 * half + r;
-          const float val = (ap[4 * g + r] + bp[c]) * sigmoidf_(ag[4 * g + r] + bg[c]) * m;
+          const float val = (ap[4 * g + r] + bp[c]) * gate_from_u(ag[4 * g + r] + bg[c]) * m;
           dst[(int64_t)c * plane] = cvt<T>(val);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 1b. bf16 prologue: persistent, one 1024-thread block per CU with the four
+//     packed c_z->c weights resident in LDS (4 x 32 KiB, loaded with direct
+//     global->LDS copies); every wave then loops over 32-pair tiles with no
+//     further synchronisation.  Lane (l&31) owns one pair of the tile, so the
+//     mask is one value per lane and each plane store instruction writes two
+//     64-byte runs (32 consecutive pairs of two channels).
+// ---------------------------------------------------------------------------
+template <int CZ, int CH>
+__global__ __launch_bounds__(1024) void trimul_prologue_bf16_kernel(
+    const bf16* __restrict__ z, const float* __restrict__ mask, bf16* __restrict__ pa,
+    bf16* __restrict__ pb, TriMulPacked<bf16> w, int N, int Np, int outgoing, float eps,
+    int64_t ntiles) {
+  constexpr int KCH = CZ / 16;
+  constexpr int PE = (CH / 32) * KCH * 512;  // packed elements of one projection
+  __shared__ __attribute__((aligned(1024))) bf16 wl[4][PE];
+  copy_to_lds_async(wl[0], w.w_ap, PE * 2);
+  copy_to_lds_async(wl[1], w.w_ag, PE * 2);
+  copy_to_lds_async(wl[2], w.w_bp, PE * 2);
+  copy_to_lds_async(wl[3], w.w_bg, PE * 2);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int half = lane >> 5;
+  const int t32 = lane & 31;
+  const int vtiles = Np / 32;
+  const int64_t plane = (int64_t)Np * Np;
+  for (int64_t tile = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 6); tile < ntiles;
+       tile += (int64_t)gridDim.x * 16) {
+    const int vt = (int)(tile % vtiles);
+    const int f = (int)((tile / vtiles) % Np);
+    const int b = (int)(tile / ((int64_t)vtiles * Np));
+    const int v = vt * 32 + t32;
+    const int p = outgoing ? f : v, q = outgoing ? v : f;
+    const bool valid = p < N && q < N;
+    const int64_t pair = ((int64_t)b * N + (valid ? p : 0)) * N + (valid ? q : 0);
+    Frag<bf16> xf[KCH];
+    ln_row_bf16<CZ>(xf, z + pair * CZ, valid, eps);
+    const float mk = valid ? (mask ? mask[pair] : 1.f) : 0.f;
+#pragma unroll 1
+    for (int side = 0; side < 2; ++side) {
+      const bf16* wp = wl[2 * side];
+      const bf16* wg = wl[2 * side + 1];
+      const float* bp = side ? w.b_bp : w.b_ap;
+      const float* bg = side ? w.b_bg : w.b_ag;
+      bf16* dst = (side ? pb : pa) + (int64_t)b * CH * plane + (int64_t)f * Np + v;
+#pragma unroll 1
+      for (int ct = 0; ct < CH / 32; ++ct) {
+        Frag<bf16> wfp, wfg;
+        load_wfrag_lds(wfp, wp, ct, 0, KCH);
+        load_wfrag_lds(wfg, wg, ct, 0, KCH);
+        f32x16 ap = mma0(wfp, xf[0]);
+        f32x16 ag = mma0(wfg, xf[0]);
+#pragma unroll 1
+        for (int ks = 1; ks < KCH; ++ks) {
+          load_wfrag_lds(wfp, wp, ct, ks, KCH);
+          load_wfrag_lds(wfg, wg, ct, ks, KCH);
+          mma(ap, wfp, xf[ks]);
+          mma(ag, wfg, xf[ks]);
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int c0 = ct * 32 + 8 * g + 4 * half;
+          const f32x4 bp4 = *reinterpret_cast<const f32x4*>(bp + c0);
+          const f32x4 bg4 = *reinterpret_cast<const f32x4*>(bg + c0);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float o = (ap[4 * g + r] + bp4[r]) * gate_from_u(ag[4 * g + r] + bg4[r]) * mk;
+            dst[(int64_t)(c0 + r) * plane] = (bf16)o;
+          }
         }
       }
     }
@@ -251,7 +334,7 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(
     load_row_half<T, CZ>(rh, z + pair * CZ, valid);
     const f32x2 st = row_stats<CZ>(rh, eps_in);
     Frag<T> xf[CZ / 16];
-    ln_to_frags<T, CZ>(xf, rh, st, w.ln_in_w, w.ln_in_b);
+    ln_to_frags<T, CZ>(xf, rh, st);
 #pragma unroll
     for (int nt = 0; nt < CZ / 32; ++nt) {
       gate[nt] = row_gemm_tile<T, CZ, true>(xf, w.w_g, nt);
@@ -260,7 +343,7 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int c = nt * 32 + 8 * g + 4 * half + r;
-          gate[nt][4 * g + r] = sigmoidf_(gate[nt][4 * g + r] + w.b_g[c]);
+          gate[nt][4 * g + r] = gate_from_u(gate[nt][4 * g + r] + w.b_g[c]);
         }
     }
   }
@@ -298,7 +381,7 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(
   }
   const f32x2 st = row_stats<CH>(xh, eps_out);
   Frag<T> yf[CH / 16];
-  ln_to_frags<T, CH>(yf, xh, st, w.ln_out_w, w.ln_out_b);
+  ln_to_frags<T, CH>(yf, xh, st);
 
 #pragma unroll
   for (int nt = 0; nt < CZ / 32; ++nt) {
@@ -456,23 +539,28 @@ static int pack_trimul(const gtk_tri_mul_weights* w, int cz, int c, void* packed
   TriMulPacked<T> p = carve_trimul<T>(cv, cz, c);
   const int wd = w->dtype;
   int rc = 0;
-  // nn.Linear weight [out][in]: s_out = in, s_in = 1.
-  if ((rc = launch_pack<T>(p.w_ap, w->a_p_w, wd, c, cz, cz, 1, 1.f, st))) return rc;
-  if ((rc = launch_pack<T>(p.w_ag, w->a_g_w, wd, c, cz, cz, 1, 1.f, st))) return rc;
-  if ((rc = launch_pack<T>(p.w_bp, w->b_p_w, wd, c, cz, cz, 1, 1.f, st))) return rc;
-  if ((rc = launch_pack<T>(p.w_bg, w->b_g_w, wd, c, cz, cz, 1, 1.f, st))) return rc;
-  if ((rc = launch_pack<T>(p.w_g, w->g_w, wd, cz, cz, cz, 1, 1.f, st))) return rc;
-  if ((rc = launch_pack<T>(p.w_z, w->z_w, wd, cz, c, c, 1, 1.f, st))) return rc;
+  // fp32 LayerNorm parameters first: they are folded into what follows
   if ((rc = launch_to_f32(p.ln_in_w, w->ln_in_w, wd, cz, 1.f, 1.f, st))) return rc;
   if ((rc = launch_to_f32(p.ln_in_b, w->ln_in_b, wd, cz, 1.f, 0.f, st))) return rc;
-  if ((rc = launch_to_f32(p.b_ap, w->a_p_b, wd, c, 1.f, 0.f, st))) return rc;
-  if ((rc = launch_to_f32(p.b_ag, w->a_g_b, wd, c, 1.f, 0.f, st))) return rc;
-  if ((rc = launch_to_f32(p.b_bp, w->b_p_b, wd, c, 1.f, 0.f, st))) return rc;
-  if ((rc = launch_to_f32(p.b_bg, w->b_g_b, wd, c, 1.f, 0.f, st))) return rc;
-  if ((rc = launch_to_f32(p.b_g, w->g_b, wd, cz, 1.f, 0.f, st))) return rc;
   if ((rc = launch_to_f32(p.ln_out_w, w->ln_out_w, wd, c, 1.f, 1.f, st))) return rc;
   if ((rc = launch_to_f32(p.ln_out_b, w->ln_out_b, wd, c, 1.f, 0.f, st))) return rc;
-  if ((rc = launch_to_f32(p.b_z, w->z_b, wd, cz, 1.f, 0.f, st))) return rc;
+  // nn.Linear weight [out][in]: s_out = in, s_in = 1.
+  // Gate projections (a_g, b_g, g) are packed pre-scaled by -log2(e): the
+  // kernels evaluate sigmoid(x) as 1 / (1 + 2^u) with u = -log2(e) x.
+  struct Lin { T* dst; float* bdst; const void* wsrc; const void* bsrc; int out, in; const float *g, *beta; float scale; };
+  const float gs = -kLog2e;
+  const Lin lins[6] = {
+      {p.w_ap, p.b_ap, w->a_p_w, w->a_p_b, c, cz, p.ln_in_w, p.ln_in_b, 1.f},
+      {p.w_ag, p.b_ag, w->a_g_w, w->a_g_b, c, cz, p.ln_in_w, p.ln_in_b, gs},
+      {p.w_bp, p.b_bp, w->b_p_w, w->b_p_b, c, cz, p.ln_in_w, p.ln_in_b, 1.f},
+      {p.w_bg, p.b_bg, w->b_g_w, w->b_g_b, c, cz, p.ln_in_w, p.ln_in_b, gs},
+      {p.w_g, p.b_g, w->g_w, w->g_b, cz, cz, p.ln_in_w, p.ln_in_b, gs},
+      {p.w_z, p.b_z, w->z_w, w->z_b, cz, c, p.ln_out_w, p.ln_out_b, 1.f}};
+  for (const Lin& l : lins) {
+    if ((rc = launch_pack<T>(l.dst, l.wsrc, wd, l.out, l.in, l.in, 1, l.scale, st, l.g))) return rc;
+    if ((rc = launch_fold_bias(l.bdst, l.wsrc, l.bsrc, wd, l.beta, l.out, l.in, l.in, 1, l.scale, st)))
+      return rc;
+  }
   return GTK_OK;
 }
 
@@ -488,7 +576,12 @@ static int fwd_trimul(const void* z, const float* mask, void* out, const void* p
   T* pb = cv.take<T>(B * CH * (int64_t)Np * Np);
   T* px = cv.take<T>(B * CH * (int64_t)Np * Np);
   const int64_t ptiles = B * (int64_t)Np * (Np / 32);
-  {
+  if constexpr (sizeof(T) == 2) {
+    const int grid = (int)std::min<int64_t>(device_cus(), (ptiles + 15) / 16);
+    StageTimer timer("trimul_prologue", st);
+    trimul_prologue_bf16_kernel<CZ, CH><<<grid, 1024, 0, st>>>(
+        (const bf16*)z, mask, (bf16*)pa, (bf16*)pb, w, (int)N, Np, outgoing, eps_in, ptiles);
+  } else {
     StageTimer timer("trimul_prologue", st);
     trimul_prologue_kernel<T, CZ, CH><<<(unsigned)((ptiles + 3) / 4), 256, 0, st>>>(
         (const T*)z, mask, pa, pb, w, (int)B, (int)N, Np, outgoing, eps_in);
