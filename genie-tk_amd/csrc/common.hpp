@@ -99,6 +99,14 @@ __device__ __forceinline__ void store4(bf16* p, float a, float b, float c, float
 __device__ __forceinline__ void store4(float* p, float a, float b, float c, float d) {
   *reinterpret_cast<f32x4*>(p) = f32x4{a, b, c, d};
 }
+// Two values as packed bf16 (low half = a).
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  bf16x2 v;
+  v[0] = (bf16)a;
+  v[1] = (bf16)b;
+  return __builtin_bit_cast(uint32_t, v);
+}
 // Load 4 consecutive values as fp32.
 __device__ __forceinline__ f32x4 load4f(const bf16* p) {
   bf16x4 v = *reinterpret_cast<const bf16x4*>(p);

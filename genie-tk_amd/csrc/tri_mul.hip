@@ -126,9 +126,15 @@ __global__ __launch_bounds__(256) void trimul_prologue_kernel(
 // 1b. bf16 prologue: persistent, one 1024-thread block per CU with the four
 //     packed c_z->c weights resident in LDS (4 x 32 KiB, loaded with direct
 //     global->LDS copies); every wave then loops over 32-pair tiles with no
-//     further synchronisation.  Lane (l&31) owns one pair of the tile, so the
-//     mask is one value per lane and each plane store instruction writes two
-//     64-byte runs (32 consecutive pairs of two channels).
+//     further synchronisation.
+//
+//     The pairs are the MFMA A operand (rows) and the weights the B operand
+//     (columns = channels).  A-operand row i carries tile pair
+//     16*((i>>2)&1) + 4*(i>>3) + (i&3), which makes accumulator register j of
+//     lane l hold pair 16*(l>>5) + j of channel (l&31): every lane ends with 16
+//     consecutive pairs of one channel and writes them as two 16-byte stores.
+//     The gate bias enters as a factor, 2^(u+b) = 2^u * 2^b, so the gate costs
+//     one FMA beside its two transcendental instructions.
 // ---------------------------------------------------------------------------
 template <int CZ, int CH>
 __global__ __launch_bounds__(1024) void trimul_prologue_bf16_kernel(
@@ -147,7 +153,8 @@ __global__ __launch_bounds__(1024) void trimul_prologue_bf16_kernel(
 
   const int lane = threadIdx.x & 63;
   const int half = lane >> 5;
-  const int t32 = lane & 31;
+  const int i32 = lane & 31;
+  const int prow = 16 * ((i32 >> 2) & 1) + 4 * (i32 >> 3) + (i32 & 3);
   const int vtiles = Np / 32;
   const int64_t plane = (int64_t)Np * Np;
   for (int64_t tile = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 6); tile < ntiles;
@@ -155,45 +162,64 @@ __global__ __launch_bounds__(1024) void trimul_prologue_bf16_kernel(
     const int vt = (int)(tile % vtiles);
     const int f = (int)((tile / vtiles) % Np);
     const int b = (int)(tile / ((int64_t)vtiles * Np));
-    const int v = vt * 32 + t32;
-    const int p = outgoing ? f : v, q = outgoing ? v : f;
-    const bool valid = p < N && q < N;
-    const int64_t pair = ((int64_t)b * N + (valid ? p : 0)) * N + (valid ? q : 0);
     Frag<bf16> xf[KCH];
-    ln_row_bf16<CZ>(xf, z + pair * CZ, valid, eps);
-    const float mk = valid ? (mask ? mask[pair] : 1.f) : 0.f;
+    {
+      const int v = vt * 32 + prow;
+      const int p = outgoing ? f : v, q = outgoing ? v : f;
+      const bool valid = p < N && q < N;
+      const int64_t pair = ((int64_t)b * N + (valid ? p : 0)) * N + (valid ? q : 0);
+      ln_row_bf16<CZ>(xf, z + pair * CZ, valid, eps);
+    }
+    // mask of the 16 output pairs of this lane (zero outside the N x N pair grid)
+    float mk[16];
+    {
+      const int v0 = vt * 32 + 16 * half;
+      const bool frow = f < N;
+      const int64_t base = ((int64_t)b * N + (outgoing ? f : 0)) * N + (outgoing ? 0 : f);
+      const int64_t step = outgoing ? 1 : N;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const bool ok = frow && v0 + j < N;
+        mk[j] = ok ? (mask ? mask[base + (int64_t)(v0 + j) * step] : 1.f) : 0.f;
+      }
+    }
 #pragma unroll 1
     for (int side = 0; side < 2; ++side) {
       const bf16* wp = wl[2 * side];
       const bf16* wg = wl[2 * side + 1];
       const float* bp = side ? w.b_bp : w.b_ap;
       const float* bg = side ? w.b_bg : w.b_ag;
-      bf16* dst = (side ? pb : pa) + (int64_t)b * CH * plane + (int64_t)f * Np + v;
+      bf16* dst = (side ? pb : pa) + (int64_t)b * CH * plane + (int64_t)f * Np + vt * 32 + 16 * half;
 #pragma unroll 1
       for (int ct = 0; ct < CH / 32; ++ct) {
         Frag<bf16> wfp, wfg;
         load_wfrag_lds(wfp, wp, ct, 0, KCH);
         load_wfrag_lds(wfg, wg, ct, 0, KCH);
-        f32x16 ap = mma0(wfp, xf[0]);
-        f32x16 ag = mma0(wfg, xf[0]);
-#pragma unroll 1
+        f32x16 ap = mma0(xf[0], wfp);
+        f32x16 ag = mma0(xf[0], wfg);
+#pragma unroll
         for (int ks = 1; ks < KCH; ++ks) {
           load_wfrag_lds(wfp, wp, ct, ks, KCH);
           load_wfrag_lds(wfg, wg, ct, ks, KCH);
-          mma(ap, wfp, xf[ks]);
-          mma(ag, wfg, xf[ks]);
+          mma(ap, xf[ks], wfp);
+          mma(ag, xf[ks], wfg);
         }
+        const int cc = ct * 32 + i32;
+        const float bpc = bp[cc];
+        const float ebg = fmaxf(__builtin_amdgcn_exp2f(bg[cc]), 1.17549435e-38f);
+        uint32_t pk[8];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int c0 = ct * 32 + 8 * g + 4 * half;
-          const f32x4 bp4 = *reinterpret_cast<const f32x4*>(bp + c0);
-          const f32x4 bg4 = *reinterpret_cast<const f32x4*>(bg + c0);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float o = (ap[4 * g + r] + bp4[r]) * gate_from_u(ag[4 * g + r] + bg4[r]) * mk;
-            dst[(int64_t)(c0 + r) * plane] = (bf16)o;
-          }
+        for (int j = 0; j < 16; j += 2) {
+          const float o0 = (ap[j] + bpc) *
+                           __builtin_amdgcn_rcpf(fmaf(__builtin_amdgcn_exp2f(ag[j]), ebg, 1.f)) * mk[j];
+          const float o1 = (ap[j + 1] + bpc) *
+                           __builtin_amdgcn_rcpf(fmaf(__builtin_amdgcn_exp2f(ag[j + 1]), ebg, 1.f)) *
+                           mk[j + 1];
+          pk[j / 2] = pack_bf16x2(o0, o1);
         }
+        uint4* o = reinterpret_cast<uint4*>(dst + (int64_t)cc * plane);
+        o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        o[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
       }
     }
   }
