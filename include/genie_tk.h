@@ -79,7 +79,7 @@ int gtk_fused_layernorm_linear(const void* x, void* y, const float* gamma, const
  * incoming: x[b][i][j][c] = sum_k a[b][k][i][c] * b[b][k][j][c]
  * a, b, x: [B][N][N][C] of `dtype`.  `mask` ([B][N][N] float) is accepted for
  * signature compatibility and not read: a and b arrive masked.
- * C % 8 == 0.
+ * C % 16 == 0, N <= 16384.
  * ------------------------------------------------------------------------ */
 size_t gtk_triangle_mul_workspace_size(int64_t B, int64_t N, int64_t C, int dtype);
 int gtk_triangle_mul_outgoing(const void* a, const void* b, const float* mask, void* x, int64_t B,
@@ -103,7 +103,7 @@ int gtk_triangle_mul_incoming(const void* a, const void* b, const float* mask, v
  *                              + mask_bias[b,k,j] + bias[b,h,q,k]) * v[b,h,k,j,d]
  * mask_bias is -inf for mask == 0 keys; a row with no valid key attends
  * uniformly over all N keys (the limit of the reference's -1e9 additive
- * bias).  D == 32.
+ * bias).  D == 32, N <= 8192.
  * ------------------------------------------------------------------------ */
 size_t gtk_triangle_attention_workspace_size(int64_t B, int64_t H, int64_t N, int64_t D, int dtype);
 int gtk_triangle_attention_starting(const void* q, const void* k, const void* v, const float* bias,
@@ -125,7 +125,8 @@ int gtk_triangle_attention_ending(const void* q, const void* k, const void* v, c
  *   x   = outgoing ? einsum(bikc,bjkc->bijc) : einsum(bkic,bkjc->bijc)
  *   out = (LN_out(x) W_z^T + b_z) * sigmoid(zn W_g^T + b_g)   [+ z if residual]
  * Weights are first packed once with gtk_tri_mul_pack (the packed buffer
- * stays valid until the parameters change).  c_z == 128, c in {64, 128}.
+ * stays valid until the parameters change).  c_z == 128, c in {64, 128},
+ * N <= 16384.
  * ------------------------------------------------------------------------ */
 typedef struct gtk_tri_mul_weights {
   int dtype;                     /* element type of every pointer below */
@@ -158,7 +159,7 @@ int gtk_tri_mul_forward(const void* z, const float* mask, void* out, const void*
  *   o    = softmax(q k^T / sqrt(d) + mask_bias + tri) v        per row, head
  *   out  = (o * sigmoid(xn W_g^T + b_g)) W_o^T + b_o    [+ x if residual]
  * Mask semantics as gtk_triangle_attention_starting.
- * c_in == 128, H*d == c_h, d == 32, H <= 8.
+ * c_in == 128, H == 4, d == 32 (c_h == 128), N <= 8192.
  * ------------------------------------------------------------------------ */
 typedef struct gtk_tri_attn_weights {
   int dtype;                 /* element type of every pointer below */

@@ -133,3 +133,55 @@ def layer_norm(x: np.ndarray, w, b, eps: float = 1e-5) -> np.ndarray:
     for r in range(flat.shape[0]):
         of[r] = _ln([float(t) for t in flat[r]], w, b, eps)
     return out
+
+
+def contract(a: np.ndarray, b: np.ndarray, outgoing: bool) -> np.ndarray:
+    """x[b,i,j,c] = sum_k a[b,i,k,c] b[b,j,k,c] (outgoing, triangle_mul.py:77-89) or
+    sum_k a[b,k,i,c] b[b,k,j,c] (incoming, triangle_mul.py:91-101), element by element."""
+    B, N, _, C = a.shape
+    out = np.zeros((B, N, N, C))
+    for bb in range(B):
+        for i in range(N):
+            for j in range(N):
+                for c in range(C):
+                    s = 0.0
+                    for k in range(N):
+                        if outgoing:
+                            s += float(a[bb, i, k, c]) * float(b[bb, j, k, c])
+                        else:
+                            s += float(a[bb, k, i, c]) * float(b[bb, k, j, c])
+                    out[bb, i, j, c] = s
+    return out
+
+
+def attention_core(q, k, v, bias, mask, scale: float, starting: bool, inf: float = 1e9) -> np.ndarray:
+    """_C.triangle_attention_starting/ending semantics (kernels/bindings.cpp:82-90):
+    q, k, v [B,H,N,N,D]; bias [B,H,N,N] indexed (query, key); mask [B,N,N].
+    Starting: row i = axis 2, positions along axis 3; ending: row j = axis 3,
+    positions along axis 2.  Masked keys score -inf (uniform weights if a row
+    has no valid key).  Returns [B,N,N,H*D]."""
+    B, H, N, _, D = q.shape
+    out = np.zeros((B, N, N, H * D))
+
+    def at(r, j):
+        return (r, j) if starting else (j, r)
+
+    for bb in range(B):
+        for r in range(N):
+            for h in range(H):
+                for qi in range(N):
+                    logits = []
+                    for ki in range(N):
+                        s = sum(float(q[(bb, h) + at(r, qi) + (t,)]) * float(k[(bb, h) + at(r, ki) + (t,)])
+                                for t in range(D)) * scale
+                        s += float(bias[bb, h, qi, ki])
+                        if float(mask[(bb,) + at(r, ki)]) == 0.0:
+                            s = -inf
+                        logits.append(s)
+                    mx = max(logits)
+                    w = [math.exp(t - mx) for t in logits]
+                    tot = sum(w)
+                    for t in range(D):
+                        o = sum(w[ki] * float(v[(bb, h) + at(r, ki) + (t,)]) for ki in range(N)) / tot
+                        out[(bb,) + at(r, qi) + (h * D + t,)] = o
+    return out

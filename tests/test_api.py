@@ -1,0 +1,266 @@
+"""The genie_tk Python API on the CPU: names, constructors, parameters,
+PyTorch-path numerics against the oracle, the kernel/fallback switch and the
+utilities.  Mirrors the reference's tests/test_triangle_mul.py:26-111 and
+tests/test_triangle_attention.py:25-175 (shape, gradient flow, mask, pair
+transform) and adds value checks, since the reference's own checks pass on
+all-zero outputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+import genie_tk
+from genie_tk import (PairTransformLayer, PairTransformNet, TriangleAttention,
+                      TriangleAttentionEndingNode, TriangleAttentionStartingNode,
+                      TriangleMultiplicationIncoming, TriangleMultiplicationOutgoing,
+                      TriangleMultiplicativeUpdate)
+from genie_tk import utils
+from oracle import pair_ops
+from tests import helpers as H
+
+REFERENCE_ALL = [
+    "TriangleMultiplicativeUpdate", "TriangleMultiplicationOutgoing",
+    "TriangleMultiplicationIncoming", "TriangleAttention", "TriangleAttentionStartingNode",
+    "TriangleAttentionEndingNode", "PairTransformLayer", "PairTransformNet",
+    "has_cuda_kernels", "get_device_info",
+]
+
+
+def _load(module, params):
+    sd = {k: torch.from_numpy(np.ascontiguousarray(v)) for k, v in params.items()}
+    missing, unexpected = module.load_state_dict(sd, strict=True)
+    assert not missing and not unexpected
+    return module
+
+
+def _pair(B, N, C, seed):
+    return torch.from_numpy(H.pair_input(B, N, C, seed))
+
+
+def test_public_names_match_reference():
+    assert sorted(genie_tk.__all__) == sorted(REFERENCE_ALL)
+    for name in REFERENCE_ALL:
+        assert hasattr(genie_tk, name)
+
+
+def test_tri_mul_state_dict_layout():
+    m = TriangleMultiplicationOutgoing(c_z=32, c_hidden=16, use_fused_kernel=False)
+    got = {k: tuple(v.shape) for k, v in m.state_dict().items()}
+    assert got == H.tri_mul_shapes(32, 16)
+    # AlphaFold initialisers: gates W=0 b=1, final projection zero
+    for g in ("linear_a_g", "linear_b_g", "linear_g"):
+        assert torch.all(getattr(m, g).weight == 0) and torch.all(getattr(m, g).bias == 1)
+    assert torch.all(m.linear_z.weight == 0) and torch.all(m.linear_z.bias == 0)
+
+
+def test_tri_attn_state_dict_layout():
+    m = TriangleAttentionStartingNode(c_in=32, c_hidden=16, no_heads=2, use_fused_kernel=False)
+    got = {k: tuple(v.shape) for k, v in m.state_dict().items()}
+    assert got == H.tri_attn_shapes(32, 16, 2)
+    assert m.linear.bias is None and m.mha.linear_q.bias is None
+    assert m.inf == 1e9 and m.starting
+    assert not TriangleAttentionEndingNode(32, 16, 2).starting
+
+
+def test_default_init_outputs_zero():
+    """The final-init output projections make a fresh module's update exactly 0."""
+    z = _pair(1, 8, 32, 0)
+    assert torch.count_nonzero(TriangleMultiplicationOutgoing(32, 16)(z)) == 0
+    assert torch.count_nonzero(TriangleAttentionStartingNode(32, 16, 2)(z)) == 0
+
+
+@pytest.mark.parametrize("cls,outgoing", [(TriangleMultiplicationOutgoing, True),
+                                          (TriangleMultiplicationIncoming, False)])
+def test_tri_mul_pytorch_path_matches_oracle(cls, outgoing):
+    P = H.draw_params(H.tri_mul_shapes(32, 16), 3, ln_random=True, bias_random=True)
+    z = H.pair_input(2, 12, 32, seed=3)
+    mask = H.tail_mask(2, 12, [12, 9])
+    mod = _load(cls(c_z=32, c_hidden=16, use_fused_kernel=False), P)
+    with torch.no_grad():
+        y = mod(torch.from_numpy(z), torch.from_numpy(mask)).numpy()
+    ref = pair_ops.tri_mul(z, mask, P, outgoing, dtype=np.float64)
+    np.testing.assert_allclose(y, ref, atol=2e-5, rtol=1e-4)
+
+
+@pytest.mark.parametrize("cls,starting", [(TriangleAttentionStartingNode, True),
+                                          (TriangleAttentionEndingNode, False)])
+def test_tri_attn_pytorch_path_matches_oracle(cls, starting):
+    P = H.draw_params(H.tri_attn_shapes(32, 16, 2), 4, ln_random=True, bias_random=True)
+    x = H.pair_input(2, 10, 32, seed=4)
+    mask = H.tail_mask(2, 10, [10, 7])
+    mod = _load(cls(c_in=32, c_hidden=16, no_heads=2, use_fused_kernel=False), P)
+    with torch.no_grad():
+        y = mod(torch.from_numpy(x), torch.from_numpy(mask)).numpy()
+    ref = pair_ops.tri_attn(x, mask, P, starting, 2, dtype=np.float64)
+    np.testing.assert_allclose(y, ref, atol=2e-5, rtol=1e-4)
+
+
+def test_mask_default_is_all_ones():
+    P = H.draw_params(H.tri_mul_shapes(16, 8), 5, bias_random=True)
+    mod = _load(TriangleMultiplicationOutgoing(16, 8, use_fused_kernel=False), P)
+    z = _pair(1, 6, 16, 5)
+    with torch.no_grad():
+        assert torch.equal(mod(z), mod(z, torch.ones(1, 6, 6)))
+
+
+@pytest.mark.parametrize("kind", ["mul", "attn"])
+def test_gradient_flow(kind):
+    """Gradients reach the input and every parameter (PyTorch path)."""
+    if kind == "mul":
+        mod = TriangleMultiplicationOutgoing(16, 8, use_fused_kernel=True)
+        _load(mod, H.draw_params(H.tri_mul_shapes(16, 8), 6, bias_random=True))
+    else:
+        mod = TriangleAttentionStartingNode(16, 8, 2, use_fused_kernel=True)
+        _load(mod, H.draw_params(H.tri_attn_shapes(16, 8, 2), 6, bias_random=True))
+    z = _pair(1, 8, 16, 6).requires_grad_(True)
+    mod(z, torch.ones(1, 8, 8)).square().sum().backward()
+    assert z.grad is not None and torch.isfinite(z.grad).all() and z.grad.abs().sum() > 0
+    for name, p in mod.named_parameters():
+        assert p.grad is not None, name
+
+
+def test_masked_pairs_do_not_contribute():
+    """Tri-mul outgoing: changing z on masked pairs (i, k) with k masked leaves rows
+    whose contraction only sees masked k unchanged except through the gate."""
+    P = H.draw_params(H.tri_mul_shapes(16, 8), 7, bias_random=True)
+    mod = _load(TriangleMultiplicationOutgoing(16, 8, use_fused_kernel=False), P)
+    mask = torch.ones(1, 8, 8)
+    mask[:, :, 5:] = 0
+    z1 = _pair(1, 8, 16, 7)
+    z2 = z1.clone()
+    # pairs (i, k>=5) are masked in a and b: perturbing them must not change
+    # x[i, j] for any (i, j) with j < 5, whose gate reads z[i, j] only
+    z2[:, :, 5:] += 3.0
+    with torch.no_grad():
+        y1, y2 = mod(z1, mask), mod(z2, mask)
+    assert torch.allclose(y1[:, :, :5], y2[:, :, :5], atol=1e-6)
+
+
+def test_tri_attn_masked_keys_are_ignored():
+    P = H.draw_params(H.tri_attn_shapes(16, 8, 2), 8, bias_random=True)
+    mod = _load(TriangleAttentionStartingNode(16, 8, 2, use_fused_kernel=False), P)
+    mask = torch.ones(1, 8, 8)
+    mask[:, :, 6:] = 0
+    x1 = _pair(1, 8, 16, 8)
+    x2 = x1.clone()
+    x2[:, :, 6:] += 2.0  # masked keys; their own query outputs change, others must not
+    with torch.no_grad():
+        y1, y2 = mod(x1, mask), mod(x2, mask)
+    # the triangle bias tri[q, k] is read from pair (q, k): masked keys k>=6 feed
+    # only through -inf scores, so queries q<6 of every row are unchanged
+    assert torch.allclose(y1[:, :, :6], y2[:, :, :6], atol=1e-5)
+
+
+def test_batch_dims_are_flattened():
+    P = H.draw_params(H.tri_mul_shapes(16, 8), 9, bias_random=True)
+    mod = _load(TriangleMultiplicationIncoming(16, 8, use_fused_kernel=False), P)
+    z = torch.from_numpy(H.pair_input(6, 5, 16, 9)).reshape(2, 3, 5, 5, 16)
+    with torch.no_grad():
+        y = mod(z)
+        y0 = mod(z[1, 2])
+    assert y.shape == z.shape
+    assert torch.allclose(y[1, 2], y0, atol=1e-6)
+
+
+def test_cpu_host_switch():
+    """No GPU here: the kernel switch is off and CPU tensors use the PyTorch path."""
+    assert utils.has_cuda_kernels() is False or torch.cuda.is_available()
+    m = TriangleMultiplicationOutgoing(128, 128, use_fused_kernel=True)
+    assert m.use_fused_kernel == (m._fused_requested and utils.has_cuda_kernels())
+    assert m._kernel_supported(torch.zeros(1, 4, 4, 128))
+    assert not m._kernel_supported(torch.zeros(1, 4, 5, 128))
+    assert not m._kernel_supported(torch.zeros(1, 4, 4, 128, dtype=torch.float16))
+    assert not TriangleMultiplicationOutgoing(64, 32)._kernel_supported(torch.zeros(1, 4, 4, 64))
+    a = TriangleAttentionEndingNode(128, 128, 4)
+    assert a._kernel_supported(torch.zeros(2, 4, 4, 128, dtype=torch.bfloat16))
+    assert not TriangleAttentionEndingNode(128, 64, 4)._kernel_supported(torch.zeros(1, 4, 4, 128))
+    assert not TriangleAttentionEndingNode(128, 128, 8)._kernel_supported(torch.zeros(1, 4, 4, 128))
+
+
+def test_device_info_keys():
+    info = genie_tk.get_device_info()
+    assert set(info) == {"cuda_available", "cuda_kernels_available", "device_count", "devices"}
+    assert info["device_count"] == len(info["devices"])
+    for d in info["devices"]:
+        assert set(d) == {"name", "total_memory", "major", "minor", "multi_processor_count"}
+
+
+def test_layout_helpers():
+    t = torch.arange(2 * 3 * 4 * 5).reshape(2, 3, 4, 5)
+    assert torch.equal(utils.permute_final_dims(t, 2, 0, 1), t.permute(0, 3, 1, 2))
+    assert utils.flatten_final_dims(t, 2).shape == (2, 3, 20)
+
+    def layer(x, y):
+        return x * 2 + y
+
+    x = torch.randn(4, 6, 3)
+    y = torch.randn(4, 6, 3)
+    out = utils.chunk_layer(layer, {"x": x, "y": y}, chunk_size=5, no_batch_dims=2)
+    assert torch.equal(out, layer(x, y))
+
+
+def test_pair_transform_layer_and_net():
+    """Reference tests/test_triangle_attention.py:123-165, plus block semantics."""
+    torch.manual_seed(0)
+    p = torch.randn(1, 12, 12, 32)
+    m = torch.ones(1, 12, 12)
+    m[:, 10:, :] = 0
+    m[:, :, 10:] = 0
+    layer = PairTransformLayer(c_p=32, c_hidden_mul=16, c_hidden_tri_att=16, n_head_tri=4,
+                               tri_dropout=0.0, use_fused_kernel=False).eval()
+    for mod in layer.modules():  # non-trivial weights so every branch contributes
+        if isinstance(mod, torch.nn.Linear):
+            torch.nn.init.normal_(mod.weight, std=mod.in_features ** -0.5)
+    with torch.no_grad():
+        out, out_m = layer((p, m))
+        q = p
+        for name in ("tri_mul_out", "tri_mul_in", "tri_att_start", "tri_att_end"):
+            q = q + getattr(layer, name)(q, m)
+        q = q + layer.pair_transition(q, m)
+        q = q * m.unsqueeze(-1)
+    assert out.shape == p.shape and out_m is m
+    assert torch.allclose(out, q, atol=1e-6)
+    assert torch.all(out[:, 10:] == 0)
+    net = PairTransformNet(c_p=32, n_layers=2, c_hidden_mul=16, c_hidden_tri_att=16,
+                           n_head_tri=4, tri_dropout=0.0, use_fused_kernel=False)
+    with torch.no_grad():
+        y = net(p, m)
+    assert y.shape == p.shape and torch.isfinite(y).all()
+
+
+def test_shared_dropout_broadcasts():
+    from genie_tk.pair_transform import DropoutColumnwise, DropoutRowwise
+    x = torch.ones(2, 6, 6, 4)
+    torch.manual_seed(1)
+    r = DropoutRowwise(0.5).train()(x)
+    assert torch.all(r == r[:, :1])          # same mask for every row
+    c = DropoutColumnwise(0.5).train()(x)
+    assert torch.all(c == c[:, :, :1])       # same mask for every column
+    assert torch.equal(DropoutRowwise(0.5).eval()(x), x)
+
+
+def test_fused_path_on_gpu_tensor_requires_extension(monkeypatch):
+    """A GPU tensor with use_fused_kernel=True never falls back silently when the
+    extension is missing: forward raises ImportError."""
+    from genie_tk import _ext, triangle_mul
+
+    class FakeCuda(torch.Tensor):
+        @property
+        def is_cuda(self):
+            return True
+
+    monkeypatch.setattr(_ext, "C", None)
+    monkeypatch.setattr(triangle_mul, "_CUDA_AVAILABLE", False)
+    mod = TriangleMultiplicationOutgoing(16, 8, use_fused_kernel=True)
+    z = torch.zeros(1, 4, 4, 16).as_subclass(FakeCuda)
+    with pytest.raises(ImportError):
+        mod(z)
+    # explicitly disabled: the PyTorch path is the documented behaviour
+    mod2 = TriangleMultiplicationOutgoing(16, 8, use_fused_kernel=False)
+    assert mod2(torch.zeros(1, 4, 4, 16)).shape == (1, 4, 4, 16)
+
+
+def test_generic_class_direction_flag():
+    assert TriangleMultiplicativeUpdate(16, 8)._outgoing
+    assert not TriangleMultiplicationIncoming(16, 8)._outgoing
+    assert TriangleAttention(16, 8, 2).starting

@@ -1,0 +1,158 @@
+"""The C ABI (include/genie_tk.h) on the CPU: the shared library loads, exports
+every declared entry point, and answers size queries and argument errors
+without touching a GPU (validation precedes every HIP call, so no compute is
+launched here)."""
+import ctypes
+import os
+import re
+
+import pytest
+import torch  # noqa: F401  (the library shares torch's HIP runtime)
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "genie_tk.h")
+LIB = os.path.join(ROOT, "genie-tk_amd", "genie_tk", "libgenie_tk_hip.so")
+
+GTK_F32, GTK_BF16 = 0, 1
+GTK_OK, GTK_EINVAL, GTK_EUNSUPPORTED, GTK_EWORKSPACE = 0, 1, 2, 3
+
+pytestmark = pytest.mark.skipif(not os.path.exists(LIB), reason="library not built")
+
+i64, sz, vp, fp = ctypes.c_int64, ctypes.c_size_t, ctypes.c_void_p, ctypes.c_float
+ci = ctypes.c_int
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(gtk_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    L = ctypes.CDLL(LIB)
+    L.gtk_last_error.restype = ctypes.c_char_p
+    for name in ("gtk_triangle_mul_workspace_size", "gtk_tri_mul_workspace_size",
+                 "gtk_tri_mul_packed_size", "gtk_tri_attn_packed_size",
+                 "gtk_tri_attn_workspace_size", "gtk_triangle_attention_workspace_size",
+                 "gtk_fused_layernorm_linear_workspace_size"):
+        getattr(L, name).restype = sz
+    L.gtk_triangle_mul_workspace_size.argtypes = [i64, i64, i64, ci]
+    L.gtk_tri_mul_workspace_size.argtypes = [i64, i64, i64, i64, ci]
+    L.gtk_tri_mul_packed_size.argtypes = [i64, i64, ci]
+    L.gtk_tri_attn_packed_size.argtypes = [i64, i64, i64, ci]
+    L.gtk_tri_attn_workspace_size.argtypes = [i64, i64, i64, i64, i64, ci]
+    L.gtk_triangle_attention_workspace_size.argtypes = [i64, i64, i64, i64, ci]
+    L.gtk_fused_layernorm_linear_workspace_size.argtypes = [i64, i64, ci]
+    L.gtk_layernorm.argtypes = [vp, vp, vp, vp, i64, i64, fp, ci, vp]
+    L.gtk_tri_mul_forward.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, ci, ci, fp, fp, ci,
+                                      vp, sz, vp]
+    L.gtk_tri_attn_forward.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, ci, fp, ci,
+                                       vp, sz, vp]
+    L.gtk_triangle_mul_outgoing.argtypes = [vp, vp, vp, vp, i64, i64, i64, ci, vp, sz, vp]
+    L.gtk_triangle_attention_starting.argtypes = [vp, vp, vp, vp, vp, fp, vp, i64, i64, i64,
+                                                  i64, ci, vp, sz, vp]
+    L.gtk_fused_layernorm_linear.argtypes = [vp, vp, vp, vp, vp, ci, vp, i64, i64, i64, fp, ci,
+                                             vp, sz, vp]
+    L.gtk_timing_report.argtypes = [ctypes.c_char_p, sz]
+    return L
+
+
+def test_header_declares_the_operator_surface():
+    names = declared_functions()
+    # the reference's _C operators (kernels/bindings.cpp:69-101) and the fused forwards
+    for n in ("gtk_layernorm", "gtk_fused_layernorm_linear", "gtk_triangle_mul_outgoing",
+              "gtk_triangle_mul_incoming", "gtk_triangle_attention_starting",
+              "gtk_triangle_attention_ending", "gtk_tri_mul_forward", "gtk_tri_attn_forward"):
+        assert n in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    missing = [n for n in declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_version_and_error_string(lib):
+    assert lib.gtk_version() == 100
+    assert isinstance(lib.gtk_last_error(), bytes)
+
+
+def test_workspace_sizes(lib):
+    # three bf16 planes [B][C][Np][Np], Np = N rounded up to 64, 256 B alignment slack
+    plane = lambda B, N, C, e: B * C * ((N + 63) // 64 * 64) ** 2 * e
+    assert lib.gtk_triangle_mul_workspace_size(1, 512, 128, GTK_BF16) == 3 * (plane(1, 512, 128, 2) + 256)
+    assert lib.gtk_triangle_mul_workspace_size(2, 200, 64, GTK_F32) == 3 * (plane(2, 200, 64, 4) + 256)
+    assert lib.gtk_tri_mul_workspace_size(1, 512, 128, 128, GTK_BF16) == 3 * (plane(1, 512, 128, 2) + 256)
+    assert lib.gtk_triangle_mul_workspace_size(-1, 8, 16, GTK_F32) == 0
+    # packed weights exist only for the shapes the kernels are built for
+    assert lib.gtk_tri_mul_packed_size(128, 128, GTK_BF16) > 0
+    assert lib.gtk_tri_mul_packed_size(128, 64, GTK_F32) > lib.gtk_tri_mul_packed_size(128, 64, GTK_BF16)
+    assert lib.gtk_tri_mul_packed_size(64, 64, GTK_BF16) == 0
+    assert lib.gtk_tri_attn_packed_size(128, 128, 4, GTK_BF16) > 0
+    assert lib.gtk_tri_attn_packed_size(128, 64, 2, GTK_BF16) == 0
+    ws = lib.gtk_tri_attn_workspace_size(1, 512, 128, 128, 4, GTK_BF16)
+    assert ws >= 4 * 512 * 512 * 128 * 2  # q, k, v^T, gate planes at least
+    assert lib.gtk_tri_attn_workspace_size(1, 512, 128, 64, 2, GTK_BF16) == 0
+    assert lib.gtk_fused_layernorm_linear_workspace_size(128, 256, GTK_BF16) > 0
+
+
+def _err(lib):
+    return lib.gtk_last_error().decode()
+
+
+def test_bad_dtype_and_shapes_are_rejected(lib):
+    assert lib.gtk_layernorm(None, None, None, None, 4, 128, 1e-5, 7, None) == GTK_EINVAL
+    assert "dtype" in _err(lib)
+    assert lib.gtk_layernorm(None, None, None, None, -1, 128, 1e-5, GTK_F32, None) == GTK_EINVAL
+    assert lib.gtk_layernorm(None, None, None, None, 4, 128, 1e-5, GTK_F32, None) == GTK_EINVAL
+    assert "null" in _err(lib)
+    rc = lib.gtk_tri_mul_forward(None, None, None, None, 1, 8, 64, 64, 1, 0, 1e-5, 1e-5,
+                                 GTK_BF16, None, 0, None)
+    assert rc == GTK_EUNSUPPORTED and "c_z=64" in _err(lib)
+    rc = lib.gtk_tri_mul_forward(None, None, None, None, 1, 8, 128, 128, 1, 0, 1e-5, 1e-5,
+                                 GTK_BF16, None, 0, None)
+    assert rc == GTK_EINVAL and "null" in _err(lib)
+    dummy = ctypes.c_void_p(16)  # never dereferenced: the size check fails first
+    rc = lib.gtk_tri_mul_forward(dummy, None, dummy, dummy, 1, 8, 128, 128, 1, 0, 1e-5, 1e-5,
+                                 GTK_BF16, dummy, 10, None)
+    assert rc == GTK_EWORKSPACE and "workspace" in _err(lib)
+    rc = lib.gtk_tri_attn_forward(None, None, None, None, 1, 8, 128, 128, 8, 1, 0, 1e-5,
+                                  GTK_BF16, None, 0, None)
+    assert rc == GTK_EUNSUPPORTED
+    rc = lib.gtk_triangle_mul_outgoing(None, None, None, None, 1, 8, 24, GTK_BF16, None, 0, None)
+    assert rc == GTK_EUNSUPPORTED and "multiple of 16" in _err(lib)
+    rc = lib.gtk_triangle_attention_starting(None, None, None, None, None, 0.2, None, 1, 4, 8,
+                                             64, GTK_BF16, None, 0, None)
+    assert rc == GTK_EUNSUPPORTED and "head dim" in _err(lib)
+    rc = lib.gtk_fused_layernorm_linear(None, None, None, None, None, GTK_F32, None, 4, 96, 8,
+                                        1e-5, GTK_F32, None, 0, None)
+    assert rc == GTK_EUNSUPPORTED
+
+
+def test_empty_inputs_are_no_ops(lib):
+    """B = 0 or N = 0 (or rows = 0) succeed without reading any pointer."""
+    assert lib.gtk_layernorm(None, None, None, None, 0, 128, 1e-5, GTK_BF16, None) == GTK_OK
+    assert lib.gtk_tri_mul_forward(None, None, None, None, 0, 8, 128, 128, 1, 0, 1e-5, 1e-5,
+                                   GTK_BF16, None, 0, None) == GTK_OK
+    assert lib.gtk_tri_mul_forward(None, None, None, None, 1, 0, 128, 64, 0, 0, 1e-5, 1e-5,
+                                   GTK_F32, None, 0, None) == GTK_OK
+    assert lib.gtk_tri_attn_forward(None, None, None, None, 2, 0, 128, 128, 4, 0, 0, 1e-5,
+                                    GTK_BF16, None, 0, None) == GTK_OK
+    assert lib.gtk_triangle_mul_outgoing(None, None, None, None, 0, 8, 16, GTK_F32, None, 0,
+                                         None) == GTK_OK
+
+
+def test_timing_report_when_idle(lib):
+    buf = ctypes.create_string_buffer(256)
+    assert lib.gtk_timing_report(buf, 256) == GTK_OK
+    assert buf.value == b""
+
+
+def test_torch_extension_exposes_reference_operators():
+    from genie_tk import _ext
+    if _ext.C is None:
+        pytest.skip(f"extension not built: {_ext.IMPORT_ERROR}")
+    for name in ("triangle_mul_outgoing", "triangle_mul_incoming", "triangle_attention_starting",
+                 "triangle_attention_ending", "layernorm", "fused_layernorm_linear",
+                 "tri_mul_pack", "tri_mul_forward", "tri_attn_pack", "tri_attn_forward"):
+        assert hasattr(_ext.C, name), name
