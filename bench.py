@@ -155,6 +155,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--n", type=int, default=512, help="pair length N")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="after the measurements, copy a MIB-MiB fp32 tensor 3 times (a plain "
+                         "copy kernel of known traffic, for scaling HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -219,6 +222,12 @@ def main() -> int:
         z2 = torch.randn(1, 2 * N, 2 * N, C_Z, device=dev).to(torch.bfloat16)
         ln2_ms = statistics.median(event_time_ms(torch, lambda: C.layernorm(z2, ln_w, ln_b, 1e-5), reps))
         del z2
+        if args.calibrate_copy > 0:
+            src = torch.ones((args.calibrate_copy << 20) // 4, device=dev)
+            dst = torch.empty_like(src)
+            for _ in range(3):
+                dst.copy_(src)
+            del src, dst
     torch.cuda.synchronize()
 
     fm, fa = trimul_flops(N), triattn_flops(N)
