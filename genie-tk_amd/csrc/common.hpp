@@ -266,6 +266,15 @@ __device__ __forceinline__ void copy_to_lds_async(void* dst, const void* __restr
     g2lds16((const char*)src + blk * 1024 + lane * 16, (char*)dst + blk * 1024);
 }
 
+// A zero the compiler cannot see through.  Adding it to a loop-invariant LDS
+// address inside a loop keeps the loads in the loop: hoisted out, the
+// fragments would stay live across the whole loop and spill.
+__device__ __forceinline__ int opaque_zero() {
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return z;
+}
+
 // acc = A . B with a zero accumulator input (inline constant, no register init).
 __device__ __forceinline__ f32x16 mma0(const Frag<bf16>& a, const Frag<bf16>& b) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a.v, b.v, zero16(), 0, 0, 0);

@@ -24,6 +24,8 @@
 // Masking: key k of row r is excluded when mask == 0.  A row without any
 // valid key attends uniformly over all N keys: that is what the reference's
 // additive -1e9 bias produces in fp32 (every logit rounds to -1e9).
+#include <algorithm>
+
 #include "capi_util.hpp"
 #include "common.hpp"
 #include "pack.hpp"
@@ -172,6 +174,152 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
           const int h = 8 * g + 4 * half + rr;
           if (h >= 4 && h < H) ws.bias[(((int64_t)b * H + h) * Np + r) * Np + j] = cvt<T>((ab[4 * g + rr] + w.b_b[h]) * keep);
         }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 1b. bf16 prologue: persistent, one 1024-thread block per CU with the packed
+//     q/k/v/gate weights and the triangle-bias tile resident in LDS
+//     (4 x 32 KiB + 8 KiB, direct global->LDS copies) and the folded biases
+//     beside them; each wave then loops over 32-pair tiles.
+//     Lane i32 of a wave normalises pair 16*((i32>>2)&1) + 4*(i32>>3) + (i32&3)
+//     of the tile.  q, k and the gate (channel-contiguous layouts) take the
+//     weights as the A operand: a lane's accumulators are 16 channels of its
+//     own pair.  v^T and the triangle bias (position-contiguous layouts) take
+//     the pairs as the A operand: the row permutation above then gives every
+//     lane 16 consecutive positions of one channel, stored as 32 bytes.
+//     Output values and padding are those of triattn_prologue_kernel.
+// ---------------------------------------------------------------------------
+template <int CIN, int H>
+__global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
+    const bf16* __restrict__ x, TriAttnPacked<bf16> w, AttnWs<bf16> ws, int N, int Np,
+    int starting, float eps, int64_t ntiles) {
+  constexpr int CH = H * HD;
+  constexpr int KCH = CIN / 16;
+  constexpr int PE = (CH / 32) * KCH * 512;  // one packed c_in -> c_h projection
+  constexpr int PB = KCH * 512;              // the packed c_in -> H tile (rows >= H are zero)
+  static_assert(CH / 32 == H, "one 32-channel tile per head");
+  __shared__ __attribute__((aligned(1024))) bf16 wl[4 * PE + PB];
+  __shared__ __attribute__((aligned(16))) float bl[4 * CH + 32];
+  copy_to_lds_async(wl, w.w_q, PE * 2);
+  copy_to_lds_async(wl + PE, w.w_k, PE * 2);
+  copy_to_lds_async(wl + 2 * PE, w.w_v, PE * 2);
+  copy_to_lds_async(wl + 3 * PE, w.w_g, PE * 2);
+  copy_to_lds_async(wl + 4 * PE, w.w_b, PB * 2);
+  for (int t = threadIdx.x; t < CH; t += blockDim.x) {
+    bl[t] = w.b_q[t];
+    bl[CH + t] = w.b_k[t];
+    bl[2 * CH + t] = w.b_v[t];
+    bl[3 * CH + t] = w.b_g[t];
+  }
+  if (threadIdx.x < 32) bl[4 * CH + threadIdx.x] = w.b_b[threadIdx.x];
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int half = lane >> 5;
+  const int i32 = lane & 31;
+  const int prow = 16 * ((i32 >> 2) & 1) + 4 * (i32 >> 3) + (i32 & 3);
+  const int vtiles = Np / 32;
+  for (int64_t tile = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 6); tile < ntiles;
+       tile += (int64_t)gridDim.x * 16) {
+    const int vt = (int)(tile % vtiles);
+    const int r = (int)((tile / vtiles) % Np);  // destination row
+    const int b = (int)(tile / ((int64_t)vtiles * Np));
+    const int jown = vt * 32 + prow;            // this lane's pair (A/B operand side)
+    Frag<bf16> xf[KCH];
+    bool valid;
+    {
+      valid = r < N && jown < N;
+      const int p = starting ? r : jown, q = starting ? jown : r;
+      const int64_t pair = ((int64_t)b * N + (valid ? p : 0)) * N + (valid ? q : 0);
+      ln_row_bf16<CIN>(xf, x + pair * CIN, valid, eps);
+    }
+    const float keep = valid ? 1.f : 0.f;
+    const int64_t rowbase = (int64_t)b * Np + r;
+    const int j0 = vt * 32 + 16 * half;         // first of this lane's 16 positions
+    // validity of the 16 positions j0 + jj, as a bit mask
+    const int nvalid = r < N ? min(max(N - j0, 0), 16) : 0;
+
+    // q, k, v, gate: one 32-channel tile (one head) per step, one MFMA chain each
+#pragma unroll 1
+    for (int step = 0; step < 4 * H; ++step) {
+      const int kind = step / H;  // 0 q, 1 k, 2 v, 3 gate
+      const int h = step % H;
+      const bf16* wt = wl + kind * PE;
+      Frag<bf16> fw;
+      load_wfrag_lds(fw, wt, h, 0, KCH);
+      f32x16 acc = kind == 2 ? mma0(xf[0], fw) : mma0(fw, xf[0]);
+      if (kind == 2) {
+#pragma unroll
+        for (int ks = 1; ks < KCH; ++ks) {
+          load_wfrag_lds(fw, wt, h, ks, KCH);
+          mma(acc, xf[ks], fw);
+        }
+        // v^T: position-contiguous [b][r][h][32][j] in vt_pos order
+        const float bv = bl[2 * CH + h * HD + i32];
+        uint32_t pk[8];
+#pragma unroll
+        for (int m = 0; m < 16; m += 2) {
+          // vt_pos swaps bits 2 and 3 of the position inside its group of 16
+          const int s0 = (m & 3) | ((m & 4) << 1) | ((m & 8) >> 1);
+          const int s1 = s0 + 1;
+          pk[m / 2] = pack_bf16x2(s0 < nvalid ? acc[s0] + bv : 0.f, s1 < nvalid ? acc[s1] + bv : 0.f);
+        }
+        uint4* o = reinterpret_cast<uint4*>(ws.vt + ((rowbase * H + h) * HD + i32) * (int64_t)Np + j0);
+        o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        o[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+      } else {
+#pragma unroll
+        for (int ks = 1; ks < KCH; ++ks) {
+          load_wfrag_lds(fw, wt, h, ks, KCH);
+          mma(acc, fw, xf[ks]);
+        }
+        if (kind < 2) {
+          // q, k: channel-contiguous [b][r][h][j][32]
+          bf16* dst = (kind ? ws.k : ws.q) + ((rowbase * H + h) * Np + jown) * HD;
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int d0 = 8 * g + 4 * half;
+            const f32x4 bq = *reinterpret_cast<const f32x4*>(bl + kind * CH + h * HD + d0);
+            store4(dst + d0, (acc[4 * g] + bq[0]) * keep, (acc[4 * g + 1] + bq[1]) * keep,
+                   (acc[4 * g + 2] + bq[2]) * keep, (acc[4 * g + 3] + bq[3]) * keep);
+          }
+        } else {
+          // gate: channel-contiguous [b][r][j][c_h]
+          bf16* gd = ws.gate + (rowbase * Np + jown) * CH;
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int c0 = h * 32 + 8 * g + 4 * half;
+            const f32x4 bg = *reinterpret_cast<const f32x4*>(bl + 3 * CH + c0);
+            store4(gd + c0, gate_from_u(acc[4 * g] + bg[0]), gate_from_u(acc[4 * g + 1] + bg[1]),
+                   gate_from_u(acc[4 * g + 2] + bg[2]), gate_from_u(acc[4 * g + 3] + bg[3]));
+          }
+        }
+      }
+    }
+    // triangle bias [b][h][r][j]: lanes with i32 < H hold head i32
+    {
+      const bf16* wb = wl + 4 * PE + opaque_zero();
+      Frag<bf16> fb;
+      load_wfrag_lds(fb, wb, 0, 0, KCH);
+      f32x16 ab = mma0(xf[0], fb);
+#pragma unroll
+      for (int ks = 1; ks < KCH; ++ks) {
+        load_wfrag_lds(fb, wb, 0, ks, KCH);
+        mma(ab, xf[ks], fb);
+      }
+      if (i32 < H) {
+        const float bb = bl[4 * CH + i32];
+        uint32_t pk[8];
+#pragma unroll
+        for (int m = 0; m < 16; m += 2)
+          pk[m / 2] = pack_bf16x2(m < nvalid ? ab[m] + bb : 0.f, m + 1 < nvalid ? ab[m + 1] + bb : 0.f);
+        uint4* o = reinterpret_cast<uint4*>(ws.bias + (((int64_t)b * H + i32) * Np + r) * Np + j0);
+        o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        o[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+      }
     }
   }
 }
@@ -797,7 +945,12 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
   Carve cv(ws, SIZE_MAX);
   AttnWs<T> a = carve_attn_ws<T>(cv, B, Np, H, CH);
   const int64_t ptiles = B * (int64_t)Np * (Np / 32);
-  {
+  if constexpr (sizeof(T) == 2) {
+    const int grid = (int)std::min<int64_t>(device_cus(), (ptiles + 15) / 16);
+    StageTimer timer("triattn_prologue", st);
+    triattn_prologue_bf16_kernel<CIN, H><<<grid, 1024, 0, st>>>(
+        (const bf16*)x, w, a, (int)N, Np, starting, eps, ptiles);
+  } else {
     StageTimer timer("triattn_prologue", st);
     triattn_prologue_kernel<T, CIN, H><<<(unsigned)((ptiles + 3) / 4), 256, 0, st>>>(
         (const T*)x, w, a, (int)B, (int)N, Np, starting, eps);
