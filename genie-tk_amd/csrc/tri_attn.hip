@@ -32,7 +32,8 @@
 
 namespace gtk {
 
-constexpr int HD = 32;  // head dimension handled by the kernels
+constexpr int HD = 32;      // head dimension handled by the kernels
+constexpr int MAXN = 8192;  // largest N of the attention entry points
 
 // Packed parameters of one TriangleAttention.  The LayerNorm weight is folded
 // into w_q/w_k/w_v/w_g/w_b and its bias into b_q/b_k/b_v/b_g/b_b (b = W beta
@@ -556,13 +557,14 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
   static_assert(H == 4 && H * QT * 64 == 1024, "block is 16 waves");
   static_assert(QB * OP * 2 <= NS * STAGE_BYTES, "o staging must fit in the ring");
   __shared__ __attribute__((aligned(1024))) char ring[NS][STAGE_BYTES];
-  __shared__ __attribute__((aligned(16))) float kbias[NS][KB];
-  __shared__ int kflag[NS];
+  // excluded keys of this row, one bit per key: bit j of word t is key 32t + j
+  __shared__ unsigned kmask[MAXN / 32];  // mask == 0
+  __shared__ unsigned kpad[MAXN / 32];   // key >= N
   __shared__ int row_any;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar addressing
   const int half = lane >> 5;
   const int t32 = lane & 31;
   const int h = wave / QT;
@@ -581,14 +583,26 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
   const int64_t mks = starting ? 1 : N;
   if (tid == 0) row_any = mrow ? 0 : 1;
   __syncthreads();
-  if (mrow) {
+  {
     bool any = false;
-    for (int k = tid; k < N; k += 1024) any = any || (mrow[k * mks] != 0.f);
-    if (__ballot(any) != 0ull && lane == 0) row_any = 1;
+    for (int k0 = wave * 64; k0 < Np; k0 += 1024) {
+      const int k = k0 + lane;
+      const bool inrow = k < N;
+      const bool masked = inrow && mrow && mrow[k * mks] == 0.f;
+      any = any || (inrow && !masked);
+      const unsigned long long mb = __ballot(masked);
+      const unsigned long long pb = __ballot(!inrow);
+      if (lane == 0) {
+        kmask[k0 / 32] = (unsigned)mb;
+        kmask[k0 / 32 + 1] = (unsigned)(mb >> 32);
+        kpad[k0 / 32] = (unsigned)pb;
+        kpad[k0 / 32 + 1] = (unsigned)(pb >> 32);
+      }
+    }
+    if (mrow && __ballot(any) != 0ull && lane == 0) row_any = 1;
   }
   __syncthreads();
   const bool row_valid = row_any != 0;
-  const bool use_kbias = (mrow != nullptr) || (N % KB != 0);
 
   // Async stage load.  A stage is 32 regions of 1 KiB (64 lanes x 16 B);
   // wave w moves regions 2w and 2w+1.  Regions 0..15: K, head reg/4, chunks
@@ -601,34 +615,30 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
   const bool k_region = wave < 8;          // waves 0..7 move K, 8..15 move V^T
   const int rg_head = (wave & 7) >> 1;
   const int rg_sub0 = (wave & 1) * 2;
+  // this lane's source element of region i at key 0 (a stage at key k0 adds
+  // k0 * kstride), and the wave's LDS destination offset of region i
+  const int64_t kstride = k_region ? HD : 1;
+  const bf16* gsrc[2];
+  int dst_off[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int sub = rg_sub0 + i;
+    const int P = sub * 64 + lane;
+    if (k_region) {
+      const int row = P >> 2;
+      const int c = (P & 3) ^ ((row >> 1) & 3);
+      gsrc[i] = kbase + ((int64_t)rg_head * Np + row) * HD + c * 8;
+      dst_off[i] = rg_head * HEAD_BYTES + sub * 1024;
+    } else {
+      const int d = P >> 3;
+      const int c = (P & 7) ^ (d & 7);
+      gsrc[i] = vbase + ((int64_t)rg_head * HD + d) * Np + c * 8;
+      dst_off[i] = (H + rg_head) * HEAD_BYTES + sub * 1024;
+    }
+  }
   auto issue_stage = [&](int stage, int k0) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int sub = rg_sub0 + i;
-      const int P = sub * 64 + lane;
-      const void* g;
-      char* dst;
-      if (k_region) {
-        const int row = P >> 2;
-        const int c = (P & 3) ^ ((row >> 1) & 3);
-        g = kbase + ((int64_t)rg_head * Np + k0 + row) * HD + c * 8;
-        dst = ring[stage] + rg_head * HEAD_BYTES + sub * 1024;
-      } else {
-        const int d = P >> 3;
-        const int c = (P & 7) ^ (d & 7);
-        g = vbase + ((int64_t)rg_head * HD + d) * Np + k0 + c * 8;
-        dst = ring[stage] + (H + rg_head) * HEAD_BYTES + sub * 1024;
-      }
-      g2lds16(g, dst);
-    }
-    if (use_kbias && wave == 0) {
-      const int k = k0 + lane;
-      bool ex = k >= N;
-      if (!ex && row_valid && mrow) ex = mrow[k * mks] == 0.f;
-      kbias[stage][lane] = ex ? -INFINITY : 0.f;
-      const unsigned long long anyex = __ballot(ex);
-      if (lane == 0) kflag[stage] = anyex != 0ull;
-    }
+    for (int i = 0; i < 2; ++i) g2lds16(gsrc[i] + k0 * kstride, ring[stage] + dst_off[i]);
   };
 
   // query fragments (zero for a row without valid keys: uniform attention)
@@ -653,22 +663,24 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
       bfr[1].load(brow + t * 32 + 16);
     }
   };
-  // S^T of 32-key tile t: I.Bias^T + K Q^T (zero for a row without valid keys)
-  auto s_tile = [&](int t, f32x16& s) {
-    s = zero16();
-    if (row_valid) {
-      mma(s, idf[0], bfr[0]);
-      mma(s, idf[1], bfr[1]);
-      const char* kt_base = ring[(t >> 1) % NS] + h * HEAD_BYTES;
-      const int row = (t & 1) * 32 + t32;
+  // S^T - m of 32-key tile t: the accumulation starts from negm = -m_use in
+  // every register, then adds I.Bias^T and K Q^T (no terms for a row without
+  // valid keys: uniform attention)
+  f32x16 negm = zero16();
+  auto s_tile = [&](int t) {
+    if (!row_valid) return negm;
+    f32x16 s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(idf[0].v, bfr[0].v, negm, 0, 0, 0);
+    mma(s, idf[1], bfr[1]);
+    const char* kt_base = ring[(t >> 1) % NS] + h * HEAD_BYTES;
+    const int row = (t & 1) * 32 + t32;
 #pragma unroll
-      for (int m = 0; m < 2; ++m) {
-        Frag<bf16> kf;
-        const int c = (m * 2 + half) ^ ((row >> 1) & 3);
-        kf.load(reinterpret_cast<const bf16*>(kt_base + row * 64 + c * 16));
-        mma(s, kf, qf[m]);
-      }
+    for (int m = 0; m < 2; ++m) {
+      Frag<bf16> kf;
+      const int c = (m * 2 + half) ^ ((row >> 1) & 3);
+      kf.load(reinterpret_cast<const bf16*>(kt_base + row * 64 + c * 16));
+      mma(s, kf, qf[m]);
     }
+    return s;
   };
 
   const int nkb = (N + KB - 1) / KB;
@@ -678,40 +690,38 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   if (nkb > 1) issue_stage(1, KB);
-  f32x16 s_cur, s_next;
-  s_tile(0, s_cur);
-  if (ntiles > 1) load_bias(1);
 
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
   const bf16x2_t ones2 = {(bf16)1.0f, (bf16)1.0f};
   f32x16 o = zero16();
   float m_ref = -INFINITY, l_run = 0.f;
+  float m_use = 0.f;  // the value subtracted inside S: m_ref, or 0 while m_ref = -inf
   for (int t = 0; t < ntiles; ++t) {
-    // issue the next tile's S on the matrix cores before this tile's softmax
-    if (t + 1 < ntiles) {
-      if (((t + 1) & 1) == 0) {           // tile t+1 opens key block kb
-        const int kb = (t + 1) >> 1;
-        __builtin_amdgcn_s_waitcnt(0);    // stage kb and pending bias loads landed
-        __syncthreads();                  // ... for every wave; block kb-2 fully consumed
-        if (kb + 1 < nkb) issue_stage((kb + 1) % NS, (kb + 1) * KB);
-      }
-      s_tile(t + 1, s_next);
-      if (t + 2 < ntiles) load_bias(t + 2);
+    if (t > 0 && (t & 1) == 0) {          // tile t opens key block kb
+      const int kb = t >> 1;
+      __builtin_amdgcn_s_waitcnt(0);      // stage kb and the bias of tile t landed
+      __syncthreads();                    // ... for every wave; block kb-2 fully consumed
+      if (kb + 1 < nkb) issue_stage((kb + 1) % NS, (kb + 1) * KB);
     }
+    f32x16 sc = s_tile(t);
+    if (t + 1 < ntiles) load_bias(t + 1);
     const int cur = (t >> 1) % NS;
-    if (use_kbias && kflag[cur]) {
+    // keys of tile t that take no weight: padding, and masked keys of a valid row
+    const unsigned kx = kpad[t] | (row_valid ? kmask[t] : 0u);
+    if (kx != 0u) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x4 kb4 = *reinterpret_cast<const f32x4*>(&kbias[cur][(t & 1) * 32 + 8 * g + 4 * half]);
+      for (int g = 0; g < 4; ++g)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) s_cur[4 * g + rr] += kb4[rr];
-      }
+        for (int rr = 0; rr < 4; ++rr)
+          if ((kx >> (8 * g + 4 * half + rr)) & 1u) sc[4 * g + rr] = -INFINITY;
     }
-    float mt = fmaxf(fmaxf(s_cur[0], s_cur[1]), s_cur[2]);
+    // sc holds s - m_use; the reference max m_ref moves only when a score
+    // exceeds it by more than kRescale
+    float mt = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
 #pragma unroll
-    for (int e = 3; e < 15; e += 2) mt = fmaxf(fmaxf(mt, s_cur[e]), s_cur[e + 1]);
-    mt = fmaxf(mt, s_cur[15]);
-    mt = lane_pair_max(mt);
+    for (int e = 3; e < 15; e += 2) mt = fmaxf(fmaxf(mt, sc[e]), sc[e + 1]);
+    mt = fmaxf(mt, sc[15]);
+    mt = lane_pair_max(mt) + m_use;       // the tile max of s
     if (__ballot(mt > m_ref + kRescale) != 0ull) {
       const float m_new = fmaxf(m_ref, mt);
       const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
@@ -719,14 +729,21 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) o[e] *= alpha;
       m_ref = m_new;
+      const float m_next = (m_ref == -INFINITY) ? 0.f : m_ref;
+      const float shift = m_use - m_next;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        sc[e] += shift;
+        negm[e] = -m_next;
+      }
+      m_use = m_next;
     }
-    const float m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
     const char* vt_base = ring[cur] + (H + h) * HEAD_BYTES;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       Frag<bf16> pf, vf;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pf.v[e] = (bf16)__builtin_amdgcn_exp2f(s_cur[8 * c + e] - m_use);
+      for (int e = 0; e < 8; ++e) pf.v[e] = (bf16)__builtin_amdgcn_exp2f(sc[8 * c + e]);
       // row sum over the bf16 probabilities that enter P V
 #pragma unroll
       for (int e = 0; e < 8; e += 2) {
@@ -738,7 +755,6 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
       vf.load(reinterpret_cast<const bf16*>(vt_base + t32 * 128 + lc * 16));
       mma(o, vf, pf);
     }
-    s_cur = s_next;
   }
   const float inv = 1.0f / lane_pair_sum(l_run);
 
