@@ -557,6 +557,7 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
   static_assert(H == 4 && H * QT * 64 == 1024, "block is 16 waves");
   static_assert(QB * OP * 2 <= NS * STAGE_BYTES, "o staging must fit in the ring");
   __shared__ __attribute__((aligned(1024))) char ring[NS][STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) bf16 wo_l[(CIN / 32) * (CH / 16) * 512];  // packed W_o
   // excluded keys of this row, one bit per key: bit j of word t is key 32t + j
   __shared__ unsigned kmask[MAXN / 32];  // mask == 0
   __shared__ unsigned kpad[MAXN / 32];   // key >= N
@@ -641,6 +642,15 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
     for (int i = 0; i < 2; ++i) g2lds16(gsrc[i] + k0 * kstride, ring[stage] + dst_off[i]);
   };
 
+  // W_o for the epilogue, and this lane's gate values, fetched now so that
+  // neither load is waited for at the end
+  copy_to_lds_async(wo_l, w.w_o, (int)sizeof(wo_l));
+  bf16x4 gpre[4];
+  {
+    const bf16* gr = ws.gate + (rowbase * Np + q0 + t32) * CH + h * HD;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) gpre[g] = *reinterpret_cast<const bf16x4*>(gr + 8 * g + 4 * half);
+  }
   // query fragments (zero for a row without valid keys: uniform attention)
   Frag<bf16> qf[2];
   const bf16* qrow = ws.q + ((rowbase * H + h) * Np + q0 + t32) * HD;
@@ -761,15 +771,13 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
   // o * gate for all heads, staged as [query][CH] over the ring
   __syncthreads();
   bf16* os = reinterpret_cast<bf16*>(&ring[0][0]);
-  {
-    const bf16* gr = ws.gate + (rowbase * Np + q0 + t32) * CH + h * HD;
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d0 = 8 * g + 4 * half;
-      const f32x4 gv = load4f(gr + d0);
-      store4(os + (qt * 32 + t32) * OP + h * HD + d0, o[4 * g] * inv * gv[0],
-             o[4 * g + 1] * inv * gv[1], o[4 * g + 2] * inv * gv[2], o[4 * g + 3] * inv * gv[3]);
-    }
+  for (int g = 0; g < 4; ++g) {
+    const int d0 = 8 * g + 4 * half;
+    const bf16x4 gv = gpre[g];
+    store4(os + (qt * 32 + t32) * OP + h * HD + d0, o[4 * g] * inv * (float)gv[0],
+           o[4 * g + 1] * inv * (float)gv[1], o[4 * g + 2] * inv * (float)gv[2],
+           o[4 * g + 3] * inv * (float)gv[3]);
   }
   __syncthreads();
   // output projection: wave -> (query tile, output tile)
@@ -779,7 +787,13 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
     Frag<bf16> of[CH / 16];
 #pragma unroll
     for (int ks = 0; ks < CH / 16; ++ks) of[ks].load(os + (oq * 32 + t32) * OP + half * (CH / 2) + ks * 8);
-    const f32x16 acc = row_gemm_tile<bf16, CH, true>(of, w.w_o, nt);
+    f32x16 acc = zero16();
+#pragma unroll
+    for (int ks = 0; ks < CH / 16; ++ks) {
+      Frag<bf16> wf;
+      load_wfrag_lds(wf, wo_l, nt, ks, CH / 16);
+      mma(acc, wf, of[ks]);
+    }
     const int q = qb * QB + oq * 32 + t32;
     if (q < N) {
       const int p0 = starting ? r : q, p1 = starting ? q : r;
