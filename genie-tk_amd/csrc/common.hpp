@@ -189,16 +189,11 @@ __device__ __forceinline__ void ln_to_frags(Frag<T>* frags, const RowHalf<C>& r,
 // fragments: the raw
 // half row stays packed (C/4 VGPRs) and is widened on the fly, so the peak
 // register footprint is two sets of packed fragments.
+// LayerNorm (normalisation only) of the pair row held as raw bf16 fragments:
+// lane l holds channels (l>>5)*C/2 + 8*ch + e of its row in raw[ch]; the two
+// lanes of a row exchange partial sums with one lane^32 swap.
 template <int C>
-__device__ __forceinline__ void ln_row_bf16(Frag<bf16>* xf, const bf16* row_base, bool valid,
-                                            float eps) {
-  const int half = (threadIdx.x & 63) >> 5;
-  Frag<bf16> raw[C / 16];
-#pragma unroll
-  for (int ch = 0; ch < C / 16; ++ch) {
-    if (valid) raw[ch].load(row_base + half * (C / 2) + ch * 8);
-    else raw[ch].zero();
-  }
+__device__ __forceinline__ void ln_frags_bf16(Frag<bf16>* xf, const Frag<bf16>* raw, float eps) {
   float s = 0.f;
 #pragma unroll
   for (int ch = 0; ch < C / 16; ++ch)
@@ -223,6 +218,29 @@ __device__ __forceinline__ void ln_row_bf16(Frag<bf16>* xf, const bf16* row_base
     for (int e = 0; e < 8; ++e) f[e] = (raw[ch].get(e) - mean) * rstd;
     xf[ch].set(f);
   }
+}
+
+// Load and normalise the pair row at row_base (zeros when !valid).
+template <int C>
+__device__ __forceinline__ void ln_row_bf16(Frag<bf16>* xf, const bf16* row_base, bool valid,
+                                            float eps) {
+  const int half = (threadIdx.x & 63) >> 5;
+  Frag<bf16> raw[C / 16];
+#pragma unroll
+  for (int ch = 0; ch < C / 16; ++ch) {
+    if (valid) raw[ch].load(row_base + half * (C / 2) + ch * 8);
+    else raw[ch].zero();
+  }
+  ln_frags_bf16<C>(xf, raw, eps);
+}
+
+// Transposing LDS read (ds_read_b64_tr_b16).  Within each group of 16 lanes,
+// lane L receives element L%4 of the 4 elements read at the addresses of
+// lanes L/4, 4 + L/4, 8 + L/4 and 12 + L/4 (in that order).
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ s16x4 lds_read_tr16(const void* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s16x4*)(const_cast<void*>(p)));
 }
 
 // ---------------------------------------------------------------------------

@@ -431,6 +431,169 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// 3b. bf16 epilogue: persistent, 8 waves per CU with W_g and W_z resident in
+//     LDS.  Per 32-pair tile (row i, pairs jt*32 ..):
+//   * the x tile (c rows of 32 pairs, 64 B each) lands in the wave's own LDS
+//     buffer with direct global->LDS copies, chunk-swizzled so the transposing
+//     reads below are bank-conflict free, and is read back with
+//     ds_read_b64_tr_b16 straight into MFMA fragments (lane = pair, 8
+//     consecutive channels per fragment);
+//   * the next tile's x copy and z row loads are issued before this tile's
+//     matrix work, so their latency hides behind it;
+//   * gate = sigmoid(LN_in(z) W_g^T + b_g) and (LN_out(x) W_z^T + b_z) are
+//     produced one 32-channel tile at a time and multiplied before the store.
+// ---------------------------------------------------------------------------
+template <int CZ, int CH>
+__global__ __launch_bounds__(512) void trimul_epilogue_bf16_kernel(
+    const bf16* __restrict__ z, const bf16* __restrict__ px, bf16* __restrict__ out,
+    TriMulPacked<bf16> w, int N, int Np, int residual, float eps_in, float eps_out,
+    int64_t ntiles) {
+  constexpr int WAVES = 8;
+  constexpr int KZ = CZ / 16;                 // k chunks over c_z (gate input)
+  constexpr int KX = CH / 16;                 // k chunks over c (W_z input)
+  constexpr int PG = (CZ / 32) * KZ * 512;    // packed W_g elements
+  constexpr int PZ = (CZ / 32) * KX * 512;    // packed W_z elements
+  __shared__ __attribute__((aligned(1024))) bf16 wl[PG + PZ];
+  __shared__ __attribute__((aligned(1024))) bf16 xt[WAVES][CH * 32];
+  __shared__ __attribute__((aligned(16))) float bl[2 * CZ];
+  copy_to_lds_async(wl, w.w_g, PG * 2);
+  copy_to_lds_async(wl + PG, w.w_z, PZ * 2);
+  for (int t = threadIdx.x; t < CZ; t += blockDim.x) {
+    bl[t] = w.b_g[t];
+    bl[CZ + t] = w.b_z[t];
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int half = lane >> 5;
+  const int t32 = lane & 31;
+  const int jtiles = (N + 31) / 32;
+  const int64_t plane = (int64_t)Np * Np;
+  bf16* xw = xt[wave];
+  const bf16* wg = wl;
+  const bf16* wz = wl + PG;
+
+  // x tile in LDS: channel row c at xw + 32c, physical 16-byte chunk p holds
+  // pairs 8k .. 8k+7 with k = p ^ swz(c).  Copy instruction n moves rows
+  // 16n .. 16n+15; lane l lands at row 16n + l/4, physical chunk l%4.
+  auto swz = [](int c) { return 2 * ((c >> 1) & 1); };
+  auto issue_x = [&](int64_t tile) {
+    const int jt = (int)(tile % jtiles);
+    const int i = (int)((tile / jtiles) % N);
+    const int b = (int)(tile / ((int64_t)jtiles * N));
+    const bf16* src = px + (int64_t)b * CH * plane + (int64_t)i * Np + jt * 32;
+#pragma unroll
+    for (int n = 0; n < CH / 16; ++n) {
+      const int row = 16 * n + (lane >> 2);
+      const int k = (lane & 3) ^ swz(row);
+      g2lds16(src + row * plane + 8 * k, xw + n * 512);
+    }
+  };
+  auto load_z = [&](Frag<bf16>* zr, int64_t tile) {
+    const int jt = (int)(tile % jtiles);
+    const int i = (int)((tile / jtiles) % N);
+    const int b = (int)(tile / ((int64_t)jtiles * N));
+    const int j = jt * 32 + t32;
+    const bool valid = j < N;
+    const bf16* row = z + (((int64_t)b * N + i) * N + (valid ? j : 0)) * CZ + half * (CZ / 2);
+#pragma unroll
+    for (int ch = 0; ch < KZ; ++ch) {
+      if (valid) zr[ch].load(row + ch * 8);
+      else zr[ch].zero();
+    }
+  };
+  // transposing-read addresses: fetching lane (group G = lane/16, i = lane%16)
+  // reads channel row c_m, m = i/4, at pairs 16*(G&1) + 4*(i%4) .. +3
+  const int G = lane >> 4;
+  const int fm = (lane & 15) >> 2;
+  const int fq = lane & 3;
+  const int fk = 2 * (G & 1) + (fq >> 1);      // logical chunk
+  const int fsub = 4 * (fq & 1);               // element offset inside the chunk
+  auto read_x = [&](Frag<bf16>* xr) {
+#pragma unroll
+    for (int ks = 0; ks < KX; ++ks) {
+      s16x4 part[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int c = (G >> 1) * (CH / 2) + ks * 8 + hh * 4 + fm;
+        part[hh] = lds_read_tr16(xw + c * 32 + 8 * (fk ^ swz(c)) + fsub);
+      }
+      const s16x4 lo = part[0], hi = part[1];
+      typedef short s16x8 __attribute__((ext_vector_type(8)));
+      const s16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      xr[ks].v = __builtin_bit_cast(bf16x8, v);
+    }
+  };
+
+  int64_t tile = (int64_t)blockIdx.x * WAVES + wave;
+  const int64_t stride = (int64_t)gridDim.x * WAVES;
+  Frag<bf16> zr[KZ];
+  if (tile < ntiles) {
+    issue_x(tile);
+    load_z(zr, tile);
+  }
+  for (; tile < ntiles; tile += stride) {
+    const int jt = (int)(tile % jtiles);
+    const int i = (int)((tile / jtiles) % N);
+    const int b = (int)(tile / ((int64_t)jtiles * N));
+    const int j = jt * 32 + t32;
+    const bool valid = j < N;
+    const int64_t pair = ((int64_t)b * N + i) * N + (valid ? j : 0);
+    Frag<bf16> xf[KZ], yf[KX];
+    ln_frags_bf16<CZ>(xf, zr, eps_in);
+    __builtin_amdgcn_s_waitcnt(0);  // this tile's x copy has landed in LDS
+    {
+      Frag<bf16> xr[KX];
+      read_x(xr);
+      ln_frags_bf16<CH>(yf, xr, eps_out);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // transposing reads done: the buffer is free
+    const int64_t next = tile + stride;
+    if (next < ntiles) {
+      issue_x(next);
+      load_z(zr, next);
+    }
+#pragma unroll 1
+    for (int nt = 0; nt < CZ / 32; ++nt) {
+      Frag<bf16> f;
+      load_wfrag_lds(f, wg, nt, 0, KZ);
+      f32x16 ga = mma0(f, xf[0]);
+#pragma unroll
+      for (int ks = 1; ks < KZ; ++ks) {
+        load_wfrag_lds(f, wg, nt, ks, KZ);
+        mma(ga, f, xf[ks]);
+      }
+      load_wfrag_lds(f, wz, nt, 0, KX);
+      f32x16 oa = mma0(f, yf[0]);
+#pragma unroll
+      for (int ks = 1; ks < KX; ++ks) {
+        load_wfrag_lds(f, wz, nt, ks, KX);
+        mma(oa, f, yf[ks]);
+      }
+      if (valid) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int c0 = nt * 32 + 8 * g + 4 * half;
+          const f32x4 bg = *reinterpret_cast<const f32x4*>(bl + c0);
+          const f32x4 bz = *reinterpret_cast<const f32x4*>(bl + CZ + c0);
+          float o[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[r] = (oa[4 * g + r] + bz[r]) * gate_from_u(ga[4 * g + r] + bg[r]);
+          if (residual) {
+            const f32x4 zres = load4f(z + pair * CZ + c0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o[r] += zres[r];
+          }
+          store4(out + pair * CZ + c0, o[0], o[1], o[2], o[3]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Layout conversion for the raw contraction op:
 //   pairs [B][N][N][C]  <->  planes [B][C][Np][Np]
 // ---------------------------------------------------------------------------
@@ -616,7 +779,13 @@ static int fwd_trimul(const void* z, const float* mask, void* out, const void* p
   int rc = launch_contract<T>(pa, pb, px, Np, B * CH, st);
   if (rc) return rc;
   const int64_t etiles = B * N * ((N + 31) / 32);
-  {
+  if constexpr (sizeof(T) == 2) {
+    const int grid = (int)std::min<int64_t>(device_cus(), (etiles + 7) / 8);
+    StageTimer timer("trimul_epilogue", st);
+    trimul_epilogue_bf16_kernel<CZ, CH><<<grid, 512, 0, st>>>(
+        (const bf16*)z, (const bf16*)px, (bf16*)out, w, (int)N, Np, residual, eps_in, eps_out,
+        etiles);
+  } else {
     StageTimer timer("trimul_epilogue", st);
     trimul_epilogue_kernel<T, CZ, CH><<<(unsigned)((etiles + 3) / 4), 256, 0, st>>>(
         (const T*)z, px, (T*)out, w, (int)B, (int)N, Np, residual, eps_in, eps_out);
