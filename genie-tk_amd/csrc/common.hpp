@@ -284,6 +284,13 @@ __device__ __forceinline__ void copy_to_lds_async(void* dst, const void* __restr
     g2lds16((const char*)src + blk * 1024 + lane * 16, (char*)dst + blk * 1024);
 }
 
+// s_barrier without the fence that __syncthreads() adds: that fence waits for
+// every outstanding global load, including direct-to-LDS copies meant to stay
+// in flight across the barrier.  Callers order memory themselves with
+// explicit s_waitcnt; the "memory" clobber keeps the compiler from moving
+// memory accesses across the barrier.
+__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+
 // A zero the compiler cannot see through.  Adding it to a loop-invariant LDS
 // address inside a loop keeps the loads in the loop: hoisted out, the
 // fragments would stay live across the whole loop and spill.

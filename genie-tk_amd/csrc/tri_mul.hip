@@ -331,6 +331,124 @@ __global__ __launch_bounds__(256) void trimul_contract_kernel(const T* __restric
 }
 
 // ---------------------------------------------------------------------------
+// 2b. bf16 contraction: one TI x TJ output tile per block of (TI/64)x(TJ/64)
+//     waves, each wave 64x64.  k advances in stages of 64: the A and Bm
+//     panels (TI and TJ rows x 128 bytes, whole cache lines) move by direct
+//     global->LDS copies into a double buffer, the next stage issued before
+//     the current one is consumed, so no VGPRs stage the operands.  The
+//     panels are re-read once per tile of the other operand, so the 256x256
+//     tile halves the L2->LDS traffic of a 128x128 one.  Panel rows are
+//     chunk-swizzled (16-byte chunk c of row r sits at c ^ f(r)), which makes
+//     the fragment reads bank-conflict free.
+// ---------------------------------------------------------------------------
+template <int TI, int TJ>
+__global__ __launch_bounds__(64 * (TI / 64) * (TJ / 64)) void trimul_contract_bf16_kernel(
+    const bf16* __restrict__ pa, const bf16* __restrict__ pb, bf16* __restrict__ px, int Np,
+    int64_t nplanes) {
+  constexpr int BK = 64, NS = 2;
+  constexpr int NW = (TI / 64) * (TJ / 64);         // waves
+  constexpr int RPR = 1024 / (2 * BK);              // panel rows per 1 KiB copy
+  constexpr int CPR = BK / 8;                       // 16-byte chunks per panel row
+  static_assert((TI / RPR) % NW == 0 && (TJ / RPR) % NW == 0, "copies split evenly");
+  __shared__ __attribute__((aligned(1024))) bf16 ra_l[NS][TI * BK];
+  __shared__ __attribute__((aligned(1024))) bf16 rb_l[NS][TJ * BK];
+
+  const int ti_n = Np / TI, tj_n = Np / TJ;
+  const int64_t total = (int64_t)ti_n * tj_n * nplanes;
+  const int64_t lin = xcd_remap((int64_t)blockIdx.x, total);
+  const int64_t pl = lin / ((int64_t)ti_n * tj_n);
+  const int trem = (int)(lin % ((int64_t)ti_n * tj_n));
+  const int i0 = (trem / tj_n) * TI;
+  const int j0 = (trem % tj_n) * TJ;
+  const int64_t plane = (int64_t)Np * Np;
+  const bf16* A = pa + pl * plane;
+  const bf16* Bm = pb + pl * plane;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int half = lane >> 5;
+  const int wi = (wave / (TJ / 64)) * 64;  // wave row offset (i)
+  const int wj = (wave % (TJ / 64)) * 64;  // wave col offset (j)
+  // chunk swizzle of panel row r: distinct for any rows that share LDS banks,
+  // whether 8 or 16 lanes are served per cycle
+  auto pswz = [](int r) { return (r ^ (r >> 3)) & 7; };
+
+  // copies: a panel is (rows/RPR) regions of RPR rows x CPR chunks; wave w
+  // moves regions w, w+NW, ... of both panels; lane l lands at row
+  // RPR*n + l/CPR, chunk l%CPR
+  constexpr int RA = TI / RPR / NW, RB = TJ / RPR / NW;
+  const bf16* srcA[RA];
+  const bf16* srcB[RB];
+#pragma unroll
+  for (int u = 0; u < RA; ++u) {
+    const int row = RPR * (wave + u * NW) + lane / CPR;
+    srcA[u] = A + (int64_t)(i0 + row) * Np + 8 * ((lane % CPR) ^ pswz(row));
+  }
+#pragma unroll
+  for (int u = 0; u < RB; ++u) {
+    const int row = RPR * (wave + u * NW) + lane / CPR;
+    srcB[u] = Bm + (int64_t)(j0 + row) * Np + 8 * ((lane % CPR) ^ pswz(row));
+  }
+  auto issue = [&](int stage, int k0) {
+#pragma unroll
+    for (int u = 0; u < RA; ++u) g2lds16(srcA[u] + k0, &ra_l[stage][(wave + u * NW) * 512]);
+#pragma unroll
+    for (int u = 0; u < RB; ++u) g2lds16(srcB[u] + k0, &rb_l[stage][(wave + u * NW) * 512]);
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) acc[x][y] = zero16();
+
+  const int KT = Np / BK;  // Np is a multiple of 128: KT >= 2
+  issue(0, 0);
+  for (int kt = 0; kt < KT; ++kt) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies of stage kt landed
+    barrier_only();  // stage kt visible to every wave; stage kt-1 fully consumed
+    if (kt + 1 < KT) issue((kt + 1) % NS, (kt + 1) * BK);
+    const bf16* sa = ra_l[kt % NS];
+    const bf16* sb = rb_l[kt % NS];
+    // fragments of all k chunks are read up front so later chunks' reads
+    // overlap the earlier chunks' MFMAs
+    Frag<bf16> fa[BK / 16][2], fb[BK / 16][2];
+#pragma unroll
+    for (int kc = 0; kc < BK / 16; ++kc) {
+      const int lc = kc * 2 + half;
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const int r_a = wi + x * 32 + (lane & 31);
+        const int r_b = wj + x * 32 + (lane & 31);
+        fa[kc][x].load(sa + r_a * BK + 8 * (lc ^ pswz(r_a)));
+        fb[kc][x].load(sb + r_b * BK + 8 * (lc ^ pswz(r_b)));
+      }
+    }
+#pragma unroll
+    for (int kc = 0; kc < BK / 16; ++kc)
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y) mma(acc[x][y], fb[kc][y], fa[kc][x]);  // rows j, cols i
+  }
+
+  // acc[x][y]: lane holds X[i = wi + 32x + (l&31)][j = wj + 32y + 8g + 4h + r]
+  bf16* X = px + pl * plane;
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    const int i = i0 + wi + x * 32 + (lane & 31);
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int j = j0 + wj + y * 32 + 8 * g + 4 * half;
+        store4(X + (int64_t)i * Np + j, acc[x][y][4 * g + 0], acc[x][y][4 * g + 1],
+               acc[x][y][4 * g + 2], acc[x][y][4 * g + 3]);
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // 3. Epilogue
 // ---------------------------------------------------------------------------
 template <typename T, int CZ, int CH>
@@ -659,11 +777,20 @@ __global__ __launch_bounds__(256) void planes_to_pairs_kernel(const T* __restric
 template <typename T>
 static int launch_contract(const T* pa, const T* pb, T* px, int Np, int64_t nplanes,
                            hipStream_t st) {
-  if (Np % 128 == 0) {
+  if (sizeof(T) == 2 && Np % 256 == 0) {
+    const int64_t blocks = (int64_t)(Np / 256) * (Np / 256) * nplanes;
+    GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "contraction grid too large");
+    StageTimer timer("trimul_contract", st);
+    trimul_contract_bf16_kernel<256, 256><<<(unsigned)blocks, 1024, 0, st>>>(
+        (const bf16*)pa, (const bf16*)pb, (bf16*)px, Np, nplanes);
+  } else if (Np % 128 == 0) {
     const int64_t blocks = (int64_t)(Np / 128) * (Np / 128) * nplanes;
     GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "contraction grid too large");
     StageTimer timer("trimul_contract", st);
-    trimul_contract_kernel<T, 128><<<(unsigned)blocks, 256, 0, st>>>(pa, pb, px, Np, nplanes);
+    if constexpr (sizeof(T) == 2)
+      trimul_contract_bf16_kernel<128, 128><<<(unsigned)blocks, 256, 0, st>>>(pa, pb, px, Np, nplanes);
+    else
+      trimul_contract_kernel<T, 128><<<(unsigned)blocks, 256, 0, st>>>(pa, pb, px, Np, nplanes);
   } else {
     const int64_t blocks = (int64_t)(Np / 64) * (Np / 64) * nplanes;
     GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "contraction grid too large");
