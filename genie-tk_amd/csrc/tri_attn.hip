@@ -541,23 +541,25 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t lin, int64_t total) {
 }
 
 
-template <int CIN, int H>
-__global__ __launch_bounds__(1024) void triattn_flash_kernel(
+template <int CIN, int H, int QT>
+__global__ __launch_bounds__(64 * H * QT) void triattn_flash_kernel(
     const bf16* __restrict__ x, const float* __restrict__ mask, bf16* __restrict__ out,
     TriAttnPacked<bf16> w, AttnWs<bf16> ws, int N, int Np, int starting, int residual) {
   constexpr int CH = H * HD;
-  constexpr int QB = 128;                  // queries per block
-  constexpr int QT = QB / 32;              // query tiles (waves) per head
+  constexpr int QB = 32 * QT;              // queries per block (QT query tiles per head)
+  constexpr int NW = H * QT;               // waves
   constexpr int KB = 64;                   // keys per stage
-  constexpr int NS = 3;                    // LDS ring stages
+  constexpr int NS = QT == 4 ? 3 : 2;      // LDS ring stages
+  constexpr bool WO_LDS = QT == 4;         // W_o staged in LDS (else read from L2)
   constexpr int OP = CH + 8;               // gated-o row pitch in LDS (elements)
   constexpr int HEAD_BYTES = KB * HD * 2;  // K (or V^T) bytes of one head per stage: 4 KiB
   constexpr int STAGE_BYTES = 2 * H * HEAD_BYTES;
+  constexpr int RPW = (STAGE_BYTES / 1024) / NW;  // 1 KiB copy regions per wave per stage
   constexpr float kRescale = 8.0f;         // lazy-rescale threshold (log2 units)
-  static_assert(H == 4 && H * QT * 64 == 1024, "block is 16 waves");
+  static_assert(H == 4 && (QT == 4 || QT == 2), "4 heads; 64 or 128 queries per block");
   static_assert(QB * OP * 2 <= NS * STAGE_BYTES, "o staging must fit in the ring");
   __shared__ __attribute__((aligned(1024))) char ring[NS][STAGE_BYTES];
-  __shared__ __attribute__((aligned(1024))) bf16 wo_l[(CIN / 32) * (CH / 16) * 512];  // packed W_o
+  __shared__ __attribute__((aligned(1024))) bf16 wo_l[WO_LDS ? (CIN / 32) * (CH / 16) * 512 : 8];
   // excluded keys of this row, one bit per key: bit j of word t is key 32t + j
   __shared__ unsigned kmask[MAXN / 32];  // mask == 0
   __shared__ unsigned kpad[MAXN / 32];   // key >= N
@@ -586,7 +588,7 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
   __syncthreads();
   {
     bool any = false;
-    for (int k0 = wave * 64; k0 < Np; k0 += 1024) {
+    for (int k0 = wave * 64; k0 < Np; k0 += NW * 64) {
       const int k = k0 + lane;
       const bool inrow = k < N;
       const bool masked = inrow && mrow && mrow[k * mks] == 0.f;
@@ -606,23 +608,23 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
   const bool row_valid = row_any != 0;
 
   // Async stage load.  A stage is 32 regions of 1 KiB (64 lanes x 16 B);
-  // wave w moves regions 2w and 2w+1.  Regions 0..15: K, head reg/4, chunks
-  // P = (reg%4)*64 + lane of that head's [64 keys][32 d] tile; regions
-  // 16..31: V^T, head (reg-16)/4, chunks of its [32 d][64 keys] tile.
+  // wave w moves regions RPW*w .. RPW*w + RPW-1.  Regions 0..15: K, head
+  // reg/4, chunks P = (reg%4)*64 + lane of that head's [64 keys][32 d] tile;
+  // regions 16..31: V^T, head (reg-16)/4, chunks of its [32 d][64 keys] tile.
   // Physical chunk P of a K tile holds row P/4, logical chunk
   // (P%4) ^ ((row>>1)&3); of a V^T tile row d = P/8, logical chunk (P%8) ^ (d&7).
   const bf16* kbase = ws.k + (rowbase * H) * (int64_t)Np * HD;
   const bf16* vbase = ws.vt + (rowbase * H) * (int64_t)HD * Np;
-  const bool k_region = wave < 8;          // waves 0..7 move K, 8..15 move V^T
-  const int rg_head = (wave & 7) >> 1;
-  const int rg_sub0 = (wave & 1) * 2;
+  const bool k_region = wave < NW / 2;     // the first half of the waves move K
+  const int rg_head = ((wave * RPW) & 15) >> 2;
+  const int rg_sub0 = (wave * RPW) & 3;
   // this lane's source element of region i at key 0 (a stage at key k0 adds
   // k0 * kstride), and the wave's LDS destination offset of region i
   const int64_t kstride = k_region ? HD : 1;
-  const bf16* gsrc[2];
-  int dst_off[2];
+  const bf16* gsrc[RPW];
+  int dst_off[RPW];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
+  for (int i = 0; i < RPW; ++i) {
     const int sub = rg_sub0 + i;
     const int P = sub * 64 + lane;
     if (k_region) {
@@ -639,12 +641,12 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
   }
   auto issue_stage = [&](int stage, int k0) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) g2lds16(gsrc[i] + k0 * kstride, ring[stage] + dst_off[i]);
+    for (int i = 0; i < RPW; ++i) g2lds16(gsrc[i] + k0 * kstride, ring[stage] + dst_off[i]);
   };
 
   // W_o for the epilogue, and this lane's gate values, fetched now so that
   // neither load is waited for at the end
-  copy_to_lds_async(wo_l, w.w_o, (int)sizeof(wo_l));
+  if constexpr (WO_LDS) copy_to_lds_async(wo_l, w.w_o, (int)sizeof(wo_l));
   bf16x4 gpre[4];
   {
     const bf16* gr = ws.gate + (rowbase * Np + q0 + t32) * CH + h * HD;
@@ -791,7 +793,8 @@ __global__ __launch_bounds__(1024) void triattn_flash_kernel(
 #pragma unroll
     for (int ks = 0; ks < CH / 16; ++ks) {
       Frag<bf16> wf;
-      load_wfrag_lds(wf, wo_l, nt, ks, CH / 16);
+      if constexpr (WO_LDS) load_wfrag_lds(wf, wo_l, nt, ks, CH / 16);
+      else load_wfrag<bf16>(wf, w.w_o, nt, ks, CH / 16);
       mma(acc, wf, of[ks]);
     }
     const int q = qb * QB + oq * 32 + t32;
@@ -989,9 +992,10 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
   const int64_t blocks = B * N * ((N + 31) / 32);
   GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "attention grid too large");
   if constexpr (sizeof(T) == 2) {
-    const int64_t fblocks = B * N * ((N + 127) / 128);
+    constexpr int QT = 2;  // two 8-wave blocks of 64 queries per CU
+    const int64_t fblocks = B * N * ((N + 32 * QT - 1) / (32 * QT));
     StageTimer timer("triattn_flash", st);
-    triattn_flash_kernel<CIN, H><<<(unsigned)fblocks, 1024, 0, st>>>(
+    triattn_flash_kernel<CIN, H, QT><<<(unsigned)fblocks, 64 * H * QT, 0, st>>>(
         (const bf16*)x, mask, (bf16*)out, w, a, (int)N, Np, starting, residual);
   } else {
     StageTimer timer("triattn_flash", st);
