@@ -611,8 +611,12 @@ __global__ __launch_bounds__(64 * H * QT) void triattn_flash_kernel(
   // wave w moves regions RPW*w .. RPW*w + RPW-1.  Regions 0..15: K, head
   // reg/4, chunks P = (reg%4)*64 + lane of that head's [64 keys][32 d] tile;
   // regions 16..31: V^T, head (reg-16)/4, chunks of its [32 d][64 keys] tile.
-  // Physical chunk P of a K tile holds row P/4, logical chunk
-  // (P%4) ^ ((row>>1)&3); of a V^T tile row d = P/8, logical chunk (P%8) ^ (d&7).
+  // Physical chunk P of a K tile holds row P/4, logical chunk (P%4) ^
+  // kswz(row); of a V^T tile row d = P/8, logical chunk (P%8) ^ vswz(d).  The
+  // swizzles give distinct banks to rows read together, whether 8 or 16
+  // lanes are served per LDS cycle.
+  auto kswz = [](int row) { return ((row >> 1) ^ (row >> 3)) & 3; };
+  auto vswz = [](int d) { return (d ^ (d >> 3)) & 7; };
   const bf16* kbase = ws.k + (rowbase * H) * (int64_t)Np * HD;
   const bf16* vbase = ws.vt + (rowbase * H) * (int64_t)HD * Np;
   const bool k_region = wave < NW / 2;     // the first half of the waves move K
@@ -629,12 +633,12 @@ __global__ __launch_bounds__(64 * H * QT) void triattn_flash_kernel(
     const int P = sub * 64 + lane;
     if (k_region) {
       const int row = P >> 2;
-      const int c = (P & 3) ^ ((row >> 1) & 3);
+      const int c = (P & 3) ^ kswz(row);
       gsrc[i] = kbase + ((int64_t)rg_head * Np + row) * HD + c * 8;
       dst_off[i] = rg_head * HEAD_BYTES + sub * 1024;
     } else {
       const int d = P >> 3;
-      const int c = (P & 7) ^ (d & 7);
+      const int c = (P & 7) ^ vswz(d);
       gsrc[i] = vbase + ((int64_t)rg_head * HD + d) * Np + c * 8;
       dst_off[i] = (H + rg_head) * HEAD_BYTES + sub * 1024;
     }
@@ -688,7 +692,7 @@ __global__ __launch_bounds__(64 * H * QT) void triattn_flash_kernel(
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       Frag<bf16> kf;
-      const int c = (m * 2 + half) ^ ((row >> 1) & 3);
+      const int c = (m * 2 + half) ^ kswz(row);
       kf.load(reinterpret_cast<const bf16*>(kt_base + row * 64 + c * 16));
       mma(s, kf, qf[m]);
     }
@@ -763,7 +767,7 @@ __global__ __launch_bounds__(64 * H * QT) void triattn_flash_kernel(
         l_run = __builtin_amdgcn_fdot2_f32_bf16(pp, ones2, l_run, false);
       }
       // V^T row d = t32, keys (t&1)*32 + 16c + 8*half .. +8
-      const int lc = ((t & 1) * 4 + 2 * c + half) ^ (t32 & 7);
+      const int lc = ((t & 1) * 4 + 2 * c + half) ^ vswz(t32);
       vf.load(reinterpret_cast<const bf16*>(vt_base + t32 * 128 + lc * 16));
       mma(o, vf, pf);
     }
