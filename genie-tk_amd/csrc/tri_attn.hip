@@ -8,10 +8,14 @@
 //
 //  1. prologue: per pair, LN -> q (pre-scaled by log2(e)/sqrt(d)), k, v,
 //     gate sigmoid(. + b_g) and the triangle bias (scaled by log2(e)), all on
-//     the matrix cores.  Workspace layouts (Np = N rounded up to 128):
-//        q, k  [B][Np r][H][Np j][32]     v^T [B][Np r][H][32][Np j]
-//        gate  [B][Np r][Np j][c_h]       bias [B][H][Np q][Np k]
-//     (all in the compute type: bf16 for bf16 inputs, fp32 for fp32)
+//     the matrix cores.  Workspace layouts (Np = N rounded up to 128; all in
+//     the compute type):
+//        fp32 path and the raw op:
+//          q, k  [B][Np r][H][Np j][32]     v^T [B][Np r][H][32][Np j]
+//          gate  [B][Np r][Np j][c_h]       bias [B][H][Np q][Np k]
+//        bf16 module path (channel-major, written as 32-byte runs):
+//          q, k, v^T  [B][Np r][H][32][Np j]    gate [B][Np r][c_h][Np j]
+//          bias       [B][H][Np q][Np k]
 //  2. flash core: one wave = one head x 32 queries of one row; keys in tiles
 //     of 32.  S^T = K Q^T is accumulated on top of the bias tile, so lane l
 //     owns one query and 16 of its keys; the row max needs one lane^32
@@ -185,12 +189,14 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
 //     (4 x 32 KiB + 8 KiB, direct global->LDS copies) and the folded biases
 //     beside them; each wave then loops over 32-pair tiles.
 //     Lane i32 of a wave normalises pair 16*((i32>>2)&1) + 4*(i32>>3) + (i32&3)
-//     of the tile.  q, k and the gate (channel-contiguous layouts) take the
-//     weights as the A operand: a lane's accumulators are 16 channels of its
-//     own pair.  v^T and the triangle bias (position-contiguous layouts) take
-//     the pairs as the A operand: the row permutation above then gives every
-//     lane 16 consecutive positions of one channel, stored as 32 bytes.
-//     Output values and padding are those of triattn_prologue_kernel.
+//     of the tile and the pairs are the MFMA A operand, so every accumulator
+//     lane holds 16 consecutive positions of one output channel.  All outputs
+//     of this path are channel-major over positions (below), so each lane
+//     writes them as 32 contiguous bytes.  Workspace layouts of the bf16 path
+//     (Np = N rounded up to 128):
+//        q, k  [B][Np r][H][32 d][Np j]    v^T [B][Np r][H][32 d][Np j] (vt_pos order)
+//        gate  [B][Np r][c_h][Np j]        bias [B][H][Np q][Np k]
+//     Padding values are those of triattn_prologue_kernel.
 // ---------------------------------------------------------------------------
 template <int CIN, int H>
 __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
@@ -237,13 +243,13 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
       const int64_t pair = ((int64_t)b * N + (valid ? p : 0)) * N + (valid ? q : 0);
       ln_row_bf16<CIN>(xf, x + pair * CIN, valid, eps);
     }
-    const float keep = valid ? 1.f : 0.f;
     const int64_t rowbase = (int64_t)b * Np + r;
     const int j0 = vt * 32 + 16 * half;         // first of this lane's 16 positions
     // validity of the 16 positions j0 + jj, as a bit mask
     const int nvalid = r < N ? min(max(N - j0, 0), 16) : 0;
 
-    // q, k, v, gate: one 32-channel tile (one head) per step, one MFMA chain each
+    // q, k, v, gate: one 32-channel tile (one head) per step, one MFMA chain
+    // each; lane (i32, half) ends with positions j0 .. j0+15 of channel i32
 #pragma unroll 1
     for (int step = 0; step < 4 * H; ++step) {
       const int kind = step / H;  // 0 q, 1 k, 2 v, 3 gate
@@ -251,54 +257,36 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
       const bf16* wt = wl + kind * PE;
       Frag<bf16> fw;
       load_wfrag_lds(fw, wt, h, 0, KCH);
-      f32x16 acc = kind == 2 ? mma0(xf[0], fw) : mma0(fw, xf[0]);
-      if (kind == 2) {
+      f32x16 acc = mma0(xf[0], fw);
 #pragma unroll
-        for (int ks = 1; ks < KCH; ++ks) {
-          load_wfrag_lds(fw, wt, h, ks, KCH);
-          mma(acc, xf[ks], fw);
-        }
-        // v^T: position-contiguous [b][r][h][32][j] in vt_pos order
-        const float bv = bl[2 * CH + h * HD + i32];
-        uint32_t pk[8];
+      for (int ks = 1; ks < KCH; ++ks) {
+        load_wfrag_lds(fw, wt, h, ks, KCH);
+        mma(acc, xf[ks], fw);
+      }
+      const float bc = bl[kind * CH + h * HD + i32];
+      uint32_t pk[8];
+      bf16* dst;
+      if (kind == 3) {
+        // gate = sigmoid, at every position (padding included)
+#pragma unroll
+        for (int m = 0; m < 16; m += 2)
+          pk[m / 2] = pack_bf16x2(gate_from_u(acc[m] + bc), gate_from_u(acc[m + 1] + bc));
+        dst = ws.gate + (rowbase * CH + h * HD + i32) * (int64_t)Np + j0;
+      } else {
+        // q, k, v: zero outside the N x N pair grid; v^T in vt_pos order, which
+        // swaps bits 2 and 3 of the position inside its group of 16
 #pragma unroll
         for (int m = 0; m < 16; m += 2) {
-          // vt_pos swaps bits 2 and 3 of the position inside its group of 16
-          const int s0 = (m & 3) | ((m & 4) << 1) | ((m & 8) >> 1);
+          const int s0 = kind == 2 ? ((m & 3) | ((m & 4) << 1) | ((m & 8) >> 1)) : m;
           const int s1 = s0 + 1;
-          pk[m / 2] = pack_bf16x2(s0 < nvalid ? acc[s0] + bv : 0.f, s1 < nvalid ? acc[s1] + bv : 0.f);
+          pk[m / 2] = pack_bf16x2(s0 < nvalid ? acc[s0] + bc : 0.f, s1 < nvalid ? acc[s1] + bc : 0.f);
         }
-        uint4* o = reinterpret_cast<uint4*>(ws.vt + ((rowbase * H + h) * HD + i32) * (int64_t)Np + j0);
-        o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-        o[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
-      } else {
-#pragma unroll
-        for (int ks = 1; ks < KCH; ++ks) {
-          load_wfrag_lds(fw, wt, h, ks, KCH);
-          mma(acc, fw, xf[ks]);
-        }
-        if (kind < 2) {
-          // q, k: channel-contiguous [b][r][h][j][32]
-          bf16* dst = (kind ? ws.k : ws.q) + ((rowbase * H + h) * Np + jown) * HD;
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int d0 = 8 * g + 4 * half;
-            const f32x4 bq = *reinterpret_cast<const f32x4*>(bl + kind * CH + h * HD + d0);
-            store4(dst + d0, (acc[4 * g] + bq[0]) * keep, (acc[4 * g + 1] + bq[1]) * keep,
-                   (acc[4 * g + 2] + bq[2]) * keep, (acc[4 * g + 3] + bq[3]) * keep);
-          }
-        } else {
-          // gate: channel-contiguous [b][r][j][c_h]
-          bf16* gd = ws.gate + (rowbase * Np + jown) * CH;
-#pragma unroll
-          for (int g = 0; g < 4; ++g) {
-            const int c0 = h * 32 + 8 * g + 4 * half;
-            const f32x4 bg = *reinterpret_cast<const f32x4*>(bl + 3 * CH + c0);
-            store4(gd + c0, gate_from_u(acc[4 * g] + bg[0]), gate_from_u(acc[4 * g + 1] + bg[1]),
-                   gate_from_u(acc[4 * g + 2] + bg[2]), gate_from_u(acc[4 * g + 3] + bg[3]));
-          }
-        }
+        bf16* base = kind == 0 ? ws.q : kind == 1 ? ws.k : ws.vt;
+        dst = base + ((rowbase * H + h) * HD + i32) * (int64_t)Np + j0;
       }
+      uint4* o = reinterpret_cast<uint4*>(dst);
+      o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+      o[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
     }
     // triangle bias [b][h][r][j]: lanes with i32 < H hold head i32
     {
@@ -542,7 +530,7 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t lin, int64_t total) {
 
 
 template <int CIN, int H, int QT>
-__global__ __launch_bounds__(64 * H * QT) void triattn_flash_kernel(
+__global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))) void triattn_flash_kernel(
     const bf16* __restrict__ x, const float* __restrict__ mask, bf16* __restrict__ out,
     TriAttnPacked<bf16> w, AttnWs<bf16> ws, int N, int Np, int starting, int residual) {
   constexpr int CH = H * HD;
@@ -608,63 +596,57 @@ __global__ __launch_bounds__(64 * H * QT) void triattn_flash_kernel(
   const bool row_valid = row_any != 0;
 
   // Async stage load.  A stage is 32 regions of 1 KiB (64 lanes x 16 B);
-  // wave w moves regions RPW*w .. RPW*w + RPW-1.  Regions 0..15: K, head
-  // reg/4, chunks P = (reg%4)*64 + lane of that head's [64 keys][32 d] tile;
-  // regions 16..31: V^T, head (reg-16)/4, chunks of its [32 d][64 keys] tile.
-  // Physical chunk P of a K tile holds row P/4, logical chunk (P%4) ^
-  // kswz(row); of a V^T tile row d = P/8, logical chunk (P%8) ^ vswz(d).  The
-  // swizzles give distinct banks to rows read together, whether 8 or 16
-  // lanes are served per LDS cycle.
-  auto kswz = [](int row) { return ((row >> 1) ^ (row >> 3)) & 3; };
+  // wave w moves regions RPW*w .. RPW*w + RPW-1.  Regions 0..15: K^T, head
+  // reg/4, chunks P = (reg%4)*64 + lane of that head's [32 d][64 keys] tile;
+  // regions 16..31: V^T likewise.
+  // Physical 16-byte chunk P of a K^T or V^T tile holds row d = P/8, logical
+  // chunk (P%8) ^ vswz(d): rows read together get distinct banks, whether 8
+  // or 16 lanes are served per LDS cycle.
   auto vswz = [](int d) { return (d ^ (d >> 3)) & 7; };
-  const bf16* kbase = ws.k + (rowbase * H) * (int64_t)Np * HD;
+  // K^T and V^T are both [32 d][Np keys] per (row, head); a stage holds the
+  // [32 d][64 keys] tile of each head for both.
+  const bf16* kbase = ws.k + (rowbase * H) * (int64_t)HD * Np;
   const bf16* vbase = ws.vt + (rowbase * H) * (int64_t)HD * Np;
-  const bool k_region = wave < NW / 2;     // the first half of the waves move K
+  const bool k_region = wave < NW / 2;     // the first half of the waves move K^T
   const int rg_head = ((wave * RPW) & 15) >> 2;
   const int rg_sub0 = (wave * RPW) & 3;
   // this lane's source element of region i at key 0 (a stage at key k0 adds
-  // k0 * kstride), and the wave's LDS destination offset of region i
-  const int64_t kstride = k_region ? HD : 1;
+  // k0), and the wave's LDS destination offset of region i
   const bf16* gsrc[RPW];
   int dst_off[RPW];
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
     const int sub = rg_sub0 + i;
     const int P = sub * 64 + lane;
-    if (k_region) {
-      const int row = P >> 2;
-      const int c = (P & 3) ^ kswz(row);
-      gsrc[i] = kbase + ((int64_t)rg_head * Np + row) * HD + c * 8;
-      dst_off[i] = rg_head * HEAD_BYTES + sub * 1024;
-    } else {
-      const int d = P >> 3;
-      const int c = (P & 7) ^ vswz(d);
-      gsrc[i] = vbase + ((int64_t)rg_head * HD + d) * Np + c * 8;
-      dst_off[i] = (H + rg_head) * HEAD_BYTES + sub * 1024;
-    }
+    const int d = P >> 3;
+    const int c = (P & 7) ^ vswz(d);
+    gsrc[i] = (k_region ? kbase : vbase) + ((int64_t)rg_head * HD + d) * Np + c * 8;
+    dst_off[i] = ((k_region ? 0 : H) + rg_head) * HEAD_BYTES + sub * 1024;
   }
   auto issue_stage = [&](int stage, int k0) {
 #pragma unroll
-    for (int i = 0; i < RPW; ++i) g2lds16(gsrc[i] + k0 * kstride, ring[stage] + dst_off[i]);
+    for (int i = 0; i < RPW; ++i) g2lds16(gsrc[i] + k0, ring[stage] + dst_off[i]);
   };
 
-  // W_o for the epilogue, and this lane's gate values, fetched now so that
-  // neither load is waited for at the end
+  // W_o for the epilogue, fetched now so that it is not waited for at the end
   if constexpr (WO_LDS) copy_to_lds_async(wo_l, w.w_o, (int)sizeof(wo_l));
-  bf16x4 gpre[4];
-  {
-    const bf16* gr = ws.gate + (rowbase * Np + q0 + t32) * CH + h * HD;
-#pragma unroll
-    for (int g = 0; g < 4; ++g) gpre[g] = *reinterpret_cast<const bf16x4*>(gr + 8 * g + 4 * half);
-  }
-  // query fragments (zero for a row without valid keys: uniform attention)
+  // query fragments, zero for a row without valid keys (uniform attention);
+  // q is channel-major: one 2-byte element per lane and channel, 32
+  // consecutive positions per load instruction
   Frag<bf16> qf[2];
-  const bf16* qrow = ws.q + ((rowbase * H + h) * Np + q0 + t32) * HD;
+  const bf16* qcol = ws.q + ((rowbase * H + h) * HD) * (int64_t)Np + q0 + t32;
 #pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    if (row_valid) qf[m].load(qrow + m * 16 + half * 8);
-    else qf[m].zero();
-  }
+  for (int m = 0; m < 2; ++m)
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      qf[m].v[e] = row_valid ? qcol[(int64_t)(m * 16 + half * 8 + e) * Np] : (bf16)0.0f;
+  // K fragments come from the K^T tile with transposing reads: fetching lane
+  // (group G = lane/16, i = lane%16) reads d row (i/4) of a 4-row group at
+  // keys 16*(G&1) + 4*(i%4) .. +3 of the 32-key tile; the receiving lane
+  // (key t32, half) gets d .. d+3 of its key
+  const int trG = lane >> 4;
+  const int tr_m = (lane & 15) >> 2;
+  const int tr_q = lane & 3;
   // identity fragments: row key (t32), slot half*8+e of chunk cb <-> key cb*16+half*8+e
   Frag<bf16> idf[2];
 #pragma unroll
@@ -688,12 +670,20 @@ __global__ __launch_bounds__(64 * H * QT) void triattn_flash_kernel(
     f32x16 s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(idf[0].v, bfr[0].v, negm, 0, 0, 0);
     mma(s, idf[1], bfr[1]);
     const char* kt_base = ring[(t >> 1) % NS] + h * HEAD_BYTES;
-    const int row = (t & 1) * 32 + t32;
+    const int chunk = (t & 1) * 4 + 2 * (trG & 1) + (tr_q >> 1);  // logical 8-key chunk
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
+      s16x4 part[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int d = m * 16 + (trG >> 1) * 8 + hh * 4 + tr_m;
+        part[hh] = lds_read_tr16(kt_base + d * 128 + 16 * (chunk ^ vswz(d)) + 8 * (tr_q & 1));
+      }
+      typedef short s16x8 __attribute__((ext_vector_type(8)));
+      const s16x8 v8 = {part[0][0], part[0][1], part[0][2], part[0][3],
+                        part[1][0], part[1][1], part[1][2], part[1][3]};
       Frag<bf16> kf;
-      const int c = (m * 2 + half) ^ kswz(row);
-      kf.load(reinterpret_cast<const bf16*>(kt_base + row * 64 + c * 16));
+      kf.v = __builtin_bit_cast(bf16x8, v8);
       mma(s, kf, qf[m]);
     }
     return s;
@@ -773,6 +763,15 @@ __global__ __launch_bounds__(64 * H * QT) void triattn_flash_kernel(
     }
   }
   const float inv = 1.0f / lane_pair_sum(l_run);
+  // this lane's gate values (channel-major, like q)
+  bf16x4 gpre[4];
+  {
+    const bf16* gr = ws.gate + (rowbase * CH + h * HD) * (int64_t)Np + q0 + t32;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) gpre[g][rr] = gr[(int64_t)(8 * g + 4 * half + rr) * Np];
+  }
 
   // o * gate for all heads, staged as [query][CH] over the ring
   __syncthreads();
