@@ -3,7 +3,8 @@
 // gtk_layernorm: one pass over HBM.  A row of D channels is spread over D/8
 // lanes (8 contiguous channels = 16 B of bf16 per lane), so one wave covers
 // 64*8/D rows per step with fully coalesced 16 B loads and stores; U steps
-// are issued before any arithmetic so each wave keeps U loads in flight.
+// are issued before any arithmetic so each wave keeps U loads in flight, and
+// the stores are non-temporal.
 // Statistics use an xor-butterfly inside the row's lane group.
 //
 // gtk_fused_layernorm_linear: the row is normalised in MFMA fragment layout
@@ -70,11 +71,13 @@ __global__ __launch_bounds__(256) void ln_rows_kernel(const T* __restrict__ x, T
       for (int e = 0; e < 8; ++e) o[e] = (v[u][e] - mean) * rstd * g[e] + bt[e];
       Frag<T> f;
       f.set(o);
+      // non-temporal stores: the output streams to HBM without displacing
+      // the input from the caches
       if constexpr (sizeof(T) == 2) {
-        *reinterpret_cast<bf16x8*>(y + r * D + c0) = f.v;
+        __builtin_nontemporal_store(f.v, reinterpret_cast<bf16x8*>(y + r * D + c0));
       } else {
-        *reinterpret_cast<f32x4*>(y + r * D + c0) = f.lo;
-        *reinterpret_cast<f32x4*>(y + r * D + c0 + 4) = f.hi;
+        __builtin_nontemporal_store(f.lo, reinterpret_cast<f32x4*>(y + r * D + c0));
+        __builtin_nontemporal_store(f.hi, reinterpret_cast<f32x4*>(y + r * D + c0 + 4));
       }
     }
   }
@@ -109,7 +112,7 @@ __global__ __launch_bounds__(256) void ln_rows_generic_kernel(const T* __restric
 template <typename T>
 static int launch_ln(const T* x, T* y, const float* g, const float* b, int64_t rows, int64_t d,
                      float eps, hipStream_t st) {
-  constexpr int U = 4;
+  constexpr int U = 2;
   StageTimer timer("layernorm", st);
   auto grid_for = [&](int D) {
     const int64_t rows_per_block = 4 * (64 / (D / 8)) * U;
