@@ -123,10 +123,11 @@ __global__ __launch_bounds__(256) void trimul_prologue_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// 1b. bf16 prologue: persistent, one 1024-thread block per CU with the four
-//     packed c_z->c weights resident in LDS (4 x 32 KiB, loaded with direct
-//     global->LDS copies); every wave then loops over 32-pair tiles with no
-//     further synchronisation.
+// 1b. bf16 prologue: persistent, 8 waves per CU (256 VGPRs each) with the
+//     four packed c_z->c weights resident in LDS (4 x 32 KiB, loaded with
+//     direct global->LDS copies).  Each wave step covers two 32-pair tiles of
+//     one row: every weight fragment read from LDS feeds both tiles' MFMAs,
+//     halving LDS traffic per MFMA.
 //
 //     The pairs are the MFMA A operand (rows) and the weights the B operand
 //     (columns = channels).  A-operand row i carries tile pair
@@ -137,10 +138,11 @@ __global__ __launch_bounds__(256) void trimul_prologue_kernel(
 //     one FMA beside its two transcendental instructions.
 // ---------------------------------------------------------------------------
 template <int CZ, int CH>
-__global__ __launch_bounds__(1024) void trimul_prologue_bf16_kernel(
+__global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
     const bf16* __restrict__ z, const float* __restrict__ mask, bf16* __restrict__ pa,
     bf16* __restrict__ pb, TriMulPacked<bf16> w, int N, int Np, int outgoing, float eps,
     int64_t ntiles) {
+  constexpr int WAVES = 8;
   constexpr int KCH = CZ / 16;
   constexpr int PE = (CH / 32) * KCH * 512;  // packed elements of one projection
   __shared__ __attribute__((aligned(1024))) bf16 wl[4][PE];
@@ -152,35 +154,62 @@ __global__ __launch_bounds__(1024) void trimul_prologue_bf16_kernel(
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int half = lane >> 5;
   const int i32 = lane & 31;
   const int prow = 16 * ((i32 >> 2) & 1) + 4 * (i32 >> 3) + (i32 & 3);
-  const int vtiles = Np / 32;
+  const int vtiles = Np / 32;  // even: Np is a multiple of 64
   const int64_t plane = (int64_t)Np * Np;
-  for (int64_t tile = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 6); tile < ntiles;
-       tile += (int64_t)gridDim.x * 16) {
+  const int64_t nsteps = ntiles / 2;
+
+  // raw z rows of the two tiles of step s (zeros outside the N x N pair grid)
+  auto load_z = [&](Frag<bf16> (*zr)[KCH], int64_t s) {
+    const int64_t tile = 2 * s;
     const int vt = (int)(tile % vtiles);
     const int f = (int)((tile / vtiles) % Np);
     const int b = (int)(tile / ((int64_t)vtiles * Np));
-    Frag<bf16> xf[KCH];
-    {
-      const int v = vt * 32 + prow;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int v = (vt + u) * 32 + prow;
       const int p = outgoing ? f : v, q = outgoing ? v : f;
       const bool valid = p < N && q < N;
-      const int64_t pair = ((int64_t)b * N + (valid ? p : 0)) * N + (valid ? q : 0);
-      ln_row_bf16<CZ>(xf, z + pair * CZ, valid, eps);
+      const bf16* row = z + (((int64_t)b * N + (valid ? p : 0)) * N + (valid ? q : 0)) * CZ + half * (CZ / 2);
+#pragma unroll
+      for (int ch = 0; ch < KCH; ++ch) {
+        if (valid) zr[u][ch].load(row + ch * 8);
+        else zr[u][ch].zero();
+      }
     }
-    // mask of the 16 output pairs of this lane (zero outside the N x N pair grid)
-    float mk[16];
+  };
+
+  int64_t s = (int64_t)blockIdx.x * WAVES + wave;
+  const int64_t sstride = (int64_t)gridDim.x * WAVES;
+  for (; s < nsteps; s += sstride) {
+    const int64_t tile = 2 * s;
+    const int vt = (int)(tile % vtiles);
+    const int f = (int)((tile / vtiles) % Np);
+    const int b = (int)(tile / ((int64_t)vtiles * Np));
+    Frag<bf16> xf[2][KCH];
     {
-      const int v0 = vt * 32 + 16 * half;
+      Frag<bf16> zr[2][KCH];
+      load_z(zr, s);
+      ln_frags_bf16<CZ>(xf[0], zr[0], eps);
+      ln_frags_bf16<CZ>(xf[1], zr[1], eps);
+    }
+    // mask of this lane's 16 output pairs of each tile (zero outside the grid)
+    float mk[2][16];
+    {
       const bool frow = f < N;
       const int64_t base = ((int64_t)b * N + (outgoing ? f : 0)) * N + (outgoing ? 0 : f);
-      const int64_t step = outgoing ? 1 : N;
+      const int64_t mstep = outgoing ? 1 : N;
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const bool ok = frow && v0 + j < N;
-        mk[j] = ok ? (mask ? mask[base + (int64_t)(v0 + j) * step] : 1.f) : 0.f;
+      for (int u = 0; u < 2; ++u) {
+        const int v0 = (vt + u) * 32 + 16 * half;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) {
+          const bool ok = frow && v0 + j < N;
+          mk[u][j] = ok ? (mask ? mask[base + (int64_t)(v0 + j) * mstep] : 1.f) : 0.f;
+        }
       }
     }
 #pragma unroll 1
@@ -195,31 +224,38 @@ __global__ __launch_bounds__(1024) void trimul_prologue_bf16_kernel(
         Frag<bf16> wfp, wfg;
         load_wfrag_lds(wfp, wp, ct, 0, KCH);
         load_wfrag_lds(wfg, wg, ct, 0, KCH);
-        f32x16 ap = mma0(xf[0], wfp);
-        f32x16 ag = mma0(xf[0], wfg);
+        f32x16 ap0 = mma0(xf[0][0], wfp), ap1 = mma0(xf[1][0], wfp);
+        f32x16 ag0 = mma0(xf[0][0], wfg), ag1 = mma0(xf[1][0], wfg);
 #pragma unroll
         for (int ks = 1; ks < KCH; ++ks) {
           load_wfrag_lds(wfp, wp, ct, ks, KCH);
           load_wfrag_lds(wfg, wg, ct, ks, KCH);
-          mma(ap, xf[ks], wfp);
-          mma(ag, xf[ks], wfg);
+          mma(ap0, xf[0][ks], wfp);
+          mma(ap1, xf[1][ks], wfp);
+          mma(ag0, xf[0][ks], wfg);
+          mma(ag1, xf[1][ks], wfg);
         }
         const int cc = ct * 32 + i32;
         const float bpc = bp[cc];
         const float ebg = fmaxf(__builtin_amdgcn_exp2f(bg[cc]), 1.17549435e-38f);
-        uint32_t pk[8];
 #pragma unroll
-        for (int j = 0; j < 16; j += 2) {
-          const float o0 = (ap[j] + bpc) *
-                           __builtin_amdgcn_rcpf(fmaf(__builtin_amdgcn_exp2f(ag[j]), ebg, 1.f)) * mk[j];
-          const float o1 = (ap[j + 1] + bpc) *
-                           __builtin_amdgcn_rcpf(fmaf(__builtin_amdgcn_exp2f(ag[j + 1]), ebg, 1.f)) *
-                           mk[j + 1];
-          pk[j / 2] = pack_bf16x2(o0, o1);
+        for (int u = 0; u < 2; ++u) {
+          const f32x16& ap = u ? ap1 : ap0;
+          const f32x16& ag = u ? ag1 : ag0;
+          uint32_t pk[8];
+#pragma unroll
+          for (int j = 0; j < 16; j += 2) {
+            const float o0 = (ap[j] + bpc) *
+                             __builtin_amdgcn_rcpf(fmaf(__builtin_amdgcn_exp2f(ag[j]), ebg, 1.f)) * mk[u][j];
+            const float o1 = (ap[j + 1] + bpc) *
+                             __builtin_amdgcn_rcpf(fmaf(__builtin_amdgcn_exp2f(ag[j + 1]), ebg, 1.f)) *
+                             mk[u][j + 1];
+            pk[j / 2] = pack_bf16x2(o0, o1);
+          }
+          uint4* o = reinterpret_cast<uint4*>(dst + (int64_t)cc * plane + 32 * u);
+          o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+          o[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
         }
-        uint4* o = reinterpret_cast<uint4*>(dst + (int64_t)cc * plane);
-        o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-        o[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
       }
     }
   }
@@ -893,9 +929,9 @@ static int fwd_trimul(const void* z, const float* mask, void* out, const void* p
   T* px = cv.take<T>(B * CH * (int64_t)Np * Np);
   const int64_t ptiles = B * (int64_t)Np * (Np / 32);
   if constexpr (sizeof(T) == 2) {
-    const int grid = (int)std::min<int64_t>(device_cus(), (ptiles + 15) / 16);
+    const int grid = (int)std::min<int64_t>(device_cus(), (ptiles / 2 + 7) / 8);
     StageTimer timer("trimul_prologue", st);
-    trimul_prologue_bf16_kernel<CZ, CH><<<grid, 1024, 0, st>>>(
+    trimul_prologue_bf16_kernel<CZ, CH><<<grid, 512, 0, st>>>(
         (const bf16*)z, mask, (bf16*)pa, (bf16*)pb, w, (int)N, Np, outgoing, eps_in, ptiles);
   } else {
     StageTimer timer("trimul_prologue", st);
