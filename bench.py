@@ -51,6 +51,11 @@ def triattn_flops(N: int, B: int = 1) -> dict:
     }
 
 
+def step_flops_of(fm: dict, fa: dict) -> float:
+    """Tri-mul outgoing + incoming and tri-attn starting + ending."""
+    return 2 * sum(fm.values()) + 2 * sum(fa.values())
+
+
 def ln_bytes(N: int, B: int = 1, elem: int = 2) -> float:
     return 2.0 * B * N * N * C_Z * elem
 
@@ -85,6 +90,31 @@ def build_modules(torch, N: int, dev: str):
     for m in mods.values():
         assert m.use_fused_kernel, "HIP kernel path not enabled"
     return mods
+
+
+def build_pair_layer(torch, dev: str):
+    """One PairTransformLayer (c_p = c = c_h = 128, 4 heads), random weights, eval mode."""
+    import numpy as np
+
+    from genie_tk import PairTransformLayer
+
+    layer = PairTransformLayer(c_p=C_Z, c_hidden_mul=C_HID, c_hidden_tri_att=HEADS * HEAD_DIM,
+                               n_head_tri=HEADS, tri_dropout=0.25)
+    g = torch.Generator().manual_seed(7)
+    sd = {}
+    for name, p in sorted(layer.state_dict().items()):
+        if name.endswith("weight") and p.dim() == 2:
+            sd[name] = torch.randn(p.shape, generator=g) / np.sqrt(p.shape[1])
+        elif "layer_norm" in name:
+            sd[name] = torch.ones(p.shape) if name.endswith("weight") else torch.zeros(p.shape)
+        else:
+            sd[name] = torch.zeros(p.shape)
+    layer.load_state_dict(sd)
+    return layer.to(dev, torch.bfloat16).eval()
+
+
+def transition_flops(N: int, B: int = 1) -> float:
+    return 2.0 * 2 * B * N * N * C_Z * 4 * C_Z
 
 
 def event_time_ms(torch, fn, reps: int, warm: int = 2, flush=None) -> list:
@@ -220,6 +250,12 @@ def main() -> int:
         flush_buf = torch.zeros(1 << 30, dtype=torch.uint8, device=dev)
         ln_ms_cold = statistics.median(event_time_ms(torch, ops["layernorm"], reps,
                                                      flush=lambda: flush_buf.sum()))
+        # the rest of the pair-stack block on the kernels (informational)
+        layer = build_pair_layer(torch, dev)
+        trans_ms = statistics.median(event_time_ms(
+            torch, lambda: layer.pair_transition.forward_residual_masked(z, mask), reps))
+        layer_ms = statistics.median(event_time_ms(torch, lambda: layer((z, mask)), reps))
+        del layer
         z2 = torch.randn(1, 2 * N, 2 * N, C_Z, device=dev).to(torch.bfloat16)
         ln2 = lambda: C.layernorm(z2, ln_w, ln_b, 1e-5)  # noqa: E731
         ln2_ms = statistics.median(event_time_ms(torch, ln2, reps))
@@ -260,6 +296,19 @@ def main() -> int:
         "frac_hbm_cold": round(ln2b / (ln2_ms_cold * 1e-3) / PEAK_HBM_BYTES, 4),
     }
 
+    tf = transition_flops(N)
+    per_op["pair_transition"] = {
+        "ms": round(trans_ms, 4), "gflop": round(tf / 1e9, 2),
+        "tflops": round(tf / (trans_ms * 1e-3) / 1e12, 2),
+        "frac_bf16_peak": round(tf / (trans_ms * 1e-3) / PEAK_BF16_FLOPS, 4),
+        "note": "fused LN -> c->4c -> ReLU -> 4c->c, residual and mask (informational)",
+    }
+    lf = step_flops_of(fm, fa) + tf
+    per_op["pair_layer"] = {
+        "ms": round(layer_ms, 4), "gflop": round(lf / 1e9, 2),
+        "tflops": round(lf / (layer_ms * 1e-3) / 1e12, 2),
+        "note": "one PairTransformLayer forward on the kernels, residuals fused (informational)",
+    }
     work = dict(fm)
     work.update(fa)
     kernels = {}

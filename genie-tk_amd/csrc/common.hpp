@@ -269,8 +269,29 @@ typedef __attribute__((address_space(3))) void* lds_void_ptr;
 
 // 16 bytes per lane from global memory straight into LDS at
 // (wave-uniform base) + lane * 16 (global_load_lds_dwordx4, no VGPR staging).
+//
+// Issued from inline asm on purpose.  Through the compiler builtin, the
+// waitcnt pass cannot tell which LDS bytes the copy writes, so it puts an
+// s_waitcnt vmcnt(0) before the next LDS read of ANY address: a copy of the
+// next pipeline stage then completes before the current stage is read, and
+// copies never overlap compute.  Hidden from that pass, the copy is ordered
+// only by the caller's explicit s_waitcnt vmcnt(n) (vmcnt counts every
+// vector-memory load in issue order, these included) followed by a block
+// barrier, or by __syncthreads(), whose fence waits for vmcnt(0).  M0 (the
+// copy's LDS base) is a reserved register: the asm restores it.
 __device__ __forceinline__ void g2lds16(const void* gptr, void* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(gptr, (lds_void_ptr)lds_wave_base, 16, 0, 0);
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(
+      (uint32_t)(uintptr_t)(lds_void_ptr)lds_wave_base);
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(gptr), "s"(lds)
+      : "memory");
 }
 
 // Asynchronously copy `bytes` (a multiple of 1 KiB) from global memory into
@@ -288,8 +309,12 @@ __device__ __forceinline__ void copy_to_lds_async(void* dst, const void* __restr
 // every outstanding global load, including direct-to-LDS copies meant to stay
 // in flight across the barrier.  Callers order memory themselves with
 // explicit s_waitcnt; the "memory" clobber keeps the compiler from moving
-// memory accesses across the barrier.
-__device__ __forceinline__ void barrier_only() { asm volatile("s_barrier" ::: "memory"); }
+// memory accesses across the barrier.  The lgkmcnt(0) makes this wave's LDS
+// reads complete first, so a copy issued after the barrier into a stage the
+// waves just read cannot overtake a read still in flight.
+__device__ __forceinline__ void barrier_only() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 // A zero the compiler cannot see through.  Adding it to a loop-invariant LDS
 // address inside a loop keeps the loads in the loop: hoisted out, the

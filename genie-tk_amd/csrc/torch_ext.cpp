@@ -211,6 +211,45 @@ at::Tensor tri_mul_forward(const at::Tensor& z, const c10::optional<at::Tensor>&
   return out;
 }
 
+// params: ln_w, ln_b, w1, b1, w2, b2 (PairTransition: layer_norm, linear_1, linear_2)
+at::Tensor pair_transition_pack(std::vector<at::Tensor> ps, int64_t c, int64_t n) {
+  TORCH_CHECK(ps.size() == 6, "pair_transition_pack expects 6 parameter tensors");
+  check_gpu(ps[2], "weights");
+  const at::DeviceGuard guard(ps[2].device());
+  gtk_pair_transition_weights w;
+  w.dtype = common_param_dtype(ps);
+  const void** slots[6] = {&w.ln_w, &w.ln_b, &w.w1, &w.b1, &w.w2, &w.b2};
+  for (int i = 0; i < 6; ++i) *slots[i] = ptr_or_null(ps[i]);
+  const size_t bytes = gtk_pair_transition_packed_size(c, n, GTK_BF16);
+  TORCH_CHECK(bytes > 0, "genie_tk._C: pair_transition shape c=", c, " n=", n, " unsupported");
+  auto packed = workspace(ps[2], bytes);
+  check_rc(gtk_pair_transition_pack(&w, c, n, GTK_BF16, packed.data_ptr(), packed.numel(),
+                                    cur_stream(ps[2])));
+  return packed;
+}
+
+// p: [..., c] bf16; mask: [...] (rows of p) or None
+at::Tensor pair_transition_forward(const at::Tensor& p, const c10::optional<at::Tensor>& mask,
+                                   const at::Tensor& packed, int64_t c, int64_t n, bool residual,
+                                   double eps) {
+  check_gpu(p, "p");
+  const at::DeviceGuard guard(p.device());
+  TORCH_CHECK(p.dim() >= 1 && p.size(-1) == c, "p must be [..., c]");
+  TORCH_CHECK(p.scalar_type() == at::kBFloat16, "pair_transition_forward: bf16 only");
+  auto pc = p.contiguous();
+  const int64_t rows = pc.numel() / c;
+  at::Tensor mc;
+  if (mask.has_value()) {
+    TORCH_CHECK(mask->numel() == rows, "mask must have one value per row of p");
+    mc = f32c(*mask);
+  }
+  auto out = at::empty_like(pc);
+  check_rc(gtk_pair_transition_forward(pc.data_ptr(), mask.has_value() ? mc.data_ptr<float>() : nullptr,
+                                       out.data_ptr(), packed.data_ptr(), rows, c, n,
+                                       residual ? 1 : 0, (float)eps, GTK_BF16, cur_stream(pc)));
+  return out;
+}
+
 // params: ln_w, ln_b, tri_w, q_w, k_w, v_w, g_w, g_b, o_w, o_b
 at::Tensor tri_attn_pack(std::vector<at::Tensor> ps, int64_t c_in, int64_t c_h, int64_t H,
                          bool fp32) {
@@ -297,6 +336,12 @@ PYBIND11_MODULE(_C, m) {
         py::arg("z"), py::arg("mask"), py::arg("packed"), py::arg("c_z"), py::arg("c"),
         py::arg("outgoing"), py::arg("residual") = false, py::arg("eps_in") = 1e-5,
         py::arg("eps_out") = 1e-5);
+  m.def("pair_transition_pack", &pair_transition_pack, "Pack PairTransition parameters",
+        py::arg("params"), py::arg("c"), py::arg("n"));
+  m.def("pair_transition_forward", &pair_transition_forward,
+        "Fused PairTransition forward: (residual ? p : 0) + transition(p), times mask",
+        py::arg("p"), py::arg("mask"), py::arg("packed"), py::arg("c"), py::arg("n"),
+        py::arg("residual") = false, py::arg("eps") = 1e-5);
   m.def("tri_attn_pack", &tri_attn_pack, "Pack TriangleAttention parameters", py::arg("params"),
         py::arg("c_in"), py::arg("c_h"), py::arg("no_heads"), py::arg("fp32"));
   m.def("tri_attn_forward", &tri_attn_forward, "Fused TriangleAttention forward", py::arg("x"),

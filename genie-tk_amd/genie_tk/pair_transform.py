@@ -10,8 +10,11 @@ from __future__ import annotations
 
 from typing import Optional, Tuple
 
+import torch
 import torch.nn as nn
 from torch import Tensor
+
+from genie_tk import _dispatch, _ext
 
 from genie_tk.primitives import Linear
 from genie_tk.triangle_attention import TriangleAttentionEndingNode, TriangleAttentionStartingNode
@@ -50,19 +53,56 @@ class DropoutColumnwise(_SharedDropout):
 
 
 class PairTransition(nn.Module):
-    """LN -> Linear(c_p, n*c_p) -> ReLU -> Linear(n*c_p, c_p) (final init)."""
+    """LN -> Linear(c_p, n*c_p) -> ReLU -> Linear(n*c_p, c_p) (final init).
 
-    def __init__(self, c_p: int, n: int = 4):
+    Kernel path (``use_fused_kernel``, bf16 GPU tensor, c_p in {64, 128},
+    n == 4, no autograd needed): ``genie_tk._C.pair_transition_forward``, one
+    gfx950 kernel for the whole MLP.  ``forward_residual_masked`` computes the
+    pair-stack update ``(p + transition(p)) * mask`` in the same kernel.
+    """
+
+    def __init__(self, c_p: int, n: int = 4, use_fused_kernel: bool = True):
         super().__init__()
         self.c_p = c_p
         self.n = n
+        self._fused_requested = use_fused_kernel
         self.layer_norm = nn.LayerNorm(c_p)
         self.linear_1 = Linear(c_p, c_p * n)
         self.relu = nn.ReLU()
         self.linear_2 = Linear(c_p * n, c_p, init="final")
+        self._packed = _dispatch.PackedWeights()
+
+    def _forward_pytorch(self, p: Tensor) -> Tensor:
+        return self.linear_2(self.relu(self.linear_1(self.layer_norm(p))))
+
+    def _use_kernel(self, p: Tensor) -> bool:
+        if not (p.is_cuda and self._fused_requested):
+            return False
+        _ext.require()
+        return (p.dtype == torch.bfloat16 and p.dim() >= 1 and p.shape[-1] == self.c_p
+                and self.c_p in (64, 128) and self.n == 4 and self.layer_norm.elementwise_affine
+                and not _dispatch.needs_autograd(p, self))
+
+    def _run_kernel(self, p: Tensor, mask: Optional[Tensor], residual: bool) -> Tensor:
+        C = _ext.require()
+        ps = [self.layer_norm.weight, self.layer_norm.bias, self.linear_1.weight,
+              self.linear_1.bias, self.linear_2.weight, self.linear_2.bias]
+        packed = self._packed.get(ps, False,
+                                  lambda prm, fp32: C.pair_transition_pack(prm, self.c_p, self.n))
+        m = None if mask is None else mask.expand(p.shape[:-1])
+        return C.pair_transition_forward(p, m, packed, self.c_p, self.n, residual,
+                                         self.layer_norm.eps)
 
     def forward(self, p: Tensor, mask: Optional[Tensor] = None) -> Tensor:
-        return self.linear_2(self.relu(self.linear_1(self.layer_norm(p))))
+        if self._use_kernel(p):
+            return self._run_kernel(p, None, False)
+        return self._forward_pytorch(p)
+
+    def forward_residual_masked(self, p: Tensor, mask: Tensor) -> Tensor:
+        """(p + transition(p)) * mask[..., None] (pair_transform.py:192-193)."""
+        if self._use_kernel(p):
+            return self._run_kernel(p, mask, True)
+        return (p + self._forward_pytorch(p)) * mask.unsqueeze(-1)
 
 
 class PairTransformLayer(nn.Module):
@@ -87,12 +127,23 @@ class PairTransformLayer(nn.Module):
             self.tri_att_end = TriangleAttentionEndingNode(
                 c_in=c_p, c_hidden=c_hidden_tri_att, no_heads=n_head_tri,
                 use_fused_kernel=use_fused_kernel)
-        self.pair_transition = PairTransition(c_p, pair_transition_n)
+        self.pair_transition = PairTransition(c_p, pair_transition_n,
+                                              use_fused_kernel=use_fused_kernel)
         self.dropout_row = DropoutRowwise(tri_dropout)
         self.dropout_col = DropoutColumnwise(tri_dropout)
 
     def forward(self, inputs: Tuple[Tensor, Tensor]) -> Tuple[Tensor, Tensor]:
         p, p_mask = inputs
+        if not self.training or self.dropout_row.p == 0:
+            # dropout is the identity: every residual add and the final mask
+            # fold into the operators' kernels
+            if self.include_mul_update:
+                p = self.tri_mul_out.forward_residual(p, p_mask)
+                p = self.tri_mul_in.forward_residual(p, p_mask)
+            if self.include_tri_att:
+                p = self.tri_att_start.forward_residual(p, p_mask)
+                p = self.tri_att_end.forward_residual(p, p_mask)
+            return self.pair_transition.forward_residual_masked(p, p_mask), p_mask
         if self.include_mul_update:
             p = p + self.dropout_row(self.tri_mul_out(p, p_mask))
             p = p + self.dropout_row(self.tri_mul_in(p, p_mask))

@@ -99,6 +99,13 @@ class TriangleAttention(nn.Module):
                                  self.starting, residual, self.layer_norm.eps)
         return out.reshape(*lead, *out.shape[1:])
 
+    def forward_residual(self, x: Tensor, mask: Optional[Tensor] = None) -> Tensor:
+        """x + forward(x, mask), with the add fused into the kernel's output."""
+        if (x.is_cuda and self._fused_requested and self.use_fused_kernel
+                and self._kernel_supported(x) and not _dispatch.needs_autograd(x, self)):
+            return self._forward_cuda(x, mask, residual=True)
+        return x + self.forward(x, mask)
+
     def forward(self, x: Tensor, mask: Optional[Tensor] = None) -> Tensor:
         """x: [*, N, N, c_in], mask: [*, N, N] -> update [*, N, N, c_in]."""
         if x.is_cuda and self._fused_requested:

@@ -107,6 +107,13 @@ class TriangleMultiplicativeUpdate(nn.Module):
                                 residual, self.layer_norm_in.eps, self.layer_norm_out.eps)
         return out.reshape(*lead, *out.shape[1:])
 
+    def forward_residual(self, z: Tensor, mask: Optional[Tensor] = None) -> Tensor:
+        """z + forward(z, mask), with the add fused into the kernel's output."""
+        if (z.is_cuda and self._fused_requested and self.use_fused_kernel
+                and self._kernel_supported(z) and not _dispatch.needs_autograd(z, self)):
+            return self._forward_cuda(z, mask, residual=True)
+        return z + self.forward(z, mask)
+
     def forward(self, z: Tensor, mask: Optional[Tensor] = None) -> Tensor:
         """z: [*, N, N, c_z], mask: [*, N, N] -> update [*, N, N, c_z]."""
         if z.is_cuda and self._fused_requested:

@@ -182,6 +182,30 @@ int gtk_tri_attn_forward(const void* x, const float* mask, void* out, const void
                          size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * PairTransition fused with the pair-stack residual and mask.
+ * Replaces PairTransition.forward src/genie_tk/pair_transform.py:64-84 and the
+ * update of PairTransformLayer.forward :180-193 (p = p + transition(p);
+ * p = p * mask):
+ *   out = (residual ? p : 0) + (relu(LN(p) W1^T + b1) W2^T + b2),  times mask
+ * p, out: [rows][c] bf16; mask: [rows] float or NULL.  W1 [n c][c],
+ * W2 [c][n c] (nn.Linear layout).  c in {64, 128}, n == 4, bf16 only.
+ * ------------------------------------------------------------------------ */
+typedef struct gtk_pair_transition_weights {
+  int dtype;                 /* element type of every pointer below */
+  const void *ln_w, *ln_b;   /* [c]                   layer_norm         */
+  const void *w1, *b1;       /* [n c][c], [n c]       linear_1           */
+  const void *w2, *b2;       /* [c][n c], [c]         linear_2           */
+} gtk_pair_transition_weights;
+
+size_t gtk_pair_transition_packed_size(int64_t c, int64_t n, int dtype);
+int gtk_pair_transition_pack(const gtk_pair_transition_weights* w, int64_t c, int64_t n, int dtype,
+                             void* packed, size_t packed_bytes, void* stream);
+/* out may not alias p. */
+int gtk_pair_transition_forward(const void* p, const float* mask, void* out, const void* packed,
+                                int64_t rows, int64_t c, int64_t n, int residual, float eps,
+                                int dtype, void* stream);
+
+/* ------------------------------------------------------------------------
  * Per-kernel timing (instrumentation; no counterpart in the reference).
  * gtk_timing_enable(1) makes every subsequent launch record a HIP event
  * before and after each kernel on its stream; gtk_timing_report() waits for

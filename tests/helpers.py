@@ -38,6 +38,25 @@ def tri_attn_shapes(c_in: int, c_h: int, H: int) -> Dict[str, tuple]:
     }
 
 
+def pair_transition_shapes(c: int, n: int = 4) -> Dict[str, tuple]:
+    return {
+        "layer_norm.weight": (c,), "layer_norm.bias": (c,),
+        "linear_1.weight": (n * c, c), "linear_1.bias": (n * c,),
+        "linear_2.weight": (c, n * c), "linear_2.bias": (c,),
+    }
+
+
+def pair_layer_shapes(c: int, c_mul: int, c_att: int, heads: int, n: int = 4) -> Dict[str, tuple]:
+    """state_dict shapes of PairTransformLayer (pair_transform.py:87-178)."""
+    out = {}
+    for name, sub in (("tri_mul_out", tri_mul_shapes(c, c_mul)), ("tri_mul_in", tri_mul_shapes(c, c_mul)),
+                      ("tri_att_start", tri_attn_shapes(c, c_att, heads)),
+                      ("tri_att_end", tri_attn_shapes(c, c_att, heads)),
+                      ("pair_transition", pair_transition_shapes(c, n))):
+        out.update({f"{name}.{k}": v for k, v in sub.items()})
+    return out
+
+
 def draw_params(shapes: Dict[str, tuple], seed: int, *, ln_random: bool = False,
                 bias_random: bool = False, gate_bias: Optional[float] = None,
                 gate_keys: Sequence[str] = (), tri_std: Optional[float] = None) -> Dict[str, np.ndarray]:

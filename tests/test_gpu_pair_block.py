@@ -1,0 +1,67 @@
+"""GPU parity of the pair-stack block on the kernels: the fused PairTransition
+kernel (pair_transform.py:64-84) alone and with the layer's residual and mask
+(:180-193), and a whole PairTransformLayer (eval mode) whose four triangle
+operators run with the residual add fused into their kernels.
+bf16 tolerance per operator: |y - y_ref| <= 2e-2 + 1e-2 |y_ref| against the fp32
+oracle on bf16-rounded inputs and weights."""
+import numpy as np
+import pytest
+import torch
+
+from genie_tk import PairTransformLayer
+from genie_tk.pair_transform import PairTransition
+from oracle import pair_ops
+from tests import helpers as H
+from tests.gpu_common import check_bf16, log, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(a, dtype=torch.bfloat16):
+    return torch.from_numpy(np.ascontiguousarray(a)).to("cuda", dtype)
+
+
+@pytest.mark.parametrize("c", [128, 64])
+def test_pair_transition_kernel(c):
+    log(f"pair transition kernel c={c}")
+    P = H.bf16_params(H.draw_params(H.pair_transition_shapes(c), 70 + c, ln_random=True, bias_random=True))
+    p = H.bf16_round(H.pair_input(2, 45, c, seed=c))  # 4050 rows: a ragged last tile and batch
+    mod = PairTransition(c, 4)
+    mod.load_state_dict(H.to_state_dict(P))
+    mod = mod.to("cuda", torch.bfloat16).eval()
+    pt = _dev(p)
+    with torch.no_grad():
+        assert mod._use_kernel(pt)
+        y = mod(pt)
+        m = H.tail_mask(2, 45, [45, 31])
+        m[1, 3, 5] = 0.5  # a fractional mask value is applied as a factor
+        y2 = mod.forward_residual_masked(pt, _dev(m, torch.float32))
+    ref = pair_ops.pair_transition(p, P)
+    check_bf16(to_np(y), ref, f"pair transition c={c}")
+    check_bf16(to_np(y2), (p + ref) * m[..., None], f"pair transition residual+mask c={c}")
+
+
+def test_pair_layer_kernel_path():
+    """One PairTransformLayer (eval) on the kernels vs the oracle's block.  The
+    layer composes five bf16 operators over a bf16 residual stream, so the check
+    allows 2.5x the per-operator tolerance."""
+    log("pair layer kernel path B=2 N=64")
+    B, N, c = 2, 64, 128
+    P = H.bf16_params(H.draw_params(H.pair_layer_shapes(c, 128, 128, 4), 90, ln_random=True,
+                                    bias_random=True, tri_std=1.0 / np.sqrt(128)))
+    layer = PairTransformLayer(c_p=c, c_hidden_mul=128, c_hidden_tri_att=128, n_head_tri=4,
+                               tri_dropout=0.25)
+    layer.load_state_dict(H.to_state_dict(P))
+    layer = layer.to("cuda", torch.bfloat16).eval()
+    p = H.bf16_round(H.pair_input(B, N, c, seed=91))
+    m = H.tail_mask(B, N, [N, 50])
+    with torch.no_grad():
+        out, _ = layer((_dev(p), _dev(m, torch.float32)))
+    ref = pair_ops.pair_block(p, m, P, 4, dtype=np.float32)
+    got = to_np(out)
+    assert np.isfinite(got).all()
+    err = np.abs(got - ref)
+    bound = 2.5 * (2e-2 + 1e-2 * np.abs(ref))
+    log(f"pair layer: max abs err {err.max():.3e}, worst err/bound {(err / bound).max():.2f}")
+    assert (err <= bound).all(), f"pair layer: max err {err.max():.3e}, worst ratio {(err / bound).max():.2f}"
+    assert np.all(got[1, 50:] == 0) and np.all(got[1, :, 50:] == 0)  # masked pairs are zero
