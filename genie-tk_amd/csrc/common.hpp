@@ -107,6 +107,23 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   v[1] = (bf16)b;
   return __builtin_bit_cast(uint32_t, v);
 }
+// Raw buffer resource over `bytes` bytes at `base`.  A buffer access whose
+// offset is >= bytes does nothing (a store is dropped): lanes without a valid
+// destination pass kBufSkip instead of branching around the store, so every
+// lane runs the same instruction stream (and the compiler's wait counts see
+// one path).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+constexpr uint32_t kBufSkip = 0x80000000u;
+// 4 values as bf16 (8 bytes) at byte offset `off`.
+__device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, uint32_t off, float a, float b,
+                                           float c, float d) {
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 v = {pack_bf16x2(a, b), pack_bf16x2(c, d)};
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, 0);
+}
+
 // Load 4 consecutive values as fp32.
 __device__ __forceinline__ f32x4 load4f(const bf16* p) {
   bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
@@ -294,6 +311,28 @@ __device__ __forceinline__ void g2lds16(const void* gptr, void* lds_wave_base) {
       : "memory");
 }
 
+// LDS byte address of a __shared__ object, for the copies below.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_ptr)p);
+}
+
+// g2lds16 with a wave-uniform 64-bit base in scalar registers and a 32-bit
+// per-lane byte offset (the saddr form: one VGPR per copy instead of two);
+// `lds` is the wave's LDS destination address (lds_addr).  Same ordering
+// contract as g2lds16.
+__device__ __forceinline__ void g2lds16_sv(const void* sbase, uint32_t voff, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(sbase), "s"(lds)
+      : "memory");
+}
+
 // Asynchronously copy `bytes` (a multiple of 1 KiB) from global memory into
 // LDS with the whole block: every load is issued before any is waited for.
 // The caller waits (s_waitcnt vmcnt(0)) and synchronises the block.
@@ -303,6 +342,48 @@ __device__ __forceinline__ void copy_to_lds_async(void* dst, const void* __restr
   const int nwaves = blockDim.x >> 6;
   for (int blk = wave; blk * 1024 < bytes; blk += nwaves)
     g2lds16((const char*)src + blk * 1024 + lane * 16, (char*)dst + blk * 1024);
+}
+
+// A linear tile index t = (b * rows + r) * cols + c, walked by a fixed stride
+// without divisions: a 64-bit division by a run-time value costs tens of
+// instructions, per tile, in the persistent loops.  Divides once at set-up.
+struct TileWalk {
+  int b, r, c;     // the current tile
+  int db, dr, dc;  // the stride, decomposed the same way
+  int rows, cols;
+  __device__ __forceinline__ void init(int64_t t, int64_t stride, int rows_, int cols_) {
+    rows = rows_;
+    cols = cols_;
+    const int64_t plane = (int64_t)rows * cols;
+    c = (int)(t % cols);
+    r = (int)((t / cols) % rows);
+    b = (int)(t / plane);
+    dc = (int)(stride % cols);
+    dr = (int)((stride / cols) % rows);
+    db = (int)(stride / plane);
+  }
+  __device__ __forceinline__ void next() {
+    c += dc;
+    int carry = 0;
+    if (c >= cols) {
+      c -= cols;
+      carry = 1;
+    }
+    r += dr + carry;  // < 2 * rows
+    if (r >= rows) {
+      r -= rows;
+      b += 1;
+    }
+    b += db;
+  }
+};
+
+// s_waitcnt immediate for vmcnt(N) alone (expcnt and lgkmcnt not waited for);
+// vmcnt is 6 bits on gfx950: [3:0] and [15:14].
+template <int N>
+constexpr int vmcnt_imm() {
+  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
+  return 0x0F70 | (N & 15) | ((N >> 4) << 14);
 }
 
 // s_barrier without the fence that __syncthreads() adds: that fence waits for

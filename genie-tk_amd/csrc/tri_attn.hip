@@ -552,6 +552,7 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
   __shared__ unsigned kmask[MAXN / 32];  // mask == 0
   __shared__ unsigned kpad[MAXN / 32];   // key >= N
   __shared__ int row_any;
+  __shared__ int row_dirty;  // some key of the row is masked or padding
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -572,15 +573,19 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
   // mask of this row: key k is pair (r, k) (starting) or (k, r) (ending)
   const float* mrow = mask ? mask + (int64_t)b * N * N + (starting ? (int64_t)r * N : r) : nullptr;
   const int64_t mks = starting ? 1 : N;
-  if (tid == 0) row_any = mrow ? 0 : 1;
+  if (tid == 0) {
+    row_any = mrow ? 0 : 1;
+    row_dirty = 0;
+  }
   __syncthreads();
   {
-    bool any = false;
+    bool any = false, dirty = false;
     for (int k0 = wave * 64; k0 < Np; k0 += NW * 64) {
       const int k = k0 + lane;
       const bool inrow = k < N;
       const bool masked = inrow && mrow && mrow[k * mks] == 0.f;
       any = any || (inrow && !masked);
+      dirty = dirty || masked || !inrow;
       const unsigned long long mb = __ballot(masked);
       const unsigned long long pb = __ballot(!inrow);
       if (lane == 0) {
@@ -591,9 +596,12 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
       }
     }
     if (mrow && __ballot(any) != 0ull && lane == 0) row_any = 1;
+    if (__ballot(dirty) != 0ull && lane == 0) row_dirty = 1;
   }
   __syncthreads();
-  const bool row_valid = row_any != 0;
+  // block-uniform flags, kept in scalar registers
+  const bool row_valid = __builtin_amdgcn_readfirstlane(row_any) != 0;
+  const bool row_clean = __builtin_amdgcn_readfirstlane(row_dirty) == 0;
 
   // Async stage load.  A stage is 32 regions of 1 KiB (64 lanes x 16 B);
   // wave w moves regions RPW*w .. RPW*w + RPW-1.  Regions 0..15: K^T, head
@@ -605,41 +613,59 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
   auto vswz = [](int d) { return (d ^ (d >> 3)) & 7; };
   // K^T and V^T are both [32 d][Np keys] per (row, head); a stage holds the
   // [32 d][64 keys] tile of each head for both.
-  const bf16* kbase = ws.k + (rowbase * H) * (int64_t)HD * Np;
-  const bf16* vbase = ws.vt + (rowbase * H) * (int64_t)HD * Np;
   const bool k_region = wave < NW / 2;     // the first half of the waves move K^T
+  // wave-uniform source base (K^T or V^T of this row, all heads)
+  const bf16* gbase = (k_region ? ws.k : ws.vt) + (rowbase * H) * (int64_t)HD * Np;
   const int rg_head = ((wave * RPW) & 15) >> 2;
   const int rg_sub0 = (wave * RPW) & 3;
-  // this lane's source element of region i at key 0 (a stage at key k0 adds
-  // k0), and the wave's LDS destination offset of region i
-  const bf16* gsrc[RPW];
-  int dst_off[RPW];
-#pragma unroll
-  for (int i = 0; i < RPW; ++i) {
-    const int sub = rg_sub0 + i;
-    const int P = sub * 64 + lane;
-    const int d = P >> 3;
-    const int c = (P & 7) ^ vswz(d);
-    gsrc[i] = (k_region ? kbase : vbase) + ((int64_t)rg_head * HD + d) * Np + c * 8;
-    dst_off[i] = ((k_region ? 0 : H) + rg_head) * HEAD_BYTES + sub * 1024;
-  }
+  // Lane l of region i (sub = rg_sub0 + i) moves physical chunk P = sub*64 + l:
+  // row d = sub*8 + l/8 of the head's tile, logical chunk (l%8) ^ vswz(d) =
+  // (l%8) ^ (l/8) ^ sub (mod 8).  Its byte offset from gbase at key 0 (a stage
+  // at key k0 adds 2*k0) is row_off + 16*Np*i + 16*(cx ^ (sub & 7)).
+  const uint32_t row_off0 = (uint32_t)((rg_head * HD + rg_sub0 * 8) * (int64_t)Np * 2);  // uniform
+  const uint32_t ring_lds = lds_addr(&ring[0][0]);
+  const uint32_t dst0 = ((k_region ? 0 : H) + rg_head) * HEAD_BYTES + rg_sub0 * 1024;
   auto issue_stage = [&](int stage, int k0) {
+    // The per-lane offsets are recomputed from the lane id here rather than
+    // kept across the tile loop: at the register cap they would be spilled,
+    // and a reload from scratch waits for every outstanding load.
+    const uint32_t ln = (uint32_t)(lane + opaque_zero());
+    const uint32_t cx = (ln & 7) ^ (ln >> 3);
+    const uint32_t row_off = row_off0 + (ln >> 3) * (uint32_t)(Np * 2);
 #pragma unroll
-    for (int i = 0; i < RPW; ++i) g2lds16(gsrc[i] + k0, ring[stage] + dst_off[i]);
+    for (int i = 0; i < RPW; ++i) {
+      const uint32_t goff = row_off + (uint32_t)(16 * Np * i) + 16 * (cx ^ ((rg_sub0 + i) & 7));
+      g2lds16_sv(gbase + k0, goff, ring_lds + stage * STAGE_BYTES + dst0 + i * 1024);
+    }
   };
 
   // W_o for the epilogue, fetched now so that it is not waited for at the end
   if constexpr (WO_LDS) copy_to_lds_async(wo_l, w.w_o, (int)sizeof(wo_l));
-  // query fragments, zero for a row without valid keys (uniform attention);
-  // q is channel-major: one 2-byte element per lane and channel, 32
-  // consecutive positions per load instruction
+  // q and the gate are channel-major ([32 channels][Np positions] per row and
+  // head); this wave's [32 channels][32 queries] tile of either goes through
+  // LDS (a 2 KiB region per wave, 64-byte rows) and is read back transposed.
+  // Copy j (0, 1) moves channels 16j .. 16j+15: lane l takes channel
+  // 16j + l/4, queries 8*(l%4) .. +7.
+  const bf16* q_src = ws.q + ((rowbase * H + h) * HD) * (int64_t)Np + q0;
+  const bf16* g_src = ws.gate + (rowbase * CH + h * HD) * (int64_t)Np + q0;
+  auto issue_cq = [&](const bf16* src, int stage) {
+    const uint32_t ln = (uint32_t)(lane + opaque_zero());
+    const uint32_t voff = ((ln >> 2) * (uint32_t)Np + (ln & 3) * 8) * 2;
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+      g2lds16_sv(src + (int64_t)j * 16 * Np, voff, ring_lds + stage * STAGE_BYTES + wave * 2048 + j * 1024);
+  };
+  // Channels c0 .. c0+3 of this lane's query t32 (ds_read_b64_tr_b16: lane
+  // (group G = lane/16, i = lane%16) reads channel c0 + i/4 at queries
+  // 16*(G&1) + 4*(i%4) .. +3; c0 carries the lane's half)
+  auto read_cq4 = [&](int stage, int c0) {
+    const int i = lane & 15;
+    return lds_read_tr16(ring[stage] + wave * 2048 + (c0 + (i >> 2)) * 64 +
+                         (16 * ((lane >> 4) & 1) + 4 * (i & 3)) * 2);
+  };
+  // query fragments (filled once the q tile is in LDS), zero for a row
+  // without valid keys (uniform attention)
   Frag<bf16> qf[2];
-  const bf16* qcol = ws.q + ((rowbase * H + h) * HD) * (int64_t)Np + q0 + t32;
-#pragma unroll
-  for (int m = 0; m < 2; ++m)
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      qf[m].v[e] = row_valid ? qcol[(int64_t)(m * 16 + half * 8 + e) * Np] : (bf16)0.0f;
   // K fragments come from the K^T tile with transposing reads: fetching lane
   // (group G = lane/16, i = lane%16) reads d row (i/4) of a 4-row group at
   // keys 16*(G&1) + 4*(i%4) .. +3 of the 32-key tile; the receiving lane
@@ -652,21 +678,20 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) idf[cb].v[e] = (bf16)((t32 == cb * 16 + half * 8 + e) ? 1.0f : 0.0f);
+    for (int e = 0; e < 8; ++e)
+      idf[cb].v[e] = (bf16)((row_valid && t32 == cb * 16 + half * 8 + e) ? 1.0f : 0.0f);
   const bf16* brow = ws.bias + ((int64_t)(b * H + h) * Np + q0 + t32) * Np + half * 8;
   Frag<bf16> bfr[2];  // bias fragments of the next S tile to issue
   auto load_bias = [&](int t) {
-    if (row_valid) {
-      bfr[0].load(brow + t * 32);
-      bfr[1].load(brow + t * 32 + 16);
-    }
+    bfr[0].load(brow + t * 32);
+    bfr[1].load(brow + t * 32 + 16);
   };
   // S^T - m of 32-key tile t: the accumulation starts from negm = -m_use in
-  // every register, then adds I.Bias^T and K Q^T (no terms for a row without
-  // valid keys: uniform attention)
+  // every register, then adds I.Bias^T and K Q^T.  For a row without valid
+  // keys the identity and query fragments are zero, so S = negm (uniform
+  // attention) with no per-tile work.
   f32x16 negm = zero16();
   auto s_tile = [&](int t) {
-    if (!row_valid) return negm;
     f32x16 s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(idf[0].v, bfr[0].v, negm, 0, 0, 0);
     mma(s, idf[1], bfr[1]);
     const char* kt_base = ring[(t >> 1) % NS] + h * HEAD_BYTES;
@@ -691,11 +716,24 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
 
   const int nkb = (N + KB - 1) / KB;
   const int ntiles = 2 * nkb;
+  static_assert(NW * 2048 <= STAGE_BYTES && NS >= 2, "q / gate tiles fit in one ring stage");
   issue_stage(0, 0);
+  issue_cq(q_src, 1);
   load_bias(0);
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    const s16x4 lo = read_cq4(1, m * 16 + half * 8), hi = read_cq4(1, m * 16 + half * 8 + 4);
+    const s16x8 v8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    qf[m].v = __builtin_bit_cast(bf16x8, v8);
+    if (!row_valid) qf[m].zero();
+  }
+  barrier_only();  // every wave has read its q tile: stage 1 is free
+  // stage 1, or (a single key block) the gate tile, into the free stage
   if (nkb > 1) issue_stage(1, KB);
+  else issue_cq(g_src, 1);
 
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
   const bf16x2_t ones2 = {(bf16)1.0f, (bf16)1.0f};
@@ -703,17 +741,22 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
   float m_ref = -INFINITY, l_run = 0.f;
   float m_use = 0.f;  // the value subtracted inside S: m_ref, or 0 while m_ref = -inf
   for (int t = 0; t < ntiles; ++t) {
-    if (t > 0 && (t & 1) == 0) {          // tile t opens key block kb
-      const int kb = t >> 1;
-      __builtin_amdgcn_s_waitcnt(0);      // stage kb and the bias of tile t landed
-      __syncthreads();                    // ... for every wave; block kb-2 fully consumed
-      if (kb + 1 < nkb) issue_stage((kb + 1) % NS, (kb + 1) * KB);
+    const bool opens = t > 0 && (t & 1) == 0;  // tile t opens key block t/2
+    if (opens) {
+      __builtin_amdgcn_s_waitcnt(0);      // stage t/2 and the bias of tile t landed
+      __syncthreads();                    // ... for every wave; block t/2-2 fully consumed
     }
     f32x16 sc = s_tile(t);
     if (t + 1 < ntiles) load_bias(t + 1);
+    // The next block's copy goes out after the bias of tile t+1: loads
+    // complete in issue order, so waiting for that bias does not wait for it.
+    if (opens && (t >> 1) + 1 < nkb) issue_stage(((t >> 1) + 1) % NS, ((t >> 1) + 1) * KB);
+    // the last block opens: the gate tile goes into the stage it leaves free
+    if (opens && (t >> 1) + 1 == nkb) issue_cq(g_src, nkb % NS);
     const int cur = (t >> 1) % NS;
-    // keys of tile t that take no weight: padding, and masked keys of a valid row
-    const unsigned kx = kpad[t] | (row_valid ? kmask[t] : 0u);
+    // keys of tile t that take no weight: padding, and masked keys of a valid
+    // row (none at all in a clean row: no LDS read)
+    const unsigned kx = row_clean ? 0u : (kpad[t] | (row_valid ? kmask[t] : 0u));
     if (kx != 0u) {
 #pragma unroll
       for (int g = 0; g < 4; ++g)
@@ -763,15 +806,36 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
     }
   }
   const float inv = 1.0f / lane_pair_sum(l_run);
-  // this lane's gate values (channel-major, like q)
-  bf16x4 gpre[4];
-  {
-    const bf16* gr = ws.gate + (rowbase * CH + h * HD) * (int64_t)Np + q0 + t32;
+  // Epilogue.  Every global load it needs (the W_o fragments and the
+  // residual rows of this wave's output tile, the gate) is issued here,
+  // before the first store: vmcnt counts stores too, so a load issued after
+  // a store is only waited for together with that store.
+  constexpr int NT = CIN / 32;
+  static_assert(QT * NT == H * QT, "one output tile per wave");
+  const int oq = wave / NT, nt = wave % NT;
+  Frag<bf16> wof[CH / 16];
+  if constexpr (!WO_LDS) {
+#pragma unroll
+    for (int ks = 0; ks < CH / 16; ++ks) load_wfrag<bf16>(wof[ks], w.w_o, nt, ks, CH / 16);
+  }
+  const int q_out = qb * QB + oq * 32 + t32;
+  const bool q_ok = q_out < N;
+  const int64_t pair_out =
+      ((int64_t)b * N + (starting ? r : (q_ok ? q_out : 0))) * N + (starting ? (q_ok ? q_out : 0) : r);
+  f32x4 bo[4];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) bo[g] = *reinterpret_cast<const f32x4*>(w.b_o + nt * 32 + 8 * g + 4 * half);
+  bf16x4 xres[4];
+  if (residual) {
 #pragma unroll
     for (int g = 0; g < 4; ++g)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) gpre[g][rr] = gr[(int64_t)(8 * g + 4 * half + rr) * Np];
+      xres[g] = *reinterpret_cast<const bf16x4*>(x + pair_out * CIN + nt * 32 + 8 * g + 4 * half);
   }
+  // this lane's gate values (channel-major, like q)
+  bf16x4 gpre[4];
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's gate tile has landed (wave-local region)
+#pragma unroll
+  for (int g = 0; g < 4; ++g) gpre[g] = __builtin_bit_cast(bf16x4, read_cq4(nkb % NS, 8 * g + 4 * half));
 
   // o * gate for all heads, staged as [query][CH] over the ring
   __syncthreads();
@@ -785,37 +849,28 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
            o[4 * g + 3] * inv * (float)gv[3]);
   }
   __syncthreads();
-  // output projection: wave -> (query tile, output tile)
-  constexpr int NT = CIN / 32;
-  for (int tt = wave; tt < QT * NT; tt += H * QT) {
-    const int oq = tt / NT, nt = tt % NT;
+  // output projection: wave -> (query tile oq, output tile nt)
+  {
     Frag<bf16> of[CH / 16];
 #pragma unroll
     for (int ks = 0; ks < CH / 16; ++ks) of[ks].load(os + (oq * 32 + t32) * OP + half * (CH / 2) + ks * 8);
     f32x16 acc = zero16();
 #pragma unroll
     for (int ks = 0; ks < CH / 16; ++ks) {
-      Frag<bf16> wf;
-      if constexpr (WO_LDS) load_wfrag_lds(wf, wo_l, nt, ks, CH / 16);
-      else load_wfrag<bf16>(wf, w.w_o, nt, ks, CH / 16);
-      mma(acc, wf, of[ks]);
+      if constexpr (WO_LDS) load_wfrag_lds(wof[ks], wo_l, nt, ks, CH / 16);
+      mma(acc, wof[ks], of[ks]);
     }
-    const int q = qb * QB + oq * 32 + t32;
-    if (q < N) {
-      const int p0 = starting ? r : q, p1 = starting ? q : r;
-      const int64_t pair = ((int64_t)b * N + p0) * N + p1;
+    if (q_ok) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int c0 = nt * 32 + 8 * g + 4 * half;
         float v[4];
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) v[rr] = acc[4 * g + rr] + w.b_o[c0 + rr];
-        if (residual) {
-          const f32x4 xr = load4f(x + pair * CIN + c0);
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) v[rr] += xr[rr];
+        for (int rr = 0; rr < 4; ++rr) {
+          v[rr] = acc[4 * g + rr] + bo[g][rr];
+          if (residual) v[rr] += (float)xres[g][rr];
         }
-        store4(out + pair * CIN + c0, v[0], v[1], v[2], v[3]);
+        store4(out + pair_out * CIN + c0, v[0], v[1], v[2], v[3]);
       }
     }
   }

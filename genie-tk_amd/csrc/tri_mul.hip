@@ -633,10 +633,9 @@ __global__ __launch_bounds__(512) void trimul_epilogue_bf16_kernel(
   // pairs 8k .. 8k+7 with k = p ^ swz(c).  Copy instruction n moves rows
   // 16n .. 16n+15; lane l lands at row 16n + l/4, physical chunk l%4.
   auto swz = [](int c) { return 2 * ((c >> 1) & 1); };
-  auto issue_x = [&](int64_t tile) {
-    const int jt = (int)(tile % jtiles);
-    const int i = (int)((tile / jtiles) % N);
-    const int b = (int)(tile / ((int64_t)jtiles * N));
+  // tiles: [B][N rows i][jtiles], walked without divisions
+  auto issue_x = [&](const TileWalk& tw) {
+    const int jt = tw.c, i = tw.r, b = tw.b;
     const bf16* src = px + (int64_t)b * CH * plane + (int64_t)i * Np + jt * 32;
 #pragma unroll
     for (int n = 0; n < CH / 16; ++n) {
@@ -645,18 +644,15 @@ __global__ __launch_bounds__(512) void trimul_epilogue_bf16_kernel(
       g2lds16(src + row * plane + 8 * k, xw + n * 512);
     }
   };
-  auto load_z = [&](Frag<bf16>* zr, int64_t tile) {
-    const int jt = (int)(tile % jtiles);
-    const int i = (int)((tile / jtiles) % N);
-    const int b = (int)(tile / ((int64_t)jtiles * N));
+  // Always KZ load instructions (an invalid pair reads pair j = 0; its
+  // results are never stored): the wait below counts them.
+  auto load_z = [&](Frag<bf16>* zr, const TileWalk& tw) {
+    const int jt = tw.c, i = tw.r, b = tw.b;
     const int j = jt * 32 + t32;
     const bool valid = j < N;
     const bf16* row = z + (((int64_t)b * N + i) * N + (valid ? j : 0)) * CZ + half * (CZ / 2);
 #pragma unroll
-    for (int ch = 0; ch < KZ; ++ch) {
-      if (valid) zr[ch].load(row + ch * 8);
-      else zr[ch].zero();
-    }
+    for (int ch = 0; ch < KZ; ++ch) zr[ch].load(row + ch * 8);
   };
   // transposing-read addresses: fetching lane (group G = lane/16, i = lane%16)
   // reads channel row c_m, m = i/4, at pairs 16*(G&1) + 4*(i%4) .. +3
@@ -684,32 +680,55 @@ __global__ __launch_bounds__(512) void trimul_epilogue_bf16_kernel(
   int64_t tile = (int64_t)blockIdx.x * WAVES + wave;
   const int64_t stride = (int64_t)gridDim.x * WAVES;
   Frag<bf16> zr[KZ];
-  if (tile < ntiles) {
-    issue_x(tile);
-    load_z(zr, tile);
-  }
-  for (; tile < ntiles; tile += stride) {
-    const int jt = (int)(tile % jtiles);
-    const int i = (int)((tile / jtiles) % N);
-    const int b = (int)(tile / ((int64_t)jtiles * N));
+  // One tile.  The first tile is peeled off the loop (first = true) so that
+  // every path into the loop has the previous tile's stores outstanding
+  // behind the prefetched loads, and the waits can count them exactly.
+  auto body = [&](const int64_t tile, const TileWalk& tw, const bool first) {
+    const int jt = tw.c, i = tw.r, b = tw.b;
     const int j = jt * 32 + t32;
     const bool valid = j < N;
-    const int64_t pair = ((int64_t)b * N + i) * N + (valid ? j : 0);
+    // this tile's 32 output pairs, one buffer range: every lane stores
+    // (invalid pairs are dropped by the range check), no branch
+    const auto orsrc = buf_rsrc(out + (((int64_t)b * N + i) * N + jt * 32) * CZ, 32 * CZ * 2);
     Frag<bf16> xf[KZ], yf[KX];
     ln_frags_bf16<CZ>(xf, zr, eps_in);
-    __builtin_amdgcn_s_waitcnt(0);  // this tile's x copy has landed in LDS
+    // Residual z in the accumulator layout, taken from the rows just loaded:
+    // output group q (channels 8q + 4*half + 0..3) sits in dwords 0-1
+    // (q < KZ) or 2-3 (q >= KZ) of zr[q mod KZ] once dwords 2-3 of the lower
+    // half-wave are swapped with dwords 0-1 of the upper one.
+    bf16x4 zres[2 * KZ];
+    if (residual) {
+#pragma unroll
+      for (int ch = 0; ch < KZ; ++ch) {
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x4 d = __builtin_bit_cast(u32x4, zr[ch].v);
+        const auto s02 = __builtin_amdgcn_permlane32_swap(d[0], d[2], false, false);
+        const auto s13 = __builtin_amdgcn_permlane32_swap(d[1], d[3], false, false);
+        zres[ch] = __builtin_bit_cast(bf16x4, u32x2{s02[0], s13[0]});
+        zres[ch + KZ] = __builtin_bit_cast(bf16x4, u32x2{s02[1], s13[1]});
+      }
+    }
+    // This tile's x copy has landed once at most the ops issued after it are
+    // outstanding: the KZ row loads, then (after the first tile) the previous
+    // tile's 4*CZ/32 stores.  Loads complete in issue order, so the stores
+    // need not have completed.
+    if (first) __builtin_amdgcn_s_waitcnt(vmcnt_imm<KZ>());
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm<KZ + 4 * (CZ / 32)>());
     {
       Frag<bf16> xr[KX];
       read_x(xr);
       ln_frags_bf16<CH>(yf, xr, eps_out);
     }
-    __builtin_amdgcn_s_waitcnt(0);  // transposing reads done: the buffer is free
-    const int64_t next = tile + stride;
-    if (next < ntiles) {
-      issue_x(next);
-      load_z(zr, next);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): transposing reads done, the buffer is free
+    if (tile + stride < ntiles) {
+      TileWalk nx = tw;
+      nx.next();
+      issue_x(nx);
+      load_z(zr, nx);
     }
-#pragma unroll 1
+    // unrolled: zres is indexed by nt (a run-time index would put it in scratch)
+#pragma unroll
     for (int nt = 0; nt < CZ / 32; ++nt) {
       Frag<bf16> f;
       load_wfrag_lds(f, wg, nt, 0, KZ);
@@ -726,25 +745,31 @@ __global__ __launch_bounds__(512) void trimul_epilogue_bf16_kernel(
         load_wfrag_lds(f, wz, nt, ks, KX);
         mma(oa, f, yf[ks]);
       }
-      if (valid) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int c0 = nt * 32 + 8 * g + 4 * half;
-          const f32x4 bg = *reinterpret_cast<const f32x4*>(bl + c0);
-          const f32x4 bz = *reinterpret_cast<const f32x4*>(bl + CZ + c0);
-          float o[4];
+      for (int g = 0; g < 4; ++g) {
+        const int c0 = nt * 32 + 8 * g + 4 * half;
+        const f32x4 bg = *reinterpret_cast<const f32x4*>(bl + c0);
+        const f32x4 bz = *reinterpret_cast<const f32x4*>(bl + CZ + c0);
+        float o[4];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) o[r] = (oa[4 * g + r] + bz[r]) * gate_from_u(ga[4 * g + r] + bg[r]);
-          if (residual) {
-            const f32x4 zres = load4f(z + pair * CZ + c0);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) o[r] += zres[r];
-          }
-          store4(out + pair * CZ + c0, o[0], o[1], o[2], o[3]);
+        for (int r = 0; r < 4; ++r) {
+          o[r] = (oa[4 * g + r] + bz[r]) * gate_from_u(ga[4 * g + r] + bg[r]);
+          if (residual) o[r] += (float)zres[nt * 4 + g][r];
         }
+        buf_store4(orsrc, valid ? (uint32_t)((t32 * CZ + c0) * 2) : kBufSkip, o[0], o[1], o[2], o[3]);
       }
     }
+  };
+  TileWalk tw;
+  tw.init(tile, stride, N, jtiles);
+  if (tile < ntiles) {
+    issue_x(tw);
+    load_z(zr, tw);
+    body(tile, tw, true);
+    tile += stride;
+    tw.next();
   }
+  for (; tile < ntiles; tile += stride, tw.next()) body(tile, tw, false);
 }
 
 // ---------------------------------------------------------------------------
