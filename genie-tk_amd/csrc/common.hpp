@@ -124,6 +124,12 @@ __device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, uint32_t of
   __builtin_amdgcn_raw_buffer_store_b64(v, r, off, 0, 0);
 }
 
+// 16 bytes at byte offset `off` (same range rule as buf_store4).
+__device__ __forceinline__ void buf_store16(__amdgpu_buffer_rsrc_t r, uint32_t off, uint4 v) {
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  __builtin_amdgcn_raw_buffer_store_b128(u32x4{v.x, v.y, v.z, v.w}, r, off, 0, 0);
+}
+
 // Load 4 consecutive values as fp32.
 __device__ __forceinline__ f32x4 load4f(const bf16* p) {
   bf16x4 v = *reinterpret_cast<const bf16x4*>(p);

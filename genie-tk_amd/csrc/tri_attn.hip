@@ -229,19 +229,45 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
   const int i32 = lane & 31;
   const int prow = 16 * ((i32 >> 2) & 1) + 4 * (i32 >> 3) + (i32 & 3);
   const int vtiles = Np / 32;
-  for (int64_t tile = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 6); tile < ntiles;
-       tile += (int64_t)gridDim.x * 16) {
-    const int vt = (int)(tile % vtiles);
-    const int r = (int)((tile / vtiles) % Np);  // destination row
-    const int b = (int)(tile / ((int64_t)vtiles * Np));
+  // Tiles [B][Np rows r][vtiles], walked without divisions.  The input rows of
+  // the next tile are loaded at the start of each tile, ahead of its stores:
+  // loads complete in issue order, so waiting for rows loaded after a store
+  // would wait for that store too.  A lane outside the pair grid reads pair 0
+  // and normalises to zero.
+  const int64_t tstride = (int64_t)gridDim.x * 16;
+  int64_t tile = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 6);
+  TileWalk tw;
+  tw.init(tile, tstride, Np, vtiles);
+  // (exists = false: a tile past the end, also read as pair 0)
+  auto load_rows = [&](Frag<bf16>* raw, const TileWalk& t, bool exists) {
+    const int jo = t.c * 32 + prow;
+    const bool ok = exists && t.r < N && jo < N;
+    const int p = starting ? t.r : jo, q = starting ? jo : t.r;
+    const bf16* src = x + (ok ? (((int64_t)t.b * N + p) * N + q) * CIN : 0) + half * (CIN / 2);
+#pragma unroll
+    for (int ch = 0; ch < KCH; ++ch) raw[ch].load(src + ch * 8);
+  };
+  Frag<bf16> raw[KCH];
+  // One tile.  Every path through it issues the same loads and stores (no
+  // branch around any of them), and the first tile is peeled off the loop, so
+  // the compiler's waits for the prefetched rows count the stores issued
+  // after them instead of waiting for them.
+  auto body = [&](const int64_t tile) {
+    const int vt = tw.c;
+    const int r = tw.r;  // destination row
+    const int b = tw.b;
     const int jown = vt * 32 + prow;            // this lane's pair (A/B operand side)
     Frag<bf16> xf[KCH];
-    bool valid;
+    const bool valid = r < N && jown < N;
+    ln_frags_bf16<CIN>(xf, raw, eps);
+    if (!valid) {
+#pragma unroll
+      for (int ch = 0; ch < KCH; ++ch) xf[ch].zero();
+    }
     {
-      valid = r < N && jown < N;
-      const int p = starting ? r : jown, q = starting ? jown : r;
-      const int64_t pair = ((int64_t)b * N + (valid ? p : 0)) * N + (valid ? q : 0);
-      ln_row_bf16<CIN>(xf, x + pair * CIN, valid, eps);
+      TileWalk nx = tw;
+      nx.next();
+      load_rows(raw, nx, tile + tstride < ntiles);
     }
     const int64_t rowbase = (int64_t)b * Np + r;
     const int j0 = vt * 32 + 16 * half;         // first of this lane's 16 positions
@@ -299,18 +325,25 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
         load_wfrag_lds(fb, wb, 0, ks, KCH);
         mma(ab, xf[ks], fb);
       }
-      if (i32 < H) {
-        const float bb = bl[4 * CH + i32];
-        uint32_t pk[8];
+      // lanes i32 >= H store nothing (out-of-range offset, no branch)
+      const float bb = bl[4 * CH + (i32 & (H - 1))];
+      uint32_t pk[8];
 #pragma unroll
-        for (int m = 0; m < 16; m += 2)
-          pk[m / 2] = pack_bf16x2(m < nvalid ? ab[m] + bb : 0.f, m + 1 < nvalid ? ab[m + 1] + bb : 0.f);
-        uint4* o = reinterpret_cast<uint4*>(ws.bias + (((int64_t)b * H + i32) * Np + r) * Np + j0);
-        o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-        o[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
-      }
+      for (int m = 0; m < 16; m += 2)
+        pk[m / 2] = pack_bf16x2(m < nvalid ? ab[m] + bb : 0.f, m + 1 < nvalid ? ab[m + 1] + bb : 0.f);
+      const auto brs = buf_rsrc(ws.bias + (int64_t)b * H * Np * Np, (uint32_t)(H * Np * Np * 2));
+      const uint32_t off = i32 < H ? (uint32_t)((((int64_t)i32 * Np + r) * Np + j0) * 2) : kBufSkip;
+      buf_store16(brs, off, make_uint4(pk[0], pk[1], pk[2], pk[3]));
+      buf_store16(brs, off + 16, make_uint4(pk[4], pk[5], pk[6], pk[7]));
     }
+  };
+  if (tile < ntiles) {
+    load_rows(raw, tw, true);
+    body(tile);
+    tile += tstride;
+    tw.next();
   }
+  for (; tile < ntiles; tile += tstride, tw.next()) body(tile);
 }
 
 // ---------------------------------------------------------------------------
