@@ -146,10 +146,19 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
   constexpr int KCH = CZ / 16;
   constexpr int PE = (CH / 32) * KCH * 512;  // packed elements of one projection
   __shared__ __attribute__((aligned(1024))) bf16 wl[4][PE];
+  // biases in LDS: read in the loop between stores, a global load would wait
+  // for the stores issued before it (loads complete in issue order)
+  __shared__ float bl[2][2][CH];  // [side][projection, gate as 2^b_g]
   copy_to_lds_async(wl[0], w.w_ap, PE * 2);
   copy_to_lds_async(wl[1], w.w_ag, PE * 2);
   copy_to_lds_async(wl[2], w.w_bp, PE * 2);
   copy_to_lds_async(wl[3], w.w_bg, PE * 2);
+  for (int t = threadIdx.x; t < CH; t += blockDim.x) {
+    bl[0][0][t] = w.b_ap[t];
+    bl[0][1][t] = fmaxf(__builtin_amdgcn_exp2f(w.b_ag[t]), 1.17549435e-38f);
+    bl[1][0][t] = w.b_bp[t];
+    bl[1][1][t] = fmaxf(__builtin_amdgcn_exp2f(w.b_bg[t]), 1.17549435e-38f);
+  }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
@@ -216,8 +225,8 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
     for (int side = 0; side < 2; ++side) {
       const bf16* wp = wl[2 * side];
       const bf16* wg = wl[2 * side + 1];
-      const float* bp = side ? w.b_bp : w.b_ap;
-      const float* bg = side ? w.b_bg : w.b_ag;
+      const float* bp = bl[side][0];
+      const float* ebgs = bl[side][1];
       bf16* dst = (side ? pb : pa) + (int64_t)b * CH * plane + (int64_t)f * Np + vt * 32 + 16 * half;
 #pragma unroll 1
       for (int ct = 0; ct < CH / 32; ++ct) {
@@ -237,7 +246,7 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
         }
         const int cc = ct * 32 + i32;
         const float bpc = bp[cc];
-        const float ebg = fmaxf(__builtin_amdgcn_exp2f(bg[cc]), 1.17549435e-38f);
+        const float ebg = ebgs[cc];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const f32x16& ap = u ? ap1 : ap0;
