@@ -636,39 +636,35 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
   const bool row_valid = __builtin_amdgcn_readfirstlane(row_any) != 0;
   const bool row_clean = __builtin_amdgcn_readfirstlane(row_dirty) == 0;
 
-  // Async stage load.  A stage is 32 regions of 1 KiB (64 lanes x 16 B);
-  // wave w moves regions RPW*w .. RPW*w + RPW-1.  Regions 0..15: K^T, head
-  // reg/4, chunks P = (reg%4)*64 + lane of that head's [32 d][64 keys] tile;
-  // regions 16..31: V^T likewise.
-  // Physical 16-byte chunk P of a K^T or V^T tile holds row d = P/8, logical
-  // chunk (P%8) ^ vswz(d): rows read together get distinct banks, whether 8
-  // or 16 lanes are served per LDS cycle.
-  auto vswz = [](int d) { return (d ^ (d >> 3)) & 7; };
-  // K^T and V^T are both [32 d][Np keys] per (row, head); a stage holds the
-  // [32 d][64 keys] tile of each head for both.
-  const bool k_region = wave < NW / 2;     // the first half of the waves move K^T
-  // wave-uniform source base (K^T or V^T of this row, all heads)
+  // Async stage load.  A stage holds, for each head, the K^T and the V^T
+  // block of 64 keys ([32 d][64 keys] each, 4 KiB); each splits into two 2 KiB
+  // sub-blocks of 32 keys (sb), rows d of 64 bytes.  A stage is 32 regions of
+  // 1 KiB (64 lanes x 16 B): region r is kind r>>4 (K^T, V^T), head (r>>2)&3,
+  // sub-block (r>>1)&1, rows 16*(r&1) .. +15; lane l lands at row l/4,
+  // physical 16-byte chunk l%4.  K^T chunks are unswizzled: the transposing
+  // reads of a 16-lane group cover 4 consecutive rows x 32 bytes and the
+  // paired group the other halves, every bank once.  V^T chunk p of row d sits
+  // at physical chunk p ^ ((d>>2)&3), so the 16-byte reads of rows d, d+4,
+  // d+8, d+12 fall in distinct banks.  Wave w moves regions RPW*w ..
+  // RPW*w + RPW-1, all of one kind.
+  static_assert(2 * H * 4 == 32 && (16 % RPW) == 0, "32 regions per stage, one kind per wave");
+  const int rg0 = wave * RPW;
+  const bool k_region = rg0 < 16;  // the first half of the waves move K^T
   const bf16* gbase = (k_region ? ws.k : ws.vt) + (rowbase * H) * (int64_t)HD * Np;
-  const int rg_head = ((wave * RPW) & 15) >> 2;
-  const int rg_sub0 = (wave * RPW) & 3;
-  // Lane l of region i (sub = rg_sub0 + i) moves physical chunk P = sub*64 + l:
-  // row d = sub*8 + l/8 of the head's tile, logical chunk (l%8) ^ vswz(d) =
-  // (l%8) ^ (l/8) ^ sub (mod 8).  Its byte offset from gbase at key 0 (a stage
-  // at key k0 adds 2*k0) is row_off + 16*Np*i + 16*(cx ^ (sub & 7)).
-  const uint32_t row_off0 = (uint32_t)((rg_head * HD + rg_sub0 * 8) * (int64_t)Np * 2);  // uniform
   const uint32_t ring_lds = lds_addr(&ring[0][0]);
-  const uint32_t dst0 = ((k_region ? 0 : H) + rg_head) * HEAD_BYTES + rg_sub0 * 1024;
   auto issue_stage = [&](int stage, int k0) {
-    // The per-lane offsets are recomputed from the lane id here rather than
-    // kept across the tile loop: at the register cap they would be spilled,
-    // and a reload from scratch waits for every outstanding load.
+    // The per-lane offset is recomputed from the lane id here rather than
+    // kept across the tile loop: at the register cap it would be spilled, and
+    // a reload from scratch waits for every outstanding load.  It is the same
+    // for every region; the rest of each source address is uniform.
     const uint32_t ln = (uint32_t)(lane + opaque_zero());
-    const uint32_t cx = (ln & 7) ^ (ln >> 3);
-    const uint32_t row_off = row_off0 + (ln >> 3) * (uint32_t)(Np * 2);
+    const uint32_t p = k_region ? (ln & 3) : ((ln & 3) ^ ((ln >> 4) & 3));
+    const uint32_t voff = ((ln >> 2) * (uint32_t)Np + 8 * p) * 2;
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
-      const uint32_t goff = row_off + (uint32_t)(16 * Np * i) + 16 * (cx ^ ((rg_sub0 + i) & 7));
-      g2lds16_sv(gbase + k0, goff, ring_lds + stage * STAGE_BYTES + dst0 + i * 1024);
+      const int r = rg0 + i;
+      const bf16* src = gbase + (int64_t)(((r >> 2) & 3) * HD + 16 * (r & 1)) * Np + 32 * ((r >> 1) & 1) + k0;
+      g2lds16_sv(src, voff, ring_lds + stage * STAGE_BYTES + r * 1024);
     }
   };
 
@@ -706,6 +702,10 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
   const int trG = lane >> 4;
   const int tr_m = (lane & 15) >> 2;
   const int tr_q = lane & 3;
+  const int kt_lane = ((trG >> 1) * 8 + tr_m) * 64 + 32 * (trG & 1) + 8 * tr_q;
+  // V^T reads (P V): row t32, chunk half ^ ((t32>>2)&3) for c = 0; c = 1 flips
+  // bit 1 of the chunk, i.e. byte offset ^ 32
+  const int vt_lane = t32 * 64 + 16 * (half ^ ((t32 >> 2) & 3));
   // identity fragments: row key (t32), slot half*8+e of chunk cb <-> key cb*16+half*8+e
   Frag<bf16> idf[2];
 #pragma unroll
@@ -727,16 +727,14 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
   auto s_tile = [&](int t) {
     f32x16 s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(idf[0].v, bfr[0].v, negm, 0, 0, 0);
     mma(s, idf[1], bfr[1]);
-    const char* kt_base = ring[(t >> 1) % NS] + h * HEAD_BYTES;
-    const int chunk = (t & 1) * 4 + 2 * (trG & 1) + (tr_q >> 1);  // logical 8-key chunk
+    // sub-block t&1 of this head's K^T; row d = m*16 + (trG>>1)*8 + hh*4 +
+    // tr_m, keys 16*(trG&1) + 4*tr_q: one base plus constant offsets
+    const char* kt_base = ring[(t >> 1) % NS] + h * HEAD_BYTES + (t & 1) * 2048 + kt_lane;
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       s16x4 part[2];
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int d = m * 16 + (trG >> 1) * 8 + hh * 4 + tr_m;
-        part[hh] = lds_read_tr16(kt_base + d * 128 + 16 * (chunk ^ vswz(d)) + 8 * (tr_q & 1));
-      }
+      for (int hh = 0; hh < 2; ++hh) part[hh] = lds_read_tr16(kt_base + (m * 16 + hh * 4) * 64);
       typedef short s16x8 __attribute__((ext_vector_type(8)));
       const s16x8 v8 = {part[0][0], part[0][1], part[0][2], part[0][3],
                         part[1][0], part[1][1], part[1][2], part[1][3]};
@@ -820,7 +818,8 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
       }
       m_use = m_next;
     }
-    const char* vt_base = ring[cur] + (H + h) * HEAD_BYTES;
+    // sub-block t&1 of this head's V^T, row t32
+    const char* vt_base = ring[cur] + (H + h) * HEAD_BYTES + (t & 1) * 2048;
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       Frag<bf16> pf, vf;
@@ -832,9 +831,8 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
         const bf16x2_t pp = {pf.v[e], pf.v[e + 1]};
         l_run = __builtin_amdgcn_fdot2_f32_bf16(pp, ones2, l_run, false);
       }
-      // V^T row d = t32, keys (t&1)*32 + 16c + 8*half .. +8
-      const int lc = ((t & 1) * 4 + 2 * c + half) ^ vswz(t32);
-      vf.load(reinterpret_cast<const bf16*>(vt_base + t32 * 128 + lc * 16));
+      // keys 16c + 8*half .. +8 of the sub-block: chunk (2c + half) ^ ((t32>>2)&3)
+      vf.load(reinterpret_cast<const bf16*>(vt_base + (c ? (vt_lane ^ 32) : vt_lane)));
       mma(o, vf, pf);
     }
   }
