@@ -256,6 +256,18 @@ def main() -> int:
             torch, lambda: layer.pair_transition.forward_residual_masked(z, mask), reps))
         layer_ms = statistics.median(event_time_ms(torch, lambda: layer((z, mask)), reps))
         del layer
+        # LayerNorm + Linear (nn.Linear-layout weight) over the pair tensor, c -> c
+        lw = (torch.randn(C_Z, C_Z, device=dev) / C_Z ** 0.5).to(torch.bfloat16)
+        lb = torch.randn(C_Z, device=dev)
+        lnlin_ms = statistics.median(event_time_ms(
+            torch, lambda: C.layernorm_linear(z, ln_w, ln_b, lw, lb, 1e-5), reps))
+        C.timing_enable(True)
+        for _ in range(reps):
+            C.layernorm_linear(z, ln_w, ln_b, lw, lb, 1e-5)
+        lnlin_rep = C.timing_report()
+        C.timing_enable(False)
+        lnlin_kernel_ms = (lnlin_rep["ln_linear"][1] / lnlin_rep["ln_linear"][0]
+                           if "ln_linear" in lnlin_rep else None)
         z2 = torch.randn(1, 2 * N, 2 * N, C_Z, device=dev).to(torch.bfloat16)
         ln2 = lambda: C.layernorm(z2, ln_w, ln_b, 1e-5)  # noqa: E731
         ln2_ms = statistics.median(event_time_ms(torch, ln2, reps))
@@ -302,6 +314,16 @@ def main() -> int:
         "tflops": round(tf / (trans_ms * 1e-3) / 1e12, 2),
         "frac_bf16_peak": round(tf / (trans_ms * 1e-3) / PEAK_BF16_FLOPS, 4),
         "note": "fused LN -> c->4c -> ReLU -> 4c->c, residual and mask (informational)",
+    }
+    llf, llb = 2.0 * N * N * C_Z * C_Z, 2 * N * N * C_Z * 2
+    per_op["layernorm_linear"] = {
+        "ms": round(lnlin_ms, 4), "gflop": round(llf / 1e9, 2), "mb": round(llb / 1e6, 1),
+        "kernel_ms": round(lnlin_kernel_ms, 4) if lnlin_kernel_ms else None,
+        "kernel_gbps": round(llb / (lnlin_kernel_ms * 1e-3) / 1e9, 1) if lnlin_kernel_ms else None,
+        "kernel_frac_hbm": (round(llb / (lnlin_kernel_ms * 1e-3) / PEAK_HBM_BYTES, 4)
+                            if lnlin_kernel_ms else None),
+        "note": "LN + Linear c->c, nn.Linear-layout weight, bf16; ms includes the per-call weight "
+                "packing, kernel_ms is the LN+Linear kernel alone (informational; HBM-bound)",
     }
     lf = step_flops_of(fm, fa) + tf
     per_op["pair_layer"] = {

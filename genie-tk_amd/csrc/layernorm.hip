@@ -9,6 +9,8 @@
 //
 // gtk_fused_layernorm_linear: the row is normalised in MFMA fragment layout
 // (see common.hpp) and multiplied with the packed weight on the matrix cores.
+#include <algorithm>
+
 #include "capi_util.hpp"
 #include "common.hpp"
 #include "pack.hpp"
@@ -154,19 +156,102 @@ __global__ __launch_bounds__(256) void ln_linear_kernel(const T* __restrict__ x,
   Frag<T> xf[DIN / 16];
   ln_to_frags<T, DIN>(xf, rh, st);
   const int ntiles = (d_out + 31) / 32;
+  const bool vec4 = (d_out & 3) == 0;  // 4 outputs per store
   for (int nt = 0; nt < ntiles; ++nt) {
     const f32x16 acc = row_gemm_tile<T, DIN, true>(xf, wp, nt);
     if (!valid) continue;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int o0 = nt * 32 + 8 * g + 4 * half;
+      if (vec4) {
+        if (o0 < d_out)
+          store4(y + row * d_out + o0, acc[4 * g] + bias[o0], acc[4 * g + 1] + bias[o0 + 1],
+                 acc[4 * g + 2] + bias[o0 + 2], acc[4 * g + 3] + bias[o0 + 3]);
+      } else {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int o = o0 + r;
-        if (o < d_out) y[row * d_out + o] = cvt<T>(acc[4 * g + r] + bias[o]);
+        for (int r = 0; r < 4; ++r) {
+          const int o = o0 + r;
+          if (o < d_out) y[row * d_out + o] = cvt<T>(acc[4 * g + r] + bias[o]);
+        }
       }
     }
   }
+}
+
+// bf16 with the packed weights and the folded bias resident in LDS (dynamic
+// shared memory, wbytes + 4 * 32 * ceil(d_out / 32) bytes): persistent blocks
+// of 8 waves, one 32-row tile per wave step.  Each output tile's weight
+// fragments are read from LDS ahead of its MFMA chain.
+template <int DIN>
+__global__ __launch_bounds__(512) void ln_linear_lds_kernel(const bf16* __restrict__ x,
+                                                            bf16* __restrict__ y,
+                                                            const bf16* __restrict__ wp,
+                                                            const float* __restrict__ bias,
+                                                            int64_t rows, int d_out, float eps,
+                                                            int64_t ntiles, int wbytes) {
+  extern __shared__ __attribute__((aligned(1024))) char ln_smem[];
+  bf16* wl = reinterpret_cast<bf16*>(ln_smem);
+  float* bl = reinterpret_cast<float*>(ln_smem + wbytes);
+  const int nto = (d_out + 31) / 32;
+  copy_to_lds_async(wl, wp, wbytes);
+  for (int t = threadIdx.x; t < nto * 32; t += blockDim.x) bl[t] = t < d_out ? bias[t] : 0.f;
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  constexpr int KC = DIN / 16;
+  const int lane = threadIdx.x & 63;
+  const int half = lane >> 5;
+  const int t32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const bool vec4 = (d_out & 3) == 0;
+  const int64_t stride = (int64_t)gridDim.x * 8;
+  // Rows of a tile; a row past the end (or a tile past the end) reads row 0.
+  // The next tile's rows are loaded before this tile's stores, the stores
+  // are branch-free (an out-of-range offset drops them) and the first tile
+  // is peeled, so the waits for prefetched rows do not wait for stores.
+  auto load_rows = [&](Frag<bf16>* raw, int64_t tile) {
+    const int64_t row = tile * 32 + t32;
+    const bf16* src = x + (row < rows ? row : 0) * DIN + half * (DIN / 2);
+#pragma unroll
+    for (int ch = 0; ch < KC; ++ch) raw[ch].load(src + ch * 8);
+  };
+  Frag<bf16> raw[KC];
+  auto body = [&](const int64_t tile) {
+    const int64_t row = tile * 32 + t32;
+    const bool valid = row < rows;
+    Frag<bf16> xf[KC];
+    ln_frags_bf16<DIN>(xf, raw, eps);
+    load_rows(raw, tile + stride);
+    const auto ors = buf_rsrc(y + tile * 32 * (int64_t)d_out, (uint32_t)(32 * d_out * 2));
+    for (int nt = 0; nt < nto; ++nt) {
+      Frag<bf16> f[KC];
+#pragma unroll
+      for (int ks = 0; ks < KC; ++ks) load_wfrag_lds(f[ks], wl, nt, ks, KC);
+      f32x16 acc = mma0(f[0], xf[0]);  // rows = outputs, columns = x rows
+#pragma unroll
+      for (int ks = 1; ks < KC; ++ks) mma(acc, f[ks], xf[ks]);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int o0 = nt * 32 + 8 * g + 4 * half;
+        const f32x4 b4 = *reinterpret_cast<const f32x4*>(bl + o0);
+        if (vec4) {
+          const bool ok = valid && o0 < d_out;
+          buf_store4(ors, ok ? (uint32_t)((t32 * d_out + o0) * 2) : kBufSkip, acc[4 * g] + b4[0],
+                     acc[4 * g + 1] + b4[1], acc[4 * g + 2] + b4[2], acc[4 * g + 3] + b4[3]);
+        } else if (valid) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (o0 + r < d_out) y[row * d_out + o0 + r] = (bf16)(acc[4 * g + r] + b4[r]);
+        }
+      }
+    }
+  };
+  int64_t tile = (int64_t)blockIdx.x * 8 + wave;
+  if (tile < ntiles) {
+    load_rows(raw, tile);
+    body(tile);
+    tile += stride;
+  }
+  for (; tile < ntiles; tile += stride) body(tile);
 }
 
 }  // namespace gtk
@@ -212,8 +297,19 @@ extern "C" int gtk_fused_layernorm_linear(const void* x, void* y, const float* g
                                           const float* bias, int64_t rows, int64_t d_in,
                                           int64_t d_out, float eps, int dtype, void* workspace,
                                           size_t workspace_bytes, void* stream) {
+  return gtk_layernorm_linear(x, y, gamma, beta, weight, weight_dtype, GTK_W_IN_OUT, bias, rows,
+                              d_in, d_out, eps, dtype, workspace, workspace_bytes, stream);
+}
+
+extern "C" int gtk_layernorm_linear(const void* x, void* y, const float* gamma, const float* beta,
+                                    const void* weight, int weight_dtype, int weight_layout,
+                                    const float* bias, int64_t rows, int64_t d_in, int64_t d_out,
+                                    float eps, int dtype, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
   GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL,
               "gtk_fused_layernorm_linear: bad dtype %d", dtype);
+  GTK_REQUIRE(weight_layout == GTK_W_IN_OUT || weight_layout == GTK_W_OUT_IN, GTK_EINVAL,
+              "gtk_layernorm_linear: bad weight layout %d", weight_layout);
   GTK_REQUIRE(weight_dtype == GTK_F32 || weight_dtype == GTK_BF16, GTK_EINVAL,
               "gtk_fused_layernorm_linear: bad weight dtype %d", weight_dtype);
   GTK_REQUIRE(d_in == 64 || d_in == 128 || d_in == 256, GTK_EUNSUPPORTED,
@@ -228,17 +324,20 @@ extern "C" int gtk_fused_layernorm_linear(const void* x, void* y, const float* g
               "gtk_fused_layernorm_linear: workspace %zu < %zu bytes", workspace_bytes, need);
   hipStream_t st = (hipStream_t)stream;
   const unsigned grid = (unsigned)(((rows + 31) / 32 + 3) / 4);
-  // weight is [d_in][d_out]: logical W[out][in] has s_out = 1, s_in = d_out.
+  // Logical W[out][in]: [d_in][d_out] has s_out = 1, s_in = d_out; the
+  // nn.Linear layout [d_out][d_in] has s_out = d_in, s_in = 1.
   // The caller's bias has fp32 type; the folded bias starts from it.
+  const int64_t s_out = weight_layout == GTK_W_IN_OUT ? 1 : d_in;
+  const int64_t s_in = weight_layout == GTK_W_IN_OUT ? d_out : 1;
   int rc;
   Carve cv(workspace, workspace_bytes);
   float* fb;
   if (dtype == GTK_F32) {
     float* wp;
     carve_ln_linear<float>(cv, d_in, d_out, &wp, &fb);
-    if ((rc = launch_pack<float>(wp, weight, weight_dtype, (int)d_out, (int)d_in, 1, d_out, 1.f, st, gamma)))
+    if ((rc = launch_pack<float>(wp, weight, weight_dtype, (int)d_out, (int)d_in, s_out, s_in, 1.f, st, gamma)))
       return rc;
-    if ((rc = launch_fold_bias(fb, weight, nullptr, weight_dtype, beta, (int)d_out, (int)d_in, 1, d_out, 1.f, st)))
+    if ((rc = launch_fold_bias(fb, weight, nullptr, weight_dtype, beta, (int)d_out, (int)d_in, s_out, s_in, 1.f, st)))
       return rc;
     if (bias && (rc = launch_add_f32(fb, bias, (int)d_out, st))) return rc;
     switch (d_in) {
@@ -249,11 +348,26 @@ extern "C" int gtk_fused_layernorm_linear(const void* x, void* y, const float* g
   } else {
     bf16* wp;
     carve_ln_linear<bf16>(cv, d_in, d_out, &wp, &fb);
-    if ((rc = launch_pack<bf16>(wp, weight, weight_dtype, (int)d_out, (int)d_in, 1, d_out, 1.f, st, gamma)))
+    if ((rc = launch_pack<bf16>(wp, weight, weight_dtype, (int)d_out, (int)d_in, s_out, s_in, 1.f, st, gamma)))
       return rc;
-    if ((rc = launch_fold_bias(fb, weight, nullptr, weight_dtype, beta, (int)d_out, (int)d_in, 1, d_out, 1.f, st)))
+    if ((rc = launch_fold_bias(fb, weight, nullptr, weight_dtype, beta, (int)d_out, (int)d_in, s_out, s_in, 1.f, st)))
       return rc;
     if (bias && (rc = launch_add_f32(fb, bias, (int)d_out, st))) return rc;
+    // weights and bias resident in LDS when they fit in 64 KiB
+    const int64_t wbytes = packed_elems(d_out, d_in) * 2;
+    const int64_t lds = wbytes + ((d_out + 31) / 32) * 32 * 4;
+    if (lds <= 64 * 1024) {
+      const int64_t ntiles = (rows + 31) / 32;
+      StageTimer timer("ln_linear", st);
+      const unsigned pgrid = (unsigned)std::min<int64_t>(2 * (int64_t)device_cus(), (ntiles + 7) / 8);
+      switch (d_in) {
+        case 64: ln_linear_lds_kernel<64><<<pgrid, 512, lds, st>>>((const bf16*)x, (bf16*)y, wp, fb, rows, (int)d_out, eps, ntiles, (int)wbytes); break;
+        case 128: ln_linear_lds_kernel<128><<<pgrid, 512, lds, st>>>((const bf16*)x, (bf16*)y, wp, fb, rows, (int)d_out, eps, ntiles, (int)wbytes); break;
+        default: ln_linear_lds_kernel<256><<<pgrid, 512, lds, st>>>((const bf16*)x, (bf16*)y, wp, fb, rows, (int)d_out, eps, ntiles, (int)wbytes); break;
+      }
+      GTK_LAUNCH_CHECK();
+      return GTK_OK;
+    }
     switch (d_in) {
       case 64: ln_linear_kernel<bf16, 64><<<grid, 256, 0, st>>>((const bf16*)x, (bf16*)y, wp, fb, rows, (int)d_out, eps); break;
       case 128: ln_linear_kernel<bf16, 128><<<grid, 256, 0, st>>>((const bf16*)x, (bf16*)y, wp, fb, rows, (int)d_out, eps); break;

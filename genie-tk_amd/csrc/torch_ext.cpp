@@ -59,16 +59,22 @@ at::Tensor layernorm(const at::Tensor& x, const at::Tensor& gamma, const at::Ten
   return y;
 }
 
-at::Tensor fused_layernorm_linear(const at::Tensor& x, const at::Tensor& gamma,
-                                  const at::Tensor& beta, const at::Tensor& weight,
-                                  const c10::optional<at::Tensor>& bias, double eps) {
+// LayerNorm + Linear over the last dimension of x; weight [D_IN, D_OUT]
+// (layout GTK_W_IN_OUT, the reference's operator) or [D_OUT, D_IN]
+// (GTK_W_OUT_IN, nn.Linear.weight).
+static at::Tensor layernorm_linear_impl(const at::Tensor& x, const at::Tensor& gamma,
+                                        const at::Tensor& beta, const at::Tensor& weight,
+                                        const c10::optional<at::Tensor>& bias, double eps,
+                                        int layout) {
   check_gpu(x, "x");
   check_gpu(weight, "weight");
   const at::DeviceGuard guard(x.device());
   auto xc = x.contiguous();
   const int64_t d_in = xc.size(-1);
-  TORCH_CHECK(weight.dim() == 2 && weight.size(0) == d_in, "weight must be [D_IN, D_OUT]");
-  const int64_t d_out = weight.size(1);
+  const int in_dim = layout == GTK_W_IN_OUT ? 0 : 1;
+  TORCH_CHECK(weight.dim() == 2 && weight.size(in_dim) == d_in,
+              layout == GTK_W_IN_OUT ? "weight must be [D_IN, D_OUT]" : "weight must be [D_OUT, D_IN]");
+  const int64_t d_out = weight.size(1 - in_dim);
   const int64_t rows = d_in ? xc.numel() / d_in : 0;
   auto g = f32c(gamma), b = f32c(beta);
   TORCH_CHECK(g.numel() == d_in && b.numel() == d_in, "gamma/beta must have ", d_in, " elements");
@@ -83,12 +89,23 @@ at::Tensor fused_layernorm_linear(const at::Tensor& x, const at::Tensor& gamma,
   auto y = at::empty(sizes, xc.options());
   const int dt = gtk_dtype_of(xc, "x");
   auto ws = workspace(xc, gtk_fused_layernorm_linear_workspace_size(d_in, d_out, dt));
-  check_rc(gtk_fused_layernorm_linear(xc.data_ptr(), y.data_ptr(), g.data_ptr<float>(),
-                                      b.data_ptr<float>(), w.data_ptr(), gtk_dtype_of(w, "weight"),
-                                      bias.has_value() ? bb.data_ptr<float>() : nullptr, rows, d_in,
-                                      d_out, (float)eps, dt, ws.data_ptr(), ws.numel(),
-                                      cur_stream(xc)));
+  check_rc(gtk_layernorm_linear(xc.data_ptr(), y.data_ptr(), g.data_ptr<float>(),
+                                b.data_ptr<float>(), w.data_ptr(), gtk_dtype_of(w, "weight"), layout,
+                                bias.has_value() ? bb.data_ptr<float>() : nullptr, rows, d_in, d_out,
+                                (float)eps, dt, ws.data_ptr(), ws.numel(), cur_stream(xc)));
   return y;
+}
+
+at::Tensor fused_layernorm_linear(const at::Tensor& x, const at::Tensor& gamma,
+                                  const at::Tensor& beta, const at::Tensor& weight,
+                                  const c10::optional<at::Tensor>& bias, double eps) {
+  return layernorm_linear_impl(x, gamma, beta, weight, bias, eps, GTK_W_IN_OUT);
+}
+
+at::Tensor layernorm_linear(const at::Tensor& x, const at::Tensor& gamma, const at::Tensor& beta,
+                            const at::Tensor& weight, const c10::optional<at::Tensor>& bias,
+                            double eps) {
+  return layernorm_linear_impl(x, gamma, beta, weight, bias, eps, GTK_W_OUT_IN);
 }
 
 at::Tensor triangle_mul_raw(const at::Tensor& a, const at::Tensor& b, const at::Tensor& mask,
@@ -330,6 +347,10 @@ PYBIND11_MODULE(_C, m) {
   m.def("fused_layernorm_linear", &fused_layernorm_linear, "LayerNorm + Linear forward",
         py::arg("x"), py::arg("gamma"), py::arg("beta"), py::arg("weight"),
         py::arg("bias") = py::none(), py::arg("eps") = 1e-5);
+  m.def("layernorm_linear", &layernorm_linear,
+        "LayerNorm + Linear forward with an nn.Linear-layout weight [D_OUT, D_IN]", py::arg("x"),
+        py::arg("gamma"), py::arg("beta"), py::arg("weight"), py::arg("bias") = py::none(),
+        py::arg("eps") = 1e-5);
   m.def("tri_mul_pack", &tri_mul_pack, "Pack TriangleMultiplicativeUpdate parameters",
         py::arg("params"), py::arg("c_z"), py::arg("c"), py::arg("fp32"));
   m.def("tri_mul_forward", &tri_mul_forward, "Fused TriangleMultiplicativeUpdate forward",

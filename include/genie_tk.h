@@ -70,6 +70,17 @@ int gtk_fused_layernorm_linear(const void* x, void* y, const float* gamma, const
                                int64_t rows, int64_t d_in, int64_t d_out, float eps, int dtype,
                                void* workspace, size_t workspace_bytes, void* stream);
 
+/* The same operator with the weight in either layout: GTK_W_IN_OUT is
+ * [d_in][d_out] (the reference's _C.fused_layernorm_linear), GTK_W_OUT_IN is
+ * [d_out][d_in] (torch.nn.Linear.weight).  The generalisation of the
+ * reference's operator to nn.Linear-layout weights has no reference
+ * counterpart; the arithmetic is the one above.  Same workspace size. */
+enum gtk_weight_layout { GTK_W_IN_OUT = 0, GTK_W_OUT_IN = 1 };
+int gtk_layernorm_linear(const void* x, void* y, const float* gamma, const float* beta,
+                         const void* weight, int weight_dtype, int weight_layout,
+                         const float* bias, int64_t rows, int64_t d_in, int64_t d_out, float eps,
+                         int dtype, void* workspace, size_t workspace_bytes, void* stream);
+
 /* ------------------------------------------------------------------------
  * Triangle contraction on already gated and masked projections.
  * Replaces _C.triangle_mul_outgoing / _C.triangle_mul_incoming(a, b, mask)

@@ -54,6 +54,8 @@ def lib():
                                                   i64, ci, vp, sz, vp]
     L.gtk_fused_layernorm_linear.argtypes = [vp, vp, vp, vp, vp, ci, vp, i64, i64, i64, fp, ci,
                                              vp, sz, vp]
+    L.gtk_layernorm_linear.argtypes = [vp, vp, vp, vp, vp, ci, ci, vp, i64, i64, i64, fp, ci,
+                                       vp, sz, vp]
     L.gtk_timing_report.argtypes = [ctypes.c_char_p, sz]
     return L
 
@@ -127,6 +129,9 @@ def test_bad_dtype_and_shapes_are_rejected(lib):
     rc = lib.gtk_fused_layernorm_linear(None, None, None, None, None, GTK_F32, None, 4, 96, 8,
                                         1e-5, GTK_F32, None, 0, None)
     assert rc == GTK_EUNSUPPORTED
+    rc = lib.gtk_layernorm_linear(None, None, None, None, None, GTK_F32, 2, None, 4, 128, 8,
+                                  1e-5, GTK_F32, None, 0, None)
+    assert rc == GTK_EINVAL and "layout" in _err(lib)
 
 
 def test_empty_inputs_are_no_ops(lib):

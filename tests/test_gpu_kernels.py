@@ -65,6 +65,41 @@ def test_fused_layernorm_linear(dname, d_in, d_out):
     chk(to_np(y0), ref - bias, "fused_layernorm_linear (no bias)")
 
 
+@pytest.mark.parametrize("dname", ["fp32", "bf16"])
+@pytest.mark.parametrize("d_in,d_out", [(128, 128), (64, 30), (256, 4)])
+def test_layernorm_linear_nn_layout(dname, d_in, d_out):
+    """The generalised operator: nn.Linear-layout weight [d_out, d_in], a 4-D
+    input with a ragged row count, against the same LN-then-matmul oracle and
+    against the reference-layout operator given the transposed weight."""
+    log(f"layernorm_linear (nn layout) {dname} {d_in}->{d_out}")
+    rng = np.random.default_rng(7 * d_in + d_out)
+    x = rng.standard_normal((2, 3, 41, d_in)).astype(np.float32) * 1.5 - 0.3
+    w = (1 + 0.2 * rng.standard_normal(d_in)).astype(np.float32)
+    b = (0.2 * rng.standard_normal(d_in)).astype(np.float32)
+    Wnn = (rng.standard_normal((d_out, d_in)) / np.sqrt(d_in)).astype(np.float32)
+    bias = rng.standard_normal(d_out).astype(np.float32)
+    if dname == "bf16":
+        x, Wnn = H.bf16_round(x), H.bf16_round(Wnn)
+    args = (_dev(w, torch.float32), _dev(b, torch.float32))
+    y = ext().layernorm_linear(_dev(x, DT[dname]), *args, _dev(Wnn, DT[dname]), _dev(bias, torch.float32), 1e-5)
+    y_ref_layout = ext().fused_layernorm_linear(_dev(x, DT[dname]), *args,
+                                                _dev(np.ascontiguousarray(Wnn.T), DT[dname]),
+                                                _dev(bias, torch.float32), 1e-5)
+    torch.cuda.synchronize()
+    assert y.shape == (2, 3, 41, d_out) and y.dtype == DT[dname]
+    ln = pair_ops.layer_norm(x.astype(np.float64), w, b, 1e-5)
+    if dname == "bf16":
+        ln = H.bf16_round(ln.astype(np.float32)).astype(np.float64)
+    ref = ln @ Wnn.T.astype(np.float64) + bias
+    chk = check_fp32 if dname == "fp32" else check_bf16
+    chk(to_np(y), ref, "layernorm_linear (nn layout)")
+    # the two layouts pack the same logical weight: identical results
+    assert torch.equal(y, y_ref_layout)
+    if d_in != d_out:  # a reference-layout weight is rejected by the nn-layout operator
+        with pytest.raises(RuntimeError):
+            ext().layernorm_linear(_dev(x, DT[dname]), *args, _dev(Wnn.T.copy(), DT[dname]), None, 1e-5)
+
+
 # ------------------------------------------------------- raw contraction
 @pytest.mark.parametrize("dname", ["fp32", "bf16"])
 @pytest.mark.parametrize("outgoing", [True, False])
