@@ -290,7 +290,7 @@ at::Tensor tri_attn_pack(std::vector<at::Tensor> ps, int64_t c_in, int64_t c_h, 
 
 at::Tensor tri_attn_forward(const at::Tensor& x, const c10::optional<at::Tensor>& mask,
                             const at::Tensor& packed, int64_t c_in, int64_t c_h, int64_t H,
-                            bool starting, bool residual, double eps) {
+                            bool starting, bool residual, double eps, int64_t chunk_rows) {
   check_gpu(x, "x");
   const at::DeviceGuard guard(x.device());
   TORCH_CHECK(x.dim() == 4 && x.size(1) == x.size(2) && x.size(3) == c_in, "x must be [B, N, N, c_in]");
@@ -303,11 +303,11 @@ at::Tensor tri_attn_forward(const at::Tensor& x, const c10::optional<at::Tensor>
   }
   const int dt = gtk_dtype_of(xc, "x");
   auto out = at::empty_like(xc);
-  auto ws = workspace(xc, gtk_tri_attn_workspace_size(B, N, c_in, c_h, H, dt));
-  check_rc(gtk_tri_attn_forward(xc.data_ptr(), mask.has_value() ? mc.data_ptr<float>() : nullptr,
-                                out.data_ptr(), packed.data_ptr(), B, N, c_in, c_h, H,
-                                starting ? 1 : 0, residual ? 1 : 0, (float)eps, dt, ws.data_ptr(),
-                                ws.numel(), cur_stream(xc)));
+  auto ws = workspace(xc, gtk_tri_attn_workspace_size_chunked(B, N, c_in, c_h, H, chunk_rows, dt));
+  check_rc(gtk_tri_attn_forward_chunked(
+      xc.data_ptr(), mask.has_value() ? mc.data_ptr<float>() : nullptr, out.data_ptr(),
+      packed.data_ptr(), B, N, c_in, c_h, H, starting ? 1 : 0, residual ? 1 : 0, (float)eps,
+      chunk_rows, dt, ws.data_ptr(), ws.numel(), cur_stream(xc)));
   return out;
 }
 
@@ -367,7 +367,8 @@ PYBIND11_MODULE(_C, m) {
         py::arg("c_in"), py::arg("c_h"), py::arg("no_heads"), py::arg("fp32"));
   m.def("tri_attn_forward", &tri_attn_forward, "Fused TriangleAttention forward", py::arg("x"),
         py::arg("mask"), py::arg("packed"), py::arg("c_in"), py::arg("c_h"), py::arg("no_heads"),
-        py::arg("starting"), py::arg("residual") = false, py::arg("eps") = 1e-5);
+        py::arg("starting"), py::arg("residual") = false, py::arg("eps") = 1e-5,
+        py::arg("chunk_rows") = 0);
   m.def("version", []() { return gtk_version(); });
   m.def("timing_enable", [](bool on) { check_rc(gtk_timing_enable(on ? 1 : 0)); },
         "Record HIP events around every kernel launch (per-kernel timing)", py::arg("on"));

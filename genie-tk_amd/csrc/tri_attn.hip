@@ -29,6 +29,7 @@
 // valid key attends uniformly over all N keys: that is what the reference's
 // additive -1e9 bias produces in fp32 (every logit rounds to -1e9).
 #include <algorithm>
+#include <type_traits>
 
 #include "capi_util.hpp"
 #include "common.hpp"
@@ -72,6 +73,13 @@ static TriAttnPacked<T> carve_triattn(Carve& cv, int cin, int ch, int H) {
 
 template <typename T> struct AttnWs {
   T *q, *k, *vt, *gate, *bias;
+  // q, k, v^T and the gate hold `rows` rows per batch element, from absolute
+  // row r0 on: all Np rows from 0, or one chunk of rows (chunked attention).
+  // The bias always holds every row.  (The fp32 and raw-op kernels use the
+  // full layout only.)
+  int64_t rows;
+  int r0;
+  __host__ __device__ int64_t row(int b, int r) const { return (int64_t)b * rows + (r - r0); }
 };
 
 // Rows and positions are padded to a multiple of the flash kernel's query block.
@@ -85,14 +93,17 @@ __host__ __device__ __forceinline__ int vt_pos(int j) {
   return (j & ~15) | (j & 3) | ((j & 4) << 1) | ((j & 8) >> 1);
 }
 
+// rows = 0: every row (Np); otherwise a chunk of that many rows.
 template <typename T>
-static AttnWs<T> carve_attn_ws(Carve& cv, int64_t B, int64_t Np, int H, int ch) {
+static AttnWs<T> carve_attn_ws(Carve& cv, int64_t B, int64_t Np, int H, int ch, int64_t rows = 0) {
   AttnWs<T> w;
-  const int64_t qkv = B * Np * H * Np * HD;
+  w.rows = rows > 0 ? rows : Np;
+  w.r0 = 0;
+  const int64_t qkv = B * w.rows * H * Np * HD;
   w.q = cv.take<T>(qkv);
   w.k = cv.take<T>(qkv);
   w.vt = cv.take<T>(qkv);
-  w.gate = cv.take<T>(ch > 0 ? B * Np * Np * ch : 0);
+  w.gate = cv.take<T>(ch > 0 ? B * w.rows * Np * ch : 0);
   w.bias = cv.take<T>(B * H * Np * Np);
   return w;
 }
@@ -198,10 +209,13 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
 //        gate  [B][Np r][c_h][Np j]        bias [B][H][Np q][Np k]
 //     Padding values are those of triattn_prologue_kernel.
 // ---------------------------------------------------------------------------
-template <int CIN, int H>
+// MODE bit 0: q, k, v^T and gate; bit 1: the triangle bias.  The tiles cover
+// rows r0 .. r0 + nrows - 1 of every batch element: [B][nrows][Np / 32].
+template <int CIN, int H, int MODE>
 __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
     const bf16* __restrict__ x, TriAttnPacked<bf16> w, AttnWs<bf16> ws, int N, int Np,
-    int starting, float eps, int64_t ntiles) {
+    int starting, float eps, int64_t ntiles, int r0, int nrows) {
+  static_assert(MODE >= 1 && MODE <= 3, "q/k/v/gate, bias, or both");
   constexpr int CH = H * HD;
   constexpr int KCH = CIN / 16;
   constexpr int PE = (CH / 32) * KCH * 512;  // one packed c_in -> c_h projection
@@ -237,12 +251,13 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
   const int64_t tstride = (int64_t)gridDim.x * 16;
   int64_t tile = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 6);
   TileWalk tw;
-  tw.init(tile, tstride, Np, vtiles);
+  tw.init(tile, tstride, nrows, vtiles);  // row r0 + tw.r
   // (exists = false: a tile past the end, also read as pair 0)
   auto load_rows = [&](Frag<bf16>* raw, const TileWalk& t, bool exists) {
     const int jo = t.c * 32 + prow;
-    const bool ok = exists && t.r < N && jo < N;
-    const int p = starting ? t.r : jo, q = starting ? jo : t.r;
+    const int tr = r0 + t.r;
+    const bool ok = exists && tr < N && jo < N;
+    const int p = starting ? tr : jo, q = starting ? jo : tr;
     const bf16* src = x + (ok ? (((int64_t)t.b * N + p) * N + q) * CIN : 0) + half * (CIN / 2);
 #pragma unroll
     for (int ch = 0; ch < KCH; ++ch) raw[ch].load(src + ch * 8);
@@ -254,7 +269,7 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
   // after them instead of waiting for them.
   auto body = [&](const int64_t tile) {
     const int vt = tw.c;
-    const int r = tw.r;  // destination row
+    const int r = r0 + tw.r;  // destination row
     const int b = tw.b;
     const int jown = vt * 32 + prow;            // this lane's pair (A/B operand side)
     Frag<bf16> xf[KCH];
@@ -269,7 +284,7 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
       nx.next();
       load_rows(raw, nx, tile + tstride < ntiles);
     }
-    const int64_t rowbase = (int64_t)b * Np + r;
+    const int64_t rowbase = ws.row(b, r);  // q/k/v^T/gate row in the workspace
     const int j0 = vt * 32 + 16 * half;         // first of this lane's 16 positions
     // validity of the 16 positions j0 + jj, as a bit mask
     const int nvalid = r < N ? min(max(N - j0, 0), 16) : 0;
@@ -277,7 +292,7 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
     // q, k, v, gate: one 32-channel tile (one head) per step, one MFMA chain
     // each; lane (i32, half) ends with positions j0 .. j0+15 of channel i32
 #pragma unroll 1
-    for (int step = 0; step < 4 * H; ++step) {
+    for (int step = 0; step < ((MODE & 1) ? 4 * H : 0); ++step) {
       const int kind = step / H;  // 0 q, 1 k, 2 v, 3 gate
       const int h = step % H;
       const bf16* wt = wl + kind * PE;
@@ -315,7 +330,7 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
       o[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
     }
     // triangle bias [b][h][r][j]: lanes with i32 < H hold head i32
-    {
+    if constexpr ((MODE & 2) != 0) {
       const bf16* wb = wl + 4 * PE + opaque_zero();
       Frag<bf16> fb;
       load_wfrag_lds(fb, wb, 0, 0, KCH);
@@ -565,7 +580,8 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t lin, int64_t total) {
 template <int CIN, int H, int QT>
 __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))) void triattn_flash_kernel(
     const bf16* __restrict__ x, const float* __restrict__ mask, bf16* __restrict__ out,
-    TriAttnPacked<bf16> w, AttnWs<bf16> ws, int N, int Np, int starting, int residual) {
+    TriAttnPacked<bf16> w, AttnWs<bf16> ws, int N, int Np, int starting, int residual, int r0,
+    int nrows) {
   constexpr int CH = H * HD;
   constexpr int QB = 32 * QT;              // queries per block (QT query tiles per head)
   constexpr int NW = H * QT;               // waves
@@ -597,11 +613,12 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
   const int qblocks = (N + QB - 1) / QB;
   // XCD-aware order: the query blocks of one row run back to back on one XCD
   const int64_t lin = xcd_remap(blockIdx.x, gridDim.x);
+  // blocks cover rows r0 .. r0 + nrows - 1 of every batch element
   const int qb = (int)(lin % qblocks);
-  const int r = (int)((lin / qblocks) % N);
-  const int b = (int)(lin / ((int64_t)qblocks * N));
+  const int r = r0 + (int)((lin / qblocks) % nrows);
+  const int b = (int)(lin / ((int64_t)qblocks * nrows));
   const int q0 = qb * QB + qt * 32;
-  const int64_t rowbase = (int64_t)b * Np + r;
+  const int64_t rowbase = ws.row(b, r);  // q/k/v^T/gate row in the workspace
 
   // mask of this row: key k is pair (r, k) (starting) or (k, r) (ending)
   const float* mrow = mask ? mask + (int64_t)b * N * N + (starting ? (int64_t)r * N : r) : nullptr;
@@ -1057,41 +1074,74 @@ static int pack_triattn(const gtk_tri_attn_weights* w, int cin, int ch, int H, v
   return GTK_OK;
 }
 
+// chunk_rows > 0 (bf16 only): attention rows in chunks of that many rows.
+// The triangle bias needs every pair, so it is computed first over all rows;
+// then q, k, v^T and the gate of one chunk of rows are computed and attended
+// before the next chunk, in a workspace of chunk_rows rows.  Each row's
+// attention reads only its own q, k, v^T and gate rows, so the result is the
+// same as without chunks.
 template <typename T, int CIN, int H>
 static int fwd_triattn(const void* x, const float* mask, void* out, const void* packed, int64_t B,
-                       int64_t N, int starting, int residual, float eps, void* ws, hipStream_t st) {
+                       int64_t N, int starting, int residual, float eps, int64_t chunk_rows,
+                       void* ws, hipStream_t st) {
   constexpr int CH = H * HD;
   Carve pc((void*)packed, SIZE_MAX);
   TriAttnPacked<T> w = carve_triattn<T>(pc, CIN, CH, H);
   const int Np = (int)attn_pad(N);
+  const bool chunked = sizeof(T) == 2 && chunk_rows > 0 && chunk_rows < N;
   Carve cv(ws, SIZE_MAX);
-  AttnWs<T> a = carve_attn_ws<T>(cv, B, Np, H, CH);
-  const int64_t ptiles = B * (int64_t)Np * (Np / 32);
-  if constexpr (sizeof(T) == 2) {
-    const int grid = (int)std::min<int64_t>(device_cus(), (ptiles + 15) / 16);
-    StageTimer timer("triattn_prologue", st);
-    triattn_prologue_bf16_kernel<CIN, H><<<grid, 1024, 0, st>>>(
-        (const bf16*)x, w, a, (int)N, Np, starting, eps, ptiles);
-  } else {
-    StageTimer timer("triattn_prologue", st);
-    triattn_prologue_kernel<T, CIN, H><<<(unsigned)((ptiles + 3) / 4), 256, 0, st>>>(
-        (const T*)x, w, a, (int)B, (int)N, Np, starting, eps);
-  }
-  GTK_LAUNCH_CHECK();
+  AttnWs<T> a = carve_attn_ws<T>(cv, B, Np, H, CH, chunked ? chunk_rows : 0);
   const int64_t blocks = B * N * ((N + 31) / 32);
   GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "attention grid too large");
   if constexpr (sizeof(T) == 2) {
     constexpr int QT = 2;  // two 8-wave blocks of 64 queries per CU
-    const int64_t fblocks = B * N * ((N + 32 * QT - 1) / (32 * QT));
-    StageTimer timer("triattn_flash", st);
-    triattn_flash_kernel<CIN, H, QT><<<(unsigned)fblocks, 64 * H * QT, 0, st>>>(
-        (const bf16*)x, mask, (bf16*)out, w, a, (int)N, Np, starting, residual);
+    auto prologue = [&](auto mode, int r0, int nrows) {
+      constexpr int MODE = decltype(mode)::value;
+      const int64_t ptiles = B * (int64_t)nrows * (Np / 32);
+      const int grid = (int)std::min<int64_t>(device_cus(), (ptiles + 15) / 16);
+      StageTimer timer("triattn_prologue", st);
+      triattn_prologue_bf16_kernel<CIN, H, MODE><<<grid, 1024, 0, st>>>(
+          (const bf16*)x, w, a, (int)N, Np, starting, eps, ptiles, r0, nrows);
+    };
+    auto flash = [&](int r0, int nrows) {
+      const int64_t fblocks = B * nrows * ((N + 32 * QT - 1) / (32 * QT));
+      StageTimer timer("triattn_flash", st);
+      triattn_flash_kernel<CIN, H, QT><<<(unsigned)fblocks, 64 * H * QT, 0, st>>>(
+          (const bf16*)x, mask, (bf16*)out, w, a, (int)N, Np, starting, residual, r0, nrows);
+    };
+    if (!chunked) {
+      prologue(std::integral_constant<int, 3>(), 0, Np);  // every row, padding included
+      GTK_LAUNCH_CHECK();
+      flash(0, (int)N);
+      GTK_LAUNCH_CHECK();
+    } else {
+      // the bias over every row (padding rows and columns are written as zero)
+      prologue(std::integral_constant<int, 2>(), 0, Np);
+      GTK_LAUNCH_CHECK();
+      for (int64_t r0 = 0; r0 < N; r0 += chunk_rows) {
+        const int nrows = (int)std::min<int64_t>(chunk_rows, N - r0);
+        a.r0 = (int)r0;
+        prologue(std::integral_constant<int, 1>(), (int)r0, nrows);
+        GTK_LAUNCH_CHECK();
+        flash((int)r0, nrows);
+        GTK_LAUNCH_CHECK();
+      }
+    }
   } else {
-    StageTimer timer("triattn_flash", st);
-    triattn_fused_kernel<T, CIN, H><<<(unsigned)blocks, 64 * H, 0, st>>>(
-        (const T*)x, mask, (T*)out, w, a, (int)B, (int)N, Np, starting, residual);
+    const int64_t ptiles = B * (int64_t)Np * (Np / 32);
+    {
+      StageTimer timer("triattn_prologue", st);
+      triattn_prologue_kernel<T, CIN, H><<<(unsigned)((ptiles + 3) / 4), 256, 0, st>>>(
+          (const T*)x, w, a, (int)B, (int)N, Np, starting, eps);
+    }
+    GTK_LAUNCH_CHECK();
+    {
+      StageTimer timer("triattn_flash", st);
+      triattn_fused_kernel<T, CIN, H><<<(unsigned)blocks, 64 * H, 0, st>>>(
+          (const T*)x, mask, (T*)out, w, a, (int)B, (int)N, Np, starting, residual);
+    }
+    GTK_LAUNCH_CHECK();
   }
-  GTK_LAUNCH_CHECK();
   return GTK_OK;
 }
 
@@ -1155,30 +1205,52 @@ extern "C" int gtk_tri_attn_pack(const gtk_tri_attn_weights* w, int64_t c_in, in
   return pack_triattn<bf16>(w, (int)c_in, (int)c_h, (int)H, packed, st);
 }
 
+extern "C" size_t gtk_tri_attn_workspace_size_chunked(int64_t B, int64_t N, int64_t c_in,
+                                                      int64_t c_h, int64_t H, int64_t chunk_rows,
+                                                      int dtype) {
+  if (!triattn_shape_ok(c_in, c_h, H) || B < 0 || N < 0 || chunk_rows < 0) return 0;
+  if (chunk_rows > 0 && dtype != GTK_BF16) return 0;
+  Carve cv(nullptr, SIZE_MAX);
+  const int64_t rows = chunk_rows > 0 && chunk_rows < N ? chunk_rows : 0;
+  if (dtype == GTK_F32) carve_attn_ws<float>(cv, B, attn_pad(N), (int)H, (int)c_h);
+  else carve_attn_ws<bf16>(cv, B, attn_pad(N), (int)H, (int)c_h, rows);
+  return cv.off;
+}
+
 extern "C" size_t gtk_tri_attn_workspace_size(int64_t B, int64_t N, int64_t c_in, int64_t c_h,
                                               int64_t H, int dtype) {
-  if (!triattn_shape_ok(c_in, c_h, H) || B < 0 || N < 0) return 0;
-  Carve cv(nullptr, SIZE_MAX);
-  if (dtype == GTK_F32) carve_attn_ws<float>(cv, B, attn_pad(N), (int)H, (int)c_h);
-  else carve_attn_ws<bf16>(cv, B, attn_pad(N), (int)H, (int)c_h);
-  return cv.off;
+  return gtk_tri_attn_workspace_size_chunked(B, N, c_in, c_h, H, 0, dtype);
+}
+
+extern "C" int gtk_tri_attn_forward_chunked(const void* x, const float* mask, void* out,
+                                            const void* packed, int64_t B, int64_t N, int64_t c_in,
+                                            int64_t c_h, int64_t H, int starting, int residual,
+                                            float eps, int64_t chunk_rows, int dtype, void* ws,
+                                            size_t ws_bytes, void* stream) {
+  GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL, "gtk_tri_attn_forward: bad dtype %d", dtype);
+  GTK_REQUIRE(triattn_shape_ok(c_in, c_h, H), GTK_EUNSUPPORTED,
+              "gtk_tri_attn_forward: c_in=%lld c_h=%lld H=%lld unsupported (c_in=128, H=4, d=32)",
+              (long long)c_in, (long long)c_h, (long long)H);
+  GTK_REQUIRE(B >= 0 && N >= 0 && N <= 8192 && chunk_rows >= 0, GTK_EINVAL,
+              "gtk_tri_attn_forward: bad shape");
+  GTK_REQUIRE(chunk_rows == 0 || dtype == GTK_BF16, GTK_EUNSUPPORTED,
+              "gtk_tri_attn_forward_chunked: row chunks need bf16");
+  if (B == 0 || N == 0) return GTK_OK;
+  GTK_REQUIRE(x && out && packed && ws, GTK_EINVAL, "gtk_tri_attn_forward: null pointer");
+  const size_t need = gtk_tri_attn_workspace_size_chunked(B, N, c_in, c_h, H, chunk_rows, dtype);
+  GTK_REQUIRE(ws_bytes >= need, GTK_EWORKSPACE, "gtk_tri_attn_forward: workspace %zu < %zu bytes",
+              ws_bytes, need);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == GTK_F32)
+    return fwd_triattn<float, 128, 4>(x, mask, out, packed, B, N, starting, residual, eps, 0, ws, st);
+  return fwd_triattn<bf16, 128, 4>(x, mask, out, packed, B, N, starting, residual, eps, chunk_rows,
+                                   ws, st);
 }
 
 extern "C" int gtk_tri_attn_forward(const void* x, const float* mask, void* out, const void* packed,
                                     int64_t B, int64_t N, int64_t c_in, int64_t c_h, int64_t H,
                                     int starting, int residual, float eps, int dtype, void* ws,
                                     size_t ws_bytes, void* stream) {
-  GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL, "gtk_tri_attn_forward: bad dtype %d", dtype);
-  GTK_REQUIRE(triattn_shape_ok(c_in, c_h, H), GTK_EUNSUPPORTED,
-              "gtk_tri_attn_forward: c_in=%lld c_h=%lld H=%lld unsupported (c_in=128, H=4, d=32)",
-              (long long)c_in, (long long)c_h, (long long)H);
-  GTK_REQUIRE(B >= 0 && N >= 0 && N <= 8192, GTK_EINVAL, "gtk_tri_attn_forward: bad shape");
-  if (B == 0 || N == 0) return GTK_OK;
-  GTK_REQUIRE(x && out && packed && ws, GTK_EINVAL, "gtk_tri_attn_forward: null pointer");
-  const size_t need = gtk_tri_attn_workspace_size(B, N, c_in, c_h, H, dtype);
-  GTK_REQUIRE(ws_bytes >= need, GTK_EWORKSPACE, "gtk_tri_attn_forward: workspace %zu < %zu bytes",
-              ws_bytes, need);
-  hipStream_t st = (hipStream_t)stream;
-  if (dtype == GTK_F32) return fwd_triattn<float, 128, 4>(x, mask, out, packed, B, N, starting, residual, eps, ws, st);
-  return fwd_triattn<bf16, 128, 4>(x, mask, out, packed, B, N, starting, residual, eps, ws, st);
+  return gtk_tri_attn_forward_chunked(x, mask, out, packed, B, N, c_in, c_h, H, starting, residual,
+                                      eps, 0, dtype, ws, ws_bytes, stream);
 }

@@ -56,7 +56,8 @@ class TriangleAttention(nn.Module):
         """[*, I, J, C] normalised input -> [*, H, I, J]."""
         return permute_final_dims(self.linear(x), 2, 0, 1)
 
-    def _forward_pytorch(self, x: Tensor, mask: Optional[Tensor] = None) -> Tensor:
+    def _forward_pytorch(self, x: Tensor, mask: Optional[Tensor] = None,
+                         chunk_size: Optional[int] = None) -> Tensor:
         if mask is None:
             mask = x.new_ones(x.shape[:-1])
         if not self.starting:
@@ -67,7 +68,19 @@ class TriangleAttention(nn.Module):
         mask_bias = (self.inf * (mask - 1))[..., :, None, None, :]
         # [*, 1, H, Q, K]: the same triangle bias for every row
         tri = self._compute_triangle_bias(x).unsqueeze(-4)
-        x = self.mha(q_x=x, k_x=x, v_x=x, biases=[mask_bias, tri])
+        rows = x.shape[-3]
+        if chunk_size is None or chunk_size >= rows:
+            x = self.mha(q_x=x, k_x=x, v_x=x, biases=[mask_bias, tri])
+        else:
+            # rows are independent once the shared triangle bias exists: the
+            # row axis is split and re-joined as chunk_layer does
+            # (utils.py:78-123), bounding the [*, rows, H, Q, K] scores
+            parts = []
+            for s0 in range(0, rows, chunk_size):
+                xs = x[..., s0:s0 + chunk_size, :, :]
+                parts.append(self.mha(q_x=xs, k_x=xs, v_x=xs,
+                                      biases=[mask_bias[..., s0:s0 + chunk_size, :, :, :], tri]))
+            x = torch.cat(parts, dim=-3)
         if not self.starting:
             x = x.transpose(-2, -3)
         return x
@@ -90,13 +103,16 @@ class TriangleAttention(nn.Module):
         return self._packed.get(ps, fp32, self._pack)
 
     def _forward_cuda(self, x: Tensor, mask: Optional[Tensor] = None,
-                      residual: bool = False) -> Tensor:
-        """HIP path; returns the update (plus x when ``residual``)."""
+                      residual: bool = False, chunk_size: Optional[int] = None) -> Tensor:
+        """HIP path; returns the update (plus x when ``residual``).  With
+        ``chunk_size`` (bf16) the attention rows run that many at a time in a
+        workspace of that many rows."""
         C = _ext.require()
         xb, mb, lead = _dispatch.flatten_batch(x, mask)
         packed = self._packed_params(x.dtype == torch.float32)
         out = C.tri_attn_forward(xb, mb, packed, self.c_in, self.c_hidden, self.no_heads,
-                                 self.starting, residual, self.layer_norm.eps)
+                                 self.starting, residual, self.layer_norm.eps,
+                                 int(chunk_size or 0))
         return out.reshape(*lead, *out.shape[1:])
 
     def forward_residual(self, x: Tensor, mask: Optional[Tensor] = None) -> Tensor:
@@ -106,18 +122,28 @@ class TriangleAttention(nn.Module):
             return self._forward_cuda(x, mask, residual=True)
         return x + self.forward(x, mask)
 
-    def forward(self, x: Tensor, mask: Optional[Tensor] = None) -> Tensor:
-        """x: [*, N, N, c_in], mask: [*, N, N] -> update [*, N, N, c_in]."""
+    def forward(self, x: Tensor, mask: Optional[Tensor] = None,
+                chunk_size: Optional[int] = None) -> Tensor:
+        """x: [*, N, N, c_in], mask: [*, N, N] -> update [*, N, N, c_in].
+
+        ``chunk_size`` (an addition to the reference's signature, default off)
+        bounds memory: the attention rows are processed that many at a time,
+        with the same result.  It applies to the bf16 kernel path and the
+        PyTorch path; an fp32 GPU input with ``chunk_size`` runs the PyTorch
+        path."""
+        if chunk_size is not None and chunk_size < 1:
+            raise ValueError(f"chunk_size must be >= 1, got {chunk_size}")
         if x.is_cuda and self._fused_requested:
             if not _CUDA_AVAILABLE:
                 _ext.require()
-            if self.use_fused_kernel and self._kernel_supported(x):
+            if (self.use_fused_kernel and self._kernel_supported(x)
+                    and (chunk_size is None or x.dtype == torch.bfloat16)):
                 if not _dispatch.needs_autograd(x, self):
-                    return self._forward_cuda(x, mask)
+                    return self._forward_cuda(x, mask, chunk_size=chunk_size)
                 _dispatch.warn_once("tri_attn_grad", "genie_tk: gradients requested; "
                                     "TriangleAttention runs its PyTorch path "
                                     "(the HIP kernels are forward-only)")
-        return self._forward_pytorch(x, mask)
+        return self._forward_pytorch(x, mask, chunk_size)
 
 
 class TriangleAttentionStartingNode(TriangleAttention):

@@ -95,6 +95,26 @@ def test_tri_attn_pytorch_path_matches_oracle(cls, starting):
     np.testing.assert_allclose(y, ref, atol=2e-5, rtol=1e-4)
 
 
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("chunk", [1, 3, 4, 10, 64])
+def test_tri_attn_row_chunks_pytorch_path(starting, chunk):
+    """forward(chunk_size=...) attends rows a chunk at a time with the triangle
+    bias of the whole pair map: same values as without chunks (and the oracle)."""
+    P = H.draw_params(H.tri_attn_shapes(32, 16, 2), 6, ln_random=True, bias_random=True)
+    x = H.pair_input(2, 10, 32, seed=6)
+    mask = H.tail_mask(2, 10, [10, 6])
+    cls = TriangleAttentionStartingNode if starting else TriangleAttentionEndingNode
+    mod = _load(cls(c_in=32, c_hidden=16, no_heads=2, use_fused_kernel=False), P)
+    with torch.no_grad():
+        y = mod(torch.from_numpy(x), torch.from_numpy(mask), chunk_size=chunk).numpy()
+        y0 = mod(torch.from_numpy(x), torch.from_numpy(mask)).numpy()
+    np.testing.assert_allclose(y, y0, atol=1e-6, rtol=1e-6)
+    ref = pair_ops.tri_attn(x, mask, P, starting, 2, dtype=np.float64)
+    np.testing.assert_allclose(y, ref, atol=2e-5, rtol=1e-4)
+    with pytest.raises(ValueError):
+        mod(torch.from_numpy(x), chunk_size=0)
+
+
 def test_mask_default_is_all_ones():
     P = H.draw_params(H.tri_mul_shapes(16, 8), 5, bias_random=True)
     mod = _load(TriangleMultiplicationOutgoing(16, 8, use_fused_kernel=False), P)

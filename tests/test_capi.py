@@ -35,13 +35,15 @@ def lib():
     for name in ("gtk_triangle_mul_workspace_size", "gtk_tri_mul_workspace_size",
                  "gtk_tri_mul_packed_size", "gtk_tri_attn_packed_size",
                  "gtk_tri_attn_workspace_size", "gtk_triangle_attention_workspace_size",
-                 "gtk_fused_layernorm_linear_workspace_size"):
+                 "gtk_fused_layernorm_linear_workspace_size",
+                 "gtk_tri_attn_workspace_size_chunked"):
         getattr(L, name).restype = sz
     L.gtk_triangle_mul_workspace_size.argtypes = [i64, i64, i64, ci]
     L.gtk_tri_mul_workspace_size.argtypes = [i64, i64, i64, i64, ci]
     L.gtk_tri_mul_packed_size.argtypes = [i64, i64, ci]
     L.gtk_tri_attn_packed_size.argtypes = [i64, i64, i64, ci]
     L.gtk_tri_attn_workspace_size.argtypes = [i64, i64, i64, i64, i64, ci]
+    L.gtk_tri_attn_workspace_size_chunked.argtypes = [i64, i64, i64, i64, i64, i64, ci]
     L.gtk_triangle_attention_workspace_size.argtypes = [i64, i64, i64, i64, ci]
     L.gtk_fused_layernorm_linear_workspace_size.argtypes = [i64, i64, ci]
     L.gtk_layernorm.argtypes = [vp, vp, vp, vp, i64, i64, fp, ci, vp]
@@ -49,6 +51,8 @@ def lib():
                                       vp, sz, vp]
     L.gtk_tri_attn_forward.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, ci, fp, ci,
                                        vp, sz, vp]
+    L.gtk_tri_attn_forward_chunked.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, ci,
+                                               fp, i64, ci, vp, sz, vp]
     L.gtk_triangle_mul_outgoing.argtypes = [vp, vp, vp, vp, i64, i64, i64, ci, vp, sz, vp]
     L.gtk_triangle_attention_starting.argtypes = [vp, vp, vp, vp, vp, fp, vp, i64, i64, i64,
                                                   i64, ci, vp, sz, vp]
@@ -95,6 +99,15 @@ def test_workspace_sizes(lib):
     ws = lib.gtk_tri_attn_workspace_size(1, 512, 128, 128, 4, GTK_BF16)
     assert ws >= 4 * 512 * 512 * 128 * 2  # q, k, v^T, gate planes at least
     assert lib.gtk_tri_attn_workspace_size(1, 512, 128, 64, 2, GTK_BF16) == 0
+    # row chunks: q, k, v^T and the gate for chunk_rows rows, the triangle
+    # bias for all of them; chunk_rows = 0 or >= N is the unchunked size
+    wc = lambda rows: lib.gtk_tri_attn_workspace_size_chunked(1, 2048, 128, 128, 4, rows, GTK_BF16)
+    full = lib.gtk_tri_attn_workspace_size(1, 2048, 128, 128, 4, GTK_BF16)
+    assert wc(0) == full and wc(2048) == full and wc(4096) == full
+    assert wc(64) < wc(128) < full
+    assert wc(128) - wc(64) == 4 * 64 * 2048 * 128 * 2
+    assert full - wc(128) >= 4 * (2048 - 128) * 2048 * 128 * 2
+    assert lib.gtk_tri_attn_workspace_size_chunked(1, 512, 128, 128, 4, 64, GTK_F32) == 0
     assert lib.gtk_fused_layernorm_linear_workspace_size(128, 256, GTK_BF16) > 0
 
 
@@ -121,6 +134,12 @@ def test_bad_dtype_and_shapes_are_rejected(lib):
     rc = lib.gtk_tri_attn_forward(None, None, None, None, 1, 8, 128, 128, 8, 1, 0, 1e-5,
                                   GTK_BF16, None, 0, None)
     assert rc == GTK_EUNSUPPORTED
+    rc = lib.gtk_tri_attn_forward_chunked(None, None, None, None, 1, 8, 128, 128, 4, 1, 0, 1e-5,
+                                          4, GTK_F32, None, 0, None)
+    assert rc == GTK_EUNSUPPORTED and "bf16" in _err(lib)
+    rc = lib.gtk_tri_attn_forward_chunked(None, None, None, None, 1, 8, 128, 128, 4, 1, 0, 1e-5,
+                                          -1, GTK_BF16, None, 0, None)
+    assert rc == GTK_EINVAL
     rc = lib.gtk_triangle_mul_outgoing(None, None, None, None, 1, 8, 24, GTK_BF16, None, 0, None)
     assert rc == GTK_EUNSUPPORTED and "multiple of 16" in _err(lib)
     rc = lib.gtk_triangle_attention_starting(None, None, None, None, None, 0.2, None, 1, 4, 8,

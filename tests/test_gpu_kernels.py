@@ -203,6 +203,34 @@ def test_tri_attn_module(dname, starting, N):
     chk(to_np(y_nomask), ref_nm, "tri_attn mask=None")
 
 
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("N,chunks", [(45, (16, 7, 1)), (200, (64, 77)), (130, (128, 129))])
+def test_tri_attn_row_chunks(starting, N, chunks):
+    """bf16 forward with chunk_size: rows attended a chunk at a time in a
+    chunk-sized q/k/v^T/gate workspace give exactly the unchunked result
+    (residual on and off, masked keys, chunk sizes that do not divide N)."""
+    log(f"tri_attn row chunks start={starting} N={N} chunks={chunks}")
+    P = H.bf16_params(H.draw_params(H.tri_attn_shapes(128, 128, 4), seed=N + 5,
+                                    ln_random=True, bias_random=True))
+    x = H.bf16_round(H.pair_input(2, N, 128, seed=N + 6))
+    m = H.tail_mask(2, N, [N, N - 9])
+    mod = triattn_module(P, starting, 4, torch.bfloat16)
+    xd, md = _dev(x, torch.bfloat16), _dev(m, torch.bfloat16)
+    with torch.no_grad():
+        full = mod._forward_cuda(xd, md)
+        full_res = mod._forward_cuda(xd, md, residual=True)
+        for c in chunks:
+            y = mod._forward_cuda(xd, md, chunk_size=c)
+            y_res = mod._forward_cuda(xd, md, residual=True, chunk_size=c)
+            y_fwd = mod(xd, md, chunk_size=c)
+            torch.cuda.synchronize()
+            assert torch.equal(y, full), f"chunk {c}: differs from the unchunked output"
+            assert torch.equal(y_res, full_res), f"chunk {c}: residual form differs"
+            assert torch.equal(y_fwd, full), f"chunk {c}: forward(chunk_size) differs"
+    ref = pair_ops.tri_attn(x, m, P, starting, 4, dtype=np.float64)
+    check_bf16(to_np(y), ref, "tri_attn chunked")
+
+
 def test_forward_dispatches_to_hip(monkeypatch):
     """With use_fused_kernel=True, forward() on a GPU tensor under no_grad runs the
     HIP path (the PyTorch path is made to raise)."""
