@@ -281,6 +281,32 @@ def main() -> int:
             del src, dst
     torch.cuda.synchronize()
 
+    # one training step of tri-mul outgoing (forward + backward, gradients of z
+    # and every parameter): on the kernels, and through the PyTorch path's
+    # autograd for comparison (informational)
+    tm = mods["tri_mul_out"]
+    zg = z.detach().clone().requires_grad_(True)
+    dyg = torch.randn_like(z)
+    maskb = mask.to(torch.bfloat16)  # the PyTorch path keeps the mask's dtype
+
+    def fb(fwd):
+        def run():
+            zg.grad = None
+            for p in tm.parameters():
+                p.grad = None
+            fwd(zg, maskb).backward(dyg)
+        return run
+    print("[bench] tri-mul forward+backward", file=sys.stderr, flush=True)
+    fb_ms = statistics.median(event_time_ms(torch, fb(tm), reps))
+    fb_torch_ms = statistics.median(event_time_ms(torch, fb(tm._forward_pytorch), max(3, reps // 4)))
+    C.timing_enable(True)
+    for _ in range(3):
+        fb(tm)()
+    fb_rep = C.timing_report()
+    C.timing_enable(False)
+    del zg, dyg
+    torch.cuda.synchronize()
+
     fm, fa = trimul_flops(N), triattn_flops(N)
     op_flops = {"tri_mul_out": sum(fm.values()), "tri_mul_in": sum(fm.values()),
                 "tri_att_start": sum(fa.values()), "tri_att_end": sum(fa.values())}
@@ -330,6 +356,16 @@ def main() -> int:
         "ms": round(layer_ms, 4), "gflop": round(lf / 1e9, 2),
         "tflops": round(lf / (layer_ms * 1e-3) / 1e12, 2),
         "note": "one PairTransformLayer forward on the kernels, residuals fused (informational)",
+    }
+    fbf = 3 * sum(fm.values())
+    per_op["tri_mul_out_fwd_bwd"] = {
+        "ms": round(fb_ms, 4), "gflop": round(fbf / 1e9, 2),
+        "tflops": round(fbf / (fb_ms * 1e-3) / 1e12, 2),
+        "pytorch_autograd_ms": round(fb_torch_ms, 4),
+        "speedup_vs_pytorch_autograd": round(fb_torch_ms / fb_ms, 2),
+        "stage_ms_per_step": {k: round(v[1] / 3, 4) for k, v in fb_rep.items()},
+        "note": "forward + backward (dz and all parameter gradients) of tri-mul outgoing; gflop "
+                "counts 3x the forward's products (the backward recomputes the forward on top)",
     }
     work = dict(fm)
     work.update(fa)

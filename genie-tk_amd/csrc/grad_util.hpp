@@ -1,0 +1,370 @@
+// Building blocks shared by the backward passes (tri_mul_bwd.hip,
+// tri_attn_bwd.hip).
+//
+// Per-pair quantities that feed a weight gradient are written channel-major:
+// a "CM plane" is [rows][pitch] with element (r, p) = value of channel r at
+// pair p, p = (b*N + i)*N + j over the B*N*N pairs, pitch = that count rounded
+// up to 64 and the tail columns zero.  Over such planes:
+//   * wgrad:   W[m][n] = sum_p G[m][p] X[n][p]   (split over p, fp32 partials)
+//   * rowred:  s[r] = sum_p G[r][p],  d[r] = sum_p G[r][p] X[r][p]
+//   * fold:    dW[m][n] = W[m][n] gamma[n] + s[m] beta[n], the gradient of a
+//     Linear applied to gamma * x_hat + beta when X holds x_hat (the
+//     LayerNorm affine is folded into the packed forward weights, so the
+//     kernels hold x_hat, not the LayerNorm output).
+#pragma once
+#include "capi_util.hpp"
+#include "common.hpp"
+#include "pack.hpp"
+
+namespace gtk {
+
+// Pack W (logical [out][in], strides s_out / s_in) for contraction over K = in
+// with the operand taken from MFMA accumulators (SWAP orientation: lane l
+// holds pair l&31 and outputs 8g + 4(l>>5) + r of each 32-wide tile).  Chunk
+// ks = 2*t + gp, lane half h, element e  <->  k = 32t + 16gp + 8(e>>2) + 4h + (e&3),
+// so fragment gp of tile t is acc_t[8gp .. 8gp+7].
+template <typename Tout, typename Tin>
+__global__ void pack_acc_kernel(Tout* __restrict__ dst, const Tin* __restrict__ src, int out_dim,
+                                int k_dim, int64_t s_out, int64_t s_in, int64_t total) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int kch = k_dim / 16;
+  const int e = idx & 7;
+  const int l = (idx >> 3) & 63;
+  const int64_t rest = idx >> 9;
+  const int ks = (int)(rest % kch);
+  const int nt = (int)(rest / kch);
+  const int k = (ks >> 1) * 32 + 16 * (ks & 1) + 8 * (e >> 2) + 4 * (l >> 5) + (e & 3);
+  const int o = nt * 32 + (l & 31);
+  dst[idx] = cvt<Tout>(o < out_dim ? to_f32(src[o * s_out + k * s_in]) : 0.f);
+}
+
+template <typename Tout>
+inline int launch_pack_acc(Tout* dst, const void* src, int wdtype, int out_dim, int k_dim,
+                           int64_t s_out, int64_t s_in, hipStream_t st) {
+  const int64_t total = packed_elems(out_dim, k_dim);
+  const int blocks = (int)((total + 255) / 256);
+  if (wdtype == GTK_F32)
+    pack_acc_kernel<Tout, float><<<blocks, 256, 0, st>>>(dst, (const float*)src, out_dim, k_dim,
+                                                         s_out, s_in, total);
+  else
+    pack_acc_kernel<Tout, bf16><<<blocks, 256, 0, st>>>(dst, (const bf16*)src, out_dim, k_dim,
+                                                        s_out, s_in, total);
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+// Fragments gp = 0, 1 of an accumulator tile, as the A/B operand of the next
+// product (pairs as columns, the tile's 32 outputs as k).
+template <typename T>
+__device__ __forceinline__ void acc_to_frags(Frag<T>* f, const f32x16& acc) {
+  float v[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) v[e] = acc[e];
+  f[0].set(v);
+  f[1].set(v + 8);
+}
+template <typename T>
+__device__ __forceinline__ void vals_to_frags(Frag<T>* f, const float* v) {
+  f[0].set(v);
+  f[1].set(v + 8);
+}
+
+// out = in^T per [Np][Np] plane, 64x64 tiles through LDS.  Np % 64 == 0.
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_planes_kernel(const T* __restrict__ in,
+                                                               T* __restrict__ out, int Np,
+                                                               int64_t nplanes) {
+  __shared__ T tile[64][65];
+  const int t1 = Np / 64;
+  const int64_t lin = blockIdx.x;
+  const int64_t pl = lin / ((int64_t)t1 * t1);
+  const int rem = (int)(lin % ((int64_t)t1 * t1));
+  const int i0 = (rem / t1) * 64, j0 = (rem % t1) * 64;
+  const int64_t plane = (int64_t)Np * Np;
+  const T* src = in + pl * plane;
+  T* dst = out + pl * plane;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll 4
+  for (int r = ty; r < 64; r += 4) tile[r][tx] = src[(int64_t)(i0 + r) * Np + j0 + tx];
+  __syncthreads();
+#pragma unroll 4
+  for (int r = ty; r < 64; r += 4) dst[(int64_t)(j0 + r) * Np + i0 + tx] = tile[tx][r];
+}
+
+template <typename T>
+inline int launch_transpose_planes(const T* in, T* out, int Np, int64_t nplanes, hipStream_t st) {
+  const int64_t blocks = (int64_t)(Np / 64) * (Np / 64) * nplanes;
+  GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "transpose grid too large");
+  if (blocks == 0) return GTK_OK;
+  transpose_planes_kernel<T><<<(unsigned)blocks, 256, 0, st>>>(in, out, Np, nplanes);
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+// Zero columns [P, pitch) of `rows` CM rows.
+template <typename T>
+__global__ void zero_tail_kernel(T* __restrict__ base, int64_t rows, int64_t pitch, int64_t P) {
+  const int64_t w = pitch - P;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * w) return;
+  base[(idx / w) * pitch + P + idx % w] = cvt<T>(0.f);
+}
+
+template <typename T>
+inline int launch_zero_tail(T* base, int64_t rows, int64_t pitch, int64_t P, hipStream_t st) {
+  const int64_t n = rows * (pitch - P);
+  if (n <= 0) return GTK_OK;
+  zero_tail_kernel<T><<<(unsigned)((n + 255) / 256), 256, 0, st>>>(base, rows, pitch, P);
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Weight-gradient product  part[s][m][n] = sum_{p in chunk s} G[m][p] X[n][p]
+// G: [M][pitch], X: [Nn][pitch] (CM planes, k = p contiguous).  Block: 128 x TN
+// output tile, 4 waves of 64 x TN/2, k staged through LDS in 128-byte rows
+// with double buffering (the contraction kernel's scheme).  Chunk s covers
+// p in [s*kc, min((s+1)*kc, pitch)), kc a multiple of 64.
+// ---------------------------------------------------------------------------
+template <typename T, int TN>
+__global__ __launch_bounds__(256) void wgrad_kernel(const T* __restrict__ G, const T* __restrict__ X,
+                                                    float* __restrict__ part, int M, int Nn,
+                                                    int64_t pitch, int64_t kc, int nsplit) {
+  constexpr int BK = 128 / sizeof(T);
+  constexpr int PITCH = 144;
+  constexpr int ROWS = 128 + TN;
+  constexpr int CPT = ROWS * 8 / 256;  // 16-byte chunks per thread per stage
+  constexpr int EPC = 16 / sizeof(T);
+  constexpr int MBN = TN / 64;         // 32-wide blocks per wave in n
+  __shared__ __attribute__((aligned(16))) char smem[2][ROWS * PITCH];
+
+  const int mtiles = M / 128, ntiles = Nn / TN;
+  const int64_t lin = blockIdx.x;
+  const int s = (int)(lin % nsplit);
+  const int mt = (int)((lin / nsplit) % mtiles);
+  const int ntl = (int)(lin / ((int64_t)nsplit * mtiles));
+  if (ntl >= ntiles) return;
+  const int m0 = mt * 128, n0 = ntl * TN;
+  const int64_t kbeg = (int64_t)s * kc;
+  const int64_t kend = kbeg + kc < pitch ? kbeg + kc : pitch;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * (TN / 2);
+  f32x16 acc[2][MBN];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < MBN; ++y) acc[x][y] = zero16();
+
+  f32x4 rr[CPT];
+  auto gload = [&](int64_t k0) {
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+      const int id = tid + 256 * u;
+      const int row = id >> 3, cc = id & 7;
+      const T* src = row < 128 ? G + (int64_t)(m0 + row) * pitch : X + (int64_t)(n0 + row - 128) * pitch;
+      rr[u] = *reinterpret_cast<const f32x4*>(src + k0 + cc * EPC);
+    }
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < CPT; ++u) {
+      const int id = tid + 256 * u;
+      const int row = id >> 3, cc = id & 7;
+      *reinterpret_cast<f32x4*>(&smem[buf][row * PITCH + cc * 16]) = rr[u];
+    }
+  };
+  if (kbeg < kend) {
+    gload(kbeg);
+    sstore(0);
+  }
+  __syncthreads();
+  int cur = 0;
+  for (int64_t k0 = kbeg; k0 < kend; k0 += BK) {
+    const bool more = k0 + BK < kend;
+    if (more) gload(k0 + BK);
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int koff = (kk * 16 + half * 8) * (int)sizeof(T);
+      Frag<T> fg[2], fx[MBN];
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+        fg[x].load(reinterpret_cast<const T*>(&smem[cur][(wm + 32 * x + (lane & 31)) * PITCH + koff]));
+#pragma unroll
+      for (int y = 0; y < MBN; ++y)
+        fx[y].load(reinterpret_cast<const T*>(&smem[cur][(128 + wn + 32 * y + (lane & 31)) * PITCH + koff]));
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < MBN; ++y) mma(acc[x][y], fx[y], fg[x]);  // rows n, cols m
+    }
+    if (more) sstore(cur ^ 1);
+    __syncthreads();
+    cur ^= 1;
+  }
+  // acc[x][y]: lane holds W[m = m0 + wm + 32x + (l&31)][n = n0 + wn + 32y + 8g + 4h + r]
+  float* out = part + (int64_t)s * M * Nn;
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    const int m = m0 + wm + 32 * x + (lane & 31);
+#pragma unroll
+    for (int y = 0; y < MBN; ++y)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + wn + 32 * y + 8 * g + 4 * half;
+        store4(out + (int64_t)m * Nn + n, acc[x][y][4 * g], acc[x][y][4 * g + 1],
+               acc[x][y][4 * g + 2], acc[x][y][4 * g + 3]);
+      }
+  }
+}
+
+struct WgradPlan {
+  int nsplit;
+  int64_t kc;
+};
+
+inline WgradPlan wgrad_plan(int M, int64_t pitch) {
+  const int mtiles = M / 128;
+  int64_t ns = (512 + mtiles - 1) / mtiles;
+  const int64_t maxs = pitch / 64 > 0 ? pitch / 64 : 1;
+  if (ns > maxs) ns = maxs;
+  if (ns < 1) ns = 1;
+  int64_t kc = round_up((pitch + ns - 1) / ns, 64);
+  ns = (pitch + kc - 1) / kc;
+  return WgradPlan{(int)(ns > 0 ? ns : 1), kc};
+}
+
+inline size_t wgrad_part_floats(int M, int Nn, int64_t pitch) {
+  return (size_t)wgrad_plan(M, pitch).nsplit * M * Nn;
+}
+
+template <typename T>
+inline int launch_wgrad(const T* G, const T* X, float* part, int M, int Nn, int64_t pitch,
+                        hipStream_t st) {
+  GTK_REQUIRE(M % 128 == 0 && (Nn % 128 == 0 || Nn == 64), GTK_EUNSUPPORTED,
+              "weight gradient shape %d x %d unsupported", M, Nn);
+  const WgradPlan pl = wgrad_plan(M, pitch);
+  if (Nn % 128 == 0) {
+    const int64_t blocks = (int64_t)pl.nsplit * (M / 128) * (Nn / 128);
+    wgrad_kernel<T, 128><<<(unsigned)blocks, 256, 0, st>>>(G, X, part, M, Nn, pitch, pl.kc, pl.nsplit);
+  } else {
+    const int64_t blocks = (int64_t)pl.nsplit * (M / 128);
+    wgrad_kernel<T, 64><<<(unsigned)blocks, 256, 0, st>>>(G, X, part, M, Nn, pitch, pl.kc, pl.nsplit);
+  }
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+// dst[(m - m0)][n] = sum_s part[s][m][n] * (gamma ? gamma[n] : 1)
+//                    + (rowsum && beta ? rowsum[m] * beta[n] : 0),  m in [m0, m0 + rows)
+__global__ void wgrad_finish_kernel(const float* __restrict__ part, int nsplit, int M, int Nn,
+                                    int m0, int rows, const float* __restrict__ rowsum,
+                                    const float* __restrict__ gamma, const float* __restrict__ beta,
+                                    float* __restrict__ dst) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * Nn) return;
+  const int m = m0 + idx / Nn, n = idx % Nn;
+  float acc = 0.f;
+  for (int s = 0; s < nsplit; ++s) acc += part[((int64_t)s * M + m) * Nn + n];
+  if (gamma) acc *= gamma[n];
+  if (rowsum && beta) acc += rowsum[m] * beta[n];
+  dst[idx] = acc;
+}
+
+inline int launch_wgrad_finish(const float* part, int M, int Nn, int64_t pitch, int m0, int rows,
+                               const float* rowsum, const float* gamma, const float* beta,
+                               float* dst, hipStream_t st) {
+  if (!dst) return GTK_OK;
+  const int n = rows * Nn;
+  wgrad_finish_kernel<<<(n + 255) / 256, 256, 0, st>>>(part, wgrad_plan(M, pitch).nsplit, M, Nn, m0,
+                                                       rows, rowsum, gamma, beta, dst);
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Row reductions over CM planes: psum[r][s] = sum over segment s of G[r][.],
+// pdot[r][s] = the same of G[r][.] * X[r][.] (X may be null).
+// ---------------------------------------------------------------------------
+constexpr int kRowSegs = 8;
+
+template <typename T>
+__global__ __launch_bounds__(256) void rowred_kernel(const T* __restrict__ G, const T* __restrict__ X,
+                                                     int64_t pitch, int64_t P, float* __restrict__ psum,
+                                                     float* __restrict__ pdot) {
+  __shared__ float red[2][4];
+  const int r = blockIdx.x / kRowSegs, s = blockIdx.x % kRowSegs;
+  const int64_t seg = ((P + kRowSegs - 1) / kRowSegs + 7) / 8 * 8;
+  const int64_t b0 = s * seg;
+  const int64_t b1 = b0 + seg < P ? b0 + seg : P;
+  const T* g = G + (int64_t)r * pitch;
+  const T* x = X ? X + (int64_t)r * pitch : nullptr;
+  float a = 0.f, d = 0.f;
+  for (int64_t p = b0 + 8 * threadIdx.x; p < b1; p += 8 * 256) {
+    Frag<T> fg, fx;
+    fg.load(g + p);  // the row extends to pitch >= P rounded to 8; tail entries are zero
+    if (x) fx.load(x + p);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool in = p + e < b1;
+      const float v = in ? fg.get(e) : 0.f;
+      a += v;
+      if (x) d += v * (in ? fx.get(e) : 0.f);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    a += __shfl_xor(a, o, 64);
+    d += __shfl_xor(d, o, 64);
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    red[0][wave] = a;
+    red[1][wave] = d;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    psum[(int64_t)r * kRowSegs + s] = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+    if (pdot) pdot[(int64_t)r * kRowSegs + s] = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+  }
+}
+
+__global__ void rowred_finish_kernel(const float* __restrict__ part, int rows, float* __restrict__ dst) {
+  const int r = blockIdx.x * blockDim.x + threadIdx.x;
+  if (r >= rows) return;
+  float a = 0.f;
+  for (int s = 0; s < kRowSegs; ++s) a += part[(int64_t)r * kRowSegs + s];
+  dst[r] = a;
+}
+
+// sums[r] (and dots[r] when X is given) for rows [0, rows) of G.
+template <typename T>
+inline int launch_rowred(const T* G, const T* X, int rows, int64_t pitch, int64_t P, float* tmp,
+                         float* sums, float* dots, hipStream_t st) {
+  if (rows == 0) return GTK_OK;
+  float* ps = tmp;
+  float* pd = tmp + (size_t)rows * kRowSegs;
+  rowred_kernel<T><<<rows * kRowSegs, 256, 0, st>>>(G, X, pitch, P, ps, X ? pd : nullptr);
+  GTK_LAUNCH_CHECK();
+  rowred_finish_kernel<<<(rows + 255) / 256, 256, 0, st>>>(ps, rows, sums);
+  GTK_LAUNCH_CHECK();
+  if (X && dots) {
+    rowred_finish_kernel<<<(rows + 255) / 256, 256, 0, st>>>(pd, rows, dots);
+    GTK_LAUNCH_CHECK();
+  }
+  return GTK_OK;
+}
+
+__global__ void copy_f32_kernel(float* __restrict__ dst, const float* __restrict__ src, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) dst[i] = src[i];
+}
+inline int launch_copy_f32(float* dst, const float* src, int n, hipStream_t st) {
+  if (!dst || n == 0) return GTK_OK;
+  copy_f32_kernel<<<(n + 255) / 256, 256, 0, st>>>(dst, src, n);
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+}  // namespace gtk

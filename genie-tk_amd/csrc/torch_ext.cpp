@@ -205,6 +205,63 @@ at::Tensor tri_mul_pack(std::vector<at::Tensor> ps, int64_t c_z, int64_t c, bool
   return packed;
 }
 
+// Backward of tri_mul_forward (update only): returns [dz, then the gradients of
+// the 16 parameters in tri_mul_pack's order, fp32].
+std::vector<at::Tensor> tri_mul_backward(const at::Tensor& z, const c10::optional<at::Tensor>& mask,
+                                         const at::Tensor& dy, std::vector<at::Tensor> ps,
+                                         int64_t c_z, int64_t c, bool outgoing, double eps_in,
+                                         double eps_out) {
+  TORCH_CHECK(ps.size() == 16, "tri_mul_backward expects 16 parameter tensors");
+  check_gpu(z, "z");
+  check_gpu(ps[2], "weights");
+  const at::DeviceGuard guard(z.device());
+  TORCH_CHECK(z.dim() == 4 && z.size(1) == z.size(2) && z.size(3) == c_z, "z must be [B, N, N, c_z]");
+  TORCH_CHECK(dy.sizes() == z.sizes() && dy.scalar_type() == z.scalar_type(),
+              "dy must match z in shape and dtype");
+  auto zc = z.contiguous();
+  auto dyc = dy.contiguous();
+  const int64_t B = zc.size(0), N = zc.size(1);
+  at::Tensor mc;
+  if (mask.has_value()) {
+    TORCH_CHECK(mask->numel() == B * N * N, "mask must be [B, N, N]");
+    mc = f32c(*mask);
+  }
+  gtk_tri_mul_weights w;
+  w.dtype = common_param_dtype(ps);
+  const void** slots[16] = {&w.ln_in_w, &w.ln_in_b, &w.a_p_w, &w.a_p_b, &w.a_g_w, &w.a_g_b,
+                            &w.b_p_w,   &w.b_p_b,   &w.b_g_w, &w.b_g_b, &w.g_w,   &w.g_b,
+                            &w.ln_out_w, &w.ln_out_b, &w.z_w, &w.z_b};
+  std::vector<at::Tensor> pc(16);
+  for (int i = 0; i < 16; ++i) {
+    if (ps[i].defined()) pc[i] = ps[i].contiguous();
+    *slots[i] = ptr_or_null(pc[i]);
+  }
+  const int dt = gtk_dtype_of(zc, "z");
+  std::vector<at::Tensor> out;
+  out.push_back(at::empty_like(zc));
+  gtk_tri_mul_grads g;
+  float** gs[16] = {&g.ln_in_w, &g.ln_in_b, &g.a_p_w, &g.a_p_b, &g.a_g_w, &g.a_g_b, &g.b_p_w,
+                    &g.b_p_b,   &g.b_g_w,   &g.b_g_b, &g.g_w,   &g.g_b,   &g.ln_out_w,
+                    &g.ln_out_b, &g.z_w,    &g.z_b};
+  const int64_t shapes[16][2] = {{c_z, 1}, {c_z, 1}, {c, c_z}, {c, 1}, {c, c_z}, {c, 1},
+                                 {c, c_z}, {c, 1},   {c, c_z}, {c, 1}, {c_z, c_z}, {c_z, 1},
+                                 {c, 1},   {c, 1},   {c_z, c}, {c_z, 1}};
+  for (int i = 0; i < 16; ++i) {
+    auto t = shapes[i][1] == 1 ? at::empty({shapes[i][0]}, zc.options().dtype(at::kFloat))
+                               : at::empty({shapes[i][0], shapes[i][1]}, zc.options().dtype(at::kFloat));
+    *gs[i] = t.data_ptr<float>();
+    out.push_back(t);
+  }
+  const size_t bytes = gtk_tri_mul_backward_workspace_size(B, N, c_z, c, dt);
+  TORCH_CHECK(bytes > 0, "genie_tk._C: tri_mul backward shape c_z=", c_z, " c=", c, " unsupported");
+  auto ws = workspace(zc, bytes);
+  check_rc(gtk_tri_mul_backward(zc.data_ptr(), mask.has_value() ? mc.data_ptr<float>() : nullptr,
+                                dyc.data_ptr(), &w, out[0].data_ptr(), &g, B, N, c_z, c,
+                                outgoing ? 1 : 0, (float)eps_in, (float)eps_out, dt, ws.data_ptr(),
+                                ws.numel(), cur_stream(zc)));
+  return out;
+}
+
 at::Tensor tri_mul_forward(const at::Tensor& z, const c10::optional<at::Tensor>& mask,
                            const at::Tensor& packed, int64_t c_z, int64_t c, bool outgoing,
                            bool residual, double eps_in, double eps_out) {
@@ -357,6 +414,10 @@ PYBIND11_MODULE(_C, m) {
         py::arg("z"), py::arg("mask"), py::arg("packed"), py::arg("c_z"), py::arg("c"),
         py::arg("outgoing"), py::arg("residual") = false, py::arg("eps_in") = 1e-5,
         py::arg("eps_out") = 1e-5);
+  m.def("tri_mul_backward", &tri_mul_backward,
+        "TriangleMultiplicativeUpdate backward: [dz, 16 parameter gradients (fp32)]",
+        py::arg("z"), py::arg("mask"), py::arg("dy"), py::arg("params"), py::arg("c_z"),
+        py::arg("c"), py::arg("outgoing"), py::arg("eps_in") = 1e-5, py::arg("eps_out") = 1e-5);
   m.def("pair_transition_pack", &pair_transition_pack, "Pack PairTransition parameters",
         py::arg("params"), py::arg("c"), py::arg("n"));
   m.def("pair_transition_forward", &pair_transition_forward,

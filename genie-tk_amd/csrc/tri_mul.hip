@@ -23,40 +23,9 @@
 #include "capi_util.hpp"
 #include "common.hpp"
 #include "pack.hpp"
+#include "tri_mul_internal.hpp"
 
 namespace gtk {
-
-// Packed parameters of one TriangleMultiplicativeUpdate, carved in this order.
-// The weights carry the LayerNorm weights folded in (w_ap..w_g: layer_norm_in,
-// w_z: layer_norm_out) and the biases the LayerNorm biases (b = W beta + c).
-// ln_* keep fp32 copies of the LayerNorm parameters, used only while packing.
-template <typename T> struct TriMulPacked {
-  T *w_ap, *w_ag, *w_bp, *w_bg, *w_g, *w_z;
-  float *b_ap, *b_ag, *b_bp, *b_bg, *b_g, *b_z;
-  float *ln_in_w, *ln_in_b, *ln_out_w, *ln_out_b;
-};
-
-template <typename T>
-static TriMulPacked<T> carve_trimul(Carve& cv, int cz, int c) {
-  TriMulPacked<T> p;
-  p.w_ap = cv.take<T>(packed_elems(c, cz));
-  p.w_ag = cv.take<T>(packed_elems(c, cz));
-  p.w_bp = cv.take<T>(packed_elems(c, cz));
-  p.w_bg = cv.take<T>(packed_elems(c, cz));
-  p.w_g = cv.take<T>(packed_elems(cz, cz));
-  p.w_z = cv.take<T>(packed_elems(cz, c));
-  p.b_ap = cv.take<float>(c);
-  p.b_ag = cv.take<float>(c);
-  p.b_bp = cv.take<float>(c);
-  p.b_bg = cv.take<float>(c);
-  p.b_g = cv.take<float>(cz);
-  p.b_z = cv.take<float>(cz);
-  p.ln_in_w = cv.take<float>(cz);
-  p.ln_in_b = cv.take<float>(cz);
-  p.ln_out_w = cv.take<float>(c);
-  p.ln_out_b = cv.take<float>(c);
-  return p;
-}
 
 // XCD-aware block order: hardware deals consecutive block ids to the 8 XCDs
 // round-robin; remap so that each XCD receives a contiguous range of logical
@@ -951,16 +920,9 @@ static int pack_trimul(const gtk_tri_mul_weights* w, int cz, int c, void* packed
 }
 
 template <typename T, int CZ, int CH>
-static int fwd_trimul(const void* z, const float* mask, void* out, const void* packed, int64_t B,
-                      int64_t N, int outgoing, int residual, float eps_in, float eps_out, void* ws,
-                      hipStream_t st) {
-  Carve pc((void*)packed, SIZE_MAX);
-  TriMulPacked<T> w = carve_trimul<T>(pc, CZ, CH);
-  const int Np = (int)round_up(N, 64);
-  Carve cv(ws, SIZE_MAX);
-  T* pa = cv.take<T>(B * CH * (int64_t)Np * Np);
-  T* pb = cv.take<T>(B * CH * (int64_t)Np * Np);
-  T* px = cv.take<T>(B * CH * (int64_t)Np * Np);
+static int launch_trimul_prologue(const void* z, const float* mask, const TriMulPacked<T>& w, T* pa,
+                                  T* pb, int64_t B, int64_t N, int Np, int outgoing, float eps_in,
+                                  hipStream_t st) {
   const int64_t ptiles = B * (int64_t)Np * (Np / 32);
   if constexpr (sizeof(T) == 2) {
     const int grid = (int)std::min<int64_t>(device_cus(), (ptiles / 2 + 7) / 8);
@@ -973,7 +935,23 @@ static int fwd_trimul(const void* z, const float* mask, void* out, const void* p
         (const T*)z, mask, pa, pb, w, (int)B, (int)N, Np, outgoing, eps_in);
   }
   GTK_LAUNCH_CHECK();
-  int rc = launch_contract<T>(pa, pb, px, Np, B * CH, st);
+  return GTK_OK;
+}
+
+template <typename T, int CZ, int CH>
+static int fwd_trimul(const void* z, const float* mask, void* out, const void* packed, int64_t B,
+                      int64_t N, int outgoing, int residual, float eps_in, float eps_out, void* ws,
+                      hipStream_t st) {
+  Carve pc((void*)packed, SIZE_MAX);
+  TriMulPacked<T> w = carve_trimul<T>(pc, CZ, CH);
+  const int Np = (int)round_up(N, 64);
+  Carve cv(ws, SIZE_MAX);
+  T* pa = cv.take<T>(B * CH * (int64_t)Np * Np);
+  T* pb = cv.take<T>(B * CH * (int64_t)Np * Np);
+  T* px = cv.take<T>(B * CH * (int64_t)Np * Np);
+  int rc = launch_trimul_prologue<T, CZ, CH>(z, mask, w, pa, pb, B, N, Np, outgoing, eps_in, st);
+  if (rc) return rc;
+  rc = launch_contract<T>(pa, pb, px, Np, B * CH, st);
   if (rc) return rc;
   const int64_t etiles = B * N * ((N + 31) / 32);
   if constexpr (sizeof(T) == 2) {
@@ -989,6 +967,37 @@ static int fwd_trimul(const void* z, const float* mask, void* out, const void* p
   }
   GTK_LAUNCH_CHECK();
   return GTK_OK;
+}
+
+template <typename T, int CZ, int CH>
+static int recompute_planes(const void* z, const float* mask, const void* packed, int64_t B,
+                            int64_t N, int outgoing, float eps_in, void* pa, void* pb, void* px,
+                            hipStream_t st) {
+  Carve pc((void*)packed, SIZE_MAX);
+  TriMulPacked<T> w = carve_trimul<T>(pc, CZ, CH);
+  const int Np = (int)round_up(N, 64);
+  int rc = launch_trimul_prologue<T, CZ, CH>(z, mask, w, (T*)pa, (T*)pb, B, N, Np, outgoing,
+                                             eps_in, st);
+  if (rc) return rc;
+  return launch_contract<T>((const T*)pa, (const T*)pb, (T*)px, Np, B * CH, st);
+}
+
+int trimul_recompute_planes(const void* z, const float* mask, const void* packed, int64_t B,
+                            int64_t N, int64_t c_z, int64_t c, int outgoing, float eps_in,
+                            int dtype, void* pa, void* pb, void* px, hipStream_t st) {
+  GTK_REQUIRE(c_z == 128 && (c == 64 || c == 128), GTK_EUNSUPPORTED, "tri-mul shape unsupported");
+  if (dtype == GTK_F32)
+    return c == 128 ? recompute_planes<float, 128, 128>(z, mask, packed, B, N, outgoing, eps_in, pa, pb, px, st)
+                    : recompute_planes<float, 128, 64>(z, mask, packed, B, N, outgoing, eps_in, pa, pb, px, st);
+  return c == 128 ? recompute_planes<bf16, 128, 128>(z, mask, packed, B, N, outgoing, eps_in, pa, pb, px, st)
+                  : recompute_planes<bf16, 128, 64>(z, mask, packed, B, N, outgoing, eps_in, pa, pb, px, st);
+}
+
+int trimul_contract_planes(const void* pl, const void* pr, void* out, int Np, int64_t nplanes,
+                           int dtype, hipStream_t st) {
+  if (dtype == GTK_F32)
+    return launch_contract<float>((const float*)pl, (const float*)pr, (float*)out, Np, nplanes, st);
+  return launch_contract<bf16>((const bf16*)pl, (const bf16*)pr, (bf16*)out, Np, nplanes, st);
 }
 
 }  // namespace gtk

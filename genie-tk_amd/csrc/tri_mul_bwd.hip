@@ -1,0 +1,532 @@
+// Backward of the triangle multiplicative update (outgoing / incoming).
+//
+// The reference computes gradients with torch autograd over its PyTorch path
+// (triangle_mul.py:103-132); this is the same chain rule on the gfx950
+// kernels.  Forward activations are recomputed from z, not stored:
+//
+//  0. pack: the forward's folded weights, and W^T of W_ap, W_ag, W_bp, W_bg,
+//     W_g, W_z (unfolded) in accumulator order for the data gradients.
+//  1. recompute the A, Bm planes and X = A Bm^T (the forward's kernels).
+//  2. epilogue backward, one 32-pair tile per wave:
+//       s = sigmoid(g_pre), p = LN_out(x) W_z^T + b_z,   y = s * p
+//       dp = dy s,  dg_pre = dy p s (1 - s),  dxn = dp W_z
+//       dX = LN_out backward(dxn)            -> dX planes (pair orientation)
+//     and dp, dg_pre, x_hat_out, dxn as CM planes (grad_util.hpp).
+//  3. contraction backward on the matrix cores, per channel plane:
+//       outgoing  dA = dX Bm,       dB = dX^T A
+//       incoming  dA^T = Bm^T dX^T, dB^T = A^T dX       (pair orientation)
+//     as X = L R^T products of transposed planes.
+//  4. prologue backward, one 32-pair tile per wave: the gate algebra of
+//     a = m * a_p * sigmoid(a_g) (and b), dzn = sum of the five d_pre W
+//     products, dz = LN_in backward(dzn); d_pre, x_hat_in, dzn as CM planes.
+//  5. weight gradients: two split-K products over the pairs, row sums for
+//     biases and LayerNorm parameters, folded back through gamma and beta.
+#include <algorithm>
+
+#include "capi_util.hpp"
+#include "common.hpp"
+#include "grad_util.hpp"
+#include "pack.hpp"
+#include "tri_mul_internal.hpp"
+
+namespace gtk {
+
+// ---------------------------------------------------------------------------
+// 2. Epilogue backward.  Tiles cover all Np x Np plane positions so that the
+//    padding of the dX planes is written as zero.
+// ---------------------------------------------------------------------------
+template <typename T, int CZ, int CH>
+__global__ __launch_bounds__(256) void trimul_bwd_epilogue_kernel(
+    const T* __restrict__ z, const T* __restrict__ px, const T* __restrict__ dy,
+    T* __restrict__ pdx, T* __restrict__ cm_dp, T* __restrict__ cm_dg, T* __restrict__ cm_xo,
+    T* __restrict__ cm_dxo, TriMulPacked<T> w, const T* __restrict__ wzt, int B, int N, int Np,
+    int64_t pitch, float eps_in, float eps_out) {
+  constexpr int XPITCH = CH + 8;
+  __shared__ __attribute__((aligned(16))) T xs[4][32 * XPITCH];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int half = lane >> 5;
+  const int t32 = lane & 31;
+  const int jtiles = Np / 32;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave;
+  if (tile >= (int64_t)B * Np * jtiles) return;
+  const int jt = (int)(tile % jtiles);
+  const int i = (int)((tile / jtiles) % Np);
+  const int b = (int)(tile / ((int64_t)jtiles * Np));
+  const int j = jt * 32 + t32;
+  const int64_t plane = (int64_t)Np * Np;
+  T* dxo = pdx + (int64_t)b * CH * plane + (int64_t)i * Np + j;
+  if (i >= N || jt * 32 >= N) {
+    for (int c = half * (CH / 2); c < (half + 1) * (CH / 2); ++c) dxo[(int64_t)c * plane] = cvt<T>(0.f);
+    return;
+  }
+  const bool valid = j < N;
+  const int64_t pair = ((int64_t)b * N + i) * N + (valid ? j : 0);
+
+  // gate s = sigmoid(LN_in(z) W_g^T + b_g), accumulator layout
+  f32x16 sg[CZ / 32];
+  {
+    RowHalf<CZ> rh;
+    load_row_half<T, CZ>(rh, z + pair * CZ, valid);
+    const f32x2 st = row_stats<CZ>(rh, eps_in);
+    Frag<T> xf[CZ / 16];
+    ln_to_frags<T, CZ>(xf, rh, st);
+#pragma unroll
+    for (int nt = 0; nt < CZ / 32; ++nt) {
+      sg[nt] = row_gemm_tile<T, CZ, true>(xf, w.w_g, nt);
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int c = nt * 32 + 8 * g + 4 * half + r;
+          sg[nt][4 * g + r] = gate_from_u(sg[nt][4 * g + r] + w.b_g[c]);
+        }
+    }
+  }
+
+  // x tile X[b][c][i][jt*32 ..] -> LDS [pair][c]
+  T* s = xs[wave];
+  {
+    constexpr int EPC = 16 / sizeof(T);
+    constexpr int CPR = 32 / EPC;
+    const T* xb = px + (int64_t)b * CH * plane + (int64_t)i * Np + jt * 32;
+#pragma unroll 4
+    for (int id = lane; id < CH * CPR; id += 64) {
+      const int c = id / CPR, part = id % CPR;
+      const f32x4 raw = *reinterpret_cast<const f32x4*>(xb + (int64_t)c * plane + part * EPC);
+      const T* e = reinterpret_cast<const T*>(&raw);
+#pragma unroll
+      for (int k = 0; k < EPC; ++k) s[(part * EPC + k) * XPITCH + c] = e[k];
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __builtin_amdgcn_wave_barrier();
+  RowHalf<CH> xh;
+  {
+    const T* sr = s + t32 * XPITCH + half * (CH / 2);
+#pragma unroll
+    for (int ch = 0; ch < CH / 16; ++ch) {
+      Frag<T> f;
+      f.load(sr + ch * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xh.v[ch * 8 + e] = f.get(e);
+    }
+  }
+  const f32x2 so = row_stats<CH>(xh, eps_out);
+  Frag<T> yf[CH / 16];
+  ln_to_frags<T, CH>(yf, xh, so);
+
+  // dp = dy s, dg_pre = dy p s (1 - s)
+  Frag<T> dpf[CZ / 16];
+#pragma unroll
+  for (int nt = 0; nt < CZ / 32; ++nt) {
+    const f32x16 pacc = row_gemm_tile<T, CH, true>(yf, w.w_z, nt);
+    float dpv[16], dgv[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int c0 = nt * 32 + 8 * g + 4 * half;
+      const f32x4 d4 = valid ? load4f(dy + pair * CZ + c0) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float sv = sg[nt][4 * g + r];
+        const float pv = pacc[4 * g + r] + w.b_z[c0 + r];
+        dpv[4 * g + r] = d4[r] * sv;
+        dgv[4 * g + r] = d4[r] * pv * sv * (1.f - sv);
+      }
+    }
+    if (valid) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t o = (int64_t)(nt * 32 + 8 * g + 4 * half + r) * pitch + pair;
+          cm_dp[o] = cvt<T>(dpv[4 * g + r]);
+          cm_dg[o] = cvt<T>(dgv[4 * g + r]);
+        }
+    }
+    vals_to_frags<T>(&dpf[2 * nt], dpv);
+  }
+
+  // dxn = dp W_z  (outputs over c, accumulator layout)
+  f32x16 dxn[CH / 32];
+#pragma unroll
+  for (int nt = 0; nt < CH / 32; ++nt) {
+    dxn[nt] = zero16();
+#pragma unroll
+    for (int ks = 0; ks < CZ / 16; ++ks) {
+      Frag<T> wf;
+      load_wfrag<T>(wf, wzt, nt, ks, CZ / 16);
+      mma(dxn[nt], wf, dpf[ks]);
+    }
+  }
+
+  // LayerNorm backward: x_hat from the LDS tile, dx_hat = gamma * dxn
+  const T* sr = s + t32 * XPITCH;
+  float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int nt = 0; nt < CH / 32; ++nt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int c = nt * 32 + 8 * g + 4 * half + r;
+        const float xhat = (to_f32(sr[c]) - so[0]) * so[1];
+        const float dxh = w.ln_out_w[c] * dxn[nt][4 * g + r];
+        s1 += dxh;
+        s2 += dxh * xhat;
+      }
+  s1 += xor32(s1);
+  s2 += xor32(s2);
+  const float m1 = s1 * (1.0f / CH), m2 = s2 * (1.0f / CH);
+#pragma unroll
+  for (int nt = 0; nt < CH / 32; ++nt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int c = nt * 32 + 8 * g + 4 * half + r;
+        const float xhat = (to_f32(sr[c]) - so[0]) * so[1];
+        const float dxh = w.ln_out_w[c] * dxn[nt][4 * g + r];
+        const float dxv = so[1] * (dxh - m1 - xhat * m2);
+        dxo[(int64_t)c * plane] = cvt<T>(valid ? dxv : 0.f);
+        if (valid) {
+          cm_xo[(int64_t)c * pitch + pair] = cvt<T>(xhat);
+          cm_dxo[(int64_t)c * pitch + pair] = cvt<T>(dxn[nt][4 * g + r]);
+        }
+      }
+}
+
+// ---------------------------------------------------------------------------
+// 4. Prologue backward.  Tiles over valid rows; da/db planes in pair
+//    orientation [b][c][i][j].
+// ---------------------------------------------------------------------------
+template <typename T, int CZ, int CH>
+__global__ __launch_bounds__(256) void trimul_bwd_prologue_kernel(
+    const T* __restrict__ z, const float* __restrict__ mask, const T* __restrict__ pda,
+    const T* __restrict__ pdb, T* __restrict__ dz, T* __restrict__ cm_stack,
+    T* __restrict__ cm_xi, T* __restrict__ cm_dzn, TriMulPacked<T> w, const T* __restrict__ wt,
+    const T* __restrict__ wgt, int B, int N, int Np, int64_t pitch, float eps_in) {
+  constexpr int64_t PE = (CZ / 32) * (CH / 16) * 512;  // packed_elems(CZ, CH)
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int half = lane >> 5;
+  const int t32 = lane & 31;
+  const int jtiles = (N + 31) / 32;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave;
+  if (tile >= (int64_t)B * N * jtiles) return;
+  const int jt = (int)(tile % jtiles);
+  const int i = (int)((tile / jtiles) % N);
+  const int b = (int)(tile / ((int64_t)jtiles * N));
+  const int j = jt * 32 + t32;
+  const bool valid = j < N;
+  const int64_t pair = ((int64_t)b * N + i) * N + (valid ? j : 0);
+  const int64_t plane = (int64_t)Np * Np;
+
+  RowHalf<CZ> rh;
+  load_row_half<T, CZ>(rh, z + pair * CZ, valid);
+  const f32x2 st = row_stats<CZ>(rh, eps_in);
+  Frag<T> xf[CZ / 16];
+  ln_to_frags<T, CZ>(xf, rh, st);
+  const float m = valid ? (mask ? mask[pair] : 1.0f) : 0.0f;
+
+  f32x16 dzn[CZ / 32];
+#pragma unroll
+  for (int nt = 0; nt < CZ / 32; ++nt) dzn[nt] = zero16();
+
+#pragma unroll 1
+  for (int side = 0; side < 2; ++side) {
+    const T* wp = side ? w.w_bp : w.w_ap;
+    const T* wg = side ? w.w_bg : w.w_ag;
+    const float* bp = side ? w.b_bp : w.b_ap;
+    const float* bg = side ? w.b_bg : w.b_ag;
+    const T* src = (side ? pdb : pda) + (int64_t)b * CH * plane + (int64_t)i * Np + j;
+    const T* wtp = wt + (2 * side) * PE;
+    const T* wtg = wt + (2 * side + 1) * PE;
+    T* cm_p = cm_stack + (int64_t)(2 * side) * CH * pitch;
+    T* cm_g = cm_stack + (int64_t)(2 * side + 1) * CH * pitch;
+#pragma unroll 1
+    for (int nt = 0; nt < CH / 32; ++nt) {
+      const f32x16 pre = row_gemm_tile<T, CZ, true>(xf, wp, nt);
+      const f32x16 u = row_gemm_tile<T, CZ, true>(xf, wg, nt);
+      float d_p[16], d_g[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int c = nt * 32 + 8 * g + 4 * half + r;
+          const float v = pre[4 * g + r] + bp[c];
+          const float sv = gate_from_u(u[4 * g + r] + bg[c]);
+          const float d = valid ? to_f32(src[(int64_t)c * plane]) * m : 0.f;
+          d_p[4 * g + r] = d * sv;
+          d_g[4 * g + r] = d * v * sv * (1.f - sv);
+        }
+      if (valid) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int64_t o = (int64_t)(nt * 32 + 8 * g + 4 * half + r) * pitch + pair;
+            cm_p[o] = cvt<T>(d_p[4 * g + r]);
+            cm_g[o] = cvt<T>(d_g[4 * g + r]);
+          }
+      }
+      Frag<T> fp[2], fg[2];
+      vals_to_frags<T>(fp, d_p);
+      vals_to_frags<T>(fg, d_g);
+#pragma unroll
+      for (int nt2 = 0; nt2 < CZ / 32; ++nt2)
+#pragma unroll
+        for (int gp = 0; gp < 2; ++gp) {
+          Frag<T> wf;
+          load_wfrag<T>(wf, wtp, nt2, 2 * nt + gp, CH / 16);
+          mma(dzn[nt2], wf, fp[gp]);
+          load_wfrag<T>(wf, wtg, nt2, 2 * nt + gp, CH / 16);
+          mma(dzn[nt2], wf, fg[gp]);
+        }
+    }
+  }
+  // the output gate's share: dg_pre W_g
+  {
+    const T* cm_dg = cm_stack + (int64_t)4 * CH * pitch;
+#pragma unroll 1
+    for (int nt = 0; nt < CZ / 32; ++nt) {
+      float d[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          d[4 * g + r] = valid ? to_f32(cm_dg[(int64_t)(nt * 32 + 8 * g + 4 * half + r) * pitch + pair]) : 0.f;
+      Frag<T> f[2];
+      vals_to_frags<T>(f, d);
+#pragma unroll
+      for (int nt2 = 0; nt2 < CZ / 32; ++nt2)
+#pragma unroll
+        for (int gp = 0; gp < 2; ++gp) {
+          Frag<T> wf;
+          load_wfrag<T>(wf, wgt, nt2, 2 * nt + gp, CZ / 16);
+          mma(dzn[nt2], wf, f[gp]);
+        }
+    }
+  }
+
+  // LayerNorm backward in accumulator layout
+  float xh[CZ / 2];
+  float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int nt = 0; nt < CZ / 32; ++nt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int c0 = nt * 32 + 8 * g + 4 * half;
+      const f32x4 z4 = valid ? load4f(z + pair * CZ + c0) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float xv = (z4[r] - st[0]) * st[1];
+        xh[16 * nt + 4 * g + r] = xv;
+        const float dxh = w.ln_in_w[c0 + r] * dzn[nt][4 * g + r];
+        s1 += dxh;
+        s2 += dxh * xv;
+      }
+    }
+  s1 += xor32(s1);
+  s2 += xor32(s2);
+  const float m1 = s1 * (1.0f / CZ), m2 = s2 * (1.0f / CZ);
+  if (!valid) return;
+#pragma unroll
+  for (int nt = 0; nt < CZ / 32; ++nt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int c0 = nt * 32 + 8 * g + 4 * half;
+      float o[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float xv = xh[16 * nt + 4 * g + r];
+        const float dxh = w.ln_in_w[c0 + r] * dzn[nt][4 * g + r];
+        o[r] = st[1] * (dxh - m1 - xv * m2);
+        cm_xi[(int64_t)(c0 + r) * pitch + pair] = cvt<T>(xv);
+        cm_dzn[(int64_t)(c0 + r) * pitch + pair] = cvt<T>(dzn[nt][4 * g + r]);
+      }
+      store4(dz + pair * CZ + c0, o[0], o[1], o[2], o[3]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Workspace
+// ---------------------------------------------------------------------------
+template <typename T> struct TriMulBwdWs {
+  void* packed;
+  T *wzt, *wt, *wgt;
+  T *pa, *pb, *px, *pdx, *pat, *pbt, *pda, *pdb;
+  T *cm_stack, *cm_dp, *cm_xi, *cm_xo, *cm_dzn, *cm_dxo;
+  float *part1, *part2, *red, *sums_stack, *sums_dp, *sums_dzn, *dots_dzn, *sums_dxo, *dots_dxo;
+  int64_t pitch;
+};
+
+template <typename T>
+static TriMulBwdWs<T> carve_trimul_bwd(Carve& cv, int64_t B, int64_t N, int cz, int c, int dtype) {
+  TriMulBwdWs<T> w;
+  const int64_t Np = round_up(N, 64);
+  const int64_t P = B * N * N;
+  w.pitch = round_up(P, 64);
+  const int M1 = 4 * c + cz;
+  w.packed = cv.take<char>((int64_t)gtk_tri_mul_packed_size(cz, c, dtype));
+  w.wzt = cv.take<T>(packed_elems(c, cz));
+  w.wt = cv.take<T>(4 * packed_elems(cz, c));
+  w.wgt = cv.take<T>(packed_elems(cz, cz));
+  const int64_t pe = B * c * Np * Np;
+  T** planes[] = {&w.pa, &w.pb, &w.px, &w.pdx, &w.pat, &w.pbt, &w.pda, &w.pdb};
+  for (T** p : planes) *p = cv.take<T>(pe);
+  w.cm_stack = cv.take<T>(M1 * w.pitch);
+  w.cm_dp = cv.take<T>(cz * w.pitch);
+  w.cm_xi = cv.take<T>(cz * w.pitch);
+  w.cm_xo = cv.take<T>(c * w.pitch);
+  w.cm_dzn = cv.take<T>(cz * w.pitch);
+  w.cm_dxo = cv.take<T>(c * w.pitch);
+  w.part1 = cv.take<float>(wgrad_part_floats(M1, cz, w.pitch));
+  w.part2 = cv.take<float>(wgrad_part_floats(cz, c, w.pitch));
+  w.red = cv.take<float>((int64_t)2 * M1 * kRowSegs);
+  w.sums_stack = cv.take<float>(M1);
+  w.sums_dp = cv.take<float>(cz);
+  w.sums_dzn = cv.take<float>(cz);
+  w.dots_dzn = cv.take<float>(cz);
+  w.sums_dxo = cv.take<float>(c);
+  w.dots_dxo = cv.take<float>(c);
+  return w;
+}
+
+template <typename T, int CZ, int CH>
+static int bwd_trimul(const void* z, const float* mask, const void* dy,
+                      const gtk_tri_mul_weights* wts, void* dz, const gtk_tri_mul_grads* gr,
+                      int64_t B, int64_t N, int outgoing, float eps_in, float eps_out, int dtype,
+                      void* ws, hipStream_t st) {
+  Carve cv(ws, SIZE_MAX);
+  TriMulBwdWs<T> a = carve_trimul_bwd<T>(cv, B, N, CZ, CH, dtype);
+  const int Np = (int)round_up(N, 64);
+  const int64_t P = B * N * N, pitch = a.pitch;
+  const int64_t nplanes = B * CH;
+  const int M1 = 4 * CH + CZ;
+  const int wd = wts->dtype;
+  int rc;
+  // 0. weights
+  if ((rc = gtk_tri_mul_pack(wts, CZ, CH, dtype, a.packed, gtk_tri_mul_packed_size(CZ, CH, dtype), st)))
+    return rc;
+  Carve pc(a.packed, SIZE_MAX);
+  TriMulPacked<T> w = carve_trimul<T>(pc, CZ, CH);
+  if ((rc = launch_pack_acc<T>(a.wzt, wts->z_w, wd, CH, CZ, 1, CH, st))) return rc;
+  const void* wsrc[4] = {wts->a_p_w, wts->a_g_w, wts->b_p_w, wts->b_g_w};
+  for (int k = 0; k < 4; ++k)
+    if ((rc = launch_pack_acc<T>(a.wt + k * packed_elems(CZ, CH), wsrc[k], wd, CZ, CH, 1, CZ, st))) return rc;
+  if ((rc = launch_pack_acc<T>(a.wgt, wts->g_w, wd, CZ, CZ, 1, CZ, st))) return rc;
+  // 1. forward planes
+  if ((rc = trimul_recompute_planes(z, mask, a.packed, B, N, CZ, CH, outgoing, eps_in, dtype, a.pa,
+                                    a.pb, a.px, st)))
+    return rc;
+  // 2. epilogue backward
+  {
+    const int64_t tiles = B * (int64_t)Np * (Np / 32);
+    StageTimer timer("trimul_bwd_epilogue", st);
+    trimul_bwd_epilogue_kernel<T, CZ, CH><<<(unsigned)((tiles + 3) / 4), 256, 0, st>>>(
+        (const T*)z, a.px, (const T*)dy, a.pdx, a.cm_dp, a.cm_stack + (int64_t)4 * CH * pitch,
+        a.cm_xo, a.cm_dxo, w, a.wzt, (int)B, (int)N, Np, pitch, eps_in, eps_out);
+    GTK_LAUNCH_CHECK();
+  }
+  // 3. contraction backward (px is free from here on: it takes dX^T)
+  T* pdxt = a.px;
+  if ((rc = launch_transpose_planes<T>(a.pa, a.pat, Np, nplanes, st))) return rc;
+  if ((rc = launch_transpose_planes<T>(a.pb, a.pbt, Np, nplanes, st))) return rc;
+  if ((rc = launch_transpose_planes<T>(a.pdx, pdxt, Np, nplanes, st))) return rc;
+  if (outgoing) {
+    if ((rc = trimul_contract_planes(a.pdx, a.pbt, a.pda, Np, nplanes, dtype, st))) return rc;
+    if ((rc = trimul_contract_planes(pdxt, a.pat, a.pdb, Np, nplanes, dtype, st))) return rc;
+  } else {
+    if ((rc = trimul_contract_planes(a.pbt, a.pdx, a.pda, Np, nplanes, dtype, st))) return rc;
+    if ((rc = trimul_contract_planes(a.pat, pdxt, a.pdb, Np, nplanes, dtype, st))) return rc;
+  }
+  // 4. prologue backward
+  {
+    const int64_t tiles = B * N * ((N + 31) / 32);
+    StageTimer timer("trimul_bwd_prologue", st);
+    trimul_bwd_prologue_kernel<T, CZ, CH><<<(unsigned)((tiles + 3) / 4), 256, 0, st>>>(
+        (const T*)z, mask, a.pda, a.pdb, (T*)dz, a.cm_stack, a.cm_xi, a.cm_dzn, w, a.wt, a.wgt,
+        (int)B, (int)N, Np, pitch, eps_in);
+    GTK_LAUNCH_CHECK();
+  }
+  // 5. weight gradients
+  if ((rc = launch_zero_tail<T>(a.cm_stack, M1, pitch, P, st))) return rc;
+  if ((rc = launch_zero_tail<T>(a.cm_dp, CZ, pitch, P, st))) return rc;
+  if ((rc = launch_zero_tail<T>(a.cm_xi, CZ, pitch, P, st))) return rc;
+  if ((rc = launch_zero_tail<T>(a.cm_xo, CH, pitch, P, st))) return rc;
+  if ((rc = launch_rowred<T>(a.cm_stack, nullptr, M1, pitch, P, a.red, a.sums_stack, nullptr, st))) return rc;
+  if ((rc = launch_rowred<T>(a.cm_dp, nullptr, CZ, pitch, P, a.red, a.sums_dp, nullptr, st))) return rc;
+  if ((rc = launch_rowred<T>(a.cm_dzn, a.cm_xi, CZ, pitch, P, a.red, a.sums_dzn, a.dots_dzn, st))) return rc;
+  if ((rc = launch_rowred<T>(a.cm_dxo, a.cm_xo, CH, pitch, P, a.red, a.sums_dxo, a.dots_dxo, st))) return rc;
+  {
+    StageTimer timer("trimul_bwd_wgrad", st);
+    if ((rc = launch_wgrad<T>(a.cm_stack, a.cm_xi, a.part1, M1, CZ, pitch, st))) return rc;
+    if ((rc = launch_wgrad<T>(a.cm_dp, a.cm_xo, a.part2, CZ, CH, pitch, st))) return rc;
+  }
+  float* wdst[5] = {gr->a_p_w, gr->a_g_w, gr->b_p_w, gr->b_g_w, gr->g_w};
+  float* bdst[5] = {gr->a_p_b, gr->a_g_b, gr->b_p_b, gr->b_g_b, gr->g_b};
+  for (int k = 0; k < 5; ++k) {
+    const int m0 = k * CH, rows = k < 4 ? CH : CZ;
+    if ((rc = launch_wgrad_finish(a.part1, M1, CZ, pitch, m0, rows, a.sums_stack, w.ln_in_w,
+                                  w.ln_in_b, wdst[k], st)))
+      return rc;
+    if ((rc = launch_copy_f32(bdst[k], a.sums_stack + m0, rows, st))) return rc;
+  }
+  if ((rc = launch_wgrad_finish(a.part2, CZ, CH, pitch, 0, CZ, a.sums_dp, w.ln_out_w, w.ln_out_b,
+                                gr->z_w, st)))
+    return rc;
+  if ((rc = launch_copy_f32(gr->z_b, a.sums_dp, CZ, st))) return rc;
+  if ((rc = launch_copy_f32(gr->ln_in_w, a.dots_dzn, CZ, st))) return rc;
+  if ((rc = launch_copy_f32(gr->ln_in_b, a.sums_dzn, CZ, st))) return rc;
+  if ((rc = launch_copy_f32(gr->ln_out_w, a.dots_dxo, CH, st))) return rc;
+  if ((rc = launch_copy_f32(gr->ln_out_b, a.sums_dxo, CH, st))) return rc;
+  return GTK_OK;
+}
+
+}  // namespace gtk
+
+using namespace gtk;
+
+extern "C" size_t gtk_tri_mul_backward_workspace_size(int64_t B, int64_t N, int64_t c_z, int64_t c,
+                                                      int dtype) {
+  if (!(c_z == 128 && (c == 64 || c == 128)) || B < 0 || N < 0) return 0;
+  if (dtype != GTK_F32 && dtype != GTK_BF16) return 0;
+  Carve cv(nullptr, SIZE_MAX);
+  if (dtype == GTK_F32) carve_trimul_bwd<float>(cv, B, N, (int)c_z, (int)c, dtype);
+  else carve_trimul_bwd<bf16>(cv, B, N, (int)c_z, (int)c, dtype);
+  return cv.off;
+}
+
+extern "C" int gtk_tri_mul_backward(const void* z, const float* mask, const void* dy,
+                                    const gtk_tri_mul_weights* w, void* dz,
+                                    const gtk_tri_mul_grads* grads, int64_t B, int64_t N,
+                                    int64_t c_z, int64_t c, int outgoing, float eps_in,
+                                    float eps_out, int dtype, void* ws, size_t ws_bytes,
+                                    void* stream) {
+  GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL, "gtk_tri_mul_backward: bad dtype %d", dtype);
+  GTK_REQUIRE(c_z == 128 && (c == 64 || c == 128), GTK_EUNSUPPORTED,
+              "gtk_tri_mul_backward: c_z=%lld c=%lld unsupported (c_z=128, c in {64,128})",
+              (long long)c_z, (long long)c);
+  GTK_REQUIRE(B >= 0 && N >= 0 && N <= 4096, GTK_EINVAL, "gtk_tri_mul_backward: bad shape");
+  if (B == 0 || N == 0) return GTK_OK;
+  GTK_REQUIRE(z && dy && w && dz && grads && ws, GTK_EINVAL, "gtk_tri_mul_backward: null pointer");
+  GTK_REQUIRE(w->dtype == GTK_F32 || w->dtype == GTK_BF16, GTK_EINVAL,
+              "gtk_tri_mul_backward: bad weight dtype %d", w->dtype);
+  GTK_REQUIRE(w->a_p_w && w->a_g_w && w->b_p_w && w->b_g_w && w->g_w && w->z_w, GTK_EINVAL,
+              "gtk_tri_mul_backward: null weight");
+  const float* gp[] = {grads->ln_in_w, grads->ln_in_b, grads->a_p_w, grads->a_p_b, grads->a_g_w,
+                       grads->a_g_b, grads->b_p_w, grads->b_p_b, grads->b_g_w, grads->b_g_b,
+                       grads->g_w, grads->g_b, grads->ln_out_w, grads->ln_out_b, grads->z_w,
+                       grads->z_b};
+  for (const float* p : gp) GTK_REQUIRE(p, GTK_EINVAL, "gtk_tri_mul_backward: null gradient pointer");
+  const size_t need = gtk_tri_mul_backward_workspace_size(B, N, c_z, c, dtype);
+  GTK_REQUIRE(ws_bytes >= need, GTK_EWORKSPACE, "gtk_tri_mul_backward: workspace %zu < %zu bytes",
+              ws_bytes, need);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == GTK_F32)
+    return c == 128 ? bwd_trimul<float, 128, 128>(z, mask, dy, w, dz, grads, B, N, outgoing, eps_in, eps_out, dtype, ws, st)
+                    : bwd_trimul<float, 128, 64>(z, mask, dy, w, dz, grads, B, N, outgoing, eps_in, eps_out, dtype, ws, st);
+  return c == 128 ? bwd_trimul<bf16, 128, 128>(z, mask, dy, w, dz, grads, B, N, outgoing, eps_in, eps_out, dtype, ws, st)
+                  : bwd_trimul<bf16, 128, 64>(z, mask, dy, w, dz, grads, B, N, outgoing, eps_in, eps_out, dtype, ws, st);
+}

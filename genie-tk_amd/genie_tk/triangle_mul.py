@@ -4,11 +4,14 @@ Drop-in for ``src/genie_tk/triangle_mul.py`` of the reference: same classes,
 constructor arguments, parameter names (state_dict keys) and ``forward(z,
 mask=None)`` returning the update (no residual).
 
-Kernel path (``use_fused_kernel=True``, GPU tensor, no autograd needed):
+Kernel path (``use_fused_kernel=True``, GPU tensor):
 ``genie_tk._C.tri_mul_forward``, three gfx950 kernels (prologue
 LN + gated projections + mask, matrix-core contraction per channel, epilogue
-LN + output projection + gate).  PyTorch path: ``_forward_pytorch``, the
-reference fallback semantics (triangle_mul.py:103-132).
+LN + output projection + gate).  When autograd needs gradients the same
+forward runs inside ``_TriMulFunction``, whose backward is
+``genie_tk._C.tri_mul_backward`` (gradients of z and every parameter).
+PyTorch path: ``_forward_pytorch``, the reference fallback semantics
+(triangle_mul.py:103-132).
 """
 from __future__ import annotations
 
@@ -24,6 +27,34 @@ from genie_tk.primitives import Linear
 from genie_tk.utils import has_cuda_kernels, permute_final_dims
 
 _CUDA_AVAILABLE = has_cuda_kernels()
+
+
+class _TriMulFunction(torch.autograd.Function):
+    """The update on the HIP kernels, forward and backward.
+
+    The reference trains through torch autograd of its PyTorch path
+    (triangle_mul.py:103-132); this computes the same gradients on the
+    kernels.  Activations are recomputed in the backward from z (only z, the
+    mask and the parameters are saved)."""
+
+    @staticmethod
+    def forward(ctx, module, z, mask, *params):
+        ctx.module = module
+        ctx.save_for_backward(z, mask, *params)
+        return module._forward_cuda(z, mask)
+
+    @staticmethod
+    def backward(ctx, dy):
+        z, mask, *params = ctx.saved_tensors
+        mod = ctx.module
+        zb, mb, lead = _dispatch.flatten_batch(z, mask)
+        res = _ext.require().tri_mul_backward(
+            zb, mb, dy.reshape(zb.shape).to(z.dtype), list(params), mod.c_z, mod.c_hidden,
+            mod._outgoing, mod.layer_norm_in.eps, mod.layer_norm_out.eps)
+        dz = res[0].reshape(z.shape) if ctx.needs_input_grad[1] else None
+        grads = [g.to(p.dtype) if ctx.needs_input_grad[3 + k] else None
+                 for k, (g, p) in enumerate(zip(res[1:], params))]
+        return (None, dz, None, *grads)
 
 
 class TriangleMultiplicativeUpdate(nn.Module):
@@ -86,16 +117,18 @@ class TriangleMultiplicativeUpdate(nn.Module):
     def _pack(self, params, fp32: bool) -> Tensor:
         return _ext.require().tri_mul_pack(params, self.c_z, self.c_hidden, fp32)
 
+    def _param_list(self):
+        return [self.layer_norm_in.weight, self.layer_norm_in.bias,
+                self.linear_a_p.weight, self.linear_a_p.bias,
+                self.linear_a_g.weight, self.linear_a_g.bias,
+                self.linear_b_p.weight, self.linear_b_p.bias,
+                self.linear_b_g.weight, self.linear_b_g.bias,
+                self.linear_g.weight, self.linear_g.bias,
+                self.layer_norm_out.weight, self.layer_norm_out.bias,
+                self.linear_z.weight, self.linear_z.bias]
+
     def _packed_params(self, fp32: bool) -> Tensor:
-        ps = [self.layer_norm_in.weight, self.layer_norm_in.bias,
-              self.linear_a_p.weight, self.linear_a_p.bias,
-              self.linear_a_g.weight, self.linear_a_g.bias,
-              self.linear_b_p.weight, self.linear_b_p.bias,
-              self.linear_b_g.weight, self.linear_b_g.bias,
-              self.linear_g.weight, self.linear_g.bias,
-              self.layer_norm_out.weight, self.layer_norm_out.bias,
-              self.linear_z.weight, self.linear_z.bias]
-        return self._packed.get(ps, fp32, self._pack)
+        return self._packed.get(self._param_list(), fp32, self._pack)
 
     def _forward_cuda(self, z: Tensor, mask: Optional[Tensor] = None,
                       residual: bool = False) -> Tensor:
@@ -122,9 +155,7 @@ class TriangleMultiplicativeUpdate(nn.Module):
             if self.use_fused_kernel and self._kernel_supported(z):
                 if not _dispatch.needs_autograd(z, self):
                     return self._forward_cuda(z, mask)
-                _dispatch.warn_once("tri_mul_grad", "genie_tk: gradients requested; "
-                                    "TriangleMultiplicativeUpdate runs its PyTorch path "
-                                    "(the HIP kernels are forward-only)")
+                return _TriMulFunction.apply(self, z, mask, *self._param_list())
         return self._forward_pytorch(z, mask)
 
 

@@ -161,6 +161,26 @@ int gtk_tri_mul_forward(const void* z, const float* mask, void* out, const void*
                         float eps_in, float eps_out, int dtype, void* workspace,
                         size_t workspace_bytes, void* stream);
 
+/* Backward of gtk_tri_mul_forward (update only, no residual): given dL/dy,
+ * writes dL/dz (element type dtype) and the gradient of every parameter
+ * (fp32, the nn.Linear / LayerNorm layouts of gtk_tri_mul_weights).  The
+ * reference has no backward kernel: its gradients are torch autograd over
+ * TriangleMultiplicativeUpdate._forward_pytorch src/genie_tk/triangle_mul.py:103-132,
+ * which this computes (forward activations recomputed from z and the raw
+ * weights in w).  Gradients are written, not accumulated. */
+typedef struct gtk_tri_mul_grads {
+  float *ln_in_w, *ln_in_b, *a_p_w, *a_p_b, *a_g_w, *a_g_b, *b_p_w, *b_p_b;
+  float *b_g_w, *b_g_b, *g_w, *g_b, *ln_out_w, *ln_out_b, *z_w, *z_b;
+} gtk_tri_mul_grads;
+
+size_t gtk_tri_mul_backward_workspace_size(int64_t B, int64_t N, int64_t c_z, int64_t c,
+                                           int dtype);
+int gtk_tri_mul_backward(const void* z, const float* mask, const void* dy,
+                         const gtk_tri_mul_weights* w, void* dz, const gtk_tri_mul_grads* grads,
+                         int64_t B, int64_t N, int64_t c_z, int64_t c, int outgoing, float eps_in,
+                         float eps_out, int dtype, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
 /* ------------------------------------------------------------------------
  * Fused TriangleAttention forward (starting / ending node).
  * Replaces TriangleAttention._forward_cuda src/genie_tk/triangle_attention.py:145-179

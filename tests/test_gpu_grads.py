@@ -1,0 +1,83 @@
+"""Backward kernels against the float64 backward oracle (oracle/grads.py).
+
+The modules run forward on the kernels inside their autograd Function and
+backward through genie_tk._C.*_backward (the C ABI's gtk_*_backward).  The
+oracle is evaluated on the same (bf16-rounded, for bf16) inputs, parameters
+and upstream gradient.
+
+Tolerances, per gradient tensor g against the oracle's r:
+  * fp32: max|g - r| <= 1e-4 * max(1, max|r|);
+  * bf16: max|g - r| <= 3e-2 * max|r| and ||g - r||_2 <= 1e-2 * ||r||_2.  The
+    bf16 backward rounds its intermediate planes (dX, dA, dB and the
+    per-pair operands of the weight-gradient products) to bf16, so errors
+    are relative to the tensor's scale rather than per element.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import grads
+from tests import helpers as H
+from tests.gpu_common import log, trimul_module
+
+pytestmark = pytest.mark.gpu
+
+DT = {"fp32": torch.float32, "bf16": torch.bfloat16}
+
+
+def _check_grad(got: np.ndarray, ref: np.ndarray, dname: str, what: str) -> float:
+    """Asserts the tolerance; returns max|g - r| / max|r| for the log."""
+    assert np.isfinite(got).all(), f"{what}: non-finite gradient"
+    err = np.abs(got - ref)
+    scale = np.abs(ref).max()
+    if dname == "fp32":
+        assert err.max() <= 1e-4 * max(1.0, scale), f"{what}: max err {err.max():.3e} (scale {scale:.3e})"
+    else:
+        rel = np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
+        assert err.max() <= 3e-2 * scale, f"{what}: max err {err.max():.3e} > 3e-2 * {scale:.3e}"
+        assert rel <= 1e-2, f"{what}: normwise relative error {rel:.3e}"
+    return float(err.max() / max(scale, 1e-30))
+
+
+def _np(t):
+    return t.detach().float().cpu().numpy()
+
+
+@pytest.mark.parametrize("dname", ["fp32", "bf16"])
+@pytest.mark.parametrize("outgoing", [True, False])
+@pytest.mark.parametrize("N,c", [(64, 128), (37, 64), (130, 128)])
+def test_tri_mul_backward(dname, outgoing, N, c):
+    log(f"tri_mul backward {dname} outgoing={outgoing} N={N} c={c}")
+    dt = DT[dname]
+    P = H.draw_params(H.tri_mul_shapes(128, c), seed=N + c, ln_random=True, bias_random=True)
+    z = H.pair_input(2, N, 128, seed=N + 1)
+    m = H.tail_mask(2, N, [N, N - 5])
+    dy = H.pair_input(2, N, 128, seed=N + 2)
+    if dname == "bf16":
+        P, z, dy = H.bf16_params(P), H.bf16_round(z), H.bf16_round(dy)
+    mod = trimul_module(P, outgoing, dt)
+    zt = torch.from_numpy(z).to("cuda", dt).requires_grad_(True)
+    mt = torch.from_numpy(m).to("cuda")
+    y = mod(zt, mt)
+    y.backward(torch.from_numpy(dy).to("cuda", dt))
+    torch.cuda.synchronize()
+    dz_ref, g_ref = grads.tri_mul_grad(z, m, P, outgoing, dy)
+    worst = [(_check_grad(_np(zt.grad), dz_ref, dname, "dz"), "dz")]
+    for name, prm in mod.named_parameters():
+        assert prm.grad is not None and prm.grad.dtype == dt, name
+        worst.append((_check_grad(_np(prm.grad), g_ref[name], dname, name), name))
+    log(f"  worst max|g - r| / max|r|: {max(worst)[0]:.2e} ({max(worst)[1]})")
+
+
+def test_tri_mul_backward_runs_the_kernels(monkeypatch):
+    """With gradients required, forward and backward go through the kernels
+    (the PyTorch path is made to raise), for leading batch dimensions too."""
+    P = H.draw_params(H.tri_mul_shapes(128, 128), seed=9, bias_random=True)
+    mod = trimul_module(P, True, torch.bfloat16)
+    monkeypatch.setattr(mod, "_forward_pytorch",
+                        lambda *a, **k: (_ for _ in ()).throw(AssertionError("fallback")))
+    z = torch.randn(2, 1, 40, 40, 128, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    y = mod(z)
+    y.float().square().sum().backward()
+    assert z.grad is not None and z.grad.shape == z.shape and torch.isfinite(z.grad).all()
+    assert all(p.grad is not None and torch.isfinite(p.grad).all() for p in mod.parameters())
