@@ -305,6 +305,27 @@ def main() -> int:
     fb_rep = C.timing_report()
     C.timing_enable(False)
     del zg, dyg
+    # the same for tri-attn starting node
+    ta = mods["tri_att_start"]
+    xg = z.detach().clone().requires_grad_(True)
+    dya = torch.randn_like(z)
+
+    def fba(fwd):
+        def run():
+            xg.grad = None
+            for p in ta.parameters():
+                p.grad = None
+            fwd(xg, maskb).backward(dya)
+        return run
+    print("[bench] tri-attn forward+backward", file=sys.stderr, flush=True)
+    fba_ms = statistics.median(event_time_ms(torch, fba(ta), reps))
+    fba_torch_ms = statistics.median(event_time_ms(torch, fba(ta._forward_pytorch), 3, warm=1))
+    C.timing_enable(True)
+    for _ in range(3):
+        fba(ta)()
+    fba_rep = C.timing_report()
+    C.timing_enable(False)
+    del xg, dya
     torch.cuda.synchronize()
 
     fm, fa = trimul_flops(N), triattn_flops(N)
@@ -366,6 +387,16 @@ def main() -> int:
         "stage_ms_per_step": {k: round(v[1] / 3, 4) for k, v in fb_rep.items()},
         "note": "forward + backward (dz and all parameter gradients) of tri-mul outgoing; gflop "
                 "counts 3x the forward's products (the backward recomputes the forward on top)",
+    }
+    fbaf = 3 * sum(fa.values())
+    per_op["tri_att_start_fwd_bwd"] = {
+        "ms": round(fba_ms, 4), "gflop": round(fbaf / 1e9, 2),
+        "tflops": round(fbaf / (fba_ms * 1e-3) / 1e12, 2),
+        "pytorch_autograd_ms": round(fba_torch_ms, 4),
+        "speedup_vs_pytorch_autograd": round(fba_torch_ms / fba_ms, 2),
+        "stage_ms_per_step": {k: round(v[1] / 3, 4) for k, v in fba_rep.items()},
+        "note": "forward + backward (dx and all parameter gradients) of tri-attn starting node; "
+                "gflop counts 3x the forward's products",
     }
     work = dict(fm)
     work.update(fa)

@@ -24,7 +24,8 @@ ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["layernorm.hip", "tri_mul.hip", "tri_mul_bwd.hip", "tri_attn.hip", "pair_transition.hip",
+HIP_SOURCES = ["layernorm.hip", "tri_mul.hip", "tri_mul_bwd.hip", "tri_attn.hip", "tri_attn_bwd.hip",
+               "pair_transition.hip",
                "capi.cpp"]
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",

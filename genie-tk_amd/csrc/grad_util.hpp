@@ -258,7 +258,7 @@ inline int launch_wgrad(const T* G, const T* X, float* part, int M, int Nn, int6
 
 // dst[(m - m0)][n] = sum_s part[s][m][n] * (gamma ? gamma[n] : 1)
 //                    + (rowsum && beta ? rowsum[m] * beta[n] : 0),  m in [m0, m0 + rows)
-__global__ void wgrad_finish_kernel(const float* __restrict__ part, int nsplit, int M, int Nn,
+static __global__ void wgrad_finish_kernel(const float* __restrict__ part, int nsplit, int M, int Nn,
                                     int m0, int rows, const float* __restrict__ rowsum,
                                     const float* __restrict__ gamma, const float* __restrict__ beta,
                                     float* __restrict__ dst) {
@@ -330,7 +330,7 @@ __global__ __launch_bounds__(256) void rowred_kernel(const T* __restrict__ G, co
   }
 }
 
-__global__ void rowred_finish_kernel(const float* __restrict__ part, int rows, float* __restrict__ dst) {
+static __global__ void rowred_finish_kernel(const float* __restrict__ part, int rows, float* __restrict__ dst) {
   const int r = blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= rows) return;
   float a = 0.f;
@@ -356,7 +356,7 @@ inline int launch_rowred(const T* G, const T* X, int rows, int64_t pitch, int64_
   return GTK_OK;
 }
 
-__global__ void copy_f32_kernel(float* __restrict__ dst, const float* __restrict__ src, int n) {
+static __global__ void copy_f32_kernel(float* __restrict__ dst, const float* __restrict__ src, int n) {
   const int i = blockIdx.x * blockDim.x + threadIdx.x;
   if (i < n) dst[i] = src[i];
 }

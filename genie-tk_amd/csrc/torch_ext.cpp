@@ -262,6 +262,56 @@ std::vector<at::Tensor> tri_mul_backward(const at::Tensor& z, const c10::optiona
   return out;
 }
 
+// Backward of tri_attn_forward (update only): returns [dx, then the gradients of
+// the 10 parameters in tri_attn_pack's order, fp32].
+std::vector<at::Tensor> tri_attn_backward(const at::Tensor& x, const c10::optional<at::Tensor>& mask,
+                                          const at::Tensor& dy, std::vector<at::Tensor> ps,
+                                          int64_t c_in, int64_t c_h, int64_t H, bool starting,
+                                          double eps) {
+  TORCH_CHECK(ps.size() == 10, "tri_attn_backward expects 10 parameter tensors");
+  check_gpu(x, "x");
+  check_gpu(ps[3], "weights");
+  const at::DeviceGuard guard(x.device());
+  TORCH_CHECK(x.dim() == 4 && x.size(1) == x.size(2) && x.size(3) == c_in, "x must be [B, N, N, c_in]");
+  TORCH_CHECK(dy.sizes() == x.sizes() && dy.scalar_type() == x.scalar_type(),
+              "dy must match x in shape and dtype");
+  auto xc = x.contiguous();
+  auto dyc = dy.contiguous();
+  const int64_t B = xc.size(0), N = xc.size(1);
+  at::Tensor mc;
+  if (mask.has_value()) {
+    TORCH_CHECK(mask->numel() == B * N * N, "mask must be [B, N, N]");
+    mc = f32c(*mask);
+  }
+  gtk_tri_attn_weights w;
+  w.dtype = common_param_dtype(ps);
+  const void** slots[10] = {&w.ln_w, &w.ln_b, &w.tri_w, &w.q_w, &w.k_w,
+                            &w.v_w,  &w.g_w,  &w.g_b,   &w.o_w, &w.o_b};
+  for (int i = 0; i < 10; ++i) *slots[i] = ptr_or_null(ps[i]);
+  const int dt = gtk_dtype_of(xc, "x");
+  std::vector<at::Tensor> out;
+  out.push_back(at::empty_like(xc));
+  gtk_tri_attn_grads g;
+  float** gs[10] = {&g.ln_w, &g.ln_b, &g.tri_w, &g.q_w, &g.k_w, &g.v_w, &g.g_w, &g.g_b, &g.o_w, &g.o_b};
+  const int64_t shapes[10][2] = {{c_in, 1}, {c_in, 1}, {H, c_in}, {c_h, c_in}, {c_h, c_in},
+                                 {c_h, c_in}, {c_h, c_in}, {c_h, 1}, {c_in, c_h}, {c_in, 1}};
+  for (int i = 0; i < 10; ++i) {
+    auto t = shapes[i][1] == 1 ? at::empty({shapes[i][0]}, xc.options().dtype(at::kFloat))
+                               : at::empty({shapes[i][0], shapes[i][1]}, xc.options().dtype(at::kFloat));
+    *gs[i] = t.data_ptr<float>();
+    out.push_back(t);
+  }
+  const size_t bytes = gtk_tri_attn_backward_workspace_size(B, N, c_in, c_h, H, dt);
+  TORCH_CHECK(bytes > 0, "genie_tk._C: tri_attn backward shape c_in=", c_in, " c_h=", c_h, " H=", H,
+              " unsupported");
+  auto ws = workspace(xc, bytes);
+  check_rc(gtk_tri_attn_backward(xc.data_ptr(), mask.has_value() ? mc.data_ptr<float>() : nullptr,
+                                 dyc.data_ptr(), &w, out[0].data_ptr(), &g, B, N, c_in, c_h, H,
+                                 starting ? 1 : 0, (float)eps, dt, ws.data_ptr(), ws.numel(),
+                                 cur_stream(xc)));
+  return out;
+}
+
 at::Tensor tri_mul_forward(const at::Tensor& z, const c10::optional<at::Tensor>& mask,
                            const at::Tensor& packed, int64_t c_z, int64_t c, bool outgoing,
                            bool residual, double eps_in, double eps_out) {
@@ -418,6 +468,10 @@ PYBIND11_MODULE(_C, m) {
         "TriangleMultiplicativeUpdate backward: [dz, 16 parameter gradients (fp32)]",
         py::arg("z"), py::arg("mask"), py::arg("dy"), py::arg("params"), py::arg("c_z"),
         py::arg("c"), py::arg("outgoing"), py::arg("eps_in") = 1e-5, py::arg("eps_out") = 1e-5);
+  m.def("tri_attn_backward", &tri_attn_backward,
+        "TriangleAttention backward: [dx, 10 parameter gradients (fp32)]", py::arg("x"),
+        py::arg("mask"), py::arg("dy"), py::arg("params"), py::arg("c_in"), py::arg("c_h"),
+        py::arg("no_heads"), py::arg("starting"), py::arg("eps") = 1e-5);
   m.def("pair_transition_pack", &pair_transition_pack, "Pack PairTransition parameters",
         py::arg("params"), py::arg("c"), py::arg("n"));
   m.def("pair_transition_forward", &pair_transition_forward,

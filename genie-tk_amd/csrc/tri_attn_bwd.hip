@@ -1,0 +1,860 @@
+// Backward of triangle attention (starting / ending node).
+//
+// The reference trains through torch autograd of its PyTorch path
+// (triangle_attention.py:100-143 with Attention.forward, primitives.py:114-178);
+// this is the same chain rule on gfx950 kernels.  Everything runs in the
+// attention orientation (rows r, positions j; the ending node reads x, the
+// mask and dL/dy transposed and writes dL/dx transposed).  Forward activations
+// are recomputed from x:
+//
+//  proj   LN(x), q, k, v (position-major and d-major copies), the gate
+//         sigmoid, the triangle bias and the key mask of every row.
+//  fwd    attention forward per (row, head, 32 queries) with an online
+//         softmax: O, the running max m and 1/l per query.
+//  epi    dgo = dy W_o, dO = dgo * gate, dg_pre = dgo * O * gate (1 - gate),
+//         D = sum_d dO O per (query, head).
+//  dkdv   per (row, head, 32 keys): over all queries, P = exp(S - m) / l,
+//         dP = dO V^T, dS = P (dP - D); dV = P^T dO, dK = scale dS^T Q.
+//  dq     per (row, head, 32 queries): dQ = scale dS K over all keys.
+//  dbias  per (head, 32 queries, 32 keys): dB = sum over rows of dS.
+//  pro    dxn = dq W_q + dk W_k + dv W_v + dg_pre W_g + dB W_b, LayerNorm
+//         backward -> dx; the per-pair operands of the weight gradients.
+//  then   split-K weight-gradient products and row sums (grad_util.hpp).
+//
+// Scores: S = scale q.k + bias for a valid key, exactly -1e9 for a masked key
+// (the fp32 reference's qk + (-1e9) + tri rounds to -1e9) and -inf for the
+// positions past N.  A row whose keys are all masked is uniform over its N
+// keys, and its dS still flows into q, k and the bias: torch autograd of the
+// reference differentiates qk + mask_bias + tri term by term.  m and 1/l are
+// kept separately (not m + log l): for such a row m = -1e9 and fp32 cannot
+// hold -1e9 + log l.
+#include <algorithm>
+#include <cmath>
+
+#include "capi_util.hpp"
+#include "common.hpp"
+#include "grad_util.hpp"
+#include "pack.hpp"
+
+namespace gtk {
+
+constexpr int AD = 32;            // head dimension
+constexpr float kMaskScore = -1e9f;
+
+template <typename T> struct AttnBwdW {
+  T *w_q, *w_k, *w_v, *w_g, *w_b;      // natural units, LayerNorm weight folded in
+  float *b_q, *b_k, *b_v, *b_g, *b_b;  // W beta (+ the Linear's bias)
+  T *wt_q, *wt_k, *wt_v, *wt_g;        // W^T (unfolded), accumulator order: dxn = d W
+  T* wt_o;                             // W_o^T, fragment order: dgo = dy W_o
+  float* wb_raw;                       // W_b [H][C], fp32
+  float *ln_w, *ln_b;
+};
+
+template <typename T> struct AttnBwdBufs {
+  T *qr, *qt, *kr, *kt, *vr, *vt;  // [B][N][H][np][32] and [B][N][H][32][np]
+  T *o, *dor, *dot, *dq, *dk, *dv; // o, dO, dq, dk, dv position-major; dot d-major
+  T* gt;                           // gate sigmoid [B][N][np][CH]
+  T* bias;                         // triangle bias [B][H][N][N]
+  float* kmask;                    // [B][N][np]: 1 valid key, 0 masked
+  float *mrow, *linv, *dd;         // [B][N][H][np]
+  float* db;                       // dL/dbias [B][H][N][N]
+  T *cm_stack, *cm_xh, *cm_dxn, *cm_dy, *cm_go, *cm_dtri;
+  int64_t pitch;
+};
+
+// Two k-steps over d = 32 of a 32x32 product: rows from `a`, columns from `b`,
+// both operands position-major [pos][32] (lane = position, 8 consecutive d).
+template <typename T>
+__device__ __forceinline__ f32x16 qk_tile(const T* a_rows, const T* b_rows) {
+  const int lane = threadIdx.x & 63;
+  const int t32 = lane & 31, half = lane >> 5;
+  Frag<T> fa, fb;
+  f32x16 acc = zero16();
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    fa.load(a_rows + t32 * AD + 16 * s + 8 * half);
+    fb.load(b_rows + t32 * AD + 16 * s + 8 * half);
+    mma(acc, fa, fb);
+  }
+  return acc;
+}
+
+// Operand with lane = d and k = 32 positions in accumulator order, from a
+// d-major [32][np] block at position p0: chunk gp holds positions
+// p0 + 16gp + 8(e>>2) + 4h + (e&3).
+template <typename T>
+__device__ __forceinline__ void dmajor_frags(Frag<T>* f, const T* base, int64_t np, int p0) {
+  const int lane = threadIdx.x & 63;
+  const int t32 = lane & 31, half = lane >> 5;
+  const T* row = base + (int64_t)t32 * np + p0 + 4 * half;
+#pragma unroll
+  for (int gp = 0; gp < 2; ++gp) {
+    const f32x4 lo = load4f(row + 16 * gp);
+    const f32x4 hi = load4f(row + 16 * gp + 8);
+    float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    f[gp].set(v);
+  }
+}
+
+__device__ __forceinline__ float score_of(float acc, float scale, float bias, float km, bool exists) {
+  return exists ? (km > 0.5f ? scale * acc + bias : kMaskScore) : -INFINITY;
+}
+
+// ---------------------------------------------------------------------------
+// proj: one 32-position tile of one attention row per wave
+// ---------------------------------------------------------------------------
+template <typename T, int C, int H>
+__global__ __launch_bounds__(256) void attn_bwd_proj_kernel(const T* __restrict__ x,
+                                                            const float* __restrict__ mask,
+                                                            AttnBwdW<T> w, AttnBwdBufs<T> bf,
+                                                            int B, int N, int np, int starting,
+                                                            float eps) {
+  constexpr int CH = H * AD;
+  const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
+  const int jtiles = np / 32;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile >= (int64_t)B * N * jtiles) return;
+  const int jt = (int)(tile % jtiles);
+  const int r = (int)((tile / jtiles) % N);
+  const int b = (int)(tile / ((int64_t)jtiles * N));
+  const int j = jt * 32 + t32;
+  const bool valid = j < N;
+  const int64_t xp = valid ? ((int64_t)b * N + (starting ? r : j)) * N + (starting ? j : r) : 0;
+
+  RowHalf<C> rh;
+  load_row_half<T, C>(rh, x + xp * C, valid);
+  const f32x2 st = row_stats<C>(rh, eps);
+  Frag<T> xf[C / 16];
+  ln_to_frags<T, C>(xf, rh, st);
+
+  const T* wk[3] = {w.w_q, w.w_k, w.w_v};
+  const float* bk[3] = {w.b_q, w.b_k, w.b_v};
+  T* dr[3] = {bf.qr, bf.kr, bf.vr};
+  T* dt[3] = {bf.qt, bf.kt, bf.vt};
+#pragma unroll 1
+  for (int kind = 0; kind < 3; ++kind) {
+#pragma unroll 1
+    for (int h = 0; h < H; ++h) {
+      const f32x16 acc = row_gemm_tile<T, C, true>(xf, wk[kind], h);
+      const int64_t rh_ = ((int64_t)b * N + r) * H + h;
+      T* rowm = dr[kind] + (rh_ * np + j) * AD;
+      T* dmaj = dt[kind] + rh_ * AD * np + j;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int d0 = 8 * g + 4 * half;
+        float v[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) v[q] = valid ? acc[4 * g + q] + bk[kind][h * AD + d0 + q] : 0.f;
+        store4(rowm + d0, v[0], v[1], v[2], v[3]);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) dmaj[(int64_t)(d0 + q) * np] = cvt<T>(v[q]);
+      }
+    }
+  }
+#pragma unroll 1
+  for (int h = 0; h < H; ++h) {
+    const f32x16 acc = row_gemm_tile<T, C, true>(xf, w.w_g, h);
+    T* gp = bf.gt + (((int64_t)b * N + r) * np + j) * CH + h * AD;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 8 * g + 4 * half;
+      float v[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) v[q] = sigmoidf_(acc[4 * g + q] + w.b_g[h * AD + d0 + q]);
+      store4(gp + d0, v[0], v[1], v[2], v[3]);
+    }
+  }
+  {
+    // triangle bias: outputs 0..H-1 sit in lanes of half 0, acc[0..H-1]
+    const f32x16 acc = row_gemm_tile<T, C, true>(xf, w.w_b, 0);
+    if (valid && half == 0) {
+#pragma unroll
+      for (int h = 0; h < H; ++h)
+        bf.bias[(((int64_t)b * H + h) * N + r) * N + j] = cvt<T>(acc[h] + w.b_b[h]);
+    }
+  }
+  if (half == 0) bf.kmask[((int64_t)b * N + r) * np + j] = valid ? (mask ? mask[xp] : 1.f) : 0.f;
+}
+
+// ---------------------------------------------------------------------------
+// fwd: O, m, 1/l per (row, head, 32 queries); lane = query
+// ---------------------------------------------------------------------------
+template <typename T, int H>
+__global__ __launch_bounds__(256) void attn_bwd_fwd_kernel(AttnBwdBufs<T> bf, int B, int N, int np,
+                                                           float scale) {
+  const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
+  const int qtiles = np / 32;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile >= (int64_t)B * N * H * qtiles) return;
+  const int qt = (int)(tile % qtiles);
+  const int64_t rh = tile / qtiles;  // (b*N + r)*H + h
+  const int h = (int)(rh % H);
+  const int64_t br = rh / H;         // b*N + r
+  const int b = (int)(br / N);
+  const int q = qt * 32 + t32;
+  const T* Q = bf.qr + rh * np * AD;
+  const T* K = bf.kr + rh * np * AD;
+  const T* VT = bf.vt + rh * AD * np;
+  const T* Bh = bf.bias + ((int64_t)b * H + h) * N * N;
+  const float* km = bf.kmask + br * np;
+
+  float m = -INFINITY, l = 0.f;
+  f32x16 oacc = zero16();
+  for (int kt = 0; kt < qtiles; ++kt) {
+    const f32x16 acc = qk_tile<T>(K + (int64_t)kt * 32 * AD, Q + (int64_t)qt * 32 * AD);
+    float s[16];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int k0 = kt * 32 + 8 * g + 4 * half;
+      const f32x4 k4 = *reinterpret_cast<const f32x4*>(km + k0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int key = k0 + e;
+        const float bv = (q < N && key < N) ? to_f32(Bh[(int64_t)q * N + key]) : 0.f;
+        s[4 * g + e] = score_of(acc[4 * g + e], scale, bv, k4[e], key < N);
+        mx = fmaxf(mx, s[4 * g + e]);
+      }
+    }
+    mx = fmaxf(mx, xor32(mx));
+    const float mn = fmaxf(m, mx);
+    const float alpha = __expf(m - mn);
+    float ps = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      s[e] = __expf(s[e] - mn);
+      ps += s[e];
+    }
+    ps += xor32(ps);
+    l = l * alpha + ps;
+    m = mn;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) oacc[e] *= alpha;
+    Frag<T> fp[2], fv[2];
+    vals_to_frags<T>(fp, s);
+    dmajor_frags<T>(fv, VT, np, kt * 32);
+    mma(oacc, fv[0], fp[0]);
+    mma(oacc, fv[1], fp[1]);
+  }
+  const float li = 1.0f / l;
+  T* O = bf.o + (rh * np + q) * AD;
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+    store4(O + 8 * g + 4 * half, oacc[4 * g] * li, oacc[4 * g + 1] * li, oacc[4 * g + 2] * li,
+           oacc[4 * g + 3] * li);
+  if (half == 0) {
+    bf.mrow[rh * np + q] = m;
+    bf.linv[rh * np + q] = li;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// epi: dgo = dy W_o, dO, dg_pre, D; per 32-position tile of one row
+// ---------------------------------------------------------------------------
+template <typename T, int C, int H>
+__global__ __launch_bounds__(256) void attn_bwd_epi_kernel(const T* __restrict__ dy, AttnBwdW<T> w,
+                                                           AttnBwdBufs<T> bf, int B, int N, int np,
+                                                           int starting) {
+  constexpr int CH = H * AD;
+  const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
+  const int jtiles = np / 32;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile >= (int64_t)B * N * jtiles) return;
+  const int jt = (int)(tile % jtiles);
+  const int r = (int)((tile / jtiles) % N);
+  const int b = (int)(tile / ((int64_t)jtiles * N));
+  const int j = jt * 32 + t32;
+  const bool valid = j < N;
+  const int64_t xp = valid ? ((int64_t)b * N + (starting ? r : j)) * N + (starting ? j : r) : 0;
+  const int64_t p = ((int64_t)b * N + r) * N + j;  // pair index, attention orientation
+  const int64_t pitch = bf.pitch;
+
+  RowHalf<C> dh;
+  load_row_half<T, C>(dh, dy + xp * C, valid);
+  Frag<T> fdy[C / 16];
+#pragma unroll
+  for (int ch = 0; ch < C / 16; ++ch) fdy[ch].set(&dh.v[ch * 8]);
+  if (valid) {
+#pragma unroll
+    for (int i = 0; i < C / 2; ++i) bf.cm_dy[(int64_t)(half * (C / 2) + i) * pitch + p] = cvt<T>(dh.v[i]);
+  }
+  T* cm_dg = bf.cm_stack + (int64_t)3 * CH * pitch;
+#pragma unroll 1
+  for (int h = 0; h < H; ++h) {
+    const f32x16 dog = row_gemm_tile<T, C, true>(fdy, w.wt_o, h);
+    const int64_t rh = ((int64_t)b * N + r) * H + h;
+    const T* O = bf.o + (rh * np + j) * AD;
+    const T* G = bf.gt + (((int64_t)b * N + r) * np + j) * CH + h * AD;
+    T* dor = bf.dor + (rh * np + j) * AD;
+    T* dot = bf.dot + rh * AD * np + j;
+    float dsum = 0.f;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 8 * g + 4 * half;
+      const f32x4 o4 = load4f(O + d0);
+      const f32x4 g4 = load4f(G + d0);
+      float dov[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float dg = dog[4 * g + e];
+        dov[e] = valid ? dg * g4[e] : 0.f;
+        dsum += dov[e] * o4[e];
+        if (valid) {
+          const int64_t o = (int64_t)(h * AD + d0 + e) * pitch + p;
+          cm_dg[o] = cvt<T>(dg * o4[e] * g4[e] * (1.f - g4[e]));
+          bf.cm_go[o] = cvt<T>(o4[e] * g4[e]);
+        }
+        dot[(int64_t)(d0 + e) * np] = cvt<T>(dov[e]);
+      }
+      store4(dor + d0, dov[0], dov[1], dov[2], dov[3]);
+    }
+    dsum += xor32(dsum);
+    if (half == 0) bf.dd[rh * np + j] = dsum;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dkdv: per (row, head, 32 keys); lane = key
+// ---------------------------------------------------------------------------
+template <typename T, int H>
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdBufs<T> bf, int B, int N, int np,
+                                                            float scale) {
+  const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
+  const int tiles1 = np / 32;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile >= (int64_t)B * N * H * tiles1) return;
+  const int kt = (int)(tile % tiles1);
+  const int64_t rh = tile / tiles1;
+  const int h = (int)(rh % H);
+  const int64_t br = rh / H;
+  const int b = (int)(br / N);
+  const int key = kt * 32 + t32;
+  const bool kexists = key < N;
+  const float km = bf.kmask[br * np + key];
+  const T* Q = bf.qr + rh * np * AD;
+  const T* QT = bf.qt + rh * AD * np;
+  const T* K = bf.kr + rh * np * AD + (int64_t)kt * 32 * AD;
+  const T* V = bf.vr + rh * np * AD + (int64_t)kt * 32 * AD;
+  const T* DO = bf.dor + rh * np * AD;
+  const T* DOT = bf.dot + rh * AD * np;
+  const T* Bh = bf.bias + ((int64_t)b * H + h) * N * N;
+  const float* mr = bf.mrow + rh * np;
+  const float* lr = bf.linv + rh * np;
+  const float* dr = bf.dd + rh * np;
+
+  f32x16 dk = zero16(), dv = zero16();
+  for (int qt = 0; qt < tiles1; ++qt) {
+    const f32x16 sa = qk_tile<T>(Q + (int64_t)qt * 32 * AD, K);   // [q][key]: lane = key
+    const f32x16 pa = qk_tile<T>(DO + (int64_t)qt * 32 * AD, V);  // dP
+    float pv[16], ds[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int q0 = qt * 32 + 8 * g + 4 * half;
+      const f32x4 m4 = *reinterpret_cast<const f32x4*>(mr + q0);
+      const f32x4 l4 = *reinterpret_cast<const f32x4*>(lr + q0);
+      const f32x4 d4 = *reinterpret_cast<const f32x4*>(dr + q0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int q = q0 + e;
+        const float bv = (q < N && kexists) ? to_f32(Bh[(int64_t)q * N + key]) : 0.f;
+        const float s = score_of(sa[4 * g + e], scale, bv, km, kexists);
+        const float pr = __expf(s - m4[e]) * l4[e];
+        pv[4 * g + e] = pr;
+        ds[4 * g + e] = pr * (pa[4 * g + e] - d4[e]);
+      }
+    }
+    Frag<T> fp[2], fs[2], fa[2];
+    vals_to_frags<T>(fp, pv);
+    vals_to_frags<T>(fs, ds);
+    dmajor_frags<T>(fa, DOT, np, qt * 32);
+    mma(dv, fa[0], fp[0]);
+    mma(dv, fa[1], fp[1]);
+    dmajor_frags<T>(fa, QT, np, qt * 32);
+    mma(dk, fa[0], fs[0]);
+    mma(dk, fa[1], fs[1]);
+  }
+  T* dko = bf.dk + (rh * np + key) * AD;
+  T* dvo = bf.dv + (rh * np + key) * AD;
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    const int d0 = 8 * g + 4 * half;
+    store4(dko + d0, scale * dk[4 * g], scale * dk[4 * g + 1], scale * dk[4 * g + 2], scale * dk[4 * g + 3]);
+    store4(dvo + d0, dv[4 * g], dv[4 * g + 1], dv[4 * g + 2], dv[4 * g + 3]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dq: per (row, head, 32 queries); lane = query
+// ---------------------------------------------------------------------------
+template <typename T, int H>
+__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdBufs<T> bf, int B, int N, int np,
+                                                          float scale) {
+  const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
+  const int tiles1 = np / 32;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile >= (int64_t)B * N * H * tiles1) return;
+  const int qt = (int)(tile % tiles1);
+  const int64_t rh = tile / tiles1;
+  const int h = (int)(rh % H);
+  const int64_t br = rh / H;
+  const int b = (int)(br / N);
+  const int q = qt * 32 + t32;
+  const T* Q = bf.qr + rh * np * AD + (int64_t)qt * 32 * AD;
+  const T* DO = bf.dor + rh * np * AD + (int64_t)qt * 32 * AD;
+  const T* K = bf.kr + rh * np * AD;
+  const T* KT = bf.kt + rh * AD * np;
+  const T* V = bf.vr + rh * np * AD;
+  const T* Bh = bf.bias + ((int64_t)b * H + h) * N * N;
+  const float* km = bf.kmask + br * np;
+  const float mq = bf.mrow[rh * np + q];
+  const float lq = bf.linv[rh * np + q];
+  const float dq_ = bf.dd[rh * np + q];
+
+  f32x16 dq = zero16();
+  for (int kt = 0; kt < tiles1; ++kt) {
+    const f32x16 sa = qk_tile<T>(K + (int64_t)kt * 32 * AD, Q);   // [key][q]: lane = q
+    const f32x16 pa = qk_tile<T>(V + (int64_t)kt * 32 * AD, DO);  // dP^T
+    float ds[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int k0 = kt * 32 + 8 * g + 4 * half;
+      const f32x4 k4 = *reinterpret_cast<const f32x4*>(km + k0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int key = k0 + e;
+        const float bv = (q < N && key < N) ? to_f32(Bh[(int64_t)q * N + key]) : 0.f;
+        const float s = score_of(sa[4 * g + e], scale, bv, k4[e], key < N);
+        const float pr = __expf(s - mq) * lq;
+        ds[4 * g + e] = pr * (pa[4 * g + e] - dq_);
+      }
+    }
+    Frag<T> fs[2], fk[2];
+    vals_to_frags<T>(fs, ds);
+    dmajor_frags<T>(fk, KT, np, kt * 32);
+    mma(dq, fk[0], fs[0]);
+    mma(dq, fk[1], fs[1]);
+  }
+  T* dqo = bf.dq + (rh * np + q) * AD;
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+    store4(dqo + 8 * g + 4 * half, scale * dq[4 * g], scale * dq[4 * g + 1], scale * dq[4 * g + 2],
+           scale * dq[4 * g + 3]);
+}
+
+// ---------------------------------------------------------------------------
+// dbias: per (batch, head, 32 queries, 32 keys), summed over the rows; lane = query
+// ---------------------------------------------------------------------------
+template <typename T, int H>
+__global__ __launch_bounds__(256) void attn_bwd_dbias_kernel(AttnBwdBufs<T> bf, int B, int N, int np,
+                                                             float scale) {
+  const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
+  const int t1 = np / 32;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile >= (int64_t)B * H * t1 * t1) return;
+  const int kt = (int)(tile % t1);
+  const int qt = (int)((tile / t1) % t1);
+  const int h = (int)((tile / ((int64_t)t1 * t1)) % H);
+  const int b = (int)(tile / ((int64_t)t1 * t1 * H));
+  const int q = qt * 32 + t32;
+  const T* Bh = bf.bias + ((int64_t)b * H + h) * N * N;
+  float bv[16];
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int key = kt * 32 + 8 * g + 4 * half + e;
+      bv[4 * g + e] = (q < N && key < N) ? to_f32(Bh[(int64_t)q * N + key]) : 0.f;
+    }
+  float acc[16];
+#pragma unroll
+  for (int e = 0; e < 16; ++e) acc[e] = 0.f;
+  for (int r = 0; r < N; ++r) {
+    const int64_t br = (int64_t)b * N + r;
+    const int64_t rh = br * H + h;
+    const f32x16 sa = qk_tile<T>(bf.kr + (rh * np + (int64_t)kt * 32) * AD,
+                                 bf.qr + (rh * np + (int64_t)qt * 32) * AD);
+    const f32x16 pa = qk_tile<T>(bf.vr + (rh * np + (int64_t)kt * 32) * AD,
+                                 bf.dor + (rh * np + (int64_t)qt * 32) * AD);
+    const float mq = bf.mrow[rh * np + q];
+    const float lq = bf.linv[rh * np + q];
+    const float dq_ = bf.dd[rh * np + q];
+    const float* km = bf.kmask + br * np;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int k0 = kt * 32 + 8 * g + 4 * half;
+      const f32x4 k4 = *reinterpret_cast<const f32x4*>(km + k0);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float s = score_of(sa[4 * g + e], scale, bv[4 * g + e], k4[e], k0 + e < N);
+        const float pr = __expf(s - mq) * lq;
+        acc[4 * g + e] += pr * (pa[4 * g + e] - dq_);
+      }
+    }
+  }
+  if (q >= N) return;
+  float* dst = bf.db + (((int64_t)b * H + h) * N + q) * N;
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int key = kt * 32 + 8 * g + 4 * half + e;
+      if (key < N) dst[key] = acc[4 * g + e];
+    }
+}
+
+// ---------------------------------------------------------------------------
+// pro: dxn and the LayerNorm backward; per 32-position tile of one row
+// ---------------------------------------------------------------------------
+template <typename T, int C, int H>
+__global__ __launch_bounds__(256) void attn_bwd_pro_kernel(const T* __restrict__ x, T* __restrict__ dx,
+                                                           AttnBwdW<T> w, AttnBwdBufs<T> bf, int B,
+                                                           int N, int np, int starting, float eps) {
+  constexpr int CH = H * AD;
+  const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
+  const int jtiles = np / 32;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile >= (int64_t)B * N * jtiles) return;
+  const int jt = (int)(tile % jtiles);
+  const int r = (int)((tile / jtiles) % N);
+  const int b = (int)(tile / ((int64_t)jtiles * N));
+  const int j = jt * 32 + t32;
+  const bool valid = j < N;
+  const int64_t xp = valid ? ((int64_t)b * N + (starting ? r : j)) * N + (starting ? j : r) : 0;
+  const int64_t p = ((int64_t)b * N + r) * N + j;
+  const int64_t pitch = bf.pitch;
+
+  RowHalf<C> rhx;
+  load_row_half<T, C>(rhx, x + xp * C, valid);
+  const f32x2 st = row_stats<C>(rhx, eps);
+
+  f32x16 dzn[C / 32];
+#pragma unroll
+  for (int nt = 0; nt < C / 32; ++nt) dzn[nt] = zero16();
+  const T* src[3] = {bf.dq, bf.dk, bf.dv};
+  const T* wts[4] = {w.wt_q, w.wt_k, w.wt_v, w.wt_g};
+#pragma unroll 1
+  for (int kind = 0; kind < 4; ++kind) {
+#pragma unroll 1
+    for (int h = 0; h < H; ++h) {
+      float d[16];
+      if (kind < 3) {
+        const T* s = src[kind] + ((((int64_t)b * N + r) * H + h) * np + j) * AD;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 v4 = valid ? load4f(s + 8 * g + 4 * half) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) d[4 * g + e] = v4[e];
+        }
+        if (valid) {
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              bf.cm_stack[(int64_t)(kind * CH + h * AD + 8 * g + 4 * half + e) * pitch + p] =
+                  cvt<T>(d[4 * g + e]);
+        }
+      } else {
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            d[4 * g + e] = valid ? to_f32(bf.cm_stack[(int64_t)(3 * CH + h * AD + 8 * g + 4 * half + e) * pitch + p]) : 0.f;
+      }
+      Frag<T> f[2];
+      vals_to_frags<T>(f, d);
+#pragma unroll
+      for (int nt2 = 0; nt2 < C / 32; ++nt2)
+#pragma unroll
+        for (int gp = 0; gp < 2; ++gp) {
+          Frag<T> wf;
+          load_wfrag<T>(wf, wts[kind], nt2, 2 * h + gp, CH / 16);
+          mma(dzn[nt2], wf, f[gp]);
+        }
+    }
+  }
+  // triangle bias: dxn += sum_h dB[h][r][j] W_b[h][.]
+  float dtri[H];
+#pragma unroll
+  for (int h = 0; h < H; ++h) {
+    dtri[h] = valid ? bf.db[(((int64_t)b * H + h) * N + r) * N + j] : 0.f;
+    if (valid && half == 0) bf.cm_dtri[(int64_t)h * pitch + p] = cvt<T>(dtri[h]);
+  }
+  float xh[C / 2];
+  float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int nt = 0; nt < C / 32; ++nt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int c0 = nt * 32 + 8 * g + 4 * half;
+      const f32x4 x4 = valid ? load4f(x + xp * C + c0) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float t = dzn[nt][4 * g + e];
+#pragma unroll
+        for (int h = 0; h < H; ++h) t += dtri[h] * w.wb_raw[h * C + c0 + e];
+        dzn[nt][4 * g + e] = t;
+        const float xv = (x4[e] - st[0]) * st[1];
+        xh[16 * nt + 4 * g + e] = xv;
+        const float dxh = w.ln_w[c0 + e] * t;
+        s1 += dxh;
+        s2 += dxh * xv;
+      }
+    }
+  s1 += xor32(s1);
+  s2 += xor32(s2);
+  const float m1 = s1 * (1.0f / C), m2 = s2 * (1.0f / C);
+  if (!valid) return;
+#pragma unroll
+  for (int nt = 0; nt < C / 32; ++nt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int c0 = nt * 32 + 8 * g + 4 * half;
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float xv = xh[16 * nt + 4 * g + e];
+        const float t = dzn[nt][4 * g + e];
+        o[e] = st[1] * (w.ln_w[c0 + e] * t - m1 - xv * m2);
+        bf.cm_xh[(int64_t)(c0 + e) * pitch + p] = cvt<T>(xv);
+        bf.cm_dxn[(int64_t)(c0 + e) * pitch + p] = cvt<T>(t);
+      }
+      store4(dx + xp * C + c0, o[0], o[1], o[2], o[3]);
+    }
+}
+
+// dW_b[h][c] = W3[c][h] gamma[c] + s[h] beta[c]  (W3 = sum_s part[s][c][h], 64 columns)
+__global__ void attn_dwb_finish_kernel(const float* __restrict__ part, int nsplit, int C, int H,
+                                       const float* __restrict__ gamma, const float* __restrict__ beta,
+                                       const float* __restrict__ sums, float* __restrict__ dst) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= H * C) return;
+  const int h = idx / C, c = idx % C;
+  float a = 0.f;
+  for (int s = 0; s < nsplit; ++s) a += part[((int64_t)s * C + c) * 64 + h];
+  dst[idx] = a * gamma[c] + sums[h] * beta[c];
+}
+
+// ---------------------------------------------------------------------------
+// Workspace
+// ---------------------------------------------------------------------------
+template <typename T> struct AttnBwdWs {
+  AttnBwdW<T> w;
+  AttnBwdBufs<T> b;
+  float *part1, *part2, *part3, *red, *sums_stack, *sums_dy, *sums_dxn, *dots_dxn, *sums_dtri;
+};
+
+template <typename T>
+static AttnBwdWs<T> carve_attn_bwd(Carve& cv, int64_t B, int64_t N, int C, int H) {
+  const int CH = H * AD;
+  AttnBwdWs<T> a;
+  AttnBwdW<T>& w = a.w;
+  w.w_q = cv.take<T>(packed_elems(CH, C));
+  w.w_k = cv.take<T>(packed_elems(CH, C));
+  w.w_v = cv.take<T>(packed_elems(CH, C));
+  w.w_g = cv.take<T>(packed_elems(CH, C));
+  w.w_b = cv.take<T>(packed_elems(H, C));
+  w.b_q = cv.take<float>(CH);
+  w.b_k = cv.take<float>(CH);
+  w.b_v = cv.take<float>(CH);
+  w.b_g = cv.take<float>(CH);
+  w.b_b = cv.take<float>(32);
+  w.wt_q = cv.take<T>(packed_elems(C, CH));
+  w.wt_k = cv.take<T>(packed_elems(C, CH));
+  w.wt_v = cv.take<T>(packed_elems(C, CH));
+  w.wt_g = cv.take<T>(packed_elems(C, CH));
+  w.wt_o = cv.take<T>(packed_elems(CH, C));
+  w.wb_raw = cv.take<float>((int64_t)H * C);
+  w.ln_w = cv.take<float>(C);
+  w.ln_b = cv.take<float>(C);
+  AttnBwdBufs<T>& b = a.b;
+  const int64_t np = round_up(N, 32);
+  const int64_t hp = B * N * H * np * AD;
+  T** big[] = {&b.qr, &b.qt, &b.kr, &b.kt, &b.vr, &b.vt, &b.o, &b.dor, &b.dot, &b.dq, &b.dk, &b.dv};
+  for (T** t : big) *t = cv.take<T>(hp);
+  b.gt = cv.take<T>(B * N * np * CH);
+  b.bias = cv.take<T>(B * H * N * N);
+  b.kmask = cv.take<float>(B * N * np);
+  b.mrow = cv.take<float>(B * N * H * np);
+  b.linv = cv.take<float>(B * N * H * np);
+  b.dd = cv.take<float>(B * N * H * np);
+  b.db = cv.take<float>(B * H * N * N);
+  b.pitch = round_up(B * N * N, 64);
+  b.cm_stack = cv.take<T>(4 * CH * b.pitch);
+  b.cm_xh = cv.take<T>(C * b.pitch);
+  b.cm_dxn = cv.take<T>(C * b.pitch);
+  b.cm_dy = cv.take<T>(C * b.pitch);
+  b.cm_go = cv.take<T>(CH * b.pitch);
+  b.cm_dtri = cv.take<T>(64 * b.pitch);
+  a.part1 = cv.take<float>(wgrad_part_floats(4 * CH, C, b.pitch));
+  a.part2 = cv.take<float>(wgrad_part_floats(C, CH, b.pitch));
+  a.part3 = cv.take<float>(wgrad_part_floats(C, 64, b.pitch));
+  a.red = cv.take<float>((int64_t)2 * 4 * CH * kRowSegs);
+  a.sums_stack = cv.take<float>(4 * CH);
+  a.sums_dy = cv.take<float>(C);
+  a.sums_dxn = cv.take<float>(C);
+  a.dots_dxn = cv.take<float>(C);
+  a.sums_dtri = cv.take<float>(64);
+  return a;
+}
+
+template <typename T>
+static int pack_attn_bwd(const gtk_tri_attn_weights* wt, AttnBwdW<T>& w, int C, int H,
+                         hipStream_t st) {
+  const int CH = H * AD, wd = wt->dtype;
+  int rc;
+  if ((rc = launch_to_f32(w.ln_w, wt->ln_w, wd, C, 1.f, 1.f, st))) return rc;
+  if ((rc = launch_to_f32(w.ln_b, wt->ln_b, wd, C, 1.f, 0.f, st))) return rc;
+  struct Lin { T* dst; float* bdst; const void* wsrc; const void* bsrc; int out; };
+  const Lin lins[5] = {{w.w_q, w.b_q, wt->q_w, nullptr, CH}, {w.w_k, w.b_k, wt->k_w, nullptr, CH},
+                       {w.w_v, w.b_v, wt->v_w, nullptr, CH}, {w.w_g, w.b_g, wt->g_w, wt->g_b, CH},
+                       {w.w_b, w.b_b, wt->tri_w, nullptr, H}};
+  for (const Lin& l : lins) {
+    if ((rc = launch_pack<T>(l.dst, l.wsrc, wd, l.out, C, C, 1, 1.f, st, w.ln_w))) return rc;
+    if ((rc = launch_fold_bias(l.bdst, l.wsrc, l.bsrc, wd, w.ln_b, l.out, C, C, 1, 1.f, st))) return rc;
+  }
+  T* wts[4] = {w.wt_q, w.wt_k, w.wt_v, w.wt_g};
+  const void* srcs[4] = {wt->q_w, wt->k_w, wt->v_w, wt->g_w};
+  for (int k = 0; k < 4; ++k)
+    if ((rc = launch_pack_acc<T>(wts[k], srcs[k], wd, C, CH, 1, C, st))) return rc;
+  if ((rc = launch_pack<T>(w.wt_o, wt->o_w, wd, CH, C, 1, CH, 1.f, st))) return rc;
+  return launch_to_f32(w.wb_raw, wt->tri_w, wd, H * C, 1.f, 0.f, st);
+}
+
+template <typename T, int C, int H>
+static int bwd_triattn(const void* x, const float* mask, const void* dy,
+                       const gtk_tri_attn_weights* wts, void* dx, const gtk_tri_attn_grads* gr,
+                       int64_t B, int64_t N, int starting, float eps, void* ws, hipStream_t st) {
+  constexpr int CH = H * AD;
+  Carve cv(ws, SIZE_MAX);
+  AttnBwdWs<T> a = carve_attn_bwd<T>(cv, B, N, C, H);
+  int rc;
+  if ((rc = pack_attn_bwd<T>(wts, a.w, C, H, st))) return rc;
+  const int np = (int)round_up(N, 32);
+  const int64_t P = B * N * N, pitch = a.b.pitch;
+  const float scale = 1.0f / sqrtf((float)AD);
+  const int64_t rowtiles = B * N * (np / 32);
+  const int64_t headtiles = B * N * H * (np / 32);
+  const int64_t pairtiles = B * H * (int64_t)(np / 32) * (np / 32);
+  GTK_REQUIRE(headtiles / 4 < (1ll << 31) && pairtiles / 4 < (1ll << 31), GTK_EUNSUPPORTED,
+              "attention backward grid too large");
+  auto g4 = [](int64_t t) { return (unsigned)((t + 3) / 4); };
+  {
+    StageTimer timer("triattn_bwd_proj", st);
+    attn_bwd_proj_kernel<T, C, H><<<g4(rowtiles), 256, 0, st>>>((const T*)x, mask, a.w, a.b,
+                                                                 (int)B, (int)N, np, starting, eps);
+    GTK_LAUNCH_CHECK();
+  }
+  {
+    StageTimer timer("triattn_bwd_fwd", st);
+    attn_bwd_fwd_kernel<T, H><<<g4(headtiles), 256, 0, st>>>(a.b, (int)B, (int)N, np, scale);
+    GTK_LAUNCH_CHECK();
+  }
+  {
+    StageTimer timer("triattn_bwd_epi", st);
+    attn_bwd_epi_kernel<T, C, H><<<g4(rowtiles), 256, 0, st>>>((const T*)dy, a.w, a.b, (int)B,
+                                                                (int)N, np, starting);
+    GTK_LAUNCH_CHECK();
+  }
+  {
+    StageTimer timer("triattn_bwd_dkdv", st);
+    attn_bwd_dkdv_kernel<T, H><<<g4(headtiles), 256, 0, st>>>(a.b, (int)B, (int)N, np, scale);
+    GTK_LAUNCH_CHECK();
+  }
+  {
+    StageTimer timer("triattn_bwd_dq", st);
+    attn_bwd_dq_kernel<T, H><<<g4(headtiles), 256, 0, st>>>(a.b, (int)B, (int)N, np, scale);
+    GTK_LAUNCH_CHECK();
+  }
+  {
+    StageTimer timer("triattn_bwd_dbias", st);
+    attn_bwd_dbias_kernel<T, H><<<g4(pairtiles), 256, 0, st>>>(a.b, (int)B, (int)N, np, scale);
+    GTK_LAUNCH_CHECK();
+  }
+  // rows H..63 of the dtri operand stay zero
+  if ((rc = launch_zero(a.b.cm_dtri + (int64_t)H * pitch, (size_t)(64 - H) * pitch * sizeof(T), st)))
+    return rc;
+  {
+    StageTimer timer("triattn_bwd_pro", st);
+    attn_bwd_pro_kernel<T, C, H><<<g4(rowtiles), 256, 0, st>>>((const T*)x, (T*)dx, a.w, a.b,
+                                                                (int)B, (int)N, np, starting, eps);
+    GTK_LAUNCH_CHECK();
+  }
+  const AttnBwdBufs<T>& b = a.b;
+  if ((rc = launch_zero_tail<T>(b.cm_stack, 4 * CH, pitch, P, st))) return rc;
+  if ((rc = launch_zero_tail<T>(b.cm_xh, C, pitch, P, st))) return rc;
+  if ((rc = launch_zero_tail<T>(b.cm_dy, C, pitch, P, st))) return rc;
+  if ((rc = launch_zero_tail<T>(b.cm_go, CH, pitch, P, st))) return rc;
+  if ((rc = launch_zero_tail<T>(b.cm_dtri, H, pitch, P, st))) return rc;
+  if ((rc = launch_rowred<T>(b.cm_stack, nullptr, 4 * CH, pitch, P, a.red, a.sums_stack, nullptr, st))) return rc;
+  if ((rc = launch_rowred<T>(b.cm_dy, nullptr, C, pitch, P, a.red, a.sums_dy, nullptr, st))) return rc;
+  if ((rc = launch_rowred<T>(b.cm_dxn, b.cm_xh, C, pitch, P, a.red, a.sums_dxn, a.dots_dxn, st))) return rc;
+  if ((rc = launch_rowred<T>(b.cm_dtri, nullptr, H, pitch, P, a.red, a.sums_dtri, nullptr, st))) return rc;
+  {
+    StageTimer timer("triattn_bwd_wgrad", st);
+    if ((rc = launch_wgrad<T>(b.cm_stack, b.cm_xh, a.part1, 4 * CH, C, pitch, st))) return rc;
+    if ((rc = launch_wgrad<T>(b.cm_dy, b.cm_go, a.part2, C, CH, pitch, st))) return rc;
+    if ((rc = launch_wgrad<T>(b.cm_xh, b.cm_dtri, a.part3, C, 64, pitch, st))) return rc;
+  }
+  float* wdst[4] = {gr->q_w, gr->k_w, gr->v_w, gr->g_w};
+  for (int k = 0; k < 4; ++k)
+    if ((rc = launch_wgrad_finish(a.part1, 4 * CH, C, pitch, k * CH, CH, a.sums_stack, a.w.ln_w,
+                                  a.w.ln_b, wdst[k], st)))
+      return rc;
+  if ((rc = launch_copy_f32(gr->g_b, a.sums_stack + 3 * CH, CH, st))) return rc;
+  if ((rc = launch_wgrad_finish(a.part2, C, CH, pitch, 0, C, nullptr, nullptr, nullptr, gr->o_w, st)))
+    return rc;
+  if ((rc = launch_copy_f32(gr->o_b, a.sums_dy, C, st))) return rc;
+  attn_dwb_finish_kernel<<<(H * C + 255) / 256, 256, 0, st>>>(
+      a.part3, wgrad_plan(C, pitch).nsplit, C, H, a.w.ln_w, a.w.ln_b, a.sums_dtri, gr->tri_w);
+  GTK_LAUNCH_CHECK();
+  if ((rc = launch_copy_f32(gr->ln_w, a.dots_dxn, C, st))) return rc;
+  if ((rc = launch_copy_f32(gr->ln_b, a.sums_dxn, C, st))) return rc;
+  return GTK_OK;
+}
+
+}  // namespace gtk
+
+using namespace gtk;
+
+static bool attn_bwd_shape_ok(int64_t c_in, int64_t c_h, int64_t H) {
+  return c_in == 128 && H == 4 && c_h == H * AD;
+}
+
+extern "C" size_t gtk_tri_attn_backward_workspace_size(int64_t B, int64_t N, int64_t c_in,
+                                                       int64_t c_h, int64_t H, int dtype) {
+  if (!attn_bwd_shape_ok(c_in, c_h, H) || B < 0 || N < 0) return 0;
+  if (dtype != GTK_F32 && dtype != GTK_BF16) return 0;
+  Carve cv(nullptr, SIZE_MAX);
+  if (dtype == GTK_F32) carve_attn_bwd<float>(cv, B, N, (int)c_in, (int)H);
+  else carve_attn_bwd<bf16>(cv, B, N, (int)c_in, (int)H);
+  return cv.off;
+}
+
+extern "C" int gtk_tri_attn_backward(const void* x, const float* mask, const void* dy,
+                                     const gtk_tri_attn_weights* w, void* dx,
+                                     const gtk_tri_attn_grads* grads, int64_t B, int64_t N,
+                                     int64_t c_in, int64_t c_h, int64_t H, int starting, float eps,
+                                     int dtype, void* ws, size_t ws_bytes, void* stream) {
+  GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL,
+              "gtk_tri_attn_backward: bad dtype %d", dtype);
+  GTK_REQUIRE(attn_bwd_shape_ok(c_in, c_h, H), GTK_EUNSUPPORTED,
+              "gtk_tri_attn_backward: c_in=%lld c_h=%lld H=%lld unsupported (c_in=128, H=4, d=32)",
+              (long long)c_in, (long long)c_h, (long long)H);
+  GTK_REQUIRE(B >= 0 && N >= 0 && N <= 4096, GTK_EINVAL, "gtk_tri_attn_backward: bad shape");
+  if (B == 0 || N == 0) return GTK_OK;
+  GTK_REQUIRE(x && dy && w && dx && grads && ws, GTK_EINVAL, "gtk_tri_attn_backward: null pointer");
+  GTK_REQUIRE(w->dtype == GTK_F32 || w->dtype == GTK_BF16, GTK_EINVAL,
+              "gtk_tri_attn_backward: bad weight dtype %d", w->dtype);
+  GTK_REQUIRE(w->tri_w && w->q_w && w->k_w && w->v_w && w->g_w && w->o_w, GTK_EINVAL,
+              "gtk_tri_attn_backward: null weight");
+  const float* gp[] = {grads->ln_w, grads->ln_b, grads->tri_w, grads->q_w, grads->k_w,
+                       grads->v_w,  grads->g_w,  grads->g_b,   grads->o_w, grads->o_b};
+  for (const float* p : gp) GTK_REQUIRE(p, GTK_EINVAL, "gtk_tri_attn_backward: null gradient pointer");
+  const size_t need = gtk_tri_attn_backward_workspace_size(B, N, c_in, c_h, H, dtype);
+  GTK_REQUIRE(ws_bytes >= need, GTK_EWORKSPACE, "gtk_tri_attn_backward: workspace %zu < %zu bytes",
+              ws_bytes, need);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == GTK_F32)
+    return bwd_triattn<float, 128, 4>(x, mask, dy, w, dx, grads, B, N, starting, eps, ws, st);
+  return bwd_triattn<bf16, 128, 4>(x, mask, dy, w, dx, grads, B, N, starting, eps, ws, st);
+}

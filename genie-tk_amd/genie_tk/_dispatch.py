@@ -1,10 +1,12 @@
 """Shared plumbing of the modules' kernel path: capability checks, the packed
 weight cache and the autograd rule.
 
-The HIP kernels are forward-only.  A call that must produce gradients
-(autograd enabled and the input or a parameter requires grad) runs the
-module's PyTorch path, which is autograd-capable; every other call on a GPU
-tensor with ``use_fused_kernel=True`` runs the HIP kernels.
+A call on a GPU tensor with ``use_fused_kernel=True`` runs the HIP kernels.
+When it must produce gradients (autograd enabled and the input or a
+parameter requires grad), the triangle modules run their kernel forward
+inside an autograd Function whose backward is the kernels' backward; the
+modules without backward kernels (PairTransition) run their PyTorch path
+then.
 """
 from __future__ import annotations
 

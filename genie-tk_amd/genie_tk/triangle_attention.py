@@ -4,10 +4,12 @@ Drop-in for ``src/genie_tk/triangle_attention.py`` of the reference: same
 classes, constructor arguments, parameter names and ``forward(x, mask=None)``
 returning the update (no residual).
 
-Kernel path (``use_fused_kernel=True``, GPU tensor, no autograd needed):
+Kernel path (``use_fused_kernel=True``, GPU tensor):
 ``genie_tk._C.tri_attn_forward`` — a gfx950 prologue (LN, q/k/v/gate and
 triangle-bias projections on the matrix cores) and a flash-style kernel
 (online softmax, bias streamed from HBM, gate and output projection fused).
+When autograd needs gradients the same forward runs inside
+``_TriAttnFunction``, whose backward is ``genie_tk._C.tri_attn_backward``.
 PyTorch path: ``_forward_pytorch``, the reference fallback semantics
 (triangle_attention.py:100-143).
 
@@ -30,6 +32,34 @@ from genie_tk.primitives import Attention, Linear
 from genie_tk.utils import has_cuda_kernels, permute_final_dims
 
 _CUDA_AVAILABLE = has_cuda_kernels()
+
+
+class _TriAttnFunction(torch.autograd.Function):
+    """The update on the HIP kernels, forward and backward.
+
+    The reference trains through torch autograd of its PyTorch path
+    (triangle_attention.py:100-143, primitives.py:114-178); this computes the
+    same gradients on the kernels.  Activations are recomputed in the backward
+    from x (only x, the mask and the parameters are saved)."""
+
+    @staticmethod
+    def forward(ctx, module, x, mask, chunk_size, *params):
+        ctx.module = module
+        ctx.save_for_backward(x, mask, *params)
+        return module._forward_cuda(x, mask, chunk_size=chunk_size)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, mask, *params = ctx.saved_tensors
+        mod = ctx.module
+        xb, mb, lead = _dispatch.flatten_batch(x, mask)
+        res = _ext.require().tri_attn_backward(
+            xb, mb, dy.reshape(xb.shape).to(x.dtype), list(params), mod.c_in, mod.c_hidden,
+            mod.no_heads, mod.starting, mod.layer_norm.eps)
+        dx = res[0].reshape(x.shape) if ctx.needs_input_grad[1] else None
+        grads = [g.to(p.dtype) if ctx.needs_input_grad[4 + k] else None
+                 for k, (g, p) in enumerate(zip(res[1:], params))]
+        return (None, dx, None, None, *grads)
 
 
 class TriangleAttention(nn.Module):
@@ -95,12 +125,14 @@ class TriangleAttention(nn.Module):
     def _pack(self, params, fp32: bool) -> Tensor:
         return _ext.require().tri_attn_pack(params, self.c_in, self.c_hidden, self.no_heads, fp32)
 
-    def _packed_params(self, fp32: bool) -> Tensor:
+    def _param_list(self):
         m = self.mha
-        ps = [self.layer_norm.weight, self.layer_norm.bias, self.linear.weight,
-              m.linear_q.weight, m.linear_k.weight, m.linear_v.weight,
-              m.linear_g.weight, m.linear_g.bias, m.linear_o.weight, m.linear_o.bias]
-        return self._packed.get(ps, fp32, self._pack)
+        return [self.layer_norm.weight, self.layer_norm.bias, self.linear.weight,
+                m.linear_q.weight, m.linear_k.weight, m.linear_v.weight,
+                m.linear_g.weight, m.linear_g.bias, m.linear_o.weight, m.linear_o.bias]
+
+    def _packed_params(self, fp32: bool) -> Tensor:
+        return self._packed.get(self._param_list(), fp32, self._pack)
 
     def _forward_cuda(self, x: Tensor, mask: Optional[Tensor] = None,
                       residual: bool = False, chunk_size: Optional[int] = None) -> Tensor:
@@ -140,9 +172,7 @@ class TriangleAttention(nn.Module):
                     and (chunk_size is None or x.dtype == torch.bfloat16)):
                 if not _dispatch.needs_autograd(x, self):
                     return self._forward_cuda(x, mask, chunk_size=chunk_size)
-                _dispatch.warn_once("tri_attn_grad", "genie_tk: gradients requested; "
-                                    "TriangleAttention runs its PyTorch path "
-                                    "(the HIP kernels are forward-only)")
+                return _TriAttnFunction.apply(self, x, mask, chunk_size, *self._param_list())
         return self._forward_pytorch(x, mask, chunk_size)
 
 

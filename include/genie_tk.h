@@ -228,6 +228,28 @@ int gtk_tri_attn_forward_chunked(const void* x, const float* mask, void* out, co
                                  int starting, int residual, float eps, int64_t chunk_rows,
                                  int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Backward of gtk_tri_attn_forward (update only, no residual): given dL/dy,
+ * writes dL/dx (element type dtype) and the gradient of every parameter
+ * (fp32, the layouts of gtk_tri_attn_weights).  The reference has no backward
+ * kernel: its gradients are torch autograd over TriangleAttention._forward_pytorch
+ * src/genie_tk/triangle_attention.py:100-143 and Attention.forward
+ * src/genie_tk/primitives.py:114-178, which this computes, including autograd's
+ * treatment of rows whose keys are all masked (their uniform softmax still
+ * passes its gradient to q, k and the triangle bias).  Activations are
+ * recomputed from x and the raw weights in w.  Gradients are written, not
+ * accumulated.  c_in == 128, H == 4, d == 32, N <= 4096. */
+typedef struct gtk_tri_attn_grads {
+  float *ln_w, *ln_b, *tri_w, *q_w, *k_w, *v_w, *g_w, *g_b, *o_w, *o_b;
+} gtk_tri_attn_grads;
+
+size_t gtk_tri_attn_backward_workspace_size(int64_t B, int64_t N, int64_t c_in, int64_t c_h,
+                                            int64_t H, int dtype);
+int gtk_tri_attn_backward(const void* x, const float* mask, const void* dy,
+                          const gtk_tri_attn_weights* w, void* dx, const gtk_tri_attn_grads* grads,
+                          int64_t B, int64_t N, int64_t c_in, int64_t c_h, int64_t H, int starting,
+                          float eps, int dtype, void* workspace, size_t workspace_bytes,
+                          void* stream);
+
 /* ------------------------------------------------------------------------
  * PairTransition fused with the pair-stack residual and mask.
  * Replaces PairTransition.forward src/genie_tk/pair_transform.py:64-84 and the

@@ -21,7 +21,7 @@ from typing import Dict, Optional, Tuple
 
 import numpy as np
 
-from oracle.pair_ops import Params, _p, contract, sigmoid
+from oracle.pair_ops import Params, _masked_scores, _p, _softmax_rows, contract, sigmoid
 
 Grads = Dict[str, np.ndarray]
 
@@ -113,3 +113,75 @@ def tri_mul_grad(z: np.ndarray, mask: Optional[np.ndarray], params: Params, outg
     dz, grads["layer_norm_in.weight"], grads["layer_norm_in.bias"] = layer_norm_bwd(
         zh, zr, P("layer_norm_in.weight"), dzn)
     return dz, grads
+
+
+def tri_attn_grad(x: np.ndarray, mask: Optional[np.ndarray], params: Params, starting: bool,
+                  no_heads: int, dy: np.ndarray, inf: float = 1e9, dtype=np.float64,
+                  eps: float = 1e-5) -> Tuple[np.ndarray, Grads]:
+    """Backward of pair_ops.tri_attn (triangle_attention.py:100-143,
+    primitives.py:114-178) for dL/dy.
+
+    The softmax gradient ds = p (dp - sum_k p dp) flows into q.k and the
+    triangle bias with derivative one, also for a row whose keys are all
+    masked: there the forward's scores are the constant -inf (absorbed in
+    fp32, primitives.py:156-158) and p is uniform, but torch autograd of the
+    reference still differentiates the sum qk + mask_bias + tri term by term.
+    That is the reference's gradient, and the one restated here.
+    """
+    P = lambda k: _p(params, k, dtype)  # noqa: E731
+    x = np.asarray(x, dtype=dtype)
+    dy = np.asarray(dy, dtype=dtype)
+    m = np.ones(x.shape[:-1], dtype=dtype) if mask is None else np.asarray(mask, dtype=dtype)
+    if not starting:
+        x, m, dy = x.swapaxes(1, 2), m.swapaxes(1, 2), dy.swapaxes(1, 2)
+    B, N, _, C = x.shape
+    H = no_heads
+    Wq, Wk, Wv = P("mha.linear_q.weight"), P("mha.linear_k.weight"), P("mha.linear_v.weight")
+    Wg, bg = P("mha.linear_g.weight"), P("mha.linear_g.bias")
+    Wo, bo = P("mha.linear_o.weight"), P("mha.linear_o.bias")
+    Wb = P("linear.weight")
+    ch = Wq.shape[0]
+    d = ch // H
+    scale = dtype(1.0 / np.sqrt(d))
+    xh, xr = layer_norm_fwd(x, eps)
+    xn = xh * P("layer_norm.weight") + P("layer_norm.bias")
+    tri = (xn @ Wb.T).transpose(0, 3, 1, 2)  # [B, H, Q, K]
+    g = {k: np.zeros_like(v, dtype=dtype) for k, v in params.items()}
+    dxn = np.zeros_like(xn)
+    dtri = np.zeros_like(tri)
+    heads = lambda t: t.reshape(N, H, d).transpose(1, 0, 2)  # noqa: E731  [J, ch] -> [H, J, d]
+    flat = lambda t: t.transpose(1, 0, 2).reshape(N, ch)    # noqa: E731
+    for b in range(B):
+        for i in range(N):
+            xi = xn[b, i]
+            q, k, v = heads(xi @ Wq.T), heads(xi @ Wk.T), heads(xi @ Wv.T)
+            s = _masked_scores((q @ k.transpose(0, 2, 1)) * scale, m[b, i][None, None, :],
+                               tri[b], inf, dtype)
+            p = _softmax_rows(s)
+            of = flat(p @ v)
+            gt = sigmoid(xi @ Wg.T + bg)
+            dyi = dy[b, i]
+            g["mha.linear_o.weight"] += dyi.T @ (of * gt)
+            g["mha.linear_o.bias"] += dyi.sum(axis=0)
+            dog = dyi @ Wo
+            dgpre = dog * of * gt * (1 - gt)
+            g["mha.linear_g.weight"] += dgpre.T @ xi
+            g["mha.linear_g.bias"] += dgpre.sum(axis=0)
+            do = heads(dog * gt)
+            dp = do @ v.transpose(0, 2, 1)                        # [H, Q, K]
+            dv = p.transpose(0, 2, 1) @ do                        # [H, K, d]
+            ds = p * (dp - (dp * p).sum(axis=-1, keepdims=True))
+            dtri[b] += ds
+            dq = (ds @ k) * scale
+            dk = (ds.transpose(0, 2, 1) @ q) * scale
+            for name, dt_, W in (("q", dq, Wq), ("k", dk, Wk), ("v", dv, Wv)):
+                g[f"mha.linear_{name}.weight"] += flat(dt_).T @ xi
+            dxn[b, i] += dgpre @ Wg + flat(dq) @ Wq + flat(dk) @ Wk + flat(dv) @ Wv
+    dtp = dtri.transpose(0, 2, 3, 1)                              # [B, Q, K, H]
+    dxn += dtp @ Wb
+    g["linear.weight"] = dtp.reshape(-1, H).T @ xn.reshape(-1, C)
+    dx, g["layer_norm.weight"], g["layer_norm.bias"] = layer_norm_bwd(
+        xh, xr, P("layer_norm.weight"), dxn)
+    if not starting:
+        dx = dx.swapaxes(1, 2)
+    return dx, g

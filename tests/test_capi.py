@@ -36,7 +36,8 @@ def lib():
                  "gtk_tri_mul_packed_size", "gtk_tri_attn_packed_size",
                  "gtk_tri_attn_workspace_size", "gtk_triangle_attention_workspace_size",
                  "gtk_fused_layernorm_linear_workspace_size",
-                 "gtk_tri_attn_workspace_size_chunked", "gtk_tri_mul_backward_workspace_size"):
+                 "gtk_tri_attn_workspace_size_chunked", "gtk_tri_mul_backward_workspace_size",
+                 "gtk_tri_attn_backward_workspace_size"):
         getattr(L, name).restype = sz
     L.gtk_triangle_mul_workspace_size.argtypes = [i64, i64, i64, ci]
     L.gtk_tri_mul_workspace_size.argtypes = [i64, i64, i64, i64, ci]
@@ -46,6 +47,9 @@ def lib():
     L.gtk_tri_mul_backward_workspace_size.argtypes = [i64, i64, i64, i64, ci]
     L.gtk_tri_mul_backward.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, ci, fp, fp, ci,
                                        vp, sz, vp]
+    L.gtk_tri_attn_backward_workspace_size.argtypes = [i64, i64, i64, i64, i64, ci]
+    L.gtk_tri_attn_backward.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, fp,
+                                        ci, vp, sz, vp]
     L.gtk_tri_attn_workspace_size_chunked.argtypes = [i64, i64, i64, i64, i64, i64, ci]
     L.gtk_triangle_attention_workspace_size.argtypes = [i64, i64, i64, i64, ci]
     L.gtk_fused_layernorm_linear_workspace_size.argtypes = [i64, i64, ci]
@@ -116,6 +120,9 @@ def test_workspace_sizes(lib):
     wb = lib.gtk_tri_mul_backward_workspace_size(1, 512, 128, 128, GTK_BF16)
     assert wb >= 8 * plane(1, 512, 128, 2) + 1280 * 512 * 512 * 2
     assert lib.gtk_tri_mul_backward_workspace_size(1, 512, 128, 96, GTK_BF16) == 0
+    # twelve [B][N][H][N][32] activation/gradient buffers at least
+    assert lib.gtk_tri_attn_backward_workspace_size(1, 512, 128, 128, 4, GTK_BF16) >= 12 * 512 * 512 * 128 * 2
+    assert lib.gtk_tri_attn_backward_workspace_size(1, 512, 128, 64, 4, GTK_BF16) == 0
 
 
 def _err(lib):
@@ -153,6 +160,12 @@ def test_bad_dtype_and_shapes_are_rejected(lib):
     rc = lib.gtk_tri_mul_backward(None, None, None, None, None, None, 1, 8, 128, 64, 1, 1e-5,
                                   1e-5, GTK_BF16, None, 0, None)
     assert rc == GTK_EINVAL and "null" in _err(lib)
+    rc = lib.gtk_tri_attn_backward(None, None, None, None, None, None, 1, 8, 128, 128, 8, 1,
+                                   1e-5, GTK_BF16, None, 0, None)
+    assert rc == GTK_EUNSUPPORTED and "H=8" in _err(lib)
+    rc = lib.gtk_tri_attn_backward(None, None, None, None, None, None, 1, 8, 128, 128, 4, 1,
+                                   1e-5, 5, None, 0, None)
+    assert rc == GTK_EINVAL and "dtype" in _err(lib)
     rc = lib.gtk_triangle_mul_outgoing(None, None, None, None, 1, 8, 24, GTK_BF16, None, 0, None)
     assert rc == GTK_EUNSUPPORTED and "multiple of 16" in _err(lib)
     rc = lib.gtk_triangle_attention_starting(None, None, None, None, None, 0.2, None, 1, 4, 8,
@@ -179,6 +192,8 @@ def test_empty_inputs_are_no_ops(lib):
                                          None) == GTK_OK
     assert lib.gtk_tri_mul_backward(None, None, None, None, None, None, 0, 8, 128, 128, 0, 1e-5,
                                     1e-5, GTK_BF16, None, 0, None) == GTK_OK
+    assert lib.gtk_tri_attn_backward(None, None, None, None, None, None, 3, 0, 128, 128, 4, 0,
+                                     1e-5, GTK_F32, None, 0, None) == GTK_OK
 
 
 def test_timing_report_when_idle(lib):

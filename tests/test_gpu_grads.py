@@ -18,7 +18,7 @@ import torch
 
 from oracle import grads
 from tests import helpers as H
-from tests.gpu_common import log, trimul_module
+from tests.gpu_common import log, triattn_module, trimul_module
 
 pytestmark = pytest.mark.gpu
 
@@ -80,4 +80,44 @@ def test_tri_mul_backward_runs_the_kernels(monkeypatch):
     y = mod(z)
     y.float().square().sum().backward()
     assert z.grad is not None and z.grad.shape == z.shape and torch.isfinite(z.grad).all()
+    assert all(p.grad is not None and torch.isfinite(p.grad).all() for p in mod.parameters())
+
+
+@pytest.mark.parametrize("dname", ["fp32", "bf16"])
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("N", [40, 77])
+def test_tri_attn_backward(dname, starting, N):
+    """Includes fully masked rows (the padded rows of the second batch
+    element), whose uniform softmax passes its gradient to q, k and the
+    triangle bias as torch autograd of the reference does."""
+    log(f"tri_attn backward {dname} starting={starting} N={N}")
+    dt = DT[dname]
+    P = H.draw_params(H.tri_attn_shapes(128, 128, 4), seed=N + 7, ln_random=True, bias_random=True)
+    x = H.pair_input(2, N, 128, seed=N + 8)
+    m = H.tail_mask(2, N, [N, N - 6])
+    dy = H.pair_input(2, N, 128, seed=N + 9)
+    if dname == "bf16":
+        P, x, dy = H.bf16_params(P), H.bf16_round(x), H.bf16_round(dy)
+    mod = triattn_module(P, starting, 4, dt)
+    xt = torch.from_numpy(x).to("cuda", dt).requires_grad_(True)
+    y = mod(xt, torch.from_numpy(m).to("cuda"))
+    y.backward(torch.from_numpy(dy).to("cuda", dt))
+    torch.cuda.synchronize()
+    dx_ref, g_ref = grads.tri_attn_grad(x, m, P, starting, 4, dy)
+    worst = [(_check_grad(_np(xt.grad), dx_ref, dname, "dx"), "dx")]
+    for name, prm in mod.named_parameters():
+        assert prm.grad is not None and prm.grad.dtype == dt, name
+        worst.append((_check_grad(_np(prm.grad), g_ref[name], dname, name), name))
+    log(f"  worst max|g - r| / max|r|: {max(worst)[0]:.2e} ({max(worst)[1]})")
+
+
+def test_tri_attn_backward_runs_the_kernels(monkeypatch):
+    P = H.draw_params(H.tri_attn_shapes(128, 128, 4), seed=11, bias_random=True)
+    mod = triattn_module(P, False, 4, torch.bfloat16)
+    monkeypatch.setattr(mod, "_forward_pytorch",
+                        lambda *a, **k: (_ for _ in ()).throw(AssertionError("fallback")))
+    x = torch.randn(1, 2, 33, 33, 128, device="cuda", dtype=torch.bfloat16, requires_grad=True)
+    y = mod(x)
+    y.float().square().sum().backward()
+    assert x.grad is not None and x.grad.shape == x.shape and torch.isfinite(x.grad).all()
     assert all(p.grad is not None and torch.isfinite(p.grad).all() for p in mod.parameters())

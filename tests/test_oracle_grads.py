@@ -97,3 +97,65 @@ def test_planted_contraction_mistake_is_caught():
         grads.contract_bwd = orig
     with pytest.raises(AssertionError):
         _fd_check(lambda zz: float((pair_ops.tri_mul(zz, mask, P, False, dtype=F64) * dy).sum()), z, dz)
+
+
+def _tri_attn_case(seed=0, B=2, N=4, C=6, ch=4, H=2):
+    P = H_.draw_params(H_.tri_attn_shapes(C, ch, H), seed, ln_random=True, bias_random=True)
+    P = {k: v.astype(F64) for k, v in P.items()}
+    rng = np.random.default_rng(seed + 1)
+    x = rng.standard_normal((B, N, N, C))
+    # every row keeps at least one key (the diagonal), some keys masked
+    mask = (rng.random((B, N, N)) > 0.3).astype(np.float32)
+    mask[:, np.arange(N), np.arange(N)] = 1.0
+    dy = rng.standard_normal(x.shape)
+    return P, x, mask, dy
+
+
+H_ = H
+
+
+@pytest.mark.parametrize("starting", [True, False])
+def test_tri_attn_grad_finite_differences(starting):
+    P, x, mask, dy = _tri_attn_case()
+    dx, g = grads.tri_attn_grad(x, mask, P, starting, 2, dy)
+    loss = lambda xx, PP: float((pair_ops.tri_attn(xx, mask, PP, starting, 2, dtype=F64) * dy).sum())  # noqa: E731
+    _fd_check(lambda xx: loss(xx, P), x, dx)
+    assert set(g) == set(P)
+    for key in P:
+        def f(v, key=key):
+            PP = dict(P)
+            PP[key] = v
+            return loss(x, PP)
+        _fd_check(f, P[key], g[key])
+
+
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float64, torch.float32])
+def test_tri_attn_grad_matches_torch_autograd(starting, dtype):
+    """float64 autograd without fully masked rows; float32 autograd with a
+    tail mask, whose padded rows are fully masked: there the fp32 reference's
+    scores absorb -inf and the softmax is uniform, and autograd still passes
+    its gradient to q.k and the triangle bias (the oracle's convention)."""
+    from genie_tk import TriangleAttentionEndingNode, TriangleAttentionStartingNode
+
+    P = H.draw_params(H.tri_attn_shapes(16, 8, 2), 3, ln_random=True, bias_random=True)
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((2, 7, 7, 16))
+    dy = rng.standard_normal(x.shape)
+    if dtype == torch.float64:
+        mask = (rng.random((2, 7, 7)) > 0.3).astype(np.float32)
+        mask[:, np.arange(7), np.arange(7)] = 1.0
+    else:
+        mask = H.tail_mask(2, 7, [7, 4])
+        x, dy = x.astype(np.float32), dy.astype(np.float32)
+    cls = TriangleAttentionStartingNode if starting else TriangleAttentionEndingNode
+    mod = cls(16, 8, 2, use_fused_kernel=False).to(dtype)
+    mod.load_state_dict(H.to_state_dict(P, dtype=dtype))
+    xt = torch.from_numpy(x).to(dtype).requires_grad_(True)
+    y = mod(xt, torch.from_numpy(mask).to(dtype))
+    (y * torch.from_numpy(dy).to(dtype)).sum().backward()
+    dx, g = grads.tri_attn_grad(x, mask, P, starting, 2, dy)
+    tol = dict(rtol=1e-9, atol=1e-10) if dtype == torch.float64 else dict(rtol=2e-4, atol=2e-4)
+    np.testing.assert_allclose(xt.grad.double().numpy(), dx, **tol)
+    for name, prm in mod.named_parameters():
+        np.testing.assert_allclose(prm.grad.double().numpy(), g[name], err_msg=name, **tol)
