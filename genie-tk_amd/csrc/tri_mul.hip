@@ -364,8 +364,10 @@ __global__ __launch_bounds__(64 * (TI / 64) * (TJ / 64)) void trimul_contract_bf
   constexpr int RPR = 1024 / (2 * BK);              // panel rows per 1 KiB copy
   constexpr int CPR = BK / 8;                       // 16-byte chunks per panel row
   static_assert((TI / RPR) % NW == 0 && (TJ / RPR) % NW == 0, "copies split evenly");
-  __shared__ __attribute__((aligned(1024))) bf16 ra_l[NS][TI * BK];
-  __shared__ __attribute__((aligned(1024))) bf16 rb_l[NS][TJ * BK];
+  // one LDS array: the A and Bm stages, reused for the output tile at the end
+  __shared__ __attribute__((aligned(1024))) bf16 ring[NS * (TI + TJ) * BK];
+  bf16(*ra_l)[TI * BK] = reinterpret_cast<bf16(*)[TI * BK]>(ring);
+  bf16(*rb_l)[TJ * BK] = reinterpret_cast<bf16(*)[TJ * BK]>(ring + NS * TI * BK);
 
   const int ti_n = Np / TI, tj_n = Np / TJ;
   const int64_t total = (int64_t)ti_n * tj_n * nplanes;
@@ -446,19 +448,39 @@ __global__ __launch_bounds__(64 * (TI / 64) * (TJ / 64)) void trimul_contract_bf
         for (int y = 0; y < 2; ++y) mma(acc[x][y], fb[kc][y], fa[kc][x]);  // rows j, cols i
   }
 
-  // acc[x][y]: lane holds X[i = wi + 32x + (l&31)][j = wj + 32y + 8g + 4h + r]
-  bf16* X = px + pl * plane;
+  // acc[x][y]: lane holds X[i = wi + 32x + (l&31)][j = wj + 32y + 8g + 4h + r].
+  // Stored straight from the accumulators, a store instruction would write
+  // 16 bytes into each of 32 rows.  The tile is transposed through the (now
+  // free) ring instead: [TI][TJ] bf16, 16-byte chunk c of row r at physical
+  // chunk c ^ (r & (CPO-1)), so the 32 rows of one accumulator write land in
+  // distinct chunks; then each lane stores 16 bytes and a wave writes whole
+  // rows of TJ*2 contiguous bytes.
+  constexpr int CPO = TJ / 8;  // 16-byte chunks per output row
+  static_assert(TI * TJ * 2 <= NS * (TI + TJ) * BK * 2, "output tile fits in the ring");
+  static_assert(CPO >= 16 && (64 * NW) % CPO == 0 && TI % (64 * NW / CPO) == 0, "store split");
+  bf16* tl = ring;
+  barrier_only();          // every wave is done with the last stage
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
-    const int i = i0 + wi + x * 32 + (lane & 31);
+    const int il = wi + x * 32 + (lane & 31);
 #pragma unroll
     for (int y = 0; y < 2; ++y)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int j = j0 + wj + y * 32 + 8 * g + 4 * half;
-        store4(X + (int64_t)i * Np + j, acc[x][y][4 * g + 0], acc[x][y][4 * g + 1],
-               acc[x][y][4 * g + 2], acc[x][y][4 * g + 3]);
+        const int jl = wj + y * 32 + 8 * g + 4 * half;
+        store4(tl + il * TJ + ((((jl >> 3) ^ (il & (CPO - 1))) << 3) | (jl & 7)), acc[x][y][4 * g + 0],
+               acc[x][y][4 * g + 1], acc[x][y][4 * g + 2], acc[x][y][4 * g + 3]);
       }
+  }
+  barrier_only();
+  bf16* X = px + pl * plane;
+  constexpr int RPI = 64 * NW / CPO;  // output rows per pass of the block
+  const int rr = (int)threadIdx.x / CPO, cc = (int)threadIdx.x % CPO;
+#pragma unroll
+  for (int r0 = 0; r0 < TI; r0 += RPI) {
+    const int r = r0 + rr;
+    const uint4 v = *reinterpret_cast<const uint4*>(tl + r * TJ + ((cc ^ (r & (CPO - 1))) << 3));
+    *reinterpret_cast<uint4*>(X + (int64_t)(i0 + r) * Np + j0 + cc * 8) = v;
   }
 }
 

@@ -103,7 +103,7 @@ def test_layernorm_linear_nn_layout(dname, d_in, d_out):
 # ------------------------------------------------------- raw contraction
 @pytest.mark.parametrize("dname", ["fp32", "bf16"])
 @pytest.mark.parametrize("outgoing", [True, False])
-@pytest.mark.parametrize("N,C", [(64, 32), (48, 16), (130, 32), (256, 64)])
+@pytest.mark.parametrize("N,C", [(64, 32), (48, 16), (130, 32), (256, 64), (384, 16)])
 def test_raw_triangle_mul(dname, outgoing, N, C):
     log(f"triangle_mul raw {dname} out={outgoing} N={N} C={C}")
     rng = np.random.default_rng(N * 7 + C)
