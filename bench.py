@@ -45,10 +45,15 @@ def trimul_flops(N: int, B: int = 1) -> dict:
 
 def triattn_flops(N: int, B: int = 1) -> dict:
     ch = HEADS * HEAD_DIM
-    return {
-        "triattn_prologue": 2.0 * B * N * N * C_Z * (4 * ch + HEADS),
-        "triattn_flash": 4.0 * B * HEADS * HEAD_DIM * N ** 3 + 2.0 * B * N * N * ch * C_Z,
-    }
+    core = 4.0 * B * HEADS * HEAD_DIM * N ** 3  # Q K^T and P V
+    w_o = 2.0 * B * N * N * ch * C_Z           # output projection
+    out = {"triattn_prologue": 2.0 * B * N * N * C_Z * (4 * ch + HEADS)}
+    if -(-N // 128) * 128 <= 1024:
+        # (row, head) flash kernel; the output projection runs in its own kernel
+        out.update({"triattn_flash": core, "triattn_out": w_o})
+    else:
+        out["triattn_flash"] = core + w_o
+    return out
 
 
 def step_flops_of(fm: dict, fa: dict) -> float:

@@ -73,6 +73,12 @@ static TriAttnPacked<T> carve_triattn(Carve& cv, int cin, int ch, int H) {
 
 template <typename T> struct AttnWs {
   T *q, *k, *vt, *gate, *bias;
+  // (row, head) flash path (bf16 module forward with Np <= kFlashRhMaxNp),
+  // else null: the gated attention output [B][rows][Np q][c_h], and the
+  // triangle bias in fp32, B x H x Np x Np in the flash kernel's fragment
+  // order (bias_frag_off; then bias is empty)
+  T* og;
+  float* biasf;
   // q, k, v^T and the gate hold `rows` rows per batch element, from absolute
   // row r0 on: all Np rows from 0, or one chunk of rows (chunked attention).
   // The bias always holds every row.  (The fp32 and raw-op kernels use the
@@ -84,6 +90,23 @@ template <typename T> struct AttnWs {
 
 // Rows and positions are padded to a multiple of the flash kernel's query block.
 inline int64_t attn_pad(int64_t N) { return round_up(N, 128); }
+
+// Largest padded N of the (row, head) flash path: K^T and V^T of one row and
+// head (2 x 32 x Np bf16) stay in LDS.
+constexpr int64_t kFlashRhMaxNp = 1024;
+
+// fp32 triangle bias of the (row, head) path, per batch element, in the flash
+// kernel's S^T fragment order: tile (query tile qt, key tile kt) of head h is
+// 4 slabs g of [64 lanes][4], lane = 32 * ((kk >> 2) & 1) + (q & 31) for the
+// tile's key kk = 8g + 4 * ((kk >> 2) & 1) + rr, rr = kk & 3.  A wave loads
+// its bias tile as 4 contiguous 1 KiB pieces.  Element offset of (h, query
+// q, key tile kt, keys kk .. kk+3 with kk % 4 == 0):
+__host__ __device__ __forceinline__ uint32_t bias_frag_off(int h, int q, int kt, int kk, int Np) {
+  const int nt = Np / 32;
+  const uint32_t tile = (uint32_t)((h * nt + (q >> 5)) * nt + kt);
+  const int g = kk >> 3, hh = (kk >> 2) & 1;
+  return ((tile * 4 + g) * 64 + hh * 32 + (q & 31)) * 4;
+}
 
 // Position of key j inside a V^T row: within each group of 16 keys, keys
 // 4..7 and 8..11 trade places, so that the 8 keys one lane feeds to the PV
@@ -104,7 +127,10 @@ static AttnWs<T> carve_attn_ws(Carve& cv, int64_t B, int64_t Np, int H, int ch, 
   w.k = cv.take<T>(qkv);
   w.vt = cv.take<T>(qkv);
   w.gate = cv.take<T>(ch > 0 ? B * w.rows * Np * ch : 0);
-  w.bias = cv.take<T>(B * H * Np * Np);
+  const bool rh = ch > 0 && sizeof(T) == 2 && Np <= kFlashRhMaxNp;
+  w.bias = rh ? nullptr : cv.take<T>(B * H * Np * Np);
+  w.og = rh ? cv.take<T>(B * w.rows * Np * ch) : nullptr;
+  w.biasf = rh ? cv.take<float>(B * H * Np * Np) : nullptr;
   return w;
 }
 
@@ -209,13 +235,14 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
 //        gate  [B][Np r][c_h][Np j]        bias [B][H][Np q][Np k]
 //     Padding values are those of triattn_prologue_kernel.
 // ---------------------------------------------------------------------------
-// MODE bit 0: q, k, v^T and gate; bit 1: the triangle bias.  The tiles cover
-// rows r0 .. r0 + nrows - 1 of every batch element: [B][nrows][Np / 32].
+// MODE bit 0: q, k, v^T and gate; bit 1: the triangle bias; bit 2: the bias
+// in fp32 (ws.biasf) instead of bf16 (ws.bias).  The tiles cover rows r0 ..
+// r0 + nrows - 1 of every batch element: [B][nrows][Np / 32].
 template <int CIN, int H, int MODE>
 __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
     const bf16* __restrict__ x, TriAttnPacked<bf16> w, AttnWs<bf16> ws, int N, int Np,
     int starting, float eps, int64_t ntiles, int r0, int nrows) {
-  static_assert(MODE >= 1 && MODE <= 3, "q/k/v/gate, bias, or both");
+  static_assert((MODE & 3) != 0 && MODE <= 7, "q/k/v/gate, bias, or both");
   constexpr int CH = H * HD;
   constexpr int KCH = CIN / 16;
   constexpr int PE = (CH / 32) * KCH * 512;  // one packed c_in -> c_h projection
@@ -342,14 +369,30 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
       }
       // lanes i32 >= H store nothing (out-of-range offset, no branch)
       const float bb = bl[4 * CH + (i32 & (H - 1))];
-      uint32_t pk[8];
+      if constexpr ((MODE & 4) != 0) {
+        // fp32, in the flash kernel's S^T fragment order (bias_frag_off)
+        float bv[16];
 #pragma unroll
-      for (int m = 0; m < 16; m += 2)
-        pk[m / 2] = pack_bf16x2(m < nvalid ? ab[m] + bb : 0.f, m + 1 < nvalid ? ab[m + 1] + bb : 0.f);
-      const auto brs = buf_rsrc(ws.bias + (int64_t)b * H * Np * Np, (uint32_t)(H * Np * Np * 2));
-      const uint32_t off = i32 < H ? (uint32_t)((((int64_t)i32 * Np + r) * Np + j0) * 2) : kBufSkip;
-      buf_store16(brs, off, make_uint4(pk[0], pk[1], pk[2], pk[3]));
-      buf_store16(brs, off + 16, make_uint4(pk[4], pk[5], pk[6], pk[7]));
+        for (int m = 0; m < 16; ++m) bv[m] = m < nvalid ? ab[m] + bb : 0.f;
+        const auto brs = buf_rsrc(ws.biasf + (int64_t)b * H * Np * Np, (uint32_t)(H * Np * Np * 4));
+#pragma unroll
+        for (int a = 0; a < 4; ++a) {
+          // positions j0 + 4a .. +3: key kk = 16*half + 4a + rr of key tile vt
+          const uint32_t off = i32 < H ? bias_frag_off(i32, r, vt, 16 * half + 4 * a, Np) * 4 : kBufSkip;
+          buf_store16(brs, off,
+                      make_uint4(__float_as_uint(bv[4 * a]), __float_as_uint(bv[4 * a + 1]),
+                                 __float_as_uint(bv[4 * a + 2]), __float_as_uint(bv[4 * a + 3])));
+        }
+      } else {
+        uint32_t pk[8];
+#pragma unroll
+        for (int m = 0; m < 16; m += 2)
+          pk[m / 2] = pack_bf16x2(m < nvalid ? ab[m] + bb : 0.f, m + 1 < nvalid ? ab[m + 1] + bb : 0.f);
+        const auto brs = buf_rsrc(ws.bias + (int64_t)b * H * Np * Np, (uint32_t)(H * Np * Np * 2));
+        const uint32_t off = i32 < H ? (uint32_t)((((int64_t)i32 * Np + r) * Np + j0) * 2) : kBufSkip;
+        buf_store16(brs, off, make_uint4(pk[0], pk[1], pk[2], pk[3]));
+        buf_store16(brs, off + 16, make_uint4(pk[4], pk[5], pk[6], pk[7]));
+      }
     }
   };
   if (tile < ntiles) {
@@ -925,6 +968,413 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
 }
 
 // ---------------------------------------------------------------------------
+// 3d. bf16 flash kernel, one block per (row, head), for Np <= NPM (1024).
+//   * K^T and V^T of the row and head (2 x 32 x Np bf16, 64 KiB at Np = 512)
+//     are copied into LDS once, with direct global->LDS loads, and stay there
+//     for the whole block: after one barrier the key loop runs without any.
+//     Layout: [kind][key tile t][32 d rows][64 bytes]; K^T rows unswizzled,
+//     V^T chunk p of row d at physical chunk p ^ ((d>>2)&3) (the read
+//     patterns of the module kernel above).
+//   * Eight waves; wave w attends query tiles w, w+8, ... in turn.  Each
+//     query tile: q copied into the wave's 2 KiB LDS region and read back
+//     transposed, the gate tile copied into the same region behind it, then
+//     the key loop (fp32 bias tiles prefetched a tile ahead, S^T
+//     accumulated on top of them), then o / l *
+//     gate transposed through the region and stored as 16-byte pieces into
+//     og [rows][Np q][c_h] (destination coordinates, this head's 32
+//     channels).  The next tile's q copy and first bias fragments are issued
+//     before those stores.
+//   * The excluded-key bits of the row are kept in one VGPR (lane t: key
+//     tile t) and read with v_readlane per tile.
+//   * Blocks run head-major, so the blocks of one XCD read one or two heads'
+//     triangle bias.
+// The output projection (W_o, b_o, residual) runs in triattn_out_kernel.
+// ---------------------------------------------------------------------------
+template <int NPM>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void triattn_flash_rh_kernel(
+    const float* __restrict__ mask, AttnWs<bf16> ws, int N, int Np, int starting, int r0, int nrows) {
+  constexpr int H = 4, NW = 8, CH = H * HD;
+  constexpr int NTM = NPM / 32;       // key tiles at most
+  constexpr float kRescale = 8.0f;    // lazy-rescale threshold (log2 units)
+  static_assert(NTM <= 64, "excluded-key bits: one word per lane");
+  __shared__ __attribute__((aligned(1024))) char kv[2 * NTM * 2048];
+  __shared__ __attribute__((aligned(1024))) char stg[NW][2048];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5;
+  const int t32 = lane & 31;
+  const int nt = Np / 32;             // key tiles (even: Np is a multiple of 128)
+  const int nq = (N + 31) / 32;       // query tiles holding real queries
+  const int64_t per_h = (int64_t)gridDim.x / H;
+  const int64_t lin = xcd_remap(blockIdx.x, gridDim.x);
+  const int h = (int)(lin / per_h);
+  const int64_t rem = lin - h * per_h;
+  const int b = (int)(rem / nrows);
+  const int r = r0 + (int)(rem - (int64_t)b * nrows);
+  const int64_t rowbase = ws.row(b, r);
+
+  // K^T / V^T of (row, head): 4 * nt copies of 1 KiB (kind, tile, row half)
+  {
+    const bf16* kbase = ws.k + (rowbase * H + h) * (int64_t)HD * Np;
+    const bf16* vbase = ws.vt + (rowbase * H + h) * (int64_t)HD * Np;
+    const uint32_t ln = (uint32_t)lane;
+    const uint32_t rowoff = (ln >> 2) * (uint32_t)Np * 2;
+    const uint32_t voff_k = rowoff + (ln & 3) * 16;
+    const uint32_t voff_v = rowoff + (((ln & 3) ^ ((ln >> 4) & 3)) * 16);
+    const uint32_t kv_lds = lds_addr(kv);
+    for (int c = wave; c < 4 * nt; c += NW) {
+      const int kind = c >= 2 * nt;
+      const int cr = c - kind * 2 * nt;
+      const int t = cr >> 1, rh = cr & 1;
+      const bf16* src = (kind ? vbase : kbase) + (int64_t)(16 * rh) * Np + 32 * t;
+      g2lds16_sv(src, kind ? voff_v : voff_k, kv_lds + ((kind * NTM + t) * 2 + rh) * 1024);
+    }
+  }
+
+  // excluded keys of this row: bit j of lane t's word is key 32t + j
+  // (padding, and masked keys of a row with at least one valid key)
+  const float* mrow = mask ? mask + (int64_t)b * N * N + (starting ? (int64_t)r * N : r) : nullptr;
+  const int64_t mks = starting ? 1 : N;
+  uint32_t kmv = 0, kpv = 0;
+  bool any = mrow == nullptr;
+  for (int k0 = 0; k0 < Np; k0 += 64) {
+    const int k = k0 + lane;
+    const bool inrow = k < N;
+    const bool masked = inrow && mrow && mrow[k * mks] == 0.f;
+    any = any || (inrow && !masked);
+    const unsigned long long mb = __ballot(masked);
+    const unsigned long long pb = __ballot(!inrow);
+    const int w0 = k0 >> 5;
+    if (lane == w0) { kmv = (uint32_t)mb; kpv = (uint32_t)pb; }
+    if (lane == w0 + 1) { kmv = (uint32_t)(mb >> 32); kpv = (uint32_t)(pb >> 32); }
+  }
+  const bool row_valid = __ballot(any) != 0ull;  // wave-uniform (every wave reads the same row)
+  const uint32_t kxv = kpv | (row_valid ? kmv : 0u);
+
+  const uint32_t stg_lds = lds_addr(stg[wave]);
+  char* const sw = stg[wave];
+  // q or gate tile, channel-major [32 channels][32 queries] -> the wave's
+  // region, 64-byte rows; copy j moves channels 16j .. 16j+15, lane l takes
+  // channel 16j + l/4, queries 8*(l%4) .. +7
+  auto issue_cq = [&](const bf16* src) {
+    const uint32_t ln = (uint32_t)(lane + opaque_zero());
+    const uint32_t voff = ((ln >> 2) * (uint32_t)Np + (ln & 3) * 8) * 2;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) g2lds16_sv(src + (int64_t)j * 16 * Np, voff, stg_lds + j * 1024);
+  };
+  // channels c0 .. c0+3 of this lane's query t32 (transposing read); ln is
+  // the lane id through opaque_zero, so that these per-lane addresses are
+  // recomputed where they are used instead of held across the key loop
+  auto read_cq4 = [&](int ln, int c0) {
+    const int i = ln & 15;
+    return lds_read_tr16(sw + (c0 + (i >> 2)) * 64 + (16 * ((ln >> 4) & 1) + 4 * (i & 3)) * 2);
+  };
+  const bf16* q_row = ws.q + ((rowbase * H + h) * HD) * (int64_t)Np;
+  const bf16* g_row = ws.gate + (rowbase * CH + h * HD) * (int64_t)Np;
+  const float* b_head = ws.biasf + (int64_t)(b * H + h) * Np * Np;  // wave-uniform
+  bf16* og_row = ws.og + rowbase * (int64_t)Np * CH + h * HD;
+
+  // K fragments (transposing reads of K^T) and V^T fragments: per-lane offsets
+  const int trG = lane >> 4;
+  const int kt_lane = ((trG >> 1) * 8 + ((lane & 15) >> 2)) * 64 + 32 * (trG & 1) + 8 * (lane & 3);
+  const int vt_lane = t32 * 64 + 16 * (half ^ ((t32 >> 2) & 3));
+
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  const bf16x2_t ones2 = {(bf16)1.0f, (bf16)1.0f};
+  // Bias tile t of query tile q0 in the S^T accumulator layout: register
+  // 4g + rr <-> key 32t + 8g + 4*half + rr, stored in that order
+  // (bias_frag_off): 4 loads of 1 KiB contiguous per wave (a wave-uniform
+  // base plus a 32-bit per-lane byte offset, the saddr form).
+  const uint32_t b_lane = (uint32_t)lane * 16;
+  auto load_bias = [&](f32x16& dst, int q0, int t) {
+    const uint32_t off = b_lane + (uint32_t)(((q0 >> 5) * nt + t) * 4096);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(reinterpret_cast<const char*>(b_head) + off + 1024 * g);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) dst[4 * g + rr] = v[rr];
+    }
+  };
+  // s += K Q^T for key tile t (s holds the bias tile: S^T in log2 units)
+  auto s_tile = [&](int t, f32x16& s, const Frag<bf16>* qf) {
+    const char* kt_base = kv + t * 2048 + kt_lane;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const s16x4 p0 = lds_read_tr16(kt_base + (m * 16) * 64);
+      const s16x4 p1 = lds_read_tr16(kt_base + (m * 16 + 4) * 64);
+      const s16x8 v8 = {p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]};
+      Frag<bf16> kf;
+      kf.v = __builtin_bit_cast(bf16x8, v8);
+      mma(s, kf, qf[m]);
+    }
+  };
+  // excluded keys of tile t take no weight
+  auto mask_tile = [&](int t, f32x16& sc) {
+    const unsigned kx = __builtin_amdgcn_readlane(kxv, t);
+    if (kx != 0u) {
+      // this lane's keys 8g + 4*half + rr: bits 8g + rr after the shift
+      const unsigned kl = kx >> (4 * (lane >> 5));
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+          if (__builtin_amdgcn_ubfe(kl, 8 * g + rr, 1)) sc[4 * g + rr] = -INFINITY;
+    }
+  };
+  // P = 2^sc (bf16), l += row sums of P, O^T += V^T P^T
+  auto pv_tile = [&](int t, const f32x16& sc, f32x16& o, float& l_run) {
+    const char* vt_base = kv + (NTM + t) * 2048;
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      Frag<bf16> pf, vf;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pf.v[e] = (bf16)__builtin_amdgcn_exp2f(sc[8 * c + e]);
+#pragma unroll
+      for (int e = 0; e < 8; e += 2) {
+        const bf16x2_t pp = {pf.v[e], pf.v[e + 1]};
+        l_run = __builtin_amdgcn_fdot2_f32_bf16(pp, ones2, l_run, false);
+      }
+      vf.load(reinterpret_cast<const bf16*>(vt_base + (c ? (vt_lane ^ 32) : vt_lane)));
+      mma(o, vf, pf);
+    }
+  };
+
+  // Bias of the next KB S tiles, prefetched KB - 1 tiles ahead; S^T
+  // accumulates in place.  Each tile's loads go out unconditionally (the
+  // last KB of a query tile fetch the first KB of the wave's next query
+  // tile, or again the current one at the end), so the compiler's waits
+  // count them exactly.
+  constexpr int KB = 2;
+  // Epilogue of query tile q0: o / l * gate -> the region ([32 queries][32
+  // channels], 16-byte chunk g of query q at physical chunk g ^ ((q>>2)&3))
+  // -> og.  next_q: the q tile to copy into the region before the stores
+  // (null: none).
+  auto finish = [&](int q0, const f32x16& o, float l_tot, const bf16* next_q) {
+    const float inv = 1.0f / l_tot;
+    const int lne = lane + opaque_zero();
+    const int e32 = lne & 31, ehalf = lne >> 5;
+    __builtin_amdgcn_s_waitcnt(0);  // the gate tile has landed (wave-local region)
+    bf16x4 gv[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) gv[g] = __builtin_bit_cast(bf16x4, read_cq4(lne, 8 * g + 4 * ehalf));
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // gate values in registers before the region is rewritten
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      store4(reinterpret_cast<bf16*>(sw + e32 * 64 + ((g ^ ((e32 >> 2) & 3)) * 16) + ehalf * 8),
+             o[4 * g] * inv * (float)gv[g][0], o[4 * g + 1] * inv * (float)gv[g][1],
+             o[4 * g + 2] * inv * (float)gv[g][2], o[4 * g + 3] * inv * (float)gv[g][3]);
+    // lane l: queries q1 = l/4 and 16 + l/4, channel chunk l%4
+    const int q1 = lne >> 2, oc = lne & 3;
+    const f32x4 ov0 = *reinterpret_cast<const f32x4*>(sw + q1 * 64 + ((oc ^ ((q1 >> 2) & 3)) * 16));
+    const f32x4 ov1 = *reinterpret_cast<const f32x4*>(sw + (q1 + 16) * 64 + ((oc ^ (((q1 + 16) >> 2) & 3)) * 16));
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // read back: the region is free for the next q copy
+    if (next_q) issue_cq(next_q);
+    const uint32_t o_off = (uint32_t)((q0 + q1) * CH + oc * 8) * 2;
+    *reinterpret_cast<f32x4*>(reinterpret_cast<char*>(og_row) + o_off) = ov0;
+    *reinterpret_cast<f32x4*>(reinterpret_cast<char*>(og_row) + o_off + 16 * CH * 2) = ov1;
+  };
+
+  if (!row_valid) {
+    // No valid key: every logit is the same -1e9 in the reference, so the row
+    // attends uniformly over its N keys (P = 1, padding excluded); q and the
+    // bias do not matter.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // K^T / V^T resident for every wave
+    for (int qt = wave; qt < nq; qt += NW) {
+      issue_cq(g_row + qt * 32);
+      f32x16 o = zero16();
+      float l_run = 0.f;
+      for (int t = 0; t < nt; ++t) {
+        f32x16 sc = zero16();
+        mask_tile(t, sc);
+        pv_tile(t, sc, o, l_run);
+      }
+      finish(qt * 32, o, lane_pair_sum(l_run), nullptr);
+    }
+    return;
+  }
+
+  f32x16 bq[KB];
+  int qt = wave;
+  if (qt < nq) {
+    issue_cq(q_row + qt * 32);
+#pragma unroll
+    for (int u = 0; u < KB; ++u) load_bias(bq[u], qt * 32, u);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();  // K^T / V^T resident for every wave
+  for (; qt < nq; qt += NW) {
+    const int q0 = qt * 32;
+    const int q0n = (qt + NW < nq ? qt + NW : qt) * 32;  // the query tile to prefetch for
+    // this tile's q copy landed: behind it are, after the first tile, the
+    // previous tile's og stores (2)
+    if (qt != wave) __builtin_amdgcn_s_waitcnt(vmcnt_imm<2>());
+    Frag<bf16> qf[2];
+    const int lnq = lane + opaque_zero();
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const s16x4 lo = read_cq4(lnq, m * 16 + half * 8), hi = read_cq4(lnq, m * 16 + half * 8 + 4);
+      const s16x8 v8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      qf[m].v = __builtin_bit_cast(bf16x8, v8);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): q read back, the region is free
+    issue_cq(g_row + q0);                // the gate tile lands behind the key loop
+
+    // Fast pass: P = 2^s with no running maximum.  Exact (softmax is shift
+    // invariant, and fp32 / bf16 keep relative precision) while every 2^s
+    // stays in range; checked at the end through l, else the exact pass runs.
+    f32x16 o = zero16();
+    float l_run = 0.f;
+    for (int t = 0; t < nt; t += KB) {
+#pragma unroll
+      for (int u = 0; u < KB; ++u) {
+        s_tile(t + u, bq[u], qf);
+        mask_tile(t + u, bq[u]);
+        pv_tile(t + u, bq[u], o, l_run);
+        const bool wrap = t + u + KB >= nt;
+        load_bias(bq[u], wrap ? q0n : q0, wrap ? t + u + KB - nt : t + u + KB);
+        // one sub-tile at a time: interleaving them would need several S
+        // tiles and their fragments live at once
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    float l_tot = lane_pair_sum(l_run);
+    // In range: the largest term 2^max(s) is within [2^-69, 2^64], so no P
+    // overflows and no term that underflows matters.  (NaN fails too.)
+    if (__ballot(!(l_tot >= 0x1p-60f && l_tot <= 0x1p64f)) != 0ull) {
+      // Exact pass: online softmax with a running maximum, lazily moved (only
+      // when a tile exceeds it by more than kRescale), bias loaded per tile.
+      o = zero16();
+      l_run = 0.f;
+      float m_ref = -INFINITY, m_use = 0.f;
+      for (int t = 0; t < nt; ++t) {
+        f32x16 sc;
+        load_bias(sc, q0, t);
+        s_tile(t, sc, qf);
+        mask_tile(t, sc);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sc[e] -= m_use;
+        float mt = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
+#pragma unroll
+        for (int e = 3; e < 15; e += 2) mt = fmaxf(fmaxf(mt, sc[e]), sc[e + 1]);
+        mt = fmaxf(mt, sc[15]);
+        mt = lane_pair_max(mt) + m_use;  // the tile max of s
+        if (__ballot(mt > m_ref + kRescale) != 0ull) {
+          const float m_new = fmaxf(m_ref, mt);
+          const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
+          l_run *= alpha;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) o[e] *= alpha;
+          m_ref = m_new;
+          const float m_next = (m_ref == -INFINITY) ? 0.f : m_ref;
+#pragma unroll
+          for (int e = 0; e < 16; ++e) sc[e] += m_use - m_next;
+          m_use = m_next;
+        }
+        pv_tile(t, sc, o, l_run);
+      }
+      l_tot = lane_pair_sum(l_run);
+    }
+    finish(q0, o, l_tot, qt + NW < nq ? q_row + (qt + NW) * 32 : nullptr);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 3e. Output projection of the (row, head) flash path:
+//     out[pair] = og[row][q] . W_o^T + b_o (+ x[pair]) at the source pair of
+//     (row, q).  Persistent 8-wave blocks, W_o (packed, 32 KiB) and b_o in
+//     LDS; one tile = 32 consecutive queries of one row.  og rows are read
+//     straight into MFMA fragments; the residual rows are regrouped into the
+//     accumulator layout with v_permlane32_swap.  Stores are branch-free
+//     buffer stores (queries >= N get an out-of-range offset).
+// ---------------------------------------------------------------------------
+template <int CIN>
+__global__ __launch_bounds__(512) void triattn_out_kernel(const bf16* __restrict__ x, bf16* __restrict__ out,
+                                                          TriAttnPacked<bf16> w, AttnWs<bf16> ws, int N,
+                                                          int Np, int starting, int residual, int r0,
+                                                          int nrows, int64_t ntiles) {
+  constexpr int CH = 4 * HD;
+  constexpr int KC = CH / 16;   // k chunks over c_h
+  constexpr int NTO = CIN / 32; // output tiles
+  constexpr int KR = CIN / 16;  // residual fragments per lane
+  __shared__ __attribute__((aligned(1024))) bf16 wl[NTO * KC * 512];
+  __shared__ __attribute__((aligned(16))) float bl[CIN];
+  copy_to_lds_async(wl, w.w_o, (int)sizeof(wl));
+  for (int t = threadIdx.x; t < CIN; t += blockDim.x) bl[t] = w.b_o[t];
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int half = lane >> 5;
+  const int t32 = lane & 31;
+  const int qtiles = (N + 31) / 32;
+  const int64_t stride = (int64_t)gridDim.x * 8;
+  for (int64_t tile = (int64_t)blockIdx.x * 8 + wave; tile < ntiles; tile += stride) {
+    const int qtl = (int)(tile % qtiles);
+    const int64_t br = tile / qtiles;
+    const int b = (int)(br / nrows);
+    const int r = r0 + (int)(br - (int64_t)b * nrows);
+    const int q = qtl * 32 + t32;
+    const bool valid = q < N;
+    const int qc = valid ? q : 0;
+    Frag<bf16> of[KC];
+    const bf16* src = ws.og + (ws.row(b, r) * (int64_t)Np + qtl * 32 + t32) * CH + half * (CH / 2);
+#pragma unroll
+    for (int ks = 0; ks < KC; ++ks) of[ks].load(src + ks * 8);
+    const int64_t pair = starting ? ((int64_t)r * N + qc) : ((int64_t)qc * N + r);
+    Frag<bf16> xr[KR];
+    if (residual) {
+      const bf16* xs = x + ((int64_t)b * N * N + pair) * CIN + half * (CIN / 2);
+#pragma unroll
+      for (int ch = 0; ch < KR; ++ch) xr[ch].load(xs + ch * 8);
+    }
+    bf16x4 xres[2 * KR];
+    if (residual) {
+#pragma unroll
+      for (int ch = 0; ch < KR; ++ch) {
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        const u32x4 d = __builtin_bit_cast(u32x4, xr[ch].v);
+        const auto s02 = __builtin_amdgcn_permlane32_swap(d[0], d[2], false, false);
+        const auto s13 = __builtin_amdgcn_permlane32_swap(d[1], d[3], false, false);
+        xres[ch] = __builtin_bit_cast(bf16x4, u32x2{s02[0], s13[0]});
+        xres[ch + KR] = __builtin_bit_cast(bf16x4, u32x2{s02[1], s13[1]});
+      }
+    }
+    const auto ors = buf_rsrc(out + (int64_t)b * N * N * CIN, (uint32_t)((int64_t)N * N * CIN * 2));
+    // an address the compiler cannot see through: the W_o fragment reads stay
+    // in the loop instead of being hoisted (and held) across tiles
+    const bf16* wlt = wl + opaque_zero();
+#pragma unroll
+    for (int nt = 0; nt < NTO; ++nt) {
+      Frag<bf16> f;
+      load_wfrag_lds(f, wlt, nt, 0, KC);
+      f32x16 acc = mma0(f, of[0]);  // rows = outputs, columns = queries
+#pragma unroll
+      for (int ks = 1; ks < KC; ++ks) {
+        load_wfrag_lds(f, wlt, nt, ks, KC);
+        mma(acc, f, of[ks]);
+      }
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c0 = nt * 32 + 8 * g + 4 * half;
+        const f32x4 b4 = *reinterpret_cast<const f32x4*>(bl + c0);
+        float v[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          v[rr] = acc[4 * g + rr] + b4[rr];
+          if (residual) v[rr] += (float)xres[nt * 4 + g][rr];
+        }
+        buf_store4(ors, valid ? (uint32_t)((pair * CIN + c0) * 2) : kBufSkip, v[0], v[1], v[2], v[3]);
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // 3b. Raw attention op: relayout of q/k/v/bias, then flash per (row, head).
 // ---------------------------------------------------------------------------
 // src: [B][H][N][N][D]; element (b, h, a1, a2, d).  Destination row/position:
@@ -1094,7 +1544,8 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
   const int64_t blocks = B * N * ((N + 31) / 32);
   GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "attention grid too large");
   if constexpr (sizeof(T) == 2) {
-    constexpr int QT = 2;  // two 8-wave blocks of 64 queries per CU
+    constexpr int QT = 2;  // two 8-wave blocks of 64 queries per CU (Np > kFlashRhMaxNp)
+    const bool rh = Np <= kFlashRhMaxNp;  // (row, head) flash path, fp32 bias
     auto prologue = [&](auto mode, int r0, int nrows) {
       constexpr int MODE = decltype(mode)::value;
       const int64_t ptiles = B * (int64_t)nrows * (Np / 32);
@@ -1104,19 +1555,43 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
           (const bf16*)x, w, a, (int)N, Np, starting, eps, ptiles, r0, nrows);
     };
     auto flash = [&](int r0, int nrows) {
+      if (rh) {
+        // (row, head) blocks, then the output projection
+        const int64_t fblocks = B * nrows * H;
+        {
+          StageTimer timer("triattn_flash", st);
+          if (Np <= 256)
+            triattn_flash_rh_kernel<256><<<(unsigned)fblocks, 512, 0, st>>>(mask, a, (int)N, Np, starting, r0, nrows);
+          else if (Np <= 512)
+            triattn_flash_rh_kernel<512><<<(unsigned)fblocks, 512, 0, st>>>(mask, a, (int)N, Np, starting, r0, nrows);
+          else
+            triattn_flash_rh_kernel<1024><<<(unsigned)fblocks, 512, 0, st>>>(mask, a, (int)N, Np, starting, r0, nrows);
+        }
+        GTK_HIP_CHECK(hipGetLastError());
+        const int64_t otiles = B * nrows * ((N + 31) / 32);
+        const int grid = (int)std::min<int64_t>(2 * device_cus(), (otiles + 7) / 8);
+        StageTimer timer("triattn_out", st);
+        triattn_out_kernel<CIN><<<grid, 512, 0, st>>>((const bf16*)x, (bf16*)out, w, a, (int)N, Np, starting,
+                                                      residual, r0, nrows, otiles);
+        return GTK_OK;
+      }
       const int64_t fblocks = B * nrows * ((N + 32 * QT - 1) / (32 * QT));
       StageTimer timer("triattn_flash", st);
       triattn_flash_kernel<CIN, H, QT><<<(unsigned)fblocks, 64 * H * QT, 0, st>>>(
           (const bf16*)x, mask, (bf16*)out, w, a, (int)N, Np, starting, residual, r0, nrows);
+      return GTK_OK;
     };
     if (!chunked) {
-      prologue(std::integral_constant<int, 3>(), 0, Np);  // every row, padding included
+      // every row, padding included
+      if (rh) prologue(std::integral_constant<int, 7>(), 0, Np);
+      else prologue(std::integral_constant<int, 3>(), 0, Np);
       GTK_LAUNCH_CHECK();
       flash(0, (int)N);
       GTK_LAUNCH_CHECK();
     } else {
       // the bias over every row (padding rows and columns are written as zero)
-      prologue(std::integral_constant<int, 2>(), 0, Np);
+      if (rh) prologue(std::integral_constant<int, 6>(), 0, Np);
+      else prologue(std::integral_constant<int, 2>(), 0, Np);
       GTK_LAUNCH_CHECK();
       for (int64_t r0 = 0; r0 < N; r0 += chunk_rows) {
         const int nrows = (int)std::min<int64_t>(chunk_rows, N - r0);
