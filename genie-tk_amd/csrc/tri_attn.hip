@@ -74,7 +74,8 @@ static TriAttnPacked<T> carve_triattn(Carve& cv, int cin, int ch, int H) {
 template <typename T> struct AttnWs {
   T *q, *k, *vt, *gate, *bias;
   // (row, head) flash path (bf16 module forward with Np <= kFlashRhMaxNp),
-  // else null: the gated attention output [B][rows][Np q][c_h], and the
+  // else null: the gated attention output (B x rows x Np x c_h, fragment
+  // order: see the flash kernel), and the
   // triangle bias in fp32, B x H x Np x Np in the flash kernel's fragment
   // order (bias_frag_off; then bias is empty)
   T* og;
@@ -94,6 +95,16 @@ inline int64_t attn_pad(int64_t N) { return round_up(N, 128); }
 // Largest padded N of the (row, head) flash path: K^T and V^T of one row and
 // head (2 x 32 x Np bf16) stay in LDS.
 constexpr int64_t kFlashRhMaxNp = 1024;
+
+// Gated attention output og of the (row, head) path, in the output
+// projection's B-fragment order: tile (workspace row, query tile qt) is 8
+// chunks ks of [64 lanes][8 channels]; lane = 32 * (c >= c_h/2) + (q & 31)
+// holds channels c = (c_h/2) * (lane >= 32) + 8 ks .. +7 of query q.  The
+// projection kernel reads each chunk as 1 KiB contiguous.  Element offset of
+// (og tile = workspace row * Np/32 + qt, chunk ks, lane):
+__host__ __device__ __forceinline__ int64_t og_frag_off(int64_t tile, int ks, int lane) {
+  return ((tile * 8 + ks) * 64 + lane) * 8;
+}
 
 // fp32 triangle bias of the (row, head) path, per batch element, in the flash
 // kernel's S^T fragment order: tile (query tile qt, key tile kt) of head h is
@@ -979,11 +990,9 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
 //     query tile: q copied into the wave's 2 KiB LDS region and read back
 //     transposed, the gate tile copied into the same region behind it, then
 //     the key loop (fp32 bias tiles prefetched a tile ahead, S^T
-//     accumulated on top of them), then o / l *
-//     gate transposed through the region and stored as 16-byte pieces into
-//     og [rows][Np q][c_h] (destination coordinates, this head's 32
-//     channels).  The next tile's q copy and first bias fragments are issued
-//     before those stores.
+//     accumulated on top of them), then o / l * gate stored into og in the
+//     output projection's fragment order (og_frag_off).  The next tile's q
+//     copy is issued before those stores.
 //   * The excluded-key bits of the row are kept in one VGPR (lane t: key
 //     tile t) and read with v_readlane per tile.
 //   * Blocks run head-major, so the blocks of one XCD read one or two heads'
@@ -1074,7 +1083,6 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
   const bf16* q_row = ws.q + ((rowbase * H + h) * HD) * (int64_t)Np;
   const bf16* g_row = ws.gate + (rowbase * CH + h * HD) * (int64_t)Np;
   const float* b_head = ws.biasf + (int64_t)(b * H + h) * Np * Np;  // wave-uniform
-  bf16* og_row = ws.og + rowbase * (int64_t)Np * CH + h * HD;
 
   // K fragments (transposing reads of K^T) and V^T fragments: per-lane offsets
   const int trG = lane >> 4;
@@ -1148,33 +1156,43 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
   // tile, or again the current one at the end), so the compiler's waits
   // count them exactly.
   constexpr int KB = 2;
-  // Epilogue of query tile q0: o / l * gate -> the region ([32 queries][32
-  // channels], 16-byte chunk g of query q at physical chunk g ^ ((q>>2)&3))
-  // -> og.  next_q: the q tile to copy into the region before the stores
-  // (null: none).
+  // Epilogue of query tile q0: o / l * gate, stored into og in the output
+  // projection's B-fragment order (og_frag_off): this head's 32 channels are
+  // 4 chunks of 8; the two half-waves trade quads (v_permlane32_swap) so that
+  // the lower one writes chunks 0-1 and the upper one chunks 2-3, each store
+  // 32 lanes x 16 bytes contiguous.  next_q: the q tile to copy into the
+  // wave's region before the stores (null: none).
+  const int64_t og_tiles = rowbase * (int64_t)nt;  // og tile index of (row, query tile 0)
   auto finish = [&](int q0, const f32x16& o, float l_tot, const bf16* next_q) {
     const float inv = 1.0f / l_tot;
     const int lne = lane + opaque_zero();
-    const int e32 = lne & 31, ehalf = lne >> 5;
+    const int ehalf = lne >> 5;
     __builtin_amdgcn_s_waitcnt(0);  // the gate tile has landed (wave-local region)
     bf16x4 gv[4];
 #pragma unroll
     for (int g = 0; g < 4; ++g) gv[g] = __builtin_bit_cast(bf16x4, read_cq4(lne, 8 * g + 4 * ehalf));
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // gate values in registers before the region is rewritten
+    // quad g of this lane: channels 8g + 4*half .. +3 of query t32
+    uint32_t px[4], py[4];
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
-      store4(reinterpret_cast<bf16*>(sw + e32 * 64 + ((g ^ ((e32 >> 2) & 3)) * 16) + ehalf * 8),
-             o[4 * g] * inv * (float)gv[g][0], o[4 * g + 1] * inv * (float)gv[g][1],
-             o[4 * g + 2] * inv * (float)gv[g][2], o[4 * g + 3] * inv * (float)gv[g][3]);
-    // lane l: queries q1 = l/4 and 16 + l/4, channel chunk l%4
-    const int q1 = lne >> 2, oc = lne & 3;
-    const f32x4 ov0 = *reinterpret_cast<const f32x4*>(sw + q1 * 64 + ((oc ^ ((q1 >> 2) & 3)) * 16));
-    const f32x4 ov1 = *reinterpret_cast<const f32x4*>(sw + (q1 + 16) * 64 + ((oc ^ (((q1 + 16) >> 2) & 3)) * 16));
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // read back: the region is free for the next q copy
+    for (int g = 0; g < 4; ++g) {
+      px[g] = pack_bf16x2(o[4 * g] * inv * (float)gv[g][0], o[4 * g + 1] * inv * (float)gv[g][1]);
+      py[g] = pack_bf16x2(o[4 * g + 2] * inv * (float)gv[g][2], o[4 * g + 3] * inv * (float)gv[g][3]);
+    }
+    // lower half receives the upper's quads of chunks 0, 1; the upper half
+    // the lower's quads of chunks 2, 3
+    const auto s0x = __builtin_amdgcn_permlane32_swap(px[0], px[2], false, false);
+    const auto s0y = __builtin_amdgcn_permlane32_swap(py[0], py[2], false, false);
+    const auto s1x = __builtin_amdgcn_permlane32_swap(px[1], px[3], false, false);
+    const auto s1y = __builtin_amdgcn_permlane32_swap(py[1], py[3], false, false);
+    const bool up = ehalf != 0;
+    const uint4 cA = up ? make_uint4(s0x[0], s0y[0], px[2], py[2]) : make_uint4(px[0], py[0], s0x[1], s0y[1]);
+    const uint4 cB = up ? make_uint4(s1x[0], s1y[0], px[3], py[3]) : make_uint4(px[1], py[1], s1x[1], s1y[1]);
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // gate read: the region is free for the next q copy
     if (next_q) issue_cq(next_q);
-    const uint32_t o_off = (uint32_t)((q0 + q1) * CH + oc * 8) * 2;
-    *reinterpret_cast<f32x4*>(reinterpret_cast<char*>(og_row) + o_off) = ov0;
-    *reinterpret_cast<f32x4*>(reinterpret_cast<char*>(og_row) + o_off + 16 * CH * 2) = ov1;
+    const int ks = (h & 1) * 4 + (up ? 2 : 0);  // chunk of cA; cB is ks + 1
+    const uint32_t o_off = (uint32_t)og_frag_off(og_tiles + (q0 >> 5), ks, (h >> 1) * 32 + (lne & 31)) * 2;
+    *reinterpret_cast<uint4*>(reinterpret_cast<char*>(ws.og) + o_off) = cA;
+    *reinterpret_cast<uint4*>(reinterpret_cast<char*>(ws.og) + o_off + 1024) = cB;
   };
 
   if (!row_valid) {
@@ -1285,23 +1303,31 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
 // ---------------------------------------------------------------------------
 // 3e. Output projection of the (row, head) flash path:
 //     out[pair] = og[row][q] . W_o^T + b_o (+ x[pair]) at the source pair of
-//     (row, q).  Persistent 8-wave blocks, W_o (packed, 32 KiB) and b_o in
-//     LDS; one tile = 32 consecutive queries of one row.  og rows are read
-//     straight into MFMA fragments; the residual rows are regrouped into the
-//     accumulator layout with v_permlane32_swap.  Stores are branch-free
-//     buffer stores (queries >= N get an out-of-range offset).
+//     (row, q).  Persistent blocks of 8 waves (two per CU), W_o (packed, 32
+//     KiB) and b_o in LDS; one tile = 32 consecutive queries of one row.
+//   * og arrives in fragment order (og_frag_off): 8 loads of 1 KiB
+//     contiguous, issued with the residual rows at the start of the tile
+//     (four waves per SIMD hide their latency).
+//   * The result is transposed through the wave's 4 KiB LDS region in two
+//     halves of 64 channels (bf16 update, rows of 128 bytes, chunk c of row q
+//     at physical chunk c ^ (q & 7)), then every lane adds 8 residual
+//     channels and stores 16 bytes: 8 lanes write one 128-byte line, for the
+//     starting node's consecutive pairs and the ending node's strided ones.
+//     The update is rounded to bf16 before the residual add, as the module's
+//     bf16 output is before the caller's residual add.
 // ---------------------------------------------------------------------------
 template <int CIN>
-__global__ __launch_bounds__(512) void triattn_out_kernel(const bf16* __restrict__ x, bf16* __restrict__ out,
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void triattn_out_kernel(const bf16* __restrict__ x, bf16* __restrict__ out,
                                                           TriAttnPacked<bf16> w, AttnWs<bf16> ws, int N,
                                                           int Np, int starting, int residual, int r0,
                                                           int nrows, int64_t ntiles) {
   constexpr int CH = 4 * HD;
   constexpr int KC = CH / 16;   // k chunks over c_h
-  constexpr int NTO = CIN / 32; // output tiles
-  constexpr int KR = CIN / 16;  // residual fragments per lane
+  constexpr int NTO = CIN / 32; // output tiles of 32 channels
+  static_assert(CIN == 128 && NTO == 4, "two halves of 64 output channels");
   __shared__ __attribute__((aligned(1024))) bf16 wl[NTO * KC * 512];
   __shared__ __attribute__((aligned(16))) float bl[CIN];
+  __shared__ __attribute__((aligned(1024))) char stg[8][4096];
   copy_to_lds_async(wl, w.w_o, (int)sizeof(wl));
   for (int t = threadIdx.x; t < CIN; t += blockDim.x) bl[t] = w.b_o[t];
   __builtin_amdgcn_s_waitcnt(0);
@@ -1310,66 +1336,88 @@ __global__ __launch_bounds__(512) void triattn_out_kernel(const bf16* __restrict
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int half = lane >> 5;
   const int t32 = lane & 31;
+  char* const sw = stg[wave];
   const int qtiles = (N + 31) / 32;
+  const int ntq = Np / 32;  // og tiles per workspace row
   const int64_t stride = (int64_t)gridDim.x * 8;
+  auto og_tile = [&](int64_t tile) {
+    const int qtl = (int)(tile % qtiles);
+    const int64_t br = tile / qtiles;
+    const int b = (int)(br / nrows);
+    const int r = r0 + (int)(br - (int64_t)b * nrows);
+    return ws.row(b, r) * ntq + qtl;
+  };
+  auto load_og = [&](Frag<bf16>* of, int64_t tile) {
+    const bf16* src = ws.og + og_frag_off(og_tile(tile), 0, lane);
+#pragma unroll
+    for (int ks = 0; ks < KC; ++ks) of[ks].load(src + ks * 512);
+  };
   for (int64_t tile = (int64_t)blockIdx.x * 8 + wave; tile < ntiles; tile += stride) {
     const int qtl = (int)(tile % qtiles);
     const int64_t br = tile / qtiles;
     const int b = (int)(br / nrows);
     const int r = r0 + (int)(br - (int64_t)b * nrows);
-    const int q = qtl * 32 + t32;
-    const bool valid = q < N;
-    const int qc = valid ? q : 0;
-    Frag<bf16> of[KC];
-    const bf16* src = ws.og + (ws.row(b, r) * (int64_t)Np + qtl * 32 + t32) * CH + half * (CH / 2);
-#pragma unroll
-    for (int ks = 0; ks < KC; ++ks) of[ks].load(src + ks * 8);
-    const int64_t pair = starting ? ((int64_t)r * N + qc) : ((int64_t)qc * N + r);
-    Frag<bf16> xr[KR];
-    if (residual) {
-      const bf16* xs = x + ((int64_t)b * N * N + pair) * CIN + half * (CIN / 2);
-#pragma unroll
-      for (int ch = 0; ch < KR; ++ch) xr[ch].load(xs + ch * 8);
-    }
-    bf16x4 xres[2 * KR];
-    if (residual) {
-#pragma unroll
-      for (int ch = 0; ch < KR; ++ch) {
-        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-        const u32x4 d = __builtin_bit_cast(u32x4, xr[ch].v);
-        const auto s02 = __builtin_amdgcn_permlane32_swap(d[0], d[2], false, false);
-        const auto s13 = __builtin_amdgcn_permlane32_swap(d[1], d[3], false, false);
-        xres[ch] = __builtin_bit_cast(bf16x4, u32x2{s02[0], s13[0]});
-        xres[ch + KR] = __builtin_bit_cast(bf16x4, u32x2{s02[1], s13[1]});
-      }
-    }
+    // row-pass lanes: query qq = 8i + lane/8 of the tile, 16-byte chunk lane%8
+    // of a 64-channel half
+    const int rq = lane >> 3, rc = lane & 7;
     const auto ors = buf_rsrc(out + (int64_t)b * N * N * CIN, (uint32_t)((int64_t)N * N * CIN * 2));
-    // an address the compiler cannot see through: the W_o fragment reads stay
-    // in the loop instead of being hoisted (and held) across tiles
-    const bf16* wlt = wl + opaque_zero();
+    auto pair_of = [&](int q) {  // source pair of (row r, query q), q < N
+      return starting ? ((int64_t)r * N + q) : ((int64_t)q * N + r);
+    };
+    // residual rows of this tile (queries >= N read pair 0 and are not stored)
+    uint4 xr[2][4];
+    if (residual) {
 #pragma unroll
-    for (int nt = 0; nt < NTO; ++nt) {
-      Frag<bf16> f;
-      load_wfrag_lds(f, wlt, nt, 0, KC);
-      f32x16 acc = mma0(f, of[0]);  // rows = outputs, columns = queries
+      for (int hp = 0; hp < 2; ++hp)
 #pragma unroll
-      for (int ks = 1; ks < KC; ++ks) {
-        load_wfrag_lds(f, wlt, nt, ks, KC);
-        mma(acc, f, of[ks]);
-      }
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int c0 = nt * 32 + 8 * g + 4 * half;
-        const f32x4 b4 = *reinterpret_cast<const f32x4*>(bl + c0);
-        float v[4];
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          v[rr] = acc[4 * g + rr] + b4[rr];
-          if (residual) v[rr] += (float)xres[nt * 4 + g][rr];
+        for (int i = 0; i < 4; ++i) {
+          const int q = qtl * 32 + 8 * i + rq;
+          const int64_t pr = q < N ? pair_of(q) : 0;
+          xr[hp][i] = *reinterpret_cast<const uint4*>(x + ((int64_t)b * N * N + pr) * CIN + hp * 64 + rc * 8);
         }
-        buf_store4(ors, valid ? (uint32_t)((pair * CIN + c0) * 2) : kBufSkip, v[0], v[1], v[2], v[3]);
+    }
+    Frag<bf16> cur[KC];
+    load_og(cur, tile);
+    const bf16* wlt = wl + opaque_zero();  // keep the W_o reads in the loop
+#pragma unroll
+    for (int hp = 0; hp < 2; ++hp) {
+#pragma unroll
+      for (int n2 = 0; n2 < 2; ++n2) {
+        const int nt = 2 * hp + n2;
+        Frag<bf16> f;
+        load_wfrag_lds(f, wlt, nt, 0, KC);
+        f32x16 acc = mma0(f, cur[0]);  // rows = outputs, columns = queries
+#pragma unroll
+        for (int ks = 1; ks < KC; ++ks) {
+          load_wfrag_lds(f, wlt, nt, ks, KC);
+          mma(acc, f, cur[ks]);
+        }
+        // outputs 32 n2 + 8g + 4*half .. +3 of the half, query t32
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int c = 32 * n2 + 8 * g + 4 * half;  // channel within the half
+          const f32x4 b4 = *reinterpret_cast<const f32x4*>(bl + hp * 64 + c);
+          store4(reinterpret_cast<bf16*>(sw + t32 * 128 + (((c >> 3) ^ (t32 & 7)) << 4) + (c & 7) * 2),
+                 acc[4 * g] + b4[0], acc[4 * g + 1] + b4[1], acc[4 * g + 2] + b4[2],
+                 acc[4 * g + 3] + b4[3]);
+        }
       }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int qq = 8 * i + rq;
+        uint4 v = *reinterpret_cast<const uint4*>(sw + qq * 128 + ((rc ^ (qq & 7)) << 4));
+        if (residual) {
+          const bf16x8 a = __builtin_bit_cast(bf16x8, v), xv = __builtin_bit_cast(bf16x8, xr[hp][i]);
+          float s[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) s[e] = (float)a[e] + (float)xv[e];
+          v = make_uint4(pack_bf16x2(s[0], s[1]), pack_bf16x2(s[2], s[3]), pack_bf16x2(s[4], s[5]),
+                         pack_bf16x2(s[6], s[7]));
+        }
+        const int q = qtl * 32 + qq;
+        buf_store16(ors, q < N ? (uint32_t)((pair_of(q) * CIN + hp * 64 + rc * 8) * 2) : kBufSkip, v);
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // the region is read back before the next half
     }
   }
 }

@@ -203,6 +203,52 @@ def test_tri_attn_module(dname, starting, N):
     chk(to_np(y_nomask), ref_nm, "tri_attn mask=None")
 
 
+def logit_offset_params(offset: float, seed: int = 11):
+    """Tri-attn parameters whose logits are shifted by the constant `offset`
+    (natural units) for every query and key, which the softmax ignores.
+    Channels 64..127 carry only the shift: LayerNorm weight 0 and bias
+    offset/64 there, triangle-bias weight 1 there, and no q/k/v/gate weight
+    on them; channels 0..63 form an ordinary module."""
+    P = H.draw_params(H.tri_attn_shapes(128, 128, 4), seed=seed, bias_random=True)
+    hi = slice(64, 128)
+    P["layer_norm.weight"][hi] = 0.0
+    P["layer_norm.bias"][hi] = offset / 64
+    P["linear.weight"][:, hi] = 1.0
+    for k in ("mha.linear_q.weight", "mha.linear_k.weight", "mha.linear_v.weight", "mha.linear_g.weight"):
+        P[k][:, hi] = 0.0
+    return H.bf16_params(P)
+
+
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("offset", [200.0, -200.0])
+def test_tri_attn_logit_offset(starting, offset):
+    """Logits shifted by +-200 for every key overflow (or underflow) the
+    kernels' max-free pass; the exact online-softmax pass must then produce
+    the reference result, for masked and unmasked keys."""
+    N = 64
+    log(f"tri_attn logit offset start={starting} offset={offset}")
+    P = logit_offset_params(offset)
+    x = H.bf16_round(H.pair_input(2, N, 128, seed=12))
+    # masked keys in every row and column, but none fully masked: a row with
+    # no valid key is uniform in the reference only while |logit| < 32
+    m = (np.random.default_rng(13).random((2, N, N)) < 0.8).astype(np.float32)
+    m[:, np.arange(N), np.arange(N)] = 1.0
+    mod = triattn_module(P, starting, 4, torch.bfloat16)
+    with torch.no_grad():
+        y = mod._forward_cuda(_dev(x, torch.bfloat16), _dev(m, torch.bfloat16))
+        y_nm = mod._forward_cuda(_dev(x, torch.bfloat16), None)
+    torch.cuda.synchronize()
+    # masked keys: the reference's own fp32 arithmetic (the float64 oracle's
+    # masking shortcut holds only for |logit| < 32)
+    ref = pair_ops.tri_attn(x, m, P, starting, 4, dtype=np.float32)
+    check_bf16(to_np(y), ref, "tri_attn logit offset")
+    ref_nm = pair_ops.tri_attn(x, None, P, starting, 4, dtype=np.float64)
+    check_bf16(to_np(y_nm), ref_nm, "tri_attn logit offset, mask=None")
+    # the shift changes nothing: the same module without it
+    ref0 = pair_ops.tri_attn(x, None, logit_offset_params(0.0), starting, 4, dtype=np.float64)
+    np.testing.assert_allclose(ref_nm, ref0, atol=1e-6)
+
+
 @pytest.mark.parametrize("starting", [True, False])
 @pytest.mark.parametrize("N,chunks", [(45, (16, 7, 1)), (200, (64, 77)), (130, (128, 129))])
 def test_tri_attn_row_chunks(starting, N, chunks):
