@@ -183,6 +183,131 @@ def cpu_baseline(N: int, seed: int = 0) -> dict:
     }
 
 
+# rocprofv3 kernel names -> the per-kernel names used above (first match wins)
+KERNEL_KEYS = [
+    ("trimul_prologue_bf16_kernel", "trimul_prologue"),
+    ("trimul_contract_bf16_kernel", "trimul_contract"),
+    ("trimul_epilogue_bf16_kernel", "trimul_epilogue"),
+    ("triattn_prologue_bf16_kernel", "triattn_prologue"),
+    ("triattn_flash_rh_kernel", "triattn_flash"),
+    ("triattn_flash_kernel", "triattn_flash"),
+    ("triattn_out_kernel", "triattn_out"),
+    ("ln_rows_kernel", "layernorm"),
+    ("pair_transition_bf16_kernel", "pair_transition"),
+]
+
+
+def algorithmic_bytes(N: int, B: int = 1) -> dict:
+    """Compulsory HBM bytes per launch of each forward kernel (bf16 pair
+    tensors, fp32 mask; the bench's modules run without residual)."""
+    pair = 2.0 * B * N * N * C_Z
+    mask = 4.0 * B * N * N
+    plane = 2.0 * B * N * N * C_HID
+    bias32 = 4.0 * B * HEADS * N * N
+    return {
+        "trimul_prologue": pair + mask + 2 * plane,
+        "trimul_contract": 3 * plane,
+        "trimul_epilogue": plane + 2 * pair,
+        "triattn_prologue": pair + 4 * pair + bias32,
+        "triattn_flash": 4 * pair + bias32 + mask + pair,
+        "triattn_out": 2 * pair,
+        "layernorm": 2 * pair,
+        "pair_transition": 2 * pair + mask,
+    }
+
+
+def _kernel_key(name: str):
+    for frag, key in KERNEL_KEYS:
+        if frag in name:
+            return key
+    return None
+
+
+def _pmc_per_dispatch(path: str, counter: str) -> dict:
+    """{dispatch id: (kernel name, grid size, summed counter value)} of a
+    rocprofv3 counter_collection.csv."""
+    import csv
+
+    out = {}
+    with open(path) as fh:
+        for r in csv.DictReader(fh):
+            if r["Counter_Name"] != counter:
+                continue
+            d = r["Dispatch_Id"]
+            name, grid, val = out.get(d, (r["Kernel_Name"], int(r["Grid_Size"]), 0.0))
+            out[d] = (name, grid, val + float(r["Counter_Value"]))
+    return out
+
+
+def summarize_traffic(fetch_csv: str, write_csv: str, N: int, copy_mib: int) -> int:
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of a bench run under
+    rocprofv3 --pmc, scaled by what the counters read for the calibration copy
+    (--calibrate-copy: copy_mib MiB read and written), as bytes per launch;
+    medians over each kernel's launches at this N.  Writes
+    profiles/traffic.json and prints a markdown table."""
+    fetch = _pmc_per_dispatch(fetch_csv, "FETCH_SIZE")
+    write = _pmc_per_dispatch(write_csv, "WRITE_SIZE")
+    copy_bytes = copy_mib * 2.0 ** 20
+    # the calibration copy: --calibrate-copy's copy_() runs as HIP's own
+    # buffer-copy kernel (the largest launch of it)
+    def calib(d):
+        return max(v for (n, g, v) in d.values() if "copyBuffer" in n)
+    f_fac = copy_bytes / (calib(fetch) * 1024.0)
+    w_fac = copy_bytes / (calib(write) * 1024.0)
+    alg = algorithmic_bytes(N)
+    ln_grid = None
+    by = {}
+    for src, fac, kind in ((fetch, f_fac, "fetch"), (write, w_fac, "write")):
+        for name, grid, val in src.values():
+            key = _kernel_key(name)
+            if key is None:
+                continue
+            if key == "layernorm":  # the N-sized launches only (bench also runs 2N)
+                ln_grid = min(ln_grid or grid, grid)
+                if grid != ln_grid:
+                    continue
+            by.setdefault(key, {}).setdefault(kind, []).append((grid, val * 1024.0 * fac))
+    out = {"_calibration": {"copy_bytes": int(copy_bytes), "fetch_factor": round(f_fac, 4),
+                            "write_factor": round(w_fac, 4)}}
+    print("| kernel | read MiB | written MiB | HBM MiB | algorithmic MiB | HBM / algorithmic |")
+    print("|---|---:|---:|---:|---:|---:|")
+    for key in alg:
+        if key not in by:
+            continue
+        kinds = by[key]
+        if key == "layernorm":
+            kinds = {k: [x for x in v if x[0] == ln_grid] for k, v in kinds.items()}
+        fb = statistics.median(v for _, v in kinds["fetch"])
+        wb = statistics.median(v for _, v in kinds["write"])
+        out[f"{key}@N={N}"] = {"fetch_bytes": int(fb), "write_bytes": int(wb), "hbm_bytes": int(fb + wb),
+                               "algorithmic_bytes": int(alg[key]), "ratio": round((fb + wb) / alg[key], 3)}
+        mib = 2.0 ** 20
+        print(f"| {key} | {fb / mib:.1f} | {wb / mib:.1f} | {(fb + wb) / mib:.1f} | {alg[key] / mib:.1f} | "
+              f"{(fb + wb) / alg[key]:.2f} |")
+    print(f"\ncalibration: fetch bytes = FETCH_SIZE x {f_fac:.4f} KiB, write bytes = WRITE_SIZE x {w_fac:.4f} KiB")
+    with open(os.path.join(ROOT, "profiles", "traffic.json"), "w") as fh:
+        json.dump(out, fh, indent=1)
+        fh.write("\n")
+    return 0
+
+
+def summarize_stats(stats_csv: str) -> int:
+    """Markdown table of a rocprofv3 --kernel-trace --stats kernel_stats.csv
+    (durations in microseconds per launch)."""
+    import csv
+
+    rows = list(csv.DictReader(open(stats_csv)))
+    total = sum(float(r["TotalDurationNs"]) for r in rows)
+    print("| kernel | calls | avg us | min us | max us | % of GPU time |")
+    print("|---|---:|---:|---:|---:|---:|")
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
+        name = r["Name"]
+        short = name.split("(")[0].replace("void ", "").replace("gtk::", "")
+        print(f"| {short} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | {float(r['MinNs']) / 1e3:.1f} | "
+              f"{float(r['MaxNs']) / 1e3:.1f} | {100 * float(r['TotalDurationNs']) / total:.2f} |")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -193,7 +318,17 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="after the measurements, copy a MIB-MiB fp32 tensor 3 times (a plain "
                          "copy kernel of known traffic, for scaling HBM byte counters)")
+    ap.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="no run: summarize the counter_collection.csv files of FETCH_SIZE and "
+                         "WRITE_SIZE passes over a bench run with --calibrate-copy (its MiB in "
+                         "--calibrate-copy) into profiles/traffic.json")
+    ap.add_argument("--summarize-stats", metavar="STATS_CSV",
+                    help="no run: markdown table of a rocprofv3 kernel_stats.csv")
     args = ap.parse_args()
+    if args.summarize_traffic:
+        return summarize_traffic(*args.summarize_traffic, N=args.n, copy_mib=args.calibrate_copy)
+    if args.summarize_stats:
+        return summarize_stats(args.summarize_stats)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the path has no multi-GPU implementation)", file=sys.stderr)
