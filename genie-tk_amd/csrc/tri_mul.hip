@@ -118,6 +118,8 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
   // biases in LDS: read in the loop between stores, a global load would wait
   // for the stores issued before it (loads complete in issue order)
   __shared__ float bl[2][2][CH];  // [side][projection, gate as 2^b_g]
+  // the pair mask of each wave's current step (64 consecutive pairs)
+  __shared__ __attribute__((aligned(16))) float ml[WAVES][64];
   copy_to_lds_async(wl[0], w.w_ap, PE * 2);
   copy_to_lds_async(wl[1], w.w_ag, PE * 2);
   copy_to_lds_async(wl[2], w.w_bp, PE * 2);
@@ -160,35 +162,42 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
     }
   };
 
+  // The mask of the step's 64 pairs (zero outside the grid): one load per
+  // lane (pair vt*32 + lane), staged in the wave's LDS slot and read back by
+  // each lane as its 16 output pairs of a tile when it stores.
+  auto load_mask = [&](int64_t s) {
+    const int64_t tile = 2 * s;
+    const int vt = (int)(tile % vtiles);
+    const int f = (int)((tile / vtiles) % Np);
+    const int b = (int)(tile / ((int64_t)vtiles * Np));
+    const int v = vt * 32 + lane;
+    const bool ok = f < N && v < N;
+    const int64_t idx = ((int64_t)b * N + (outgoing ? f : v)) * N + (outgoing ? v : f);
+    return ok ? (mask ? mask[ok ? idx : 0] : 1.f) : 0.f;
+  };
+
   int64_t s = (int64_t)blockIdx.x * WAVES + wave;
   const int64_t sstride = (int64_t)gridDim.x * WAVES;
+  // this wave's first step: rows and mask in flight (the next step's are
+  // loaded ahead of each step's stores)
+  Frag<bf16> zr[2][KCH];
+  float mv = 0.f;
+  if (s < nsteps) {
+    load_z(zr, s);
+    mv = load_mask(s);
+  }
   for (; s < nsteps; s += sstride) {
     const int64_t tile = 2 * s;
     const int vt = (int)(tile % vtiles);
     const int f = (int)((tile / vtiles) % Np);
     const int b = (int)(tile / ((int64_t)vtiles * Np));
     Frag<bf16> xf[2][KCH];
-    {
-      Frag<bf16> zr[2][KCH];
-      load_z(zr, s);
-      ln_frags_bf16<CZ>(xf[0], zr[0], eps);
-      ln_frags_bf16<CZ>(xf[1], zr[1], eps);
-    }
-    // mask of this lane's 16 output pairs of each tile (zero outside the grid)
-    float mk[2][16];
-    {
-      const bool frow = f < N;
-      const int64_t base = ((int64_t)b * N + (outgoing ? f : 0)) * N + (outgoing ? 0 : f);
-      const int64_t mstep = outgoing ? 1 : N;
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int v0 = (vt + u) * 32 + 16 * half;
-#pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const bool ok = frow && v0 + j < N;
-          mk[u][j] = ok ? (mask ? mask[base + (int64_t)(v0 + j) * mstep] : 1.f) : 0.f;
-        }
-      }
+    ln_frags_bf16<CZ>(xf[0], zr[0], eps);
+    ln_frags_bf16<CZ>(xf[1], zr[1], eps);
+    ml[wave][lane] = mv;
+    if (s + sstride < nsteps) {
+      load_z(zr, s + sstride);
+      mv = load_mask(s + sstride);
     }
 #pragma unroll 1
     for (int side = 0; side < 2; ++side) {
@@ -220,14 +229,22 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
         for (int u = 0; u < 2; ++u) {
           const f32x16& ap = u ? ap1 : ap0;
           const f32x16& ag = u ? ag1 : ag0;
+          // mask of this lane's pairs 32u + 16*half .. +15
+          float mk[16];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const f32x4 m4 = *reinterpret_cast<const f32x4*>(&ml[wave][32 * u + 16 * half + 4 * q]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mk[4 * q + e] = m4[e];
+          }
           uint32_t pk[8];
 #pragma unroll
           for (int j = 0; j < 16; j += 2) {
             const float o0 = (ap[j] + bpc) *
-                             __builtin_amdgcn_rcpf(fmaf(__builtin_amdgcn_exp2f(ag[j]), ebg, 1.f)) * mk[u][j];
+                             __builtin_amdgcn_rcpf(fmaf(__builtin_amdgcn_exp2f(ag[j]), ebg, 1.f)) * mk[j];
             const float o1 = (ap[j + 1] + bpc) *
                              __builtin_amdgcn_rcpf(fmaf(__builtin_amdgcn_exp2f(ag[j + 1]), ebg, 1.f)) *
-                             mk[u][j + 1];
+                             mk[j + 1];
             pk[j / 2] = pack_bf16x2(o0, o1);
           }
           uint4* o = reinterpret_cast<uint4*>(dst + (int64_t)cc * plane + 32 * u);
