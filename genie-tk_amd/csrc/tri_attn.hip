@@ -247,13 +247,16 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
 //     Padding values are those of triattn_prologue_kernel.
 // ---------------------------------------------------------------------------
 // MODE bit 0: q, k, v^T and gate; bit 1: the triangle bias; bit 2: the bias
-// in fp32 (ws.biasf) instead of bf16 (ws.bias).  The tiles cover rows r0 ..
-// r0 + nrows - 1 of every batch element: [B][nrows][Np / 32].
+// in fp32 (ws.biasf) instead of bf16 (ws.bias); bit 3: q, k, v^T and gate in
+// the tiled layout of the (row, head) flash kernel (each (row, head) block of
+// 32 channels x Np positions as Np/32 tiles [32 channels][32 positions],
+// 2 KiB contiguous) instead of channel-major rows.  The tiles cover rows r0
+// .. r0 + nrows - 1 of every batch element: [B][nrows][Np / 32].
 template <int CIN, int H, int MODE>
 __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
     const bf16* __restrict__ x, TriAttnPacked<bf16> w, AttnWs<bf16> ws, int N, int Np,
     int starting, float eps, int64_t ntiles, int r0, int nrows) {
-  static_assert((MODE & 3) != 0 && MODE <= 7, "q/k/v/gate, bias, or both");
+  static_assert((MODE & 3) != 0 && MODE <= 15, "q/k/v/gate, bias, or both");
   constexpr int CH = H * HD;
   constexpr int KCH = CIN / 16;
   constexpr int PE = (CH / 32) * KCH * 512;  // one packed c_in -> c_h projection
@@ -351,6 +354,8 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
         for (int m = 0; m < 16; m += 2)
           pk[m / 2] = pack_bf16x2(gate_from_u(acc[m] + bc), gate_from_u(acc[m + 1] + bc));
         dst = ws.gate + (rowbase * CH + h * HD + i32) * (int64_t)Np + j0;
+        if constexpr ((MODE & 8) != 0)
+          dst = ws.gate + (rowbase * CH + h * HD) * (int64_t)Np + vt * 1024 + i32 * 32 + 16 * half;
       } else {
         // q, k, v: zero outside the N x N pair grid; v^T in vt_pos order, which
         // swaps bits 2 and 3 of the position inside its group of 16
@@ -362,6 +367,8 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
         }
         bf16* base = kind == 0 ? ws.q : kind == 1 ? ws.k : ws.vt;
         dst = base + ((rowbase * H + h) * HD + i32) * (int64_t)Np + j0;
+        if constexpr ((MODE & 8) != 0)
+          dst = base + (rowbase * H + h) * HD * (int64_t)Np + vt * 1024 + i32 * 32 + 16 * half;
       }
       uint4* o = reinterpret_cast<uint4*>(dst);
       o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
@@ -1028,8 +1035,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
   {
     const bf16* kbase = ws.k + (rowbase * H + h) * (int64_t)HD * Np;
     const bf16* vbase = ws.vt + (rowbase * H + h) * (int64_t)HD * Np;
+    // tiled layout: key tile t is [32 d][32 keys], 2 KiB contiguous
     const uint32_t ln = (uint32_t)lane;
-    const uint32_t rowoff = (ln >> 2) * (uint32_t)Np * 2;
+    const uint32_t rowoff = (ln >> 2) * 64;
     const uint32_t voff_k = rowoff + (ln & 3) * 16;
     const uint32_t voff_v = rowoff + (((ln & 3) ^ ((ln >> 4) & 3)) * 16);
     const uint32_t kv_lds = lds_addr(kv);
@@ -1037,7 +1045,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
       const int kind = c >= 2 * nt;
       const int cr = c - kind * 2 * nt;
       const int t = cr >> 1, rh = cr & 1;
-      const bf16* src = (kind ? vbase : kbase) + (int64_t)(16 * rh) * Np + 32 * t;
+      const bf16* src = (kind ? vbase : kbase) + t * 1024 + rh * 512;
       g2lds16_sv(src, kind ? voff_v : voff_k, kv_lds + ((kind * NTM + t) * 2 + rh) * 1024);
     }
   }
@@ -1064,14 +1072,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
 
   const uint32_t stg_lds = lds_addr(stg[wave]);
   char* const sw = stg[wave];
-  // q or gate tile, channel-major [32 channels][32 queries] -> the wave's
-  // region, 64-byte rows; copy j moves channels 16j .. 16j+15, lane l takes
-  // channel 16j + l/4, queries 8*(l%4) .. +7
+  // q or gate tile [32 channels][32 queries] (2 KiB contiguous in the tiled
+  // layout) -> the wave's region, 64-byte rows; copy j moves channels
+  // 16j .. 16j+15, lane l takes channel 16j + l/4, queries 8*(l%4) .. +7
   auto issue_cq = [&](const bf16* src) {
     const uint32_t ln = (uint32_t)(lane + opaque_zero());
-    const uint32_t voff = ((ln >> 2) * (uint32_t)Np + (ln & 3) * 8) * 2;
+    const uint32_t voff = ln * 16;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) g2lds16_sv(src + (int64_t)j * 16 * Np, voff, stg_lds + j * 1024);
+    for (int j = 0; j < 2; ++j) g2lds16_sv(src + j * 512, voff, stg_lds + j * 1024);
   };
   // channels c0 .. c0+3 of this lane's query t32 (transposing read); ln is
   // the lane id through opaque_zero, so that these per-lane addresses are
@@ -1202,7 +1210,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();  // K^T / V^T resident for every wave
     for (int qt = wave; qt < nq; qt += NW) {
-      issue_cq(g_row + qt * 32);
+      issue_cq(g_row + qt * 1024);
       f32x16 o = zero16();
       float l_run = 0.f;
       for (int t = 0; t < nt; ++t) {
@@ -1218,7 +1226,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
   f32x16 bq[KB];
   int qt = wave;
   if (qt < nq) {
-    issue_cq(q_row + qt * 32);
+    issue_cq(q_row + qt * 1024);
 #pragma unroll
     for (int u = 0; u < KB; ++u) load_bias(bq[u], qt * 32, u);
   }
@@ -1239,7 +1247,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
       qf[m].v = __builtin_bit_cast(bf16x8, v8);
     }
     __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0): q read back, the region is free
-    issue_cq(g_row + q0);                // the gate tile lands behind the key loop
+    issue_cq(g_row + qt * 1024);                // the gate tile lands behind the key loop
 
     // Fast pass: P = 2^s with no running maximum.  Exact (softmax is shift
     // invariant, and fp32 / bf16 keep relative precision) while every 2^s
@@ -1296,7 +1304,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
       }
       l_tot = lane_pair_sum(l_run);
     }
-    finish(q0, o, l_tot, qt + NW < nq ? q_row + (qt + NW) * 32 : nullptr);
+    finish(q0, o, l_tot, qt + NW < nq ? q_row + (qt + NW) * 1024 : nullptr);
   }
 }
 
@@ -1631,7 +1639,7 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
     };
     if (!chunked) {
       // every row, padding included
-      if (rh) prologue(std::integral_constant<int, 7>(), 0, Np);
+      if (rh) prologue(std::integral_constant<int, 15>(), 0, Np);
       else prologue(std::integral_constant<int, 3>(), 0, Np);
       GTK_LAUNCH_CHECK();
       flash(0, (int)N);
@@ -1644,7 +1652,8 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
       for (int64_t r0 = 0; r0 < N; r0 += chunk_rows) {
         const int nrows = (int)std::min<int64_t>(chunk_rows, N - r0);
         a.r0 = (int)r0;
-        prologue(std::integral_constant<int, 1>(), (int)r0, nrows);
+        if (rh) prologue(std::integral_constant<int, 9>(), (int)r0, nrows);
+        else prologue(std::integral_constant<int, 1>(), (int)r0, nrows);
         GTK_LAUNCH_CHECK();
         flash((int)r0, nrows);
         GTK_LAUNCH_CHECK();
