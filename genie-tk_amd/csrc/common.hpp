@@ -403,6 +403,14 @@ __device__ __forceinline__ void barrier_only() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// XCD-aware block order: hardware deals consecutive block ids to the 8 XCDs
+// round-robin; remap so that each XCD receives a contiguous range of logical
+// blocks (blocks that share operands then share that XCD's L2).
+__device__ __forceinline__ int64_t xcd_remap(int64_t lin, int64_t total) {
+  if (total % 8 != 0) return lin;
+  return (lin % 8) * (total / 8) + lin / 8;
+}
+
 // A zero the compiler cannot see through.  Adding it to a loop-invariant LDS
 // address inside a loop keeps the loads in the loop: hoisted out, the
 // fragments would stay live across the whole loop and spill.

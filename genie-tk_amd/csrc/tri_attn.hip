@@ -630,13 +630,6 @@ __device__ __forceinline__ float lane_pair_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Hardware deals consecutive block ids to the 8 XCDs round-robin; remap so
-// each XCD receives a contiguous range of logical blocks.
-__device__ __forceinline__ int64_t xcd_remap(int64_t lin, int64_t total) {
-  if (total % 8 != 0) return lin;
-  return (lin % 8) * (total / 8) + lin / 8;
-}
-
 
 template <int CIN, int H, int QT>
 __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))) void triattn_flash_kernel(

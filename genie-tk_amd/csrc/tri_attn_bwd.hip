@@ -30,6 +30,7 @@
 // hold -1e9 + log l.
 #include <algorithm>
 #include <cmath>
+#include <type_traits>
 
 #include "capi_util.hpp"
 #include "common.hpp"
@@ -55,6 +56,7 @@ template <typename T> struct AttnBwdBufs {
   T *o, *dor, *dot, *dq, *dk, *dv; // o, dO, dq, dk, dv position-major; dot d-major
   T* gt;                           // gate sigmoid [B][N][np][CH]
   T* bias;                         // triangle bias [B][H][N][N]
+  float *biasT, *biasS;            // bias / scale, fp32, fragment order (bias_frag_elem)
   float* kmask;                    // [B][N][np]: 1 valid key, 0 masked
   float *mrow, *linv, *dd;         // [B][N][H][np]
   float* db;                       // dL/dbias [B][H][N][N]
@@ -100,6 +102,21 @@ __device__ __forceinline__ float score_of(float acc, float scale, float bias, fl
   return exists ? (km > 0.5f ? scale * acc + bias : kMaskScore) : -INFINITY;
 }
 
+// Triangle-bias copies of the (row, head) kernels: fp32 tiles of 32 x 32 in
+// the accumulator order of the score tile that consumes them, 4 KiB each.
+// Element (h, a, k) of an orientation whose lanes are positions a and whose
+// registers are positions k (register 4g + rr of lane hh*32 + a%32 <-> k%32 =
+// 8g + 4hh + rr), at float index
+//   (((h * nt + a/32) * nt + k/32) * 4 + g) * 64 + hh*32 + a%32) * 4 + rr.
+// biasT has lanes = queries, registers = keys (S^T = K Q^T); biasS has lanes =
+// keys, registers = queries (S = Q K^T).  Both hold bias / scale, so the score
+// MFMA accumulates q.k onto them directly.
+__host__ __device__ __forceinline__ int64_t bias_frag_elem(int h, int a, int k, int np) {
+  const int nt = np / 32;
+  const int64_t tile = ((int64_t)h * nt + (a >> 5)) * nt + (k >> 5);
+  return (((tile * 4 + ((k & 31) >> 3)) * 64 + ((k >> 2) & 1) * 32 + (a & 31)) << 2) + (k & 3);
+}
+
 // ---------------------------------------------------------------------------
 // proj: one 32-position tile of one attention row per wave
 // ---------------------------------------------------------------------------
@@ -108,7 +125,7 @@ __global__ __launch_bounds__(256) void attn_bwd_proj_kernel(const T* __restrict_
                                                             const float* __restrict__ mask,
                                                             AttnBwdW<T> w, AttnBwdBufs<T> bf,
                                                             int B, int N, int np, int starting,
-                                                            float eps) {
+                                                            float eps, float inv_scale) {
   constexpr int CH = H * AD;
   const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
   const int jtiles = np / 32;
@@ -168,9 +185,16 @@ __global__ __launch_bounds__(256) void attn_bwd_proj_kernel(const T* __restrict_
     // triangle bias: outputs 0..H-1 sit in lanes of half 0, acc[0..H-1]
     const f32x16 acc = row_gemm_tile<T, C, true>(xf, w.w_b, 0);
     if (valid && half == 0) {
+      float* bT = bf.biasT + (int64_t)b * H * np * np;
+      float* bS = bf.biasS + (int64_t)b * H * np * np;
 #pragma unroll
-      for (int h = 0; h < H; ++h)
-        bf.bias[(((int64_t)b * H + h) * N + r) * N + j] = cvt<T>(acc[h] + w.b_b[h]);
+      for (int h = 0; h < H; ++h) {
+        const T bv = cvt<T>(acc[h] + w.b_b[h]);
+        bf.bias[(((int64_t)b * H + h) * N + r) * N + j] = bv;
+        const float bs = to_f32(bv) * inv_scale;  // query r, key j
+        bT[bias_frag_elem(h, r, j, np)] = bs;
+        bS[bias_frag_elem(h, j, r, np)] = bs;
+      }
     }
   }
   if (half == 0) bf.kmask[((int64_t)b * N + r) * np + j] = valid ? (mask ? mask[xp] : 1.f) : 0.f;
@@ -503,6 +527,310 @@ __global__ __launch_bounds__(256) void attn_bwd_dbias_kernel(AttnBwdBufs<T> bf, 
 }
 
 // ---------------------------------------------------------------------------
+// (row, head) kernels of the bf16 path (np <= 1024): one 8-wave block per
+// (row, head).  The operands every wave of the block reads (Q and dO for
+// dK / dV, K and V for dQ) sit in LDS as [np][32] bf16 rows of 64 bytes, with
+// 16-byte chunk c of row p at chunk c ^ ((p >> 2) & 3).  They are read both
+// as fragments with d along k (ds_read_b128, conflict free) and transposed,
+// with positions along k in the accumulator order of vals_to_frags
+// (ds_read_b64_tr_b16).  Scores are taken in log2 units: with acc = bias /
+// scale + q.k (the MFMA accumulates onto the fragment-order bias copies),
+// s * log2(e) - lse2 = fma(acc, scale * log2(e), -lse2) and P = 2^that, where
+// lse2 = (m + log l) * log2(e) of the query.  A row without a valid key
+// attends uniformly (P = 1/l = 1/N over its real keys), as in
+// attn_bwd_fwd_kernel.
+// ---------------------------------------------------------------------------
+constexpr int kRhWaves = 8;
+
+// [np][32] rows of two operands of one (row, head) into swizzled LDS rows:
+// np / 16 copies of 1 KiB each, spread over the block's waves.  The caller
+// waits for its copies and synchronises the block.
+__device__ __forceinline__ void rows2_to_lds(const bf16* a, char* la, const bf16* b, char* lb, int np) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t rin = (uint32_t)lane >> 2;  // row within the copy (16 rows of 64 bytes)
+  const uint32_t voff = rin * 64 + ((((uint32_t)lane & 3) ^ ((rin >> 2) & 3)) << 4);
+  const int per = np / 16;
+  for (int c = wave; c < 2 * per; c += kRhWaves) {
+    const bool second = c >= per;
+    const int cc = second ? c - per : c;
+    g2lds16_sv(reinterpret_cast<const char*>(second ? b : a) + cc * 1024, voff,
+               lds_addr(second ? lb : la) + cc * 1024);
+  }
+}
+
+// Per-lane byte offsets into a swizzled 32-row tile.
+struct RhOffsets {
+  int nrm[2];  // fragment with rows = positions (lane&31), k = d 16m .. 16m+15 (k-step m)
+  int tr[2];   // transposed reads: rows = d, k = positions 4(lane>>5) + {0..3, 8..11} (+ 1024 for the
+               // positions 16..31 of the tile)
+  __device__ __forceinline__ RhOffsets() {
+    const int lane = threadIdx.x & 63;
+    const int half = lane >> 5, t32 = lane & 31;
+    const int sw = (t32 >> 2) & 3;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) nrm[m] = t32 * 64 + (((2 * m + half) ^ sw) << 4);
+    // ds_read_b64_tr_b16: within 16 lanes, lane L takes element L%4 of the 4
+    // elements at the addresses of lanes L/4, 4 + L/4, 8 + L/4, 12 + L/4.
+    // Lane j of group G supplies row 4(G>>1) + j/4 (+8), columns
+    // 16(G&1) + 4(j&3) .. +3.
+    const int G = lane >> 4, j = lane & 15;
+    const int chunk = 2 * (G & 1) + ((j & 3) >> 1);
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+      tr[p] = (4 * (G >> 1) + (j >> 2) + 8 * p) * 64 + ((chunk ^ ((G >> 1) + 2 * p)) << 4) + 8 * (j & 1);
+  }
+};
+
+__device__ __forceinline__ Frag<bf16> lds_frag(const char* p) {
+  Frag<bf16> f;
+  f.load(reinterpret_cast<const bf16*>(p));
+  return f;
+}
+
+// Transposed fragment gp (positions 16gp .. 16gp+15 of the tile at `tile`).
+__device__ __forceinline__ Frag<bf16> lds_frag_tr(const char* tile, const RhOffsets& o, int gp) {
+  typedef short s16x8 __attribute__((ext_vector_type(8)));
+  const s16x4 p0 = lds_read_tr16(tile + gp * 1024 + o.tr[0]);
+  const s16x4 p1 = lds_read_tr16(tile + gp * 1024 + o.tr[1]);
+  const s16x8 v8 = {p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]};
+  Frag<bf16> f;
+  f.v = __builtin_bit_cast(bf16x8, v8);
+  return f;
+}
+
+// Does row br have a valid key?  (wave-uniform)
+__device__ __forceinline__ bool rh_row_valid(const float* km_row, int N) {
+  const int lane = threadIdx.x & 63;
+  bool any = false;
+  for (int k0 = 0; k0 < N; k0 += 64) {
+    const int k = k0 + lane;
+    any = any || (k < N && km_row[k] > 0.5f);
+  }
+  return __ballot(any) != 0ull;
+}
+
+// lse2 of query q of (row, head) rh: (m + log l) log2(e), or -log2(1/l) when
+// the row has no valid key (its scores are then taken as 0)
+__device__ __forceinline__ float rh_lse2(const AttnBwdBufs<bf16>& bf, int64_t idx, bool row_valid) {
+  const float li = bf.linv[idx];
+  return row_valid ? (bf.mrow[idx] - logf(li)) * kLog2e : -log2f(li);
+}
+
+// dK and dV: block (row, head), wave w owns key tiles w, w + 8, ...; lane = key.
+template <int NPM>
+__global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dkdv_rh_kernel(AttnBwdBufs<bf16> bf, int B,
+                                                                      int N, int np, float scale) {
+  constexpr int H = 4;
+  __shared__ __attribute__((aligned(1024))) char qs[NPM * 64];
+  __shared__ __attribute__((aligned(1024))) char dos[NPM * 64];
+  __shared__ __attribute__((aligned(16))) float lse_s[NPM];
+  __shared__ __attribute__((aligned(16))) float dd_s[NPM];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5, t32 = lane & 31;
+  const int nt = np / 32;
+  const int64_t rows = (int64_t)B * N;
+  const int64_t lin = xcd_remap(blockIdx.x, gridDim.x);
+  const int h = (int)(lin / rows);  // head-major: the blocks of one XCD share one head's bias
+  const int64_t br = lin - (int64_t)h * rows;
+  const int b = (int)(br / N);
+  const int64_t rh = br * H + h;
+  rows2_to_lds(bf.qr + rh * np * AD, qs, bf.dor + rh * np * AD, dos, np);
+  const float* km_row = bf.kmask + br * np;
+  const bool row_valid = rh_row_valid(km_row, N);
+  for (int q = tid; q < np; q += 64 * kRhWaves) {
+    lse_s[q] = rh_lse2(bf, rh * np + q, row_valid);
+    dd_s[q] = bf.dd[rh * np + q];
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  const RhOffsets off;
+  const float c2 = scale * kLog2e;
+  const int nq = (N + 31) / 32;  // query tiles with a real query
+  const float* bS = bf.biasS + ((int64_t)b * H + h) * np * np + lane * 4;
+  for (int kt = wave; kt < nt; kt += kRhWaves) {
+    const int key = kt * 32 + t32;
+    const bf16* krow = bf.kr + (rh * np + key) * AD + 8 * half;
+    const bf16* vrow = bf.vr + (rh * np + key) * AD + 8 * half;
+    Frag<bf16> kf[2], vf[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      kf[m].load(krow + 16 * m);
+      vf[m].load(vrow + 16 * m);
+    }
+    // excluded key (no weight): padding, or masked in a row with a valid key
+    const bool excl = row_valid ? !(km_row[key] > 0.5f) : key >= N;
+    const bool any_excl = __ballot(excl) != 0ull;
+    const float* btile = bS + (int64_t)kt * nt * 1024;
+    f32x16 dk = zero16(), dv = zero16();
+    for (int qt = 0; qt < nq; ++qt) {
+      const char* qtile = qs + qt * 2048;
+      const char* dtile = dos + qt * 2048;
+      f32x16 sc = zero16();
+      if (row_valid) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(btile + qt * 1024 + g * 256);
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) sc[4 * g + rr] = v[rr];
+        }
+#pragma unroll
+        for (int m = 0; m < 2; ++m) mma(sc, lds_frag(qtile + off.nrm[m]), kf[m]);  // S: rows q, cols key
+      }
+      f32x16 dp = mma0(lds_frag(dtile + off.nrm[0]), vf[0]);
+      mma(dp, lds_frag(dtile + off.nrm[1]), vf[1]);
+      float pv[16], dsv[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int q0 = qt * 32 + 8 * g + 4 * half;
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(lse_s + q0);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(dd_s + q0);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const float s2 = row_valid ? fmaf(sc[4 * g + rr], c2, -l4[rr]) : -l4[rr];
+          pv[4 * g + rr] = __builtin_amdgcn_exp2f(s2);
+        }
+        if (qt * 32 + 32 > N) {
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr)
+            if (q0 + rr >= N) pv[4 * g + rr] = 0.f;  // padded query
+        }
+        if (any_excl && excl) {
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) pv[4 * g + rr] = 0.f;
+        }
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) dsv[4 * g + rr] = pv[4 * g + rr] * (dp[4 * g + rr] - d4[rr]);
+      }
+      Frag<bf16> fp[2], fs[2];
+      vals_to_frags<bf16>(fp, pv);
+      vals_to_frags<bf16>(fs, dsv);
+#pragma unroll
+      for (int gp = 0; gp < 2; ++gp) {
+        mma(dv, lds_frag_tr(dtile, off, gp), fp[gp]);  // dV^T[d][key] += dO^T P
+        mma(dk, lds_frag_tr(qtile, off, gp), fs[gp]);  // dK^T[d][key] += Q^T dS
+      }
+    }
+    bf16* dko = bf.dk + (rh * np + key) * AD;
+    bf16* dvo = bf.dv + (rh * np + key) * AD;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int d0 = 8 * g + 4 * half;
+      store4(dko + d0, scale * dk[4 * g], scale * dk[4 * g + 1], scale * dk[4 * g + 2], scale * dk[4 * g + 3]);
+      store4(dvo + d0, dv[4 * g], dv[4 * g + 1], dv[4 * g + 2], dv[4 * g + 3]);
+    }
+  }
+}
+
+// dQ: block (row, head), wave w owns query tiles w, w + 8, ...; lane = query.
+template <int NPM>
+__global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dq_rh_kernel(AttnBwdBufs<bf16> bf, int B,
+                                                                    int N, int np, float scale) {
+  constexpr int H = 4;
+  __shared__ __attribute__((aligned(1024))) char ks[NPM * 64];
+  __shared__ __attribute__((aligned(1024))) char vs[NPM * 64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5, t32 = lane & 31;
+  const int nt = np / 32;
+  const int64_t rows = (int64_t)B * N;
+  const int64_t lin = xcd_remap(blockIdx.x, gridDim.x);
+  const int h = (int)(lin / rows);
+  const int64_t br = lin - (int64_t)h * rows;
+  const int b = (int)(br / N);
+  const int64_t rh = br * H + h;
+  rows2_to_lds(bf.kr + rh * np * AD, ks, bf.vr + rh * np * AD, vs, np);
+  const float* km_row = bf.kmask + br * np;
+  const bool row_valid = rh_row_valid(km_row, N);
+  // excluded keys (padding, and masked keys of a row with a valid key): bit j
+  // of lane t's word is key 32t + j
+  uint32_t kxv = 0;
+  for (int k0 = 0; k0 < np; k0 += 64) {
+    const int k = k0 + lane;
+    const bool ex = k < np ? (row_valid ? !(km_row[k] > 0.5f) : k >= N) : true;
+    const unsigned long long eb = __ballot(ex);
+    const int w0 = k0 >> 5;
+    if (lane == w0) kxv = (uint32_t)eb;
+    if (lane == w0 + 1) kxv = (uint32_t)(eb >> 32);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  const RhOffsets off;
+  const float c2 = scale * kLog2e;
+  const int nk = (N + 31) / 32;  // key tiles with a real key
+  const float* bT = bf.biasT + ((int64_t)b * H + h) * np * np + lane * 4;
+  for (int qt = wave; qt < nt; qt += kRhWaves) {
+    const int q = qt * 32 + t32;
+    const bf16* qrow = bf.qr + (rh * np + q) * AD + 8 * half;
+    const bf16* drow = bf.dor + (rh * np + q) * AD + 8 * half;
+    Frag<bf16> qf[2], df[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      qf[m].load(qrow + 16 * m);
+      df[m].load(drow + 16 * m);
+    }
+    const float lse2 = rh_lse2(bf, rh * np + q, row_valid);
+    const float dq_ = bf.dd[rh * np + q];
+    const bool qpad = q >= N;
+    const bool tile_pad = qt * 32 + 32 > N;
+    const float* btile = bT + (int64_t)qt * nt * 1024;
+    f32x16 dq = zero16();
+    for (int kt = 0; kt < nk; ++kt) {
+      const char* ktile = ks + kt * 2048;
+      const char* vtile = vs + kt * 2048;
+      f32x16 sc = zero16();
+      if (row_valid) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(btile + kt * 1024 + g * 256);
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) sc[4 * g + rr] = v[rr];
+        }
+#pragma unroll
+        for (int m = 0; m < 2; ++m) mma(sc, lds_frag(ktile + off.nrm[m]), qf[m]);  // S^T: rows key, cols q
+      }
+      f32x16 dp = mma0(lds_frag(vtile + off.nrm[0]), df[0]);  // dP^T
+      mma(dp, lds_frag(vtile + off.nrm[1]), df[1]);
+      float pv[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float s2 = row_valid ? fmaf(sc[e], c2, -lse2) : -lse2;
+        pv[e] = __builtin_amdgcn_exp2f(s2);
+      }
+      const unsigned kx = __builtin_amdgcn_readlane(kxv, kt);
+      if (kx != 0u) {
+        // this lane's keys 8g + 4*half + rr: bits 8g + rr after the shift
+        const unsigned kl = kx >> (4 * half);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr)
+            if (__builtin_amdgcn_ubfe(kl, 8 * g + rr, 1)) pv[4 * g + rr] = 0.f;
+      }
+      if (tile_pad && qpad) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) pv[e] = 0.f;
+      }
+      float dsv[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) dsv[e] = pv[e] * (dp[e] - dq_);
+      Frag<bf16> fs[2];
+      vals_to_frags<bf16>(fs, dsv);
+#pragma unroll
+      for (int gp = 0; gp < 2; ++gp) mma(dq, lds_frag_tr(ktile, off, gp), fs[gp]);  // dQ^T[d][q] += K^T dS^T
+    }
+    bf16* dqo = bf.dq + (rh * np + q) * AD;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      store4(dqo + 8 * g + 4 * half, scale * dq[4 * g], scale * dq[4 * g + 1], scale * dq[4 * g + 2],
+             scale * dq[4 * g + 3]);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // pro: dxn and the LayerNorm backward; per 32-position tile of one row
 // ---------------------------------------------------------------------------
 template <typename T, int C, int H>
@@ -673,6 +1001,8 @@ static AttnBwdWs<T> carve_attn_bwd(Carve& cv, int64_t B, int64_t N, int C, int H
   for (T** t : big) *t = cv.take<T>(hp);
   b.gt = cv.take<T>(B * N * np * CH);
   b.bias = cv.take<T>(B * H * N * N);
+  b.biasT = cv.take<float>(B * H * np * np);
+  b.biasS = cv.take<float>(B * H * np * np);
   b.kmask = cv.take<float>(B * N * np);
   b.mrow = cv.take<float>(B * N * H * np);
   b.linv = cv.take<float>(B * N * H * np);
@@ -740,8 +1070,8 @@ static int bwd_triattn(const void* x, const float* mask, const void* dy,
   auto g4 = [](int64_t t) { return (unsigned)((t + 3) / 4); };
   {
     StageTimer timer("triattn_bwd_proj", st);
-    attn_bwd_proj_kernel<T, C, H><<<g4(rowtiles), 256, 0, st>>>((const T*)x, mask, a.w, a.b,
-                                                                 (int)B, (int)N, np, starting, eps);
+    attn_bwd_proj_kernel<T, C, H><<<g4(rowtiles), 256, 0, st>>>(
+        (const T*)x, mask, a.w, a.b, (int)B, (int)N, np, starting, eps, 1.0f / scale);
     GTK_LAUNCH_CHECK();
   }
   {
@@ -755,15 +1085,46 @@ static int bwd_triattn(const void* x, const float* mask, const void* dy,
                                                                 (int)N, np, starting);
     GTK_LAUNCH_CHECK();
   }
-  {
-    StageTimer timer("triattn_bwd_dkdv", st);
-    attn_bwd_dkdv_kernel<T, H><<<g4(headtiles), 256, 0, st>>>(a.b, (int)B, (int)N, np, scale);
-    GTK_LAUNCH_CHECK();
+  bool rh_done = false;
+  if constexpr (std::is_same<T, bf16>::value) {
+    if (np <= 1024) {
+      // (row, head) blocks: Q, dO (dK, dV) or K, V (dQ) of the row resident in LDS
+      const int64_t rblocks = B * N * H;
+      GTK_REQUIRE(rblocks < (1ll << 31), GTK_EUNSUPPORTED, "attention backward grid too large");
+      auto launch_rh = [&](auto npm) {
+        constexpr int NPM = decltype(npm)::value;
+        {
+          StageTimer timer("triattn_bwd_dkdv", st);
+          attn_bwd_dkdv_rh_kernel<NPM><<<(unsigned)rblocks, 64 * kRhWaves, 0, st>>>(a.b, (int)B, (int)N, np,
+                                                                                   scale);
+          GTK_LAUNCH_CHECK();
+        }
+        {
+          StageTimer timer("triattn_bwd_dq", st);
+          attn_bwd_dq_rh_kernel<NPM><<<(unsigned)rblocks, 64 * kRhWaves, 0, st>>>(a.b, (int)B, (int)N, np,
+                                                                                 scale);
+          GTK_LAUNCH_CHECK();
+        }
+        return GTK_OK;
+      };
+      if (np <= 256) rc = launch_rh(std::integral_constant<int, 256>());
+      else if (np <= 512) rc = launch_rh(std::integral_constant<int, 512>());
+      else rc = launch_rh(std::integral_constant<int, 1024>());
+      if (rc) return rc;
+      rh_done = true;
+    }
   }
-  {
-    StageTimer timer("triattn_bwd_dq", st);
-    attn_bwd_dq_kernel<T, H><<<g4(headtiles), 256, 0, st>>>(a.b, (int)B, (int)N, np, scale);
-    GTK_LAUNCH_CHECK();
+  if (!rh_done) {
+    {
+      StageTimer timer("triattn_bwd_dkdv", st);
+      attn_bwd_dkdv_kernel<T, H><<<g4(headtiles), 256, 0, st>>>(a.b, (int)B, (int)N, np, scale);
+      GTK_LAUNCH_CHECK();
+    }
+    {
+      StageTimer timer("triattn_bwd_dq", st);
+      attn_bwd_dq_kernel<T, H><<<g4(headtiles), 256, 0, st>>>(a.b, (int)B, (int)N, np, scale);
+      GTK_LAUNCH_CHECK();
+    }
   }
   {
     StageTimer timer("triattn_bwd_dbias", st);

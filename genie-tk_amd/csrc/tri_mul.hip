@@ -27,15 +27,6 @@
 
 namespace gtk {
 
-// XCD-aware block order: hardware deals consecutive block ids to the 8 XCDs
-// round-robin; remap so that each XCD receives a contiguous range of logical
-// blocks (tiles of the same channel share that XCD's L2).
-__device__ __forceinline__ int64_t xcd_remap(int64_t lin, int64_t total) {
-  if (total % 8 != 0) return lin;
-  const int64_t per = total / 8;
-  return (lin % 8) * per + lin / 8;
-}
-
 // ---------------------------------------------------------------------------
 // 1. Prologue
 // ---------------------------------------------------------------------------

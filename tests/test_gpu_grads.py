@@ -85,7 +85,7 @@ def test_tri_mul_backward_runs_the_kernels(monkeypatch):
 
 @pytest.mark.parametrize("dname", ["fp32", "bf16"])
 @pytest.mark.parametrize("starting", [True, False])
-@pytest.mark.parametrize("N", [40, 77])
+@pytest.mark.parametrize("N", [40, 77, 130])
 def test_tri_attn_backward(dname, starting, N):
     """Includes fully masked rows (the padded rows of the second batch
     element), whose uniform softmax passes its gradient to q, k and the
