@@ -617,6 +617,117 @@ __device__ __forceinline__ float rh_lse2(const AttnBwdBufs<bf16>& bf, int64_t id
   return row_valid ? (bf.mrow[idx] - logf(li)) * kLog2e : -log2f(li);
 }
 
+// Forward recompute: block (row, head), wave w owns query tiles w, w + 8, ...;
+// lane = query.  Online softmax over the key tiles with the exact running
+// maximum; writes O (normalised), m (natural units) and 1/l like
+// attn_bwd_fwd_kernel.  Padded queries attend uniformly, so that their O,
+// m and l stay finite.
+template <int NPM>
+__global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_fwd_rh_kernel(AttnBwdBufs<bf16> bf, int B,
+                                                                     int N, int np, float scale) {
+  constexpr int H = 4;
+  __shared__ __attribute__((aligned(1024))) char ks[NPM * 64];
+  __shared__ __attribute__((aligned(1024))) char vs[NPM * 64];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5, t32 = lane & 31;
+  const int nt = np / 32;
+  const int64_t rows = (int64_t)B * N;
+  const int64_t lin = xcd_remap(blockIdx.x, gridDim.x);
+  const int h = (int)(lin / rows);
+  const int64_t br = lin - (int64_t)h * rows;
+  const int b = (int)(br / N);
+  const int64_t rh = br * H + h;
+  rows2_to_lds(bf.kr + rh * np * AD, ks, bf.vr + rh * np * AD, vs, np);
+  const float* km_row = bf.kmask + br * np;
+  const bool row_valid = rh_row_valid(km_row, N);
+  uint32_t kxv = 0;
+  for (int k0 = 0; k0 < np; k0 += 64) {
+    const int k = k0 + lane;
+    const bool ex = k < np ? (row_valid ? !(km_row[k] > 0.5f) : k >= N) : true;
+    const unsigned long long eb = __ballot(ex);
+    const int w0 = k0 >> 5;
+    if (lane == w0) kxv = (uint32_t)eb;
+    if (lane == w0 + 1) kxv = (uint32_t)(eb >> 32);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  const RhOffsets off;
+  const float c2 = scale * kLog2e;
+  const int nk = (N + 31) / 32;
+  const float* bT = bf.biasT + ((int64_t)b * H + h) * np * np + lane * 4;
+  for (int qt = wave; qt < nt; qt += kRhWaves) {
+    const int q = qt * 32 + t32;
+    const bf16* qrow = bf.qr + (rh * np + q) * AD + 8 * half;
+    Frag<bf16> qf[2];
+#pragma unroll
+    for (int m = 0; m < 2; ++m) qf[m].load(qrow + 16 * m);
+    // scores taken as 0 (uniform attention): rows without a valid key, padded queries
+    const bool uni = !row_valid || q >= N;
+    const float* btile = bT + (int64_t)qt * nt * 1024;
+    float m2 = -INFINITY, l = 0.f;
+    f32x16 o = zero16();
+    for (int kt = 0; kt < nk; ++kt) {
+      const char* ktile = ks + kt * 2048;
+      f32x16 sc = zero16();
+      if (row_valid) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(btile + kt * 1024 + g * 256);
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) sc[4 * g + rr] = v[rr];
+        }
+#pragma unroll
+        for (int m = 0; m < 2; ++m) mma(sc, lds_frag(ktile + off.nrm[m]), qf[m]);  // S^T: rows key, cols q
+      }
+      float s2[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s2[e] = uni ? 0.f : sc[e] * c2;
+      const unsigned kx = __builtin_amdgcn_readlane(kxv, kt);
+      if (kx != 0u) {
+        const unsigned kl = kx >> (4 * half);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr)
+            if (__builtin_amdgcn_ubfe(kl, 8 * g + rr, 1)) s2[4 * g + rr] = -INFINITY;
+      }
+      float mt = s2[0];
+#pragma unroll
+      for (int e = 1; e < 16; ++e) mt = fmaxf(mt, s2[e]);
+      mt = fmaxf(mt, __shfl_xor(mt, 32));
+      const float mn = fmaxf(m2, mt);
+      const bool none = mn == -INFINITY;  // no key so far
+      const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m2 - mn);
+      float pv[16], ps = 0.f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        pv[e] = none ? 0.f : __builtin_amdgcn_exp2f(s2[e] - mn);
+        ps += pv[e];
+      }
+      l = l * alpha + ps;
+      m2 = mn;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) o[e] *= alpha;
+      Frag<bf16> fp[2];
+      vals_to_frags<bf16>(fp, pv);
+#pragma unroll
+      for (int gp = 0; gp < 2; ++gp) mma(o, lds_frag_tr(vs + kt * 2048, off, gp), fp[gp]);  // O^T += V^T P^T
+    }
+    l += __shfl_xor(l, 32);
+    const float li = 1.0f / l;
+    bf16* O = bf.o + (rh * np + q) * AD;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      store4(O + 8 * g + 4 * half, o[4 * g] * li, o[4 * g + 1] * li, o[4 * g + 2] * li, o[4 * g + 3] * li);
+    if (half == 0) {
+      bf.mrow[rh * np + q] = row_valid ? (q < N ? m2 * (1.0f / kLog2e) : 0.f) : kMaskScore;
+      bf.linv[rh * np + q] = li;
+    }
+  }
+}
+
 // dK and dV: block (row, head), wave w owns key tiles w, w + 8, ...; lane = key.
 template <int NPM>
 __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dkdv_rh_kernel(AttnBwdBufs<bf16> bf, int B,
@@ -1074,9 +1185,23 @@ static int bwd_triattn(const void* x, const float* mask, const void* dy,
         (const T*)x, mask, a.w, a.b, (int)B, (int)N, np, starting, eps, 1.0f / scale);
     GTK_LAUNCH_CHECK();
   }
+  // (row, head) kernels of the bf16 path: NPM = np rounded up to 256, 512 or 1024 (0: none)
+  int npm = 0;
+  if constexpr (std::is_same<T, bf16>::value) npm = np <= 256 ? 256 : np <= 512 ? 512 : np <= 1024 ? 1024 : 0;
+  const int64_t rblocks = B * N * H;
+  GTK_REQUIRE(rblocks < (1ll << 31), GTK_EUNSUPPORTED, "attention backward grid too large");
+  auto rh_launch = [&](auto kern256, auto kern512, auto kern1024) {
+    auto k = npm == 256 ? kern256 : npm == 512 ? kern512 : kern1024;
+    k<<<(unsigned)rblocks, 64 * kRhWaves, 0, st>>>(a.b, (int)B, (int)N, np, scale);
+  };
   {
     StageTimer timer("triattn_bwd_fwd", st);
-    attn_bwd_fwd_kernel<T, H><<<g4(headtiles), 256, 0, st>>>(a.b, (int)B, (int)N, np, scale);
+    if constexpr (std::is_same<T, bf16>::value) {
+      if (npm) rh_launch(attn_bwd_fwd_rh_kernel<256>, attn_bwd_fwd_rh_kernel<512>, attn_bwd_fwd_rh_kernel<1024>);
+      else attn_bwd_fwd_kernel<T, H><<<g4(headtiles), 256, 0, st>>>(a.b, (int)B, (int)N, np, scale);
+    } else {
+      attn_bwd_fwd_kernel<T, H><<<g4(headtiles), 256, 0, st>>>(a.b, (int)B, (int)N, np, scale);
+    }
     GTK_LAUNCH_CHECK();
   }
   {
@@ -1087,30 +1212,17 @@ static int bwd_triattn(const void* x, const float* mask, const void* dy,
   }
   bool rh_done = false;
   if constexpr (std::is_same<T, bf16>::value) {
-    if (np <= 1024) {
-      // (row, head) blocks: Q, dO (dK, dV) or K, V (dQ) of the row resident in LDS
-      const int64_t rblocks = B * N * H;
-      GTK_REQUIRE(rblocks < (1ll << 31), GTK_EUNSUPPORTED, "attention backward grid too large");
-      auto launch_rh = [&](auto npm) {
-        constexpr int NPM = decltype(npm)::value;
-        {
-          StageTimer timer("triattn_bwd_dkdv", st);
-          attn_bwd_dkdv_rh_kernel<NPM><<<(unsigned)rblocks, 64 * kRhWaves, 0, st>>>(a.b, (int)B, (int)N, np,
-                                                                                   scale);
-          GTK_LAUNCH_CHECK();
-        }
-        {
-          StageTimer timer("triattn_bwd_dq", st);
-          attn_bwd_dq_rh_kernel<NPM><<<(unsigned)rblocks, 64 * kRhWaves, 0, st>>>(a.b, (int)B, (int)N, np,
-                                                                                 scale);
-          GTK_LAUNCH_CHECK();
-        }
-        return GTK_OK;
-      };
-      if (np <= 256) rc = launch_rh(std::integral_constant<int, 256>());
-      else if (np <= 512) rc = launch_rh(std::integral_constant<int, 512>());
-      else rc = launch_rh(std::integral_constant<int, 1024>());
-      if (rc) return rc;
+    if (npm) {
+      {
+        StageTimer timer("triattn_bwd_dkdv", st);
+        rh_launch(attn_bwd_dkdv_rh_kernel<256>, attn_bwd_dkdv_rh_kernel<512>, attn_bwd_dkdv_rh_kernel<1024>);
+        GTK_LAUNCH_CHECK();
+      }
+      {
+        StageTimer timer("triattn_bwd_dq", st);
+        rh_launch(attn_bwd_dq_rh_kernel<256>, attn_bwd_dq_rh_kernel<512>, attn_bwd_dq_rh_kernel<1024>);
+        GTK_LAUNCH_CHECK();
+      }
       rh_done = true;
     }
   }
