@@ -60,6 +60,7 @@ template <typename T> struct AttnBwdBufs {
   float* kmask;                    // [B][N][np]: 1 valid key, 0 masked
   float *mrow, *linv, *dd;         // [B][N][H][np]
   float* db;                       // dL/dbias [B][H][N][N]
+  float* dbp;                      // dL/dbias partial sums per row chunk (bf16 path, np <= 512)
   T *cm_stack, *cm_xh, *cm_dxn, *cm_dy, *cm_go, *cm_dtri;
   int64_t pitch;
 };
@@ -941,6 +942,202 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dq_rh_kernel(AttnBwdBu
   }
 }
 
+// dB of the bf16 path (np <= 512): block (batch b, head h, query tile qt,
+// chunk of rows).  The block's waves walk the chunk's rows together, each
+// owning key tiles w and w + 8 (lane = query, S^T orientation as in dQ).  For
+// every row, K and V of the row and its query tile of Q and dO come into LDS
+// (double buffered: the copies of row r + 1 go out before row r is computed),
+// and each wave adds dS of its tiles into fp32 accumulators.  The chunk's sums
+// go to a partial buffer in fragment order (the biasT layout), summed over
+// the chunks by attn_bwd_dbias_reduce_kernel.  Blocks of one (b, chunk, head)
+// are consecutive, so the blocks that read the same K and V rows share an
+// XCD's L2.
+constexpr int kDbChunks = 8;  // row chunks per batch element (at most)
+
+template <int NPM>
+__global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dbias_rh_kernel(AttnBwdBufs<bf16> bf,
+                                                                       float* __restrict__ part, int B,
+                                                                       int N, int np, int nch, int rpc,
+                                                                       float scale) {
+  constexpr int H = 4;
+  static_assert(NPM <= 512, "two key tiles per wave");
+  constexpr int BUF = 2 * NPM * 64 + 4096;  // K rows, V rows, Q tile, dO tile
+  __shared__ __attribute__((aligned(1024))) char lds[2 * BUF];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5, t32 = lane & 31;
+  const int nt = np / 32;
+  const int nq = (N + 31) / 32;
+  const int64_t lin = xcd_remap(blockIdx.x, gridDim.x);
+  const int qt = (int)(lin % nq);
+  int64_t rest = lin / nq;
+  const int h = (int)(rest % H);
+  rest /= H;
+  const int c = (int)(rest % nch);
+  const int b = (int)(rest / nch);
+  const int r0 = c * rpc;
+  const int r1 = min(N, r0 + rpc);
+  const int q = qt * 32 + t32;
+  const bool qpad = q >= N;
+  const int kv_bytes = np * 64;
+  const int ncopy = np / 8 + 4;  // 1 KiB copies per row: K, V, Q tile, dO tile
+
+  // copies of row r into buffer u
+  const uint32_t rin = (uint32_t)lane >> 2;
+  const uint32_t voff = rin * 64 + ((((uint32_t)lane & 3) ^ ((rin >> 2) & 3)) << 4);
+  auto issue_row = [&](int r, int u) {
+    const int64_t rh = ((int64_t)b * N + r) * H + h;
+    const char* kb = reinterpret_cast<const char*>(bf.kr + rh * np * AD);
+    const char* vb = reinterpret_cast<const char*>(bf.vr + rh * np * AD);
+    const char* qb = reinterpret_cast<const char*>(bf.qr + (rh * np + qt * 32) * AD);
+    const char* db = reinterpret_cast<const char*>(bf.dor + (rh * np + qt * 32) * AD);
+    const uint32_t base = lds_addr(lds) + u * BUF;
+    for (int i = wave; i < ncopy; i += kRhWaves) {
+      const char* src;
+      if (i < np / 16) src = kb + i * 1024;
+      else if (i < np / 8) src = vb + (i - np / 16) * 1024;
+      else if (i < np / 8 + 2) src = qb + (i - np / 8) * 1024;
+      else src = db + (i - np / 8 - 2) * 1024;
+      // wave-uniform, but selected per copy: back into scalar registers
+      // (readfirstlane returns int: widen each half as unsigned)
+      const uint64_t sa = (uint64_t)(uintptr_t)src;
+      const uint64_t su = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(sa >> 32)) << 32) |
+                          (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)sa);
+      g2lds16_sv(reinterpret_cast<const char*>(su), voff, __builtin_amdgcn_readfirstlane(base + i * 1024));
+    }
+  };
+  // per-row scalars of this lane's query and its key tiles, loaded one row ahead
+  struct RowIn {
+    float m, li, d, km[2];
+  };
+  auto load_row = [&](int r) {
+    RowIn x;
+    const int64_t br = (int64_t)b * N + r;
+    const int64_t qi = (br * H + h) * np + q;
+    x.m = bf.mrow[qi];
+    x.li = bf.linv[qi];
+    x.d = bf.dd[qi];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int kt = wave + kRhWaves * i;
+      x.km[i] = kt < nt ? bf.kmask[br * np + kt * 32 + t32] : 0.f;
+    }
+    return x;
+  };
+
+  const RhOffsets off;
+  const float c2 = scale * kLog2e;
+  // bias tiles (h, qt, kt) of this wave's key tiles
+  f32x16 bias[2], acc[2];
+  const float* bT = bf.biasT + ((int64_t)b * H + h) * np * np + lane * 4;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int kt = min(wave + kRhWaves * i, nt - 1);
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 v = *reinterpret_cast<const f32x4*>(bT + ((int64_t)qt * nt + kt) * 1024 + g * 256);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) bias[i][4 * g + rr] = v[rr];
+    }
+    acc[i] = zero16();
+  }
+  RowIn cur = load_row(r0);
+  issue_row(r0, 0);
+  for (int r = r0; r < r1; ++r) {
+    const int u = (r - r0) & 1;
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of row r and its scalars landed
+    __syncthreads();                // every wave's copies landed; row r - 1's buffer is free
+    const RowIn x = cur;
+    if (r + 1 < r1) {
+      cur = load_row(r + 1);
+      issue_row(r + 1, u ^ 1);
+    }
+    const char* buf = lds + u * BUF;
+    const char* qtile = buf + 2 * kv_bytes;
+    const char* dtile = qtile + 2048;
+    // a row without a valid key stores m = -1e9 for every query
+    const bool row_valid = __ballot(x.m != kMaskScore) != 0ull;
+    const float lse2 = row_valid ? (x.m - logf(x.li)) * kLog2e : -log2f(x.li);
+    const Frag<bf16> qf0 = lds_frag(qtile + off.nrm[0]), qf1 = lds_frag(qtile + off.nrm[1]);
+    const Frag<bf16> df0 = lds_frag(dtile + off.nrm[0]), df1 = lds_frag(dtile + off.nrm[1]);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int kt = wave + kRhWaves * i;
+      if (kt >= nt) break;
+      const int key = kt * 32 + t32;
+      const bool ex = row_valid ? !(x.km[i] > 0.5f) : key >= N;
+      const unsigned kx = (unsigned)__ballot(ex);  // lanes 0-31: the tile's 32 keys
+      const char* ktile = buf + kt * 2048;
+      const char* vtile = buf + kv_bytes + kt * 2048;
+      f32x16 sc = zero16();
+      if (row_valid) {
+        sc = bias[i];
+        mma(sc, lds_frag(ktile + off.nrm[0]), qf0);  // S^T: rows key, cols q
+        mma(sc, lds_frag(ktile + off.nrm[1]), qf1);
+      }
+      f32x16 dp = mma0(lds_frag(vtile + off.nrm[0]), df0);  // dP^T
+      mma(dp, lds_frag(vtile + off.nrm[1]), df1);
+      float pv[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e)
+        pv[e] = __builtin_amdgcn_exp2f(row_valid ? fmaf(sc[e], c2, -lse2) : -lse2);
+      if (kx != 0u) {
+        const unsigned kl = kx >> (4 * half);
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr)
+            if (__builtin_amdgcn_ubfe(kl, 8 * g + rr, 1)) pv[4 * g + rr] = 0.f;
+      }
+      if (qpad) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) pv[e] = 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][e] += pv[e] * (dp[e] - x.d);
+    }
+  }
+  float* dst = part + ((int64_t)(b * nch + c) * H + h) * np * np + lane * 4;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int kt = wave + kRhWaves * i;
+    if (kt >= nt) break;
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      *reinterpret_cast<f32x4*>(dst + ((int64_t)qt * nt + kt) * 1024 + g * 256) =
+          f32x4{acc[i][4 * g], acc[i][4 * g + 1], acc[i][4 * g + 2], acc[i][4 * g + 3]};
+  }
+}
+
+// db[b][h][q][k] = sum over the row chunks of the fragment-order partials;
+// one thread per 4 consecutive keys.
+__global__ __launch_bounds__(256) void attn_bwd_dbias_reduce_kernel(const float* __restrict__ part,
+                                                                    float* __restrict__ db, int B, int N,
+                                                                    int np, int nch) {
+  constexpr int H = 4;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int k4n = np / 4;
+  if (t >= (int64_t)B * H * N * k4n) return;
+  const int k = (int)(t % k4n) * 4;
+  int64_t rest = t / k4n;
+  const int q = (int)(rest % N);
+  rest /= N;
+  const int h = (int)(rest % H);
+  const int b = (int)(rest / H);
+  if (k >= N) return;
+  const int64_t e = bias_frag_elem(h, q, k, np);
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  for (int c = 0; c < nch; ++c) {
+    const f32x4 v = *reinterpret_cast<const f32x4*>(part + (int64_t)(b * nch + c) * H * np * np + e);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s[j] += v[j];
+  }
+  float* dst = db + (((int64_t)b * H + h) * N + q) * N + k;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    if (k + j < N) dst[j] = s[j];
+}
+
 // ---------------------------------------------------------------------------
 // pro: dxn and the LayerNorm backward; per 32-position tile of one row
 // ---------------------------------------------------------------------------
@@ -1119,6 +1316,7 @@ static AttnBwdWs<T> carve_attn_bwd(Carve& cv, int64_t B, int64_t N, int C, int H
   b.linv = cv.take<float>(B * N * H * np);
   b.dd = cv.take<float>(B * N * H * np);
   b.db = cv.take<float>(B * H * N * N);
+  b.dbp = (sizeof(T) == 2 && np <= 512) ? cv.take<float>(B * kDbChunks * H * np * np) : nullptr;
   b.pitch = round_up(B * N * N, 64);
   b.cm_stack = cv.take<T>(4 * CH * b.pitch);
   b.cm_xh = cv.take<T>(C * b.pitch);
@@ -1240,7 +1438,28 @@ static int bwd_triattn(const void* x, const float* mask, const void* dy,
   }
   {
     StageTimer timer("triattn_bwd_dbias", st);
-    attn_bwd_dbias_kernel<T, H><<<g4(pairtiles), 256, 0, st>>>(a.b, (int)B, (int)N, np, scale);
+    if (a.b.dbp) {
+      if constexpr (std::is_same<T, bf16>::value) {
+        // row chunks of rpc rows (at most kDbChunks per batch element), partial
+        // sums in fragment order, then the sum over the chunks
+        const int rpc = (int)((N + kDbChunks - 1) / kDbChunks);
+        const int nch = (int)((N + rpc - 1) / rpc);
+        const int64_t dblocks = B * nch * H * ((N + 31) / 32);
+        GTK_REQUIRE(dblocks < (1ll << 31), GTK_EUNSUPPORTED, "attention backward grid too large");
+        if (np <= 256)
+          attn_bwd_dbias_rh_kernel<256><<<(unsigned)dblocks, 64 * kRhWaves, 0, st>>>(a.b, a.b.dbp, (int)B, (int)N,
+                                                                                    np, nch, rpc, scale);
+        else
+          attn_bwd_dbias_rh_kernel<512><<<(unsigned)dblocks, 64 * kRhWaves, 0, st>>>(a.b, a.b.dbp, (int)B, (int)N,
+                                                                                    np, nch, rpc, scale);
+        GTK_LAUNCH_CHECK();
+        const int64_t rt = B * H * N * (np / 4);
+        attn_bwd_dbias_reduce_kernel<<<(unsigned)((rt + 255) / 256), 256, 0, st>>>(a.b.dbp, a.b.db, (int)B, (int)N,
+                                                                                   np, nch);
+      }
+    } else {
+      attn_bwd_dbias_kernel<T, H><<<g4(pairtiles), 256, 0, st>>>(a.b, (int)B, (int)N, np, scale);
+    }
     GTK_LAUNCH_CHECK();
   }
   // rows H..63 of the dtri operand stay zero
