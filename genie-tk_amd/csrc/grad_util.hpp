@@ -70,6 +70,97 @@ __device__ __forceinline__ void vals_to_frags(Frag<T>* f, const float* v) {
   f[1].set(v + 8);
 }
 
+// Column-major ([channel][pitch] pairs) stores of 32-pair x 32-channel tiles
+// held in accumulator order: lane l holds pair p0 + (l & 31) and v[4g + r] is
+// channel c0 + 8g + 4(l >> 5) + r.  Stored directly, every value is a 2-byte
+// store.  The fast path transposes the tile through two MFMAs against
+// identity fragments (exact: one product by 1.0 per output) so that lane l
+// holds channel c0 + (l & 31) for pairs 8g + 4(l >> 5) .. +3, and writes
+// them as 8-byte stores.  Fast requires all 32 pairs of the tile to be real
+// and p0 % 4 == 0 (8-byte alignment).
+struct CmTile {
+  Frag<bf16> id[2];  // k (channels, vals_to_frags order) -> column = channel
+  __device__ __forceinline__ CmTile() {
+    const int lane = threadIdx.x & 63;
+    const int col = lane & 31, half = lane >> 5;
+#pragma unroll
+    for (int gp = 0; gp < 2; ++gp) {
+      float f[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = (col == 16 * gp + 8 * (e >> 2) + 4 * half + (e & 3)) ? 1.f : 0.f;
+      id[gp].set(f);
+    }
+  }
+  __device__ __forceinline__ void store(bf16* cm, int64_t pitch, int64_t p0, int c0, const float* v, bool fast,
+                                        bool lane_valid) const {
+    const int lane = threadIdx.x & 63;
+    const int half = lane >> 5, t32 = lane & 31;
+    if (fast) {
+      Frag<bf16> f[2];
+      vals_to_frags<bf16>(f, v);
+      f32x16 d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[0].v, id[0].v, zero16(), 0, 0, 0);
+      d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[1].v, id[1].v, d, 0, 0, 0);
+      bf16* col = cm + (int64_t)(c0 + t32) * pitch + p0 + 4 * half;
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const uint2 w = make_uint2(pack_bf16x2(d[4 * g], d[4 * g + 1]), pack_bf16x2(d[4 * g + 2], d[4 * g + 3]));
+        *reinterpret_cast<uint2*>(col + 8 * g) = w;
+      }
+    } else if (lane_valid) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          cm[(int64_t)(c0 + 8 * g + 4 * half + r) * pitch + p0 + t32] = (bf16)v[4 * g + r];
+    }
+  }
+};
+
+// The same for a 32-pair tile of C = 128 channels in row-half order (lane l
+// holds pair p0 + (l & 31) and v[i] is channel 64(l >> 5) + i, i < 64).  Output
+// tile s0 = 0, 2, 4, 6 takes k-steps s0 and s0 + 1 (channels 8s .. 8s+7 from the
+// lower half-wave, 64 + 8s .. from the upper), so its column c is channel
+// 8 s0 + c (c < 16) or 64 + 8 s0 + c - 16.
+struct CmTileRH {
+  Frag<bf16> id[2];  // k-step s0 + u: k-slot 8h + e -> column 8u + 16h + e
+  __device__ __forceinline__ CmTileRH() {
+    const int lane = threadIdx.x & 63;
+    const int col = lane & 31, half = lane >> 5;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      float f[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = (col == 8 * u + 16 * half + e) ? 1.f : 0.f;
+      id[u].set(f);
+    }
+  }
+  __device__ __forceinline__ void store(bf16* cm, int64_t pitch, int64_t p0, const float* v, bool fast,
+                                        bool lane_valid) const {
+    const int lane = threadIdx.x & 63;
+    const int half = lane >> 5, t32 = lane & 31;
+    if (fast) {
+#pragma unroll
+      for (int s0 = 0; s0 < 8; s0 += 2) {
+        Frag<bf16> f0, f1;
+        f0.set(v + 8 * s0);
+        f1.set(v + 8 * s0 + 8);
+        f32x16 d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f0.v, id[0].v, zero16(), 0, 0, 0);
+        d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1.v, id[1].v, d, 0, 0, 0);
+        const int ch = t32 < 16 ? 8 * s0 + t32 : 64 + 8 * s0 + t32 - 16;
+        bf16* col = cm + (int64_t)ch * pitch + p0 + 4 * half;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint2 w = make_uint2(pack_bf16x2(d[4 * g], d[4 * g + 1]), pack_bf16x2(d[4 * g + 2], d[4 * g + 3]));
+          *reinterpret_cast<uint2*>(col + 8 * g) = w;
+        }
+      }
+    } else if (lane_valid) {
+#pragma unroll
+      for (int i = 0; i < 64; ++i) cm[(int64_t)(half * 64 + i) * pitch + p0 + t32] = (bf16)v[i];
+    }
+  }
+};
+
 // out = in^T per [Np][Np] plane, 64x64 tiles through LDS.  Np % 64 == 0.
 template <typename T>
 __global__ __launch_bounds__(256) void transpose_planes_kernel(const T* __restrict__ in,

@@ -126,7 +126,7 @@ __global__ __launch_bounds__(256) void attn_bwd_proj_kernel(const T* __restrict_
                                                             const float* __restrict__ mask,
                                                             AttnBwdW<T> w, AttnBwdBufs<T> bf,
                                                             int B, int N, int np, int starting,
-                                                            float eps, float inv_scale) {
+                                                            float eps, float inv_scale, int dmajor) {
   constexpr int CH = H * AD;
   const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
   const int jtiles = np / 32;
@@ -164,8 +164,10 @@ __global__ __launch_bounds__(256) void attn_bwd_proj_kernel(const T* __restrict_
 #pragma unroll
         for (int q = 0; q < 4; ++q) v[q] = valid ? acc[4 * g + q] + bk[kind][h * AD + d0 + q] : 0.f;
         store4(rowm + d0, v[0], v[1], v[2], v[3]);
+        if (dmajor) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) dmaj[(int64_t)(d0 + q) * np] = cvt<T>(v[q]);
+          for (int q = 0; q < 4; ++q) dmaj[(int64_t)(d0 + q) * np] = cvt<T>(v[q]);
+        }
       }
     }
   }
@@ -279,7 +281,7 @@ __global__ __launch_bounds__(256) void attn_bwd_fwd_kernel(AttnBwdBufs<T> bf, in
 template <typename T, int C, int H>
 __global__ __launch_bounds__(256) void attn_bwd_epi_kernel(const T* __restrict__ dy, AttnBwdW<T> w,
                                                            AttnBwdBufs<T> bf, int B, int N, int np,
-                                                           int starting) {
+                                                           int starting, int dmajor) {
   constexpr int CH = H * AD;
   const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
   const int jtiles = np / 32;
@@ -293,17 +295,24 @@ __global__ __launch_bounds__(256) void attn_bwd_epi_kernel(const T* __restrict__
   const int64_t xp = valid ? ((int64_t)b * N + (starting ? r : j)) * N + (starting ? j : r) : 0;
   const int64_t p = ((int64_t)b * N + r) * N + j;  // pair index, attention orientation
   const int64_t pitch = bf.pitch;
+  const int64_t p0 = ((int64_t)b * N + r) * N + jt * 32;
+  const bool fast = std::is_same<T, bf16>::value && jt * 32 + 32 <= N && N % 4 == 0;
 
   RowHalf<C> dh;
   load_row_half<T, C>(dh, dy + xp * C, valid);
   Frag<T> fdy[C / 16];
 #pragma unroll
   for (int ch = 0; ch < C / 16; ++ch) fdy[ch].set(&dh.v[ch * 8]);
-  if (valid) {
+  if constexpr (std::is_same<T, bf16>::value) {
+    static_assert(C == 128, "row-half tile store");
+    const CmTileRH cmr;
+    cmr.store(bf.cm_dy, pitch, p0, dh.v, fast, valid);
+  } else if (valid) {
 #pragma unroll
     for (int i = 0; i < C / 2; ++i) bf.cm_dy[(int64_t)(half * (C / 2) + i) * pitch + p] = cvt<T>(dh.v[i]);
   }
   T* cm_dg = bf.cm_stack + (int64_t)3 * CH * pitch;
+  const CmTile cmt;
 #pragma unroll 1
   for (int h = 0; h < H; ++h) {
     const f32x16 dog = row_gemm_tile<T, C, true>(fdy, w.wt_o, h);
@@ -313,6 +322,7 @@ __global__ __launch_bounds__(256) void attn_bwd_epi_kernel(const T* __restrict__
     T* dor = bf.dor + (rh * np + j) * AD;
     T* dot = bf.dot + rh * AD * np + j;
     float dsum = 0.f;
+    float vdg[16], vgo[16];
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int d0 = 8 * g + 4 * half;
@@ -324,14 +334,22 @@ __global__ __launch_bounds__(256) void attn_bwd_epi_kernel(const T* __restrict__
         const float dg = dog[4 * g + e];
         dov[e] = valid ? dg * g4[e] : 0.f;
         dsum += dov[e] * o4[e];
-        if (valid) {
-          const int64_t o = (int64_t)(h * AD + d0 + e) * pitch + p;
-          cm_dg[o] = cvt<T>(dg * o4[e] * g4[e] * (1.f - g4[e]));
-          bf.cm_go[o] = cvt<T>(o4[e] * g4[e]);
+        vdg[4 * g + e] = dg * o4[e] * g4[e] * (1.f - g4[e]);
+        vgo[4 * g + e] = o4[e] * g4[e];
+        if constexpr (!std::is_same<T, bf16>::value) {
+          if (valid) {
+            const int64_t o = (int64_t)(h * AD + d0 + e) * pitch + p;
+            cm_dg[o] = cvt<T>(vdg[4 * g + e]);
+            bf.cm_go[o] = cvt<T>(vgo[4 * g + e]);
+          }
         }
-        dot[(int64_t)(d0 + e) * np] = cvt<T>(dov[e]);
+        if (dmajor) dot[(int64_t)(d0 + e) * np] = cvt<T>(dov[e]);
       }
       store4(dor + d0, dov[0], dov[1], dov[2], dov[3]);
+    }
+    if constexpr (std::is_same<T, bf16>::value) {
+      cmt.store(cm_dg, pitch, p0, h * AD, vdg, fast, valid);
+      cmt.store(bf.cm_go, pitch, p0, h * AD, vgo, fast, valid);
     }
     dsum += xor32(dsum);
     if (half == 0) bf.dd[rh * np + j] = dsum;
@@ -1158,6 +1176,10 @@ __global__ __launch_bounds__(256) void attn_bwd_pro_kernel(const T* __restrict__
   const int64_t xp = valid ? ((int64_t)b * N + (starting ? r : j)) * N + (starting ? j : r) : 0;
   const int64_t p = ((int64_t)b * N + r) * N + j;
   const int64_t pitch = bf.pitch;
+  // column-major operand tiles: whole-tile transposed stores where possible
+  const int64_t p0 = ((int64_t)b * N + r) * N + jt * 32;
+  const bool fast = std::is_same<T, bf16>::value && jt * 32 + 32 <= N && N % 4 == 0;
+  const CmTile cmt;
 
   RowHalf<C> rhx;
   load_row_half<T, C>(rhx, x + xp * C, valid);
@@ -1181,7 +1203,9 @@ __global__ __launch_bounds__(256) void attn_bwd_pro_kernel(const T* __restrict__
 #pragma unroll
           for (int e = 0; e < 4; ++e) d[4 * g + e] = v4[e];
         }
-        if (valid) {
+        if constexpr (std::is_same<T, bf16>::value) {
+          cmt.store(bf.cm_stack, pitch, p0, kind * CH + h * AD, d, fast, valid);
+        } else if (valid) {
 #pragma unroll
           for (int g = 0; g < 4; ++g)
 #pragma unroll
@@ -1239,6 +1263,16 @@ __global__ __launch_bounds__(256) void attn_bwd_pro_kernel(const T* __restrict__
   s1 += xor32(s1);
   s2 += xor32(s2);
   const float m1 = s1 * (1.0f / C), m2 = s2 * (1.0f / C);
+  if constexpr (std::is_same<T, bf16>::value) {
+#pragma unroll
+    for (int nt = 0; nt < C / 32; ++nt) {
+      float vt[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) vt[e] = dzn[nt][e];
+      cmt.store(bf.cm_xh, pitch, p0, nt * 32, &xh[16 * nt], fast, valid);
+      cmt.store(bf.cm_dxn, pitch, p0, nt * 32, vt, fast, valid);
+    }
+  }
   if (!valid) return;
 #pragma unroll
   for (int nt = 0; nt < C / 32; ++nt)
@@ -1251,8 +1285,10 @@ __global__ __launch_bounds__(256) void attn_bwd_pro_kernel(const T* __restrict__
         const float xv = xh[16 * nt + 4 * g + e];
         const float t = dzn[nt][4 * g + e];
         o[e] = st[1] * (w.ln_w[c0 + e] * t - m1 - xv * m2);
-        bf.cm_xh[(int64_t)(c0 + e) * pitch + p] = cvt<T>(xv);
-        bf.cm_dxn[(int64_t)(c0 + e) * pitch + p] = cvt<T>(t);
+        if constexpr (!std::is_same<T, bf16>::value) {
+          bf.cm_xh[(int64_t)(c0 + e) * pitch + p] = cvt<T>(xv);
+          bf.cm_dxn[(int64_t)(c0 + e) * pitch + p] = cvt<T>(t);
+        }
       }
       store4(dx + xp * C + c0, o[0], o[1], o[2], o[3]);
     }
@@ -1377,15 +1413,17 @@ static int bwd_triattn(const void* x, const float* mask, const void* dy,
   GTK_REQUIRE(headtiles / 4 < (1ll << 31) && pairtiles / 4 < (1ll << 31), GTK_EUNSUPPORTED,
               "attention backward grid too large");
   auto g4 = [](int64_t t) { return (unsigned)((t + 3) / 4); };
-  {
-    StageTimer timer("triattn_bwd_proj", st);
-    attn_bwd_proj_kernel<T, C, H><<<g4(rowtiles), 256, 0, st>>>(
-        (const T*)x, mask, a.w, a.b, (int)B, (int)N, np, starting, eps, 1.0f / scale);
-    GTK_LAUNCH_CHECK();
-  }
   // (row, head) kernels of the bf16 path: NPM = np rounded up to 256, 512 or 1024 (0: none)
   int npm = 0;
   if constexpr (std::is_same<T, bf16>::value) npm = np <= 256 ? 256 : np <= 512 ? 512 : np <= 1024 ? 1024 : 0;
+  // the d-major copies of q, k, v and dO are read only by the per-tile kernels
+  const int dmajor = npm == 0;
+  {
+    StageTimer timer("triattn_bwd_proj", st);
+    attn_bwd_proj_kernel<T, C, H><<<g4(rowtiles), 256, 0, st>>>(
+        (const T*)x, mask, a.w, a.b, (int)B, (int)N, np, starting, eps, 1.0f / scale, dmajor);
+    GTK_LAUNCH_CHECK();
+  }
   const int64_t rblocks = B * N * H;
   GTK_REQUIRE(rblocks < (1ll << 31), GTK_EUNSUPPORTED, "attention backward grid too large");
   auto rh_launch = [&](auto kern256, auto kern512, auto kern1024) {
@@ -1405,7 +1443,7 @@ static int bwd_triattn(const void* x, const float* mask, const void* dy,
   {
     StageTimer timer("triattn_bwd_epi", st);
     attn_bwd_epi_kernel<T, C, H><<<g4(rowtiles), 256, 0, st>>>((const T*)dy, a.w, a.b, (int)B,
-                                                                (int)N, np, starting);
+                                                                (int)N, np, starting, dmajor);
     GTK_LAUNCH_CHECK();
   }
   bool rh_done = false;
