@@ -349,15 +349,25 @@ inline int launch_wgrad(const T* G, const T* X, float* part, int M, int Nn, int6
 
 // dst[(m - m0)][n] = sum_s part[s][m][n] * (gamma ? gamma[n] : 1)
 //                    + (rowsum && beta ? rowsum[m] * beta[n] : 0),  m in [m0, m0 + rows)
-static __global__ void wgrad_finish_kernel(const float* __restrict__ part, int nsplit, int M, int Nn,
-                                    int m0, int rows, const float* __restrict__ rowsum,
-                                    const float* __restrict__ gamma, const float* __restrict__ beta,
-                                    float* __restrict__ dst) {
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= rows * Nn) return;
-  const int m = m0 + idx / Nn, n = idx % Nn;
+// Block: 32 consecutive outputs x 8 chunks of the splits (chunk c takes s = c,
+// c + 8, ...), the 8 partial sums of each output added through LDS.
+static __global__ __launch_bounds__(256) void wgrad_finish_kernel(
+    const float* __restrict__ part, int nsplit, int M, int Nn, int m0, int rows,
+    const float* __restrict__ rowsum, const float* __restrict__ gamma, const float* __restrict__ beta,
+    float* __restrict__ dst) {
+  __shared__ float red[8][32];
+  const int o = threadIdx.x & 31, ch = threadIdx.x >> 5;
+  const int idx = blockIdx.x * 32 + o;
+  const bool live = idx < rows * Nn;
+  const int m = m0 + (live ? idx / Nn : 0), n = live ? idx % Nn : 0;
   float acc = 0.f;
-  for (int s = 0; s < nsplit; ++s) acc += part[((int64_t)s * M + m) * Nn + n];
+  if (live)
+    for (int sp = ch; sp < nsplit; sp += 8) acc += part[((int64_t)sp * M + m) * Nn + n];
+  red[ch][o] = acc;
+  __syncthreads();
+  if (ch != 0 || !live) return;
+#pragma unroll
+  for (int c = 1; c < 8; ++c) acc += red[c][o];
   if (gamma) acc *= gamma[n];
   if (rowsum && beta) acc += rowsum[m] * beta[n];
   dst[idx] = acc;
@@ -368,8 +378,8 @@ inline int launch_wgrad_finish(const float* part, int M, int Nn, int64_t pitch, 
                                float* dst, hipStream_t st) {
   if (!dst) return GTK_OK;
   const int n = rows * Nn;
-  wgrad_finish_kernel<<<(n + 255) / 256, 256, 0, st>>>(part, wgrad_plan(M, pitch).nsplit, M, Nn, m0,
-                                                       rows, rowsum, gamma, beta, dst);
+  wgrad_finish_kernel<<<(n + 31) / 32, 256, 0, st>>>(part, wgrad_plan(M, pitch).nsplit, M, Nn, m0,
+                                                     rows, rowsum, gamma, beta, dst);
   GTK_LAUNCH_CHECK();
   return GTK_OK;
 }

@@ -1295,14 +1295,24 @@ __global__ __launch_bounds__(256) void attn_bwd_pro_kernel(const T* __restrict__
 }
 
 // dW_b[h][c] = W3[c][h] gamma[c] + s[h] beta[c]  (W3 = sum_s part[s][c][h], 64 columns)
-__global__ void attn_dwb_finish_kernel(const float* __restrict__ part, int nsplit, int C, int H,
-                                       const float* __restrict__ gamma, const float* __restrict__ beta,
-                                       const float* __restrict__ sums, float* __restrict__ dst) {
-  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= H * C) return;
-  const int h = idx / C, c = idx % C;
+__global__ __launch_bounds__(256) void attn_dwb_finish_kernel(const float* __restrict__ part, int nsplit, int C,
+                                                            int H, const float* __restrict__ gamma,
+                                                            const float* __restrict__ beta,
+                                                            const float* __restrict__ sums, float* __restrict__ dst) {
+  // 32 outputs x 8 chunks of the splits per block, partial sums added through LDS
+  __shared__ float red[8][32];
+  const int o = threadIdx.x & 31, ch = threadIdx.x >> 5;
+  const int idx = blockIdx.x * 32 + o;
+  const bool live = idx < H * C;
+  const int h = live ? idx / C : 0, c = live ? idx % C : 0;
   float a = 0.f;
-  for (int s = 0; s < nsplit; ++s) a += part[((int64_t)s * C + c) * 64 + h];
+  if (live)
+    for (int s = ch; s < nsplit; s += 8) a += part[((int64_t)s * C + c) * 64 + h];
+  red[ch][o] = a;
+  __syncthreads();
+  if (ch != 0 || !live) return;
+#pragma unroll
+  for (int k = 1; k < 8; ++k) a += red[k][o];
   dst[idx] = a * gamma[c] + sums[h] * beta[c];
 }
 
@@ -1534,7 +1544,7 @@ static int bwd_triattn(const void* x, const float* mask, const void* dy,
   if ((rc = launch_wgrad_finish(a.part2, C, CH, pitch, 0, C, nullptr, nullptr, nullptr, gr->o_w, st)))
     return rc;
   if ((rc = launch_copy_f32(gr->o_b, a.sums_dy, C, st))) return rc;
-  attn_dwb_finish_kernel<<<(H * C + 255) / 256, 256, 0, st>>>(
+  attn_dwb_finish_kernel<<<(H * C + 31) / 32, 256, 0, st>>>(
       a.part3, wgrad_plan(C, pitch).nsplit, C, H, a.w.ln_w, a.w.ln_b, a.sums_dtri, gr->tri_w);
   GTK_LAUNCH_CHECK();
   if ((rc = launch_copy_f32(gr->ln_w, a.dots_dxn, C, st))) return rc;
