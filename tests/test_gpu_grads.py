@@ -83,19 +83,19 @@ def test_tri_mul_backward_runs_the_kernels(monkeypatch):
     assert all(p.grad is not None and torch.isfinite(p.grad).all() for p in mod.parameters())
 
 
-@pytest.mark.parametrize("dname", ["fp32", "bf16"])
-@pytest.mark.parametrize("starting", [True, False])
-@pytest.mark.parametrize("N", [40, 77, 130])
-def test_tri_attn_backward(dname, starting, N):
-    """Includes fully masked rows (the padded rows of the second batch
-    element), whose uniform softmax passes its gradient to q, k and the
-    triangle bias as torch autograd of the reference does."""
-    log(f"tri_attn backward {dname} starting={starting} N={N}")
+def _tri_attn_backward_case(dname, starting, N, lengths, inner_mask=0.0):
+    log(f"tri_attn backward {dname} starting={starting} N={N} lengths={lengths}")
     dt = DT[dname]
+    B = len(lengths)
     P = H.draw_params(H.tri_attn_shapes(128, 128, 4), seed=N + 7, ln_random=True, bias_random=True)
-    x = H.pair_input(2, N, 128, seed=N + 8)
-    m = H.tail_mask(2, N, [N, N - 6])
-    dy = H.pair_input(2, N, 128, seed=N + 9)
+    x = H.pair_input(B, N, 128, seed=N + 8)
+    m = H.tail_mask(B, N, lengths)
+    if inner_mask > 0:
+        # scattered masked pairs inside the valid block (no row loses every key)
+        rng = np.random.default_rng(N)
+        m = m * (rng.random(m.shape) >= inner_mask).astype(np.float32)
+        m[:, np.arange(N), np.arange(N)] = H.tail_mask(B, N, lengths)[:, np.arange(N), np.arange(N)]
+    dy = H.pair_input(B, N, 128, seed=N + 9)
     if dname == "bf16":
         P, x, dy = H.bf16_params(P), H.bf16_round(x), H.bf16_round(dy)
     mod = triattn_module(P, starting, 4, dt)
@@ -109,6 +109,25 @@ def test_tri_attn_backward(dname, starting, N):
         assert prm.grad is not None and prm.grad.dtype == dt, name
         worst.append((_check_grad(_np(prm.grad), g_ref[name], dname, name), name))
     log(f"  worst max|g - r| / max|r|: {max(worst)[0]:.2e} ({max(worst)[1]})")
+
+
+@pytest.mark.parametrize("dname", ["fp32", "bf16"])
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("N", [40, 77, 130])
+def test_tri_attn_backward(dname, starting, N):
+    """Includes fully masked rows (the padded rows of the second batch
+    element), whose uniform softmax passes its gradient to q, k and the
+    triangle bias as torch autograd of the reference does."""
+    _tri_attn_backward_case(dname, starting, N, [N, N - 6])
+
+
+@pytest.mark.parametrize("starting", [True, False])
+def test_tri_attn_backward_n264(starting):
+    """bf16 at N = 264 (288 padded positions, 9 key tiles): the (row, head)
+    backward kernels with 512-position LDS buffers, a dL/dbias wave owning two
+    key tiles (0 and 8), fully masked rows (the last 6) and scattered masked
+    pairs."""
+    _tri_attn_backward_case("bf16", starting, 264, [258], inner_mask=0.05)
 
 
 def test_tri_attn_backward_runs_the_kernels(monkeypatch):
