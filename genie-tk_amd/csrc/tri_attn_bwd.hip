@@ -1194,14 +1194,23 @@ __global__ __launch_bounds__(256) void attn_bwd_pro_kernel(const T* __restrict__
   for (int kind = 0; kind < 4; ++kind) {
 #pragma unroll 1
     for (int h = 0; h < H; ++h) {
+      // this (kind, head)'s weight fragments first: their loads overlap the operand loads
+      Frag<T> wf[C / 32][2];
+#pragma unroll
+      for (int nt2 = 0; nt2 < C / 32; ++nt2)
+#pragma unroll
+        for (int gp = 0; gp < 2; ++gp) load_wfrag<T>(wf[nt2][gp], wts[kind], nt2, 2 * h + gp, CH / 16);
       float d[16];
+      // the loads are unconditional (a padded lane reads position j of the
+      // padded slab, or pair p0 of the column-major planes) and selected
+      // afterwards, so they go out together instead of one branch each
       if (kind < 3) {
         const T* s = src[kind] + ((((int64_t)b * N + r) * H + h) * np + j) * AD;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-          const f32x4 v4 = valid ? load4f(s + 8 * g + 4 * half) : f32x4{0.f, 0.f, 0.f, 0.f};
+          const f32x4 v4 = load4f(s + 8 * g + 4 * half);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) d[4 * g + e] = v4[e];
+          for (int e = 0; e < 4; ++e) d[4 * g + e] = valid ? v4[e] : 0.f;
         }
         if constexpr (std::is_same<T, bf16>::value) {
           cmt.store(bf.cm_stack, pitch, p0, kind * CH + h * AD, d, fast, valid);
@@ -1214,22 +1223,21 @@ __global__ __launch_bounds__(256) void attn_bwd_pro_kernel(const T* __restrict__
                   cvt<T>(d[4 * g + e]);
         }
       } else {
+        const int64_t ps = valid ? p : p0;
 #pragma unroll
         for (int g = 0; g < 4; ++g)
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            d[4 * g + e] = valid ? to_f32(bf.cm_stack[(int64_t)(3 * CH + h * AD + 8 * g + 4 * half + e) * pitch + p]) : 0.f;
+          for (int e = 0; e < 4; ++e) {
+            const float v = to_f32(bf.cm_stack[(int64_t)(3 * CH + h * AD + 8 * g + 4 * half + e) * pitch + ps]);
+            d[4 * g + e] = valid ? v : 0.f;
+          }
       }
       Frag<T> f[2];
       vals_to_frags<T>(f, d);
 #pragma unroll
       for (int nt2 = 0; nt2 < C / 32; ++nt2)
 #pragma unroll
-        for (int gp = 0; gp < 2; ++gp) {
-          Frag<T> wf;
-          load_wfrag<T>(wf, wts[kind], nt2, 2 * h + gp, CH / 16);
-          mma(dzn[nt2], wf, f[gp]);
-        }
+        for (int gp = 0; gp < 2; ++gp) mma(dzn[nt2], wf[nt2][gp], f[gp]);
     }
   }
   // triangle bias: dxn += sum_h dB[h][r][j] W_b[h][.]
