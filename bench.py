@@ -24,6 +24,9 @@ import statistics
 import sys
 import time
 
+# the kernels or an error, never the modules' PyTorch path
+os.environ["GENIE_TK_STRICT"] = "1"
+
 ROOT = os.path.dirname(os.path.abspath(__file__))
 for _p in (ROOT, os.path.join(ROOT, "genie-tk_amd")):
     if _p not in sys.path:

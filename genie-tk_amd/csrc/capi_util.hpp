@@ -36,6 +36,15 @@ void set_error(const char* fmt, ...);
 
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
+// |f| <= lim and not NaN, tested on the bits (some sources are compiled
+// without NaN semantics, where a float compare may assume a non-NaN value).
+inline bool abs_at_most(float f, float lim) {
+  uint32_t u, l;
+  __builtin_memcpy(&u, &f, 4);
+  __builtin_memcpy(&l, &lim, 4);
+  return (u & 0x7fffffffu) <= l;
+}
+
 // Compute units of the current device (cached per device; persistent kernels
 // launch one block per CU).
 int device_cus();

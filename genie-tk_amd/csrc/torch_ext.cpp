@@ -32,6 +32,21 @@ void check_gpu(const at::Tensor& t, const char* what) {
   TORCH_CHECK(t.is_cuda(), what, " must be CUDA tensor");
 }
 
+// Every tensor whose data pointer reaches a kernel must live on the device the
+// kernels run on (the device of the main input): a host or foreign-device
+// pointer would be dereferenced by the GPU.
+void check_on(const at::Tensor& t, const at::Tensor& like, const char* what) {
+  if (!t.defined()) return;
+  TORCH_CHECK(t.device() == like.device(), "genie_tk._C: ", what, " is on ", t.device(),
+              " but the input is on ", like.device());
+}
+void check_on(const c10::optional<at::Tensor>& t, const at::Tensor& like, const char* what) {
+  if (t.has_value()) check_on(*t, like, what);
+}
+void check_all_on(const std::vector<at::Tensor>& ts, const at::Tensor& like, const char* what) {
+  for (const auto& t : ts) check_on(t, like, what);
+}
+
 at::Tensor f32c(const at::Tensor& t) { return t.to(at::kFloat).contiguous(); }
 
 at::Tensor workspace(const at::Tensor& like, size_t bytes) {
@@ -44,8 +59,8 @@ at::Tensor workspace(const at::Tensor& like, size_t bytes) {
 at::Tensor layernorm(const at::Tensor& x, const at::Tensor& gamma, const at::Tensor& beta,
                      double eps) {
   check_gpu(x, "x");
-  check_gpu(gamma, "gamma");
-  check_gpu(beta, "beta");
+  check_on(gamma, x, "gamma");
+  check_on(beta, x, "beta");
   const at::DeviceGuard guard(x.device());
   TORCH_CHECK(x.dim() >= 1, "x must have at least one dimension");
   auto xc = x.contiguous();
@@ -67,7 +82,10 @@ static at::Tensor layernorm_linear_impl(const at::Tensor& x, const at::Tensor& g
                                         const c10::optional<at::Tensor>& bias, double eps,
                                         int layout) {
   check_gpu(x, "x");
-  check_gpu(weight, "weight");
+  check_on(weight, x, "weight");
+  check_on(gamma, x, "gamma");
+  check_on(beta, x, "beta");
+  check_on(bias, x, "bias");
   const at::DeviceGuard guard(x.device());
   auto xc = x.contiguous();
   const int64_t d_in = xc.size(-1);
@@ -111,7 +129,8 @@ at::Tensor layernorm_linear(const at::Tensor& x, const at::Tensor& gamma, const 
 at::Tensor triangle_mul_raw(const at::Tensor& a, const at::Tensor& b, const at::Tensor& mask,
                             bool outgoing) {
   check_gpu(a, "a");
-  check_gpu(b, "b");
+  check_on(b, a, "b");
+  check_on(mask, a, "mask");
   const at::DeviceGuard guard(a.device());
   TORCH_CHECK(a.dim() == 4 && a.sizes() == b.sizes() && a.size(1) == a.size(2),
               "a and b must both be [B, N, N, C]");
@@ -139,6 +158,10 @@ at::Tensor triangle_attention_raw(const at::Tensor& q, const at::Tensor& k, cons
                                   const at::Tensor& bias, const at::Tensor& mask, double scale,
                                   bool starting) {
   check_gpu(q, "q");
+  check_on(k, q, "k");
+  check_on(v, q, "v");
+  check_on(bias, q, "bias");
+  check_on(mask, q, "mask");
   const at::DeviceGuard guard(q.device());
   TORCH_CHECK(q.dim() == 5 && q.sizes() == k.sizes() && q.sizes() == v.sizes() &&
                   q.size(2) == q.size(3),
@@ -190,6 +213,7 @@ const void* ptr_or_null(const at::Tensor& t) { return t.defined() ? t.data_ptr()
 at::Tensor tri_mul_pack(std::vector<at::Tensor> ps, int64_t c_z, int64_t c, bool fp32) {
   TORCH_CHECK(ps.size() == 16, "tri_mul_pack expects 16 parameter tensors");
   check_gpu(ps[2], "weights");
+  check_all_on(ps, ps[2], "a parameter");
   const at::DeviceGuard guard(ps[2].device());
   gtk_tri_mul_weights w;
   w.dtype = common_param_dtype(ps);
@@ -213,7 +237,9 @@ std::vector<at::Tensor> tri_mul_backward(const at::Tensor& z, const c10::optiona
                                          double eps_out) {
   TORCH_CHECK(ps.size() == 16, "tri_mul_backward expects 16 parameter tensors");
   check_gpu(z, "z");
-  check_gpu(ps[2], "weights");
+  check_on(mask, z, "mask");
+  check_on(dy, z, "dy");
+  check_all_on(ps, z, "a parameter");
   const at::DeviceGuard guard(z.device());
   TORCH_CHECK(z.dim() == 4 && z.size(1) == z.size(2) && z.size(3) == c_z, "z must be [B, N, N, c_z]");
   TORCH_CHECK(dy.sizes() == z.sizes() && dy.scalar_type() == z.scalar_type(),
@@ -270,7 +296,9 @@ std::vector<at::Tensor> tri_attn_backward(const at::Tensor& x, const c10::option
                                           double eps) {
   TORCH_CHECK(ps.size() == 10, "tri_attn_backward expects 10 parameter tensors");
   check_gpu(x, "x");
-  check_gpu(ps[3], "weights");
+  check_on(mask, x, "mask");
+  check_on(dy, x, "dy");
+  check_all_on(ps, x, "a parameter");
   const at::DeviceGuard guard(x.device());
   TORCH_CHECK(x.dim() == 4 && x.size(1) == x.size(2) && x.size(3) == c_in, "x must be [B, N, N, c_in]");
   TORCH_CHECK(dy.sizes() == x.sizes() && dy.scalar_type() == x.scalar_type(),
@@ -316,6 +344,8 @@ at::Tensor tri_mul_forward(const at::Tensor& z, const c10::optional<at::Tensor>&
                            const at::Tensor& packed, int64_t c_z, int64_t c, bool outgoing,
                            bool residual, double eps_in, double eps_out) {
   check_gpu(z, "z");
+  check_on(mask, z, "mask");
+  check_on(packed, z, "packed");
   const at::DeviceGuard guard(z.device());
   TORCH_CHECK(z.dim() == 4 && z.size(1) == z.size(2) && z.size(3) == c_z, "z must be [B, N, N, c_z]");
   auto zc = z.contiguous();
@@ -339,6 +369,7 @@ at::Tensor tri_mul_forward(const at::Tensor& z, const c10::optional<at::Tensor>&
 at::Tensor pair_transition_pack(std::vector<at::Tensor> ps, int64_t c, int64_t n) {
   TORCH_CHECK(ps.size() == 6, "pair_transition_pack expects 6 parameter tensors");
   check_gpu(ps[2], "weights");
+  check_all_on(ps, ps[2], "a parameter");
   const at::DeviceGuard guard(ps[2].device());
   gtk_pair_transition_weights w;
   w.dtype = common_param_dtype(ps);
@@ -357,6 +388,8 @@ at::Tensor pair_transition_forward(const at::Tensor& p, const c10::optional<at::
                                    const at::Tensor& packed, int64_t c, int64_t n, bool residual,
                                    double eps) {
   check_gpu(p, "p");
+  check_on(mask, p, "mask");
+  check_on(packed, p, "packed");
   const at::DeviceGuard guard(p.device());
   TORCH_CHECK(p.dim() >= 1 && p.size(-1) == c, "p must be [..., c]");
   TORCH_CHECK(p.scalar_type() == at::kBFloat16, "pair_transition_forward: bf16 only");
@@ -379,6 +412,7 @@ at::Tensor tri_attn_pack(std::vector<at::Tensor> ps, int64_t c_in, int64_t c_h, 
                          bool fp32) {
   TORCH_CHECK(ps.size() == 10, "tri_attn_pack expects 10 parameter tensors");
   check_gpu(ps[3], "weights");
+  check_all_on(ps, ps[3], "a parameter");
   const at::DeviceGuard guard(ps[3].device());
   gtk_tri_attn_weights w;
   w.dtype = common_param_dtype(ps);
@@ -397,8 +431,11 @@ at::Tensor tri_attn_pack(std::vector<at::Tensor> ps, int64_t c_in, int64_t c_h, 
 
 at::Tensor tri_attn_forward(const at::Tensor& x, const c10::optional<at::Tensor>& mask,
                             const at::Tensor& packed, int64_t c_in, int64_t c_h, int64_t H,
-                            bool starting, bool residual, double eps, int64_t chunk_rows) {
+                            bool starting, bool residual, double eps, int64_t chunk_rows,
+                            double inf) {
   check_gpu(x, "x");
+  check_on(mask, x, "mask");
+  check_on(packed, x, "packed");
   const at::DeviceGuard guard(x.device());
   TORCH_CHECK(x.dim() == 4 && x.size(1) == x.size(2) && x.size(3) == c_in, "x must be [B, N, N, c_in]");
   auto xc = x.contiguous();
@@ -414,7 +451,7 @@ at::Tensor tri_attn_forward(const at::Tensor& x, const c10::optional<at::Tensor>
   check_rc(gtk_tri_attn_forward_chunked(
       xc.data_ptr(), mask.has_value() ? mc.data_ptr<float>() : nullptr, out.data_ptr(),
       packed.data_ptr(), B, N, c_in, c_h, H, starting ? 1 : 0, residual ? 1 : 0, (float)eps,
-      chunk_rows, dt, ws.data_ptr(), ws.numel(), cur_stream(xc)));
+      (float)inf, chunk_rows, dt, ws.data_ptr(), ws.numel(), cur_stream(xc)));
   return out;
 }
 
@@ -483,7 +520,7 @@ PYBIND11_MODULE(_C, m) {
   m.def("tri_attn_forward", &tri_attn_forward, "Fused TriangleAttention forward", py::arg("x"),
         py::arg("mask"), py::arg("packed"), py::arg("c_in"), py::arg("c_h"), py::arg("no_heads"),
         py::arg("starting"), py::arg("residual") = false, py::arg("eps") = 1e-5,
-        py::arg("chunk_rows") = 0);
+        py::arg("chunk_rows") = 0, py::arg("inf") = 1e9);
   m.def("version", []() { return gtk_version(); });
   m.def("timing_enable", [](bool on) { check_rc(gtk_timing_enable(on ? 1 : 0)); },
         "Record HIP events around every kernel launch (per-kernel timing)", py::arg("on"));

@@ -429,6 +429,7 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
 struct MaskView {
   const float* m;  // nullptr: all valid
   int64_t row_stride, key_stride;
+  float inf;       // a key's logit takes inf * (mask - 1)
 };
 
 template <typename T>
@@ -440,24 +441,9 @@ __device__ __forceinline__ f32x16 flash_row_head(const T* __restrict__ qh, const
   const int half = lane >> 5;
   const int t32 = lane & 31;
 
-  // Does this row have any valid key?
-  bool row_valid = true;
-  if (mv.m) {
-    bool any = false;
-    for (int k0 = 0; k0 < N; k0 += 64) {
-      const int k = k0 + lane;
-      const bool ok = k < N && mv.m[k * mv.key_stride] != 0.f;
-      any = any || (__ballot(ok) != 0ull);
-    }
-    row_valid = any;
-  }
-
   Frag<T> qf[2];
 #pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    if (row_valid) qf[m].load(qh + (int64_t)(q0 + t32) * HD + m * 16 + half * 8);
-    else qf[m].zero();
-  }
+  for (int m = 0; m < 2; ++m) qf[m].load(qh + (int64_t)(q0 + t32) * HD + m * 16 + half * 8);
   const T* brow = biash + (int64_t)(q0 + t32) * Np;
 
   f32x16 o = zero16();
@@ -468,7 +454,7 @@ __device__ __forceinline__ f32x16 flash_row_head(const T* __restrict__ qh, const
     f32x16 s;
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      f32x4 bv = row_valid ? load4f(brow + k0 + 8 * g + 4 * half) : f32x4{0.f, 0.f, 0.f, 0.f};
+      const f32x4 bv = load4f(brow + k0 + 8 * g + 4 * half);
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) s[4 * g + rr] = bv[rr];
     }
@@ -478,17 +464,23 @@ __device__ __forceinline__ f32x16 flash_row_head(const T* __restrict__ qh, const
       kf.load(kh + (int64_t)(k0 + t32) * HD + m * 16 + half * 8);
       mma(s, kf, qf[m]);
     }
-    // exclusion: padded keys always, masked keys when the row has a valid key
+    // padded keys take no weight; a masked key (mask != 1) takes the
+    // reference's additive bias inf * (mask - 1), here in log2 units.  A row
+    // whose keys are all masked follows the reference's fp32 arithmetic
+    // (uniform for inf = 1e9: every score rounds to one value).
     const bool tail = k0 + 32 > N;
-    if (tail || (mv.m && row_valid)) {
+    if (tail || mv.m) {
 #pragma unroll
       for (int g = 0; g < 4; ++g)
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
           const int k = k0 + 8 * g + 4 * half + rr;
-          bool ex = k >= N;
-          if (!ex && mv.m && row_valid) ex = mv.m[k * mv.key_stride] == 0.f;
-          if (ex) s[4 * g + rr] = -INFINITY;
+          if (k >= N) {
+            s[4 * g + rr] = -INFINITY;
+          } else if (mv.m) {
+            const float mval = mv.m[k * mv.key_stride];
+            if (mval != 1.f) s[4 * g + rr] += (mv.inf * (mval - 1.f)) * kLog2e;
+          }
         }
     }
     float mt = s[0];
@@ -537,7 +529,7 @@ __global__ __launch_bounds__(64 * H) void triattn_fused_kernel(const T* __restri
                                                                T* __restrict__ out,
                                                                TriAttnPacked<T> w, AttnWs<T> ws,
                                                                int B, int N, int Np, int starting,
-                                                               int residual) {
+                                                               int residual, float inf) {
   constexpr int CH = H * HD;
   constexpr int OPITCH = CH + 8;
   __shared__ __attribute__((aligned(16))) T os[32 * OPITCH];
@@ -562,6 +554,7 @@ __global__ __launch_bounds__(64 * H) void triattn_fused_kernel(const T* __restri
     mv.m = nullptr;
     mv.row_stride = mv.key_stride = 0;
   }
+  mv.inf = inf;
   const f32x16 o = flash_row_head<T>(ws.q + (rowbase * H + h) * Np * HD,
                                      ws.k + (rowbase * H + h) * Np * HD,
                                      ws.vt + (rowbase * H + h) * HD * (int64_t)Np,
@@ -621,6 +614,14 @@ __global__ __launch_bounds__(64 * H) void triattn_fused_kernel(const T* __restri
 //     tile exceeds it by more than 8 (log2 units); exponentials stay <= 2^8
 //     and the result is exact after the final division by l.
 // ---------------------------------------------------------------------------
+// l in [2^-60, 2^64], tested on the bits: positive floats order as unsigned
+// integers; NaN, zero, negative values and infinity fall outside.  (The
+// softmax code is built without NaN semantics, so a float compare would not
+// be guaranteed to reject a NaN.)
+__device__ __forceinline__ bool l_in_range(float l) {
+  return __float_as_uint(l) - 0x21800000u <= 0x5F800000u - 0x21800000u;
+}
+
 __device__ __forceinline__ float lane_pair_max(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
@@ -635,7 +636,7 @@ template <int CIN, int H, int QT>
 __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))) void triattn_flash_kernel(
     const bf16* __restrict__ x, const float* __restrict__ mask, bf16* __restrict__ out,
     TriAttnPacked<bf16> w, AttnWs<bf16> ws, int N, int Np, int starting, int residual, int r0,
-    int nrows) {
+    int nrows, float inf) {
   constexpr int CH = H * HD;
   constexpr int QB = 32 * QT;              // queries per block (QT query tiles per head)
   constexpr int NW = H * QT;               // waves
@@ -651,10 +652,10 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
   static_assert(QB * OP * 2 <= NS * STAGE_BYTES, "o staging must fit in the ring");
   __shared__ __attribute__((aligned(1024))) char ring[NS][STAGE_BYTES];
   __shared__ __attribute__((aligned(1024))) bf16 wo_l[WO_LDS ? (CIN / 32) * (CH / 16) * 512 : 8];
-  // excluded keys of this row, one bit per key: bit j of word t is key 32t + j
-  __shared__ unsigned kmask[MAXN / 32];  // mask == 0
-  __shared__ unsigned kpad[MAXN / 32];   // key >= N
-  __shared__ int row_any;
+  // keys of this row, one bit per key: bit j of word t is key 32t + j
+  __shared__ unsigned kmask[MAXN / 32];  // mask != 1: takes the bias inf * (mask - 1)
+  __shared__ unsigned kfrac[MAXN / 32];  // ... with mask != 0 (bias from the value)
+  __shared__ unsigned kpad[MAXN / 32];   // key >= N: no weight
   __shared__ int row_dirty;  // some key of the row is masked or padding
 
   const int tid = threadIdx.x;
@@ -677,35 +678,34 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
   // mask of this row: key k is pair (r, k) (starting) or (k, r) (ending)
   const float* mrow = mask ? mask + (int64_t)b * N * N + (starting ? (int64_t)r * N : r) : nullptr;
   const int64_t mks = starting ? 1 : N;
-  if (tid == 0) {
-    row_any = mrow ? 0 : 1;
-    row_dirty = 0;
-  }
+  if (tid == 0) row_dirty = 0;
   __syncthreads();
   {
-    bool any = false, dirty = false;
+    bool dirty = false;
     for (int k0 = wave * 64; k0 < Np; k0 += NW * 64) {
       const int k = k0 + lane;
       const bool inrow = k < N;
-      const bool masked = inrow && mrow && mrow[k * mks] == 0.f;
-      any = any || (inrow && !masked);
+      const float mval = inrow && mrow ? mrow[k * mks] : 1.f;
+      const bool masked = mval != 1.f;
       dirty = dirty || masked || !inrow;
       const unsigned long long mb = __ballot(masked);
+      const unsigned long long fb = __ballot(masked && mval != 0.f);
       const unsigned long long pb = __ballot(!inrow);
       if (lane == 0) {
         kmask[k0 / 32] = (unsigned)mb;
         kmask[k0 / 32 + 1] = (unsigned)(mb >> 32);
+        kfrac[k0 / 32] = (unsigned)fb;
+        kfrac[k0 / 32 + 1] = (unsigned)(fb >> 32);
         kpad[k0 / 32] = (unsigned)pb;
         kpad[k0 / 32 + 1] = (unsigned)(pb >> 32);
       }
     }
-    if (mrow && __ballot(any) != 0ull && lane == 0) row_any = 1;
     if (__ballot(dirty) != 0ull && lane == 0) row_dirty = 1;
   }
   __syncthreads();
-  // block-uniform flags, kept in scalar registers
-  const bool row_valid = __builtin_amdgcn_readfirstlane(row_any) != 0;
+  // block-uniform flag, kept in a scalar register
   const bool row_clean = __builtin_amdgcn_readfirstlane(row_dirty) == 0;
+  const float madd0 = -inf * kLog2e;  // the bias of a key with mask == 0 (log2 units)
 
   // Async stage load.  A stage holds, for each head, the K^T and the V^T
   // block of 64 keys ([32 d][64 keys] each, 4 KiB); each splits into two 2 KiB
@@ -763,8 +763,7 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
     return lds_read_tr16(ring[stage] + wave * 2048 + (c0 + (i >> 2)) * 64 +
                          (16 * ((lane >> 4) & 1) + 4 * (i & 3)) * 2);
   };
-  // query fragments (filled once the q tile is in LDS), zero for a row
-  // without valid keys (uniform attention)
+  // query fragments (filled once the q tile is in LDS)
   Frag<bf16> qf[2];
   // K fragments come from the K^T tile with transposing reads: fetching lane
   // (group G = lane/16, i = lane%16) reads d row (i/4) of a 4-row group at
@@ -783,7 +782,7 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
   for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      idf[cb].v[e] = (bf16)((row_valid && t32 == cb * 16 + half * 8 + e) ? 1.0f : 0.0f);
+      idf[cb].v[e] = (bf16)(t32 == cb * 16 + half * 8 + e ? 1.0f : 0.0f);
   const bf16* brow = ws.bias + ((int64_t)(b * H + h) * Np + q0 + t32) * Np + half * 8;
   Frag<bf16> bfr[2];  // bias fragments of the next S tile to issue
   auto load_bias = [&](int t) {
@@ -791,9 +790,7 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
     bfr[1].load(brow + t * 32 + 16);
   };
   // S^T - m of 32-key tile t: the accumulation starts from negm = -m_use in
-  // every register, then adds I.Bias^T and K Q^T.  For a row without valid
-  // keys the identity and query fragments are zero, so S = negm (uniform
-  // attention) with no per-tile work.
+  // every register, then adds I.Bias^T and K Q^T.
   f32x16 negm = zero16();
   auto s_tile = [&](int t) {
     f32x16 s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(idf[0].v, bfr[0].v, negm, 0, 0, 0);
@@ -830,7 +827,6 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
     const s16x4 lo = read_cq4(1, m * 16 + half * 8), hi = read_cq4(1, m * 16 + half * 8 + 4);
     const s16x8 v8 = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     qf[m].v = __builtin_bit_cast(bf16x8, v8);
-    if (!row_valid) qf[m].zero();
   }
   barrier_only();  // every wave has read its q tile: stage 1 is free
   // stage 1, or (a single key block) the gate tile, into the free stage
@@ -856,15 +852,23 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
     // the last block opens: the gate tile goes into the stage it leaves free
     if (opens && (t >> 1) + 1 == nkb) issue_cq(g_src, nkb % NS);
     const int cur = (t >> 1) % NS;
-    // keys of tile t that take no weight: padding, and masked keys of a valid
-    // row (none at all in a clean row: no LDS read)
-    const unsigned kx = row_clean ? 0u : (kpad[t] | (row_valid ? kmask[t] : 0u));
+    // padding keys of tile t take no weight, masked keys their mask bias
+    // (none at all in a clean row: no LDS read).  For a row whose keys are
+    // all masked the scores follow the reference's fp32 arithmetic: with
+    // inf = 1e9 they round to one value, and the row attends uniformly.
+    const unsigned kx = row_clean ? 0u : (kpad[t] | kmask[t]);
     if (kx != 0u) {
+      const unsigned kp = kpad[t] >> (4 * half), km = kmask[t] >> (4 * half);
+      const unsigned kf = kfrac[t];
 #pragma unroll
       for (int g = 0; g < 4; ++g)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          if ((kx >> (8 * g + 4 * half + rr)) & 1u) sc[4 * g + rr] = -INFINITY;
+        for (int rr = 0; rr < 4; ++rr) {
+          float add = ((km >> (8 * g + rr)) & 1u) ? madd0 : 0.f;
+          if (kf != 0u && ((kf >> (8 * g + 4 * half + rr)) & 1u))
+            add = (inf * (mrow[(int64_t)(32 * t + 8 * g + 4 * half + rr) * mks] - 1.f)) * kLog2e;
+          sc[4 * g + rr] = ((kp >> (8 * g + rr)) & 1u) ? -INFINITY : sc[4 * g + rr] + add;
+        }
     }
     // sc holds s - m_use; the reference max m_ref moves only when a score
     // exceeds it by more than kRescale
@@ -1001,7 +1005,8 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
 // ---------------------------------------------------------------------------
 template <int NPM>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void triattn_flash_rh_kernel(
-    const float* __restrict__ mask, AttnWs<bf16> ws, int N, int Np, int starting, int r0, int nrows) {
+    const float* __restrict__ mask, AttnWs<bf16> ws, int N, int Np, int starting, int r0, int nrows,
+    float inf) {
   constexpr int H = 4, NW = 8, CH = H * HD;
   constexpr int NTM = NPM / 32;       // key tiles at most
   constexpr float kRescale = 8.0f;    // lazy-rescale threshold (log2 units)
@@ -1043,25 +1048,34 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
     }
   }
 
-  // excluded keys of this row: bit j of lane t's word is key 32t + j
-  // (padding, and masked keys of a row with at least one valid key)
+  // Masked keys of this row (mask != 1), one bit per key (bit j of lane t's
+  // word is key 32t + j).  They take the reference's additive bias
+  // inf * (mask - 1), here in log2 units; padding keys (k >= N, the tail of
+  // the last tiles) take no weight.  row_frac: some mask value is neither 0
+  // nor 1, whose bias is then computed from the value.
   const float* mrow = mask ? mask + (int64_t)b * N * N + (starting ? (int64_t)r * N : r) : nullptr;
   const int64_t mks = starting ? 1 : N;
-  uint32_t kmv = 0, kpv = 0;
-  bool any = mrow == nullptr;
+  uint32_t kmv = 0;
+  bool any = mrow == nullptr, frac = false;
   for (int k0 = 0; k0 < Np; k0 += 64) {
     const int k = k0 + lane;
-    const bool inrow = k < N;
-    const bool masked = inrow && mrow && mrow[k * mks] == 0.f;
-    any = any || (inrow && !masked);
+    const float mval = k < N && mrow ? mrow[k * mks] : 1.f;
+    const bool masked = mval != 1.f;
+    any = any || (k < N && !masked);
+    frac = frac || (masked && mval != 0.f);
     const unsigned long long mb = __ballot(masked);
-    const unsigned long long pb = __ballot(!inrow);
     const int w0 = k0 >> 5;
-    if (lane == w0) { kmv = (uint32_t)mb; kpv = (uint32_t)pb; }
-    if (lane == w0 + 1) { kmv = (uint32_t)(mb >> 32); kpv = (uint32_t)(pb >> 32); }
+    if (lane == w0) kmv = (uint32_t)mb;
+    if (lane == w0 + 1) kmv = (uint32_t)(mb >> 32);
   }
-  const bool row_valid = __ballot(any) != 0ull;  // wave-uniform (every wave reads the same row)
-  const uint32_t kxv = kpv | (row_valid ? kmv : 0u);
+  // Some key carries no mask bias: the max-free pass can hold its scores.  A
+  // row without one goes straight to the exact pass, where the reference's
+  // fp32 arithmetic is followed (with inf = 1e9 every score of such a row
+  // rounds to the same value: uniform attention).  Wave-uniform: every wave
+  // reads the same row.
+  const bool row_valid = __ballot(any) != 0ull;
+  const bool row_frac = __ballot(frac) != 0ull;
+  const float madd0 = -inf * kLog2e;  // the bias of a key with mask == 0
 
   const uint32_t stg_lds = lds_addr(stg[wave]);
   char* const sw = stg[wave];
@@ -1120,19 +1134,35 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
       mma(s, kf, qf[m]);
     }
   };
-  // excluded keys of tile t take no weight
-  auto mask_tile = [&](int t, f32x16& sc) {
-    const unsigned kx = __builtin_amdgcn_readlane(kxv, t);
-    if (kx != 0u) {
-      // this lane's keys 8g + 4*half + rr: bits 8g + rr after the shift
-      const unsigned kl = kx >> (4 * (lane >> 5));
+  // padding keys of tile t take no weight, masked keys their mask bias;
+  // FRAC: mask values other than 0 are read back for their bias (only the
+  // exact pass runs rows with such values)
+  auto mask_tile = [&](int t, f32x16& sc, auto frac_tag) {
+    constexpr bool FRAC = decltype(frac_tag)::value;
+    const unsigned km_t = __builtin_amdgcn_readlane(kmv, t);
+    const int nin = N - 32 * t;  // keys of tile t below N
+    if (km_t != 0u || nin < 32) {
+      // this lane's keys j = 8g + 4*half + rr: bits 8g + rr after the shift
+      const int sh = 4 * (lane >> 5);
+      const unsigned km = km_t >> sh;
 #pragma unroll
       for (int g = 0; g < 4; ++g)
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr)
-          if (__builtin_amdgcn_ubfe(kl, 8 * g + rr, 1)) sc[4 * g + rr] = -INFINITY;
+        for (int rr = 0; rr < 4; ++rr) {
+          const bool mk = __builtin_amdgcn_ubfe(km, 8 * g + rr, 1);
+          float add = mk ? madd0 : 0.f;
+          if constexpr (FRAC) {
+            if (row_frac && mk) add = (inf * (mrow[(int64_t)(32 * t + 8 * g + sh + rr) * mks] - 1.f)) * kLog2e;
+          }
+          sc[4 * g + rr] = 8 * g + sh + rr >= nin ? -INFINITY : sc[4 * g + rr] + add;
+        }
     }
   };
+  const std::false_type kBinary;
+  const std::true_type kFrac;
+  // the max-free pass runs when some key has no mask bias and every bias is
+  // inf * (0 - 1)
+  const bool fast_ok = row_valid && !row_frac;
   // P = 2^sc (bf16), l += row sums of P, O^T += V^T P^T
   auto pv_tile = [&](int t, const f32x16& sc, f32x16& o, float& l_run) {
     const char* vt_base = kv + (NTM + t) * 2048;
@@ -1196,32 +1226,14 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
     *reinterpret_cast<uint4*>(reinterpret_cast<char*>(ws.og) + o_off + 1024) = cB;
   };
 
-  if (!row_valid) {
-    // No valid key: every logit is the same -1e9 in the reference, so the row
-    // attends uniformly over its N keys (P = 1, padding excluded); q and the
-    // bias do not matter.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();  // K^T / V^T resident for every wave
-    for (int qt = wave; qt < nq; qt += NW) {
-      issue_cq(g_row + qt * 1024);
-      f32x16 o = zero16();
-      float l_run = 0.f;
-      for (int t = 0; t < nt; ++t) {
-        f32x16 sc = zero16();
-        mask_tile(t, sc);
-        pv_tile(t, sc, o, l_run);
-      }
-      finish(qt * 32, o, lane_pair_sum(l_run), nullptr);
-    }
-    return;
-  }
-
   f32x16 bq[KB];
   int qt = wave;
   if (qt < nq) {
     issue_cq(q_row + qt * 1024);
+    if (fast_ok) {
 #pragma unroll
-    for (int u = 0; u < KB; ++u) load_bias(bq[u], qt * 32, u);
+      for (int u = 0; u < KB; ++u) load_bias(bq[u], qt * 32, u);
+    }
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();  // K^T / V^T resident for every wave
@@ -1247,11 +1259,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
     // stays in range; checked at the end through l, else the exact pass runs.
     f32x16 o = zero16();
     float l_run = 0.f;
-    for (int t = 0; t < nt; t += KB) {
+    for (int t = 0; fast_ok && t < nt; t += KB) {
 #pragma unroll
       for (int u = 0; u < KB; ++u) {
         s_tile(t + u, bq[u], qf);
-        mask_tile(t + u, bq[u]);
+        mask_tile(t + u, bq[u], kBinary);
         pv_tile(t + u, bq[u], o, l_run);
         const bool wrap = t + u + KB >= nt;
         load_bias(bq[u], wrap ? q0n : q0, wrap ? t + u + KB - nt : t + u + KB);
@@ -1262,8 +1274,10 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
     }
     float l_tot = lane_pair_sum(l_run);
     // In range: the largest term 2^max(s) is within [2^-69, 2^64], so no P
-    // overflows and no term that underflows matters.  (NaN fails too.)
-    if (__ballot(!(l_tot >= 0x1p-60f && l_tot <= 0x1p64f)) != 0ull) {
+    // overflows and no term that underflows matters.  Tested on the bits:
+    // positive floats order as unsigned integers, and a NaN, a zero, a
+    // negative value or infinity all fall outside.
+    if (!fast_ok || __ballot(!l_in_range(l_tot)) != 0ull) {
       // Exact pass: online softmax with a running maximum, lazily moved (only
       // when a tile exceeds it by more than kRescale), bias loaded per tile.
       o = zero16();
@@ -1273,7 +1287,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
         f32x16 sc;
         load_bias(sc, q0, t);
         s_tile(t, sc, qf);
-        mask_tile(t, sc);
+        mask_tile(t, sc, kFrac);
 #pragma unroll
         for (int e = 0; e < 16; ++e) sc[e] -= m_use;
         float mt = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
@@ -1479,6 +1493,7 @@ __global__ __launch_bounds__(64) void triattn_raw_kernel(const float* __restrict
   mv.m = mask + (int64_t)b * N * N + (starting ? (int64_t)r * N : r);
   mv.row_stride = 0;
   mv.key_stride = starting ? 1 : N;
+  mv.inf = 1e9f;  // the reference's default TriangleAttention(inf=1e9)
   const f32x16 o = flash_row_head<T>(ws.q + (rowbase * H + h) * Np * HD,
                                      ws.k + (rowbase * H + h) * Np * HD,
                                      ws.vt + (rowbase * H + h) * HD * (int64_t)Np,
@@ -1581,7 +1596,7 @@ static int pack_triattn(const gtk_tri_attn_weights* w, int cin, int ch, int H, v
 // same as without chunks.
 template <typename T, int CIN, int H>
 static int fwd_triattn(const void* x, const float* mask, void* out, const void* packed, int64_t B,
-                       int64_t N, int starting, int residual, float eps, int64_t chunk_rows,
+                       int64_t N, int starting, int residual, float eps, float inf, int64_t chunk_rows,
                        void* ws, hipStream_t st) {
   constexpr int CH = H * HD;
   Carve pc((void*)packed, SIZE_MAX);
@@ -1610,11 +1625,11 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
         {
           StageTimer timer("triattn_flash", st);
           if (Np <= 256)
-            triattn_flash_rh_kernel<256><<<(unsigned)fblocks, 512, 0, st>>>(mask, a, (int)N, Np, starting, r0, nrows);
+            triattn_flash_rh_kernel<256><<<(unsigned)fblocks, 512, 0, st>>>(mask, a, (int)N, Np, starting, r0, nrows, inf);
           else if (Np <= 512)
-            triattn_flash_rh_kernel<512><<<(unsigned)fblocks, 512, 0, st>>>(mask, a, (int)N, Np, starting, r0, nrows);
+            triattn_flash_rh_kernel<512><<<(unsigned)fblocks, 512, 0, st>>>(mask, a, (int)N, Np, starting, r0, nrows, inf);
           else
-            triattn_flash_rh_kernel<1024><<<(unsigned)fblocks, 512, 0, st>>>(mask, a, (int)N, Np, starting, r0, nrows);
+            triattn_flash_rh_kernel<1024><<<(unsigned)fblocks, 512, 0, st>>>(mask, a, (int)N, Np, starting, r0, nrows, inf);
         }
         GTK_HIP_CHECK(hipGetLastError());
         const int64_t otiles = B * nrows * ((N + 31) / 32);
@@ -1627,7 +1642,7 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
       const int64_t fblocks = B * nrows * ((N + 32 * QT - 1) / (32 * QT));
       StageTimer timer("triattn_flash", st);
       triattn_flash_kernel<CIN, H, QT><<<(unsigned)fblocks, 64 * H * QT, 0, st>>>(
-          (const bf16*)x, mask, (bf16*)out, w, a, (int)N, Np, starting, residual, r0, nrows);
+          (const bf16*)x, mask, (bf16*)out, w, a, (int)N, Np, starting, residual, r0, nrows, inf);
       return GTK_OK;
     };
     if (!chunked) {
@@ -1635,7 +1650,7 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
       if (rh) prologue(std::integral_constant<int, 15>(), 0, Np);
       else prologue(std::integral_constant<int, 3>(), 0, Np);
       GTK_LAUNCH_CHECK();
-      flash(0, (int)N);
+      if (int rc = flash(0, (int)N)) return rc;
       GTK_LAUNCH_CHECK();
     } else {
       // the bias over every row (padding rows and columns are written as zero)
@@ -1648,7 +1663,7 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
         if (rh) prologue(std::integral_constant<int, 9>(), (int)r0, nrows);
         else prologue(std::integral_constant<int, 1>(), (int)r0, nrows);
         GTK_LAUNCH_CHECK();
-        flash((int)r0, nrows);
+        if (int rc = flash((int)r0, nrows)) return rc;
         GTK_LAUNCH_CHECK();
       }
     }
@@ -1663,7 +1678,7 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
     {
       StageTimer timer("triattn_flash", st);
       triattn_fused_kernel<T, CIN, H><<<(unsigned)blocks, 64 * H, 0, st>>>(
-          (const T*)x, mask, (T*)out, w, a, (int)B, (int)N, Np, starting, residual);
+          (const T*)x, mask, (T*)out, w, a, (int)B, (int)N, Np, starting, residual, inf);
     }
     GTK_LAUNCH_CHECK();
   }
@@ -1750,8 +1765,8 @@ extern "C" size_t gtk_tri_attn_workspace_size(int64_t B, int64_t N, int64_t c_in
 extern "C" int gtk_tri_attn_forward_chunked(const void* x, const float* mask, void* out,
                                             const void* packed, int64_t B, int64_t N, int64_t c_in,
                                             int64_t c_h, int64_t H, int starting, int residual,
-                                            float eps, int64_t chunk_rows, int dtype, void* ws,
-                                            size_t ws_bytes, void* stream) {
+                                            float eps, float inf, int64_t chunk_rows, int dtype,
+                                            void* ws, size_t ws_bytes, void* stream) {
   GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL, "gtk_tri_attn_forward: bad dtype %d", dtype);
   GTK_REQUIRE(triattn_shape_ok(c_in, c_h, H), GTK_EUNSUPPORTED,
               "gtk_tri_attn_forward: c_in=%lld c_h=%lld H=%lld unsupported (c_in=128, H=4, d=32)",
@@ -1760,6 +1775,8 @@ extern "C" int gtk_tri_attn_forward_chunked(const void* x, const float* mask, vo
               "gtk_tri_attn_forward: bad shape");
   GTK_REQUIRE(chunk_rows == 0 || dtype == GTK_BF16, GTK_EUNSUPPORTED,
               "gtk_tri_attn_forward_chunked: row chunks need bf16");
+  GTK_REQUIRE(abs_at_most(inf, 1e37f), GTK_EINVAL,
+              "gtk_tri_attn_forward: |inf| must be at most 1e37, got %g", (double)inf);
   if (B == 0 || N == 0) return GTK_OK;
   GTK_REQUIRE(x && out && packed && ws, GTK_EINVAL, "gtk_tri_attn_forward: null pointer");
   const size_t need = gtk_tri_attn_workspace_size_chunked(B, N, c_in, c_h, H, chunk_rows, dtype);
@@ -1767,15 +1784,15 @@ extern "C" int gtk_tri_attn_forward_chunked(const void* x, const float* mask, vo
               ws_bytes, need);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == GTK_F32)
-    return fwd_triattn<float, 128, 4>(x, mask, out, packed, B, N, starting, residual, eps, 0, ws, st);
-  return fwd_triattn<bf16, 128, 4>(x, mask, out, packed, B, N, starting, residual, eps, chunk_rows,
-                                   ws, st);
+    return fwd_triattn<float, 128, 4>(x, mask, out, packed, B, N, starting, residual, eps, inf, 0, ws, st);
+  return fwd_triattn<bf16, 128, 4>(x, mask, out, packed, B, N, starting, residual, eps, inf,
+                                   chunk_rows, ws, st);
 }
 
 extern "C" int gtk_tri_attn_forward(const void* x, const float* mask, void* out, const void* packed,
                                     int64_t B, int64_t N, int64_t c_in, int64_t c_h, int64_t H,
-                                    int starting, int residual, float eps, int dtype, void* ws,
-                                    size_t ws_bytes, void* stream) {
+                                    int starting, int residual, float eps, float inf, int dtype,
+                                    void* ws, size_t ws_bytes, void* stream) {
   return gtk_tri_attn_forward_chunked(x, mask, out, packed, B, N, c_in, c_h, H, starting, residual,
-                                      eps, 0, dtype, ws, ws_bytes, stream);
+                                      eps, inf, 0, dtype, ws, ws_bytes, stream);
 }

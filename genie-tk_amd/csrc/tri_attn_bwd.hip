@@ -200,7 +200,9 @@ __global__ __launch_bounds__(256) void attn_bwd_proj_kernel(const T* __restrict_
       }
     }
   }
-  if (half == 0) bf.kmask[((int64_t)b * N + r) * np + j] = valid ? (mask ? mask[xp] : 1.f) : 0.f;
+  // 1 for a valid key (mask == 1: no bias); 0 for a masked key, whose bias
+  // 1e9 * (mask - 1) <= -60 takes it out of any row with a valid key
+  if (half == 0) bf.kmask[((int64_t)b * N + r) * np + j] = valid && (!mask || mask[xp] == 1.f) ? 1.f : 0.f;
 }
 
 // ---------------------------------------------------------------------------

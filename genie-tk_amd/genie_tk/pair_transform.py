@@ -78,7 +78,9 @@ class PairTransition(nn.Module):
     def _use_kernel(self, p: Tensor) -> bool:
         if not (p.is_cuda and self._fused_requested):
             return False
-        _ext.require()
+        if _ext.C is None or not torch.cuda.is_available():
+            _ext.missing(type(self).__name__)
+            return False
         return (p.dtype == torch.bfloat16 and p.dim() >= 1 and p.shape[-1] == self.c_p
                 and self.c_p in (64, 128) and self.n == 4 and self.layer_norm.elementwise_affine
                 and not _dispatch.needs_autograd(p, self))

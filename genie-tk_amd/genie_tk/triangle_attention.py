@@ -13,10 +13,13 @@ When autograd needs gradients the same forward runs inside
 PyTorch path: ``_forward_pytorch``, the reference fallback semantics
 (triangle_attention.py:100-143).
 
-Mask semantics of the kernel path: keys with mask == 0 get zero weight; a row
-without any valid key attends uniformly over all keys, which is what the
-PyTorch path produces with the default ``inf=1e9`` (every logit rounds to
--1e9 in fp32 while |logit| < 32).
+Mask semantics of the kernel path: the reference's additive bias
+``inf * (mask - 1)`` (triangle_attention.py:118) with the module's ``inf``,
+in fp32.  A key with mask 1 takes no bias; a row whose keys are all masked
+follows the fp32 arithmetic of the reference, which with the default
+``inf=1e9`` makes it uniform (every logit rounds to -1e9 while |logit| < 32).
+The backward kernels implement the default ``inf=1e9``; a module with another
+``inf`` trains through autograd of its PyTorch path.
 """
 from __future__ import annotations
 
@@ -144,7 +147,7 @@ class TriangleAttention(nn.Module):
         packed = self._packed_params(x.dtype == torch.float32)
         out = C.tri_attn_forward(xb, mb, packed, self.c_in, self.c_hidden, self.no_heads,
                                  self.starting, residual, self.layer_norm.eps,
-                                 int(chunk_size or 0))
+                                 int(chunk_size or 0), float(self.inf))
         return out.reshape(*lead, *out.shape[1:])
 
     def forward_residual(self, x: Tensor, mask: Optional[Tensor] = None) -> Tensor:
@@ -167,12 +170,13 @@ class TriangleAttention(nn.Module):
             raise ValueError(f"chunk_size must be >= 1, got {chunk_size}")
         if x.is_cuda and self._fused_requested:
             if not _CUDA_AVAILABLE:
-                _ext.require()
-            if (self.use_fused_kernel and self._kernel_supported(x)
+                _ext.missing(type(self).__name__)
+            elif (self.use_fused_kernel and self._kernel_supported(x)
                     and (chunk_size is None or x.dtype == torch.bfloat16)):
                 if not _dispatch.needs_autograd(x, self):
                     return self._forward_cuda(x, mask, chunk_size=chunk_size)
-                return _TriAttnFunction.apply(self, x, mask, chunk_size, *self._param_list())
+                if self.inf == 1e9:  # the backward kernels' mask bias
+                    return _TriAttnFunction.apply(self, x, mask, chunk_size, *self._param_list())
         return self._forward_pytorch(x, mask, chunk_size)
 
 

@@ -151,8 +151,8 @@ class TriangleMultiplicativeUpdate(nn.Module):
         """z: [*, N, N, c_z], mask: [*, N, N] -> update [*, N, N, c_z]."""
         if z.is_cuda and self._fused_requested:
             if not _CUDA_AVAILABLE:
-                _ext.require()
-            if self.use_fused_kernel and self._kernel_supported(z):
+                _ext.missing(type(self).__name__)
+            elif self.use_fused_kernel and self._kernel_supported(z):
                 if not _dispatch.needs_autograd(z, self):
                     return self._forward_cuda(z, mask)
                 return _TriMulFunction.apply(self, z, mask, *self._param_list())

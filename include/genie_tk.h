@@ -112,9 +112,11 @@ int gtk_triangle_mul_incoming(const void* a, const void* b, const float* mask, v
  * ending (attention along the first spatial axis, columns j independent):
  *   out[b][q][j][h*D+d] = sum_k softmax_k(scale*<q[b,h,q,j], k[b,h,k,j]>
  *                              + mask_bias[b,k,j] + bias[b,h,q,k]) * v[b,h,k,j,d]
- * mask_bias is -inf for mask == 0 keys; a row with no valid key attends
- * uniformly over all N keys (the limit of the reference's -1e9 additive
- * bias).  D == 32, N <= 8192.
+ * mask_bias = 1e9 * (mask - 1), the additive bias of the reference's
+ * TriangleAttention with its default inf = 1e9 (triangle_attention.py:57,118),
+ * in fp32: a masked key takes no weight in a row with a valid key, and a row
+ * whose keys are all masked (mask = 0) attends uniformly, as every score of
+ * such a row rounds to -1e9 in fp32.  D == 32, N <= 8192.
  * ------------------------------------------------------------------------ */
 size_t gtk_triangle_attention_workspace_size(int64_t B, int64_t H, int64_t N, int64_t D, int dtype);
 int gtk_triangle_attention_starting(const void* q, const void* k, const void* v, const float* bias,
@@ -189,8 +191,12 @@ int gtk_tri_mul_backward(const void* z, const float* mask, const void* dy,
  *   xn   = LN(x);  tri[h,q,k] = xn[q,k] . W_tri[h]
  *   o    = softmax(q k^T / sqrt(d) + mask_bias + tri) v        per row, head
  *   out  = (o * sigmoid(xn W_g^T + b_g)) W_o^T + b_o    [+ x if residual]
- * Mask semantics as gtk_triangle_attention_starting.
- * c_in == 128, H == 4, d == 32 (c_h == 128), N <= 8192.
+ * mask_bias[k] = inf * (mask[k] - 1) in fp32, the module's constructor
+ * argument inf (triangle_attention.py:57,118; the reference default is 1e9):
+ * keys with mask == 1 take no bias, any other mask value (0 or fractional)
+ * takes that bias, and a row whose keys all carry a bias follows the fp32
+ * arithmetic of the reference (uniform attention for inf = 1e9 and mask 0).
+ * |inf| <= 1e37.  c_in == 128, H == 4, d == 32 (c_h == 128), N <= 8192.
  * ------------------------------------------------------------------------ */
 typedef struct gtk_tri_attn_weights {
   int dtype;                 /* element type of every pointer below */
@@ -209,7 +215,7 @@ size_t gtk_tri_attn_workspace_size(int64_t B, int64_t N, int64_t c_in, int64_t c
 /* mask may be NULL (all ones).  out may not alias x. */
 int gtk_tri_attn_forward(const void* x, const float* mask, void* out, const void* packed,
                          int64_t B, int64_t N, int64_t c_in, int64_t c_h, int64_t H, int starting,
-                         int residual, float eps, int dtype, void* workspace,
+                         int residual, float eps, float inf, int dtype, void* workspace,
                          size_t workspace_bytes, void* stream);
 
 /* Memory-bounded form of gtk_tri_attn_forward (bf16): the attention rows are
@@ -225,8 +231,9 @@ size_t gtk_tri_attn_workspace_size_chunked(int64_t B, int64_t N, int64_t c_in, i
                                            int64_t H, int64_t chunk_rows, int dtype);
 int gtk_tri_attn_forward_chunked(const void* x, const float* mask, void* out, const void* packed,
                                  int64_t B, int64_t N, int64_t c_in, int64_t c_h, int64_t H,
-                                 int starting, int residual, float eps, int64_t chunk_rows,
-                                 int dtype, void* workspace, size_t workspace_bytes, void* stream);
+                                 int starting, int residual, float eps, float inf,
+                                 int64_t chunk_rows, int dtype, void* workspace,
+                                 size_t workspace_bytes, void* stream);
 
 /* Backward of gtk_tri_attn_forward (update only, no residual): given dL/dy,
  * writes dL/dx (element type dtype) and the gradient of every parameter
@@ -237,7 +244,10 @@ int gtk_tri_attn_forward_chunked(const void* x, const float* mask, void* out, co
  * treatment of rows whose keys are all masked (their uniform softmax still
  * passes its gradient to q, k and the triangle bias).  Activations are
  * recomputed from x and the raw weights in w.  Gradients are written, not
- * accumulated.  c_in == 128, H == 4, d == 32, N <= 4096. */
+ * accumulated.  The mask bias is the reference default's, inf = 1e9: a key
+ * with mask == 1 is valid, any other value masks it (for a row with a valid
+ * key this is the reference's result up to weights below e^-60), and a row
+ * with no valid key is uniform.  c_in == 128, H == 4, d == 32, N <= 4096. */
 typedef struct gtk_tri_attn_grads {
   float *ln_w, *ln_b, *tri_w, *q_w, *k_w, *v_w, *g_w, *g_b, *o_w, *o_b;
 } gtk_tri_attn_grads;

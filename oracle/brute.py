@@ -36,6 +36,20 @@ def _sig(t: float) -> float:
     return 1.0 / (1.0 + math.exp(-t))
 
 
+def _score(sqk: float, tri: float, m: float, inf: float) -> float:
+    """The reference's score (qk*scale + inf*(m - 1)) + tri (primitives.py:156-158,
+    triangle_attention.py:118).  For m != 1 and |inf| >= 2^29 the fp32
+    reference's sum rounds to its mask term (|qk|, |tri| below half an ulp of
+    it), so that fp32 value is the score; a row whose keys are all masked with
+    mask 0 is then uniform."""
+    if m == 1.0:
+        return sqk + tri
+    mb = inf * (m - 1.0)
+    if abs(inf) >= 2.0 ** 29:
+        return float(np.float32(mb))
+    return (sqk + mb) + tri
+
+
 def tri_mul(z: np.ndarray, mask: Optional[np.ndarray], P: Dict[str, np.ndarray],
             outgoing: bool, eps: float = 1e-5) -> np.ndarray:
     B, N, _, cz = z.shape
@@ -78,9 +92,9 @@ def tri_attn(x: np.ndarray, mask: Optional[np.ndarray], P: Dict[str, np.ndarray]
              starting: bool, no_heads: int, inf: float = 1e9, eps: float = 1e-5) -> np.ndarray:
     """Attention over positions of each row; ending node indexes columns directly.
 
-    A masked key's score is exactly -inf_value (the fp32 absorption of the
-    reference's additive -1e9 term, valid for |logit| < 32), so a row whose
-    keys are all masked gets uniform weights.
+    Scores follow _score: a masked key's score is the fp32 value of
+    inf * (mask - 1) when that term absorbs the rest (|inf| >= 2^29), so a row
+    whose keys are all masked with mask 0 gets uniform weights.
     """
     B, N, _, cin = x.shape
     ch = P["mha.linear_q.weight"].shape[0]
@@ -109,10 +123,7 @@ def tri_attn(x: np.ndarray, mask: Optional[np.ndarray], P: Dict[str, np.ndarray]
                     logits = []
                     for k in range(N):
                         s = sum(qv[q][h * d + t] * kv[k][h * d + t] for t in range(d)) * scale
-                        s += tri[(q, k)][h]
-                        if valid[k] == 0.0:
-                            s = -inf
-                        logits.append(s)
+                        logits.append(_score(s, tri[(q, k)][h], valid[k], inf))
                     mx = max(logits)
                     w = [math.exp(t - mx) for t in logits]
                     tot = sum(w)
@@ -123,6 +134,41 @@ def tri_attn(x: np.ndarray, mask: Optional[np.ndarray], P: Dict[str, np.ndarray]
                 y = _lin(o, P["mha.linear_o.weight"], P["mha.linear_o.bias"])
                 for c in range(cin):
                     out[at(bb, r, q) + (c,)] = y[c]
+    return out
+
+
+def pair_transition(p: np.ndarray, P: Dict[str, np.ndarray], eps: float = 1e-5) -> np.ndarray:
+    """PairTransition.forward (pair_transform.py:79-84) pair by pair: LayerNorm,
+    linear_1 (c -> n c), ReLU, linear_2 (n c -> c)."""
+    out = np.zeros(p.shape)
+    flat = p.reshape(-1, p.shape[-1])
+    of = out.reshape(-1, p.shape[-1])
+    for r in range(flat.shape[0]):
+        v = _ln([float(t) for t in flat[r]], P["layer_norm.weight"], P["layer_norm.bias"], eps)
+        h = [max(t, 0.0) for t in _lin(v, P["linear_1.weight"], P["linear_1.bias"])]
+        of[r] = _lin(h, P["linear_2.weight"], P["linear_2.bias"])
+    return out
+
+
+def pair_block(p: np.ndarray, mask: np.ndarray, P: Dict[str, np.ndarray], no_heads: int) -> np.ndarray:
+    """PairTransformLayer.forward in eval mode (pair_transform.py:180-193): each
+    update added to p in turn (dropout is the identity), then p * mask."""
+    def sub(prefix):
+        return {k[len(prefix):]: v for k, v in P.items() if k.startswith(prefix)}
+
+    p = np.asarray(p, dtype=np.float64)
+    p = p + tri_mul(p, mask, sub("tri_mul_out."), True)
+    p = p + tri_mul(p, mask, sub("tri_mul_in."), False)
+    p = p + tri_attn(p, mask, sub("tri_att_start."), True, no_heads)
+    p = p + tri_attn(p, mask, sub("tri_att_end."), False, no_heads)
+    p = p + pair_transition(p, sub("pair_transition."))
+    out = np.zeros(p.shape)
+    B, N = p.shape[0], p.shape[1]
+    for bb in range(B):
+        for i in range(N):
+            for j in range(N):
+                for c in range(p.shape[-1]):
+                    out[bb, i, j, c] = p[bb, i, j, c] * float(mask[bb, i, j])
     return out
 
 
@@ -158,8 +204,8 @@ def attention_core(q, k, v, bias, mask, scale: float, starting: bool, inf: float
     """_C.triangle_attention_starting/ending semantics (kernels/bindings.cpp:82-90):
     q, k, v [B,H,N,N,D]; bias [B,H,N,N] indexed (query, key); mask [B,N,N].
     Starting: row i = axis 2, positions along axis 3; ending: row j = axis 3,
-    positions along axis 2.  Masked keys score -inf (uniform weights if a row
-    has no valid key).  Returns [B,N,N,H*D]."""
+    positions along axis 2.  Scores follow _score with the reference's
+    default inf = 1e9.  Returns [B,N,N,H*D]."""
     B, H, N, _, D = q.shape
     out = np.zeros((B, N, N, H * D))
 
@@ -174,10 +220,8 @@ def attention_core(q, k, v, bias, mask, scale: float, starting: bool, inf: float
                     for ki in range(N):
                         s = sum(float(q[(bb, h) + at(r, qi) + (t,)]) * float(k[(bb, h) + at(r, ki) + (t,)])
                                 for t in range(D)) * scale
-                        s += float(bias[bb, h, qi, ki])
-                        if float(mask[(bb,) + at(r, ki)]) == 0.0:
-                            s = -inf
-                        logits.append(s)
+                        logits.append(_score(s, float(bias[bb, h, qi, ki]),
+                                             float(mask[(bb,) + at(r, ki)]), inf))
                     mx = max(logits)
                     w = [math.exp(t - mx) for t in logits]
                     tot = sum(w)

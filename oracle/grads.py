@@ -153,6 +153,8 @@ def tri_attn_grad(x: np.ndarray, mask: Optional[np.ndarray], params: Params, sta
     flat = lambda t: t.transpose(1, 0, 2).reshape(N, ch)    # noqa: E731
     for b in range(B):
         for i in range(N):
+            if not dy[b, i].any():
+                continue  # every term of this row is a product with dy[b, i]: all zero
             xi = xn[b, i]
             q, k, v = heads(xi @ Wq.T), heads(xi @ Wk.T), heads(xi @ Wv.T)
             s = _masked_scores((q @ k.transpose(0, 2, 1)) * scale, m[b, i][None, None, :],

@@ -13,8 +13,9 @@ import numpy as np
 
 Params = Dict[str, np.ndarray]
 
-# Largest |logit| for which fl32(logit - 1e9) == -1e9 (ulp(1e9) = 64 in fp32).
-_FP32_ABSORB = 32.0
+# |inf| from which the fp32 mask term inf * (mask - 1) of a masked key absorbs
+# the logit it is added to (ulp(2^29) = 64 in fp32).
+_ABSORB_INF = 2.0 ** 29
 
 
 def _p(params: Params, key: str, dtype) -> np.ndarray:
@@ -96,22 +97,27 @@ def _softmax_rows(s: np.ndarray) -> np.ndarray:
 
 def _masked_scores(qk: np.ndarray, keymask: np.ndarray, tri: np.ndarray, inf: float,
                    dtype) -> np.ndarray:
-    """scores = (qk + inf*(m-1)) + tri, in the reference's order (primitives.py:156-158).
+    """scores = (qk + inf*(m-1)) + tri, in the reference's order (primitives.py:156-158;
+    mask bias triangle_attention.py:118).
 
-    In float32 this is the literal reference arithmetic.  In float64 the
-    fp32 absorption of the -inf term is made explicit: a masked key's score
-    is exactly -inf (valid while |qk|, |tri| < 32, asserted), so that fully
-    masked rows stay uniform as in the fp32 reference.
+    In float32 this is the literal reference arithmetic.  In float64, for
+    |inf| >= 2^29, the fp32 absorption is made explicit: the score of a key
+    with mask != 1 is the fp32 value of inf*(m-1), which the fp32 reference
+    produces while |qk| and |tri| stay below half an ulp of it (asserted), so
+    that a row whose keys are all masked with mask 0 stays uniform as in the
+    fp32 reference.  For smaller |inf| the float64 sum is used as it stands.
     """
     mb = (inf * (keymask - 1)).astype(dtype)
     if dtype == np.float32:
         return (qk + mb) + tri
     s = qk + tri
-    masked = np.broadcast_to(keymask == 0, s.shape)
-    if inf >= 2.0 ** 29 and masked.any():
-        assert np.abs(qk[masked]).max() < _FP32_ABSORB and np.abs(
-            np.broadcast_to(tri, s.shape)[masked]).max() < _FP32_ABSORB
-        return np.where(masked, -np.asarray(inf, dtype), s)
+    masked = np.broadcast_to(keymask != 1, s.shape)
+    if abs(inf) >= _ABSORB_INF and masked.any():
+        mb32 = np.broadcast_to((inf * (keymask - 1)).astype(np.float32).astype(dtype), s.shape)
+        half_ulp = np.spacing(np.abs(mb32[masked]).astype(np.float32)).astype(dtype) / 2
+        assert (np.abs(qk[masked]) < half_ulp).all() and (
+            np.abs(np.broadcast_to(tri, s.shape)[masked]) < half_ulp).all()
+        return np.where(masked, mb32, s)
     return (qk + mb) + tri
 
 

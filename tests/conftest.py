@@ -9,6 +9,10 @@ import sys
 
 import pytest
 
+# A module asked for its kernel path with the extension missing raises instead
+# of running its PyTorch path: a test must never pass on the fallback.
+os.environ.setdefault("GENIE_TK_STRICT", "1")
+
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 for p in (ROOT, os.path.join(ROOT, "genie-tk_amd")):
     if p not in sys.path:

@@ -259,22 +259,84 @@ def test_shared_dropout_broadcasts():
     assert torch.equal(DropoutRowwise(0.5).eval()(x), x)
 
 
-def test_fused_path_on_gpu_tensor_requires_extension(monkeypatch):
-    """A GPU tensor with use_fused_kernel=True never falls back silently when the
-    extension is missing: forward raises ImportError."""
-    from genie_tk import _ext, triangle_mul
+@pytest.fixture
+def no_extension(monkeypatch):
+    """genie_tk._C made unimportable (sys.modules entry None) and the loader
+    re-run, as in a tree where the extension was never built; restored after."""
+    import importlib
+    import sys
 
-    class FakeCuda(torch.Tensor):
-        @property
-        def is_cuda(self):
-            return True
+    import genie_tk
+    from genie_tk import _ext, triangle_attention, triangle_mul
 
-    monkeypatch.setattr(_ext, "C", None)
-    monkeypatch.setattr(triangle_mul, "_CUDA_AVAILABLE", False)
+    saved_mod = sys.modules.get("genie_tk._C", None)
+    had_attr = hasattr(genie_tk, "_C")
+    saved_attr = getattr(genie_tk, "_C", None)
+    saved = (_ext.C, _ext.IMPORT_ERROR)
+    sys.modules["genie_tk._C"] = None
+    if had_attr:
+        delattr(genie_tk, "_C")
+    try:
+        importlib.reload(_ext)
+        assert _ext.C is None and isinstance(_ext.IMPORT_ERROR, ImportError)
+        monkeypatch.setattr(triangle_mul, "_CUDA_AVAILABLE", False)
+        monkeypatch.setattr(triangle_attention, "_CUDA_AVAILABLE", False)
+        _ext._warned.clear()
+        yield _ext
+    finally:
+        if saved_mod is None:
+            sys.modules.pop("genie_tk._C", None)
+        else:
+            sys.modules["genie_tk._C"] = saved_mod
+        if had_attr:
+            genie_tk._C = saved_attr
+        _ext.C, _ext.IMPORT_ERROR = saved
+        _ext._warned.clear()
+
+
+class _FakeCuda(torch.Tensor):
+    """A CPU tensor that reports is_cuda, to reach the kernel switch without a GPU."""
+
+    @property
+    def is_cuda(self):
+        return True
+
+
+def test_missing_extension_falls_back_with_warning(no_extension, monkeypatch):
+    """The reference's switch (triangle_mul.py:24-30,61; triangle_attention.py:25-31,67):
+    with genie_tk._C missing, a GPU tensor with use_fused_kernel=True runs the
+    PyTorch path.  This build also warns, once per module class."""
+    monkeypatch.delenv(no_extension.STRICT_ENV, raising=False)
+    torch.manual_seed(0)
     mod = TriangleMultiplicationOutgoing(16, 8, use_fused_kernel=True)
-    z = torch.zeros(1, 4, 4, 16).as_subclass(FakeCuda)
+    att = TriangleAttentionStartingNode(16, 8, 2, use_fused_kernel=True)
+    for m in (mod, att):
+        for p in m.parameters():
+            torch.nn.init.normal_(p, std=0.3)
+    assert not mod.use_fused_kernel and not att.use_fused_kernel
+    z = torch.randn(1, 5, 5, 16)
+    with pytest.warns(RuntimeWarning, match="not available"):
+        y = mod(z.as_subclass(_FakeCuda))
+    assert torch.equal(y.as_subclass(torch.Tensor), mod._forward_pytorch(z))
+    import warnings
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")  # once per class: no second warning
+        mod(z.as_subclass(_FakeCuda))
+    with pytest.warns(RuntimeWarning, match="TriangleAttentionStartingNode"):
+        ya = att(z.as_subclass(_FakeCuda))
+    assert torch.equal(ya.as_subclass(torch.Tensor), att._forward_pytorch(z))
+
+
+def test_missing_extension_strict_raises(no_extension, monkeypatch):
+    """GENIE_TK_STRICT=1 (this repository's tests, smoke and bench) turns the
+    fallback into ImportError, so an unbuilt library never passes for a working one."""
+    monkeypatch.setenv(no_extension.STRICT_ENV, "1")
+    mod = TriangleMultiplicationOutgoing(16, 8, use_fused_kernel=True)
     with pytest.raises(ImportError):
-        mod(z)
+        mod(torch.zeros(1, 4, 4, 16).as_subclass(_FakeCuda))
+    att = TriangleAttentionEndingNode(16, 8, 2, use_fused_kernel=True)
+    with pytest.raises(ImportError):
+        att(torch.zeros(1, 4, 4, 16).as_subclass(_FakeCuda))
     # explicitly disabled: the PyTorch path is the documented behaviour
     mod2 = TriangleMultiplicationOutgoing(16, 8, use_fused_kernel=False)
     assert mod2(torch.zeros(1, 4, 4, 16)).shape == (1, 4, 4, 16)

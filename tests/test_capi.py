@@ -56,10 +56,10 @@ def lib():
     L.gtk_layernorm.argtypes = [vp, vp, vp, vp, i64, i64, fp, ci, vp]
     L.gtk_tri_mul_forward.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, ci, ci, fp, fp, ci,
                                       vp, sz, vp]
-    L.gtk_tri_attn_forward.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, ci, fp, ci,
-                                       vp, sz, vp]
+    L.gtk_tri_attn_forward.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, ci, fp, fp,
+                                       ci, vp, sz, vp]
     L.gtk_tri_attn_forward_chunked.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, ci,
-                                               fp, i64, ci, vp, sz, vp]
+                                               fp, fp, i64, ci, vp, sz, vp]
     L.gtk_triangle_mul_outgoing.argtypes = [vp, vp, vp, vp, i64, i64, i64, ci, vp, sz, vp]
     L.gtk_triangle_attention_starting.argtypes = [vp, vp, vp, vp, vp, fp, vp, i64, i64, i64,
                                                   i64, ci, vp, sz, vp]
@@ -145,15 +145,19 @@ def test_bad_dtype_and_shapes_are_rejected(lib):
     rc = lib.gtk_tri_mul_forward(dummy, None, dummy, dummy, 1, 8, 128, 128, 1, 0, 1e-5, 1e-5,
                                  GTK_BF16, dummy, 10, None)
     assert rc == GTK_EWORKSPACE and "workspace" in _err(lib)
-    rc = lib.gtk_tri_attn_forward(None, None, None, None, 1, 8, 128, 128, 8, 1, 0, 1e-5,
+    rc = lib.gtk_tri_attn_forward(None, None, None, None, 1, 8, 128, 128, 8, 1, 0, 1e-5, 1e9,
                                   GTK_BF16, None, 0, None)
     assert rc == GTK_EUNSUPPORTED
     rc = lib.gtk_tri_attn_forward_chunked(None, None, None, None, 1, 8, 128, 128, 4, 1, 0, 1e-5,
-                                          4, GTK_F32, None, 0, None)
+                                          1e9, 4, GTK_F32, None, 0, None)
     assert rc == GTK_EUNSUPPORTED and "bf16" in _err(lib)
     rc = lib.gtk_tri_attn_forward_chunked(None, None, None, None, 1, 8, 128, 128, 4, 1, 0, 1e-5,
-                                          -1, GTK_BF16, None, 0, None)
+                                          1e9, -1, GTK_BF16, None, 0, None)
     assert rc == GTK_EINVAL
+    for bad in (float("inf"), float("nan"), 2e37):  # the mask bias must stay finite
+        rc = lib.gtk_tri_attn_forward(None, None, None, None, 1, 8, 128, 128, 4, 1, 0, 1e-5, bad,
+                                      GTK_BF16, None, 0, None)
+        assert rc == GTK_EINVAL and "inf" in _err(lib)
     rc = lib.gtk_tri_mul_backward(None, None, None, None, None, None, 1, 8, 128, 96, 1, 1e-5,
                                   1e-5, GTK_BF16, None, 0, None)
     assert rc == GTK_EUNSUPPORTED and "c=96" in _err(lib)
@@ -186,7 +190,7 @@ def test_empty_inputs_are_no_ops(lib):
                                    GTK_BF16, None, 0, None) == GTK_OK
     assert lib.gtk_tri_mul_forward(None, None, None, None, 1, 0, 128, 64, 0, 0, 1e-5, 1e-5,
                                    GTK_F32, None, 0, None) == GTK_OK
-    assert lib.gtk_tri_attn_forward(None, None, None, None, 2, 0, 128, 128, 4, 0, 0, 1e-5,
+    assert lib.gtk_tri_attn_forward(None, None, None, None, 2, 0, 128, 128, 4, 0, 0, 1e-5, 1e9,
                                     GTK_BF16, None, 0, None) == GTK_OK
     assert lib.gtk_triangle_mul_outgoing(None, None, None, None, 0, 8, 16, GTK_F32, None, 0,
                                          None) == GTK_OK

@@ -184,6 +184,97 @@ def test_attention_core_matches_sdpa(starting):
     np.testing.assert_allclose(got, want, atol=1e-10)
 
 
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("inf", [2.5, 30.0, 1e4])
+def test_tri_attn_general_inf_and_fractional_mask(starting, inf):
+    """The mask bias inf * (mask - 1) with a non-default inf and fractional mask
+    values, where the reference's sum does not absorb: pair_ops (float64)
+    against the scalar loops and against SDPA with the additive mask
+    inf * (m - 1) + tri, in float64 (no fp32 absorption anywhere)."""
+    P = _ta_params(seed=40)
+    N, nh = 7, 2
+    x = H.pair_input(2, N, 16, seed=41).astype(F64)
+    m = _partial_mask(2, N, seed=42)
+    m[0, 1, :] = 0            # every key masked
+    m[1, 2, :3] = 0.5         # fractional values
+    m[1, 4, :] = 0.25         # every key fractional
+    m = m if starting else m.swapaxes(1, 2).copy()
+    got = pair_ops.tri_attn(x, m, P, starting, nh, inf=inf, dtype=F64)
+    np.testing.assert_allclose(brute.tri_attn(x, m, P, starting, nh, inf=inf), got, rtol=0, atol=1e-11)
+    # the same through torch: LN, projections, SDPA with the additive mask
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=F64))  # noqa: E731
+    xs, ms = (x, m) if starting else (x.swapaxes(1, 2), m.swapaxes(1, 2))
+    xn = F.layer_norm(t(xs), (16,), t(P["layer_norm.weight"]), t(P["layer_norm.bias"]), 1e-5)
+    tri = F.linear(xn, t(P["linear.weight"])).permute(0, 3, 1, 2)           # [B, H, Q, K]
+    heads = lambda a: a.reshape(2, N, N, nh, 4).permute(0, 1, 3, 2, 4)     # noqa: E731 [B, I, H, J, d]
+    q, k, v = (heads(F.linear(xn, t(P[f"mha.linear_{n}.weight"]))) for n in "qkv")
+    addm = inf * (t(ms) - 1)[:, :, None, None, :] + tri[:, None]
+    o = F.scaled_dot_product_attention(q, k, v, attn_mask=addm, scale=0.5)  # d = 4
+    o = o.permute(0, 1, 3, 2, 4).reshape(2, N, N, 8)
+    o = o * torch.sigmoid(F.linear(xn, t(P["mha.linear_g.weight"]), t(P["mha.linear_g.bias"])))
+    want = F.linear(o, t(P["mha.linear_o.weight"]), t(P["mha.linear_o.bias"])).numpy()
+    if not starting:
+        want = want.swapaxes(1, 2)
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-10)
+    # float32 literal arithmetic stays within the fp32 rounding of s - inf
+    got32 = pair_ops.tri_attn(x, m, P, starting, nh, inf=inf, dtype=np.float32)
+    np.testing.assert_allclose(got32, got, rtol=0, atol=4e-3 if inf > 100 else 1e-4)
+
+
+def test_fractional_mask_absorbed_default_inf():
+    """inf = 1e9 with fractional mask values: float64 uses the fp32-absorbed
+    score of every key with mask != 1; the float32 literal reference agrees,
+    also for a row whose keys are all fractional (the largest mask wins)."""
+    P = _ta_params(seed=43)
+    N = 6
+    x = H.pair_input(1, N, 16, seed=44).astype(F64)
+    m = np.ones((1, N, N), np.float32)
+    m[0, 0, :2] = 0.5
+    m[0, 3, :] = 0.0
+    m[0, 3, 4] = 0.75         # row 3: every key masked, key 4 the least
+    got = pair_ops.tri_attn(x, m, P, True, 2, dtype=F64)
+    np.testing.assert_allclose(brute.tri_attn(x, m, P, True, 2), got, rtol=0, atol=1e-11)
+    np.testing.assert_allclose(pair_ops.tri_attn(x, m, P, True, 2, dtype=np.float32), got,
+                               rtol=0, atol=1e-5)
+    # row 3 attends only to key 4: its output is that key's value path
+    xn = pair_ops.layer_norm(x[0, 3], P["layer_norm.weight"].astype(F64), P["layer_norm.bias"].astype(F64))
+    v = xn @ P["mha.linear_v.weight"].T.astype(F64)
+    o = np.broadcast_to(v[4], (N, 8)) * pair_ops.sigmoid(
+        xn @ P["mha.linear_g.weight"].T.astype(F64) + P["mha.linear_g.bias"])
+    np.testing.assert_allclose(got[0, 3], o @ P["mha.linear_o.weight"].T.astype(F64) + P["mha.linear_o.bias"],
+                               atol=1e-12)
+
+
+# ------------------------------------------------------- pair transition
+def test_pair_transition_matches_torch_and_loops():
+    """PairTransition (pair_transform.py:79-84): LayerNorm, linear_1, ReLU,
+    linear_2, against torch.nn.functional in float64 and the scalar loops."""
+    P = H.draw_params(H.pair_transition_shapes(16, 4), seed=45, ln_random=True, bias_random=True)
+    p = H.pair_input(2, 5, 16, seed=46).astype(F64) * 1.5 + 0.2
+    got = pair_ops.pair_transition(p, P, dtype=F64)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=F64))  # noqa: E731
+    h = F.linear(F.layer_norm(t(p), (16,), t(P["layer_norm.weight"]), t(P["layer_norm.bias"]), 1e-5),
+                 t(P["linear_1.weight"]), t(P["linear_1.bias"]))
+    want = F.linear(F.relu(h), t(P["linear_2.weight"]), t(P["linear_2.bias"])).numpy()
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-12)
+    np.testing.assert_allclose(brute.pair_transition(p, P), got, rtol=0, atol=1e-12)
+    # a good share of the hidden units is clipped by the ReLU, so dropping it shows
+    assert (h.numpy() < 0).mean() > 0.2
+
+
+def test_pair_block_matches_loops():
+    """PairTransformLayer in eval (pair_transform.py:180-193): the four
+    residual updates, the transition and the final mask, against the scalar
+    loops' composition, with a ragged mask (a row and a column fully masked)."""
+    P = H.draw_params(H.pair_layer_shapes(16, 8, 8, 2), seed=47, ln_random=True, bias_random=True)
+    p = H.pair_input(1, 5, 16, seed=48).astype(F64)
+    m = H.tail_mask(1, 5, [4])
+    got = pair_ops.pair_block(p, m, P, 2, dtype=F64)
+    np.testing.assert_allclose(brute.pair_block(p, m, P, 2), got, rtol=0, atol=1e-10)
+    assert np.all(got[0, 4] == 0) and np.all(got[0, :, 4] == 0)
+    assert np.abs(got[0, :4, :4]).min() > 0
+
+
 # ------------------------------------------------------- planted mistakes
 def test_planted_mistakes_are_detected(monkeypatch):
     """A transposed contraction operand, a dropped mask bias and a gate taken from
@@ -215,3 +306,19 @@ def test_planted_mistakes_are_detected(monkeypatch):
     ref_a = brute.tri_attn(x, ma, PA, True, 2)
     monkeypatch.setattr(pair_ops, "_masked_scores", lambda qk, km, tri, inf, dt: qk + tri)
     assert np.abs(pair_ops.tri_attn(x, ma, PA, True, 2, dtype=F64) - ref_a).max() > 1e-3
+    monkeypatch.undo()
+
+    # transition: the ReLU dropped, or the residual order changed
+    PT = H.draw_params(H.pair_transition_shapes(16, 4), seed=49, ln_random=True, bias_random=True)
+    pt = H.pair_input(1, 4, 16, seed=50).astype(F64)
+    ref_t = brute.pair_transition(pt, PT)
+    monkeypatch.setattr(pair_ops.np, "maximum", lambda a, b: a)
+    assert np.abs(pair_ops.pair_transition(pt, PT, dtype=F64) - ref_t).max() > 1e-3
+    monkeypatch.undo()
+    PB = H.draw_params(H.pair_layer_shapes(16, 8, 8, 2), seed=51, ln_random=True, bias_random=True)
+    pb = H.pair_input(1, 4, 16, seed=52).astype(F64)
+    mb = H.tail_mask(1, 4, [3])
+    ref_b = brute.pair_block(pb, mb, PB, 2)
+    orig_tm = pair_ops.tri_mul
+    monkeypatch.setattr(pair_ops, "tri_mul", lambda z, m, P, o, dt=np.float32, *a, **k: orig_tm(z, m, P, not o, dt))
+    assert np.abs(pair_ops.pair_block(pb, mb, PB, 2, dtype=F64) - ref_b).max() > 1e-3
