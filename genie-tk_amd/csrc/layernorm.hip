@@ -10,6 +10,7 @@
 // gtk_fused_layernorm_linear: the row is normalised in MFMA fragment layout
 // (see common.hpp) and multiplied with the packed weight on the matrix cores.
 #include <algorithm>
+#include <mutex>
 
 #include "capi_util.hpp"
 #include "common.hpp"
@@ -376,4 +377,66 @@ extern "C" int gtk_layernorm_linear(const void* x, void* y, const float* gamma, 
   }
   GTK_LAUNCH_CHECK();
   return GTK_OK;
+}
+
+// ---------------------------------------------------------------------------
+// No-allocation form of gtk_layernorm_linear.  The packed weight and the
+// folded bias (its only scratch) go into a file-scope device array instead of
+// a caller workspace; each GPU holds its own copy of the array for the life
+// of the process.  The array's name is a host-side stand-in in host code: its
+// device address is taken once per device with hipGetSymbolAddress and only
+// that address is handed to the kernels.  Every call on one GPU shares the
+// array, so calls that overlap on one GPU (different streams, or threads)
+// race; calls on one stream are ordered.  Each call rewrites every byte the
+// kernels read (the packing writes the padding too), so nothing carries over.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) char ln_linear_scratch[GTK_LAYERNORM_LINEAR_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_ln_scratch_mu;
+void* g_ln_scratch[kMaxScratchDevices] = {};  // device address of ln_linear_scratch, per device
+}  // namespace
+
+static int ln_linear_scratch_ptr(void** out) {
+  int dev = -1;
+  GTK_HIP_CHECK(hipGetDevice(&dev));
+  GTK_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, GTK_EUNSUPPORTED,
+              "gtk_layernorm_linear_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_ln_scratch_mu);
+  if (!g_ln_scratch[dev]) {
+    void* p = nullptr;
+    GTK_HIP_CHECK(hipGetSymbolAddress(&p, HIP_SYMBOL(ln_linear_scratch)));
+    GTK_REQUIRE(p != nullptr, GTK_EHIP, "gtk_layernorm_linear_noalloc: no scratch address");
+    g_ln_scratch[dev] = p;
+  }
+  *out = g_ln_scratch[dev];
+  return GTK_OK;
+}
+
+extern "C" int gtk_layernorm_linear_noalloc(const void* x, void* y, const float* gamma,
+                                            const float* beta, const void* weight,
+                                            int weight_dtype, int weight_layout, const float* bias,
+                                            int64_t rows, int64_t d_in, int64_t d_out, float eps,
+                                            int dtype, void* stream) {
+  GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL,
+              "gtk_layernorm_linear_noalloc: bad dtype %d", dtype);
+  GTK_REQUIRE(d_in == 64 || d_in == 128 || d_in == 256, GTK_EUNSUPPORTED,
+              "gtk_layernorm_linear_noalloc: d_in=%lld not in {64,128,256}", (long long)d_in);
+  GTK_REQUIRE(d_out >= 1 && d_out <= (1 << 16) && rows >= 0, GTK_EINVAL,
+              "gtk_layernorm_linear_noalloc: bad shape");
+  const size_t need = gtk_fused_layernorm_linear_workspace_size(d_in, d_out, dtype);
+  GTK_REQUIRE(need <= (size_t)GTK_LAYERNORM_LINEAR_SCRATCH_BYTES, GTK_EWORKSPACE,
+              "gtk_layernorm_linear_noalloc: d_in=%lld d_out=%lld needs %zu bytes of scratch, "
+              "more than the %zu-byte static array",
+              (long long)d_in, (long long)d_out, need, (size_t)GTK_LAYERNORM_LINEAR_SCRATCH_BYTES);
+  if (rows == 0) return GTK_OK;
+  GTK_REQUIRE(x && y && gamma && beta && weight, GTK_EINVAL,
+              "gtk_layernorm_linear_noalloc: null pointer");
+  void* scratch = nullptr;
+  int rc;
+  if ((rc = ln_linear_scratch_ptr(&scratch))) return rc;
+  return gtk_layernorm_linear(x, y, gamma, beta, weight, weight_dtype, weight_layout, bias, rows,
+                              d_in, d_out, eps, dtype, scratch, GTK_LAYERNORM_LINEAR_SCRATCH_BYTES,
+                              stream);
 }

@@ -81,6 +81,24 @@ int gtk_layernorm_linear(const void* x, void* y, const float* gamma, const float
                          const float* bias, int64_t rows, int64_t d_in, int64_t d_out, float eps,
                          int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
+/* No-allocation form of gtk_layernorm_linear, for callers that cannot
+ * allocate device memory or pass a workspace (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid allocation).  It has no
+ * counterpart in the reference.  The scratch (the packed weight and the
+ * folded bias) lives in a static device array of
+ * GTK_LAYERNORM_LINEAR_SCRATCH_BYTES that each GPU holds until the process
+ * ends; shapes whose gtk_fused_layernorm_linear_workspace_size exceeds it are
+ * rejected with GTK_EWORKSPACE (bf16: d_in=128 up to d_out=4032, d_in=256 up
+ * to d_out=2016).  The call allocates nothing.  All calls on one GPU share
+ * the array: calls that overlap on one GPU (other streams or threads) race;
+ * calls on one stream are ordered.  Same arguments and result as
+ * gtk_layernorm_linear. */
+#define GTK_LAYERNORM_LINEAR_SCRATCH_BYTES (1u << 20)
+int gtk_layernorm_linear_noalloc(const void* x, void* y, const float* gamma, const float* beta,
+                                 const void* weight, int weight_dtype, int weight_layout,
+                                 const float* bias, int64_t rows, int64_t d_in, int64_t d_out,
+                                 float eps, int dtype, void* stream);
+
 /* ------------------------------------------------------------------------
  * Triangle contraction on already gated and masked projections.
  * Replaces _C.triangle_mul_outgoing / _C.triangle_mul_incoming(a, b, mask)

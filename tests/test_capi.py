@@ -67,6 +67,8 @@ def lib():
                                              vp, sz, vp]
     L.gtk_layernorm_linear.argtypes = [vp, vp, vp, vp, vp, ci, ci, vp, i64, i64, i64, fp, ci,
                                        vp, sz, vp]
+    L.gtk_layernorm_linear_noalloc.argtypes = [vp, vp, vp, vp, vp, ci, ci, vp, i64, i64, i64, fp,
+                                               ci, vp]
     L.gtk_timing_report.argtypes = [ctypes.c_char_p, sz]
     return L
 
@@ -181,6 +183,26 @@ def test_bad_dtype_and_shapes_are_rejected(lib):
     rc = lib.gtk_layernorm_linear(None, None, None, None, None, GTK_F32, 2, None, 4, 128, 8,
                                   1e-5, GTK_F32, None, 0, None)
     assert rc == GTK_EINVAL and "layout" in _err(lib)
+
+
+def test_noalloc_layernorm_linear_validation(lib):
+    """The no-allocation form checks its shape against the static scratch
+    before any HIP call: too large a packed weight is GTK_EWORKSPACE, an
+    empty input succeeds, a null pointer is GTK_EINVAL."""
+    rc = lib.gtk_layernorm_linear_noalloc(None, None, None, None, None, GTK_BF16, 1, None, 10,
+                                          256, 2017, 1e-5, GTK_BF16, None)
+    assert rc == GTK_EWORKSPACE and "static array" in _err(lib)
+    rc = lib.gtk_layernorm_linear_noalloc(None, None, None, None, None, GTK_F32, 1, None, 10,
+                                          256, 993, 1e-5, GTK_F32, None)
+    assert rc == GTK_EWORKSPACE
+    assert lib.gtk_layernorm_linear_noalloc(None, None, None, None, None, GTK_BF16, 1, None, 0,
+                                            256, 2016, 1e-5, GTK_BF16, None) == GTK_OK
+    rc = lib.gtk_layernorm_linear_noalloc(None, None, None, None, None, GTK_BF16, 1, None, 5,
+                                          128, 64, 1e-5, GTK_BF16, None)
+    assert rc == GTK_EINVAL and "null" in _err(lib)
+    rc = lib.gtk_layernorm_linear_noalloc(None, None, None, None, None, GTK_BF16, 1, None, 5,
+                                          96, 64, 1e-5, GTK_BF16, None)
+    assert rc == GTK_EUNSUPPORTED
 
 
 def test_empty_inputs_are_no_ops(lib):
