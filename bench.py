@@ -143,46 +143,107 @@ def event_time_ms(torch, fn, reps: int, warm: int = 2, flush=None) -> list:
     return out
 
 
-def cpu_baseline(N: int, seed: int = 0) -> dict:
-    """The numpy oracle (fp32) on the host, bounded sample of the same step."""
-    import numpy as np
-
-    from oracle import pair_ops
-    from tests import helpers as H
-
+def host_cpu() -> dict:
+    """CPU model and physical core count of this host (from /proc/cpuinfo)."""
+    model, cores = None, set()
+    phys = core = None
     try:
-        from threadpoolctl import threadpool_info
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and model is None:
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                elif not k and phys is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+    except OSError:  # pragma: no cover
+        pass
+    return {"model": model, "physical_cores": len(cores) or None}
 
-        threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
-    except Exception:  # pragma: no cover
-        threads = int(os.environ.get("OMP_NUM_THREADS", "1"))
-    z = H.pair_input(1, N, C_Z, seed)
-    m = np.ones((1, N, N), np.float32)
-    Pm = H.draw_params(H.tri_mul_shapes(C_Z, C_HID), 1, gate_bias=1.0, gate_keys=H.TRI_MUL_GATES)
-    Pa = H.draw_params(H.tri_attn_shapes(C_Z, HEADS * HEAD_DIM, HEADS), 3)
-    t0 = time.perf_counter()
-    pair_ops.tri_mul(z, m, Pm, True, dtype=np.float32)
-    t_mul = time.perf_counter() - t0
-    rows = list(range(0, N, 16))  # every 16th attention row: rows are independent problems
-    t0 = time.perf_counter()
-    pair_ops.tri_attn(z, m, Pa, True, HEADS, dtype=np.float32, rows=rows)
-    t_att = (time.perf_counter() - t0) * N / len(rows)
-    t0 = time.perf_counter()
-    pair_ops.layer_norm(z, np.ones(C_Z, np.float32), np.zeros(C_Z, np.float32))
-    t_ln = time.perf_counter() - t0
-    step_s = 2 * t_mul + 2 * t_att + t_ln
-    flops = 2 * sum(trimul_flops(N).values()) + 2 * sum(triattn_flops(N).values())
+
+def cpu_threads() -> int:
+    """torch threads for the CPU baseline: the CPUs this process may run on,
+    at most 16 (the host share of a one-GPU box)."""
+    return max(1, min(len(os.sched_getaffinity(0)), 16))
+
+
+def cpu_modules(torch, mods: dict) -> dict:
+    """fp32 host copies of the GPU modules (same weights), PyTorch path only."""
+    import copy
+
+    out = {}
+    for k, m in mods.items():
+        c = copy.deepcopy(m).to("cpu", torch.float32).eval()
+        c._fused_requested = False
+        out[k] = c
+    return out
+
+
+def cpu_time_ops(torch, cmods: dict, N: int, tail: int = 0, reps: int = 3,
+                 chunk: int = 64) -> dict:
+    """Median seconds (after one warmup) of each operator's PyTorch path in
+    fp32 on the host: tri-mul outgoing / incoming, tri-attn starting / ending
+    (attention rows chunked by `chunk`, result-identical), LayerNorm.  The
+    inputs are seeded; tail > 0 masks pairs past `tail`."""
+    import torch.nn.functional as F
+
+    g = torch.Generator().manual_seed(0)
+    z = torch.randn(1, N, N, C_Z, generator=g)
+    m = torch.ones(1, N, N)
+    if tail:
+        m[:, tail:, :] = 0
+        m[:, :, tail:] = 0
+    w, b = torch.ones(C_Z), torch.zeros(C_Z)
+    fns = {
+        "tri_mul_out": lambda: cmods["tri_mul_out"](z, m),
+        "tri_mul_in": lambda: cmods["tri_mul_in"](z, m),
+        "tri_att_start": lambda: cmods["tri_att_start"](z, m, chunk_size=chunk),
+        "tri_att_end": lambda: cmods["tri_att_end"](z, m, chunk_size=chunk),
+        "layernorm": lambda: F.layer_norm(z, (C_Z,), w, b, 1e-5),
+    }
+    out = {}
+    with torch.no_grad():
+        for k, f in fns.items():
+            f()
+            ts = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                f()
+                ts.append(time.perf_counter() - t0)
+            out[k] = statistics.median(ts)
+    return out
+
+
+def cpu_baseline(torch, mods: dict, N: int) -> dict:
+    """The reference's PyTorch fallback (the modules' _forward_pytorch, fp32)
+    on the host cores, for the same step: 1 warmup, median of 3 per operator."""
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    cmods = cpu_modules(torch, mods)
+    t = cpu_time_ops(torch, cmods, N)
+    step_s = sum(t.values())
+    flops = step_flops_of(trimul_flops(N), triattn_flops(N))
+    cpu = host_cpu()
     return {
         "value": round(flops / step_s / 1e12, 4),
         "unit": "TFLOP/s",
-        "cores": int(threads),
+        "cores": threads,
         "kind": "port",
-        "sample": (f"numpy fp32 oracle of the same step at N={N}: tri-mul outgoing full "
-                   f"({t_mul:.2f} s, counted for outgoing and incoming), tri-attn starting on "
-                   f"{len(rows)} of {N} rows ({t_att * len(rows) / N:.2f} s, scaled x{N // len(rows)}, "
-                   f"counted for starting and ending), LayerNorm full ({t_ln:.2f} s); "
-                   f"step {step_s:.1f} s"),
+        "sample": (f"the modules' PyTorch path (the reference fallback) in fp32 on the host, the "
+                   f"whole step at N={N}: each operator 1 warmup + median of 3 "
+                   f"(tri-attn rows in chunks of 64, result-identical); "
+                   + ", ".join(f"{k} {v:.3f} s" for k, v in t.items())
+                   + f"; {threads} torch threads (sched_getaffinity, at most 16) on "
+                   f"{cpu['model']} ({cpu['physical_cores']} physical cores)"),
         "ms_per_step": round(step_s * 1e3, 1),
+        "op_ms": {k: round(v * 1e3, 1) for k, v in t.items()},
+        "cpu_model": cpu["model"],
+        "physical_cores": cpu["physical_cores"],
     }
 
 
@@ -294,6 +355,88 @@ def summarize_traffic(fetch_csv: str, write_csv: str, N: int, copy_mib: int) -> 
     return 0
 
 
+def _short_name(name: str) -> str:
+    """Readable kernel name: demangled by c++filt when it is on PATH, template
+    arguments kept, parameter list dropped."""
+    if name.startswith("_Z"):
+        import shutil
+        import subprocess
+
+        if shutil.which("c++filt"):
+            name = subprocess.run(["c++filt", name], capture_output=True, text=True).stdout.strip() or name
+    if name.startswith("_ZN"):
+        # left mangled (a demangler without the bf16 type): the kernel's own
+        # name and its integer template arguments
+        import re
+
+        m = re.match(r"_ZN(?:3gtk)?(\d+)", name)
+        if m:
+            base = name[m.end():m.end() + int(m.group(1))]
+            rest = name[m.end() + int(m.group(1)):]
+            tmpl = rest[:rest.find("Ev")] if "Ev" in rest else ""
+            args = ["bf16" if t == "DF16b" else t for t in re.findall(r"Li(\d+)E|(DF16b)", tmpl) for t in t if t]
+            return f"{base}<{', '.join(args)}>" if args else base
+    return name.split("(")[0].replace("void ", "").replace("gtk::", "")
+
+
+def _pmc_by_kernel(path: str) -> dict:
+    """{short kernel name: {counter: [per-dispatch values]}} of a rocprofv3
+    counter_collection.csv (values summed over a dispatch's rows)."""
+    import csv
+
+    per = {}
+    with open(path) as fh:
+        for r in csv.DictReader(fh):
+            key = (r["Dispatch_Id"], r["Counter_Name"])
+            per.setdefault(key, [r["Kernel_Name"], 0.0])[1] += float(r["Counter_Value"])
+    out, names = {}, {}
+    for (_, ctr), (raw, v) in per.items():
+        name = names.setdefault(raw, _short_name(raw))
+        out.setdefault(name, {}).setdefault(ctr, []).append(v)
+    return out
+
+
+def summarize_pmc(mfma_csv: str, issue_csv: str, stats_csv: str, N: int) -> int:
+    """Markdown table of the matrix-core and VALU counters per product kernel
+    from two rocprofv3 --pmc passes over `bench.py --only-step` (pass 1:
+    MfmaUtil MfmaFlopsBF16 VALUBusy; pass 2: SQ_INSTS_VALU_TRANS_F32
+    SQ_INSTS_VALU SQ_INSTS_MFMA SQ_VALU_MFMA_BUSY_CYCLES
+    SQ_VALU_MFMA_COEXEC_CYCLES SQ_WAIT_INST_ANY SQ_WAVE_CYCLES SQ_BUSY_CYCLES)
+    and the kernel-trace stats of the same command (durations)."""
+    import csv
+
+    a, b = _pmc_by_kernel(mfma_csv), _pmc_by_kernel(issue_csv)
+    dur = {}
+    for r in csv.DictReader(open(stats_csv)):
+        dur[_short_name(r["Name"])] = float(r["AverageNs"]) * 1e-9
+    work = dict(trimul_flops(N))
+    work.update(triattn_flops(N))
+    med = statistics.median
+    print("| kernel | avg us | MFMA GFLOP (counter) | algorithmic GFLOP | counter TFLOP/s | "
+          "% bf16 peak | MfmaUtil % | VALUBusy % | v_exp etc. (M lanes) | VALU instr (M) | "
+          "MFMA instr (M) | MFMA-VALU co-exec % of MFMA busy | wait % of wave cycles |")
+    print("|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|")
+    for name in sorted(a, key=lambda n: -dur.get(n, 0.0)):
+        key = _kernel_key(name)
+        ca, cb = a[name], b.get(name, {})
+        if "MfmaFlopsBF16" not in ca or name not in dur:
+            continue
+        fl = med(ca["MfmaFlopsBF16"])
+        t = dur[name]
+        alg = work.get(key)
+        busy = med(cb["SQ_VALU_MFMA_BUSY_CYCLES"]) if "SQ_VALU_MFMA_BUSY_CYCLES" in cb else 0.0
+        coex = med(cb["SQ_VALU_MFMA_COEXEC_CYCLES"]) if "SQ_VALU_MFMA_COEXEC_CYCLES" in cb else 0.0
+        wait = (med(cb["SQ_WAIT_INST_ANY"]) / med(cb["SQ_WAVE_CYCLES"])
+                if cb.get("SQ_WAVE_CYCLES") and med(cb["SQ_WAVE_CYCLES"]) > 0 else float("nan"))
+        cell = lambda c, f=1e-6: f"{med(cb[c]) * f:.1f}" if c in cb else "—"  # noqa: E731
+        print(f"| {name} | {t * 1e6:.1f} | {fl / 1e9:.2f} | {alg / 1e9 if alg else float('nan'):.2f} | "
+              f"{fl / t / 1e12:.0f} | {100 * fl / t / PEAK_BF16_FLOPS:.1f} | {med(ca['MfmaUtil']):.1f} | "
+              f"{med(ca['VALUBusy']):.1f} | {med(cb['SQ_INSTS_VALU_TRANS_F32']) * 64e-6 if 'SQ_INSTS_VALU_TRANS_F32' in cb else float('nan'):.0f} | "
+              f"{cell('SQ_INSTS_VALU')} | {cell('SQ_INSTS_MFMA')} | "
+              f"{100 * coex / busy if busy else float('nan'):.1f} | {100 * wait:.1f} |")
+    return 0
+
+
 def summarize_stats(stats_csv: str) -> int:
     """Markdown table of a rocprofv3 --kernel-trace --stats kernel_stats.csv
     (durations in microseconds per launch)."""
@@ -304,10 +447,152 @@ def summarize_stats(stats_csv: str) -> int:
     print("| kernel | calls | avg us | min us | max us | % of GPU time |")
     print("|---|---:|---:|---:|---:|---:|")
     for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"])):
-        name = r["Name"]
-        short = name.split("(")[0].replace("void ", "").replace("gtk::", "")
+        short = _short_name(r["Name"])
         print(f"| {short} | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | {float(r['MinNs']) / 1e3:.1f} | "
               f"{float(r['MaxNs']) / 1e3:.1f} | {100 * float(r['TotalDurationNs']) / total:.2f} |")
+    return 0
+
+
+def op_targets(N: int) -> dict:
+    """ms of each operator at the targets: 50 % of bf16 MFMA peak for the
+    triangle operators, 70 % of HBM for LayerNorm."""
+    fm, fa = sum(trimul_flops(N).values()), sum(triattn_flops(N).values())
+    return {"tri_mul": fm / (0.5 * PEAK_BF16_FLOPS) * 1e3, "tri_att": fa / (0.5 * PEAK_BF16_FLOPS) * 1e3,
+            "layernorm": ln_bytes(N) / (0.7 * PEAK_HBM_BYTES) * 1e3}
+
+
+def gpu_ops_at(torch, C, dev: str, N: int, tail: int, reps: int) -> dict:
+    """Median event time of each operator (bf16, module kernel path) at size N,
+    with the pair mask zero past `tail` (0: all ones); TFLOP/s or GB/s, and the
+    fraction of the target time."""
+    mods = build_modules(torch, N, dev)
+    g = torch.Generator(device=dev).manual_seed(N)
+    z = torch.randn(1, N, N, C_Z, device=dev, generator=g).to(torch.bfloat16)
+    m = torch.ones(1, N, N, device=dev)
+    if tail:
+        m[:, tail:, :] = 0
+        m[:, :, tail:] = 0
+    w, b = torch.ones(C_Z, device=dev), torch.zeros(C_Z, device=dev)
+    tg = op_targets(N)
+    out = {"N": N, "mask": f"pairs with i, j < {tail}" if tail else "ones"}
+    with torch.no_grad():
+        for k in ("tri_mul_out", "tri_mul_in", "tri_att_start", "tri_att_end"):
+            ms = statistics.median(event_time_ms(torch, lambda: mods[k](z, m), reps))
+            fl = sum((trimul_flops if k.startswith("tri_mul") else triattn_flops)(N).values())
+            t = tg["tri_mul" if k.startswith("tri_mul") else "tri_att"]
+            out[k] = {"ms": round(ms, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
+                      "frac_bf16_peak": round(fl / (ms * 1e-3) / PEAK_BF16_FLOPS, 4),
+                      "target_ms": round(t, 4), "time_over_target": round(ms / t, 2)}
+        ms = statistics.median(event_time_ms(torch, lambda: C.layernorm(z, w, b, 1e-5), reps))
+        out["layernorm"] = {"ms": round(ms, 4), "gbps": round(ln_bytes(N) / (ms * 1e-3) / 1e9, 1),
+                            "frac_hbm": round(ln_bytes(N) / (ms * 1e-3) / PEAK_HBM_BYTES, 4),
+                            "target_ms": round(tg["layernorm"], 4)}
+    del mods, z
+    torch.cuda.synchronize()
+    return out
+
+
+def config_table(torch, C, dev: str) -> int:
+    """GPU (bf16 kernels, fp32 for config 1) and host-CPU (the PyTorch fallback
+    in fp32) times of the operators at the benchmark configurations:
+    1: tri-mul outgoing, fp32, N=64; 2: tri-mul outgoing / incoming, N=256,
+    mask i, j < 224; 3: tri-attn starting / ending, same; 4: the pair-stack
+    block (LN-free PairTransformLayer order: tri-mul out, in, tri-attn start,
+    end, transition, each with residual, then the mask), B=2, N=512, lengths
+    384 and 512; 5: tri-mul outgoing, tri-attn starting and LayerNorm,
+    N=1024."""
+    import torch.nn.functional as F
+
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    cpu = host_cpu()
+    rows = []
+
+    def gpu_ms(fn, reps=10):
+        with torch.no_grad():
+            return statistics.median(event_time_ms(torch, fn, reps))
+
+    def cpu_ms(fn, reps=3):
+        with torch.no_grad():
+            fn()
+            ts = []
+            for _ in range(reps):
+                t0 = time.perf_counter()
+                fn()
+                ts.append(time.perf_counter() - t0)
+        return statistics.median(ts) * 1e3
+
+    def mask(B, N, lengths):
+        m = torch.zeros(B, N, N)
+        for i, L in enumerate(lengths):
+            m[i, :L, :L] = 1
+        return m
+
+    def add(cfg, op, N, gms, cms, gflop=None, mb=None):
+        perf = (f"{gflop / gms:.0f} TFLOP/s ({100 * gflop * 1e9 / (gms * 1e-3) / PEAK_BF16_FLOPS:.1f} %)"
+                if gflop else f"{mb * 1e6 / (gms * 1e-3) / 1e9:.0f} GB/s "
+                              f"({100 * mb * 1e6 / (gms * 1e-3) / PEAK_HBM_BYTES:.1f} % HBM)")
+        rows.append(f"| {cfg} | {op} | {N} | {cms:.1f} | {gms:.4f} | {cms / gms:.0f}x | {perf} |")
+        print(f"[config-table] {cfg} {op}: GPU {gms:.4f} ms, CPU {cms:.1f} ms", file=sys.stderr, flush=True)
+
+    for n_cfg, N, lengths, ops in ((1, 64, None, ("tri_mul_out",)),
+                                   (2, 256, [224], ("tri_mul_out", "tri_mul_in")),
+                                   (3, 256, [224], ("tri_att_start", "tri_att_end")),
+                                   (5, 1024, None, ("tri_mul_out", "tri_att_start"))):
+        mods = build_modules(torch, N, dev)
+        dt = torch.float32 if n_cfg == 1 else torch.bfloat16
+        if n_cfg == 1:
+            mods = {k: v.float() for k, v in mods.items()}
+        cm = cpu_modules(torch, mods)
+        g = torch.Generator().manual_seed(n_cfg)
+        zc = torch.randn(1, N, N, C_Z, generator=g)
+        mc = mask(1, N, lengths) if lengths else torch.ones(1, N, N)
+        zg, mg = zc.to(dev, dt), mc.to(dev)
+        for op in ops:
+            chunk = {"chunk_size": 64} if op.startswith("tri_att") else {}
+            gms = gpu_ms(lambda: mods[op](zg, mg))
+            cms = cpu_ms(lambda: cm[op](zc, mc, **chunk))
+            fl = sum((trimul_flops if op.startswith("tri_mul") else triattn_flops)(N).values())
+            add(n_cfg, op, N, gms, cms, gflop=fl / 1e9)
+        if n_cfg == 5:
+            w, b = torch.ones(C_Z), torch.zeros(C_Z)
+            gms = gpu_ms(lambda: C.layernorm(zg, w.to(dev), b.to(dev), 1e-5))
+            cms = cpu_ms(lambda: F.layer_norm(zc, (C_Z,), w, b, 1e-5))
+            add(5, "layernorm", N, gms, cms, mb=ln_bytes(N) / 1e6)
+        del mods, cm, zg
+        torch.cuda.synchronize()
+    # config 4: the pair-stack block, B = 2, N = 512, lengths 384 and 512
+    layer = build_pair_layer(torch, dev)
+    cl = copy_layer = cpu_modules(torch, {"l": layer})["l"]
+    for mod in cl.modules():
+        if hasattr(mod, "_fused_requested"):
+            mod._fused_requested = False
+    g = torch.Generator().manual_seed(4)
+    zc = torch.randn(2, 512, 512, C_Z, generator=g)
+    mc = mask(2, 512, [384, 512])
+    zg, mg = zc.to(dev, torch.bfloat16), mc.to(dev)
+
+    def cpu_block():
+        p = zc
+        p = p + cl.tri_mul_out(p, mc)
+        p = p + cl.tri_mul_in(p, mc)
+        p = p + cl.tri_att_start(p, mc, chunk_size=64)
+        p = p + cl.tri_att_end(p, mc, chunk_size=64)
+        p = p + cl.pair_transition(p, mc)
+        return p * mc.unsqueeze(-1)
+
+    gms = gpu_ms(lambda: layer((zg, mg)))
+    cms = cpu_ms(cpu_block, reps=1)
+    fl = 2 * (step_flops_of(trimul_flops(512), triattn_flops(512)) + transition_flops(512))
+    add(4, "pair-stack block (B=2)", 512, gms, cms, gflop=fl / 1e9)
+    del layer, copy_layer
+    print(f"Host CPU: {cpu['model']}, {cpu['physical_cores']} physical cores; {threads} torch "
+          f"threads. CPU: the modules' PyTorch path in fp32 (tri-attn rows in chunks of 64), "
+          f"1 warmup + median of 3 (config 4: 1 warmup + 1). GPU: bf16 kernels (config 1: "
+          f"fp32), median of 10 event-timed calls.\n")
+    print("| config | operator | N | CPU fp32 ms | GPU ms | speed-up | GPU throughput |")
+    print("|---|---|---:|---:|---:|---:|---|")
+    print("\n".join(rows))
     return 0
 
 
@@ -327,11 +612,21 @@ def main() -> int:
                          "--calibrate-copy) into profiles/traffic.json")
     ap.add_argument("--summarize-stats", metavar="STATS_CSV",
                     help="no run: markdown table of a rocprofv3 kernel_stats.csv")
+    ap.add_argument("--summarize-pmc", nargs=3, metavar=("MFMA_CSV", "ISSUE_CSV", "STATS_CSV"),
+                    help="no run: matrix-core / VALU counter table of two --pmc passes and the "
+                         "kernel-trace stats of `bench.py --only-step`")
+    ap.add_argument("--only-step", action="store_true",
+                    help="time the step and its kernels only (for counter collection)")
+    ap.add_argument("--config-table", action="store_true",
+                    help="no bench line: GPU and host-CPU times of the operators at the "
+                         "benchmark configurations 1-5, as a markdown table")
     args = ap.parse_args()
     if args.summarize_traffic:
         return summarize_traffic(*args.summarize_traffic, N=args.n, copy_mib=args.calibrate_copy)
     if args.summarize_stats:
         return summarize_stats(args.summarize_stats)
+    if args.summarize_pmc:
+        return summarize_pmc(*args.summarize_pmc, N=args.n)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the path has no multi-GPU implementation)", file=sys.stderr)
@@ -344,6 +639,8 @@ def main() -> int:
     C = _ext.require()
     dev = "cuda:0"
     torch.cuda.set_device(0)
+    if args.config_table:
+        return config_table(torch, C, dev)
     N = args.n
     torch.manual_seed(0)
     z = torch.randn(1, N, N, C_Z, device=dev).to(torch.bfloat16)
@@ -386,6 +683,17 @@ def main() -> int:
             step()
         rep = C.timing_report()
         C.timing_enable(False)
+        if args.only_step:
+            torch.cuda.synchronize()
+            print(json.dumps({"ms_per_step": round(step_ms, 4),
+                              "op_ms": {k: round(v, 4) for k, v in op_ms.items()},
+                              "kernels": {k: round(v[1] / v[0], 4) for k, v in rep.items()}}))
+            return 0
+        # the operators at the other benchmark sizes: N = 256 (tail mask at
+        # 224, configs 2 and 3) and N = 1024 (mask ones, config 5)
+        print("[bench] operators at N=256 and N=1024", file=sys.stderr, flush=True)
+        sizes = {f"n{n}": gpu_ops_at(torch, C, dev, n, tail, reps)
+                 for n, tail in ((256, 224), (2 * N, 0))}
 
         # LayerNorm bandwidth with the 256 MiB MALL flushed before every launch
         # cold launches: reading a 1 GiB buffer first evicts the 256 MiB MALL with
@@ -573,8 +881,8 @@ def main() -> int:
     step_flops = sum(op_flops.values())
     cpu = None
     if not args.no_cpu:
-        print("[bench] CPU baseline (numpy oracle)", file=sys.stderr, flush=True)
-        cpu = cpu_baseline(N)
+        print("[bench] CPU baseline (PyTorch fallback, fp32, host cores)", file=sys.stderr, flush=True)
+        cpu = cpu_baseline(torch, mods, N)
     out = {
         "metric": METRIC,
         "value": round(step_flops / (step_ms * 1e-3) / 1e12, 2),
@@ -592,6 +900,7 @@ def main() -> int:
                    "B": 1, "N": N, "c_z": C_Z, "c_hidden_mul": C_HID, "heads": HEADS,
                    "head_dim": HEAD_DIM, "parallelism": "single GPU"},
         "ops": per_op,
+        "ops_other_sizes": sizes,
         "kernels": kernels,
         "roofline": roofline,
         "cpu_baseline": cpu,
