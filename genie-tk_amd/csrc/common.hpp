@@ -208,6 +208,26 @@ __device__ __forceinline__ void ln_to_frags(Frag<T>* frags, const RowHalf<C>& r,
   }
 }
 
+// Normalise and apply the LayerNorm affine (gamma, beta: fp32 [C]) before the
+// conversion to the fragment type: one rounding of the LayerNorm output, for
+// linear maps packed without the affine folded in.
+template <typename T, int C>
+__device__ __forceinline__ void ln_affine_to_frags(Frag<T>* frags, const RowHalf<C>& r, f32x2 st,
+                                                   const float* __restrict__ gamma,
+                                                   const float* __restrict__ beta) {
+  const int c0 = ((threadIdx.x & 63) >> 5) * (C / 2);  // this lane's channel half
+#pragma unroll
+  for (int ch = 0; ch < C / 16; ++ch) {
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int c = c0 + ch * 8 + e;
+      f[e] = (r.v[ch * 8 + e] - st[0]) * st[1] * gamma[c] + beta[c];
+    }
+    frags[ch].set(f);
+  }
+}
+
 // Row-tile LayerNorm (normalise only) straight from bf16 storage into bf16
 // fragments: the raw
 // half row stays packed (C/4 VGPRs) and is widened on the fly, so the peak

@@ -11,6 +11,18 @@
 
 namespace gtk {
 
+// Grouped padding of one dimension: padded index i is element (i / gp) * g +
+// (i % gp) of the source, or zero when i % gp >= g.  Multi-head attention
+// pads each head of g channels to gp; {kNoPad, kNoPad} is the identity.
+constexpr int kNoPad = 1 << 30;
+struct Pad {
+  int gp = kNoPad, g = kNoPad;
+  __host__ __device__ __forceinline__ int src(int i) const {
+    const int q = i / gp, r = i - q * gp;
+    return r < g ? q * g + r : -1;
+  }
+};
+
 inline int64_t packed_elems(int64_t out_dim, int64_t k_dim) {
   return ((out_dim + 31) / 32) * (k_dim / 16) * 512;
 }
@@ -20,7 +32,8 @@ inline int64_t packed_elems(int64_t out_dim, int64_t k_dim) {
 template <typename Tout, typename Tin>
 __global__ void pack_weight_kernel(Tout* __restrict__ dst, const Tin* __restrict__ src, int out_dim,
                                    int k_dim, int64_t s_out, int64_t s_in, float scale,
-                                   const float* __restrict__ gamma, int64_t total) {
+                                   const float* __restrict__ gamma, int64_t total, Pad pout,
+                                   Pad pk) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= total) return;
   const int kch = k_dim / 16;
@@ -32,7 +45,9 @@ __global__ void pack_weight_kernel(Tout* __restrict__ dst, const Tin* __restrict
   const int o = nt * 32 + (l & 31);
   const int k = (l >> 5) * (k_dim / 2) + ks * 8 + e;
   float v = 0.f;
-  if (o < out_dim) v = scale * to_f32(src[o * s_out + k * s_in]) * (gamma ? gamma[k] : 1.f);
+  const int os = pout.src(o), ksrc = pk.src(k);
+  if (o < out_dim && os >= 0 && ksrc >= 0)
+    v = scale * to_f32(src[os * s_out + ksrc * s_in]) * (gamma ? gamma[ksrc] : 1.f);
   dst[idx] = cvt<Tout>(v);
 }
 
@@ -42,14 +57,19 @@ template <typename Tin>
 __global__ void fold_bias_kernel(float* __restrict__ dst, const Tin* __restrict__ w,
                                  const void* __restrict__ bias, int bias_bf16,
                                  const float* __restrict__ beta, int out_dim, int k_dim,
-                                 int64_t s_out, int64_t s_in, float scale) {
-  const int o = blockIdx.x * blockDim.x + threadIdx.x;
-  if (o >= out_dim) return;
+                                 int64_t s_out, int64_t s_in, float scale, Pad pout) {
+  const int op = blockIdx.x * blockDim.x + threadIdx.x;
+  if (op >= out_dim) return;
+  const int o = pout.src(op);
+  if (o < 0) {
+    dst[op] = 0.f;
+    return;
+  }
   float acc = 0.f;
   if (bias) acc = bias_bf16 ? (float)((const bf16*)bias)[o] : ((const float*)bias)[o];
   if (beta)
     for (int k = 0; k < k_dim; ++k) acc += to_f32(w[o * s_out + k * s_in]) * beta[k];
-  dst[o] = scale * acc;
+  dst[op] = scale * acc;
 }
 
 template <typename Tin>
@@ -64,15 +84,15 @@ __global__ void to_f32_kernel(float* __restrict__ dst, const Tin* __restrict__ s
 template <typename Tout>
 inline int launch_pack(Tout* dst, const void* src, int wdtype, int out_dim, int k_dim,
                        int64_t s_out, int64_t s_in, float scale, hipStream_t st,
-                       const float* gamma = nullptr) {
+                       const float* gamma = nullptr, Pad pout = Pad(), Pad pk = Pad()) {
   const int64_t total = packed_elems(out_dim, k_dim);
   const int blocks = (int)((total + 255) / 256);
   if (wdtype == GTK_F32)
     pack_weight_kernel<Tout, float><<<blocks, 256, 0, st>>>(dst, (const float*)src, out_dim, k_dim,
-                                                            s_out, s_in, scale, gamma, total);
+                                                            s_out, s_in, scale, gamma, total, pout, pk);
   else
     pack_weight_kernel<Tout, bf16><<<blocks, 256, 0, st>>>(dst, (const bf16*)src, out_dim, k_dim,
-                                                           s_out, s_in, scale, gamma, total);
+                                                           s_out, s_in, scale, gamma, total, pout, pk);
   GTK_LAUNCH_CHECK();
   return GTK_OK;
 }
@@ -81,14 +101,14 @@ inline int launch_pack(Tout* dst, const void* src, int wdtype, int out_dim, int 
 // `bias` has the weights' element type, or is null.
 inline int launch_fold_bias(float* dst, const void* w, const void* bias, int wdtype,
                             const float* beta, int out_dim, int k_dim, int64_t s_out, int64_t s_in,
-                            float scale, hipStream_t st) {
+                            float scale, hipStream_t st, Pad pout = Pad()) {
   const int blocks = (out_dim + 63) / 64;
   if (wdtype == GTK_F32)
     fold_bias_kernel<float><<<blocks, 64, 0, st>>>(dst, (const float*)w, bias, 0, beta, out_dim,
-                                                    k_dim, s_out, s_in, scale);
+                                                    k_dim, s_out, s_in, scale, pout);
   else
     fold_bias_kernel<bf16><<<blocks, 64, 0, st>>>(dst, (const bf16*)w, bias, 1, beta, out_dim,
-                                                   k_dim, s_out, s_in, scale);
+                                                   k_dim, s_out, s_in, scale, pout);
   GTK_LAUNCH_CHECK();
   return GTK_OK;
 }

@@ -45,6 +45,10 @@ constexpr int MAXN = 8192;  // largest N of the attention entry points
 // + c); w_q and b_q also carry log2(e)/sqrt(d), w_b and b_b carry log2(e), so
 // that the softmax runs on exp2; w_g and b_g carry -log2(e) (gate = 1 /
 // (1 + 2^u)).  ln_* are fp32 copies used while packing.
+// Every head is padded to HD = 32 channels (c_h -> H * HD): a head of d < 32
+// channels gets zero weight rows in w_q/w_k/w_v/w_g (zero biases) and zero
+// input columns in w_o, so its padded q, k and v channels are exactly zero
+// (q.k and P V are unchanged) and its padded gate channels multiply zeros.
 template <typename T> struct TriAttnPacked {
   T *w_q, *w_k, *w_v, *w_g, *w_b, *w_o;
   float *b_q, *b_k, *b_v, *b_g, *b_b, *b_o;
@@ -52,7 +56,8 @@ template <typename T> struct TriAttnPacked {
 };
 
 template <typename T>
-static TriAttnPacked<T> carve_triattn(Carve& cv, int cin, int ch, int H) {
+static TriAttnPacked<T> carve_triattn(Carve& cv, int cin, int /*ch*/, int H) {
+  const int ch = H * HD;  // padded heads
   TriAttnPacked<T> p;
   p.w_q = cv.take<T>(packed_elems(ch, cin));
   p.w_k = cv.take<T>(packed_elems(ch, cin));
@@ -127,9 +132,13 @@ __host__ __device__ __forceinline__ int vt_pos(int j) {
   return (j & ~15) | (j & 3) | ((j & 4) << 1) | ((j & 8) >> 1);
 }
 
-// rows = 0: every row (Np); otherwise a chunk of that many rows.
+// rows = 0: every row (Np); otherwise a chunk of that many rows.  ch: the
+// gate's channels (0: none, the raw op); fast: the bf16 module kernels
+// (c_in = 128, H = 4), whose (row, head) flash path at Np <= kFlashRhMaxNp
+// keeps the bias in fp32 fragment order and writes og.
 template <typename T>
-static AttnWs<T> carve_attn_ws(Carve& cv, int64_t B, int64_t Np, int H, int ch, int64_t rows = 0) {
+static AttnWs<T> carve_attn_ws(Carve& cv, int64_t B, int64_t Np, int H, int ch, int64_t rows = 0,
+                               bool fast = true) {
   AttnWs<T> w;
   w.rows = rows > 0 ? rows : Np;
   w.r0 = 0;
@@ -138,7 +147,7 @@ static AttnWs<T> carve_attn_ws(Carve& cv, int64_t B, int64_t Np, int H, int ch, 
   w.k = cv.take<T>(qkv);
   w.vt = cv.take<T>(qkv);
   w.gate = cv.take<T>(ch > 0 ? B * w.rows * Np * ch : 0);
-  const bool rh = ch > 0 && sizeof(T) == 2 && Np <= kFlashRhMaxNp;
+  const bool rh = fast && ch > 0 && sizeof(T) == 2 && Np <= kFlashRhMaxNp;
   w.bias = rh ? nullptr : cv.take<T>(B * H * Np * Np);
   w.og = rh ? cv.take<T>(B * w.rows * Np * ch) : nullptr;
   w.biasf = rh ? cv.take<float>(B * H * Np * Np) : nullptr;
@@ -1566,24 +1575,30 @@ static int pack_triattn(const gtk_tri_attn_weights* w, int cin, int ch, int H, v
   Carve cv(packed, SIZE_MAX);
   TriAttnPacked<T> p = carve_triattn<T>(cv, cin, ch, H);
   const int wd = w->dtype;
-  const float qscale = kLog2e / sqrtf((float)(ch / H));
+  const int d = ch / H;           // channels of a head
+  const int chp = H * HD;         // padded to HD per head
+  Pad heads;
+  heads.gp = HD;
+  heads.g = d;
+  const float qscale = kLog2e / sqrtf((float)d);
   int rc;
   if ((rc = launch_to_f32(p.ln_w, w->ln_w, wd, cin, 1.f, 1.f, st))) return rc;
   if ((rc = launch_to_f32(p.ln_b, w->ln_b, wd, cin, 1.f, 0.f, st))) return rc;
   // nn.Linear weight [out][in]: s_out = in, s_in = 1.  Linears after the LayerNorm.
-  struct Lin { T* dst; float* bdst; const void* wsrc; const void* bsrc; int out; float scale; };
-  const Lin lins[5] = {{p.w_q, p.b_q, w->q_w, nullptr, ch, qscale},
-                       {p.w_k, p.b_k, w->k_w, nullptr, ch, 1.f},
-                       {p.w_v, p.b_v, w->v_w, nullptr, ch, 1.f},
-                       {p.w_g, p.b_g, w->g_w, w->g_b, ch, -kLog2e},
-                       {p.w_b, p.b_b, w->tri_w, nullptr, H, kLog2e}};
+  struct Lin { T* dst; float* bdst; const void* wsrc; const void* bsrc; int out; float scale; Pad pad; };
+  const Lin lins[5] = {{p.w_q, p.b_q, w->q_w, nullptr, chp, qscale, heads},
+                       {p.w_k, p.b_k, w->k_w, nullptr, chp, 1.f, heads},
+                       {p.w_v, p.b_v, w->v_w, nullptr, chp, 1.f, heads},
+                       {p.w_g, p.b_g, w->g_w, w->g_b, chp, -kLog2e, heads},
+                       {p.w_b, p.b_b, w->tri_w, nullptr, H, kLog2e, Pad()}};
   for (const Lin& l : lins) {
-    if ((rc = launch_pack<T>(l.dst, l.wsrc, wd, l.out, cin, cin, 1, l.scale, st, p.ln_w))) return rc;
-    if ((rc = launch_fold_bias(l.bdst, l.wsrc, l.bsrc, wd, p.ln_b, l.out, cin, cin, 1, l.scale, st)))
+    if ((rc = launch_pack<T>(l.dst, l.wsrc, wd, l.out, cin, cin, 1, l.scale, st, p.ln_w, l.pad))) return rc;
+    if ((rc = launch_fold_bias(l.bdst, l.wsrc, l.bsrc, wd, p.ln_b, l.out, cin, cin, 1, l.scale, st, l.pad)))
       return rc;
   }
-  // output projection acts on the gated attention output (no LayerNorm)
-  if ((rc = launch_pack<T>(p.w_o, w->o_w, wd, cin, ch, ch, 1, 1.f, st))) return rc;
+  // output projection acts on the gated attention output (no LayerNorm);
+  // its input channels are the padded heads
+  if ((rc = launch_pack<T>(p.w_o, w->o_w, wd, cin, chp, ch, 1, 1.f, st, nullptr, Pad(), heads))) return rc;
   if ((rc = launch_to_f32(p.b_o, w->o_b, wd, cin, 1.f, 0.f, st))) return rc;
   return GTK_OK;
 }
@@ -1598,16 +1613,17 @@ template <typename T, int CIN, int H>
 static int fwd_triattn(const void* x, const float* mask, void* out, const void* packed, int64_t B,
                        int64_t N, int starting, int residual, float eps, float inf, int64_t chunk_rows,
                        void* ws, hipStream_t st) {
-  constexpr int CH = H * HD;
+  constexpr int CH = H * HD;  // padded heads
+  constexpr bool kFast = sizeof(T) == 2 && CIN == 128 && H == 4;
   Carve pc((void*)packed, SIZE_MAX);
   TriAttnPacked<T> w = carve_triattn<T>(pc, CIN, CH, H);
   const int Np = (int)attn_pad(N);
-  const bool chunked = sizeof(T) == 2 && chunk_rows > 0 && chunk_rows < N;
+  const bool chunked = kFast && chunk_rows > 0 && chunk_rows < N;
   Carve cv(ws, SIZE_MAX);
-  AttnWs<T> a = carve_attn_ws<T>(cv, B, Np, H, CH, chunked ? chunk_rows : 0);
+  AttnWs<T> a = carve_attn_ws<T>(cv, B, Np, H, CH, chunked ? chunk_rows : 0, kFast);
   const int64_t blocks = B * N * ((N + 31) / 32);
   GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "attention grid too large");
-  if constexpr (sizeof(T) == 2) {
+  if constexpr (kFast) {
     constexpr int QT = 2;  // two 8-wave blocks of 64 queries per CU (Np > kFlashRhMaxNp)
     const bool rh = Np <= kFlashRhMaxNp;  // (row, head) flash path, fp32 bias
     auto prologue = [&](auto mode, int r0, int nrows) {
@@ -1685,8 +1701,29 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
   return GTK_OK;
 }
 
+// c_in in {32, 64, 128}, H in {1, 2, 4}, d = c_h / H in [1, 32] (heads are
+// padded to 32 channels); the bf16 kernels built for the module's headline
+// shape (c_in = 128, H = 4) run every d, the others run the generic kernels.
 static bool triattn_shape_ok(int64_t cin, int64_t ch, int64_t H) {
-  return cin == 128 && H == 4 && ch == H * HD;
+  return (cin == 32 || cin == 64 || cin == 128) && (H == 1 || H == 2 || H == 4) && ch >= H &&
+         ch % H == 0 && ch / H <= HD;
+}
+static bool triattn_fast_shape(int64_t cin, int64_t H) { return cin == 128 && H == 4; }
+
+template <typename T>
+static int fwd_triattn_any(int64_t cin, int64_t H, const void* x, const float* mask, void* out,
+                           const void* packed, int64_t B, int64_t N, int starting, int residual,
+                           float eps, float inf, int64_t chunk_rows, void* ws, hipStream_t st) {
+#define GTK_TA(C, HH)                                                                               \
+  if (cin == C && H == HH)                                                                       \
+    return fwd_triattn<T, C, HH>(x, mask, out, packed, B, N, starting, residual, eps, inf, chunk_rows, \
+                                 ws, st);
+  GTK_TA(128, 4) GTK_TA(128, 2) GTK_TA(128, 1)
+  GTK_TA(64, 4) GTK_TA(64, 2) GTK_TA(64, 1)
+  GTK_TA(32, 4) GTK_TA(32, 2) GTK_TA(32, 1)
+#undef GTK_TA
+  set_error("tri_attn: c_in=%lld H=%lld unsupported", (long long)cin, (long long)H);
+  return GTK_EUNSUPPORTED;
 }
 
 }  // namespace gtk
@@ -1733,7 +1770,8 @@ extern "C" int gtk_tri_attn_pack(const gtk_tri_attn_weights* w, int64_t c_in, in
   GTK_REQUIRE(w->dtype == GTK_F32 || w->dtype == GTK_BF16, GTK_EINVAL,
               "gtk_tri_attn_pack: bad weight dtype %d", w->dtype);
   GTK_REQUIRE(triattn_shape_ok(c_in, c_h, H), GTK_EUNSUPPORTED,
-              "gtk_tri_attn_pack: c_in=%lld c_h=%lld H=%lld unsupported (c_in=128, H=4, d=32)",
+              "gtk_tri_attn_pack: c_in=%lld c_h=%lld H=%lld unsupported (c_in in {32,64,128}, H in "
+              "{1,2,4}, c_h / H <= 32)",
               (long long)c_in, (long long)c_h, (long long)H);
   GTK_REQUIRE(w->q_w && w->k_w && w->v_w && w->g_w && w->o_w && w->tri_w, GTK_EINVAL,
               "gtk_tri_attn_pack: null weight");
@@ -1749,11 +1787,13 @@ extern "C" size_t gtk_tri_attn_workspace_size_chunked(int64_t B, int64_t N, int6
                                                       int64_t c_h, int64_t H, int64_t chunk_rows,
                                                       int dtype) {
   if (!triattn_shape_ok(c_in, c_h, H) || B < 0 || N < 0 || chunk_rows < 0) return 0;
-  if (chunk_rows > 0 && dtype != GTK_BF16) return 0;
+  const bool fast = dtype == GTK_BF16 && triattn_fast_shape(c_in, H);
+  if (chunk_rows > 0 && !fast) return 0;
   Carve cv(nullptr, SIZE_MAX);
   const int64_t rows = chunk_rows > 0 && chunk_rows < N ? chunk_rows : 0;
-  if (dtype == GTK_F32) carve_attn_ws<float>(cv, B, attn_pad(N), (int)H, (int)c_h);
-  else carve_attn_ws<bf16>(cv, B, attn_pad(N), (int)H, (int)c_h, rows);
+  const int chp = (int)H * HD;
+  if (dtype == GTK_F32) carve_attn_ws<float>(cv, B, attn_pad(N), (int)H, chp, 0, false);
+  else carve_attn_ws<bf16>(cv, B, attn_pad(N), (int)H, chp, rows, fast);
   return cv.off;
 }
 
@@ -1769,12 +1809,13 @@ extern "C" int gtk_tri_attn_forward_chunked(const void* x, const float* mask, vo
                                             void* ws, size_t ws_bytes, void* stream) {
   GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL, "gtk_tri_attn_forward: bad dtype %d", dtype);
   GTK_REQUIRE(triattn_shape_ok(c_in, c_h, H), GTK_EUNSUPPORTED,
-              "gtk_tri_attn_forward: c_in=%lld c_h=%lld H=%lld unsupported (c_in=128, H=4, d=32)",
+              "gtk_tri_attn_forward: c_in=%lld c_h=%lld H=%lld unsupported (c_in in {32,64,128}, "
+              "H in {1,2,4}, c_h / H <= 32)",
               (long long)c_in, (long long)c_h, (long long)H);
   GTK_REQUIRE(B >= 0 && N >= 0 && N <= 8192 && chunk_rows >= 0, GTK_EINVAL,
               "gtk_tri_attn_forward: bad shape");
-  GTK_REQUIRE(chunk_rows == 0 || dtype == GTK_BF16, GTK_EUNSUPPORTED,
-              "gtk_tri_attn_forward_chunked: row chunks need bf16");
+  GTK_REQUIRE(chunk_rows == 0 || (dtype == GTK_BF16 && triattn_fast_shape(c_in, H)), GTK_EUNSUPPORTED,
+              "gtk_tri_attn_forward_chunked: row chunks need bf16, c_in = 128 and H = 4");
   GTK_REQUIRE(abs_at_most(inf, 1e37f), GTK_EINVAL,
               "gtk_tri_attn_forward: |inf| must be at most 1e37, got %g", (double)inf);
   if (B == 0 || N == 0) return GTK_OK;
@@ -1784,9 +1825,10 @@ extern "C" int gtk_tri_attn_forward_chunked(const void* x, const float* mask, vo
               ws_bytes, need);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == GTK_F32)
-    return fwd_triattn<float, 128, 4>(x, mask, out, packed, B, N, starting, residual, eps, inf, 0, ws, st);
-  return fwd_triattn<bf16, 128, 4>(x, mask, out, packed, B, N, starting, residual, eps, inf,
-                                   chunk_rows, ws, st);
+    return fwd_triattn_any<float>(c_in, H, x, mask, out, packed, B, N, starting, residual, eps, inf, 0,
+                                  ws, st);
+  return fwd_triattn_any<bf16>(c_in, H, x, mask, out, packed, B, N, starting, residual, eps, inf,
+                               chunk_rows, ws, st);
 }
 
 extern "C" int gtk_tri_attn_forward(const void* x, const float* mask, void* out, const void* packed,

@@ -53,7 +53,8 @@ __global__ __launch_bounds__(256) void trimul_prologue_kernel(
   load_row_half<T, CZ>(rh, z + pair * CZ, valid);
   const f32x2 st = row_stats<CZ>(rh, eps);
   Frag<T> xf[CZ / 16];
-  ln_to_frags<T, CZ>(xf, rh, st);
+  if constexpr (trimul_folded<CZ, CH>()) ln_to_frags<T, CZ>(xf, rh, st);
+  else ln_affine_to_frags<T, CZ>(xf, rh, st, w.ln_in_w, w.ln_in_b);
   const float m = valid ? (mask ? mask[pair] : 1.0f) : 0.0f;
 
   const int64_t plane = (int64_t)Np * Np;
@@ -522,7 +523,8 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(
     load_row_half<T, CZ>(rh, z + pair * CZ, valid);
     const f32x2 st = row_stats<CZ>(rh, eps_in);
     Frag<T> xf[CZ / 16];
-    ln_to_frags<T, CZ>(xf, rh, st);
+    if constexpr (trimul_folded<CZ, CH>()) ln_to_frags<T, CZ>(xf, rh, st);
+    else ln_affine_to_frags<T, CZ>(xf, rh, st, w.ln_in_w, w.ln_in_b);
 #pragma unroll
     for (int nt = 0; nt < CZ / 32; ++nt) {
       gate[nt] = row_gemm_tile<T, CZ, true>(xf, w.w_g, nt);
@@ -569,7 +571,8 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(
   }
   const f32x2 st = row_stats<CH>(xh, eps_out);
   Frag<T> yf[CH / 16];
-  ln_to_frags<T, CH>(yf, xh, st);
+  if constexpr (trimul_folded<CZ, CH>()) ln_to_frags<T, CH>(yf, xh, st);
+  else ln_affine_to_frags<T, CH>(yf, xh, st, w.ln_out_w, w.ln_out_b);
 
 #pragma unroll
   for (int nt = 0; nt < CZ / 32; ++nt) {
@@ -934,13 +937,19 @@ static int pack_trimul(const gtk_tri_mul_weights* w, int cz, int c, void* packed
   // kernels evaluate sigmoid(x) as 1 / (1 + 2^u) with u = -log2(e) x.
   struct Lin { T* dst; float* bdst; const void* wsrc; const void* bsrc; int out, in; const float *g, *beta; float scale; };
   const float gs = -kLog2e;
+  // LayerNorm affine folded in, or left to the kernels (trimul_folded)
+  const bool fold = trimul_folded_rt(cz, c);
+  const float* gi = fold ? p.ln_in_w : nullptr;
+  const float* bi = fold ? p.ln_in_b : nullptr;
+  const float* go = fold ? p.ln_out_w : nullptr;
+  const float* bo = fold ? p.ln_out_b : nullptr;
   const Lin lins[6] = {
-      {p.w_ap, p.b_ap, w->a_p_w, w->a_p_b, c, cz, p.ln_in_w, p.ln_in_b, 1.f},
-      {p.w_ag, p.b_ag, w->a_g_w, w->a_g_b, c, cz, p.ln_in_w, p.ln_in_b, gs},
-      {p.w_bp, p.b_bp, w->b_p_w, w->b_p_b, c, cz, p.ln_in_w, p.ln_in_b, 1.f},
-      {p.w_bg, p.b_bg, w->b_g_w, w->b_g_b, c, cz, p.ln_in_w, p.ln_in_b, gs},
-      {p.w_g, p.b_g, w->g_w, w->g_b, cz, cz, p.ln_in_w, p.ln_in_b, gs},
-      {p.w_z, p.b_z, w->z_w, w->z_b, cz, c, p.ln_out_w, p.ln_out_b, 1.f}};
+      {p.w_ap, p.b_ap, w->a_p_w, w->a_p_b, c, cz, gi, bi, 1.f},
+      {p.w_ag, p.b_ag, w->a_g_w, w->a_g_b, c, cz, gi, bi, gs},
+      {p.w_bp, p.b_bp, w->b_p_w, w->b_p_b, c, cz, gi, bi, 1.f},
+      {p.w_bg, p.b_bg, w->b_g_w, w->b_g_b, c, cz, gi, bi, gs},
+      {p.w_g, p.b_g, w->g_w, w->g_b, cz, cz, gi, bi, gs},
+      {p.w_z, p.b_z, w->z_w, w->z_b, cz, c, go, bo, 1.f}};
   for (const Lin& l : lins) {
     if ((rc = launch_pack<T>(l.dst, l.wsrc, wd, l.out, l.in, l.in, 1, l.scale, st, l.g))) return rc;
     if ((rc = launch_fold_bias(l.bdst, l.wsrc, l.bsrc, wd, l.beta, l.out, l.in, l.in, 1, l.scale, st)))
@@ -949,12 +958,20 @@ static int pack_trimul(const gtk_tri_mul_weights* w, int cz, int c, void* packed
   return GTK_OK;
 }
 
+// The bf16 kernels with LDS-resident weights are built for the module's
+// shapes c_z = 128, c in {64, 128}; every other supported shape (c_z in {32,
+// 64, 128}, c in {32, 64, 128, 256}) and fp32 run the generic kernels.
+template <typename T, int CZ, int CH>
+constexpr bool trimul_fast() {
+  return sizeof(T) == 2 && CZ == 128 && (CH == 64 || CH == 128);
+}
+
 template <typename T, int CZ, int CH>
 static int launch_trimul_prologue(const void* z, const float* mask, const TriMulPacked<T>& w, T* pa,
                                   T* pb, int64_t B, int64_t N, int Np, int outgoing, float eps_in,
                                   hipStream_t st) {
   const int64_t ptiles = B * (int64_t)Np * (Np / 32);
-  if constexpr (sizeof(T) == 2) {
+  if constexpr (trimul_fast<T, CZ, CH>()) {
     const int grid = (int)std::min<int64_t>(device_cus(), (ptiles / 2 + 7) / 8);
     StageTimer timer("trimul_prologue", st);
     trimul_prologue_bf16_kernel<CZ, CH><<<grid, 512, 0, st>>>(
@@ -984,7 +1001,7 @@ static int fwd_trimul(const void* z, const float* mask, void* out, const void* p
   rc = launch_contract<T>(pa, pb, px, Np, B * CH, st);
   if (rc) return rc;
   const int64_t etiles = B * N * ((N + 31) / 32);
-  if constexpr (sizeof(T) == 2) {
+  if constexpr (trimul_fast<T, CZ, CH>()) {
     const int grid = (int)std::min<int64_t>(device_cus(), (etiles + 7) / 8);
     StageTimer timer("trimul_epilogue", st);
     trimul_epilogue_bf16_kernel<CZ, CH><<<grid, 512, 0, st>>>(
@@ -1051,7 +1068,25 @@ extern "C" int gtk_triangle_mul_incoming(const void* a, const void* b, const flo
   return raw_trimul(a, b, mask, x, B, N, C, dtype, ws, ws_bytes, stream, 0);
 }
 
-static bool trimul_shape_ok(int64_t cz, int64_t c) { return cz == 128 && (c == 64 || c == 128); }
+static bool trimul_shape_ok(int64_t cz, int64_t c) {
+  return (cz == 32 || cz == 64 || cz == 128) && (c == 32 || c == 64 || c == 128 || c == 256);
+}
+
+template <typename T>
+static int fwd_trimul_any(int64_t cz, int64_t c, const void* z, const float* mask, void* out,
+                          const void* packed, int64_t B, int64_t N, int outgoing, int residual,
+                          float eps_in, float eps_out, void* ws, hipStream_t st) {
+#define GTK_TM(CZ_, C_)                                                                          \
+  if (cz == CZ_ && c == C_)                                                                     \
+    return fwd_trimul<T, CZ_, C_>(z, mask, out, packed, B, N, outgoing, residual, eps_in, eps_out, \
+                                  ws, st);
+  GTK_TM(128, 128) GTK_TM(128, 64) GTK_TM(128, 32) GTK_TM(128, 256)
+  GTK_TM(64, 128) GTK_TM(64, 64) GTK_TM(64, 32) GTK_TM(64, 256)
+  GTK_TM(32, 128) GTK_TM(32, 64) GTK_TM(32, 32) GTK_TM(32, 256)
+#undef GTK_TM
+  set_error("tri-mul: c_z=%lld c=%lld unsupported", (long long)cz, (long long)c);
+  return GTK_EUNSUPPORTED;
+}
 
 extern "C" size_t gtk_tri_mul_packed_size(int64_t c_z, int64_t c, int dtype) {
   if (!trimul_shape_ok(c_z, c)) return 0;
@@ -1068,7 +1103,7 @@ extern "C" int gtk_tri_mul_pack(const gtk_tri_mul_weights* w, int64_t c_z, int64
   GTK_REQUIRE(w->dtype == GTK_F32 || w->dtype == GTK_BF16, GTK_EINVAL,
               "gtk_tri_mul_pack: bad weight dtype %d", w->dtype);
   GTK_REQUIRE(trimul_shape_ok(c_z, c), GTK_EUNSUPPORTED,
-              "gtk_tri_mul_pack: c_z=%lld c=%lld unsupported (c_z == 128, c in {64,128})",
+              "gtk_tri_mul_pack: c_z=%lld c=%lld unsupported (c_z in {32,64,128}, c in {32,64,128,256})",
               (long long)c_z, (long long)c);
   GTK_REQUIRE(w->a_p_w && w->a_g_w && w->b_p_w && w->b_g_w && w->g_w && w->z_w, GTK_EINVAL,
               "gtk_tri_mul_pack: null weight");
@@ -1092,7 +1127,7 @@ extern "C" int gtk_tri_mul_forward(const void* z, const float* mask, void* out, 
                                    size_t ws_bytes, void* stream) {
   GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL, "gtk_tri_mul_forward: bad dtype %d", dtype);
   GTK_REQUIRE(trimul_shape_ok(c_z, c), GTK_EUNSUPPORTED,
-              "gtk_tri_mul_forward: c_z=%lld c=%lld unsupported (c_z == 128, c in {64,128})",
+              "gtk_tri_mul_forward: c_z=%lld c=%lld unsupported (c_z in {32,64,128}, c in {32,64,128,256})",
               (long long)c_z, (long long)c);
   GTK_REQUIRE(B >= 0 && N >= 0 && N <= 16384, GTK_EINVAL, "gtk_tri_mul_forward: bad shape B=%lld N=%lld",
               (long long)B, (long long)N);
@@ -1102,10 +1137,9 @@ extern "C" int gtk_tri_mul_forward(const void* z, const float* mask, void* out, 
   GTK_REQUIRE(ws_bytes >= need, GTK_EWORKSPACE, "gtk_tri_mul_forward: workspace %zu < %zu bytes",
               ws_bytes, need);
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == GTK_F32) {
-    if (c == 128) return fwd_trimul<float, 128, 128>(z, mask, out, packed, B, N, outgoing, residual, eps_in, eps_out, ws, st);
-    return fwd_trimul<float, 128, 64>(z, mask, out, packed, B, N, outgoing, residual, eps_in, eps_out, ws, st);
-  }
-  if (c == 128) return fwd_trimul<bf16, 128, 128>(z, mask, out, packed, B, N, outgoing, residual, eps_in, eps_out, ws, st);
-  return fwd_trimul<bf16, 128, 64>(z, mask, out, packed, B, N, outgoing, residual, eps_in, eps_out, ws, st);
+  if (dtype == GTK_F32)
+    return fwd_trimul_any<float>(c_z, c, z, mask, out, packed, B, N, outgoing, residual, eps_in,
+                                 eps_out, ws, st);
+  return fwd_trimul_any<bf16>(c_z, c, z, mask, out, packed, B, N, outgoing, residual, eps_in,
+                              eps_out, ws, st);
 }

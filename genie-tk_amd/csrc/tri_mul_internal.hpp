@@ -8,9 +8,18 @@
 namespace gtk {
 
 // Packed parameters of one TriangleMultiplicativeUpdate, carved in this order.
-// The weights carry the LayerNorm weights folded in (w_ap..w_g: layer_norm_in,
-// w_z: layer_norm_out) and the biases the LayerNorm biases (b = W beta + c).
-// ln_* keep fp32 copies of the LayerNorm parameters, used only while packing.
+// For the shapes with backward kernels (c_z = 128, c in {64, 128}) the weights
+// carry the LayerNorm weights folded in (w_ap..w_g: layer_norm_in, w_z:
+// layer_norm_out) and the biases the LayerNorm biases (b = W beta + c); the
+// other shapes keep the plain weights and biases, and their kernels apply the
+// LayerNorm affine from the fp32 copies ln_* before rounding the normalised
+// row once (one bf16 rounding instead of two for the small channel counts).
+template <int CZ, int CH>
+constexpr bool trimul_folded() {
+  return CZ == 128 && (CH == 64 || CH == 128);
+}
+inline bool trimul_folded_rt(int cz, int c) { return cz == 128 && (c == 64 || c == 128); }
+
 template <typename T> struct TriMulPacked {
   T *w_ap, *w_ag, *w_bp, *w_bg, *w_g, *w_z;
   float *b_ap, *b_ag, *b_bp, *b_bg, *b_g, *b_z;

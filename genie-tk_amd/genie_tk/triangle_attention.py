@@ -120,10 +120,18 @@ class TriangleAttention(nn.Module):
 
     # -- HIP kernel path ----------------------------------------------------
     def _kernel_supported(self, x: Tensor) -> bool:
+        """Forward kernels: c_in in {32, 64, 128}, 1, 2 or 4 heads of at most
+        32 channels (the reference layer's default c_hidden=32 with 4 heads
+        is d=8)."""
+        h, ch = self.no_heads, self.c_hidden
         return (x.dim() >= 3 and x.shape[-2] == x.shape[-3] and x.shape[-1] == self.c_in
-                and self.c_in == 128 and self.no_heads == 4 and self.c_hidden == 128
-                and self.mha.gating and x.dtype in _dispatch.SUPPORTED_DTYPES
-                and self.layer_norm.elementwise_affine)
+                and self.c_in in (32, 64, 128) and h in (1, 2, 4) and ch % h == 0
+                and 1 <= ch // h <= 32 and self.mha.gating
+                and x.dtype in _dispatch.SUPPORTED_DTYPES and self.layer_norm.elementwise_affine)
+
+    def _headline_shape(self) -> bool:
+        """The shape the backward and row-chunk kernels are built for."""
+        return self.c_in == 128 and self.no_heads == 4 and self.c_hidden == 128
 
     def _pack(self, params, fp32: bool) -> Tensor:
         return _ext.require().tri_attn_pack(params, self.c_in, self.c_hidden, self.no_heads, fp32)
@@ -163,19 +171,21 @@ class TriangleAttention(nn.Module):
 
         ``chunk_size`` (an addition to the reference's signature, default off)
         bounds memory: the attention rows are processed that many at a time,
-        with the same result.  It applies to the bf16 kernel path and the
-        PyTorch path; an fp32 GPU input with ``chunk_size`` runs the PyTorch
-        path."""
+        with the same result.  It applies to the bf16 kernel path of the
+        c_in=128, 4-head, c_hidden=128 module and to the PyTorch path; other
+        GPU inputs with ``chunk_size`` run the PyTorch path."""
         if chunk_size is not None and chunk_size < 1:
             raise ValueError(f"chunk_size must be >= 1, got {chunk_size}")
         if x.is_cuda and self._fused_requested:
             if not _CUDA_AVAILABLE:
                 _ext.missing(type(self).__name__)
             elif (self.use_fused_kernel and self._kernel_supported(x)
-                    and (chunk_size is None or x.dtype == torch.bfloat16)):
+                    and (chunk_size is None
+                         or (x.dtype == torch.bfloat16 and self._headline_shape()))):
                 if not _dispatch.needs_autograd(x, self):
                     return self._forward_cuda(x, mask, chunk_size=chunk_size)
-                if self.inf == 1e9:  # the backward kernels' mask bias
+                # the backward kernels: the headline shape and inf = 1e9
+                if self.inf == 1e9 and self._headline_shape():
                     return _TriAttnFunction.apply(self, x, mask, chunk_size, *self._param_list())
         return self._forward_pytorch(x, mask, chunk_size)
 

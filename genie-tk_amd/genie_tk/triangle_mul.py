@@ -109,10 +109,15 @@ class TriangleMultiplicativeUpdate(nn.Module):
 
     # -- HIP kernel path ----------------------------------------------------
     def _kernel_supported(self, z: Tensor) -> bool:
+        """Forward kernels: c_z in {32, 64, 128}, c_hidden in {32, 64, 128, 256}."""
         return (z.dim() >= 3 and z.shape[-2] == z.shape[-3] and z.shape[-1] == self.c_z
-                and self.c_z == 128 and self.c_hidden in (64, 128)
+                and self.c_z in (32, 64, 128) and self.c_hidden in (32, 64, 128, 256)
                 and z.dtype in _dispatch.SUPPORTED_DTYPES
                 and self.layer_norm_in.elementwise_affine and self.layer_norm_out.elementwise_affine)
+
+    def _backward_supported(self) -> bool:
+        """The shapes the backward kernels are built for."""
+        return self.c_z == 128 and self.c_hidden in (64, 128)
 
     def _pack(self, params, fp32: bool) -> Tensor:
         return _ext.require().tri_mul_pack(params, self.c_z, self.c_hidden, fp32)
@@ -155,7 +160,8 @@ class TriangleMultiplicativeUpdate(nn.Module):
             elif self.use_fused_kernel and self._kernel_supported(z):
                 if not _dispatch.needs_autograd(z, self):
                     return self._forward_cuda(z, mask)
-                return _TriMulFunction.apply(self, z, mask, *self._param_list())
+                if self._backward_supported():
+                    return _TriMulFunction.apply(self, z, mask, *self._param_list())
         return self._forward_pytorch(z, mask)
 
 

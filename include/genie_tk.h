@@ -156,7 +156,8 @@ int gtk_triangle_attention_ending(const void* q, const void* k, const void* v, c
  *   x   = outgoing ? einsum(bikc,bjkc->bijc) : einsum(bkic,bkjc->bijc)
  *   out = (LN_out(x) W_z^T + b_z) * sigmoid(zn W_g^T + b_g)   [+ z if residual]
  * Weights are first packed once with gtk_tri_mul_pack (the packed buffer
- * stays valid until the parameters change).  c_z == 128, c in {64, 128},
+ * stays valid until the parameters change).  c_z in {32, 64, 128},
+ * c in {32, 64, 128, 256},
  * N <= 16384.
  * ------------------------------------------------------------------------ */
 typedef struct gtk_tri_mul_weights {
@@ -214,7 +215,8 @@ int gtk_tri_mul_backward(const void* z, const float* mask, const void* dy,
  * keys with mask == 1 take no bias, any other mask value (0 or fractional)
  * takes that bias, and a row whose keys all carry a bias follows the fp32
  * arithmetic of the reference (uniform attention for inf = 1e9 and mask 0).
- * |inf| <= 1e37.  c_in == 128, H == 4, d == 32 (c_h == 128), N <= 8192.
+ * |inf| <= 1e37.  c_in in {32, 64, 128}, H in {1, 2, 4}, head dim c_h / H in
+ * [1, 32] (the reference layer's default c_h = 32, H = 4 is d = 8), N <= 8192.
  * ------------------------------------------------------------------------ */
 typedef struct gtk_tri_attn_weights {
   int dtype;                 /* element type of every pointer below */
@@ -244,7 +246,7 @@ int gtk_tri_attn_forward(const void* x, const float* mask, void* out, const void
  * (src/genie_tk/utils.py:78-123), which its attention module imports
  * (triangle_attention.py:23) but never calls; there is no reference kernel.
  * chunk_rows = 0, or >= N, is the unchunked operator.  The workspace size
- * query takes the same chunk_rows. */
+ * query takes the same chunk_rows.  Row chunks need bf16, c_in = 128, H = 4. */
 size_t gtk_tri_attn_workspace_size_chunked(int64_t B, int64_t N, int64_t c_in, int64_t c_h,
                                            int64_t H, int64_t chunk_rows, int dtype);
 int gtk_tri_attn_forward_chunked(const void* x, const float* mask, void* out, const void* packed,

@@ -190,11 +190,23 @@ def test_cpu_host_switch():
     assert m._kernel_supported(torch.zeros(1, 4, 4, 128))
     assert not m._kernel_supported(torch.zeros(1, 4, 5, 128))
     assert not m._kernel_supported(torch.zeros(1, 4, 4, 128, dtype=torch.float16))
-    assert not TriangleMultiplicationOutgoing(64, 32)._kernel_supported(torch.zeros(1, 4, 4, 64))
+    # the reference tests' and layer's shapes have forward kernels
+    for cz, c in ((64, 32), (32, 32), (128, 256), (64, 64)):
+        assert TriangleMultiplicationOutgoing(cz, c)._kernel_supported(torch.zeros(1, 4, 4, cz))
+    assert not TriangleMultiplicationOutgoing(96, 32)._kernel_supported(torch.zeros(1, 4, 4, 96))
+    assert not TriangleMultiplicationOutgoing(64, 48)._kernel_supported(torch.zeros(1, 4, 4, 64))
+    assert TriangleMultiplicationOutgoing(128, 64)._backward_supported()
+    assert not TriangleMultiplicationOutgoing(64, 32)._backward_supported()
     a = TriangleAttentionEndingNode(128, 128, 4)
     assert a._kernel_supported(torch.zeros(2, 4, 4, 128, dtype=torch.bfloat16))
-    assert not TriangleAttentionEndingNode(128, 64, 4)._kernel_supported(torch.zeros(1, 4, 4, 128))
+    assert a._headline_shape()
+    for cin, ch, h in ((128, 32, 4), (64, 32, 4), (32, 16, 2), (128, 64, 4), (64, 64, 2), (32, 8, 1)):
+        t = TriangleAttentionEndingNode(cin, ch, h)
+        assert t._kernel_supported(torch.zeros(1, 4, 4, cin)), (cin, ch, h)
+        assert not t._headline_shape()
     assert not TriangleAttentionEndingNode(128, 128, 8)._kernel_supported(torch.zeros(1, 4, 4, 128))
+    assert not TriangleAttentionEndingNode(128, 256, 4)._kernel_supported(torch.zeros(1, 4, 4, 128))
+    assert not TriangleAttentionEndingNode(96, 32, 4)._kernel_supported(torch.zeros(1, 4, 4, 96))
 
 
 def test_device_info_keys():

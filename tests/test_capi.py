@@ -102,12 +102,19 @@ def test_workspace_sizes(lib):
     # packed weights exist only for the shapes the kernels are built for
     assert lib.gtk_tri_mul_packed_size(128, 128, GTK_BF16) > 0
     assert lib.gtk_tri_mul_packed_size(128, 64, GTK_F32) > lib.gtk_tri_mul_packed_size(128, 64, GTK_BF16)
-    assert lib.gtk_tri_mul_packed_size(64, 64, GTK_BF16) == 0
+    assert lib.gtk_tri_mul_packed_size(64, 64, GTK_BF16) > 0
+    assert lib.gtk_tri_mul_packed_size(96, 64, GTK_BF16) == 0
+    assert lib.gtk_tri_mul_packed_size(64, 48, GTK_BF16) == 0
     assert lib.gtk_tri_attn_packed_size(128, 128, 4, GTK_BF16) > 0
-    assert lib.gtk_tri_attn_packed_size(128, 64, 2, GTK_BF16) == 0
+    # heads are padded to 32 channels: d = 8 packs like d = 32
+    assert lib.gtk_tri_attn_packed_size(128, 32, 4, GTK_BF16) == lib.gtk_tri_attn_packed_size(128, 128, 4, GTK_BF16)
+    assert lib.gtk_tri_attn_packed_size(64, 32, 4, GTK_BF16) > 0
+    assert lib.gtk_tri_attn_packed_size(128, 128, 2, GTK_BF16) == 0  # d = 64
+    assert lib.gtk_tri_attn_packed_size(128, 64, 8, GTK_BF16) == 0   # 8 heads
     ws = lib.gtk_tri_attn_workspace_size(1, 512, 128, 128, 4, GTK_BF16)
     assert ws >= 4 * 512 * 512 * 128 * 2  # q, k, v^T, gate planes at least
-    assert lib.gtk_tri_attn_workspace_size(1, 512, 128, 64, 2, GTK_BF16) == 0
+    assert lib.gtk_tri_attn_workspace_size(1, 512, 128, 64, 2, GTK_BF16) > 0
+    assert lib.gtk_tri_attn_workspace_size(1, 512, 128, 128, 2, GTK_BF16) == 0
     # row chunks: q, k, v^T and the gate for chunk_rows rows, the triangle
     # bias for all of them; chunk_rows = 0 or >= N is the unchunked size
     wc = lambda rows: lib.gtk_tri_attn_workspace_size_chunked(1, 2048, 128, 128, 4, rows, GTK_BF16)
@@ -137,9 +144,9 @@ def test_bad_dtype_and_shapes_are_rejected(lib):
     assert lib.gtk_layernorm(None, None, None, None, -1, 128, 1e-5, GTK_F32, None) == GTK_EINVAL
     assert lib.gtk_layernorm(None, None, None, None, 4, 128, 1e-5, GTK_F32, None) == GTK_EINVAL
     assert "null" in _err(lib)
-    rc = lib.gtk_tri_mul_forward(None, None, None, None, 1, 8, 64, 64, 1, 0, 1e-5, 1e-5,
+    rc = lib.gtk_tri_mul_forward(None, None, None, None, 1, 8, 96, 64, 1, 0, 1e-5, 1e-5,
                                  GTK_BF16, None, 0, None)
-    assert rc == GTK_EUNSUPPORTED and "c_z=64" in _err(lib)
+    assert rc == GTK_EUNSUPPORTED and "c_z=96" in _err(lib)
     rc = lib.gtk_tri_mul_forward(None, None, None, None, 1, 8, 128, 128, 1, 0, 1e-5, 1e-5,
                                  GTK_BF16, None, 0, None)
     assert rc == GTK_EINVAL and "null" in _err(lib)

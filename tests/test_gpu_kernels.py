@@ -276,6 +276,83 @@ def test_tri_attn_row_chunks(starting, N, chunks):
     check_bf16(to_np(y), ref, "tri_attn chunked")
 
 
+# --------------------------------------------------- shapes beyond the headline
+@pytest.mark.parametrize("dname", ["fp32", "bf16"])
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("cin,ch,heads", [(128, 32, 4), (64, 32, 4), (32, 16, 2), (128, 64, 4),
+                                          (64, 64, 2), (32, 8, 1), (128, 96, 4)])
+def test_tri_attn_other_shapes(dname, starting, cin, ch, heads):
+    """c_in, heads and head dim d = ch / heads beyond the headline (d = 8: the
+    reference layer's default c_hidden_tri_att=32 with 4 heads, and the
+    reference tests' (64, 32, 4) and (32, 16, 2); d = 24 is not a power of
+    two).  Heads are padded to 32 channels inside the packed weights."""
+    N = 45
+    log(f"tri_attn {dname} start={starting} c_in={cin} c_h={ch} H={heads}")
+    P = H.draw_params(H.tri_attn_shapes(cin, ch, heads), seed=cin + ch + heads, ln_random=True,
+                      bias_random=True)
+    x = H.pair_input(2, N, cin, seed=N + cin)
+    m = H.tail_mask(2, N, [N, N - 7])
+    m[0, 5, :] = 0.0
+    m[0, :, 9] = 0.0
+    if dname == "bf16":
+        P, x = H.bf16_params(P), H.bf16_round(x)
+    mod = triattn_module(P, starting, heads, DT[dname])
+    xd, md = _dev(x, DT[dname]), _dev(m, DT[dname])
+    with torch.no_grad():
+        assert mod._kernel_supported(xd)
+        y = mod._forward_cuda(xd, md)
+        y_res = mod.forward_residual(xd, md)
+    torch.cuda.synchronize()
+    ref = pair_ops.tri_attn(x, m, P, starting, heads, dtype=np.float64)
+    chk = check_fp32 if dname == "fp32" else check_bf16
+    chk(to_np(y), ref, "tri_attn other shape")
+    if dname == "fp32":
+        check_fp32(to_np(y_res), ref + x, "tri_attn other shape, residual")
+
+
+@pytest.mark.parametrize("dname", ["fp32", "bf16"])
+@pytest.mark.parametrize("outgoing", [True, False])
+@pytest.mark.parametrize("cz,c", [(64, 32), (32, 32), (128, 256), (64, 64), (32, 128), (128, 32),
+                                  (64, 256)])
+def test_tri_mul_other_shapes(dname, outgoing, cz, c):
+    """c_z in {32, 64} (the reference tests' widths) and c in {32, 256} (the
+    reference kernel's C_HIDDEN=256 instance, triangle_mul.cu:36-42) on the
+    generic kernels."""
+    N = 37
+    log(f"tri_mul {dname} out={outgoing} c_z={cz} c={c}")
+    P = H.draw_params(H.tri_mul_shapes(cz, c), seed=cz + c, ln_random=True, bias_random=True)
+    z = H.pair_input(2, N, cz, seed=N + cz + c)
+    m = H.tail_mask(2, N, [N, N - 9])
+    if dname == "bf16":
+        P, z = H.bf16_params(P), H.bf16_round(z)
+    mod = trimul_module(P, outgoing, DT[dname])
+    zd, md = _dev(z, DT[dname]), _dev(m, DT[dname])
+    with torch.no_grad():
+        assert mod._kernel_supported(zd)
+        y = mod._forward_cuda(zd, md)
+        y_res = mod.forward_residual(zd, md)
+    torch.cuda.synchronize()
+    ref = pair_ops.tri_mul(z, m, P, outgoing, dtype=np.float64)
+    chk = check_fp32 if dname == "fp32" else check_bf16
+    chk(to_np(y), ref, "tri_mul other shape")
+    chk(to_np(y_res), ref + z, "tri_mul other shape, residual")
+
+
+def test_other_shapes_train_through_pytorch():
+    """Shapes without backward kernels still train: autograd of the PyTorch
+    path (the reference's own training path), gradients finite."""
+    P = H.draw_params(H.tri_attn_shapes(64, 32, 4), seed=5, bias_random=True)
+    att = triattn_module(P, True, 4, torch.float32)
+    x = torch.randn(1, 12, 12, 64, device="cuda", requires_grad=True)
+    att(x).square().sum().backward()
+    assert torch.isfinite(x.grad).all() and x.grad.abs().sum() > 0
+    Pm = H.draw_params(H.tri_mul_shapes(64, 32), seed=6, bias_random=True)
+    tm = trimul_module(Pm, False, torch.float32)
+    z = torch.randn(1, 12, 12, 64, device="cuda", requires_grad=True)
+    tm(z).square().sum().backward()
+    assert torch.isfinite(z.grad).all() and z.grad.abs().sum() > 0
+
+
 def _inf_mask(N: int, seed: int) -> np.ndarray:
     """Random 80 % valid keys, a fully masked row (starting node) and column
     (ending node), fractional values on some keys and a row of them."""

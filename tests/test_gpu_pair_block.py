@@ -65,3 +65,36 @@ def test_pair_layer_kernel_path():
     log(f"pair layer: max abs err {err.max():.3e}, worst err/bound {(err / bound).max():.2f}")
     assert (err <= bound).all(), f"pair layer: max err {err.max():.3e}, worst ratio {(err / bound).max():.2f}"
     assert np.all(got[1, 50:] == 0) and np.all(got[1, :, 50:] == 0)  # masked pairs are zero
+
+
+@pytest.mark.parametrize("c,c_mul,c_att,heads", [(128, 128, 32, 4), (64, 32, 16, 2)])
+def test_pair_layer_reference_shapes(c, c_mul, c_att, heads, monkeypatch):
+    """The reference layer's default shape (c_hidden_tri_att=32 with 4 heads:
+    head dim 8; pair_transform.py:116-117) and its test's small shape
+    (tests/test_triangle_attention.py:131-136: c_hidden_mul=32,
+    c_hidden_tri_att=16, head dim 8 over 2 heads) run every triangle operator
+    on the kernels (their PyTorch paths are made to raise) and match the
+    oracle's block."""
+    log(f"pair layer reference shape c={c} c_mul={c_mul} c_att={c_att} heads={heads}")
+    B, N = 2, 40
+    P = H.bf16_params(H.draw_params(H.pair_layer_shapes(c, c_mul, c_att, heads), 92 + c,
+                                    ln_random=True, bias_random=True,
+                                    tri_std=1.0 / np.sqrt(c)))
+    layer = PairTransformLayer(c_p=c, c_hidden_mul=c_mul, c_hidden_tri_att=c_att, n_head_tri=heads,
+                               tri_dropout=0.25)
+    layer.load_state_dict(H.to_state_dict(P))
+    layer = layer.to("cuda", torch.bfloat16).eval()
+    for name in ("tri_mul_out", "tri_mul_in", "tri_att_start", "tri_att_end"):
+        monkeypatch.setattr(getattr(layer, name), "_forward_pytorch",
+                            lambda *a, **k: (_ for _ in ()).throw(AssertionError("PyTorch path")))
+    p = H.bf16_round(H.pair_input(B, N, c, seed=93))
+    m = H.tail_mask(B, N, [N, 33])
+    with torch.no_grad():
+        out, _ = layer((_dev(p), _dev(m, torch.float32)))
+    ref = pair_ops.pair_block(p, m, P, heads, dtype=np.float32)
+    got = to_np(out)
+    assert np.isfinite(got).all()
+    err = np.abs(got - ref)
+    bound = 2.5 * (2e-2 + 1e-2 * np.abs(ref))
+    log(f"  max abs err {err.max():.3e}, worst err/bound {(err / bound).max():.2f}")
+    assert (err <= bound).all(), f"max err {err.max():.3e}, worst ratio {(err / bound).max():.2f}"
