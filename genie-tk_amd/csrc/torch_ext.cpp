@@ -340,9 +340,10 @@ std::vector<at::Tensor> tri_attn_backward(const at::Tensor& x, const c10::option
   return out;
 }
 
+// chunk_rows > 0: the memory-bounded mode (output rows that many at a time)
 at::Tensor tri_mul_forward(const at::Tensor& z, const c10::optional<at::Tensor>& mask,
                            const at::Tensor& packed, int64_t c_z, int64_t c, bool outgoing,
-                           bool residual, double eps_in, double eps_out) {
+                           bool residual, double eps_in, double eps_out, int64_t chunk_rows) {
   check_gpu(z, "z");
   check_on(mask, z, "mask");
   check_on(packed, z, "packed");
@@ -357,11 +358,12 @@ at::Tensor tri_mul_forward(const at::Tensor& z, const c10::optional<at::Tensor>&
   }
   const int dt = gtk_dtype_of(zc, "z");
   auto out = at::empty_like(zc);
-  auto ws = workspace(zc, gtk_tri_mul_workspace_size(B, N, c_z, c, dt));
-  check_rc(gtk_tri_mul_forward(zc.data_ptr(), mask.has_value() ? mc.data_ptr<float>() : nullptr,
-                               out.data_ptr(), packed.data_ptr(), B, N, c_z, c, outgoing ? 1 : 0,
-                               residual ? 1 : 0, (float)eps_in, (float)eps_out, dt, ws.data_ptr(),
-                               ws.numel(), cur_stream(zc)));
+  TORCH_CHECK(chunk_rows >= 0, "tri_mul_forward: chunk_rows must be >= 0");
+  auto ws = workspace(zc, gtk_tri_mul_workspace_size_chunked(B, N, c_z, c, dt, chunk_rows));
+  check_rc(gtk_tri_mul_forward_chunked(
+      zc.data_ptr(), mask.has_value() ? mc.data_ptr<float>() : nullptr, out.data_ptr(),
+      packed.data_ptr(), B, N, c_z, c, outgoing ? 1 : 0, residual ? 1 : 0, (float)eps_in,
+      (float)eps_out, dt, chunk_rows, ws.data_ptr(), ws.numel(), cur_stream(zc)));
   return out;
 }
 
@@ -500,7 +502,7 @@ PYBIND11_MODULE(_C, m) {
   m.def("tri_mul_forward", &tri_mul_forward, "Fused TriangleMultiplicativeUpdate forward",
         py::arg("z"), py::arg("mask"), py::arg("packed"), py::arg("c_z"), py::arg("c"),
         py::arg("outgoing"), py::arg("residual") = false, py::arg("eps_in") = 1e-5,
-        py::arg("eps_out") = 1e-5);
+        py::arg("eps_out") = 1e-5, py::arg("chunk_rows") = 0);
   m.def("tri_mul_backward", &tri_mul_backward,
         "TriangleMultiplicativeUpdate backward: [dz, 16 parameter gradients (fp32)]",
         py::arg("z"), py::arg("mask"), py::arg("dy"), py::arg("params"), py::arg("c_z"),

@@ -29,20 +29,27 @@ namespace gtk {
 
 // ---------------------------------------------------------------------------
 // 1. Prologue
+//    Both prologues write plane rows f = r0 .. r0 + nrows - 1 as rows
+//    0 .. nrows - 1 of nrows x Np planes, for sides side_lo .. side_hi - 1
+//    (0: A, 1: Bm).  Whole planes: r0 = 0, nrows = Np, sides 0 .. 1; the row
+//    chunks of the memory-bounded mode write Bm once over all rows and A one
+//    chunk of rows at a time.
 // ---------------------------------------------------------------------------
 template <typename T, int CZ, int CH>
 __global__ __launch_bounds__(256) void trimul_prologue_kernel(
     const T* __restrict__ z, const float* __restrict__ mask, T* __restrict__ pa,
-    T* __restrict__ pb, TriMulPacked<T> w, int B, int N, int Np, int outgoing, float eps) {
+    T* __restrict__ pb, TriMulPacked<T> w, int B, int N, int Np, int outgoing, float eps,
+    int r0, int nrows, int side_lo, int side_hi) {
   const int lane = threadIdx.x & 63;
   const int half = lane >> 5;
   const int t32 = lane & 31;
   const int vtiles = Np / 32;
   const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (tile >= (int64_t)B * Np * vtiles) return;
+  if (tile >= (int64_t)B * nrows * vtiles) return;
   const int vt = (int)(tile % vtiles);
-  const int f = (int)((tile / vtiles) % Np);
-  const int b = (int)(tile / ((int64_t)vtiles * Np));
+  const int fl = (int)((tile / vtiles) % nrows);
+  const int f = r0 + fl;
+  const int b = (int)(tile / ((int64_t)vtiles * nrows));
   const int v = vt * 32 + t32;
   const int p = outgoing ? f : v;
   const int q = outgoing ? v : f;
@@ -57,10 +64,10 @@ __global__ __launch_bounds__(256) void trimul_prologue_kernel(
   else ln_affine_to_frags<T, CZ>(xf, rh, st, w.ln_in_w, w.ln_in_b);
   const float m = valid ? (mask ? mask[pair] : 1.0f) : 0.0f;
 
-  const int64_t plane = (int64_t)Np * Np;
-  const int64_t off_fv = (int64_t)f * Np + v;
+  const int64_t plane = (int64_t)nrows * Np;
+  const int64_t off_fv = (int64_t)fl * Np + v;
 #pragma unroll 1
-  for (int side = 0; side < 2; ++side) {
+  for (int side = side_lo; side < side_hi; ++side) {
     const T* wp = side ? w.w_bp : w.w_ap;
     const T* wg = side ? w.w_bg : w.w_ag;
     const float* bp = side ? w.b_bp : w.b_ap;
@@ -102,7 +109,7 @@ template <int CZ, int CH>
 __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
     const bf16* __restrict__ z, const float* __restrict__ mask, bf16* __restrict__ pa,
     bf16* __restrict__ pb, TriMulPacked<bf16> w, int N, int Np, int outgoing, float eps,
-    int64_t ntiles) {
+    int64_t ntiles, int r0, int nrows, int side_lo, int side_hi) {
   constexpr int WAVES = 8;
   constexpr int KCH = CZ / 16;
   constexpr int PE = (CH / 32) * KCH * 512;  // packed elements of one projection
@@ -131,15 +138,15 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
   const int i32 = lane & 31;
   const int prow = 16 * ((i32 >> 2) & 1) + 4 * (i32 >> 3) + (i32 & 3);
   const int vtiles = Np / 32;  // even: Np is a multiple of 64
-  const int64_t plane = (int64_t)Np * Np;
+  const int64_t plane = (int64_t)nrows * Np;  // written planes: nrows x Np
   const int64_t nsteps = ntiles / 2;
 
   // raw z rows of the two tiles of step s (zeros outside the N x N pair grid)
   auto load_z = [&](Frag<bf16> (*zr)[KCH], int64_t s) {
     const int64_t tile = 2 * s;
     const int vt = (int)(tile % vtiles);
-    const int f = (int)((tile / vtiles) % Np);
-    const int b = (int)(tile / ((int64_t)vtiles * Np));
+    const int f = r0 + (int)((tile / vtiles) % nrows);
+    const int b = (int)(tile / ((int64_t)vtiles * nrows));
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int v = (vt + u) * 32 + prow;
@@ -160,8 +167,8 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
   auto load_mask = [&](int64_t s) {
     const int64_t tile = 2 * s;
     const int vt = (int)(tile % vtiles);
-    const int f = (int)((tile / vtiles) % Np);
-    const int b = (int)(tile / ((int64_t)vtiles * Np));
+    const int f = r0 + (int)((tile / vtiles) % nrows);
+    const int b = (int)(tile / ((int64_t)vtiles * nrows));
     const int v = vt * 32 + lane;
     const bool ok = f < N && v < N;
     const int64_t idx = ((int64_t)b * N + (outgoing ? f : v)) * N + (outgoing ? v : f);
@@ -181,8 +188,8 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
   for (; s < nsteps; s += sstride) {
     const int64_t tile = 2 * s;
     const int vt = (int)(tile % vtiles);
-    const int f = (int)((tile / vtiles) % Np);
-    const int b = (int)(tile / ((int64_t)vtiles * Np));
+    const int fl = (int)((tile / vtiles) % nrows);  // row of the written planes
+    const int b = (int)(tile / ((int64_t)vtiles * nrows));
     Frag<bf16> xf[2][KCH];
     ln_frags_bf16<CZ>(xf[0], zr[0], eps);
     ln_frags_bf16<CZ>(xf[1], zr[1], eps);
@@ -192,12 +199,12 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
       mv = load_mask(s + sstride);
     }
 #pragma unroll 1
-    for (int side = 0; side < 2; ++side) {
+    for (int side = side_lo; side < side_hi; ++side) {
       const bf16* wp = wl[2 * side];
       const bf16* wg = wl[2 * side + 1];
       const float* bp = bl[side][0];
       const float* ebgs = bl[side][1];
-      bf16* dst = (side ? pb : pa) + (int64_t)b * CH * plane + (int64_t)f * Np + vt * 32 + 16 * half;
+      bf16* dst = (side ? pb : pa) + (int64_t)b * CH * plane + (int64_t)fl * Np + vt * 32 + 16 * half;
 #pragma unroll 1
       for (int ct = 0; ct < CH / 32; ++ct) {
         Frag<bf16> wfp, wfg;
@@ -249,12 +256,13 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// 2. Per-channel contraction  X = A . Bm^T   (A, Bm, X: [Np][Np] planes)
+// 2. Per-channel contraction  X = A . Bm^T   (Bm: [Np][Np] planes; A, X:
+//    [Mi][Np], Mi = Np for whole planes, fewer rows for a row chunk)
 // ---------------------------------------------------------------------------
 template <typename T, int TILE>
 __global__ __launch_bounds__(256) void trimul_contract_kernel(const T* __restrict__ pa,
                                                               const T* __restrict__ pb,
-                                                              T* __restrict__ px, int Np,
+                                                              T* __restrict__ px, int Np, int Mi,
                                                               int64_t nplanes) {
   constexpr int BK = 128 / sizeof(T);            // k elements per stage (128-byte rows)
   constexpr int PITCH = 144;                     // LDS row pitch in bytes (16 B pad)
@@ -265,15 +273,16 @@ __global__ __launch_bounds__(256) void trimul_contract_kernel(const T* __restric
   constexpr int EPC = 16 / sizeof(T);            // elements per 16-byte chunk
   __shared__ __attribute__((aligned(16))) char smem[2][2][TILE * PITCH];
 
-  const int tiles_1d = Np / TILE;
-  const int64_t total = (int64_t)tiles_1d * tiles_1d * nplanes;
+  const int ti_n = Mi / TILE, tj_n = Np / TILE;
+  const int64_t total = (int64_t)ti_n * tj_n * nplanes;
   const int64_t lin = xcd_remap((int64_t)blockIdx.x, total);
-  const int64_t pl = lin / ((int64_t)tiles_1d * tiles_1d);
-  const int trem = (int)(lin % ((int64_t)tiles_1d * tiles_1d));
-  const int i0 = (trem / tiles_1d) * TILE;
-  const int j0 = (trem % tiles_1d) * TILE;
-  const int64_t plane = (int64_t)Np * Np;
-  const T* A = pa + pl * plane;
+  const int64_t pl = lin / ((int64_t)ti_n * tj_n);
+  const int trem = (int)(lin % ((int64_t)ti_n * tj_n));
+  const int i0 = (trem / tj_n) * TILE;
+  const int j0 = (trem % tj_n) * TILE;
+  const int64_t plane = (int64_t)Np * Np;     // Bm: Np x Np
+  const int64_t plane_ax = (int64_t)Mi * Np;  // A, X: Mi x Np
+  const T* A = pa + pl * plane_ax;
   const T* Bm = pb + pl * plane;
 
   const int tid = threadIdx.x;
@@ -337,7 +346,7 @@ __global__ __launch_bounds__(256) void trimul_contract_kernel(const T* __restric
   }
 
   // acc[x][y]: lane holds X[i = wi + 32x + (l&31)][j = wj + 32y + 8g + 4h + r]
-  T* X = px + pl * plane;
+  T* X = px + pl * plane_ax;
 #pragma unroll
   for (int x = 0; x < MB; ++x) {
     const int i = i0 + wi + x * 32 + (lane & 31);
@@ -367,7 +376,7 @@ __global__ __launch_bounds__(256) void trimul_contract_kernel(const T* __restric
 template <int TI, int TJ>
 __global__ __launch_bounds__(64 * (TI / 64) * (TJ / 64)) void trimul_contract_bf16_kernel(
     const bf16* __restrict__ pa, const bf16* __restrict__ pb, bf16* __restrict__ px, int Np,
-    int64_t nplanes) {
+    int Mi, int64_t nplanes) {
   constexpr int BK = 64, NS = 2;
   constexpr int NW = (TI / 64) * (TJ / 64);         // waves
   constexpr int RPR = 1024 / (2 * BK);              // panel rows per 1 KiB copy
@@ -378,15 +387,16 @@ __global__ __launch_bounds__(64 * (TI / 64) * (TJ / 64)) void trimul_contract_bf
   bf16(*ra_l)[TI * BK] = reinterpret_cast<bf16(*)[TI * BK]>(ring);
   bf16(*rb_l)[TJ * BK] = reinterpret_cast<bf16(*)[TJ * BK]>(ring + NS * TI * BK);
 
-  const int ti_n = Np / TI, tj_n = Np / TJ;
+  const int ti_n = Mi / TI, tj_n = Np / TJ;
   const int64_t total = (int64_t)ti_n * tj_n * nplanes;
   const int64_t lin = xcd_remap((int64_t)blockIdx.x, total);
   const int64_t pl = lin / ((int64_t)ti_n * tj_n);
   const int trem = (int)(lin % ((int64_t)ti_n * tj_n));
   const int i0 = (trem / tj_n) * TI;
   const int j0 = (trem % tj_n) * TJ;
-  const int64_t plane = (int64_t)Np * Np;
-  const bf16* A = pa + pl * plane;
+  const int64_t plane = (int64_t)Np * Np;     // Bm: Np x Np
+  const int64_t plane_ax = (int64_t)Mi * Np;  // A, X: Mi x Np
+  const bf16* A = pa + pl * plane_ax;
   const bf16* Bm = pb + pl * plane;
 
   const int lane = threadIdx.x & 63;
@@ -482,7 +492,7 @@ __global__ __launch_bounds__(64 * (TI / 64) * (TJ / 64)) void trimul_contract_bf
       }
   }
   barrier_only();
-  bf16* X = px + pl * plane;
+  bf16* X = px + pl * plane_ax;
   constexpr int RPI = 64 * NW / CPO;  // output rows per pass of the block
   const int rr = (int)threadIdx.x / CPO, cc = (int)threadIdx.x % CPO;
 #pragma unroll
@@ -495,11 +505,14 @@ __global__ __launch_bounds__(64 * (TI / 64) * (TJ / 64)) void trimul_contract_bf
 
 // ---------------------------------------------------------------------------
 // 3. Epilogue
+//    Both epilogues produce output rows i = r0 .. r0 + nrows - 1 from rows
+//    i - r0 of the x planes, which hold xrows x Np (whole planes: r0 = 0,
+//    nrows = N, xrows = Np).
 // ---------------------------------------------------------------------------
 template <typename T, int CZ, int CH>
 __global__ __launch_bounds__(256) void trimul_epilogue_kernel(
     const T* __restrict__ z, const T* __restrict__ px, T* __restrict__ out, TriMulPacked<T> w,
-    int B, int N, int Np, int residual, float eps_in, float eps_out) {
+    int B, int N, int Np, int residual, float eps_in, float eps_out, int r0, int nrows, int xrows) {
   constexpr int XPITCH = CH + 8;  // LDS row pitch (elements) of the transposed x tile
   __shared__ __attribute__((aligned(16))) T xs[4][32 * XPITCH];
   const int lane = threadIdx.x & 63;
@@ -508,10 +521,11 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(
   const int t32 = lane & 31;
   const int jtiles = (N + 31) / 32;
   const int64_t tile = (int64_t)blockIdx.x * 4 + wave;
-  if (tile >= (int64_t)B * N * jtiles) return;
+  if (tile >= (int64_t)B * nrows * jtiles) return;
   const int jt = (int)(tile % jtiles);
-  const int i = (int)((tile / jtiles) % N);
-  const int b = (int)(tile / ((int64_t)jtiles * N));
+  const int il = (int)((tile / jtiles) % nrows);  // row of the x planes
+  const int i = r0 + il;
+  const int b = (int)(tile / ((int64_t)jtiles * nrows));
   const int j = jt * 32 + t32;
   const bool valid = j < N;
   const int64_t pair = ((int64_t)b * N + i) * N + (valid ? j : 0);
@@ -543,8 +557,8 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(
     constexpr int EPC = 16 / sizeof(T);   // elements per 16-byte chunk
     constexpr int CPR = 32 / EPC;         // chunks per c-row of 32 elements
     constexpr int TOTAL = CH * CPR;
-    const int64_t plane = (int64_t)Np * Np;
-    const T* xb = px + (int64_t)b * CH * plane + (int64_t)i * Np + jt * 32;
+    const int64_t plane = (int64_t)xrows * Np;
+    const T* xb = px + (int64_t)b * CH * plane + (int64_t)il * Np + jt * 32;
     T* s = xs[wave];
 #pragma unroll 4
     for (int id = lane; id < TOTAL; id += 64) {
@@ -612,7 +626,7 @@ template <int CZ, int CH>
 __global__ __launch_bounds__(512) void trimul_epilogue_bf16_kernel(
     const bf16* __restrict__ z, const bf16* __restrict__ px, bf16* __restrict__ out,
     TriMulPacked<bf16> w, int N, int Np, int residual, float eps_in, float eps_out,
-    int64_t ntiles) {
+    int64_t ntiles, int r0, int nrows, int xrows) {
   constexpr int WAVES = 8;
   constexpr int KZ = CZ / 16;                 // k chunks over c_z (gate input)
   constexpr int KX = CH / 16;                 // k chunks over c (W_z input)
@@ -635,7 +649,7 @@ __global__ __launch_bounds__(512) void trimul_epilogue_bf16_kernel(
   const int half = lane >> 5;
   const int t32 = lane & 31;
   const int jtiles = (N + 31) / 32;
-  const int64_t plane = (int64_t)Np * Np;
+  const int64_t plane = (int64_t)xrows * Np;  // x planes: xrows x Np
   bf16* xw = xt[wave];
   const bf16* wg = wl;
   const bf16* wz = wl + PG;
@@ -644,10 +658,10 @@ __global__ __launch_bounds__(512) void trimul_epilogue_bf16_kernel(
   // pairs 8k .. 8k+7 with k = p ^ swz(c).  Copy instruction n moves rows
   // 16n .. 16n+15; lane l lands at row 16n + l/4, physical chunk l%4.
   auto swz = [](int c) { return 2 * ((c >> 1) & 1); };
-  // tiles: [B][N rows i][jtiles], walked without divisions
+  // tiles: [B][nrows rows i - r0][jtiles], walked without divisions
   auto issue_x = [&](const TileWalk& tw) {
-    const int jt = tw.c, i = tw.r, b = tw.b;
-    const bf16* src = px + (int64_t)b * CH * plane + (int64_t)i * Np + jt * 32;
+    const int jt = tw.c, il = tw.r, b = tw.b;
+    const bf16* src = px + (int64_t)b * CH * plane + (int64_t)il * Np + jt * 32;
 #pragma unroll
     for (int n = 0; n < CH / 16; ++n) {
       const int row = 16 * n + (lane >> 2);
@@ -658,7 +672,7 @@ __global__ __launch_bounds__(512) void trimul_epilogue_bf16_kernel(
   // Always KZ load instructions (an invalid pair reads pair j = 0; its
   // results are never stored): the wait below counts them.
   auto load_z = [&](Frag<bf16>* zr, const TileWalk& tw) {
-    const int jt = tw.c, i = tw.r, b = tw.b;
+    const int jt = tw.c, i = r0 + tw.r, b = tw.b;
     const int j = jt * 32 + t32;
     const bool valid = j < N;
     const bf16* row = z + (((int64_t)b * N + i) * N + (valid ? j : 0)) * CZ + half * (CZ / 2);
@@ -695,7 +709,7 @@ __global__ __launch_bounds__(512) void trimul_epilogue_bf16_kernel(
   // every path into the loop has the previous tile's stores outstanding
   // behind the prefetched loads, and the waits can count them exactly.
   auto body = [&](const int64_t tile, const TileWalk& tw, const bool first) {
-    const int jt = tw.c, i = tw.r, b = tw.b;
+    const int jt = tw.c, i = r0 + tw.r, b = tw.b;
     const int j = jt * 32 + t32;
     const bool valid = j < N;
     // this tile's 32 output pairs, one buffer range: every lane stores
@@ -772,7 +786,7 @@ __global__ __launch_bounds__(512) void trimul_epilogue_bf16_kernel(
     }
   };
   TileWalk tw;
-  tw.init(tile, stride, N, jtiles);
+  tw.init(tile, stride, nrows, jtiles);
   if (tile < ntiles) {
     issue_x(tw);
     load_z(zr, tw);
@@ -846,28 +860,34 @@ __global__ __launch_bounds__(256) void planes_to_pairs_kernel(const T* __restric
   }
 }
 
+// Output tile of the contraction for Np (a multiple of 64): row chunks are
+// multiples of it.
+template <typename T>
+static int contract_tile(int Np) {
+  return (sizeof(T) == 2 && Np % 256 == 0) ? 256 : (Np % 128 == 0 ? 128 : 64);
+}
+
+// X = A . Bm^T per plane: A and X are Mi x Np (Mi a multiple of
+// contract_tile(Np); Mi = Np for whole planes), Bm is Np x Np.
 template <typename T>
 static int launch_contract(const T* pa, const T* pb, T* px, int Np, int64_t nplanes,
-                           hipStream_t st) {
-  if (sizeof(T) == 2 && Np % 256 == 0) {
-    const int64_t blocks = (int64_t)(Np / 256) * (Np / 256) * nplanes;
-    GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "contraction grid too large");
-    StageTimer timer("trimul_contract", st);
+                           hipStream_t st, int Mi = 0) {
+  if (Mi == 0) Mi = Np;
+  const int tile = contract_tile<T>(Np);
+  GTK_REQUIRE(Mi > 0 && Mi % tile == 0 && Mi <= Np, GTK_EINVAL, "contraction: %d rows, tile %d", Mi, tile);
+  const int64_t blocks = (int64_t)(Mi / tile) * (Np / tile) * nplanes;
+  GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "contraction grid too large");
+  StageTimer timer("trimul_contract", st);
+  if (tile == 256) {
     trimul_contract_bf16_kernel<256, 256><<<(unsigned)blocks, 1024, 0, st>>>(
-        (const bf16*)pa, (const bf16*)pb, (bf16*)px, Np, nplanes);
-  } else if (Np % 128 == 0) {
-    const int64_t blocks = (int64_t)(Np / 128) * (Np / 128) * nplanes;
-    GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "contraction grid too large");
-    StageTimer timer("trimul_contract", st);
+        (const bf16*)pa, (const bf16*)pb, (bf16*)px, Np, Mi, nplanes);
+  } else if (tile == 128) {
     if constexpr (sizeof(T) == 2)
-      trimul_contract_bf16_kernel<128, 128><<<(unsigned)blocks, 256, 0, st>>>(pa, pb, px, Np, nplanes);
+      trimul_contract_bf16_kernel<128, 128><<<(unsigned)blocks, 256, 0, st>>>(pa, pb, px, Np, Mi, nplanes);
     else
-      trimul_contract_kernel<T, 128><<<(unsigned)blocks, 256, 0, st>>>(pa, pb, px, Np, nplanes);
+      trimul_contract_kernel<T, 128><<<(unsigned)blocks, 256, 0, st>>>(pa, pb, px, Np, Mi, nplanes);
   } else {
-    const int64_t blocks = (int64_t)(Np / 64) * (Np / 64) * nplanes;
-    GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "contraction grid too large");
-    StageTimer timer("trimul_contract", st);
-    trimul_contract_kernel<T, 64><<<(unsigned)blocks, 256, 0, st>>>(pa, pb, px, Np, nplanes);
+    trimul_contract_kernel<T, 64><<<(unsigned)blocks, 256, 0, st>>>(pa, pb, px, Np, Mi, nplanes);
   }
   GTK_LAUNCH_CHECK();
   return GTK_OK;
@@ -966,53 +986,103 @@ constexpr bool trimul_fast() {
   return sizeof(T) == 2 && CZ == 128 && (CH == 64 || CH == 128);
 }
 
+// Prologue over plane rows r0 .. r0 + nrows - 1 (default: all Np rows) for
+// sides side_lo .. side_hi - 1 (0: A, 1: Bm).
 template <typename T, int CZ, int CH>
 static int launch_trimul_prologue(const void* z, const float* mask, const TriMulPacked<T>& w, T* pa,
                                   T* pb, int64_t B, int64_t N, int Np, int outgoing, float eps_in,
-                                  hipStream_t st) {
-  const int64_t ptiles = B * (int64_t)Np * (Np / 32);
+                                  hipStream_t st, int r0 = 0, int nrows = 0, int side_lo = 0,
+                                  int side_hi = 2) {
+  if (nrows == 0) nrows = Np;
+  const int64_t ptiles = B * (int64_t)nrows * (Np / 32);
   if constexpr (trimul_fast<T, CZ, CH>()) {
     const int grid = (int)std::min<int64_t>(device_cus(), (ptiles / 2 + 7) / 8);
     StageTimer timer("trimul_prologue", st);
     trimul_prologue_bf16_kernel<CZ, CH><<<grid, 512, 0, st>>>(
-        (const bf16*)z, mask, (bf16*)pa, (bf16*)pb, w, (int)N, Np, outgoing, eps_in, ptiles);
+        (const bf16*)z, mask, (bf16*)pa, (bf16*)pb, w, (int)N, Np, outgoing, eps_in, ptiles, r0,
+        nrows, side_lo, side_hi);
   } else {
     StageTimer timer("trimul_prologue", st);
     trimul_prologue_kernel<T, CZ, CH><<<(unsigned)((ptiles + 3) / 4), 256, 0, st>>>(
-        (const T*)z, mask, pa, pb, w, (int)B, (int)N, Np, outgoing, eps_in);
+        (const T*)z, mask, pa, pb, w, (int)B, (int)N, Np, outgoing, eps_in, r0, nrows, side_lo,
+        side_hi);
   }
   GTK_LAUNCH_CHECK();
   return GTK_OK;
 }
 
+// Epilogue for output rows r0 .. r0 + nrows - 1 from x planes of xrows x Np
+// (default: all N rows from whole planes).
 template <typename T, int CZ, int CH>
-static int fwd_trimul(const void* z, const float* mask, void* out, const void* packed, int64_t B,
-                      int64_t N, int outgoing, int residual, float eps_in, float eps_out, void* ws,
-                      hipStream_t st) {
-  Carve pc((void*)packed, SIZE_MAX);
-  TriMulPacked<T> w = carve_trimul<T>(pc, CZ, CH);
-  const int Np = (int)round_up(N, 64);
-  Carve cv(ws, SIZE_MAX);
-  T* pa = cv.take<T>(B * CH * (int64_t)Np * Np);
-  T* pb = cv.take<T>(B * CH * (int64_t)Np * Np);
-  T* px = cv.take<T>(B * CH * (int64_t)Np * Np);
-  int rc = launch_trimul_prologue<T, CZ, CH>(z, mask, w, pa, pb, B, N, Np, outgoing, eps_in, st);
-  if (rc) return rc;
-  rc = launch_contract<T>(pa, pb, px, Np, B * CH, st);
-  if (rc) return rc;
-  const int64_t etiles = B * N * ((N + 31) / 32);
+static int launch_trimul_epilogue(const void* z, const T* px, void* out, const TriMulPacked<T>& w,
+                                  int64_t B, int64_t N, int Np, int residual, float eps_in,
+                                  float eps_out, hipStream_t st, int r0 = 0, int nrows = 0,
+                                  int xrows = 0) {
+  if (nrows == 0) nrows = (int)N;
+  if (xrows == 0) xrows = Np;
+  const int64_t etiles = B * nrows * ((N + 31) / 32);
   if constexpr (trimul_fast<T, CZ, CH>()) {
     const int grid = (int)std::min<int64_t>(device_cus(), (etiles + 7) / 8);
     StageTimer timer("trimul_epilogue", st);
     trimul_epilogue_bf16_kernel<CZ, CH><<<grid, 512, 0, st>>>(
         (const bf16*)z, (const bf16*)px, (bf16*)out, w, (int)N, Np, residual, eps_in, eps_out,
-        etiles);
+        etiles, r0, nrows, xrows);
   } else {
     StageTimer timer("trimul_epilogue", st);
     trimul_epilogue_kernel<T, CZ, CH><<<(unsigned)((etiles + 3) / 4), 256, 0, st>>>(
-        (const T*)z, px, (T*)out, w, (int)B, (int)N, Np, residual, eps_in, eps_out);
+        (const T*)z, px, (T*)out, w, (int)B, (int)N, Np, residual, eps_in, eps_out, r0, nrows,
+        xrows);
   }
   GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+// Rows per chunk of the memory-bounded mode: chunk_rows rounded up to the
+// contraction tile; Np (whole planes) when chunk_rows is 0 or covers Np.
+template <typename T>
+static int trimul_chunk_rows(int64_t N, int64_t chunk_rows) {
+  const int Np = (int)round_up(N, 64);
+  if (chunk_rows <= 0 || chunk_rows >= Np) return Np;
+  return (int)std::min<int64_t>(round_up(chunk_rows, contract_tile<T>(Np)), Np);
+}
+
+// Forward.  Whole planes: A, Bm and X of B*c planes of Np x Np.  Row chunks
+// (R < Np rows): Bm over all rows once, then per chunk of R output rows the
+// chunk's A rows, an R x Np contraction and the epilogue of those rows; the
+// workspace holds Bm and two R x Np plane sets.  Every element takes the same
+// arithmetic either way, so chunked and whole outputs are bit-identical.
+template <typename T, int CZ, int CH>
+static int fwd_trimul(const void* z, const float* mask, void* out, const void* packed, int64_t B,
+                      int64_t N, int outgoing, int residual, float eps_in, float eps_out, void* ws,
+                      hipStream_t st, int64_t chunk_rows) {
+  Carve pc((void*)packed, SIZE_MAX);
+  TriMulPacked<T> w = carve_trimul<T>(pc, CZ, CH);
+  const int Np = (int)round_up(N, 64);
+  const int R = trimul_chunk_rows<T>(N, chunk_rows);
+  Carve cv(ws, SIZE_MAX);
+  T* pb = cv.take<T>(B * CH * (int64_t)Np * Np);
+  T* pa = cv.take<T>(B * CH * (int64_t)R * Np);
+  T* px = cv.take<T>(B * CH * (int64_t)R * Np);
+  int rc;
+  if (R == Np) {
+    if ((rc = launch_trimul_prologue<T, CZ, CH>(z, mask, w, pa, pb, B, N, Np, outgoing, eps_in, st)))
+      return rc;
+    if ((rc = launch_contract<T>(pa, pb, px, Np, B * CH, st))) return rc;
+    return launch_trimul_epilogue<T, CZ, CH>(z, px, out, w, B, N, Np, residual, eps_in, eps_out, st);
+  }
+  if ((rc = launch_trimul_prologue<T, CZ, CH>(z, mask, w, pa, pb, B, N, Np, outgoing, eps_in, st, 0,
+                                              Np, 1, 2)))
+    return rc;
+  for (int r0 = 0; r0 < N; r0 += R) {
+    const int rows = std::min(R, Np - r0);  // a multiple of the contraction tile
+    if ((rc = launch_trimul_prologue<T, CZ, CH>(z, mask, w, pa, pb, B, N, Np, outgoing, eps_in, st,
+                                                r0, rows, 0, 1)))
+      return rc;
+    if ((rc = launch_contract<T>(pa, pb, px, Np, B * CH, st, rows))) return rc;
+    if ((rc = launch_trimul_epilogue<T, CZ, CH>(z, px, out, w, B, N, Np, residual, eps_in, eps_out,
+                                                st, r0, std::min<int>(rows, (int)N - r0), rows)))
+      return rc;
+  }
   return GTK_OK;
 }
 
@@ -1075,11 +1145,11 @@ static bool trimul_shape_ok(int64_t cz, int64_t c) {
 template <typename T>
 static int fwd_trimul_any(int64_t cz, int64_t c, const void* z, const float* mask, void* out,
                           const void* packed, int64_t B, int64_t N, int outgoing, int residual,
-                          float eps_in, float eps_out, void* ws, hipStream_t st) {
+                          float eps_in, float eps_out, void* ws, hipStream_t st, int64_t chunk_rows) {
 #define GTK_TM(CZ_, C_)                                                                          \
   if (cz == CZ_ && c == C_)                                                                     \
     return fwd_trimul<T, CZ_, C_>(z, mask, out, packed, B, N, outgoing, residual, eps_in, eps_out, \
-                                  ws, st);
+                                  ws, st, chunk_rows);
   GTK_TM(128, 128) GTK_TM(128, 64) GTK_TM(128, 32) GTK_TM(128, 256)
   GTK_TM(64, 128) GTK_TM(64, 64) GTK_TM(64, 32) GTK_TM(64, 256)
   GTK_TM(32, 128) GTK_TM(32, 64) GTK_TM(32, 32) GTK_TM(32, 256)
@@ -1115,31 +1185,52 @@ extern "C" int gtk_tri_mul_pack(const gtk_tri_mul_weights* w, int64_t c_z, int64
   return pack_trimul<bf16>(w, (int)c_z, (int)c, packed, st);
 }
 
-extern "C" size_t gtk_tri_mul_workspace_size(int64_t B, int64_t N, int64_t c_z, int64_t c, int dtype) {
+extern "C" size_t gtk_tri_mul_workspace_size_chunked(int64_t B, int64_t N, int64_t c_z, int64_t c,
+                                                     int dtype, int64_t chunk_rows) {
   (void)c_z;
-  if (B < 0 || N < 0 || c < 0) return 0;
-  return 3 * (plane_bytes(B, N, c, dtype) + 256);
+  if (B < 0 || N < 0 || c < 0 || chunk_rows < 0 || N > 16384) return 0;
+  if (dtype != GTK_F32 && dtype != GTK_BF16) return 0;
+  const int64_t Np = round_up(N, 64);
+  const int64_t R = dtype == GTK_F32 ? trimul_chunk_rows<float>(N, chunk_rows)
+                                     : trimul_chunk_rows<bf16>(N, chunk_rows);
+  const size_t es = dtype_size(dtype);
+  return (size_t)(B * c * Np * Np) * es + 2 * (size_t)(B * c * R * Np) * es + 3 * 256;
+}
+
+extern "C" size_t gtk_tri_mul_workspace_size(int64_t B, int64_t N, int64_t c_z, int64_t c, int dtype) {
+  return gtk_tri_mul_workspace_size_chunked(B, N, c_z, c, dtype, 0);
+}
+
+extern "C" int gtk_tri_mul_forward_chunked(const void* z, const float* mask, void* out,
+                                           const void* packed, int64_t B, int64_t N, int64_t c_z,
+                                           int64_t c, int outgoing, int residual, float eps_in,
+                                           float eps_out, int dtype, int64_t chunk_rows, void* ws,
+                                           size_t ws_bytes, void* stream) {
+  const char* name = chunk_rows ? "gtk_tri_mul_forward_chunked" : "gtk_tri_mul_forward";
+  GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL, "%s: bad dtype %d", name, dtype);
+  GTK_REQUIRE(trimul_shape_ok(c_z, c), GTK_EUNSUPPORTED,
+              "%s: c_z=%lld c=%lld unsupported (c_z in {32,64,128}, c in {32,64,128,256})", name,
+              (long long)c_z, (long long)c);
+  GTK_REQUIRE(B >= 0 && N >= 0 && N <= 16384, GTK_EINVAL, "%s: bad shape B=%lld N=%lld", name,
+              (long long)B, (long long)N);
+  GTK_REQUIRE(chunk_rows >= 0, GTK_EINVAL, "%s: chunk_rows=%lld < 0", name, (long long)chunk_rows);
+  if (B == 0 || N == 0) return GTK_OK;
+  GTK_REQUIRE(z && out && packed && ws, GTK_EINVAL, "%s: null pointer", name);
+  const size_t need = gtk_tri_mul_workspace_size_chunked(B, N, c_z, c, dtype, chunk_rows);
+  GTK_REQUIRE(ws_bytes >= need, GTK_EWORKSPACE, "%s: workspace %zu < %zu bytes", name, ws_bytes,
+              need);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == GTK_F32)
+    return fwd_trimul_any<float>(c_z, c, z, mask, out, packed, B, N, outgoing, residual, eps_in,
+                                 eps_out, ws, st, chunk_rows);
+  return fwd_trimul_any<bf16>(c_z, c, z, mask, out, packed, B, N, outgoing, residual, eps_in,
+                              eps_out, ws, st, chunk_rows);
 }
 
 extern "C" int gtk_tri_mul_forward(const void* z, const float* mask, void* out, const void* packed,
                                    int64_t B, int64_t N, int64_t c_z, int64_t c, int outgoing,
                                    int residual, float eps_in, float eps_out, int dtype, void* ws,
                                    size_t ws_bytes, void* stream) {
-  GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL, "gtk_tri_mul_forward: bad dtype %d", dtype);
-  GTK_REQUIRE(trimul_shape_ok(c_z, c), GTK_EUNSUPPORTED,
-              "gtk_tri_mul_forward: c_z=%lld c=%lld unsupported (c_z in {32,64,128}, c in {32,64,128,256})",
-              (long long)c_z, (long long)c);
-  GTK_REQUIRE(B >= 0 && N >= 0 && N <= 16384, GTK_EINVAL, "gtk_tri_mul_forward: bad shape B=%lld N=%lld",
-              (long long)B, (long long)N);
-  if (B == 0 || N == 0) return GTK_OK;
-  GTK_REQUIRE(z && out && packed && ws, GTK_EINVAL, "gtk_tri_mul_forward: null pointer");
-  const size_t need = gtk_tri_mul_workspace_size(B, N, c_z, c, dtype);
-  GTK_REQUIRE(ws_bytes >= need, GTK_EWORKSPACE, "gtk_tri_mul_forward: workspace %zu < %zu bytes",
-              ws_bytes, need);
-  hipStream_t st = (hipStream_t)stream;
-  if (dtype == GTK_F32)
-    return fwd_trimul_any<float>(c_z, c, z, mask, out, packed, B, N, outgoing, residual, eps_in,
-                                 eps_out, ws, st);
-  return fwd_trimul_any<bf16>(c_z, c, z, mask, out, packed, B, N, outgoing, residual, eps_in,
-                              eps_out, ws, st);
+  return gtk_tri_mul_forward_chunked(z, mask, out, packed, B, N, c_z, c, outgoing, residual,
+                                     eps_in, eps_out, dtype, 0, ws, ws_bytes, stream);
 }

@@ -12,6 +12,13 @@ forward runs inside ``_TriMulFunction``, whose backward is
 ``genie_tk._C.tri_mul_backward`` (gradients of z and every parameter).
 PyTorch path: ``_forward_pytorch``, the reference fallback semantics
 (triangle_mul.py:103-132).
+
+Memory-bounded mode (``forward(z, mask, chunk_size=R)``, an addition to the
+reference's signature): the output rows i run R at a time, the row chunking of
+``chunk_layer`` (utils.py:78-123) applied to the update.  On the kernels
+(inference) the workspace shrinks from three to one full set of c planes plus
+two R-row sets, with a bit-identical output; the PyTorch path holds x and its
+output projection for one chunk at a time.
 """
 from __future__ import annotations
 
@@ -96,16 +103,31 @@ class TriangleMultiplicativeUpdate(nn.Module):
         x = torch.matmul(permute_final_dims(a, 2, 1, 0), permute_final_dims(b, 2, 0, 1))
         return permute_final_dims(x, 1, 2, 0)
 
-    def _forward_pytorch(self, z: Tensor, mask: Optional[Tensor] = None) -> Tensor:
+    def _forward_pytorch(self, z: Tensor, mask: Optional[Tensor] = None,
+                         chunk_size: Optional[int] = None) -> Tensor:
         if mask is None:
             mask = z.new_ones(z.shape[:-1])
         m = mask.unsqueeze(-1)
         zn = self.layer_norm_in(z)
         a = self.linear_a_p(zn) * self.sigmoid(self.linear_a_g(zn)) * m
         b = self.linear_b_p(zn) * self.sigmoid(self.linear_b_g(zn)) * m
-        x = self._outgoing_matmul(a, b) if self._outgoing else self._incoming_matmul(a, b)
-        x = self.linear_z(self.layer_norm_out(x))
-        return x * self.sigmoid(self.linear_g(zn))
+        n = z.shape[-3]
+        if chunk_size is None or chunk_size >= n:
+            x = self._outgoing_matmul(a, b) if self._outgoing else self._incoming_matmul(a, b)
+            x = self.linear_z(self.layer_norm_out(x))
+            return x * self.sigmoid(self.linear_g(zn))
+        # output rows i in chunks: x[i, j] needs row i of a (outgoing: a[i, k];
+        # incoming: a[k, i]) against every row of b
+        outs = []
+        for s0 in range(0, n, chunk_size):
+            rows = slice(s0, s0 + chunk_size)
+            if self._outgoing:
+                x = self._outgoing_matmul(a[..., rows, :, :], b)
+            else:
+                x = self._incoming_matmul(a[..., :, rows, :], b)
+            x = self.linear_z(self.layer_norm_out(x))
+            outs.append(x * self.sigmoid(self.linear_g(zn[..., rows, :, :])))
+        return torch.cat(outs, dim=-3)
 
     # -- HIP kernel path ----------------------------------------------------
     def _kernel_supported(self, z: Tensor) -> bool:
@@ -136,33 +158,50 @@ class TriangleMultiplicativeUpdate(nn.Module):
         return self._packed.get(self._param_list(), fp32, self._pack)
 
     def _forward_cuda(self, z: Tensor, mask: Optional[Tensor] = None,
-                      residual: bool = False) -> Tensor:
-        """HIP path; returns the update (plus z when ``residual``)."""
+                      residual: bool = False, chunk_size: Optional[int] = None) -> Tensor:
+        """HIP path; returns the update (plus z when ``residual``).  With
+        ``chunk_size`` the output rows run that many at a time (the
+        memory-bounded mode, bit-identical output)."""
         C = _ext.require()
         zb, mb, lead = _dispatch.flatten_batch(z, mask)
         packed = self._packed_params(z.dtype == torch.float32)
         out = C.tri_mul_forward(zb, mb, packed, self.c_z, self.c_hidden, self._outgoing,
-                                residual, self.layer_norm_in.eps, self.layer_norm_out.eps)
+                                residual, self.layer_norm_in.eps, self.layer_norm_out.eps,
+                                int(chunk_size or 0))
         return out.reshape(*lead, *out.shape[1:])
 
-    def forward_residual(self, z: Tensor, mask: Optional[Tensor] = None) -> Tensor:
-        """z + forward(z, mask), with the add fused into the kernel's output."""
-        if (z.is_cuda and self._fused_requested and self.use_fused_kernel
-                and self._kernel_supported(z) and not _dispatch.needs_autograd(z, self)):
-            return self._forward_cuda(z, mask, residual=True)
-        return z + self.forward(z, mask)
+    @staticmethod
+    def _check_chunk(chunk_size: Optional[int]) -> None:
+        if chunk_size is not None and chunk_size < 1:
+            raise ValueError(f"chunk_size must be >= 1, got {chunk_size}")
 
-    def forward(self, z: Tensor, mask: Optional[Tensor] = None) -> Tensor:
-        """z: [*, N, N, c_z], mask: [*, N, N] -> update [*, N, N, c_z]."""
+    def forward_residual(self, z: Tensor, mask: Optional[Tensor] = None,
+                         chunk_size: Optional[int] = None) -> Tensor:
+        """z + forward(z, mask), with the add fused into the kernel's output."""
+        self._check_chunk(chunk_size)
+        if (z.is_cuda and self._fused_requested and self.use_fused_kernel and _CUDA_AVAILABLE
+                and self._kernel_supported(z) and not _dispatch.needs_autograd(z, self)):
+            return self._forward_cuda(z, mask, residual=True, chunk_size=chunk_size)
+        return z + self.forward(z, mask, chunk_size=chunk_size)
+
+    def forward(self, z: Tensor, mask: Optional[Tensor] = None,
+                chunk_size: Optional[int] = None) -> Tensor:
+        """z: [*, N, N, c_z], mask: [*, N, N] -> update [*, N, N, c_z].
+
+        ``chunk_size`` (an addition to the reference's signature, default off)
+        runs the output rows that many at a time.  On the kernels it applies
+        to inference; when autograd needs gradients a chunked call runs the
+        PyTorch path."""
+        self._check_chunk(chunk_size)
         if z.is_cuda and self._fused_requested:
             if not _CUDA_AVAILABLE:
                 _ext.missing(type(self).__name__)
             elif self.use_fused_kernel and self._kernel_supported(z):
                 if not _dispatch.needs_autograd(z, self):
-                    return self._forward_cuda(z, mask)
-                if self._backward_supported():
+                    return self._forward_cuda(z, mask, chunk_size=chunk_size)
+                if self._backward_supported() and chunk_size is None:
                     return _TriMulFunction.apply(self, z, mask, *self._param_list())
-        return self._forward_pytorch(z, mask)
+        return self._forward_pytorch(z, mask, chunk_size)
 
 
 class TriangleMultiplicationOutgoing(TriangleMultiplicativeUpdate):

@@ -182,6 +182,23 @@ int gtk_tri_mul_forward(const void* z, const float* mask, void* out, const void*
                         float eps_in, float eps_out, int dtype, void* workspace,
                         size_t workspace_bytes, void* stream);
 
+/* Memory-bounded form of gtk_tri_mul_forward: output rows i run chunk_rows at
+ * a time (rounded up to the contraction tile: 64, 128 or 256 rows), the
+ * row-chunking of chunk_layer src/genie_tk/utils.py:78-123 applied to the
+ * update's output row axis.  The workspace drops from 3 * B*c*Np^2 elements
+ * (Np = N rounded up to 64) to B*c*Np^2 + 2 * B*c*R*Np for R chunk rows: the
+ * b projections of every row stay resident, the a projections and the
+ * contraction of one chunk at a time.  Output bit-identical to
+ * gtk_tri_mul_forward.  chunk_rows = 0 (or >= N) runs unchunked.  Every
+ * shape and dtype of gtk_tri_mul_forward. */
+size_t gtk_tri_mul_workspace_size_chunked(int64_t B, int64_t N, int64_t c_z, int64_t c, int dtype,
+                                          int64_t chunk_rows);
+int gtk_tri_mul_forward_chunked(const void* z, const float* mask, void* out, const void* packed,
+                                int64_t B, int64_t N, int64_t c_z, int64_t c, int outgoing,
+                                int residual, float eps_in, float eps_out, int dtype,
+                                int64_t chunk_rows, void* workspace, size_t workspace_bytes,
+                                void* stream);
+
 /* Backward of gtk_tri_mul_forward (update only, no residual): given dL/dy,
  * writes dL/dz (element type dtype) and the gradient of every parameter
  * (fp32, the nn.Linear / LayerNorm layouts of gtk_tri_mul_weights).  The

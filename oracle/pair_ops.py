@@ -74,11 +74,19 @@ def tri_mul(z: np.ndarray, mask: Optional[np.ndarray], params: Params, outgoing:
     z = np.asarray(z, dtype=dtype)
     m = (np.ones(z.shape[:-1], dtype=dtype) if mask is None else np.asarray(mask, dtype=dtype))[..., None]
     zn = layer_norm(z, P("layer_norm_in.weight"), P("layer_norm_in.bias"), eps)
-    a = linear(zn, P("linear_a_p.weight"), P("linear_a_p.bias")) * sigmoid(
-        linear(zn, P("linear_a_g.weight"), P("linear_a_g.bias"))) * m
+    # Output rows i need a at pairs (i, k) (outgoing) or (k, i) (incoming)
+    # only, and b everywhere: with ``rows`` a is projected for those rows
+    # alone and enters the contraction already restricted.
+    if rows is None:
+        za, ma = zn, m
+    else:
+        sel = (slice(None), list(rows)) if outgoing else (slice(None), slice(None), list(rows))
+        za, ma = zn[sel], m[sel]
+    a = linear(za, P("linear_a_p.weight"), P("linear_a_p.bias")) * sigmoid(
+        linear(za, P("linear_a_g.weight"), P("linear_a_g.bias"))) * ma
     b = linear(zn, P("linear_b_p.weight"), P("linear_b_p.bias")) * sigmoid(
         linear(zn, P("linear_b_g.weight"), P("linear_b_g.bias"))) * m
-    x = contract(a, b, outgoing, rows)
+    x = contract(a, b, outgoing)
     zr = zn if rows is None else zn[:, list(rows)]
     x = linear(layer_norm(x, P("layer_norm_out.weight"), P("layer_norm_out.bias"), eps),
                P("linear_z.weight"), P("linear_z.bias"))

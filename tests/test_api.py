@@ -115,6 +115,28 @@ def test_tri_attn_row_chunks_pytorch_path(starting, chunk):
         mod(torch.from_numpy(x), chunk_size=0)
 
 
+@pytest.mark.parametrize("outgoing", [True, False])
+@pytest.mark.parametrize("chunk", [1, 3, 4, 64])
+def test_tri_mul_row_chunks_pytorch_path(outgoing, chunk):
+    """forward(chunk_size=R) runs the output rows R at a time and equals the
+    unchunked update (and the oracle)."""
+    cls = TriangleMultiplicationOutgoing if outgoing else TriangleMultiplicationIncoming
+    P = H.draw_params(H.tri_mul_shapes(16, 8), seed=31, ln_random=True, bias_random=True)
+    mod = _load(cls(16, 8), P)
+    z = _pair(2, 7, 16, seed=32)
+    m = torch.from_numpy(H.tail_mask(2, 7, [7, 5]))
+    with torch.no_grad():
+        full = mod(z, m)
+        got = mod(z, m, chunk_size=chunk)
+        res = mod.forward_residual(z, m, chunk_size=chunk)
+    torch.testing.assert_close(got, full, rtol=0, atol=1e-6)
+    torch.testing.assert_close(res, z + full, rtol=0, atol=1e-6)
+    ref = pair_ops.tri_mul(z.numpy(), m.numpy(), P, outgoing, dtype=np.float64)
+    np.testing.assert_allclose(got.numpy(), ref, rtol=0, atol=1e-5)
+    with pytest.raises(ValueError):
+        mod(z, m, chunk_size=0)
+
+
 def test_mask_default_is_all_ones():
     P = H.draw_params(H.tri_mul_shapes(16, 8), 5, bias_random=True)
     mod = _load(TriangleMultiplicationOutgoing(16, 8, use_fused_kernel=False), P)

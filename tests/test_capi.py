@@ -37,6 +37,7 @@ def lib():
                  "gtk_tri_attn_workspace_size", "gtk_triangle_attention_workspace_size",
                  "gtk_fused_layernorm_linear_workspace_size",
                  "gtk_tri_attn_workspace_size_chunked", "gtk_tri_mul_backward_workspace_size",
+                 "gtk_tri_mul_workspace_size_chunked",
                  "gtk_tri_attn_backward_workspace_size"):
         getattr(L, name).restype = sz
     L.gtk_triangle_mul_workspace_size.argtypes = [i64, i64, i64, ci]
@@ -51,11 +52,14 @@ def lib():
     L.gtk_tri_attn_backward.argtypes = [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, fp,
                                         ci, vp, sz, vp]
     L.gtk_tri_attn_workspace_size_chunked.argtypes = [i64, i64, i64, i64, i64, i64, ci]
+    L.gtk_tri_mul_workspace_size_chunked.argtypes = [i64, i64, i64, i64, ci, i64]
     L.gtk_triangle_attention_workspace_size.argtypes = [i64, i64, i64, i64, ci]
     L.gtk_fused_layernorm_linear_workspace_size.argtypes = [i64, i64, ci]
     L.gtk_layernorm.argtypes = [vp, vp, vp, vp, i64, i64, fp, ci, vp]
     L.gtk_tri_mul_forward.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, ci, ci, fp, fp, ci,
                                       vp, sz, vp]
+    L.gtk_tri_mul_forward_chunked.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, ci, ci, fp, fp,
+                                              ci, i64, vp, sz, vp]
     L.gtk_tri_attn_forward.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, ci, fp, fp,
                                        ci, vp, sz, vp]
     L.gtk_tri_attn_forward_chunked.argtypes = [vp, vp, vp, vp, i64, i64, i64, i64, i64, ci, ci,
@@ -99,6 +103,18 @@ def test_workspace_sizes(lib):
     assert lib.gtk_triangle_mul_workspace_size(2, 200, 64, GTK_F32) == 3 * (plane(2, 200, 64, 4) + 256)
     assert lib.gtk_tri_mul_workspace_size(1, 512, 128, 128, GTK_BF16) == 3 * (plane(1, 512, 128, 2) + 256)
     assert lib.gtk_triangle_mul_workspace_size(-1, 8, 16, GTK_F32) == 0
+    # tri-mul row chunks: b planes for every row, a and x planes for R rows,
+    # R = chunk_rows rounded up to the contraction tile (bf16: 256 rows when
+    # Np is a multiple of 256, else 128 or 64; fp32: 128 or 64)
+    tc = lambda N, c, dt, rows: lib.gtk_tri_mul_workspace_size_chunked(1, N, 128, c, dt, rows)
+    Np = lambda N: (N + 63) // 64 * 64
+    chunked = lambda N, c, e, R: c * Np(N) ** 2 * e + 2 * c * R * Np(N) * e + 3 * 256
+    assert tc(2048, 128, GTK_BF16, 0) == tc(2048, 128, GTK_BF16, 2048) == 3 * (plane(1, 2048, 128, 2) + 256)
+    assert tc(2048, 128, GTK_BF16, 1) == tc(2048, 128, GTK_BF16, 256) == chunked(2048, 128, 2, 256)
+    assert tc(2048, 128, GTK_BF16, 300) == chunked(2048, 128, 2, 512)
+    assert tc(300, 64, GTK_BF16, 100) == chunked(300, 64, 2, 128)    # Np = 320: 64-row tiles
+    assert tc(200, 64, GTK_F32, 100) == chunked(200, 64, 4, 128)     # Np = 256: 128-row tiles (fp32)
+    assert tc(2048, 128, GTK_BF16, -1) == 0 and tc(2048, 128, 7, 64) == 0
     # packed weights exist only for the shapes the kernels are built for
     assert lib.gtk_tri_mul_packed_size(128, 128, GTK_BF16) > 0
     assert lib.gtk_tri_mul_packed_size(128, 64, GTK_F32) > lib.gtk_tri_mul_packed_size(128, 64, GTK_BF16)
@@ -154,6 +170,18 @@ def test_bad_dtype_and_shapes_are_rejected(lib):
     rc = lib.gtk_tri_mul_forward(dummy, None, dummy, dummy, 1, 8, 128, 128, 1, 0, 1e-5, 1e-5,
                                  GTK_BF16, dummy, 10, None)
     assert rc == GTK_EWORKSPACE and "workspace" in _err(lib)
+    rc = lib.gtk_tri_mul_forward_chunked(None, None, None, None, 1, 8, 128, 128, 1, 0, 1e-5, 1e-5,
+                                         GTK_BF16, -3, None, 0, None)
+    assert rc == GTK_EINVAL and "chunk_rows" in _err(lib)
+    # 1.25 GiB (+ alignment) at 256 rows, 3 GiB unchunked: both checked before any launch
+    need = lib.gtk_tri_mul_workspace_size_chunked(1, 2048, 128, 128, GTK_BF16, 256)
+    assert need == (5 << 28) + 768
+    rc = lib.gtk_tri_mul_forward_chunked(dummy, None, dummy, dummy, 1, 2048, 128, 128, 1, 0, 1e-5,
+                                         1e-5, GTK_BF16, 256, dummy, need - 1, None)
+    assert rc == GTK_EWORKSPACE and "workspace" in _err(lib)
+    rc = lib.gtk_tri_mul_forward(dummy, None, dummy, dummy, 1, 2048, 128, 128, 1, 0, 1e-5, 1e-5,
+                                 GTK_BF16, dummy, need, None)
+    assert rc == GTK_EWORKSPACE
     rc = lib.gtk_tri_attn_forward(None, None, None, None, 1, 8, 128, 128, 8, 1, 0, 1e-5, 1e9,
                                   GTK_BF16, None, 0, None)
     assert rc == GTK_EUNSUPPORTED

@@ -338,6 +338,37 @@ def test_tri_mul_other_shapes(dname, outgoing, cz, c):
     chk(to_np(y_res), ref + z, "tri_mul other shape, residual")
 
 
+@pytest.mark.parametrize("dname,cz,c,N", [("bf16", 128, 128, 500), ("bf16", 128, 64, 300),
+                                          ("fp32", 128, 128, 300), ("bf16", 64, 32, 200)])
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_tri_mul_row_chunks(dname, cz, c, N, outgoing):
+    """Row chunks (the memory-bounded mode) are bit-identical to the unchunked
+    kernels, with and without the fused residual, for chunk sizes that round
+    to one tile, that do not divide N and whose last chunk is partial (bf16
+    N = 500: 256-row tiles; N = 300 and 200: 64/128-row tiles); sampled
+    chunked rows also match the oracle."""
+    log(f"tri_mul row chunks {dname} c_z={cz} c={c} N={N} out={outgoing}")
+    P = H.draw_params(H.tri_mul_shapes(cz, c), seed=N + c, ln_random=True, bias_random=True)
+    z = H.pair_input(1, N, cz, seed=N + 1)
+    m = H.tail_mask(1, N, [N - 11])
+    if dname == "bf16":
+        P, z = H.bf16_params(P), H.bf16_round(z)
+    mod = trimul_module(P, outgoing, DT[dname])
+    zd, md = _dev(z, DT[dname]), _dev(m, DT[dname])
+    with torch.no_grad():
+        full = mod._forward_cuda(zd, md)
+        full_res = mod._forward_cuda(zd, md, residual=True)
+        for chunk in (1, 100, 130):
+            y = mod(zd, md, chunk_size=chunk)
+            y_res = mod.forward_residual(zd, md, chunk_size=chunk)
+            torch.cuda.synchronize()
+            assert torch.equal(y, full), f"chunk {chunk}: differs from the unchunked update"
+            assert torch.equal(y_res, full_res), f"chunk {chunk}: residual differs"
+    rows = sorted(r for r in {0, 63, 64, 129, 256, N - 12, N - 1} if r < N)
+    ref = pair_ops.tri_mul(z, m, P, outgoing, dtype=np.float64, rows=rows)
+    (check_fp32 if dname == "fp32" else check_bf16)(to_np(y[:, rows]), ref, "tri_mul row chunks")
+
+
 def test_other_shapes_train_through_pytorch():
     """Shapes without backward kernels still train: autograd of the PyTorch
     path (the reference's own training path), gradients finite."""

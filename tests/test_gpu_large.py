@@ -1,6 +1,6 @@
-"""Large-N parity: the attention kernels that only run past N = 1024 (forward)
-and the backward kernels between N = 512 and N = 1024 and beyond, against the
-oracle on sampled rows.
+"""Large-N parity: the attention kernels that only run past N = 1024 (forward),
+the backward kernels between N = 512 and N = 1024 and beyond, and the
+triangle update's row chunks at N = 2048, against the oracle on sampled rows.
 
 A row of triangle attention is an independent problem once the shared
 triangle bias exists, so the oracle evaluates only the sampled rows
@@ -18,7 +18,7 @@ import torch
 
 from oracle import grads, pair_ops
 from tests import helpers as H
-from tests.gpu_common import check_bf16, log, to_np, triattn_module
+from tests.gpu_common import check_bf16, log, to_np, triattn_module, trimul_module
 from tests.test_gpu_grads import _check_grad
 
 pytestmark = pytest.mark.gpu
@@ -124,3 +124,30 @@ def test_tri_attn_backward_large(starting, N):
         assert prm.grad is not None and prm.grad.dtype == torch.bfloat16, name
         worst.append((_check_grad(to_np(prm.grad), g_ref[name], "bf16", name), name))
     log(f"  worst max|g - r| / max|r|: {max(worst)[0]:.2e} ({max(worst)[1]})")
+
+
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_tri_mul_row_chunks_2048(outgoing):
+    """The memory-bounded mode at N = 2048 (bf16, c_z = c = 128): 512-row
+    chunks (workspace 1.5 GiB instead of 3 GiB) bit-identical to the unchunked
+    update, sampled rows against the oracle (fp32 arithmetic on the
+    bf16-rounded inputs)."""
+    N = 2048
+    log(f"tri_mul row chunks N={N} outgoing={outgoing}")
+    x, m, _, L = _inputs(N)
+    P = H.bf16_params(H.draw_params(H.tri_mul_shapes(128, 128), seed=N + 7, ln_random=True,
+                                    bias_random=True))
+    rows = _rows(N, L)
+    mod = trimul_module(P, outgoing, torch.bfloat16)
+    zd = torch.from_numpy(x).to("cuda", torch.bfloat16)
+    md = torch.from_numpy(m).to("cuda")
+    with torch.no_grad():
+        y = mod(zd, md, chunk_size=512)
+        full = mod(zd, md)
+        torch.cuda.synchronize()
+        assert torch.equal(y, full), "512-row chunks differ from the unchunked update"
+        del full
+        got = to_np(y[:, rows])
+    del y
+    ref = pair_ops.tri_mul(x, m, P, outgoing, dtype=np.float32, rows=rows)
+    check_bf16(got, ref, f"tri_mul chunks N={N} outgoing={outgoing}")
