@@ -18,10 +18,24 @@
 // the 4c-wide hidden activation never leaves registers.  W1 and W2 (256 KiB
 // at c = 128) stream through a 4-stage LDS ring, 16 KiB per hidden tile,
 // shared by the 8 waves of a block; the block persists over row tiles.
+//
+// fp32 (and the backward's forward recompute) use a generic kernel of the
+// same algebra: one wave per 32-row tile, weight fragments read from L2.
+//
+// Backward (gtk_pair_transition_backward), the gradients torch autograd
+// gives the reference's PairTransition (pair_transform.py:79-84):
+//   h = W1 xn + b1, a = relu(h), y = W2 a + b2, xn = x_hat * g + beta
+//   da = W2^T dy, dh = da [h > 0], dxn = W1^T dh, dx = LN backward of dxn
+//   dW2 = sum dy a^T, db2 = sum dy, dW1 = sum dh xn^T, db1 = sum dh,
+//   dg = sum dxn x_hat, dbeta = sum dxn
+// One kernel per 32-row tile recomputes h, forms da, dh, dxn and dx, and
+// writes x_hat, dxn, dy, a and dh channel-major; the weight gradients are
+// then split-K products and row sums over those planes (grad_util.hpp).
 #include <algorithm>
 
 #include "capi_util.hpp"
 #include "common.hpp"
+#include "grad_util.hpp"
 #include "pack.hpp"
 
 namespace gtk {
@@ -31,43 +45,26 @@ namespace gtk {
 #endif
 
 // Packed parameters: W1 [hid][c] with the LayerNorm weight folded in
-// (standard fragment order), b1' = b1 + W1 beta, W2 [c][hid] in accumulator
-// order (pack_w2_kernel), b2; ln_* are fp32 copies used while packing.
-struct PtPacked {
-  bf16 *w1, *w2;
+// (standard fragment order), b1' = b1 + W1 beta, W2 [c][hid] for contraction
+// over the hidden units in the order the W1 accumulators produce them
+// (launch_pack_acc: chunk 2*ht + gp, lane half h, element e <-> hidden unit
+// ht*32 + 16*gp + 8*(e>>2) + 4*h + (e&3)), b2; ln_* are fp32 copies.
+template <typename T> struct PtPackedT {
+  T *w1, *w2;
   float *b1, *b2, *ln_w, *ln_b;
 };
+using PtPacked = PtPackedT<bf16>;
 
-static PtPacked carve_pt(Carve& cv, int c, int hid) {
-  PtPacked p;
-  p.w1 = cv.take<bf16>(packed_elems(hid, c));
-  p.w2 = cv.take<bf16>(packed_elems(c, hid));
+template <typename T>
+static PtPackedT<T> carve_pt(Carve& cv, int c, int hid) {
+  PtPackedT<T> p;
+  p.w1 = cv.take<T>(packed_elems(hid, c));
+  p.w2 = cv.take<T>(packed_elems(c, hid));
   p.b1 = cv.take<float>(hid);
   p.b2 = cv.take<float>(c);
   p.ln_w = cv.take<float>(c);
   p.ln_b = cv.take<float>(c);
   return p;
-}
-
-// W2 [c][hid] (nn.Linear layout) for contraction over the hidden units in the
-// order the W1 accumulators produce them: chunk ks2 = 2*ht + gp, lane l
-// (output row nt*32 + (l&31), half h = l>>5), element e <-> hidden unit
-//   ht*32 + 16*gp + 8*(e>>2) + 4*h + (e&3).
-template <typename Tin>
-__global__ void pack_w2_kernel(bf16* __restrict__ dst, const Tin* __restrict__ src, int c_out,
-                               int hid, int64_t total) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= total) return;
-  const int kch = hid / 16;
-  const int e = idx & 7;
-  const int l = (idx >> 3) & 63;
-  const int64_t rest = idx >> 9;
-  const int ks2 = (int)(rest % kch);
-  const int nt = (int)(rest / kch);
-  const int ht = ks2 >> 1, gp = ks2 & 1, h = l >> 5;
-  const int u = ht * 32 + 16 * gp + 8 * (e >> 2) + 4 * h + (e & 3);
-  const int o = nt * 32 + (l & 31);
-  dst[idx] = (bf16)(o < c_out ? to_f32(src[(int64_t)o * hid + u]) : 0.f);
 }
 
 // s_waitcnt vmcnt(min(after, K) * RPW): the immediate must be a constant.
@@ -268,16 +265,314 @@ __global__ __launch_bounds__(512) void pair_transition_bf16_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// Generic forward (fp32; any T): one wave per 32-row tile, weights from L2.
+//   h = W1 . x (accumulators: lane = row, registers = hidden units), relu +
+//   b1 straight into two B fragments, y += W2 . relu(h) per hidden tile.
+// ---------------------------------------------------------------------------
+template <typename T, int C, int HID>
+__global__ __launch_bounds__(256) void pair_transition_kernel(
+    const T* __restrict__ p, const float* __restrict__ mask, T* __restrict__ out, PtPackedT<T> w,
+    int64_t rows, int residual, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int half = lane >> 5;
+  const int t32 = lane & 31;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile * 32 >= rows) return;
+  const int64_t r = tile * 32 + t32;
+  const bool valid = r < rows;
+  const int64_t rr = valid ? r : 0;
+  RowHalf<C> rh;
+  load_row_half<T, C>(rh, p + rr * C, valid);
+  const f32x2 st = row_stats<C>(rh, eps);
+  Frag<T> xf[C / 16];
+  ln_to_frags<T, C>(xf, rh, st);
+  f32x16 y[C / 32];
+#pragma unroll
+  for (int nt = 0; nt < C / 32; ++nt) y[nt] = zero16();
+#pragma unroll 1
+  for (int ht = 0; ht < HID / 32; ++ht) {
+    const f32x16 h = row_gemm_tile<T, C, true>(xf, w.w1, ht);
+    float hv[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) hv[4 * g + q] = fmaxf(h[4 * g + q] + w.b1[ht * 32 + 8 * g + 4 * half + q], 0.f);
+    Frag<T> hf[2];
+    vals_to_frags<T>(hf, hv);
+#pragma unroll
+    for (int nt = 0; nt < C / 32; ++nt)
+#pragma unroll
+      for (int gp = 0; gp < 2; ++gp) {
+        Frag<T> wf;
+        load_wfrag<T>(wf, w.w2, nt, 2 * ht + gp, HID / 16);
+        mma(y[nt], wf, hf[gp]);
+      }
+  }
+  if (!valid) return;
+  const float m = mask ? mask[rr] : 1.f;
+#pragma unroll
+  for (int nt = 0; nt < C / 32; ++nt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int c0 = nt * 32 + 8 * g + 4 * half;
+      const f32x4 xr = residual ? load4f(p + rr * C + c0) : f32x4{0.f, 0.f, 0.f, 0.f};
+      float o[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) o[q] = (y[nt][4 * g + q] + w.b2[c0 + q] + xr[q]) * m;
+      store4(out + rr * C + c0, o[0], o[1], o[2], o[3]);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Backward, per 32-row tile (one wave): recompute x_hat and h, then per hidden
+// tile da = W2^T dy (w2t: W2^T in standard fragment order), dh = da [h > 0],
+// dxn += W1^T dh (w1t: W1^T, unfolded, for an operand from accumulators);
+// then the LayerNorm backward dx = rstd (g dxn - mean(g dxn) - x_hat
+// mean(g dxn x_hat)).  x_hat, dxn, dy (c rows) and a, dh (hid rows) go to
+// channel-major planes of `pitch` columns for the weight gradients.
+// ---------------------------------------------------------------------------
+template <typename T, int C, int HID>
+__global__ __launch_bounds__(256) void pair_transition_bwd_kernel(
+    const T* __restrict__ p, const T* __restrict__ dy, T* __restrict__ dp, T* __restrict__ cm_xh,
+    T* __restrict__ cm_dxn, T* __restrict__ cm_dy, T* __restrict__ cm_a, T* __restrict__ cm_dh,
+    PtPackedT<T> w, const T* __restrict__ w2t, const T* __restrict__ w1t, int64_t rows,
+    int64_t pitch, float eps) {
+  const int lane = threadIdx.x & 63;
+  const int half = lane >> 5;
+  const int t32 = lane & 31;
+  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (tile * 32 >= rows) return;
+  const int64_t r = tile * 32 + t32;
+  const bool valid = r < rows;
+  const int64_t rr = valid ? r : 0;
+  RowHalf<C> rh;
+  load_row_half<T, C>(rh, p + rr * C, valid);
+  const f32x2 st = row_stats<C>(rh, eps);
+  Frag<T> xf[C / 16];
+  ln_to_frags<T, C>(xf, rh, st);
+  Frag<T> dyf[C / 16];
+  {
+    RowHalf<C> dr;
+    load_row_half<T, C>(dr, dy + rr * C, valid);
+#pragma unroll
+    for (int ch = 0; ch < C / 16; ++ch) dyf[ch].set(dr.v + 8 * ch);
+  }
+  f32x16 dxn[C / 32];
+#pragma unroll
+  for (int nt = 0; nt < C / 32; ++nt) dxn[nt] = zero16();
+#pragma unroll 1
+  for (int ht = 0; ht < HID / 32; ++ht) {
+    const f32x16 h = row_gemm_tile<T, C, true>(xf, w.w1, ht);
+    const f32x16 da = row_gemm_tile<T, C, true>(dyf, w2t, ht);
+    float av[16], dhv[16];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float hb = h[4 * g + q] + w.b1[ht * 32 + 8 * g + 4 * half + q];
+        av[4 * g + q] = fmaxf(hb, 0.f);
+        dhv[4 * g + q] = hb > 0.f ? da[4 * g + q] : 0.f;
+      }
+    if (valid) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t o = (int64_t)(ht * 32 + 8 * g + 4 * half + q) * pitch + rr;
+          cm_a[o] = cvt<T>(av[4 * g + q]);
+          cm_dh[o] = cvt<T>(dhv[4 * g + q]);
+        }
+    }
+    Frag<T> dhf[2];
+    vals_to_frags<T>(dhf, dhv);
+#pragma unroll
+    for (int nt = 0; nt < C / 32; ++nt)
+#pragma unroll
+      for (int gp = 0; gp < 2; ++gp) {
+        Frag<T> wf;
+        load_wfrag<T>(wf, w1t, nt, 2 * ht + gp, HID / 16);
+        mma(dxn[nt], wf, dhf[gp]);
+      }
+  }
+  // LayerNorm backward in the accumulator layout (lane = row, channels
+  // nt*32 + 8g + 4*half + q); x_hat re-read in that layout
+  float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+  for (int nt = 0; nt < C / 32; ++nt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int c0 = nt * 32 + 8 * g + 4 * half;
+      const f32x4 xv = valid ? load4f(p + rr * C + c0) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float xh = (xv[q] - st[0]) * st[1];
+        const float dxh = w.ln_w[c0 + q] * dxn[nt][4 * g + q];
+        s1 += dxh;
+        s2 += dxh * xh;
+      }
+    }
+  s1 += xor32(s1);
+  s2 += xor32(s2);
+  const float m1 = s1 * (1.0f / C), m2 = s2 * (1.0f / C);
+  if (!valid) return;
+#pragma unroll
+  for (int nt = 0; nt < C / 32; ++nt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int c0 = nt * 32 + 8 * g + 4 * half;
+      const f32x4 xv = load4f(p + rr * C + c0);
+      const f32x4 dv = load4f(dy + rr * C + c0);
+      float o[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float xh = (xv[q] - st[0]) * st[1];
+        const float dxh = w.ln_w[c0 + q] * dxn[nt][4 * g + q];
+        o[q] = st[1] * (dxh - m1 - xh * m2);
+        const int64_t cm = (int64_t)(c0 + q) * pitch + rr;
+        cm_xh[cm] = cvt<T>(xh);
+        cm_dxn[cm] = cvt<T>(dxn[nt][4 * g + q]);
+        cm_dy[cm] = cvt<T>(dv[q]);
+      }
+      store4(dp + rr * C + c0, o[0], o[1], o[2], o[3]);
+    }
+}
+
+// dst[n][m] = sum_s part[s][m][n]: a weight-gradient product finished into
+// the transposed layout (dW2 [c][hid] from the product over hid x c).
+static __global__ void wgrad_finish_t_kernel(const float* __restrict__ part, int nsplit, int M, int Nn,
+                                             float* __restrict__ dst) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= M * Nn) return;
+  const int n = idx / M, m = idx % M;
+  float acc = 0.f;
+  for (int sp = 0; sp < nsplit; ++sp) acc += part[((int64_t)sp * M + m) * Nn + n];
+  dst[idx] = acc;
+}
+
 static bool pt_shape_ok(int64_t c, int64_t n) { return (c == 128 || c == 64) && n == 4; }
+
+template <typename T>
+static int pack_pt(const gtk_pair_transition_weights* w, int ci, int hid, void* packed, hipStream_t st) {
+  const int wd = w->dtype;
+  Carve cv(packed, SIZE_MAX);
+  PtPackedT<T> p = carve_pt<T>(cv, ci, hid);
+  int rc;
+  if ((rc = launch_to_f32(p.ln_w, w->ln_w, wd, ci, 1.f, 1.f, st))) return rc;
+  if ((rc = launch_to_f32(p.ln_b, w->ln_b, wd, ci, 1.f, 0.f, st))) return rc;
+  if ((rc = launch_pack<T>(p.w1, w->w1, wd, hid, ci, ci, 1, 1.f, st, p.ln_w))) return rc;
+  if ((rc = launch_fold_bias(p.b1, w->w1, w->b1, wd, p.ln_b, hid, ci, ci, 1, 1.f, st))) return rc;
+  if ((rc = launch_pack_acc<T>(p.w2, w->w2, wd, ci, hid, hid, 1, st))) return rc;
+  return launch_to_f32(p.b2, w->b2, wd, ci, 1.f, 0.f, st);
+}
+
+template <typename T, int C, int HID>
+static int launch_pt_generic(const void* p, const float* mask, void* out, const PtPackedT<T>& w,
+                             int64_t rows, int residual, float eps, hipStream_t st) {
+  const int64_t ntiles = (rows + 31) / 32;
+  GTK_REQUIRE((ntiles + 3) / 4 < (1ll << 31), GTK_EUNSUPPORTED, "pair transition: too many rows");
+  StageTimer timer("pair_transition", st);
+  pair_transition_kernel<T, C, HID><<<(unsigned)((ntiles + 3) / 4), 256, 0, st>>>(
+      (const T*)p, mask, (T*)out, w, rows, residual, eps);
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+// Backward workspace: the packed forward weights, W2^T and W1^T for the
+// backward products, five channel-major planes, the split-K partials and the
+// row sums.
+template <typename T> struct PtBwdWs {
+  void* packed;
+  T *w2t, *w1t, *cm_xh, *cm_dxn, *cm_dy, *cm_a, *cm_dh;
+  float *part1, *part2, *red, *sums_dh, *sums_dy, *sums_dxn, *dots_dxn;
+  int64_t pitch;
+};
+
+template <typename T>
+static PtBwdWs<T> carve_pt_bwd(Carve& cv, int64_t rows, int c, int hid) {
+  PtBwdWs<T> a;
+  a.pitch = round_up(rows, 64);
+  Carve pc(nullptr, SIZE_MAX);
+  carve_pt<T>(pc, c, hid);
+  a.packed = cv.take<char>((int64_t)pc.off);
+  a.w2t = cv.take<T>(packed_elems(hid, c));
+  a.w1t = cv.take<T>(packed_elems(c, hid));
+  a.cm_xh = cv.take<T>(c * a.pitch);
+  a.cm_dxn = cv.take<T>(c * a.pitch);
+  a.cm_dy = cv.take<T>(c * a.pitch);
+  a.cm_a = cv.take<T>(hid * a.pitch);
+  a.cm_dh = cv.take<T>(hid * a.pitch);
+  a.part1 = cv.take<float>(wgrad_part_floats(hid, c, a.pitch));
+  a.part2 = cv.take<float>(wgrad_part_floats(hid, c, a.pitch));
+  a.red = cv.take<float>((int64_t)2 * hid * kRowSegs);
+  a.sums_dh = cv.take<float>(hid);
+  a.sums_dy = cv.take<float>(c);
+  a.sums_dxn = cv.take<float>(c);
+  a.dots_dxn = cv.take<float>(c);
+  return a;
+}
+
+template <typename T, int C, int HID>
+static int bwd_pt(const void* p, const void* dy, const gtk_pair_transition_weights* wts, void* dp,
+                  const gtk_pair_transition_grads* gr, int64_t rows, float eps, void* ws,
+                  hipStream_t st) {
+  Carve cv(ws, SIZE_MAX);
+  PtBwdWs<T> a = carve_pt_bwd<T>(cv, rows, C, HID);
+  const int64_t pitch = a.pitch;
+  const int wd = wts->dtype;
+  int rc;
+  if ((rc = pack_pt<T>(wts, C, HID, a.packed, st))) return rc;
+  Carve pc(a.packed, SIZE_MAX);
+  const PtPackedT<T> w = carve_pt<T>(pc, C, HID);
+  // W2^T as [hid][c] (element (u, o) = W2[o][u]); W1^T as [c][hid] for dh
+  // taken from the accumulators
+  if ((rc = launch_pack<T>(a.w2t, wts->w2, wd, HID, C, 1, HID, 1.f, st))) return rc;
+  if ((rc = launch_pack_acc<T>(a.w1t, wts->w1, wd, C, HID, 1, C, st))) return rc;
+  {
+    const int64_t ntiles = (rows + 31) / 32;
+    GTK_REQUIRE((ntiles + 3) / 4 < (1ll << 31), GTK_EUNSUPPORTED, "pair transition backward: too many rows");
+    StageTimer timer("pair_transition_bwd", st);
+    pair_transition_bwd_kernel<T, C, HID><<<(unsigned)((ntiles + 3) / 4), 256, 0, st>>>(
+        (const T*)p, (const T*)dy, (T*)dp, a.cm_xh, a.cm_dxn, a.cm_dy, a.cm_a, a.cm_dh, w, a.w2t,
+        a.w1t, rows, pitch, eps);
+    GTK_LAUNCH_CHECK();
+  }
+  T* planes[5] = {a.cm_xh, a.cm_dxn, a.cm_dy, a.cm_a, a.cm_dh};
+  const int prow[5] = {C, C, C, HID, HID};
+  for (int k = 0; k < 5; ++k)
+    if ((rc = launch_zero_tail<T>(planes[k], prow[k], pitch, rows, st))) return rc;
+  if ((rc = launch_rowred<T>(a.cm_dh, nullptr, HID, pitch, rows, a.red, a.sums_dh, nullptr, st))) return rc;
+  if ((rc = launch_rowred<T>(a.cm_dy, nullptr, C, pitch, rows, a.red, a.sums_dy, nullptr, st))) return rc;
+  if ((rc = launch_rowred<T>(a.cm_dxn, a.cm_xh, C, pitch, rows, a.red, a.sums_dxn, a.dots_dxn, st)))
+    return rc;
+  {
+    StageTimer timer("pair_transition_bwd_wgrad", st);
+    if ((rc = launch_wgrad<T>(a.cm_dh, a.cm_xh, a.part1, HID, C, pitch, st))) return rc;
+    if ((rc = launch_wgrad<T>(a.cm_a, a.cm_dy, a.part2, HID, C, pitch, st))) return rc;
+  }
+  // dW1 = (sum dh x_hat^T) diag(g) + (sum dh) beta^T
+  if ((rc = launch_wgrad_finish(a.part1, HID, C, pitch, 0, HID, a.sums_dh, w.ln_w, w.ln_b, gr->w1, st)))
+    return rc;
+  if (gr->w2) {
+    wgrad_finish_t_kernel<<<(HID * C + 255) / 256, 256, 0, st>>>(a.part2, wgrad_plan(HID, pitch).nsplit,
+                                                                 HID, C, gr->w2);
+    GTK_LAUNCH_CHECK();
+  }
+  if ((rc = launch_copy_f32(gr->b1, a.sums_dh, HID, st))) return rc;
+  if ((rc = launch_copy_f32(gr->b2, a.sums_dy, C, st))) return rc;
+  if ((rc = launch_copy_f32(gr->ln_w, a.dots_dxn, C, st))) return rc;
+  return launch_copy_f32(gr->ln_b, a.sums_dxn, C, st);
+}
 
 }  // namespace gtk
 
 using namespace gtk;
 
 extern "C" size_t gtk_pair_transition_packed_size(int64_t c, int64_t n, int dtype) {
-  if (dtype != GTK_BF16 || !pt_shape_ok(c, n)) return 0;
+  if ((dtype != GTK_BF16 && dtype != GTK_F32) || !pt_shape_ok(c, n)) return 0;
   Carve cv(nullptr, SIZE_MAX);
-  carve_pt(cv, (int)c, (int)(c * n));
+  if (dtype == GTK_BF16) carve_pt<bf16>(cv, (int)c, (int)(c * n));
+  else carve_pt<float>(cv, (int)c, (int)(c * n));
   return cv.off;
 }
 
@@ -285,7 +580,8 @@ extern "C" int gtk_pair_transition_pack(const gtk_pair_transition_weights* w, in
                                         int dtype, void* packed, size_t packed_bytes,
                                         void* stream) {
   GTK_REQUIRE(w && packed, GTK_EINVAL, "gtk_pair_transition_pack: null pointer");
-  GTK_REQUIRE(dtype == GTK_BF16, GTK_EUNSUPPORTED, "gtk_pair_transition_pack: bf16 only");
+  GTK_REQUIRE(dtype == GTK_BF16 || dtype == GTK_F32, GTK_EINVAL, "gtk_pair_transition_pack: bad dtype %d",
+              dtype);
   GTK_REQUIRE(w->dtype == GTK_F32 || w->dtype == GTK_BF16, GTK_EINVAL,
               "gtk_pair_transition_pack: bad weight dtype %d", w->dtype);
   GTK_REQUIRE(pt_shape_ok(c, n), GTK_EUNSUPPORTED,
@@ -296,28 +592,15 @@ extern "C" int gtk_pair_transition_pack(const gtk_pair_transition_weights* w, in
   GTK_REQUIRE(packed_bytes >= need, GTK_EWORKSPACE, "gtk_pair_transition_pack: buffer %zu < %zu bytes",
               packed_bytes, need);
   hipStream_t st = (hipStream_t)stream;
-  const int ci = (int)c, hid = (int)(c * n), wd = w->dtype;
-  Carve cv(packed, SIZE_MAX);
-  PtPacked p = carve_pt(cv, ci, hid);
-  int rc;
-  if ((rc = launch_to_f32(p.ln_w, w->ln_w, wd, ci, 1.f, 1.f, st))) return rc;
-  if ((rc = launch_to_f32(p.ln_b, w->ln_b, wd, ci, 1.f, 0.f, st))) return rc;
-  if ((rc = launch_pack<bf16>(p.w1, w->w1, wd, hid, ci, ci, 1, 1.f, st, p.ln_w))) return rc;
-  if ((rc = launch_fold_bias(p.b1, w->w1, w->b1, wd, p.ln_b, hid, ci, ci, 1, 1.f, st))) return rc;
-  const int64_t total = packed_elems(ci, hid);
-  const unsigned blocks = (unsigned)((total + 255) / 256);
-  if (wd == GTK_F32)
-    pack_w2_kernel<float><<<blocks, 256, 0, st>>>(p.w2, (const float*)w->w2, ci, hid, total);
-  else
-    pack_w2_kernel<bf16><<<blocks, 256, 0, st>>>(p.w2, (const bf16*)w->w2, ci, hid, total);
-  GTK_LAUNCH_CHECK();
-  return launch_to_f32(p.b2, w->b2, wd, ci, 1.f, 0.f, st);
+  if (dtype == GTK_BF16) return pack_pt<bf16>(w, (int)c, (int)(c * n), packed, st);
+  return pack_pt<float>(w, (int)c, (int)(c * n), packed, st);
 }
 
 extern "C" int gtk_pair_transition_forward(const void* p, const float* mask, void* out,
                                            const void* packed, int64_t rows, int64_t c, int64_t n,
                                            int residual, float eps, int dtype, void* stream) {
-  GTK_REQUIRE(dtype == GTK_BF16, GTK_EUNSUPPORTED, "gtk_pair_transition_forward: bf16 only");
+  GTK_REQUIRE(dtype == GTK_BF16 || dtype == GTK_F32, GTK_EINVAL,
+              "gtk_pair_transition_forward: bad dtype %d", dtype);
   GTK_REQUIRE(pt_shape_ok(c, n), GTK_EUNSUPPORTED,
               "gtk_pair_transition_forward: c=%lld n=%lld unsupported (c in {64,128}, n == 4)",
               (long long)c, (long long)n);
@@ -327,7 +610,12 @@ extern "C" int gtk_pair_transition_forward(const void* p, const float* mask, voi
   GTK_REQUIRE(p && out && packed, GTK_EINVAL, "gtk_pair_transition_forward: null pointer");
   hipStream_t st = (hipStream_t)stream;
   Carve pc((void*)packed, SIZE_MAX);
-  const PtPacked w = carve_pt(pc, (int)c, (int)(c * n));
+  if (dtype == GTK_F32) {
+    const PtPackedT<float> w = carve_pt<float>(pc, (int)c, (int)(c * n));
+    if (c == 128) return launch_pt_generic<float, 128, 512>(p, mask, out, w, rows, residual, eps, st);
+    return launch_pt_generic<float, 64, 256>(p, mask, out, w, rows, residual, eps, st);
+  }
+  const PtPacked w = carve_pt<bf16>(pc, (int)c, (int)(c * n));
   const int64_t ntiles = (rows + 31) / 32;
   const int grid = (int)std::min<int64_t>(device_cus(), (ntiles + 7) / 8);
   StageTimer timer("pair_transition", st);
@@ -339,4 +627,44 @@ extern "C" int gtk_pair_transition_forward(const void* p, const float* mask, voi
         (const bf16*)p, mask, (bf16*)out, w, rows, residual, eps, ntiles);
   GTK_LAUNCH_CHECK();
   return GTK_OK;
+}
+
+extern "C" size_t gtk_pair_transition_backward_workspace_size(int64_t rows, int64_t c, int64_t n,
+                                                              int dtype) {
+  if ((dtype != GTK_BF16 && dtype != GTK_F32) || !pt_shape_ok(c, n) || rows < 0 ||
+      rows > ((int64_t)1 << 31))
+    return 0;
+  Carve cv(nullptr, SIZE_MAX);
+  if (dtype == GTK_BF16) carve_pt_bwd<bf16>(cv, rows, (int)c, (int)(c * n));
+  else carve_pt_bwd<float>(cv, rows, (int)c, (int)(c * n));
+  return cv.off;
+}
+
+extern "C" int gtk_pair_transition_backward(const void* p, const void* dy,
+                                            const gtk_pair_transition_weights* w, void* dp,
+                                            const gtk_pair_transition_grads* g, int64_t rows,
+                                            int64_t c, int64_t n, float eps, int dtype, void* ws,
+                                            size_t ws_bytes, void* stream) {
+  GTK_REQUIRE(dtype == GTK_BF16 || dtype == GTK_F32, GTK_EINVAL,
+              "gtk_pair_transition_backward: bad dtype %d", dtype);
+  GTK_REQUIRE(pt_shape_ok(c, n), GTK_EUNSUPPORTED,
+              "gtk_pair_transition_backward: c=%lld n=%lld unsupported (c in {64,128}, n == 4)",
+              (long long)c, (long long)n);
+  GTK_REQUIRE(rows >= 0 && rows <= ((int64_t)1 << 31), GTK_EINVAL,
+              "gtk_pair_transition_backward: bad rows %lld", (long long)rows);
+  GTK_REQUIRE(w && g, GTK_EINVAL, "gtk_pair_transition_backward: null weights or gradients");
+  GTK_REQUIRE(w->dtype == GTK_F32 || w->dtype == GTK_BF16, GTK_EINVAL,
+              "gtk_pair_transition_backward: bad weight dtype %d", w->dtype);
+  if (rows == 0) return GTK_OK;
+  GTK_REQUIRE(p && dy && dp && ws && w->w1 && w->w2 && w->b1 && w->b2 && w->ln_w && w->ln_b,
+              GTK_EINVAL, "gtk_pair_transition_backward: null pointer");
+  const size_t need = gtk_pair_transition_backward_workspace_size(rows, c, n, dtype);
+  GTK_REQUIRE(ws_bytes >= need, GTK_EWORKSPACE, "gtk_pair_transition_backward: workspace %zu < %zu bytes",
+              ws_bytes, need);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == GTK_F32)
+    return c == 128 ? bwd_pt<float, 128, 512>(p, dy, w, dp, g, rows, eps, ws, st)
+                    : bwd_pt<float, 64, 256>(p, dy, w, dp, g, rows, eps, ws, st);
+  return c == 128 ? bwd_pt<bf16, 128, 512>(p, dy, w, dp, g, rows, eps, ws, st)
+                  : bwd_pt<bf16, 64, 256>(p, dy, w, dp, g, rows, eps, ws, st);
 }

@@ -368,7 +368,8 @@ at::Tensor tri_mul_forward(const at::Tensor& z, const c10::optional<at::Tensor>&
 }
 
 // params: ln_w, ln_b, w1, b1, w2, b2 (PairTransition: layer_norm, linear_1, linear_2)
-at::Tensor pair_transition_pack(std::vector<at::Tensor> ps, int64_t c, int64_t n) {
+// fp32: pack for the fp32 forward (else bf16)
+at::Tensor pair_transition_pack(std::vector<at::Tensor> ps, int64_t c, int64_t n, bool fp32) {
   TORCH_CHECK(ps.size() == 6, "pair_transition_pack expects 6 parameter tensors");
   check_gpu(ps[2], "weights");
   check_all_on(ps, ps[2], "a parameter");
@@ -377,10 +378,11 @@ at::Tensor pair_transition_pack(std::vector<at::Tensor> ps, int64_t c, int64_t n
   w.dtype = common_param_dtype(ps);
   const void** slots[6] = {&w.ln_w, &w.ln_b, &w.w1, &w.b1, &w.w2, &w.b2};
   for (int i = 0; i < 6; ++i) *slots[i] = ptr_or_null(ps[i]);
-  const size_t bytes = gtk_pair_transition_packed_size(c, n, GTK_BF16);
+  const int dt = fp32 ? GTK_F32 : GTK_BF16;
+  const size_t bytes = gtk_pair_transition_packed_size(c, n, dt);
   TORCH_CHECK(bytes > 0, "genie_tk._C: pair_transition shape c=", c, " n=", n, " unsupported");
   auto packed = workspace(ps[2], bytes);
-  check_rc(gtk_pair_transition_pack(&w, c, n, GTK_BF16, packed.data_ptr(), packed.numel(),
+  check_rc(gtk_pair_transition_pack(&w, c, n, dt, packed.data_ptr(), packed.numel(),
                                     cur_stream(ps[2])));
   return packed;
 }
@@ -394,8 +396,8 @@ at::Tensor pair_transition_forward(const at::Tensor& p, const c10::optional<at::
   check_on(packed, p, "packed");
   const at::DeviceGuard guard(p.device());
   TORCH_CHECK(p.dim() >= 1 && p.size(-1) == c, "p must be [..., c]");
-  TORCH_CHECK(p.scalar_type() == at::kBFloat16, "pair_transition_forward: bf16 only");
   auto pc = p.contiguous();
+  const int dt = gtk_dtype_of(pc, "p");
   const int64_t rows = pc.numel() / c;
   at::Tensor mc;
   if (mask.has_value()) {
@@ -405,7 +407,52 @@ at::Tensor pair_transition_forward(const at::Tensor& p, const c10::optional<at::
   auto out = at::empty_like(pc);
   check_rc(gtk_pair_transition_forward(pc.data_ptr(), mask.has_value() ? mc.data_ptr<float>() : nullptr,
                                        out.data_ptr(), packed.data_ptr(), rows, c, n,
-                                       residual ? 1 : 0, (float)eps, GTK_BF16, cur_stream(pc)));
+                                       residual ? 1 : 0, (float)eps, dt, cur_stream(pc)));
+  return out;
+}
+
+// Backward of pair_transition_forward (no residual, no mask): returns [dp,
+// then the gradients of ln_w, ln_b, w1, b1, w2, b2 (fp32)].
+std::vector<at::Tensor> pair_transition_backward(const at::Tensor& p, const at::Tensor& dy,
+                                                 std::vector<at::Tensor> ps, int64_t c, int64_t n,
+                                                 double eps) {
+  TORCH_CHECK(ps.size() == 6, "pair_transition_backward expects 6 parameter tensors");
+  check_gpu(p, "p");
+  check_on(dy, p, "dy");
+  check_all_on(ps, p, "a parameter");
+  const at::DeviceGuard guard(p.device());
+  TORCH_CHECK(p.dim() >= 1 && p.size(-1) == c, "p must be [..., c]");
+  TORCH_CHECK(dy.sizes() == p.sizes() && dy.scalar_type() == p.scalar_type(),
+              "dy must match p in shape and dtype");
+  auto pc = p.contiguous();
+  auto dyc = dy.contiguous();
+  const int64_t rows = pc.numel() / c;
+  gtk_pair_transition_weights w;
+  w.dtype = common_param_dtype(ps);
+  const void** slots[6] = {&w.ln_w, &w.ln_b, &w.w1, &w.b1, &w.w2, &w.b2};
+  std::vector<at::Tensor> prm(6);
+  for (int i = 0; i < 6; ++i) {
+    if (ps[i].defined()) prm[i] = ps[i].contiguous();
+    *slots[i] = ptr_or_null(prm[i]);
+  }
+  const int dt = gtk_dtype_of(pc, "p");
+  std::vector<at::Tensor> out;
+  out.push_back(at::empty_like(pc));
+  gtk_pair_transition_grads g;
+  float** gs[6] = {&g.ln_w, &g.ln_b, &g.w1, &g.b1, &g.w2, &g.b2};
+  const int64_t hid = c * n;
+  const std::vector<std::vector<int64_t>> shapes = {{c}, {c}, {hid, c}, {hid}, {c, hid}, {c}};
+  for (int i = 0; i < 6; ++i) {
+    auto t = at::empty(shapes[i], pc.options().dtype(at::kFloat));
+    *gs[i] = t.data_ptr<float>();
+    out.push_back(t);
+  }
+  const size_t bytes = gtk_pair_transition_backward_workspace_size(rows, c, n, dt);
+  TORCH_CHECK(bytes > 0, "genie_tk._C: pair_transition backward shape c=", c, " n=", n, " unsupported");
+  auto ws = workspace(pc, bytes);
+  check_rc(gtk_pair_transition_backward(pc.data_ptr(), dyc.data_ptr(), &w, out[0].data_ptr(), &g,
+                                        rows, c, n, (float)eps, dt, ws.data_ptr(), ws.numel(),
+                                        cur_stream(pc)));
   return out;
 }
 
@@ -512,11 +559,14 @@ PYBIND11_MODULE(_C, m) {
         py::arg("mask"), py::arg("dy"), py::arg("params"), py::arg("c_in"), py::arg("c_h"),
         py::arg("no_heads"), py::arg("starting"), py::arg("eps") = 1e-5);
   m.def("pair_transition_pack", &pair_transition_pack, "Pack PairTransition parameters",
-        py::arg("params"), py::arg("c"), py::arg("n"));
+        py::arg("params"), py::arg("c"), py::arg("n"), py::arg("fp32") = false);
   m.def("pair_transition_forward", &pair_transition_forward,
         "Fused PairTransition forward: (residual ? p : 0) + transition(p), times mask",
         py::arg("p"), py::arg("mask"), py::arg("packed"), py::arg("c"), py::arg("n"),
         py::arg("residual") = false, py::arg("eps") = 1e-5);
+  m.def("pair_transition_backward", &pair_transition_backward,
+        "PairTransition backward: [dp, 6 parameter gradients (fp32)]", py::arg("p"), py::arg("dy"),
+        py::arg("params"), py::arg("c"), py::arg("n"), py::arg("eps") = 1e-5);
   m.def("tri_attn_pack", &tri_attn_pack, "Pack TriangleAttention parameters", py::arg("params"),
         py::arg("c_in"), py::arg("c_h"), py::arg("no_heads"), py::arg("fp32"));
   m.def("tri_attn_forward", &tri_attn_forward, "Fused TriangleAttention forward", py::arg("x"),

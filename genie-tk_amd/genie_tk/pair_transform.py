@@ -52,13 +52,42 @@ class DropoutColumnwise(_SharedDropout):
         super().__init__(p, -2)
 
 
+class _PairTransitionFunction(torch.autograd.Function):
+    """PairTransition on the HIP kernels, forward and backward.
+
+    The reference trains through torch autograd of its PyTorch path
+    (pair_transform.py:79-84); this computes the same gradients with
+    ``genie_tk._C.pair_transition_backward`` (the hidden activation is
+    recomputed from p; only p and the parameters are saved)."""
+
+    @staticmethod
+    def forward(ctx, module, p, *params):
+        ctx.module = module
+        ctx.save_for_backward(p, *params)
+        return module._run_kernel(p, None, False)
+
+    @staticmethod
+    def backward(ctx, dy):
+        p, *params = ctx.saved_tensors
+        mod = ctx.module
+        res = _ext.require().pair_transition_backward(
+            p, dy.reshape(p.shape).to(p.dtype), list(params), mod.c_p, mod.n, mod.layer_norm.eps)
+        dp = res[0] if ctx.needs_input_grad[1] else None
+        grads = [g.to(q.dtype) if ctx.needs_input_grad[2 + k] else None
+                 for k, (g, q) in enumerate(zip(res[1:], params))]
+        return (None, dp, *grads)
+
+
 class PairTransition(nn.Module):
     """LN -> Linear(c_p, n*c_p) -> ReLU -> Linear(n*c_p, c_p) (final init).
 
-    Kernel path (``use_fused_kernel``, bf16 GPU tensor, c_p in {64, 128},
-    n == 4, no autograd needed): ``genie_tk._C.pair_transition_forward``, one
-    gfx950 kernel for the whole MLP.  ``forward_residual_masked`` computes the
-    pair-stack update ``(p + transition(p)) * mask`` in the same kernel.
+    Kernel path (``use_fused_kernel``, bf16 or fp32 GPU tensor, c_p in
+    {64, 128}, n == 4): ``genie_tk._C.pair_transition_forward``, one gfx950
+    kernel for the whole MLP; when autograd needs gradients the same forward
+    runs inside ``_PairTransitionFunction``, whose backward is
+    ``genie_tk._C.pair_transition_backward``.  ``forward_residual_masked``
+    computes the pair-stack update ``(p + transition(p)) * mask`` in the same
+    kernel (inference).
     """
 
     def __init__(self, c_p: int, n: int = 4, use_fused_kernel: bool = True):
@@ -75,36 +104,46 @@ class PairTransition(nn.Module):
     def _forward_pytorch(self, p: Tensor) -> Tensor:
         return self.linear_2(self.relu(self.linear_1(self.layer_norm(p))))
 
-    def _use_kernel(self, p: Tensor) -> bool:
+    def _kernel_supported(self, p: Tensor) -> bool:
+        """Kernel shapes: c_p in {64, 128}, n == 4, bf16 or fp32."""
         if not (p.is_cuda and self._fused_requested):
             return False
         if _ext.C is None or not torch.cuda.is_available():
             _ext.missing(type(self).__name__)
             return False
-        return (p.dtype == torch.bfloat16 and p.dim() >= 1 and p.shape[-1] == self.c_p
-                and self.c_p in (64, 128) and self.n == 4 and self.layer_norm.elementwise_affine
-                and not _dispatch.needs_autograd(p, self))
+        return (p.dtype in (torch.bfloat16, torch.float32) and p.dim() >= 1
+                and p.shape[-1] == self.c_p and self.c_p in (64, 128) and self.n == 4
+                and self.layer_norm.elementwise_affine)
+
+    def _use_kernel(self, p: Tensor) -> bool:
+        """Inference on the kernels (no gradient needed)."""
+        return self._kernel_supported(p) and not _dispatch.needs_autograd(p, self)
+
+    def _param_list(self):
+        return [self.layer_norm.weight, self.layer_norm.bias, self.linear_1.weight,
+                self.linear_1.bias, self.linear_2.weight, self.linear_2.bias]
 
     def _run_kernel(self, p: Tensor, mask: Optional[Tensor], residual: bool) -> Tensor:
         C = _ext.require()
-        ps = [self.layer_norm.weight, self.layer_norm.bias, self.linear_1.weight,
-              self.linear_1.bias, self.linear_2.weight, self.linear_2.bias]
-        packed = self._packed.get(ps, False,
-                                  lambda prm, fp32: C.pair_transition_pack(prm, self.c_p, self.n))
+        fp32 = p.dtype == torch.float32
+        packed = self._packed.get(self._param_list(), fp32,
+                                  lambda prm, f: C.pair_transition_pack(prm, self.c_p, self.n, f))
         m = None if mask is None else mask.expand(p.shape[:-1])
         return C.pair_transition_forward(p, m, packed, self.c_p, self.n, residual,
                                          self.layer_norm.eps)
 
     def forward(self, p: Tensor, mask: Optional[Tensor] = None) -> Tensor:
-        if self._use_kernel(p):
-            return self._run_kernel(p, None, False)
+        if self._kernel_supported(p):
+            if not _dispatch.needs_autograd(p, self):
+                return self._run_kernel(p, None, False)
+            return _PairTransitionFunction.apply(self, p, *self._param_list())
         return self._forward_pytorch(p)
 
     def forward_residual_masked(self, p: Tensor, mask: Tensor) -> Tensor:
         """(p + transition(p)) * mask[..., None] (pair_transform.py:192-193)."""
         if self._use_kernel(p):
             return self._run_kernel(p, mask, True)
-        return (p + self._forward_pytorch(p)) * mask.unsqueeze(-1)
+        return (p + self.forward(p)) * mask.unsqueeze(-1)
 
 
 class PairTransformLayer(nn.Module):

@@ -303,8 +303,10 @@ int gtk_tri_attn_backward(const void* x, const float* mask, const void* dy,
  * update of PairTransformLayer.forward :180-193 (p = p + transition(p);
  * p = p * mask):
  *   out = (residual ? p : 0) + (relu(LN(p) W1^T + b1) W2^T + b2),  times mask
- * p, out: [rows][c] bf16; mask: [rows] float or NULL.  W1 [n c][c],
- * W2 [c][n c] (nn.Linear layout).  c in {64, 128}, n == 4, bf16 only.
+ * p, out: [rows][c] (dtype: GTK_BF16 or GTK_F32); mask: [rows] float or
+ * NULL.  W1 [n c][c], W2 [c][n c] (nn.Linear layout).  c in {64, 128},
+ * n == 4.  The packed weights are built for one dtype (pack and forward
+ * with the same dtype).
  * ------------------------------------------------------------------------ */
 typedef struct gtk_pair_transition_weights {
   int dtype;                 /* element type of every pointer below */
@@ -320,6 +322,25 @@ int gtk_pair_transition_pack(const gtk_pair_transition_weights* w, int64_t c, in
 int gtk_pair_transition_forward(const void* p, const float* mask, void* out, const void* packed,
                                 int64_t rows, int64_t c, int64_t n, int residual, float eps,
                                 int dtype, void* stream);
+
+/* Backward of PairTransition.forward (no residual, no mask): given dL/dy,
+ * writes dL/dp (element type dtype) and the gradient of every parameter
+ * (fp32, nn.Linear / LayerNorm layouts).  The reference has no backward
+ * kernel: its gradients are torch autograd over PairTransition.forward
+ * src/genie_tk/pair_transform.py:79-84, which this computes (h recomputed
+ * from p; the ReLU passes the gradient where its input is > 0).  w holds the
+ * raw parameters (packed into the workspace on each call).  Gradients are
+ * written, not accumulated; a NULL gradient pointer skips that output.
+ * rows <= 2^31. */
+typedef struct gtk_pair_transition_grads {
+  float *ln_w, *ln_b, *w1, *b1, *w2, *b2;
+} gtk_pair_transition_grads;
+
+size_t gtk_pair_transition_backward_workspace_size(int64_t rows, int64_t c, int64_t n, int dtype);
+int gtk_pair_transition_backward(const void* p, const void* dy, const gtk_pair_transition_weights* w,
+                                 void* dp, const gtk_pair_transition_grads* g, int64_t rows,
+                                 int64_t c, int64_t n, float eps, int dtype, void* workspace,
+                                 size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Per-kernel timing (instrumentation; no counterpart in the reference).

@@ -5,7 +5,8 @@ rule over the same operation sequence as the reference fallback:
   * TriangleMultiplicativeUpdate._forward_pytorch, triangle_mul.py:103-132
     (contractions :77-101);
   * TriangleAttention._forward_pytorch, triangle_attention.py:100-143, with
-    Attention.forward, primitives.py:114-178.
+    Attention.forward, primitives.py:114-178;
+  * PairTransition.forward, pair_transform.py:79-84.
 The reference has no backward of its own: its gradients are torch autograd
 over those lines.  These functions are pinned against central finite
 differences (float64) and against torch autograd of the PyTorch path in
@@ -186,4 +187,38 @@ def tri_attn_grad(x: np.ndarray, mask: Optional[np.ndarray], params: Params, sta
         xh, xr, P("layer_norm.weight"), dxn)
     if not starting:
         dx = dx.swapaxes(1, 2)
+    return dx, g
+
+
+def relu_bwd(h: np.ndarray, da: np.ndarray) -> np.ndarray:
+    """Gradient through relu(h): passed where h > 0 (torch's convention at 0)."""
+    return da * (h > 0)
+
+
+def pair_transition_grad(p: np.ndarray, params: Params, dy: np.ndarray, dtype=np.float64,
+                         eps: float = 1e-5,
+                         gate: Optional[np.ndarray] = None) -> Tuple[np.ndarray, Grads]:
+    """Backward of pair_ops.pair_transition (PairTransition.forward,
+    pair_transform.py:79-84: LayerNorm -> linear_1 -> ReLU -> linear_2) for
+    dL/dy over every leading axis.  The ReLU passes the gradient where its
+    input is > 0 (torch's convention at 0).
+
+    ``gate`` (boolean, the shape of the hidden activation) replaces the ReLU's
+    pass pattern h > 0, for comparing with an implementation whose h is
+    rounded differently: the derivative of ReLU is discontinuous, so a unit
+    with h within rounding distance of 0 passes its gradient in one and not
+    in the other."""
+    P = lambda k: _p(params, k, dtype)  # noqa: E731
+    x = np.asarray(p, dtype=dtype)
+    dy = np.asarray(dy, dtype=dtype)
+    xh, rstd = layer_norm_fwd(x, eps)
+    xn = xh * P("layer_norm.weight") + P("layer_norm.bias")
+    h = xn @ P("linear_1.weight").T + P("linear_1.bias")
+    a = np.maximum(h, 0)
+    g: Grads = {}
+    da, g["linear_2.weight"], g["linear_2.bias"] = linear_bwd(a, P("linear_2.weight"), dy)
+    dh = relu_bwd(h, da) if gate is None else da * gate
+    dxn, g["linear_1.weight"], g["linear_1.bias"] = linear_bwd(xn, P("linear_1.weight"), dh)
+    dx, g["layer_norm.weight"], g["layer_norm.bias"] = layer_norm_bwd(
+        xh, rstd, P("layer_norm.weight"), dxn)
     return dx, g

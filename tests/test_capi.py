@@ -37,7 +37,8 @@ def lib():
                  "gtk_tri_attn_workspace_size", "gtk_triangle_attention_workspace_size",
                  "gtk_fused_layernorm_linear_workspace_size",
                  "gtk_tri_attn_workspace_size_chunked", "gtk_tri_mul_backward_workspace_size",
-                 "gtk_tri_mul_workspace_size_chunked",
+                 "gtk_tri_mul_workspace_size_chunked", "gtk_pair_transition_packed_size",
+                 "gtk_pair_transition_backward_workspace_size",
                  "gtk_tri_attn_backward_workspace_size"):
         getattr(L, name).restype = sz
     L.gtk_triangle_mul_workspace_size.argtypes = [i64, i64, i64, ci]
@@ -53,6 +54,10 @@ def lib():
                                         ci, vp, sz, vp]
     L.gtk_tri_attn_workspace_size_chunked.argtypes = [i64, i64, i64, i64, i64, i64, ci]
     L.gtk_tri_mul_workspace_size_chunked.argtypes = [i64, i64, i64, i64, ci, i64]
+    L.gtk_pair_transition_packed_size.argtypes = [i64, i64, ci]
+    L.gtk_pair_transition_backward_workspace_size.argtypes = [i64, i64, i64, ci]
+    L.gtk_pair_transition_forward.argtypes = [vp, vp, vp, vp, i64, i64, i64, ci, fp, ci, vp]
+    L.gtk_pair_transition_backward.argtypes = [vp, vp, vp, vp, vp, i64, i64, i64, fp, ci, vp, sz, vp]
     L.gtk_triangle_attention_workspace_size.argtypes = [i64, i64, i64, i64, ci]
     L.gtk_fused_layernorm_linear_workspace_size.argtypes = [i64, i64, ci]
     L.gtk_layernorm.argtypes = [vp, vp, vp, vp, i64, i64, fp, ci, vp]
@@ -271,3 +276,43 @@ def test_torch_extension_exposes_reference_operators():
                  "triangle_attention_ending", "layernorm", "fused_layernorm_linear",
                  "tri_mul_pack", "tri_mul_forward", "tri_attn_pack", "tri_attn_forward"):
         assert hasattr(_ext.C, name), name
+
+
+class _PtWeights(ctypes.Structure):  # gtk_pair_transition_weights
+    _fields_ = [("dtype", ctypes.c_int)] + [(n, ctypes.c_void_p) for n in
+                                            ("ln_w", "ln_b", "w1", "b1", "w2", "b2")]
+
+
+class _PtGrads(ctypes.Structure):  # gtk_pair_transition_grads
+    _fields_ = [(n, ctypes.c_void_p) for n in ("ln_w", "ln_b", "w1", "b1", "w2", "b2")]
+
+
+def test_pair_transition_sizes_and_validation(lib):
+    """PairTransition: packed sizes for both dtypes, the backward workspace
+    (five channel-major planes at least), and argument checks that fail
+    before any launch."""
+    bf, f32 = lib.gtk_pair_transition_packed_size(128, 4, GTK_BF16), lib.gtk_pair_transition_packed_size(128, 4, GTK_F32)
+    assert 0 < bf < f32
+    assert lib.gtk_pair_transition_packed_size(96, 4, GTK_BF16) == 0
+    assert lib.gtk_pair_transition_packed_size(128, 2, GTK_F32) == 0
+    rows = 4050
+    pitch = (rows + 63) // 64 * 64
+    ws = lib.gtk_pair_transition_backward_workspace_size(rows, 128, 4, GTK_BF16)
+    assert ws >= (3 * 128 + 2 * 512) * pitch * 2
+    assert lib.gtk_pair_transition_backward_workspace_size(rows, 128, 4, GTK_F32) > ws
+    assert lib.gtk_pair_transition_backward_workspace_size(rows, 96, 4, GTK_BF16) == 0
+    assert lib.gtk_pair_transition_backward_workspace_size(-1, 128, 4, GTK_BF16) == 0
+    dummy = ctypes.c_void_p(16)  # never dereferenced: every check below fails first
+    w = _PtWeights(GTK_F32, *([16] * 6))
+    g = _PtGrads(*([None] * 6))
+    args = lambda rows, c, dt, wsb: (dummy, dummy, ctypes.byref(w), dummy, ctypes.byref(g), rows, c, 4,  # noqa: E731
+                                     1e-5, dt, dummy, wsb, None)
+    assert lib.gtk_pair_transition_backward(*args(rows, 128, 7, ws)) == GTK_EINVAL
+    assert lib.gtk_pair_transition_backward(*args(rows, 96, GTK_BF16, ws)) == GTK_EUNSUPPORTED
+    assert lib.gtk_pair_transition_backward(*args(rows, 128, GTK_BF16, ws - 1)) == GTK_EWORKSPACE
+    assert "workspace" in _err(lib)
+    assert lib.gtk_pair_transition_backward(*args(0, 128, GTK_BF16, 0)) == GTK_OK
+    assert lib.gtk_pair_transition_backward(None, None, ctypes.byref(w), None, ctypes.byref(g), 8, 128, 4,
+                                            1e-5, GTK_BF16, None, 0, None) == GTK_EINVAL
+    assert lib.gtk_pair_transition_forward(None, None, None, None, 0, 128, 4, 0, 1e-5, GTK_F32, None) == GTK_OK
+    assert lib.gtk_pair_transition_forward(None, None, None, None, 8, 128, 4, 0, 1e-5, 5, None) == GTK_EINVAL

@@ -8,6 +8,8 @@
   float64, a second, independent derivation of the reference's graph.
 * A planted mistake in a copy of the backward (the incoming contraction's
   operands swapped) is caught by the finite differences.
+* PairTransition (pair_transform.py:79-84): the same two pins, and a
+  dropped ReLU gate in the backward is caught.
 """
 import numpy as np
 import pytest
@@ -159,3 +161,54 @@ def test_tri_attn_grad_matches_torch_autograd(starting, dtype):
     np.testing.assert_allclose(xt.grad.double().numpy(), dx, **tol)
     for name, prm in mod.named_parameters():
         np.testing.assert_allclose(prm.grad.double().numpy(), g[name], err_msg=name, **tol)
+
+
+def _pt_case(seed=0, c=6, n=4):
+    P = H.draw_params(H.pair_transition_shapes(c, n), seed, ln_random=True, bias_random=True)
+    P = {k: v.astype(F64) for k, v in P.items()}
+    p = H.pair_input(2, 3, c, seed + 1).astype(F64) * 1.5 + 0.2
+    dy = np.random.default_rng(seed + 2).standard_normal(p.shape)
+    return P, p, dy
+
+
+def test_pair_transition_grad_finite_differences():
+    P, p, dy = _pt_case()
+    dp, g = grads.pair_transition_grad(p, P, dy)
+    loss = lambda pp, PP: float((pair_ops.pair_transition(pp, PP, dtype=F64) * dy).sum())  # noqa: E731
+    _fd_check(lambda pp: loss(pp, P), p, dp)
+    assert set(g) == set(P)
+    for key in P:
+        def f(v, key=key):
+            PP = dict(P)
+            PP[key] = v
+            return loss(p, PP)
+        _fd_check(f, P[key], g[key])
+
+
+def test_pair_transition_grad_matches_torch_autograd():
+    from genie_tk.pair_transform import PairTransition
+
+    P = H.draw_params(H.pair_transition_shapes(16, 4), 8, ln_random=True, bias_random=True)
+    p = H.pair_input(2, 5, 16, 9).astype(F64)
+    dy = np.random.default_rng(10).standard_normal(p.shape)
+    mod = PairTransition(16, 4, use_fused_kernel=False).double()
+    mod.load_state_dict(H.to_state_dict(P, dtype=torch.float64))
+    pt = torch.from_numpy(p).requires_grad_(True)
+    (mod(pt) * torch.from_numpy(dy)).sum().backward()
+    dp, g = grads.pair_transition_grad(p, P, dy)
+    np.testing.assert_allclose(pt.grad.numpy(), dp, rtol=1e-9, atol=1e-10)
+    for name, prm in mod.named_parameters():
+        np.testing.assert_allclose(prm.grad.numpy(), g[name], rtol=1e-9, atol=1e-10, err_msg=name)
+
+
+def test_planted_relu_gate_mistake_is_caught(monkeypatch):
+    """The backward with the ReLU gate dropped (dh = da) fails the finite
+    differences: the case has clipped hidden units."""
+    P, p, dy = _pt_case(seed=11)
+    xn = pair_ops.layer_norm(p, P["layer_norm.weight"], P["layer_norm.bias"])
+    assert (xn @ P["linear_1.weight"].T + P["linear_1.bias"] < 0).mean() > 0.2
+    monkeypatch.setattr(grads, "relu_bwd", lambda h, da: da)
+    dp, _ = grads.pair_transition_grad(p, P, dy)
+    monkeypatch.undo()
+    with pytest.raises(AssertionError):
+        _fd_check(lambda pp: float((pair_ops.pair_transition(pp, P, dtype=F64) * dy).sum()), p, dp)
