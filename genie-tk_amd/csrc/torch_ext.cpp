@@ -367,6 +367,48 @@ at::Tensor tri_mul_forward(const at::Tensor& z, const c10::optional<at::Tensor>&
   return out;
 }
 
+// The fp8 a/b storage experiment (bf16 z; packed from tri_mul_pack(fp32=False)).
+at::Tensor tri_mul_forward_fp8ab(const at::Tensor& z, const c10::optional<at::Tensor>& mask,
+                                 const at::Tensor& packed, int64_t c_z, int64_t c, bool outgoing,
+                                 bool residual, double eps_in, double eps_out) {
+  check_gpu(z, "z");
+  check_on(mask, z, "mask");
+  check_on(packed, z, "packed");
+  const at::DeviceGuard guard(z.device());
+  TORCH_CHECK(z.dim() == 4 && z.size(1) == z.size(2) && z.size(3) == c_z, "z must be [B, N, N, c_z]");
+  TORCH_CHECK(z.scalar_type() == at::kBFloat16, "tri_mul_forward_fp8ab: bf16 only");
+  auto zc = z.contiguous();
+  const int64_t B = zc.size(0), N = zc.size(1);
+  at::Tensor mc;
+  if (mask.has_value()) {
+    TORCH_CHECK(mask->numel() == B * N * N, "mask must be [B, N, N]");
+    mc = f32c(*mask);
+  }
+  auto out = at::empty_like(zc);
+  const size_t bytes = gtk_tri_mul_fp8ab_workspace_size(B, N, c_z, c);
+  TORCH_CHECK(bytes > 0, "tri_mul_forward_fp8ab: shape unsupported");
+  auto ws = workspace(zc, bytes);
+  check_rc(gtk_tri_mul_forward_fp8ab(zc.data_ptr(), mask.has_value() ? mc.data_ptr<float>() : nullptr,
+                                     out.data_ptr(), packed.data_ptr(), B, N, c_z, c, outgoing ? 1 : 0,
+                                     residual ? 1 : 0, (float)eps_in, (float)eps_out, ws.data_ptr(),
+                                     ws.numel(), cur_stream(zc)));
+  return out;
+}
+
+// a, b: uint8 [P, Np, Np] (fp8 E4M3 bytes) -> bf16 [P, Np, Np]
+at::Tensor tri_mul_contract_fp8(const at::Tensor& a, const at::Tensor& b) {
+  check_gpu(a, "a");
+  check_on(b, a, "b");
+  const at::DeviceGuard guard(a.device());
+  TORCH_CHECK(a.scalar_type() == at::kByte && b.scalar_type() == at::kByte, "a, b must be uint8");
+  TORCH_CHECK(a.dim() == 3 && a.size(1) == a.size(2) && a.sizes() == b.sizes(), "a, b must be [P, Np, Np]");
+  auto ac = a.contiguous(), bc = b.contiguous();
+  auto x = at::empty(ac.sizes(), ac.options().dtype(at::kBFloat16));
+  check_rc(gtk_tri_mul_contract_fp8(ac.data_ptr(), bc.data_ptr(), x.data_ptr(), ac.size(0), ac.size(1),
+                                    cur_stream(ac)));
+  return x;
+}
+
 // params: ln_w, ln_b, w1, b1, w2, b2 (PairTransition: layer_norm, linear_1, linear_2)
 // fp32: pack for the fp32 forward (else bf16)
 at::Tensor pair_transition_pack(std::vector<at::Tensor> ps, int64_t c, int64_t n, bool fp32) {
@@ -550,6 +592,13 @@ PYBIND11_MODULE(_C, m) {
         py::arg("z"), py::arg("mask"), py::arg("packed"), py::arg("c_z"), py::arg("c"),
         py::arg("outgoing"), py::arg("residual") = false, py::arg("eps_in") = 1e-5,
         py::arg("eps_out") = 1e-5, py::arg("chunk_rows") = 0);
+  m.def("tri_mul_forward_fp8ab", &tri_mul_forward_fp8ab,
+        "TriangleMultiplicativeUpdate forward with a and b stored in fp8 E4M3 (experiment)",
+        py::arg("z"), py::arg("mask"), py::arg("packed"), py::arg("c_z"), py::arg("c"),
+        py::arg("outgoing"), py::arg("residual") = false, py::arg("eps_in") = 1e-5,
+        py::arg("eps_out") = 1e-5);
+  m.def("tri_mul_contract_fp8", &tri_mul_contract_fp8,
+        "x[p] = a[p] . b[p]^T over fp8 E4M3 planes, bf16 out (experiment)", py::arg("a"), py::arg("b"));
   m.def("tri_mul_backward", &tri_mul_backward,
         "TriangleMultiplicativeUpdate backward: [dz, 16 parameter gradients (fp32)]",
         py::arg("z"), py::arg("mask"), py::arg("dy"), py::arg("params"), py::arg("c_z"),

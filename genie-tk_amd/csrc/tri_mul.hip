@@ -19,6 +19,7 @@
 // Np = N rounded up to 64; the prologue writes zeros for padded pairs so the
 // contraction needs no bounds checks.
 #include <algorithm>
+#include <type_traits>
 
 #include "capi_util.hpp"
 #include "common.hpp"
@@ -104,12 +105,23 @@ __global__ __launch_bounds__(256) void trimul_prologue_kernel(
 //     consecutive pairs of one channel and writes them as two 16-byte stores.
 //     The gate bias enters as a factor, 2^(u+b) = 2^u * 2^b, so the gate costs
 //     one FMA beside its two transcendental instructions.
+//     FP8 (the fp8 a/b storage experiment): the planes hold OCP fp8 E4M3
+//     values (v_cvt_pk_fp8_f32, round to nearest even; clamped to +-448
+//     first), one 16-byte store per lane and channel tile.
 // ---------------------------------------------------------------------------
-template <int CZ, int CH>
+template <int CZ, int CH, bool FP8 = false, bool RANGE = false>
 __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
-    const bf16* __restrict__ z, const float* __restrict__ mask, bf16* __restrict__ pa,
-    bf16* __restrict__ pb, TriMulPacked<bf16> w, int N, int Np, int outgoing, float eps,
-    int64_t ntiles, int r0, int nrows, int side_lo, int side_hi) {
+    const bf16* __restrict__ z, const float* __restrict__ mask,
+    std::conditional_t<FP8, uint8_t, bf16>* __restrict__ pa,
+    std::conditional_t<FP8, uint8_t, bf16>* __restrict__ pb, TriMulPacked<bf16> w, int N, int Np,
+    int outgoing, float eps, int64_t ntiles, int r0, int nrows, int side_lo, int side_hi) {
+  using OutT = std::conditional_t<FP8, uint8_t, bf16>;
+  if constexpr (!RANGE) {  // whole planes, both sides: the range is known here
+    r0 = 0;
+    nrows = Np;
+    side_lo = 0;
+    side_hi = 2;
+  }
   constexpr int WAVES = 8;
   constexpr int KCH = CZ / 16;
   constexpr int PE = (CH / 32) * KCH * 512;  // packed elements of one projection
@@ -204,7 +216,7 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
       const bf16* wg = wl[2 * side + 1];
       const float* bp = bl[side][0];
       const float* ebgs = bl[side][1];
-      bf16* dst = (side ? pb : pa) + (int64_t)b * CH * plane + (int64_t)fl * Np + vt * 32 + 16 * half;
+      OutT* dst = (side ? pb : pa) + (int64_t)b * CH * plane + (int64_t)fl * Np + vt * 32 + 16 * half;
 #pragma unroll 1
       for (int ct = 0; ct < CH / 32; ++ct) {
         Frag<bf16> wfp, wfg;
@@ -236,7 +248,7 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
 #pragma unroll
             for (int e = 0; e < 4; ++e) mk[4 * q + e] = m4[e];
           }
-          uint32_t pk[8];
+          uint32_t pk[8] = {};
 #pragma unroll
           for (int j = 0; j < 16; j += 2) {
             const float o0 = (ap[j] + bpc) *
@@ -244,11 +256,25 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
             const float o1 = (ap[j + 1] + bpc) *
                              __builtin_amdgcn_rcpf(fmaf(__builtin_amdgcn_exp2f(ag[j + 1]), ebg, 1.f)) *
                              mk[j + 1];
-            pk[j / 2] = pack_bf16x2(o0, o1);
+            if constexpr (FP8) {
+              const float c0 = __builtin_amdgcn_fmed3f(o0, -448.f, 448.f);
+              const float c1 = __builtin_amdgcn_fmed3f(o1, -448.f, 448.f);
+              // pairs j, j+1 -> bytes (j & 3), (j & 3) + 1 of dword j / 4
+              if ((j & 2) == 0)
+                pk[j / 4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c0, c1, (int)pk[j / 4], false);
+              else
+                pk[j / 4] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(c0, c1, (int)pk[j / 4], true);
+            } else {
+              pk[j / 2] = pack_bf16x2(o0, o1);
+            }
           }
           uint4* o = reinterpret_cast<uint4*>(dst + (int64_t)cc * plane + 32 * u);
-          o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-          o[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+          if constexpr (FP8) {
+            o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+          } else {
+            o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+            o[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+          }
         }
       }
     }
@@ -494,6 +520,136 @@ __global__ __launch_bounds__(64 * (TI / 64) * (TJ / 64)) void trimul_contract_bf
   barrier_only();
   bf16* X = px + pl * plane_ax;
   constexpr int RPI = 64 * NW / CPO;  // output rows per pass of the block
+  const int rr = (int)threadIdx.x / CPO, cc = (int)threadIdx.x % CPO;
+#pragma unroll
+  for (int r0 = 0; r0 < TI; r0 += RPI) {
+    const int r = r0 + rr;
+    const uint4 v = *reinterpret_cast<const uint4*>(tl + r * TJ + ((cc ^ (r & (CPO - 1))) << 3));
+    *reinterpret_cast<uint4*>(X + (int64_t)(i0 + r) * Np + j0 + cc * 8) = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// 2c. fp8 contraction (the fp8 a/b storage experiment): A and Bm planes in
+//     OCP fp8 E4M3 (1 byte per element), X in bf16.  The bf16 kernel's
+//     structure with stages of 128 k (128-byte panel rows, the same geometry
+//     and swizzle) and v_mfma_f32_32x32x64_f8f6f4: each lane feeds 32 bytes
+//     of its row per operand, and the A and B lanes of a half-wave read the
+//     same k bytes, so every product pairs A and B at the same k whatever the
+//     instruction's internal slot order.  Np % 256 == 0.
+// ---------------------------------------------------------------------------
+template <int TI, int TJ>
+__global__ __launch_bounds__(64 * (TI / 64) * (TJ / 64)) void trimul_contract_fp8_kernel(
+    const uint8_t* __restrict__ pa, const uint8_t* __restrict__ pb, bf16* __restrict__ px, int Np,
+    int64_t nplanes) {
+  constexpr int BK = 128, NS = 2;                   // k per stage = bytes per panel row
+  constexpr int NW = (TI / 64) * (TJ / 64);         // waves
+  constexpr int RPR = 1024 / BK;                    // panel rows per 1 KiB copy
+  constexpr int CPR = BK / 16;                      // 16-byte chunks per panel row
+  static_assert((TI / RPR) % NW == 0 && (TJ / RPR) % NW == 0, "copies split evenly");
+  typedef int v8i __attribute__((ext_vector_type(8)));
+  typedef int v4i __attribute__((ext_vector_type(4)));
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[NS * (TI + TJ) * BK];
+  uint8_t(*ra_l)[TI * BK] = reinterpret_cast<uint8_t(*)[TI * BK]>(ring);
+  uint8_t(*rb_l)[TJ * BK] = reinterpret_cast<uint8_t(*)[TJ * BK]>(ring + NS * TI * BK);
+
+  const int ti_n = Np / TI, tj_n = Np / TJ;
+  const int64_t total = (int64_t)ti_n * tj_n * nplanes;
+  const int64_t lin = xcd_remap((int64_t)blockIdx.x, total);
+  const int64_t pl = lin / ((int64_t)ti_n * tj_n);
+  const int trem = (int)(lin % ((int64_t)ti_n * tj_n));
+  const int i0 = (trem / tj_n) * TI;
+  const int j0 = (trem % tj_n) * TJ;
+  const int64_t plane = (int64_t)Np * Np;
+  const uint8_t* A = pa + pl * plane;
+  const uint8_t* Bm = pb + pl * plane;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int half = lane >> 5;
+  const int wi = (wave / (TJ / 64)) * 64;
+  const int wj = (wave % (TJ / 64)) * 64;
+  auto pswz = [](int r) { return (r ^ (r >> 3)) & 7; };
+
+  constexpr int RA = TI / RPR / NW, RB = TJ / RPR / NW;
+  const uint8_t* srcA[RA];
+  const uint8_t* srcB[RB];
+#pragma unroll
+  for (int u = 0; u < RA; ++u) {
+    const int row = RPR * (wave + u * NW) + lane / CPR;
+    srcA[u] = A + (int64_t)(i0 + row) * Np + 16 * ((lane % CPR) ^ pswz(row));
+  }
+#pragma unroll
+  for (int u = 0; u < RB; ++u) {
+    const int row = RPR * (wave + u * NW) + lane / CPR;
+    srcB[u] = Bm + (int64_t)(j0 + row) * Np + 16 * ((lane % CPR) ^ pswz(row));
+  }
+  auto issue = [&](int stage, int k0) {
+#pragma unroll
+    for (int u = 0; u < RA; ++u) g2lds16(srcA[u] + k0, &ra_l[stage][(wave + u * NW) * 1024]);
+#pragma unroll
+    for (int u = 0; u < RB; ++u) g2lds16(srcB[u] + k0, &rb_l[stage][(wave + u * NW) * 1024]);
+  };
+  // 32 bytes of panel row r: logical chunks 2m, 2m+1 (m = 2 kc + half)
+  auto frag = [&](const uint8_t* base, int r, int m) {
+    const v4i lo = *reinterpret_cast<const v4i*>(base + r * BK + 16 * ((2 * m) ^ pswz(r)));
+    const v4i hi = *reinterpret_cast<const v4i*>(base + r * BK + 16 * ((2 * m + 1) ^ pswz(r)));
+    return v8i{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < 2; ++y) acc[x][y] = zero16();
+
+  const int KT = Np / BK;  // Np % 256 == 0: KT >= 2
+  issue(0, 0);
+  for (int kt = 0; kt < KT; ++kt) {
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): this wave's copies of stage kt landed
+    barrier_only();  // stage kt visible to every wave; stage kt-1 fully consumed
+    if (kt + 1 < KT) issue((kt + 1) % NS, (kt + 1) * BK);
+    const uint8_t* sa = ra_l[kt % NS];
+    const uint8_t* sb = rb_l[kt % NS];
+    v8i fa[BK / 64][2], fb[BK / 64][2];
+#pragma unroll
+    for (int kc = 0; kc < BK / 64; ++kc)
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        fa[kc][x] = frag(sa, wi + x * 32 + (lane & 31), 2 * kc + half);
+        fb[kc][x] = frag(sb, wj + x * 32 + (lane & 31), 2 * kc + half);
+      }
+#pragma unroll
+    for (int kc = 0; kc < BK / 64; ++kc)
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y)  // rows j, cols i; formats: fp8 E4M3 for both operands
+          acc[x][y] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb[kc][y], fa[kc][x], acc[x][y],
+                                                                      0, 0, 0, 0, 0, 0);
+  }
+
+  // the bf16 kernel's output path: transpose through the ring, whole rows out
+  constexpr int CPO = TJ / 8;
+  static_assert(TI * TJ * 2 <= NS * (TI + TJ) * BK, "output tile fits in the ring");
+  static_assert(CPO >= 16 && (64 * NW) % CPO == 0 && TI % (64 * NW / CPO) == 0, "store split");
+  bf16* tl = reinterpret_cast<bf16*>(ring);
+  barrier_only();
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    const int il = wi + x * 32 + (lane & 31);
+#pragma unroll
+    for (int y = 0; y < 2; ++y)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int jl = wj + y * 32 + 8 * g + 4 * half;
+        store4(tl + il * TJ + ((((jl >> 3) ^ (il & (CPO - 1))) << 3) | (jl & 7)), acc[x][y][4 * g + 0],
+               acc[x][y][4 * g + 1], acc[x][y][4 * g + 2], acc[x][y][4 * g + 3]);
+      }
+  }
+  barrier_only();
+  bf16* X = px + pl * plane;
+  constexpr int RPI = 64 * NW / CPO;
   const int rr = (int)threadIdx.x / CPO, cc = (int)threadIdx.x % CPO;
 #pragma unroll
   for (int r0 = 0; r0 < TI; r0 += RPI) {
@@ -998,9 +1154,15 @@ static int launch_trimul_prologue(const void* z, const float* mask, const TriMul
   if constexpr (trimul_fast<T, CZ, CH>()) {
     const int grid = (int)std::min<int64_t>(device_cus(), (ptiles / 2 + 7) / 8);
     StageTimer timer("trimul_prologue", st);
-    trimul_prologue_bf16_kernel<CZ, CH><<<grid, 512, 0, st>>>(
-        (const bf16*)z, mask, (bf16*)pa, (bf16*)pb, w, (int)N, Np, outgoing, eps_in, ptiles, r0,
-        nrows, side_lo, side_hi);
+    const bool whole = r0 == 0 && nrows == Np && side_lo == 0 && side_hi == 2;
+    if (whole)
+      trimul_prologue_bf16_kernel<CZ, CH><<<grid, 512, 0, st>>>(
+          (const bf16*)z, mask, (bf16*)pa, (bf16*)pb, w, (int)N, Np, outgoing, eps_in, ptiles, 0,
+          Np, 0, 2);
+    else
+      trimul_prologue_bf16_kernel<CZ, CH, false, true><<<grid, 512, 0, st>>>(
+          (const bf16*)z, mask, (bf16*)pa, (bf16*)pb, w, (int)N, Np, outgoing, eps_in, ptiles, r0,
+          nrows, side_lo, side_hi);
   } else {
     StageTimer timer("trimul_prologue", st);
     trimul_prologue_kernel<T, CZ, CH><<<(unsigned)((ptiles + 3) / 4), 256, 0, st>>>(
@@ -1084,6 +1246,47 @@ static int fwd_trimul(const void* z, const float* mask, void* out, const void* p
       return rc;
   }
   return GTK_OK;
+}
+
+// fp8 a/b experiment: planes padded to Np = N rounded up to 256 (the fp8
+// contraction's tile); the prologue writes fp8 a and b, the contraction bf16
+// x, and the bf16 epilogue finishes as in the bf16 forward.
+static int64_t fp8_np(int64_t N) { return round_up(N, 256); }
+
+static int launch_contract_fp8(const uint8_t* pa, const uint8_t* pb, bf16* px, int Np, int64_t nplanes,
+                               hipStream_t st) {
+  GTK_REQUIRE(Np % 256 == 0, GTK_EINVAL, "fp8 contraction: Np=%d not a multiple of 256", Np);
+  const int64_t blocks = (int64_t)(Np / 256) * (Np / 256) * nplanes;
+  GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "contraction grid too large");
+  StageTimer timer("trimul_contract_fp8", st);
+  trimul_contract_fp8_kernel<256, 256><<<(unsigned)blocks, 1024, 0, st>>>(pa, pb, px, Np, nplanes);
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+template <int CZ, int CH>
+static int fwd_trimul_fp8(const void* z, const float* mask, void* out, const void* packed, int64_t B,
+                          int64_t N, int outgoing, int residual, float eps_in, float eps_out, void* ws,
+                          hipStream_t st) {
+  Carve pc((void*)packed, SIZE_MAX);
+  TriMulPacked<bf16> w = carve_trimul<bf16>(pc, CZ, CH);
+  const int Np = (int)fp8_np(N);
+  const int64_t pe = B * CH * (int64_t)Np * Np;
+  Carve cv(ws, SIZE_MAX);
+  uint8_t* pa = cv.take<uint8_t>(pe);
+  uint8_t* pb = cv.take<uint8_t>(pe);
+  bf16* px = cv.take<bf16>(pe);
+  {
+    const int64_t ptiles = B * (int64_t)Np * (Np / 32);
+    const int grid = (int)std::min<int64_t>(device_cus(), (ptiles / 2 + 7) / 8);
+    StageTimer timer("trimul_prologue_fp8", st);
+    trimul_prologue_bf16_kernel<CZ, CH, true><<<grid, 512, 0, st>>>(
+        (const bf16*)z, mask, pa, pb, w, (int)N, Np, outgoing, eps_in, ptiles, 0, Np, 0, 2);
+    GTK_LAUNCH_CHECK();
+  }
+  int rc;
+  if ((rc = launch_contract_fp8(pa, pb, px, Np, B * CH, st))) return rc;
+  return launch_trimul_epilogue<bf16, CZ, CH>(z, px, out, w, B, N, Np, residual, eps_in, eps_out, st);
 }
 
 template <typename T, int CZ, int CH>
@@ -1233,4 +1436,39 @@ extern "C" int gtk_tri_mul_forward(const void* z, const float* mask, void* out, 
                                    size_t ws_bytes, void* stream) {
   return gtk_tri_mul_forward_chunked(z, mask, out, packed, B, N, c_z, c, outgoing, residual,
                                      eps_in, eps_out, dtype, 0, ws, ws_bytes, stream);
+}
+
+extern "C" size_t gtk_tri_mul_fp8ab_workspace_size(int64_t B, int64_t N, int64_t c_z, int64_t c) {
+  if (B < 0 || N < 0 || N > 16384 || c_z != 128 || (c != 64 && c != 128)) return 0;
+  const int64_t Np = fp8_np(N);
+  return (size_t)(B * c * Np * Np) * 4 + 3 * 256;  // a, b (1 byte), x (2 bytes)
+}
+
+extern "C" int gtk_tri_mul_forward_fp8ab(const void* z, const float* mask, void* out,
+                                         const void* packed, int64_t B, int64_t N, int64_t c_z,
+                                         int64_t c, int outgoing, int residual, float eps_in,
+                                         float eps_out, void* ws, size_t ws_bytes, void* stream) {
+  GTK_REQUIRE(c_z == 128 && (c == 64 || c == 128), GTK_EUNSUPPORTED,
+              "gtk_tri_mul_forward_fp8ab: c_z=%lld c=%lld unsupported (c_z 128, c in {64, 128})",
+              (long long)c_z, (long long)c);
+  GTK_REQUIRE(B >= 0 && N >= 0 && N <= 16384, GTK_EINVAL, "gtk_tri_mul_forward_fp8ab: bad shape");
+  if (B == 0 || N == 0) return GTK_OK;
+  GTK_REQUIRE(z && out && packed && ws, GTK_EINVAL, "gtk_tri_mul_forward_fp8ab: null pointer");
+  const size_t need = gtk_tri_mul_fp8ab_workspace_size(B, N, c_z, c);
+  GTK_REQUIRE(ws_bytes >= need, GTK_EWORKSPACE, "gtk_tri_mul_forward_fp8ab: workspace %zu < %zu bytes",
+              ws_bytes, need);
+  hipStream_t st = (hipStream_t)stream;
+  if (c == 128)
+    return fwd_trimul_fp8<128, 128>(z, mask, out, packed, B, N, outgoing, residual, eps_in, eps_out, ws, st);
+  return fwd_trimul_fp8<128, 64>(z, mask, out, packed, B, N, outgoing, residual, eps_in, eps_out, ws, st);
+}
+
+extern "C" int gtk_tri_mul_contract_fp8(const void* a, const void* b, void* x, int64_t nplanes,
+                                        int64_t Np, void* stream) {
+  GTK_REQUIRE(nplanes >= 0 && Np >= 0 && Np % 256 == 0 && Np <= 16384, GTK_EINVAL,
+              "gtk_tri_mul_contract_fp8: Np=%lld must be a multiple of 256 (<= 16384)", (long long)Np);
+  if (nplanes == 0 || Np == 0) return GTK_OK;
+  GTK_REQUIRE(a && b && x, GTK_EINVAL, "gtk_tri_mul_contract_fp8: null pointer");
+  return launch_contract_fp8((const uint8_t*)a, (const uint8_t*)b, (bf16*)x, (int)Np, nplanes,
+                             (hipStream_t)stream);
 }

@@ -199,6 +199,27 @@ int gtk_tri_mul_forward_chunked(const void* z, const float* mask, void* out, con
                                 int64_t chunk_rows, void* workspace, size_t workspace_bytes,
                                 void* stream);
 
+/* Experiment (fp8 a/b storage, outside the bf16 parity contract): the
+ * forward of gtk_tri_mul_forward with the gated projections a and b stored
+ * as OCP fp8 E4M3 (1 byte per element instead of 2, no scaling; values
+ * clamped to +-448) and contracted on the fp8 matrix cores
+ * (v_mfma_f32_32x32x64_f8f6f4, fp32 accumulation); x and the epilogue stay
+ * bf16.  Its error against the fp32 reference is that of 3-bit mantissas in
+ * a and b, well beyond the bf16 tolerance; it is reported beside the bf16
+ * path, not as it.  bf16 z, c_z = 128, c in {64, 128}; planes padded to N
+ * rounded up to 256.  packed: gtk_tri_mul_pack with GTK_BF16.  No
+ * counterpart in the reference (whose large-N path is chunk_layer,
+ * src/genie_tk/utils.py:78-123). */
+size_t gtk_tri_mul_fp8ab_workspace_size(int64_t B, int64_t N, int64_t c_z, int64_t c);
+int gtk_tri_mul_forward_fp8ab(const void* z, const float* mask, void* out, const void* packed,
+                              int64_t B, int64_t N, int64_t c_z, int64_t c, int outgoing,
+                              int residual, float eps_in, float eps_out, void* workspace,
+                              size_t workspace_bytes, void* stream);
+/* Its contraction alone: x[p][i][j] = sum_k a[p][i][k] * b[p][j][k] over
+ * nplanes planes of Np x Np fp8 E4M3 bytes, x in bf16.  Np % 256 == 0. */
+int gtk_tri_mul_contract_fp8(const void* a, const void* b, void* x, int64_t nplanes, int64_t Np,
+                             void* stream);
+
 /* Backward of gtk_tri_mul_forward (update only, no residual): given dL/dy,
  * writes dL/dz (element type dtype) and the gradient of every parameter
  * (fp32, the nn.Linear / LayerNorm layouts of gtk_tri_mul_weights).  The

@@ -120,3 +120,26 @@ def bf16_round(x: np.ndarray) -> np.ndarray:
 
 def bf16_params(params: Dict[str, np.ndarray]) -> Dict[str, np.ndarray]:
     return {k: bf16_round(v) for k, v in params.items()}
+
+
+# ---------------------------------------------------------------------------
+# OCP fp8 E4M3 (the "fn" variant: bias 7, 3 mantissa bits, no infinity,
+# S.1111.111 = NaN, largest finite 448), for the fp8 a/b storage experiment.
+# ---------------------------------------------------------------------------
+def e4m3_decode(b: np.ndarray) -> np.ndarray:
+    """Bytes -> float64 values (NaN codes give NaN)."""
+    b = np.asarray(b, dtype=np.uint8).astype(np.int64)
+    s = np.where(b & 0x80, -1.0, 1.0)
+    e = (b >> 3) & 0xF
+    m = b & 0x7
+    val = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1 + m / 8.0) * 2.0 ** (e - 7))
+    return np.where((b & 0x7F) == 0x7F, np.nan, s * val)
+
+
+def e4m3_round(x: np.ndarray) -> np.ndarray:
+    """Nearest E4M3 value (ties to even), after clamping to +-448; float64."""
+    x = np.clip(np.asarray(x, dtype=np.float64), -448.0, 448.0)
+    a = np.abs(x)
+    e = np.floor(np.log2(np.maximum(a, 2.0 ** -6)))  # subnormals share the 2^-6 binade's step
+    q = 2.0 ** (e - 3)                                # spacing of the values in that binade
+    return np.sign(x) * np.round(a / q) * q           # np.round: ties to even
