@@ -701,6 +701,17 @@ def main() -> int:
         flush_buf = torch.zeros(1 << 30, dtype=torch.uint8, device=dev)
         ln_ms_cold = statistics.median(event_time_ms(torch, ops["layernorm"], reps,
                                                      flush=lambda: flush_buf.sum()))
+        # the fp8 a/b storage experiment (outside the bf16 contract): the
+        # tri-mul outgoing forward with a and b in fp8 E4M3, against the bf16
+        # kernels' output (informational)
+        tmo = mods["tri_mul_out"]
+        pk8 = tmo._packed_params(False)
+        fp8_fwd = lambda: C.tri_mul_forward_fp8ab(z, mask, pk8, C_Z, tmo.c_hidden, True)  # noqa: E731
+        fp8_ms = statistics.median(event_time_ms(torch, fp8_fwd, reps))
+        y8, y16 = fp8_fwd().float(), tmo(z, mask).float()
+        fp8_rel = ((y8 - y16).norm() / y16.norm()).item()
+        fp8_max = (y8 - y16).abs().max().item()
+        del y8, y16
         # the rest of the pair-stack block on the kernels (informational)
         layer = build_pair_layer(torch, dev)
         trans_ms = statistics.median(event_time_ms(
@@ -806,6 +817,14 @@ def main() -> int:
         "frac_hbm_cold": round(ln2b / (ln2_ms_cold * 1e-3) / PEAK_HBM_BYTES, 4),
     }
 
+    per_op["tri_mul_out_fp8ab"] = {
+        "ms": round(fp8_ms, 4), "bf16_ms": round(op_ms["tri_mul_out"], 4),
+        "speedup_vs_bf16": round(op_ms["tri_mul_out"] / fp8_ms, 3),
+        "rel_diff_vs_bf16": round(fp8_rel, 5), "max_abs_diff_vs_bf16": round(fp8_max, 5),
+        "workspace_mib": round(C_HID * (N + 255) // 256 * 256 * ((N + 255) // 256 * 256) * 4 / 2 ** 20, 1),
+        "note": "experiment: a and b stored as fp8 E4M3 and contracted on the fp8 matrix cores "
+                "(x and the epilogue bf16); outside the bf16 tolerance, reported beside it",
+    }
     tf = transition_flops(N)
     per_op["pair_transition"] = {
         "ms": round(trans_ms, 4), "gflop": round(tf / 1e9, 2),
