@@ -11,9 +11,11 @@ each through the genie_tk modules' HIP kernel path (forward).
 Prints one JSON line.  value = algorithmic TFLOP/s of the step (dense
 2*M*N*K of every projection and contraction; LayerNorm and softmax count 0),
 with per-operator ms / TFLOP/s / fraction of the 2516.6 TFLOP/s bf16 MFMA
-peak, LayerNorm GB/s against 8 TB/s HBM, the roofline of the dominant kernel
-(per-kernel durations from HIP events recorded on the launch stream) and the
-CPU baseline (the numpy oracle on the host cores, bounded sample).
+peak (each the mean over 5 back-to-back calls between two events, median of
+the repetitions), LayerNorm GB/s against 8 TB/s HBM, the roofline of the
+dominant kernel (per-kernel durations from HIP events recorded on the launch
+stream) and the CPU baseline (the modules' PyTorch path in fp32 on the host
+cores).
 """
 from __future__ import annotations
 
@@ -36,6 +38,9 @@ PEAK_BF16_FLOPS = 2516.6e12
 PEAK_HBM_BYTES = 8.0e12
 METRIC = "fwd ms + % bf16 MFMA peak, tri-mul & tri-attn at N=512 c_z=128; LN GB/s"
 C_Z, C_HID, HEADS, HEAD_DIM = 128, 128, 4, 32
+# per-operator timings: calls back to back between two events (the step runs
+# its operators the same way)
+OP_INNER = 5
 
 
 def trimul_flops(N: int, B: int = 1) -> dict:
@@ -125,8 +130,11 @@ def transition_flops(N: int, B: int = 1) -> float:
     return 2.0 * 2 * B * N * N * C_Z * 4 * C_Z
 
 
-def event_time_ms(torch, fn, reps: int, warm: int = 2, flush=None) -> list:
-    """Per-repetition durations from events on the current stream."""
+def event_time_ms(torch, fn, reps: int, warm: int = 2, flush=None, inner: int = 1) -> list:
+    """Per-call durations from events on the current stream: each repetition
+    times `inner` back-to-back calls between two events (a pipeline of calls,
+    as in the step; inner = 1 also counts the host's launch latency of the
+    call) and reports their mean."""
     for _ in range(warm):
         fn()
     out = []
@@ -136,10 +144,11 @@ def event_time_ms(torch, fn, reps: int, warm: int = 2, flush=None) -> list:
         a = torch.cuda.Event(enable_timing=True)
         b = torch.cuda.Event(enable_timing=True)
         a.record()
-        fn()
+        for _ in range(inner):
+            fn()
         b.record()
         b.synchronize()
-        out.append(a.elapsed_time(b))
+        out.append(a.elapsed_time(b) / inner)
     return out
 
 
@@ -477,13 +486,14 @@ def gpu_ops_at(torch, C, dev: str, N: int, tail: int, reps: int) -> dict:
     out = {"N": N, "mask": f"pairs with i, j < {tail}" if tail else "ones"}
     with torch.no_grad():
         for k in ("tri_mul_out", "tri_mul_in", "tri_att_start", "tri_att_end"):
-            ms = statistics.median(event_time_ms(torch, lambda: mods[k](z, m), reps))
+            ms = statistics.median(event_time_ms(torch, lambda: mods[k](z, m), reps, inner=OP_INNER))
             fl = sum((trimul_flops if k.startswith("tri_mul") else triattn_flops)(N).values())
             t = tg["tri_mul" if k.startswith("tri_mul") else "tri_att"]
             out[k] = {"ms": round(ms, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
                       "frac_bf16_peak": round(fl / (ms * 1e-3) / PEAK_BF16_FLOPS, 4),
                       "target_ms": round(t, 4), "time_over_target": round(ms / t, 2)}
-        ms = statistics.median(event_time_ms(torch, lambda: C.layernorm(z, w, b, 1e-5), reps))
+        ms = statistics.median(event_time_ms(torch, lambda: C.layernorm(z, w, b, 1e-5), reps,
+                                             inner=OP_INNER))
         out["layernorm"] = {"ms": round(ms, 4), "gbps": round(ln_bytes(N) / (ms * 1e-3) / 1e9, 1),
                             "frac_hbm": round(ln_bytes(N) / (ms * 1e-3) / PEAK_HBM_BYTES, 4),
                             "target_ms": round(tg["layernorm"], 4)}
@@ -675,7 +685,8 @@ def main() -> int:
 
         # per-operator event timing
         reps = max(5, args.steps)
-        op_ms = {k: statistics.median(event_time_ms(torch, f, reps)) for k, f in ops.items()}
+        op_ms = {k: statistics.median(event_time_ms(torch, f, reps, inner=OP_INNER))
+                 for k, f in ops.items()}
 
         # per-kernel durations from events around each launch
         C.timing_enable(True)

@@ -298,8 +298,10 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
   // loads complete in issue order, so waiting for rows loaded after a store
   // would wait for that store too.  A lane outside the pair grid reads pair 0
   // and normalises to zero.
+  // tiles dealt round-robin over the blocks first, so a small problem still
+  // reaches every CU (a block may then run fewer than 16 busy waves)
   const int64_t tstride = (int64_t)gridDim.x * 16;
-  int64_t tile = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 6);
+  int64_t tile = (int64_t)(threadIdx.x >> 6) * gridDim.x + blockIdx.x;
   TileWalk tw;
   tw.init(tile, tstride, nrows, vtiles);  // row r0 + tw.r
   // (exists = false: a tile past the end, also read as pair 0)
@@ -1629,7 +1631,7 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
     auto prologue = [&](auto mode, int r0, int nrows) {
       constexpr int MODE = decltype(mode)::value;
       const int64_t ptiles = B * (int64_t)nrows * (Np / 32);
-      const int grid = (int)std::min<int64_t>(device_cus(), (ptiles + 15) / 16);
+      const int grid = (int)std::min<int64_t>(device_cus(), (ptiles + 7) / 8);
       StageTimer timer("triattn_prologue", st);
       triattn_prologue_bf16_kernel<CIN, H, MODE><<<grid, 1024, 0, st>>>(
           (const bf16*)x, w, a, (int)N, Np, starting, eps, ptiles, r0, nrows);

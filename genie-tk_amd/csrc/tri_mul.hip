@@ -187,7 +187,9 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
     return ok ? (mask ? mask[ok ? idx : 0] : 1.f) : 0.f;
   };
 
-  int64_t s = (int64_t)blockIdx.x * WAVES + wave;
+  // steps dealt round-robin over the blocks first, so a small problem still
+  // reaches every CU (a block may then run fewer than WAVES busy waves)
+  int64_t s = (int64_t)wave * gridDim.x + blockIdx.x;
   const int64_t sstride = (int64_t)gridDim.x * WAVES;
   // this wave's first step: rows and mask in flight (the next step's are
   // loaded ahead of each step's stores)
@@ -1018,9 +1020,13 @@ __global__ __launch_bounds__(256) void planes_to_pairs_kernel(const T* __restric
 
 // Output tile of the contraction for Np (a multiple of 64): row chunks are
 // multiples of it.
+// 256-row tiles need bf16 and Np % 256 == 0; with fewer than two of them per
+// CU across the planes (small N), 128-row tiles keep every CU busy.
 template <typename T>
-static int contract_tile(int Np) {
-  return (sizeof(T) == 2 && Np % 256 == 0) ? 256 : (Np % 128 == 0 ? 128 : 64);
+static int contract_tile(int Np, int64_t nplanes = 1 << 20) {
+  if (sizeof(T) == 2 && Np % 256 == 0 && (int64_t)(Np / 256) * (Np / 256) * nplanes >= 2 * device_cus())
+    return 256;
+  return Np % 128 == 0 ? 128 : 64;
 }
 
 // X = A . Bm^T per plane: A and X are Mi x Np (Mi a multiple of
@@ -1029,7 +1035,7 @@ template <typename T>
 static int launch_contract(const T* pa, const T* pb, T* px, int Np, int64_t nplanes,
                            hipStream_t st, int Mi = 0) {
   if (Mi == 0) Mi = Np;
-  const int tile = contract_tile<T>(Np);
+  const int tile = contract_tile<T>(Np, nplanes);
   GTK_REQUIRE(Mi > 0 && Mi % tile == 0 && Mi <= Np, GTK_EINVAL, "contraction: %d rows, tile %d", Mi, tile);
   const int64_t blocks = (int64_t)(Mi / tile) * (Np / tile) * nplanes;
   GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "contraction grid too large");
@@ -1152,7 +1158,7 @@ static int launch_trimul_prologue(const void* z, const float* mask, const TriMul
   if (nrows == 0) nrows = Np;
   const int64_t ptiles = B * (int64_t)nrows * (Np / 32);
   if constexpr (trimul_fast<T, CZ, CH>()) {
-    const int grid = (int)std::min<int64_t>(device_cus(), (ptiles / 2 + 7) / 8);
+    const int grid = (int)std::min<int64_t>(device_cus(), (ptiles / 2 + 3) / 4);
     StageTimer timer("trimul_prologue", st);
     const bool whole = r0 == 0 && nrows == Np && side_lo == 0 && side_hi == 2;
     if (whole)
@@ -1200,7 +1206,8 @@ static int launch_trimul_epilogue(const void* z, const T* px, void* out, const T
 }
 
 // Rows per chunk of the memory-bounded mode: chunk_rows rounded up to the
-// contraction tile; Np (whole planes) when chunk_rows is 0 or covers Np.
+// largest contraction tile for Np (a multiple of whichever tile a launch
+// picks); Np (whole planes) when chunk_rows is 0 or covers Np.
 template <typename T>
 static int trimul_chunk_rows(int64_t N, int64_t chunk_rows) {
   const int Np = (int)round_up(N, 64);
@@ -1278,7 +1285,7 @@ static int fwd_trimul_fp8(const void* z, const float* mask, void* out, const voi
   bf16* px = cv.take<bf16>(pe);
   {
     const int64_t ptiles = B * (int64_t)Np * (Np / 32);
-    const int grid = (int)std::min<int64_t>(device_cus(), (ptiles / 2 + 7) / 8);
+    const int grid = (int)std::min<int64_t>(device_cus(), (ptiles / 2 + 3) / 4);
     StageTimer timer("trimul_prologue_fp8", st);
     trimul_prologue_bf16_kernel<CZ, CH, true><<<grid, 512, 0, st>>>(
         (const bf16*)z, mask, pa, pb, w, (int)N, Np, outgoing, eps_in, ptiles, 0, Np, 0, 2);
