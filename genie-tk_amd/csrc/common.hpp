@@ -359,6 +359,22 @@ __device__ __forceinline__ void g2lds16_sv(const void* sbase, uint32_t voff, uin
       : "memory");
 }
 
+// g2lds16_sv for data read once (the non-temporal hint): the copy is streamed
+// through the caches with low retention, so it does not evict data that other
+// waves re-read from L2.
+__device__ __forceinline__ void g2lds16_sv_nt(const void* sbase, uint32_t voff, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2 nt\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(sbase), "s"(lds)
+      : "memory");
+}
+
 // Asynchronously copy `bytes` (a multiple of 1 KiB) from global memory into
 // LDS with the whole block: every load is issued before any is waited for.
 // The caller waits (s_waitcnt vmcnt(0)) and synchronises the block.

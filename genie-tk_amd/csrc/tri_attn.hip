@@ -1011,7 +1011,11 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
 //   * The excluded-key bits of the row are kept in one VGPR (lane t: key
 //     tile t) and read with v_readlane per tile.
 //   * Blocks run head-major, so the blocks of one XCD read one or two heads'
-//     triangle bias.
+//     triangle bias.  That bias (1 MiB per head at Np = 512) is re-read by
+//     every row's block, while K^T, V^T, q and the gate are read once: their
+//     copies carry the non-temporal hint so they do not evict the bias from
+//     L2 (150 -> 141 us standalone at N = 512; with every bias load hitting a
+//     64 KiB window the kernel takes 133 us).
 // The output projection (W_o, b_o, residual) runs in triattn_out_kernel.
 // ---------------------------------------------------------------------------
 template <int NPM>
@@ -1055,7 +1059,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
       const int cr = c - kind * 2 * nt;
       const int t = cr >> 1, rh = cr & 1;
       const bf16* src = (kind ? vbase : kbase) + t * 1024 + rh * 512;
-      g2lds16_sv(src, kind ? voff_v : voff_k, kv_lds + ((kind * NTM + t) * 2 + rh) * 1024);
+      g2lds16_sv_nt(src, kind ? voff_v : voff_k, kv_lds + ((kind * NTM + t) * 2 + rh) * 1024);
     }
   }
 
@@ -1097,7 +1101,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
     const uint32_t ln = (uint32_t)(lane + opaque_zero());
     const uint32_t voff = ln * 16;
 #pragma unroll
-    for (int j = 0; j < 2; ++j) g2lds16_sv(src + j * 512, voff, stg_lds + j * 1024);
+    for (int j = 0; j < 2; ++j) g2lds16_sv_nt(src + j * 512, voff, stg_lds + j * 1024);
   };
   // channels c0 .. c0+3 of this lane's query t32 (transposing read); ln is
   // the lane id through opaque_zero, so that these per-lane addresses are
