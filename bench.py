@@ -520,7 +520,7 @@ def config_table(torch, C, dev: str) -> int:
 
     def gpu_ms(fn, reps=10):
         with torch.no_grad():
-            return statistics.median(event_time_ms(torch, fn, reps))
+            return statistics.median(event_time_ms(torch, fn, reps, inner=OP_INNER))
 
     def cpu_ms(fn, reps=3):
         with torch.no_grad():
@@ -599,7 +599,8 @@ def config_table(torch, C, dev: str) -> int:
     print(f"Host CPU: {cpu['model']}, {cpu['physical_cores']} physical cores; {threads} torch "
           f"threads. CPU: the modules' PyTorch path in fp32 (tri-attn rows in chunks of 64), "
           f"1 warmup + median of 3 (config 4: 1 warmup + 1). GPU: bf16 kernels (config 1: "
-          f"fp32), median of 10 event-timed calls.\n")
+          f"fp32), median of 10 repetitions, each {OP_INNER} back-to-back calls between two "
+          f"events.\n")
     print("| config | operator | N | CPU fp32 ms | GPU ms | speed-up | GPU throughput |")
     print("|---|---|---:|---:|---:|---:|---|")
     print("\n".join(rows))
