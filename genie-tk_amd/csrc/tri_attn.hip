@@ -155,23 +155,26 @@ static AttnWs<T> carve_attn_ws(Carve& cv, int64_t B, int64_t Np, int H, int ch, 
 }
 
 // ---------------------------------------------------------------------------
-// 1. Prologue (fused module path)
+// 1. Prologue (fused module path).  Destination rows r0 .. r0 + nrows - 1;
+//    mode bit 0: q, k, v^T and the gate (into the workspace rows of ws), bit
+//    1: the triangle bias (every row of it is read by every row's attention,
+//    so row chunks compute it over all rows first).
 // ---------------------------------------------------------------------------
 template <typename T, int CIN, int H>
 __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restrict__ x,
                                                                TriAttnPacked<T> w, AttnWs<T> ws,
                                                                int B, int N, int Np, int starting,
-                                                               float eps) {
+                                                               float eps, int r0, int nrows, int mode) {
   constexpr int CH = H * HD;
   const int lane = threadIdx.x & 63;
   const int half = lane >> 5;
   const int t32 = lane & 31;
   const int vtiles = Np / 32;
   const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (tile >= (int64_t)B * Np * vtiles) return;
+  if (tile >= (int64_t)B * nrows * vtiles) return;
   const int vt = (int)(tile % vtiles);
-  const int r = (int)((tile / vtiles) % Np);  // destination row
-  const int b = (int)(tile / ((int64_t)vtiles * Np));
+  const int r = r0 + (int)((tile / vtiles) % nrows);  // destination row
+  const int b = (int)(tile / ((int64_t)vtiles * nrows));
   const int j = vt * 32 + t32;                // destination position
   const bool valid = r < N && j < N;
   const int p = starting ? r : j, q = starting ? j : r;  // source pair
@@ -184,9 +187,9 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
   ln_to_frags<T, CIN>(xf, rh, st);
   const float keep = valid ? 1.f : 0.f;
 
-  const int64_t rowbase = ((int64_t)b * Np + r);  // (b, r)
+  const int64_t rowbase = ws.row(b, r);  // (b, r) in the workspace rows
 #pragma unroll 1
-  for (int h = 0; h < H; ++h) {
+  for (int h = 0; h < ((mode & 1) ? H : 0); ++h) {
     // q, k: [b][r][h][j][d], lane holds d = 8g + 4*half + rr -> 4 consecutive d
     const f32x16 aq = row_gemm_tile<T, CIN, true>(xf, w.w_q, h);
     const f32x16 ak = row_gemm_tile<T, CIN, true>(xf, w.w_k, h);
@@ -211,7 +214,7 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
   // gate: [b][r][j][CH]
   T* gd = ws.gate + (rowbase * Np + j) * CH;
 #pragma unroll 1
-  for (int nt = 0; nt < CH / 32; ++nt) {
+  for (int nt = 0; nt < ((mode & 1) ? CH / 32 : 0); ++nt) {
     const f32x16 ag = row_gemm_tile<T, CIN, true>(xf, w.w_g, nt);
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
@@ -221,7 +224,7 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
     }
   }
   // triangle bias: [b][h][r][j] (rows h >= H of the packed tile are zero)
-  {
+  if (mode & 2) {
     const f32x16 ab = row_gemm_tile<T, CIN, true>(xf, w.w_b, 0);
     if (half == 0) {
 #pragma unroll
@@ -540,7 +543,8 @@ __global__ __launch_bounds__(64 * H) void triattn_fused_kernel(const T* __restri
                                                                T* __restrict__ out,
                                                                TriAttnPacked<T> w, AttnWs<T> ws,
                                                                int B, int N, int Np, int starting,
-                                                               int residual, float inf) {
+                                                               int residual, float inf, int r0,
+                                                               int nrows) {
   constexpr int CH = H * HD;
   constexpr int OPITCH = CH + 8;
   __shared__ __attribute__((aligned(16))) T os[32 * OPITCH];
@@ -550,11 +554,11 @@ __global__ __launch_bounds__(64 * H) void triattn_fused_kernel(const T* __restri
   const int t32 = lane & 31;
   const int qtiles = (N + 31) / 32;
   const int qt = blockIdx.x % qtiles;
-  const int r = (blockIdx.x / qtiles) % N;
-  const int b = blockIdx.x / (qtiles * N);
+  const int r = r0 + (blockIdx.x / qtiles) % nrows;  // rows r0 .. r0 + nrows - 1
+  const int b = blockIdx.x / (qtiles * nrows);
   const int q0 = qt * 32;
 
-  const int64_t rowbase = (int64_t)b * Np + r;
+  const int64_t rowbase = ws.row(b, r);
   MaskView mv;
   if (mask) {
     // starting: key k of row r is pair (r, k); ending: pair (k, r)
@@ -1609,7 +1613,7 @@ static int pack_triattn(const gtk_tri_attn_weights* w, int cin, int ch, int H, v
   return GTK_OK;
 }
 
-// chunk_rows > 0 (bf16 only): attention rows in chunks of that many rows.
+// chunk_rows > 0: attention rows in chunks of that many rows.
 // The triangle bias needs every pair, so it is computed first over all rows;
 // then q, k, v^T and the gate of one chunk of rows are computed and attended
 // before the next chunk, in a workspace of chunk_rows rows.  Each row's
@@ -1624,7 +1628,7 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
   Carve pc((void*)packed, SIZE_MAX);
   TriAttnPacked<T> w = carve_triattn<T>(pc, CIN, CH, H);
   const int Np = (int)attn_pad(N);
-  const bool chunked = kFast && chunk_rows > 0 && chunk_rows < N;
+  const bool chunked = chunk_rows > 0 && chunk_rows < N;
   Carve cv(ws, SIZE_MAX);
   AttnWs<T> a = carve_attn_ws<T>(cv, B, Np, H, CH, chunked ? chunk_rows : 0, kFast);
   const int64_t blocks = B * N * ((N + 31) / 32);
@@ -1690,19 +1694,35 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
       }
     }
   } else {
-    const int64_t ptiles = B * (int64_t)Np * (Np / 32);
-    {
+    auto prologue = [&](int r0, int nrows, int mode) {
+      const int64_t ptiles = B * (int64_t)nrows * (Np / 32);
       StageTimer timer("triattn_prologue", st);
       triattn_prologue_kernel<T, CIN, H><<<(unsigned)((ptiles + 3) / 4), 256, 0, st>>>(
-          (const T*)x, w, a, (int)B, (int)N, Np, starting, eps);
-    }
-    GTK_LAUNCH_CHECK();
-    {
+          (const T*)x, w, a, (int)B, (int)N, Np, starting, eps, r0, nrows, mode);
+    };
+    auto attend = [&](int r0, int nrows) {
+      const int64_t ablocks = B * nrows * ((N + 31) / 32);
       StageTimer timer("triattn_flash", st);
-      triattn_fused_kernel<T, CIN, H><<<(unsigned)blocks, 64 * H, 0, st>>>(
-          (const T*)x, mask, (T*)out, w, a, (int)B, (int)N, Np, starting, residual, inf);
+      triattn_fused_kernel<T, CIN, H><<<(unsigned)ablocks, 64 * H, 0, st>>>(
+          (const T*)x, mask, (T*)out, w, a, (int)B, (int)N, Np, starting, residual, inf, r0, nrows);
+    };
+    if (!chunked) {
+      prologue(0, Np, 3);  // every row, padding included
+      GTK_LAUNCH_CHECK();
+      attend(0, (int)N);
+      GTK_LAUNCH_CHECK();
+    } else {
+      prologue(0, Np, 2);  // the bias over every row
+      GTK_LAUNCH_CHECK();
+      for (int64_t r0 = 0; r0 < N; r0 += chunk_rows) {
+        const int nrows = (int)std::min<int64_t>(chunk_rows, N - r0);
+        a.r0 = (int)r0;
+        prologue((int)r0, nrows, 1);
+        GTK_LAUNCH_CHECK();
+        attend((int)r0, nrows);
+        GTK_LAUNCH_CHECK();
+      }
     }
-    GTK_LAUNCH_CHECK();
   }
   return GTK_OK;
 }
@@ -1793,12 +1813,12 @@ extern "C" size_t gtk_tri_attn_workspace_size_chunked(int64_t B, int64_t N, int6
                                                       int64_t c_h, int64_t H, int64_t chunk_rows,
                                                       int dtype) {
   if (!triattn_shape_ok(c_in, c_h, H) || B < 0 || N < 0 || chunk_rows < 0) return 0;
+  if (dtype != GTK_F32 && dtype != GTK_BF16) return 0;
   const bool fast = dtype == GTK_BF16 && triattn_fast_shape(c_in, H);
-  if (chunk_rows > 0 && !fast) return 0;
   Carve cv(nullptr, SIZE_MAX);
   const int64_t rows = chunk_rows > 0 && chunk_rows < N ? chunk_rows : 0;
   const int chp = (int)H * HD;
-  if (dtype == GTK_F32) carve_attn_ws<float>(cv, B, attn_pad(N), (int)H, chp, 0, false);
+  if (dtype == GTK_F32) carve_attn_ws<float>(cv, B, attn_pad(N), (int)H, chp, rows, false);
   else carve_attn_ws<bf16>(cv, B, attn_pad(N), (int)H, chp, rows, fast);
   return cv.off;
 }
@@ -1820,8 +1840,6 @@ extern "C" int gtk_tri_attn_forward_chunked(const void* x, const float* mask, vo
               (long long)c_in, (long long)c_h, (long long)H);
   GTK_REQUIRE(B >= 0 && N >= 0 && N <= 8192 && chunk_rows >= 0, GTK_EINVAL,
               "gtk_tri_attn_forward: bad shape");
-  GTK_REQUIRE(chunk_rows == 0 || (dtype == GTK_BF16 && triattn_fast_shape(c_in, H)), GTK_EUNSUPPORTED,
-              "gtk_tri_attn_forward_chunked: row chunks need bf16, c_in = 128 and H = 4");
   GTK_REQUIRE(abs_at_most(inf, 1e37f), GTK_EINVAL,
               "gtk_tri_attn_forward: |inf| must be at most 1e37, got %g", (double)inf);
   if (B == 0 || N == 0) return GTK_OK;
@@ -1831,8 +1849,8 @@ extern "C" int gtk_tri_attn_forward_chunked(const void* x, const float* mask, vo
               ws_bytes, need);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == GTK_F32)
-    return fwd_triattn_any<float>(c_in, H, x, mask, out, packed, B, N, starting, residual, eps, inf, 0,
-                                  ws, st);
+    return fwd_triattn_any<float>(c_in, H, x, mask, out, packed, B, N, starting, residual, eps, inf,
+                                  chunk_rows, ws, st);
   return fwd_triattn_any<bf16>(c_in, H, x, mask, out, packed, B, N, starting, residual, eps, inf,
                                chunk_rows, ws, st);
 }

@@ -130,7 +130,7 @@ class TriangleAttention(nn.Module):
                 and x.dtype in _dispatch.SUPPORTED_DTYPES and self.layer_norm.elementwise_affine)
 
     def _headline_shape(self) -> bool:
-        """The shape the backward and row-chunk kernels are built for."""
+        """The shape the backward kernels are built for."""
         return self.c_in == 128 and self.no_heads == 4 and self.c_hidden == 128
 
     def _pack(self, params, fp32: bool) -> Tensor:
@@ -148,8 +148,8 @@ class TriangleAttention(nn.Module):
     def _forward_cuda(self, x: Tensor, mask: Optional[Tensor] = None,
                       residual: bool = False, chunk_size: Optional[int] = None) -> Tensor:
         """HIP path; returns the update (plus x when ``residual``).  With
-        ``chunk_size`` (bf16) the attention rows run that many at a time in a
-        workspace of that many rows."""
+        ``chunk_size`` the attention rows run that many at a time in a
+        workspace of that many rows (bit-identical output)."""
         C = _ext.require()
         xb, mb, lead = _dispatch.flatten_batch(x, mask)
         packed = self._packed_params(x.dtype == torch.float32)
@@ -171,17 +171,15 @@ class TriangleAttention(nn.Module):
 
         ``chunk_size`` (an addition to the reference's signature, default off)
         bounds memory: the attention rows are processed that many at a time,
-        with the same result.  It applies to the bf16 kernel path of the
-        c_in=128, 4-head, c_hidden=128 module and to the PyTorch path; other
-        GPU inputs with ``chunk_size`` run the PyTorch path."""
+        with the same result, on the kernels (every kernel shape and dtype, in
+        inference) and on the PyTorch path (which also serves chunked calls
+        that need gradients)."""
         if chunk_size is not None and chunk_size < 1:
             raise ValueError(f"chunk_size must be >= 1, got {chunk_size}")
         if x.is_cuda and self._fused_requested:
             if not _CUDA_AVAILABLE:
                 _ext.missing(type(self).__name__)
-            elif (self.use_fused_kernel and self._kernel_supported(x)
-                    and (chunk_size is None
-                         or (x.dtype == torch.bfloat16 and self._headline_shape()))):
+            elif self.use_fused_kernel and self._kernel_supported(x):
                 if not _dispatch.needs_autograd(x, self):
                     return self._forward_cuda(x, mask, chunk_size=chunk_size)
                 # the backward kernels: the headline shape and inf = 1e9

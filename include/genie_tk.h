@@ -276,7 +276,7 @@ int gtk_tri_attn_forward(const void* x, const float* mask, void* out, const void
                          int residual, float eps, float inf, int dtype, void* workspace,
                          size_t workspace_bytes, void* stream);
 
-/* Memory-bounded form of gtk_tri_attn_forward (bf16): the attention rows are
+/* Memory-bounded form of gtk_tri_attn_forward: the attention rows are
  * processed chunk_rows at a time, so the q/k/v/gate workspace holds
  * chunk_rows rows instead of N (the N x N x H triangle bias stays whole: it
  * is shared by every row).  The result equals gtk_tri_attn_forward's.  It is
@@ -284,7 +284,8 @@ int gtk_tri_attn_forward(const void* x, const float* mask, void* out, const void
  * (src/genie_tk/utils.py:78-123), which its attention module imports
  * (triangle_attention.py:23) but never calls; there is no reference kernel.
  * chunk_rows = 0, or >= N, is the unchunked operator.  The workspace size
- * query takes the same chunk_rows.  Row chunks need bf16, c_in = 128, H = 4. */
+ * query takes the same chunk_rows.  Every shape and dtype of
+ * gtk_tri_attn_forward. */
 size_t gtk_tri_attn_workspace_size_chunked(int64_t B, int64_t N, int64_t c_in, int64_t c_h,
                                            int64_t H, int64_t chunk_rows, int dtype);
 int gtk_tri_attn_forward_chunked(const void* x, const float* mask, void* out, const void* packed,

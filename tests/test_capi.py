@@ -144,7 +144,13 @@ def test_workspace_sizes(lib):
     assert wc(64) < wc(128) < full
     assert wc(128) - wc(64) == 4 * 64 * 2048 * 128 * 2
     assert full - wc(128) >= 4 * (2048 - 128) * 2048 * 128 * 2
-    assert lib.gtk_tri_attn_workspace_size_chunked(1, 512, 128, 128, 4, 64, GTK_F32) == 0
+    # every shape and dtype chunks: fp32 and the generic bf16 shapes hold q, k,
+    # v and the gate (4 x rows x H*32 x Np) for the chunk's rows only
+    wf = lambda rows: lib.gtk_tri_attn_workspace_size_chunked(1, 512, 128, 128, 4, rows, GTK_F32)  # noqa: E731
+    assert wf(64) < wf(128) < wf(0) == lib.gtk_tri_attn_workspace_size(1, 512, 128, 128, 4, GTK_F32)
+    assert wf(128) - wf(64) == 4 * 64 * 512 * 128 * 4
+    wg = lambda rows: lib.gtk_tri_attn_workspace_size_chunked(1, 512, 64, 64, 2, rows, GTK_BF16)  # noqa: E731
+    assert wg(64) < wg(0)
     assert lib.gtk_fused_layernorm_linear_workspace_size(128, 256, GTK_BF16) > 0
     # backward: eight [c][Np][Np] planes and the per-pair operand planes at least
     wb = lib.gtk_tri_mul_backward_workspace_size(1, 512, 128, 128, GTK_BF16)
@@ -190,9 +196,9 @@ def test_bad_dtype_and_shapes_are_rejected(lib):
     rc = lib.gtk_tri_attn_forward(None, None, None, None, 1, 8, 128, 128, 8, 1, 0, 1e-5, 1e9,
                                   GTK_BF16, None, 0, None)
     assert rc == GTK_EUNSUPPORTED
-    rc = lib.gtk_tri_attn_forward_chunked(None, None, None, None, 1, 8, 128, 128, 4, 1, 0, 1e-5,
+    rc = lib.gtk_tri_attn_forward_chunked(None, None, None, None, 1, 8, 96, 128, 4, 1, 0, 1e-5,
                                           1e9, 4, GTK_F32, None, 0, None)
-    assert rc == GTK_EUNSUPPORTED and "bf16" in _err(lib)
+    assert rc == GTK_EUNSUPPORTED and "c_in=96" in _err(lib)
     rc = lib.gtk_tri_attn_forward_chunked(None, None, None, None, 1, 8, 128, 128, 4, 1, 0, 1e-5,
                                           1e9, -1, GTK_BF16, None, 0, None)
     assert rc == GTK_EINVAL

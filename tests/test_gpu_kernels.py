@@ -276,6 +276,36 @@ def test_tri_attn_row_chunks(starting, N, chunks):
     check_bf16(to_np(y), ref, "tri_attn chunked")
 
 
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("dname,cin,ch,heads", [("fp32", 128, 128, 4), ("bf16", 64, 64, 2),
+                                                ("fp32", 32, 16, 1)])
+def test_tri_attn_row_chunks_generic_kernels(starting, dname, cin, ch, heads):
+    """Row chunks on the generic kernels (fp32, and bf16 shapes other than
+    c_in = 128 with four heads): bit-identical to the unchunked output, with
+    and without the residual, and within tolerance of the oracle."""
+    N = 70
+    log(f"tri_attn generic row chunks {dname} c_in={cin} c_h={ch} H={heads} start={starting}")
+    P = H.draw_params(H.tri_attn_shapes(cin, ch, heads), seed=cin + ch + heads, ln_random=True,
+                      bias_random=True)
+    x = H.pair_input(1, N, cin, seed=N + cin)
+    m = H.tail_mask(1, N, [N - 6])
+    if dname == "bf16":
+        P, x = H.bf16_params(P), H.bf16_round(x)
+    mod = triattn_module(P, starting, heads, DT[dname])
+    xd, md = _dev(x, DT[dname]), _dev(m, DT[dname])
+    with torch.no_grad():
+        full = mod._forward_cuda(xd, md)
+        full_res = mod._forward_cuda(xd, md, residual=True)
+        for c in (1, 16, 33):
+            y = mod(xd, md, chunk_size=c)
+            y_res = mod._forward_cuda(xd, md, residual=True, chunk_size=c)
+            torch.cuda.synchronize()
+            assert torch.equal(y, full), f"chunk {c}: differs from the unchunked output"
+            assert torch.equal(y_res, full_res), f"chunk {c}: residual form differs"
+    ref = pair_ops.tri_attn(x, m, P, starting, heads, dtype=np.float64)
+    (check_fp32 if dname == "fp32" else check_bf16)(to_np(y), ref, "tri_attn generic chunks")
+
+
 # --------------------------------------------------- shapes beyond the headline
 @pytest.mark.parametrize("dname", ["fp32", "bf16"])
 @pytest.mark.parametrize("starting", [True, False])
