@@ -74,6 +74,11 @@ __device__ __forceinline__ void mma(f32x16& acc, const Frag<float>& a, const Fra
   for (int e = 0; e < 4; ++e) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a.hi[e], b.hi[e], acc, 0, 0, 0);
 }
 
+// This wave's index in its block, as a wave-uniform value (readfirstlane):
+// index math derived from it stays in scalar registers, and buffer
+// resources built from it need no per-lane waterfall loop.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
   for (int e = 0; e < 16; ++e) z[e] = 0.f;
@@ -380,7 +385,7 @@ __device__ __forceinline__ void g2lds16_sv_nt(const void* sbase, uint32_t voff, 
 // The caller waits (s_waitcnt vmcnt(0)) and synchronises the block.
 __device__ __forceinline__ void copy_to_lds_async(void* dst, const void* __restrict__ src, int bytes) {
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int nwaves = blockDim.x >> 6;
   for (int blk = wave; blk * 1024 < bytes; blk += nwaves)
     g2lds16((const char*)src + blk * 1024 + lane * 16, (char*)dst + blk * 1024);

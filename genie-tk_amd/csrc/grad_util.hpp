@@ -175,7 +175,7 @@ __global__ __launch_bounds__(256) void transpose_planes_kernel(const T* __restri
   const int64_t plane = (int64_t)Np * Np;
   const T* src = in + pl * plane;
   T* dst = out + pl * plane;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int tx = threadIdx.x & 63, ty = wave_id();
 #pragma unroll 4
   for (int r = ty; r < 64; r += 4) tile[r][tx] = src[(int64_t)(i0 + r) * Np + j0 + tx];
   __syncthreads();
@@ -419,7 +419,7 @@ __global__ __launch_bounds__(256) void rowred_kernel(const T* __restrict__ G, co
     a += __shfl_xor(a, o, 64);
     d += __shfl_xor(d, o, 64);
   }
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   if ((threadIdx.x & 63) == 0) {
     red[0][wave] = a;
     red[1][wave] = d;

@@ -29,7 +29,7 @@ __global__ __launch_bounds__(512) void ln_rows_kernel(const T* __restrict__ x, T
   constexpr int LPR = D / 8;     // lanes per row
   constexpr int RPW = 64 / LPR;  // rows per wave per step
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int sub = lane / LPR;
   const int c0 = (lane % LPR) * 8;
   float g[8], bt[8];
@@ -95,7 +95,7 @@ __global__ __launch_bounds__(256) void ln_rows_generic_kernel(const T* __restric
                                                               const float* __restrict__ beta,
                                                               int64_t rows, int D, float eps) {
   const int lane = threadIdx.x & 63;
-  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t r = (int64_t)blockIdx.x * 4 + wave_id();
   if (r >= rows) return;
   const T* xr = x + r * D;
   float s = 0.f;
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(256) void ln_linear_kernel(const T* __restrict__ x,
                                                         int64_t rows, int d_out, float eps) {
   const int lane = threadIdx.x & 63;
   const int half = lane >> 5;
-  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave_id();
   const int64_t row = tile * 32 + (lane & 31);
   if (tile * 32 >= rows) return;  // whole wave idle (uniform)
   const bool valid = row < rows;
@@ -203,7 +203,7 @@ __global__ __launch_bounds__(512) void ln_linear_lds_kernel(const bf16* __restri
   const int lane = threadIdx.x & 63;
   const int half = lane >> 5;
   const int t32 = lane & 31;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = wave_id();
   const bool vec4 = (d_out & 3) == 0;
   const int64_t stride = (int64_t)gridDim.x * 8;
   // Rows of a tile; a row past the end (or a tile past the end) reads row 0.

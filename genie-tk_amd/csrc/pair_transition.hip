@@ -100,7 +100,7 @@ __global__ __launch_bounds__(512) void pair_transition_bf16_kernel(
   for (int t = threadIdx.x; t < C; t += blockDim.x) b2l[t] = w.b2[t];
 
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = wave_id();
   const int half = lane >> 5;
   const int t32 = lane & 31;
   // The weight stream is the same for every row tile, so the ring runs on
@@ -277,7 +277,7 @@ __global__ __launch_bounds__(256) void pair_transition_kernel(
   const int lane = threadIdx.x & 63;
   const int half = lane >> 5;
   const int t32 = lane & 31;
-  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave_id();
   if (tile * 32 >= rows) return;
   const int64_t r = tile * 32 + t32;
   const bool valid = r < rows;
@@ -341,7 +341,7 @@ __global__ __launch_bounds__(256) void pair_transition_bwd_kernel(
   const int lane = threadIdx.x & 63;
   const int half = lane >> 5;
   const int t32 = lane & 31;
-  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave_id();
   if (tile * 32 >= rows) return;
   const int64_t r = tile * 32 + t32;
   const bool valid = r < rows;

@@ -170,7 +170,7 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
   const int half = lane >> 5;
   const int t32 = lane & 31;
   const int vtiles = Np / 32;
-  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave_id();
   if (tile >= (int64_t)B * nrows * vtiles) return;
   const int vt = (int)(tile % vtiles);
   const int r = r0 + (int)((tile / vtiles) % nrows);  // destination row
@@ -304,7 +304,10 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
   // tiles dealt round-robin over the blocks first, so a small problem still
   // reaches every CU (a block may then run fewer than 16 busy waves)
   const int64_t tstride = (int64_t)gridDim.x * 16;
-  int64_t tile = (int64_t)(threadIdx.x >> 6) * gridDim.x + blockIdx.x;
+  // wave-uniform (readfirstlane): the tile walk, row bases and buffer
+  // resources then live in scalar registers
+  const int wave = wave_id();
+  int64_t tile = (int64_t)wave * gridDim.x + blockIdx.x;
   TileWalk tw;
   tw.init(tile, tstride, nrows, vtiles);  // row r0 + tw.r
   // (exists = false: a tile past the end, also read as pair 0)
@@ -549,7 +552,7 @@ __global__ __launch_bounds__(64 * H) void triattn_fused_kernel(const T* __restri
   constexpr int OPITCH = CH + 8;
   __shared__ __attribute__((aligned(16))) T os[32 * OPITCH];
   const int lane = threadIdx.x & 63;
-  const int h = threadIdx.x >> 6;
+  const int h = wave_id();
   const int half = lane >> 5;
   const int t32 = lane & 31;
   const int qtiles = (N + 31) / 32;
@@ -1367,7 +1370,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = wave_id();
   const int half = lane >> 5;
   const int t32 = lane & 31;
   char* const sw = stg[wave];

@@ -130,7 +130,7 @@ __global__ __launch_bounds__(256) void attn_bwd_proj_kernel(const T* __restrict_
   constexpr int CH = H * AD;
   const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
   const int jtiles = np / 32;
-  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave_id();
   if (tile >= (int64_t)B * N * jtiles) return;
   const int jt = (int)(tile % jtiles);
   const int r = (int)((tile / jtiles) % N);
@@ -213,7 +213,7 @@ __global__ __launch_bounds__(256) void attn_bwd_fwd_kernel(AttnBwdBufs<T> bf, in
                                                            float scale) {
   const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
   const int qtiles = np / 32;
-  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave_id();
   if (tile >= (int64_t)B * N * H * qtiles) return;
   const int qt = (int)(tile % qtiles);
   const int64_t rh = tile / qtiles;  // (b*N + r)*H + h
@@ -287,7 +287,7 @@ __global__ __launch_bounds__(256) void attn_bwd_epi_kernel(const T* __restrict__
   constexpr int CH = H * AD;
   const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
   const int jtiles = np / 32;
-  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave_id();
   if (tile >= (int64_t)B * N * jtiles) return;
   const int jt = (int)(tile % jtiles);
   const int r = (int)((tile / jtiles) % N);
@@ -366,7 +366,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnBwdBufs<T> bf, i
                                                             float scale) {
   const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
   const int tiles1 = np / 32;
-  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave_id();
   if (tile >= (int64_t)B * N * H * tiles1) return;
   const int kt = (int)(tile % tiles1);
   const int64_t rh = tile / tiles1;
@@ -436,7 +436,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnBwdBufs<T> bf, int
                                                           float scale) {
   const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
   const int tiles1 = np / 32;
-  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave_id();
   if (tile >= (int64_t)B * N * H * tiles1) return;
   const int qt = (int)(tile % tiles1);
   const int64_t rh = tile / tiles1;
@@ -494,7 +494,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dbias_kernel(AttnBwdBufs<T> bf, 
                                                              float scale) {
   const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
   const int t1 = np / 32;
-  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave_id();
   if (tile >= (int64_t)B * H * t1 * t1) return;
   const int kt = (int)(tile % t1);
   const int qt = (int)((tile / t1) % t1);
@@ -568,7 +568,7 @@ constexpr int kRhWaves = 8;
 // waits for its copies and synchronises the block.
 __device__ __forceinline__ void rows2_to_lds(const bf16* a, char* la, const bf16* b, char* lb, int np) {
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = wave_id();
   const uint32_t rin = (uint32_t)lane >> 2;  // row within the copy (16 rows of 64 bytes)
   const uint32_t voff = rin * 64 + ((((uint32_t)lane & 3) ^ ((rin >> 2) & 3)) << 4);
   const int per = np / 16;
@@ -1168,7 +1168,7 @@ __global__ __launch_bounds__(256) void attn_bwd_pro_kernel(const T* __restrict__
   constexpr int CH = H * AD;
   const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
   const int jtiles = np / 32;
-  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave_id();
   if (tile >= (int64_t)B * N * jtiles) return;
   const int jt = (int)(tile % jtiles);
   const int r = (int)((tile / jtiles) % N);

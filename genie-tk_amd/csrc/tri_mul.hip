@@ -45,7 +45,7 @@ __global__ __launch_bounds__(256) void trimul_prologue_kernel(
   const int half = lane >> 5;
   const int t32 = lane & 31;
   const int vtiles = Np / 32;
-  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave_id();
   if (tile >= (int64_t)B * nrows * vtiles) return;
   const int vt = (int)(tile % vtiles);
   const int fl = (int)((tile / vtiles) % nrows);
@@ -145,7 +145,7 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = wave_id();
   const int half = lane >> 5;
   const int i32 = lane & 31;
   const int prow = 16 * ((i32 >> 2) & 1) + 4 * (i32 >> 3) + (i32 & 3);
@@ -428,7 +428,7 @@ __global__ __launch_bounds__(64 * (TI / 64) * (TJ / 64)) void trimul_contract_bf
   const bf16* Bm = pb + pl * plane;
 
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = wave_id();
   const int half = lane >> 5;
   const int wi = (wave / (TJ / 64)) * 64;  // wave row offset (i)
   const int wj = (wave % (TJ / 64)) * 64;  // wave col offset (j)
@@ -567,7 +567,7 @@ __global__ __launch_bounds__(64 * (TI / 64) * (TJ / 64)) void trimul_contract_fp
   const uint8_t* Bm = pb + pl * plane;
 
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = wave_id();
   const int half = lane >> 5;
   const int wi = (wave / (TJ / 64)) * 64;
   const int wj = (wave % (TJ / 64)) * 64;
@@ -674,7 +674,7 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(
   constexpr int XPITCH = CH + 8;  // LDS row pitch (elements) of the transposed x tile
   __shared__ __attribute__((aligned(16))) T xs[4][32 * XPITCH];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int half = lane >> 5;
   const int t32 = lane & 31;
   const int jtiles = (N + 31) / 32;
@@ -803,7 +803,7 @@ __global__ __launch_bounds__(512) void trimul_epilogue_bf16_kernel(
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wave = wave_id();
   const int half = lane >> 5;
   const int t32 = lane & 31;
   const int jtiles = (N + 31) / 32;
@@ -966,7 +966,7 @@ __global__ __launch_bounds__(256) void pairs_to_planes_kernel(const T* __restric
   const int lane = threadIdx.x & 63;
   const int half = lane >> 5;
   const int vtiles = Np / 32;
-  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave_id();
   if (tile >= (int64_t)B * Np * vtiles) return;
   const int vt = (int)(tile % vtiles);
   const int f = (int)((tile / vtiles) % Np);
@@ -993,7 +993,7 @@ __global__ __launch_bounds__(256) void planes_to_pairs_kernel(const T* __restric
   const int lane = threadIdx.x & 63;
   const int half = lane >> 5;
   const int jtiles = (N + 31) / 32;
-  const int64_t tile = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t tile = (int64_t)blockIdx.x * 4 + wave_id();
   if (tile >= (int64_t)B * N * jtiles) return;
   const int jt = (int)(tile % jtiles);
   const int i = (int)((tile / jtiles) % N);

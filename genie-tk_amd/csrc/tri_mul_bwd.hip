@@ -44,7 +44,7 @@ __global__ __launch_bounds__(256) void trimul_bwd_epilogue_kernel(
   constexpr int XPITCH = CH + 8;
   __shared__ __attribute__((aligned(16))) T xs[4][32 * XPITCH];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int half = lane >> 5;
   const int t32 = lane & 31;
   const int jtiles = Np / 32;
@@ -208,7 +208,7 @@ __global__ __launch_bounds__(256) void trimul_bwd_prologue_kernel(
     const T* __restrict__ wgt, int B, int N, int Np, int64_t pitch, float eps_in) {
   constexpr int64_t PE = (CZ / 32) * (CH / 16) * 512;  // packed_elems(CZ, CH)
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = wave_id();
   const int half = lane >> 5;
   const int t32 = lane & 31;
   const int jtiles = (N + 31) / 32;
