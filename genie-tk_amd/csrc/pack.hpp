@@ -53,23 +53,31 @@ __global__ void pack_weight_kernel(Tout* __restrict__ dst, const Tin* __restrict
 
 // dst[o] = scale * (bias[o] + sum_k W[o][k] * beta[k]): the bias of a linear
 // map applied after a LayerNorm whose elementwise bias beta is folded in.
+// One wave per output: lane l sums k = l, l + 64, ..., then a butterfly over
+// the wave (a fixed order, so the result is the same on every call).
+constexpr int kFoldWaves = 4;  // outputs per 256-thread block
 template <typename Tin>
-__global__ void fold_bias_kernel(float* __restrict__ dst, const Tin* __restrict__ w,
-                                 const void* __restrict__ bias, int bias_bf16,
-                                 const float* __restrict__ beta, int out_dim, int k_dim,
-                                 int64_t s_out, int64_t s_in, float scale, Pad pout) {
-  const int op = blockIdx.x * blockDim.x + threadIdx.x;
-  if (op >= out_dim) return;
+__global__ __launch_bounds__(64 * kFoldWaves) void fold_bias_kernel(
+    float* __restrict__ dst, const Tin* __restrict__ w, const void* __restrict__ bias, int bias_bf16,
+    const float* __restrict__ beta, int out_dim, int k_dim, int64_t s_out, int64_t s_in, float scale,
+    Pad pout) {
+  const int op = blockIdx.x * kFoldWaves + (int)(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (op >= out_dim) return;  // wave-uniform
   const int o = pout.src(op);
   if (o < 0) {
-    dst[op] = 0.f;
+    if (lane == 0) dst[op] = 0.f;
     return;
   }
   float acc = 0.f;
-  if (bias) acc = bias_bf16 ? (float)((const bf16*)bias)[o] : ((const float*)bias)[o];
   if (beta)
-    for (int k = 0; k < k_dim; ++k) acc += to_f32(w[o * s_out + k * s_in]) * beta[k];
-  dst[op] = scale * acc;
+    for (int k = lane; k < k_dim; k += 64) acc += to_f32(w[o * s_out + k * s_in]) * beta[k];
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+  if (lane == 0) {
+    const float b = bias ? (bias_bf16 ? (float)((const bf16*)bias)[o] : ((const float*)bias)[o]) : 0.f;
+    dst[op] = scale * (b + acc);
+  }
 }
 
 template <typename Tin>
@@ -102,13 +110,13 @@ inline int launch_pack(Tout* dst, const void* src, int wdtype, int out_dim, int 
 inline int launch_fold_bias(float* dst, const void* w, const void* bias, int wdtype,
                             const float* beta, int out_dim, int k_dim, int64_t s_out, int64_t s_in,
                             float scale, hipStream_t st, Pad pout = Pad()) {
-  const int blocks = (out_dim + 63) / 64;
+  const int blocks = (out_dim + kFoldWaves - 1) / kFoldWaves;
   if (wdtype == GTK_F32)
-    fold_bias_kernel<float><<<blocks, 64, 0, st>>>(dst, (const float*)w, bias, 0, beta, out_dim,
-                                                    k_dim, s_out, s_in, scale, pout);
+    fold_bias_kernel<float><<<blocks, 64 * kFoldWaves, 0, st>>>(dst, (const float*)w, bias, 0, beta,
+                                                                 out_dim, k_dim, s_out, s_in, scale, pout);
   else
-    fold_bias_kernel<bf16><<<blocks, 64, 0, st>>>(dst, (const bf16*)w, bias, 1, beta, out_dim,
-                                                   k_dim, s_out, s_in, scale, pout);
+    fold_bias_kernel<bf16><<<blocks, 64 * kFoldWaves, 0, st>>>(dst, (const bf16*)w, bias, 1, beta,
+                                                                out_dim, k_dim, s_out, s_in, scale, pout);
   GTK_LAUNCH_CHECK();
   return GTK_OK;
 }
