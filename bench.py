@@ -11,8 +11,8 @@ each through the genie_tk modules' HIP kernel path (forward).
 Prints one JSON line.  value = algorithmic TFLOP/s of the step (dense
 2*M*N*K of every projection and contraction; LayerNorm and softmax count 0),
 with per-operator ms / TFLOP/s / fraction of the 2516.6 TFLOP/s bf16 MFMA
-peak (each the mean over 5 back-to-back calls between two events, median of
-the repetitions), LayerNorm GB/s against 8 TB/s HBM, the roofline of the
+peak (each the mean over 5 back-to-back calls between two events; 10 warmup
+calls, then the median of 50 repetitions), LayerNorm GB/s against 8 TB/s HBM, the roofline of the
 dominant kernel (per-kernel durations from HIP events recorded on the launch
 stream) and the CPU baseline (the modules' PyTorch path in fp32 on the host
 cores).
@@ -39,8 +39,10 @@ PEAK_HBM_BYTES = 8.0e12
 METRIC = "fwd ms + % bf16 MFMA peak, tri-mul & tri-attn at N=512 c_z=128; LN GB/s"
 C_Z, C_HID, HEADS, HEAD_DIM = 128, 128, 4, 32
 # per-operator timings: calls back to back between two events (the step runs
-# its operators the same way)
+# its operators the same way), OP_WARM untimed calls, the median of OP_REPS
 OP_INNER = 5
+OP_WARM = 10
+OP_REPS = 50
 
 
 def trimul_flops(N: int, B: int = 1) -> dict:
@@ -130,7 +132,7 @@ def transition_flops(N: int, B: int = 1) -> float:
     return 2.0 * 2 * B * N * N * C_Z * 4 * C_Z
 
 
-def event_time_ms(torch, fn, reps: int, warm: int = 2, flush=None, inner: int = 1) -> list:
+def event_time_ms(torch, fn, reps: int, warm: int = OP_WARM, flush=None, inner: int = 1) -> list:
     """Per-call durations from events on the current stream: each repetition
     times `inner` back-to-back calls between two events (a pipeline of calls,
     as in the step; inner = 1 also counts the host's launch latency of the
@@ -518,7 +520,7 @@ def config_table(torch, C, dev: str) -> int:
     cpu = host_cpu()
     rows = []
 
-    def gpu_ms(fn, reps=10):
+    def gpu_ms(fn, reps=OP_REPS):
         with torch.no_grad():
             return statistics.median(event_time_ms(torch, fn, reps, inner=OP_INNER))
 
@@ -599,7 +601,7 @@ def config_table(torch, C, dev: str) -> int:
     print(f"Host CPU: {cpu['model']}, {cpu['physical_cores']} physical cores; {threads} torch "
           f"threads. CPU: the modules' PyTorch path in fp32 (tri-attn rows in chunks of 64), "
           f"1 warmup + median of 3 (config 4: 1 warmup + 1). GPU: bf16 kernels (config 1: "
-          f"fp32), median of 10 repetitions, each {OP_INNER} back-to-back calls between two "
+          f"fp32), median of {OP_REPS} repetitions after {OP_WARM} warmup calls, each {OP_INNER} back-to-back calls between two "
           f"events.\n")
     print("| config | operator | N | CPU fp32 ms | GPU ms | speed-up | GPU throughput |")
     print("|---|---|---:|---:|---:|---:|---|")
@@ -685,7 +687,7 @@ def main() -> int:
         print(f"[bench] timed {args.steps} steps: {step_ms:.3f} ms/step", file=sys.stderr, flush=True)
 
         # per-operator event timing
-        reps = max(5, args.steps)
+        reps = max(OP_REPS, args.steps)
         op_ms = {k: statistics.median(event_time_ms(torch, f, reps, inner=OP_INNER))
                  for k, f in ops.items()}
 
