@@ -154,6 +154,40 @@ def event_time_ms(torch, fn, reps: int, warm: int = OP_WARM, flush=None, inner: 
     return out
 
 
+def ln_cold_ms(torch, C, n: int, ln_w, ln_b, reps: int, dev) -> float:
+    """Per-launch LayerNorm time over [1, n, n, 128] bf16 with inputs and
+    outputs outside every cache: K launches, launch k reading its own input
+    (K inputs in rotation, together at least 768 MiB, three times the
+    256 MiB MALL, so an input was last touched K - 1 launches earlier) and
+    writing its own output.  The K launches are captured in a HIP graph and
+    replayed between two events, so the figure is device time (no host
+    dispatch between launches); a 1 GiB read ahead of the first event keeps
+    the queue busy.  Median over reps of (elapsed / K)."""
+    per = n * n * C_Z * 2
+    k = max(4, -(-(768 << 20) // per))
+    xs = [torch.randn(1, n, n, C_Z, device=dev).to(torch.bfloat16) for _ in range(k)]
+    flush = torch.zeros(1 << 30, dtype=torch.uint8, device=dev)
+    run = lambda: [C.layernorm(x, ln_w, ln_b, 1e-5) for x in xs]  # noqa: E731
+    run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ys = run()
+    out = []
+    for rep in range(reps + 2):
+        flush.sum()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        b.synchronize()
+        if rep >= 2:
+            out.append(a.elapsed_time(b) / k)
+    del ys, graph, xs, flush
+    return statistics.median(out)
+
+
 def host_cpu() -> dict:
     """CPU model and physical core count of this host (from /proc/cpuinfo)."""
     model, cores = None, set()
@@ -709,12 +743,15 @@ def main() -> int:
         sizes = {f"n{n}": gpu_ops_at(torch, C, dev, n, tail, reps)
                  for n, tail in ((256, 224), (2 * N, 0))}
 
-        # LayerNorm bandwidth with the 256 MiB MALL flushed before every launch
-        # cold launches: reading a 1 GiB buffer first evicts the 256 MiB MALL with
-        # clean lines (a write would leave dirty lines to drain during the launch)
+        # LayerNorm bandwidth with cold caches: launches over rotating inputs
+        # larger than the 256 MiB MALL (ln_cold_ms); and, for comparison, one
+        # launch after a 1 GiB read that evicts the MALL with clean lines,
+        # timed between two events (that figure also holds the launch's
+        # dispatch latency after the first event)
         flush_buf = torch.zeros(1 << 30, dtype=torch.uint8, device=dev)
-        ln_ms_cold = statistics.median(event_time_ms(torch, ops["layernorm"], reps,
-                                                     flush=lambda: flush_buf.sum()))
+        ln_ms_cold = ln_cold_ms(torch, C, N, ln_w, ln_b, reps, dev)
+        ln_ms_cold_single = statistics.median(event_time_ms(torch, ops["layernorm"], reps,
+                                                            flush=lambda: flush_buf.sum()))
         # the fp8 a/b storage experiment (outside the bf16 contract): the
         # tri-mul outgoing forward with a and b in fp8 E4M3, against the bf16
         # kernels' output (informational)
@@ -747,8 +784,8 @@ def main() -> int:
         z2 = torch.randn(1, 2 * N, 2 * N, C_Z, device=dev).to(torch.bfloat16)
         ln2 = lambda: C.layernorm(z2, ln_w, ln_b, 1e-5)  # noqa: E731
         ln2_ms = statistics.median(event_time_ms(torch, ln2, reps))
-        ln2_ms_cold = statistics.median(event_time_ms(torch, ln2, reps, flush=lambda: flush_buf.sum()))
         del z2, flush_buf
+        ln2_ms_cold = ln_cold_ms(torch, C, 2 * N, ln_w, ln_b, reps, dev)
         if args.calibrate_copy > 0:
             src = torch.ones((args.calibrate_copy << 20) // 4, device=dev)
             dst = torch.empty_like(src)
@@ -819,7 +856,11 @@ def main() -> int:
         "ms_cold": round(ln_ms_cold, 4),
         "gbps_cold": round(lnb / (ln_ms_cold * 1e-3) / 1e9, 1),
         "frac_hbm_cold": round(lnb / (ln_ms_cold * 1e-3) / PEAK_HBM_BYTES, 4),
-        "note": "cold = a 1 GiB read before each launch evicts the 256 MiB MALL",
+        "ms_cold_single_launch": round(ln_ms_cold_single, 4),
+        "note": ("cold = launches replayed back to back from a HIP graph, each over its own input, "
+                 "the inputs in rotation (at least 768 MiB, 3x the 256 MiB MALL); "
+                 "ms_cold_single_launch = one launch after a 1 GiB read, between two events "
+                 "(includes the launch's dispatch latency)"),
     }
     ln2b = ln_bytes(2 * N)
     per_op[f"layernorm_n{2 * N}"] = {
