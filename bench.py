@@ -317,8 +317,8 @@ def algorithmic_bytes(N: int, B: int = 1) -> dict:
         "trimul_prologue": pair + mask + 2 * plane,
         "trimul_contract": 3 * plane,
         "trimul_epilogue": plane + 2 * pair,
-        "triattn_prologue": pair + 4 * pair + bias32,
-        "triattn_flash": 4 * pair + bias32 + mask + pair,
+        "triattn_prologue": pair + 4 * pair + bias32 + mask + mask / 16,
+        "triattn_flash": 4 * pair + bias32 + mask / 16 + pair,
         "triattn_out": 2 * pair,
         "layernorm": 2 * pair,
         "pair_transition": 2 * pair + mask,

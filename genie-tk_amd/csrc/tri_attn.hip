@@ -85,6 +85,13 @@ template <typename T> struct AttnWs {
   // order (bias_frag_off; then bias is empty)
   T* og;
   float* biasf;
+  // (row, head) flash path, else null: the key-mask bits of every attention
+  // row (B x Np x Np/32 words: bit j of word t is key 32t + j, set for a
+  // mask value other than 1) and the flags of each key tile (B x Np x Np/32:
+  // bit 0 some key below N without mask bias, bit 1 some mask value neither
+  // 0 nor 1), written by the prologue's bias pass
+  uint32_t* mbits;
+  int* mflags;
   // q, k, v^T and the gate hold `rows` rows per batch element, from absolute
   // row r0 on: all Np rows from 0, or one chunk of rows (chunked attention).
   // The bias always holds every row.  (The fp32 and raw-op kernels use the
@@ -151,6 +158,8 @@ static AttnWs<T> carve_attn_ws(Carve& cv, int64_t B, int64_t Np, int H, int ch, 
   w.bias = rh ? nullptr : cv.take<T>(B * H * Np * Np);
   w.og = rh ? cv.take<T>(B * w.rows * Np * ch) : nullptr;
   w.biasf = rh ? cv.take<float>(B * H * Np * Np) : nullptr;
+  w.mbits = rh ? cv.take<uint32_t>(B * Np * (Np / 32)) : nullptr;
+  w.mflags = rh ? cv.take<int>(B * Np * (Np / 32)) : nullptr;
   return w;
 }
 
@@ -266,8 +275,8 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
 // .. r0 + nrows - 1 of every batch element: [B][nrows][Np / 32].
 template <int CIN, int H, int MODE>
 __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
-    const bf16* __restrict__ x, TriAttnPacked<bf16> w, AttnWs<bf16> ws, int N, int Np,
-    int starting, float eps, int64_t ntiles, int r0, int nrows) {
+    const bf16* __restrict__ x, const float* __restrict__ mask, TriAttnPacked<bf16> w, AttnWs<bf16> ws,
+    int N, int Np, int starting, float eps, int64_t ntiles, int r0, int nrows) {
   static_assert((MODE & 3) != 0 && MODE <= 15, "q/k/v/gate, bias, or both");
   constexpr int CH = H * HD;
   constexpr int KCH = CIN / 16;
@@ -310,8 +319,13 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
   int64_t tile = (int64_t)wave * gridDim.x + blockIdx.x;
   TileWalk tw;
   tw.init(tile, tstride, nrows, vtiles);  // row r0 + tw.r
-  // (exists = false: a tile past the end, also read as pair 0)
-  auto load_rows = [&](Frag<bf16>* raw, const TileWalk& t, bool exists) {
+  // (exists = false: a tile past the end, also read as pair 0).  With the
+  // bias (mode bit 1) on the (row, head) path, also the mask value of key
+  // position t.c * 32 + i32 of attention row r (pair (r, k) for the starting
+  // node, (k, r) for the ending node; 1 outside the grid).
+  constexpr bool kMaskBits = (MODE & 2) != 0;
+  const bool mbits_on = kMaskBits && ws.mbits != nullptr;
+  auto load_rows = [&](Frag<bf16>* raw, float& mv, const TileWalk& t, bool exists) {
     const int jo = t.c * 32 + prow;
     const int tr = r0 + t.r;
     const bool ok = exists && tr < N && jo < N;
@@ -319,8 +333,15 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
     const bf16* src = x + (ok ? (((int64_t)t.b * N + p) * N + q) * CIN : 0) + half * (CIN / 2);
 #pragma unroll
     for (int ch = 0; ch < KCH; ++ch) raw[ch].load(src + ch * 8);
+    if (mbits_on) {
+      const int k = t.c * 32 + i32;
+      const bool mok = exists && mask != nullptr && tr < N && k < N;
+      const int64_t mi = (int64_t)t.b * N * N + (starting ? (int64_t)tr * N + k : (int64_t)k * N + tr);
+      mv = mok ? mask[mok ? mi : 0] : 1.f;
+    }
   };
   Frag<bf16> raw[KCH];
+  float mval = 1.f;  // the mask value of this tile's key position (mbits_on)
   // One tile.  Every path through it issues the same loads and stores (no
   // branch around any of them), and the first tile is peeled off the loop, so
   // the compiler's waits for the prefetched rows count the stores issued
@@ -329,6 +350,7 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
     const int vt = tw.c;
     const int r = r0 + tw.r;  // destination row
     const int b = tw.b;
+    const float m_this = mval;
     const int jown = vt * 32 + prow;            // this lane's pair (A/B operand side)
     Frag<bf16> xf[KCH];
     const bool valid = r < N && jown < N;
@@ -340,7 +362,7 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
     {
       TileWalk nx = tw;
       nx.next();
-      load_rows(raw, nx, tile + tstride < ntiles);
+      load_rows(raw, mval, nx, tile + tstride < ntiles);
     }
     const int64_t rowbase = ws.row(b, r);  // q/k/v^T/gate row in the workspace
     const int j0 = vt * 32 + 16 * half;         // first of this lane's 16 positions
@@ -391,6 +413,21 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
       o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
       o[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
     }
+    // key-mask word and flags of (row r, key tile vt): bit j of the word is
+    // key 32 vt + j (mask != 1); flags bit 0: some key below N without mask
+    // bias, bit 1: some mask value neither 0 nor 1
+    if (mbits_on) {
+      const int k = vt * 32 + i32;
+      const bool masked = m_this != 1.f;
+      const uint32_t word = (uint32_t)__ballot(masked);  // lanes 0-31 (the upper half repeats them)
+      const int fl = (__ballot(k < N && !masked) != 0ull ? 1 : 0) |
+                     (__ballot(masked && m_this != 0.f) != 0ull ? 2 : 0);
+      const int64_t wi = ((int64_t)b * Np + r) * (Np / 32) + vt;
+      if (lane == 0) {
+        ws.mbits[wi] = word;
+        ws.mflags[wi] = fl;
+      }
+    }
     // triangle bias [b][h][r][j]: lanes with i32 < H hold head i32
     if constexpr ((MODE & 2) != 0) {
       const bf16* wb = wl + 4 * PE + opaque_zero();
@@ -431,7 +468,7 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
     }
   };
   if (tile < ntiles) {
-    load_rows(raw, tw, true);
+    load_rows(raw, mval, tw, true);
     body(tile);
     tile += tstride;
     tw.next();
@@ -1016,7 +1053,11 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
 //     output projection's fragment order (og_frag_off).  The next tile's q
 //     copy is issued before those stores.
 //   * The excluded-key bits of the row are kept in one VGPR (lane t: key
-//     tile t) and read with v_readlane per tile.
+//     tile t) and read with v_readlane per tile.  The prologue's bias pass
+//     wrote them (one word and one flags word per key tile): the block loads
+//     64 contiguous bytes instead of the row's mask values, which for the
+//     ending node are a column of the mask, one cache line per key, read by
+//     every wave of every head's block.
 //   * Blocks run head-major, so the blocks of one XCD read one or two heads'
 //     triangle bias.  That bias (1 MiB per head at Np = 512) is re-read by
 //     every row's block, while K^T, V^T, q and the gate are read once: their
@@ -1071,32 +1112,22 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
   }
 
   // Masked keys of this row (mask != 1), one bit per key (bit j of lane t's
-  // word is key 32t + j).  They take the reference's additive bias
-  // inf * (mask - 1), here in log2 units; padding keys (k >= N, the tail of
-  // the last tiles) take no weight.  row_frac: some mask value is neither 0
-  // nor 1, whose bias is then computed from the value.
+  // word is key 32t + j), from the row's mask words (written with the bias).
+  // They take the reference's additive bias inf * (mask - 1), here in log2
+  // units; padding keys (k >= N, the tail of the last tiles) take no weight.
+  // row_frac: some mask value is neither 0 nor 1, whose bias is then
+  // computed from the value (mrow).  A row where every key carries a mask
+  // bias goes straight to the exact pass, where the reference's fp32
+  // arithmetic is followed (with inf = 1e9 every score of such a row rounds
+  // to the same value: uniform attention).  Wave-uniform: every wave reads
+  // the same row.
   const float* mrow = mask ? mask + (int64_t)b * N * N + (starting ? (int64_t)r * N : r) : nullptr;
   const int64_t mks = starting ? 1 : N;
-  uint32_t kmv = 0;
-  bool any = mrow == nullptr, frac = false;
-  for (int k0 = 0; k0 < Np; k0 += 64) {
-    const int k = k0 + lane;
-    const float mval = k < N && mrow ? mrow[k * mks] : 1.f;
-    const bool masked = mval != 1.f;
-    any = any || (k < N && !masked);
-    frac = frac || (masked && mval != 0.f);
-    const unsigned long long mb = __ballot(masked);
-    const int w0 = k0 >> 5;
-    if (lane == w0) kmv = (uint32_t)mb;
-    if (lane == w0 + 1) kmv = (uint32_t)(mb >> 32);
-  }
-  // Some key carries no mask bias: the max-free pass can hold its scores.  A
-  // row without one goes straight to the exact pass, where the reference's
-  // fp32 arithmetic is followed (with inf = 1e9 every score of such a row
-  // rounds to the same value: uniform attention).  Wave-uniform: every wave
-  // reads the same row.
-  const bool row_valid = __ballot(any) != 0ull;
-  const bool row_frac = __ballot(frac) != 0ull;
+  const int64_t mwi = ((int64_t)b * Np + r) * (Np / 32) + lane;
+  const uint32_t kmv = lane < nt ? ws.mbits[mwi] : 0u;
+  const int mfl = lane < nt ? ws.mflags[mwi] : 0;
+  const bool row_valid = __ballot((mfl & 1) != 0) != 0ull;
+  const bool row_frac = __ballot((mfl & 2) != 0) != 0ull;
   const float madd0 = -inf * kLog2e;  // the bias of a key with mask == 0
 
   const uint32_t stg_lds = lds_addr(stg[wave]);
@@ -1645,7 +1676,7 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
       const int grid = (int)std::min<int64_t>(device_cus(), (ptiles + 7) / 8);
       StageTimer timer("triattn_prologue", st);
       triattn_prologue_bf16_kernel<CIN, H, MODE><<<grid, 1024, 0, st>>>(
-          (const bf16*)x, w, a, (int)N, Np, starting, eps, ptiles, r0, nrows);
+          (const bf16*)x, mask, w, a, (int)N, Np, starting, eps, ptiles, r0, nrows);
     };
     auto flash = [&](int r0, int nrows) {
       if (rh) {
