@@ -417,11 +417,12 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
     // key 32 vt + j (mask != 1); flags bit 0: some key below N without mask
     // bias, bit 1: some mask value neither 0 nor 1
     if (mbits_on) {
-      const int k = vt * 32 + i32;
       const bool masked = m_this != 1.f;
       const uint32_t word = (uint32_t)__ballot(masked);  // lanes 0-31 (the upper half repeats them)
-      const int fl = (__ballot(k < N && !masked) != 0ull ? 1 : 0) |
-                     (__ballot(masked && m_this != 0.f) != 0ull ? 2 : 0);
+      const int nin = N - vt * 32;                         // keys of the tile below N
+      const uint32_t inside = nin >= 32 ? 0xffffffffu : nin > 0 ? (1u << nin) - 1u : 0u;
+      const int fl = ((inside & ~word) != 0u ? 1 : 0) |
+                     (word != 0u && __ballot(masked && m_this != 0.f) != 0ull ? 2 : 0);
       const int64_t wi = ((int64_t)b * Np + r) * (Np / 32) + vt;
       if (lane == 0) {
         ws.mbits[wi] = word;
@@ -1251,7 +1252,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
     const float inv = 1.0f / l_tot;
     const int lne = lane + opaque_zero();
     const int ehalf = lne >> 5;
-    __builtin_amdgcn_s_waitcnt(0);  // the gate tile has landed (wave-local region)
+    // The gate tile has landed (wave-local region): it was copied before
+    // every bias load of this query tile, and at most the last KB tiles'
+    // bias loads (the next query tile's first) may still be outstanding;
+    // the exact pass waits for each of its own loads.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm<4 * KB>());
     bf16x4 gv[4];
 #pragma unroll
     for (int g = 0; g < 4; ++g) gv[g] = __builtin_bit_cast(bf16x4, read_cq4(lne, 8 * g + 4 * ehalf));
