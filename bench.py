@@ -312,13 +312,13 @@ def algorithmic_bytes(N: int, B: int = 1) -> dict:
     pair = 2.0 * B * N * N * C_Z
     mask = 4.0 * B * N * N
     plane = 2.0 * B * N * N * C_HID
-    bias32 = 4.0 * B * HEADS * N * N
+    bias16 = 2.0 * B * HEADS * N * N  # the triangle bias, bf16
     return {
         "trimul_prologue": pair + mask + 2 * plane,
         "trimul_contract": 3 * plane,
         "trimul_epilogue": plane + 2 * pair,
-        "triattn_prologue": pair + 4 * pair + bias32 + mask + mask / 16,
-        "triattn_flash": 4 * pair + bias32 + mask / 16 + pair,
+        "triattn_prologue": pair + 4 * pair + bias16 + mask + mask / 16,
+        "triattn_flash": 4 * pair + bias16 + mask / 16 + pair,
         "triattn_out": 2 * pair,
         "layernorm": 2 * pair,
         "pair_transition": 2 * pair + mask,

@@ -81,10 +81,10 @@ template <typename T> struct AttnWs {
   // (row, head) flash path (bf16 module forward with Np <= kFlashRhMaxNp),
   // else null: the gated attention output (B x rows x Np x c_h, fragment
   // order: see the flash kernel), and the
-  // triangle bias in fp32, B x H x Np x Np in the flash kernel's fragment
-  // order (bias_frag_off; then bias is empty)
+  // triangle bias without its per-head constant in bf16, B x H x Np x Np in
+  // the flash kernel's fragment order (bias_frag_off; then bias is empty)
   T* og;
-  float* biasf;
+  bf16* biasfr;
   // (row, head) flash path, else null: the key-mask bits of every attention
   // row (B x Np x Np/32 words: bit j of word t is key 32t + j, set for a
   // mask value other than 1) and the flags of each key tile (B x Np x Np/32:
@@ -118,17 +118,18 @@ __host__ __device__ __forceinline__ int64_t og_frag_off(int64_t tile, int ks, in
   return ((tile * 8 + ks) * 64 + lane) * 8;
 }
 
-// fp32 triangle bias of the (row, head) path, per batch element, in the flash
-// kernel's S^T fragment order: tile (query tile qt, key tile kt) of head h is
-// 4 slabs g of [64 lanes][4], lane = 32 * ((kk >> 2) & 1) + (q & 31) for the
-// tile's key kk = 8g + 4 * ((kk >> 2) & 1) + rr, rr = kk & 3.  A wave loads
-// its bias tile as 4 contiguous 1 KiB pieces.  Element offset of (h, query
-// q, key tile kt, keys kk .. kk+3 with kk % 4 == 0):
+// bf16 triangle bias of the (row, head) path, per batch element, in the
+// flash kernel's S^T fragment order: tile (query tile qt, key tile kt) of
+// head h is 2 slabs s of [64 lanes][8], lane = 32 * ((kk >> 2) & 1) + (q & 31)
+// for the tile's key kk = 8g + 4 * ((kk >> 2) & 1) + rr (rr = kk & 3), at
+// element 4 * (g & 1) + rr of slab s = g / 2: S^T register 4g + rr of the
+// lane.  A wave loads its bias tile as 2 contiguous 1 KiB pieces.  Element
+// offset of (h, query q, key tile kt, keys kk .. kk+3 with kk % 4 == 0):
 __host__ __device__ __forceinline__ uint32_t bias_frag_off(int h, int q, int kt, int kk, int Np) {
   const int nt = Np / 32;
   const uint32_t tile = (uint32_t)((h * nt + (q >> 5)) * nt + kt);
   const int g = kk >> 3, hh = (kk >> 2) & 1;
-  return ((tile * 4 + g) * 64 + hh * 32 + (q & 31)) * 4;
+  return ((tile * 2 + (g >> 1)) * 64 + hh * 32 + (q & 31)) * 8 + (g & 1) * 4;
 }
 
 // Position of key j inside a V^T row: within each group of 16 keys, keys
@@ -157,7 +158,7 @@ static AttnWs<T> carve_attn_ws(Carve& cv, int64_t B, int64_t Np, int H, int ch, 
   const bool rh = fast && ch > 0 && sizeof(T) == 2 && Np <= kFlashRhMaxNp;
   w.bias = rh ? nullptr : cv.take<T>(B * H * Np * Np);
   w.og = rh ? cv.take<T>(B * w.rows * Np * ch) : nullptr;
-  w.biasf = rh ? cv.take<float>(B * H * Np * Np) : nullptr;
+  w.biasfr = rh ? cv.take<bf16>(B * H * Np * Np) : nullptr;
   w.mbits = rh ? cv.take<uint32_t>(B * Np * (Np / 32)) : nullptr;
   w.mflags = rh ? cv.take<int>(B * Np * (Np / 32)) : nullptr;
   return w;
@@ -268,7 +269,8 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
 //     Padding values are those of triattn_prologue_kernel.
 // ---------------------------------------------------------------------------
 // MODE bit 0: q, k, v^T and gate; bit 1: the triangle bias; bit 2: the bias
-// in fp32 (ws.biasf) instead of bf16 (ws.bias); bit 3: q, k, v^T and gate in
+// in the flash kernel's fragment order without its per-head constant
+// (ws.biasfr) instead of row-major (ws.bias); bit 3: q, k, v^T and gate in
 // the tiled layout of the (row, head) flash kernel (each (row, head) block of
 // 32 channels x Np positions as Np/32 tiles [32 channels][32 positions],
 // 2 KiB contiguous) instead of channel-major rows.  The tiles cover rows r0
@@ -460,18 +462,21 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
       // lanes i32 >= H store nothing (out-of-range offset, no branch)
       const float bb = bl[4 * CH + (i32 & (H - 1))];
       if constexpr ((MODE & 4) != 0) {
-        // fp32, in the flash kernel's S^T fragment order (bias_frag_off)
-        float bv[16];
-#pragma unroll
-        for (int m = 0; m < 16; ++m) bv[m] = m < nvalid ? ab[m] + bb : 0.f;
-        const auto brs = buf_rsrc(ws.biasf + (int64_t)b * H * Np * Np, (uint32_t)(H * Np * Np * 4));
+        // bf16 in the flash kernel's S^T fragment order (bias_frag_off),
+        // without the head's constant bb: a logit offset shared by every
+        // query and key of the head, which the softmax cancels.  bb carries
+        // the LayerNorm beta (folded in at packing), so what remains,
+        // LN(x) . (gamma * w), is the part that varies between pairs.
+        (void)bb;
+        const auto brs = buf_rsrc(ws.biasfr + (int64_t)b * H * Np * Np, (uint32_t)(H * Np * Np * 2));
 #pragma unroll
         for (int a = 0; a < 4; ++a) {
           // positions j0 + 4a .. +3: key kk = 16*half + 4a + rr of key tile vt
-          const uint32_t off = i32 < H ? bias_frag_off(i32, r, vt, 16 * half + 4 * a, Np) * 4 : kBufSkip;
-          buf_store16(brs, off,
-                      make_uint4(__float_as_uint(bv[4 * a]), __float_as_uint(bv[4 * a + 1]),
-                                 __float_as_uint(bv[4 * a + 2]), __float_as_uint(bv[4 * a + 3])));
+          const uint32_t off = i32 < H ? bias_frag_off(i32, r, vt, 16 * half + 4 * a, Np) * 2 : kBufSkip;
+          float bv[4];
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) bv[rr] = 4 * a + rr < nvalid ? ab[4 * a + rr] : 0.f;
+          buf_store4(brs, off, bv[0], bv[1], bv[2], bv[3]);
         }
       } else {
         uint32_t pk[8];
@@ -1168,7 +1173,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
   };
   const bf16* q_row = ws.q + ((rowbase * H + h) * HD) * (int64_t)Np;
   const bf16* g_row = ws.gate + (rowbase * CH + h * HD) * (int64_t)Np;
-  const float* b_head = ws.biasf + (int64_t)(b * H + h) * Np * Np;  // wave-uniform
+  const bf16* b_head = ws.biasfr + (int64_t)(b * H + h) * Np * Np;  // wave-uniform
 
   // K fragments (transposing reads of K^T) and V^T fragments: per-lane offsets
   const int trG = lane >> 4;
@@ -1178,18 +1183,27 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
   typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
   typedef short s16x8 __attribute__((ext_vector_type(8)));
   const bf16x2_t ones2 = {(bf16)1.0f, (bf16)1.0f};
-  // Bias tile t of query tile q0 in the S^T accumulator layout: register
-  // 4g + rr <-> key 32t + 8g + 4*half + rr, stored in that order
-  // (bias_frag_off): 4 loads of 1 KiB contiguous per wave (a wave-uniform
-  // base plus a 32-bit per-lane byte offset, the saddr form).
+  // Bias tile t of query tile q0 (bf16) in the S^T accumulator layout:
+  // register 4g + rr <-> key 32t + 8g + 4*half + rr, stored in that order
+  // (bias_frag_off): 2 loads of 1 KiB contiguous per wave (a wave-uniform
+  // base plus a 32-bit per-lane byte offset, the saddr form), widened to
+  // fp32 where the tile's S accumulation starts.
   const uint32_t b_lane = (uint32_t)lane * 16;
-  auto load_bias = [&](f32x16& dst, int q0, int t) {
-    const uint32_t off = b_lane + (uint32_t)(((q0 >> 5) * nt + t) * 4096);
+  auto load_bias = [&](uint4* dst, int q0, int t) {
+    const uint32_t off = b_lane + (uint32_t)(((q0 >> 5) * nt + t) * 2048);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(reinterpret_cast<const char*>(b_head) + off + 1024 * g);
+    for (int sl = 0; sl < 2; ++sl)
+      dst[sl] = *reinterpret_cast<const uint4*>(reinterpret_cast<const char*>(b_head) + off + 1024 * sl);
+  };
+  auto widen_bias = [](f32x16& dst, const uint4* p) {
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) dst[4 * g + rr] = v[rr];
+    for (int sl = 0; sl < 2; ++sl) {
+      const uint32_t d[4] = {p[sl].x, p[sl].y, p[sl].z, p[sl].w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        dst[8 * sl + 2 * k] = __uint_as_float(d[k] << 16);
+        dst[8 * sl + 2 * k + 1] = __uint_as_float(d[k] & 0xffff0000u);
+      }
     }
   };
   // s += K Q^T for key tile t (s holds the bias tile: S^T in log2 units)
@@ -1252,8 +1266,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
     }
   };
 
-  // Bias of the next KB S tiles, prefetched KB - 1 tiles ahead; S^T
-  // accumulates in place.  Each tile's loads go out unconditionally (the
+  // Bias of the next KB S tiles, prefetched KB - 1 tiles ahead (bf16, 8
+  // registers a tile; four tiles ahead measured slower); S^T accumulates on
+  // the widened bias.  Each tile's loads go out unconditionally (the
   // last KB of a query tile fetch the first KB of the wave's next query
   // tile, or again the current one at the end), so the compiler's waits
   // count them exactly.
@@ -1273,7 +1288,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
     // every bias load of this query tile, and at most the last KB tiles'
     // bias loads (the next query tile's first) may still be outstanding;
     // the exact pass waits for each of its own loads.
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm<4 * KB>());
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm<2 * KB>());
     bf16x4 gv[4];
 #pragma unroll
     for (int g = 0; g < 4; ++g) gv[g] = __builtin_bit_cast(bf16x4, read_cq4(lne, 8 * g + 4 * ehalf));
@@ -1301,7 +1316,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
     *reinterpret_cast<uint4*>(reinterpret_cast<char*>(ws.og) + o_off + 1024) = cB;
   };
 
-  f32x16 bq[KB];
+  uint4 bq[KB][2];
   int qt = wave;
   if (qt < nq) {
     issue_cq(q_row + qt * 1024);
@@ -1337,9 +1352,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
     for (int t = 0; fast_ok && t < nt; t += KB) {
 #pragma unroll
       for (int u = 0; u < KB; ++u) {
-        s_tile(t + u, bq[u], qf);
-        mask_tile(t + u, bq[u], kBinary);
-        pv_tile(t + u, bq[u], o, l_run);
+        f32x16 sc;
+        widen_bias(sc, bq[u]);
+        s_tile(t + u, sc, qf);
+        mask_tile(t + u, sc, kBinary);
+        pv_tile(t + u, sc, o, l_run);
         const bool wrap = t + u + KB >= nt;
         load_bias(bq[u], wrap ? q0n : q0, wrap ? t + u + KB - nt : t + u + KB);
         // one sub-tile at a time: interleaving them would need several S
@@ -1360,7 +1377,11 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
       float m_ref = -INFINITY, m_use = 0.f;
       for (int t = 0; t < nt; ++t) {
         f32x16 sc;
-        load_bias(sc, q0, t);
+        {
+          uint4 bp[2];
+          load_bias(bp, q0, t);
+          widen_bias(sc, bp);
+        }
         s_tile(t, sc, qf);
         mask_tile(t, sc, kFrac);
 #pragma unroll
