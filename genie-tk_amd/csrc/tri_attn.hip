@@ -1206,18 +1206,26 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
       }
     }
   };
-  // s += K Q^T for key tile t (s holds the bias tile: S^T in log2 units)
-  auto s_tile = [&](int t, f32x16& s, const Frag<bf16>* qf) {
+  // K fragments of key tile t (transposing reads of K^T)
+  auto k_read = [&](int t, Frag<bf16>* kf) {
     const char* kt_base = kv + t * 2048 + kt_lane;
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       const s16x4 p0 = lds_read_tr16(kt_base + (m * 16) * 64);
       const s16x4 p1 = lds_read_tr16(kt_base + (m * 16 + 4) * 64);
       const s16x8 v8 = {p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]};
-      Frag<bf16> kf;
-      kf.v = __builtin_bit_cast(bf16x8, v8);
-      mma(s, kf, qf[m]);
+      kf[m].v = __builtin_bit_cast(bf16x8, v8);
     }
+  };
+  // s += K Q^T for key tile t (s holds the bias tile: S^T in log2 units)
+  auto s_mma = [&](f32x16& s, const Frag<bf16>* kf, const Frag<bf16>* qf) {
+#pragma unroll
+    for (int m = 0; m < 2; ++m) mma(s, kf[m], qf[m]);
+  };
+  auto s_tile = [&](int t, f32x16& s, const Frag<bf16>* qf) {
+    Frag<bf16> kf[2];
+    k_read(t, kf);
+    s_mma(s, kf, qf);
   };
   // padding keys of tile t take no weight, masked keys their mask bias;
   // FRAC: mask values other than 0 are read back for their bias (only the
@@ -1317,6 +1325,9 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
   };
 
   uint4 bq[KB][2];
+  // K fragments of the fast pass's next tile, read one tile ahead (the last
+  // tile of a query tile reads tile 0 for the next query tile)
+  Frag<bf16> kn[2];
   int qt = wave;
   if (qt < nq) {
     issue_cq(q_row + qt * 1024);
@@ -1327,6 +1338,7 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();  // K^T / V^T resident for every wave
+  k_read(0, kn);
   for (; qt < nq; qt += NW) {
     const int q0 = qt * 32;
     const int q0n = (qt + NW < nq ? qt + NW : qt) * 32;  // the query tile to prefetch for
@@ -1354,7 +1366,8 @@ __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void t
       for (int u = 0; u < KB; ++u) {
         f32x16 sc;
         widen_bias(sc, bq[u]);
-        s_tile(t + u, sc, qf);
+        s_mma(sc, kn, qf);
+        k_read(t + u + 1 < nt ? t + u + 1 : 0, kn);
         mask_tile(t + u, sc, kBinary);
         pv_tile(t + u, sc, o, l_run);
         const bool wrap = t + u + KB >= nt;
