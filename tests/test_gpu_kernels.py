@@ -218,15 +218,45 @@ def logit_offset_params(offset: float, seed: int = 11):
     return H.bf16_params(P)
 
 
+def logit_offset_qk_params(offset: float, seed: int = 11):
+    """Tri-attn parameters whose logits are shifted by about `offset`
+    (natural units) through q . k: channels 64..127 are the constant 1 after
+    the LayerNorm (weight 0, bias 1) and feed only the last head dimension
+    d0 of each head, q[d0] = 64 w and k[d0] = +-64 w, so q . k / sqrt(32)
+    gains the same constant for every query and key.  The triangle bias and
+    the other dimensions see channels 0..63 only."""
+    P = H.draw_params(H.tri_attn_shapes(128, 128, 4), seed=seed, bias_random=True)
+    hi = slice(64, 128)
+    P["layer_norm.weight"][hi] = 0.0
+    P["layer_norm.bias"][hi] = 1.0
+    P["linear.weight"][:, hi] = 0.0
+    for k in ("mha.linear_q.weight", "mha.linear_k.weight", "mha.linear_v.weight", "mha.linear_g.weight"):
+        P[k][:, hi] = 0.0
+    w = float(np.sqrt(abs(offset) * np.sqrt(32.0)) / 64.0)
+    for h in range(4):
+        d0 = 32 * h + 31
+        P["mha.linear_q.weight"][d0, :] = 0.0
+        P["mha.linear_k.weight"][d0, :] = 0.0
+        P["mha.linear_q.weight"][d0, hi] = w
+        P["mha.linear_k.weight"][d0, hi] = w if offset >= 0 else -w
+    return H.bf16_params(P)
+
+
 @pytest.mark.parametrize("starting", [True, False])
 @pytest.mark.parametrize("offset", [200.0, -200.0])
-def test_tri_attn_logit_offset(starting, offset):
-    """Logits shifted by +-200 for every key overflow (or underflow) the
-    kernels' max-free pass; the exact online-softmax pass must then produce
-    the reference result, for masked and unmasked keys."""
+@pytest.mark.parametrize("via", ["bias", "qk"])
+def test_tri_attn_logit_offset(starting, offset, via):
+    """Logits shifted by +-200 for every key.  Through the triangle bias the
+    shift sits in the bias's per-head constant (the LayerNorm beta folded at
+    packing), which the N <= 1024 bf16 kernels drop because the softmax
+    cancels it; the other kernels add it and overflow (or underflow) their
+    max-free pass.  Through q . k every kernel's max-free pass overflows
+    (or underflows), and the exact online-softmax pass must produce the
+    reference result, for masked and unmasked keys."""
     N = 64
-    log(f"tri_attn logit offset start={starting} offset={offset}")
-    P = logit_offset_params(offset)
+    log(f"tri_attn logit offset start={starting} offset={offset} via={via}")
+    params = logit_offset_params if via == "bias" else logit_offset_qk_params
+    P = params(offset)
     x = H.bf16_round(H.pair_input(2, N, 128, seed=12))
     # masked keys in every row and column, but none fully masked: a row with
     # no valid key is uniform in the reference only while |logit| < 32
@@ -244,7 +274,7 @@ def test_tri_attn_logit_offset(starting, offset):
     ref_nm = pair_ops.tri_attn(x, None, P, starting, 4, dtype=np.float64)
     check_bf16(to_np(y_nm), ref_nm, "tri_attn logit offset, mask=None")
     # the shift changes nothing: the same module without it
-    ref0 = pair_ops.tri_attn(x, None, logit_offset_params(0.0), starting, 4, dtype=np.float64)
+    ref0 = pair_ops.tri_attn(x, None, params(0.0), starting, 4, dtype=np.float64)
     np.testing.assert_allclose(ref_nm, ref0, atol=1e-6)
 
 
