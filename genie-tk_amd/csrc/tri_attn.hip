@@ -1089,11 +1089,15 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
 //     64 KiB window the kernel takes 133 us).
 // The output projection (W_o, b_o, residual) runs in triattn_out_kernel.
 // ---------------------------------------------------------------------------
-template <int NPM>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) void triattn_flash_rh_kernel(
+// NW waves per block: 8 at Np <= 512 (two blocks per CU), 16 at Np = 1024,
+// where K^T and V^T take 128 KiB of LDS and one block fills the CU (16 x 2 KiB
+// of staging beside them: 160 KiB), so the CU still holds 16 waves.
+template <int NPM, int NW>
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) void triattn_flash_rh_kernel(
     const float* __restrict__ mask, AttnWs<bf16> ws, int N, int Np, int starting, int r0, int nrows,
     float inf) {
-  constexpr int H = 4, NW = 8, CH = H * HD;
+  constexpr int H = 4, CH = H * HD;
+  static_assert(2 * NPM / 32 * 2048 + NW * 2048 <= 160 * 1024, "K^T, V^T and staging in one CU's LDS");
   constexpr int NTM = NPM / 32;       // key tiles at most
   constexpr float kRescale = 8.0f;    // lazy-rescale threshold (log2 units)
   static_assert(NTM <= 64, "excluded-key bits: one word per lane");
@@ -1741,11 +1745,11 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
         {
           StageTimer timer("triattn_flash", st);
           if (Np <= 256)
-            triattn_flash_rh_kernel<256><<<(unsigned)fblocks, 512, 0, st>>>(mask, a, (int)N, Np, starting, r0, nrows, inf);
+            triattn_flash_rh_kernel<256, 8><<<(unsigned)fblocks, 512, 0, st>>>(mask, a, (int)N, Np, starting, r0, nrows, inf);
           else if (Np <= 512)
-            triattn_flash_rh_kernel<512><<<(unsigned)fblocks, 512, 0, st>>>(mask, a, (int)N, Np, starting, r0, nrows, inf);
+            triattn_flash_rh_kernel<512, 8><<<(unsigned)fblocks, 512, 0, st>>>(mask, a, (int)N, Np, starting, r0, nrows, inf);
           else
-            triattn_flash_rh_kernel<1024><<<(unsigned)fblocks, 512, 0, st>>>(mask, a, (int)N, Np, starting, r0, nrows, inf);
+            triattn_flash_rh_kernel<1024, 16><<<(unsigned)fblocks, 1024, 0, st>>>(mask, a, (int)N, Np, starting, r0, nrows, inf);
         }
         GTK_HIP_CHECK(hipGetLastError());
         const int64_t otiles = B * nrows * ((N + 31) / 32);

@@ -80,6 +80,31 @@ def test_tri_attn_forward_beyond_1024(starting, N):
 
 
 @pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("N", [600, 1024])
+def test_tri_attn_forward_np1024(starting, N):
+    """bf16 forward for 512 < Np <= 1024: the (row, head) flash kernel with
+    1024-position K^T/V^T buffers (128 KiB of LDS) in 16-wave blocks, sampled
+    rows against the float64 oracle, plus row chunks bit-identical to the
+    unchunked output."""
+    log(f"tri_attn forward (row, head) Np<=1024 N={N} starting={starting}")
+    x, m, P, L = _inputs(N)
+    rows = _rows(N, L)
+    mod = triattn_module(P, starting, 4, torch.bfloat16)
+    xd = torch.from_numpy(x).to("cuda", torch.bfloat16)
+    md = torch.from_numpy(m).to("cuda")
+    with torch.no_grad():
+        y = mod(xd, md)
+        y_chunk = mod(xd, md, chunk_size=250)
+    torch.cuda.synchronize()
+    assert torch.equal(y_chunk, y), "row chunks of 250 differ from the unchunked output"
+    sel = (lambda a: a[:, rows]) if starting else (lambda a: a[:, :, rows])
+    got = to_np(sel(y))
+    del y, y_chunk
+    ref = pair_ops.tri_attn(x, m, P, starting, 4, dtype=np.float64, rows=rows)
+    check_bf16(got, ref, f"tri_attn N={N} starting={starting}")
+
+
+@pytest.mark.parametrize("starting", [True, False])
 def test_tri_attn_row_chunks_beyond_1024(starting):
     """Row chunks on the Np > 1024 path: bit-identical to the unchunked
     output (chunk sizes that do and do not divide N)."""
