@@ -261,9 +261,10 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
 //     Lane i32 of a wave normalises pair 16*((i32>>2)&1) + 4*(i32>>3) + (i32&3)
 //     of the tile and the pairs are the MFMA A operand, so every accumulator
 //     lane holds 16 consecutive positions of one output channel.  All outputs
-//     of this path are channel-major over positions (below), so each lane
-//     writes them as 32 contiguous bytes.  Workspace layouts of the bf16 path
-//     (Np = N rounded up to 128):
+//     of this path are channel-major over positions (below): each lane writes
+//     32 contiguous bytes, or, in the (row, head) path's tiles, its pieces
+//     after a register swap so that each store writes 1 KiB whole.  Workspace
+//     layouts of the bf16 path (Np = N rounded up to 128):
 //        q, k  [B][Np r][H][32 d][Np j]    v^T [B][Np r][H][32 d][Np j] (vt_pos order)
 //        gate  [B][Np r][c_h][Np j]        bias [B][H][Np q][Np k]
 //     Padding values are those of triattn_prologue_kernel.
@@ -1068,11 +1069,13 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
 //     Layout: [kind][key tile t][32 d rows][64 bytes]; K^T rows unswizzled,
 //     V^T chunk p of row d at physical chunk p ^ ((d>>2)&3) (the read
 //     patterns of the module kernel above).
-//   * Eight waves; wave w attends query tiles w, w+8, ... in turn.  Each
+//   * NW waves (8, or 16 at Np = 1024); wave w attends query tiles w,
+//     w+NW, ... in turn.  Each
 //     query tile: q copied into the wave's 2 KiB LDS region and read back
 //     transposed, the gate tile copied into the same region behind it, then
-//     the key loop (fp32 bias tiles prefetched a tile ahead, S^T
-//     accumulated on top of them), then o / l * gate stored into og in the
+//     the key loop (bf16 bias tiles prefetched two tiles ahead and widened
+//     into the S^T accumulator, the next tile's K fragments read a tile
+//     ahead), then o / l * gate stored into og in the
 //     output projection's fragment order (og_frag_off).  The next tile's q
 //     copy is issued before those stores.
 //   * The excluded-key bits of the row are kept in one VGPR (lane t: key
@@ -1729,7 +1732,7 @@ static int fwd_triattn(const void* x, const float* mask, void* out, const void* 
   GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "attention grid too large");
   if constexpr (kFast) {
     constexpr int QT = 2;  // two 8-wave blocks of 64 queries per CU (Np > kFlashRhMaxNp)
-    const bool rh = Np <= kFlashRhMaxNp;  // (row, head) flash path, fp32 bias
+    const bool rh = Np <= kFlashRhMaxNp;  // (row, head) flash path, fragment-order bf16 bias
     auto prologue = [&](auto mode, int r0, int nrows) {
       constexpr int MODE = decltype(mode)::value;
       const int64_t ptiles = B * (int64_t)nrows * (Np / 32);
