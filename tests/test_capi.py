@@ -106,15 +106,18 @@ def test_workspace_sizes(lib):
     plane = lambda B, N, C, e: B * C * ((N + 63) // 64 * 64) ** 2 * e
     assert lib.gtk_triangle_mul_workspace_size(1, 512, 128, GTK_BF16) == 3 * (plane(1, 512, 128, 2) + 256)
     assert lib.gtk_triangle_mul_workspace_size(2, 200, 64, GTK_F32) == 3 * (plane(2, 200, 64, 4) + 256)
-    assert lib.gtk_tri_mul_workspace_size(1, 512, 128, 128, GTK_BF16) == 3 * (plane(1, 512, 128, 2) + 256)
+    # the fused forward pads each channel plane by 256 bytes (power-of-two
+    # plane strides put a prologue step's plane stores on the same HBM channels)
+    padded = lambda B, N, C, e: B * C * (((N + 63) // 64 * 64) ** 2 * e + 256)
+    assert lib.gtk_tri_mul_workspace_size(1, 512, 128, 128, GTK_BF16) == 3 * padded(1, 512, 128, 2) + 3 * 256
     assert lib.gtk_triangle_mul_workspace_size(-1, 8, 16, GTK_F32) == 0
     # tri-mul row chunks: b planes for every row, a and x planes for R rows,
     # R = chunk_rows rounded up to the contraction tile (bf16: 256 rows when
     # Np is a multiple of 256, else 128 or 64; fp32: 128 or 64)
     tc = lambda N, c, dt, rows: lib.gtk_tri_mul_workspace_size_chunked(1, N, 128, c, dt, rows)
     Np = lambda N: (N + 63) // 64 * 64
-    chunked = lambda N, c, e, R: c * Np(N) ** 2 * e + 2 * c * R * Np(N) * e + 3 * 256
-    assert tc(2048, 128, GTK_BF16, 0) == tc(2048, 128, GTK_BF16, 2048) == 3 * (plane(1, 2048, 128, 2) + 256)
+    chunked = lambda N, c, e, R: c * (Np(N) ** 2 * e + 256) + 2 * c * (R * Np(N) * e + 256) + 3 * 256
+    assert tc(2048, 128, GTK_BF16, 0) == tc(2048, 128, GTK_BF16, 2048) == 3 * padded(1, 2048, 128, 2) + 3 * 256
     assert tc(2048, 128, GTK_BF16, 1) == tc(2048, 128, GTK_BF16, 256) == chunked(2048, 128, 2, 256)
     assert tc(2048, 128, GTK_BF16, 300) == chunked(2048, 128, 2, 512)
     assert tc(300, 64, GTK_BF16, 100) == chunked(300, 64, 2, 128)    # Np = 320: 64-row tiles
@@ -184,9 +187,10 @@ def test_bad_dtype_and_shapes_are_rejected(lib):
     rc = lib.gtk_tri_mul_forward_chunked(None, None, None, None, 1, 8, 128, 128, 1, 0, 1e-5, 1e-5,
                                          GTK_BF16, -3, None, 0, None)
     assert rc == GTK_EINVAL and "chunk_rows" in _err(lib)
-    # 1.25 GiB (+ alignment) at 256 rows, 3 GiB unchunked: both checked before any launch
+    # 1.25 GiB (+ alignment, + 256 bytes per channel plane of the b, a and x
+    # sets) at 256 rows, 3 GiB unchunked: both checked before any launch
     need = lib.gtk_tri_mul_workspace_size_chunked(1, 2048, 128, 128, GTK_BF16, 256)
-    assert need == (5 << 28) + 768
+    assert need == (5 << 28) + 768 + 3 * 128 * 256
     rc = lib.gtk_tri_mul_forward_chunked(dummy, None, dummy, dummy, 1, 2048, 128, 128, 1, 0, 1e-5,
                                          1e-5, GTK_BF16, 256, dummy, need - 1, None)
     assert rc == GTK_EWORKSPACE and "workspace" in _err(lib)
