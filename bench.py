@@ -188,6 +188,105 @@ def ln_cold_ms(torch, C, n: int, ln_w, ln_b, reps: int, dev) -> float:
     return statistics.median(out)
 
 
+def calibration_copy(torch, dev, mib: int) -> None:
+    """Three copies of a mib-MiB fp32 tensor (HIP's own copy kernel, mib MiB
+    read and mib MiB written): the known traffic that scales the HBM byte
+    counters."""
+    src = torch.ones((mib << 20) // 4, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    del src, dst
+
+
+LN_ROTATIONS = {1024: 3, 512: 12}  # inputs in rotation per N (>= 768 MiB each)
+
+
+def ln_counter_run(torch, C, dev, calibrate_mib: int) -> int:
+    """LayerNorm launches only, for HBM byte counters (rocprofv3 --pmc
+    FETCH_SIZE, then WRITE_SIZE) and a kernel trace of the same launches.
+    For each N in LN_ROTATIONS: K bf16 inputs [1, N, N, 128] (K x N^2 x 256 B
+    >= 768 MiB, three times the 256 MiB MALL), launched in rotation for two
+    passes, each launch writing its own output; so the input a launch reads
+    was last touched K - 1 launches earlier and cannot be cached.  Then the
+    calibration copy.  Prints per-launch kernel times (HIP events around each
+    launch, second pass) as one JSON line."""
+    w, b = torch.ones(C_Z, device=dev), torch.zeros(C_Z, device=dev)
+    times = {}
+    with torch.no_grad():
+        for n, k in LN_ROTATIONS.items():
+            print(f"[bench] LayerNorm counter run: N={n}, {k} inputs x 2 passes", file=sys.stderr,
+                  flush=True)
+            xs = [torch.randn(1, n, n, C_Z, device=dev).to(torch.bfloat16) for _ in range(k)]
+            ys = [C.layernorm(x, w, b, 1e-5) for x in xs]
+            torch.cuda.synchronize()
+            C.timing_enable(True)
+            ys = [C.layernorm(x, w, b, 1e-5) for x in xs]
+            rep = C.timing_report()
+            C.timing_enable(False)
+            torch.cuda.synchronize()
+            cnt, total, mn, mx = rep["layernorm"]
+            avg = total / cnt
+            times[f"n{n}"] = {"launches": cnt, "avg_ms": round(avg, 4), "min_ms": round(mn, 4),
+                              "gbps": round(ln_bytes(n) / (avg * 1e-3) / 1e9, 1),
+                              "frac_hbm": round(ln_bytes(n) / (avg * 1e-3) / PEAK_HBM_BYTES, 4)}
+            del xs, ys
+            torch.cuda.empty_cache()
+        if calibrate_mib > 0:
+            calibration_copy(torch, dev, calibrate_mib)
+    torch.cuda.synchronize()
+    print(json.dumps({"layernorm_rotation": times}))
+    return 0
+
+
+def summarize_ln(fetch_csv: str, write_csv: str, trace_csv: str, copy_mib: int) -> int:
+    """Markdown table of HBM bytes and rate per LayerNorm launch from
+    `bench.py --only-ln` run three times: under rocprofv3 --pmc FETCH_SIZE,
+    --pmc WRITE_SIZE (both with --calibrate-copy copy_mib) and --kernel-trace.
+    Launches are grouped by N (grid = 8 N^2 threads); each group's second
+    rotation pass is summarised (median bytes, calibrated by the copy kernel;
+    mean duration from the kernel trace)."""
+    import csv
+
+    fetch = _pmc_per_dispatch(fetch_csv, "FETCH_SIZE")
+    write = _pmc_per_dispatch(write_csv, "WRITE_SIZE")
+    copy_bytes = copy_mib * 2.0 ** 20
+    f_fac = copy_bytes / (max(v for (n, g, v) in fetch.values() if "copyBuffer" in n) * 1024.0)
+    w_fac = copy_bytes / (max(v for (n, g, v) in write.values() if "copyBuffer" in n) * 1024.0)
+
+    def second_pass(d, grid):
+        ids = sorted((int(i) for i, (n, g, _) in d.items() if "ln_rows_kernel" in n and g == grid))
+        return ids[len(ids) // 2:]
+
+    durs = {}
+    for r in csv.DictReader(open(trace_csv)):
+        if "ln_rows_kernel" not in r["Kernel_Name"]:
+            continue
+        grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+        durs.setdefault(grid, []).append(
+            (int(r["Dispatch_Id"]), (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-9))
+    mib = 2.0 ** 20
+    print("| N | launches | read MiB | written MiB | HBM MiB | algorithmic MiB | HBM / algorithmic | "
+          "avg us (kernel trace) | GB/s (algorithmic bytes) | GB/s (counter bytes) | % of 8 TB/s |")
+    print("|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|")
+    for n in sorted(LN_ROTATIONS):
+        grid = 8 * n * n
+        fi, wi = second_pass(fetch, grid), second_pass(write, grid)
+        if not fi or not wi or grid not in durs:
+            continue
+        fb = statistics.median(fetch[str(i)][2] * 1024.0 * f_fac for i in fi)
+        wb = statistics.median(write[str(i)][2] * 1024.0 * w_fac for i in wi)
+        d = sorted(durs[grid])
+        t = statistics.mean(x for _, x in d[len(d) // 2:])
+        alg = ln_bytes(n)
+        print(f"| {n} | {len(fi)} | {fb / mib:.1f} | {wb / mib:.1f} | {(fb + wb) / mib:.1f} | "
+              f"{alg / mib:.1f} | {(fb + wb) / alg:.3f} | {t * 1e6:.1f} | {alg / t / 1e9:.0f} | "
+              f"{(fb + wb) / t / 1e9:.0f} | {100 * (fb + wb) / t / PEAK_HBM_BYTES:.1f} |")
+    print(f"\ncalibration ({copy_mib} MiB copy): fetch bytes = FETCH_SIZE x {f_fac:.4f} KiB, "
+          f"write bytes = WRITE_SIZE x {w_fac:.4f} KiB")
+    return 0
+
+
 def host_cpu() -> dict:
     """CPU model and physical core count of this host (from /proc/cpuinfo)."""
     model, cores = None, set()
@@ -364,17 +463,18 @@ def summarize_traffic(fetch_csv: str, write_csv: str, N: int, copy_mib: int) -> 
     f_fac = copy_bytes / (calib(fetch) * 1024.0)
     w_fac = copy_bytes / (calib(write) * 1024.0)
     alg = algorithmic_bytes(N)
-    ln_grid = None
+    # meant for a run of `--only-step`, where every launch is at this N; a
+    # full bench run also launches every kernel at N = 256 and 2N, and of
+    # those only LayerNorm's are told apart here (grid 8 N^2 threads)
+    ln_grid = 8 * N * N
     by = {}
     for src, fac, kind in ((fetch, f_fac, "fetch"), (write, w_fac, "write")):
         for name, grid, val in src.values():
             key = _kernel_key(name)
             if key is None:
                 continue
-            if key == "layernorm":  # the N-sized launches only (bench also runs 2N)
-                ln_grid = min(ln_grid or grid, grid)
-                if grid != ln_grid:
-                    continue
+            if key == "layernorm" and grid != ln_grid:
+                continue
             by.setdefault(key, {}).setdefault(kind, []).append((grid, val * 1024.0 * fac))
     out = {"_calibration": {"copy_bytes": int(copy_bytes), "fetch_factor": round(f_fac, 4),
                             "write_factor": round(w_fac, 4)}}
@@ -664,6 +764,13 @@ def main() -> int:
                          "kernel-trace stats of `bench.py --only-step`")
     ap.add_argument("--only-step", action="store_true",
                     help="time the step and its kernels only (for counter collection)")
+    ap.add_argument("--only-ln", action="store_true",
+                    help="no bench line: LayerNorm launches over rotating inputs at N=1024 and "
+                         "N=512 (for HBM byte counters and a kernel trace), then --calibrate-copy")
+    ap.add_argument("--summarize-ln", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "TRACE_CSV"),
+                    help="no run: LayerNorm HBM bytes and rate per launch from FETCH_SIZE / "
+                         "WRITE_SIZE passes and a kernel trace of `bench.py --only-ln` (its MiB "
+                         "in --calibrate-copy)")
     ap.add_argument("--config-table", action="store_true",
                     help="no bench line: GPU and host-CPU times of the operators at the "
                          "benchmark configurations 1-5, as a markdown table")
@@ -674,6 +781,8 @@ def main() -> int:
         return summarize_stats(args.summarize_stats)
     if args.summarize_pmc:
         return summarize_pmc(*args.summarize_pmc, N=args.n)
+    if args.summarize_ln:
+        return summarize_ln(*args.summarize_ln, copy_mib=args.calibrate_copy)
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
               "(the path has no multi-GPU implementation)", file=sys.stderr)
@@ -688,6 +797,8 @@ def main() -> int:
     torch.cuda.set_device(0)
     if args.config_table:
         return config_table(torch, C, dev)
+    if args.only_ln:
+        return ln_counter_run(torch, C, dev, args.calibrate_copy)
     N = args.n
     torch.manual_seed(0)
     z = torch.randn(1, N, N, C_Z, device=dev).to(torch.bfloat16)
@@ -732,6 +843,8 @@ def main() -> int:
         rep = C.timing_report()
         C.timing_enable(False)
         if args.only_step:
+            if args.calibrate_copy > 0:
+                calibration_copy(torch, dev, args.calibrate_copy)
             torch.cuda.synchronize()
             print(json.dumps({"ms_per_step": round(step_ms, 4),
                               "op_ms": {k: round(v, 4) for k, v in op_ms.items()},
@@ -787,11 +900,7 @@ def main() -> int:
         del z2, flush_buf
         ln2_ms_cold = ln_cold_ms(torch, C, 2 * N, ln_w, ln_b, reps, dev)
         if args.calibrate_copy > 0:
-            src = torch.ones((args.calibrate_copy << 20) // 4, device=dev)
-            dst = torch.empty_like(src)
-            for _ in range(3):
-                dst.copy_(src)
-            del src, dst
+            calibration_copy(torch, dev, args.calibrate_copy)
     torch.cuda.synchronize()
 
     # one training step of tri-mul outgoing (forward + backward, gradients of z

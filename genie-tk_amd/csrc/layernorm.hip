@@ -4,10 +4,13 @@
 // lanes (8 contiguous channels = 16 B of bf16 per lane), so one wave covers
 // 64*8/D rows per step with fully coalesced 16 B loads and stores; U steps
 // are issued before any arithmetic so each wave keeps U loads in flight.
-// Blocks of 8 waves, ordinary (cached) stores: measured on MI355X at N = 512
-// / 1024 (bf16, c = 128) after a MALL-evicting read, 24.3 / 78.8 us against
-// 26.5 / 89.5 us with 4-wave blocks and non-temporal stores, where a plain
-// copy of the same bytes takes 24.1-24.4 / 77.6 us.
+// Blocks of 8 waves.  Loads carry the non-temporal hint and stores the
+// device-scope policy (written through the L2): measured on MI355X at
+// N = 512 / 1024 (bf16, c = 128, inputs in a rotation larger than the MALL,
+// launches replayed back to back, variants interleaved), 22.3 / 78.9 us
+// against 25.1 / 88.8 us with plain loads and stores, where a plain copy of
+// the same bytes took 24.1-24.9 / 87-91 us.  Non-temporal stores, 4- or
+// 16-wave blocks and U = 1 or 4 were slower.
 // Statistics use an xor-butterfly inside the row's lane group.
 //
 // gtk_fused_layernorm_linear: the row is normalised in MFMA fragment layout
@@ -26,8 +29,9 @@ __global__ __launch_bounds__(512) void ln_rows_kernel(const T* __restrict__ x, T
                                                       const float* __restrict__ gamma,
                                                       const float* __restrict__ beta, int64_t rows,
                                                       float eps) {
-  constexpr int LPR = D / 8;     // lanes per row
-  constexpr int RPW = 64 / LPR;  // rows per wave per step
+  constexpr int LPR = D / 8;              // lanes per row
+  constexpr int RPW = 64 / LPR;           // rows per wave per step
+  constexpr int VEC = 8 * sizeof(T) / 16; // 16-byte pieces per lane and row
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
   const int sub = lane / LPR;
@@ -38,21 +42,30 @@ __global__ __launch_bounds__(512) void ln_rows_kernel(const T* __restrict__ x, T
     g[e] = gamma[c0 + e];
     bt[e] = beta[c0 + e];
   }
-  const int64_t row0 = ((int64_t)blockIdx.x * 8 + wave) * (RPW * U) + sub;
-  float v[U][8];
+  const int64_t wrow0 = ((int64_t)blockIdx.x * 8 + wave) * (RPW * U);  // the wave's first row
+  const int64_t row0 = wrow0 + sub;
+  // every load is issued before any is used: rows past the last one read
+  // the last row (rows >= 1) and are not stored
+  uint4 raw_in[U][VEC];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int64_t r = row0 + (int64_t)u * RPW;
-    if (r < rows) {
-      Frag<T> f;
-      f.load(x + r * D + c0);
+    const int64_t rc = r < rows ? r : rows - 1;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[u][e] = f.get(e);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[u][e] = 0.f;
-    }
+    for (int h = 0; h < VEC; ++h) raw_in[u][h] = load16_nt(x + rc * D + c0 + h * (8 / VEC));
   }
+  float v[U][8];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    Frag<T> f;
+    __builtin_memcpy(&f, raw_in[u], sizeof(raw_in[u]));
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[u][e] = f.get(e);
+  }
+  // the wave's rows as one buffer range (an empty range for a wave past the
+  // last row; rows past the last one take an offset outside the range)
+  const int64_t wrows = rows <= wrow0 ? 0 : (rows - wrow0 < RPW * U ? rows - wrow0 : RPW * U);
+  const __amdgpu_buffer_rsrc_t out = buf_rsrc(y + wrow0 * D, (uint32_t)(wrows * D * sizeof(T)));
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     float s = 0.f;
@@ -71,19 +84,16 @@ __global__ __launch_bounds__(512) void ln_rows_kernel(const T* __restrict__ x, T
     for (int off = LPR / 2; off > 0; off >>= 1) q += __shfl_xor(q, off, 64);
     const float rstd = 1.0f / sqrtf(q * (1.0f / D) + eps);
     const int64_t r = row0 + (int64_t)u * RPW;
-    if (r < rows) {
-      float o[8];
+    float o[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = (v[u][e] - mean) * rstd * g[e] + bt[e];
-      Frag<T> f;
-      f.set(o);
-      if constexpr (sizeof(T) == 2) {
-        *reinterpret_cast<bf16x8*>(y + r * D + c0) = f.v;
-      } else {
-        *reinterpret_cast<f32x4*>(y + r * D + c0) = f.lo;
-        *reinterpret_cast<f32x4*>(y + r * D + c0 + 4) = f.hi;
-      }
-    }
+    for (int e = 0; e < 8; ++e) o[e] = (v[u][e] - mean) * rstd * g[e] + bt[e];
+    Frag<T> f;
+    f.set(o);
+    uint4 raw[VEC];
+    __builtin_memcpy(raw, &f, sizeof(raw));
+    const uint32_t off = r < rows ? (uint32_t)(((r - wrow0) * D + c0) * sizeof(T)) : kBufSkip;
+#pragma unroll
+    for (int h = 0; h < VEC; ++h) buf_store16_sc1(out, off + 16u * h, raw[h]);
   }
 }
 
