@@ -27,6 +27,12 @@ def needs_autograd(x: Tensor, module: nn.Module) -> bool:
     return x.requires_grad or any(p.requires_grad for p in module.parameters())
 
 
+def binary_mask(mask: Optional[Tensor]) -> bool:
+    """True when every mask value is 0 or 1 (or there is no mask).  One
+    reduction and a host synchronisation: used only on the training path."""
+    return mask is None or bool(((mask == 0) | (mask == 1)).all())
+
+
 def warn_once(key: str, msg: str) -> None:
     if key not in _warned:
         _warned.add(key)

@@ -18,8 +18,9 @@ Mask semantics of the kernel path: the reference's additive bias
 in fp32.  A key with mask 1 takes no bias; a row whose keys are all masked
 follows the fp32 arithmetic of the reference, which with the default
 ``inf=1e9`` makes it uniform (every logit rounds to -1e9 while |logit| < 32).
-The backward kernels implement the default ``inf=1e9``; a module with another
-``inf`` trains through autograd of its PyTorch path.
+The backward kernels implement the default ``inf=1e9`` with a binary mask; a
+module with another ``inf``, or a call with mask values other than 0 and 1,
+trains through autograd of its PyTorch path.
 """
 from __future__ import annotations
 
@@ -182,8 +183,10 @@ class TriangleAttention(nn.Module):
             elif self.use_fused_kernel and self._kernel_supported(x):
                 if not _dispatch.needs_autograd(x, self):
                     return self._forward_cuda(x, mask, chunk_size=chunk_size)
-                # the backward kernels: the headline shape and inf = 1e9
-                if self.inf == 1e9 and self._headline_shape():
+                # the backward kernels: the headline shape, inf = 1e9 and a
+                # binary mask (they model no other mask bias than 0 or -inf)
+                if (self.inf == 1e9 and self._headline_shape()
+                        and _dispatch.binary_mask(mask)):
                     return _TriAttnFunction.apply(self, x, mask, chunk_size, *self._param_list())
         return self._forward_pytorch(x, mask, chunk_size)
 

@@ -303,10 +303,14 @@ int gtk_tri_attn_forward_chunked(const void* x, const float* mask, void* out, co
  * treatment of rows whose keys are all masked (their uniform softmax still
  * passes its gradient to q, k and the triangle bias).  Activations are
  * recomputed from x and the raw weights in w.  Gradients are written, not
- * accumulated.  The mask bias is the reference default's, inf = 1e9: a key
- * with mask == 1 is valid, any other value masks it (for a row with a valid
- * key this is the reference's result up to weights below e^-60), and a row
- * with no valid key is uniform.  c_in == 128, H == 4, d == 32, N <= 4096. */
+ * accumulated.  The mask bias is the reference default's, inf = 1e9, and
+ * the mask must be binary: a key with mask == 1 is valid, a key with
+ * mask == 0 is masked, and a row with no valid key is uniform.  Other mask
+ * values (fractional, or above 1) are not differentiated correctly: the
+ * forward gives them the bias inf * (mask - 1), which this backward does
+ * not model, so callers must send such masks elsewhere (the genie_tk
+ * modules use autograd of their PyTorch path for them).  c_in == 128,
+ * H == 4, d == 32, N <= 4096. */
 typedef struct gtk_tri_attn_grads {
   float *ln_w, *ln_b, *tri_w, *q_w, *k_w, *v_w, *g_w, *g_b, *o_w, *o_b;
 } gtk_tri_attn_grads;

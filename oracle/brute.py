@@ -38,15 +38,17 @@ def _sig(t: float) -> float:
 
 def _score(sqk: float, tri: float, m: float, inf: float) -> float:
     """The reference's score (qk*scale + inf*(m - 1)) + tri (primitives.py:156-158,
-    triangle_attention.py:118).  For m != 1 and |inf| >= 2^29 the fp32
-    reference's sum rounds to its mask term (|qk|, |tri| below half an ulp of
-    it), so that fp32 value is the score; a row whose keys are all masked with
-    mask 0 is then uniform."""
+    triangle_attention.py:118).  For m != 1 and |inf| >= 2^29 the score takes
+    the fp32 reference's roundings of both sums, fl32(fl32(qk + fl32(mb)) +
+    tri); with |qk| below half an ulp of mb the first is mb itself, and a row
+    whose keys are all masked with mask 0 is uniform while its bias values
+    round to one value."""
     if m == 1.0:
         return sqk + tri
     mb = inf * (m - 1.0)
     if abs(inf) >= 2.0 ** 29:
-        return float(np.float32(mb))
+        f32 = lambda t: float(np.float32(t))  # noqa: E731
+        return f32(f32(sqk + f32(mb)) + tri)
     return (sqk + mb) + tri
 
 
@@ -92,9 +94,9 @@ def tri_attn(x: np.ndarray, mask: Optional[np.ndarray], P: Dict[str, np.ndarray]
              starting: bool, no_heads: int, inf: float = 1e9, eps: float = 1e-5) -> np.ndarray:
     """Attention over positions of each row; ending node indexes columns directly.
 
-    Scores follow _score: a masked key's score is the fp32 value of
-    inf * (mask - 1) when that term absorbs the rest (|inf| >= 2^29), so a row
-    whose keys are all masked with mask 0 gets uniform weights.
+    Scores follow _score: a masked key's score takes the fp32 reference's
+    roundings when |inf| >= 2^29, so a row whose keys are all masked with
+    mask 0 gets uniform weights while its bias values round to one value.
     """
     B, N, _, cin = x.shape
     ch = P["mha.linear_q.weight"].shape[0]

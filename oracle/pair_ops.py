@@ -13,8 +13,8 @@ import numpy as np
 
 Params = Dict[str, np.ndarray]
 
-# |inf| from which the fp32 mask term inf * (mask - 1) of a masked key absorbs
-# the logit it is added to (ulp(2^29) = 64 in fp32).
+# |inf| from which the fp32 rounding of a masked key's score is modelled in
+# float64 (ulp(2^29) = 64 in fp32: the mask term absorbs |logits| below 32).
 _ABSORB_INF = 2.0 ** 29
 
 
@@ -109,11 +109,15 @@ def _masked_scores(qk: np.ndarray, keymask: np.ndarray, tri: np.ndarray, inf: fl
     mask bias triangle_attention.py:118).
 
     In float32 this is the literal reference arithmetic.  In float64, for
-    |inf| >= 2^29, the fp32 absorption is made explicit: the score of a key
-    with mask != 1 is the fp32 value of inf*(m-1), which the fp32 reference
-    produces while |qk| and |tri| stay below half an ulp of it (asserted), so
-    that a row whose keys are all masked with mask 0 stays uniform as in the
-    fp32 reference.  For smaller |inf| the float64 sum is used as it stands.
+    |inf| >= 2^29, a masked key's score takes the reference's two fp32
+    roundings, fl32(fl32(qk + fl32(inf*(m-1))) + tri), on the float64 values
+    of qk and tri (each float64 sum is exact or within 2^-29 of exact, far
+    inside the fp32 rounding step).  With inf = 1e9 and |qk| < 32 the scores
+    are -1e9 plus multiples of 64: a row whose keys are all masked with mask 0
+    is uniform when its bias values round to one multiple (|tri| < 32, or a
+    per-head constant with small variation), and otherwise puts its weight on
+    the keys whose fl32(-1e9 + tri) is largest, as the fp32 reference does.
+    For smaller |inf| the float64 sum is used as it stands.
     """
     mb = (inf * (keymask - 1)).astype(dtype)
     if dtype == np.float32:
@@ -122,10 +126,9 @@ def _masked_scores(qk: np.ndarray, keymask: np.ndarray, tri: np.ndarray, inf: fl
     masked = np.broadcast_to(keymask != 1, s.shape)
     if abs(inf) >= _ABSORB_INF and masked.any():
         mb32 = np.broadcast_to((inf * (keymask - 1)).astype(np.float32).astype(dtype), s.shape)
-        half_ulp = np.spacing(np.abs(mb32[masked]).astype(np.float32)).astype(dtype) / 2
-        assert (np.abs(qk[masked]) < half_ulp).all() and (
-            np.abs(np.broadcast_to(tri, s.shape)[masked]) < half_ulp).all()
-        return np.where(masked, mb32, s)
+        f32 = lambda a: a.astype(np.float32).astype(dtype)  # noqa: E731
+        masked_s = f32(f32(qk + mb32) + np.broadcast_to(tri, s.shape))
+        return np.where(masked, masked_s, s)
     return (qk + mb) + tri
 
 

@@ -161,6 +161,58 @@ def test_tri_attn_fully_masked_row_is_uniform():
         np.testing.assert_allclose(got[0, 4], want, atol=1e-5 if dt == np.float32 else 1e-12)
 
 
+def _head_constant_params(const: float, seed: int):
+    """Small tri-attn parameters whose triangle bias carries the per-head
+    constant `const`: channels 8..15 are the constant const/8 after the
+    LayerNorm (weight 0, bias const/8) and feed only the bias (weight 1
+    there, no q/k/v/gate weight); channels 0..7 form an ordinary module."""
+    P = _ta_params(seed=seed)
+    hi = slice(8, 16)
+    P["layer_norm.weight"][hi] = 0.0
+    P["layer_norm.bias"][hi] = const / 8
+    P["linear.weight"][:, hi] = 1.0
+    for k in ("mha.linear_q.weight", "mha.linear_k.weight", "mha.linear_v.weight", "mha.linear_g.weight"):
+        P[k][:, hi] = 0.0
+    return P
+
+
+@pytest.mark.parametrize("const,uniform", [(200.0, True), (224.0, False)])
+def test_fully_masked_row_with_bias_constant(const, uniform):
+    """A row whose keys are all masked (inf = 1e9) under a triangle bias with
+    a per-head constant.  The fp32 reference's scores fl32(fl32(qk - 1e9) +
+    tri) are -1e9 plus multiples of 64.  A constant of 200 (bias values
+    200 +- 1) rounds every score of the row to -1e9 + 192: uniform, as with
+    no constant.  224 sits on a rounding boundary: keys with tri > 224 take
+    -1e9 + 256 and all the weight.  The float64 oracle and the scalar loops
+    model both roundings and match the literal fp32 arithmetic."""
+    P = _head_constant_params(const, seed=47)
+    N = 7
+    x = H.pair_input(1, N, 16, seed=48).astype(F64)
+    m = np.ones((1, N, N), np.float32)
+    m[0, 4, :] = 0
+    xn = pair_ops.layer_norm(x[0, 4], P["layer_norm.weight"].astype(F64), P["layer_norm.bias"].astype(F64))
+    tri = xn @ P["linear.weight"].T.astype(F64)  # [K, H] of row 4
+    assert np.abs(tri - const).max() < 8
+    if not uniform:  # the precondition of the split: bias values on both sides of 224
+        assert (tri > 224).any() and (tri < 224).any()
+    got = pair_ops.tri_attn(x, m, P, True, 2, dtype=F64)
+    np.testing.assert_allclose(brute.tri_attn(x, m, P, True, 2), got, rtol=0, atol=1e-11)
+    np.testing.assert_allclose(pair_ops.tri_attn(x, m, P, True, 2, dtype=np.float32), got,
+                               rtol=0, atol=2e-5)
+    v = xn @ P["mha.linear_v.weight"].T.astype(F64)
+    o = np.broadcast_to(v.mean(axis=0), (N, 8))
+    o = o * pair_ops.sigmoid(xn @ P["mha.linear_g.weight"].T.astype(F64) + P["mha.linear_g.bias"])
+    want = o @ P["mha.linear_o.weight"].T.astype(F64) + P["mha.linear_o.bias"]
+    if uniform:
+        np.testing.assert_allclose(got[0, 4], want, atol=1e-12)
+    else:
+        assert np.abs(got[0, 4] - want).max() > 1e-2
+    # rows with a valid key do not see the constant: softmax cancels it
+    np.testing.assert_allclose(np.delete(got[0], 4, axis=0),
+                               np.delete(pair_ops.tri_attn(x, m, _head_constant_params(0.0, 47), True, 2,
+                                                           dtype=F64)[0], 4, axis=0), atol=1e-9)
+
+
 @pytest.mark.parametrize("starting", [True, False])
 def test_attention_core_matches_sdpa(starting):
     rng = np.random.default_rng(19)
