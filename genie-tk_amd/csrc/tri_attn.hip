@@ -916,7 +916,15 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
   const bf16x2_t ones2 = {(bf16)1.0f, (bf16)1.0f};
   f32x16 o = zero16();
   float m_ref = -INFINITY, l_run = 0.f;
-  float m_use = 0.f;  // the value subtracted inside S: m_ref, or 0 while m_ref = -inf
+  float m_use = 0.f;  // the reference subtracted from the scores: m_ref, or 0 while m_ref = -inf
+  // The part of m_use subtracted inside S (negm = -m_in): m_use while
+  // |m_use| < kFar, else 0.  A reference set by masked keys only (about
+  // -inf log2 e) folded into the fp32 accumulation would round the logits of
+  // the valid keys that follow to multiples of its ulp; such a lane
+  // subtracts it on the VALU instead (a rare path: a row whose running
+  // maximum so far comes from masked keys).
+  constexpr float kFar = 4096.f;
+  float m_in = 0.f;
   for (int t = 0; t < ntiles; ++t) {
     const bool opens = t > 0 && (t & 1) == 0;  // tile t opens key block t/2
     if (opens) {
@@ -949,13 +957,13 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
           sc[4 * g + rr] = ((kp >> (8 * g + rr)) & 1u) ? -INFINITY : sc[4 * g + rr] + add;
         }
     }
-    // sc holds s - m_use; the reference max m_ref moves only when a score
+    // sc holds s - m_in; the reference max m_ref moves only when a score
     // exceeds it by more than kRescale
     float mt = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
 #pragma unroll
     for (int e = 3; e < 15; e += 2) mt = fmaxf(fmaxf(mt, sc[e]), sc[e + 1]);
     mt = fmaxf(mt, sc[15]);
-    mt = lane_pair_max(mt) + m_use;       // the tile max of s
+    mt = lane_pair_max(mt) + m_in;        // the tile max of s
     if (__ballot(mt > m_ref + kRescale) != 0ull) {
       const float m_new = fmaxf(m_ref, mt);
       const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
@@ -963,14 +971,19 @@ __global__ __launch_bounds__(64 * H * QT) __attribute__((amdgpu_waves_per_eu(4))
 #pragma unroll
       for (int e = 0; e < 16; ++e) o[e] *= alpha;
       m_ref = m_new;
-      const float m_next = (m_ref == -INFINITY) ? 0.f : m_ref;
-      const float shift = m_use - m_next;
+      m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
+      const float m_in_new = fabsf(m_use) < kFar ? m_use : 0.f;
+      const float shift = m_in - m_use;
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         sc[e] += shift;
-        negm[e] = -m_next;
+        negm[e] = -m_in_new;
       }
-      m_use = m_next;
+      m_in = m_in_new;
+    } else if (__ballot(m_in != m_use) != 0ull) {
+      // a lane whose reference stays beyond kFar: its scores are raw
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sc[e] += m_in - m_use;
     }
     // sub-block t&1 of this head's V^T, row t32
     const char* vt_base = ring[cur] + (H + h) * HEAD_BYTES + (t & 1) * 2048;
@@ -1404,13 +1417,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
         }
         s_tile(t, sc, qf);
         mask_tile(t, sc, kFrac);
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sc[e] -= m_use;
+        // the tile max of the raw scores; the reference is subtracted
+        // afterwards.  (Subtracted first, a reference set by a tile of
+        // masked keys only, about -inf log2 e, would round the logits of the
+        // valid keys that follow to multiples of its fp32 ulp.)
         float mt = fmaxf(fmaxf(sc[0], sc[1]), sc[2]);
 #pragma unroll
         for (int e = 3; e < 15; e += 2) mt = fmaxf(fmaxf(mt, sc[e]), sc[e + 1]);
-        mt = fmaxf(mt, sc[15]);
-        mt = lane_pair_max(mt) + m_use;  // the tile max of s
+        mt = lane_pair_max(fmaxf(mt, sc[15]));
         if (__ballot(mt > m_ref + kRescale) != 0ull) {
           const float m_new = fmaxf(m_ref, mt);
           const float alpha = (m_new == -INFINITY) ? 1.f : __builtin_amdgcn_exp2f(m_ref - m_new);
@@ -1418,11 +1432,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(4))) vo
 #pragma unroll
           for (int e = 0; e < 16; ++e) o[e] *= alpha;
           m_ref = m_new;
-          const float m_next = (m_ref == -INFINITY) ? 0.f : m_ref;
-#pragma unroll
-          for (int e = 0; e < 16; ++e) sc[e] += m_use - m_next;
-          m_use = m_next;
+          m_use = (m_ref == -INFINITY) ? 0.f : m_ref;
         }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) sc[e] -= m_use;
         pv_tile(t, sc, o, l_run);
       }
       l_tot = lane_pair_sum(l_run);
