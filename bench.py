@@ -53,11 +53,11 @@ def trimul_flops(N: int, B: int = 1) -> dict:
     }
 
 
-def triattn_flops(N: int, B: int = 1) -> dict:
-    ch = HEADS * HEAD_DIM
-    core = 4.0 * B * HEADS * HEAD_DIM * N ** 3  # Q K^T and P V
+def triattn_flops(N: int, B: int = 1, heads: int = HEADS, head_dim: int = HEAD_DIM) -> dict:
+    ch = heads * head_dim
+    core = 4.0 * B * heads * head_dim * N ** 3  # Q K^T and P V
     w_o = 2.0 * B * N * N * ch * C_Z           # output projection
-    out = {"triattn_prologue": 2.0 * B * N * N * C_Z * (4 * ch + HEADS)}
+    out = {"triattn_prologue": 2.0 * B * N * N * C_Z * (4 * ch + heads)}
     if -(-N // 128) * 128 <= 1024:
         # (row, head) flash kernel; the output projection runs in its own kernel
         out.update({"triattn_flash": core, "triattn_out": w_o})
@@ -107,13 +107,14 @@ def build_modules(torch, N: int, dev: str):
     return mods
 
 
-def build_pair_layer(torch, dev: str):
-    """One PairTransformLayer (c_p = c = c_h = 128, 4 heads), random weights, eval mode."""
+def build_pair_layer(torch, dev: str, c_att: int = HEADS * HEAD_DIM):
+    """One PairTransformLayer (c_p = c = 128, attention c_hidden c_att over 4
+    heads), random weights, eval mode."""
     import numpy as np
 
     from genie_tk import PairTransformLayer
 
-    layer = PairTransformLayer(c_p=C_Z, c_hidden_mul=C_HID, c_hidden_tri_att=HEADS * HEAD_DIM,
+    layer = PairTransformLayer(c_p=C_Z, c_hidden_mul=C_HID, c_hidden_tri_att=c_att,
                                n_head_tri=HEADS, tri_dropout=0.25)
     g = torch.Generator().manual_seed(7)
     sd = {}
@@ -606,6 +607,29 @@ def op_targets(N: int) -> dict:
             "layernorm": ln_bytes(N) / (0.7 * PEAK_HBM_BYTES) * 1e3}
 
 
+def call_split(torch, C, call, reps: int) -> dict:
+    """Where one operator call's time goes: device_ms, the sum of its kernels'
+    durations (HIP events around each launch on its stream), and host_us,
+    the host time to issue one call (Python, binding, allocations and
+    launches; calls issued back to back, the GPU synchronised only at the
+    end).  A call time (ms) near device_ms means the operator is bound by
+    the GPU, not by the host."""
+    C.timing_enable(True)
+    for _ in range(reps):
+        call()
+    rep = C.timing_report()
+    C.timing_enable(False)
+    dev_ms = sum(v[1] for v in rep.values()) / reps
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        call()
+    host_us = (time.perf_counter() - t0) / reps * 1e6
+    torch.cuda.synchronize()
+    return {"device_ms": round(dev_ms, 4), "host_us": round(host_us, 1),
+            "kernels_ms": {k: round(v[1] / reps, 4) for k, v in rep.items()}}
+
+
 def gpu_ops_at(torch, C, dev: str, N: int, tail: int, reps: int) -> dict:
     """Median event time of each operator (bf16, module kernel path) at size N,
     with the pair mask zero past `tail` (0: all ones); TFLOP/s or GB/s, and the
@@ -622,12 +646,15 @@ def gpu_ops_at(torch, C, dev: str, N: int, tail: int, reps: int) -> dict:
     out = {"N": N, "mask": f"pairs with i, j < {tail}" if tail else "ones"}
     with torch.no_grad():
         for k in ("tri_mul_out", "tri_mul_in", "tri_att_start", "tri_att_end"):
-            ms = statistics.median(event_time_ms(torch, lambda: mods[k](z, m), reps, inner=OP_INNER))
+            call = lambda: mods[k](z, m)  # noqa: E731
+            ms = statistics.median(event_time_ms(torch, call, reps, inner=OP_INNER))
             fl = sum((trimul_flops if k.startswith("tri_mul") else triattn_flops)(N).values())
             t = tg["tri_mul" if k.startswith("tri_mul") else "tri_att"]
             out[k] = {"ms": round(ms, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 1),
                       "frac_bf16_peak": round(fl / (ms * 1e-3) / PEAK_BF16_FLOPS, 4),
                       "target_ms": round(t, 4), "time_over_target": round(ms / t, 2)}
+            if N <= 256:
+                out[k].update(call_split(torch, C, call, reps))
         ms = statistics.median(event_time_ms(torch, lambda: C.layernorm(z, w, b, 1e-5), reps,
                                              inner=OP_INNER))
         out["layernorm"] = {"ms": round(ms, 4), "gbps": round(ln_bytes(N) / (ms * 1e-3) / 1e9, 1),
@@ -882,6 +909,15 @@ def main() -> int:
             torch, lambda: layer.pair_transition.forward_residual_masked(z, mask), reps))
         layer_ms = statistics.median(event_time_ms(torch, lambda: layer((z, mask)), reps))
         del layer
+        # the reference layer's default attention shape, c_hidden_tri_att = 32
+        # over 4 heads (head dim 8; pair_transform.py:116-117), which the
+        # packed weights pad to heads of 32 channels
+        layer8 = build_pair_layer(torch, dev, c_att=32)
+        att8 = layer8.tri_att_start
+        assert att8._kernel_supported(z)
+        att8_ms = statistics.median(event_time_ms(torch, lambda: att8(z, mask), reps, inner=OP_INNER))
+        layer8_ms = statistics.median(event_time_ms(torch, lambda: layer8((z, mask)), reps))
+        del layer8, att8
         # LayerNorm + Linear (nn.Linear-layout weight) over the pair tensor, c -> c
         lw = (torch.randn(C_Z, C_Z, device=dev) / C_Z ** 0.5).to(torch.bfloat16)
         lb = torch.randn(C_Z, device=dev)
@@ -1011,6 +1047,24 @@ def main() -> int:
         "ms": round(layer_ms, 4), "gflop": round(lf / 1e9, 2),
         "tflops": round(lf / (layer_ms * 1e-3) / 1e12, 2),
         "note": "one PairTransformLayer forward on the kernels, residuals fused (informational)",
+    }
+    fa8 = sum(triattn_flops(N, head_dim=8).values())
+    per_op["tri_att_start_d8"] = {
+        "ms": round(att8_ms, 4), "gflop": round(fa8 / 1e9, 2),
+        "tflops": round(fa8 / (att8_ms * 1e-3) / 1e12, 2),
+        "frac_bf16_peak": round(fa8 / (att8_ms * 1e-3) / PEAK_BF16_FLOPS, 4),
+        "gflop_as_run": round(sum(fa.values()) / 1e9, 2),
+        "ms_head_dim_32": round(op_ms["tri_att_start"], 4),
+        "note": "tri-attn starting node of the reference layer's default shape (4 heads of 8 "
+                "channels, c_hidden 32); gflop counts head dim 8, the kernels run the heads "
+                "padded to 32 (gflop_as_run)",
+    }
+    lf8 = 2 * sum(fm.values()) + 2 * fa8 + tf
+    per_op["pair_layer_default"] = {
+        "ms": round(layer8_ms, 4), "gflop": round(lf8 / 1e9, 2),
+        "tflops": round(lf8 / (layer8_ms * 1e-3) / 1e12, 2),
+        "note": "one PairTransformLayer forward with the reference's default c_hidden_tri_att "
+                "= 32 over 4 heads, on the kernels (gflop at head dim 8)",
     }
     fbf = 3 * sum(fm.values())
     per_op["tri_mul_out_fwd_bwd"] = {

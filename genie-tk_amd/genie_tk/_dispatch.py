@@ -39,30 +39,52 @@ def warn_once(key: str, msg: str) -> None:
         warnings.warn(msg, stacklevel=3)
 
 
+def params_at(module: nn.Module, paths: Tuple[Tuple[str, ...], ...]) -> List[Tensor]:
+    """The parameters of ``module`` at ``paths`` (("linear_a_p", "weight"),
+    ("mha", "linear_q", "weight"), ...), read through the submodules'
+    ``_modules`` and ``_parameters`` dicts: an attribute lookup through
+    nn.Module.__getattr__ costs about half a microsecond, and the kernel path
+    reads 6-16 parameters on every call.  A replaced submodule or parameter
+    is seen at once (nothing is cached here)."""
+    out = []
+    for path in paths:
+        mod = module
+        for name in path[:-1]:
+            mod = mod._modules[name]
+        out.append(mod._parameters[path[-1]])
+    return out
+
+
 class PackedWeights:
     """Device copy of a module's parameters in the kernels' fragment order.
 
-    Rebuilt when any parameter is replaced, modified in place (tensor version
-    counter), moved, or when the compute precision changes.
+    Rebuilt when any parameter is replaced or moved (its data pointer),
+    modified in place (its version counter), or when the compute precision
+    changes.
     """
 
     def __init__(self) -> None:
         self._key: Optional[Tuple] = None
         self._packed: Optional[Tensor] = None
 
-    def get(self, params: List[Optional[Tensor]], fp32: bool,
-            pack: Callable[[List[Optional[Tensor]], bool], Tensor]) -> Tensor:
-        key = (fp32,) + tuple(
-            (None if p is None else (p.data_ptr(), p._version, p.dtype, p.device)) for p in params)
+    def get(self, params: List[Tensor], fp32: bool,
+            pack: Callable[[List[Tensor], bool], Tensor]) -> Tensor:
+        p0 = params[0]
+        key = [fp32, p0.device, p0.dtype]
+        for p in params:
+            key.append(p.data_ptr())
+            key.append(p._version)
         if key != self._key or self._packed is None:
             with torch.no_grad():
-                self._packed = pack([None if p is None else p.detach() for p in params], fp32)
+                self._packed = pack([p.detach() for p in params], fp32)
             self._key = key
         return self._packed
 
 
 def flatten_batch(x: Tensor, mask: Optional[Tensor]) -> Tuple[Tensor, Optional[Tensor], Tuple]:
     """[*, N, N, C] -> [B, N, N, C] (and the mask likewise); returns the leading shape."""
+    if x.dim() == 4 and (mask is None or mask.shape == x.shape[:-1]):
+        return x, mask, (x.shape[0],)  # already [B, N, N, C] (the common call)
     lead = tuple(x.shape[:-3])
     n, c = x.shape[-2], x.shape[-1]
     xb = x.reshape(-1, n, n, c)

@@ -119,9 +119,11 @@ class PairTransition(nn.Module):
         """Inference on the kernels (no gradient needed)."""
         return self._kernel_supported(p) and not _dispatch.needs_autograd(p, self)
 
+    # the parameters in the order of pair_transition_pack
+    _PARAMS = tuple((m, w) for m in ("layer_norm", "linear_1", "linear_2") for w in ("weight", "bias"))
+
     def _param_list(self):
-        return [self.layer_norm.weight, self.layer_norm.bias, self.linear_1.weight,
-                self.linear_1.bias, self.linear_2.weight, self.linear_2.bias]
+        return _dispatch.params_at(self, self._PARAMS)
 
     def _run_kernel(self, p: Tensor, mask: Optional[Tensor], residual: bool) -> Tensor:
         C = _ext.require()

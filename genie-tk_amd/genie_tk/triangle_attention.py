@@ -137,11 +137,15 @@ class TriangleAttention(nn.Module):
     def _pack(self, params, fp32: bool) -> Tensor:
         return _ext.require().tri_attn_pack(params, self.c_in, self.c_hidden, self.no_heads, fp32)
 
+    # the parameters in the order of tri_attn_pack / gtk_tri_attn_weights
+    _PARAMS = (("layer_norm", "weight"), ("layer_norm", "bias"), ("linear", "weight"),
+               ("mha", "linear_q", "weight"), ("mha", "linear_k", "weight"),
+               ("mha", "linear_v", "weight"), ("mha", "linear_g", "weight"),
+               ("mha", "linear_g", "bias"), ("mha", "linear_o", "weight"),
+               ("mha", "linear_o", "bias"))
+
     def _param_list(self):
-        m = self.mha
-        return [self.layer_norm.weight, self.layer_norm.bias, self.linear.weight,
-                m.linear_q.weight, m.linear_k.weight, m.linear_v.weight,
-                m.linear_g.weight, m.linear_g.bias, m.linear_o.weight, m.linear_o.bias]
+        return _dispatch.params_at(self, self._PARAMS)
 
     def _packed_params(self, fp32: bool) -> Tensor:
         return self._packed.get(self._param_list(), fp32, self._pack)

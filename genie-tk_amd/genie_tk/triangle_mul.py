@@ -144,15 +144,13 @@ class TriangleMultiplicativeUpdate(nn.Module):
     def _pack(self, params, fp32: bool) -> Tensor:
         return _ext.require().tri_mul_pack(params, self.c_z, self.c_hidden, fp32)
 
+    # the parameters in the order of tri_mul_pack / gtk_tri_mul_weights
+    _PARAMS = tuple((m, w) for m in ("layer_norm_in", "linear_a_p", "linear_a_g", "linear_b_p",
+                                     "linear_b_g", "linear_g", "layer_norm_out", "linear_z")
+                    for w in ("weight", "bias"))
+
     def _param_list(self):
-        return [self.layer_norm_in.weight, self.layer_norm_in.bias,
-                self.linear_a_p.weight, self.linear_a_p.bias,
-                self.linear_a_g.weight, self.linear_a_g.bias,
-                self.linear_b_p.weight, self.linear_b_p.bias,
-                self.linear_b_g.weight, self.linear_b_g.bias,
-                self.linear_g.weight, self.linear_g.bias,
-                self.layer_norm_out.weight, self.layer_norm_out.bias,
-                self.linear_z.weight, self.linear_z.bias]
+        return _dispatch.params_at(self, self._PARAMS)
 
     def _packed_params(self, fp32: bool) -> Tensor:
         return self._packed.get(self._param_list(), fp32, self._pack)
