@@ -315,8 +315,18 @@ struct WgradPlan {
   int64_t kc;
 };
 
+// The product runs on the kernel's tiles: M rounded up to 128 and Nn to 64 or
+// a multiple of 128.  Output (m, n) reads only rows m of G and n of X, so the
+// extra rows may hold anything: the callers' G and X buffers have at least
+// wgrad_m_rows(M) and wgrad_n_rows(Nn) rows of `pitch`, and the outputs of
+// the extra rows are never read.
+inline int wgrad_m_rows(int M) { return (M + 127) / 128 * 128; }
+inline int wgrad_n_rows(int Nn) { return Nn <= 64 ? 64 : (Nn + 127) / 128 * 128; }
+// rows of a buffer used as G of one product and X of another
+inline int wgrad_rows(int rows) { return wgrad_m_rows(rows); }
+
 inline WgradPlan wgrad_plan(int M, int64_t pitch) {
-  const int mtiles = M / 128;
+  const int mtiles = wgrad_m_rows(M) / 128;
   int64_t ns = (512 + mtiles - 1) / mtiles;
   const int64_t maxs = pitch / 64 > 0 ? pitch / 64 : 1;
   if (ns > maxs) ns = maxs;
@@ -327,32 +337,35 @@ inline WgradPlan wgrad_plan(int M, int64_t pitch) {
 }
 
 inline size_t wgrad_part_floats(int M, int Nn, int64_t pitch) {
-  return (size_t)wgrad_plan(M, pitch).nsplit * M * Nn;
+  return (size_t)wgrad_plan(M, pitch).nsplit * wgrad_m_rows(M) * wgrad_n_rows(Nn);
 }
 
+// part[s][m][n] (m < wgrad_m_rows(M), n < wgrad_n_rows(Nn)): split s of
+// sum_k G[m][k] X[n][k]
 template <typename T>
 inline int launch_wgrad(const T* G, const T* X, float* part, int M, int Nn, int64_t pitch,
                         hipStream_t st) {
-  GTK_REQUIRE(M % 128 == 0 && (Nn % 128 == 0 || Nn == 64), GTK_EUNSUPPORTED,
-              "weight gradient shape %d x %d unsupported", M, Nn);
+  GTK_REQUIRE(M >= 1 && Nn >= 1, GTK_EUNSUPPORTED, "weight gradient shape %d x %d unsupported", M, Nn);
+  const int Mp = wgrad_m_rows(M), Np = wgrad_n_rows(Nn);
   const WgradPlan pl = wgrad_plan(M, pitch);
-  if (Nn % 128 == 0) {
-    const int64_t blocks = (int64_t)pl.nsplit * (M / 128) * (Nn / 128);
-    wgrad_kernel<T, 128><<<(unsigned)blocks, 256, 0, st>>>(G, X, part, M, Nn, pitch, pl.kc, pl.nsplit);
+  if (Np % 128 == 0) {
+    const int64_t blocks = (int64_t)pl.nsplit * (Mp / 128) * (Np / 128);
+    wgrad_kernel<T, 128><<<(unsigned)blocks, 256, 0, st>>>(G, X, part, Mp, Np, pitch, pl.kc, pl.nsplit);
   } else {
-    const int64_t blocks = (int64_t)pl.nsplit * (M / 128);
-    wgrad_kernel<T, 64><<<(unsigned)blocks, 256, 0, st>>>(G, X, part, M, Nn, pitch, pl.kc, pl.nsplit);
+    const int64_t blocks = (int64_t)pl.nsplit * (Mp / 128);
+    wgrad_kernel<T, 64><<<(unsigned)blocks, 256, 0, st>>>(G, X, part, Mp, Np, pitch, pl.kc, pl.nsplit);
   }
   GTK_LAUNCH_CHECK();
   return GTK_OK;
 }
 
 // dst[(m - m0)][n] = sum_s part[s][m][n] * (gamma ? gamma[n] : 1)
-//                    + (rowsum && beta ? rowsum[m] * beta[n] : 0),  m in [m0, m0 + rows)
+//                    + (rowsum && beta ? rowsum[m] * beta[n] : 0),  m in [m0, m0 + rows),
+// n < Nn, with part laid out as [nsplit][Mp][Np] (the padded product).
 // Block: 32 consecutive outputs x 8 chunks of the splits (chunk c takes s = c,
 // c + 8, ...), the 8 partial sums of each output added through LDS.
 static __global__ __launch_bounds__(256) void wgrad_finish_kernel(
-    const float* __restrict__ part, int nsplit, int M, int Nn, int m0, int rows,
+    const float* __restrict__ part, int nsplit, int Mp, int Np, int Nn, int m0, int rows,
     const float* __restrict__ rowsum, const float* __restrict__ gamma, const float* __restrict__ beta,
     float* __restrict__ dst) {
   __shared__ float red[8][32];
@@ -362,7 +375,7 @@ static __global__ __launch_bounds__(256) void wgrad_finish_kernel(
   const int m = m0 + (live ? idx / Nn : 0), n = live ? idx % Nn : 0;
   float acc = 0.f;
   if (live)
-    for (int sp = ch; sp < nsplit; sp += 8) acc += part[((int64_t)sp * M + m) * Nn + n];
+    for (int sp = ch; sp < nsplit; sp += 8) acc += part[((int64_t)sp * Mp + m) * Np + n];
   red[ch][o] = acc;
   __syncthreads();
   if (ch != 0 || !live) return;
@@ -378,8 +391,9 @@ inline int launch_wgrad_finish(const float* part, int M, int Nn, int64_t pitch, 
                                float* dst, hipStream_t st) {
   if (!dst) return GTK_OK;
   const int n = rows * Nn;
-  wgrad_finish_kernel<<<(n + 31) / 32, 256, 0, st>>>(part, wgrad_plan(M, pitch).nsplit, M, Nn, m0,
-                                                     rows, rowsum, gamma, beta, dst);
+  wgrad_finish_kernel<<<(n + 31) / 32, 256, 0, st>>>(part, wgrad_plan(M, pitch).nsplit, wgrad_m_rows(M),
+                                                     wgrad_n_rows(Nn), Nn, m0, rows, rowsum, gamma,
+                                                     beta, dst);
   GTK_LAUNCH_CHECK();
   return GTK_OK;
 }

@@ -305,9 +305,8 @@ __global__ __launch_bounds__(256) void attn_bwd_epi_kernel(const T* __restrict__
   Frag<T> fdy[C / 16];
 #pragma unroll
   for (int ch = 0; ch < C / 16; ++ch) fdy[ch].set(&dh.v[ch * 8]);
-  if constexpr (std::is_same<T, bf16>::value) {
-    static_assert(C == 128, "row-half tile store");
-    const CmTileRH cmr;
+  if constexpr (std::is_same<T, bf16>::value && C == 128) {
+    const CmTileRH cmr;  // whole transposed tiles of the lane's row half
     cmr.store(bf.cm_dy, pitch, p0, dh.v, fast, valid);
   } else if (valid) {
 #pragma unroll
@@ -1304,9 +1303,10 @@ __global__ __launch_bounds__(256) void attn_bwd_pro_kernel(const T* __restrict__
     }
 }
 
-// dW_b[h][c] = W3[c][h] gamma[c] + s[h] beta[c]  (W3 = sum_s part[s][c][h], 64 columns)
+// dW_b[h][c] = W3[c][h] gamma[c] + s[h] beta[c]  (W3 = sum_s part[s][c][h]: the
+// product's layout [nsplit][Cp][64], Cp = C rounded up to its row tile)
 __global__ __launch_bounds__(256) void attn_dwb_finish_kernel(const float* __restrict__ part, int nsplit, int C,
-                                                            int H, const float* __restrict__ gamma,
+                                                            int Cp, int H, const float* __restrict__ gamma,
                                                             const float* __restrict__ beta,
                                                             const float* __restrict__ sums, float* __restrict__ dst) {
   // 32 outputs x 8 chunks of the splits per block, partial sums added through LDS
@@ -1317,7 +1317,7 @@ __global__ __launch_bounds__(256) void attn_dwb_finish_kernel(const float* __res
   const int h = live ? idx / C : 0, c = live ? idx % C : 0;
   float a = 0.f;
   if (live)
-    for (int s = ch; s < nsplit; s += 8) a += part[((int64_t)s * C + c) * 64 + h];
+    for (int s = ch; s < nsplit; s += 8) a += part[((int64_t)s * Cp + c) * 64 + h];
   red[ch][o] = a;
   __syncthreads();
   if (ch != 0 || !live) return;
@@ -1374,11 +1374,12 @@ static AttnBwdWs<T> carve_attn_bwd(Carve& cv, int64_t B, int64_t N, int C, int H
   b.db = cv.take<float>(B * H * N * N);
   b.dbp = (sizeof(T) == 2 && np <= 512) ? cv.take<float>(B * kDbChunks * H * np * np) : nullptr;
   b.pitch = round_up(B * N * N, 64);
-  b.cm_stack = cv.take<T>(4 * CH * b.pitch);
-  b.cm_xh = cv.take<T>(C * b.pitch);
+  // operands of the weight-gradient products: rows padded to their tiles
+  b.cm_stack = cv.take<T>((int64_t)wgrad_rows(4 * CH) * b.pitch);
+  b.cm_xh = cv.take<T>((int64_t)wgrad_rows(C) * b.pitch);
   b.cm_dxn = cv.take<T>(C * b.pitch);
-  b.cm_dy = cv.take<T>(C * b.pitch);
-  b.cm_go = cv.take<T>(CH * b.pitch);
+  b.cm_dy = cv.take<T>((int64_t)wgrad_rows(C) * b.pitch);
+  b.cm_go = cv.take<T>((int64_t)wgrad_rows(CH) * b.pitch);
   b.cm_dtri = cv.take<T>(64 * b.pitch);
   a.part1 = cv.take<float>(wgrad_part_floats(4 * CH, C, b.pitch));
   a.part2 = cv.take<float>(wgrad_part_floats(C, CH, b.pitch));
@@ -1555,7 +1556,7 @@ static int bwd_triattn(const void* x, const float* mask, const void* dy,
     return rc;
   if ((rc = launch_copy_f32(gr->o_b, a.sums_dy, C, st))) return rc;
   attn_dwb_finish_kernel<<<(H * C + 31) / 32, 256, 0, st>>>(
-      a.part3, wgrad_plan(C, pitch).nsplit, C, H, a.w.ln_w, a.w.ln_b, a.sums_dtri, gr->tri_w);
+      a.part3, wgrad_plan(C, pitch).nsplit, C, wgrad_m_rows(C), H, a.w.ln_w, a.w.ln_b, a.sums_dtri, gr->tri_w);
   GTK_LAUNCH_CHECK();
   if ((rc = launch_copy_f32(gr->ln_w, a.dots_dxn, C, st))) return rc;
   if ((rc = launch_copy_f32(gr->ln_b, a.sums_dxn, C, st))) return rc;
@@ -1566,8 +1567,21 @@ static int bwd_triattn(const void* x, const float* mask, const void* dy,
 
 using namespace gtk;
 
+// Shapes of the backward kernels: c_in in {32, 64, 128}, four heads of 32
+// (modules with fewer or narrower heads pass their weights padded to this).
 static bool attn_bwd_shape_ok(int64_t c_in, int64_t c_h, int64_t H) {
-  return c_in == 128 && H == 4 && c_h == H * AD;
+  return (c_in == 32 || c_in == 64 || c_in == 128) && H == 4 && c_h == H * AD;
+}
+
+template <typename T>
+static int bwd_triattn_any(int64_t c_in, const void* x, const float* mask, const void* dy,
+                           const gtk_tri_attn_weights* w, void* dx, const gtk_tri_attn_grads* grads,
+                           int64_t B, int64_t N, int starting, float eps, void* ws, hipStream_t st) {
+  switch (c_in) {
+    case 32: return bwd_triattn<T, 32, 4>(x, mask, dy, w, dx, grads, B, N, starting, eps, ws, st);
+    case 64: return bwd_triattn<T, 64, 4>(x, mask, dy, w, dx, grads, B, N, starting, eps, ws, st);
+    default: return bwd_triattn<T, 128, 4>(x, mask, dy, w, dx, grads, B, N, starting, eps, ws, st);
+  }
 }
 
 extern "C" size_t gtk_tri_attn_backward_workspace_size(int64_t B, int64_t N, int64_t c_in,
@@ -1588,7 +1602,7 @@ extern "C" int gtk_tri_attn_backward(const void* x, const float* mask, const voi
   GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL,
               "gtk_tri_attn_backward: bad dtype %d", dtype);
   GTK_REQUIRE(attn_bwd_shape_ok(c_in, c_h, H), GTK_EUNSUPPORTED,
-              "gtk_tri_attn_backward: c_in=%lld c_h=%lld H=%lld unsupported (c_in=128, H=4, d=32)",
+              "gtk_tri_attn_backward: c_in=%lld c_h=%lld H=%lld unsupported (c_in in {32, 64, 128}, H=4, d=32)",
               (long long)c_in, (long long)c_h, (long long)H);
   GTK_REQUIRE(B >= 0 && N >= 0 && N <= 4096, GTK_EINVAL, "gtk_tri_attn_backward: bad shape");
   if (B == 0 || N == 0) return GTK_OK;
@@ -1604,7 +1618,6 @@ extern "C" int gtk_tri_attn_backward(const void* x, const float* mask, const voi
   GTK_REQUIRE(ws_bytes >= need, GTK_EWORKSPACE, "gtk_tri_attn_backward: workspace %zu < %zu bytes",
               ws_bytes, need);
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == GTK_F32)
-    return bwd_triattn<float, 128, 4>(x, mask, dy, w, dx, grads, B, N, starting, eps, ws, st);
-  return bwd_triattn<bf16, 128, 4>(x, mask, dy, w, dx, grads, B, N, starting, eps, ws, st);
+  if (dtype == GTK_F32) return bwd_triattn_any<float>(c_in, x, mask, dy, w, dx, grads, B, N, starting, eps, ws, st);
+  return bwd_triattn_any<bf16>(c_in, x, mask, dy, w, dx, grads, B, N, starting, eps, ws, st);
 }

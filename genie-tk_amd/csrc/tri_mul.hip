@@ -1371,12 +1371,17 @@ static int recompute_planes(const void* z, const float* mask, const void* packed
 int trimul_recompute_planes(const void* z, const float* mask, const void* packed, int64_t B,
                             int64_t N, int64_t c_z, int64_t c, int outgoing, float eps_in,
                             int dtype, void* pa, void* pb, void* px, hipStream_t st) {
-  GTK_REQUIRE(c_z == 128 && (c == 64 || c == 128), GTK_EUNSUPPORTED, "tri-mul shape unsupported");
-  if (dtype == GTK_F32)
-    return c == 128 ? recompute_planes<float, 128, 128>(z, mask, packed, B, N, outgoing, eps_in, pa, pb, px, st)
-                    : recompute_planes<float, 128, 64>(z, mask, packed, B, N, outgoing, eps_in, pa, pb, px, st);
-  return c == 128 ? recompute_planes<bf16, 128, 128>(z, mask, packed, B, N, outgoing, eps_in, pa, pb, px, st)
-                  : recompute_planes<bf16, 128, 64>(z, mask, packed, B, N, outgoing, eps_in, pa, pb, px, st);
+#define GTK_RP(CZ_, C_)                                                                          \
+  if (c_z == CZ_ && c == C_)                                                                    \
+    return dtype == GTK_F32                                                                     \
+               ? recompute_planes<float, CZ_, C_>(z, mask, packed, B, N, outgoing, eps_in, pa, pb, px, st) \
+               : recompute_planes<bf16, CZ_, C_>(z, mask, packed, B, N, outgoing, eps_in, pa, pb, px, st);
+  GTK_RP(128, 128) GTK_RP(128, 64) GTK_RP(128, 32)
+  GTK_RP(64, 128) GTK_RP(64, 64) GTK_RP(64, 32)
+  GTK_RP(32, 128) GTK_RP(32, 64) GTK_RP(32, 32)
+#undef GTK_RP
+  set_error("tri-mul plane recompute: c_z=%lld c=%lld unsupported", (long long)c_z, (long long)c);
+  return GTK_EUNSUPPORTED;
 }
 
 int trimul_contract_planes(const void* pl, const void* pr, void* out, int Np, int64_t nplanes,

@@ -70,7 +70,9 @@ __global__ __launch_bounds__(256) void trimul_bwd_epilogue_kernel(
     load_row_half<T, CZ>(rh, z + pair * CZ, valid);
     const f32x2 st = row_stats<CZ>(rh, eps_in);
     Frag<T> xf[CZ / 16];
-    ln_to_frags<T, CZ>(xf, rh, st);
+    // the forward's packed weights: LayerNorm affine folded in, or applied here
+    if constexpr (trimul_folded<CZ, CH>()) ln_to_frags<T, CZ>(xf, rh, st);
+    else ln_affine_to_frags<T, CZ>(xf, rh, st, w.ln_in_w, w.ln_in_b);
 #pragma unroll
     for (int nt = 0; nt < CZ / 32; ++nt) {
       sg[nt] = row_gemm_tile<T, CZ, true>(xf, w.w_g, nt);
@@ -114,7 +116,8 @@ __global__ __launch_bounds__(256) void trimul_bwd_epilogue_kernel(
   }
   const f32x2 so = row_stats<CH>(xh, eps_out);
   Frag<T> yf[CH / 16];
-  ln_to_frags<T, CH>(yf, xh, so);
+  if constexpr (trimul_folded<CZ, CH>()) ln_to_frags<T, CH>(yf, xh, so);
+  else ln_affine_to_frags<T, CH>(yf, xh, so, w.ln_out_w, w.ln_out_b);
 
   // dp = dy s, dg_pre = dy p s (1 - s)
   Frag<T> dpf[CZ / 16];
@@ -226,7 +229,8 @@ __global__ __launch_bounds__(256) void trimul_bwd_prologue_kernel(
   load_row_half<T, CZ>(rh, z + pair * CZ, valid);
   const f32x2 st = row_stats<CZ>(rh, eps_in);
   Frag<T> xf[CZ / 16];
-  ln_to_frags<T, CZ>(xf, rh, st);
+  if constexpr (trimul_folded<CZ, CH>()) ln_to_frags<T, CZ>(xf, rh, st);
+  else ln_affine_to_frags<T, CZ>(xf, rh, st, w.ln_in_w, w.ln_in_b);
   const float m = valid ? (mask ? mask[pair] : 1.0f) : 0.0f;
 
   f32x16 dzn[CZ / 32];
@@ -375,10 +379,11 @@ static TriMulBwdWs<T> carve_trimul_bwd(Carve& cv, int64_t B, int64_t N, int cz, 
   const int64_t pe = B * c * Np * Np;
   T** planes[] = {&w.pa, &w.pb, &w.px, &w.pdx, &w.pat, &w.pbt, &w.pda, &w.pdb};
   for (T** p : planes) *p = cv.take<T>(pe);
-  w.cm_stack = cv.take<T>(M1 * w.pitch);
-  w.cm_dp = cv.take<T>(cz * w.pitch);
-  w.cm_xi = cv.take<T>(cz * w.pitch);
-  w.cm_xo = cv.take<T>(c * w.pitch);
+  // operands of the weight-gradient products: rows padded to their tiles
+  w.cm_stack = cv.take<T>((int64_t)wgrad_rows(M1) * w.pitch);
+  w.cm_dp = cv.take<T>((int64_t)wgrad_rows(cz) * w.pitch);
+  w.cm_xi = cv.take<T>((int64_t)wgrad_rows(cz) * w.pitch);
+  w.cm_xo = cv.take<T>((int64_t)wgrad_rows(c) * w.pitch);
   w.cm_dzn = cv.take<T>(cz * w.pitch);
   w.cm_dxo = cv.take<T>(c * w.pitch);
   w.part1 = cv.take<float>(wgrad_part_floats(M1, cz, w.pitch));
@@ -488,9 +493,38 @@ static int bwd_trimul(const void* z, const float* mask, const void* dy,
 
 using namespace gtk;
 
+// Shapes of the backward kernels: c_z and c in {32, 64, 128}.
+static bool trimul_bwd_shape_ok(int64_t c_z, int64_t c) {
+  return (c_z == 32 || c_z == 64 || c_z == 128) && (c == 32 || c == 64 || c == 128);
+}
+
+template <typename T, int CZ>
+static int bwd_trimul_c(int64_t c, const void* z, const float* mask, const void* dy,
+                        const gtk_tri_mul_weights* w, void* dz, const gtk_tri_mul_grads* grads,
+                        int64_t B, int64_t N, int outgoing, float eps_in, float eps_out, int dtype,
+                        void* ws, hipStream_t st) {
+  switch (c) {
+    case 32: return bwd_trimul<T, CZ, 32>(z, mask, dy, w, dz, grads, B, N, outgoing, eps_in, eps_out, dtype, ws, st);
+    case 64: return bwd_trimul<T, CZ, 64>(z, mask, dy, w, dz, grads, B, N, outgoing, eps_in, eps_out, dtype, ws, st);
+    default: return bwd_trimul<T, CZ, 128>(z, mask, dy, w, dz, grads, B, N, outgoing, eps_in, eps_out, dtype, ws, st);
+  }
+}
+
+template <typename T>
+static int bwd_trimul_any(int64_t c_z, int64_t c, const void* z, const float* mask, const void* dy,
+                          const gtk_tri_mul_weights* w, void* dz, const gtk_tri_mul_grads* grads,
+                          int64_t B, int64_t N, int outgoing, float eps_in, float eps_out, int dtype,
+                          void* ws, hipStream_t st) {
+  switch (c_z) {
+    case 32: return bwd_trimul_c<T, 32>(c, z, mask, dy, w, dz, grads, B, N, outgoing, eps_in, eps_out, dtype, ws, st);
+    case 64: return bwd_trimul_c<T, 64>(c, z, mask, dy, w, dz, grads, B, N, outgoing, eps_in, eps_out, dtype, ws, st);
+    default: return bwd_trimul_c<T, 128>(c, z, mask, dy, w, dz, grads, B, N, outgoing, eps_in, eps_out, dtype, ws, st);
+  }
+}
+
 extern "C" size_t gtk_tri_mul_backward_workspace_size(int64_t B, int64_t N, int64_t c_z, int64_t c,
                                                       int dtype) {
-  if (!(c_z == 128 && (c == 64 || c == 128)) || B < 0 || N < 0) return 0;
+  if (!trimul_bwd_shape_ok(c_z, c) || B < 0 || N < 0) return 0;
   if (dtype != GTK_F32 && dtype != GTK_BF16) return 0;
   Carve cv(nullptr, SIZE_MAX);
   if (dtype == GTK_F32) carve_trimul_bwd<float>(cv, B, N, (int)c_z, (int)c, dtype);
@@ -505,8 +539,8 @@ extern "C" int gtk_tri_mul_backward(const void* z, const float* mask, const void
                                     float eps_out, int dtype, void* ws, size_t ws_bytes,
                                     void* stream) {
   GTK_REQUIRE(dtype == GTK_F32 || dtype == GTK_BF16, GTK_EINVAL, "gtk_tri_mul_backward: bad dtype %d", dtype);
-  GTK_REQUIRE(c_z == 128 && (c == 64 || c == 128), GTK_EUNSUPPORTED,
-              "gtk_tri_mul_backward: c_z=%lld c=%lld unsupported (c_z=128, c in {64,128})",
+  GTK_REQUIRE(trimul_bwd_shape_ok(c_z, c), GTK_EUNSUPPORTED,
+              "gtk_tri_mul_backward: c_z=%lld c=%lld unsupported (c_z and c in {32, 64, 128})",
               (long long)c_z, (long long)c);
   GTK_REQUIRE(B >= 0 && N >= 0 && N <= 4096, GTK_EINVAL, "gtk_tri_mul_backward: bad shape");
   if (B == 0 || N == 0) return GTK_OK;
@@ -525,8 +559,6 @@ extern "C" int gtk_tri_mul_backward(const void* z, const float* mask, const void
               ws_bytes, need);
   hipStream_t st = (hipStream_t)stream;
   if (dtype == GTK_F32)
-    return c == 128 ? bwd_trimul<float, 128, 128>(z, mask, dy, w, dz, grads, B, N, outgoing, eps_in, eps_out, dtype, ws, st)
-                    : bwd_trimul<float, 128, 64>(z, mask, dy, w, dz, grads, B, N, outgoing, eps_in, eps_out, dtype, ws, st);
-  return c == 128 ? bwd_trimul<bf16, 128, 128>(z, mask, dy, w, dz, grads, B, N, outgoing, eps_in, eps_out, dtype, ws, st)
-                  : bwd_trimul<bf16, 128, 64>(z, mask, dy, w, dz, grads, B, N, outgoing, eps_in, eps_out, dtype, ws, st);
+    return bwd_trimul_any<float>(c_z, c, z, mask, dy, w, dz, grads, B, N, outgoing, eps_in, eps_out, dtype, ws, st);
+  return bwd_trimul_any<bf16>(c_z, c, z, mask, dy, w, dz, grads, B, N, outgoing, eps_in, eps_out, dtype, ws, st);
 }

@@ -41,6 +41,40 @@ def _init_weights(linear: nn.Linear, init: str = "default", std: float = 0.02) -
             nn.init.zeros_(b)
 
 
+class _DenseMatmul(torch.autograd.Function):
+    """a @ b over equal leading (batch) dims, every operand made contiguous
+    first, in the forward and in the backward (dA = G B^T, dB = A^T G).
+
+    torch.matmul over batches on a transposed or permuted view makes a strided
+    batched product, and so does its autograd backward by itself; in bfloat16
+    that form has faulted gfx950 devices.  The products here are the same ones
+    on contiguous copies."""
+
+    @staticmethod
+    def forward(ctx, a: Tensor, b: Tensor) -> Tensor:
+        a, b = a.contiguous(), b.contiguous()
+        ctx.save_for_backward(a, b)
+        return torch.matmul(a, b)
+
+    @staticmethod
+    def backward(ctx, g: Tensor):
+        a, b = ctx.saved_tensors
+        g = g.contiguous()
+        ga = gb = None
+        if ctx.needs_input_grad[0]:
+            ga = torch.matmul(g, b.transpose(-1, -2).contiguous())
+        if ctx.needs_input_grad[1]:
+            gb = torch.matmul(a.transpose(-1, -2).contiguous(), g)
+        return ga, gb
+
+
+def dense_matmul(a: Tensor, b: Tensor) -> Tensor:
+    """``torch.matmul(a, b)`` for operands of equal leading dims, computed on
+    contiguous operands in the forward and the backward."""
+    assert a.shape[:-2] == b.shape[:-2], (a.shape, b.shape)
+    return _DenseMatmul.apply(a, b)
+
+
 class Linear(nn.Linear):
     """``nn.Linear`` whose parameters are initialised by ``_init_weights(init)``."""
 
@@ -86,10 +120,10 @@ class Attention(nn.Module):
         q = self._heads(self.linear_q(q_x))
         k = self._heads(self.linear_k(k_x))
         v = self._heads(self.linear_v(v_x))
-        scores = torch.matmul(q, k.transpose(-1, -2)) * (1.0 / math.sqrt(self.head_dim))
+        scores = dense_matmul(q, k.transpose(-1, -2)) * (1.0 / math.sqrt(self.head_dim))
         for extra in biases or ():
             scores = scores + extra
-        o = torch.matmul(self.softmax(scores), v)          # [*, H, Q, D]
+        o = dense_matmul(self.softmax(scores), v)           # [*, H, Q, D]
         o = o.transpose(-2, -3).flatten(-2)                 # [*, Q, H*D]
         if self.gating:
             o = o * self.sigmoid(self.linear_g(q_x))

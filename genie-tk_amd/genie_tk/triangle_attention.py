@@ -24,6 +24,7 @@ trains through autograd of its PyTorch path.
 """
 from __future__ import annotations
 
+import math
 from functools import partialmethod
 from typing import Optional
 
@@ -38,13 +39,49 @@ from genie_tk.utils import has_cuda_kernels, permute_final_dims
 _CUDA_AVAILABLE = has_cuda_kernels()
 
 
+# The backward kernels' head shape: four heads of HD_BWD channels.
+H_BWD, HD_BWD = 4, 32
+
+
+def _pad_heads(params, H: int, ch: int):
+    """The module's parameters for the backward kernels' four heads of 32:
+    head h's d = ch / H channels go to padded channels 32 h .. 32 h + d - 1,
+    every other row of W_q, W_k, W_v, W_g and b_g and column of W_o is zero,
+    and so are the triangle-bias rows of heads H .. 3.  W_q is scaled by
+    sqrt(32 / d), so that the kernels' score scale 1/sqrt(32) is the module's
+    1/sqrt(d).  The zero channels and heads add nothing to the output (their
+    v and their W_o columns are zero), so the padded module's gradients
+    restricted to the real parameters are the module's own.  Returns the
+    padded list and the channel index of the real ones."""
+    ln_w, ln_b, tri_w, q_w, k_w, v_w, g_w, g_b, o_w, o_b = params
+    d = ch // H
+    idx = (torch.arange(H, device=q_w.device)[:, None] * HD_BWD
+           + torch.arange(d, device=q_w.device)[None, :]).reshape(-1)
+    cp = H_BWD * HD_BWD
+    scale = math.sqrt(HD_BWD / d)
+
+    def rows(w, s=1.0):
+        out = w.new_zeros((cp,) + tuple(w.shape[1:]))
+        out[idx] = w * s if s != 1.0 else w
+        return out
+
+    o_p = o_w.new_zeros(o_w.shape[0], cp)
+    o_p[:, idx] = o_w
+    tri_p = tri_w.new_zeros(H_BWD, tri_w.shape[1])
+    tri_p[:H] = tri_w
+    return [ln_w, ln_b, tri_p, rows(q_w, scale), rows(k_w), rows(v_w), rows(g_w), rows(g_b), o_p,
+            o_b], idx, scale
+
+
 class _TriAttnFunction(torch.autograd.Function):
     """The update on the HIP kernels, forward and backward.
 
     The reference trains through torch autograd of its PyTorch path
     (triangle_attention.py:100-143, primitives.py:114-178); this computes the
     same gradients on the kernels.  Activations are recomputed in the backward
-    from x (only x, the mask and the parameters are saved)."""
+    from x (only x, the mask and the parameters are saved).  Modules with
+    fewer than four heads, or heads narrower than 32 channels, run the
+    backward on their weights padded to four heads of 32 (_pad_heads)."""
 
     @staticmethod
     def forward(ctx, module, x, mask, chunk_size, *params):
@@ -57,12 +94,25 @@ class _TriAttnFunction(torch.autograd.Function):
         x, mask, *params = ctx.saved_tensors
         mod = ctx.module
         xb, mb, lead = _dispatch.flatten_batch(x, mask)
+        padded = (mod.no_heads, mod.c_hidden) != (H_BWD, H_BWD * HD_BWD)
+        bparams = list(params)
+        if padded:
+            with torch.no_grad():
+                bparams, idx, scale = _pad_heads(params, mod.no_heads, mod.c_hidden)
         res = _ext.require().tri_attn_backward(
-            xb, mb, dy.reshape(xb.shape).to(x.dtype), list(params), mod.c_in, mod.c_hidden,
-            mod.no_heads, mod.starting, mod.layer_norm.eps)
+            xb, mb, dy.reshape(xb.shape).to(x.dtype), bparams, mod.c_in, H_BWD * HD_BWD,
+            H_BWD, mod.starting, mod.layer_norm.eps)
         dx = res[0].reshape(x.shape) if ctx.needs_input_grad[1] else None
-        grads = [g.to(p.dtype) if ctx.needs_input_grad[4 + k] else None
-                 for k, (g, p) in enumerate(zip(res[1:], params))]
+        g = list(res[1:])
+        if padded:
+            # back to the module's parameters (order of _PARAMS)
+            g[2] = g[2][:mod.no_heads]
+            g[3] = g[3][idx] * scale
+            for k in (4, 5, 6, 7):
+                g[k] = g[k][idx]
+            g[8] = g[8][:, idx]
+        grads = [gk.to(p.dtype) if ctx.needs_input_grad[4 + k] else None
+                 for k, (gk, p) in enumerate(zip(g, params))]
         return (None, dx, None, None, *grads)
 
 
@@ -92,8 +142,10 @@ class TriangleAttention(nn.Module):
 
     def _forward_pytorch(self, x: Tensor, mask: Optional[Tensor] = None,
                          chunk_size: Optional[int] = None) -> Tensor:
-        if mask is None:
-            mask = x.new_ones(x.shape[:-1])
+        # the mask in the input's dtype: the reference's own path (its mask
+        # bias added to the scores) accepts only that pairing, and gives this
+        # result for a mask passed in the input's dtype
+        mask = x.new_ones(x.shape[:-1]) if mask is None else mask.to(x.dtype)
         if not self.starting:
             x = x.transpose(-2, -3)
             mask = mask.transpose(-1, -2)
@@ -130,9 +182,11 @@ class TriangleAttention(nn.Module):
                 and 1 <= ch // h <= 32 and self.mha.gating
                 and x.dtype in _dispatch.SUPPORTED_DTYPES and self.layer_norm.elementwise_affine)
 
-    def _headline_shape(self) -> bool:
-        """The shape the backward kernels are built for."""
-        return self.c_in == 128 and self.no_heads == 4 and self.c_hidden == 128
+    def _backward_supported(self) -> bool:
+        """The backward kernels: c_in in {32, 64, 128}; every head shape of the
+        forward kernels (1, 2 or 4 heads of at most 32 channels) runs padded
+        to four heads of 32."""
+        return self.c_in in (32, 64, 128)
 
     def _pack(self, params, fp32: bool) -> Tensor:
         return _ext.require().tri_attn_pack(params, self.c_in, self.c_hidden, self.no_heads, fp32)
@@ -187,9 +241,9 @@ class TriangleAttention(nn.Module):
             elif self.use_fused_kernel and self._kernel_supported(x):
                 if not _dispatch.needs_autograd(x, self):
                     return self._forward_cuda(x, mask, chunk_size=chunk_size)
-                # the backward kernels: the headline shape, inf = 1e9 and a
-                # binary mask (they model no other mask bias than 0 or -inf)
-                if (self.inf == 1e9 and self._headline_shape()
+                # the backward kernels: their shapes, inf = 1e9 and a binary
+                # mask (they model no other mask bias than 0 or -inf)
+                if (self.inf == 1e9 and self._backward_supported()
                         and _dispatch.binary_mask(mask)):
                     return _TriAttnFunction.apply(self, x, mask, chunk_size, *self._param_list())
         return self._forward_pytorch(x, mask, chunk_size)

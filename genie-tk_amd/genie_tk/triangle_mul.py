@@ -30,7 +30,7 @@ import torch.nn as nn
 from torch import Tensor
 
 from genie_tk import _dispatch, _ext
-from genie_tk.primitives import Linear
+from genie_tk.primitives import Linear, dense_matmul
 from genie_tk.utils import has_cuda_kernels, permute_final_dims
 
 _CUDA_AVAILABLE = has_cuda_kernels()
@@ -95,18 +95,19 @@ class TriangleMultiplicativeUpdate(nn.Module):
     # -- reference fallback -------------------------------------------------
     def _outgoing_matmul(self, a: Tensor, b: Tensor) -> Tensor:
         """x[*, i, j, c] = sum_k a[*, i, k, c] b[*, j, k, c] as a batched [c] matmul."""
-        x = torch.matmul(permute_final_dims(a, 2, 0, 1), permute_final_dims(b, 2, 1, 0))
+        x = dense_matmul(permute_final_dims(a, 2, 0, 1), permute_final_dims(b, 2, 1, 0))
         return permute_final_dims(x, 1, 2, 0)
 
     def _incoming_matmul(self, a: Tensor, b: Tensor) -> Tensor:
         """x[*, i, j, c] = sum_k a[*, k, i, c] b[*, k, j, c] as a batched [c] matmul."""
-        x = torch.matmul(permute_final_dims(a, 2, 1, 0), permute_final_dims(b, 2, 0, 1))
+        x = dense_matmul(permute_final_dims(a, 2, 1, 0), permute_final_dims(b, 2, 0, 1))
         return permute_final_dims(x, 1, 2, 0)
 
     def _forward_pytorch(self, z: Tensor, mask: Optional[Tensor] = None,
                          chunk_size: Optional[int] = None) -> Tensor:
-        if mask is None:
-            mask = z.new_ones(z.shape[:-1])
+        # the mask in the input's dtype (the reference's own path multiplies
+        # in that dtype; a float32 mask on a bf16 input would promote a and b)
+        mask = z.new_ones(z.shape[:-1]) if mask is None else mask.to(z.dtype)
         m = mask.unsqueeze(-1)
         zn = self.layer_norm_in(z)
         a = self.linear_a_p(zn) * self.sigmoid(self.linear_a_g(zn)) * m
@@ -138,8 +139,9 @@ class TriangleMultiplicativeUpdate(nn.Module):
                 and self.layer_norm_in.elementwise_affine and self.layer_norm_out.elementwise_affine)
 
     def _backward_supported(self) -> bool:
-        """The shapes the backward kernels are built for."""
-        return self.c_z == 128 and self.c_hidden in (64, 128)
+        """The shapes the backward kernels are built for: c_z and c_hidden in
+        {32, 64, 128}."""
+        return self.c_z in (32, 64, 128) and self.c_hidden in (32, 64, 128)
 
     def _pack(self, params, fp32: bool) -> Tensor:
         return _ext.require().tri_mul_pack(params, self.c_z, self.c_hidden, fp32)

@@ -226,7 +226,8 @@ int gtk_tri_mul_contract_fp8(const void* a, const void* b, void* x, int64_t npla
  * reference has no backward kernel: its gradients are torch autograd over
  * TriangleMultiplicativeUpdate._forward_pytorch src/genie_tk/triangle_mul.py:103-132,
  * which this computes (forward activations recomputed from z and the raw
- * weights in w).  Gradients are written, not accumulated. */
+ * weights in w).  Gradients are written, not accumulated.  c_z and c each
+ * in {32, 64, 128}. */
 typedef struct gtk_tri_mul_grads {
   float *ln_in_w, *ln_in_b, *a_p_w, *a_p_b, *a_g_w, *a_g_b, *b_p_w, *b_p_b;
   float *b_g_w, *b_g_b, *g_w, *g_b, *ln_out_w, *ln_out_b, *z_w, *z_b;
@@ -309,8 +310,13 @@ int gtk_tri_attn_forward_chunked(const void* x, const float* mask, void* out, co
  * values (fractional, or above 1) are not differentiated correctly: the
  * forward gives them the bias inf * (mask - 1), which this backward does
  * not model, so callers must send such masks elsewhere (the genie_tk
- * modules use autograd of their PyTorch path for them).  c_in == 128,
- * H == 4, d == 32, N <= 4096. */
+ * modules use autograd of their PyTorch path for them).  c_in in
+ * {32, 64, 128}, H == 4, d == 32 (c_h == 128), N <= 4096.  Other head
+ * shapes (the reference layer's default of four heads of 8, two heads of 8)
+ * are computed here by padding: zero q/k/v/gate/output weight columns up
+ * to four heads of 32, W_q scaled by sqrt(32 / d) so the scores keep
+ * their 1/sqrt(d), the triangle bias of the missing heads zero, and the
+ * padded gradients dropped (genie_tk.triangle_attention does this). */
 typedef struct gtk_tri_attn_grads {
   float *ln_w, *ln_b, *tri_w, *q_w, *k_w, *v_w, *g_w, *g_b, *o_w, *o_b;
 } gtk_tri_attn_grads;

@@ -217,15 +217,18 @@ def test_cpu_host_switch():
         assert TriangleMultiplicationOutgoing(cz, c)._kernel_supported(torch.zeros(1, 4, 4, cz))
     assert not TriangleMultiplicationOutgoing(96, 32)._kernel_supported(torch.zeros(1, 4, 4, 96))
     assert not TriangleMultiplicationOutgoing(64, 48)._kernel_supported(torch.zeros(1, 4, 4, 64))
-    assert TriangleMultiplicationOutgoing(128, 64)._backward_supported()
-    assert not TriangleMultiplicationOutgoing(64, 32)._backward_supported()
+    # backward kernels: c_z and c in {32, 64, 128}
+    for cz, c in ((128, 64), (64, 32), (32, 32), (128, 128)):
+        assert TriangleMultiplicationOutgoing(cz, c)._backward_supported(), (cz, c)
+    assert not TriangleMultiplicationOutgoing(128, 256)._backward_supported()
     a = TriangleAttentionEndingNode(128, 128, 4)
     assert a._kernel_supported(torch.zeros(2, 4, 4, 128, dtype=torch.bfloat16))
-    assert a._headline_shape()
+    assert a._backward_supported()
+    # every forward head shape trains on the backward kernels (heads padded to 4 x 32)
     for cin, ch, h in ((128, 32, 4), (64, 32, 4), (32, 16, 2), (128, 64, 4), (64, 64, 2), (32, 8, 1)):
         t = TriangleAttentionEndingNode(cin, ch, h)
         assert t._kernel_supported(torch.zeros(1, 4, 4, cin)), (cin, ch, h)
-        assert not t._headline_shape()
+        assert t._backward_supported(), (cin, ch, h)
     assert not TriangleAttentionEndingNode(128, 128, 8)._kernel_supported(torch.zeros(1, 4, 4, 128))
     assert not TriangleAttentionEndingNode(128, 256, 4)._kernel_supported(torch.zeros(1, 4, 4, 128))
     assert not TriangleAttentionEndingNode(96, 32, 4)._kernel_supported(torch.zeros(1, 4, 4, 96))
@@ -380,3 +383,71 @@ def test_generic_class_direction_flag():
     assert TriangleMultiplicativeUpdate(16, 8)._outgoing
     assert not TriangleMultiplicationIncoming(16, 8)._outgoing
     assert TriangleAttention(16, 8, 2).starting
+
+
+def test_head_padding_for_the_backward_kernels():
+    """The attention backward kernels take four heads of 32 channels; a module
+    with fewer or narrower heads runs them on its weights padded with zero
+    channels and heads (triangle_attention._pad_heads), W_q scaled by
+    sqrt(32 / d).  The padded module computes the same function: checked
+    here in float64 on the PyTorch path, with the gradient of the real
+    parameters recovered as the backward does."""
+    from genie_tk import triangle_attention as ta
+
+    torch.manual_seed(0)
+    for cin, ch, h in ((32, 16, 2), (64, 32, 4), (32, 8, 1)):
+        mod = TriangleAttentionStartingNode(cin, ch, h, use_fused_kernel=False).double()
+        for p in mod.parameters():
+            with torch.no_grad():
+                p.copy_(torch.randn_like(p) * 0.3)
+        params = mod._param_list()
+        padded, idx, scale = ta._pad_heads([p.detach() for p in params], h, ch)
+        big = TriangleAttentionStartingNode(cin, 128, 4, use_fused_kernel=False).double()
+        with torch.no_grad():
+            for p, v in zip(big._param_list(), padded):
+                p.copy_(v)
+        x = torch.randn(2, 6, 6, cin, dtype=torch.float64)
+        m = (torch.rand(2, 6, 6) > 0.2).double()
+        torch.testing.assert_close(big(x, m), mod(x, m), rtol=0, atol=1e-12)
+        dy = torch.randn(2, 6, 6, cin, dtype=torch.float64)
+        g_small = torch.autograd.grad((mod(x, m) * dy).sum(), params)
+        g_big = list(torch.autograd.grad((big(x, m) * dy).sum(), big._param_list()))
+        g_big[2] = g_big[2][:h]
+        g_big[3] = g_big[3][idx] * scale
+        for k in (4, 5, 6, 7):
+            g_big[k] = g_big[k][idx]
+        g_big[8] = g_big[8][:, idx]
+        for a, b in zip(g_big, g_small):
+            torch.testing.assert_close(a, b, rtol=0, atol=1e-10)
+
+
+def test_dense_matmul_gradients():
+    """primitives.dense_matmul (the PyTorch path's batched products, taken on
+    contiguous operands with its own backward) against torch.autograd's
+    numerical Jacobian, on the permuted views the modules pass it."""
+    from genie_tk.primitives import dense_matmul
+    g = torch.Generator().manual_seed(3)
+    a = torch.randn(2, 5, 3, 4, dtype=torch.float64, generator=g).requires_grad_(True)
+    b = torch.randn(2, 6, 3, 4, dtype=torch.float64, generator=g).requires_grad_(True)
+    f = lambda a, b: dense_matmul(a.permute(0, 3, 1, 2), b.permute(0, 3, 2, 1))  # noqa: E731
+    assert torch.autograd.gradcheck(f, (a, b))
+    ref = torch.matmul(a.permute(0, 3, 1, 2), b.permute(0, 3, 2, 1))
+    assert torch.equal(f(a, b), ref)
+
+
+@pytest.mark.parametrize("cls", [TriangleMultiplicationOutgoing, TriangleMultiplicationIncoming,
+                                 TriangleAttentionStartingNode, TriangleAttentionEndingNode])
+def test_float32_mask_on_bf16_input(cls):
+    """The PyTorch path takes a float32 mask with a bf16 input (the kernel path
+    does): the mask is converted to the input's dtype, which gives the result
+    the reference's path gives for the mask passed in that dtype."""
+    mod = cls(32, 16) if "Multiplication" in cls.__name__ else cls(32, 8, 1)
+    mod = mod.bfloat16()
+    z = _pair(1, 10, 32, 7).bfloat16().requires_grad_(True)
+    m = torch.ones(1, 10, 10)
+    m[0, :, 8:] = 0.25
+    y = mod(z, m)
+    assert y.dtype == torch.bfloat16
+    assert torch.equal(y, mod(z, m.bfloat16()))
+    y.float().sum().backward()
+    assert z.grad is not None and torch.isfinite(z.grad.float()).all()

@@ -162,6 +162,13 @@ def test_workspace_sizes(lib):
     # twelve [B][N][H][N][32] activation/gradient buffers at least
     assert lib.gtk_tri_attn_backward_workspace_size(1, 512, 128, 128, 4, GTK_BF16) >= 12 * 512 * 512 * 128 * 2
     assert lib.gtk_tri_attn_backward_workspace_size(1, 512, 128, 64, 4, GTK_BF16) == 0
+    # the backward kernels' other shapes: c_z and c in {32, 64, 128}; c_in in {32, 64, 128}
+    for cz, c in ((64, 32), (32, 32), (32, 128)):
+        assert lib.gtk_tri_mul_backward_workspace_size(1, 64, cz, c, GTK_BF16) > 0
+    assert lib.gtk_tri_mul_backward_workspace_size(1, 64, 128, 256, GTK_BF16) == 0
+    for cin in (32, 64):
+        assert lib.gtk_tri_attn_backward_workspace_size(1, 64, cin, 128, 4, GTK_BF16) > 0
+    assert lib.gtk_tri_attn_backward_workspace_size(1, 64, 96, 128, 4, GTK_BF16) == 0
 
 
 def _err(lib):

@@ -10,7 +10,12 @@ Tolerances, per gradient tensor g against the oracle's r:
   * bf16: max|g - r| <= 3e-2 * max|r| and ||g - r||_2 <= 1e-2 * ||r||_2.  The
     bf16 backward rounds its intermediate planes (dX, dA, dB and the
     per-pair operands of the weight-gradient products) to bf16, so errors
-    are relative to the tensor's scale rather than per element.
+    are relative to the tensor's scale rather than per element.  A tensor
+    over the normwise bound passes if its error is at most 1.25 times that
+    of the reference's own bf16 path on the same case (autograd of the
+    module's PyTorch path in bf16, on the CPU): a bias gradient is a sum over
+    every pair with cancellation, whose bf16 error can exceed 1e-2 of its
+    norm in the reference too (the gate bias of one head of 8: 1.06e-2).
 """
 import numpy as np
 import pytest
@@ -25,18 +30,49 @@ pytestmark = pytest.mark.gpu
 DT = {"fp32": torch.float32, "bf16": torch.bfloat16}
 
 
-def _check_grad(got: np.ndarray, ref: np.ndarray, dname: str, what: str) -> float:
-    """Asserts the tolerance; returns max|g - r| / max|r| for the log."""
+def _normwise(got: np.ndarray, ref: np.ndarray) -> float:
+    return float(np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30))
+
+
+def _check_grad(got: np.ndarray, ref: np.ndarray, dname: str, what: str, floor: float = 0.0) -> float:
+    """Asserts the tolerance (``floor``: the reference bf16 path's normwise
+    error on this tensor, when measured); returns max|g - r| / max|r|."""
     assert np.isfinite(got).all(), f"{what}: non-finite gradient"
     err = np.abs(got - ref)
     scale = np.abs(ref).max()
     if dname == "fp32":
         assert err.max() <= 1e-4 * max(1.0, scale), f"{what}: max err {err.max():.3e} (scale {scale:.3e})"
     else:
-        rel = np.linalg.norm(got - ref) / max(np.linalg.norm(ref), 1e-30)
+        rel = _normwise(got, ref)
         assert err.max() <= 3e-2 * scale, f"{what}: max err {err.max():.3e} > 3e-2 * {scale:.3e}"
-        assert rel <= 1e-2, f"{what}: normwise relative error {rel:.3e}"
+        assert rel <= max(1e-2, 1.25 * floor), \
+            f"{what}: normwise relative error {rel:.3e} (reference bf16 path: {floor:.3e})"
     return float(err.max() / max(scale, 1e-30))
+
+
+def _reference_bf16_errors(module, P, x, m, dy, dx_ref, g_ref) -> dict:
+    """Normwise errors of the reference's own bf16 path (``module``, a fresh
+    PyTorch-path module: autograd in bf16 on the CPU) against the oracle."""
+    module.load_state_dict(H.to_state_dict(P))
+    module = module.bfloat16()
+    xt = torch.from_numpy(x).bfloat16().requires_grad_(True)
+    module(xt, torch.from_numpy(m)).backward(torch.from_numpy(dy).bfloat16())
+    out = {"dx": _normwise(_np(xt.grad), dx_ref)}
+    for name, prm in module.named_parameters():
+        out[name] = _normwise(_np(prm.grad), g_ref[name])
+    return out
+
+
+def _check_all(dname, got: dict, refs: dict, reference_module) -> list:
+    """Checks every gradient; for bf16 tensors over the fixed normwise bound,
+    measures the reference bf16 path once (``reference_module()`` returns its
+    errors) and allows 1.25 times its error."""
+    floors = {}
+    if dname == "bf16" and any(_normwise(got[k], refs[k]) > 1e-2 for k in got):
+        floors = reference_module()
+        log("  reference bf16 path normwise errors: "
+            + ", ".join(f"{k} {v:.2e}" for k, v in floors.items() if _normwise(got[k], refs[k]) > 1e-2))
+    return [(_check_grad(got[k], refs[k], dname, k, floors.get(k, 0.0)), k) for k in got]
 
 
 def _np(t):
@@ -62,10 +98,13 @@ def test_tri_mul_backward(dname, outgoing, N, c):
     y.backward(torch.from_numpy(dy).to("cuda", dt))
     torch.cuda.synchronize()
     dz_ref, g_ref = grads.tri_mul_grad(z, m, P, outgoing, dy)
-    worst = [(_check_grad(_np(zt.grad), dz_ref, dname, "dz"), "dz")]
+    got, refs = {"dx": _np(zt.grad)}, {"dx": dz_ref}
     for name, prm in mod.named_parameters():
         assert prm.grad is not None and prm.grad.dtype == dt, name
-        worst.append((_check_grad(_np(prm.grad), g_ref[name], dname, name), name))
+        got[name], refs[name] = _np(prm.grad), g_ref[name]
+    cls = type(mod)
+    worst = _check_all(dname, got, refs, lambda: _reference_bf16_errors(
+        cls(128, c, use_fused_kernel=False), P, z, m, dy, dz_ref, g_ref))
     log(f"  worst max|g - r| / max|r|: {max(worst)[0]:.2e} ({max(worst)[1]})")
 
 
@@ -83,31 +122,35 @@ def test_tri_mul_backward_runs_the_kernels(monkeypatch):
     assert all(p.grad is not None and torch.isfinite(p.grad).all() for p in mod.parameters())
 
 
-def _tri_attn_backward_case(dname, starting, N, lengths, inner_mask=0.0):
-    log(f"tri_attn backward {dname} starting={starting} N={N} lengths={lengths}")
+def _tri_attn_backward_case(dname, starting, N, lengths, inner_mask=0.0, cin=128, ch=128, heads=4):
+    log(f"tri_attn backward {dname} starting={starting} N={N} lengths={lengths} c_in={cin} c_h={ch} H={heads}")
     dt = DT[dname]
     B = len(lengths)
-    P = H.draw_params(H.tri_attn_shapes(128, 128, 4), seed=N + 7, ln_random=True, bias_random=True)
-    x = H.pair_input(B, N, 128, seed=N + 8)
+    P = H.draw_params(H.tri_attn_shapes(cin, ch, heads), seed=N + 7, ln_random=True, bias_random=True)
+    x = H.pair_input(B, N, cin, seed=N + 8)
     m = H.tail_mask(B, N, lengths)
     if inner_mask > 0:
         # scattered masked pairs inside the valid block (no row loses every key)
         rng = np.random.default_rng(N)
         m = m * (rng.random(m.shape) >= inner_mask).astype(np.float32)
         m[:, np.arange(N), np.arange(N)] = H.tail_mask(B, N, lengths)[:, np.arange(N), np.arange(N)]
-    dy = H.pair_input(B, N, 128, seed=N + 9)
+    dy = H.pair_input(B, N, cin, seed=N + 9)
     if dname == "bf16":
         P, x, dy = H.bf16_params(P), H.bf16_round(x), H.bf16_round(dy)
-    mod = triattn_module(P, starting, 4, dt)
+    mod = triattn_module(P, starting, heads, dt)
+    mod._forward_pytorch = lambda *a, **k: (_ for _ in ()).throw(AssertionError("PyTorch path"))
     xt = torch.from_numpy(x).to("cuda", dt).requires_grad_(True)
     y = mod(xt, torch.from_numpy(m).to("cuda"))
     y.backward(torch.from_numpy(dy).to("cuda", dt))
     torch.cuda.synchronize()
-    dx_ref, g_ref = grads.tri_attn_grad(x, m, P, starting, 4, dy)
-    worst = [(_check_grad(_np(xt.grad), dx_ref, dname, "dx"), "dx")]
+    dx_ref, g_ref = grads.tri_attn_grad(x, m, P, starting, heads, dy)
+    got, refs = {"dx": _np(xt.grad)}, {"dx": dx_ref}
     for name, prm in mod.named_parameters():
         assert prm.grad is not None and prm.grad.dtype == dt, name
-        worst.append((_check_grad(_np(prm.grad), g_ref[name], dname, name), name))
+        got[name], refs[name] = _np(prm.grad), g_ref[name]
+    cls = type(mod)
+    worst = _check_all(dname, got, refs, lambda: _reference_bf16_errors(
+        cls(cin, ch, heads, use_fused_kernel=False), P, x, m, dy, dx_ref, g_ref))
     log(f"  worst max|g - r| / max|r|: {max(worst)[0]:.2e} ({max(worst)[1]})")
 
 
@@ -140,3 +183,47 @@ def test_tri_attn_backward_runs_the_kernels(monkeypatch):
     y.float().square().sum().backward()
     assert x.grad is not None and x.grad.shape == x.shape and torch.isfinite(x.grad).all()
     assert all(p.grad is not None and torch.isfinite(p.grad).all() for p in mod.parameters())
+
+
+@pytest.mark.parametrize("dname", ["fp32", "bf16"])
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("cin,ch,heads", [(128, 32, 4), (64, 32, 4), (32, 16, 2), (32, 8, 1)])
+def test_tri_attn_backward_other_shapes(dname, starting, cin, ch, heads):
+    """The reference layer's default attention (c_in = 128, four heads of 8;
+    pair_transform.py:116-117), its tests' shapes (c_in = 64 with four heads
+    of 8, tests/test_triangle_attention.py:36; c_in = 32 with two heads of 8,
+    :74) and one head of 8: the backward kernels of c_in 32 / 64 / 128, on
+    the weights padded to four heads of 32, with fully masked rows."""
+    _tri_attn_backward_case(dname, starting, 40, [40, 33], cin=cin, ch=ch, heads=heads)
+
+
+@pytest.mark.parametrize("dname", ["fp32", "bf16"])
+@pytest.mark.parametrize("outgoing", [True, False])
+@pytest.mark.parametrize("cz,c,N", [(64, 32, 40), (32, 32, 37), (64, 64, 33), (32, 128, 24)])
+def test_tri_mul_backward_other_shapes(dname, outgoing, cz, c, N):
+    """The backward kernels of c_z in {32, 64} and c in {32, 64, 128} (the
+    reference tests' c_z = 64, c = 32, tests/test_triangle_mul.py:37), whose
+    forward packing leaves the LayerNorm affine to the kernels."""
+    log(f"tri_mul backward {dname} outgoing={outgoing} c_z={cz} c={c} N={N}")
+    dt = DT[dname]
+    P = H.draw_params(H.tri_mul_shapes(cz, c), seed=N + c + cz, ln_random=True, bias_random=True)
+    z = H.pair_input(2, N, cz, seed=N + 1)
+    m = H.tail_mask(2, N, [N, N - 5])
+    dy = H.pair_input(2, N, cz, seed=N + 2)
+    if dname == "bf16":
+        P, z, dy = H.bf16_params(P), H.bf16_round(z), H.bf16_round(dy)
+    mod = trimul_module(P, outgoing, dt)
+    mod._forward_pytorch = lambda *a, **k: (_ for _ in ()).throw(AssertionError("PyTorch path"))
+    zt = torch.from_numpy(z).to("cuda", dt).requires_grad_(True)
+    y = mod(zt, torch.from_numpy(m).to("cuda"))
+    y.backward(torch.from_numpy(dy).to("cuda", dt))
+    torch.cuda.synchronize()
+    dz_ref, g_ref = grads.tri_mul_grad(z, m, P, outgoing, dy)
+    got, refs = {"dx": _np(zt.grad)}, {"dx": dz_ref}
+    for name, prm in mod.named_parameters():
+        assert prm.grad is not None and prm.grad.dtype == dt, name
+        got[name], refs[name] = _np(prm.grad), g_ref[name]
+    cls = type(mod)
+    worst = _check_all(dname, got, refs, lambda: _reference_bf16_errors(
+        cls(cz, c, use_fused_kernel=False), P, z, m, dy, dz_ref, g_ref))
+    log(f"  worst max|g - r| / max|r|: {max(worst)[0]:.2e} ({max(worst)[1]})")
