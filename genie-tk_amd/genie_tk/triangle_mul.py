@@ -35,6 +35,40 @@ from genie_tk.utils import has_cuda_kernels, permute_final_dims
 
 _CUDA_AVAILABLE = has_cuda_kernels()
 
+# hidden widths below the kernels' 32-channel tile run as 32 channels, each
+# real channel repeated 32 / c_hidden times (_repeat_channels)
+_NARROW = (8, 16)
+# parameter positions (_PARAMS order) whose leading axis is the hidden channel
+_HIDDEN_ROWS = (2, 3, 4, 5, 6, 7, 8, 9, 12, 13)
+
+
+def _repeat_channels(params, r: int):
+    """The module's parameters for r copies of every hidden channel (c_hidden
+    c -> r c, copy k of channel j at r-channel index k c + j): the a/b
+    projection and gate rows and biases and the LN_out affine repeated, the
+    columns of W_z repeated and scaled by 1/r (exact: r is 2 or 4).  The
+    copies of a and b are equal, so are the copies of x; LN_out over the r c
+    channels has the mean and variance of x's c; and the scaled W_z adds the
+    r equal copies back to one.  The update is the module's own."""
+    out = list(params)
+    for k in _HIDDEN_ROWS:
+        out[k] = params[k].repeat(r, *([1] * (params[k].dim() - 1)))
+    out[14] = params[14].repeat(1, r) * (1.0 / r)
+    return out
+
+
+def _fold_channel_grads(grads, c: int, r: int):
+    """Gradients of the repeated parameters back to the module's: the sum
+    over the r copies (the chain rule through the repetition), and 1/r of it
+    for W_z's columns."""
+    out = list(grads)
+    for k in _HIDDEN_ROWS:
+        g = grads[k]
+        out[k] = g.reshape(r, c, *g.shape[1:]).sum(0)
+    gz = grads[14]
+    out[14] = gz.reshape(gz.shape[0], r, c).sum(1) * (1.0 / r)
+    return out
+
 
 class _TriMulFunction(torch.autograd.Function):
     """The update on the HIP kernels, forward and backward.
@@ -55,12 +89,20 @@ class _TriMulFunction(torch.autograd.Function):
         z, mask, *params = ctx.saved_tensors
         mod = ctx.module
         zb, mb, lead = _dispatch.flatten_batch(z, mask)
+        r = mod._repeats()
+        bparams = list(params)
+        if r > 1:
+            with torch.no_grad():
+                bparams = _repeat_channels(bparams, r)
         res = _ext.require().tri_mul_backward(
-            zb, mb, dy.reshape(zb.shape).to(z.dtype), list(params), mod.c_z, mod.c_hidden,
+            zb, mb, dy.reshape(zb.shape).to(z.dtype), bparams, mod.c_z, mod.c_hidden * r,
             mod._outgoing, mod.layer_norm_in.eps, mod.layer_norm_out.eps)
         dz = res[0].reshape(z.shape) if ctx.needs_input_grad[1] else None
-        grads = [g.to(p.dtype) if ctx.needs_input_grad[3 + k] else None
-                 for k, (g, p) in enumerate(zip(res[1:], params))]
+        g = list(res[1:])
+        if r > 1:
+            g = _fold_channel_grads(g, mod.c_hidden, r)
+        grads = [gk.to(p.dtype) if ctx.needs_input_grad[3 + k] else None
+                 for k, (gk, p) in enumerate(zip(g, params))]
         return (None, dz, None, *grads)
 
 
@@ -132,19 +174,28 @@ class TriangleMultiplicativeUpdate(nn.Module):
 
     # -- HIP kernel path ----------------------------------------------------
     def _kernel_supported(self, z: Tensor) -> bool:
-        """Forward kernels: c_z in {32, 64, 128}, c_hidden in {32, 64, 128, 256}."""
+        """Forward kernels: c_z in {32, 64, 128}, c_hidden in {32, 64, 128,
+        256}, and 8 or 16 run as 32 (_repeat_channels)."""
         return (z.dim() >= 3 and z.shape[-2] == z.shape[-3] and z.shape[-1] == self.c_z
-                and self.c_z in (32, 64, 128) and self.c_hidden in (32, 64, 128, 256)
+                and self.c_z in (32, 64, 128) and self.c_hidden in (*_NARROW, 32, 64, 128, 256)
                 and z.dtype in _dispatch.SUPPORTED_DTYPES
                 and self.layer_norm_in.elementwise_affine and self.layer_norm_out.elementwise_affine)
 
     def _backward_supported(self) -> bool:
         """The shapes the backward kernels are built for: c_z and c_hidden in
-        {32, 64, 128}."""
-        return self.c_z in (32, 64, 128) and self.c_hidden in (32, 64, 128)
+        {32, 64, 128}, and c_hidden 8 or 16 run as 32."""
+        return self.c_z in (32, 64, 128) and self.c_hidden in (*_NARROW, 32, 64, 128)
+
+    def _repeats(self) -> int:
+        """Copies of each hidden channel on the kernels: 32 / c_hidden for the
+        narrow widths, else 1."""
+        return 32 // self.c_hidden if self.c_hidden in _NARROW else 1
 
     def _pack(self, params, fp32: bool) -> Tensor:
-        return _ext.require().tri_mul_pack(params, self.c_z, self.c_hidden, fp32)
+        r = self._repeats()
+        if r > 1:
+            params = _repeat_channels(params, r)
+        return _ext.require().tri_mul_pack(params, self.c_z, self.c_hidden * r, fp32)
 
     # the parameters in the order of tri_mul_pack / gtk_tri_mul_weights
     _PARAMS = tuple((m, w) for m in ("layer_norm_in", "linear_a_p", "linear_a_g", "linear_b_p",
@@ -165,9 +216,9 @@ class TriangleMultiplicativeUpdate(nn.Module):
         C = _ext.require()
         zb, mb, lead = _dispatch.flatten_batch(z, mask)
         packed = self._packed_params(z.dtype == torch.float32)
-        out = C.tri_mul_forward(zb, mb, packed, self.c_z, self.c_hidden, self._outgoing,
-                                residual, self.layer_norm_in.eps, self.layer_norm_out.eps,
-                                int(chunk_size or 0))
+        out = C.tri_mul_forward(zb, mb, packed, self.c_z, self.c_hidden * self._repeats(),
+                                self._outgoing, residual, self.layer_norm_in.eps,
+                                self.layer_norm_out.eps, int(chunk_size or 0))
         return out.reshape(*lead, *out.shape[1:])
 
     @staticmethod

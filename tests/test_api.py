@@ -451,3 +451,44 @@ def test_float32_mask_on_bf16_input(cls):
     assert torch.equal(y, mod(z, m.bfloat16()))
     y.float().sum().backward()
     assert z.grad is not None and torch.isfinite(z.grad.float()).all()
+
+
+@pytest.mark.parametrize("c,outgoing", [(16, True), (16, False), (8, True)])
+def test_channel_repetition_for_narrow_hidden_widths(c, outgoing):
+    """Tri-mul with c_hidden 8 or 16 runs on the kernels as 32 channels, each
+    repeated 32 / c times (triangle_mul._repeat_channels).  The repeated
+    module computes the same update, and summing its gradients over the
+    copies (_fold_channel_grads) gives the module's own: float64, PyTorch
+    path.  A plain zero padding would not: LN_out's mean and variance run
+    over every hidden channel (checked too)."""
+    from genie_tk import triangle_mul as tm
+
+    torch.manual_seed(c)
+    cls = TriangleMultiplicationOutgoing if outgoing else TriangleMultiplicationIncoming
+    mod = cls(32, c, use_fused_kernel=False).double()
+    for p in mod.parameters():
+        with torch.no_grad():
+            p.copy_(torch.randn_like(p) * 0.3)
+    r = 32 // c
+    params = mod._param_list()
+    big = cls(32, 32, use_fused_kernel=False).double()
+    with torch.no_grad():
+        for p, v in zip(big._param_list(), tm._repeat_channels([p.detach() for p in params], r)):
+            p.copy_(v)
+    z = torch.randn(2, 7, 7, 32, dtype=torch.float64)
+    m = (torch.rand(2, 7, 7) > 0.2).double()
+    torch.testing.assert_close(big(z, m), mod(z, m), rtol=0, atol=1e-12)
+    dy = torch.randn(2, 7, 7, 32, dtype=torch.float64)
+    g_small = torch.autograd.grad((mod(z, m) * dy).sum(), params)
+    g_big = tm._fold_channel_grads(torch.autograd.grad((big(z, m) * dy).sum(), big._param_list()), c, r)
+    for a, b in zip(g_big, g_small):
+        torch.testing.assert_close(a, b, rtol=0, atol=1e-10)
+    # zero channels instead of copies change LN_out's statistics
+    with torch.no_grad():
+        for k in tm._HIDDEN_ROWS:
+            p = big._param_list()[k]
+            p[c:] = 0
+        big.layer_norm_out.weight[c:] = 0
+        big.linear_z.weight.zero_()
+        big.linear_z.weight[:, :c] = mod.linear_z.weight
+    assert (big(z, m) - mod(z, m)).abs().max() > 1e-3
