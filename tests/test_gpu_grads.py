@@ -12,8 +12,9 @@ Tolerances, per gradient tensor g against the oracle's r:
     per-pair operands of the weight-gradient products) to bf16, so errors
     are relative to the tensor's scale rather than per element.  A tensor
     over the normwise bound passes if its error is at most 1.25 times that
-    of the reference's own bf16 path on the same case (autograd of the
-    module's PyTorch path in bf16, on the CPU): a bias gradient is a sum over
+    of the reference's bf16 computation on the same case (autograd of the
+    module's PyTorch path, the reference's operation sequence op for op, in
+    bf16 on the CPU): a bias gradient is a sum over
     every pair with cancellation, whose bf16 error can exceed 1e-2 of its
     norm in the reference too (the gate bias of one head of 8: 1.06e-2).
 """
@@ -51,8 +52,9 @@ def _check_grad(got: np.ndarray, ref: np.ndarray, dname: str, what: str, floor: 
 
 
 def _reference_bf16_errors(module, P, x, m, dy, dx_ref, g_ref) -> dict:
-    """Normwise errors of the reference's own bf16 path (``module``, a fresh
-    PyTorch-path module: autograd in bf16 on the CPU) against the oracle."""
+    """Normwise errors of the reference's bf16 computation against the
+    oracle: ``module`` is a fresh PyTorch-path module (the reference's
+    operation sequence op for op), run with autograd in bf16 on the CPU."""
     module.load_state_dict(H.to_state_dict(P))
     module = module.bfloat16()
     xt = torch.from_numpy(x).bfloat16().requires_grad_(True)

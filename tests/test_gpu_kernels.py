@@ -188,9 +188,11 @@ def test_tri_mul_narrow_hidden(dname, outgoing, c_z, c, N):
     times): the update, the residual form and row chunks against the oracle
     of the module's own c.  bf16: LN_out over 8 channels magnifies the bf16
     rounding of x (held in bf16 by the kernels' planes and by the reference's
-    bf16 path alike) where a pair's 8 values are close, beyond the fixed
-    bound on a few elements.  There the output passes if it is no worse than
-    the reference's own bf16 path on the same inputs (at c_z = 64, c = 8,
+    bf16 computation alike) where a pair's 8 values are close, beyond the
+    fixed bound on a few elements.  There the output passes if it is no
+    worse than the reference's bf16 computation on the same inputs (the
+    module's PyTorch path in bf16: the reference's operation sequence op
+    for op; at c_z = 64, c = 8,
     N = 70 that path puts 37 of 627 200 elements over the bound, worst
     ratio 1.60): at most as many elements over the bound, and a worst
     error/bound ratio within 1.25 times that path's."""
@@ -222,7 +224,8 @@ def test_tri_mul_narrow_hidden(dname, outgoing, c_z, c, N):
 
 
 def _reference_bf16_forward(module, P, z, m):
-    """The reference's bf16 path (the module's PyTorch path in bf16, CPU)."""
+    """The reference's bf16 computation: the module's PyTorch path (the
+    reference's operation sequence op for op) in bf16 on the CPU."""
     module.load_state_dict(H.to_state_dict(P))
     with torch.no_grad():
         return module.bfloat16()(torch.from_numpy(z).bfloat16(), torch.from_numpy(m)).float().numpy()
