@@ -113,6 +113,13 @@ __global__ __launch_bounds__(256) void trimul_prologue_kernel(
 //     consecutive pairs of one channel and writes them as two 16-byte stores.
 //     The gate bias enters as a factor, 2^(u+b) = 2^u * 2^b, so the gate costs
 //     one FMA beside its two transcendental instructions.
+//     Each 32-channel tile of the result goes out through the wave's LDS
+//     staging rows, 16 channels at a time (the lanes of those channels write
+//     their 2 x 32 bytes, then every lane stores 16 bytes of one channel's
+//     128-byte row): each store instruction writes 8 whole cache lines
+//     instead of 32 lines in two 16-byte pieces each (59.6 -> 58.7 us at
+//     N = 512, bit-identical).  The z rows load without a branch: an
+//     invalid pair reads pair (b, 0, 0) and its mask of 0 zeroes its output.
 //     FP8 (the fp8 a/b storage experiment): the planes hold OCP fp8 E4M3
 //     values (v_cvt_pk_fp8_f32, round to nearest even; clamped to +-448
 //     first), one 16-byte store per lane and channel tile.
@@ -140,6 +147,9 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
   __shared__ float bl[2][2][CH];  // [side][projection, gate as 2^b_g]
   // the pair mask of each wave's current step (64 consecutive pairs)
   __shared__ __attribute__((aligned(16))) float ml[WAVES][64];
+  // output staging: 16 channel rows x 128 bytes (64 pairs), pitch 144
+  constexpr int SPITCH = 144;
+  __shared__ __attribute__((aligned(16))) char stg[FP8 ? 1 : WAVES][FP8 ? 16 : 16 * SPITCH];
   copy_to_lds_async(wl[0], w.w_ap, PE * 2);
   copy_to_lds_async(wl[1], w.w_ag, PE * 2);
   copy_to_lds_async(wl[2], w.w_bp, PE * 2);
@@ -172,12 +182,11 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
       const int v = (vt + u) * 32 + prow;
       const int p = outgoing ? f : v, q = outgoing ? v : f;
       const bool valid = p < N && q < N;
+      // an invalid pair reads pair (b, 0, 0): its mask is 0, so its outputs
+      // are zero all the same, and the loads need no branch
       const bf16* row = z + (((int64_t)b * N + (valid ? p : 0)) * N + (valid ? q : 0)) * CZ + half * (CZ / 2);
 #pragma unroll
-      for (int ch = 0; ch < KCH; ++ch) {
-        if (valid) zr[u][ch].load(row + ch * 8);
-        else zr[u][ch].zero();
-      }
+      for (int ch = 0; ch < KCH; ++ch) zr[u][ch].load(row + ch * 8);
     }
   };
 
@@ -246,6 +255,7 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
         const int cc = ct * 32 + i32;
         const float bpc = bp[cc];
         const float ebg = ebgs[cc];
+        uint32_t pku[2][8];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const f32x16& ap = u ? ap1 : ap0;
@@ -278,12 +288,41 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
               pk[j / 2] = pack_bf16x2(o0, o1);
             }
           }
-          uint4* o = reinterpret_cast<uint4*>(dst + (int64_t)cc * plane + 32 * u);
           if constexpr (FP8) {
+            uint4* o = reinterpret_cast<uint4*>(dst + (int64_t)cc * plane + 32 * u);
             o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
           } else {
-            o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-            o[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) pku[u][e] = pk[e];
+          }
+        }
+        if constexpr (!FP8) {
+          // Through the wave's staging rows, 16 channels at a time: lanes of
+          // channels 16h' .. 16h'+15 write their 2 x 32 bytes, then every
+          // lane stores 16 bytes of one channel's 128-byte row, so each store
+          // instruction covers 8 whole cache lines.
+          char* const sw = stg[wave];
+          OutT* const row0 = dst - 16 * half;  // pair vt*32 of plane 0, row fl
+#pragma unroll
+          for (int hp = 0; hp < 2; ++hp) {
+            if ((i32 >> 4) == hp) {
+              char* wr = sw + (i32 & 15) * SPITCH + 32 * half;
+#pragma unroll
+              for (int u = 0; u < 2; ++u) {
+                *reinterpret_cast<uint4*>(wr + 64 * u) =
+                    make_uint4(pku[u][0], pku[u][1], pku[u][2], pku[u][3]);
+                *reinterpret_cast<uint4*>(wr + 64 * u + 16) =
+                    make_uint4(pku[u][4], pku[u][5], pku[u][6], pku[u][7]);
+              }
+            }
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int m = 0; m < 2; ++m) {
+              const int r = (lane >> 3) + 8 * m;
+              const uint4 v = *reinterpret_cast<const uint4*>(sw + r * SPITCH + (lane & 7) * 16);
+              *reinterpret_cast<uint4*>(row0 + (int64_t)(ct * 32 + 16 * hp + r) * plane + (lane & 7) * 8) = v;
+            }
+            __builtin_amdgcn_wave_barrier();
           }
         }
       }
@@ -797,7 +836,10 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(
 // 3b. bf16 epilogue: persistent, 8 waves per CU with W_g and W_z resident in
 //     LDS.  Per 32-pair tile (row i, pairs jt*32 ..):
 //   * the x tile (c rows of 32 pairs, 64 B each) lands in the wave's own LDS
-//     buffer with direct global->LDS copies, chunk-swizzled so the transposing
+//     buffer with direct global->LDS copies (non-temporal: this is the x
+//     planes' last read, and streaming it keeps z and the next planes in
+//     the caches; prologue and contraction 2 us faster each at N = 512),
+//     chunk-swizzled so the transposing
 //     reads below are bank-conflict free, and is read back with
 //     ds_read_b64_tr_b16 straight into MFMA fragments (lane = pair, 8
 //     consecutive channels per fragment);
@@ -856,7 +898,7 @@ __global__ __launch_bounds__(512) void trimul_epilogue_bf16_kernel(
     for (int n = 0; n < CH / 16; ++n) {
       const int row = 16 * n + (lane >> 2);
       const int k = (lane & 3) ^ swz(row);
-      g2lds16(src + row * plane + 8 * k, xw + n * 512);
+      g2lds16_nt(src + row * plane + 8 * k, xw + n * 512);
     }
   };
   // Always KZ load instructions (an invalid pair reads pair j = 0; its
