@@ -120,11 +120,14 @@ __global__ __launch_bounds__(256) void trimul_prologue_kernel(
 //     instead of 32 lines in two 16-byte pieces each (59.6 -> 58.7 us at
 //     N = 512, bit-identical).  The z rows load without a branch: an
 //     invalid pair reads pair (b, 0, 0) and its mask of 0 zeroes its output.
+//     TPS = 1 (one tile a step) when two-tile steps would leave waves of the
+//     grid without work (N = 256: 1024 steps for 2048 waves; 23.6 -> 19.5 us,
+//     bit-identical): then each weight fragment feeds one tile's products.
 //     FP8 (the fp8 a/b storage experiment): the planes hold OCP fp8 E4M3
 //     values (v_cvt_pk_fp8_f32, round to nearest even; clamped to +-448
 //     first), one 16-byte store per lane and channel tile.
 // ---------------------------------------------------------------------------
-template <int CZ, int CH, bool FP8 = false, bool RANGE = false>
+template <int CZ, int CH, bool FP8 = false, bool RANGE = false, int TPS = 2>
 __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
     const bf16* __restrict__ z, const float* __restrict__ mask,
     std::conditional_t<FP8, uint8_t, bf16>* __restrict__ pa,
@@ -169,16 +172,16 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
   const int i32 = lane & 31;
   const int prow = 16 * ((i32 >> 2) & 1) + 4 * (i32 >> 3) + (i32 & 3);
   const int vtiles = Np / 32;  // even: Np is a multiple of 64
-  const int64_t nsteps = ntiles / 2;
+  const int64_t nsteps = ntiles / TPS;  // ntiles is even (Np / 32 tiles a row)
 
-  // raw z rows of the two tiles of step s (zeros outside the N x N pair grid)
+  // raw z rows of the TPS tiles of step s (zeros outside the N x N pair grid)
   auto load_z = [&](Frag<bf16> (*zr)[KCH], int64_t s) {
-    const int64_t tile = 2 * s;
+    const int64_t tile = (int64_t)TPS * s;
     const int vt = (int)(tile % vtiles);
     const int f = r0 + (int)((tile / vtiles) % nrows);
     const int b = (int)(tile / ((int64_t)vtiles * nrows));
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < TPS; ++u) {
       const int v = (vt + u) * 32 + prow;
       const int p = outgoing ? f : v, q = outgoing ? v : f;
       const bool valid = p < N && q < N;
@@ -194,7 +197,7 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
   // lane (pair vt*32 + lane), staged in the wave's LDS slot and read back by
   // each lane as its 16 output pairs of a tile when it stores.
   auto load_mask = [&](int64_t s) {
-    const int64_t tile = 2 * s;
+    const int64_t tile = (int64_t)TPS * s;
     const int vt = (int)(tile % vtiles);
     const int f = r0 + (int)((tile / vtiles) % nrows);
     const int b = (int)(tile / ((int64_t)vtiles * nrows));
@@ -210,20 +213,20 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
   const int64_t sstride = (int64_t)gridDim.x * WAVES;
   // this wave's first step: rows and mask in flight (the next step's are
   // loaded ahead of each step's stores)
-  Frag<bf16> zr[2][KCH];
+  Frag<bf16> zr[TPS][KCH];
   float mv = 0.f;
   if (s < nsteps) {
     load_z(zr, s);
     mv = load_mask(s);
   }
   for (; s < nsteps; s += sstride) {
-    const int64_t tile = 2 * s;
+    const int64_t tile = (int64_t)TPS * s;
     const int vt = (int)(tile % vtiles);
     const int fl = (int)((tile / vtiles) % nrows);  // row of the written planes
     const int b = (int)(tile / ((int64_t)vtiles * nrows));
-    Frag<bf16> xf[2][KCH];
-    ln_frags_bf16<CZ>(xf[0], zr[0], eps);
-    ln_frags_bf16<CZ>(xf[1], zr[1], eps);
+    Frag<bf16> xf[TPS][KCH];
+#pragma unroll
+    for (int u = 0; u < TPS; ++u) ln_frags_bf16<CZ>(xf[u], zr[u], eps);
     ml[wave][lane] = mv;
     if (s + sstride < nsteps) {
       load_z(zr, s + sstride);
@@ -241,25 +244,30 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
         Frag<bf16> wfp, wfg;
         load_wfrag_lds(wfp, wp, ct, 0, KCH);
         load_wfrag_lds(wfg, wg, ct, 0, KCH);
-        f32x16 ap0 = mma0(xf[0][0], wfp), ap1 = mma0(xf[1][0], wfp);
-        f32x16 ag0 = mma0(xf[0][0], wfg), ag1 = mma0(xf[1][0], wfg);
+        f32x16 apv[TPS], agv[TPS];
+#pragma unroll
+        for (int u = 0; u < TPS; ++u) {
+          apv[u] = mma0(xf[u][0], wfp);
+          agv[u] = mma0(xf[u][0], wfg);
+        }
 #pragma unroll
         for (int ks = 1; ks < KCH; ++ks) {
           load_wfrag_lds(wfp, wp, ct, ks, KCH);
           load_wfrag_lds(wfg, wg, ct, ks, KCH);
-          mma(ap0, xf[0][ks], wfp);
-          mma(ap1, xf[1][ks], wfp);
-          mma(ag0, xf[0][ks], wfg);
-          mma(ag1, xf[1][ks], wfg);
+#pragma unroll
+          for (int u = 0; u < TPS; ++u) {
+            mma(apv[u], xf[u][ks], wfp);
+            mma(agv[u], xf[u][ks], wfg);
+          }
         }
         const int cc = ct * 32 + i32;
         const float bpc = bp[cc];
         const float ebg = ebgs[cc];
-        uint32_t pku[2][8];
+        uint32_t pku[TPS][8];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const f32x16& ap = u ? ap1 : ap0;
-          const f32x16& ag = u ? ag1 : ag0;
+        for (int u = 0; u < TPS; ++u) {
+          const f32x16& ap = apv[u];
+          const f32x16& ag = agv[u];
           // mask of this lane's pairs 32u + 16*half .. +15
           float mk[16];
 #pragma unroll
@@ -308,7 +316,7 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
             if ((i32 >> 4) == hp) {
               char* wr = sw + (i32 & 15) * SPITCH + 32 * half;
 #pragma unroll
-              for (int u = 0; u < 2; ++u) {
+              for (int u = 0; u < TPS; ++u) {
                 *reinterpret_cast<uint4*>(wr + 64 * u) =
                     make_uint4(pku[u][0], pku[u][1], pku[u][2], pku[u][3]);
                 *reinterpret_cast<uint4*>(wr + 64 * u + 16) =
@@ -316,11 +324,14 @@ __global__ __launch_bounds__(512) void trimul_prologue_bf16_kernel(
               }
             }
             __builtin_amdgcn_wave_barrier();
+            // rows of 64 * TPS bytes: LPR lanes a row, 16 / TPS rows an instruction
+            constexpr int LPR = 4 * TPS;
 #pragma unroll
-            for (int m = 0; m < 2; ++m) {
-              const int r = (lane >> 3) + 8 * m;
-              const uint4 v = *reinterpret_cast<const uint4*>(sw + r * SPITCH + (lane & 7) * 16);
-              *reinterpret_cast<uint4*>(row0 + (int64_t)(ct * 32 + 16 * hp + r) * plane + (lane & 7) * 8) = v;
+            for (int m = 0; m < TPS; ++m) {
+              const int r = lane / LPR + (16 / TPS) * m;
+              const int c16 = lane % LPR;
+              const uint4 v = *reinterpret_cast<const uint4*>(sw + r * SPITCH + c16 * 16);
+              *reinterpret_cast<uint4*>(row0 + (int64_t)(ct * 32 + 16 * hp + r) * plane + c16 * 8) = v;
             }
             __builtin_amdgcn_wave_barrier();
           }
@@ -1251,17 +1262,24 @@ static int launch_trimul_prologue(const void* z, const float* mask, const TriMul
   if (ps == 0) ps = (int64_t)nrows * Np;
   const int64_t ptiles = B * (int64_t)nrows * (Np / 32);
   if constexpr (trimul_fast<T, CZ, CH>()) {
-    const int grid = (int)std::min<int64_t>(device_cus(), (ptiles / 2 + 3) / 4);
+    // two tiles a step (each weight fragment read from LDS feeds both tiles'
+    // products) while that still gives every wave of the grid a step; one
+    // tile a step below that (N = 256: 1024 two-tile steps for 2048 waves)
+    const bool one = ptiles / 2 < (int64_t)device_cus() * 8;
+    const int grid = (int)std::min<int64_t>(device_cus(), (ptiles / (one ? 1 : 2) + 3) / 4);
     StageTimer timer("trimul_prologue", st);
     const bool whole = r0 == 0 && nrows == Np && side_lo == 0 && side_hi == 2;
-    if (whole)
-      trimul_prologue_bf16_kernel<CZ, CH><<<grid, 512, 0, st>>>(
-          (const bf16*)z, mask, (bf16*)pa, (bf16*)pb, w, (int)N, Np, outgoing, eps_in, ptiles, 0,
-          Np, 0, 2, ps);
-    else
-      trimul_prologue_bf16_kernel<CZ, CH, false, true><<<grid, 512, 0, st>>>(
-          (const bf16*)z, mask, (bf16*)pa, (bf16*)pb, w, (int)N, Np, outgoing, eps_in, ptiles, r0,
-          nrows, side_lo, side_hi, ps);
+    auto go = [&](auto kern) {
+      kern<<<grid, 512, 0, st>>>((const bf16*)z, mask, (bf16*)pa, (bf16*)pb, w, (int)N, Np, outgoing,
+                                 eps_in, ptiles, r0, nrows, side_lo, side_hi, ps);
+    };
+    if (whole) {
+      if (one) go(trimul_prologue_bf16_kernel<CZ, CH, false, false, 1>);
+      else go(trimul_prologue_bf16_kernel<CZ, CH, false, false, 2>);
+    } else {
+      if (one) go(trimul_prologue_bf16_kernel<CZ, CH, false, true, 1>);
+      else go(trimul_prologue_bf16_kernel<CZ, CH, false, true, 2>);
+    }
   } else {
     StageTimer timer("trimul_prologue", st);
     trimul_prologue_kernel<T, CZ, CH><<<(unsigned)((ptiles + 3) / 4), 256, 0, st>>>(
