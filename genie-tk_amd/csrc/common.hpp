@@ -361,24 +361,6 @@ __device__ __forceinline__ void g2lds16(const void* gptr, void* lds_wave_base) {
       : "memory");
 }
 
-// g2lds16 for the last read of data (the non-temporal hint): the copy
-// streams through the caches with low retention, so it does not evict data
-// that later kernels read again.
-__device__ __forceinline__ void g2lds16_nt(const void* gptr, void* lds_wave_base) {
-  const uint32_t lds = __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(lds_void_ptr)lds_wave_base);
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %2\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, off nt\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(gptr), "s"(lds)
-      : "memory");
-}
-
 // LDS byte address of a __shared__ object, for the copies below.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_ptr)p);

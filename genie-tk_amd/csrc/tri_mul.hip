@@ -847,10 +847,7 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(
 // 3b. bf16 epilogue: persistent, 8 waves per CU with W_g and W_z resident in
 //     LDS.  Per 32-pair tile (row i, pairs jt*32 ..):
 //   * the x tile (c rows of 32 pairs, 64 B each) lands in the wave's own LDS
-//     buffer with direct global->LDS copies (non-temporal: this is the x
-//     planes' last read, and streaming it keeps z and the next planes in
-//     the caches; prologue and contraction 2 us faster each at N = 512),
-//     chunk-swizzled so the transposing
+//     buffer with direct global->LDS copies, chunk-swizzled so the transposing
 //     reads below are bank-conflict free, and is read back with
 //     ds_read_b64_tr_b16 straight into MFMA fragments (lane = pair, 8
 //     consecutive channels per fragment);
@@ -909,7 +906,7 @@ __global__ __launch_bounds__(512) void trimul_epilogue_bf16_kernel(
     for (int n = 0; n < CH / 16; ++n) {
       const int row = 16 * n + (lane >> 2);
       const int k = (lane & 3) ^ swz(row);
-      g2lds16_nt(src + row * plane + 8 * k, xw + n * 512);
+      g2lds16(src + row * plane + 8 * k, xw + n * 512);
     }
   };
   // Always KZ load instructions (an invalid pair reads pair j = 0; its
