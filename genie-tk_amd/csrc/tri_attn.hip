@@ -268,6 +268,11 @@ __global__ __launch_bounds__(256) void triattn_prologue_kernel(const T* __restri
 //        q, k  [B][Np r][H][32 d][Np j]    v^T [B][Np r][H][32 d][Np j] (vt_pos order)
 //        gate  [B][Np r][c_h][Np j]        bias [B][H][Np q][Np k]
 //     Padding values are those of triattn_prologue_kernel.
+//     The (row, head) tiles leave as device-scope (sc1) buffer stores of
+//     1 KiB runs (N = 256: 22.4 -> 20.0 us; no change at N = 512), and MODE
+//     15 unrolls its 16 projection steps so that the wait for the next
+//     tile's prefetched rows counts the stores behind them (73.5 -> 71.6 us
+//     at N = 512).
 // ---------------------------------------------------------------------------
 // MODE bit 0: q, k, v^T and gate; bit 1: the triangle bias; bit 2: the bias
 // in the flash kernel's fragment order without its per-head constant
@@ -374,8 +379,7 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
 
     // q, k, v, gate: one 32-channel tile (one head) per step, one MFMA chain
     // each; lane (i32, half) ends with positions j0 .. j0+15 of channel i32
-#pragma unroll 1
-    for (int step = 0; step < ((MODE & 1) ? 4 * H : 0); ++step) {
+    auto step_body = [&](const int step) {
       const int kind = step / H;  // 0 q, 1 k, 2 v, 3 gate
       const int h = step % H;
       const bf16* wt = wl + kind * PE;
@@ -399,12 +403,19 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
         if constexpr ((MODE & 8) != 0) dst = ws.gate + (rowbase * CH + h * HD) * (int64_t)Np + vt * 1024;
       } else {
         // q, k, v: zero outside the N x N pair grid; v^T in vt_pos order, which
-        // swaps bits 2 and 3 of the position inside its group of 16
+        // swaps bits 2 and 3 of the position inside its group of 16: packed
+        // in position order, that exchanges words 2-3 with words 4-5 (a
+        // select on the wave-uniform kind; permuting the accumulator index
+        // instead made every element an indexed register move)
 #pragma unroll
-        for (int m = 0; m < 16; m += 2) {
-          const int s0 = kind == 2 ? ((m & 3) | ((m & 4) << 1) | ((m & 8) >> 1)) : m;
-          const int s1 = s0 + 1;
-          pk[m / 2] = pack_bf16x2(s0 < nvalid ? acc[s0] + bc : 0.f, s1 < nvalid ? acc[s1] + bc : 0.f);
+        for (int m = 0; m < 16; m += 2)
+          pk[m / 2] = pack_bf16x2(m < nvalid ? acc[m] + bc : 0.f, m + 1 < nvalid ? acc[m + 1] + bc : 0.f);
+        if (kind == 2) {
+          const uint32_t w2 = pk[2], w3 = pk[3];
+          pk[2] = pk[4];
+          pk[3] = pk[5];
+          pk[4] = w2;
+          pk[5] = w3;
         }
         bf16* base = kind == 0 ? ws.q : kind == 1 ? ws.k : ws.vt;
         dst = base + ((rowbase * H + h) * HD + i32) * (int64_t)Np + j0;
@@ -426,12 +437,24 @@ __global__ __launch_bounds__(1024) void triattn_prologue_bf16_kernel(
           hi[d] = sw[1];
         }
         const int sl = 4 * (lane & 15) + 2 * half + ((lane >> 4) & 1);
-        o[sl] = make_uint4(lo[0], lo[1], lo[2], lo[3]);
-        o[64 + sl] = make_uint4(hi[0], hi[1], hi[2], hi[3]);
+        const auto trs = buf_rsrc(dst, 2048);
+        buf_store16_sc1(trs, (uint32_t)sl * 16, make_uint4(lo[0], lo[1], lo[2], lo[3]));
+        buf_store16_sc1(trs, (uint32_t)(64 + sl) * 16, make_uint4(hi[0], hi[1], hi[2], hi[3]));
       } else {
         o[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
         o[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
       }
+    };
+    // MODE 15 unrolls the steps (a constant trip count, 128 VGPRs): the
+    // compiler then counts the stores issued after the prefetched rows, so
+    // the next tile's wait for them does not wait for this tile's stores.
+    // The other modes would spill unrolled.
+    if constexpr (MODE == 15) {
+#pragma unroll
+      for (int step = 0; step < 4 * H; ++step) step_body(step);
+    } else {
+#pragma unroll 1
+      for (int step = 0; step < ((MODE & 1) ? 4 * H : 0); ++step) step_body(step);
     }
     // key-mask word and flags of (row r, key tile vt): bit j of the word is
     // key 32 vt + j (mask != 1); flags bit 0: some key below N without mask
