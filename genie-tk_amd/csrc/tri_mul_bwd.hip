@@ -354,6 +354,233 @@ __global__ __launch_bounds__(256) void trimul_bwd_prologue_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// 4b. bf16 prologue backward, one launch per side.  The kernel above reads
+//     every weight fragment of its matrix products from L2 (about 256 KiB a
+//     32-pair tile) at one wave per SIMD (over 400 registers), and waits on
+//     each.  Here each launch keeps one side's forward and transposed
+//     weights (4 x c x c_z bf16, 128 KiB at c_z = c = 128) in LDS, and the
+//     blocks are persistent, 8 waves (two a SIMD, at most 256 registers).  SIDE 0 (a) writes its share of dL/dzn as an
+//     fp32 partial in the accumulator layout ([tile][c_z / 32][4][64 lanes]
+//     x 4 floats, 1 KiB contiguous a store), with the output gate's share
+//     (dg_pre W_g, W_g^T from L2) added; SIDE 1 (b) adds its own share and
+//     runs the LayerNorm backward.
+// ---------------------------------------------------------------------------
+// one bf16 value through a buffer descriptor: byte offset = voff (per lane)
+// + soff (wave-uniform, a scalar operand); an offset past the descriptor's
+// range reads 0 / drops the store
+__device__ __forceinline__ float buf_load_bf16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const unsigned short v = __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+  return __uint_as_float((uint32_t)v << 16);
+}
+__device__ __forceinline__ void buf_store_bf16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float x) {
+  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, cvt<bf16>(x)), r, voff, soff, 0);
+}
+
+template <int CZ, int CH, int SIDE>
+__global__ __launch_bounds__(512) void trimul_bwd_prologue_side_kernel(
+    const bf16* __restrict__ z, const float* __restrict__ mask, const bf16* __restrict__ pd,
+    bf16* __restrict__ dz, bf16* __restrict__ cm_stack, bf16* __restrict__ cm_xi,
+    bf16* __restrict__ cm_dzn, TriMulPacked<bf16> w, const bf16* __restrict__ wt,
+    const bf16* __restrict__ wgt, float* __restrict__ part, int B, int N, int Np, int64_t pitch,
+    float eps_in, int64_t ntiles) {
+  constexpr int PW = CH * CZ;  // elements of one packed c_z x c weight
+  // [0] W_p, [1] W_g of this side (forward, the kernels' packing, folded as
+  // the forward's); [2] W_p^T, [3] W_g^T (raw, accumulator packing)
+  __shared__ __attribute__((aligned(1024))) bf16 wl[4][PW];
+  copy_to_lds_async(wl[0], SIDE ? w.w_bp : w.w_ap, PW * 2);
+  copy_to_lds_async(wl[1], SIDE ? w.w_bg : w.w_ag, PW * 2);
+  copy_to_lds_async(wl[2], wt + (int64_t)(2 * SIDE) * PW, PW * 2);
+  copy_to_lds_async(wl[3], wt + (int64_t)(2 * SIDE + 1) * PW, PW * 2);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  const int half = lane >> 5;
+  const int t32 = lane & 31;
+  const int jtiles = (N + 31) / 32;
+  const int64_t plane = (int64_t)Np * Np;
+  const float* bp = SIDE ? w.b_bp : w.b_ap;
+  const float* bg = SIDE ? w.b_bg : w.b_ag;
+  bf16* const cm_p = cm_stack + (int64_t)(2 * SIDE) * CH * pitch;
+  bf16* const cm_g = cm_stack + (int64_t)(2 * SIDE + 1) * CH * pitch;
+
+  for (int64_t tile = (int64_t)blockIdx.x * 8 + wave; tile < ntiles; tile += (int64_t)gridDim.x * 8) {
+    const int jt = (int)(tile % jtiles);
+    const int i = (int)((tile / jtiles) % N);
+    const int b = (int)(tile / ((int64_t)jtiles * N));
+    const int j = jt * 32 + t32;
+    const bool valid = j < N;
+    const int64_t pair = ((int64_t)b * N + i) * N + (valid ? j : 0);
+    const int oz = opaque_zero();
+
+    RowHalf<CZ> rh;
+    load_row_half<bf16, CZ>(rh, z + pair * CZ, valid);
+    const f32x2 st = row_stats<CZ>(rh, eps_in);
+    Frag<bf16> xf[CZ / 16];
+    if constexpr (trimul_folded<CZ, CH>()) ln_to_frags<bf16, CZ>(xf, rh, st);
+    else ln_affine_to_frags<bf16, CZ>(xf, rh, st, w.ln_in_w, w.ln_in_b);
+    const float m = valid ? (mask ? mask[pair] : 1.0f) : 0.0f;
+
+    // this tile's partial: [c_z / 32][4 groups][64 lanes] x f32x4
+    float* const pt = part + tile * (int64_t)(CZ * 64);
+    f32x16 dzn[CZ / 32];
+#pragma unroll
+    for (int nt = 0; nt < CZ / 32; ++nt) {
+      if constexpr (SIDE == 0) {
+        dzn[nt] = zero16();
+      } else {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 v = *reinterpret_cast<const f32x4*>(pt + ((nt * 4 + g) * 64 + lane) * 4);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dzn[nt][4 * g + r] = v[r];
+        }
+      }
+    }
+
+    // the dA / dB planes and the CM planes through descriptors whose bases
+    // are the tile's first pair (wave-uniform) and whose per-lane offsets are
+    // 32-bit (the host checks the ranges fit); lanes past N store nothing
+    const int64_t pair0 = ((int64_t)b * N + i) * N + jt * 32;
+    const auto srs = buf_rsrc(pd + (int64_t)b * CH * plane + (int64_t)i * Np + jt * 32,
+                              (uint32_t)(CH * plane * 2));
+    const auto prs = buf_rsrc(cm_p + pair0, (uint32_t)(CH * pitch * 2));
+    const auto grs = buf_rsrc(cm_g + pair0, (uint32_t)(CH * pitch * 2));
+    // per-lane byte offsets (channel 4*half, pair t32); the channel offsets
+    // of a (nt, g, r) are wave-uniform and go in the scalar operand
+    const uint32_t soff = (uint32_t)(4 * half * plane + t32) * 2;
+    const uint32_t coff = valid ? (uint32_t)(4 * half * pitch + t32) * 2 : kBufSkip;
+#pragma unroll 1
+    for (int nt = 0; nt < CH / 32; ++nt) {
+      // the forward's pre-activations of channels nt*32 .. +31 (lane = pair)
+      f32x16 pre = zero16(), u = zero16();
+#pragma unroll
+      for (int ks = 0; ks < CZ / 16; ++ks) {
+        Frag<bf16> wf;
+        load_wfrag_lds(wf, wl[0], nt, ks, CZ / 16);
+        mma(pre, wf, xf[ks]);
+        load_wfrag_lds(wf, wl[1], nt, ks, CZ / 16);
+        mma(u, wf, xf[ks]);
+      }
+      float d_p[16], d_g[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int c = nt * 32 + 8 * g + 4 * half + r;
+          // per-tile reads (opaque index): hoisted out of the tile loop,
+          // the 2 x 64 biases of a lane would stay in registers
+          const int cx = c + oz;
+          const float v = pre[4 * g + r] + bp[cx];
+          const float sv = gate_from_u(u[4 * g + r] + bg[cx]);
+          const float d = m * buf_load_bf16(srs, soff, (uint32_t)((nt * 32 + 8 * g + r) * plane) * 2);
+          d_p[4 * g + r] = d * sv;
+          d_g[4 * g + r] = d * v * sv * (1.f - sv);
+        }
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t so = (uint32_t)((nt * 32 + 8 * g + r) * pitch) * 2;
+          buf_store_bf16(prs, coff, so, d_p[4 * g + r]);
+          buf_store_bf16(grs, coff, so, d_g[4 * g + r]);
+        }
+      Frag<bf16> fp[2], fg[2];
+      vals_to_frags<bf16>(fp, d_p);
+      vals_to_frags<bf16>(fg, d_g);
+#pragma unroll
+      for (int nt2 = 0; nt2 < CZ / 32; ++nt2)
+#pragma unroll
+        for (int gp = 0; gp < 2; ++gp) {
+          Frag<bf16> wf;
+          load_wfrag_lds(wf, wl[2], nt2, 2 * nt + gp, CH / 16);
+          mma(dzn[nt2], wf, fp[gp]);
+          load_wfrag_lds(wf, wl[3], nt2, 2 * nt + gp, CH / 16);
+          mma(dzn[nt2], wf, fg[gp]);
+        }
+    }
+    // the output gate's share: dg_pre W_g (side a's launch)
+    if constexpr (SIDE == 0) {
+      const auto drs = buf_rsrc(cm_stack + (int64_t)4 * CH * pitch + pair0, (uint32_t)(CZ * pitch * 2));
+#pragma unroll 1
+      for (int nt = 0; nt < CZ / 32; ++nt) {
+        float d[16];
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            d[4 * g + r] = buf_load_bf16(drs, coff, (uint32_t)((nt * 32 + 8 * g + r) * pitch) * 2);
+        Frag<bf16> f[2];
+        vals_to_frags<bf16>(f, d);
+#pragma unroll
+        for (int nt2 = 0; nt2 < CZ / 32; ++nt2)
+#pragma unroll
+          for (int gp = 0; gp < 2; ++gp) {
+            Frag<bf16> wf;
+            load_wfrag<bf16>(wf, wgt, nt2, 2 * nt + gp, CZ / 16);
+            mma(dzn[nt2], wf, f[gp]);
+          }
+      }
+    }
+    if constexpr (SIDE == 0) {
+#pragma unroll
+      for (int nt = 0; nt < CZ / 32; ++nt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<f32x4*>(pt + ((nt * 4 + g) * 64 + lane) * 4) =
+              f32x4{dzn[nt][4 * g], dzn[nt][4 * g + 1], dzn[nt][4 * g + 2], dzn[nt][4 * g + 3]};
+      continue;
+    }
+    // LayerNorm backward in accumulator layout (x_hat recomputed from z)
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < CZ / 32; ++nt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c0 = nt * 32 + 8 * g + 4 * half;
+        const f32x4 z4 = valid ? load4f(z + pair * CZ + c0) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float xv = (z4[r] - st[0]) * st[1];
+          const float dxh = w.ln_in_w[c0 + r + oz] * dzn[nt][4 * g + r];
+          s1 += dxh;
+          s2 += dxh * xv;
+        }
+      }
+    s1 += xor32(s1);
+    s2 += xor32(s2);
+    const float m1 = s1 * (1.0f / CZ), m2 = s2 * (1.0f / CZ);
+    // the rows are read again below rather than kept (64 values a lane)
+    asm volatile("" ::: "memory");
+    const auto xrs = buf_rsrc(cm_xi + pair0, (uint32_t)(CZ * pitch * 2));
+    const auto nrs = buf_rsrc(cm_dzn + pair0, (uint32_t)(CZ * pitch * 2));
+    const auto zrs = buf_rsrc(dz + pair0 * CZ, (uint32_t)(32 * CZ * 2));
+    const uint32_t zoff = valid ? (uint32_t)(t32 * CZ) * 2 : kBufSkip;
+#pragma unroll
+    for (int nt = 0; nt < CZ / 32; ++nt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c0 = nt * 32 + 8 * g + 4 * half;
+        const f32x4 z4 = valid ? load4f(z + pair * CZ + c0) : f32x4{0.f, 0.f, 0.f, 0.f};
+        float o[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float xv = (z4[r] - st[0]) * st[1];
+          const float dxh = w.ln_in_w[c0 + r + oz] * dzn[nt][4 * g + r];
+          o[r] = st[1] * (dxh - m1 - xv * m2);
+          const uint32_t so = (uint32_t)((nt * 32 + 8 * g + r) * pitch) * 2;
+          buf_store_bf16(xrs, coff, so, xv);
+          buf_store_bf16(nrs, coff, so, dzn[nt][4 * g + r]);
+        }
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])}, zrs,
+                                              zoff + (uint32_t)c0 * 2, 0, 0);
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Workspace
 // ---------------------------------------------------------------------------
 template <typename T> struct TriMulBwdWs {
@@ -362,6 +589,7 @@ template <typename T> struct TriMulBwdWs {
   T *pa, *pb, *px, *pdx, *pat, *pbt, *pda, *pdb;
   T *cm_stack, *cm_dp, *cm_xi, *cm_xo, *cm_dzn, *cm_dxo;
   float *part1, *part2, *red, *sums_stack, *sums_dp, *sums_dzn, *dots_dzn, *sums_dxo, *dots_dxo;
+  float* part_dzn;  // bf16: side a's share of dL/dzn between the two prologue launches
   int64_t pitch;
 };
 
@@ -395,6 +623,8 @@ static TriMulBwdWs<T> carve_trimul_bwd(Carve& cv, int64_t B, int64_t N, int cz, 
   w.dots_dzn = cv.take<float>(cz);
   w.sums_dxo = cv.take<float>(c);
   w.dots_dxo = cv.take<float>(c);
+  w.part_dzn = nullptr;
+  if constexpr (sizeof(T) == 2) w.part_dzn = cv.take<float>(B * N * ((N + 31) / 32) * (int64_t)cz * 64);
   return w;
 }
 
@@ -450,9 +680,20 @@ static int bwd_trimul(const void* z, const float* mask, const void* dy,
   {
     const int64_t tiles = B * N * ((N + 31) / 32);
     StageTimer timer("trimul_bwd_prologue", st);
-    trimul_bwd_prologue_kernel<T, CZ, CH><<<(unsigned)((tiles + 3) / 4), 256, 0, st>>>(
-        (const T*)z, mask, a.pda, a.pdb, (T*)dz, a.cm_stack, a.cm_xi, a.cm_dzn, w, a.wt, a.wgt,
-        (int)B, (int)N, Np, pitch, eps_in);
+    if constexpr (sizeof(T) == 2) {
+      const int grid = (int)std::min<int64_t>(device_cus(), (tiles + 7) / 8);
+      trimul_bwd_prologue_side_kernel<CZ, CH, 0><<<grid, 512, 0, st>>>(
+          (const bf16*)z, mask, a.pda, (bf16*)dz, a.cm_stack, a.cm_xi, a.cm_dzn, w, a.wt, a.wgt,
+          a.part_dzn, (int)B, (int)N, Np, pitch, eps_in, tiles);
+      GTK_LAUNCH_CHECK();
+      trimul_bwd_prologue_side_kernel<CZ, CH, 1><<<grid, 512, 0, st>>>(
+          (const bf16*)z, mask, a.pdb, (bf16*)dz, a.cm_stack, a.cm_xi, a.cm_dzn, w, a.wt, a.wgt,
+          a.part_dzn, (int)B, (int)N, Np, pitch, eps_in, tiles);
+    } else {
+      trimul_bwd_prologue_kernel<T, CZ, CH><<<(unsigned)((tiles + 3) / 4), 256, 0, st>>>(
+          (const T*)z, mask, a.pda, a.pdb, (T*)dz, a.cm_stack, a.cm_xi, a.cm_dzn, w, a.wt, a.wgt,
+          (int)B, (int)N, Np, pitch, eps_in);
+    }
     GTK_LAUNCH_CHECK();
   }
   // 5. weight gradients
