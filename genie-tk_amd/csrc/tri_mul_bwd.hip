@@ -22,6 +22,7 @@
 //  5. weight gradients: two split-K products over the pairs, row sums for
 //     biases and LayerNorm parameters, folded back through gamma and beta.
 #include <algorithm>
+#include <type_traits>
 
 #include "capi_util.hpp"
 #include "common.hpp"
@@ -376,7 +377,76 @@ __device__ __forceinline__ void buf_store_bf16(__amdgpu_buffer_rsrc_t r, uint32_
   __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, cvt<bf16>(x)), r, voff, soff, 0);
 }
 
-template <int CZ, int CH, int SIDE>
+// Channel-major rows of a full 32-pair tile through a per-wave LDS tile of
+// 32 x 32 bf16 (rows of 72 bytes: the pad spreads both the row writes and the
+// transposing reads over the banks).  One 32-channel block then costs two
+// 16-byte loads or stores a lane instead of sixteen 2-byte ones.  For tiles
+// whose 32 pairs are all valid and whose rows start 16-byte aligned.
+constexpr int kCmRow = 36;
+constexpr int kCmTile = 32 * kCmRow;
+typedef uint32_t cm_u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t cm_u32x4 __attribute__((ext_vector_type(4)));
+
+// per-lane byte offsets of the 16-byte accesses: cm_store_tile's lane holds
+// pairs 8 * (L / 4) .. +7 of channel 4 * G + L % 4 (L = lane % 16,
+// G = lane / 16); cm_load_tile's lane reads pairs 8 * (lane % 4) .. +7 of
+// channel lane / 4 (and 16 + lane / 4)
+__device__ __forceinline__ uint32_t cm_store_voff(int64_t stride) {
+  const int lane = threadIdx.x & 63, L = lane & 15, G = lane >> 4;
+  return (uint32_t)((4 * G + (L & 3)) * stride + 8 * (L >> 2)) * 2;
+}
+__device__ __forceinline__ uint32_t cm_load_voff(int64_t stride) {
+  const int lane = threadIdx.x & 63;
+  return (uint32_t)((lane >> 2) * stride + 8 * (lane & 3)) * 2;
+}
+
+// accumulator values of a 32-channel block (value 4g + r: channel
+// 8g + 4 * half + r of pair lane % 32) -> the block's 32 rows at byte offset
+// soff (channel 0 of the block) + voff; rows are stride elements apart
+__device__ __forceinline__ void cm_store_tile(bf16* sw, const float* v, __amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                              uint32_t soff, int64_t stride) {
+  const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
+  const int L = lane & 15, G = lane >> 4;
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+    *reinterpret_cast<cm_u32x2*>(sw + t32 * kCmRow + 8 * g + 4 * half) =
+        cm_u32x2{pack_bf16x2(v[4 * g], v[4 * g + 1]), pack_bf16x2(v[4 * g + 2], v[4 * g + 3])};
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    // supplier L: pair row 8 * (L % 4) + 4e + L / 4, channels 16h + 4G .. +3
+    const s16x4 p0 = lds_read_tr16(sw + (8 * (L & 3) + (L >> 2)) * kCmRow + 16 * h + 4 * G);
+    const s16x4 p1 = lds_read_tr16(sw + (8 * (L & 3) + 4 + (L >> 2)) * kCmRow + 16 * h + 4 * G);
+    const cm_u32x4 q = __builtin_bit_cast(cm_u32x4, __builtin_shufflevector(p0, p1, 0, 1, 2, 3, 4, 5, 6, 7));
+    __builtin_amdgcn_raw_buffer_store_b128(q, r, voff, soff + (uint32_t)(16 * h * stride) * 2, 0);
+  }
+}
+
+// the 32 rows of a block at byte offset soff + voff -> accumulator values
+__device__ __forceinline__ void cm_load_tile(bf16* sw, float* v, __amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                             uint32_t soff, int64_t stride) {
+  const int lane = threadIdx.x & 63, half = lane >> 5;
+  const int L = lane & 15, G = lane >> 4;
+  const cm_u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  const cm_u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff + (uint32_t)(16 * stride) * 2, 0);
+  __builtin_amdgcn_wave_barrier();
+  bf16* const w0 = sw + (lane >> 2) * kCmRow + 8 * (lane & 3);
+  *reinterpret_cast<cm_u32x2*>(w0) = cm_u32x2{a[0], a[1]};
+  *reinterpret_cast<cm_u32x2*>(w0 + 4) = cm_u32x2{a[2], a[3]};
+  *reinterpret_cast<cm_u32x2*>(w0 + 16 * kCmRow) = cm_u32x2{b[0], b[1]};
+  *reinterpret_cast<cm_u32x2*>(w0 + 16 * kCmRow + 4) = cm_u32x2{b[2], b[3]};
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    // supplier L: channel row 8g + 4 * half + L / 4, pairs 16 * (G % 2) + 4 * (L % 4) .. +3
+    const s16x4 p = lds_read_tr16(sw + (8 * g + 4 * half + (L >> 2)) * kCmRow + 16 * (G & 1) + 4 * (L & 3));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[4 * g + k] = __uint_as_float((uint32_t)(unsigned short)p[k] << 16);
+  }
+}
+
+template <int CZ, int CH, int SIDE, bool FULL>
 __global__ __launch_bounds__(512) void trimul_bwd_prologue_side_kernel(
     const bf16* __restrict__ z, const float* __restrict__ mask, const bf16* __restrict__ pd,
     bf16* __restrict__ dz, bf16* __restrict__ cm_stack, bf16* __restrict__ cm_xi,
@@ -391,11 +461,15 @@ __global__ __launch_bounds__(512) void trimul_bwd_prologue_side_kernel(
   copy_to_lds_async(wl[1], SIDE ? w.w_bg : w.w_ag, PW * 2);
   copy_to_lds_async(wl[2], wt + (int64_t)(2 * SIDE) * PW, PW * 2);
   copy_to_lds_async(wl[3], wt + (int64_t)(2 * SIDE + 1) * PW, PW * 2);
+  // FULL (N % 32 == 0): every tile is 32 valid pairs on one row, and the
+  // channel-major blocks go through a per-wave LDS tile
+  __shared__ __attribute__((aligned(16))) bf16 cst[FULL ? 8 : 1][FULL ? kCmTile : 1];
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
+  bf16* const sw = cst[FULL ? wave : 0];
   const int half = lane >> 5;
   const int t32 = lane & 31;
   const int jtiles = (N + 31) / 32;
@@ -464,6 +538,8 @@ __global__ __launch_bounds__(512) void trimul_bwd_prologue_side_kernel(
         mma(u, wf, xf[ks]);
       }
       float d_p[16], d_g[16];
+      float dd[16];
+      if constexpr (FULL) cm_load_tile(sw, dd, srs, cm_load_voff(plane), (uint32_t)(nt * 32 * plane) * 2, plane);
 #pragma unroll
       for (int g = 0; g < 4; ++g)
 #pragma unroll
@@ -474,18 +550,25 @@ __global__ __launch_bounds__(512) void trimul_bwd_prologue_side_kernel(
           const int cx = c + oz;
           const float v = pre[4 * g + r] + bp[cx];
           const float sv = gate_from_u(u[4 * g + r] + bg[cx]);
-          const float d = m * buf_load_bf16(srs, soff, (uint32_t)((nt * 32 + 8 * g + r) * plane) * 2);
+          const float d = m * (FULL ? dd[4 * g + r]
+                                    : buf_load_bf16(srs, soff, (uint32_t)((nt * 32 + 8 * g + r) * plane) * 2));
           d_p[4 * g + r] = d * sv;
           d_g[4 * g + r] = d * v * sv * (1.f - sv);
         }
+      if constexpr (FULL) {
+        const uint32_t so = (uint32_t)(nt * 32 * pitch) * 2;
+        cm_store_tile(sw, d_p, prs, cm_store_voff(pitch), so, pitch);
+        cm_store_tile(sw, d_g, grs, cm_store_voff(pitch), so, pitch);
+      } else {
 #pragma unroll
-      for (int g = 0; g < 4; ++g)
+        for (int g = 0; g < 4; ++g)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t so = (uint32_t)((nt * 32 + 8 * g + r) * pitch) * 2;
-          buf_store_bf16(prs, coff, so, d_p[4 * g + r]);
-          buf_store_bf16(grs, coff, so, d_g[4 * g + r]);
-        }
+          for (int r = 0; r < 4; ++r) {
+            const uint32_t so = (uint32_t)((nt * 32 + 8 * g + r) * pitch) * 2;
+            buf_store_bf16(prs, coff, so, d_p[4 * g + r]);
+            buf_store_bf16(grs, coff, so, d_g[4 * g + r]);
+          }
+      }
       Frag<bf16> fp[2], fg[2];
       vals_to_frags<bf16>(fp, d_p);
       vals_to_frags<bf16>(fg, d_g);
@@ -506,11 +589,15 @@ __global__ __launch_bounds__(512) void trimul_bwd_prologue_side_kernel(
 #pragma unroll 1
       for (int nt = 0; nt < CZ / 32; ++nt) {
         float d[16];
+        if constexpr (FULL) {
+          cm_load_tile(sw, d, drs, cm_load_voff(pitch), (uint32_t)(nt * 32 * pitch) * 2, pitch);
+        } else {
 #pragma unroll
-        for (int g = 0; g < 4; ++g)
+          for (int g = 0; g < 4; ++g)
 #pragma unroll
-          for (int r = 0; r < 4; ++r)
-            d[4 * g + r] = buf_load_bf16(drs, coff, (uint32_t)((nt * 32 + 8 * g + r) * pitch) * 2);
+            for (int r = 0; r < 4; ++r)
+              d[4 * g + r] = buf_load_bf16(drs, coff, (uint32_t)((nt * 32 + 8 * g + r) * pitch) * 2);
+        }
         Frag<bf16> f[2];
         vals_to_frags<bf16>(f, d);
 #pragma unroll
@@ -558,7 +645,8 @@ __global__ __launch_bounds__(512) void trimul_bwd_prologue_side_kernel(
     const auto zrs = buf_rsrc(dz + pair0 * CZ, (uint32_t)(32 * CZ * 2));
     const uint32_t zoff = valid ? (uint32_t)(t32 * CZ) * 2 : kBufSkip;
 #pragma unroll
-    for (int nt = 0; nt < CZ / 32; ++nt)
+    for (int nt = 0; nt < CZ / 32; ++nt) {
+      float xs[16];
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int c0 = nt * 32 + 8 * g + 4 * half;
@@ -569,14 +657,25 @@ __global__ __launch_bounds__(512) void trimul_bwd_prologue_side_kernel(
           const float xv = (z4[r] - st[0]) * st[1];
           const float dxh = w.ln_in_w[c0 + r + oz] * dzn[nt][4 * g + r];
           o[r] = st[1] * (dxh - m1 - xv * m2);
-          const uint32_t so = (uint32_t)((nt * 32 + 8 * g + r) * pitch) * 2;
-          buf_store_bf16(xrs, coff, so, xv);
-          buf_store_bf16(nrs, coff, so, dzn[nt][4 * g + r]);
+          xs[4 * g + r] = xv;
+          if constexpr (!FULL) {
+            const uint32_t so = (uint32_t)((nt * 32 + 8 * g + r) * pitch) * 2;
+            buf_store_bf16(xrs, coff, so, xv);
+            buf_store_bf16(nrs, coff, so, dzn[nt][4 * g + r]);
+          }
         }
-        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-        __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])}, zrs,
+        __builtin_amdgcn_raw_buffer_store_b64(cm_u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])}, zrs,
                                               zoff + (uint32_t)c0 * 2, 0, 0);
       }
+      if constexpr (FULL) {
+        const uint32_t so = (uint32_t)(nt * 32 * pitch) * 2;
+        float dn[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) dn[k] = dzn[nt][k];
+        cm_store_tile(sw, xs, xrs, cm_store_voff(pitch), so, pitch);
+        cm_store_tile(sw, dn, nrs, cm_store_voff(pitch), so, pitch);
+      }
+    }
   }
 }
 
@@ -682,13 +781,20 @@ static int bwd_trimul(const void* z, const float* mask, const void* dy,
     StageTimer timer("trimul_bwd_prologue", st);
     if constexpr (sizeof(T) == 2) {
       const int grid = (int)std::min<int64_t>(device_cus(), (tiles + 7) / 8);
-      trimul_bwd_prologue_side_kernel<CZ, CH, 0><<<grid, 512, 0, st>>>(
-          (const bf16*)z, mask, a.pda, (bf16*)dz, a.cm_stack, a.cm_xi, a.cm_dzn, w, a.wt, a.wgt,
-          a.part_dzn, (int)B, (int)N, Np, pitch, eps_in, tiles);
-      GTK_LAUNCH_CHECK();
-      trimul_bwd_prologue_side_kernel<CZ, CH, 1><<<grid, 512, 0, st>>>(
-          (const bf16*)z, mask, a.pdb, (bf16*)dz, a.cm_stack, a.cm_xi, a.cm_dzn, w, a.wt, a.wgt,
-          a.part_dzn, (int)B, (int)N, Np, pitch, eps_in, tiles);
+      auto side = [&](auto full) -> int {
+        constexpr bool F = decltype(full)::value;
+        trimul_bwd_prologue_side_kernel<CZ, CH, 0, F><<<grid, 512, 0, st>>>(
+            (const bf16*)z, mask, a.pda, (bf16*)dz, a.cm_stack, a.cm_xi, a.cm_dzn, w, a.wt, a.wgt,
+            a.part_dzn, (int)B, (int)N, Np, pitch, eps_in, tiles);
+        GTK_LAUNCH_CHECK();
+        trimul_bwd_prologue_side_kernel<CZ, CH, 1, F><<<grid, 512, 0, st>>>(
+            (const bf16*)z, mask, a.pdb, (bf16*)dz, a.cm_stack, a.cm_xi, a.cm_dzn, w, a.wt, a.wgt,
+            a.part_dzn, (int)B, (int)N, Np, pitch, eps_in, tiles);
+        GTK_LAUNCH_CHECK();
+        return 0;
+      };
+      // whole 32-pair tiles on one row: the staged channel-major path
+      if ((rc = N % 32 == 0 ? side(std::true_type{}) : side(std::false_type{}))) return rc;
     } else {
       trimul_bwd_prologue_kernel<T, CZ, CH><<<(unsigned)((tiles + 3) / 4), 256, 0, st>>>(
           (const T*)z, mask, a.pda, a.pdb, (T*)dz, a.cm_stack, a.cm_xi, a.cm_dzn, w, a.wt, a.wgt,

@@ -202,13 +202,14 @@ def test_tri_attn_backward_other_shapes(dname, starting, cin, ch, heads):
 @pytest.mark.parametrize("dname", ["fp32", "bf16"])
 @pytest.mark.parametrize("outgoing", [True, False])
 @pytest.mark.parametrize("cz,c,N", [(64, 32, 40), (32, 32, 37), (64, 64, 33), (32, 128, 24),
-                                    (32, 16, 16), (64, 8, 30)])
+                                    (32, 16, 16), (64, 8, 30), (64, 32, 32), (32, 64, 64)])
 def test_tri_mul_backward_other_shapes(dname, outgoing, cz, c, N):
     """The backward kernels of c_z in {32, 64} and c in {32, 64, 128} (the
     reference tests' c_z = 64, c = 32, tests/test_triangle_mul.py:37), whose
     forward packing leaves the LayerNorm affine to the kernels; and c = 16
     (the reference's gradient test, c_z = 32, N = 16, :73) and 8, which run
-    as 32 repeated channels."""
+    as 32 repeated channels.  N = 32 and 64 take the whole-tile path of the
+    bf16 prologue backward (channel-major blocks staged through LDS)."""
     log(f"tri_mul backward {dname} outgoing={outgoing} c_z={cz} c={c} N={N}")
     dt = DT[dname]
     P = H.draw_params(H.tri_mul_shapes(cz, c), seed=N + c + cz, ln_random=True, bias_random=True)
