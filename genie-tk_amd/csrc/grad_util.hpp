@@ -404,28 +404,49 @@ inline int launch_wgrad_finish(const float* part, int M, int Nn, int64_t pitch, 
 // ---------------------------------------------------------------------------
 constexpr int kRowSegs = 8;
 
-template <typename T>
+template <typename T, bool DOT>
 __global__ __launch_bounds__(256) void rowred_kernel(const T* __restrict__ G, const T* __restrict__ X,
                                                      int64_t pitch, int64_t P, float* __restrict__ psum,
                                                      float* __restrict__ pdot) {
   __shared__ float red[2][4];
+  constexpr int STEP = 8 * 256;  // entries a block reads per pass
   const int r = blockIdx.x / kRowSegs, s = blockIdx.x % kRowSegs;
   const int64_t seg = ((P + kRowSegs - 1) / kRowSegs + 7) / 8 * 8;
   const int64_t b0 = s * seg;
   const int64_t b1 = b0 + seg < P ? b0 + seg : P;
+  const int64_t full = b0 + (b1 > b0 ? (b1 - b0) / 8 * 8 : 0);  // end of the whole 8-entry chunks
   const T* g = G + (int64_t)r * pitch;
-  const T* x = X ? X + (int64_t)r * pitch : nullptr;
+  const T* x = DOT ? X + (int64_t)r * pitch : nullptr;
   float a = 0.f, d = 0.f;
-  for (int64_t p = b0 + 8 * threadIdx.x; p < b1; p += 8 * 256) {
+  int64_t p = b0 + 8 * threadIdx.x;
+  // four independent 16-byte loads in flight a thread (one at a time leaves
+  // the reduction bound by load latency at well under the HBM rate)
+  for (; p + 3 * STEP < full; p += 4 * STEP) {
+    Frag<T> fg[4], fx[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      fg[u].load(g + p + u * STEP);
+      if constexpr (DOT) fx[u].load(x + p + u * STEP);
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float v = fg[u].get(e);
+        a += v;
+        if constexpr (DOT) d += v * fx[u].get(e);
+      }
+  }
+  for (; p < b1; p += STEP) {
     Frag<T> fg, fx;
-    fg.load(g + p);  // the row extends to pitch >= P rounded to 8; tail entries are zero
-    if (x) fx.load(x + p);
+    fg.load(g + p);  // the row extends to pitch >= P rounded to 8
+    if constexpr (DOT) fx.load(x + p);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const bool in = p + e < b1;
       const float v = in ? fg.get(e) : 0.f;
       a += v;
-      if (x) d += v * (in ? fx.get(e) : 0.f);
+      if constexpr (DOT) d += v * (in ? fx.get(e) : 0.f);
     }
   }
 #pragma unroll
@@ -441,7 +462,7 @@ __global__ __launch_bounds__(256) void rowred_kernel(const T* __restrict__ G, co
   __syncthreads();
   if (threadIdx.x == 0) {
     psum[(int64_t)r * kRowSegs + s] = red[0][0] + red[0][1] + red[0][2] + red[0][3];
-    if (pdot) pdot[(int64_t)r * kRowSegs + s] = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    if (DOT) pdot[(int64_t)r * kRowSegs + s] = red[1][0] + red[1][1] + red[1][2] + red[1][3];
   }
 }
 
@@ -460,7 +481,8 @@ inline int launch_rowred(const T* G, const T* X, int rows, int64_t pitch, int64_
   if (rows == 0) return GTK_OK;
   float* ps = tmp;
   float* pd = tmp + (size_t)rows * kRowSegs;
-  rowred_kernel<T><<<rows * kRowSegs, 256, 0, st>>>(G, X, pitch, P, ps, X ? pd : nullptr);
+  if (X) rowred_kernel<T, true><<<rows * kRowSegs, 256, 0, st>>>(G, X, pitch, P, ps, pd);
+  else rowred_kernel<T, false><<<rows * kRowSegs, 256, 0, st>>>(G, nullptr, pitch, P, ps, nullptr);
   GTK_LAUNCH_CHECK();
   rowred_finish_kernel<<<(rows + 255) / 256, 256, 0, st>>>(ps, rows, sums);
   GTK_LAUNCH_CHECK();

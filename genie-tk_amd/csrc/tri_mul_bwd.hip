@@ -32,20 +32,107 @@
 
 namespace gtk {
 
+// one bf16 value through a buffer descriptor: byte offset = voff (per lane)
+// + soff (wave-uniform, a scalar operand); an offset past the descriptor's
+// range reads 0 / drops the store
+__device__ __forceinline__ float buf_load_bf16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  const unsigned short v = __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+  return __uint_as_float((uint32_t)v << 16);
+}
+__device__ __forceinline__ void buf_store_bf16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float x) {
+  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, cvt<bf16>(x)), r, voff, soff, 0);
+}
+
+// Channel-major rows of a full 32-pair tile through a per-wave LDS tile of
+// 32 x 32 bf16 (rows of 72 bytes: the pad spreads both the row writes and the
+// transposing reads over the banks).  One 32-channel block then costs two
+// 16-byte loads or stores a lane instead of sixteen 2-byte ones.  For tiles
+// whose 32 pairs are all valid and whose rows start 16-byte aligned.
+constexpr int kCmRow = 36;
+constexpr int kCmTile = 32 * kCmRow;
+typedef uint32_t cm_u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t cm_u32x4 __attribute__((ext_vector_type(4)));
+
+// per-lane byte offsets of the 16-byte accesses: cm_store_tile's lane holds
+// pairs 8 * (L / 4) .. +7 of channel 4 * G + L % 4 (L = lane % 16,
+// G = lane / 16); cm_load_tile's lane reads pairs 8 * (lane % 4) .. +7 of
+// channel lane / 4 (and 16 + lane / 4)
+__device__ __forceinline__ uint32_t cm_store_voff(int64_t stride) {
+  const int lane = threadIdx.x & 63, L = lane & 15, G = lane >> 4;
+  return (uint32_t)((4 * G + (L & 3)) * stride + 8 * (L >> 2)) * 2;
+}
+__device__ __forceinline__ uint32_t cm_load_voff(int64_t stride) {
+  const int lane = threadIdx.x & 63;
+  return (uint32_t)((lane >> 2) * stride + 8 * (lane & 3)) * 2;
+}
+
+// accumulator values of a 32-channel block (value 4g + r: channel
+// 8g + 4 * half + r of pair lane % 32) -> the block's 32 rows at byte offset
+// soff (channel 0 of the block) + voff; rows are stride elements apart
+__device__ __forceinline__ void cm_store_tile(bf16* sw, const float* v, __amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                              uint32_t soff, int64_t stride) {
+  const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
+  const int L = lane & 15, G = lane >> 4;
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+    *reinterpret_cast<cm_u32x2*>(sw + t32 * kCmRow + 8 * g + 4 * half) =
+        cm_u32x2{pack_bf16x2(v[4 * g], v[4 * g + 1]), pack_bf16x2(v[4 * g + 2], v[4 * g + 3])};
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    // supplier L: pair row 8 * (L % 4) + 4e + L / 4, channels 16h + 4G .. +3
+    const s16x4 p0 = lds_read_tr16(sw + (8 * (L & 3) + (L >> 2)) * kCmRow + 16 * h + 4 * G);
+    const s16x4 p1 = lds_read_tr16(sw + (8 * (L & 3) + 4 + (L >> 2)) * kCmRow + 16 * h + 4 * G);
+    const cm_u32x4 q = __builtin_bit_cast(cm_u32x4, __builtin_shufflevector(p0, p1, 0, 1, 2, 3, 4, 5, 6, 7));
+    __builtin_amdgcn_raw_buffer_store_b128(q, r, voff, soff + (uint32_t)(16 * h * stride) * 2, 0);
+  }
+}
+
+// the 32 rows of a block at byte offset soff + voff -> accumulator values
+__device__ __forceinline__ void cm_load_tile(bf16* sw, float* v, __amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                             uint32_t soff, int64_t stride) {
+  const int lane = threadIdx.x & 63, half = lane >> 5;
+  const int L = lane & 15, G = lane >> 4;
+  const cm_u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  const cm_u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff + (uint32_t)(16 * stride) * 2, 0);
+  __builtin_amdgcn_wave_barrier();
+  bf16* const w0 = sw + (lane >> 2) * kCmRow + 8 * (lane & 3);
+  *reinterpret_cast<cm_u32x2*>(w0) = cm_u32x2{a[0], a[1]};
+  *reinterpret_cast<cm_u32x2*>(w0 + 4) = cm_u32x2{a[2], a[3]};
+  *reinterpret_cast<cm_u32x2*>(w0 + 16 * kCmRow) = cm_u32x2{b[0], b[1]};
+  *reinterpret_cast<cm_u32x2*>(w0 + 16 * kCmRow + 4) = cm_u32x2{b[2], b[3]};
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    // supplier L: channel row 8g + 4 * half + L / 4, pairs 16 * (G % 2) + 4 * (L % 4) .. +3
+    const s16x4 p = lds_read_tr16(sw + (8 * g + 4 * half + (L >> 2)) * kCmRow + 16 * (G & 1) + 4 * (L & 3));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[4 * g + k] = __uint_as_float((uint32_t)(unsigned short)p[k] << 16);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // 2. Epilogue backward.  Tiles cover all Np x Np plane positions so that the
 //    padding of the dX planes is written as zero.
 // ---------------------------------------------------------------------------
-template <typename T, int CZ, int CH>
+template <typename T, int CZ, int CH, bool FULL = false>
 __global__ __launch_bounds__(256) void trimul_bwd_epilogue_kernel(
     const T* __restrict__ z, const T* __restrict__ px, const T* __restrict__ dy,
     T* __restrict__ pdx, T* __restrict__ cm_dp, T* __restrict__ cm_dg, T* __restrict__ cm_xo,
     T* __restrict__ cm_dxo, TriMulPacked<T> w, const T* __restrict__ wzt, int B, int N, int Np,
     int64_t pitch, float eps_in, float eps_out) {
   constexpr int XPITCH = CH + 8;
+  // bf16: the dX planes' 32-channel blocks go through a per-wave LDS tile,
+  // and for FULL (N % 32 == 0: every tile is 32 valid pairs on one row) the
+  // channel-major blocks too
+  constexpr bool STG = sizeof(T) == 2;
+  static_assert(STG || !FULL, "staged stores are bf16");
   __shared__ __attribute__((aligned(16))) T xs[4][32 * XPITCH];
+  __shared__ __attribute__((aligned(16))) bf16 cst[STG ? 4 : 1][STG ? kCmTile : 1];
   const int lane = threadIdx.x & 63;
   const int wave = wave_id();
+  bf16* const sw = cst[STG ? wave : 0];
   const int half = lane >> 5;
   const int t32 = lane & 31;
   const int jtiles = Np / 32;
@@ -63,6 +150,7 @@ __global__ __launch_bounds__(256) void trimul_bwd_epilogue_kernel(
   }
   const bool valid = j < N;
   const int64_t pair = ((int64_t)b * N + i) * N + (valid ? j : 0);
+  const int64_t pair0 = ((int64_t)b * N + i) * N + jt * 32;
 
   // gate s = sigmoid(LN_in(z) W_g^T + b_g), accumulator layout
   f32x16 sg[CZ / 32];
@@ -138,7 +226,11 @@ __global__ __launch_bounds__(256) void trimul_bwd_epilogue_kernel(
         dgv[4 * g + r] = d4[r] * pv * sv * (1.f - sv);
       }
     }
-    if (valid) {
+    if constexpr (FULL) {
+      const uint32_t so = (uint32_t)(nt * 32 * pitch) * 2;
+      cm_store_tile(sw, dpv, buf_rsrc(cm_dp + pair0, (uint32_t)(CZ * pitch * 2)), cm_store_voff(pitch), so, pitch);
+      cm_store_tile(sw, dgv, buf_rsrc(cm_dg + pair0, (uint32_t)(CZ * pitch * 2)), cm_store_voff(pitch), so, pitch);
+    } else if (valid) {
 #pragma unroll
       for (int g = 0; g < 4; ++g)
 #pragma unroll
@@ -183,7 +275,8 @@ __global__ __launch_bounds__(256) void trimul_bwd_epilogue_kernel(
   s2 += xor32(s2);
   const float m1 = s1 * (1.0f / CH), m2 = s2 * (1.0f / CH);
 #pragma unroll
-  for (int nt = 0; nt < CH / 32; ++nt)
+  for (int nt = 0; nt < CH / 32; ++nt) {
+    float xv[16], dv[16];
 #pragma unroll
     for (int g = 0; g < 4; ++g)
 #pragma unroll
@@ -192,12 +285,31 @@ __global__ __launch_bounds__(256) void trimul_bwd_epilogue_kernel(
         const float xhat = (to_f32(sr[c]) - so[0]) * so[1];
         const float dxh = w.ln_out_w[c] * dxn[nt][4 * g + r];
         const float dxv = so[1] * (dxh - m1 - xhat * m2);
-        dxo[(int64_t)c * plane] = cvt<T>(valid ? dxv : 0.f);
-        if (valid) {
-          cm_xo[(int64_t)c * pitch + pair] = cvt<T>(xhat);
-          cm_dxo[(int64_t)c * pitch + pair] = cvt<T>(dxn[nt][4 * g + r]);
+        xv[4 * g + r] = xhat;
+        dv[4 * g + r] = valid ? dxv : 0.f;
+        if constexpr (!STG) dxo[(int64_t)c * plane] = cvt<T>(dv[4 * g + r]);
+        if constexpr (!FULL) {
+          if (valid) {
+            cm_xo[(int64_t)c * pitch + pair] = cvt<T>(xhat);
+            cm_dxo[(int64_t)c * pitch + pair] = cvt<T>(dxn[nt][4 * g + r]);
+          }
         }
       }
+    if constexpr (STG) {
+      // the tile's 32 plane positions, padding included (written as zero)
+      const T* const d0 = pdx + (int64_t)b * CH * plane + (int64_t)i * Np + jt * 32;
+      cm_store_tile(sw, dv, buf_rsrc(d0, (uint32_t)(CH * plane * 2)), cm_store_voff(plane),
+                    (uint32_t)(nt * 32 * plane) * 2, plane);
+    }
+    if constexpr (FULL) {
+      const uint32_t so2 = (uint32_t)(nt * 32 * pitch) * 2;
+      float dn[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) dn[k] = dxn[nt][k];
+      cm_store_tile(sw, xv, buf_rsrc(cm_xo + pair0, (uint32_t)(CH * pitch * 2)), cm_store_voff(pitch), so2, pitch);
+      cm_store_tile(sw, dn, buf_rsrc(cm_dxo + pair0, (uint32_t)(CH * pitch * 2)), cm_store_voff(pitch), so2, pitch);
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -366,86 +478,6 @@ __global__ __launch_bounds__(256) void trimul_bwd_prologue_kernel(
 //     (dg_pre W_g, W_g^T from L2) added; SIDE 1 (b) adds its own share and
 //     runs the LayerNorm backward.
 // ---------------------------------------------------------------------------
-// one bf16 value through a buffer descriptor: byte offset = voff (per lane)
-// + soff (wave-uniform, a scalar operand); an offset past the descriptor's
-// range reads 0 / drops the store
-__device__ __forceinline__ float buf_load_bf16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  const unsigned short v = __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
-  return __uint_as_float((uint32_t)v << 16);
-}
-__device__ __forceinline__ void buf_store_bf16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float x) {
-  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, cvt<bf16>(x)), r, voff, soff, 0);
-}
-
-// Channel-major rows of a full 32-pair tile through a per-wave LDS tile of
-// 32 x 32 bf16 (rows of 72 bytes: the pad spreads both the row writes and the
-// transposing reads over the banks).  One 32-channel block then costs two
-// 16-byte loads or stores a lane instead of sixteen 2-byte ones.  For tiles
-// whose 32 pairs are all valid and whose rows start 16-byte aligned.
-constexpr int kCmRow = 36;
-constexpr int kCmTile = 32 * kCmRow;
-typedef uint32_t cm_u32x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t cm_u32x4 __attribute__((ext_vector_type(4)));
-
-// per-lane byte offsets of the 16-byte accesses: cm_store_tile's lane holds
-// pairs 8 * (L / 4) .. +7 of channel 4 * G + L % 4 (L = lane % 16,
-// G = lane / 16); cm_load_tile's lane reads pairs 8 * (lane % 4) .. +7 of
-// channel lane / 4 (and 16 + lane / 4)
-__device__ __forceinline__ uint32_t cm_store_voff(int64_t stride) {
-  const int lane = threadIdx.x & 63, L = lane & 15, G = lane >> 4;
-  return (uint32_t)((4 * G + (L & 3)) * stride + 8 * (L >> 2)) * 2;
-}
-__device__ __forceinline__ uint32_t cm_load_voff(int64_t stride) {
-  const int lane = threadIdx.x & 63;
-  return (uint32_t)((lane >> 2) * stride + 8 * (lane & 3)) * 2;
-}
-
-// accumulator values of a 32-channel block (value 4g + r: channel
-// 8g + 4 * half + r of pair lane % 32) -> the block's 32 rows at byte offset
-// soff (channel 0 of the block) + voff; rows are stride elements apart
-__device__ __forceinline__ void cm_store_tile(bf16* sw, const float* v, __amdgpu_buffer_rsrc_t r, uint32_t voff,
-                                              uint32_t soff, int64_t stride) {
-  const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
-  const int L = lane & 15, G = lane >> 4;
-  __builtin_amdgcn_wave_barrier();
-#pragma unroll
-  for (int g = 0; g < 4; ++g)
-    *reinterpret_cast<cm_u32x2*>(sw + t32 * kCmRow + 8 * g + 4 * half) =
-        cm_u32x2{pack_bf16x2(v[4 * g], v[4 * g + 1]), pack_bf16x2(v[4 * g + 2], v[4 * g + 3])};
-  __builtin_amdgcn_wave_barrier();
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    // supplier L: pair row 8 * (L % 4) + 4e + L / 4, channels 16h + 4G .. +3
-    const s16x4 p0 = lds_read_tr16(sw + (8 * (L & 3) + (L >> 2)) * kCmRow + 16 * h + 4 * G);
-    const s16x4 p1 = lds_read_tr16(sw + (8 * (L & 3) + 4 + (L >> 2)) * kCmRow + 16 * h + 4 * G);
-    const cm_u32x4 q = __builtin_bit_cast(cm_u32x4, __builtin_shufflevector(p0, p1, 0, 1, 2, 3, 4, 5, 6, 7));
-    __builtin_amdgcn_raw_buffer_store_b128(q, r, voff, soff + (uint32_t)(16 * h * stride) * 2, 0);
-  }
-}
-
-// the 32 rows of a block at byte offset soff + voff -> accumulator values
-__device__ __forceinline__ void cm_load_tile(bf16* sw, float* v, __amdgpu_buffer_rsrc_t r, uint32_t voff,
-                                             uint32_t soff, int64_t stride) {
-  const int lane = threadIdx.x & 63, half = lane >> 5;
-  const int L = lane & 15, G = lane >> 4;
-  const cm_u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-  const cm_u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff + (uint32_t)(16 * stride) * 2, 0);
-  __builtin_amdgcn_wave_barrier();
-  bf16* const w0 = sw + (lane >> 2) * kCmRow + 8 * (lane & 3);
-  *reinterpret_cast<cm_u32x2*>(w0) = cm_u32x2{a[0], a[1]};
-  *reinterpret_cast<cm_u32x2*>(w0 + 4) = cm_u32x2{a[2], a[3]};
-  *reinterpret_cast<cm_u32x2*>(w0 + 16 * kCmRow) = cm_u32x2{b[0], b[1]};
-  *reinterpret_cast<cm_u32x2*>(w0 + 16 * kCmRow + 4) = cm_u32x2{b[2], b[3]};
-  __builtin_amdgcn_wave_barrier();
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    // supplier L: channel row 8g + 4 * half + L / 4, pairs 16 * (G % 2) + 4 * (L % 4) .. +3
-    const s16x4 p = lds_read_tr16(sw + (8 * g + 4 * half + (L >> 2)) * kCmRow + 16 * (G & 1) + 4 * (L & 3));
-#pragma unroll
-    for (int k = 0; k < 4; ++k) v[4 * g + k] = __uint_as_float((uint32_t)(unsigned short)p[k] << 16);
-  }
-}
-
 template <int CZ, int CH, int SIDE, bool FULL>
 __global__ __launch_bounds__(512) void trimul_bwd_prologue_side_kernel(
     const bf16* __restrict__ z, const float* __restrict__ mask, const bf16* __restrict__ pd,
@@ -758,9 +790,13 @@ static int bwd_trimul(const void* z, const float* mask, const void* dy,
   {
     const int64_t tiles = B * (int64_t)Np * (Np / 32);
     StageTimer timer("trimul_bwd_epilogue", st);
-    trimul_bwd_epilogue_kernel<T, CZ, CH><<<(unsigned)((tiles + 3) / 4), 256, 0, st>>>(
-        (const T*)z, a.px, (const T*)dy, a.pdx, a.cm_dp, a.cm_stack + (int64_t)4 * CH * pitch,
-        a.cm_xo, a.cm_dxo, w, a.wzt, (int)B, (int)N, Np, pitch, eps_in, eps_out);
+    auto epi = [&](auto full) {
+      trimul_bwd_epilogue_kernel<T, CZ, CH, decltype(full)::value><<<(unsigned)((tiles + 3) / 4), 256, 0, st>>>(
+          (const T*)z, a.px, (const T*)dy, a.pdx, a.cm_dp, a.cm_stack + (int64_t)4 * CH * pitch,
+          a.cm_xo, a.cm_dxo, w, a.wzt, (int)B, (int)N, Np, pitch, eps_in, eps_out);
+    };
+    if (sizeof(T) == 2 && N % 32 == 0) epi(std::integral_constant<bool, sizeof(T) == 2>{});
+    else epi(std::false_type{});
     GTK_LAUNCH_CHECK();
   }
   // 3. contraction backward (px is free from here on: it takes dX^T)
