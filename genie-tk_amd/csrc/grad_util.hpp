@@ -12,6 +12,8 @@
 //     LayerNorm affine is folded into the packed forward weights, so the
 //     kernels hold x_hat, not the LayerNorm output).
 #pragma once
+#include <type_traits>
+
 #include "capi_util.hpp"
 #include "common.hpp"
 #include "pack.hpp"
@@ -217,11 +219,15 @@ inline int launch_zero_tail(T* base, int64_t rows, int64_t pitch, int64_t P, hip
 // output tile, 4 waves of 64 x TN/2, k staged through LDS in 128-byte rows
 // with double buffering (the contraction kernel's scheme).  Chunk s covers
 // p in [s*kc, min((s+1)*kc, pitch)), kc a multiple of 64.
+// RS: also rs[s][m] = sum_{p in chunk s} G[m][p] (the bias gradients), summed
+// from the staged G chunks by the blocks of the first n tile; this replaces a
+// separate pass over G.
 // ---------------------------------------------------------------------------
-template <typename T, int TN>
+template <typename T, int TN, bool RS = false>
 __global__ __launch_bounds__(256) void wgrad_kernel(const T* __restrict__ G, const T* __restrict__ X,
                                                     float* __restrict__ part, int M, int Nn,
-                                                    int64_t pitch, int64_t kc, int nsplit) {
+                                                    int64_t pitch, int64_t kc, int nsplit,
+                                                    float* __restrict__ rs) {
   constexpr int BK = 128 / sizeof(T);
   constexpr int PITCH = 144;
   constexpr int ROWS = 128 + TN;
@@ -249,6 +255,9 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const T* __restrict__ G, con
     for (int y = 0; y < MBN; ++y) acc[x][y] = zero16();
 
   f32x4 rr[CPT];
+  // G rows tid/8 + 32u (u < 4) of this thread's chunks: their partial sums
+  float rsum[4] = {0.f, 0.f, 0.f, 0.f};
+  const bool do_rs = RS && ntl == 0;
   auto gload = [&](int64_t k0) {
 #pragma unroll
     for (int u = 0; u < CPT; ++u) {
@@ -264,6 +273,14 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const T* __restrict__ G, con
       const int id = tid + 256 * u;
       const int row = id >> 3, cc = id & 7;
       *reinterpret_cast<f32x4*>(&smem[buf][row * PITCH + cc * 16]) = rr[u];
+    }
+    if (do_rs) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const T* e = reinterpret_cast<const T*>(&rr[u]);
+#pragma unroll
+        for (int k = 0; k < EPC; ++k) rsum[u] += to_f32(e[k]);
+      }
     }
   };
   if (kbeg < kend) {
@@ -293,6 +310,17 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const T* __restrict__ G, con
     if (more) sstore(cur ^ 1);
     __syncthreads();
     cur ^= 1;
+  }
+  if (do_rs) {
+    // the 8 threads of a row (tid % 8) are 8 consecutive lanes
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float v = rsum[u];
+      v += __shfl_xor(v, 1, 64);
+      v += __shfl_xor(v, 2, 64);
+      v += __shfl_xor(v, 4, 64);
+      if ((tid & 7) == 0) rs[(int64_t)s * M + m0 + (tid >> 3) + 32 * u] = v;
+    }
   }
   // acc[x][y]: lane holds W[m = m0 + wm + 32x + (l&31)][n = n0 + wn + 32y + 8g + 4h + r]
   float* out = part + (int64_t)s * M * Nn;
@@ -339,24 +367,9 @@ inline WgradPlan wgrad_plan(int M, int64_t pitch) {
 inline size_t wgrad_part_floats(int M, int Nn, int64_t pitch) {
   return (size_t)wgrad_plan(M, pitch).nsplit * wgrad_m_rows(M) * wgrad_n_rows(Nn);
 }
-
-// part[s][m][n] (m < wgrad_m_rows(M), n < wgrad_n_rows(Nn)): split s of
-// sum_k G[m][k] X[n][k]
-template <typename T>
-inline int launch_wgrad(const T* G, const T* X, float* part, int M, int Nn, int64_t pitch,
-                        hipStream_t st) {
-  GTK_REQUIRE(M >= 1 && Nn >= 1, GTK_EUNSUPPORTED, "weight gradient shape %d x %d unsupported", M, Nn);
-  const int Mp = wgrad_m_rows(M), Np = wgrad_n_rows(Nn);
-  const WgradPlan pl = wgrad_plan(M, pitch);
-  if (Np % 128 == 0) {
-    const int64_t blocks = (int64_t)pl.nsplit * (Mp / 128) * (Np / 128);
-    wgrad_kernel<T, 128><<<(unsigned)blocks, 256, 0, st>>>(G, X, part, Mp, Np, pitch, pl.kc, pl.nsplit);
-  } else {
-    const int64_t blocks = (int64_t)pl.nsplit * (Mp / 128);
-    wgrad_kernel<T, 64><<<(unsigned)blocks, 256, 0, st>>>(G, X, part, Mp, Np, pitch, pl.kc, pl.nsplit);
-  }
-  GTK_LAUNCH_CHECK();
-  return GTK_OK;
+// floats of the row-sum partials rs[nsplit][wgrad_m_rows(M)]
+inline size_t wgrad_rowsum_floats(int M, int64_t pitch) {
+  return (size_t)wgrad_plan(M, pitch).nsplit * wgrad_m_rows(M);
 }
 
 // dst[(m - m0)][n] = sum_s part[s][m][n] * (gamma ? gamma[n] : 1)
@@ -386,6 +399,41 @@ static __global__ __launch_bounds__(256) void wgrad_finish_kernel(
   dst[idx] = acc;
 }
 
+// part[s][m][n] (m < wgrad_m_rows(M), n < wgrad_n_rows(Nn)): split s of
+// sum_k G[m][k] X[n][k].  With rs and sums: also sums[m] = sum_k G[m][k] for
+// m < M (rs: wgrad_rowsum_floats(M, pitch) floats of partials).
+template <typename T>
+inline int launch_wgrad(const T* G, const T* X, float* part, int M, int Nn, int64_t pitch,
+                        hipStream_t st, float* rs = nullptr, float* sums = nullptr) {
+  GTK_REQUIRE(M >= 1 && Nn >= 1, GTK_EUNSUPPORTED, "weight gradient shape %d x %d unsupported", M, Nn);
+  const int Mp = wgrad_m_rows(M), Np = wgrad_n_rows(Nn);
+  const WgradPlan pl = wgrad_plan(M, pitch);
+  const bool with_rs = rs && sums;
+  auto go = [&](auto tn, auto r) {
+    constexpr int TN = decltype(tn)::value;
+    const int64_t blocks = (int64_t)pl.nsplit * (Mp / 128) * (TN == 128 ? Np / 128 : 1);
+    wgrad_kernel<T, TN, decltype(r)::value><<<(unsigned)blocks, 256, 0, st>>>(G, X, part, Mp, Np, pitch,
+                                                                             pl.kc, pl.nsplit, rs);
+  };
+  using I128 = std::integral_constant<int, 128>;
+  using I64 = std::integral_constant<int, 64>;
+  if (Np % 128 == 0) {
+    if (with_rs) go(I128{}, std::true_type{});
+    else go(I128{}, std::false_type{});
+  } else {
+    if (with_rs) go(I64{}, std::true_type{});
+    else go(I64{}, std::false_type{});
+  }
+  GTK_LAUNCH_CHECK();
+  if (with_rs) {
+    // rs is a product output of one column: the same split reduction
+    wgrad_finish_kernel<<<(M + 31) / 32, 256, 0, st>>>(rs, pl.nsplit, Mp, 1, 1, 0, M, nullptr, nullptr,
+                                                       nullptr, sums);
+    GTK_LAUNCH_CHECK();
+  }
+  return GTK_OK;
+}
+
 inline int launch_wgrad_finish(const float* part, int M, int Nn, int64_t pitch, int m0, int rows,
                                const float* rowsum, const float* gamma, const float* beta,
                                float* dst, hipStream_t st) {
@@ -406,12 +454,13 @@ constexpr int kRowSegs = 8;
 
 template <typename T, bool DOT>
 __global__ __launch_bounds__(256) void rowred_kernel(const T* __restrict__ G, const T* __restrict__ X,
-                                                     int64_t pitch, int64_t P, float* __restrict__ psum,
-                                                     float* __restrict__ pdot) {
+                                                     int rows, int64_t pitch, int64_t P,
+                                                     float* __restrict__ psum, float* __restrict__ pdot) {
   __shared__ float red[2][4];
   constexpr int STEP = 8 * 256;  // entries a block reads per pass
-  const int r = blockIdx.x / kRowSegs, s = blockIdx.x % kRowSegs;
-  const int64_t seg = ((P + kRowSegs - 1) / kRowSegs + 7) / 8 * 8;
+  const int nseg = (int)(gridDim.x / rows);
+  const int r = blockIdx.x / nseg, s = blockIdx.x % nseg;
+  const int64_t seg = ((P + nseg - 1) / nseg + 7) / 8 * 8;
   const int64_t b0 = s * seg;
   const int64_t b1 = b0 + seg < P ? b0 + seg : P;
   const int64_t full = b0 + (b1 > b0 ? (b1 - b0) / 8 * 8 : 0);  // end of the whole 8-entry chunks
@@ -461,35 +510,43 @@ __global__ __launch_bounds__(256) void rowred_kernel(const T* __restrict__ G, co
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    psum[(int64_t)r * kRowSegs + s] = red[0][0] + red[0][1] + red[0][2] + red[0][3];
-    if (DOT) pdot[(int64_t)r * kRowSegs + s] = red[1][0] + red[1][1] + red[1][2] + red[1][3];
+    psum[(int64_t)r * nseg + s] = red[0][0] + red[0][1] + red[0][2] + red[0][3];
+    if (DOT) pdot[(int64_t)r * nseg + s] = red[1][0] + red[1][1] + red[1][2] + red[1][3];
   }
 }
 
-static __global__ void rowred_finish_kernel(const float* __restrict__ part, int rows, float* __restrict__ dst) {
+static __global__ void rowred_finish_kernel(const float* __restrict__ ps, const float* __restrict__ pd, int rows,
+                                            int nseg, float* __restrict__ sums, float* __restrict__ dots) {
   const int r = blockIdx.x * blockDim.x + threadIdx.x;
   if (r >= rows) return;
-  float a = 0.f;
-  for (int s = 0; s < kRowSegs; ++s) a += part[(int64_t)r * kRowSegs + s];
-  dst[r] = a;
+  float a = 0.f, d = 0.f;
+  for (int s = 0; s < nseg; ++s) {
+    a += ps[(int64_t)r * nseg + s];
+    if (dots) d += pd[(int64_t)r * nseg + s];
+  }
+  sums[r] = a;
+  if (dots) dots[r] = d;
 }
 
-// sums[r] (and dots[r] when X is given) for rows [0, rows) of G.
+// Segments a row is split into: kRowSegs, or more for few rows (so that the
+// launch still has about 1024 blocks); rows x segments <= max(8 rows, 1024),
+// which bounds the partials in tmp (2 x that many floats).
+inline int rowred_segs(int rows) { return rows >= 128 ? kRowSegs : 1024 / rows; }
+
+// sums[r] (and dots[r] when X is given) for rows [0, rows) of G; tmp holds
+// 2 * rows * rowred_segs(rows) floats of partials.
 template <typename T>
 inline int launch_rowred(const T* G, const T* X, int rows, int64_t pitch, int64_t P, float* tmp,
                          float* sums, float* dots, hipStream_t st) {
   if (rows == 0) return GTK_OK;
+  const int nseg = rowred_segs(rows);
   float* ps = tmp;
-  float* pd = tmp + (size_t)rows * kRowSegs;
-  if (X) rowred_kernel<T, true><<<rows * kRowSegs, 256, 0, st>>>(G, X, pitch, P, ps, pd);
-  else rowred_kernel<T, false><<<rows * kRowSegs, 256, 0, st>>>(G, nullptr, pitch, P, ps, nullptr);
+  float* pd = tmp + (size_t)rows * nseg;
+  if (X) rowred_kernel<T, true><<<rows * nseg, 256, 0, st>>>(G, X, rows, pitch, P, ps, pd);
+  else rowred_kernel<T, false><<<rows * nseg, 256, 0, st>>>(G, nullptr, rows, pitch, P, ps, nullptr);
   GTK_LAUNCH_CHECK();
-  rowred_finish_kernel<<<(rows + 255) / 256, 256, 0, st>>>(ps, rows, sums);
+  rowred_finish_kernel<<<(rows + 255) / 256, 256, 0, st>>>(ps, pd, rows, nseg, sums, X ? dots : nullptr);
   GTK_LAUNCH_CHECK();
-  if (X && dots) {
-    rowred_finish_kernel<<<(rows + 255) / 256, 256, 0, st>>>(pd, rows, dots);
-    GTK_LAUNCH_CHECK();
-  }
   return GTK_OK;
 }
 
@@ -500,6 +557,34 @@ static __global__ void copy_f32_kernel(float* __restrict__ dst, const float* __r
 inline int launch_copy_f32(float* dst, const float* src, int n, hipStream_t st) {
   if (!dst || n == 0) return GTK_OK;
   copy_f32_kernel<<<(n + 255) / 256, 256, 0, st>>>(dst, src, n);
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+// Several small fp32 copies in one launch (block y = copy k).
+struct CopyList {
+  static constexpr int kMax = 8;
+  float* dst[kMax];
+  const float* src[kMax];
+  int n[kMax];
+  int count = 0;
+  void add(float* d, const float* s, int len) {
+    if (!d || len == 0) return;
+    dst[count] = d;
+    src[count] = s;
+    n[count] = len;
+    ++count;
+  }
+};
+static __global__ void copy_list_kernel(CopyList l) {
+  const int k = blockIdx.y;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < l.n[k]; i += gridDim.x * blockDim.x)
+    l.dst[k][i] = l.src[k][i];
+}
+inline int launch_copy_list(const CopyList& l, hipStream_t st) {
+  if (l.count == 0) return GTK_OK;
+  GTK_REQUIRE(l.count <= CopyList::kMax, GTK_EINVAL, "copy list overflow");
+  copy_list_kernel<<<dim3(1, l.count), 256, 0, st>>>(l);
   GTK_LAUNCH_CHECK();
   return GTK_OK;
 }

@@ -484,7 +484,7 @@ static int launch_pt_generic(const void* p, const float* mask, void* out, const 
 template <typename T> struct PtBwdWs {
   void* packed;
   T *w2t, *w1t, *cm_xh, *cm_dxn, *cm_dy, *cm_a, *cm_dh;
-  float *part1, *part2, *red, *sums_dh, *sums_dy, *sums_dxn, *dots_dxn;
+  float *part1, *part2, *red, *rs, *sums_dh, *sums_dy, *sums_dxn, *dots_dxn;
   int64_t pitch;
 };
 
@@ -505,6 +505,7 @@ static PtBwdWs<T> carve_pt_bwd(Carve& cv, int64_t rows, int c, int hid) {
   a.part1 = cv.take<float>(wgrad_part_floats(hid, c, a.pitch));
   a.part2 = cv.take<float>(wgrad_part_floats(hid, c, a.pitch));
   a.red = cv.take<float>((int64_t)2 * hid * kRowSegs);
+  a.rs = cv.take<float>(wgrad_rowsum_floats(hid, a.pitch));
   a.sums_dh = cv.take<float>(hid);
   a.sums_dy = cv.take<float>(c);
   a.sums_dxn = cv.take<float>(c);
@@ -541,13 +542,17 @@ static int bwd_pt(const void* p, const void* dy, const gtk_pair_transition_weigh
   const int prow[5] = {C, C, C, HID, HID};
   for (int k = 0; k < 5; ++k)
     if ((rc = launch_zero_tail<T>(planes[k], prow[k], pitch, rows, st))) return rc;
-  if ((rc = launch_rowred<T>(a.cm_dh, nullptr, HID, pitch, rows, a.red, a.sums_dh, nullptr, st))) return rc;
-  if ((rc = launch_rowred<T>(a.cm_dy, nullptr, C, pitch, rows, a.red, a.sums_dy, nullptr, st))) return rc;
-  if ((rc = launch_rowred<T>(a.cm_dxn, a.cm_xh, C, pitch, rows, a.red, a.sums_dxn, a.dots_dxn, st)))
+  // bias and LayerNorm gradients straight into the outputs where requested
+  auto or_tmp = [](float* dst, float* tmp) { return dst ? dst : tmp; };
+  if ((rc = launch_rowred<T>(a.cm_dy, nullptr, C, pitch, rows, a.red, or_tmp(gr->b2, a.sums_dy), nullptr, st)))
+    return rc;
+  if ((rc = launch_rowred<T>(a.cm_dxn, a.cm_xh, C, pitch, rows, a.red, or_tmp(gr->ln_b, a.sums_dxn),
+                             or_tmp(gr->ln_w, a.dots_dxn), st)))
     return rc;
   {
+    // the first product also sums its G rows (dh): the b1 gradient
     StageTimer timer("pair_transition_bwd_wgrad", st);
-    if ((rc = launch_wgrad<T>(a.cm_dh, a.cm_xh, a.part1, HID, C, pitch, st))) return rc;
+    if ((rc = launch_wgrad<T>(a.cm_dh, a.cm_xh, a.part1, HID, C, pitch, st, a.rs, a.sums_dh))) return rc;
     if ((rc = launch_wgrad<T>(a.cm_a, a.cm_dy, a.part2, HID, C, pitch, st))) return rc;
   }
   // dW1 = (sum dh x_hat^T) diag(g) + (sum dh) beta^T
@@ -558,10 +563,7 @@ static int bwd_pt(const void* p, const void* dy, const gtk_pair_transition_weigh
                                                                  HID, C, gr->w2);
     GTK_LAUNCH_CHECK();
   }
-  if ((rc = launch_copy_f32(gr->b1, a.sums_dh, HID, st))) return rc;
-  if ((rc = launch_copy_f32(gr->b2, a.sums_dy, C, st))) return rc;
-  if ((rc = launch_copy_f32(gr->ln_w, a.dots_dxn, C, st))) return rc;
-  return launch_copy_f32(gr->ln_b, a.sums_dxn, C, st);
+  return launch_copy_f32(gr->b1, a.sums_dh, HID, st);
 }
 
 }  // namespace gtk

@@ -1332,7 +1332,7 @@ __global__ __launch_bounds__(256) void attn_dwb_finish_kernel(const float* __res
 template <typename T> struct AttnBwdWs {
   AttnBwdW<T> w;
   AttnBwdBufs<T> b;
-  float *part1, *part2, *part3, *red, *sums_stack, *sums_dy, *sums_dxn, *dots_dxn, *sums_dtri;
+  float *part1, *part2, *part3, *red, *rs, *sums_stack, *sums_dy, *sums_dxn, *dots_dxn, *sums_dtri;
 };
 
 template <typename T>
@@ -1385,6 +1385,7 @@ static AttnBwdWs<T> carve_attn_bwd(Carve& cv, int64_t B, int64_t N, int C, int H
   a.part2 = cv.take<float>(wgrad_part_floats(C, CH, b.pitch));
   a.part3 = cv.take<float>(wgrad_part_floats(C, 64, b.pitch));
   a.red = cv.take<float>((int64_t)2 * 4 * CH * kRowSegs);
+  a.rs = cv.take<float>(std::max(wgrad_rowsum_floats(4 * CH, b.pitch), wgrad_rowsum_floats(C, b.pitch)));
   a.sums_stack = cv.take<float>(4 * CH);
   a.sums_dy = cv.take<float>(C);
   a.sums_dxn = cv.take<float>(C);
@@ -1536,14 +1537,18 @@ static int bwd_triattn(const void* x, const float* mask, const void* dy,
   if ((rc = launch_zero_tail<T>(b.cm_dy, C, pitch, P, st))) return rc;
   if ((rc = launch_zero_tail<T>(b.cm_go, CH, pitch, P, st))) return rc;
   if ((rc = launch_zero_tail<T>(b.cm_dtri, H, pitch, P, st))) return rc;
-  if ((rc = launch_rowred<T>(b.cm_stack, nullptr, 4 * CH, pitch, P, a.red, a.sums_stack, nullptr, st))) return rc;
-  if ((rc = launch_rowred<T>(b.cm_dy, nullptr, C, pitch, P, a.red, a.sums_dy, nullptr, st))) return rc;
-  if ((rc = launch_rowred<T>(b.cm_dxn, b.cm_xh, C, pitch, P, a.red, a.sums_dxn, a.dots_dxn, st))) return rc;
+  // LayerNorm parameter gradients straight into the outputs where requested
+  auto or_tmp = [](float* dst, float* tmp) { return dst ? dst : tmp; };
+  if ((rc = launch_rowred<T>(b.cm_dxn, b.cm_xh, C, pitch, P, a.red, or_tmp(gr->ln_b, a.sums_dxn),
+                             or_tmp(gr->ln_w, a.dots_dxn), st)))
+    return rc;
   if ((rc = launch_rowred<T>(b.cm_dtri, nullptr, H, pitch, P, a.red, a.sums_dtri, nullptr, st))) return rc;
+  // the weight-gradient products also sum their G rows: the bias gradients
   {
     StageTimer timer("triattn_bwd_wgrad", st);
-    if ((rc = launch_wgrad<T>(b.cm_stack, b.cm_xh, a.part1, 4 * CH, C, pitch, st))) return rc;
-    if ((rc = launch_wgrad<T>(b.cm_dy, b.cm_go, a.part2, C, CH, pitch, st))) return rc;
+    if ((rc = launch_wgrad<T>(b.cm_stack, b.cm_xh, a.part1, 4 * CH, C, pitch, st, a.rs, a.sums_stack))) return rc;
+    if ((rc = launch_wgrad<T>(b.cm_dy, b.cm_go, a.part2, C, CH, pitch, st, a.rs, or_tmp(gr->o_b, a.sums_dy))))
+      return rc;
     if ((rc = launch_wgrad<T>(b.cm_xh, b.cm_dtri, a.part3, C, 64, pitch, st))) return rc;
   }
   float* wdst[4] = {gr->q_w, gr->k_w, gr->v_w, gr->g_w};
@@ -1554,12 +1559,9 @@ static int bwd_triattn(const void* x, const float* mask, const void* dy,
   if ((rc = launch_copy_f32(gr->g_b, a.sums_stack + 3 * CH, CH, st))) return rc;
   if ((rc = launch_wgrad_finish(a.part2, C, CH, pitch, 0, C, nullptr, nullptr, nullptr, gr->o_w, st)))
     return rc;
-  if ((rc = launch_copy_f32(gr->o_b, a.sums_dy, C, st))) return rc;
   attn_dwb_finish_kernel<<<(H * C + 31) / 32, 256, 0, st>>>(
       a.part3, wgrad_plan(C, pitch).nsplit, C, wgrad_m_rows(C), H, a.w.ln_w, a.w.ln_b, a.sums_dtri, gr->tri_w);
   GTK_LAUNCH_CHECK();
-  if ((rc = launch_copy_f32(gr->ln_w, a.dots_dxn, C, st))) return rc;
-  if ((rc = launch_copy_f32(gr->ln_b, a.sums_dxn, C, st))) return rc;
   return GTK_OK;
 }
 

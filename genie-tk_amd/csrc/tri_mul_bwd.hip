@@ -719,7 +719,7 @@ template <typename T> struct TriMulBwdWs {
   T *wzt, *wt, *wgt;
   T *pa, *pb, *px, *pdx, *pat, *pbt, *pda, *pdb;
   T *cm_stack, *cm_dp, *cm_xi, *cm_xo, *cm_dzn, *cm_dxo;
-  float *part1, *part2, *red, *sums_stack, *sums_dp, *sums_dzn, *dots_dzn, *sums_dxo, *dots_dxo;
+  float *part1, *part2, *red, *rs, *sums_stack, *sums_dp, *sums_dzn, *dots_dzn, *sums_dxo, *dots_dxo;
   float* part_dzn;  // bf16: side a's share of dL/dzn between the two prologue launches
   int64_t pitch;
 };
@@ -748,6 +748,7 @@ static TriMulBwdWs<T> carve_trimul_bwd(Carve& cv, int64_t B, int64_t N, int cz, 
   w.part1 = cv.take<float>(wgrad_part_floats(M1, cz, w.pitch));
   w.part2 = cv.take<float>(wgrad_part_floats(cz, c, w.pitch));
   w.red = cv.take<float>((int64_t)2 * M1 * kRowSegs);
+  w.rs = cv.take<float>(std::max(wgrad_rowsum_floats(M1, w.pitch), wgrad_rowsum_floats(cz, w.pitch)));
   w.sums_stack = cv.take<float>(M1);
   w.sums_dp = cv.take<float>(cz);
   w.sums_dzn = cv.take<float>(cz);
@@ -843,32 +844,35 @@ static int bwd_trimul(const void* z, const float* mask, const void* dy,
   if ((rc = launch_zero_tail<T>(a.cm_dp, CZ, pitch, P, st))) return rc;
   if ((rc = launch_zero_tail<T>(a.cm_xi, CZ, pitch, P, st))) return rc;
   if ((rc = launch_zero_tail<T>(a.cm_xo, CH, pitch, P, st))) return rc;
-  if ((rc = launch_rowred<T>(a.cm_stack, nullptr, M1, pitch, P, a.red, a.sums_stack, nullptr, st))) return rc;
-  if ((rc = launch_rowred<T>(a.cm_dp, nullptr, CZ, pitch, P, a.red, a.sums_dp, nullptr, st))) return rc;
-  if ((rc = launch_rowred<T>(a.cm_dzn, a.cm_xi, CZ, pitch, P, a.red, a.sums_dzn, a.dots_dzn, st))) return rc;
-  if ((rc = launch_rowred<T>(a.cm_dxo, a.cm_xo, CH, pitch, P, a.red, a.sums_dxo, a.dots_dxo, st))) return rc;
+  // LayerNorm parameter gradients straight into the outputs where requested
+  auto or_tmp = [](float* dst, float* tmp) { return dst ? dst : tmp; };
+  if ((rc = launch_rowred<T>(a.cm_dzn, a.cm_xi, CZ, pitch, P, a.red, or_tmp(gr->ln_in_b, a.sums_dzn),
+                             or_tmp(gr->ln_in_w, a.dots_dzn), st)))
+    return rc;
+  if ((rc = launch_rowred<T>(a.cm_dxo, a.cm_xo, CH, pitch, P, a.red, or_tmp(gr->ln_out_b, a.sums_dxo),
+                             or_tmp(gr->ln_out_w, a.dots_dxo), st)))
+    return rc;
+  // the weight-gradient products also sum their G rows: the bias gradients
+  float* const sums_dp = or_tmp(gr->z_b, a.sums_dp);
   {
     StageTimer timer("trimul_bwd_wgrad", st);
-    if ((rc = launch_wgrad<T>(a.cm_stack, a.cm_xi, a.part1, M1, CZ, pitch, st))) return rc;
-    if ((rc = launch_wgrad<T>(a.cm_dp, a.cm_xo, a.part2, CZ, CH, pitch, st))) return rc;
+    if ((rc = launch_wgrad<T>(a.cm_stack, a.cm_xi, a.part1, M1, CZ, pitch, st, a.rs, a.sums_stack))) return rc;
+    if ((rc = launch_wgrad<T>(a.cm_dp, a.cm_xo, a.part2, CZ, CH, pitch, st, a.rs, sums_dp))) return rc;
   }
   float* wdst[5] = {gr->a_p_w, gr->a_g_w, gr->b_p_w, gr->b_g_w, gr->g_w};
   float* bdst[5] = {gr->a_p_b, gr->a_g_b, gr->b_p_b, gr->b_g_b, gr->g_b};
+  CopyList biases;
   for (int k = 0; k < 5; ++k) {
     const int m0 = k * CH, rows = k < 4 ? CH : CZ;
     if ((rc = launch_wgrad_finish(a.part1, M1, CZ, pitch, m0, rows, a.sums_stack, w.ln_in_w,
                                   w.ln_in_b, wdst[k], st)))
       return rc;
-    if ((rc = launch_copy_f32(bdst[k], a.sums_stack + m0, rows, st))) return rc;
+    biases.add(bdst[k], a.sums_stack + m0, rows);
   }
-  if ((rc = launch_wgrad_finish(a.part2, CZ, CH, pitch, 0, CZ, a.sums_dp, w.ln_out_w, w.ln_out_b,
+  if ((rc = launch_copy_list(biases, st))) return rc;
+  if ((rc = launch_wgrad_finish(a.part2, CZ, CH, pitch, 0, CZ, sums_dp, w.ln_out_w, w.ln_out_b,
                                 gr->z_w, st)))
     return rc;
-  if ((rc = launch_copy_f32(gr->z_b, a.sums_dp, CZ, st))) return rc;
-  if ((rc = launch_copy_f32(gr->ln_in_w, a.dots_dzn, CZ, st))) return rc;
-  if ((rc = launch_copy_f32(gr->ln_in_b, a.sums_dzn, CZ, st))) return rc;
-  if ((rc = launch_copy_f32(gr->ln_out_w, a.dots_dxo, CH, st))) return rc;
-  if ((rc = launch_copy_f32(gr->ln_out_b, a.sums_dxo, CH, st))) return rc;
   return GTK_OK;
 }
 
