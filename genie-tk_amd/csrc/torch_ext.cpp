@@ -208,6 +208,30 @@ int common_param_dtype(std::vector<at::Tensor>& ps) {
 
 const void* ptr_or_null(const at::Tensor& t) { return t.defined() ? t.data_ptr() : nullptr; }
 
+// Parameter gradients as views of one fp32 buffer, each starting 16-byte
+// aligned (one allocation; the caller casts them with one conversion of the
+// buffer, which follows the views in out).
+void flat_grads(std::vector<at::Tensor>& out, const at::Tensor& like,
+                const std::vector<std::vector<int64_t>>& shapes, float** const* gs) {
+  auto numel = [](const std::vector<int64_t>& s) {
+    int64_t n = 1;
+    for (auto d : s) n *= d;
+    return n;
+  };
+  int64_t total = 0;
+  for (auto& s : shapes) total += (numel(s) + 3) / 4 * 4;
+  auto flat = at::empty({total}, like.options().dtype(at::kFloat));
+  int64_t o = 0;
+  for (size_t i = 0; i < shapes.size(); ++i) {
+    const int64_t n = numel(shapes[i]);
+    auto t = flat.narrow(0, o, n).view(shapes[i]);
+    *gs[i] = t.data_ptr<float>();
+    out.push_back(t);
+    o += (n + 3) / 4 * 4;
+  }
+  out.push_back(flat);
+}
+
 // params: ln_in_w, ln_in_b, a_p_w, a_p_b, a_g_w, a_g_b, b_p_w, b_p_b, b_g_w, b_g_b,
 //         g_w, g_b, ln_out_w, ln_out_b, z_w, z_b
 at::Tensor tri_mul_pack(std::vector<at::Tensor> ps, int64_t c_z, int64_t c, bool fp32) {
@@ -230,7 +254,8 @@ at::Tensor tri_mul_pack(std::vector<at::Tensor> ps, int64_t c_z, int64_t c, bool
 }
 
 // Backward of tri_mul_forward (update only): returns [dz, then the gradients of
-// the 16 parameters in tri_mul_pack's order, fp32].
+// the 16 parameters in tri_mul_pack's order (fp32 views of one buffer), then
+// that buffer].
 std::vector<at::Tensor> tri_mul_backward(const at::Tensor& z, const c10::optional<at::Tensor>& mask,
                                          const at::Tensor& dy, std::vector<at::Tensor> ps,
                                          int64_t c_z, int64_t c, bool outgoing, double eps_in,
@@ -269,15 +294,10 @@ std::vector<at::Tensor> tri_mul_backward(const at::Tensor& z, const c10::optiona
   float** gs[16] = {&g.ln_in_w, &g.ln_in_b, &g.a_p_w, &g.a_p_b, &g.a_g_w, &g.a_g_b, &g.b_p_w,
                     &g.b_p_b,   &g.b_g_w,   &g.b_g_b, &g.g_w,   &g.g_b,   &g.ln_out_w,
                     &g.ln_out_b, &g.z_w,    &g.z_b};
-  const int64_t shapes[16][2] = {{c_z, 1}, {c_z, 1}, {c, c_z}, {c, 1}, {c, c_z}, {c, 1},
-                                 {c, c_z}, {c, 1},   {c, c_z}, {c, 1}, {c_z, c_z}, {c_z, 1},
-                                 {c, 1},   {c, 1},   {c_z, c}, {c_z, 1}};
-  for (int i = 0; i < 16; ++i) {
-    auto t = shapes[i][1] == 1 ? at::empty({shapes[i][0]}, zc.options().dtype(at::kFloat))
-                               : at::empty({shapes[i][0], shapes[i][1]}, zc.options().dtype(at::kFloat));
-    *gs[i] = t.data_ptr<float>();
-    out.push_back(t);
-  }
+  flat_grads(out, zc,
+             {{c_z}, {c_z}, {c, c_z}, {c}, {c, c_z}, {c}, {c, c_z}, {c}, {c, c_z}, {c}, {c_z, c_z}, {c_z},
+              {c}, {c}, {c_z, c}, {c_z}},
+             gs);
   const size_t bytes = gtk_tri_mul_backward_workspace_size(B, N, c_z, c, dt);
   TORCH_CHECK(bytes > 0, "genie_tk._C: tri_mul backward shape c_z=", c_z, " c=", c, " unsupported");
   auto ws = workspace(zc, bytes);
@@ -289,7 +309,8 @@ std::vector<at::Tensor> tri_mul_backward(const at::Tensor& z, const c10::optiona
 }
 
 // Backward of tri_attn_forward (update only): returns [dx, then the gradients of
-// the 10 parameters in tri_attn_pack's order, fp32].
+// the 10 parameters in tri_attn_pack's order (fp32 views of one buffer), then
+// that buffer].
 std::vector<at::Tensor> tri_attn_backward(const at::Tensor& x, const c10::optional<at::Tensor>& mask,
                                           const at::Tensor& dy, std::vector<at::Tensor> ps,
                                           int64_t c_in, int64_t c_h, int64_t H, bool starting,
@@ -321,14 +342,10 @@ std::vector<at::Tensor> tri_attn_backward(const at::Tensor& x, const c10::option
   out.push_back(at::empty_like(xc));
   gtk_tri_attn_grads g;
   float** gs[10] = {&g.ln_w, &g.ln_b, &g.tri_w, &g.q_w, &g.k_w, &g.v_w, &g.g_w, &g.g_b, &g.o_w, &g.o_b};
-  const int64_t shapes[10][2] = {{c_in, 1}, {c_in, 1}, {H, c_in}, {c_h, c_in}, {c_h, c_in},
-                                 {c_h, c_in}, {c_h, c_in}, {c_h, 1}, {c_in, c_h}, {c_in, 1}};
-  for (int i = 0; i < 10; ++i) {
-    auto t = shapes[i][1] == 1 ? at::empty({shapes[i][0]}, xc.options().dtype(at::kFloat))
-                               : at::empty({shapes[i][0], shapes[i][1]}, xc.options().dtype(at::kFloat));
-    *gs[i] = t.data_ptr<float>();
-    out.push_back(t);
-  }
+  flat_grads(out, xc,
+             {{c_in}, {c_in}, {H, c_in}, {c_h, c_in}, {c_h, c_in}, {c_h, c_in}, {c_h, c_in}, {c_h},
+              {c_in, c_h}, {c_in}},
+             gs);
   const size_t bytes = gtk_tri_attn_backward_workspace_size(B, N, c_in, c_h, H, dt);
   TORCH_CHECK(bytes > 0, "genie_tk._C: tri_attn backward shape c_in=", c_in, " c_h=", c_h, " H=", H,
               " unsupported");
@@ -454,7 +471,8 @@ at::Tensor pair_transition_forward(const at::Tensor& p, const c10::optional<at::
 }
 
 // Backward of pair_transition_forward (no residual, no mask): returns [dp,
-// then the gradients of ln_w, ln_b, w1, b1, w2, b2 (fp32)].
+// then the gradients of ln_w, ln_b, w1, b1, w2, b2 (fp32 views of one
+// buffer), then that buffer].
 std::vector<at::Tensor> pair_transition_backward(const at::Tensor& p, const at::Tensor& dy,
                                                  std::vector<at::Tensor> ps, int64_t c, int64_t n,
                                                  double eps) {
@@ -483,12 +501,7 @@ std::vector<at::Tensor> pair_transition_backward(const at::Tensor& p, const at::
   gtk_pair_transition_grads g;
   float** gs[6] = {&g.ln_w, &g.ln_b, &g.w1, &g.b1, &g.w2, &g.b2};
   const int64_t hid = c * n;
-  const std::vector<std::vector<int64_t>> shapes = {{c}, {c}, {hid, c}, {hid}, {c, hid}, {c}};
-  for (int i = 0; i < 6; ++i) {
-    auto t = at::empty(shapes[i], pc.options().dtype(at::kFloat));
-    *gs[i] = t.data_ptr<float>();
-    out.push_back(t);
-  }
+  flat_grads(out, pc, {{c}, {c}, {hid, c}, {hid}, {c, hid}, {c}}, gs);
   const size_t bytes = gtk_pair_transition_backward_workspace_size(rows, c, n, dt);
   TORCH_CHECK(bytes > 0, "genie_tk._C: pair_transition backward shape c=", c, " n=", n, " unsupported");
   auto ws = workspace(pc, bytes);
@@ -600,11 +613,11 @@ PYBIND11_MODULE(_C, m) {
   m.def("tri_mul_contract_fp8", &tri_mul_contract_fp8,
         "x[p] = a[p] . b[p]^T over fp8 E4M3 planes, bf16 out (experiment)", py::arg("a"), py::arg("b"));
   m.def("tri_mul_backward", &tri_mul_backward,
-        "TriangleMultiplicativeUpdate backward: [dz, 16 parameter gradients (fp32)]",
+        "TriangleMultiplicativeUpdate backward: [dz, 16 parameter gradients (fp32), their buffer]",
         py::arg("z"), py::arg("mask"), py::arg("dy"), py::arg("params"), py::arg("c_z"),
         py::arg("c"), py::arg("outgoing"), py::arg("eps_in") = 1e-5, py::arg("eps_out") = 1e-5);
   m.def("tri_attn_backward", &tri_attn_backward,
-        "TriangleAttention backward: [dx, 10 parameter gradients (fp32)]", py::arg("x"),
+        "TriangleAttention backward: [dx, 10 parameter gradients (fp32), their buffer]", py::arg("x"),
         py::arg("mask"), py::arg("dy"), py::arg("params"), py::arg("c_in"), py::arg("c_h"),
         py::arg("no_heads"), py::arg("starting"), py::arg("eps") = 1e-5);
   m.def("pair_transition_pack", &pair_transition_pack, "Pack PairTransition parameters",
@@ -614,7 +627,7 @@ PYBIND11_MODULE(_C, m) {
         py::arg("p"), py::arg("mask"), py::arg("packed"), py::arg("c"), py::arg("n"),
         py::arg("residual") = false, py::arg("eps") = 1e-5);
   m.def("pair_transition_backward", &pair_transition_backward,
-        "PairTransition backward: [dp, 6 parameter gradients (fp32)]", py::arg("p"), py::arg("dy"),
+        "PairTransition backward: [dp, 6 parameter gradients (fp32), their buffer]", py::arg("p"), py::arg("dy"),
         py::arg("params"), py::arg("c"), py::arg("n"), py::arg("eps") = 1e-5);
   m.def("tri_attn_pack", &tri_attn_pack, "Pack TriangleAttention parameters", py::arg("params"),
         py::arg("c_in"), py::arg("c_h"), py::arg("no_heads"), py::arg("fp32"));

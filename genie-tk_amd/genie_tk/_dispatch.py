@@ -81,6 +81,18 @@ class PackedWeights:
         return self._packed
 
 
+def grads_as_params(grads: List[Tensor], flat: Optional[Tensor], params: List[Tensor]) -> List[Tensor]:
+    """Parameter gradients in their parameters' dtypes.  ``grads`` are fp32;
+    when ``flat`` is given they are views of it (the backward bindings'
+    layout) and, if every parameter has one non-fp32 dtype, one cast of
+    ``flat`` replaces a cast per gradient."""
+    dt = params[0].dtype
+    if flat is not None and dt != torch.float32 and all(p.dtype == dt for p in params):
+        fc = flat.to(dt)
+        return [fc.as_strided(g.shape, g.stride(), g.storage_offset()) for g in grads]
+    return [g.to(p.dtype) for g, p in zip(grads, params)]
+
+
 def flatten_batch(x: Tensor, mask: Optional[Tensor]) -> Tuple[Tensor, Optional[Tensor], Tuple]:
     """[*, N, N, C] -> [B, N, N, C] (and the mask likewise); returns the leading shape."""
     if x.dim() == 4 and (mask is None or mask.shape == x.shape[:-1]):

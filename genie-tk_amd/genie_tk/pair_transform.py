@@ -73,8 +73,8 @@ class _PairTransitionFunction(torch.autograd.Function):
         res = _ext.require().pair_transition_backward(
             p, dy.reshape(p.shape).to(p.dtype), list(params), mod.c_p, mod.n, mod.layer_norm.eps)
         dp = res[0] if ctx.needs_input_grad[1] else None
-        grads = [g.to(q.dtype) if ctx.needs_input_grad[2 + k] else None
-                 for k, (g, q) in enumerate(zip(res[1:], params))]
+        g = _dispatch.grads_as_params(list(res[1:-1]), res[-1], params)
+        grads = [gk if ctx.needs_input_grad[2 + k] else None for k, gk in enumerate(g)]
         return (None, dp, *grads)
 
 

@@ -103,16 +103,17 @@ class _TriAttnFunction(torch.autograd.Function):
             xb, mb, dy.reshape(xb.shape).to(x.dtype), bparams, mod.c_in, H_BWD * HD_BWD,
             H_BWD, mod.starting, mod.layer_norm.eps)
         dx = res[0].reshape(x.shape) if ctx.needs_input_grad[1] else None
-        g = list(res[1:])
+        g, flat = list(res[1:-1]), res[-1]
         if padded:
+            flat = None
             # back to the module's parameters (order of _PARAMS)
             g[2] = g[2][:mod.no_heads]
             g[3] = g[3][idx] * scale
             for k in (4, 5, 6, 7):
                 g[k] = g[k][idx]
             g[8] = g[8][:, idx]
-        grads = [gk.to(p.dtype) if ctx.needs_input_grad[4 + k] else None
-                 for k, (gk, p) in enumerate(zip(g, params))]
+        g = _dispatch.grads_as_params(g, flat, params)
+        grads = [gk if ctx.needs_input_grad[4 + k] else None for k, gk in enumerate(g)]
         return (None, dx, None, None, *grads)
 
 

@@ -98,11 +98,11 @@ class _TriMulFunction(torch.autograd.Function):
             zb, mb, dy.reshape(zb.shape).to(z.dtype), bparams, mod.c_z, mod.c_hidden * r,
             mod._outgoing, mod.layer_norm_in.eps, mod.layer_norm_out.eps)
         dz = res[0].reshape(z.shape) if ctx.needs_input_grad[1] else None
-        g = list(res[1:])
+        g, flat = list(res[1:-1]), res[-1]
         if r > 1:
-            g = _fold_channel_grads(g, mod.c_hidden, r)
-        grads = [gk.to(p.dtype) if ctx.needs_input_grad[3 + k] else None
-                 for k, (gk, p) in enumerate(zip(g, params))]
+            g, flat = _fold_channel_grads(g, mod.c_hidden, r), None
+        g = _dispatch.grads_as_params(g, flat, params)
+        grads = [gk if ctx.needs_input_grad[3 + k] else None for k, gk in enumerate(g)]
         return (None, dz, None, *grads)
 
 
