@@ -372,23 +372,50 @@ inline size_t wgrad_rowsum_floats(int M, int64_t pitch) {
   return (size_t)wgrad_plan(M, pitch).nsplit * wgrad_m_rows(M);
 }
 
-// dst[(m - m0)][n] = sum_s part[s][m][n] * (gamma ? gamma[n] : 1)
-//                    + (rowsum && beta ? rowsum[m] * beta[n] : 0),  m in [m0, m0 + rows),
+// Row ranges of one product's output, each finished into its own tensor.
+struct WgradSegs {
+  static constexpr int kMax = 8;
+  float* dst[kMax];
+  int m0[kMax];
+  int rows[kMax];
+  int count = 0;
+  void add(float* d, int m, int r) {
+    if (!d || r == 0) return;
+    dst[count] = d;
+    m0[count] = m;
+    rows[count] = r;
+    ++count;
+  }
+};
+
+// Segment k = blockIdx.y: dst_k[(m - m0_k)][n] = sum_s part[s][m][n] * (gamma ? gamma[n] : 1)
+//   + (rowsum && beta ? rowsum[m] * beta[n] : 0),  m in [m0_k, m0_k + rows_k),
 // n < Nn, with part laid out as [nsplit][Mp][Np] (the padded product).
 // Block: 32 consecutive outputs x 8 chunks of the splits (chunk c takes s = c,
-// c + 8, ...), the 8 partial sums of each output added through LDS.
+// c + 8, ..., four loads in flight), the 8 partial sums of each output added
+// through LDS.
 static __global__ __launch_bounds__(256) void wgrad_finish_kernel(
-    const float* __restrict__ part, int nsplit, int Mp, int Np, int Nn, int m0, int rows,
-    const float* __restrict__ rowsum, const float* __restrict__ gamma, const float* __restrict__ beta,
-    float* __restrict__ dst) {
+    const float* __restrict__ part, int nsplit, int Mp, int Np, int Nn, WgradSegs segs,
+    const float* __restrict__ rowsum, const float* __restrict__ gamma, const float* __restrict__ beta) {
   __shared__ float red[8][32];
+  const int k = blockIdx.y;
   const int o = threadIdx.x & 31, ch = threadIdx.x >> 5;
   const int idx = blockIdx.x * 32 + o;
-  const bool live = idx < rows * Nn;
-  const int m = m0 + (live ? idx / Nn : 0), n = live ? idx % Nn : 0;
+  if (blockIdx.x * 32 >= segs.rows[k] * Nn) return;  // block-uniform
+  const bool live = idx < segs.rows[k] * Nn;
+  const int m = segs.m0[k] + (live ? idx / Nn : 0), n = live ? idx % Nn : 0;
   float acc = 0.f;
-  if (live)
-    for (int sp = ch; sp < nsplit; sp += 8) acc += part[((int64_t)sp * Mp + m) * Np + n];
+  if (live) {
+    const float* src = part + (int64_t)m * Np + n;
+    const int64_t step = (int64_t)Mp * Np;
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+    int sp = ch;
+    for (; sp + 24 < nsplit; sp += 32)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) a[u] += src[(sp + 8 * u) * step];
+    for (; sp < nsplit; sp += 8) a[0] += src[sp * step];
+    acc = (a[0] + a[1]) + (a[2] + a[3]);
+  }
   red[ch][o] = acc;
   __syncthreads();
   if (ch != 0 || !live) return;
@@ -396,7 +423,27 @@ static __global__ __launch_bounds__(256) void wgrad_finish_kernel(
   for (int c = 1; c < 8; ++c) acc += red[c][o];
   if (gamma) acc *= gamma[n];
   if (rowsum && beta) acc += rowsum[m] * beta[n];
-  dst[idx] = acc;
+  segs.dst[k][idx] = acc;
+}
+
+inline int launch_wgrad_finish(const float* part, int M, int Nn, int64_t pitch, const WgradSegs& segs,
+                               const float* rowsum, const float* gamma, const float* beta, hipStream_t st) {
+  if (segs.count == 0) return GTK_OK;
+  int most = 0;
+  for (int k = 0; k < segs.count; ++k) most = segs.rows[k] > most ? segs.rows[k] : most;
+  const int n = most * Nn;
+  wgrad_finish_kernel<<<dim3((n + 31) / 32, segs.count), 256, 0, st>>>(
+      part, wgrad_plan(M, pitch).nsplit, wgrad_m_rows(M), wgrad_n_rows(Nn), Nn, segs, rowsum, gamma, beta);
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
+}
+
+inline int launch_wgrad_finish(const float* part, int M, int Nn, int64_t pitch, int m0, int rows,
+                               const float* rowsum, const float* gamma, const float* beta,
+                               float* dst, hipStream_t st) {
+  WgradSegs segs;
+  segs.add(dst, m0, rows);
+  return launch_wgrad_finish(part, M, Nn, pitch, segs, rowsum, gamma, beta, st);
 }
 
 // part[s][m][n] (m < wgrad_m_rows(M), n < wgrad_n_rows(Nn)): split s of
@@ -427,24 +474,15 @@ inline int launch_wgrad(const T* G, const T* X, float* part, int M, int Nn, int6
   GTK_LAUNCH_CHECK();
   if (with_rs) {
     // rs is a product output of one column: the same split reduction
-    wgrad_finish_kernel<<<(M + 31) / 32, 256, 0, st>>>(rs, pl.nsplit, Mp, 1, 1, 0, M, nullptr, nullptr,
-                                                       nullptr, sums);
+    WgradSegs one;
+    one.add(sums, 0, M);
+    wgrad_finish_kernel<<<dim3((M + 31) / 32, 1), 256, 0, st>>>(rs, pl.nsplit, Mp, 1, 1, one, nullptr, nullptr,
+                                                                nullptr);
     GTK_LAUNCH_CHECK();
   }
   return GTK_OK;
 }
 
-inline int launch_wgrad_finish(const float* part, int M, int Nn, int64_t pitch, int m0, int rows,
-                               const float* rowsum, const float* gamma, const float* beta,
-                               float* dst, hipStream_t st) {
-  if (!dst) return GTK_OK;
-  const int n = rows * Nn;
-  wgrad_finish_kernel<<<(n + 31) / 32, 256, 0, st>>>(part, wgrad_plan(M, pitch).nsplit, wgrad_m_rows(M),
-                                                     wgrad_n_rows(Nn), Nn, m0, rows, rowsum, gamma,
-                                                     beta, dst);
-  GTK_LAUNCH_CHECK();
-  return GTK_OK;
-}
 
 // ---------------------------------------------------------------------------
 // Row reductions over CM planes: psum[r][s] = sum over segment s of G[r][.],
@@ -515,17 +553,25 @@ __global__ __launch_bounds__(256) void rowred_kernel(const T* __restrict__ G, co
   }
 }
 
-static __global__ void rowred_finish_kernel(const float* __restrict__ ps, const float* __restrict__ pd, int rows,
-                                            int nseg, float* __restrict__ sums, float* __restrict__ dots) {
-  const int r = blockIdx.x * blockDim.x + threadIdx.x;
-  if (r >= rows) return;
+// One wave a row: lane l adds segments l, l + 64, ...
+static __global__ __launch_bounds__(64) void rowred_finish_kernel(const float* __restrict__ ps,
+                                                                 const float* __restrict__ pd, int rows, int nseg,
+                                                                 float* __restrict__ sums, float* __restrict__ dots) {
+  const int r = blockIdx.x, l = threadIdx.x;
   float a = 0.f, d = 0.f;
-  for (int s = 0; s < nseg; ++s) {
+  for (int s = l; s < nseg; s += 64) {
     a += ps[(int64_t)r * nseg + s];
     if (dots) d += pd[(int64_t)r * nseg + s];
   }
-  sums[r] = a;
-  if (dots) dots[r] = d;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    a += __shfl_xor(a, o, 64);
+    d += __shfl_xor(d, o, 64);
+  }
+  if (l == 0) {
+    sums[r] = a;
+    if (dots) dots[r] = d;
+  }
 }
 
 // Segments a row is split into: kRowSegs, or more for few rows (so that the
@@ -545,7 +591,7 @@ inline int launch_rowred(const T* G, const T* X, int rows, int64_t pitch, int64_
   if (X) rowred_kernel<T, true><<<rows * nseg, 256, 0, st>>>(G, X, rows, pitch, P, ps, pd);
   else rowred_kernel<T, false><<<rows * nseg, 256, 0, st>>>(G, nullptr, rows, pitch, P, ps, nullptr);
   GTK_LAUNCH_CHECK();
-  rowred_finish_kernel<<<(rows + 255) / 256, 256, 0, st>>>(ps, pd, rows, nseg, sums, X ? dots : nullptr);
+  rowred_finish_kernel<<<rows, 64, 0, st>>>(ps, pd, rows, nseg, sums, X ? dots : nullptr);
   GTK_LAUNCH_CHECK();
   return GTK_OK;
 }

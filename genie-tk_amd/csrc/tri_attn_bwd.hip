@@ -1309,21 +1309,30 @@ __global__ __launch_bounds__(256) void attn_dwb_finish_kernel(const float* __res
                                                             int Cp, int H, const float* __restrict__ gamma,
                                                             const float* __restrict__ beta,
                                                             const float* __restrict__ sums, float* __restrict__ dst) {
-  // 32 outputs x 8 chunks of the splits per block, partial sums added through LDS
-  __shared__ float red[8][32];
-  const int o = threadIdx.x & 31, ch = threadIdx.x >> 5;
-  const int idx = blockIdx.x * 32 + o;
+  // 8 outputs x 32 chunks of the splits per block (four loads in flight a
+  // thread), partial sums added through LDS
+  __shared__ float red[32][8];
+  const int o = threadIdx.x & 7, ch = threadIdx.x >> 3;
+  const int idx = blockIdx.x * 8 + o;
   const bool live = idx < H * C;
   const int h = live ? idx / C : 0, c = live ? idx % C : 0;
-  float a = 0.f;
-  if (live)
-    for (int s = ch; s < nsplit; s += 8) a += part[((int64_t)s * Cp + c) * 64 + h];
-  red[ch][o] = a;
+  float acc = 0.f;
+  if (live) {
+    const float* src = part + (int64_t)c * 64 + h;
+    const int64_t step = (int64_t)Cp * 64;
+    float a[4] = {0.f, 0.f, 0.f, 0.f};
+    int s = ch;
+    for (; s + 96 < nsplit; s += 128)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) a[u] += src[(s + 32 * u) * step];
+    for (; s < nsplit; s += 32) a[0] += src[s * step];
+    acc = (a[0] + a[1]) + (a[2] + a[3]);
+  }
+  red[ch][o] = acc;
   __syncthreads();
   if (ch != 0 || !live) return;
-#pragma unroll
-  for (int k = 1; k < 8; ++k) a += red[k][o];
-  dst[idx] = a * gamma[c] + sums[h] * beta[c];
+  for (int k = 1; k < 32; ++k) acc += red[k][o];
+  dst[idx] = acc * gamma[c] + sums[h] * beta[c];
 }
 
 // ---------------------------------------------------------------------------
@@ -1552,14 +1561,14 @@ static int bwd_triattn(const void* x, const float* mask, const void* dy,
     if ((rc = launch_wgrad<T>(b.cm_xh, b.cm_dtri, a.part3, C, 64, pitch, st))) return rc;
   }
   float* wdst[4] = {gr->q_w, gr->k_w, gr->v_w, gr->g_w};
-  for (int k = 0; k < 4; ++k)
-    if ((rc = launch_wgrad_finish(a.part1, 4 * CH, C, pitch, k * CH, CH, a.sums_stack, a.w.ln_w,
-                                  a.w.ln_b, wdst[k], st)))
-      return rc;
+  WgradSegs wsegs;
+  for (int k = 0; k < 4; ++k) wsegs.add(wdst[k], k * CH, CH);
+  if ((rc = launch_wgrad_finish(a.part1, 4 * CH, C, pitch, wsegs, a.sums_stack, a.w.ln_w, a.w.ln_b, st)))
+    return rc;
   if ((rc = launch_copy_f32(gr->g_b, a.sums_stack + 3 * CH, CH, st))) return rc;
   if ((rc = launch_wgrad_finish(a.part2, C, CH, pitch, 0, C, nullptr, nullptr, nullptr, gr->o_w, st)))
     return rc;
-  attn_dwb_finish_kernel<<<(H * C + 31) / 32, 256, 0, st>>>(
+  attn_dwb_finish_kernel<<<(H * C + 7) / 8, 256, 0, st>>>(
       a.part3, wgrad_plan(C, pitch).nsplit, C, wgrad_m_rows(C), H, a.w.ln_w, a.w.ln_b, a.sums_dtri, gr->tri_w);
   GTK_LAUNCH_CHECK();
   return GTK_OK;

@@ -862,13 +862,14 @@ static int bwd_trimul(const void* z, const float* mask, const void* dy,
   float* wdst[5] = {gr->a_p_w, gr->a_g_w, gr->b_p_w, gr->b_g_w, gr->g_w};
   float* bdst[5] = {gr->a_p_b, gr->a_g_b, gr->b_p_b, gr->b_g_b, gr->g_b};
   CopyList biases;
+  WgradSegs wsegs;
   for (int k = 0; k < 5; ++k) {
     const int m0 = k * CH, rows = k < 4 ? CH : CZ;
-    if ((rc = launch_wgrad_finish(a.part1, M1, CZ, pitch, m0, rows, a.sums_stack, w.ln_in_w,
-                                  w.ln_in_b, wdst[k], st)))
-      return rc;
+    wsegs.add(wdst[k], m0, rows);
     biases.add(bdst[k], a.sums_stack + m0, rows);
   }
+  if ((rc = launch_wgrad_finish(a.part1, M1, CZ, pitch, wsegs, a.sums_stack, w.ln_in_w, w.ln_in_b, st)))
+    return rc;
   if ((rc = launch_copy_list(biases, st))) return rc;
   if ((rc = launch_wgrad_finish(a.part2, CZ, CH, pitch, 0, CZ, sums_dp, w.ln_out_w, w.ln_out_b,
                                 gr->z_w, st)))
