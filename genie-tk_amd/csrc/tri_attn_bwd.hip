@@ -1303,6 +1303,187 @@ __global__ __launch_bounds__(256) void attn_bwd_pro_kernel(const T* __restrict__
     }
 }
 
+// ---------------------------------------------------------------------------
+// pro, bf16: the same algebra as attn_bwd_pro_kernel in persistent blocks of
+// 8 waves.  The kernel above reads the (kind, head) weight fragments of its
+// 16 d W products from L2 (128 KiB a 32-position tile at c_in = 128) and
+// holds them in registers (one wave a SIMD); here W^T of q, k, v and the gate
+// (4 x c_in x c_h bf16), W_b and the LayerNorm weight sit in LDS, two waves a
+// SIMD.  Whole tiles (32 valid positions, rows 16-byte aligned: N % 8 == 0)
+// move their channel-major blocks through a per-wave LDS tile, 16 bytes a
+// lane (the gate's d rows are read the same way); other tiles take the
+// element path.  The rows of x are read again for the LayerNorm backward
+// rather than kept (64 values a lane).
+// ---------------------------------------------------------------------------
+template <int C, int H>
+__global__ __launch_bounds__(512) void attn_bwd_pro_lds_kernel(const bf16* __restrict__ x, bf16* __restrict__ dx,
+                                                               AttnBwdW<bf16> w, AttnBwdBufs<bf16> bf, int B, int N,
+                                                               int np, int starting, float eps, int64_t ntiles) {
+  constexpr int CH = H * AD;
+  constexpr int PW = C * CH;  // elements of one packed W^T
+  __shared__ __attribute__((aligned(1024))) bf16 wl[4][PW];
+  __shared__ __attribute__((aligned(16))) bf16 cst[8][kCmTile];
+  __shared__ __attribute__((aligned(16))) float wbl[H * C];
+  __shared__ __attribute__((aligned(16))) float lnw[C];
+  copy_to_lds_async(wl[0], w.wt_q, PW * 2);
+  copy_to_lds_async(wl[1], w.wt_k, PW * 2);
+  copy_to_lds_async(wl[2], w.wt_v, PW * 2);
+  copy_to_lds_async(wl[3], w.wt_g, PW * 2);
+  for (int t = threadIdx.x; t < H * C; t += blockDim.x) wbl[t] = w.wb_raw[t];
+  for (int t = threadIdx.x; t < C; t += blockDim.x) lnw[t] = w.ln_w[t];
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
+  const int wave = wave_id();
+  bf16* const sw = cst[wave];
+  const int jtiles = np / 32;
+  const int64_t pitch = bf.pitch;
+  const bf16* src[3] = {bf.dq, bf.dk, bf.dv};
+  // channel-major planes through descriptors based at the tile's first
+  // position, per-lane offsets 32-bit and a channel's offset in the scalar
+  // operand (the host checks the ranges fit)
+  const uint32_t svo = cm_store_voff(pitch), lvo = cm_load_voff(pitch);
+  const uint32_t evo = (uint32_t)(4 * half * pitch + t32) * 2;  // element path: channel 4*half, position t32
+  for (int64_t tile = (int64_t)blockIdx.x * 8 + wave; tile < ntiles; tile += (int64_t)gridDim.x * 8) {
+    const int jt = (int)(tile % jtiles);
+    const int r = (int)((tile / jtiles) % N);
+    const int b = (int)(tile / ((int64_t)jtiles * N));
+    const int j = jt * 32 + t32;
+    const bool valid = j < N;
+    const int64_t xp = valid ? ((int64_t)b * N + (starting ? r : j)) * N + (starting ? j : r) : 0;
+    const int64_t p = ((int64_t)b * N + r) * N + j;
+    const int64_t p0 = ((int64_t)b * N + r) * N + jt * 32;
+    const bool fast = jt * 32 + 32 <= N && N % 8 == 0;  // wave-uniform
+    const uint32_t eoff = valid ? evo : kBufSkip;  // stores of padded lanes are dropped
+    // per-tile LDS reads of W_b and the LayerNorm weight through an opaque
+    // index: hoisted out of the tile loop, 320 of them would stay in registers
+    const int oz = opaque_zero();
+    const auto srs = buf_rsrc(bf.cm_stack + p0, (uint32_t)(4 * CH * pitch * 2));
+
+    f32x2 st;
+    {
+      RowHalf<C> rhx;
+      load_row_half<bf16, C>(rhx, x + xp * C, valid);
+      st = row_stats<C>(rhx, eps);
+    }
+    f32x16 dzn[C / 32];
+#pragma unroll
+    for (int nt = 0; nt < C / 32; ++nt) dzn[nt] = zero16();
+#pragma unroll 1
+    for (int kind = 0; kind < 4; ++kind) {
+#pragma unroll 1
+      for (int h = 0; h < H; ++h) {
+        float d[16];
+        const uint32_t soff = (uint32_t)((kind * CH + h * AD) * pitch * 2);
+        if (kind < 3) {
+          const bf16* s = src[kind] + ((((int64_t)b * N + r) * H + h) * np + j) * AD;
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const f32x4 v4 = load4f(s + 8 * g + 4 * half);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) d[4 * g + e] = valid ? v4[e] : 0.f;
+          }
+          if (fast) {
+            cm_store_tile(sw, d, srs, svo, soff, pitch);
+          } else {
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                buf_store_bf16(srs, eoff, soff + (uint32_t)((8 * g + e) * pitch * 2), d[4 * g + e]);
+          }
+        } else if (fast) {
+          cm_load_tile(sw, d, srs, lvo, soff, pitch);
+        } else {
+          // padded lanes read past the row (or past the range: 0) and are zeroed
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const float v = buf_load_bf16(srs, evo, soff + (uint32_t)((8 * g + e) * pitch * 2));
+              d[4 * g + e] = valid ? v : 0.f;
+            }
+        }
+        Frag<bf16> f[2];
+        vals_to_frags<bf16>(f, d);
+#pragma unroll
+        for (int nt2 = 0; nt2 < C / 32; ++nt2)
+#pragma unroll
+          for (int gp = 0; gp < 2; ++gp) {
+            Frag<bf16> wf;
+            load_wfrag_lds(wf, wl[kind], nt2, 2 * h + gp, CH / 16);
+            mma(dzn[nt2], wf, f[gp]);
+          }
+      }
+    }
+    // triangle bias: dxn += sum_h dB[h][r][j] W_b[h][.]
+    float dtri[H];
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+      dtri[h] = valid ? bf.db[(((int64_t)b * H + h) * N + r) * N + j] : 0.f;
+      if (valid && half == 0) bf.cm_dtri[(int64_t)h * pitch + p] = (bf16)dtri[h];
+    }
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < C / 32; ++nt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c0 = nt * 32 + 8 * g + 4 * half;
+        const f32x4 x4 = load4f(x + xp * C + c0);  // padded lanes: pair 0, their t is 0
+        const f32x4 lw = *reinterpret_cast<const f32x4*>(lnw + c0 + oz);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float t = dzn[nt][4 * g + e];
+#pragma unroll
+          for (int h = 0; h < H; ++h) t += dtri[h] * wbl[h * C + c0 + e + oz];
+          dzn[nt][4 * g + e] = t;
+          const float xv = (x4[e] - st[0]) * st[1];
+          const float dxh = lw[e] * t;
+          s1 += dxh;
+          s2 += dxh * xv;
+        }
+      }
+    s1 += xor32(s1);
+    s2 += xor32(s2);
+    const float m1 = s1 * (1.0f / C), m2 = s2 * (1.0f / C);
+    // the rows are read again below rather than kept
+    asm volatile("" ::: "memory");
+    const auto xrs = buf_rsrc(bf.cm_xh + p0, (uint32_t)(C * pitch * 2));
+    const auto nrs = buf_rsrc(bf.cm_dxn + p0, (uint32_t)(C * pitch * 2));
+#pragma unroll
+    for (int nt = 0; nt < C / 32; ++nt) {
+      float xs[16], dn[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c0 = nt * 32 + 8 * g + 4 * half;
+        const f32x4 x4 = load4f(x + xp * C + c0);  // padded lanes: pair 0, their t is 0
+        const f32x4 lw = *reinterpret_cast<const f32x4*>(lnw + c0 + oz);
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float xv = (x4[e] - st[0]) * st[1];
+          const float t = dzn[nt][4 * g + e];
+          o[e] = st[1] * (lw[e] * t - m1 - xv * m2);
+          xs[4 * g + e] = xv;
+          dn[4 * g + e] = t;
+          if (!fast) {
+            const uint32_t so = (uint32_t)((nt * 32 + 8 * g + e) * pitch * 2);
+            buf_store_bf16(xrs, eoff, so, xv);
+            buf_store_bf16(nrs, eoff, so, t);
+          }
+        }
+        if (valid) store4(dx + xp * C + c0, o[0], o[1], o[2], o[3]);
+      }
+      if (fast) {
+        const uint32_t so = (uint32_t)(nt * 32 * pitch * 2);
+        cm_store_tile(sw, xs, xrs, svo, so, pitch);
+        cm_store_tile(sw, dn, nrs, svo, so, pitch);
+      }
+    }
+  }
+}
+
 // dW_b[h][c] = W3[c][h] gamma[c] + s[h] beta[c]  (W3 = sum_s part[s][c][h]: the
 // product's layout [nsplit][Cp][64], Cp = C rounded up to its row tile)
 __global__ __launch_bounds__(256) void attn_dwb_finish_kernel(const float* __restrict__ part, int nsplit, int C,
@@ -1536,8 +1717,19 @@ static int bwd_triattn(const void* x, const float* mask, const void* dy,
     return rc;
   {
     StageTimer timer("triattn_bwd_pro", st);
-    attn_bwd_pro_kernel<T, C, H><<<g4(rowtiles), 256, 0, st>>>((const T*)x, (T*)dx, a.w, a.b,
-                                                                (int)B, (int)N, np, starting, eps);
+    bool lds = false;
+    if constexpr (std::is_same<T, bf16>::value) {
+      // the LDS kernel addresses cm_stack through 32-bit offsets
+      if ((int64_t)4 * CH * pitch * 2 < (1ll << 31)) {
+        const int grid = (int)std::min<int64_t>(device_cus(), (rowtiles + 7) / 8);
+        attn_bwd_pro_lds_kernel<C, H><<<grid, 512, 0, st>>>((const bf16*)x, (bf16*)dx, a.w, a.b, (int)B,
+                                                            (int)N, np, starting, eps, rowtiles);
+        lds = true;
+      }
+    }
+    if (!lds)
+      attn_bwd_pro_kernel<T, C, H><<<g4(rowtiles), 256, 0, st>>>((const T*)x, (T*)dx, a.w, a.b,
+                                                                  (int)B, (int)N, np, starting, eps);
     GTK_LAUNCH_CHECK();
   }
   const AttnBwdBufs<T>& b = a.b;

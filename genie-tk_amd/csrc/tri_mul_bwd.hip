@@ -32,85 +32,6 @@
 
 namespace gtk {
 
-// one bf16 value through a buffer descriptor: byte offset = voff (per lane)
-// + soff (wave-uniform, a scalar operand); an offset past the descriptor's
-// range reads 0 / drops the store
-__device__ __forceinline__ float buf_load_bf16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  const unsigned short v = __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
-  return __uint_as_float((uint32_t)v << 16);
-}
-__device__ __forceinline__ void buf_store_bf16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float x) {
-  __builtin_amdgcn_raw_buffer_store_b16(__builtin_bit_cast(unsigned short, cvt<bf16>(x)), r, voff, soff, 0);
-}
-
-// Channel-major rows of a full 32-pair tile through a per-wave LDS tile of
-// 32 x 32 bf16 (rows of 72 bytes: the pad spreads both the row writes and the
-// transposing reads over the banks).  One 32-channel block then costs two
-// 16-byte loads or stores a lane instead of sixteen 2-byte ones.  For tiles
-// whose 32 pairs are all valid and whose rows start 16-byte aligned.
-constexpr int kCmRow = 36;
-constexpr int kCmTile = 32 * kCmRow;
-typedef uint32_t cm_u32x2 __attribute__((ext_vector_type(2)));
-typedef uint32_t cm_u32x4 __attribute__((ext_vector_type(4)));
-
-// per-lane byte offsets of the 16-byte accesses: cm_store_tile's lane holds
-// pairs 8 * (L / 4) .. +7 of channel 4 * G + L % 4 (L = lane % 16,
-// G = lane / 16); cm_load_tile's lane reads pairs 8 * (lane % 4) .. +7 of
-// channel lane / 4 (and 16 + lane / 4)
-__device__ __forceinline__ uint32_t cm_store_voff(int64_t stride) {
-  const int lane = threadIdx.x & 63, L = lane & 15, G = lane >> 4;
-  return (uint32_t)((4 * G + (L & 3)) * stride + 8 * (L >> 2)) * 2;
-}
-__device__ __forceinline__ uint32_t cm_load_voff(int64_t stride) {
-  const int lane = threadIdx.x & 63;
-  return (uint32_t)((lane >> 2) * stride + 8 * (lane & 3)) * 2;
-}
-
-// accumulator values of a 32-channel block (value 4g + r: channel
-// 8g + 4 * half + r of pair lane % 32) -> the block's 32 rows at byte offset
-// soff (channel 0 of the block) + voff; rows are stride elements apart
-__device__ __forceinline__ void cm_store_tile(bf16* sw, const float* v, __amdgpu_buffer_rsrc_t r, uint32_t voff,
-                                              uint32_t soff, int64_t stride) {
-  const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
-  const int L = lane & 15, G = lane >> 4;
-  __builtin_amdgcn_wave_barrier();
-#pragma unroll
-  for (int g = 0; g < 4; ++g)
-    *reinterpret_cast<cm_u32x2*>(sw + t32 * kCmRow + 8 * g + 4 * half) =
-        cm_u32x2{pack_bf16x2(v[4 * g], v[4 * g + 1]), pack_bf16x2(v[4 * g + 2], v[4 * g + 3])};
-  __builtin_amdgcn_wave_barrier();
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    // supplier L: pair row 8 * (L % 4) + 4e + L / 4, channels 16h + 4G .. +3
-    const s16x4 p0 = lds_read_tr16(sw + (8 * (L & 3) + (L >> 2)) * kCmRow + 16 * h + 4 * G);
-    const s16x4 p1 = lds_read_tr16(sw + (8 * (L & 3) + 4 + (L >> 2)) * kCmRow + 16 * h + 4 * G);
-    const cm_u32x4 q = __builtin_bit_cast(cm_u32x4, __builtin_shufflevector(p0, p1, 0, 1, 2, 3, 4, 5, 6, 7));
-    __builtin_amdgcn_raw_buffer_store_b128(q, r, voff, soff + (uint32_t)(16 * h * stride) * 2, 0);
-  }
-}
-
-// the 32 rows of a block at byte offset soff + voff -> accumulator values
-__device__ __forceinline__ void cm_load_tile(bf16* sw, float* v, __amdgpu_buffer_rsrc_t r, uint32_t voff,
-                                             uint32_t soff, int64_t stride) {
-  const int lane = threadIdx.x & 63, half = lane >> 5;
-  const int L = lane & 15, G = lane >> 4;
-  const cm_u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
-  const cm_u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff + (uint32_t)(16 * stride) * 2, 0);
-  __builtin_amdgcn_wave_barrier();
-  bf16* const w0 = sw + (lane >> 2) * kCmRow + 8 * (lane & 3);
-  *reinterpret_cast<cm_u32x2*>(w0) = cm_u32x2{a[0], a[1]};
-  *reinterpret_cast<cm_u32x2*>(w0 + 4) = cm_u32x2{a[2], a[3]};
-  *reinterpret_cast<cm_u32x2*>(w0 + 16 * kCmRow) = cm_u32x2{b[0], b[1]};
-  *reinterpret_cast<cm_u32x2*>(w0 + 16 * kCmRow + 4) = cm_u32x2{b[2], b[3]};
-  __builtin_amdgcn_wave_barrier();
-#pragma unroll
-  for (int g = 0; g < 4; ++g) {
-    // supplier L: channel row 8g + 4 * half + L / 4, pairs 16 * (G % 2) + 4 * (L % 4) .. +3
-    const s16x4 p = lds_read_tr16(sw + (8 * g + 4 * half + (L >> 2)) * kCmRow + 16 * (G & 1) + 4 * (L & 3));
-#pragma unroll
-    for (int k = 0; k < 4; ++k) v[4 * g + k] = __uint_as_float((uint32_t)(unsigned short)p[k] << 16);
-  }
-}
 
 // ---------------------------------------------------------------------------
 // 2. Epilogue backward.  Tiles cover all Np x Np plane positions so that the
@@ -658,7 +579,7 @@ __global__ __launch_bounds__(512) void trimul_bwd_prologue_side_kernel(
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int c0 = nt * 32 + 8 * g + 4 * half;
-        const f32x4 z4 = valid ? load4f(z + pair * CZ + c0) : f32x4{0.f, 0.f, 0.f, 0.f};
+        const f32x4 z4 = load4f(z + pair * CZ + c0);  // padded lanes: pair j = 0, dzn 0
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float xv = (z4[r] - st[0]) * st[1];
@@ -682,7 +603,7 @@ __global__ __launch_bounds__(512) void trimul_bwd_prologue_side_kernel(
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int c0 = nt * 32 + 8 * g + 4 * half;
-        const f32x4 z4 = valid ? load4f(z + pair * CZ + c0) : f32x4{0.f, 0.f, 0.f, 0.f};
+        const f32x4 z4 = load4f(z + pair * CZ + c0);  // padded lanes: pair j = 0, dzn 0
         float o[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
