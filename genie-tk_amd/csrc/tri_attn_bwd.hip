@@ -206,6 +206,113 @@ __global__ __launch_bounds__(256) void attn_bwd_proj_kernel(const T* __restrict_
 }
 
 // ---------------------------------------------------------------------------
+// proj, bf16 (position-major outputs only): the same products as
+// attn_bwd_proj_kernel in persistent blocks of NW waves with W_q, W_k, W_v, W_g,
+// W_b (c_h x c_in each, 136 KiB at c_in = 128) and their biases in LDS; the
+// kernel above reads 136 KiB of weight fragments from L2 per 32-position tile.
+// ---------------------------------------------------------------------------
+template <int C, int H, int NW>
+__global__ __launch_bounds__(64 * NW) void attn_bwd_proj_lds_kernel(const bf16* __restrict__ x,
+                                                                const float* __restrict__ mask,
+                                                                AttnBwdW<bf16> w, AttnBwdBufs<bf16> bf, int B,
+                                                                int N, int np, int starting, float eps,
+                                                                float inv_scale, int64_t ntiles) {
+  constexpr int CH = H * AD;
+  constexpr int PW = C * CH;   // elements of one packed projection
+  constexpr int PB = 32 * C;   // the triangle-bias projection (H outputs padded to 32)
+  __shared__ __attribute__((aligned(1024))) bf16 wl[4 * PW + PB];
+  __shared__ __attribute__((aligned(16))) float bl[4 * CH + 32];
+  copy_to_lds_async(wl, w.w_q, PW * 2);
+  copy_to_lds_async(wl + PW, w.w_k, PW * 2);
+  copy_to_lds_async(wl + 2 * PW, w.w_v, PW * 2);
+  copy_to_lds_async(wl + 3 * PW, w.w_g, PW * 2);
+  copy_to_lds_async(wl + 4 * PW, w.w_b, PB * 2);
+  for (int t = threadIdx.x; t < CH; t += blockDim.x) {
+    bl[t] = w.b_q[t];
+    bl[CH + t] = w.b_k[t];
+    bl[2 * CH + t] = w.b_v[t];
+    bl[3 * CH + t] = w.b_g[t];
+  }
+  if (threadIdx.x < H) bl[4 * CH + threadIdx.x] = w.b_b[threadIdx.x];
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  const int lane = threadIdx.x & 63, half = lane >> 5, t32 = lane & 31;
+  const int wave = wave_id();
+  const int jtiles = np / 32;
+  bf16* const dr[3] = {bf.qr, bf.kr, bf.vr};
+  for (int64_t tile = (int64_t)blockIdx.x * NW + wave; tile < ntiles; tile += (int64_t)gridDim.x * NW) {
+    const int jt = (int)(tile % jtiles);
+    const int r = (int)((tile / jtiles) % N);
+    const int b = (int)(tile / ((int64_t)jtiles * N));
+    const int j = jt * 32 + t32;
+    const bool valid = j < N;
+    const int64_t xp = valid ? ((int64_t)b * N + (starting ? r : j)) * N + (starting ? j : r) : 0;
+    // per-tile LDS reads of the biases through an opaque index (hoisted out of
+    // the tile loop they would stay in registers)
+    const int oz = opaque_zero();
+
+    Frag<bf16> xf[C / 16];
+    {
+      RowHalf<C> rh;
+      load_row_half<bf16, C>(rh, x + xp * C, valid);
+      const f32x2 st = row_stats<C>(rh, eps);
+      ln_to_frags<bf16, C>(xf, rh, st);
+    }
+    auto gemm = [&](const bf16* wp, int nt) {
+      f32x16 acc = zero16();
+#pragma unroll
+      for (int ks = 0; ks < C / 16; ++ks) {
+        Frag<bf16> wf;
+        load_wfrag_lds(wf, wp, nt, ks, C / 16);
+        mma(acc, wf, xf[ks]);
+      }
+      return acc;
+    };
+#pragma unroll 1
+    for (int kind = 0; kind < 4; ++kind) {
+#pragma unroll 1
+      for (int h = 0; h < H; ++h) {
+        const f32x16 acc = gemm(wl + kind * PW, h);
+        const float* bk = bl + kind * CH + h * AD + oz;
+        bf16* const dst = kind < 3 ? dr[kind] + ((((int64_t)b * N + r) * H + h) * np + j) * AD
+                                   : bf.gt + (((int64_t)b * N + r) * np + j) * CH + h * AD;
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int d0 = 8 * g + 4 * half;
+          const f32x4 bv = *reinterpret_cast<const f32x4*>(bk + d0);
+          float v[4];
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const float u = acc[4 * g + q] + bv[q];
+            v[q] = kind < 3 ? (valid ? u : 0.f) : sigmoidf_(u);
+          }
+          store4(dst + d0, v[0], v[1], v[2], v[3]);
+        }
+      }
+    }
+    {
+      // triangle bias: outputs 0..H-1 sit in lanes of half 0, acc[0..H-1]
+      const f32x16 acc = gemm(wl + 4 * PW, 0);
+      if (valid && half == 0) {
+        float* bT = bf.biasT + (int64_t)b * H * np * np;
+        float* bS = bf.biasS + (int64_t)b * H * np * np;
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+          const bf16 bv = cvt<bf16>(acc[h] + bl[4 * CH + h + oz]);
+          bf.bias[(((int64_t)b * H + h) * N + r) * N + j] = bv;
+          const float bs = to_f32(bv) * inv_scale;  // query r, key j
+          bT[bias_frag_elem(h, r, j, np)] = bs;
+          bS[bias_frag_elem(h, j, r, np)] = bs;
+        }
+      }
+    }
+    // 1 for a valid key (mask == 1: no bias); 0 for a masked key
+    if (half == 0) bf.kmask[((int64_t)b * N + r) * np + j] = valid && (!mask || mask[xp] == 1.f) ? 1.f : 0.f;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // fwd: O, m, 1/l per (row, head, 32 queries); lane = query
 // ---------------------------------------------------------------------------
 template <typename T, int H>
@@ -1632,8 +1739,17 @@ static int bwd_triattn(const void* x, const float* mask, const void* dy,
   const int dmajor = npm == 0;
   {
     StageTimer timer("triattn_bwd_proj", st);
-    attn_bwd_proj_kernel<T, C, H><<<g4(rowtiles), 256, 0, st>>>(
-        (const T*)x, mask, a.w, a.b, (int)B, (int)N, np, starting, eps, 1.0f / scale, dmajor);
+    if constexpr (std::is_same<T, bf16>::value) {
+      if (!dmajor) {
+        // 16 waves a block (about 100 registers each): four a SIMD
+        const int grid = (int)std::min<int64_t>(device_cus(), (rowtiles + 15) / 16);
+        attn_bwd_proj_lds_kernel<C, H, 16><<<grid, 1024, 0, st>>>((const bf16*)x, mask, a.w, a.b, (int)B, (int)N,
+                                                                  np, starting, eps, 1.0f / scale, rowtiles);
+      }
+    }
+    if (!std::is_same<T, bf16>::value || dmajor)
+      attn_bwd_proj_kernel<T, C, H><<<g4(rowtiles), 256, 0, st>>>(
+          (const T*)x, mask, a.w, a.b, (int)B, (int)N, np, starting, eps, 1.0f / scale, dmajor);
     GTK_LAUNCH_CHECK();
   }
   const int64_t rblocks = B * N * H;
