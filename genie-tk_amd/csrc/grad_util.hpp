@@ -215,8 +215,10 @@ struct CmTile {
       id[gp].set(f);
     }
   }
+  // oz: 0 (an opaque zero in persistent loops, so that the per-lane channel
+  // offsets are not hoisted out of them into registers)
   __device__ __forceinline__ void store(bf16* cm, int64_t pitch, int64_t p0, int c0, const float* v, bool fast,
-                                        bool lane_valid) const {
+                                        bool lane_valid, int oz = 0) const {
     const int lane = threadIdx.x & 63;
     const int half = lane >> 5, t32 = lane & 31;
     if (fast) {
@@ -224,7 +226,7 @@ struct CmTile {
       vals_to_frags<bf16>(f, v);
       f32x16 d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[0].v, id[0].v, zero16(), 0, 0, 0);
       d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f[1].v, id[1].v, d, 0, 0, 0);
-      bf16* col = cm + (int64_t)(c0 + t32) * pitch + p0 + 4 * half;
+      bf16* col = cm + (int64_t)(c0 + t32 + oz) * pitch + p0 + 4 * half;
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const uint2 w = make_uint2(pack_bf16x2(d[4 * g], d[4 * g + 1]), pack_bf16x2(d[4 * g + 2], d[4 * g + 3]));
@@ -235,7 +237,7 @@ struct CmTile {
       for (int g = 0; g < 4; ++g)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          cm[(int64_t)(c0 + 8 * g + 4 * half + r) * pitch + p0 + t32] = (bf16)v[4 * g + r];
+          cm[(int64_t)(c0 + 8 * g + 4 * half + r + oz) * pitch + p0 + t32] = (bf16)v[4 * g + r];
     }
   }
 };
@@ -259,7 +261,7 @@ struct CmTileRH {
     }
   }
   __device__ __forceinline__ void store(bf16* cm, int64_t pitch, int64_t p0, const float* v, bool fast,
-                                        bool lane_valid) const {
+                                        bool lane_valid, int oz = 0) const {
     const int lane = threadIdx.x & 63;
     const int half = lane >> 5, t32 = lane & 31;
     if (fast) {
@@ -271,7 +273,7 @@ struct CmTileRH {
         f32x16 d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f0.v, id[0].v, zero16(), 0, 0, 0);
         d = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f1.v, id[1].v, d, 0, 0, 0);
         const int ch = t32 < 16 ? 8 * s0 + t32 : 64 + 8 * s0 + t32 - 16;
-        bf16* col = cm + (int64_t)ch * pitch + p0 + 4 * half;
+        bf16* col = cm + (int64_t)(ch + oz) * pitch + p0 + 4 * half;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const uint2 w = make_uint2(pack_bf16x2(d[4 * g], d[4 * g + 1]), pack_bf16x2(d[4 * g + 2], d[4 * g + 3]));
@@ -280,7 +282,7 @@ struct CmTileRH {
       }
     } else if (lane_valid) {
 #pragma unroll
-      for (int i = 0; i < 64; ++i) cm[(int64_t)(half * 64 + i) * pitch + p0 + t32] = (bf16)v[i];
+      for (int i = 0; i < 64; ++i) cm[(int64_t)(half * 64 + i + oz) * pitch + p0 + t32] = (bf16)v[i];
     }
   }
 };
