@@ -22,6 +22,7 @@
 //  5. weight gradients: two split-K products over the pairs, row sums for
 //     biases and LayerNorm parameters, folded back through gamma and beta.
 #include <algorithm>
+#include <cstdlib>
 #include <type_traits>
 
 #include "capi_util.hpp"
@@ -37,17 +38,17 @@ namespace gtk {
 // 2. Epilogue backward.  Tiles cover all Np x Np plane positions so that the
 //    padding of the dX planes is written as zero.
 // ---------------------------------------------------------------------------
-template <typename T, int CZ, int CH, bool FULL = false>
+template <typename T, int CZ, int CH, bool FULL = false, bool STGP = true>
 __global__ __launch_bounds__(256) void trimul_bwd_epilogue_kernel(
     const T* __restrict__ z, const T* __restrict__ px, const T* __restrict__ dy,
     T* __restrict__ pdx, T* __restrict__ cm_dp, T* __restrict__ cm_dg, T* __restrict__ cm_xo,
     T* __restrict__ cm_dxo, TriMulPacked<T> w, const T* __restrict__ wzt, int B, int N, int Np,
     int64_t pitch, float eps_in, float eps_out) {
   constexpr int XPITCH = CH + 8;
-  // bf16: the dX planes' 32-channel blocks go through a per-wave LDS tile,
-  // and for FULL (N % 32 == 0: every tile is 32 valid pairs on one row) the
-  // channel-major blocks too
-  constexpr bool STG = sizeof(T) == 2;
+  // bf16 (STGP: the planes' byte offsets fit 32 bits): the dX planes'
+  // 32-channel blocks go through a per-wave LDS tile, and for FULL (N % 32 ==
+  // 0: every tile is 32 valid pairs on one row) the channel-major blocks too
+  constexpr bool STG = sizeof(T) == 2 && STGP;
   static_assert(STG || !FULL, "staged stores are bf16");
   __shared__ __attribute__((aligned(16))) T xs[4][32 * XPITCH];
   __shared__ __attribute__((aligned(16))) bf16 cst[STG ? 4 : 1][STG ? kCmTile : 1];
@@ -694,6 +695,14 @@ static int bwd_trimul(const void* z, const float* mask, const void* dy,
   const int M1 = 4 * CH + CZ;
   const int wd = wts->dtype;
   int rc;
+  // The bf16 kernels' descriptor paths address the channel-major buffers and
+  // the dA / dB / dX planes with 32-bit byte offsets; beyond that (N above
+  // about 2900 at B = 1) the element-pointer kernels run.  The environment
+  // variable GENIE_TK_ELEMENT_PATHS=1 selects them at any size (for tests).
+  const char* ep = std::getenv("GENIE_TK_ELEMENT_PATHS");
+  const bool fits32 =
+      (int64_t)std::max(CZ, CH) * std::max<int64_t>(pitch, (int64_t)Np * Np) * 2 < (1ll << 31) &&
+      !(ep && ep[0] == '1');
   // 0. weights
   if ((rc = gtk_tri_mul_pack(wts, CZ, CH, dtype, a.packed, gtk_tri_mul_packed_size(CZ, CH, dtype), st)))
     return rc;
@@ -712,13 +721,16 @@ static int bwd_trimul(const void* z, const float* mask, const void* dy,
   {
     const int64_t tiles = B * (int64_t)Np * (Np / 32);
     StageTimer timer("trimul_bwd_epilogue", st);
-    auto epi = [&](auto full) {
-      trimul_bwd_epilogue_kernel<T, CZ, CH, decltype(full)::value><<<(unsigned)((tiles + 3) / 4), 256, 0, st>>>(
-          (const T*)z, a.px, (const T*)dy, a.pdx, a.cm_dp, a.cm_stack + (int64_t)4 * CH * pitch,
-          a.cm_xo, a.cm_dxo, w, a.wzt, (int)B, (int)N, Np, pitch, eps_in, eps_out);
+    auto epi = [&](auto full, auto stg) {
+      trimul_bwd_epilogue_kernel<T, CZ, CH, decltype(full)::value, decltype(stg)::value>
+          <<<(unsigned)((tiles + 3) / 4), 256, 0, st>>>(
+              (const T*)z, a.px, (const T*)dy, a.pdx, a.cm_dp, a.cm_stack + (int64_t)4 * CH * pitch,
+              a.cm_xo, a.cm_dxo, w, a.wzt, (int)B, (int)N, Np, pitch, eps_in, eps_out);
     };
-    if (sizeof(T) == 2 && N % 32 == 0) epi(std::integral_constant<bool, sizeof(T) == 2>{});
-    else epi(std::false_type{});
+    using BF = std::integral_constant<bool, sizeof(T) == 2>;
+    if (!fits32) epi(std::false_type{}, std::false_type{});
+    else if (sizeof(T) == 2 && N % 32 == 0) epi(BF{}, std::true_type{});
+    else epi(std::false_type{}, std::true_type{});
     GTK_LAUNCH_CHECK();
   }
   // 3. contraction backward (px is free from here on: it takes dX^T)
@@ -737,27 +749,31 @@ static int bwd_trimul(const void* z, const float* mask, const void* dy,
   {
     const int64_t tiles = B * N * ((N + 31) / 32);
     StageTimer timer("trimul_bwd_prologue", st);
+    bool sides = false;
     if constexpr (sizeof(T) == 2) {
-      const int grid = (int)std::min<int64_t>(device_cus(), (tiles + 7) / 8);
-      auto side = [&](auto full) -> int {
-        constexpr bool F = decltype(full)::value;
-        trimul_bwd_prologue_side_kernel<CZ, CH, 0, F><<<grid, 512, 0, st>>>(
-            (const bf16*)z, mask, a.pda, (bf16*)dz, a.cm_stack, a.cm_xi, a.cm_dzn, w, a.wt, a.wgt,
-            a.part_dzn, (int)B, (int)N, Np, pitch, eps_in, tiles);
-        GTK_LAUNCH_CHECK();
-        trimul_bwd_prologue_side_kernel<CZ, CH, 1, F><<<grid, 512, 0, st>>>(
-            (const bf16*)z, mask, a.pdb, (bf16*)dz, a.cm_stack, a.cm_xi, a.cm_dzn, w, a.wt, a.wgt,
-            a.part_dzn, (int)B, (int)N, Np, pitch, eps_in, tiles);
-        GTK_LAUNCH_CHECK();
-        return 0;
-      };
-      // whole 32-pair tiles on one row: the staged channel-major path
-      if ((rc = N % 32 == 0 ? side(std::true_type{}) : side(std::false_type{}))) return rc;
-    } else {
+      if (fits32) {
+        const int grid = (int)std::min<int64_t>(device_cus(), (tiles + 7) / 8);
+        auto side = [&](auto full) -> int {
+          constexpr bool F = decltype(full)::value;
+          trimul_bwd_prologue_side_kernel<CZ, CH, 0, F><<<grid, 512, 0, st>>>(
+              (const bf16*)z, mask, a.pda, (bf16*)dz, a.cm_stack, a.cm_xi, a.cm_dzn, w, a.wt, a.wgt,
+              a.part_dzn, (int)B, (int)N, Np, pitch, eps_in, tiles);
+          GTK_LAUNCH_CHECK();
+          trimul_bwd_prologue_side_kernel<CZ, CH, 1, F><<<grid, 512, 0, st>>>(
+              (const bf16*)z, mask, a.pdb, (bf16*)dz, a.cm_stack, a.cm_xi, a.cm_dzn, w, a.wt, a.wgt,
+              a.part_dzn, (int)B, (int)N, Np, pitch, eps_in, tiles);
+          GTK_LAUNCH_CHECK();
+          return 0;
+        };
+        // whole 32-pair tiles on one row: the staged channel-major path
+        if ((rc = N % 32 == 0 ? side(std::true_type{}) : side(std::false_type{}))) return rc;
+        sides = true;
+      }
+    }
+    if (!sides)
       trimul_bwd_prologue_kernel<T, CZ, CH><<<(unsigned)((tiles + 3) / 4), 256, 0, st>>>(
           (const T*)z, mask, a.pda, a.pdb, (T*)dz, a.cm_stack, a.cm_xi, a.cm_dzn, w, a.wt, a.wgt,
           (int)B, (int)N, Np, pitch, eps_in);
-    }
     GTK_LAUNCH_CHECK();
   }
   // 5. weight gradients

@@ -85,6 +85,20 @@ def _np(t):
 @pytest.mark.parametrize("outgoing", [True, False])
 @pytest.mark.parametrize("N,c", [(64, 128), (37, 64), (130, 128)])
 def test_tri_mul_backward(dname, outgoing, N, c):
+    _tri_mul_backward_case(dname, outgoing, N, c)
+
+
+@pytest.mark.parametrize("outgoing", [True, False])
+@pytest.mark.parametrize("N", [64, 37])
+def test_tri_mul_backward_element_paths(monkeypatch, outgoing, N):
+    """bf16 through the element-pointer kernels, the path taken where the
+    buffers' byte offsets exceed 32 bits (N above about 2900), selected here
+    at a small N by GENIE_TK_ELEMENT_PATHS."""
+    monkeypatch.setenv("GENIE_TK_ELEMENT_PATHS", "1")
+    _tri_mul_backward_case("bf16", outgoing, N, 128)
+
+
+def _tri_mul_backward_case(dname, outgoing, N, c):
     log(f"tri_mul backward {dname} outgoing={outgoing} N={N} c={c}")
     dt = DT[dname]
     P = H.draw_params(H.tri_mul_shapes(128, c), seed=N + c, ln_random=True, bias_random=True)
