@@ -29,6 +29,7 @@
 // kept separately (not m + log l): for such a row m = -1e9 and fp32 cannot
 // hold -1e9 + log l.
 #include <algorithm>
+#include <cstdlib>
 #include <cmath>
 #include <type_traits>
 
@@ -1835,8 +1836,11 @@ static int bwd_triattn(const void* x, const float* mask, const void* dy,
     StageTimer timer("triattn_bwd_pro", st);
     bool lds = false;
     if constexpr (std::is_same<T, bf16>::value) {
-      // the LDS kernel addresses cm_stack through 32-bit offsets
-      if ((int64_t)4 * CH * pitch * 2 < (1ll << 31)) {
+      // the LDS kernel addresses cm_stack through 32-bit offsets (N up to
+      // about 1440 at B = 1); GENIE_TK_ELEMENT_PATHS=1 selects the
+      // element-pointer kernel at any size (for tests)
+      const char* ep = std::getenv("GENIE_TK_ELEMENT_PATHS");
+      if ((int64_t)4 * CH * pitch * 2 < (1ll << 31) && !(ep && ep[0] == '1')) {
         const int grid = (int)std::min<int64_t>(device_cus(), (rowtiles + 7) / 8);
         attn_bwd_pro_lds_kernel<C, H><<<grid, 512, 0, st>>>((const bf16*)x, (bf16*)dx, a.w, a.b, (int)B,
                                                             (int)N, np, starting, eps, rowtiles);

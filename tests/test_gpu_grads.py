@@ -189,6 +189,15 @@ def test_tri_attn_backward_n264(starting):
     _tri_attn_backward_case("bf16", starting, 264, [258], inner_mask=0.05)
 
 
+@pytest.mark.parametrize("starting", [True, False])
+def test_tri_attn_backward_element_paths(monkeypatch, starting):
+    """bf16 with the prologue backward's element-pointer kernel, the path
+    taken where the channel-major buffers' byte offsets exceed 32 bits (N
+    above about 1440), selected here at a small N by GENIE_TK_ELEMENT_PATHS."""
+    monkeypatch.setenv("GENIE_TK_ELEMENT_PATHS", "1")
+    _tri_attn_backward_case("bf16", starting, 77, [77, 71])
+
+
 def test_tri_attn_backward_runs_the_kernels(monkeypatch):
     P = H.draw_params(H.tri_attn_shapes(128, 128, 4), seed=11, bias_random=True)
     mod = triattn_module(P, False, 4, torch.bfloat16)
