@@ -235,6 +235,220 @@ __global__ __launch_bounds__(256) void trimul_bwd_epilogue_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// 2b. bf16 epilogue backward for whole tiles (N % 32 == 0) of the shapes whose
+//     forward packing folds the LayerNorm affines: the same algebra as the
+//     kernel above in persistent 4-wave blocks with W_g, W_z and W_z^T
+//     (96 KiB at c_z = c = 128), b_g, b_z and gamma_out in LDS.  The kernel
+//     above reads the three matrices from L2 for every 32-pair tile.
+// ---------------------------------------------------------------------------
+template <int CZ, int CH>
+__global__ __launch_bounds__(256) void trimul_bwd_epilogue_lds_kernel(
+    const bf16* __restrict__ z, const bf16* __restrict__ px, const bf16* __restrict__ dy,
+    bf16* __restrict__ pdx, bf16* __restrict__ cm_dp, bf16* __restrict__ cm_dg, bf16* __restrict__ cm_xo,
+    bf16* __restrict__ cm_dxo, TriMulPacked<bf16> w, const bf16* __restrict__ wzt, int B, int N, int Np,
+    int64_t pitch, float eps_in, float eps_out, int64_t ntiles) {
+  static_assert(trimul_folded<CZ, CH>(), "the LayerNorm affines are in the packed weights");
+  constexpr int XPITCH = CH + 8;
+  constexpr int PG = CZ * CZ, PZ = CZ * CH;
+  __shared__ __attribute__((aligned(1024))) bf16 wl[PG + 2 * PZ];
+  __shared__ __attribute__((aligned(16))) bf16 xs[4][32 * XPITCH];
+  __shared__ __attribute__((aligned(16))) bf16 cst[4][kCmTile];
+  __shared__ __attribute__((aligned(16))) float bl[2 * CZ + CH];
+  copy_to_lds_async(wl, w.w_g, PG * 2);
+  copy_to_lds_async(wl + PG, w.w_z, PZ * 2);
+  copy_to_lds_async(wl + PG + PZ, wzt, PZ * 2);
+  for (int t = threadIdx.x; t < CZ; t += blockDim.x) {
+    bl[t] = w.b_g[t];
+    bl[CZ + t] = w.b_z[t];
+  }
+  for (int t = threadIdx.x; t < CH; t += blockDim.x) bl[2 * CZ + t] = w.ln_out_w[t];
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  const bf16* const wg = wl;
+  const bf16* const wz = wl + PG;
+  const bf16* const wzl = wl + PG + PZ;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = wave_id();
+  bf16* const sw = cst[wave];
+  bf16* const s = xs[wave];
+  const int half = lane >> 5;
+  const int t32 = lane & 31;
+  const int jtiles = Np / 32;
+  const int64_t plane = (int64_t)Np * Np;
+  const uint32_t pvo = cm_store_voff(plane), cvo = cm_store_voff(pitch);
+  for (int64_t tile = (int64_t)blockIdx.x * 4 + wave; tile < ntiles; tile += (int64_t)gridDim.x * 4) {
+    const int jt = (int)(tile % jtiles);
+    const int i = (int)((tile / jtiles) % Np);
+    const int b = (int)(tile / ((int64_t)jtiles * Np));
+    const int j = jt * 32 + t32;
+    // per-tile reads of the LDS vectors through an opaque index (hoisted out
+    // of the tile loop they would stay in registers)
+    const int oz = opaque_zero();
+    const bf16* const d0 = pdx + (int64_t)b * CH * plane + (int64_t)i * Np + jt * 32;
+    const auto drs = buf_rsrc(d0, (uint32_t)(CH * plane * 2));
+    if (i >= N || jt * 32 >= N) {
+      // padding positions of the dX planes: zero
+      float zf[16];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) zf[k] = 0.f;
+#pragma unroll
+      for (int nt = 0; nt < CH / 32; ++nt) cm_store_tile(sw, zf, drs, pvo, (uint32_t)(nt * 32 * plane) * 2, plane);
+      continue;
+    }
+    const int64_t pair = ((int64_t)b * N + i) * N + j;  // every pair of the tile is valid
+    const int64_t pair0 = ((int64_t)b * N + i) * N + jt * 32;
+
+    // gate s = sigmoid(LN_in(z) W_g^T + b_g), accumulator layout
+    f32x16 sg[CZ / 32];
+    {
+      RowHalf<CZ> rh;
+      load_row_half<bf16, CZ>(rh, z + pair * CZ, true);
+      const f32x2 st = row_stats<CZ>(rh, eps_in);
+      Frag<bf16> xf[CZ / 16];
+      ln_to_frags<bf16, CZ>(xf, rh, st);
+#pragma unroll
+      for (int nt = 0; nt < CZ / 32; ++nt) {
+        f32x16 acc = zero16();
+#pragma unroll
+        for (int ks = 0; ks < CZ / 16; ++ks) {
+          Frag<bf16> wf;
+          load_wfrag_lds(wf, wg, nt, ks, CZ / 16);
+          mma(acc, wf, xf[ks]);
+        }
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const f32x4 bg = *reinterpret_cast<const f32x4*>(bl + nt * 32 + 8 * g + 4 * half + oz);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[4 * g + r] = gate_from_u(acc[4 * g + r] + bg[r]);
+        }
+        sg[nt] = acc;
+      }
+    }
+
+    // x tile X[b][c][i][jt*32 ..] -> LDS [pair][c]
+    {
+      constexpr int CPR = 4;  // 16-byte chunks of a channel's 32 pairs
+      const bf16* xb = px + (int64_t)b * CH * plane + (int64_t)i * Np + jt * 32;
+#pragma unroll 4
+      for (int id = lane; id < CH * CPR; id += 64) {
+        const int c = id / CPR, part = id % CPR;
+        const f32x4 raw = *reinterpret_cast<const f32x4*>(xb + (int64_t)c * plane + part * 8);
+        const bf16* e = reinterpret_cast<const bf16*>(&raw);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) s[(part * 8 + k) * XPITCH + c] = e[k];
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    RowHalf<CH> xh;
+    {
+      const bf16* sr = s + t32 * XPITCH + half * (CH / 2);
+#pragma unroll
+      for (int ch = 0; ch < CH / 16; ++ch) {
+        Frag<bf16> f;
+        f.load(sr + ch * 8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xh.v[ch * 8 + e] = f.get(e);
+      }
+    }
+    const f32x2 so = row_stats<CH>(xh, eps_out);
+    Frag<bf16> yf[CH / 16];
+    ln_to_frags<bf16, CH>(yf, xh, so);
+
+    // dp = dy s, dg_pre = dy p s (1 - s)
+    Frag<bf16> dpf[CZ / 16];
+    const auto prs = buf_rsrc(cm_dp + pair0, (uint32_t)(CZ * pitch * 2));
+    const auto grs = buf_rsrc(cm_dg + pair0, (uint32_t)(CZ * pitch * 2));
+#pragma unroll
+    for (int nt = 0; nt < CZ / 32; ++nt) {
+      f32x16 pacc = zero16();
+#pragma unroll
+      for (int ks = 0; ks < CH / 16; ++ks) {
+        Frag<bf16> wf;
+        load_wfrag_lds(wf, wz, nt, ks, CH / 16);
+        mma(pacc, wf, yf[ks]);
+      }
+      float dpv[16], dgv[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c0 = nt * 32 + 8 * g + 4 * half;
+        const f32x4 d4 = load4f(dy + pair * CZ + c0);
+        const f32x4 bz = *reinterpret_cast<const f32x4*>(bl + CZ + c0 + oz);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float sv = sg[nt][4 * g + r];
+          const float pv = pacc[4 * g + r] + bz[r];
+          dpv[4 * g + r] = d4[r] * sv;
+          dgv[4 * g + r] = d4[r] * pv * sv * (1.f - sv);
+        }
+      }
+      const uint32_t so2 = (uint32_t)(nt * 32 * pitch) * 2;
+      cm_store_tile(sw, dpv, prs, cvo, so2, pitch);
+      cm_store_tile(sw, dgv, grs, cvo, so2, pitch);
+      vals_to_frags<bf16>(&dpf[2 * nt], dpv);
+    }
+
+    // dxn = dp W_z  (outputs over c, accumulator layout)
+    f32x16 dxn[CH / 32];
+#pragma unroll
+    for (int nt = 0; nt < CH / 32; ++nt) {
+      dxn[nt] = zero16();
+#pragma unroll
+      for (int ks = 0; ks < CZ / 16; ++ks) {
+        Frag<bf16> wf;
+        load_wfrag_lds(wf, wzl, nt, ks, CZ / 16);
+        mma(dxn[nt], wf, dpf[ks]);
+      }
+    }
+
+    // LayerNorm backward: x_hat from the LDS tile, dx_hat = gamma * dxn
+    const bf16* sr = s + t32 * XPITCH;
+    float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+    for (int nt = 0; nt < CH / 32; ++nt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c0 = nt * 32 + 8 * g + 4 * half;
+        const f32x4 lw = *reinterpret_cast<const f32x4*>(bl + 2 * CZ + c0 + oz);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float xhat = (to_f32(sr[c0 + r]) - so[0]) * so[1];
+          const float dxh = lw[r] * dxn[nt][4 * g + r];
+          s1 += dxh;
+          s2 += dxh * xhat;
+        }
+      }
+    s1 += xor32(s1);
+    s2 += xor32(s2);
+    const float m1 = s1 * (1.0f / CH), m2 = s2 * (1.0f / CH);
+    const auto xrs = buf_rsrc(cm_xo + pair0, (uint32_t)(CH * pitch * 2));
+    const auto nrs = buf_rsrc(cm_dxo + pair0, (uint32_t)(CH * pitch * 2));
+#pragma unroll
+    for (int nt = 0; nt < CH / 32; ++nt) {
+      float xv[16], dv[16], dn[16];
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c0 = nt * 32 + 8 * g + 4 * half;
+        const f32x4 lw = *reinterpret_cast<const f32x4*>(bl + 2 * CZ + c0 + oz);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float xhat = (to_f32(sr[c0 + r]) - so[0]) * so[1];
+          const float dxh = lw[r] * dxn[nt][4 * g + r];
+          xv[4 * g + r] = xhat;
+          dv[4 * g + r] = so[1] * (dxh - m1 - xhat * m2);
+          dn[4 * g + r] = dxn[nt][4 * g + r];
+        }
+      }
+      cm_store_tile(sw, dv, drs, pvo, (uint32_t)(nt * 32 * plane) * 2, plane);
+      const uint32_t so2 = (uint32_t)(nt * 32 * pitch) * 2;
+      cm_store_tile(sw, xv, xrs, cvo, so2, pitch);
+      cm_store_tile(sw, dn, nrs, cvo, so2, pitch);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // 4. Prologue backward.  Tiles over valid rows; da/db planes in pair
 //    orientation [b][c][i][j].
 // ---------------------------------------------------------------------------
@@ -728,9 +942,24 @@ static int bwd_trimul(const void* z, const float* mask, const void* dy,
               a.cm_xo, a.cm_dxo, w, a.wzt, (int)B, (int)N, Np, pitch, eps_in, eps_out);
     };
     using BF = std::integral_constant<bool, sizeof(T) == 2>;
-    if (!fits32) epi(std::false_type{}, std::false_type{});
-    else if (sizeof(T) == 2 && N % 32 == 0) epi(BF{}, std::true_type{});
-    else epi(std::false_type{}, std::true_type{});
+    bool lds = false;
+    if constexpr (sizeof(T) == 2 && trimul_folded<CZ, CH>()) {
+      if (fits32 && N % 32 == 0) {
+        const int grid = (int)std::min<int64_t>(device_cus(), (tiles + 3) / 4);
+        trimul_bwd_epilogue_lds_kernel<CZ, CH><<<grid, 256, 0, st>>>(
+            (const bf16*)z, a.px, (const bf16*)dy, a.pdx, a.cm_dp, a.cm_stack + (int64_t)4 * CH * pitch, a.cm_xo,
+            a.cm_dxo, w, a.wzt, (int)B, (int)N, Np, pitch, eps_in, eps_out, tiles);
+        lds = true;
+      }
+    }
+    if (lds) {
+    } else if (!fits32) {
+      epi(std::false_type{}, std::false_type{});
+    } else if (sizeof(T) == 2 && N % 32 == 0) {
+      epi(BF{}, std::true_type{});
+    } else {
+      epi(std::false_type{}, std::true_type{});
+    }
     GTK_LAUNCH_CHECK();
   }
   // 3. contraction backward (px is free from here on: it takes dX^T)
