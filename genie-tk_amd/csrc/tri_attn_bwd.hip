@@ -745,14 +745,22 @@ __device__ __forceinline__ float rh_lse2(const AttnBwdBufs<bf16>& bf, int64_t id
   return row_valid ? (bf.mrow[idx] - logf(li)) * kLog2e : -log2f(li);
 }
 
+// l in [2^-60, 2^64], tested on the bits: positive floats order as unsigned
+// integers; NaN, zero, negative values and infinity fall outside.
+__device__ __forceinline__ bool l_in_range_bits(float l) {
+  return __float_as_uint(l) - 0x21800000u <= 0x5F800000u - 0x21800000u;
+}
+
 // Forward recompute: block (row, head), wave w owns query tiles w, w + 8, ...;
-// lane = query.  Online softmax over the key tiles with the exact running
-// maximum; writes O (normalised), m (natural units) and 1/l like
-// attn_bwd_fwd_kernel.  Padded queries attend uniformly, so that their O,
+// lane = query.  A pass without a running maximum (m = 0, as in the forward
+// flash kernel), and where its l leaves the safe range an online softmax over
+// the key tiles with the exact running maximum; writes O (normalised), m
+// (natural units) and 1/l like attn_bwd_fwd_kernel.  Padded queries attend uniformly, so that their O,
 // m and l stay finite.
 template <int NPM>
 __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_fwd_rh_kernel(AttnBwdBufs<bf16> bf, int B,
-                                                                     int N, int np, float scale) {
+                                                                     int N, int np, float scale,
+                                                                     int exact_only) {
   constexpr int H = 4;
   __shared__ __attribute__((aligned(1024))) char ks[NPM * 64];
   __shared__ __attribute__((aligned(1024))) char vs[NPM * 64];
@@ -794,10 +802,8 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_fwd_rh_kernel(AttnBwdB
     // scores taken as 0 (uniform attention): rows without a valid key, padded queries
     const bool uni = !row_valid || q >= N;
     const float* btile = bT + (int64_t)qt * nt * 1024;
-    float m2 = -INFINITY, l = 0.f;
-    f32x16 o = zero16();
-    for (int kt = 0; kt < nk; ++kt) {
-      const char* ktile = ks + kt * 2048;
+    // scores of key tile kt in log2 units, excluded keys at -inf
+    auto scores = [&](int kt, float* s2) {
       f32x16 sc = zero16();
       if (row_valid) {
 #pragma unroll
@@ -807,9 +813,8 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_fwd_rh_kernel(AttnBwdB
           for (int rr = 0; rr < 4; ++rr) sc[4 * g + rr] = v[rr];
         }
 #pragma unroll
-        for (int m = 0; m < 2; ++m) mma(sc, lds_frag(ktile + off.nrm[m]), qf[m]);  // S^T: rows key, cols q
+        for (int m = 0; m < 2; ++m) mma(sc, lds_frag(ks + kt * 2048 + off.nrm[m]), qf[m]);  // S^T: rows key, cols q
       }
-      float s2[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) s2[e] = uni ? 0.f : sc[e] * c2;
       const unsigned kx = __builtin_amdgcn_readlane(kxv, kt);
@@ -821,29 +826,59 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_fwd_rh_kernel(AttnBwdB
           for (int rr = 0; rr < 4; ++rr)
             if (__builtin_amdgcn_ubfe(kl, 8 * g + rr, 1)) s2[4 * g + rr] = -INFINITY;
       }
-      float mt = s2[0];
-#pragma unroll
-      for (int e = 1; e < 16; ++e) mt = fmaxf(mt, s2[e]);
-      mt = fmaxf(mt, __shfl_xor(mt, 32));
-      const float mn = fmaxf(m2, mt);
-      const bool none = mn == -INFINITY;  // no key so far
-      const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m2 - mn);
-      float pv[16], ps = 0.f;
+    };
+    // Fast pass: P = 2^s with no running maximum (m = 0), exact while every
+    // 2^s stays in range, which l shows: l in [2^-60, 2^64] (the forward
+    // flash kernel's test).  Otherwise (or with exact_only, for tests) the
+    // exact pass below redoes the tile.
+    float m2 = 0.f, l = 0.f;
+    f32x16 o = zero16();
+    for (int kt = 0; !exact_only && kt < nk; ++kt) {
+      float s2[16], pv[16], ps = 0.f;
+      scores(kt, s2);
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        pv[e] = none ? 0.f : __builtin_amdgcn_exp2f(s2[e] - mn);
+        pv[e] = __builtin_amdgcn_exp2f(s2[e]);
         ps += pv[e];
       }
-      l = l * alpha + ps;
-      m2 = mn;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) o[e] *= alpha;
+      l += ps;
       Frag<bf16> fp[2];
       vals_to_frags<bf16>(fp, pv);
 #pragma unroll
       for (int gp = 0; gp < 2; ++gp) mma(o, lds_frag_tr(vs + kt * 2048, off, gp), fp[gp]);  // O^T += V^T P^T
     }
     l += __shfl_xor(l, 32);
+    if (exact_only || __ballot(!l_in_range_bits(l)) != 0ull) {
+      m2 = -INFINITY;
+      l = 0.f;
+      o = zero16();
+      for (int kt = 0; kt < nk; ++kt) {
+        float s2[16];
+        scores(kt, s2);
+        float mt = s2[0];
+#pragma unroll
+        for (int e = 1; e < 16; ++e) mt = fmaxf(mt, s2[e]);
+        mt = fmaxf(mt, __shfl_xor(mt, 32));
+        const float mn = fmaxf(m2, mt);
+        const bool none = mn == -INFINITY;  // no key so far
+        const float alpha = none ? 1.f : __builtin_amdgcn_exp2f(m2 - mn);
+        float pv[16], ps = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          pv[e] = none ? 0.f : __builtin_amdgcn_exp2f(s2[e] - mn);
+          ps += pv[e];
+        }
+        l = l * alpha + ps;
+        m2 = mn;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) o[e] *= alpha;
+        Frag<bf16> fp[2];
+        vals_to_frags<bf16>(fp, pv);
+#pragma unroll
+        for (int gp = 0; gp < 2; ++gp) mma(o, lds_frag_tr(vs + kt * 2048, off, gp), fp[gp]);  // O^T += V^T P^T
+      }
+      l += __shfl_xor(l, 32);
+    }
     const float li = 1.0f / l;
     bf16* O = bf.o + (rh * np + q) * AD;
 #pragma unroll
@@ -1762,8 +1797,18 @@ static int bwd_triattn(const void* x, const float* mask, const void* dy,
   {
     StageTimer timer("triattn_bwd_fwd", st);
     if constexpr (std::is_same<T, bf16>::value) {
-      if (npm) rh_launch(attn_bwd_fwd_rh_kernel<256>, attn_bwd_fwd_rh_kernel<512>, attn_bwd_fwd_rh_kernel<1024>);
-      else attn_bwd_fwd_kernel<T, H><<<g4(headtiles), 256, 0, st>>>(a.b, (int)B, (int)N, np, scale);
+      if (npm) {
+        // GENIE_TK_EXACT_SOFTMAX=1: the exact online softmax for every query
+        // tile (for tests; otherwise only where the pass without a running
+        // maximum leaves its range)
+        const char* ex = std::getenv("GENIE_TK_EXACT_SOFTMAX");
+        const int exact_only = ex && ex[0] == '1';
+        auto k = npm == 256 ? attn_bwd_fwd_rh_kernel<256> : npm == 512 ? attn_bwd_fwd_rh_kernel<512>
+                                                                       : attn_bwd_fwd_rh_kernel<1024>;
+        k<<<(unsigned)rblocks, 64 * kRhWaves, 0, st>>>(a.b, (int)B, (int)N, np, scale, exact_only);
+      } else {
+        attn_bwd_fwd_kernel<T, H><<<g4(headtiles), 256, 0, st>>>(a.b, (int)B, (int)N, np, scale);
+      }
     } else {
       attn_bwd_fwd_kernel<T, H><<<g4(headtiles), 256, 0, st>>>(a.b, (int)B, (int)N, np, scale);
     }

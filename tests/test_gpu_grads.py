@@ -190,6 +190,17 @@ def test_tri_attn_backward_n264(starting):
 
 
 @pytest.mark.parametrize("starting", [True, False])
+def test_tri_attn_backward_exact_recompute(monkeypatch, starting):
+    """bf16 with the forward recompute's exact online softmax for every query
+    tile (GENIE_TK_EXACT_SOFTMAX=1).  The kernel takes it where the pass
+    without a running maximum leaves l's safe range: scores beyond about 60
+    log2 units, where bf16 inputs are too coarse for a well-conditioned
+    gradient check."""
+    monkeypatch.setenv("GENIE_TK_EXACT_SOFTMAX", "1")
+    _tri_attn_backward_case("bf16", starting, 77, [77, 71], inner_mask=0.05)
+
+
+@pytest.mark.parametrize("starting", [True, False])
 def test_tri_attn_backward_element_paths(monkeypatch, starting):
     """bf16 with the prologue backward's element-pointer kernel, the path
     taken where the channel-major buffers' byte offsets exceed 32 bits (N
