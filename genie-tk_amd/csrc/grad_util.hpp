@@ -462,6 +462,127 @@ __global__ __launch_bounds__(256) void wgrad_kernel(const T* __restrict__ G, con
   }
 }
 
+// bf16 form of wgrad_kernel with the k stages copied straight into a 4-stage
+// LDS ring (global_load_lds_dwordx4, three stages in flight, no VGPR
+// staging).  The stage is 128 + TN rows of 128 bytes, 16-byte chunk c of row r
+// at c ^ ((r ^ (r >> 3)) & 7), so the fragment reads are bank-conflict free;
+// copy n of a stage moves rows 8n .. 8n + 7 (1 KiB), wave w the copies
+// w, w + 4, ...  RS: the waves of n half 0 add the G fragments they read.
+template <int TN, bool RS>
+__global__ __launch_bounds__(256) void wgrad_ring_kernel(const bf16* __restrict__ G, const bf16* __restrict__ X,
+                                                         float* __restrict__ part, int M, int Nn, int64_t pitch,
+                                                         int64_t kc, int nsplit, float* __restrict__ rs) {
+  constexpr int BK = 64, NS = 4;
+  constexpr int ROWS = 128 + TN;
+  constexpr int CPW = ROWS / 8 / 4;  // copies per wave per stage
+  constexpr int MBN = TN / 64;       // 32-wide blocks per wave in n
+  __shared__ __attribute__((aligned(1024))) char ring[NS][ROWS * 128];
+
+  const int mtiles = M / 128, ntiles = Nn / TN;
+  // the m and n tiles of one split are consecutive logical blocks, and each
+  // XCD takes a contiguous range of them (the grid is padded to a multiple of
+  // 8), so the blocks that read a split's X chunk share that XCD's L2
+  const int64_t lin = xcd_remap(blockIdx.x, gridDim.x);
+  if (lin >= (int64_t)nsplit * mtiles * ntiles) return;
+  const int mt = (int)(lin % mtiles);
+  const int ntl = (int)((lin / mtiles) % ntiles);
+  const int s = (int)(lin / ((int64_t)mtiles * ntiles));
+  const int m0 = mt * 128, n0 = ntl * TN;
+  const int64_t kbeg = (int64_t)s * kc;
+  const int64_t kend = kbeg + kc < pitch ? kbeg + kc : pitch;
+  const int S = kbeg < kend ? (int)((kend - kbeg) / BK) : 0;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id(), half = lane >> 5;
+  const int wm = (wave >> 1) * 64, wn = (wave & 1) * (TN / 2);
+  f32x16 acc[2][MBN];
+#pragma unroll
+  for (int x = 0; x < 2; ++x)
+#pragma unroll
+    for (int y = 0; y < MBN; ++y) acc[x][y] = zero16();
+
+  // per-lane byte offsets of copy u (n = wave + 4u): row n*8 + lane/8,
+  // physical chunk lane%8 holding logical chunk (lane%8) ^ swz(row)
+  uint32_t voff[CPW];
+#pragma unroll
+  for (int u = 0; u < CPW; ++u) {
+    const int n = wave + 4 * u, j = lane >> 3;
+    voff[u] = (uint32_t)((j * pitch + 8 * (((lane & 7) ^ (j ^ n)) & 7)) * 2);
+  }
+  const uint32_t ring_lds = lds_addr(ring);
+  auto issue = [&](int st) {
+    const int64_t k0 = kbeg + (int64_t)st * BK;
+#pragma unroll
+    for (int u = 0; u < CPW; ++u) {
+      const int n = wave + 4 * u;
+      const int row = 8 * n;
+      const bf16* base = row < 128 ? G + (int64_t)(m0 + row) * pitch + k0 : X + (int64_t)(n0 + row - 128) * pitch + k0;
+      g2lds16_sv(base, voff[u], ring_lds + (uint32_t)((st % NS) * ROWS * 128 + n * 1024));
+    }
+  };
+  auto swz = [](int r) { return (r ^ (r >> 3)) & 7; };
+  float rsum[2] = {0.f, 0.f};
+  const bool do_rs = RS && ntl == 0 && (wave & 1) == 0;
+
+  for (int st = 0; st < 3 && st < S; ++st) issue(st);
+  for (int st = 0; st < S; ++st) {
+    // this wave's copies of stage st landed: behind them are those of the
+    // (at most two) stages issued after it
+    const int later = S - 1 - st < 2 ? S - 1 - st : 2;
+    if (later == 2) __builtin_amdgcn_s_waitcnt(vmcnt_imm<2 * CPW>());
+    else if (later == 1) __builtin_amdgcn_s_waitcnt(vmcnt_imm<CPW>());
+    else __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
+    barrier_only();  // stage st visible to every wave; stage st - 1 fully read
+    if (st + 3 < S) issue(st + 3);
+    const char* sb = ring[st % NS];
+#pragma unroll
+    for (int kk = 0; kk < BK / 16; ++kk) {
+      const int lc = kk * 2 + half;  // logical 16-byte chunk
+      Frag<bf16> fg[2], fx[MBN];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const int r = wm + 32 * x + (lane & 31);
+        fg[x].load(reinterpret_cast<const bf16*>(sb + r * 128 + 16 * (lc ^ swz(r))));
+      }
+#pragma unroll
+      for (int y = 0; y < MBN; ++y) {
+        const int r = 128 + wn + 32 * y + (lane & 31);
+        fx[y].load(reinterpret_cast<const bf16*>(sb + r * 128 + 16 * (lc ^ swz(r))));
+      }
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < MBN; ++y) mma(acc[x][y], fx[y], fg[x]);  // rows n, cols m
+      if (do_rs) {
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) rsum[x] += fg[x].get(e);
+      }
+    }
+  }
+  if (do_rs) {
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      const float v = rsum[x] + xor32(rsum[x]);
+      if (half == 0) rs[(int64_t)s * M + m0 + wm + 32 * x + (lane & 31)] = v;
+    }
+  }
+  // acc[x][y]: lane holds W[m = m0 + wm + 32x + (l&31)][n = n0 + wn + 32y + 8g + 4h + r]
+  float* out = part + (int64_t)s * M * Nn;
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    const int m = m0 + wm + 32 * x + (lane & 31);
+#pragma unroll
+    for (int y = 0; y < MBN; ++y)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int n = n0 + wn + 32 * y + 8 * g + 4 * half;
+        store4(out + (int64_t)m * Nn + n, acc[x][y][4 * g], acc[x][y][4 * g + 1],
+               acc[x][y][4 * g + 2], acc[x][y][4 * g + 3]);
+      }
+  }
+}
+
 struct WgradPlan {
   int nsplit;
   int64_t kc;
@@ -477,9 +598,14 @@ inline int wgrad_n_rows(int Nn) { return Nn <= 64 ? 64 : (Nn + 127) / 128 * 128;
 // rows of a buffer used as G of one product and X of another
 inline int wgrad_rows(int rows) { return wgrad_m_rows(rows); }
 
+// Splits: about one block per CU (MI355X: 256) and never more than that, so
+// that no straggler round of a few blocks doubles the launch (515 blocks of
+// 2 per CU ran as two rounds of one block's time each); the bf16 ring kernel
+// holds one block per CU.
+constexpr int kWgradBlocks = 256;
 inline WgradPlan wgrad_plan(int M, int64_t pitch) {
   const int mtiles = wgrad_m_rows(M) / 128;
-  int64_t ns = (512 + mtiles - 1) / mtiles;
+  int64_t ns = kWgradBlocks / mtiles;
   const int64_t maxs = pitch / 64 > 0 ? pitch / 64 : 1;
   if (ns > maxs) ns = maxs;
   if (ns < 1) ns = 1;
@@ -583,8 +709,12 @@ inline int launch_wgrad(const T* G, const T* X, float* part, int M, int Nn, int6
   auto go = [&](auto tn, auto r) {
     constexpr int TN = decltype(tn)::value;
     const int64_t blocks = (int64_t)pl.nsplit * (Mp / 128) * (TN == 128 ? Np / 128 : 1);
-    wgrad_kernel<T, TN, decltype(r)::value><<<(unsigned)blocks, 256, 0, st>>>(G, X, part, Mp, Np, pitch,
-                                                                             pl.kc, pl.nsplit, rs);
+    if constexpr (sizeof(T) == 2)
+      wgrad_ring_kernel<TN, decltype(r)::value><<<(unsigned)((blocks + 7) / 8 * 8), 256, 0, st>>>(
+          (const bf16*)G, (const bf16*)X, part, Mp, Np, pitch, pl.kc, pl.nsplit, rs);
+    else
+      wgrad_kernel<T, TN, decltype(r)::value><<<(unsigned)blocks, 256, 0, st>>>(G, X, part, Mp, Np, pitch,
+                                                                               pl.kc, pl.nsplit, rs);
   };
   using I128 = std::integral_constant<int, 128>;
   using I64 = std::integral_constant<int, 64>;
