@@ -770,6 +770,30 @@ def config_table(torch, C, dev: str) -> int:
     return 0
 
 
+def fwd_bwd_run(torch, mods, z, mask, steps: int, warmup: int) -> int:
+    """Forward + backward (the input's and every parameter's gradient) of
+    tri-mul outgoing and tri-attn starting node, `steps` times each after
+    `warmup`; prints their median times as one JSON line."""
+    maskb = mask.to(torch.bfloat16)
+    out = {}
+    for name in ("tri_mul_out", "tri_att_start"):
+        mod = mods[name]
+        zg = z.detach().clone().requires_grad_(True)
+        dy = torch.randn_like(z)
+
+        def run():
+            zg.grad = None
+            for p in mod.parameters():
+                p.grad = None
+            mod(zg, maskb).backward(dy)
+        for _ in range(warmup):
+            run()
+        out[name] = round(statistics.median(event_time_ms(torch, run, steps)), 4)
+        print(f"[bench] {name} forward+backward {out[name]:.3f} ms", file=sys.stderr, flush=True)
+    print(json.dumps({"fwd_bwd_ms": out}))
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -791,6 +815,9 @@ def main() -> int:
                          "kernel-trace stats of `bench.py --only-step`")
     ap.add_argument("--only-step", action="store_true",
                     help="time the step and its kernels only (for counter collection)")
+    ap.add_argument("--only-fwd-bwd", action="store_true",
+                    help="no bench line: forward + backward of tri-mul outgoing and tri-attn "
+                         "starting at N (for a kernel trace of the backward kernels)")
     ap.add_argument("--only-ln", action="store_true",
                     help="no bench line: LayerNorm launches over rotating inputs at N=1024 and "
                          "N=512 (for HBM byte counters and a kernel trace), then --calibrate-copy")
@@ -833,6 +860,8 @@ def main() -> int:
     ln_w = torch.ones(C_Z, device=dev)
     ln_b = torch.zeros(C_Z, device=dev)
     mods = build_modules(torch, N, dev)
+    if args.only_fwd_bwd:
+        return fwd_bwd_run(torch, mods, z, mask, args.steps, args.warmup)
 
     ops = {
         "tri_mul_out": lambda: mods["tri_mul_out"](z, mask),

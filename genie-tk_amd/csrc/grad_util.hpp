@@ -44,6 +44,12 @@ __global__ void pack_acc_kernel(Tout* __restrict__ dst, const Tin* __restrict__ 
 template <typename Tout>
 inline int launch_pack_acc(Tout* dst, const void* src, int wdtype, int out_dim, int k_dim,
                            int64_t s_out, int64_t s_in, hipStream_t st) {
+  if (PackBatch* b = pack_batch()) {
+    batch_wjob(*b, sizeof(Tout) == 2, wdtype,
+               WJob{dst, src, out_dim, k_dim, s_out, s_in, 1.f, nullptr, packed_elems(out_dim, k_dim), Pad(),
+                    Pad(), 1});
+    return GTK_OK;
+  }
   const int64_t total = packed_elems(out_dim, k_dim);
   const int blocks = (int)((total + 255) / 256);
   if (wdtype == GTK_F32)

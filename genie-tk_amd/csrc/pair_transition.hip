@@ -455,6 +455,7 @@ static bool pt_shape_ok(int64_t c, int64_t n) { return (c == 128 || c == 64) && 
 template <typename T>
 static int pack_pt(const gtk_pair_transition_weights* w, int ci, int hid, void* packed, hipStream_t st) {
   const int wd = w->dtype;
+  PackScope batch(st);  // the packing launches issued as 3
   Carve cv(packed, SIZE_MAX);
   PtPackedT<T> p = carve_pt<T>(cv, ci, hid);
   int rc;
@@ -463,7 +464,8 @@ static int pack_pt(const gtk_pair_transition_weights* w, int ci, int hid, void* 
   if ((rc = launch_pack<T>(p.w1, w->w1, wd, hid, ci, ci, 1, 1.f, st, p.ln_w))) return rc;
   if ((rc = launch_fold_bias(p.b1, w->w1, w->b1, wd, p.ln_b, hid, ci, ci, 1, 1.f, st))) return rc;
   if ((rc = launch_pack_acc<T>(p.w2, w->w2, wd, ci, hid, hid, 1, st))) return rc;
-  return launch_to_f32(p.b2, w->b2, wd, ci, 1.f, 0.f, st);
+  if ((rc = launch_to_f32(p.b2, w->b2, wd, ci, 1.f, 0.f, st))) return rc;
+  return batch.flush();
 }
 
 template <typename T, int C, int HID>
@@ -522,13 +524,17 @@ static int bwd_pt(const void* p, const void* dy, const gtk_pair_transition_weigh
   const int64_t pitch = a.pitch;
   const int wd = wts->dtype;
   int rc;
-  if ((rc = pack_pt<T>(wts, C, HID, a.packed, st))) return rc;
   Carve pc(a.packed, SIZE_MAX);
   const PtPackedT<T> w = carve_pt<T>(pc, C, HID);
-  // W2^T as [hid][c] (element (u, o) = W2[o][u]); W1^T as [c][hid] for dh
-  // taken from the accumulators
-  if ((rc = launch_pack<T>(a.w2t, wts->w2, wd, HID, C, 1, HID, 1.f, st))) return rc;
-  if ((rc = launch_pack_acc<T>(a.w1t, wts->w1, wd, C, HID, 1, C, st))) return rc;
+  {
+    PackScope batch(st);  // the forward's packing and the transposed packs, batched
+    if ((rc = pack_pt<T>(wts, C, HID, a.packed, st))) return rc;
+    // W2^T as [hid][c] (element (u, o) = W2[o][u]); W1^T as [c][hid] for dh
+    // taken from the accumulators
+    if ((rc = launch_pack<T>(a.w2t, wts->w2, wd, HID, C, 1, HID, 1.f, st))) return rc;
+    if ((rc = launch_pack_acc<T>(a.w1t, wts->w1, wd, C, HID, 1, C, st))) return rc;
+    if ((rc = batch.flush())) return rc;
+  }
   {
     const int64_t ntiles = (rows + 31) / 32;
     GTK_REQUIRE((ntiles + 3) / 4 < (1ll << 31), GTK_EUNSUPPORTED, "pair transition backward: too many rows");

@@ -1715,6 +1715,7 @@ static int raw_attn_entry(const void* q, const void* k, const void* v, const flo
 template <typename T>
 static int pack_triattn(const gtk_tri_attn_weights* w, int cin, int ch, int H, void* packed,
                         hipStream_t st) {
+  PackScope batch(st);  // the packing launches issued as 3
   Carve cv(packed, SIZE_MAX);
   TriAttnPacked<T> p = carve_triattn<T>(cv, cin, ch, H);
   const int wd = w->dtype;
@@ -1743,7 +1744,7 @@ static int pack_triattn(const gtk_tri_attn_weights* w, int cin, int ch, int H, v
   // its input channels are the padded heads
   if ((rc = launch_pack<T>(p.w_o, w->o_w, wd, cin, chp, ch, 1, 1.f, st, nullptr, Pad(), heads))) return rc;
   if ((rc = launch_to_f32(p.b_o, w->o_b, wd, cin, 1.f, 0.f, st))) return rc;
-  return GTK_OK;
+  return batch.flush();
 }
 
 // chunk_rows > 0: attention rows in chunks of that many rows.

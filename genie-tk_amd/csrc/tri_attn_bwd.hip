@@ -1731,6 +1731,7 @@ template <typename T>
 static int pack_attn_bwd(const gtk_tri_attn_weights* wt, AttnBwdW<T>& w, int C, int H,
                          hipStream_t st) {
   const int CH = H * AD, wd = wt->dtype;
+  PackScope batch(st);  // the packing launches issued as 3
   int rc;
   if ((rc = launch_to_f32(w.ln_w, wt->ln_w, wd, C, 1.f, 1.f, st))) return rc;
   if ((rc = launch_to_f32(w.ln_b, wt->ln_b, wd, C, 1.f, 0.f, st))) return rc;
@@ -1747,7 +1748,8 @@ static int pack_attn_bwd(const gtk_tri_attn_weights* wt, AttnBwdW<T>& w, int C, 
   for (int k = 0; k < 4; ++k)
     if ((rc = launch_pack_acc<T>(wts[k], srcs[k], wd, C, CH, 1, C, st))) return rc;
   if ((rc = launch_pack<T>(w.wt_o, wt->o_w, wd, CH, C, 1, CH, 1.f, st))) return rc;
-  return launch_to_f32(w.wb_raw, wt->tri_w, wd, H * C, 1.f, 0.f, st);
+  if ((rc = launch_to_f32(w.wb_raw, wt->tri_w, wd, H * C, 1.f, 0.f, st))) return rc;
+  return batch.flush();
 }
 
 template <typename T, int C, int H>

@@ -1204,6 +1204,7 @@ static int raw_trimul(const void* a, const void* b, const float* mask, void* x, 
 // ---------------------------------------------------------------------------
 template <typename T>
 static int pack_trimul(const gtk_tri_mul_weights* w, int cz, int c, void* packed, hipStream_t st) {
+  PackScope batch(st);  // 16 packing launches issued as 3
   Carve cv(packed, SIZE_MAX);
   TriMulPacked<T> p = carve_trimul<T>(cv, cz, c);
   const int wd = w->dtype;
@@ -1236,7 +1237,7 @@ static int pack_trimul(const gtk_tri_mul_weights* w, int cz, int c, void* packed
     if ((rc = launch_fold_bias(l.bdst, l.wsrc, l.bsrc, wd, l.beta, l.out, l.in, l.in, 1, l.scale, st)))
       return rc;
   }
-  return GTK_OK;
+  return batch.flush();
 }
 
 // The bf16 kernels with LDS-resident weights are built for the module's

@@ -917,16 +917,22 @@ static int bwd_trimul(const void* z, const float* mask, const void* dy,
   const bool fits32 =
       (int64_t)std::max(CZ, CH) * std::max<int64_t>(pitch, (int64_t)Np * Np) * 2 < (1ll << 31) &&
       !(ep && ep[0] == '1');
-  // 0. weights
-  if ((rc = gtk_tri_mul_pack(wts, CZ, CH, dtype, a.packed, gtk_tri_mul_packed_size(CZ, CH, dtype), st)))
-    return rc;
+  // 0. weights: the forward's packing and the transposed packs, batched
+  //    into three launches
   Carve pc(a.packed, SIZE_MAX);
   TriMulPacked<T> w = carve_trimul<T>(pc, CZ, CH);
-  if ((rc = launch_pack_acc<T>(a.wzt, wts->z_w, wd, CH, CZ, 1, CH, st))) return rc;
-  const void* wsrc[4] = {wts->a_p_w, wts->a_g_w, wts->b_p_w, wts->b_g_w};
-  for (int k = 0; k < 4; ++k)
-    if ((rc = launch_pack_acc<T>(a.wt + k * packed_elems(CZ, CH), wsrc[k], wd, CZ, CH, 1, CZ, st))) return rc;
-  if ((rc = launch_pack_acc<T>(a.wgt, wts->g_w, wd, CZ, CZ, 1, CZ, st))) return rc;
+  {
+    PackScope batch(st);
+    if ((rc = gtk_tri_mul_pack(wts, CZ, CH, dtype, a.packed, gtk_tri_mul_packed_size(CZ, CH, dtype), st)))
+      return rc;
+    if ((rc = launch_pack_acc<T>(a.wzt, wts->z_w, wd, CH, CZ, 1, CH, st))) return rc;
+    const void* wsrc[4] = {wts->a_p_w, wts->a_g_w, wts->b_p_w, wts->b_g_w};
+    for (int k = 0; k < 4; ++k)
+      if ((rc = launch_pack_acc<T>(a.wt + k * packed_elems(CZ, CH), wsrc[k], wd, CZ, CH, 1, CZ, st)))
+        return rc;
+    if ((rc = launch_pack_acc<T>(a.wgt, wts->g_w, wd, CZ, CZ, 1, CZ, st))) return rc;
+    if ((rc = batch.flush())) return rc;
+  }
   // 1. forward planes
   if ((rc = trimul_recompute_planes(z, mask, a.packed, B, N, CZ, CH, outgoing, eps_in, dtype, a.pa,
                                     a.pb, a.px, st)))
