@@ -11,7 +11,8 @@ then.
 from __future__ import annotations
 
 import warnings
-from typing import Callable, List, Optional, Tuple
+import weakref
+from typing import Callable, Dict, List, Optional, Tuple
 
 import torch
 from torch import Tensor, nn
@@ -27,10 +28,29 @@ def needs_autograd(x: Tensor, module: nn.Module) -> bool:
     return x.requires_grad or any(p.requires_grad for p in module.parameters())
 
 
+# binary_mask results per live mask tensor: id -> (weak reference, version, result)
+_binary_seen: Dict[int, Tuple["weakref.ref", int, bool]] = {}
+
+
 def binary_mask(mask: Optional[Tensor]) -> bool:
     """True when every mask value is 0 or 1 (or there is no mask).  One
-    reduction and a host synchronisation: used only on the training path."""
-    return mask is None or bool(((mask == 0) | (mask == 1)).all())
+    reduction and a host synchronisation, used only on the training path and
+    remembered for the tensor until it is modified in place or freed: the
+    layers of a network share one mask, which then costs one synchronisation
+    instead of one per attention call."""
+    if mask is None:
+        return True
+    key = id(mask)
+    seen = _binary_seen.get(key)
+    if seen is not None and seen[0]() is mask and seen[1] == mask._version:
+        return seen[2]
+    result = bool(((mask == 0) | (mask == 1)).all())
+    if len(_binary_seen) >= 64:
+        _binary_seen.clear()
+    # the entry goes when the tensor does, before its id can be reused
+    _binary_seen[key] = (weakref.ref(mask, lambda _, k=key: _binary_seen.pop(k, None)),
+                         mask._version, result)
+    return result
 
 
 def warn_once(key: str, msg: str) -> None:

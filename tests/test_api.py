@@ -492,3 +492,33 @@ def test_channel_repetition_for_narrow_hidden_widths(c, outgoing):
         big.linear_z.weight.zero_()
         big.linear_z.weight[:, :c] = mod.linear_z.weight
     assert (big(z, m) - mod(z, m)).abs().max() > 1e-3
+
+
+def test_binary_mask_check_is_remembered_per_tensor():
+    """The training path's binary-mask check (a reduction and a host
+    synchronisation) runs once per mask tensor: again after an in-place
+    change, and its entry goes with the tensor."""
+    from genie_tk import _dispatch as D
+    m = torch.ones(2, 5, 5)
+    calls = []
+    orig = torch.Tensor.all
+
+    def counting_all(self, *a, **k):
+        calls.append(1)
+        return orig(self, *a, **k)
+
+    torch.Tensor.all = counting_all
+    try:
+        assert D.binary_mask(m) and D.binary_mask(m)
+        assert len(calls) == 1
+        m[0, 1, 2] = 0.5
+        assert not D.binary_mask(m)
+        assert len(calls) == 2
+        other = torch.zeros(3)
+        assert D.binary_mask(other)
+        n = len(D._binary_seen)
+        del other
+        assert len(D._binary_seen) == n - 1
+        assert D.binary_mask(None)
+    finally:
+        torch.Tensor.all = orig
