@@ -361,6 +361,23 @@ __device__ __forceinline__ void g2lds16(const void* gptr, void* lds_wave_base) {
       : "memory");
 }
 
+// 4 bytes per lane from global memory into LDS at (wave-uniform base) +
+// lane * 4: used to pull lines into L2 ahead of their real copies (the LDS
+// bytes are a scratch area nobody reads, and no VGPR is written, so nothing
+// depends on when the load lands).  Same ordering contract as g2lds16.
+__device__ __forceinline__ void g2lds4(const void* gptr, uint32_t lds) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(gptr), "s"(lds)
+      : "memory");
+}
+
 // LDS byte address of a __shared__ object, for the copies below.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_void_ptr)p);

@@ -751,6 +751,21 @@ __device__ __forceinline__ bool l_in_range_bits(float l) {
   return __float_as_uint(l) - 0x21800000u <= 0x5F800000u - 0x21800000u;
 }
 
+// One fp32 bias tile in fragment order (lane * 4 already in `p`): 4 loads of
+// 16 bytes a lane, and the accumulator they initialise.
+__device__ __forceinline__ void load_bias_tile(f32x4* dst, const float* p) {
+#pragma unroll
+  for (int g = 0; g < 4; ++g) dst[g] = *reinterpret_cast<const f32x4*>(p + g * 256);
+}
+__device__ __forceinline__ f32x16 bias_acc(const f32x4* v) {
+  f32x16 a;
+#pragma unroll
+  for (int g = 0; g < 4; ++g)
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) a[4 * g + rr] = v[g][rr];
+  return a;
+}
+
 // Forward recompute: block (row, head), wave w owns query tiles w, w + 8, ...;
 // lane = query.  A pass without a running maximum (m = 0, as in the forward
 // flash kernel), and where its l leaves the safe range an online softmax over
@@ -799,24 +814,21 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_fwd_rh_kernel(AttnBwdB
     Frag<bf16> qf[2];
 #pragma unroll
     for (int m = 0; m < 2; ++m) qf[m].load(qrow + 16 * m);
-    // scores taken as 0 (uniform attention): rows without a valid key, padded queries
-    const bool uni = !row_valid || q >= N;
+    // scores taken as 0 (uniform attention): rows without a valid key, padded
+    // queries (their scores are finite, so a zero factor gives 0)
+    const float c2l = (!row_valid || q >= N) ? 0.f : c2;
     const float* btile = bT + (int64_t)qt * nt * 1024;
-    // scores of key tile kt in log2 units, excluded keys at -inf
-    auto scores = [&](int kt, float* s2) {
-      f32x16 sc = zero16();
+    // scores of key tile kt in log2 units (bias tile in bias), excluded keys at -inf
+    auto scores = [&](int kt, float* s2, const f32x4* bias) {
+      f32x16 sc = bias_acc(bias);
       if (row_valid) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 v = *reinterpret_cast<const f32x4*>(btile + kt * 1024 + g * 256);
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) sc[4 * g + rr] = v[rr];
-        }
-#pragma unroll
         for (int m = 0; m < 2; ++m) mma(sc, lds_frag(ks + kt * 2048 + off.nrm[m]), qf[m]);  // S^T: rows key, cols q
+      } else {
+        sc = zero16();
       }
 #pragma unroll
-      for (int e = 0; e < 16; ++e) s2[e] = uni ? 0.f : sc[e] * c2;
+      for (int e = 0; e < 16; ++e) s2[e] = sc[e] * c2l;
       const unsigned kx = __builtin_amdgcn_readlane(kxv, kt);
       if (kx != 0u) {
         const unsigned kl = kx >> (4 * half);
@@ -830,12 +842,14 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_fwd_rh_kernel(AttnBwdB
     // Fast pass: P = 2^s with no running maximum (m = 0), exact while every
     // 2^s stays in range, which l shows: l in [2^-60, 2^64] (the forward
     // flash kernel's test).  Otherwise (or with exact_only, for tests) the
-    // exact pass below redoes the tile.
+    // exact pass below redoes the tile.  Bias tiles in two alternating
+    // register sets, loaded one key tile ahead.
     float m2 = 0.f, l = 0.f;
     f32x16 o = zero16();
-    for (int kt = 0; !exact_only && kt < nk; ++kt) {
+    auto fast_unit = [&](int kt, const f32x4* cur, f32x4* nxt) {
+      load_bias_tile(nxt, btile + (kt + 1 < nk ? kt + 1 : kt) * 1024);
       float s2[16], pv[16], ps = 0.f;
-      scores(kt, s2);
+      scores(kt, s2, cur);
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         pv[e] = __builtin_amdgcn_exp2f(s2[e]);
@@ -846,6 +860,14 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_fwd_rh_kernel(AttnBwdB
       vals_to_frags<bf16>(fp, pv);
 #pragma unroll
       for (int gp = 0; gp < 2; ++gp) mma(o, lds_frag_tr(vs + kt * 2048, off, gp), fp[gp]);  // O^T += V^T P^T
+    };
+    if (!exact_only) {
+      f32x4 ba[4], bb[4];
+      load_bias_tile(ba, btile);
+      for (int kt = 0; kt < nk; kt += 2) {
+        fast_unit(kt, ba, bb);
+        if (kt + 1 < nk) fast_unit(kt + 1, bb, ba);
+      }
     }
     l += __shfl_xor(l, 32);
     if (exact_only || __ballot(!l_in_range_bits(l)) != 0ull) {
@@ -854,7 +876,11 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_fwd_rh_kernel(AttnBwdB
       o = zero16();
       for (int kt = 0; kt < nk; ++kt) {
         float s2[16];
-        scores(kt, s2);
+        {
+          f32x4 bt[4];
+          load_bias_tile(bt, btile + kt * 1024);
+          scores(kt, s2, bt);
+        }
         float mt = s2[0];
 #pragma unroll
         for (int e = 1; e < 16; ++e) mt = fmaxf(mt, s2[e]);
@@ -892,14 +918,22 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_fwd_rh_kernel(AttnBwdB
 }
 
 // dK and dV: block (row, head), wave w owns key tiles w, w + 8, ...; lane = key.
+// Padded queries carry lse2 = +inf (P = 0) and D = 0; an excluded key's
+// column of dK^T and dV^T (its lane) is zeroed at the end instead of its P
+// values per tile: each column of an MFMA product reads only that column of
+// the B operand.  The bias tiles alternate between two register sets, so the
+// next tile's loads go out before the current one is used, without copies.
 template <int NPM>
 __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dkdv_rh_kernel(AttnBwdBufs<bf16> bf, int B,
                                                                       int N, int np, float scale) {
   constexpr int H = 4;
-  __shared__ __attribute__((aligned(1024))) char qs[NPM * 64];
-  __shared__ __attribute__((aligned(1024))) char dos[NPM * 64];
-  __shared__ __attribute__((aligned(16))) float lse_s[NPM];
-  __shared__ __attribute__((aligned(16))) float dd_s[NPM];
+  // lse2 and D first, so that their offsets fit the LDS instructions' 16-bit
+  // immediate; then Q and dO rows
+  __shared__ __attribute__((aligned(1024))) char lds[8 * NPM + 2 * NPM * 64];
+  float* const lse_s = reinterpret_cast<float*>(lds);
+  float* const dd_s = lse_s + NPM;
+  char* const qs = lds + 8 * NPM;
+  char* const dos = qs + NPM * 64;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, t32 = lane & 31;
@@ -914,8 +948,8 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dkdv_rh_kernel(AttnBwd
   const float* km_row = bf.kmask + br * np;
   const bool row_valid = rh_row_valid(km_row, N);
   for (int q = tid; q < np; q += 64 * kRhWaves) {
-    lse_s[q] = rh_lse2(bf, rh * np + q, row_valid);
-    dd_s[q] = bf.dd[rh * np + q];
+    lse_s[q] = q < N ? rh_lse2(bf, rh * np + q, row_valid) : INFINITY;
+    dd_s[q] = q < N ? bf.dd[rh * np + q] : 0.f;
   }
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
@@ -936,22 +970,19 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dkdv_rh_kernel(AttnBwd
     }
     // excluded key (no weight): padding, or masked in a row with a valid key
     const bool excl = row_valid ? !(km_row[key] > 0.5f) : key >= N;
-    const bool any_excl = __ballot(excl) != 0ull;
     const float* btile = bS + (int64_t)kt * nt * 1024;
     f32x16 dk = zero16(), dv = zero16();
-    for (int qt = 0; qt < nq; ++qt) {
+    // query tile qt with its bias in cur; the next tile's bias goes to nxt
+    auto unit = [&](int qt, const f32x4* cur, f32x4* nxt) {
+      load_bias_tile(nxt, btile + (qt + 1 < nq ? qt + 1 : qt) * 1024);
       const char* qtile = qs + qt * 2048;
       const char* dtile = dos + qt * 2048;
-      f32x16 sc = zero16();
+      f32x16 sc = bias_acc(cur);
       if (row_valid) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 v = *reinterpret_cast<const f32x4*>(btile + qt * 1024 + g * 256);
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) sc[4 * g + rr] = v[rr];
-        }
-#pragma unroll
         for (int m = 0; m < 2; ++m) mma(sc, lds_frag(qtile + off.nrm[m]), kf[m]);  // S: rows q, cols key
+      } else {
+        sc = zero16();
       }
       f32x16 dp = mma0(lds_frag(dtile + off.nrm[0]), vf[0]);
       mma(dp, lds_frag(dtile + off.nrm[1]), vf[1]);
@@ -963,20 +994,9 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dkdv_rh_kernel(AttnBwd
         const f32x4 d4 = *reinterpret_cast<const f32x4*>(dd_s + q0);
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) {
-          const float s2 = row_valid ? fmaf(sc[4 * g + rr], c2, -l4[rr]) : -l4[rr];
-          pv[4 * g + rr] = __builtin_amdgcn_exp2f(s2);
+          pv[4 * g + rr] = __builtin_amdgcn_exp2f(fmaf(sc[4 * g + rr], c2, -l4[rr]));
+          dsv[4 * g + rr] = pv[4 * g + rr] * (dp[4 * g + rr] - d4[rr]);
         }
-        if (qt * 32 + 32 > N) {
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr)
-            if (q0 + rr >= N) pv[4 * g + rr] = 0.f;  // padded query
-        }
-        if (any_excl && excl) {
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) pv[4 * g + rr] = 0.f;
-        }
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) dsv[4 * g + rr] = pv[4 * g + rr] * (dp[4 * g + rr] - d4[rr]);
       }
       Frag<bf16> fp[2], fs[2];
       vals_to_frags<bf16>(fp, pv);
@@ -986,6 +1006,16 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dkdv_rh_kernel(AttnBwd
         mma(dv, lds_frag_tr(dtile, off, gp), fp[gp]);  // dV^T[d][key] += dO^T P
         mma(dk, lds_frag_tr(qtile, off, gp), fs[gp]);  // dK^T[d][key] += Q^T dS
       }
+    };
+    f32x4 ba[4], bb[4];
+    load_bias_tile(ba, btile);
+    for (int qt = 0; qt < nq; qt += 2) {
+      unit(qt, ba, bb);
+      if (qt + 1 < nq) unit(qt + 1, bb, ba);
+    }
+    if (excl) {
+      dk = zero16();
+      dv = zero16();
     }
     bf16* dko = bf.dk + (rh * np + key) * AD;
     bf16* dvo = bf.dv + (rh * np + key) * AD;
@@ -999,8 +1029,9 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dkdv_rh_kernel(AttnBwd
 }
 
 // dQ: block (row, head), wave w owns query tiles w, w + 8, ...; lane = query.
+// Bias tiles in two alternating register sets, as in the dK / dV kernel.
 template <int NPM>
-__global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dq_rh_kernel(AttnBwdBufs<bf16> bf, int B,
+__global__ __launch_bounds__(64 * kRhWaves) __attribute__((amdgpu_waves_per_eu(4))) void attn_bwd_dq_rh_kernel(AttnBwdBufs<bf16> bf, int B,
                                                                     int N, int np, float scale) {
   constexpr int H = 4;
   __shared__ __attribute__((aligned(1024))) char ks[NPM * 64];
@@ -1048,32 +1079,26 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dq_rh_kernel(AttnBwdBu
     }
     const float lse2 = rh_lse2(bf, rh * np + q, row_valid);
     const float dq_ = bf.dd[rh * np + q];
-    const bool qpad = q >= N;
-    const bool tile_pad = qt * 32 + 32 > N;
+    const bool qpad = q >= N;  // a padded query's column of dQ^T is zeroed at the end
     const float* btile = bT + (int64_t)qt * nt * 1024;
     f32x16 dq = zero16();
-    for (int kt = 0; kt < nk; ++kt) {
+    // key tile kt with its bias in cur; the next tile's bias goes to nxt
+    auto unit = [&](int kt, const f32x4* cur, f32x4* nxt) {
+      load_bias_tile(nxt, btile + (kt + 1 < nk ? kt + 1 : kt) * 1024);
       const char* ktile = ks + kt * 2048;
       const char* vtile = vs + kt * 2048;
-      f32x16 sc = zero16();
+      f32x16 sc = bias_acc(cur);
       if (row_valid) {
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const f32x4 v = *reinterpret_cast<const f32x4*>(btile + kt * 1024 + g * 256);
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) sc[4 * g + rr] = v[rr];
-        }
-#pragma unroll
         for (int m = 0; m < 2; ++m) mma(sc, lds_frag(ktile + off.nrm[m]), qf[m]);  // S^T: rows key, cols q
+      } else {
+        sc = zero16();
       }
       f32x16 dp = mma0(lds_frag(vtile + off.nrm[0]), df[0]);  // dP^T
       mma(dp, lds_frag(vtile + off.nrm[1]), df[1]);
       float pv[16];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const float s2 = row_valid ? fmaf(sc[e], c2, -lse2) : -lse2;
-        pv[e] = __builtin_amdgcn_exp2f(s2);
-      }
+      for (int e = 0; e < 16; ++e) pv[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], c2, -lse2));
       const unsigned kx = __builtin_amdgcn_readlane(kxv, kt);
       if (kx != 0u) {
         // this lane's keys 8g + 4*half + rr: bits 8g + rr after the shift
@@ -1084,10 +1109,6 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dq_rh_kernel(AttnBwdBu
           for (int rr = 0; rr < 4; ++rr)
             if (__builtin_amdgcn_ubfe(kl, 8 * g + rr, 1)) pv[4 * g + rr] = 0.f;
       }
-      if (tile_pad && qpad) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) pv[e] = 0.f;
-      }
       float dsv[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) dsv[e] = pv[e] * (dp[e] - dq_);
@@ -1095,7 +1116,14 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dq_rh_kernel(AttnBwdBu
       vals_to_frags<bf16>(fs, dsv);
 #pragma unroll
       for (int gp = 0; gp < 2; ++gp) mma(dq, lds_frag_tr(ktile, off, gp), fs[gp]);  // dQ^T[d][q] += K^T dS^T
+    };
+    f32x4 ba[4], bb[4];
+    load_bias_tile(ba, btile);
+    for (int kt = 0; kt < nk; kt += 2) {
+      unit(kt, ba, bb);
+      if (kt + 1 < nk) unit(kt + 1, bb, ba);
     }
+    if (qpad) dq = zero16();
     bf16* dqo = bf.dq + (rh * np + q) * AD;
 #pragma unroll
     for (int g = 0; g < 4; ++g)
@@ -1125,6 +1153,8 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dbias_rh_kernel(AttnBw
   static_assert(NPM <= 512, "two key tiles per wave");
   constexpr int BUF = 2 * NPM * 64 + 4096;  // K rows, V rows, Q tile, dO tile
   __shared__ __attribute__((aligned(1024))) char lds[2 * BUF];
+  __shared__ __attribute__((aligned(256))) char pf_scratch[kRhWaves][256];  // L2 prefetch landing area
+  __shared__ __attribute__((aligned(256))) char row_sc[2 * kRhWaves * 768];  // per-row scalars, two rows
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, t32 = lane & 31;
@@ -1168,22 +1198,32 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dbias_rh_kernel(AttnBw
       g2lds16_sv(reinterpret_cast<const char*>(su), voff, __builtin_amdgcn_readfirstlane(base + i * 1024));
     }
   };
-  // per-row scalars of this lane's query and its key tiles, loaded one row ahead
+  // Per-row scalars of the block's 32 queries (m, 1/l, D) and of the wave's
+  // key tiles (mask values) come into LDS like the rows, one row ahead: three
+  // 4-byte direct loads a wave into its 768-byte slot of the row's buffer
+  // (lanes 0-31 / 32-63: m / 1/l, D / mask of key tile w, mask of key tile
+  // w + 8 twice).  A key tile past the last reads tile nt - 1 (unused).
+  const int kt0c = min(wave, nt - 1), kt1c = min(wave + kRhWaves, nt - 1);
+  auto issue_scalars = [&](int r, int u) {
+    const int64_t br = (int64_t)b * N + r;
+    const int64_t qi = (br * H + h) * np + q;
+    const float* km = bf.kmask + br * np + t32;
+    const uint32_t base = lds_addr(row_sc) + (uint32_t)((u * kRhWaves + wave) * 768);
+    g2lds4(half ? bf.linv + qi : bf.mrow + qi, base);
+    g2lds4(half ? km + kt0c * 32 : bf.dd + qi, base + 256);
+    g2lds4(km + kt1c * 32, base + 512);
+  };
   struct RowIn {
     float m, li, d, km[2];
   };
-  auto load_row = [&](int r) {
+  auto read_scalars = [&](int u) {
+    const float* sl = reinterpret_cast<const float*>(row_sc + (u * kRhWaves + wave) * 768);
     RowIn x;
-    const int64_t br = (int64_t)b * N + r;
-    const int64_t qi = (br * H + h) * np + q;
-    x.m = bf.mrow[qi];
-    x.li = bf.linv[qi];
-    x.d = bf.dd[qi];
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int kt = wave + kRhWaves * i;
-      x.km[i] = kt < nt ? bf.kmask[br * np + kt * 32 + t32] : 0.f;
-    }
+    x.m = sl[t32];
+    x.li = sl[32 + t32];
+    x.d = sl[64 + t32];
+    x.km[0] = sl[96 + t32];
+    x.km[1] = sl[128 + t32];
     return x;
   };
 
@@ -1203,23 +1243,47 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dbias_rh_kernel(AttnBw
     }
     acc[i] = zero16();
   }
-  RowIn cur = load_row(r0);
+  // One 4-byte load a lane per row, two rows ahead, brings that row's K and
+  // V lines (np / 2 lines of 128 bytes each; lane l of wave w takes line
+  // 64w + l) into L2, so that its copies, issued a row later, hit there
+  // instead of waiting on HBM.  It lands in a per-wave LDS scratch area that
+  // nothing reads.  Each row's top waits for all but the newest load (this
+  // prefetch, issued after the row's copies and scalars).
+  const int gl = wave * 64 + lane;
+  const uint32_t pf_lds = lds_addr(pf_scratch[wave]);
+  auto prefetch_row = [&](int r) {
+    const int64_t rh = ((int64_t)b * N + r) * H + h;
+    const int kind = gl < np / 2 ? 0 : gl < np ? 1 : 2;
+    const char* p = reinterpret_cast<const char*>((kind == 1 ? bf.vr : bf.kr) + rh * np * AD) +
+                    (kind == 0 ? gl : kind == 1 ? gl - np / 2 : 0) * 128;
+    g2lds4(p, pf_lds);
+  };
+  // Every load in the row loop is a direct-to-LDS copy issued from asm, so
+  // the compiler adds no wait of its own there; the bias tiles (ordinary
+  // loads) have landed before the loop.
+  issue_scalars(r0, 0);
   issue_row(r0, 0);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
   for (int r = r0; r < r1; ++r) {
     const int u = (r - r0) & 1;
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's copies of row r and its scalars landed
-    __syncthreads();                // every wave's copies landed; row r - 1's buffer is free
-    const RowIn x = cur;
+    // this wave's copies of row r landed (the prefetch of row r + 1, issued
+    // after them, may still be in flight)
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm<1>());
+    barrier_only();  // every wave's copies landed; row r - 1's buffer is free
     if (r + 1 < r1) {
-      cur = load_row(r + 1);
+      issue_scalars(r + 1, u ^ 1);
       issue_row(r + 1, u ^ 1);
     }
+    prefetch_row(min(r + 2, r1 - 1));
+    const RowIn x = read_scalars(u);
     const char* buf = lds + u * BUF;
     const char* qtile = buf + 2 * kv_bytes;
     const char* dtile = qtile + 2048;
     // a row without a valid key stores m = -1e9 for every query
     const bool row_valid = __ballot(x.m != kMaskScore) != 0ull;
-    const float lse2 = row_valid ? (x.m - logf(x.li)) * kLog2e : -log2f(x.li);
+    // a padded query takes lse2 = +inf: P = 0
+    const float lse2 = qpad ? INFINITY : row_valid ? (x.m - logf(x.li)) * kLog2e : -log2f(x.li);
+    const float dd = qpad ? 0.f : x.d;
     const Frag<bf16> qf0 = lds_frag(qtile + off.nrm[0]), qf1 = lds_frag(qtile + off.nrm[1]);
     const Frag<bf16> df0 = lds_frag(dtile + off.nrm[0]), df1 = lds_frag(dtile + off.nrm[1]);
 #pragma unroll
@@ -1241,8 +1305,7 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dbias_rh_kernel(AttnBw
       mma(dp, lds_frag(vtile + off.nrm[1]), df1);
       float pv[16];
 #pragma unroll
-      for (int e = 0; e < 16; ++e)
-        pv[e] = __builtin_amdgcn_exp2f(row_valid ? fmaf(sc[e], c2, -lse2) : -lse2);
+      for (int e = 0; e < 16; ++e) pv[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], c2, -lse2));  // sc = 0 in an invalid row
       if (kx != 0u) {
         const unsigned kl = kx >> (4 * half);
 #pragma unroll
@@ -1251,14 +1314,12 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dbias_rh_kernel(AttnBw
           for (int rr = 0; rr < 4; ++rr)
             if (__builtin_amdgcn_ubfe(kl, 8 * g + rr, 1)) pv[4 * g + rr] = 0.f;
       }
-      if (qpad) {
 #pragma unroll
-        for (int e = 0; e < 16; ++e) pv[e] = 0.f;
-      }
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][e] += pv[e] * (dp[e] - x.d);
+      for (int e = 0; e < 16; ++e) acc[i][e] += pv[e] * (dp[e] - dd);
     }
   }
+  // the last prefetches land before the block's LDS can pass to another block
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
   float* dst = part + ((int64_t)(b * nch + c) * H + h) * np * np + lane * 4;
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
