@@ -216,7 +216,7 @@ __device__ __forceinline__ f32x2 row_stats(const RowHalf<C>& r, float eps) {
   }
   q += xor32(q);
   const float var = q * (1.0f / C);
-  return f32x2{mean, 1.0f / sqrtf(var + eps)};
+  return f32x2{mean, __builtin_amdgcn_rsqf(var + eps)};  // v_rsq_f32 (1 ulp)
 }
 
 // Normalise (no affine: the LayerNorm weight and bias are folded into the
@@ -277,7 +277,7 @@ __device__ __forceinline__ void ln_frags_bf16(Frag<bf16>* xf, const Frag<bf16>* 
       q += d * d;
     }
   q += xor32(q);
-  const float rstd = 1.0f / sqrtf(q * (1.0f / C) + eps);
+  const float rstd = __builtin_amdgcn_rsqf(q * (1.0f / C) + eps);  // v_rsq_f32 (1 ulp)
 #pragma unroll
   for (int ch = 0; ch < C / 16; ++ch) {
     float f[8];

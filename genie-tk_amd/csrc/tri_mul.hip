@@ -860,12 +860,15 @@ __global__ __launch_bounds__(256) void trimul_epilogue_kernel(
 //     k ^ (p & 3)) and leaves as two 16-byte-per-lane stores, each 16 pairs x
 //     64 contiguous bytes, instead of four 8-byte stores per lane that touch a
 //     cache line per pair (52.8 -> 51.6 us at N = 512, bit-identical output).
+//   * RES (the residual add) is a template parameter: as a run-time flag the
+//     compiler computed both sums of every output and selected one.
 // ---------------------------------------------------------------------------
-template <int CZ, int CH>
+template <int CZ, int CH, bool RES>
 __global__ __launch_bounds__(512) void trimul_epilogue_bf16_kernel(
     const bf16* __restrict__ z, const bf16* __restrict__ px, bf16* __restrict__ out,
-    TriMulPacked<bf16> w, int N, int Np, int residual, float eps_in, float eps_out,
+    TriMulPacked<bf16> w, int N, int Np, float eps_in, float eps_out,
     int64_t ntiles, int r0, int nrows, int xrows, int64_t plane) {
+  constexpr bool residual = RES;
   constexpr int WAVES = 8;
   constexpr int KZ = CZ / 16;                 // k chunks over c_z (gate input)
   constexpr int KX = CH / 16;                 // k chunks over c (W_z input)
@@ -961,7 +964,7 @@ __global__ __launch_bounds__(512) void trimul_epilogue_bf16_kernel(
     // (q < KZ) or 2-3 (q >= KZ) of zr[q mod KZ] once dwords 2-3 of the lower
     // half-wave are swapped with dwords 0-1 of the upper one.
     bf16x4 zres[2 * KZ];
-    if (residual) {
+    if constexpr (residual) {
 #pragma unroll
       for (int ch = 0; ch < KZ; ++ch) {
         typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -1018,7 +1021,7 @@ __global__ __launch_bounds__(512) void trimul_epilogue_bf16_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           o[r] = (oa[4 * g + r] + bz[r]) * gate_from_u(ga[4 * g + r] + bg[r]);
-          if (residual) o[r] += (float)zres[nt * 4 + g][r];
+          if constexpr (residual) o[r] += (float)zres[nt * 4 + g][r];
         }
         typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
         *reinterpret_cast<u32x2*>(sw + t32 * 64 + ((g ^ (t32 & 3)) << 4) + half * 8) =
@@ -1302,9 +1305,9 @@ static int launch_trimul_epilogue(const void* z, const T* px, void* out, const T
   if constexpr (trimul_fast<T, CZ, CH>()) {
     const int grid = (int)std::min<int64_t>(device_cus(), (etiles + 7) / 8);
     StageTimer timer("trimul_epilogue", st);
-    trimul_epilogue_bf16_kernel<CZ, CH><<<grid, 512, 0, st>>>(
-        (const bf16*)z, (const bf16*)px, (bf16*)out, w, (int)N, Np, residual, eps_in, eps_out,
-        etiles, r0, nrows, xrows, ps_x);
+    auto kern = residual ? trimul_epilogue_bf16_kernel<CZ, CH, true> : trimul_epilogue_bf16_kernel<CZ, CH, false>;
+    kern<<<grid, 512, 0, st>>>((const bf16*)z, (const bf16*)px, (bf16*)out, w, (int)N, Np, eps_in, eps_out,
+                               etiles, r0, nrows, xrows, ps_x);
   } else {
     StageTimer timer("trimul_epilogue", st);
     trimul_epilogue_kernel<T, CZ, CH><<<(unsigned)((etiles + 3) / 4), 256, 0, st>>>(
