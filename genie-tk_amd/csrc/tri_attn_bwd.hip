@@ -1132,17 +1132,20 @@ __global__ __launch_bounds__(64 * kRhWaves) __attribute__((amdgpu_waves_per_eu(4
   }
 }
 
-// dB of the bf16 path (np <= 512): block (batch b, head h, query tile qt,
-// chunk of rows).  The block's waves walk the chunk's rows together, each
-// owning key tiles w and w + 8 (lane = query, S^T orientation as in dQ).  For
-// every row, K and V of the row and its query tile of Q and dO come into LDS
-// (double buffered: the copies of row r + 1 go out before row r is computed),
-// and each wave adds dS of its tiles into fp32 accumulators.  The chunk's sums
-// go to a partial buffer in fragment order (the biasT layout), summed over
-// the chunks by attn_bwd_dbias_reduce_kernel.  Blocks of one (b, chunk, head)
-// are consecutive, so the blocks that read the same K and V rows share an
-// XCD's L2.
+// dB of the bf16 path (np <= 512): block (batch b, head h, pair of query
+// tiles, chunk of rows).  The block's waves walk the chunk's rows together,
+// each owning key tiles w and w + 8 (lane = query, S^T orientation as in dQ)
+// for both query tiles, so each K and V fragment read serves two tiles.  For
+// every row, K and V of the row and the two query tiles of Q and dO come into
+// LDS (double buffered: the copies of row r + 1 go out before row r is
+// computed), and each wave adds dS of its tiles into fp32 accumulators.  The
+// chunk's sums go to a partial buffer in fragment order (the biasT layout),
+// summed over the chunks by attn_bwd_dbias_reduce_kernel.  Blocks of one
+// (b, chunk, head) are consecutive, so the blocks that read the same K and V
+// rows share an XCD's L2.  Two query tiles a block halve the K/V bytes moved
+// per unit of work and make the launch one round of blocks at N = 512.
 constexpr int kDbChunks = 8;  // row chunks per batch element (at most)
+constexpr int kDbQt = 2;      // query tiles per block
 
 template <int NPM>
 __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dbias_rh_kernel(AttnBwdBufs<bf16> bf,
@@ -1150,29 +1153,38 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dbias_rh_kernel(AttnBw
                                                                        int N, int np, int nch, int rpc,
                                                                        float scale) {
   constexpr int H = 4;
+  constexpr int QP = kDbQt;
   static_assert(NPM <= 512, "two key tiles per wave");
-  constexpr int BUF = 2 * NPM * 64 + 4096;  // K rows, V rows, Q tile, dO tile
+  constexpr int BUF = 2 * NPM * 64 + QP * 4096;  // K rows, V rows, then Q and dO tiles of each query tile
+  // per-row scalars: m, 1/l and D of the block's 64 queries (768 bytes,
+  // loaded by wave 0), then the mask values of each wave's key tiles (256
+  // bytes a wave)
+  constexpr int SCB = 768 + kRhWaves * 256;
   __shared__ __attribute__((aligned(1024))) char lds[2 * BUF];
   __shared__ __attribute__((aligned(256))) char pf_scratch[kRhWaves][256];  // L2 prefetch landing area
-  __shared__ __attribute__((aligned(256))) char row_sc[2 * kRhWaves * 768];  // per-row scalars, two rows
+  __shared__ __attribute__((aligned(256))) char row_sc[2 * SCB];             // per-row scalars, two rows
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int half = lane >> 5, t32 = lane & 31;
   const int nt = np / 32;
   const int nq = (N + 31) / 32;
+  const int nqp = (nq + QP - 1) / QP;
   const int64_t lin = xcd_remap(blockIdx.x, gridDim.x);
-  const int qt = (int)(lin % nq);
-  int64_t rest = lin / nq;
+  const int qp = (int)(lin % nqp);
+  int64_t rest = lin / nqp;
   const int h = (int)(rest % H);
   rest /= H;
   const int c = (int)(rest % nch);
   const int b = (int)(rest / nch);
   const int r0 = c * rpc;
   const int r1 = min(N, r0 + rpc);
-  const int q = qt * 32 + t32;
-  const bool qpad = q >= N;
+  const int qt0 = qp * QP;
+  const bool two = qt0 + 1 < nq;  // block-uniform: a second query tile exists
+  int qtq[QP];                    // query tile q (the second reads the first's data when absent)
+  qtq[0] = qt0;
+  qtq[1] = two ? qt0 + 1 : qt0;
   const int kv_bytes = np * 64;
-  const int ncopy = np / 8 + 4;  // 1 KiB copies per row: K, V, Q tile, dO tile
+  const int ncopy = np / 8 + 4 * QP;  // 1 KiB copies per row: K, V, and a Q and dO tile per query tile
 
   // copies of row r into buffer u
   const uint32_t rin = (uint32_t)lane >> 2;
@@ -1181,15 +1193,20 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dbias_rh_kernel(AttnBw
     const int64_t rh = ((int64_t)b * N + r) * H + h;
     const char* kb = reinterpret_cast<const char*>(bf.kr + rh * np * AD);
     const char* vb = reinterpret_cast<const char*>(bf.vr + rh * np * AD);
-    const char* qb = reinterpret_cast<const char*>(bf.qr + (rh * np + qt * 32) * AD);
-    const char* db = reinterpret_cast<const char*>(bf.dor + (rh * np + qt * 32) * AD);
+    const char* qb0 = reinterpret_cast<const char*>(bf.qr + (rh * np + qtq[0] * 32) * AD);
+    const char* db0 = reinterpret_cast<const char*>(bf.dor + (rh * np + qtq[0] * 32) * AD);
+    const char* qb1 = reinterpret_cast<const char*>(bf.qr + (rh * np + qtq[1] * 32) * AD);
+    const char* db1 = reinterpret_cast<const char*>(bf.dor + (rh * np + qtq[1] * 32) * AD);
     const uint32_t base = lds_addr(lds) + u * BUF;
     for (int i = wave; i < ncopy; i += kRhWaves) {
       const char* src;
+      const int j = i - np / 8;  // copy j of the query tiles' 8
       if (i < np / 16) src = kb + i * 1024;
       else if (i < np / 8) src = vb + (i - np / 16) * 1024;
-      else if (i < np / 8 + 2) src = qb + (i - np / 8) * 1024;
-      else src = db + (i - np / 8 - 2) * 1024;
+      else if (j < 2) src = qb0 + j * 1024;
+      else if (j < 4) src = db0 + (j - 2) * 1024;
+      else if (j < 6) src = qb1 + (j - 4) * 1024;
+      else src = db1 + (j - 6) * 1024;
       // wave-uniform, but selected per copy: back into scalar registers
       // (readfirstlane returns int: widen each half as unsigned)
       const uint64_t sa = (uint64_t)(uintptr_t)src;
@@ -1198,57 +1215,30 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dbias_rh_kernel(AttnBw
       g2lds16_sv(reinterpret_cast<const char*>(su), voff, __builtin_amdgcn_readfirstlane(base + i * 1024));
     }
   };
-  // Per-row scalars of the block's 32 queries (m, 1/l, D) and of the wave's
-  // key tiles (mask values) come into LDS like the rows, one row ahead: three
-  // 4-byte direct loads a wave into its 768-byte slot of the row's buffer
-  // (lanes 0-31 / 32-63: m / 1/l, D / mask of key tile w, mask of key tile
-  // w + 8 twice).  A key tile past the last reads tile nt - 1 (unused).
+  // Per-row scalars come into LDS like the rows, one row ahead, as 4-byte
+  // direct loads: wave 0 brings m, 1/l and D of the 64 queries (lanes 0-31
+  // the first tile's, 32-63 the second's), every wave the mask values of its
+  // key tiles (lanes 0-31 tile w, 32-63 tile w + 8; a tile past the last
+  // reads tile nt - 1, unused).
   const int kt0c = min(wave, nt - 1), kt1c = min(wave + kRhWaves, nt - 1);
+  const int myq = qtq[half] * 32 + t32;  // the query this lane brings in
   auto issue_scalars = [&](int r, int u) {
     const int64_t br = (int64_t)b * N + r;
-    const int64_t qi = (br * H + h) * np + q;
-    const float* km = bf.kmask + br * np + t32;
-    const uint32_t base = lds_addr(row_sc) + (uint32_t)((u * kRhWaves + wave) * 768);
-    g2lds4(half ? bf.linv + qi : bf.mrow + qi, base);
-    g2lds4(half ? km + kt0c * 32 : bf.dd + qi, base + 256);
-    g2lds4(km + kt1c * 32, base + 512);
-  };
-  struct RowIn {
-    float m, li, d, km[2];
-  };
-  auto read_scalars = [&](int u) {
-    const float* sl = reinterpret_cast<const float*>(row_sc + (u * kRhWaves + wave) * 768);
-    RowIn x;
-    x.m = sl[t32];
-    x.li = sl[32 + t32];
-    x.d = sl[64 + t32];
-    x.km[0] = sl[96 + t32];
-    x.km[1] = sl[128 + t32];
-    return x;
-  };
-
-  const RhOffsets off;
-  const float c2 = scale * kLog2e;
-  // bias tiles (h, qt, kt) of this wave's key tiles
-  f32x16 bias[2], acc[2];
-  const float* bT = bf.biasT + ((int64_t)b * H + h) * np * np + lane * 4;
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int kt = min(wave + kRhWaves * i, nt - 1);
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(bT + ((int64_t)qt * nt + kt) * 1024 + g * 256);
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) bias[i][4 * g + rr] = v[rr];
+    const int64_t qi = (br * H + h) * np + myq;
+    const uint32_t base = lds_addr(row_sc) + (uint32_t)(u * SCB);
+    if (wave == 0) {
+      g2lds4(bf.mrow + qi, base);
+      g2lds4(bf.linv + qi, base + 256);
+      g2lds4(bf.dd + qi, base + 512);
     }
-    acc[i] = zero16();
-  }
-  // One 4-byte load a lane per row, two rows ahead, brings that row's K and
-  // V lines (np / 2 lines of 128 bytes each; lane l of wave w takes line
-  // 64w + l) into L2, so that its copies, issued a row later, hit there
-  // instead of waiting on HBM.  It lands in a per-wave LDS scratch area that
-  // nothing reads.  Each row's top waits for all but the newest load (this
-  // prefetch, issued after the row's copies and scalars).
+    g2lds4(bf.kmask + br * np + (half ? kt1c : kt0c) * 32 + t32, base + 768 + wave * 256);
+  };
+  // L2 prefetch, two rows ahead: one 4-byte load a lane brings the row's K
+  // and V lines (np / 2 lines of 128 bytes each; lane l of wave w takes line
+  // 64w + l) into L2, so that the copies issued a row later hit there; it
+  // lands in a per-wave LDS scratch area nothing reads.  Each row's top waits
+  // for all but the newest load (this prefetch, issued after the row's
+  // copies and scalars).
   const int gl = wave * 64 + lane;
   const uint32_t pf_lds = lds_addr(pf_scratch[wave]);
   auto prefetch_row = [&](int r) {
@@ -1258,6 +1248,25 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dbias_rh_kernel(AttnBw
                     (kind == 0 ? gl : kind == 1 ? gl - np / 2 : 0) * 128;
     g2lds4(p, pf_lds);
   };
+
+  const RhOffsets off;
+  const float c2 = scale * kLog2e;
+  // bias tiles (h, qt, kt) of this wave's key tiles for both query tiles
+  f32x16 bias[QP][2], acc[QP][2];
+  const float* bT = bf.biasT + ((int64_t)b * H + h) * np * np + lane * 4;
+#pragma unroll
+  for (int q = 0; q < QP; ++q)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int kt = min(wave + kRhWaves * i, nt - 1);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(bT + ((int64_t)qtq[q] * nt + kt) * 1024 + g * 256);
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) bias[q][i][4 * g + rr] = v[rr];
+      }
+      acc[q][i] = zero16();
+    }
   // Every load in the row loop is a direct-to-LDS copy issued from asm, so
   // the compiler adds no wait of its own there; the bias tiles (ordinary
   // loads) have landed before the loop.
@@ -1275,86 +1284,112 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dbias_rh_kernel(AttnBw
       issue_row(r + 1, u ^ 1);
     }
     prefetch_row(min(r + 2, r1 - 1));
-    const RowIn x = read_scalars(u);
     const char* buf = lds + u * BUF;
-    const char* qtile = buf + 2 * kv_bytes;
-    const char* dtile = qtile + 2048;
+    const float* sq = reinterpret_cast<const float*>(row_sc + u * SCB);
+    const float* skm = reinterpret_cast<const float*>(row_sc + u * SCB + 768 + wave * 256);
     // a row without a valid key stores m = -1e9 for every query
-    const bool row_valid = __ballot(x.m != kMaskScore) != 0ull;
-    // a padded query takes lse2 = +inf: P = 0
-    const float lse2 = qpad ? INFINITY : row_valid ? (x.m - logf(x.li)) * kLog2e : -log2f(x.li);
-    const float dd = qpad ? 0.f : x.d;
-    const Frag<bf16> qf0 = lds_frag(qtile + off.nrm[0]), qf1 = lds_frag(qtile + off.nrm[1]);
-    const Frag<bf16> df0 = lds_frag(dtile + off.nrm[0]), df1 = lds_frag(dtile + off.nrm[1]);
+    const bool row_valid = __ballot(sq[t32] != kMaskScore) != 0ull;
+    float lse2[QP], dd[QP];
+    Frag<bf16> qf[QP][2], df[QP][2];
+#pragma unroll
+    for (int q = 0; q < QP; ++q) {
+      // a padded query takes lse2 = +inf: P = 0
+      const bool qpad = qtq[q] * 32 + t32 >= N;
+      const float m = sq[32 * q + t32], li = sq[64 + 32 * q + t32];
+      lse2[q] = qpad ? INFINITY : row_valid ? (m - logf(li)) * kLog2e : -log2f(li);
+      dd[q] = qpad ? 0.f : sq[128 + 32 * q + t32];
+      const char* qtile = buf + 2 * kv_bytes + q * 4096;
+#pragma unroll
+      for (int m2 = 0; m2 < 2; ++m2) {
+        qf[q][m2] = lds_frag(qtile + off.nrm[m2]);
+        df[q][m2] = lds_frag(qtile + 2048 + off.nrm[m2]);
+      }
+    }
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int kt = wave + kRhWaves * i;
       if (kt >= nt) break;
       const int key = kt * 32 + t32;
-      const bool ex = row_valid ? !(x.km[i] > 0.5f) : key >= N;
+      const bool ex = row_valid ? !(skm[32 * i + t32] > 0.5f) : key >= N;
       const unsigned kx = (unsigned)__ballot(ex);  // lanes 0-31: the tile's 32 keys
       const char* ktile = buf + kt * 2048;
       const char* vtile = buf + kv_bytes + kt * 2048;
-      f32x16 sc = zero16();
-      if (row_valid) {
-        sc = bias[i];
-        mma(sc, lds_frag(ktile + off.nrm[0]), qf0);  // S^T: rows key, cols q
-        mma(sc, lds_frag(ktile + off.nrm[1]), qf1);
+      const Frag<bf16> kf0 = lds_frag(ktile + off.nrm[0]), kf1 = lds_frag(ktile + off.nrm[1]);
+      const Frag<bf16> vf0 = lds_frag(vtile + off.nrm[0]), vf1 = lds_frag(vtile + off.nrm[1]);
+#pragma unroll
+      for (int q = 0; q < QP; ++q) {
+        if (q > 0 && !two) break;
+        f32x16 sc = zero16();
+        if (row_valid) {
+          sc = bias[q][i];
+          mma(sc, kf0, qf[q][0]);  // S^T: rows key, cols q
+          mma(sc, kf1, qf[q][1]);
+        }
+        f32x16 dp = mma0(vf0, df[q][0]);  // dP^T
+        mma(dp, vf1, df[q][1]);
+        float pv[16];
+#pragma unroll
+        for (int e = 0; e < 16; ++e) pv[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], c2, -lse2[q]));  // sc = 0 in an invalid row
+        if (kx != 0u) {
+          const unsigned kl = kx >> (4 * half);
+#pragma unroll
+          for (int g = 0; g < 4; ++g)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr)
+              if (__builtin_amdgcn_ubfe(kl, 8 * g + rr, 1)) pv[4 * g + rr] = 0.f;
+        }
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[q][i][e] += pv[e] * (dp[e] - dd[q]);
       }
-      f32x16 dp = mma0(lds_frag(vtile + off.nrm[0]), df0);  // dP^T
-      mma(dp, lds_frag(vtile + off.nrm[1]), df1);
-      float pv[16];
-#pragma unroll
-      for (int e = 0; e < 16; ++e) pv[e] = __builtin_amdgcn_exp2f(fmaf(sc[e], c2, -lse2));  // sc = 0 in an invalid row
-      if (kx != 0u) {
-        const unsigned kl = kx >> (4 * half);
-#pragma unroll
-        for (int g = 0; g < 4; ++g)
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr)
-            if (__builtin_amdgcn_ubfe(kl, 8 * g + rr, 1)) pv[4 * g + rr] = 0.f;
-      }
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc[i][e] += pv[e] * (dp[e] - dd);
     }
   }
   // the last prefetches land before the block's LDS can pass to another block
   __builtin_amdgcn_s_waitcnt(vmcnt_imm<0>());
   float* dst = part + ((int64_t)(b * nch + c) * H + h) * np * np + lane * 4;
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int kt = wave + kRhWaves * i;
-    if (kt >= nt) break;
+  for (int q = 0; q < QP; ++q) {
+    if (q > 0 && !two) break;
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
-      *reinterpret_cast<f32x4*>(dst + ((int64_t)qt * nt + kt) * 1024 + g * 256) =
-          f32x4{acc[i][4 * g], acc[i][4 * g + 1], acc[i][4 * g + 2], acc[i][4 * g + 3]};
+    for (int i = 0; i < 2; ++i) {
+      const int kt = wave + kRhWaves * i;
+      if (kt >= nt) break;
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<f32x4*>(dst + ((int64_t)qtq[q] * nt + kt) * 1024 + g * 256) =
+            f32x4{acc[q][i][4 * g], acc[q][i][4 * g + 1], acc[q][i][4 * g + 2], acc[q][i][4 * g + 3]};
+    }
   }
 }
 
-// db[b][h][q][k] = sum over the row chunks of the fragment-order partials;
-// one thread per 4 consecutive keys.
+// db[b][h][q][k] = sum over the row chunks of the fragment-order partials.
+// Thread t sums the t-th 16-byte piece of the fragment-order layout (keys
+// 8g + 4 half .. +3 of query a in tile (h, qt, kt), as bias_frag_elem lays
+// them out), so the partials are read in whole lines; a 256-thread block
+// covers one 32 x 32 tile, whose 32 output rows of 128 bytes its four waves
+// write together.  Tiles outside the N x N grid are skipped.
 __global__ __launch_bounds__(256) void attn_bwd_dbias_reduce_kernel(const float* __restrict__ part,
                                                                     float* __restrict__ db, int B, int N,
                                                                     int np, int nch) {
   constexpr int H = 4;
-  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  const int k4n = np / 4;
-  if (t >= (int64_t)B * H * N * k4n) return;
-  const int k = (int)(t % k4n) * 4;
-  int64_t rest = t / k4n;
-  const int q = (int)(rest % N);
-  rest /= N;
-  const int h = (int)(rest % H);
-  const int b = (int)(rest / H);
-  if (k >= N) return;
-  const int64_t e = bias_frag_elem(h, q, k, np);
+  const int nt = np / 32;
+  const int64_t tile = blockIdx.x;  // [B][H][qt][kt]
+  const int kt = (int)(tile % nt), qt = (int)((tile / nt) % nt);
+  const int64_t bh = tile / ((int64_t)nt * nt);
+  if (qt * 32 >= N || kt * 32 >= N) return;  // block-uniform
+  const int b = (int)(bh / H), h = (int)(bh % H);
+  const int tid = threadIdx.x;
+  const int g = tid >> 6, l = tid & 63;
+  const int q = qt * 32 + (l & 31), k = kt * 32 + 8 * g + 4 * (l >> 5);
+  const int64_t e = (((int64_t)h * nt + qt) * nt + kt) * 1024 + tid * 4;  // == bias_frag_elem(h, q, k, np)
+  const int64_t slab = (int64_t)H * np * np;
+  const float* src = part + (int64_t)b * nch * slab + e;
   f32x4 s = {0.f, 0.f, 0.f, 0.f};
   for (int c = 0; c < nch; ++c) {
-    const f32x4 v = *reinterpret_cast<const f32x4*>(part + (int64_t)(b * nch + c) * H * np * np + e);
+    const f32x4 v = *reinterpret_cast<const f32x4*>(src + c * slab);
 #pragma unroll
     for (int j = 0; j < 4; ++j) s[j] += v[j];
   }
+  if (q >= N) return;
   float* dst = db + (((int64_t)b * H + h) * N + q) * N + k;
 #pragma unroll
   for (int j = 0; j < 4; ++j)
@@ -1919,7 +1954,7 @@ static int bwd_triattn(const void* x, const float* mask, const void* dy,
         // sums in fragment order, then the sum over the chunks
         const int rpc = (int)((N + kDbChunks - 1) / kDbChunks);
         const int nch = (int)((N + rpc - 1) / rpc);
-        const int64_t dblocks = B * nch * H * ((N + 31) / 32);
+        const int64_t dblocks = B * nch * H * (((N + 31) / 32 + kDbQt - 1) / kDbQt);
         GTK_REQUIRE(dblocks < (1ll << 31), GTK_EUNSUPPORTED, "attention backward grid too large");
         if (np <= 256)
           attn_bwd_dbias_rh_kernel<256><<<(unsigned)dblocks, 64 * kRhWaves, 0, st>>>(a.b, a.b.dbp, (int)B, (int)N,
@@ -1928,9 +1963,8 @@ static int bwd_triattn(const void* x, const float* mask, const void* dy,
           attn_bwd_dbias_rh_kernel<512><<<(unsigned)dblocks, 64 * kRhWaves, 0, st>>>(a.b, a.b.dbp, (int)B, (int)N,
                                                                                     np, nch, rpc, scale);
         GTK_LAUNCH_CHECK();
-        const int64_t rt = B * H * N * (np / 4);
-        attn_bwd_dbias_reduce_kernel<<<(unsigned)((rt + 255) / 256), 256, 0, st>>>(a.b.dbp, a.b.db, (int)B, (int)N,
-                                                                                   np, nch);
+        const int64_t rtiles = B * H * (int64_t)(np / 32) * (np / 32);
+        attn_bwd_dbias_reduce_kernel<<<(unsigned)rtiles, 256, 0, st>>>(a.b.dbp, a.b.db, (int)B, (int)N, np, nch);
       }
     } else {
       attn_bwd_dbias_kernel<T, H><<<g4(pairtiles), 256, 0, st>>>(a.b, (int)B, (int)N, np, scale);
