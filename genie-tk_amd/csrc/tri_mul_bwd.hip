@@ -632,6 +632,14 @@ __global__ __launch_bounds__(512) void trimul_bwd_prologue_side_kernel(
   // FULL (N % 32 == 0): every tile is 32 valid pairs on one row, and the
   // channel-major blocks go through a per-wave LDS tile
   __shared__ __attribute__((aligned(16))) bf16 cst[FULL ? 8 : 1][FULL ? kCmTile : 1];
+  // this side's biases and the LayerNorm weight: read per tile from LDS, so
+  // that no global load of theirs makes a stage wait for every load in flight
+  __shared__ __attribute__((aligned(16))) float bl[2 * CH + CZ];
+  for (int t = threadIdx.x; t < CH; t += blockDim.x) {
+    bl[t] = (SIDE ? w.b_bp : w.b_ap)[t];
+    bl[CH + t] = (SIDE ? w.b_bg : w.b_ag)[t];
+  }
+  for (int t = threadIdx.x; t < CZ; t += blockDim.x) bl[2 * CH + t] = w.ln_in_w[t];
   __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
@@ -642,8 +650,9 @@ __global__ __launch_bounds__(512) void trimul_bwd_prologue_side_kernel(
   const int t32 = lane & 31;
   const int jtiles = (N + 31) / 32;
   const int64_t plane = (int64_t)Np * Np;
-  const float* bp = SIDE ? w.b_bp : w.b_ap;
-  const float* bg = SIDE ? w.b_bg : w.b_ag;
+  const float* const bp = bl;
+  const float* const bg = bl + CH;
+  const float* const lnw = bl + 2 * CH;
   bf16* const cm_p = cm_stack + (int64_t)(2 * SIDE) * CH * pitch;
   bf16* const cm_g = cm_stack + (int64_t)(2 * SIDE + 1) * CH * pitch;
 
@@ -798,7 +807,7 @@ __global__ __launch_bounds__(512) void trimul_bwd_prologue_side_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float xv = (z4[r] - st[0]) * st[1];
-          const float dxh = w.ln_in_w[c0 + r + oz] * dzn[nt][4 * g + r];
+          const float dxh = lnw[c0 + r + oz] * dzn[nt][4 * g + r];
           s1 += dxh;
           s2 += dxh * xv;
         }
@@ -823,7 +832,7 @@ __global__ __launch_bounds__(512) void trimul_bwd_prologue_side_kernel(
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float xv = (z4[r] - st[0]) * st[1];
-          const float dxh = w.ln_in_w[c0 + r + oz] * dzn[nt][4 * g + r];
+          const float dxh = lnw[c0 + r + oz] * dzn[nt][4 * g + r];
           o[r] = st[1] * (dxh - m1 - xv * m2);
           xs[4 * g + r] = xv;
           if constexpr (!FULL) {
