@@ -464,8 +464,21 @@ __global__ __launch_bounds__(256) void trimul_contract_kernel(const T* __restric
 //     freed, and the finished tile is stored from the accumulators while that
 //     copy is in flight (one block per CU at 256x256: its stores would
 //     otherwise overlap no copy or MFMA; 48.4 -> 44.5 us at N = 512).
+//   * LT / RT: the operand is given transposed, as the plane L^T [k][i]
+//     (R^T [k][j]) of whole Np x Np planes, which is how the backward's
+//     dA = dX Bm and dB = dX^T A read the forward planes without transposing
+//     them first.  Such a panel sits in LDS as 64 k rows of TI (TJ) columns,
+//     16-byte chunk c of row r at c ^ tswz(r), and its fragments (8
+//     consecutive k of one column a lane) come from two transposing reads
+//     (ds_read_b64_tr_b16): within 16 lanes, lane L takes element L % 4 of
+//     the pieces at the addresses of lanes L/4, 4 + L/4, 8 + L/4 and
+//     12 + L/4, so with supplier lane s at row k0 + s/4, columns cb + 4(s%4)
+//     .. +3, lane L receives rows k0 .. k0 + 3 of column cb + L.  The four
+//     rows of a read then sit in four distinct chunk pairs (the swizzle), so
+//     the 16 addresses fall on distinct banks.  Products, sums and their
+//     order are those of the plain form on the transposed planes.
 // ---------------------------------------------------------------------------
-template <int TI, int TJ>
+template <int TI, int TJ, bool LT = false, bool RT = false>
 __global__ __launch_bounds__(64 * (TI / 64) * (TJ / 64)) void trimul_contract_bf16_kernel(
     const bf16* __restrict__ pa, const bf16* __restrict__ pb, bf16* __restrict__ px, int Np,
     int Mi, int64_t nplanes, int64_t plane, int64_t plane_ax) {
@@ -474,6 +487,10 @@ __global__ __launch_bounds__(64 * (TI / 64) * (TJ / 64)) void trimul_contract_bf
   constexpr int RPR = 1024 / (2 * BK);              // panel rows per 1 KiB copy
   constexpr int CPR = BK / 8;                       // 16-byte chunks per panel row
   static_assert((TI / RPR) % NW == 0 && (TJ / RPR) % NW == 0, "copies split evenly");
+  // transposed panels: 64 rows of TI (TJ) columns, 1 KiB copies of RPT rows
+  constexpr int RPTA = 512 / TI, CPTA = TI / 8, RPTB = 512 / TJ, CPTB = TJ / 8;
+  static_assert((BK / RPTA) == TI / RPR && (BK / RPTB) == TJ / RPR, "same copy count either way");
+  auto tswz = [](int r) { return 2 * (r & 3); };
   __shared__ __attribute__((aligned(1024))) bf16 ring[NS * (TI + TJ) * BK];
 
   const int ti_n = Mi / TI, tj_n = Np / TJ;
@@ -497,13 +514,23 @@ __global__ __launch_bounds__(64 * (TI / 64) * (TJ / 64)) void trimul_contract_bf
   uint32_t voA[RA], voB[RB];
 #pragma unroll
   for (int u = 0; u < RA; ++u) {
-    const int row = RPR * (wave + u * NW) + lane / CPR;
-    voA[u] = (uint32_t)((row * Np + 8 * ((lane % CPR) ^ pswz(row))) * 2);
+    if constexpr (LT) {
+      const int row = RPTA * (wave + u * NW) + lane / CPTA;  // k row
+      voA[u] = (uint32_t)((row * Np + 8 * ((lane % CPTA) ^ tswz(row))) * 2);
+    } else {
+      const int row = RPR * (wave + u * NW) + lane / CPR;
+      voA[u] = (uint32_t)((row * Np + 8 * ((lane % CPR) ^ pswz(row))) * 2);
+    }
   }
 #pragma unroll
   for (int u = 0; u < RB; ++u) {
-    const int row = RPR * (wave + u * NW) + lane / CPR;
-    voB[u] = (uint32_t)((row * Np + 8 * ((lane % CPR) ^ pswz(row))) * 2);
+    if constexpr (RT) {
+      const int row = RPTB * (wave + u * NW) + lane / CPTB;  // k row
+      voB[u] = (uint32_t)((row * Np + 8 * ((lane % CPTB) ^ tswz(row))) * 2);
+    } else {
+      const int row = RPR * (wave + u * NW) + lane / CPR;
+      voB[u] = (uint32_t)((row * Np + 8 * ((lane % CPR) ^ pswz(row))) * 2);
+    }
   }
   const uint32_t lds_a = lds_addr(ring), lds_b = lds_addr(ring + NS * TI * BK);
   const bf16* Ab = nullptr;  // panel bases of the tile being loaded
@@ -515,17 +542,32 @@ __global__ __launch_bounds__(64 * (TI / 64) * (TJ / 64)) void trimul_contract_bf
     const int trem = (int)(lin % ((int64_t)ti_n * tj_n));
     const int i0 = (trem / tj_n) * TI;
     const int j0 = (trem % tj_n) * TJ;
-    Ab = pa + pl * plane_ax + (int64_t)i0 * Np;
-    Bb = pb + pl * plane + (int64_t)j0 * Np;
+    Ab = pa + pl * plane_ax + (LT ? (int64_t)i0 : (int64_t)i0 * Np);
+    Bb = pb + pl * plane + (RT ? (int64_t)j0 : (int64_t)j0 * Np);
     X = px + pl * plane_ax + (int64_t)i0 * Np + j0;
   };
   auto issue = [&](int stage, int k0) {
+    const bf16* As = Ab + (LT ? (int64_t)k0 * Np : (int64_t)k0);
+    const bf16* Bs = Bb + (RT ? (int64_t)k0 * Np : (int64_t)k0);
 #pragma unroll
     for (int u = 0; u < RA; ++u)
-      g2lds16_sv(Ab + k0, voA[u], lds_a + (uint32_t)((stage * TI * BK + (wave + u * NW) * 512) * 2));
+      g2lds16_sv(As, voA[u], lds_a + (uint32_t)((stage * TI * BK + (wave + u * NW) * 512) * 2));
 #pragma unroll
     for (int u = 0; u < RB; ++u)
-      g2lds16_sv(Bb + k0, voB[u], lds_b + (uint32_t)((stage * TJ * BK + (wave + u * NW) * 512) * 2));
+      g2lds16_sv(Bs, voB[u], lds_b + (uint32_t)((stage * TJ * BK + (wave + u * NW) * 512) * 2));
+  };
+  // fragment of a transposed panel (cols columns a row): lane l takes column
+  // c0 + (l & 31), k 16 kc + 8 (l >> 5) .. +7
+  auto tfrag = [&](const bf16* panel, int cols, int c0, int kc) {
+    const int G = lane >> 4, sl = lane & 15;
+    const int col = c0 + 16 * (G & 1) + 4 * (sl & 3);  // this lane's supplier column (4 elements)
+    const int k0 = 16 * kc + 8 * (G >> 1) + (sl >> 2);  // and row, first read
+    auto at = [&](int r) { return panel + r * cols + 8 * ((col >> 3) ^ tswz(r)) + (col & 7); };
+    typedef short s16x8 __attribute__((ext_vector_type(8)));
+    const s16x4 p0 = lds_read_tr16(at(k0)), p1 = lds_read_tr16(at(k0 + 4));
+    Frag<bf16> f;
+    f.v = __builtin_bit_cast(bf16x8, s16x8{p0[0], p0[1], p0[2], p0[3], p1[0], p1[1], p1[2], p1[3]});
+    return f;
   };
   constexpr int kStores = 8;  // store instructions per wave and tile
 
@@ -566,8 +608,10 @@ __global__ __launch_bounds__(64 * (TI / 64) * (TJ / 64)) void trimul_contract_bf
         for (int x = 0; x < 2; ++x) {
           const int r_a = wi + x * 32 + (lane & 31);
           const int r_b = wj + x * 32 + (lane & 31);
-          fa[kc][x].load(sa + r_a * BK + 8 * (lc ^ pswz(r_a)));
-          fb[kc][x].load(sb + r_b * BK + 8 * (lc ^ pswz(r_b)));
+          if constexpr (LT) fa[kc][x] = tfrag(sa, TI, wi + x * 32, kc);
+          else fa[kc][x].load(sa + r_a * BK + 8 * (lc ^ pswz(r_a)));
+          if constexpr (RT) fb[kc][x] = tfrag(sb, TJ, wj + x * 32, kc);
+          else fb[kc][x].load(sb + r_b * BK + 8 * (lc ^ pswz(r_b)));
         }
       }
 #pragma unroll
@@ -1450,6 +1494,40 @@ int trimul_contract_planes(const void* pl, const void* pr, void* out, int Np, in
   if (dtype == GTK_F32)
     return launch_contract<float>((const float*)pl, (const float*)pr, (float*)out, Np, nplanes, st);
   return launch_contract<bf16>((const bf16*)pl, (const bf16*)pr, (bf16*)out, Np, nplanes, st);
+}
+
+bool trimul_contract_t_ok(int Np, int64_t nplanes, int dtype) {
+  return dtype != GTK_F32 && contract_tile<bf16>(Np, nplanes) >= 128;
+}
+
+int trimul_contract_planes_t(const void* pl, const void* pr, void* out, int Np, int64_t nplanes, bool lt,
+                             bool rt, hipStream_t st) {
+  GTK_REQUIRE(trimul_contract_t_ok(Np, nplanes, GTK_BF16), GTK_EUNSUPPORTED,
+              "transposed-operand contraction: Np %d", Np);
+  const int tile = contract_tile<bf16>(Np, nplanes);
+  const int64_t blocks = (int64_t)(Np / tile) * (Np / tile) * nplanes;
+  GTK_REQUIRE(blocks < (1ll << 31), GTK_EUNSUPPORTED, "contraction grid too large");
+  const int64_t ps = (int64_t)Np * Np;
+  const bf16* a = (const bf16*)pl;
+  const bf16* b = (const bf16*)pr;
+  bf16* x = (bf16*)out;
+  StageTimer timer("trimul_contract", st);
+  auto go = [&](auto kern, int threads, int64_t most) {
+    kern<<<(unsigned)std::min<int64_t>(blocks, most), threads, 0, st>>>(a, b, x, Np, Np, nplanes, ps, ps);
+  };
+  if (tile == 256) {
+    if (lt && rt) go(trimul_contract_bf16_kernel<256, 256, true, true>, 1024, device_cus());
+    else if (lt) go(trimul_contract_bf16_kernel<256, 256, true, false>, 1024, device_cus());
+    else if (rt) go(trimul_contract_bf16_kernel<256, 256, false, true>, 1024, device_cus());
+    else go(trimul_contract_bf16_kernel<256, 256>, 1024, device_cus());
+  } else {
+    if (lt && rt) go(trimul_contract_bf16_kernel<128, 128, true, true>, 256, 2 * device_cus());
+    else if (lt) go(trimul_contract_bf16_kernel<128, 128, true, false>, 256, 2 * device_cus());
+    else if (rt) go(trimul_contract_bf16_kernel<128, 128, false, true>, 256, 2 * device_cus());
+    else go(trimul_contract_bf16_kernel<128, 128>, 256, 2 * device_cus());
+  }
+  GTK_LAUNCH_CHECK();
+  return GTK_OK;
 }
 
 }  // namespace gtk

@@ -977,17 +977,35 @@ static int bwd_trimul(const void* z, const float* mask, const void* dy,
     }
     GTK_LAUNCH_CHECK();
   }
-  // 3. contraction backward (px is free from here on: it takes dX^T)
-  T* pdxt = a.px;
-  if ((rc = launch_transpose_planes<T>(a.pa, a.pat, Np, nplanes, st))) return rc;
-  if ((rc = launch_transpose_planes<T>(a.pb, a.pbt, Np, nplanes, st))) return rc;
-  if ((rc = launch_transpose_planes<T>(a.pdx, pdxt, Np, nplanes, st))) return rc;
-  if (outgoing) {
-    if ((rc = trimul_contract_planes(a.pdx, a.pbt, a.pda, Np, nplanes, dtype, st))) return rc;
-    if ((rc = trimul_contract_planes(pdxt, a.pat, a.pdb, Np, nplanes, dtype, st))) return rc;
+  // 3. contraction backward.  Outgoing: dA = dX Bm, dB = dX^T A; incoming
+  // (planes stored so that X = A Bm^T as well): dA^T = Bm^T dX, dB^T =
+  // A^T dX^T.  The bf16 tile kernels read the operands that enter
+  // transposed straight from the planes (trimul_contract_planes_t);
+  // otherwise the planes are transposed first (px is free from here on: it
+  // takes dX^T).  GENIE_TK_TRANSPOSE_PLANES=1 selects the transposing form
+  // everywhere (for tests: the two forms give identical bits).
+  const char* tp = std::getenv("GENIE_TK_TRANSPOSE_PLANES");
+  const bool force_transpose = tp && tp[0] == '1';
+  if (!force_transpose && trimul_contract_t_ok(Np, nplanes, dtype)) {
+    if (outgoing) {
+      if ((rc = trimul_contract_planes_t(a.pdx, a.pb, a.pda, Np, nplanes, false, true, st))) return rc;
+      if ((rc = trimul_contract_planes_t(a.pdx, a.pa, a.pdb, Np, nplanes, true, true, st))) return rc;
+    } else {
+      if ((rc = trimul_contract_planes_t(a.pb, a.pdx, a.pda, Np, nplanes, true, false, st))) return rc;
+      if ((rc = trimul_contract_planes_t(a.pa, a.pdx, a.pdb, Np, nplanes, true, true, st))) return rc;
+    }
   } else {
-    if ((rc = trimul_contract_planes(a.pbt, a.pdx, a.pda, Np, nplanes, dtype, st))) return rc;
-    if ((rc = trimul_contract_planes(a.pat, pdxt, a.pdb, Np, nplanes, dtype, st))) return rc;
+    T* pdxt = a.px;
+    if ((rc = launch_transpose_planes<T>(a.pa, a.pat, Np, nplanes, st))) return rc;
+    if ((rc = launch_transpose_planes<T>(a.pb, a.pbt, Np, nplanes, st))) return rc;
+    if ((rc = launch_transpose_planes<T>(a.pdx, pdxt, Np, nplanes, st))) return rc;
+    if (outgoing) {
+      if ((rc = trimul_contract_planes(a.pdx, a.pbt, a.pda, Np, nplanes, dtype, st))) return rc;
+      if ((rc = trimul_contract_planes(pdxt, a.pat, a.pdb, Np, nplanes, dtype, st))) return rc;
+    } else {
+      if ((rc = trimul_contract_planes(a.pbt, a.pdx, a.pda, Np, nplanes, dtype, st))) return rc;
+      if ((rc = trimul_contract_planes(a.pat, pdxt, a.pdb, Np, nplanes, dtype, st))) return rc;
+    }
   }
   // 4. prologue backward
   {

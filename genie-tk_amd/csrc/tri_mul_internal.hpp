@@ -57,5 +57,11 @@ int trimul_recompute_planes(const void* z, const float* mask, const void* packed
 // out = L R^T per [Np][Np] plane (nplanes planes).
 int trimul_contract_planes(const void* pl, const void* pr, void* out, int Np, int64_t nplanes,
                            int dtype, hipStream_t st);
+// The same with L given as the plane L^T (lt) and / or R as R^T (rt):
+// bf16 planes whose contraction takes the 256 or 128 tile kernels
+// (trimul_contract_t_ok); elsewhere the caller transposes the planes.
+bool trimul_contract_t_ok(int Np, int64_t nplanes, int dtype);
+int trimul_contract_planes_t(const void* pl, const void* pr, void* out, int Np, int64_t nplanes, bool lt,
+                             bool rt, hipStream_t st);
 
 }  // namespace gtk

@@ -83,9 +83,41 @@ def _np(t):
 
 @pytest.mark.parametrize("dname", ["fp32", "bf16"])
 @pytest.mark.parametrize("outgoing", [True, False])
-@pytest.mark.parametrize("N,c", [(64, 128), (37, 64), (130, 128)])
+@pytest.mark.parametrize("N,c", [(64, 128), (37, 64), (130, 128), (100, 128)])
 def test_tri_mul_backward(dname, outgoing, N, c):
+    """N = 100 (planes of 128): the bf16 contraction backward reads the
+    operands that enter transposed straight from the planes."""
     _tri_mul_backward_case(dname, outgoing, N, c)
+
+
+@pytest.mark.parametrize("outgoing", [True, False])
+@pytest.mark.parametrize("B,N", [(1, 512), (2, 100)])
+def test_tri_mul_backward_transposed_operands_bit_exact(monkeypatch, outgoing, B, N):
+    """The contraction backward with the transposed operands read from the
+    planes (256 x 256 tiles at N = 512, 128 x 128 at N = 100) gives the same
+    bits as transposing the planes first (GENIE_TK_TRANSPOSE_PLANES=1): the
+    same products are summed in the same order."""
+    log(f"tri_mul backward transposed operands B={B} N={N} outgoing={outgoing}")
+    P = H.bf16_params(H.draw_params(H.tri_mul_shapes(128, 128), seed=N + 3, ln_random=True,
+                                    bias_random=True))
+    z = H.bf16_round(H.pair_input(B, N, 128, seed=N + 4))
+    m = H.tail_mask(B, N, [N - 9] * B)
+    dy = H.bf16_round(H.pair_input(B, N, 128, seed=N + 5))
+    mod = trimul_module(P, outgoing, torch.bfloat16)
+    runs = []
+    for force in ("0", "1"):
+        monkeypatch.setenv("GENIE_TK_TRANSPOSE_PLANES", force)
+        mod.zero_grad(set_to_none=True)
+        zt = torch.from_numpy(z).to("cuda", torch.bfloat16).requires_grad_(True)
+        y = mod(zt, torch.from_numpy(m).to("cuda"))
+        y.backward(torch.from_numpy(dy).to("cuda", torch.bfloat16))
+        torch.cuda.synchronize()
+        g = {"dx": zt.grad.clone()}
+        for name, prm in mod.named_parameters():
+            g[name] = prm.grad.clone()
+        runs.append(g)
+    for name in runs[0]:
+        assert torch.equal(runs[0][name], runs[1][name]), f"{name} differs between the two forms"
 
 
 @pytest.mark.parametrize("outgoing", [True, False])
