@@ -120,6 +120,16 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
+// buf_rsrc for a base the caller knows is wave-uniform but the compiler may
+// not (64-bit address arithmetic it did on the VALU): both halves go through
+// readfirstlane, so the descriptor lands in SGPRs and no buffer access needs
+// a waterfall loop.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc_u(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  const uint64_t u = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32) |
+                     (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a);
+  return buf_rsrc(reinterpret_cast<const void*>(u), bytes);
+}
 constexpr uint32_t kBufSkip = 0x80000000u;
 // 4 values as bf16 (8 bytes) at byte offset `off`.
 __device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, uint32_t off, float a, float b,

@@ -1585,9 +1585,12 @@ __global__ __launch_bounds__(512) void attn_bwd_pro_lds_kernel(const bf16* __res
   const uint32_t svo = cm_store_voff(pitch), lvo = cm_load_voff(pitch);
   const uint32_t evo = (uint32_t)(4 * half * pitch + t32) * 2;  // element path: channel 4*half, position t32
   for (int64_t tile = (int64_t)blockIdx.x * 8 + wave; tile < ntiles; tile += (int64_t)gridDim.x * 8) {
-    const int jt = (int)(tile % jtiles);
-    const int r = (int)((tile / jtiles) % N);
-    const int b = (int)(tile / ((int64_t)jtiles * N));
+    // tile coordinates through readfirstlane: the 64-bit divisions run on the
+    // VALU, and descriptors built from their results would otherwise sit in
+    // VGPRs, each buffer access in a waterfall loop
+    const int jt = __builtin_amdgcn_readfirstlane((int)(tile % jtiles));
+    const int r = __builtin_amdgcn_readfirstlane((int)((tile / jtiles) % N));
+    const int b = __builtin_amdgcn_readfirstlane((int)(tile / ((int64_t)jtiles * N)));
     const int j = jt * 32 + t32;
     const bool valid = j < N;
     const int64_t xp = valid ? ((int64_t)b * N + (starting ? r : j)) * N + (starting ? j : r) : 0;
@@ -1598,7 +1601,7 @@ __global__ __launch_bounds__(512) void attn_bwd_pro_lds_kernel(const bf16* __res
     // per-tile LDS reads of W_b and the LayerNorm weight through an opaque
     // index: hoisted out of the tile loop, 320 of them would stay in registers
     const int oz = opaque_zero();
-    const auto srs = buf_rsrc(bf.cm_stack + p0, (uint32_t)(4 * CH * pitch * 2));
+    const auto srs = buf_rsrc_u(bf.cm_stack + p0, (uint32_t)(4 * CH * pitch * 2));
 
     f32x2 st;
     {
@@ -1688,8 +1691,8 @@ __global__ __launch_bounds__(512) void attn_bwd_pro_lds_kernel(const bf16* __res
     const float m1 = s1 * (1.0f / C), m2 = s2 * (1.0f / C);
     // the rows are read again below rather than kept
     asm volatile("" ::: "memory");
-    const auto xrs = buf_rsrc(bf.cm_xh + p0, (uint32_t)(C * pitch * 2));
-    const auto nrs = buf_rsrc(bf.cm_dxn + p0, (uint32_t)(C * pitch * 2));
+    const auto xrs = buf_rsrc_u(bf.cm_xh + p0, (uint32_t)(C * pitch * 2));
+    const auto nrs = buf_rsrc_u(bf.cm_dxn + p0, (uint32_t)(C * pitch * 2));
 #pragma unroll
     for (int nt = 0; nt < C / 32; ++nt) {
       float xs[16], dn[16];
