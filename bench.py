@@ -666,8 +666,9 @@ def gpu_ops_at(torch, C, dev: str, N: int, tail: int, reps: int) -> dict:
 
 
 def config_table(torch, C, dev: str) -> int:
-    """GPU (bf16 kernels, fp32 for config 1) and host-CPU (the PyTorch fallback
-    in fp32) times of the operators at the benchmark configurations:
+    """GPU (bf16 kernels, fp32 for the N=64 tri-mul) and host-CPU (the PyTorch
+    fallback in fp32) times of the operators at the five benchmark workloads,
+    numbered in the table's first column:
     1: tri-mul outgoing, fp32, N=64; 2: tri-mul outgoing / incoming, N=256,
     mask i, j < 224; 3: tri-attn starting / ending, same; 4: the pair-stack
     block (LN-free PairTransformLayer order: tri-mul out, in, tri-attn start,
@@ -734,7 +735,7 @@ def config_table(torch, C, dev: str) -> int:
             add(5, "layernorm", N, gms, cms, mb=ln_bytes(N) / 1e6)
         del mods, cm, zg
         torch.cuda.synchronize()
-    # config 4: the pair-stack block, B = 2, N = 512, lengths 384 and 512
+    # workload 4: the pair-stack block, B = 2, N = 512, lengths 384 and 512
     layer = build_pair_layer(torch, dev)
     cl = copy_layer = cpu_modules(torch, {"l": layer})["l"]
     for mod in cl.modules():
@@ -761,7 +762,7 @@ def config_table(torch, C, dev: str) -> int:
     del layer, copy_layer
     print(f"Host CPU: {cpu['model']}, {cpu['physical_cores']} physical cores; {threads} torch "
           f"threads. CPU: the modules' PyTorch path in fp32 (tri-attn rows in chunks of 64), "
-          f"1 warmup + median of 3 (config 4: 1 warmup + 1). GPU: bf16 kernels (config 1: "
+          f"1 warmup + median of 3 (the pair-stack block: 1 warmup + 1). GPU: bf16 kernels (the N=64 tri-mul: "
           f"fp32), median of {OP_REPS} repetitions after {OP_WARM} warmup calls, each {OP_INNER} back-to-back calls between two "
           f"events.\n")
     print("| config | operator | N | CPU fp32 ms | GPU ms | speed-up | GPU throughput |")
@@ -907,7 +908,7 @@ def main() -> int:
                               "kernels": {k: round(v[1] / v[0], 4) for k, v in rep.items()}}))
             return 0
         # the operators at the other benchmark sizes: N = 256 (tail mask at
-        # 224, configs 2 and 3) and N = 1024 (mask ones, config 5)
+        # 224) and N = 1024 (mask ones)
         print("[bench] operators at N=256 and N=1024", file=sys.stderr, flush=True)
         sizes = {f"n{n}": gpu_ops_at(torch, C, dev, n, tail, reps)
                  for n, tail in ((256, 224), (2 * N, 0))}

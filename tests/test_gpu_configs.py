@@ -1,13 +1,13 @@
-"""GPU parity at the benchmark configurations (BASELINE.json ``configs``).
+"""GPU parity at the benchmark workloads:
 
-config 1  tri-mul outgoing, fp32, B=1 N=64, LN gamma=1 beta=0, biases 0   (max abs err <= 1e-4)
-config 2  tri-mul outgoing + incoming, bf16, B=1 N=256, tail mask (224), gate biases 1
-config 3  tri-attn starting + ending, bf16, B=1 N=256, H=4 d=32, tail mask (224)
-config 4  pair block (tri-mul out -> in -> tri-attn start -> end, residual each),
-          bf16, B=2 N=512, lengths (384, 512): each operator checked on the GPU's
-          own input to it; tri-attn on sampled rows (rows are independent)
-config 5  B=1 N=1024, mask ones: tri-mul outgoing and tri-attn starting on sampled
-          output rows, LayerNorm in full
+tri-mul outgoing, fp32, B=1 N=64, LN gamma=1 beta=0, biases 0   (max abs err <= 1e-4)
+tri-mul outgoing + incoming, bf16, B=1 N=256, tail mask (224), gate biases 1
+tri-attn starting + ending, bf16, B=1 N=256, H=4 d=32, tail mask (224)
+pair block (tri-mul out -> in -> tri-attn start -> end, residual each),
+    bf16, B=2 N=512, lengths (384, 512): each operator checked on the GPU's
+    own input to it; tri-attn on sampled rows (rows are independent)
+B=1 N=1024, mask ones: tri-mul outgoing and tri-attn starting on sampled
+    output rows, LayerNorm in full
 plus size-independent properties at N=512 (incoming = transposed outgoing with
 swapped a/b projections; ending = transposed starting).
 bf16 tolerance: |y - y_ref| <= 2e-2 + 1e-2 |y_ref|, y_ref = fp32/fp64 oracle on
@@ -37,8 +37,8 @@ def _triattn_params(seed):
     return H.draw_params(H.tri_attn_shapes(128, 128, 4), seed, tri_std=1.0 / np.sqrt(128))
 
 
-def test_config1_trimul_fp32():
-    log("config 1: tri-mul outgoing fp32 N=64")
+def test_trimul_fp32_n64():
+    log("tri-mul outgoing fp32 N=64")
     P = _trimul_params(0)
     z = H.pair_input(1, 64, 128, seed=0)
     m = np.ones((1, 64, 64), np.float32)
@@ -46,12 +46,12 @@ def test_config1_trimul_fp32():
     with torch.no_grad():
         y = mod(_dev(z, torch.float32), _dev(m, torch.float32))
     ref = pair_ops.tri_mul(z, m, P, True, dtype=np.float64)
-    check_fp32(to_np(y), ref, "config 1")
+    check_fp32(to_np(y), ref, "tri-mul fp32 N=64")
 
 
 @pytest.mark.parametrize("outgoing", [True, False])
-def test_config2_trimul_bf16(outgoing):
-    log(f"config 2: tri-mul bf16 N=256 outgoing={outgoing}")
+def test_trimul_bf16_n256(outgoing):
+    log(f"tri-mul bf16 N=256 outgoing={outgoing}")
     P = H.bf16_params(_trimul_params(1, gates=True))
     z = H.bf16_round(H.pair_input(1, 256, 128, seed=1))
     m = H.tail_mask(1, 256, [224])
@@ -59,12 +59,12 @@ def test_config2_trimul_bf16(outgoing):
     with torch.no_grad():
         y = mod(_dev(z, torch.bfloat16), _dev(m, torch.float32))
     ref = pair_ops.tri_mul(z, m, P, outgoing, dtype=np.float32)
-    check_bf16(to_np(y), ref, f"config 2 outgoing={outgoing}")
+    check_bf16(to_np(y), ref, f"tri-mul bf16 N=256 outgoing={outgoing}")
 
 
 @pytest.mark.parametrize("starting", [True, False])
-def test_config3_triattn_bf16(starting):
-    log(f"config 3: tri-attn bf16 N=256 starting={starting}")
+def test_triattn_bf16_n256(starting):
+    log(f"tri-attn bf16 N=256 starting={starting}")
     P = H.bf16_params(_triattn_params(2))
     x = H.bf16_round(H.pair_input(1, 256, 128, seed=2))
     m = H.tail_mask(1, 256, [224])
@@ -72,7 +72,7 @@ def test_config3_triattn_bf16(starting):
     with torch.no_grad():
         y = mod(_dev(x, torch.bfloat16), _dev(m, torch.float32))
     ref = pair_ops.tri_attn(x, m, P, starting, 4, dtype=np.float32)
-    check_bf16(to_np(y), ref, f"config 3 starting={starting}")
+    check_bf16(to_np(y), ref, f"tri-attn bf16 N=256 starting={starting}")
 
 
 @pytest.mark.parametrize("starting", [True, False])
@@ -91,8 +91,8 @@ def test_triattn_multi_block_ragged(starting, N):
     check_bf16(to_np(y), ref, f"tri-attn N={N}")
 
 
-def test_config4_pair_block():
-    log("config 4: pair block bf16 B=2 N=512 lengths (384, 512)")
+def test_pair_block_b2_n512():
+    log("pair block bf16 B=2 N=512 lengths (384, 512)")
     B, N = 2, 512
     m = H.tail_mask(B, N, [384, 512])
     Pm_out = H.bf16_params(_trimul_params(40))
@@ -112,19 +112,19 @@ def test_config4_pair_block():
         if idx < 2:
             P = (Pm_out, Pm_in)[idx]
             ref = pair_ops.tri_mul(p_in, m, P, idx == 0, dtype=np.float32)
-            check_bf16(got, ref, f"config 4 op {idx}")
+            check_bf16(got, ref, f"pair block op {idx}")
         else:
             P = (Pa_s, Pa_e)[idx - 2]
             starting = idx == 2
             ref = pair_ops.tri_attn(p_in, m, P, starting, 4, dtype=np.float32, rows=rows)
             sel = got[:, rows] if starting else got[:, :, rows]
-            check_bf16(sel, ref, f"config 4 op {idx}")
+            check_bf16(sel, ref, f"pair block op {idx}")
         p = p + upd
     assert torch.isfinite(p).all()
 
 
-def test_config5_n1024():
-    log("config 5: N=1024 tri-mul outgoing, tri-attn starting (sampled rows), LayerNorm")
+def test_trimul_triattn_layernorm_n1024():
+    log("N=1024 tri-mul outgoing, tri-attn starting (sampled rows), LayerNorm")
     N = 1024
     z = H.bf16_round(H.pair_input(1, N, 128, seed=5))
     zt = _dev(z, torch.bfloat16)
@@ -133,16 +133,16 @@ def test_config5_n1024():
     with torch.no_grad():
         y = trimul_module(Pm, True, torch.bfloat16)(zt)
     ref = pair_ops.tri_mul(z, None, Pm, True, dtype=np.float32, rows=rows)
-    check_bf16(to_np(y)[:, rows], ref, "config 5 tri-mul")
+    check_bf16(to_np(y)[:, rows], ref, "N=1024 tri-mul")
     Pa = H.bf16_params(_triattn_params(51))
     with torch.no_grad():
         y = triattn_module(Pa, True, 4, torch.bfloat16)(zt)
     ref = pair_ops.tri_attn(z, None, Pa, True, 4, dtype=np.float32, rows=rows)
-    check_bf16(to_np(y)[:, rows], ref, "config 5 tri-attn")
+    check_bf16(to_np(y)[:, rows], ref, "N=1024 tri-attn")
     w = np.ones(128, np.float32)
     bb = np.zeros(128, np.float32)
     y = ext().layernorm(zt, _dev(w, torch.float32), _dev(bb, torch.float32), 1e-5)
-    check_bf16(to_np(y), pair_ops.layer_norm(z, w, bb), "config 5 layernorm")
+    check_bf16(to_np(y), pair_ops.layer_norm(z, w, bb), "N=1024 layernorm")
 
 
 def test_transpose_identities_n512():

@@ -1,5 +1,5 @@
-"""GPU parity at corners of the reference's semantics that the configuration
-tests do not reach.
+"""GPU parity at corners of the reference's semantics that the benchmark
+workload tests do not reach.
 
 * Tri-mul with fractional mask values: the reference multiplies a and b by
   the mask value itself (src/genie_tk/triangle_mul.py:115,117), so 0.25,
@@ -13,7 +13,7 @@ tests do not reach.
 * Training with a mask that is not binary: the backward kernels model only
   0/1 masks, so the module must run autograd of its PyTorch path, and its
   gradients match the float64 oracle.
-* Config 4 (B=2, N=512, lengths 384 / 512) through ``forward_residual``,
+* The pair block (B=2, N=512, lengths 384 / 512) through ``forward_residual``,
   the fused-residual path a PairTransformLayer takes in eval, each operator
   on the previous one's output, against the oracle on sampled rows.
 
@@ -153,13 +153,13 @@ def test_tri_attn_backward_binary_mask_uses_kernels(monkeypatch):
     assert calls == [1] and x.grad is not None
 
 
-def test_config4_forward_residual():
-    """Config 4 (B=2, N=512, lengths 384 / 512, bf16) through the modules'
+def test_pair_block_b2_n512_forward_residual():
+    """The pair block (B=2, N=512, lengths 384 / 512, bf16) through the modules'
     forward_residual (residual add fused into the last kernel of each
     operator), chained tri-mul out -> in -> tri-attn start -> end: each
     operator's output p + update against the GPU's own input p plus the
     oracle's update, on sampled rows."""
-    log("config 4 via forward_residual: B=2 N=512 lengths (384, 512)")
+    log("pair block via forward_residual: B=2 N=512 lengths (384, 512)")
     B, N = 2, 512
     m = H.tail_mask(B, N, [384, 512])
     tm = lambda s: H.bf16_params(H.draw_params(H.tri_mul_shapes(128, 128), s))  # noqa: E731
@@ -185,6 +185,6 @@ def test_config4_forward_residual():
             upd = pair_ops.tri_attn(p_in, m, params[idx], starting, 4, dtype=np.float32, rows=rows)
             sel = (lambda a: a[:, rows]) if starting else (lambda a: a[:, :, rows])
             got, base = sel(to_np(p_next)), sel(p_in)
-        check_bf16(got, base + upd, f"config 4 forward_residual op {idx}")
+        check_bf16(got, base + upd, f"pair block forward_residual op {idx}")
         p = p_next
     assert torch.isfinite(p).all()
