@@ -468,15 +468,17 @@ __global__ __launch_bounds__(256) void trimul_contract_kernel(const T* __restric
 //     (R^T [k][j]) of whole Np x Np planes, which is how the backward's
 //     dA = dX Bm and dB = dX^T A read the forward planes without transposing
 //     them first.  Such a panel sits in LDS as 64 k rows of TI (TJ) columns,
-//     16-byte chunk c of row r at c ^ tswz(r), and its fragments (8
+//     16-byte chunk c of row r at c ^ 4(r % 4), and its fragments (8
 //     consecutive k of one column a lane) come from two transposing reads
 //     (ds_read_b64_tr_b16): within 16 lanes, lane L takes element L % 4 of
 //     the pieces at the addresses of lanes L/4, 4 + L/4, 8 + L/4 and
 //     12 + L/4, so with supplier lane s at row k0 + s/4, columns cb + 4(s%4)
-//     .. +3, lane L receives rows k0 .. k0 + 3 of column cb + L.  The four
-//     rows of a read then sit in four distinct chunk pairs (the swizzle), so
-//     the 16 addresses fall on distinct banks.  Products, sums and their
-//     order are those of the plain form on the transposed planes.
+//     .. +3, lane L receives rows k0 .. k0 + 3 of column cb + L.  The 32
+//     lanes served together read four rows at four chunks each, which the
+//     swizzle places in 16 distinct chunks of a 256-byte bank window (with
+//     c ^ 2(r % 4) the two 16-lane halves collided: 4 conflict cycles a
+//     read in the counters).  Products, sums and their order are those of
+//     the plain form on the transposed planes.
 // ---------------------------------------------------------------------------
 template <int TI, int TJ, bool LT = false, bool RT = false>
 __global__ __launch_bounds__(64 * (TI / 64) * (TJ / 64)) void trimul_contract_bf16_kernel(
@@ -490,7 +492,7 @@ __global__ __launch_bounds__(64 * (TI / 64) * (TJ / 64)) void trimul_contract_bf
   // transposed panels: 64 rows of TI (TJ) columns, 1 KiB copies of RPT rows
   constexpr int RPTA = 512 / TI, CPTA = TI / 8, RPTB = 512 / TJ, CPTB = TJ / 8;
   static_assert((BK / RPTA) == TI / RPR && (BK / RPTB) == TJ / RPR, "same copy count either way");
-  auto tswz = [](int r) { return 2 * (r & 3); };
+  auto tswz = [](int r) { return 4 * (r & 3); };
   __shared__ __attribute__((aligned(1024))) bf16 ring[NS * (TI + TJ) * BK];
 
   const int ti_n = Mi / TI, tj_n = Np / TJ;
