@@ -869,6 +869,16 @@ template <typename T> struct TriMulBwdWs {
   int64_t pitch;
 };
 
+// Does the contraction backward transpose its planes first?  Only where the
+// tile kernels cannot read the operands transposed, or when the test switch
+// GENIE_TK_TRANSPOSE_PLANES=1 asks for it (the transposed planes then take
+// workspace).
+static bool trimul_bwd_transposes(int64_t B, int64_t N, int c, int dtype) {
+  const char* tp = std::getenv("GENIE_TK_TRANSPOSE_PLANES");
+  if (tp && tp[0] == '1') return true;
+  return !trimul_contract_t_ok((int)round_up(N, 64), B * c, dtype);
+}
+
 template <typename T>
 static TriMulBwdWs<T> carve_trimul_bwd(Carve& cv, int64_t B, int64_t N, int cz, int c, int dtype) {
   TriMulBwdWs<T> w;
@@ -881,8 +891,13 @@ static TriMulBwdWs<T> carve_trimul_bwd(Carve& cv, int64_t B, int64_t N, int cz, 
   w.wt = cv.take<T>(4 * packed_elems(cz, c));
   w.wgt = cv.take<T>(packed_elems(cz, cz));
   const int64_t pe = B * c * Np * Np;
-  T** planes[] = {&w.pa, &w.pb, &w.px, &w.pdx, &w.pat, &w.pbt, &w.pda, &w.pdb};
+  T** planes[] = {&w.pa, &w.pb, &w.px, &w.pdx, &w.pda, &w.pdb};
   for (T** p : planes) *p = cv.take<T>(pe);
+  w.pat = w.pbt = nullptr;
+  if (trimul_bwd_transposes(B, N, c, dtype)) {
+    w.pat = cv.take<T>(pe);
+    w.pbt = cv.take<T>(pe);
+  }
   // operands of the weight-gradient products: rows padded to their tiles
   w.cm_stack = cv.take<T>((int64_t)wgrad_rows(M1) * w.pitch);
   w.cm_dp = cv.take<T>((int64_t)wgrad_rows(cz) * w.pitch);
@@ -984,9 +999,7 @@ static int bwd_trimul(const void* z, const float* mask, const void* dy,
   // otherwise the planes are transposed first (px is free from here on: it
   // takes dX^T).  GENIE_TK_TRANSPOSE_PLANES=1 selects the transposing form
   // everywhere (for tests: the two forms give identical bits).
-  const char* tp = std::getenv("GENIE_TK_TRANSPOSE_PLANES");
-  const bool force_transpose = tp && tp[0] == '1';
-  if (!force_transpose && trimul_contract_t_ok(Np, nplanes, dtype)) {
+  if (!a.pat) {
     if (outgoing) {
       if ((rc = trimul_contract_planes_t(a.pdx, a.pb, a.pda, Np, nplanes, false, true, st))) return rc;
       if ((rc = trimul_contract_planes_t(a.pdx, a.pa, a.pdb, Np, nplanes, true, true, st))) return rc;

@@ -155,9 +155,17 @@ def test_workspace_sizes(lib):
     wg = lambda rows: lib.gtk_tri_attn_workspace_size_chunked(1, 512, 64, 64, 2, rows, GTK_BF16)  # noqa: E731
     assert wg(64) < wg(0)
     assert lib.gtk_fused_layernorm_linear_workspace_size(128, 256, GTK_BF16) > 0
-    # backward: eight [c][Np][Np] planes and the per-pair operand planes at least
+    # backward: six [c][Np][Np] planes and the per-pair operand planes at least;
+    # two more planes where the contraction backward transposes its planes
+    # first (fp32, or GENIE_TK_TRANSPOSE_PLANES=1)
     wb = lib.gtk_tri_mul_backward_workspace_size(1, 512, 128, 128, GTK_BF16)
-    assert wb >= 8 * plane(1, 512, 128, 2) + 1280 * 512 * 512 * 2
+    assert wb >= 6 * plane(1, 512, 128, 2) + 1280 * 512 * 512 * 2
+    os.environ["GENIE_TK_TRANSPOSE_PLANES"] = "1"
+    try:
+        assert lib.gtk_tri_mul_backward_workspace_size(1, 512, 128, 128, GTK_BF16) == wb + 2 * plane(1, 512, 128, 2)
+    finally:
+        del os.environ["GENIE_TK_TRANSPOSE_PLANES"]
+    assert lib.gtk_tri_mul_backward_workspace_size(1, 512, 128, 128, GTK_F32) >= 8 * plane(1, 512, 128, 4)
     assert lib.gtk_tri_mul_backward_workspace_size(1, 512, 128, 96, GTK_BF16) == 0
     # twelve [B][N][H][N][32] activation/gradient buffers at least
     assert lib.gtk_tri_attn_backward_workspace_size(1, 512, 128, 128, 4, GTK_BF16) >= 12 * 512 * 512 * 128 * 2
