@@ -278,6 +278,11 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_proj_lds_kernel(const bf16* 
         const float* bk = bl + kind * CH + h * AD + oz;
         bf16* const dst = kind < 3 ? dr[kind] + ((((int64_t)b * N + r) * H + h) * np + j) * AD
                                    : bf.gt + (((int64_t)b * N + r) * np + j) * CH + h * AD;
+        // lane (t32, half) holds channels 8g + 4 half .. +3 (g = 0..3) of
+        // position t32; the half-waves trade quads (v_permlane32_swap) so that
+        // the lower half holds channels 0-7 and 16-23, the upper 8-15 and
+        // 24-31: two 16-byte stores a lane instead of four 8-byte ones
+        uint32_t pk[4][2];
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int d0 = 8 * g + 4 * half;
@@ -288,7 +293,18 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_proj_lds_kernel(const bf16* 
             const float u = acc[4 * g + q] + bv[q];
             v[q] = kind < 3 ? (valid ? u : 0.f) : sigmoidf_(u);
           }
-          store4(dst + d0, v[0], v[1], v[2], v[3]);
+          pk[g][0] = pack_bf16x2(v[0], v[1]);
+          pk[g][1] = pack_bf16x2(v[2], v[3]);
+        }
+#pragma unroll
+        for (int p2 = 0; p2 < 2; ++p2) {  // channel groups 2 p2 (lower) and 2 p2 + 1 (upper)
+          const auto s0 = __builtin_amdgcn_permlane32_swap(pk[2 * p2][0], pk[2 * p2 + 1][0], false, false);
+          const auto s1 = __builtin_amdgcn_permlane32_swap(pk[2 * p2][1], pk[2 * p2 + 1][1], false, false);
+          // lower: own quad of group 2 p2, then the upper's; upper: the
+          // lower's quad of group 2 p2 + 1, then its own
+          const uint4 c = half ? make_uint4(s0[0], s1[0], pk[2 * p2 + 1][0], pk[2 * p2 + 1][1])
+                               : make_uint4(pk[2 * p2][0], pk[2 * p2][1], s0[1], s1[1]);
+          *reinterpret_cast<uint4*>(dst + 16 * p2 + 8 * half) = c;
         }
       }
     }
