@@ -404,6 +404,30 @@ __global__ __launch_bounds__(256) void attn_bwd_fwd_kernel(AttnBwdBufs<T> bf, in
 // ---------------------------------------------------------------------------
 // epi: dgo = dy W_o, dO, dg_pre, D; per 32-position tile of one row
 // ---------------------------------------------------------------------------
+// Row store of one position from the accumulator layout: value 4g + r of
+// lane (t32, half) is channel 8g + 4 half + r of the position; the half-waves
+// trade channel quads (v_permlane32_swap) so that each lane stores two
+// 16-byte pieces of 8 consecutive channels (the lower half channels 0-7 and
+// 16-23, the upper 8-15 and 24-31) instead of four 8-byte ones.  Every lane
+// of the wave must take part.
+__device__ __forceinline__ void store_row32_bf16(bf16* row, const float* v) {
+  const int half = (threadIdx.x & 63) >> 5;
+  uint32_t pk[4][2];
+#pragma unroll
+  for (int g = 0; g < 4; ++g) {
+    pk[g][0] = pack_bf16x2(v[4 * g], v[4 * g + 1]);
+    pk[g][1] = pack_bf16x2(v[4 * g + 2], v[4 * g + 3]);
+  }
+#pragma unroll
+  for (int p2 = 0; p2 < 2; ++p2) {
+    const auto s0 = __builtin_amdgcn_permlane32_swap(pk[2 * p2][0], pk[2 * p2 + 1][0], false, false);
+    const auto s1 = __builtin_amdgcn_permlane32_swap(pk[2 * p2][1], pk[2 * p2 + 1][1], false, false);
+    const uint4 c = half ? make_uint4(s0[0], s1[0], pk[2 * p2 + 1][0], pk[2 * p2 + 1][1])
+                         : make_uint4(pk[2 * p2][0], pk[2 * p2][1], s0[1], s1[1]);
+    *reinterpret_cast<uint4*>(row + 16 * p2 + 8 * half) = c;
+  }
+}
+
 template <typename T, int C, int H>
 __global__ __launch_bounds__(256) void attn_bwd_epi_kernel(const T* __restrict__ dy, AttnBwdW<T> w,
                                                            AttnBwdBufs<T> bf, int B, int N, int np,
@@ -686,6 +710,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dbias_kernel(AttnBwdBufs<T> bf, 
 // ---------------------------------------------------------------------------
 constexpr int kRhWaves = 8;
 
+
 // [np][32] rows of two operands of one (row, head) into swizzled LDS rows:
 // np / 16 copies of 1 KiB each, spread over the block's waves.  The caller
 // waits for its copies and synchronises the block.
@@ -922,10 +947,12 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_fwd_rh_kernel(AttnBwdB
       l += __shfl_xor(l, 32);
     }
     const float li = 1.0f / l;
-    bf16* O = bf.o + (rh * np + q) * AD;
+    {
+      float ov[16];
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
-      store4(O + 8 * g + 4 * half, o[4 * g] * li, o[4 * g + 1] * li, o[4 * g + 2] * li, o[4 * g + 3] * li);
+      for (int e = 0; e < 16; ++e) ov[e] = o[e] * li;
+      store_row32_bf16(bf.o + (rh * np + q) * AD, ov);
+    }
     if (half == 0) {
       bf.mrow[rh * np + q] = row_valid ? (q < N ? m2 * (1.0f / kLog2e) : 0.f) : kMaskScore;
       bf.linv[rh * np + q] = li;
@@ -1033,13 +1060,15 @@ __global__ __launch_bounds__(64 * kRhWaves) void attn_bwd_dkdv_rh_kernel(AttnBwd
       dk = zero16();
       dv = zero16();
     }
-    bf16* dko = bf.dk + (rh * np + key) * AD;
-    bf16* dvo = bf.dv + (rh * np + key) * AD;
+    {
+      float kv[16], vv[16];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int d0 = 8 * g + 4 * half;
-      store4(dko + d0, scale * dk[4 * g], scale * dk[4 * g + 1], scale * dk[4 * g + 2], scale * dk[4 * g + 3]);
-      store4(dvo + d0, dv[4 * g], dv[4 * g + 1], dv[4 * g + 2], dv[4 * g + 3]);
+      for (int e = 0; e < 16; ++e) {
+        kv[e] = scale * dk[e];
+        vv[e] = dv[e];
+      }
+      store_row32_bf16(bf.dk + (rh * np + key) * AD, kv);
+      store_row32_bf16(bf.dv + (rh * np + key) * AD, vv);
     }
   }
 }
@@ -1140,11 +1169,12 @@ __global__ __launch_bounds__(64 * kRhWaves) __attribute__((amdgpu_waves_per_eu(4
       if (kt + 1 < nk) unit(kt + 1, bb, ba);
     }
     if (qpad) dq = zero16();
-    bf16* dqo = bf.dq + (rh * np + q) * AD;
+    {
+      float qv[16];
 #pragma unroll
-    for (int g = 0; g < 4; ++g)
-      store4(dqo + 8 * g + 4 * half, scale * dq[4 * g], scale * dq[4 * g + 1], scale * dq[4 * g + 2],
-             scale * dq[4 * g + 3]);
+      for (int e = 0; e < 16; ++e) qv[e] = scale * dq[e];
+      store_row32_bf16(bf.dq + (rh * np + q) * AD, qv);
+    }
   }
 }
 
