@@ -246,21 +246,39 @@ __global__ __launch_bounds__(512) void pair_transition_bf16_kernel(
       pr[ch] = __builtin_bit_cast(bf16x4, u32x2{s02[0], s13[0]});
       pr[ch + KC] = __builtin_bit_cast(bf16x4, u32x2{s02[1], s13[1]});
     }
-    if (valid) {
+    // Stores: the half-waves trade channel quads (v_permlane32_swap) so
+    // that each lane writes two 16-byte pieces of 8 consecutive channels a
+    // 32-channel block instead of four 8-byte ones; every lane takes part,
+    // and the stores of rows past the end are dropped (out-of-range offset
+    // of the tile's buffer descriptor).
+    const int64_t tile = first + it * stride + wave;
+    const auto ors = buf_rsrc_u(out + tile * 32 * C, (uint32_t)(32 * C * 2));
 #pragma unroll
-      for (int nt = 0; nt < NT; ++nt)
+    for (int nt = 0; nt < NT; ++nt) {
+      uint32_t pk[4][2];
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int c0 = nt * 32 + 8 * g + 4 * half;
-          const f32x4 b2 = *reinterpret_cast<const f32x4*>(b2l + c0);
-          float o[4];
+      for (int g = 0; g < 4; ++g) {
+        const int c0 = nt * 32 + 8 * g + 4 * half;
+        const f32x4 b2 = *reinterpret_cast<const f32x4*>(b2l + c0);
+        float o[4];
 #pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            o[rr] = y[nt][4 * g + rr] + b2[rr];
-            if (res) o[rr] += (float)pr[nt * 4 + g][rr];
-          }
-          store4(out + r * C + c0, o[0] * m, o[1] * m, o[2] * m, o[3] * m);
+        for (int rr = 0; rr < 4; ++rr) {
+          o[rr] = y[nt][4 * g + rr] + b2[rr];
+          if (res) o[rr] += (float)pr[nt * 4 + g][rr];
+          o[rr] *= m;
         }
+        pk[g][0] = pack_bf16x2(o[0], o[1]);
+        pk[g][1] = pack_bf16x2(o[2], o[3]);
+      }
+#pragma unroll
+      for (int p2 = 0; p2 < 2; ++p2) {
+        const auto s0 = __builtin_amdgcn_permlane32_swap(pk[2 * p2][0], pk[2 * p2 + 1][0], false, false);
+        const auto s1 = __builtin_amdgcn_permlane32_swap(pk[2 * p2][1], pk[2 * p2 + 1][1], false, false);
+        const uint4 c = half ? make_uint4(s0[0], s1[0], pk[2 * p2 + 1][0], pk[2 * p2 + 1][1])
+                             : make_uint4(pk[2 * p2][0], pk[2 * p2][1], s0[1], s1[1]);
+        const uint32_t off = (uint32_t)((t32 * C + nt * 32 + 16 * p2 + 8 * half) * 2);
+        buf_store16(ors, valid ? off : kBufSkip, c);
+      }
     }
   }
 }
