@@ -824,6 +824,7 @@ __global__ __launch_bounds__(512) void trimul_bwd_prologue_side_kernel(
 #pragma unroll
     for (int nt = 0; nt < CZ / 32; ++nt) {
       float xs[16];
+      uint32_t pk[4][2];
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int c0 = nt * 32 + 8 * g + 4 * half;
@@ -841,8 +842,19 @@ __global__ __launch_bounds__(512) void trimul_bwd_prologue_side_kernel(
             buf_store_bf16(nrs, coff, so, dzn[nt][4 * g + r]);
           }
         }
-        __builtin_amdgcn_raw_buffer_store_b64(cm_u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])}, zrs,
-                                              zoff + (uint32_t)c0 * 2, 0, 0);
+        pk[g][0] = pack_bf16x2(o[0], o[1]);
+        pk[g][1] = pack_bf16x2(o[2], o[3]);
+      }
+      // dz leaves as two 16-byte stores a lane: the half-waves trade channel
+      // quads (v_permlane32_swap) so that each lane holds 8 consecutive
+      // channels of its row
+#pragma unroll
+      for (int p2 = 0; p2 < 2; ++p2) {
+        const auto s0 = __builtin_amdgcn_permlane32_swap(pk[2 * p2][0], pk[2 * p2 + 1][0], false, false);
+        const auto s1 = __builtin_amdgcn_permlane32_swap(pk[2 * p2][1], pk[2 * p2 + 1][1], false, false);
+        const uint4 c = half ? make_uint4(s0[0], s1[0], pk[2 * p2 + 1][0], pk[2 * p2 + 1][1])
+                             : make_uint4(pk[2 * p2][0], pk[2 * p2][1], s0[1], s1[1]);
+        buf_store16(zrs, zoff + (uint32_t)(nt * 32 + 16 * p2 + 8 * half) * 2, c);
       }
       if constexpr (FULL) {
         const uint32_t so = (uint32_t)(nt * 32 * pitch) * 2;
